@@ -1,0 +1,169 @@
+/*
+ * zs.h -- C ABI of libzs, the MI355X (gfx950) logits post-processing and
+ * sampling path that replaces fankh/zllm's per-step sampler and
+ * constrained-decoding engine (src/engine/{sampler,decode_ctrl,logit_fsm,
+ * logprobs,hallucination,spec_decode}.rs and the batched-lane helpers in
+ * src/backend/gpu/{sampling,shaders}.rs).
+ *
+ * Conventions
+ *  - Every entry point returns int status: 0 = ok, < 0 = error (ZS_E*). The
+ *    message of the last error is kept per context (zs_last_error). Nothing
+ *    aborts or throws across the boundary.
+ *  - Pointers named d_* are device memory (hipMalloc'd by the caller) and are
+ *    read or written asynchronously on `stream` (a hipStream_t passed as void*;
+ *    NULL = the default stream). The caller synchronises. Host pointers (h_*)
+ *    are read before the call returns.
+ *  - A context is not thread-safe: use one per host thread. zs_ctx_create
+ *    sizes all device scratch for (max_rows, max_vocab); zs_sample and
+ *    zs_dfa_mask allocate nothing per call.
+ *  - Vocab ids are uint32; logits are fp32 rows of width V with row stride ld
+ *    (elements, ld >= V, ld % 4 == 0, base 16-byte aligned).
+ */
+#ifndef ZS_H
+#define ZS_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ZS_ABI_VERSION 1
+
+#define ZS_OK 0
+#define ZS_EINVAL (-1)   /* bad argument (null pointer, size out of range) */
+#define ZS_EHIP (-2)     /* HIP runtime error */
+#define ZS_ENOMEM (-3)   /* device allocation failed */
+#define ZS_ELIMIT (-4)   /* request exceeds a documented limit */
+
+typedef struct zs_ctx zs_ctx;
+typedef struct zs_vocab zs_vocab;
+typedef struct zs_dfa zs_dfa;
+
+/* ABI version of the library (compare with ZS_ABI_VERSION). New entry point;
+ * the reference has no FFI (docs/PLUGIN_PLAN.md:93-136 sketches a versioned
+ * C ABI that was never implemented). */
+int zs_abi_version(void);
+
+/* Context on HIP device `device`, with scratch sized for batches of up to
+ * max_rows rows of up to max_vocab logits. */
+int zs_ctx_create(int device, uint32_t max_rows, uint32_t max_vocab, zs_ctx** out);
+void zs_ctx_destroy(zs_ctx* ctx);
+const char* zs_last_error(const zs_ctx* ctx);
+
+/* ---- token byte table -------------------------------------------------
+ * Replaces TokenByteTable (src/engine/logit_fsm.rs:43-46): token t has bytes
+ * h_bytes[h_offsets[t] .. h_offsets[t+1]); h_valid[t] == 0 marks a None entry
+ * (special / non-UTF-8 piece, never allowed under a grammar). ntab entries,
+ * `eos` the end-of-sequence id (may be >= ntab, as in the reference tests).
+ * Each token is at most 255 bytes. */
+int zs_vocab_create(zs_ctx* ctx, const uint32_t* h_offsets, const uint8_t* h_bytes,
+                    const uint8_t* h_valid, uint32_t ntab, uint32_t eos, zs_vocab** out);
+void zs_vocab_destroy(zs_vocab* vocab);
+
+/* ---- byte DFA ---------------------------------------------------------
+ * Replaces RegexEngine (logit_fsm.rs:54-183) over an already-built dense DFA:
+ * h_trans[s*256 + b] = next state; h_dead[s] != 0 for the dead and quit
+ * states (logit_fsm.rs:101); h_accept[s] != 0 iff the text consumed so far is
+ * a complete match, i.e. is_match(next_eoi_state(s)) (logit_fsm.rs:110-112).
+ * Liveness (logit_fsm.rs:121-161) is computed here, once, on the host. */
+int zs_dfa_create(zs_ctx* ctx, const uint32_t* h_trans, uint32_t nstates, const uint8_t* h_dead,
+                  const uint8_t* h_accept, zs_dfa** out);
+void zs_dfa_destroy(zs_dfa* dfa);
+/* logit_fsm.rs:121 is_live / :110 is_accept for one state (host). */
+int zs_dfa_is_live(const zs_dfa* dfa, uint32_t state);
+int zs_dfa_is_accept(const zs_dfa* dfa, uint32_t state);
+/* logit_fsm.rs:275-290 advance: the state after committing `token` (unchanged
+ * for eos, a None/out-of-table token, or a walk into the dead state; *viable
+ * is set to 0 in the last case, the reference's warning). Host-side. */
+int zs_dfa_advance(const zs_dfa* dfa, const zs_vocab* vocab, uint32_t state, uint32_t token,
+                   uint32_t* out_state, int* viable);
+
+/* logit_fsm.rs:247-270 apply_mask (regex branch) + :166-182 allowed_mask,
+ * vocab-parallel on the GPU for B rows at once. Row r is at DFA state
+ * d_states[r] (int32; < 0 = row unconstrained: all bits set). Writes the
+ * packed allow bitset d_out_bits[r*words + w] (bit i of word w = id 32w+i is
+ * allowed, words = ceil(V/32)), with the EOS rule applied: eos is allowed iff
+ * is_accept(state) or no table token is viable. Ids >= ntab other than eos
+ * are disallowed. d_any (optional, uint32[B]) receives any(allowed). */
+int zs_dfa_mask(zs_ctx* ctx, const zs_dfa* dfa, const zs_vocab* vocab, const int32_t* d_states,
+                uint32_t B, uint32_t V, uint32_t* d_out_bits, uint32_t* d_any, void* stream);
+
+/* ---- sampler ------------------------------------------------------------
+ * Per-row knobs: SamplerConfig (sampler.rs:3-22) + PenaltyConfig
+ * (decode_ctrl.rs:21-43) + LogprobsCollector::top_n (logprobs.rs:27, clamped
+ * to 20). */
+typedef struct zs_row_params {
+    float temperature;     /* <= 0: greedy (sampler.rs:35) */
+    uint32_t top_k;        /* 0 = off */
+    float top_p;           /* >= 1 = off */
+    float min_p;           /* 0 = off */
+    float repeat;          /* 1 = off */
+    float presence;        /* 0 = off */
+    float frequency;       /* 0 = off */
+    uint32_t top_logprobs; /* N alternatives to report, clamped to 20 */
+    uint32_t flags;        /* ZS_ROW_* */
+    uint32_t pad;
+} zs_row_params;
+
+#define ZS_ROW_MASKED 1u       /* apply the row's allow bitset (grammar mask) */
+#define ZS_ROW_LOGPROBS 2u     /* logprob of the token + top_logprobs list (logprobs.rs:34-54) */
+#define ZS_ROW_UNCERTAINTY 4u  /* entropy / max_prob / margin / chosen_lp (hallucination.rs:232-257) */
+
+/* Output status bits per row (d_status). */
+#define ZS_ST_GREEDY 1u        /* temperature <= 0: argmax path */
+#define ZS_ST_NONFINITE 2u     /* NaN/+inf/all -inf after adjustment: id V-1 (sampler.rs:127) */
+#define ZS_ST_SMALL 4u         /* survivors fit the on-chip exact path */
+#define ZS_ST_TOPLP_AMBIG 8u   /* top_logprobs order depends on the last bit of lse */
+
+/* One step over B rows (the decode loop order of rest.rs:2594-2624):
+ *   mask (bans, then the allow bitset)  -> x~        (observers see x~)
+ *   bias + penalties over the count map -> y         (decode_ctrl.rs:107-126)
+ *   sample_with_rng(y, params, r)       -> token     (sampler.rs:31-128)
+ *   logprobs(x~, token), token_uncertainty(x~, token)
+ * r is the row's Philox4x32-10 uniform for (seed, counter) -- the reference
+ * draws it from StdRng; parity is defined with the same r injected.
+ * CSR lists are indexed by row: entries off[r] .. off[r+1]. Count-map ids
+ * must be distinct within a row; bias entries apply in list order. */
+typedef struct zs_batch {
+    uint32_t B, V;
+    uint64_t ld;
+    const float* d_logits;            /* [B][ld] */
+    const zs_row_params* d_params;    /* [B] */
+    const uint32_t* d_cnt_off;        /* [B+1] count map (token, count) */
+    const uint32_t* d_cnt_ids;
+    const uint32_t* d_cnt_vals;
+    const uint32_t* d_bias_off;       /* [B+1] logit_bias (token, bias) */
+    const uint32_t* d_bias_ids;
+    const float* d_bias_vals;
+    const uint32_t* d_ban_off;        /* [B+1] ban: ids */
+    const uint32_t* d_ban_ids;
+    const uint32_t* d_allow_bits;     /* [B][allow_words] or NULL */
+    uint32_t allow_words;
+    uint32_t top_stride;              /* >= max top_logprobs */
+    const uint64_t* d_seed;           /* [B] */
+    const uint64_t* d_counter;        /* [B] */
+    /* outputs */
+    uint32_t* d_token;                /* [B] */
+    /* observer outputs are written for rows that request them (ZS_ROW_LOGPROBS
+     * / ZS_ROW_UNCERTAINTY); other rows get NaN / top_n = 0 */
+    float* d_logprob;                 /* [B] ln p(token) (logprobs.rs:37) */
+    uint32_t* d_top_ids;              /* [B][top_stride] */
+    float* d_top_lps;                 /* [B][top_stride] */
+    uint32_t* d_top_n;                /* [B] entries written */
+    float* d_entropy;                 /* [B] hallucination.rs:232-257 */
+    float* d_max_prob;
+    float* d_margin;
+    float* d_chosen_lp;               /* [B] token_uncertainty.chosen_logprob */
+    uint32_t* d_status;               /* [B] ZS_ST_* */
+} zs_batch;
+
+/* Maximum entries per row in the merged bias+count+ban list. */
+#define ZS_MAX_PATCHES 4096
+
+int zs_sample(zs_ctx* ctx, const zs_batch* batch, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,90 @@
+"""GPU parity: zs_dfa_mask allow bitsets against the oracle's apply_mask
+(logit_fsm.rs:247-270) -- bit-exact."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.tiny import TINY_EOS, TINY_TOKENS, dfa_ab_opt, dfa_ab_plus_c, dfa_ab_star_c, dfa_abc
+from zllm_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _gpu_bits(trans, dead, acc, tokens_csr, eos, states, V):
+    from tests.gpu_util import ctx
+    from zllm_amd.engine import ByteDfa, TokenByteTable
+    c = ctx()
+    offs, data, valid = tokens_csr
+    table = TokenByteTable.from_csr(c, offs, data, valid, eos)
+    dfa = ByteDfa(c, trans, dead, acc)
+    st = torch.tensor(np.asarray(states, np.int32), device="cuda")
+    anyv = torch.zeros(len(states), dtype=torch.int32, device="cuda")
+    bits = dfa.mask(table, st, V, any_out=anyv)
+    torch.cuda.synchronize()
+    return bits.cpu().numpy().view(np.uint32), anyv.cpu().numpy(), dfa, table
+
+
+def _csr(tokens):
+    offs = [0]
+    buf = bytearray()
+    valid = []
+    for t in tokens:
+        valid.append(0 if t is None else 1)
+        if t is not None:
+            buf += t
+        offs.append(len(buf))
+    return np.array(offs, np.uint32), np.frombuffer(bytes(buf) or b"\0", np.uint8), np.array(valid, np.uint8)
+
+
+@pytest.mark.parametrize("mk", [dfa_ab_star_c, dfa_abc, dfa_ab_opt, dfa_ab_plus_c])
+def test_tiny_table_every_state(mk):
+    trans, dead, acc = mk()
+    S = trans.shape[0]
+    V = 6
+    print(f"[case] tiny {mk.__name__}", flush=True)
+    bits, anyv, dfa, table = _gpu_bits(trans, dead, acc, _csr(TINY_TOKENS), TINY_EOS, list(range(S)) + [-1], V)
+    od, ov = O.Dfa(trans, dead, acc), O.Vocab(TINY_TOKENS, TINY_EOS)
+    for s in range(S):
+        want = O.mask_bits(V, dfa=od, vocab=ov, state=s)
+        assert bits[s].tolist() == want.tolist(), (s, bits[s], want)
+        assert dfa.is_live(s) == bool(od.live[s])
+    assert bits[S].tolist() == O.pack_bits(np.ones(V, bool)).tolist()
+
+
+@pytest.mark.parametrize("S,V,ntab_delta", [(64, 5000, 0), (64, 128256, 0), (512, 20000, 0), (40, 3000, -100),
+                                            (40, 3000, 37)])
+def test_random_dfa_synthetic_vocab(S, V, ntab_delta):
+    print(f"[case] S={S} V={V}", flush=True)
+    ntab = V + ntab_delta
+    offs, data = synth.synthetic_vocab(ntab, S + V)
+    valid = np.ones(ntab, np.uint8)
+    valid[::97] = 0
+    eos = ntab - 3 if ntab_delta <= 0 else V + 5  # eos inside or beyond the table
+    trans, dead, acc = synth.random_dfa(S, S * 7 + V, dead_rate=0.3)
+    rng = np.random.default_rng(S + V)
+    states = list(rng.integers(0, S, 24)) + [S - 1, -1]  # incl. the dead state and a free row
+    bits, anyv, dfa, table = _gpu_bits(trans, dead, acc, (offs, data, valid), eos, states, V)
+    tokens = [None if not valid[t] else bytes(data[offs[t]:offs[t + 1]]) for t in range(ntab)]
+    od, ov = O.Dfa(trans, dead, acc), O.Vocab(tokens, eos)
+    for i, s in enumerate(states):
+        if s < 0:
+            want = O.pack_bits(np.ones(V, bool))
+        else:
+            want = O.mask_bits(V, dfa=od, vocab=ov, state=int(s))
+            allowed, a = O.dfa_allowed(od, ov, int(s))
+            assert bool(anyv[i]) == a
+        assert np.array_equal(bits[i], want), (i, s)
+
+
+def test_advance_matches_oracle():
+    from tests.gpu_util import ctx
+    from zllm_amd.engine import ByteDfa, TokenByteTable
+    trans, dead, acc = dfa_ab_star_c()
+    c = ctx()
+    table = TokenByteTable(c, TINY_TOKENS, TINY_EOS)
+    dfa = ByteDfa(c, trans, dead, acc)
+    od, ov = O.Dfa(trans, dead, acc), O.Vocab(TINY_TOKENS, TINY_EOS)
+    for s in range(trans.shape[0]):
+        for tok in range(7):
+            assert dfa.advance(table, s, tok)[0] == O.advance(od, ov, s, tok)

@@ -1,0 +1,107 @@
+"""GPU parity: zs_sample against the CPU oracle on the same seeded rows.
+
+Tokens and top_logprobs ids must be bit-identical; logprobs / entropy /
+max_prob / margin within 1e-5 relative (abs floors stated in gpu_util.close).
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from zllm_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(x, params, allow_bits=None, allow=None):
+    from tests.gpu_util import compare, run_gpu
+    print(f"[case] B={x.shape[0]} V={x.shape[1]}", flush=True)
+    out = run_gpu(x, params, allow_bits)
+    errs = compare(x, params, out, allow)
+    assert not errs, "\n".join(errs[:20])
+    return out
+
+
+def test_config1_single_row():
+    x = synth.logits_c1(0)
+    rng = np.random.default_rng(0)
+    hist = rng.integers(0, 32000, 64)
+    ids, cnt = np.unique(hist, return_counts=True)
+    p = dict(temperature=0.8, top_k=40, top_p=0.95, repeat=1.1, counts=list(zip(ids.tolist(), cnt.tolist())),
+             top_logprobs=5, seed=0)
+    out = _run(x, [p])
+    assert out["status"][0] & 4  # small path
+
+
+@pytest.mark.parametrize("seed", [1, 2])
+def test_mixed_rows_small_vocab(seed):
+    B, V = 24, 5000
+    x = synth.logits_powerlaw(B, V, seed)
+    params = synth.mixed_params(B, V, seed, hist=64)
+    rng = np.random.default_rng(seed)
+    for i, p in enumerate(params):
+        p["top_logprobs"] = int(rng.integers(0, 21))
+        p["seed"] = 1000 + i
+        p["counter"] = seed
+        if i % 6 == 1:
+            p["temperature"] = 0.0
+        if i % 6 == 2:
+            p["min_p"] = 0.05
+        if i % 6 == 3:
+            p["bias"] = [(int(rng.integers(0, V)), float(rng.normal(0, 5))) for _ in range(5)]
+        if i % 6 == 4:
+            p["ban"] = [int(v) for v in rng.integers(0, V, 50)]
+    _run(x, params)
+
+
+def test_big_rows_full_vocab():
+    B, V = 6, 151936
+    x = synth.logits_powerlaw(B, V, 11)
+    params = [dict(temperature=t, top_k=0, top_p=tp, seed=i, top_logprobs=5)
+              for i, (t, tp) in enumerate([(1.0, 1.0), (0.7, 0.9), (1.2, 0.95), (1.0, 0.8), (0.5, 0.99), (1.1, 1.0)])]
+    out = _run(x, params)
+    assert not any(out["status"] & 4)  # all through the big-row engine
+
+
+def test_big_rows_min_p_and_flat():
+    V = 20000
+    x = synth.logits_normal(4, V, 5, sigma=0.3)
+    params = [dict(temperature=1.0, top_k=0, top_p=0.5, min_p=0.2, seed=3),
+              dict(temperature=2.0, top_k=0, top_p=0.9, seed=4),
+              dict(temperature=1.0, top_k=300, top_p=0.9, seed=5),   # k beyond the candidate lists
+              dict(temperature=0.9, top_k=0, top_p=1.0, min_p=0.01, seed=6)]
+    _run(x, params)
+
+
+def test_edge_rows():
+    V = 3000
+    rng = np.random.default_rng(9)
+    x = rng.normal(0, 1, (8, V)).astype(np.float32)
+    x[0, 17] = np.nan                      # NaN: sampler returns V-1, observers NaN
+    x[1, :] = -np.inf                      # all masked
+    x[2, :] = 1.0                          # all ties
+    x[3, ::2] = -np.inf                    # half masked
+    x[4, 100] = np.inf                     # +inf logit
+    x[5, :] = np.float32(0.25)
+    x[5, 7] = 3.0
+    params = [dict(temperature=1.0, top_k=0, top_p=1.0, seed=1, top_logprobs=3),
+              dict(temperature=1.0, top_k=10, top_p=0.9, seed=2, top_logprobs=3),
+              dict(temperature=0.0, top_logprobs=4),
+              dict(temperature=0.8, top_k=0, top_p=0.9, seed=3, top_logprobs=2),
+              dict(temperature=1.0, top_k=5, seed=4, top_logprobs=2),
+              dict(temperature=1.0, top_k=4, top_p=0.5, seed=5, top_logprobs=5),
+              dict(temperature=1.0, top_k=0, top_p=0.0, seed=6),
+              dict(temperature=1.0, top_k=1, seed=7, top_logprobs=1)]
+    _run(x, params)
+
+
+def test_allow_bits_rows():
+    from oracle import oracle as O
+    B, V = 8, 40000
+    x = synth.logits_powerlaw(B, V, 21)
+    rng = np.random.default_rng(21)
+    allow = rng.random((B, V)) < np.array([0.5, 0.01, 0.001, 0.3, 1.0, 0.2, 0.0, 0.7])[:, None]
+    bits = np.stack([O.pack_bits(a) for a in allow])
+    params = [dict(temperature=0.9, top_k=0, top_p=0.9, seed=i, masked=True, top_logprobs=3) for i in range(B)]
+    params[3]["top_k"] = 20
+    _run(x, params, allow_bits=bits, allow=allow)

@@ -1,0 +1,120 @@
+"""ctypes binding of libzs.so (include/zs.h).
+
+This module only loads the library and declares the C structs; it raises if
+the HIP library is missing -- there is no CPU fallback anywhere in the product.
+"""
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libzs.so")
+
+ZS_OK = 0
+ZS_EINVAL = -1
+ZS_EHIP = -2
+ZS_ENOMEM = -3
+ZS_ELIMIT = -4
+
+ZS_ROW_MASKED = 1
+ZS_ROW_LOGPROBS = 2
+ZS_ROW_UNCERTAINTY = 4
+
+ZS_ST_GREEDY = 1
+ZS_ST_NONFINITE = 2
+ZS_ST_SMALL = 4
+ZS_ST_TOPLP_AMBIG = 8
+ZS_ST_LIMIT = 0x100
+ZS_ST_FALLBACK = 0x200
+
+ZS_MAX_PATCHES = 4096
+
+
+class RowParams(C.Structure):
+    _fields_ = [
+        ("temperature", C.c_float),
+        ("top_k", C.c_uint32),
+        ("top_p", C.c_float),
+        ("min_p", C.c_float),
+        ("repeat", C.c_float),
+        ("presence", C.c_float),
+        ("frequency", C.c_float),
+        ("top_logprobs", C.c_uint32),
+        ("flags", C.c_uint32),
+        ("pad", C.c_uint32),
+    ]
+
+
+class Batch(C.Structure):
+    _fields_ = [
+        ("B", C.c_uint32),
+        ("V", C.c_uint32),
+        ("ld", C.c_uint64),
+        ("d_logits", C.c_void_p),
+        ("d_params", C.c_void_p),
+        ("d_cnt_off", C.c_void_p),
+        ("d_cnt_ids", C.c_void_p),
+        ("d_cnt_vals", C.c_void_p),
+        ("d_bias_off", C.c_void_p),
+        ("d_bias_ids", C.c_void_p),
+        ("d_bias_vals", C.c_void_p),
+        ("d_ban_off", C.c_void_p),
+        ("d_ban_ids", C.c_void_p),
+        ("d_allow_bits", C.c_void_p),
+        ("allow_words", C.c_uint32),
+        ("top_stride", C.c_uint32),
+        ("d_seed", C.c_void_p),
+        ("d_counter", C.c_void_p),
+        ("d_token", C.c_void_p),
+        ("d_logprob", C.c_void_p),
+        ("d_top_ids", C.c_void_p),
+        ("d_top_lps", C.c_void_p),
+        ("d_top_n", C.c_void_p),
+        ("d_entropy", C.c_void_p),
+        ("d_max_prob", C.c_void_p),
+        ("d_margin", C.c_void_p),
+        ("d_chosen_lp", C.c_void_p),
+        ("d_status", C.c_void_p),
+    ]
+
+
+# name -> (restype, argtypes); every symbol include/zs.h declares
+SIGNATURES = {
+    "zs_abi_version": (C.c_int, []),
+    "zs_ctx_create": (C.c_int, [C.c_int, C.c_uint32, C.c_uint32, C.POINTER(C.c_void_p)]),
+    "zs_ctx_destroy": (None, [C.c_void_p]),
+    "zs_last_error": (C.c_char_p, [C.c_void_p]),
+    "zs_vocab_create": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32,
+                                  C.POINTER(C.c_void_p)]),
+    "zs_vocab_destroy": (None, [C.c_void_p]),
+    "zs_dfa_create": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p,
+                                C.POINTER(C.c_void_p)]),
+    "zs_dfa_destroy": (None, [C.c_void_p]),
+    "zs_dfa_is_live": (C.c_int, [C.c_void_p, C.c_uint32]),
+    "zs_dfa_is_accept": (C.c_int, [C.c_void_p, C.c_uint32]),
+    "zs_dfa_advance": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.POINTER(C.c_uint32),
+                                 C.POINTER(C.c_int)]),
+    "zs_dfa_mask": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32,
+                              C.c_void_p, C.c_void_p, C.c_void_p]),
+    "zs_sample": (C.c_int, [C.c_void_p, C.POINTER(Batch), C.c_void_p]),
+}
+
+_lib = None
+
+
+class ZsError(RuntimeError):
+    pass
+
+
+def lib():
+    """Load libzs.so (built by zllm_amd.build). Raises if it is missing."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ZsError(f"{LIB_PATH} not built: run `python -m zllm_amd.build` (hipcc, gfx950)")
+        lib_ = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib_, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib_
+    return _lib

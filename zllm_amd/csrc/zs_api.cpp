@@ -1,0 +1,390 @@
+// zs_api.cpp -- host side of libzs: contexts, token tables, DFAs (liveness on
+// the host), argument validation, and the C entry points of include/zs.h.
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <map>
+#include <vector>
+#include "zs_internal.h"
+
+// launchers (zs_sample.hip, zs_dfa.hip)
+extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t stream);
+extern "C" int zs_dfa_mask_launch(const dm_args& a, bool lds, uint32_t* any_scratch, hipStream_t stream);
+
+int zs_set_error(zs_ctx* ctx, int code, const char* fmt, ...) {
+    if (ctx) {
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(ctx->err, sizeof(ctx->err), fmt, ap);
+        va_end(ap);
+    }
+    return code;
+}
+
+#define ZS_HIP(ctx, call)                                                                   \
+    do {                                                                                    \
+        hipError_t e_ = (call);                                                             \
+        if (e_ != hipSuccess)                                                               \
+            return zs_set_error((ctx), ZS_EHIP, "%s: %s", #call, hipGetErrorString(e_));   \
+    } while (0)
+
+template <typename T>
+static int zs_alloc(zs_ctx* ctx, T** p, size_t n) {
+    *p = nullptr;
+    if (n == 0) n = 1;
+    hipError_t e = hipMalloc((void**)p, n * sizeof(T));
+    if (e != hipSuccess) {
+        *p = nullptr;
+        return zs_set_error(ctx, ZS_ENOMEM, "hipMalloc(%zu bytes): %s", n * sizeof(T), hipGetErrorString(e));
+    }
+    return ZS_OK;
+}
+
+extern "C" int zs_abi_version(void) { return ZS_ABI_VERSION; }
+
+extern "C" const char* zs_last_error(const zs_ctx* ctx) { return ctx ? ctx->err : "null context"; }
+
+extern "C" void zs_ctx_destroy(zs_ctx* ctx) {
+    if (!ctx) return;
+    int dev = 0;
+    hipGetDevice(&dev);
+    hipSetDevice(ctx->device);
+    void* ptrs[] = {ctx->p_cnt, ctx->p_id, ctx->p_flags, ctx->p_y, ctx->cst, ctx->cs_key, ctx->cs_idx,
+                    ctx->co_key, ctx->co_idx, ctx->rst, ctx->pairs, ctx->mask_scratch};
+    for (void* p : ptrs)
+        if (p) hipFree(p);
+    hipSetDevice(dev);
+    free(ctx);
+}
+
+extern "C" int zs_ctx_create(int device, uint32_t max_rows, uint32_t max_vocab, zs_ctx** out) {
+    if (!out) return ZS_EINVAL;
+    *out = nullptr;
+    zs_ctx* ctx = (zs_ctx*)calloc(1, sizeof(zs_ctx));
+    if (!ctx) return ZS_ENOMEM;
+    if (max_rows == 0 || max_vocab == 0 || max_vocab > ZS_MAX_VOCAB) {
+        free(ctx);
+        return ZS_EINVAL;
+    }
+    ctx->device = device;
+    ctx->max_rows = max_rows;
+    ctx->max_vocab = max_vocab;
+    ctx->max_chunks = (max_vocab + ZS_P1_CH - 1) / ZS_P1_CH;
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || device < 0 || device >= ndev) {
+        free(ctx);
+        return ZS_EHIP;
+    }
+    int prev = 0;
+    hipGetDevice(&prev);
+    hipSetDevice(device);
+    int rc = ZS_OK;
+    const size_t R = max_rows, C = ctx->max_chunks;
+    if (!rc) rc = zs_alloc(ctx, &ctx->p_cnt, R);
+    if (!rc) rc = zs_alloc(ctx, &ctx->p_id, R * ZS_MAX_PATCHES);
+    if (!rc) rc = zs_alloc(ctx, &ctx->p_flags, R * ZS_MAX_PATCHES);
+    if (!rc) rc = zs_alloc(ctx, &ctx->p_y, R * ZS_MAX_PATCHES);
+    if (!rc) rc = zs_alloc(ctx, &ctx->cst, R * C);
+    if (!rc) rc = zs_alloc(ctx, &ctx->cs_key, R * C * ZS_KS);
+    if (!rc) rc = zs_alloc(ctx, &ctx->cs_idx, R * C * ZS_KS);
+    if (!rc) rc = zs_alloc(ctx, &ctx->co_key, R * C * ZS_KO);
+    if (!rc) rc = zs_alloc(ctx, &ctx->co_idx, R * C * ZS_KO);
+    if (!rc) rc = zs_alloc(ctx, &ctx->rst, R);
+    if (!rc) rc = zs_alloc(ctx, &ctx->pairs, R * (size_t)max_vocab * 2);
+    if (!rc) rc = zs_alloc(ctx, (uint32_t**)&ctx->mask_scratch, R);
+    hipSetDevice(prev);
+    if (rc) {
+        zs_ctx_destroy(ctx);
+        return rc;
+    }
+    *out = ctx;
+    return ZS_OK;
+}
+
+// ---------------------------------------------------------------------------
+// token byte table
+// ---------------------------------------------------------------------------
+struct zs_vocab_dev {
+    uint32_t* tok16;
+    uint8_t* tlen;
+};
+
+extern "C" void zs_vocab_destroy(zs_vocab* v) {
+    if (!v) return;
+    hipFree(v->d_offsets);
+    hipFree(v->d_bytes);
+    hipFree(v->d_valid);
+    hipFree(v->d_packed);
+    free(v->h_offsets);
+    free(v->h_bytes);
+    free(v->h_valid);
+    free(v);
+}
+
+extern "C" int zs_vocab_create(zs_ctx* ctx, const uint32_t* h_offsets, const uint8_t* h_bytes,
+                               const uint8_t* h_valid, uint32_t ntab, uint32_t eos, zs_vocab** out) {
+    if (!ctx || !out || !h_offsets || !h_valid || (!h_bytes && h_offsets[ntab] > 0))
+        return zs_set_error(ctx, ZS_EINVAL, "zs_vocab_create: null argument");
+    *out = nullptr;
+    for (uint32_t t = 0; t < ntab; t++) {
+        if (h_offsets[t + 1] < h_offsets[t])
+            return zs_set_error(ctx, ZS_EINVAL, "zs_vocab_create: offsets decrease at %u", t);
+        if (h_offsets[t + 1] - h_offsets[t] > 255)
+            return zs_set_error(ctx, ZS_ELIMIT, "zs_vocab_create: token %u longer than 255 bytes", t);
+    }
+    zs_vocab* v = (zs_vocab*)calloc(1, sizeof(zs_vocab));
+    v->ctx = ctx;
+    v->ntab = ntab;
+    v->eos = eos;
+    v->nbytes = h_offsets[ntab] - h_offsets[0];
+    v->h_offsets = (uint32_t*)malloc(sizeof(uint32_t) * (ntab + 1));
+    v->h_bytes = (uint8_t*)malloc(v->nbytes + 1);
+    v->h_valid = (uint8_t*)malloc(ntab + 1);
+    for (uint32_t t = 0; t <= ntab; t++) v->h_offsets[t] = h_offsets[t] - h_offsets[0];
+    if (v->nbytes) memcpy(v->h_bytes, h_bytes + h_offsets[0], v->nbytes);
+    memcpy(v->h_valid, h_valid, ntab);
+    // dense 16-byte prefix + length per token
+    std::vector<uint32_t> tok16((size_t)ntab * 4 + 4, 0);
+    std::vector<uint8_t> tlen(ntab + 1, 0);
+    uint32_t maxlen = 0;
+    for (uint32_t t = 0; t < ntab; t++) {
+        uint32_t o = v->h_offsets[t], n = v->h_offsets[t + 1] - o;
+        if (n > maxlen) maxlen = n;
+        tlen[t] = (uint8_t)(n > 255 ? 255 : n);
+        for (uint32_t i = 0; i < n && i < 16; i++) tok16[(size_t)t * 4 + i / 4] |= (uint32_t)v->h_bytes[o + i] << (8 * (i % 4));
+    }
+    v->maxlen = maxlen;
+    int prev = 0;
+    hipGetDevice(&prev);
+    hipSetDevice(ctx->device);
+    int rc = ZS_OK;
+    // d_packed holds tok16 followed by tlen (bytes)
+    size_t tok_words = (size_t)ntab * 4 + 4;
+    size_t len_words = (ntab + 4) / 4 + 1;
+    if (!rc) rc = zs_alloc(ctx, &v->d_offsets, ntab + 1);
+    if (!rc) rc = zs_alloc(ctx, &v->d_bytes, v->nbytes + 1);
+    if (!rc) rc = zs_alloc(ctx, &v->d_valid, ntab + 1);
+    if (!rc) rc = zs_alloc(ctx, &v->d_packed, tok_words + len_words);
+    if (!rc) {
+        hipMemcpy(v->d_offsets, v->h_offsets, sizeof(uint32_t) * (ntab + 1), hipMemcpyHostToDevice);
+        if (v->nbytes) hipMemcpy(v->d_bytes, v->h_bytes, v->nbytes, hipMemcpyHostToDevice);
+        hipMemcpy(v->d_valid, v->h_valid, ntab, hipMemcpyHostToDevice);
+        hipMemcpy(v->d_packed, tok16.data(), tok_words * 4, hipMemcpyHostToDevice);
+        hipError_t e = hipMemcpy((uint8_t*)(v->d_packed + tok_words), tlen.data(), ntab + 1, hipMemcpyHostToDevice);
+        if (e != hipSuccess) rc = zs_set_error(ctx, ZS_EHIP, "zs_vocab_create: %s", hipGetErrorString(e));
+    }
+    hipSetDevice(prev);
+    if (rc) {
+        zs_vocab_destroy(v);
+        return rc;
+    }
+    *out = v;
+    return ZS_OK;
+}
+
+// ---------------------------------------------------------------------------
+// DFA
+// ---------------------------------------------------------------------------
+extern "C" void zs_dfa_destroy(zs_dfa* d) {
+    if (!d) return;
+    hipFree(d->d_trans);
+    hipFree(d->d_cls);
+    hipFree(d->d_bad);
+    hipFree(d->d_accept);
+    free(d->h_trans);
+    free(d->h_dead);
+    free(d->h_accept);
+    free(d->h_live);
+    free(d);
+}
+
+// is_live for every state (logit_fsm.rs:121-161): live(u) iff an accepting
+// state is reachable from u through non-dead transitions, u included. The
+// reference explores forward and iterates a fixpoint; the same set is the
+// reverse-reachability closure of the accepting states.
+static void zs_compute_live(const uint32_t* trans, const uint8_t* dead, const uint8_t* accept, uint32_t S,
+                            uint8_t* live) {
+    std::vector<uint32_t> roff(S + 1, 0), radj;
+    for (uint32_t u = 0; u < S; u++)
+        for (uint32_t b = 0; b < 256; b++) {
+            uint32_t v = trans[(size_t)u * 256 + b];
+            if (!dead[v]) roff[v + 1]++;
+        }
+    for (uint32_t i = 0; i < S; i++) roff[i + 1] += roff[i];
+    radj.resize(roff[S]);
+    std::vector<uint32_t> fill(roff.begin(), roff.end() - 1);
+    for (uint32_t u = 0; u < S; u++)
+        for (uint32_t b = 0; b < 256; b++) {
+            uint32_t v = trans[(size_t)u * 256 + b];
+            if (!dead[v]) radj[fill[v]++] = u;
+        }
+    std::vector<uint32_t> q;
+    for (uint32_t u = 0; u < S; u++) {
+        live[u] = accept[u] ? 1 : 0;
+        if (live[u]) q.push_back(u);
+    }
+    for (size_t h = 0; h < q.size(); h++) {
+        uint32_t v = q[h];
+        for (uint32_t k = roff[v]; k < roff[v + 1]; k++) {
+            uint32_t u = radj[k];
+            if (!live[u]) { live[u] = 1; q.push_back(u); }
+        }
+    }
+}
+
+extern "C" int zs_dfa_create(zs_ctx* ctx, const uint32_t* h_trans, uint32_t nstates, const uint8_t* h_dead,
+                             const uint8_t* h_accept, zs_dfa** out) {
+    if (!ctx || !out || !h_trans || !h_dead || !h_accept || nstates == 0)
+        return zs_set_error(ctx, ZS_EINVAL, "zs_dfa_create: null argument");
+    *out = nullptr;
+    if (nstates >= 0xffffu) return zs_set_error(ctx, ZS_ELIMIT, "zs_dfa_create: %u states (max 65534)", nstates);
+    for (size_t i = 0; i < (size_t)nstates * 256; i++)
+        if (h_trans[i] >= nstates) return zs_set_error(ctx, ZS_EINVAL, "zs_dfa_create: transition %zu out of range", i);
+    zs_dfa* d = (zs_dfa*)calloc(1, sizeof(zs_dfa));
+    d->ctx = ctx;
+    d->nstates = nstates;
+    d->h_trans = (uint32_t*)malloc(sizeof(uint32_t) * nstates * 256);
+    d->h_dead = (uint8_t*)malloc(nstates);
+    d->h_accept = (uint8_t*)malloc(nstates);
+    d->h_live = (uint8_t*)malloc(nstates);
+    memcpy(d->h_trans, h_trans, sizeof(uint32_t) * nstates * 256);
+    for (uint32_t s = 0; s < nstates; s++) {
+        d->h_dead[s] = h_dead[s] ? 1 : 0;
+        d->h_accept[s] = h_accept[s] ? 1 : 0;
+    }
+    zs_compute_live(d->h_trans, d->h_dead, d->h_accept, nstates, d->h_live);
+    // fold dead / quit / non-live targets into the sentinel, then byte classes
+    std::vector<uint8_t> bad(nstates);
+    for (uint32_t s = 0; s < nstates; s++) bad[s] = (d->h_dead[s] || !d->h_live[s]) ? 1 : 0;
+    std::vector<uint16_t> col(nstates);
+    std::map<std::vector<uint16_t>, uint32_t> classes;
+    uint8_t cls[256];
+    std::vector<std::vector<uint16_t>> cols;
+    for (uint32_t b = 0; b < 256; b++) {
+        for (uint32_t s = 0; s < nstates; s++) {
+            uint32_t v = d->h_trans[(size_t)s * 256 + b];
+            col[s] = bad[v] ? 0xffffu : (uint16_t)v;
+        }
+        auto it = classes.find(col);
+        if (it == classes.end()) {
+            uint32_t id = (uint32_t)classes.size();
+            classes.emplace(col, id);
+            cols.push_back(col);
+            cls[b] = (uint8_t)id;
+        } else {
+            cls[b] = (uint8_t)it->second;
+        }
+    }
+    uint32_t ncls = (uint32_t)cols.size();
+    std::vector<uint16_t> tab((size_t)nstates * ncls);
+    for (uint32_t c = 0; c < ncls; c++)
+        for (uint32_t s = 0; s < nstates; s++) tab[(size_t)s * ncls + c] = cols[c][s];
+    d->ncls = ncls;
+    int prev = 0;
+    hipGetDevice(&prev);
+    hipSetDevice(ctx->device);
+    int rc = ZS_OK;
+    if (!rc) rc = zs_alloc(ctx, &d->d_trans, tab.size());
+    if (!rc) rc = zs_alloc(ctx, &d->d_cls, 256);
+    if (!rc) rc = zs_alloc(ctx, &d->d_bad, nstates);
+    if (!rc) rc = zs_alloc(ctx, &d->d_accept, nstates);
+    if (!rc) {
+        hipMemcpy(d->d_trans, tab.data(), tab.size() * 2, hipMemcpyHostToDevice);
+        hipMemcpy(d->d_cls, cls, 256, hipMemcpyHostToDevice);
+        hipMemcpy(d->d_bad, bad.data(), nstates, hipMemcpyHostToDevice);
+        hipError_t e = hipMemcpy(d->d_accept, d->h_accept, nstates, hipMemcpyHostToDevice);
+        if (e != hipSuccess) rc = zs_set_error(ctx, ZS_EHIP, "zs_dfa_create: %s", hipGetErrorString(e));
+    }
+    hipSetDevice(prev);
+    if (rc) {
+        zs_dfa_destroy(d);
+        return rc;
+    }
+    *out = d;
+    return ZS_OK;
+}
+
+extern "C" int zs_dfa_is_live(const zs_dfa* d, uint32_t s) { return (d && s < d->nstates) ? d->h_live[s] : 0; }
+extern "C" int zs_dfa_is_accept(const zs_dfa* d, uint32_t s) {
+    return (d && s < d->nstates) ? d->h_accept[s] : 0;
+}
+
+extern "C" int zs_dfa_advance(const zs_dfa* d, const zs_vocab* v, uint32_t state, uint32_t token,
+                              uint32_t* out_state, int* viable) {
+    if (!d || !v || !out_state || state >= d->nstates) return ZS_EINVAL;
+    *out_state = state;
+    if (viable) *viable = 1;
+    if (token == v->eos) return ZS_OK;                    // logit_fsm.rs:277-279
+    if (token >= v->ntab || !v->h_valid[token]) return ZS_OK;
+    uint32_t s = state;
+    for (uint32_t i = v->h_offsets[token]; i < v->h_offsets[token + 1]; i++) {
+        s = d->h_trans[(size_t)s * 256 + v->h_bytes[i]];
+        if (d->h_dead[s]) {                               // logit_fsm.rs:283-287
+            if (viable) *viable = 0;
+            return ZS_OK;
+        }
+    }
+    *out_state = s;
+    return ZS_OK;
+}
+
+extern "C" int zs_dfa_mask(zs_ctx* ctx, const zs_dfa* dfa, const zs_vocab* vocab, const int32_t* d_states,
+                           uint32_t B, uint32_t V, uint32_t* d_out_bits, uint32_t* d_any, void* stream) {
+    if (!ctx || !dfa || !vocab || !d_states || !d_out_bits)
+        return zs_set_error(ctx, ZS_EINVAL, "zs_dfa_mask: null argument");
+    if (B == 0) return ZS_OK;
+    if (B > ctx->max_rows) return zs_set_error(ctx, ZS_ELIMIT, "zs_dfa_mask: B=%u > max_rows=%u", B, ctx->max_rows);
+    dm_args a{};
+    a.trans = dfa->d_trans;
+    a.cls = dfa->d_cls;
+    a.bad_start = dfa->d_bad;
+    a.accept = dfa->d_accept;
+    size_t tok_words = (size_t)vocab->ntab * 4 + 4;
+    a.tok16 = vocab->d_packed;
+    a.tlen = (const uint8_t*)(vocab->d_packed + tok_words);
+    a.offsets = vocab->d_offsets;
+    a.bytes = vocab->d_bytes;
+    a.valid = vocab->d_valid;
+    a.ntab = vocab->ntab;
+    a.eos = vocab->eos;
+    a.nstates = dfa->nstates;
+    a.ncls = dfa->ncls;
+    a.states = d_states;
+    a.B = B;
+    a.V = V;
+    a.words = (V + 31) / 32;
+    a.out = d_out_bits;
+    bool lds = (size_t)dfa->nstates * dfa->ncls <= 32768;
+    uint32_t* any = d_any ? d_any : (uint32_t*)ctx->mask_scratch;
+    if (zs_dfa_mask_launch(a, lds, any, (hipStream_t)stream))
+        return zs_set_error(ctx, ZS_EHIP, "zs_dfa_mask: launch failed: %s", hipGetErrorString(hipGetLastError()));
+    return ZS_OK;
+}
+
+extern "C" int zs_sample(zs_ctx* ctx, const zs_batch* b, void* stream) {
+    if (!ctx || !b) return zs_set_error(ctx, ZS_EINVAL, "zs_sample: null argument");
+    if (b->B == 0) return ZS_OK;
+    if (b->B > ctx->max_rows) return zs_set_error(ctx, ZS_ELIMIT, "zs_sample: B=%u > max_rows=%u", b->B, ctx->max_rows);
+    if (b->V == 0 || b->V > ctx->max_vocab)
+        return zs_set_error(ctx, ZS_ELIMIT, "zs_sample: V=%u outside 1..max_vocab=%u", b->V, ctx->max_vocab);
+    if (b->ld < b->V || (b->ld & 3u) || ((uintptr_t)b->d_logits & 15u))
+        return zs_set_error(ctx, ZS_EINVAL, "zs_sample: ld must be >= V and a multiple of 4, logits 16-byte aligned");
+    if (!b->d_logits || !b->d_params || !b->d_seed || !b->d_counter || !b->d_token || !b->d_logprob ||
+        !b->d_top_ids || !b->d_top_lps || !b->d_top_n || !b->d_entropy || !b->d_max_prob || !b->d_margin ||
+        !b->d_chosen_lp || !b->d_status)
+        return zs_set_error(ctx, ZS_EINVAL, "zs_sample: null required pointer");
+    if (b->top_stride == 0) return zs_set_error(ctx, ZS_EINVAL, "zs_sample: top_stride must be >= 1");
+    if ((b->d_cnt_off && (!b->d_cnt_ids || !b->d_cnt_vals)) || (b->d_bias_off && (!b->d_bias_ids || !b->d_bias_vals)) ||
+        (b->d_ban_off && !b->d_ban_ids))
+        return zs_set_error(ctx, ZS_EINVAL, "zs_sample: CSR offsets without entries");
+    if (b->d_allow_bits && b->allow_words < (b->V + 31) / 32)
+        return zs_set_error(ctx, ZS_EINVAL, "zs_sample: allow_words < ceil(V/32)");
+    int prev = 0;
+    hipGetDevice(&prev);
+    if (prev != ctx->device) hipSetDevice(ctx->device);
+    int rc = zs_sample_launch(ctx, b, (hipStream_t)stream);
+    if (prev != ctx->device) hipSetDevice(prev);
+    return rc;
+}

@@ -1,0 +1,167 @@
+// zs_dev.h -- wave64 / workgroup primitives for gfx950 (CDNA4).
+#pragma once
+#include <hip/hip_runtime.h>
+#include "zs_math.h"
+
+#define ZS_WAVE 64
+#define ZS_BIGI 0x7fffffff
+
+__device__ __forceinline__ int zs_lane() { return (int)(threadIdx.x & 63); }
+__device__ __forceinline__ int zs_wid() { return (int)(threadIdx.x >> 6); }
+
+__device__ __forceinline__ float wave_max_f(float v) {
+    for (int d = 32; d > 0; d >>= 1) v = fmaxf(v, __shfl_xor(v, d, 64));
+    return v;
+}
+__device__ __forceinline__ double wave_sum_d(double v) {
+    for (int d = 32; d > 0; d >>= 1) v += __shfl_xor(v, d, 64);
+    return v;
+}
+__device__ __forceinline__ uint32_t wave_sum_u(uint32_t v) {
+    for (int d = 32; d > 0; d >>= 1) v += __shfl_xor(v, d, 64);
+    return v;
+}
+__device__ __forceinline__ int wave_min_i(int v) {
+    for (int d = 32; d > 0; d >>= 1) v = min(v, __shfl_xor(v, d, 64));
+    return v;
+}
+__device__ __forceinline__ int wave_max_i(int v) {
+    for (int d = 32; d > 0; d >>= 1) v = max(v, __shfl_xor(v, d, 64));
+    return v;
+}
+__device__ __forceinline__ uint32_t wave_or_u(uint32_t v) {
+    for (int d = 32; d > 0; d >>= 1) v |= __shfl_xor(v, d, 64);
+    return v;
+}
+// Inclusive scan (plain add) over the wave.
+__device__ __forceinline__ uint32_t wave_incl_scan_u(uint32_t x) {
+    int lane = zs_lane();
+    for (int d = 1; d < 64; d <<= 1) {
+        uint32_t y = __shfl_up(x, d, 64);
+        if (lane >= d) x += y;
+    }
+    return x;
+}
+// Inclusive scan with saturation at ZS_INC_CAP.
+__device__ __forceinline__ uint32_t wave_incl_scan_sat(uint32_t x) {
+    int lane = zs_lane();
+    for (int d = 1; d < 64; d <<= 1) {
+        uint32_t y = __shfl_up(x, d, 64);
+        if (lane >= d) x = zs_sat_add(x, y);
+    }
+    return x;
+}
+
+// Workgroup-wide reductions. `sh` needs NT/64 slots of the given type.
+template <int NT>
+__device__ __forceinline__ float block_max_f(float v, float* sh) {
+    v = wave_max_f(v);
+    if (zs_lane() == 0) sh[zs_wid()] = v;
+    __syncthreads();
+    float r = sh[0];
+    for (int i = 1; i < NT / 64; i++) r = fmaxf(r, sh[i]);
+    __syncthreads();
+    return r;
+}
+template <int NT>
+__device__ __forceinline__ double block_sum_d(double v, double* sh) {
+    v = wave_sum_d(v);
+    if (zs_lane() == 0) sh[zs_wid()] = v;
+    __syncthreads();
+    double r = 0.0;
+    for (int i = 0; i < NT / 64; i++) r += sh[i];
+    __syncthreads();
+    return r;
+}
+template <int NT>
+__device__ __forceinline__ uint32_t block_sum_u(uint32_t v, uint32_t* sh) {
+    v = wave_sum_u(v);
+    if (zs_lane() == 0) sh[zs_wid()] = v;
+    __syncthreads();
+    uint32_t r = 0;
+    for (int i = 0; i < NT / 64; i++) r += sh[i];
+    __syncthreads();
+    return r;
+}
+template <int NT>
+__device__ __forceinline__ int block_min_i(int v, int* sh) {
+    v = wave_min_i(v);
+    if (zs_lane() == 0) sh[zs_wid()] = v;
+    __syncthreads();
+    int r = sh[0];
+    for (int i = 1; i < NT / 64; i++) r = min(r, sh[i]);
+    __syncthreads();
+    return r;
+}
+template <int NT>
+__device__ __forceinline__ int block_max_i(int v, int* sh) {
+    v = wave_max_i(v);
+    if (zs_lane() == 0) sh[zs_wid()] = v;
+    __syncthreads();
+    int r = sh[0];
+    for (int i = 1; i < NT / 64; i++) r = max(r, sh[i]);
+    __syncthreads();
+    return r;
+}
+template <int NT>
+__device__ __forceinline__ uint32_t block_or_u(uint32_t v, uint32_t* sh) {
+    v = wave_or_u(v);
+    if (zs_lane() == 0) sh[zs_wid()] = v;
+    __syncthreads();
+    uint32_t r = 0;
+    for (int i = 0; i < NT / 64; i++) r |= sh[i];
+    __syncthreads();
+    return r;
+}
+// Exclusive scan in thread order; returns the exclusive prefix, sets *total.
+template <int NT>
+__device__ __forceinline__ uint32_t block_excl_scan_u(uint32_t v, uint32_t* sh, uint32_t* total) {
+    uint32_t inc = wave_incl_scan_u(v);
+    if (zs_lane() == 63) sh[zs_wid()] = inc;
+    __syncthreads();
+    uint32_t pre = 0, tot = 0;
+    for (int i = 0; i < NT / 64; i++) {
+        uint32_t w = sh[i];
+        if (i < zs_wid()) pre += w;
+        tot += w;
+    }
+    __syncthreads();
+    *total = tot;
+    return pre + inc - v;
+}
+// Same with saturating add (exclusive value computed without subtraction).
+template <int NT>
+__device__ __forceinline__ uint32_t block_excl_scan_sat(uint32_t v, uint32_t* sh, uint32_t* total) {
+    uint32_t inc = wave_incl_scan_sat(v);
+    uint32_t ex = __shfl_up(inc, 1, 64);
+    if (zs_lane() == 0) ex = 0;
+    if (zs_lane() == 63) sh[zs_wid()] = inc;
+    __syncthreads();
+    uint32_t pre = 0, tot = 0;
+    for (int i = 0; i < NT / 64; i++) {
+        uint32_t w = sh[i];
+        if (i < zs_wid()) pre = zs_sat_add(pre, w);
+        tot = zs_sat_add(tot, w);
+    }
+    __syncthreads();
+    *total = tot;
+    return zs_sat_add(pre, ex);
+}
+
+// In-LDS bitonic sort, ascending, of n (power of two) 64-bit keys.
+template <int NT>
+__device__ void block_bitonic_u64(unsigned long long* a, int n) {
+    for (int k = 2; k <= n; k <<= 1) {
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            for (int i = threadIdx.x; i < n; i += NT) {
+                int ixj = i ^ j;
+                if (ixj > i) {
+                    unsigned long long x = a[i], y = a[ixj];
+                    bool up = (i & k) == 0;
+                    if ((x > y) == up) { a[i] = y; a[ixj] = x; }
+                }
+            }
+            __syncthreads();
+        }
+    }
+}

@@ -1,0 +1,146 @@
+// zs_internal.h -- context and scratch layout shared by the host code and the
+// HIP kernels of libzs.
+#pragma once
+#include <stdint.h>
+#include "../../include/zs.h"
+
+// Pass-1 chunking: 256 threads x 32 elements (8 float4 loads per thread).
+#define ZS_P1_NT 256
+#define ZS_P1_CH 8192
+// Candidate lists kept per chunk: sampler (top-k threshold / small-survivor
+// detection) and observers (top_logprobs + margin).
+#define ZS_KS 128
+#define ZS_KO 32
+// Largest vocabulary a context accepts (chunk lists of one row must fit the
+// combine kernel's on-chip sort: 32 chunks x 128).
+#define ZS_MAX_VOCAB 262144
+#define ZS_MAX_CHUNKS (ZS_MAX_VOCAB / ZS_P1_CH)
+// Big-row engine: 1024 threads, 4 consecutive elements per thread.
+#define ZS_BIG_NT 1024
+#define ZS_BIG_G 4096
+#define ZS_SORT_CAP 8192
+
+// Patch flags (merged bias / count-map / ban list, one entry per token id).
+#define ZS_PF_BAN 1u
+#define ZS_PF_Y 2u
+
+// Chunk-stat flags.
+#define ZS_CF_OBS_NAN 1u
+#define ZS_CF_Z_NAN 2u
+#define ZS_CF_Z_PINF 4u
+#define ZS_CF_OBS_PINF 8u
+
+struct zs_chunk_stat {
+    float obs_max;       // NaN-ignoring max of x~
+    float z_max;         // NaN-ignoring max of z
+    uint32_t flags;
+    uint32_t z_finite;   // count of z that are not -inf and not NaN
+    int32_t g_last_nan;  // last index with NaN z (row index) or -1
+    uint32_t g_arg_all;  // argmax-last of z over the chunk (ties -> later)
+    float g_val_all;
+    uint32_t g_arg_tail; // argmax-last over elements after g_last_nan
+    float g_val_tail;
+    int32_t g_tail_n;    // number of elements after g_last_nan in the chunk
+    uint32_t ns, no;     // candidates written
+    uint32_t s_kth, o_kth; // key of the last (K-th) candidate when the list is full
+    uint32_t s_full, o_full;
+};
+
+// Row modes decided by the combine kernel.
+#define ZS_MODE_DONE 1u   // token final (greedy / non-finite / small path)
+#define ZS_MODE_BIG 2u    // big-row engine must run
+
+#define ZS_OBS_CAND 28
+
+// Observer needs (zs_row_state.obs_need).
+#define ZS_OBS_S 1u   // exact sequential sum S = sum exp(x~ - max)
+#define ZS_OBS_H 2u   // exact sequential entropy sum
+
+struct zs_row_state {
+    float z_max;
+    uint32_t thr_key;     // top-k threshold key (total order), valid if has_thr
+    uint32_t has_thr;     // 0: no top-k; 1: thr_key valid; 2: big engine must select it
+    uint32_t mode;
+    uint32_t token;
+    uint32_t status;
+    uint32_t z_is_x;      // sampler input equals x~ (T == 1, no bias / penalty)
+    // observers over x~
+    float obs_max;
+    uint32_t obs_special; // lse is NaN (NaN / +inf / all -inf row)
+    uint32_t obs_need;
+    float obs_S;          // sequential f32 sum (hallucination.rs:237-238, logprobs.rs:36)
+    float obs_H;          // sequential f32 entropy (hallucination.rs:242-248)
+    uint32_t n_cand;      // observer candidates by (x~ desc, id asc)
+    uint32_t cand_id[ZS_OBS_CAND];
+    float cand_x[ZS_OBS_CAND];
+};
+
+struct zs_ctx {
+    int device;
+    uint32_t max_rows, max_vocab, max_chunks;
+    char err[512];
+    // device scratch
+    uint32_t* p_cnt;
+    uint32_t* p_id;
+    uint32_t* p_flags;
+    float* p_y;
+    zs_chunk_stat* cst;
+    uint32_t* cs_key;
+    uint32_t* cs_idx;
+    uint32_t* co_key;
+    uint32_t* co_idx;
+    zs_row_state* rst;
+    uint32_t* pairs;       // big-row gather area [rows][max_vocab][2]
+    void* mask_scratch;    // DFA mask staging
+};
+
+struct zs_vocab {
+    zs_ctx* ctx;
+    uint32_t ntab, eos, nbytes;
+    uint32_t* d_offsets;   // [ntab+1]
+    uint8_t* d_bytes;
+    uint8_t* d_valid;
+    uint32_t* d_packed;    // per token: (offset << 8) | len, len==0xff... see zs_dfa.hip
+    uint32_t maxlen;
+    // host copies for advance()
+    uint32_t* h_offsets;
+    uint8_t* h_bytes;
+    uint8_t* h_valid;
+};
+
+struct zs_dfa {
+    zs_ctx* ctx;
+    uint32_t nstates;
+    uint32_t ncls;         // byte classes of the folded table
+    uint32_t* h_trans;     // [nstates*256] as given
+    uint8_t* h_dead;
+    uint8_t* h_accept;
+    uint8_t* h_live;
+    // device: class-compressed table with dead / quit / non-live targets
+    // folded into the sentinel 0xffff (see zs_dfa.hip)
+    uint16_t* d_trans;     // [nstates][ncls]
+    uint8_t* d_cls;        // [256] byte -> class
+    uint8_t* d_bad;        // [nstates] dead or not live
+    uint8_t* d_accept;     // [nstates]
+};
+
+// Arguments of the DFA mask kernels (zs_dfa.hip).
+struct dm_args {
+    const uint16_t* trans;    // [nstates][ncls], DM_SENT = fail
+    const uint8_t* cls;       // [256]
+    const uint8_t* bad_start; // [nstates] 1 = start state can allow nothing
+    const uint8_t* accept;    // [nstates]
+    const uint32_t* tok16;    // [ntab][4] first 16 bytes
+    const uint8_t* tlen;      // [ntab] length, 255 = longer than 254 (use CSR)
+    const uint32_t* offsets;  // CSR for long tokens
+    const uint8_t* bytes;
+    const uint8_t* valid;
+    uint32_t ntab, eos, nstates, ncls;
+    const int32_t* states;
+    uint32_t B, V, words;
+    uint32_t* out;
+    uint32_t* any;
+};
+
+// Error helper (host).
+int zs_set_error(zs_ctx* ctx, int code, const char* fmt, ...);

@@ -1,0 +1,1343 @@
+// zs_sample.hip -- the per-step sampler over a batch of fp32 logit rows.
+//
+// Reference semantics (per row, in the order of rest.rs:2594-2624):
+//   x~ = apply_mask(x)                    logit_fsm.rs:247-270 (bans, allow bits)
+//   y  = adjust_logits(x~)                decode_ctrl.rs:107-126
+//   token = sample_with_rng(y, cfg, r)    sampler.rs:31-128
+//   logprobs / token_uncertainty on x~    logprobs.rs:34-54, hallucination.rs:232-257
+//
+// Kernels (one launch each, in stream order):
+//   zs_k_prep     one workgroup per row: merge ban / bias / count-map lists into a
+//                 per-row list of patched token ids (y values computed exactly).
+//   zs_k_pass1    one workgroup per 8192-logit chunk: the only full HBM read.
+//                 Observer statistics, sampler max / greedy argmax / flags, and
+//                 exact top-K candidate lists (LDS radix select on total-order keys).
+//   zs_k_combine  one workgroup per row: merges chunk results; finishes greedy,
+//                 non-finite and small-survivor rows exactly on chip.
+//   zs_k_big      one 1024-thread workgroup per remaining row: exact emulation of
+//                 the reference's sequential f32 sums (S, min-p, top-p, draw).
+//   zs_k_final    chosen-token outputs.
+//
+// Exactness: every value that decides the sampled id is computed with the same
+// IEEE f32 operations as the reference (glibc-identical expf, IEEE division,
+// sequential sums reproduced exactly, see zs_math.h), so sampled ids are
+// bit-identical to sampler.rs for the same uniform r.
+#include <hip/hip_runtime.h>
+#include "zs_internal.h"
+#include "zs_dev.h"
+#include "zs_seq.h"
+
+struct zs_sargs {
+    zs_batch b;
+    uint32_t* p_cnt;
+    uint32_t* p_id;
+    uint32_t* p_flags;
+    float* p_y;
+    zs_chunk_stat* cst;
+    uint32_t* cs_key;
+    uint32_t* cs_idx;
+    uint32_t* co_key;
+    uint32_t* co_idx;
+    zs_row_state* rst;
+    uint32_t* pairs;
+    uint32_t nch;
+    uint32_t max_vocab;
+};
+
+#define ZS_ST_LIMIT 0x100u
+#define ZS_ST_FALLBACK 0x200u
+
+__device__ __forceinline__ bool zs_penalty_active(const zs_row_params& P) {
+    return P.repeat != 1.0f || P.presence != 0.0f || P.frequency != 0.0f;
+}
+__device__ __forceinline__ float zs_temper(float y, float T) {
+    // sampler.rs:47-51: divide only when T != 1 (T > 0 here)
+    return (T > 0.0f && T != 1.0f) ? y / T : y;
+}
+__device__ __forceinline__ bool zs_allowed_bit(const zs_batch& b, uint32_t r, uint32_t idx) {
+    uint32_t w = b.d_allow_bits[(size_t)r * b.allow_words + (idx >> 5)];
+    return (w >> (idx & 31)) & 1u;
+}
+
+// ===========================================================================
+// zs_k_prep: per-row patch list.
+// Entries are (id << 32) | (kind << 28) | order with kind 0 = ban, 1 = bias,
+// 2 = count; sorting groups them by id with bans first and biases in list
+// order, which reproduces the reference's per-token operation sequence.
+// ===========================================================================
+#define ZS_PREP_NT 256
+__global__ __launch_bounds__(ZS_PREP_NT) void zs_k_prep(zs_sargs a) {
+    const uint32_t r = blockIdx.x;
+    const zs_batch& b = a.b;
+    __shared__ unsigned long long ent[ZS_MAX_PATCHES];
+    __shared__ uint32_t scan_sh[ZS_PREP_NT / 64];
+    __shared__ uint32_t n_sh;
+    const zs_row_params P = b.d_params[r];
+    const uint32_t V = b.V;
+    uint32_t ban0 = b.d_ban_off ? b.d_ban_off[r] : 0, ban1 = b.d_ban_off ? b.d_ban_off[r + 1] : 0;
+    uint32_t bi0 = b.d_bias_off ? b.d_bias_off[r] : 0, bi1 = b.d_bias_off ? b.d_bias_off[r + 1] : 0;
+    uint32_t c0 = b.d_cnt_off ? b.d_cnt_off[r] : 0, c1 = b.d_cnt_off ? b.d_cnt_off[r + 1] : 0;
+    const bool pen = zs_penalty_active(P);
+    if (!pen) { c1 = c0; }  // counts only matter when penalties are active
+    uint32_t nb = ban1 - ban0, nbi = bi1 - bi0, nc = c1 - c0;
+    uint32_t total = nb + nbi + nc;
+    if (threadIdx.x == 0) n_sh = 0;
+    __syncthreads();
+    if (total > ZS_MAX_PATCHES) {
+        if (threadIdx.x == 0) {
+            a.p_cnt[r] = 0;
+            a.rst[r].status = ZS_ST_LIMIT;
+        }
+        return;
+    }
+    // gather entries with id < V
+    for (uint32_t i = threadIdx.x; i < total; i += ZS_PREP_NT) {
+        uint32_t id, kind, ord;
+        if (i < nb) { id = b.d_ban_ids[ban0 + i]; kind = 0; ord = i; }
+        else if (i < nb + nbi) { ord = i - nb; id = b.d_bias_ids[bi0 + ord]; kind = 1; }
+        else { ord = i - nb - nbi; id = b.d_cnt_ids[c0 + ord]; kind = 2; }
+        if (id < V) {
+            uint32_t pos = atomicAdd(&n_sh, 1u);
+            ent[pos] = ((unsigned long long)id << 32) | ((unsigned long long)kind << 28) | ord;
+        }
+    }
+    __syncthreads();
+    uint32_t n = n_sh;
+    uint32_t np2 = 1;
+    while (np2 < n) np2 <<= 1;
+    for (uint32_t i = n + threadIdx.x; i < np2; i += ZS_PREP_NT) ent[i] = ~0ull;
+    __syncthreads();
+    if (np2 > 1) block_bitonic_u64<ZS_PREP_NT>(ent, (int)np2);
+    // segment starts -> output slots
+    uint32_t* out_id = a.p_id + (size_t)r * ZS_MAX_PATCHES;
+    uint32_t* out_fl = a.p_flags + (size_t)r * ZS_MAX_PATCHES;
+    float* out_y = a.p_y + (size_t)r * ZS_MAX_PATCHES;
+    uint32_t base_out = 0;
+    for (uint32_t s0 = 0; s0 < n; s0 += ZS_PREP_NT) {
+        uint32_t i = s0 + threadIdx.x;
+        uint32_t is_start = 0;
+        if (i < n) {
+            uint32_t id = (uint32_t)(ent[i] >> 32);
+            is_start = (i == 0) || ((uint32_t)(ent[i - 1] >> 32) != id);
+        }
+        uint32_t tot;
+        uint32_t ex = block_excl_scan_u<ZS_PREP_NT>(is_start, scan_sh, &tot);
+        if (is_start) {
+            uint32_t id = (uint32_t)(ent[i] >> 32);
+            float x = b.d_logits[(size_t)r * b.ld + id];
+            if ((P.flags & ZS_ROW_MASKED) && b.d_allow_bits && !zs_allowed_bit(b, r, id)) x = -INFINITY;
+            uint32_t fl = 0;
+            float y;
+            uint32_t j = i;
+            // bans (logit_fsm.rs:248-252)
+            while (j < n && (uint32_t)(ent[j] >> 32) == id && ((ent[j] >> 28) & 3ull) == 0) {
+                fl |= ZS_PF_BAN;
+                j++;
+            }
+            if (fl & ZS_PF_BAN) x = -INFINITY;
+            y = x;
+            // logit_bias in list order (decode_ctrl.rs:108-112)
+            while (j < n && (uint32_t)(ent[j] >> 32) == id && ((ent[j] >> 28) & 3ull) == 1) {
+                uint32_t ord = (uint32_t)(ent[j] & 0x0fffffffull);
+                y = y + b.d_bias_vals[bi0 + ord];
+                fl |= ZS_PF_Y;
+                j++;
+            }
+            // penalty (decode_ctrl.rs:113-125)
+            if (j < n && (uint32_t)(ent[j] >> 32) == id && ((ent[j] >> 28) & 3ull) == 2) {
+                uint32_t ord = (uint32_t)(ent[j] & 0x0fffffffull);
+                uint32_t cnt = b.d_cnt_vals[c0 + ord];
+                if (P.repeat != 1.0f) {
+                    if (y > 0.0f) y = y / P.repeat;
+                    else y = y * P.repeat;
+                }
+                float pen_v = __fmul_rn(P.frequency, (float)cnt);
+                pen_v = __fadd_rn(pen_v, P.presence);
+                y = __fsub_rn(y, pen_v);
+                fl |= ZS_PF_Y;
+            }
+            out_id[base_out + ex] = id;
+            out_fl[base_out + ex] = fl;
+            out_y[base_out + ex] = y;
+        }
+        base_out += tot;
+    }
+    if (threadIdx.x == 0) {
+        a.p_cnt[r] = base_out;
+        a.rst[r].status = 0;
+    }
+}
+
+// ===========================================================================
+// zs_k_pass1
+// ===========================================================================
+#define P1_EPT 32
+
+struct p1_shared {
+    uint32_t hist[256];
+    uint32_t u[8];
+    int i[8];
+    float f[8];
+    double d[8];
+    uint32_t cnt;
+    uint32_t prefix, need, found;
+    uint32_t pcur0, pcur1;
+};
+
+// Exact top-K (key desc, index asc) of the chunk's valid keys; writes the
+// candidates (unordered) to out_key/out_idx. Element e = j*4+q of thread t has
+// index base + (j*256 + t)*4 + q.
+__device__ void p1_topk(const uint32_t (&key)[P1_EPT], uint32_t vmask, uint32_t K, uint32_t base,
+                        uint32_t* out_key, uint32_t* out_idx, uint32_t* n_out, uint32_t* kth,
+                        uint32_t* full, p1_shared& sh) {
+    const int t = threadIdx.x;
+    uint32_t nvalid = block_sum_u<ZS_P1_NT>(__popc(vmask), sh.u);
+    if (t == 0) sh.cnt = 0;
+    __syncthreads();
+    if (nvalid <= K) {
+        for (int e = 0; e < P1_EPT; e++) {
+            if ((vmask >> e) & 1u) {
+                uint32_t pos = atomicAdd(&sh.cnt, 1u);
+                if (pos < K) {
+                    out_key[pos] = key[e];
+                    out_idx[pos] = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
+                }
+            }
+        }
+        __syncthreads();
+        *n_out = min(sh.cnt, K);
+        *kth = 0;
+        *full = 0;
+        return;
+    }
+    uint32_t prefix = 0, mask = 0, need = K;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        sh.hist[t] = 0;  // 256 threads == 256 bins
+        __syncthreads();
+        for (int e = 0; e < P1_EPT; e++)
+            if (((vmask >> e) & 1u) && (key[e] & mask) == prefix)
+                atomicAdd(&sh.hist[(key[e] >> shift) & 255u], 1u);
+        __syncthreads();
+        if (t < 64) {
+            // lane l owns bins 255-4l .. 252-4l (descending)
+            uint32_t c[4], loc = 0;
+            for (int q = 0; q < 4; q++) { c[q] = sh.hist[255 - 4 * t - q]; loc += c[q]; }
+            uint32_t inc = wave_incl_scan_u(loc);
+            uint32_t before = inc - loc;
+            for (int q = 0; q < 4; q++) {
+                if (before < need && need <= before + c[q]) {
+                    sh.found = 255 - 4 * t - q;
+                    sh.need = need - before;
+                }
+                before += c[q];
+            }
+        }
+        __syncthreads();
+        prefix |= sh.found << shift;
+        mask |= 0xffu << shift;
+        need = sh.need;
+        __syncthreads();
+    }
+    const uint32_t kk = prefix;
+    uint32_t my_eq = 0;
+    for (int e = 0; e < P1_EPT; e++) {
+        if (!((vmask >> e) & 1u)) continue;
+        if (key[e] > kk) {
+            uint32_t pos = atomicAdd(&sh.cnt, 1u);
+            if (pos < K) {
+                out_key[pos] = key[e];
+                out_idx[pos] = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
+            }
+        } else if (key[e] == kk) {
+            my_eq++;
+        }
+    }
+    uint32_t n_eq = block_sum_u<ZS_P1_NT>(my_eq, sh.u);
+    if (n_eq == need) {
+        for (int e = 0; e < P1_EPT; e++) {
+            if (((vmask >> e) & 1u) && key[e] == kk) {
+                uint32_t pos = atomicAdd(&sh.cnt, 1u);
+                if (pos < K) {
+                    out_key[pos] = key[e];
+                    out_idx[pos] = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
+                }
+            }
+        }
+    } else {
+        // lowest-index `need` elements among the equal ones, in index order
+        uint32_t carry = 0;
+        for (int j = 0; j < P1_EPT / 4; j++) {
+            uint32_t c = 0;
+            for (int q = 0; q < 4; q++) {
+                int e = j * 4 + q;
+                c += (((vmask >> e) & 1u) && key[e] == kk) ? 1u : 0u;
+            }
+            uint32_t tot;
+            uint32_t ex = block_excl_scan_u<ZS_P1_NT>(c, sh.u, &tot);
+            uint32_t rank = carry + ex;
+            for (int q = 0; q < 4; q++) {
+                int e = j * 4 + q;
+                if (((vmask >> e) & 1u) && key[e] == kk) {
+                    if (rank < need) {
+                        uint32_t pos = atomicAdd(&sh.cnt, 1u);
+                        if (pos < K) {
+                            out_key[pos] = key[e];
+                            out_idx[pos] = base + (j * ZS_P1_NT + t) * 4 + q;
+                        }
+                    }
+                    rank++;
+                }
+            }
+            carry += tot;
+        }
+    }
+    __syncthreads();
+    *n_out = min(sh.cnt, K);
+    *kth = kk;
+    *full = (n_eq > need) ? 2u : 1u;  // 2: equal keys were left out
+    __syncthreads();
+}
+
+__global__ __launch_bounds__(ZS_P1_NT) void zs_k_pass1(zs_sargs a) {
+    const uint32_t c = blockIdx.x, r = blockIdx.y;
+    const zs_batch& b = a.b;
+    const uint32_t V = b.V;
+    const uint32_t base = c * ZS_P1_CH;
+    if (base >= V) return;
+    __shared__ p1_shared sh;
+    const int t = threadIdx.x;
+    const zs_row_params P = b.d_params[r];
+    const float T = P.temperature;
+    const bool masked = (P.flags & ZS_ROW_MASKED) && b.d_allow_bits;
+    const float* row = b.d_logits + (size_t)r * b.ld;
+
+    // patch range of this chunk (patch ids are sorted)
+    const uint32_t np = a.p_cnt[r];
+    const uint32_t* pid = a.p_id + (size_t)r * ZS_MAX_PATCHES;
+    if (t == 0) {
+        uint32_t lo = 0, hi = np;
+        while (lo < hi) { uint32_t mid = (lo + hi) >> 1; if (pid[mid] < base) lo = mid + 1; else hi = mid; }
+        uint32_t p0 = lo;
+        hi = np;
+        while (lo < hi) { uint32_t mid = (lo + hi) >> 1; if (pid[mid] < base + ZS_P1_CH) lo = mid + 1; else hi = mid; }
+        sh.pcur0 = p0;
+        sh.pcur1 = lo;
+    }
+
+    float xo[P1_EPT], zv[P1_EPT];
+    uint32_t vmask = 0;
+#pragma unroll
+    for (int j = 0; j < P1_EPT / 4; j++) {
+        uint32_t idx = base + (j * ZS_P1_NT + t) * 4;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        uint32_t w = 0xffffffffu;
+        if (idx < V) {
+            v = *reinterpret_cast<const float4*>(row + idx);
+            if (masked) w = b.d_allow_bits[(size_t)r * b.allow_words + (idx >> 5)] >> (idx & 31);
+        }
+        float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            int e = j * 4 + q;
+            bool valid = idx + q < V;
+            float x = vv[q];
+            if (masked && !((w >> q) & 1u)) x = -INFINITY;
+            xo[e] = x;
+            zv[e] = x;
+            if (valid) vmask |= 1u << e;
+        }
+    }
+    __syncthreads();
+    // patches: bans change x~, bias/penalty set y
+    {
+        const uint32_t* pfl = a.p_flags + (size_t)r * ZS_MAX_PATCHES;
+        const float* py = a.p_y + (size_t)r * ZS_MAX_PATCHES;
+        for (uint32_t p = sh.pcur0; p < sh.pcur1; p++) {
+            uint32_t off = pid[p] - base;
+            uint32_t q = off & 3, tt = (off >> 2) % ZS_P1_NT, j = off >> 10;
+            if ((int)tt == t) {
+#pragma unroll
+                for (int jj = 0; jj < P1_EPT / 4; jj++)
+#pragma unroll
+                    for (int qq = 0; qq < 4; qq++)
+                        if (jj == (int)j && qq == (int)q) {
+                            uint32_t fl = pfl[p];
+                            if (fl & ZS_PF_BAN) { xo[jj * 4 + qq] = -INFINITY; zv[jj * 4 + qq] = -INFINITY; }
+                            if (fl & ZS_PF_Y) zv[jj * 4 + qq] = py[p];
+                        }
+            }
+        }
+    }
+    // z = y / T
+#pragma unroll
+    for (int e = 0; e < P1_EPT; e++) zv[e] = zs_temper(zv[e], T);
+
+    // ---- observers over x~
+    float omax = -INFINITY;
+    uint32_t fl = 0;
+#pragma unroll
+    for (int e = 0; e < P1_EPT; e++) {
+        if (!((vmask >> e) & 1u)) continue;
+        float x = xo[e];
+        if (x != x) fl |= ZS_CF_OBS_NAN;
+        omax = fmaxf(omax, x);
+    }
+    omax = block_max_f<ZS_P1_NT>(omax, sh.f);
+
+    // ---- sampler over z
+    float zmax = -INFINITY;
+    uint32_t zfin = 0;
+    int last_nan = -1;
+    for (int e = 0; e < P1_EPT; e++) {
+        if (!((vmask >> e) & 1u)) continue;
+        float z = zv[e];
+        uint32_t idx = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
+        if (z != z) { fl |= ZS_CF_Z_NAN; last_nan = max(last_nan, (int)idx); }
+        else if (z == INFINITY) fl |= ZS_CF_Z_PINF;
+        if (z == z && z > -INFINITY) zfin++;
+        zmax = fmaxf(zmax, z);
+    }
+    zmax = block_max_f<ZS_P1_NT>(zmax, sh.f);
+    zfin = block_sum_u<ZS_P1_NT>(zfin, sh.u);
+    last_nan = block_max_i<ZS_P1_NT>(last_nan, sh.i);
+    fl = block_or_u<ZS_P1_NT>(fl, sh.u);
+    // greedy: argmax-last (ties -> larger index) over all, and over the tail
+    // after the chunk's last NaN. Encode (value key, index) so that a max over
+    // 64-bit composites picks the larger value, then the larger index.
+    unsigned long long best_all = 0, best_tail = 0;
+    int tail_n = 0;
+    for (int e = 0; e < P1_EPT; e++) {
+        if (!((vmask >> e) & 1u)) continue;
+        float z = zv[e];
+        if (z != z) continue;
+        uint32_t idx = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
+        // -0.0 and +0.0 compare equal in the reference (partial_cmp): map both to +0
+        float zz = (z == 0.0f) ? 0.0f : z;
+        unsigned long long comp = ((unsigned long long)zs_total_key(zz) << 32) | (idx + 1);
+        if (comp > best_all) best_all = comp;
+        if ((int)idx > last_nan) {
+            tail_n++;
+            if (comp > best_tail) best_tail = comp;
+        }
+    }
+    {
+        // block max of two u64 via the double slots
+        __shared__ unsigned long long u64sh[2][ZS_P1_NT / 64];
+        for (int d = 32; d > 0; d >>= 1) {
+            unsigned long long o1 = __shfl_xor(best_all, d, 64);
+            unsigned long long o2 = __shfl_xor(best_tail, d, 64);
+            best_all = o1 > best_all ? o1 : best_all;
+            best_tail = o2 > best_tail ? o2 : best_tail;
+        }
+        if (zs_lane() == 0) { u64sh[0][zs_wid()] = best_all; u64sh[1][zs_wid()] = best_tail; }
+        __syncthreads();
+        for (int i = 0; i < ZS_P1_NT / 64; i++) {
+            best_all = u64sh[0][i] > best_all ? u64sh[0][i] : best_all;
+            best_tail = u64sh[1][i] > best_tail ? u64sh[1][i] : best_tail;
+        }
+        __syncthreads();
+    }
+    tail_n = (int)block_sum_u<ZS_P1_NT>((uint32_t)tail_n, sh.u);
+
+    // ---- candidate lists
+    uint32_t key[P1_EPT];
+    const size_t lofs = ((size_t)r * a.nch + c);
+    // sampler list size: top_k when the row has a top-k cut within range
+    const bool has_topk = P.top_k > 0 && P.top_k < V;
+    const uint32_t Ks = (has_topk && P.top_k <= ZS_KS) ? P.top_k : ZS_KS;
+#pragma unroll
+    for (int e = 0; e < P1_EPT; e++) key[e] = zs_total_key(zv[e]);
+    uint32_t ns, s_kth, s_full;
+    p1_topk(key, vmask, Ks, base, a.cs_key + lofs * ZS_KS, a.cs_idx + lofs * ZS_KS, &ns, &s_kth,
+            &s_full, sh);
+    uint32_t ntl = P.top_logprobs > 20 ? 20 : P.top_logprobs;
+    uint32_t Ko = ntl + 8;
+    if (Ko > ZS_KO) Ko = ZS_KO;
+#pragma unroll
+    for (int e = 0; e < P1_EPT; e++) key[e] = zs_total_key(xo[e]);
+    uint32_t no, o_kth, o_full;
+    p1_topk(key, vmask, Ko, base, a.co_key + lofs * ZS_KO, a.co_idx + lofs * ZS_KO, &no, &o_kth,
+            &o_full, sh);
+
+    if (t == 0) {
+        zs_chunk_stat cs;
+        cs.obs_max = omax;
+        cs.z_max = zmax;
+        cs.flags = fl;
+        cs.z_finite = zfin;
+        cs.g_last_nan = last_nan;
+        cs.g_arg_all = best_all ? (uint32_t)(best_all & 0xffffffffull) - 1u : 0xffffffffu;
+        cs.g_val_all = best_all ? zs_key_to_float((uint32_t)(best_all >> 32)) : -INFINITY;
+        cs.g_arg_tail = best_tail ? (uint32_t)(best_tail & 0xffffffffull) - 1u : 0xffffffffu;
+        cs.g_val_tail = best_tail ? zs_key_to_float((uint32_t)(best_tail >> 32)) : -INFINITY;
+        cs.g_tail_n = tail_n;
+        cs.ns = ns;
+        cs.no = no;
+        cs.s_kth = s_kth;
+        cs.o_kth = o_kth;
+        cs.s_full = s_full;
+        cs.o_full = o_full;
+        a.cst[lofs] = cs;
+    }
+}
+
+// ===========================================================================
+// zs_k_combine
+// ===========================================================================
+#define CB_NT 256
+#define ZS_SMALL_CAP 512
+
+
+// Exact sampler over a small survivor set (n <= ZS_SMALL_CAP, all other
+// logits are -inf after top-k / mask): every sequential sum of sampler.rs is
+// reproduced with seq_group over survivors in index order; zero terms of the
+// reference's full-vocabulary loops do not change a running sum.
+#define SP_EPT (ZS_SMALL_CAP / CB_NT)
+__device__ uint32_t small_path_sample(const zs_sargs& a, uint32_t r, const zs_row_params& P, uint32_t n,
+                                      float m, float* sval, uint32_t* sidx, unsigned long long* sbuf,
+                                      seq_sh<CB_NT>& sq) {
+    const int t = threadIdx.x;
+    const zs_batch& b = a.b;
+    const uint32_t V = b.V;
+    // order survivors by index: composite (idx << 32 | value bits)
+    uint32_t np = 1;
+    while (np < n) np <<= 1;
+    for (uint32_t i = t; i < np; i += CB_NT)
+        sbuf[i] = i < n ? (((unsigned long long)sidx[i] << 32) | zs_f2u(sval[i])) : ~0ull;
+    __syncthreads();
+    if (np > 1) block_bitonic_u64<CB_NT>(sbuf, (int)np);
+    float p[SP_EPT];
+    uint32_t id[SP_EPT];
+#pragma unroll
+    for (int j = 0; j < SP_EPT; j++) {
+        uint32_t i = SP_EPT * t + j;
+        if (i < n) {
+            id[j] = (uint32_t)(sbuf[i] >> 32);
+            p[j] = zs_expf(zs_u2f((uint32_t)(sbuf[i] & 0xffffffffull)) - m);
+        } else {
+            id[j] = 0xffffffffu;
+            p[j] = 0.0f;
+        }
+    }
+    __syncthreads();
+    // softmax (sampler.rs:67-69)
+    float S = -0.0f;
+    seq_group<CB_NT, SP_EPT>(p, 0, S, NAN, sq);
+#pragma unroll
+    for (int j = 0; j < SP_EPT; j++) p[j] = p[j] / S;
+    // min-p (sampler.rs:72-88)
+    if (P.min_p > 0.0f) {
+        float pm = 0.0f;
+#pragma unroll
+        for (int j = 0; j < SP_EPT; j++) pm = fmaxf(pm, p[j]);
+        pm = block_max_f<CB_NT>(pm, reinterpret_cast<float*>(sq.scan));
+        float cut = P.min_p * pm;
+        float tv[SP_EPT];
+#pragma unroll
+        for (int j = 0; j < SP_EPT; j++) { if (p[j] < cut) p[j] = 0.0f; tv[j] = p[j]; }
+        float kept = 0.0f;
+        seq_group<CB_NT, SP_EPT>(tv, 0, kept, NAN, sq);
+        if (kept > 0.0f)
+#pragma unroll
+            for (int j = 0; j < SP_EPT; j++) p[j] = p[j] / kept;
+    }
+    // top-p (sampler.rs:91-115): cumsum in (p desc, idx asc) order
+    if (P.top_p < 1.0f) {
+        uint32_t vstar = 0, istar = 0xffffffffu;
+        bool none = !(P.top_p > 0.0f);  // cumsum 0 >= top_p: nothing kept
+        if (!none) {
+#pragma unroll
+            for (int j = 0; j < SP_EPT; j++) {
+                uint32_t i = SP_EPT * t + j;
+                if (i < np) sbuf[i] = i < n ? (((unsigned long long)(~zs_f2u(p[j])) << 32) | id[j]) : ~0ull;
+            }
+            __syncthreads();
+            if (np > 1) block_bitonic_u64<CB_NT>(sbuf, (int)np);
+            float tv[SP_EPT];
+#pragma unroll
+            for (int j = 0; j < SP_EPT; j++) {
+                uint32_t i = SP_EPT * t + j;
+                tv[j] = i < n ? zs_u2f(~(uint32_t)(sbuf[i] >> 32)) : 0.0f;
+            }
+            float cum = 0.0f;
+            int stp = seq_group<CB_NT, SP_EPT>(tv, 0, cum, P.top_p, sq);
+            if (stp >= 0) {
+                vstar = ~(uint32_t)(sbuf[stp] >> 32);
+                istar = (uint32_t)(sbuf[stp] & 0xffffffffull);
+            }
+            __syncthreads();
+        }
+        float f[SP_EPT];
+#pragma unroll
+        for (int j = 0; j < SP_EPT; j++) {
+            uint32_t pb = zs_f2u(p[j]);
+            bool keep = !none && (pb > vstar || (pb == vstar && id[j] <= istar));
+            f[j] = keep ? p[j] : 0.0f;
+        }
+        float sum = -0.0f;
+        seq_group<CB_NT, SP_EPT>(f, 0, sum, NAN, sq);
+        if (sum > 0.0f)
+#pragma unroll
+            for (int j = 0; j < SP_EPT; j++) p[j] = f[j] / sum;
+    }
+    // draw (sampler.rs:118-127); r == 0 stops at index 0 whatever its p
+    const float rr = zs_philox_uniform(b.d_seed[r], b.d_counter[r], 0u);
+    if (rr <= 0.0f) return 0;
+    float cum = 0.0f;
+    int stp = seq_group<CB_NT, SP_EPT>(p, 0, cum, rr, sq);
+    uint32_t tok = V - 1;
+    if (stp >= 0) {
+        __syncthreads();
+        if (t == stp / SP_EPT) {
+#pragma unroll
+            for (int j = 0; j < SP_EPT; j++) if (j == stp % SP_EPT) sq.stop = (int)id[j];
+        }
+        __syncthreads();
+        tok = (uint32_t)sq.stop;
+        __syncthreads();
+    }
+    return tok;
+}
+
+__global__ __launch_bounds__(CB_NT) void zs_k_combine(zs_sargs a) {
+    const uint32_t r = blockIdx.x;
+    const zs_batch& b = a.b;
+    const uint32_t V = b.V;
+    const int t = threadIdx.x;
+    const uint32_t nch = (V + ZS_P1_CH - 1) / ZS_P1_CH;
+    __shared__ unsigned long long sbuf[ZS_MAX_CHUNKS * ZS_KS];
+    __shared__ float sval[ZS_SMALL_CAP];
+    __shared__ uint32_t sidx[ZS_SMALL_CAP];
+    __shared__ seq_sh<CB_NT> sq;
+    __shared__ uint32_t n_sh;
+    __shared__ uint32_t cid_sh[ZS_OBS_CAND];
+    __shared__ float cx_sh[ZS_OBS_CAND];
+    const zs_row_params P = b.d_params[r];
+    zs_row_state st = a.rst[r];
+    if (st.status & ZS_ST_LIMIT) {
+        if (t == 0) {
+            st.mode = ZS_MODE_DONE;
+            st.token = 0xffffffffu;
+            st.obs_need = 0;
+            st.n_cand = 0;
+            a.rst[r] = st;
+        }
+        return;
+    }
+    const zs_chunk_stat* cs = a.cst + (size_t)r * a.nch;
+
+    // ---------------- observers: max, special rows, top candidates ----------------
+    float M = -INFINITY;
+    uint32_t fl = 0;
+    for (uint32_t c = 0; c < nch; c++) { M = fmaxf(M, cs[c].obs_max); fl |= cs[c].flags; }
+    // lse = max + ln(sum) is NaN for a NaN, a +inf or an all -inf row
+    const bool special = (fl & ZS_CF_OBS_NAN) || M == INFINITY || M == -INFINITY;
+    const bool want_lp = (P.flags & ZS_ROW_LOGPROBS) != 0;
+    const bool want_unc = (P.flags & ZS_ROW_UNCERTAINTY) != 0;
+    uint32_t status = 0;
+    uint32_t obs_need = 0;
+    if (!special && (want_lp || want_unc)) obs_need |= ZS_OBS_S;
+    if (!special && want_unc) obs_need |= ZS_OBS_H;
+    uint32_t n_cand = 0;
+    if (want_lp || want_unc) {
+        if (t == 0) n_sh = 0;
+        __syncthreads();
+        for (uint32_t c = 0; c < nch; c++) {
+            uint32_t no = cs[c].no;
+            const uint32_t* kk = a.co_key + ((size_t)r * a.nch + c) * ZS_KO;
+            const uint32_t* ii = a.co_idx + ((size_t)r * a.nch + c) * ZS_KO;
+            for (uint32_t i = t; i < no; i += CB_NT) {
+                uint32_t pos = atomicAdd(&n_sh, 1u);
+                sbuf[pos] = ((unsigned long long)(~kk[i]) << 32) | ii[i];
+            }
+        }
+        __syncthreads();
+        uint32_t nco = n_sh;
+        uint32_t np2 = 1;
+        while (np2 < nco) np2 <<= 1;
+        for (uint32_t i = nco + t; i < np2; i += CB_NT) sbuf[i] = ~0ull;
+        __syncthreads();
+        if (np2 > 1) block_bitonic_u64<CB_NT>(sbuf, (int)np2);
+        n_cand = nco < ZS_OBS_CAND ? nco : ZS_OBS_CAND;
+        if (t < (int)n_cand) {
+            cid_sh[t] = (uint32_t)(sbuf[t] & 0xffffffffull);
+            cx_sh[t] = zs_key_to_float(~(uint32_t)(sbuf[t] >> 32));
+        }
+        __syncthreads();
+    }
+    // the sampler sees x~ itself when T == 1 and no bias / penalty applies
+    uint32_t has_y = 0;
+    {
+        const uint32_t np = a.p_cnt[r];
+        const uint32_t* pfl = a.p_flags + (size_t)r * ZS_MAX_PATCHES;
+        for (uint32_t i = t; i < np; i += CB_NT) has_y |= (pfl[i] & ZS_PF_Y) ? 1u : 0u;
+        has_y = block_or_u<CB_NT>(has_y, reinterpret_cast<uint32_t*>(sq.scan));
+    }
+    const uint32_t z_is_x = (P.temperature == 1.0f && !has_y) ? 1u : 0u;
+
+    // ---------------- sampler ----------------
+    const float T = P.temperature;
+    uint32_t token = 0;
+    uint32_t mode = ZS_MODE_DONE;
+    uint32_t has_thr = 0, thr_key = 0;
+    float zmax = -INFINITY;
+    for (uint32_t c = 0; c < nch; c++) zmax = fmaxf(zmax, cs[c].z_max);
+    if (T <= 0.0f) {
+        // sampler.rs:35-42, max_by over partial_cmp: the last maximal element,
+        // and a NaN restarts the fold (partial_cmp -> Equal keeps the later one).
+        status |= ZS_ST_GREEDY;
+        int L = -1;
+        for (uint32_t c = 0; c < nch; c++) L = max(L, cs[c].g_last_nan);
+        float bv = 0.f;
+        uint32_t bi = 0xffffffffu;
+        bool any = false;
+        uint32_t cstart = 0;
+        if (L >= 0) {
+            uint32_t cl = (uint32_t)L / ZS_P1_CH;
+            if (cs[cl].g_tail_n > 0) { bv = cs[cl].g_val_tail; bi = cs[cl].g_arg_tail; any = true; }
+            cstart = cl + 1;
+        }
+        for (uint32_t c = cstart; c < nch; c++) {
+            if (cs[c].g_arg_all == 0xffffffffu) continue;
+            float v = cs[c].g_val_all;
+            if (!any || !(bv > v)) { bv = v; bi = cs[c].g_arg_all; any = true; }
+        }
+        token = any ? bi : (uint32_t)L;
+        if (!any && L < 0) token = 0;
+    } else if ((fl & (ZS_CF_Z_NAN | ZS_CF_Z_PINF)) || zmax == -INFINITY) {
+        // exp_sum is NaN: every comparison in the draw fails -> V-1 (sampler.rs:127)
+        status |= ZS_ST_NONFINITE;
+        token = V - 1;
+    } else {
+        const bool has_topk = P.top_k > 0 && P.top_k < V;
+        // gather sampler candidates
+        if (t == 0) n_sh = 0;
+        __syncthreads();
+        for (uint32_t c = 0; c < nch; c++) {
+            uint32_t ns = cs[c].ns;
+            const uint32_t* kk = a.cs_key + ((size_t)r * a.nch + c) * ZS_KS;
+            const uint32_t* ii = a.cs_idx + ((size_t)r * a.nch + c) * ZS_KS;
+            for (uint32_t i = t; i < ns; i += CB_NT) {
+                uint32_t pos = atomicAdd(&n_sh, 1u);
+                sbuf[pos] = ((unsigned long long)(~kk[i]) << 32) | ii[i];
+            }
+        }
+        __syncthreads();
+        uint32_t ncs = n_sh;
+        uint32_t np2 = 1;
+        while (np2 < ncs) np2 <<= 1;
+        for (uint32_t i = ncs + t; i < np2; i += CB_NT) sbuf[i] = ~0ull;
+        __syncthreads();
+        if (np2 > 1) block_bitonic_u64<CB_NT>(sbuf, (int)np2);
+        bool small = false;
+        float thr = -INFINITY;
+        if (has_topk && P.top_k <= ZS_KS) {
+            thr_key = ~(uint32_t)(sbuf[P.top_k - 1] >> 32);
+            has_thr = 1;
+            thr = zs_key_to_float(thr_key);
+            bool complete = true;
+            for (uint32_t c = 0; c < nch; c++) {
+                if (!cs[c].s_full) continue;
+                if (cs[c].s_kth == thr_key && cs[c].s_full == 2) complete = false;
+                if (thr == 0.0f) complete = false;  // the other zero also survives
+            }
+            small = complete;
+        } else if (has_topk) {
+            has_thr = 2;
+        } else {
+            uint32_t fin = 0;
+            bool ok = true;
+            for (uint32_t c = 0; c < nch; c++) {
+                fin += cs[c].z_finite;
+                if (cs[c].z_finite > ZS_KS) ok = false;
+            }
+            small = ok && fin <= ZS_SMALL_CAP;
+        }
+        if (small) {
+            // survivors: !(z < thr) (sampler.rs:59-63) and finite, gathered by index
+            if (t == 0) n_sh = 0;
+            __syncthreads();
+            for (uint32_t i = t; i < ncs; i += CB_NT) {
+                float z = zs_key_to_float(~(uint32_t)(sbuf[i] >> 32));
+                bool surv = !(z < thr) && z > -INFINITY;
+                if (surv) {
+                    uint32_t pos = atomicAdd(&n_sh, 1u);
+                    if (pos < ZS_SMALL_CAP) { sval[pos] = z; sidx[pos] = (uint32_t)(sbuf[i] & 0xffffffffull); }
+                }
+            }
+            __syncthreads();
+            uint32_t n = n_sh;
+            __syncthreads();
+            if (n > ZS_SMALL_CAP) {
+                small = false;
+            } else {
+                token = small_path_sample(a, r, P, n, zmax, sval, sidx, sbuf, sq);
+                status |= ZS_ST_SMALL;
+            }
+        }
+        if (!small) mode = ZS_MODE_BIG;
+    }
+    if (t == 0) {
+        st.z_max = zmax;
+        st.has_thr = has_thr;
+        st.thr_key = thr_key;
+        st.mode = mode;
+        st.token = token;
+        st.status = status;
+        st.obs_max = M;
+        st.obs_special = special ? 1u : 0u;
+        st.obs_need = obs_need;
+        st.n_cand = n_cand;
+        for (uint32_t j = 0; j < n_cand; j++) { st.cand_id[j] = cid_sh[j]; st.cand_x[j] = cx_sh[j]; }
+        st.z_is_x = z_is_x;
+        a.rst[r] = st;
+    }
+}
+
+// ===========================================================================
+// zs_k_big: exact emulation of the reference's sequential sums over a full row.
+// ===========================================================================
+struct big_shared {
+    seq_sh<ZS_BIG_NT> q;
+    uint32_t u[4];
+    float s;
+    uint32_t pc0, pc1;
+    uint32_t hist[2048];
+    uint32_t cnt[2048];
+    unsigned long long sortbuf[ZS_SORT_CAP];
+};
+
+struct big_row {
+    const float* row;
+    const uint32_t* allow;
+    bool masked;
+    const uint32_t* pid;
+    const uint32_t* pfl;
+    const float* py;
+    uint32_t np;
+    uint32_t V;
+    float T;
+};
+
+// z for the 4 elements idx0..idx0+3 of group g (patch cursor in sh.pc0/pc1).
+// obs = true: the observers' x~ (mask and bans only); false: the sampler's z.
+__device__ __forceinline__ void big_load(const big_row& R, uint32_t g, float (&z)[4], big_shared& sh, bool obs) {
+    const int t = threadIdx.x;
+    const uint32_t g0 = g * ZS_BIG_G;
+    if (t == 0) {
+        uint32_t p = sh.pc1;  // groups are visited in increasing order within a pass
+        if (g0 == 0) p = 0;
+        while (p < R.np && R.pid[p] < g0) p++;
+        uint32_t q = p;
+        while (q < R.np && R.pid[q] < g0 + ZS_BIG_G) q++;
+        sh.pc0 = p;
+        sh.pc1 = q;
+    }
+    __syncthreads();
+    const uint32_t idx0 = g0 + 4 * t;
+    float4 v = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+    uint32_t w = 0xffffffffu;
+    if (idx0 < R.V) {
+        v = *reinterpret_cast<const float4*>(R.row + idx0);
+        if (R.masked) w = R.allow[idx0 >> 5] >> (idx0 & 31);
+    }
+    z[0] = v.x; z[1] = v.y; z[2] = v.z; z[3] = v.w;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        if (idx0 + q >= R.V) z[q] = -INFINITY;
+        else if (R.masked && !((w >> q) & 1u)) z[q] = -INFINITY;
+    }
+    for (uint32_t p = sh.pc0; p < sh.pc1; p++) {
+        uint32_t off = R.pid[p] - idx0;
+        if (off < 4) {
+            uint32_t fl = R.pfl[p];
+            float nv = z[off];
+            if (fl & ZS_PF_BAN) nv = -INFINITY;
+            if (!obs && (fl & ZS_PF_Y)) nv = R.py[p];
+#pragma unroll
+            for (int q = 0; q < 4; q++) if ((uint32_t)q == off) z[q] = nv;
+        }
+    }
+    if (!obs) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) z[q] = zs_temper(z[q], R.T);
+    }
+    __syncthreads();
+}
+__device__ __forceinline__ void big_load_z(const big_row& R, uint32_t g, float (&z)[4], big_shared& sh) {
+    big_load(R, g, z, sh, false);
+}
+
+__device__ __forceinline__ float big_term_e(float z, bool has_thr, float thr, float m) {
+    if (has_thr && z < thr) return 0.0f;
+    return zs_expf(z - m);
+}
+
+__global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
+    const uint32_t r = blockIdx.x;
+    zs_row_state stt = a.rst[r];
+    const bool run_samp = stt.mode == ZS_MODE_BIG;
+    if (!run_samp && !stt.obs_need) return;
+    __shared__ big_shared sh;
+    const int t = threadIdx.x;
+    const zs_batch& b = a.b;
+    const zs_row_params P = b.d_params[r];
+    big_row R;
+    R.row = b.d_logits + (size_t)r * b.ld;
+    R.masked = (P.flags & ZS_ROW_MASKED) && b.d_allow_bits;
+    R.allow = R.masked ? b.d_allow_bits + (size_t)r * b.allow_words : nullptr;
+    R.pid = a.p_id + (size_t)r * ZS_MAX_PATCHES;
+    R.pfl = a.p_flags + (size_t)r * ZS_MAX_PATCHES;
+    R.py = a.p_y + (size_t)r * ZS_MAX_PATCHES;
+    R.np = a.p_cnt[r];
+    R.V = b.V;
+    R.T = P.temperature;
+    const uint32_t V = b.V;
+    const uint32_t ng = (V + ZS_BIG_G - 1) / ZS_BIG_G;
+    const float m = stt.z_max;
+    if (t == 0) sh.pc1 = 0;
+    __syncthreads();
+
+    // ---- observers: the reference's sequential sums over x~
+    //   sum     = sum exp(l - max)                  hallucination.rs:237-238, logprobs.rs:36
+    //   entropy -= p * ((l - max) - ln(sum)), p > 0 hallucination.rs:242-248
+    float S_obs = -0.0f, H_obs = 0.0f;
+    if (stt.obs_need & ZS_OBS_S) {
+        const float M = stt.obs_max;
+        for (uint32_t g = 0; g < ng; g++) {
+            float x[4], tv[4];
+            big_load(R, g, x, sh, true);
+#pragma unroll
+            for (int q = 0; q < 4; q++) tv[q] = zs_expf(x[q] - M);
+            seq_group<ZS_BIG_NT, 4>(tv, 0, S_obs, NAN, sh.q);
+        }
+        if (stt.obs_need & ZS_OBS_H) {
+            const float inv = 1.0f / S_obs;
+            const float lns = (float)log((double)S_obs);
+            for (uint32_t g = 0; g < ng; g++) {
+                float x[4], tv[4];
+                big_load(R, g, x, sh, true);
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    float d = x[q] - M;
+                    float p = zs_expf(d) * inv;
+                    float tt = d - lns;
+                    tv[q] = p > 0.0f ? -(p * tt) : 0.0f;
+                }
+                seq_group<ZS_BIG_NT, 4>(tv, 0, H_obs, NAN, sh.q);
+            }
+        }
+    }
+    stt.obs_S = S_obs;
+    stt.obs_H = H_obs;
+    if (!run_samp) {
+        if (t == 0) a.rst[r] = stt;
+        return;
+    }
+
+    // ---- top-k threshold by radix select when the candidates could not give it
+    uint32_t has_thr = stt.has_thr;
+    uint32_t thr_key = stt.thr_key;
+    if (has_thr == 2) {
+        uint32_t prefix = 0, mask = 0, need = P.top_k;
+        for (int shift = 24; shift >= 0; shift -= 8) {
+            for (int i = t; i < 256; i += ZS_BIG_NT) sh.hist[i] = 0;
+            __syncthreads();
+            for (uint32_t g = 0; g < ng; g++) {
+                float z[4];
+                big_load_z(R, g, z, sh);
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    if (g * ZS_BIG_G + 4 * t + q >= V) continue;
+                    uint32_t k = zs_total_key(z[q]);
+                    if ((k & mask) == prefix) atomicAdd(&sh.hist[(k >> shift) & 255u], 1u);
+                }
+            }
+            __syncthreads();
+            if (t < 64) {
+                uint32_t c[4], loc = 0;
+                for (int q = 0; q < 4; q++) { c[q] = sh.hist[255 - 4 * t - q]; loc += c[q]; }
+                uint32_t inc = wave_incl_scan_u(loc);
+                uint32_t before = inc - loc;
+                for (int q = 0; q < 4; q++) {
+                    if (before < need && need <= before + c[q]) { sh.u[0] = 255 - 4 * t - q; sh.u[1] = need - before; }
+                    before += c[q];
+                }
+            }
+            __syncthreads();
+            prefix |= sh.u[0] << shift;
+            mask |= 0xffu << shift;
+            need = sh.u[1];
+            __syncthreads();
+        }
+        thr_key = prefix;
+        has_thr = 1;
+    }
+    const bool use_thr = has_thr != 0;
+    const float thr = zs_key_to_float(thr_key);
+
+    // ---- S = sum exp(z - m) in index order (sampler.rs:67-68); identical to the
+    // observers' sum when z == x~ and no top-k cut applies
+    float S = -0.0f;
+    const bool reuse = stt.z_is_x && !use_thr && (stt.obs_need & ZS_OBS_S);
+    if (reuse) S = S_obs;
+    for (uint32_t g = 0; g < (reuse ? 0u : ng); g++) {
+        float z[4], tv[4];
+        big_load_z(R, g, z, sh);
+#pragma unroll
+        for (int q = 0; q < 4; q++) tv[q] = big_term_e(z[q], use_thr, thr, m);
+        seq_group<ZS_BIG_NT, 4>(tv, 0, S, NAN, sh.q);
+    }
+
+    // ---- min-p (sampler.rs:72-88)
+    const bool minp = P.min_p > 0.0f;
+    float cut = 0.0f, kept = 0.0f;
+    if (minp) {
+        float pmax = 1.0f / S;  // the max element has exp(0) = 1
+        cut = P.min_p * pmax;
+        for (uint32_t g = 0; g < ng; g++) {
+            float z[4], tv[4];
+            big_load_z(R, g, z, sh);
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                float p = big_term_e(z[q], use_thr, thr, m) / S;
+                tv[q] = (p < cut) ? 0.0f : p;
+            }
+            seq_group<ZS_BIG_NT, 4>(tv, 0, kept, NAN, sh.q);
+        }
+    }
+    auto p1_of = [&](float z) -> float {
+        float p = big_term_e(z, use_thr, thr, m) / S;
+        if (minp) {
+            if (p < cut) p = 0.0f;
+            else if (kept > 0.0f) p = p / kept;
+        }
+        return p;
+    };
+
+    // ---- top-p (sampler.rs:91-115)
+    const bool topp = P.top_p < 1.0f && P.top_p > 0.0f;
+    uint32_t vstar = 0, istar = 0xffffffffu;  // kept: p1 > v* or (p1 == v* and idx <= i*)
+    float sum2 = 0.0f;
+    bool stopped = false;
+    if (topp) {
+        uint32_t* pairs = a.pairs + (size_t)r * a.max_vocab * 2;
+        for (int i = t; i < 2048; i += ZS_BIG_NT) sh.hist[i] = 0;
+        __syncthreads();
+        for (uint32_t g = 0; g < ng; g++) {
+            float z[4];
+            big_load_z(R, g, z, sh);
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                float p = p1_of(z[q]);
+                if (p > 0.0f) atomicAdd(&sh.hist[min(zs_f2u(p) >> 19, 2047u)], 1u);
+            }
+        }
+        __syncthreads();
+        // offsets in descending bucket order, and the first candidate range:
+        // buckets whose guaranteed mass reaches 1.02 * top_p
+        if (t == 0) {
+            uint32_t off = 0;
+            double lb = 0.0;
+            int blo = 0;
+            bool found = false;
+            for (int bk = 2047; bk >= 0; bk--) {
+                uint32_t n = sh.hist[bk];
+                sh.cnt[bk] = n;
+                sh.hist[bk] = off;  // becomes the bucket start
+                off += n;
+                lb += (double)n * (double)zs_u2f((uint32_t)bk << 19);
+                if (!found && lb >= 1.02 * (double)P.top_p) { blo = bk; found = true; }
+            }
+            sh.u[0] = (uint32_t)blo;
+        }
+        __syncthreads();
+        int blo = (int)sh.u[0];
+        int bhi = 2047;
+        float s = 0.0f, s_bstart = 0.0f;
+        uint32_t pos = 0;
+        for (int round = 0; round < 2 && !stopped; round++) {
+            // gather buckets [blo, bhi] into their slots
+            for (int i = t; i < 2048; i += ZS_BIG_NT) {
+                // cursor = bucket start (kept in hist); use the upper half of sortbuf as cursors
+                reinterpret_cast<uint32_t*>(sh.sortbuf)[i] = sh.hist[i];
+            }
+            __syncthreads();
+            uint32_t* cursor = reinterpret_cast<uint32_t*>(sh.sortbuf);
+            for (uint32_t g = 0; g < ng; g++) {
+                float z[4];
+                big_load_z(R, g, z, sh);
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    float p = p1_of(z[q]);
+                    if (p > 0.0f) {
+                        int bk = (int)min(zs_f2u(p) >> 19, 2047u);
+                        if (bk >= blo && bk <= bhi) {
+                            uint32_t ps = atomicAdd(&cursor[bk], 1u);
+                            pairs[2 * ps] = zs_f2u(p);
+                            pairs[2 * ps + 1] = g * ZS_BIG_G + 4 * t + q;
+                        }
+                    }
+                }
+            }
+            __syncthreads();
+            __threadfence_block();
+            const uint32_t nend = sh.hist[blo] + sh.cnt[blo];
+            // walk pos .. nend in bucket-major order
+            while (pos < nend && !stopped) {
+                float tv[4];
+                uint32_t bits[4];
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    uint32_t ps = pos + 4 * t + q;
+                    bits[q] = ps < nend ? pairs[2 * ps] : 0u;
+                    tv[q] = zs_u2f(bits[q]);
+                }
+                uint32_t excl[4];
+                seq_find_res F = seq_find<ZS_BIG_NT, 4>(tv, 0, s, P.top_p, excl, sh.q);
+                int first = min(F.ev, F.st);
+                // bucket open at the end of this group, and its start
+                uint32_t last = min(pos + ZS_BIG_G, nend) - 1;
+                if (first == ZS_BIGI) {
+                    uint32_t bl = min(pairs[2 * last] >> 19, 2047u);
+                    uint32_t bst = sh.hist[bl];
+                    if (bst >= pos) s_bstart = seq_value_at<ZS_BIG_NT, 4>(F, excl, (int)(bst - pos), sh.q);
+                    s = zs_grid_value(F.k0 + F.total, F.eg);
+                    pos += ZS_BIG_G;
+                    continue;
+                }
+                // an event or the stop lies in bucket bk: restart that bucket in
+                // exact (p desc, idx asc) order from the sum at its start
+                uint32_t bk = min(pairs[2 * min(pos + (uint32_t)first, nend - 1)] >> 19, 2047u);
+                uint32_t bst = sh.hist[bk], bn = sh.cnt[bk];
+                if (bst >= pos) s = seq_value_at<ZS_BIG_NT, 4>(F, excl, (int)(bst - pos), sh.q);
+                else s = s_bstart;
+                if (bn > ZS_SORT_CAP) {
+                    // not handled on chip: flag the row (the token stays invalid);
+                    // every thread takes this branch (bn is uniform)
+                    stt.status |= ZS_ST_FALLBACK;
+                    stopped = true;
+                    vstar = 0; istar = 0xffffffffu;
+                    break;
+                }
+                uint32_t np2 = 1;
+                while (np2 < bn) np2 <<= 1;
+                for (uint32_t i = t; i < np2; i += ZS_BIG_NT) {
+                    unsigned long long v = ~0ull;
+                    if (i < bn) v = ((unsigned long long)(~pairs[2 * (bst + i)]) << 32) | pairs[2 * (bst + i) + 1];
+                    sh.sortbuf[i] = v;
+                }
+                __syncthreads();
+                if (np2 > 1) block_bitonic_u64<ZS_BIG_NT>(sh.sortbuf, (int)np2);
+                for (uint32_t q0 = 0; q0 < bn && !stopped; q0 += ZS_BIG_G) {
+                    float tv2[4];
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        uint32_t i = q0 + 4 * t + q;
+                        tv2[q] = i < bn ? zs_u2f(~(uint32_t)(sh.sortbuf[i] >> 32)) : 0.0f;
+                    }
+                    int stp = seq_group<ZS_BIG_NT, 4>(tv2, 0, s, P.top_p, sh.q);
+                    if (stp >= 0) {
+                        unsigned long long v = sh.sortbuf[q0 + stp];
+                        vstar = ~(uint32_t)(v >> 32);
+                        istar = (uint32_t)(v & 0xffffffffull);
+                        stopped = true;
+                    }
+                }
+                __syncthreads();
+                s_bstart = s;
+                pos = bst + bn;
+            }
+            // extend to every remaining bucket once
+            if (!stopped) {
+                if (blo == 0) break;
+                bhi = blo - 1;
+                blo = 0;
+            }
+        }
+        if (!stopped) { vstar = 0; istar = 0xffffffffu; }  // every positive p kept
+        // ---- sum over the kept set in index order (sampler.rs:107)
+        sum2 = -0.0f;
+        for (uint32_t g = 0; g < ng; g++) {
+            float z[4], tv[4];
+            big_load_z(R, g, z, sh);
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                float p = p1_of(z[q]);
+                uint32_t pb = zs_f2u(p), idx = g * ZS_BIG_G + 4 * t + q;
+                bool keep = pb > vstar || (pb == vstar && idx <= istar);
+                tv[q] = keep ? p : 0.0f;
+            }
+            seq_group<ZS_BIG_NT, 4>(tv, 0, sum2, NAN, sh.q);
+        }
+    }
+    // ---- draw (sampler.rs:118-127)
+    const float rr = zs_philox_uniform(b.d_seed[r], b.d_counter[r], 0u);
+    uint32_t token = V - 1;
+    if (!(stt.status & ZS_ST_FALLBACK)) {
+        if (rr <= 0.0f) {
+            token = 0;
+        } else {
+            float cum = 0.0f;
+            const bool renorm = topp && sum2 > 0.0f;
+            for (uint32_t g = 0; g < ng; g++) {
+                float z[4], tv[4];
+                big_load_z(R, g, z, sh);
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    float p = p1_of(z[q]);
+                    if (renorm) {
+                        uint32_t pb = zs_f2u(p), idx = g * ZS_BIG_G + 4 * t + q;
+                        bool keep = pb > vstar || (pb == vstar && idx <= istar);
+                        p = keep ? p / sum2 : 0.0f;
+                    }
+                    tv[q] = p;
+                }
+                int stp = seq_group<ZS_BIG_NT, 4>(tv, 0, cum, rr, sh.q);
+                if (stp >= 0) { token = g * ZS_BIG_G + stp; break; }
+            }
+        }
+    } else {
+        token = 0xffffffffu;
+    }
+    if (t == 0) {
+        stt.token = token;
+        stt.mode = ZS_MODE_DONE;
+        a.rst[r] = stt;
+    }
+}
+
+// ===========================================================================
+// zs_k_final: per-row outputs (logprobs.rs:34-54, hallucination.rs:232-257)
+// ===========================================================================
+__global__ void zs_k_final(zs_sargs a) {
+    const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
+    const zs_batch& b = a.b;
+    if (r >= b.B) return;
+    const zs_row_state& st = a.rst[r];
+    const uint32_t tok = st.token;
+    uint32_t status = st.status;
+    b.d_token[r] = tok;
+    const zs_row_params P = b.d_params[r];
+    const bool want_lp = (P.flags & ZS_ROW_LOGPROBS) != 0;
+    const bool want_unc = (P.flags & ZS_ROW_UNCERTAINTY) != 0;
+    b.d_top_n[r] = 0;
+    b.d_logprob[r] = NAN;
+    b.d_entropy[r] = NAN;
+    b.d_max_prob[r] = NAN;
+    b.d_margin[r] = NAN;
+    b.d_chosen_lp[r] = NAN;
+    if (status & ZS_ST_LIMIT) {
+        b.d_status[r] = status;
+        return;
+    }
+    // x~ of the chosen token
+    float xc = -INFINITY;
+    const bool in_range = tok < b.V;
+    if (in_range) {
+        xc = b.d_logits[(size_t)r * b.ld + tok];
+        if ((P.flags & ZS_ROW_MASKED) && b.d_allow_bits && !zs_allowed_bit(b, r, tok)) xc = -INFINITY;
+        const uint32_t* pid = a.p_id + (size_t)r * ZS_MAX_PATCHES;
+        uint32_t lo = 0, hi = a.p_cnt[r];
+        while (lo < hi) { uint32_t mid = (lo + hi) >> 1; if (pid[mid] < tok) lo = mid + 1; else hi = mid; }
+        if (lo < a.p_cnt[r] && pid[lo] == tok && (a.p_flags[(size_t)r * ZS_MAX_PATCHES + lo] & ZS_PF_BAN))
+            xc = -INFINITY;
+    }
+    const float M = st.obs_max;
+    if (want_lp) {
+        uint32_t ntl = P.top_logprobs > 20 ? 20 : P.top_logprobs;
+        if (ntl > b.top_stride) ntl = b.top_stride;
+        uint32_t* tid = b.d_top_ids + (size_t)r * b.top_stride;
+        float* tlp = b.d_top_lps + (size_t)r * b.top_stride;
+        if (st.obs_special) {
+            // lse is NaN: every lp is NaN and partition_point(x >= NaN) == 0 inserts
+            // each entry first, leaving ids n-1 .. 0 (logprobs.rs:41-51)
+            uint32_t n = ntl < b.V ? ntl : b.V;
+            for (uint32_t j = 0; j < n; j++) { tid[j] = n - 1 - j; tlp[j] = NAN; }
+            b.d_top_n[r] = n;
+            b.d_logprob[r] = in_range ? NAN : -INFINITY;
+        } else {
+            const float lse = M + (float)log((double)st.obs_S);  // logprobs.rs:36
+            b.d_logprob[r] = in_range ? xc - lse : -INFINITY;
+            uint32_t nc = st.n_cand;
+            uint32_t ids[ZS_OBS_CAND];
+            float xs[ZS_OBS_CAND], lps[ZS_OBS_CAND];
+            for (uint32_t j = 0; j < nc; j++) { ids[j] = st.cand_id[j]; xs[j] = st.cand_x[j]; lps[j] = xs[j] - lse; }
+            // candidates arrive by (x~ desc, id asc); equal lp values keep id order
+            for (uint32_t j = 1; j < nc; j++) {
+                uint32_t id = ids[j];
+                float lp = lps[j], xv = xs[j];
+                int k = (int)j - 1;
+                while (k >= 0 && (lps[k] < lp || (lps[k] == lp && ids[k] > id))) {
+                    ids[k + 1] = ids[k]; lps[k + 1] = lps[k]; xs[k + 1] = xs[k];
+                    k--;
+                }
+                ids[k + 1] = id; lps[k + 1] = lp; xs[k + 1] = xv;
+            }
+            // the order must not hinge on the last bit of lse (its logf may differ
+            // from glibc's by one ulp)
+            float lo = nextafterf(lse, -INFINITY), hi = nextafterf(lse, INFINITY);
+            uint32_t lim = nc < ntl + 1 ? nc : ntl + 1;
+            for (uint32_t j = 0; j + 1 < lim; j++) {
+                bool e0 = (xs[j] - lse) == (xs[j + 1] - lse);
+                bool e1 = (xs[j] - lo) == (xs[j + 1] - lo);
+                bool e2 = (xs[j] - hi) == (xs[j + 1] - hi);
+                if (e0 != e1 || e0 != e2) status |= ZS_ST_TOPLP_AMBIG;
+            }
+            uint32_t n = ntl < nc ? ntl : nc;
+            for (uint32_t j = 0; j < n; j++) { tid[j] = ids[j]; tlp[j] = lps[j]; }
+            b.d_top_n[r] = n;
+        }
+    }
+    if (want_unc) {
+        if (st.obs_special) {
+            // sum is NaN: no p > 0, top1 stays -inf (hallucination.rs:243-256)
+            b.d_entropy[r] = 0.0f;
+            b.d_max_prob[r] = 0.0f;
+            b.d_margin[r] = 0.0f;
+            b.d_chosen_lp[r] = -INFINITY;
+        } else {
+            const float inv = 1.0f / st.obs_S;
+            const float top1 = inv;  // the max element has exp(0) = 1
+            float top2 = -INFINITY;
+            if (st.n_cand >= 2) top2 = zs_expf(st.cand_x[1] - M) * inv;
+            b.d_entropy[r] = fmaxf(st.obs_H, 0.0f);
+            b.d_max_prob[r] = fmaxf(top1, 0.0f);
+            b.d_margin[r] = fmaxf(top1 - top2, 0.0f);
+            float pc = in_range ? zs_expf(xc - M) * inv : 0.0f;
+            b.d_chosen_lp[r] = pc > 0.0f ? (float)log((double)pc) : -INFINITY;
+        }
+    }
+    b.d_status[r] = status;
+}
+
+// ===========================================================================
+// host launcher
+// ===========================================================================
+extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t stream) {
+    zs_sargs a;
+    a.b = *bt;
+    a.p_cnt = ctx->p_cnt;
+    a.p_id = ctx->p_id;
+    a.p_flags = ctx->p_flags;
+    a.p_y = ctx->p_y;
+    a.cst = ctx->cst;
+    a.cs_key = ctx->cs_key;
+    a.cs_idx = ctx->cs_idx;
+    a.co_key = ctx->co_key;
+    a.co_idx = ctx->co_idx;
+    a.rst = ctx->rst;
+    a.pairs = ctx->pairs;
+    a.nch = ctx->max_chunks;
+    a.max_vocab = ctx->max_vocab;
+    const uint32_t B = bt->B;
+    const uint32_t nch = (bt->V + ZS_P1_CH - 1) / ZS_P1_CH;
+    hipLaunchKernelGGL(zs_k_prep, dim3(B), dim3(ZS_PREP_NT), 0, stream, a);
+    hipLaunchKernelGGL(zs_k_pass1, dim3(nch, B), dim3(ZS_P1_NT), 0, stream, a);
+    hipLaunchKernelGGL(zs_k_combine, dim3(B), dim3(CB_NT), 0, stream, a);
+    hipLaunchKernelGGL(zs_k_big, dim3(B), dim3(ZS_BIG_NT), 0, stream, a);
+    hipLaunchKernelGGL(zs_k_final, dim3((B + 63) / 64), dim3(64), 0, stream, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return zs_set_error(ctx, ZS_EHIP, "zs_sample launch: %s", hipGetErrorString(e));
+    return ZS_OK;
+}

@@ -1,0 +1,362 @@
+"""Host-side mirror of the reference engine interface over libzs.
+
+Names follow src/engine/: SamplerConfig (sampler.rs:3-22), PenaltyConfig and
+DecodeControl (decode_ctrl.rs:21-153), TokenByteTable / LogitFSM
+(logit_fsm.rs:33-323). The batched entry point `sample_batch` replaces the
+per-request `apply_mask -> sample_token -> observe` sequence of
+rest.rs:2594-2624 for B rows at once on the GPU.
+
+torch is used only for device memory and the stream; every computation runs
+in libzs's HIP kernels.
+"""
+import ctypes as C
+from dataclasses import dataclass, field
+from typing import Dict, List, Optional, Sequence, Tuple
+
+import numpy as np
+import torch
+
+from ._lib import (Batch, RowParams, ZS_OK, ZS_ROW_LOGPROBS, ZS_ROW_MASKED, ZS_ROW_UNCERTAINTY, ZsError, lib)
+
+OPENAI_TOP_LOGPROBS_CAP = 20  # logprobs.rs:27-29
+
+
+def _check(ctx_handle, rc, what):
+    if rc != ZS_OK:
+        msg = lib().zs_last_error(ctx_handle)
+        raise ZsError(f"{what} failed ({rc}): {msg.decode() if msg else ''}")
+
+
+class Context:
+    """One libzs context (device scratch sized for max_rows x max_vocab)."""
+
+    def __init__(self, device: int = 0, max_rows: int = 256, max_vocab: int = 151936):
+        self.device = device
+        self.max_rows = max_rows
+        self.max_vocab = max_vocab
+        h = C.c_void_p()
+        rc = lib().zs_ctx_create(device, max_rows, max_vocab, C.byref(h))
+        if rc != ZS_OK:
+            raise ZsError(f"zs_ctx_create failed ({rc})")
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().zs_ctx_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+@dataclass
+class SamplerConfig:
+    """sampler.rs:3-22 (defaults as there)."""
+    temperature: float = 1.0
+    top_k: int = 50
+    top_p: float = 0.9
+    min_p: float = 0.0
+
+
+@dataclass
+class PenaltyConfig:
+    """decode_ctrl.rs:21-43."""
+    repeat: float = 1.0
+    presence: float = 0.0
+    frequency: float = 0.0
+
+    def is_active(self) -> bool:
+        return self.repeat != 1.0 or self.presence != 0.0 or self.frequency != 0.0
+
+
+class DecodeControl:
+    """decode_ctrl.rs:45-153: penalties, logit_bias, the per-request RNG and the
+    count map. The RNG is Philox4x32-10 keyed by `seed` with a per-step counter
+    (the reference uses StdRng)."""
+
+    def __init__(self, penalties: Optional[PenaltyConfig] = None, logit_bias: Sequence[Tuple[int, float]] = (),
+                 seed: Optional[int] = None):
+        self.penalties = penalties or PenaltyConfig()
+        self.logit_bias = [(int(t), float(b)) for t, b in logit_bias]
+        self.counts: Dict[int, int] = {}
+        self.seed = 0 if seed is None else int(seed) & (2**64 - 1)
+        self.counter = 0
+
+    def observe_prompt_tail(self, prompt: Sequence[int], last_n: int):  # decode_ctrl.rs:90-97
+        if not self.penalties.is_active():
+            return
+        for t in list(prompt)[::-1][:last_n]:
+            self.counts[int(t)] = self.counts.get(int(t), 0) + 1
+
+    def modifies_logits(self) -> bool:  # decode_ctrl.rs:102-104
+        return self.penalties.is_active() or bool(self.logit_bias)
+
+    def observe(self, token: int):  # decode_ctrl.rs:149-153
+        if self.penalties.is_active():
+            self.counts[int(token)] = self.counts.get(int(token), 0) + 1
+
+
+class TokenByteTable:
+    """logit_fsm.rs:43-46: per-token surface bytes (None = never allowed under a
+    grammar) and the EOS id, uploaded once per model."""
+
+    def __init__(self, ctx: Context, tokens: Sequence[Optional[bytes]], eos: int):
+        self.ctx = ctx
+        self.ntab = len(tokens)
+        self.eos = int(eos)
+        offs = np.zeros(self.ntab + 1, np.uint32)
+        valid = np.zeros(max(self.ntab, 1), np.uint8)
+        buf = bytearray()
+        for i, t in enumerate(tokens):
+            if t is not None:
+                valid[i] = 1
+                buf += t
+            offs[i + 1] = len(buf)
+        data = np.frombuffer(bytes(buf) or b"\0", np.uint8).copy()
+        h = C.c_void_p()
+        rc = lib().zs_vocab_create(ctx.h, offs.ctypes.data, data.ctypes.data, valid.ctypes.data, self.ntab,
+                                   self.eos, C.byref(h))
+        _check(ctx.h, rc, "zs_vocab_create")
+        self.h = h
+
+    @classmethod
+    def from_csr(cls, ctx, offsets, data, valid, eos):
+        obj = cls.__new__(cls)
+        obj.ctx = ctx
+        obj.ntab = len(offsets) - 1
+        obj.eos = int(eos)
+        offs = np.ascontiguousarray(offsets, np.uint32)
+        data = np.ascontiguousarray(data, np.uint8)
+        if data.size == 0:
+            data = np.zeros(1, np.uint8)
+        valid = np.ascontiguousarray(valid, np.uint8)
+        h = C.c_void_p()
+        rc = lib().zs_vocab_create(ctx.h, offs.ctypes.data, data.ctypes.data, valid.ctypes.data, obj.ntab,
+                                   obj.eos, C.byref(h))
+        _check(ctx.h, rc, "zs_vocab_create")
+        obj.h = h
+        return obj
+
+    def __del__(self):
+        try:
+            if self.h:
+                lib().zs_vocab_destroy(self.h)
+        except Exception:
+            pass
+
+
+class ByteDfa:
+    """A built anchored byte DFA (the table regex-automata would produce):
+    trans[S,256], dead/quit flags, accept = is_match(next_eoi_state(s))."""
+
+    def __init__(self, ctx: Context, trans, dead, accept):
+        self.ctx = ctx
+        trans = np.ascontiguousarray(trans, np.uint32).reshape(-1)
+        self.nstates = trans.size // 256
+        dead = np.ascontiguousarray(dead, np.uint8)
+        accept = np.ascontiguousarray(accept, np.uint8)
+        h = C.c_void_p()
+        rc = lib().zs_dfa_create(ctx.h, trans.ctypes.data, self.nstates, dead.ctypes.data, accept.ctypes.data,
+                                 C.byref(h))
+        _check(ctx.h, rc, "zs_dfa_create")
+        self.h = h
+
+    def is_live(self, s: int) -> bool:
+        return bool(lib().zs_dfa_is_live(self.h, s))
+
+    def is_accept(self, s: int) -> bool:
+        return bool(lib().zs_dfa_is_accept(self.h, s))
+
+    def advance(self, table: TokenByteTable, state: int, token: int) -> Tuple[int, bool]:
+        out = C.c_uint32()
+        viable = C.c_int()
+        rc = lib().zs_dfa_advance(self.h, table.h, state, token, C.byref(out), C.byref(viable))
+        _check(self.ctx.h, rc, "zs_dfa_advance")
+        return int(out.value), bool(viable.value)
+
+    def mask(self, table: TokenByteTable, states: torch.Tensor, V: int, out: Optional[torch.Tensor] = None,
+             any_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Allow bitsets for rows at `states` (int32 device tensor, -1 = free)."""
+        B = states.numel()
+        words = (V + 31) // 32
+        if out is None:
+            out = torch.empty((B, words), dtype=torch.int32, device=states.device)
+        stream = torch.cuda.current_stream(states.device).cuda_stream
+        rc = lib().zs_dfa_mask(self.ctx.h, self.h, table.h, states.data_ptr(), B, V, out.data_ptr(),
+                               any_out.data_ptr() if any_out is not None else None, stream)
+        _check(self.ctx.h, rc, "zs_dfa_mask")
+        return out
+
+    def __del__(self):
+        try:
+            if self.h:
+                lib().zs_dfa_destroy(self.h)
+        except Exception:
+            pass
+
+
+class LogitFSM:
+    """logit_fsm.rs:33-37: either a `ban:` list or a byte-DFA constraint with
+    its current state. Regex / JSON-schema compilation to a DFA is not part of
+    this build; pass the built DFA."""
+
+    def __init__(self, banned: Sequence[int] = (), dfa: Optional[ByteDfa] = None,
+                 table: Optional[TokenByteTable] = None, state: int = 0):
+        self.banned = [int(b) for b in banned]
+        self.dfa = dfa
+        self.table = table
+        self.state = state
+
+    @classmethod
+    def compile(cls, grammar: str, table: Optional[TokenByteTable] = None):  # logit_fsm.rs:190-228
+        g = grammar.strip()
+        if g.startswith("ban:"):
+            banned = []
+            for piece in g[4:].split(","):
+                piece = piece.strip()
+                if piece.isdigit() and int(piece) < 2**32:
+                    banned.append(int(piece))
+            return cls(banned=banned)
+        if g == "":
+            return cls()
+        for mode in ("regex", "json_schema", "json", "bnf"):
+            if g.startswith(mode + ":"):
+                raise NotImplementedError(f"grammar mode {mode!r} needs a compiled DFA: use LogitFSM(dfa=...)")
+        raise ValueError('grammar mode "unknown" is not implemented yet; supported: "ban:<id>,<id>,...", '
+                         '"regex:<pattern>", "json_schema:<schema>", "json:"')
+
+    def is_active(self) -> bool:  # logit_fsm.rs:299-301
+        return bool(self.banned) or self.dfa is not None
+
+    def advance(self, token: int):  # logit_fsm.rs:275-290
+        if self.dfa is not None:
+            self.state, _ = self.dfa.advance(self.table, self.state, token)
+
+
+@dataclass
+class RowRequest:
+    """One row of a batched step: sampler knobs + per-request state."""
+    config: SamplerConfig = field(default_factory=SamplerConfig)
+    ctrl: DecodeControl = field(default_factory=DecodeControl)
+    fsm: Optional[LogitFSM] = None
+    top_logprobs: int = 0
+    masked: bool = False  # apply the row's allow bitset (set automatically for a DFA constraint)
+    logprobs: bool = False              # OpenAI `logprobs` (LogprobsCollector, logprobs.rs)
+    detect_hallucination: bool = False  # token_uncertainty (hallucination.rs)
+
+
+class StepOutput:
+    def __init__(self, **kw):
+        self.__dict__.update(kw)
+
+
+class BatchSampler:
+    """Packs B requests into the zs_batch layout and runs zs_sample."""
+
+    def __init__(self, ctx: Context, device="cuda"):
+        self.ctx = ctx
+        self.device = torch.device(device)
+
+    @staticmethod
+    def _csr(lists, dtype):
+        off = np.zeros(len(lists) + 1, np.uint32)
+        for i, l in enumerate(lists):
+            off[i + 1] = off[i] + len(l)
+        flat = np.concatenate([np.asarray(l, dtype) for l in lists]) if off[-1] else np.zeros(1, dtype)
+        return off, flat
+
+    def pack(self, logits: torch.Tensor, rows: List[RowRequest], allow_bits: Optional[torch.Tensor] = None):
+        B, V = logits.shape
+        dev = logits.device
+        params = (RowParams * B)()
+        cnt_ids, cnt_vals, bias_ids, bias_vals, bans = [], [], [], [], []
+        seeds = np.zeros(B, np.uint64)
+        counters = np.zeros(B, np.uint64)
+        for i, rq in enumerate(rows):
+            c, p = rq.config, rq.ctrl.penalties
+            masked = rq.masked or (rq.fsm is not None and rq.fsm.dfa is not None)
+            flags = (ZS_ROW_MASKED if masked else 0) | (ZS_ROW_LOGPROBS if (rq.logprobs or rq.top_logprobs) else 0) \
+                | (ZS_ROW_UNCERTAINTY if rq.detect_hallucination else 0)
+            params[i] = RowParams(c.temperature, c.top_k, c.top_p, c.min_p, p.repeat, p.presence, p.frequency,
+                                  min(rq.top_logprobs, OPENAI_TOP_LOGPROBS_CAP), flags, 0)
+            items = list(rq.ctrl.counts.items()) if p.is_active() else []
+            cnt_ids.append([t for t, _ in items])
+            cnt_vals.append([n for _, n in items])
+            bias_ids.append([t for t, _ in rq.ctrl.logit_bias])
+            bias_vals.append([b for _, b in rq.ctrl.logit_bias])
+            bans.append(rq.fsm.banned if rq.fsm is not None else [])
+            seeds[i] = rq.ctrl.seed
+            counters[i] = rq.ctrl.counter
+        t = lambda a, dt: torch.from_numpy(np.ascontiguousarray(a)).to(dev, dtype=dt) if a is not None else None
+        co, ci = self._csr(cnt_ids, np.uint32)
+        _, cv = self._csr(cnt_vals, np.uint32)
+        bo, bi = self._csr(bias_ids, np.uint32)
+        _, bv = self._csr(bias_vals, np.float32)
+        no, ni = self._csr(bans, np.uint32)
+        bufs = dict(
+            params=torch.frombuffer(bytearray(params), dtype=torch.uint8).to(dev),
+            cnt_off=t(co.view(np.int32), torch.int32), cnt_ids=t(ci.view(np.int32), torch.int32),
+            cnt_vals=t(cv.view(np.int32), torch.int32),
+            bias_off=t(bo.view(np.int32), torch.int32), bias_ids=t(bi.view(np.int32), torch.int32),
+            bias_vals=t(bv, torch.float32),
+            ban_off=t(no.view(np.int32), torch.int32), ban_ids=t(ni.view(np.int32), torch.int32),
+            seed=t(seeds.view(np.int64), torch.int64), counter=t(counters.view(np.int64), torch.int64),
+        )
+        return bufs
+
+    def run(self, logits: torch.Tensor, bufs: dict, allow_bits: Optional[torch.Tensor] = None,
+            top_stride: int = OPENAI_TOP_LOGPROBS_CAP, out: Optional[dict] = None):
+        B, V = logits.shape
+        dev = logits.device
+        assert logits.dtype == torch.float32 and logits.stride(1) == 1
+        if out is None:
+            out = dict(
+                token=torch.empty(B, dtype=torch.int32, device=dev),
+                logprob=torch.empty(B, dtype=torch.float32, device=dev),
+                top_ids=torch.zeros((B, top_stride), dtype=torch.int32, device=dev),
+                top_lps=torch.zeros((B, top_stride), dtype=torch.float32, device=dev),
+                top_n=torch.empty(B, dtype=torch.int32, device=dev),
+                entropy=torch.empty(B, dtype=torch.float32, device=dev),
+                max_prob=torch.empty(B, dtype=torch.float32, device=dev),
+                margin=torch.empty(B, dtype=torch.float32, device=dev),
+                chosen_lp=torch.empty(B, dtype=torch.float32, device=dev),
+                status=torch.empty(B, dtype=torch.int32, device=dev),
+            )
+        b = Batch()
+        b.B, b.V, b.ld = B, V, logits.stride(0)
+        b.d_logits = logits.data_ptr()
+        b.d_params = bufs["params"].data_ptr()
+        b.d_cnt_off, b.d_cnt_ids, b.d_cnt_vals = bufs["cnt_off"].data_ptr(), bufs["cnt_ids"].data_ptr(), \
+            bufs["cnt_vals"].data_ptr()
+        b.d_bias_off, b.d_bias_ids, b.d_bias_vals = bufs["bias_off"].data_ptr(), bufs["bias_ids"].data_ptr(), \
+            bufs["bias_vals"].data_ptr()
+        b.d_ban_off, b.d_ban_ids = bufs["ban_off"].data_ptr(), bufs["ban_ids"].data_ptr()
+        if allow_bits is not None:
+            b.d_allow_bits = allow_bits.data_ptr()
+            b.allow_words = allow_bits.shape[1]
+        b.top_stride = top_stride
+        b.d_seed, b.d_counter = bufs["seed"].data_ptr(), bufs["counter"].data_ptr()
+        for k in ("token", "logprob", "top_ids", "top_lps", "top_n", "entropy", "max_prob", "margin", "chosen_lp",
+                  "status"):
+            setattr(b, "d_" + k, out[k].data_ptr())
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        rc = lib().zs_sample(self.ctx.h, C.byref(b), stream)
+        _check(self.ctx.h, rc, "zs_sample")
+        return out
+
+    def step(self, logits: torch.Tensor, rows: List[RowRequest], allow_bits: Optional[torch.Tensor] = None):
+        """One decode step for every row; advances each row's RNG counter, count
+        map and FSM state with the sampled token (rest.rs:2594-2624)."""
+        bufs = self.pack(logits, rows, allow_bits)
+        out = self.run(logits, bufs, allow_bits)
+        torch.cuda.current_stream(logits.device).synchronize()
+        toks = out["token"].cpu().numpy().view(np.uint32)
+        for rq, tok in zip(rows, toks):
+            rq.ctrl.counter += 1
+            if rq.fsm is not None:
+                rq.fsm.advance(int(tok))
+            rq.ctrl.observe(int(tok))
+        return out
