@@ -163,6 +163,57 @@ typedef struct zs_batch {
 
 int zs_sample(zs_ctx* ctx, const zs_batch* batch, void* stream);
 
+/* ---- speculative decoding ------------------------------------------------
+ * Verification of k draft tokens per row (k <= ZS_SPEC_KMAX). temperature <= 0
+ * (or d_draft == NULL) is greedy verification exactly as verify_drafts
+ * (spec_decode.rs:241-279): d_accepted = accepted drafts, d_next = the bonus /
+ * corrected token. temperature > 0 is rejection sampling against the draft
+ * distributions (the reference has none, rest.rs:2639); probabilities are
+ * exact integer weights rint(expf(z - max) * 2^24), uniforms are Philox words
+ * of (seed, counter, tag) -- tag 1+i for the test of draft i, 1+k+i for the
+ * replacement draw at a rejection at i, 1+2k for the bonus draw. */
+#define ZS_SPEC_KMAX 16
+typedef struct zs_spec_batch {
+    uint32_t B, V, k;
+    uint64_t ld;
+    const float* d_target;          /* [B][k+1][ld] target logits per position */
+    const float* d_draft;           /* [B][k][ld] draft logits, or NULL */
+    const uint32_t* d_draft_ids;    /* [B][k] */
+    const float* d_temperature;     /* [B] */
+    const uint64_t* d_seed;         /* [B] */
+    const uint64_t* d_counter;      /* [B] */
+    uint32_t* d_accepted;           /* [B] */
+    uint32_t* d_next;               /* [B] */
+} zs_spec_batch;
+int zs_spec_verify(zs_ctx* ctx, const zs_spec_batch* batch, void* stream);
+
+/* ---- batched lane (continuous batching, gpu/batch.rs:176-192) --------------
+ * Device-side versions of the WGSL sampling kernels with their exact
+ * semantics: BARGMAX (shaders.rs:761-789), BSAMPLE Gumbel-max (:796-850; WGSL
+ * `log` fixed as the correctly rounded f32 log), BTOPK (:859-905, K <= 1024),
+ * and sample_topk over the top-K pool (gpu/sampling.rs:35-56) so the lane needs
+ * no readback of candidate pools. */
+int zs_lane_argmax(zs_ctx* ctx, const float* d_logits, uint32_t B, uint32_t V, uint64_t ld, uint32_t* d_out,
+                   void* stream);
+int zs_lane_sample(zs_ctx* ctx, const float* d_logits, uint32_t B, uint32_t V, uint64_t ld,
+                   const float* d_temperature, const uint32_t* d_seed, uint32_t* d_out, void* stream);
+int zs_lane_topk(zs_ctx* ctx, const float* d_logits, uint32_t B, uint32_t V, uint64_t ld, uint32_t K,
+                 float* d_vals, uint32_t* d_idxs, void* stream);
+int zs_lane_sample_topk(zs_ctx* ctx, const float* d_vals, const uint32_t* d_idxs, uint32_t B, uint32_t K,
+                        const float* d_temperature, const uint32_t* d_top_k, const float* d_top_p,
+                        const uint32_t* d_seed, uint32_t* d_out, void* stream);
+/* gpu/sampling.rs:9 step_seed: base + gen_idx * 0x9E3779B1 (wrapping). */
+uint32_t zs_step_seed(uint32_t base, uint32_t gen_idx);
+
+/* ---- profiling ----------------------------------------------------------
+ * When enabled, zs_sample records a HIP event around each of its kernel
+ * launches (no synchronisation is added). zs_last_timings waits for the last
+ * call's events and writes up to `cap` kernel names / durations (ms); returns
+ * the number of kernels. Stands in for the reference's in-process timing
+ * (Cargo feature `profile`, Cargo.toml:121-126). */
+int zs_set_profiling(zs_ctx* ctx, int on);
+int zs_last_timings(zs_ctx* ctx, const char** names, float* ms, int cap);
+
 #ifdef __cplusplus
 }
 #endif

@@ -55,6 +55,8 @@ def _load():
         "zo_btopk": (None, [f32p, C.c_uint32, C.c_uint32, f32p, u32p]),
         "zo_philox4x32_10": (None, [u32p, u32p, u32p]),
         "zo_philox_uniform": (C.c_float, [C.c_uint64, C.c_uint64, C.c_uint32]),
+        "zo_spec_verify": (C.c_uint32, [f32p, f32p, u32p, C.c_uint32, C.c_uint32, C.c_float, C.c_uint64,
+                                        C.c_uint64, u32p]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -281,6 +283,22 @@ def philox4x32_10(ctr, key):
 
 def philox_uniform(seed, counter, tag=0):
     return float(lib().zo_philox_uniform(seed & (2**64 - 1), counter & (2**64 - 1), tag))
+
+
+def spec_verify(target, draft, drafts, temperature, seed=0, counter=0):
+    """target [k+1, V], draft [k, V] or None -> (accepted, next)."""
+    t, tp = _f32(np.asarray(target, np.float32).reshape(-1))
+    k = len(drafts)
+    V = t.size // (k + 1)
+    if draft is None:
+        dp = None
+    else:
+        d, dp = _f32(np.asarray(draft, np.float32).reshape(-1))
+    ids, ip = _u32(list(drafts) or [0])
+    nxt = C.c_uint32(0)
+    acc = lib().zo_spec_verify(tp, dp, ip, k, V, temperature, seed & (2**64 - 1), counter & (2**64 - 1),
+                               C.byref(nxt))
+    return int(acc), int(nxt.value)
 
 
 # ---- one row through the reference decode-loop order ------------------------------

@@ -566,3 +566,118 @@ ZO_API float zo_philox_uniform(uint64_t seed, uint64_t counter, uint32_t tag) {
     zo_philox4x32_10(ctr, key, o);
     return (float)(o[0] >> 9) * 0x1p-23f;
 }
+
+/* -------------------------------------------------------------------------
+ * Speculative-decode verification. temperature <= 0: verify_drafts
+ * (spec_decode.rs:241-267). temperature > 0: rejection sampling
+ * (Leviathan et al. 2023, Chen et al. 2023) as libzs defines it with
+ * integer weights W_v = rint(expf(z_v - max z) * 2^24), z = x / T; accept
+ * draft d at step i iff U_i * Q_d * sum(P) <= P_d * sum(Q) * 2^32 (U_i the
+ * 32-bit Philox word, tag 1+i); at the first rejection draw from
+ * max(0, P sum(Q) - Q sum(P)) (P if that is all zero) with tag 1+k+i; after k
+ * acceptances draw from target row k with tag 1+2k. A draw returns the first
+ * id whose inclusive prefix exceeds floor(U * total / 2^32). Rows with NaN /
+ * +inf / all -inf logits are verified greedily; draft ids >= V are rejected.
+ * The reference has no stochastic verification (rest.rs:2639): parity of this
+ * branch is pinned by the greedy special case and a distribution test.
+ * ------------------------------------------------------------------------- */
+typedef unsigned __int128 zo_u128;
+
+static uint32_t zo_philox_u32(uint64_t seed, uint64_t counter, uint32_t tag) {
+    uint32_t ctr[4] = {(uint32_t)counter, (uint32_t)(counter >> 32), tag, 0u};
+    uint32_t key[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
+    uint32_t o[4];
+    zo_philox4x32_10(ctr, key, o);
+    return o[0];
+}
+
+static float zo_spec_z(float x, float T) { return (T > 0.0f && T != 1.0f) ? x / T : x; }
+
+/* row stats: max z (NaN ignored), degenerate flag */
+static int zo_spec_row_max(const float* x, uint32_t V, float T, float* m) {
+    float mm = -INFINITY;
+    int bad = 0;
+    for (uint32_t v = 0; v < V; v++) {
+        float z = zo_spec_z(x[v], T);
+        if (z != z || z == INFINITY) bad = 1;
+        mm = rmax(mm, z);
+    }
+    if (mm == -INFINITY) bad = 1;
+    *m = mm;
+    return bad;
+}
+
+static uint64_t zo_spec_w(float x, float T, float m) {
+    float e = expf(zo_spec_z(x, T) - m);
+    return (uint64_t)rint((double)e * 16777216.0);
+}
+
+ZO_API uint32_t zo_spec_verify(const float* target, const float* draft, const uint32_t* drafts, uint32_t k,
+                               uint32_t V, float T, uint64_t seed, uint64_t counter, uint32_t* next) {
+    int greedy = !(T > 0.0f) || draft == 0;
+    float mt[64], md[64];
+    uint64_t st[64], sd[64];
+    if (!greedy) {
+        for (uint32_t p = 0; p <= k && !greedy; p++)
+            if (zo_spec_row_max(target + (size_t)p * V, V, T, &mt[p])) greedy = 1;
+        for (uint32_t p = 0; p < k && !greedy; p++)
+            if (zo_spec_row_max(draft + (size_t)p * V, V, T, &md[p])) greedy = 1;
+    }
+    if (greedy) return zo_verify_drafts(drafts, k, target, k + 1, V, next);
+    for (uint32_t p = 0; p <= k; p++) {
+        uint64_t s = 0;
+        for (uint32_t v = 0; v < V; v++) s += zo_spec_w(target[(size_t)p * V + v], T, mt[p]);
+        st[p] = s;
+    }
+    for (uint32_t p = 0; p < k; p++) {
+        uint64_t s = 0;
+        for (uint32_t v = 0; v < V; v++) s += zo_spec_w(draft[(size_t)p * V + v], T, md[p]);
+        sd[p] = s;
+    }
+    uint32_t i = 0;
+    for (; i < k; i++) {
+        uint32_t d = drafts[i];
+        if (d >= V) break;
+        uint64_t P = zo_spec_w(target[(size_t)i * V + d], T, mt[i]);
+        uint64_t Q = zo_spec_w(draft[(size_t)i * V + d], T, md[i]);
+        uint32_t U = zo_philox_u32(seed, counter, 1u + i);
+        zo_u128 lhs = (zo_u128)U * Q * st[i];
+        zo_u128 rhs = ((zo_u128)P * sd[i]) << 32;
+        if (!(lhs <= rhs)) break;
+    }
+    /* weights of the final draw */
+    const uint32_t pos = i < k ? i : k;
+    const float* trow = target + (size_t)pos * V;
+    const float* drow = i < k ? draft + (size_t)i * V : 0;
+    int residual = i < k;
+    zo_u128 total = 0;
+    uint32_t word;
+    if (residual) {
+        for (uint32_t v = 0; v < V; v++) {
+            zo_u128 pp = (zo_u128)zo_spec_w(trow[v], T, mt[i]) * sd[i];
+            zo_u128 qq = (zo_u128)zo_spec_w(drow[v], T, md[i]) * st[i];
+            total += pp > qq ? pp - qq : 0;
+        }
+        word = zo_philox_u32(seed, counter, 1u + k + i);
+        if (total == 0) { residual = 0; total = st[i]; }
+    } else {
+        total = st[k];
+        word = zo_philox_u32(seed, counter, 1u + 2 * k);
+    }
+    const zo_u128 thr = ((zo_u128)word * total) >> 32;
+    zo_u128 run = 0;
+    *next = V - 1;
+    for (uint32_t v = 0; v < V; v++) {
+        zo_u128 w;
+        if (residual) {
+            zo_u128 pp = (zo_u128)zo_spec_w(trow[v], T, mt[i]) * sd[i];
+            zo_u128 qq = (zo_u128)zo_spec_w(drow[v], T, md[i]) * st[i];
+            w = pp > qq ? pp - qq : 0;
+        } else {
+            w = zo_spec_w(trow[v], T, mt[pos]);
+        }
+        run += w;
+        if (w > 0 && run > thr) { *next = v; break; }
+    }
+    return i;
+}

@@ -555,3 +555,34 @@ def test_philox_uniform_range_and_mapping():
         w = int(O.philox4x32_10([c, 0, 0, 0], [7, 0])[0])
         assert u == np.float32((w >> 9) * 2.0 ** -23)
         assert 0.0 <= u < 1.0
+
+
+# ---------------------------------------------------------------- spec decode (rejection sampling)
+def test_spec_greedy_equals_verify_drafts():  # spec_decode.rs:422-443
+    t = np.stack([_mk(16, 5), _mk(16, 7), _mk(16, 9)])
+    assert O.spec_verify(t, None, [5, 7], 0.0) == (2, 9)
+    t = np.stack([_mk(8, 5), _mk(8, 7), _mk(8, 1)])
+    assert O.spec_verify(t, np.zeros((2, 8)), [5, 99], 0.0) == (1, 7)
+
+
+def test_spec_rejection_sampling_preserves_target_distribution():
+    # first emitted token ~ target distribution (Leviathan et al. 2023, Thm 1)
+    rng = np.random.default_rng(0)
+    V = 6
+    tl = np.array([[1.0, 0.2, -1.0, 2.0, 0.5, 0.0], [0.0] * 6], np.float32)
+    dl = np.array([[0.0, 1.5, 0.3, -0.5, 1.0, 0.2]], np.float32)
+
+    def weights(x):
+        e = np.array([np.float32(np.exp(np.float32(v - x.max()))) for v in x], np.float64)
+        return np.rint(e * 2 ** 24)
+
+    p = weights(tl[0]) / weights(tl[0]).sum()
+    q = weights(dl[0]) / weights(dl[0]).sum()
+    N = 30000
+    counts = np.zeros(V)
+    for c in range(N):
+        d = int(rng.choice(V, p=q))
+        acc, nxt = O.spec_verify(tl, dl, [d], 1.0, seed=11, counter=c)
+        counts[d if acc == 1 else nxt] += 1
+    chi2 = (((counts - N * p) ** 2) / (N * p)).sum()
+    assert chi2 < 25.0, (chi2, counts / N, p)  # 5 dof: p(chi2 > 25) ~ 1e-4

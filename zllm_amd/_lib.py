@@ -77,6 +77,16 @@ class Batch(C.Structure):
     ]
 
 
+class SpecBatch(C.Structure):
+    _fields_ = [
+        ("B", C.c_uint32), ("V", C.c_uint32), ("k", C.c_uint32),
+        ("ld", C.c_uint64),
+        ("d_target", C.c_void_p), ("d_draft", C.c_void_p), ("d_draft_ids", C.c_void_p),
+        ("d_temperature", C.c_void_p), ("d_seed", C.c_void_p), ("d_counter", C.c_void_p),
+        ("d_accepted", C.c_void_p), ("d_next", C.c_void_p),
+    ]
+
+
 # name -> (restype, argtypes); every symbol include/zs.h declares
 SIGNATURES = {
     "zs_abi_version": (C.c_int, []),
@@ -96,6 +106,17 @@ SIGNATURES = {
     "zs_dfa_mask": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32,
                               C.c_void_p, C.c_void_p, C.c_void_p]),
     "zs_sample": (C.c_int, [C.c_void_p, C.POINTER(Batch), C.c_void_p]),
+    "zs_set_profiling": (C.c_int, [C.c_void_p, C.c_int]),
+    "zs_spec_verify": (C.c_int, [C.c_void_p, C.POINTER(SpecBatch), C.c_void_p]),
+    "zs_lane_argmax": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint64, C.c_void_p, C.c_void_p]),
+    "zs_lane_sample": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint64, C.c_void_p, C.c_void_p,
+                                 C.c_void_p, C.c_void_p]),
+    "zs_lane_topk": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint64, C.c_uint32, C.c_void_p,
+                               C.c_void_p, C.c_void_p]),
+    "zs_lane_sample_topk": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p,
+                                      C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),
+    "zs_step_seed": (C.c_uint32, [C.c_uint32, C.c_uint32]),
+    "zs_last_timings": (C.c_int, [C.c_void_p, C.POINTER(C.c_char_p), C.POINTER(C.c_float), C.c_int]),
 }
 
 _lib = None

@@ -11,6 +11,14 @@
 
 // launchers (zs_sample.hip, zs_dfa.hip)
 extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t stream);
+extern "C" int zs_spec_launch(const zs_spec_args& a, hipStream_t stream);
+extern "C" int zs_lane_argmax_launch(const float* logits, uint32_t B, uint32_t V, uint64_t ld, const float* temp,
+                                     const uint32_t* seed, uint32_t* out, hipStream_t stream);
+extern "C" int zs_lane_topk_launch(const float* logits, uint32_t B, uint32_t V, uint64_t ld, uint32_t K,
+                                   float* vals, uint32_t* idxs, hipStream_t stream);
+extern "C" int zs_lane_sample_topk_launch(const float* vals, const uint32_t* idxs, uint32_t B, uint32_t K,
+                                          const float* temp, const uint32_t* top_k, const float* top_p,
+                                          const uint32_t* seed, uint32_t* out, hipStream_t stream);
 extern "C" int zs_dfa_mask_launch(const dm_args& a, bool lds, uint32_t* any_scratch, hipStream_t stream);
 
 int zs_set_error(zs_ctx* ctx, int code, const char* fmt, ...) {
@@ -51,8 +59,11 @@ extern "C" void zs_ctx_destroy(zs_ctx* ctx) {
     int dev = 0;
     hipGetDevice(&dev);
     hipSetDevice(ctx->device);
+    for (int i = 0; i < 16; i++)
+        if (ctx->events[i]) hipEventDestroy((hipEvent_t)ctx->events[i]);
     void* ptrs[] = {ctx->p_cnt, ctx->p_id, ctx->p_flags, ctx->p_y, ctx->cst, ctx->cs_key, ctx->cs_idx,
-                    ctx->co_key, ctx->co_idx, ctx->rst, ctx->pairs, ctx->mask_scratch};
+                    ctx->co_key, ctx->co_idx, ctx->rst, ctx->pairs, ctx->mask_scratch, ctx->spec_chunks,
+                    ctx->spec_rows};
     for (void* p : ptrs)
         if (p) hipFree(p);
     hipSetDevice(dev);
@@ -94,6 +105,8 @@ extern "C" int zs_ctx_create(int device, uint32_t max_rows, uint32_t max_vocab, 
     if (!rc) rc = zs_alloc(ctx, &ctx->rst, R);
     if (!rc) rc = zs_alloc(ctx, &ctx->pairs, R * (size_t)max_vocab * 2);
     if (!rc) rc = zs_alloc(ctx, (uint32_t**)&ctx->mask_scratch, R);
+    if (!rc) rc = zs_alloc(ctx, &ctx->spec_chunks, R * (2 * ZS_SPEC_KMAX + 1) * C);
+    if (!rc) rc = zs_alloc(ctx, &ctx->spec_rows, R);
     hipSetDevice(prev);
     if (rc) {
         zs_ctx_destroy(ctx);
@@ -388,3 +401,129 @@ extern "C" int zs_sample(zs_ctx* ctx, const zs_batch* b, void* stream) {
     if (prev != ctx->device) hipSetDevice(prev);
     return rc;
 }
+
+extern "C" int zs_set_profiling(zs_ctx* ctx, int on) {
+    if (!ctx) return ZS_EINVAL;
+    if (on && !ctx->events[0]) {
+        int prev = 0;
+        hipGetDevice(&prev);
+        hipSetDevice(ctx->device);
+        for (int i = 0; i < 16; i++) {
+            hipEvent_t e;
+            ZS_HIP(ctx, hipEventCreate(&e));
+            ctx->events[i] = e;
+        }
+        hipSetDevice(prev);
+    }
+    ctx->profiling = on ? 1 : 0;
+    ctx->n_timed = 0;
+    return ZS_OK;
+}
+
+extern "C" int zs_last_timings(zs_ctx* ctx, const char** names, float* ms, int cap) {
+    if (!ctx) return ZS_EINVAL;
+    int n = ctx->n_timed;
+    if (n <= 0) return 0;
+    ZS_HIP(ctx, hipEventSynchronize((hipEvent_t)ctx->events[n]));
+    for (int i = 0; i < n && i < cap; i++) {
+        float t = 0.f;
+        ZS_HIP(ctx, hipEventElapsedTime(&t, (hipEvent_t)ctx->events[i], (hipEvent_t)ctx->events[i + 1]));
+        if (names) names[i] = ctx->timed_names[i + 1];
+        if (ms) ms[i] = t;
+    }
+    return n;
+}
+
+static int zs_device_guard_begin(zs_ctx* ctx) {
+    int prev = 0;
+    hipGetDevice(&prev);
+    if (prev != ctx->device) hipSetDevice(ctx->device);
+    return prev;
+}
+static void zs_device_guard_end(zs_ctx* ctx, int prev) {
+    if (prev != ctx->device) hipSetDevice(prev);
+}
+
+extern "C" int zs_spec_verify(zs_ctx* ctx, const zs_spec_batch* b, void* stream) {
+    if (!ctx || !b) return zs_set_error(ctx, ZS_EINVAL, "zs_spec_verify: null argument");
+    if (b->B == 0) return ZS_OK;
+    if (b->B > ctx->max_rows || b->V == 0 || b->V > ctx->max_vocab || b->k > ZS_SPEC_KMAX)
+        return zs_set_error(ctx, ZS_ELIMIT, "zs_spec_verify: B=%u V=%u k=%u outside the context limits", b->B, b->V,
+                            b->k);
+    if (!b->d_target || (b->k && !b->d_draft_ids) || !b->d_temperature || !b->d_seed || !b->d_counter ||
+        !b->d_accepted || !b->d_next)
+        return zs_set_error(ctx, ZS_EINVAL, "zs_spec_verify: null required pointer");
+    if (b->ld < b->V) return zs_set_error(ctx, ZS_EINVAL, "zs_spec_verify: ld < V");
+    zs_spec_args a{};
+    a.B = b->B; a.V = b->V; a.k = b->k; a.ld = b->ld;
+    a.target = b->d_target; a.draft = b->k ? b->d_draft : nullptr; a.draft_ids = b->d_draft_ids;
+    a.temperature = b->d_temperature; a.seed = b->d_seed; a.counter = b->d_counter;
+    a.accepted = b->d_accepted; a.next = b->d_next;
+    a.cst = ctx->spec_chunks; a.rs = ctx->spec_rows;
+    a.nch = ctx->max_chunks; a.npos_max = 2 * ZS_SPEC_KMAX + 1;
+    int prev = zs_device_guard_begin(ctx);
+    int rc = zs_spec_launch(a, (hipStream_t)stream);
+    zs_device_guard_end(ctx, prev);
+    if (rc) return zs_set_error(ctx, ZS_EHIP, "zs_spec_verify: launch failed: %s", hipGetErrorString(hipGetLastError()));
+    return ZS_OK;
+}
+
+static int lane_check(zs_ctx* ctx, uint32_t B, uint32_t V, uint64_t ld, const void* logits, const char* who) {
+    if (!ctx || !logits) return zs_set_error(ctx, ZS_EINVAL, "%s: null argument", who);
+    if (ld < V || (ld & 3u) || ((uintptr_t)logits & 15u))
+        return zs_set_error(ctx, ZS_EINVAL, "%s: ld must be >= V and a multiple of 4, logits 16-byte aligned", who);
+    return ZS_OK;
+}
+
+extern "C" int zs_lane_argmax(zs_ctx* ctx, const float* d_logits, uint32_t B, uint32_t V, uint64_t ld,
+                              uint32_t* d_out, void* stream) {
+    int rc = lane_check(ctx, B, V, ld, d_logits, "zs_lane_argmax");
+    if (rc) return rc;
+    if (!d_out) return zs_set_error(ctx, ZS_EINVAL, "zs_lane_argmax: null output");
+    if (B == 0) return ZS_OK;
+    int prev = zs_device_guard_begin(ctx);
+    rc = zs_lane_argmax_launch(d_logits, B, V, ld, nullptr, nullptr, d_out, (hipStream_t)stream);
+    zs_device_guard_end(ctx, prev);
+    return rc ? zs_set_error(ctx, ZS_EHIP, "zs_lane_argmax: launch failed") : ZS_OK;
+}
+
+extern "C" int zs_lane_sample(zs_ctx* ctx, const float* d_logits, uint32_t B, uint32_t V, uint64_t ld,
+                              const float* d_temperature, const uint32_t* d_seed, uint32_t* d_out, void* stream) {
+    int rc = lane_check(ctx, B, V, ld, d_logits, "zs_lane_sample");
+    if (rc) return rc;
+    if (!d_out || !d_temperature || !d_seed) return zs_set_error(ctx, ZS_EINVAL, "zs_lane_sample: null argument");
+    if (B == 0) return ZS_OK;
+    int prev = zs_device_guard_begin(ctx);
+    rc = zs_lane_argmax_launch(d_logits, B, V, ld, d_temperature, d_seed, d_out, (hipStream_t)stream);
+    zs_device_guard_end(ctx, prev);
+    return rc ? zs_set_error(ctx, ZS_EHIP, "zs_lane_sample: launch failed") : ZS_OK;
+}
+
+extern "C" int zs_lane_topk(zs_ctx* ctx, const float* d_logits, uint32_t B, uint32_t V, uint64_t ld, uint32_t K,
+                            float* d_vals, uint32_t* d_idxs, void* stream) {
+    int rc = lane_check(ctx, B, V, ld, d_logits, "zs_lane_topk");
+    if (rc) return rc;
+    if (!d_vals || !d_idxs) return zs_set_error(ctx, ZS_EINVAL, "zs_lane_topk: null output");
+    if (K == 0 || K > 1024) return zs_set_error(ctx, ZS_ELIMIT, "zs_lane_topk: K=%u outside 1..1024", K);
+    if (B == 0) return ZS_OK;
+    int prev = zs_device_guard_begin(ctx);
+    rc = zs_lane_topk_launch(d_logits, B, V, ld, K, d_vals, d_idxs, (hipStream_t)stream);
+    zs_device_guard_end(ctx, prev);
+    return rc ? zs_set_error(ctx, ZS_EHIP, "zs_lane_topk: launch failed") : ZS_OK;
+}
+
+extern "C" int zs_lane_sample_topk(zs_ctx* ctx, const float* d_vals, const uint32_t* d_idxs, uint32_t B, uint32_t K,
+                                   const float* d_temperature, const uint32_t* d_top_k, const float* d_top_p,
+                                   const uint32_t* d_seed, uint32_t* d_out, void* stream) {
+    if (!ctx || !d_vals || !d_idxs || !d_temperature || !d_top_k || !d_top_p || !d_seed || !d_out)
+        return zs_set_error(ctx, ZS_EINVAL, "zs_lane_sample_topk: null argument");
+    if (K == 0) return zs_set_error(ctx, ZS_EINVAL, "zs_lane_sample_topk: K == 0");
+    if (B == 0) return ZS_OK;
+    int prev = zs_device_guard_begin(ctx);
+    int rc = zs_lane_sample_topk_launch(d_vals, d_idxs, B, K, d_temperature, d_top_k, d_top_p, d_seed, d_out,
+                                        (hipStream_t)stream);
+    zs_device_guard_end(ctx, prev);
+    return rc ? zs_set_error(ctx, ZS_EHIP, "zs_lane_sample_topk: launch failed") : ZS_OK;
+}
+
+extern "C" uint32_t zs_step_seed(uint32_t base, uint32_t gen_idx) { return base + gen_idx * 0x9E3779B1u; }

@@ -75,6 +75,37 @@ struct zs_row_state {
     float cand_x[ZS_OBS_CAND];
 };
 
+// Speculative-decode verification scratch (zs_spec.hip).
+#define ZS_SPEC_KMAX 16
+struct zs_spec_chunk {
+    float zmax;
+    uint32_t flags;
+    float amax_val;
+    uint32_t amax_idx;
+    unsigned long long wsum;
+};
+struct zs_spec_row {
+    uint32_t mode, pos, residual, word;
+    float m_t, m_d;
+    unsigned long long sum_t, sum_d;
+};
+
+struct zs_spec_args {
+    uint32_t B, V, k;
+    uint64_t ld;
+    const float* target;        // [B][k+1][ld]
+    const float* draft;         // [B][k][ld] or null
+    const uint32_t* draft_ids;  // [B][k]
+    const float* temperature;   // [B]
+    const uint64_t* seed;
+    const uint64_t* counter;
+    uint32_t* accepted;
+    uint32_t* next;
+    zs_spec_chunk* cst;         // scratch [B][npos_max][nch]
+    zs_spec_row* rs;            // scratch [B]
+    uint32_t nch, npos_max;
+};
+
 struct zs_ctx {
     int device;
     uint32_t max_rows, max_vocab, max_chunks;
@@ -92,6 +123,13 @@ struct zs_ctx {
     zs_row_state* rst;
     uint32_t* pairs;       // big-row gather area [rows][max_vocab][2]
     void* mask_scratch;    // DFA mask staging
+    zs_spec_chunk* spec_chunks;  // [rows][2*ZS_SPEC_KMAX+1][max_chunks]
+    zs_spec_row* spec_rows;      // [rows]
+    // profiling (zs_set_profiling)
+    int profiling;
+    int n_timed;
+    void* events[16];      // hipEvent_t
+    const char* timed_names[16];
 };
 
 struct zs_vocab {

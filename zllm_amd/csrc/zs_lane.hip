@@ -1,0 +1,254 @@
+// zs_lane.hip -- the batched GPU lane of the reference (continuous batching,
+// gpu/batch.rs:176-192): batched argmax, Gumbel-max temperature sampling,
+// top-K extraction and the top-K nucleus draw, with the reference semantics of
+// shaders.rs:758-937 and gpu/sampling.rs:9-56, on-device (no readback).
+//
+// The WGSL kernels reduce with a 256-thread workgroup: thread t scans ids
+// t, t+256, ... keeping the first strict maximum, then a stride-128..1 tree
+// keeps the lower slot unless the upper one is strictly greater. The winner
+// among equal maxima is therefore the slot with the smallest bit-reversed
+// 8-bit slot number, then the smallest id within that slot; candidates must be
+// strictly greater than the initial -1e30 (NaN never wins). These kernels
+// reduce a composite key that encodes exactly that order, which lets any
+// workgroup shape reproduce the WGSL result.
+#include <hip/hip_runtime.h>
+#include "zs_internal.h"
+#include "zs_dev.h"
+
+#define LN_NT 1024
+
+__device__ __forceinline__ uint32_t zs_bitrev8(uint32_t x) { return __brev(x) >> 24; }
+
+// composite for the WGSL argmax order: larger value, then preferred slot, then lower id
+__device__ __forceinline__ unsigned long long wg_key(float v, uint32_t idx) {
+    if (!(v > -1e30f)) return 0ull;  // not a candidate (also NaN)
+    float vv = (v == 0.0f) ? 0.0f : v;
+    uint32_t slot = idx & 255u, hi = idx >> 8;
+    return ((unsigned long long)zs_total_key(vv) << 32) | ((unsigned long long)(255u - zs_bitrev8(slot)) << 24) |
+           (unsigned long long)(0xffffffu - (hi & 0xffffffu));
+}
+__device__ __forceinline__ uint32_t wg_key_idx(unsigned long long k) {
+    uint32_t slot = zs_bitrev8(255u - (uint32_t)((k >> 24) & 255u));
+    uint32_t hi = 0xffffffu - (uint32_t)(k & 0xffffffu);
+    return (hi << 8) | slot;
+}
+
+__device__ __forceinline__ unsigned long long block_max_u64(unsigned long long v, unsigned long long* sh) {
+    for (int d = 32; d > 0; d >>= 1) {
+        unsigned long long o = __shfl_xor(v, d, 64);
+        v = o > v ? o : v;
+    }
+    if (zs_lane() == 0) sh[zs_wid()] = v;
+    __syncthreads();
+    unsigned long long r = 0;
+    for (int i = 0; i < LN_NT / 64; i++) r = sh[i] > r ? sh[i] : r;
+    __syncthreads();
+    return r;
+}
+
+// shaders.rs:805-815
+__device__ __forceinline__ uint32_t zs_hash_u32(uint32_t x) {
+    uint32_t h = x;
+    h ^= h >> 16; h *= 0x7feb352du;
+    h ^= h >> 15; h *= 0x846ca68bu;
+    h ^= h >> 16;
+    return h;
+}
+__device__ __forceinline__ float zs_rand01(uint32_t s, uint32_t i) {
+    uint32_t r = zs_hash_u32(s ^ zs_hash_u32(i));
+    return ((float)(r >> 8) + 0.5f) / 16777216.0f;
+}
+// WGSL `log` has no precision contract; this build fixes it as the correctly
+// rounded f32 log (double log rounded once).
+__device__ __forceinline__ float zs_log_cr(float x) { return (float)log((double)x); }
+
+// BARGMAX (shaders.rs:761-789) and BSAMPLE (:796-850): temp == nullptr -> argmax.
+__global__ __launch_bounds__(LN_NT) void zs_k_bargmax(const float* logits, uint32_t V, uint64_t ld,
+                                                       const float* temp, const uint32_t* seed, uint32_t* out) {
+    __shared__ unsigned long long sh[LN_NT / 64];
+    const uint32_t r = blockIdx.x;
+    const float* row = logits + (size_t)r * ld;
+    bool greedy = true;
+    float inv_t = 1.0f;
+    uint32_t sd = 0;
+    if (temp) {
+        float ts = temp[r];
+        greedy = ts <= 0.0f;
+        inv_t = greedy ? 1.0f : 1.0f / ts;
+        sd = seed[r];
+    }
+    unsigned long long best = 0;
+    for (uint32_t i0 = threadIdx.x * 4; i0 < V; i0 += LN_NT * 4) {
+        float4 v4 = *reinterpret_cast<const float4*>(row + i0);
+        float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            uint32_t i = i0 + q;
+            if (i >= V) continue;
+            float v = vv[q];
+            if (!greedy) {
+                float u = zs_rand01(sd, i);
+                float g = -zs_log_cr(-zs_log_cr(u));
+                v = v * inv_t;
+                v = v + g;
+            }
+            unsigned long long k = wg_key(v, i);
+            best = k > best ? k : best;
+        }
+    }
+    best = block_max_u64(best, sh);
+    if (threadIdx.x == 0) out[r] = best ? wg_key_idx(best) : 0u;
+}
+
+// BTOPK (shaders.rs:859-905): the K largest (value desc, id asc) among values in
+// [-3e38, 3e38) (NaN and values outside never qualify: they are never "below"
+// the previous winner or "better" than the -3e38 seed); sentinel (-3e38,
+// 0xffffffff) pads rows with fewer candidates. Keys merge -0.0 and +0.0 (they
+// compare equal in WGSL); the output keeps each element's own value.
+#define TK_MAX 1024
+__device__ __forceinline__ bool tk_cand(float v) { return v >= -3.0e38f && v < 3.0e38f; }
+__device__ __forceinline__ uint32_t tk_key(float v) { return zs_total_key(v == 0.0f ? 0.0f : v); }
+
+__global__ __launch_bounds__(LN_NT) void zs_k_btopk(const float* logits, uint32_t V, uint64_t ld, uint32_t K,
+                                                     float* vals, uint32_t* idxs) {
+    __shared__ uint32_t hist[256];
+    __shared__ uint32_t u[4];
+    __shared__ unsigned long long buf[TK_MAX];
+    __shared__ uint32_t scan_sh[LN_NT / 64];
+    const uint32_t r = blockIdx.x;
+    const int t = threadIdx.x;
+    const float* row = logits + (size_t)r * ld;
+    // radix select of the K-th largest candidate key
+    uint32_t ncand = 0;
+    for (uint32_t i = t; i < V; i += LN_NT) ncand += tk_cand(row[i]) ? 1u : 0u;
+    ncand = block_sum_u<LN_NT>(ncand, scan_sh);
+    const uint32_t KK = ncand < K ? ncand : K;
+    uint32_t prefix = 0, mask = 0, need = KK;
+    if (KK > 0) {
+        for (int shift = 24; shift >= 0; shift -= 8) {
+            if (t < 256) hist[t] = 0;
+            __syncthreads();
+            for (uint32_t i = t; i < V; i += LN_NT) {
+                float v = row[i];
+                if (!tk_cand(v)) continue;
+                uint32_t k = tk_key(v);
+                if ((k & mask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1u);
+            }
+            __syncthreads();
+            if (t < 64) {
+                uint32_t c[4], loc = 0;
+                for (int q = 0; q < 4; q++) { c[q] = hist[255 - 4 * t - q]; loc += c[q]; }
+                uint32_t inc = wave_incl_scan_u(loc);
+                uint32_t before = inc - loc;
+                for (int q = 0; q < 4; q++) {
+                    if (before < need && need <= before + c[q]) { u[0] = 255 - 4 * t - q; u[1] = need - before; }
+                    before += c[q];
+                }
+            }
+            __syncthreads();
+            prefix |= u[0] << shift;
+            mask |= 0xffu << shift;
+            need = u[1];
+            __syncthreads();
+        }
+    }
+    // gather: keys above the K-th, then the lowest-id `need` equal ones (ids in order)
+    if (t == 0) u[2] = 0;
+    __syncthreads();
+    uint32_t carry = 0;
+    for (uint32_t base = 0; base < V && KK > 0; base += LN_NT) {
+        uint32_t i = base + t;
+        float v = i < V ? row[i] : NAN;
+        bool c = i < V && tk_cand(v);
+        uint32_t k = c ? tk_key(v) : 0;
+        bool gt = c && k > prefix, eq = c && k == prefix;
+        uint32_t tot;
+        uint32_t ex = block_excl_scan_u<LN_NT>(eq ? 1u : 0u, scan_sh, &tot);
+        if (gt || (eq && carry + ex < need)) {
+            uint32_t pos = atomicAdd(&u[2], 1u);
+            if (pos < TK_MAX) buf[pos] = ((unsigned long long)(~k) << 32) | i;
+        }
+        carry += tot;
+    }
+    __syncthreads();
+    uint32_t n = KK;
+    uint32_t np2 = 1;
+    while (np2 < n) np2 <<= 1;
+    for (uint32_t i = n + t; i < np2; i += LN_NT) buf[i] = ~0ull;
+    __syncthreads();
+    if (np2 > 1) block_bitonic_u64<LN_NT>(buf, (int)np2);
+    for (uint32_t j = t; j < K; j += LN_NT) {
+        if (j < n) {
+            uint32_t id = (uint32_t)(buf[j] & 0xffffffffull);
+            vals[(size_t)r * K + j] = row[id];
+            idxs[(size_t)r * K + j] = id;
+        } else {
+            vals[(size_t)r * K + j] = -3.0e38f;
+            idxs[(size_t)r * K + j] = 0xffffffffu;
+        }
+    }
+}
+
+// gpu/sampling.rs:24-31
+__device__ __forceinline__ float zs_rng01(uint32_t seed) {
+    uint64_t z = (uint64_t)seed * 0x9E3779B97F4A7C15ull + 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z ^= z >> 31;
+    return ((float)(z >> 40) + 0.5f) / 16777216.0f;
+}
+
+// gpu/sampling.rs:35-56, one thread per row over its descending pool.
+__global__ void zs_k_sample_topk(const float* vals, const uint32_t* idxs, uint32_t B, uint32_t K,
+                                 const float* temp, const uint32_t* top_k, const float* top_p,
+                                 const uint32_t* seed, uint32_t* out) {
+    uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= B) return;
+    const float* v = vals + (size_t)r * K;
+    const uint32_t* id = idxs + (size_t)r * K;
+    uint32_t n = 0;
+    while (n < K && v[n] > -3.0e37f) n++;
+    if (n == 0 || temp[r] <= 0.0f) { out[r] = id[0]; return; }
+    const float T = temp[r];
+    uint32_t kk = top_k[r] == 0 ? n : (top_k[r] < n ? top_k[r] : n);
+    const float maxv = v[0];
+    float z = -0.0f;
+    for (uint32_t i = 0; i < kk; i++) z = z + zs_expf((v[i] - maxv) / T);
+    uint32_t cut = kk;
+    const float tp = top_p[r];
+    if (tp > 0.0f && tp < 1.0f) {
+        float cum = 0.0f;
+        for (uint32_t i = 0; i < kk; i++) {
+            cum = cum + zs_expf((v[i] - maxv) / T) / z;
+            if (cum >= tp) { cut = i + 1; break; }
+        }
+    }
+    float zc = -0.0f;
+    for (uint32_t i = 0; i < cut; i++) zc = zc + zs_expf((v[i] - maxv) / T) / z;
+    const float target = zs_rng01(seed[r]) * zc;
+    float acc = 0.0f;
+    uint32_t res = id[cut - 1];
+    for (uint32_t i = 0; i < cut; i++) {
+        acc = acc + zs_expf((v[i] - maxv) / T) / z;
+        if (acc >= target) { res = id[i]; break; }
+    }
+    out[r] = res;
+}
+
+extern "C" int zs_lane_argmax_launch(const float* logits, uint32_t B, uint32_t V, uint64_t ld, const float* temp,
+                                     const uint32_t* seed, uint32_t* out, hipStream_t stream) {
+    hipLaunchKernelGGL(zs_k_bargmax, dim3(B), dim3(LN_NT), 0, stream, logits, V, ld, temp, seed, out);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+extern "C" int zs_lane_topk_launch(const float* logits, uint32_t B, uint32_t V, uint64_t ld, uint32_t K,
+                                   float* vals, uint32_t* idxs, hipStream_t stream) {
+    hipLaunchKernelGGL(zs_k_btopk, dim3(B), dim3(LN_NT), 0, stream, logits, V, ld, K, vals, idxs);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+extern "C" int zs_lane_sample_topk_launch(const float* vals, const uint32_t* idxs, uint32_t B, uint32_t K,
+                                          const float* temp, const uint32_t* top_k, const float* top_p,
+                                          const uint32_t* seed, uint32_t* out, hipStream_t stream) {
+    hipLaunchKernelGGL(zs_k_sample_topk, dim3((B + 63) / 64), dim3(64), 0, stream, vals, idxs, B, K, temp, top_k,
+                       top_p, seed, out);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}

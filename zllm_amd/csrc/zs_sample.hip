@@ -1332,11 +1332,26 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
     a.max_vocab = ctx->max_vocab;
     const uint32_t B = bt->B;
     const uint32_t nch = (bt->V + ZS_P1_CH - 1) / ZS_P1_CH;
+    const bool prof = ctx->profiling != 0;
+    int ev = 0;
+    auto mark = [&](const char* name) {
+        if (!prof) return;
+        if (name) ctx->timed_names[ev] = name;
+        hipEventRecord((hipEvent_t)ctx->events[ev], stream);
+        ev++;
+    };
+    mark(nullptr);
     hipLaunchKernelGGL(zs_k_prep, dim3(B), dim3(ZS_PREP_NT), 0, stream, a);
+    mark("zs_k_prep");
     hipLaunchKernelGGL(zs_k_pass1, dim3(nch, B), dim3(ZS_P1_NT), 0, stream, a);
+    mark("zs_k_pass1");
     hipLaunchKernelGGL(zs_k_combine, dim3(B), dim3(CB_NT), 0, stream, a);
+    mark("zs_k_combine");
     hipLaunchKernelGGL(zs_k_big, dim3(B), dim3(ZS_BIG_NT), 0, stream, a);
+    mark("zs_k_big");
     hipLaunchKernelGGL(zs_k_final, dim3((B + 63) / 64), dim3(64), 0, stream, a);
+    mark("zs_k_final");
+    if (prof) ctx->n_timed = ev - 1;
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return zs_set_error(ctx, ZS_EHIP, "zs_sample launch: %s", hipGetErrorString(e));
     return ZS_OK;

@@ -16,7 +16,7 @@ from typing import Dict, List, Optional, Sequence, Tuple
 import numpy as np
 import torch
 
-from ._lib import (Batch, RowParams, ZS_OK, ZS_ROW_LOGPROBS, ZS_ROW_MASKED, ZS_ROW_UNCERTAINTY, ZsError, lib)
+from ._lib import (Batch, RowParams, SpecBatch, ZS_OK, ZS_ROW_LOGPROBS, ZS_ROW_MASKED, ZS_ROW_UNCERTAINTY, ZsError, lib)
 
 OPENAI_TOP_LOGPROBS_CAP = 20  # logprobs.rs:27-29
 
@@ -44,6 +44,18 @@ class Context:
         if self.h:
             lib().zs_ctx_destroy(self.h)
             self.h = None
+
+    def set_profiling(self, on: bool):
+        _check(self.h, lib().zs_set_profiling(self.h, 1 if on else 0), "zs_set_profiling")
+
+    def last_timings(self) -> Dict[str, float]:
+        """Per-kernel durations (ms) of the last zs_sample call (profiling on)."""
+        names = (C.c_char_p * 16)()
+        ms = (C.c_float * 16)()
+        n = lib().zs_last_timings(self.h, names, ms, 16)
+        if n < 0:
+            _check(self.h, n, "zs_last_timings")
+        return {names[i].decode(): float(ms[i]) for i in range(n)}
 
     def __del__(self):
         try:
@@ -360,3 +372,75 @@ class BatchSampler:
                 rq.fsm.advance(int(tok))
             rq.ctrl.observe(int(tok))
         return out
+
+
+# ---------------------------------------------------------------- spec decode
+def verify_drafts(ctx: Context, target: torch.Tensor, draft_ids: torch.Tensor, temperature: torch.Tensor,
+                  seed: torch.Tensor, counter: torch.Tensor, draft: Optional[torch.Tensor] = None):
+    """Batched spec_decode::verify_drafts (spec_decode.rs:241-267) and, for
+    temperature > 0 with draft logits, rejection sampling. target [B, k+1, V],
+    draft [B, k, V], draft_ids [B, k] (int32). Returns (accepted, next)."""
+    B, kp1, V = target.shape
+    k = kp1 - 1
+    dev = target.device
+    acc = torch.empty(B, dtype=torch.int32, device=dev)
+    nxt = torch.empty(B, dtype=torch.int32, device=dev)
+    sb = SpecBatch()
+    sb.B, sb.V, sb.k, sb.ld = B, V, k, target.stride(1)
+    sb.d_target = target.data_ptr()
+    sb.d_draft = draft.data_ptr() if draft is not None else None
+    sb.d_draft_ids = draft_ids.data_ptr()
+    sb.d_temperature, sb.d_seed, sb.d_counter = temperature.data_ptr(), seed.data_ptr(), counter.data_ptr()
+    sb.d_accepted, sb.d_next = acc.data_ptr(), nxt.data_ptr()
+    rc = lib().zs_spec_verify(ctx.h, C.byref(sb), torch.cuda.current_stream(dev).cuda_stream)
+    _check(ctx.h, rc, "zs_spec_verify")
+    return acc, nxt
+
+
+# ---------------------------------------------------------------- batched lane
+def lane_argmax(ctx: Context, logits: torch.Tensor) -> torch.Tensor:
+    """BARGMAX_WGSL (shaders.rs:761-789) on [B, V] logits."""
+    B, V = logits.shape
+    out = torch.empty(B, dtype=torch.int32, device=logits.device)
+    rc = lib().zs_lane_argmax(ctx.h, logits.data_ptr(), B, V, logits.stride(0), out.data_ptr(),
+                              torch.cuda.current_stream(logits.device).cuda_stream)
+    _check(ctx.h, rc, "zs_lane_argmax")
+    return out
+
+
+def lane_sample(ctx: Context, logits: torch.Tensor, temperature: torch.Tensor, seed: torch.Tensor) -> torch.Tensor:
+    """BSAMPLE_WGSL Gumbel-max (shaders.rs:796-850); seed uint32 per row."""
+    B, V = logits.shape
+    out = torch.empty(B, dtype=torch.int32, device=logits.device)
+    rc = lib().zs_lane_sample(ctx.h, logits.data_ptr(), B, V, logits.stride(0), temperature.data_ptr(),
+                              seed.data_ptr(), out.data_ptr(), torch.cuda.current_stream(logits.device).cuda_stream)
+    _check(ctx.h, rc, "zs_lane_sample")
+    return out
+
+
+def lane_topk(ctx: Context, logits: torch.Tensor, K: int = 64):
+    """BTOPK_WGSL (shaders.rs:859-905): [B, K] values (desc) and ids."""
+    B, V = logits.shape
+    vals = torch.empty((B, K), dtype=torch.float32, device=logits.device)
+    idxs = torch.empty((B, K), dtype=torch.int32, device=logits.device)
+    rc = lib().zs_lane_topk(ctx.h, logits.data_ptr(), B, V, logits.stride(0), K, vals.data_ptr(), idxs.data_ptr(),
+                            torch.cuda.current_stream(logits.device).cuda_stream)
+    _check(ctx.h, rc, "zs_lane_topk")
+    return vals, idxs
+
+
+def lane_sample_topk(ctx: Context, vals: torch.Tensor, idxs: torch.Tensor, temperature: torch.Tensor,
+                     top_k: torch.Tensor, top_p: torch.Tensor, seed: torch.Tensor) -> torch.Tensor:
+    """gpu/sampling.rs:35-56 sample_topk per row over its top-K pool."""
+    B, K = vals.shape
+    out = torch.empty(B, dtype=torch.int32, device=vals.device)
+    rc = lib().zs_lane_sample_topk(ctx.h, vals.data_ptr(), idxs.data_ptr(), B, K, temperature.data_ptr(),
+                                   top_k.data_ptr(), top_p.data_ptr(), seed.data_ptr(), out.data_ptr(),
+                                   torch.cuda.current_stream(vals.device).cuda_stream)
+    _check(ctx.h, rc, "zs_lane_sample_topk")
+    return out
+
+
+def step_seed(base: int, gen_idx: int) -> int:
+    """gpu/sampling.rs:9."""
+    return int(lib().zs_step_seed(base & 0xFFFFFFFF, gen_idx & 0xFFFFFFFF))
