@@ -63,7 +63,7 @@ extern "C" void zs_ctx_destroy(zs_ctx* ctx) {
         if (ctx->events[i]) hipEventDestroy((hipEvent_t)ctx->events[i]);
     void* ptrs[] = {ctx->p_cnt, ctx->p_id, ctx->p_flags, ctx->p_y, ctx->cst, ctx->cs_key, ctx->cs_idx,
                     ctx->co_key, ctx->co_idx, ctx->rst, ctx->pairs, ctx->mask_scratch, ctx->spec_chunks,
-                    ctx->spec_rows};
+                    ctx->spec_rows, ctx->sub_mom, ctx->sub_sum, ctx->p_sub};
     for (void* p : ptrs)
         if (p) hipFree(p);
     hipSetDevice(dev);
@@ -83,6 +83,7 @@ extern "C" int zs_ctx_create(int device, uint32_t max_rows, uint32_t max_vocab, 
     ctx->max_rows = max_rows;
     ctx->max_vocab = max_vocab;
     ctx->max_chunks = (max_vocab + ZS_P1_CH - 1) / ZS_P1_CH;
+    ctx->max_subs = ctx->max_chunks * ZS_SUBS_PER_CHUNK;
     int ndev = 0;
     if (hipGetDeviceCount(&ndev) != hipSuccess || device < 0 || device >= ndev) {
         free(ctx);
@@ -106,6 +107,9 @@ extern "C" int zs_ctx_create(int device, uint32_t max_rows, uint32_t max_vocab, 
     if (!rc) rc = zs_alloc(ctx, &ctx->pairs, R * (size_t)max_vocab * 2);
     if (!rc) rc = zs_alloc(ctx, (uint32_t**)&ctx->mask_scratch, R);
     if (!rc) rc = zs_alloc(ctx, &ctx->spec_chunks, R * (2 * ZS_SPEC_KMAX + 1) * C);
+    if (!rc) rc = zs_alloc(ctx, &ctx->sub_mom, R * ctx->max_subs);
+    if (!rc) rc = zs_alloc(ctx, &ctx->sub_sum, R * ZS_NSUM * ctx->max_subs);
+    if (!rc) rc = zs_alloc(ctx, &ctx->p_sub, R * (ctx->max_subs + 1));
     if (!rc) rc = zs_alloc(ctx, &ctx->spec_rows, R);
     hipSetDevice(prev);
     if (rc) {

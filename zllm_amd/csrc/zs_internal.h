@@ -46,6 +46,37 @@ struct zs_chunk_stat {
     uint32_t s_full, o_full;
 };
 
+// Sub-chunks of 1024 logits: the unit of the parallel exact-sum rounds.
+// Sub-chunk j of pass-1 chunk c is the j-th float4 of every pass-1 thread.
+#define ZS_SUB 1024
+#define ZS_SUBS_PER_CHUNK (ZS_P1_CH / ZS_SUB)
+#define ZS_MAX_SUBS (ZS_MAX_VOCAB / ZS_SUB)
+
+// Approximate moments of a sub-chunk relative to its chunk's maxima (pass 1):
+// e1 = sum exp(x~ - obs_max_c), ed = sum (x~ - obs_max_c) exp(x~ - obs_max_c),
+// ez = sum exp(z - z_max_c).
+struct zs_sub_mom {
+    float e1, ed, ez, pad;
+};
+
+// Sums reproduced by the rounds.
+#define ZS_SUM_OBS_S 0
+#define ZS_SUM_SAMP_S 1
+#define ZS_SUM_OBS_H 2
+#define ZS_NSUM 3
+
+// Per (row, sum, sub-chunk): predicted grid exponent of the running sum at the
+// sub-chunk start and the sub-chunk's total increment on that grid.
+#define ZS_SF_FRAGILE 1u  // prediction unsafe (binade crossing nearby): process exactly
+#define ZS_SF_TIE 2u      // an exact half-way term met: process exactly
+#define ZS_SF_DONE 4u     // total valid
+struct zs_sub_sum {
+    int32_t eg;
+    uint32_t flags;
+    uint32_t total;
+    uint32_t pad;
+};
+
 // Row modes decided by the combine kernel.
 #define ZS_MODE_DONE 1u   // token final (greedy / non-finite / small path)
 #define ZS_MODE_BIG 2u    // big-row engine must run
@@ -68,6 +99,8 @@ struct zs_row_state {
     float obs_max;
     uint32_t obs_special; // lse is NaN (NaN / +inf / all -inf row)
     uint32_t obs_need;
+    uint32_t rounds;      // ZS_SUM_* bits computed by the parallel rounds
+    float samp_S;         // sampler softmax denominator (sampler.rs:68) when computed by the rounds
     float obs_S;          // sequential f32 sum (hallucination.rs:237-238, logprobs.rs:36)
     float obs_H;          // sequential f32 entropy (hallucination.rs:242-248)
     uint32_t n_cand;      // observer candidates by (x~ desc, id asc)
@@ -123,6 +156,10 @@ struct zs_ctx {
     zs_row_state* rst;
     uint32_t* pairs;       // big-row gather area [rows][max_vocab][2]
     void* mask_scratch;    // DFA mask staging
+    zs_sub_mom* sub_mom;         // [rows][max_subs]
+    zs_sub_sum* sub_sum;         // [rows][ZS_NSUM][max_subs]
+    uint32_t* p_sub;             // [rows][max_subs+1] patch index range per sub-chunk
+    uint32_t max_subs;
     zs_spec_chunk* spec_chunks;  // [rows][2*ZS_SPEC_KMAX+1][max_chunks]
     zs_spec_row* spec_rows;      // [rows]
     // profiling (zs_set_profiling)

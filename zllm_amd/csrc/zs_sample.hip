@@ -26,6 +26,7 @@
 #include "zs_internal.h"
 #include "zs_dev.h"
 #include "zs_seq.h"
+#include "zs_terms.h"
 
 struct zs_sargs {
     zs_batch b;
@@ -42,6 +43,10 @@ struct zs_sargs {
     uint32_t* pairs;
     uint32_t nch;
     uint32_t max_vocab;
+    zs_sub_mom* sub_mom;
+    zs_sub_sum* sub_sum;
+    uint32_t* p_sub;
+    uint32_t max_subs;
 };
 
 #define ZS_ST_LIMIT 0x100u
@@ -88,6 +93,8 @@ __global__ __launch_bounds__(ZS_PREP_NT) void zs_k_prep(zs_sargs a) {
             a.p_cnt[r] = 0;
             a.rst[r].status = ZS_ST_LIMIT;
         }
+        const uint32_t nsub = (V + ZS_SUB - 1) / ZS_SUB;
+        for (uint32_t j = threadIdx.x; j <= nsub; j += ZS_PREP_NT) a.p_sub[(size_t)r * (a.max_subs + 1) + j] = 0;
         return;
     }
     // gather entries with id < V
@@ -166,6 +173,16 @@ __global__ __launch_bounds__(ZS_PREP_NT) void zs_k_prep(zs_sargs a) {
         a.p_cnt[r] = base_out;
         a.rst[r].status = 0;
     }
+    // first patch of every sub-chunk (patch ids are sorted and unique)
+    __threadfence_block();
+    __syncthreads();
+    const uint32_t nsub = (V + ZS_SUB - 1) / ZS_SUB;
+    uint32_t* psub = a.p_sub + (size_t)r * (a.max_subs + 1);
+    for (uint32_t j = threadIdx.x; j <= nsub; j += ZS_PREP_NT) {
+        uint32_t lo = 0, hi = base_out, key = j * ZS_SUB;
+        while (lo < hi) { uint32_t mid = (lo + hi) >> 1; if (out_id[mid] < key) lo = mid + 1; else hi = mid; }
+        psub[j] = lo;
+    }
 }
 
 // ===========================================================================
@@ -173,6 +190,7 @@ __global__ __launch_bounds__(ZS_PREP_NT) void zs_k_prep(zs_sargs a) {
 // ===========================================================================
 #define P1_EPT 32
 
+#define P1_SUP 1024
 struct p1_shared {
     uint32_t hist[256];
     uint32_t u[8];
@@ -182,6 +200,10 @@ struct p1_shared {
     uint32_t cnt;
     uint32_t prefix, need, found;
     uint32_t pcur0, pcur1;
+    uint32_t tmax[ZS_P1_NT];
+    uint32_t skey[P1_SUP];
+    uint32_t sidx[P1_SUP];
+    uint32_t sel[4];
 };
 
 // Exact top-K (key desc, index asc) of the chunk's valid keys; writes the
@@ -298,6 +320,101 @@ __device__ void p1_topk(const uint32_t (&key)[P1_EPT], uint32_t vmask, uint32_t 
     __syncthreads();
 }
 
+
+// Fast exact top-K: the K-th largest of the 256 per-thread maxima is a lower
+// bound theta of the chunk's K-th largest key, so the elements >= theta (a
+// small superset) contain the top-K. One wave selects inside the superset by
+// binary search over key bits (ballot counts); degenerate chunks whose
+// superset exceeds P1_SUP fall back to the LDS radix select.
+__device__ __forceinline__ uint32_t p1_wave_count_ge(const uint32_t* a, uint32_t n, uint32_t v) {
+    uint32_t c = 0;
+    for (uint32_t i = zs_lane(); i < n; i += 64) c += a[i] >= v ? 1u : 0u;
+    return wave_sum_u(c);
+}
+__device__ void p1_topk_fast(const uint32_t (&key)[P1_EPT], uint32_t vmask, uint32_t K, uint32_t base,
+                             uint32_t* out_key, uint32_t* out_idx, uint32_t* n_out, uint32_t* kth,
+                             uint32_t* full, p1_shared& sh) {
+    const int t = threadIdx.x;
+    uint32_t tm = 0;
+    bool anyv = false;
+#pragma unroll
+    for (int e = 0; e < P1_EPT; e++)
+        if ((vmask >> e) & 1u) { tm = max(tm, key[e]); anyv = true; }
+    uint32_t nvalid = block_sum_u<ZS_P1_NT>(__popc(vmask), sh.u);
+    if (nvalid <= K || K > ZS_P1_NT) {
+        p1_topk(key, vmask, K, base, out_key, out_idx, n_out, kth, full, sh);
+        return;
+    }
+    sh.tmax[t] = anyv ? tm : 0u;
+    __syncthreads();
+    if (t < 64) {
+        // theta = K-th largest thread maximum (threads without elements hold 0)
+        uint32_t pre = 0;
+        for (int bit = 31; bit >= 0; bit--) {
+            uint32_t cand = pre | (1u << bit);
+            if (p1_wave_count_ge(sh.tmax, ZS_P1_NT, cand) >= K) pre = cand;
+        }
+        if (t == 0) sh.sel[0] = pre;
+    }
+    __syncthreads();
+    const uint32_t theta = sh.sel[0];
+    uint32_t c = 0;
+#pragma unroll
+    for (int e = 0; e < P1_EPT; e++) c += (((vmask >> e) & 1u) && key[e] >= theta) ? 1u : 0u;
+    uint32_t nsup;
+    uint32_t pos = block_excl_scan_u<ZS_P1_NT>(c, sh.u, &nsup);
+    if (nsup > P1_SUP) {
+        p1_topk(key, vmask, K, base, out_key, out_idx, n_out, kth, full, sh);
+        return;
+    }
+#pragma unroll
+    for (int e = 0; e < P1_EPT; e++) {
+        if (((vmask >> e) & 1u) && key[e] >= theta) {
+            sh.skey[pos] = key[e];
+            sh.sidx[pos] = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
+            pos++;
+        }
+    }
+    __syncthreads();
+    if (t < 64) {
+        // K-th largest key of the superset, then the need-th smallest id among its ties
+        uint32_t kk = 0;
+        for (int bit = 31; bit >= 0; bit--) {
+            uint32_t cand = kk | (1u << bit);
+            if (p1_wave_count_ge(sh.skey, nsup, cand) >= K) kk = cand;
+        }
+        uint32_t gt = 0, eq = 0;
+        for (uint32_t i = t; i < nsup; i += 64) { gt += sh.skey[i] > kk; eq += sh.skey[i] == kk; }
+        gt = wave_sum_u(gt);
+        eq = wave_sum_u(eq);
+        uint32_t need = K - gt;
+        // smallest id I with #(key == kk && id <= I) >= need
+        uint32_t lo = 0;
+        for (int bit = 31; bit >= 0; bit--) {
+            uint32_t cand = lo | (1u << bit);  // test: count(id < cand) < need  => id bound >= cand
+            uint32_t cc = 0;
+            for (uint32_t i = t; i < nsup; i += 64) cc += (sh.skey[i] == kk && sh.sidx[i] < cand) ? 1u : 0u;
+            if (wave_sum_u(cc) < need) lo = cand;
+        }
+        if (t == 0) { sh.sel[1] = kk; sh.sel[2] = lo; sh.sel[3] = eq > need ? 2u : 1u; }
+    }
+    if (t == 0) sh.cnt = 0;
+    __syncthreads();
+    const uint32_t kk = sh.sel[1], ilim = sh.sel[2];
+    for (uint32_t i = t; i < nsup; i += ZS_P1_NT) {
+        uint32_t k = sh.skey[i], id = sh.sidx[i];
+        if (k > kk || (k == kk && id <= ilim)) {
+            uint32_t p = atomicAdd(&sh.cnt, 1u);
+            if (p < K) { out_key[p] = k; out_idx[p] = id; }
+        }
+    }
+    __syncthreads();
+    *n_out = min(sh.cnt, K);
+    *kth = kk;
+    *full = sh.sel[3];
+    __syncthreads();
+}
+
 __global__ __launch_bounds__(ZS_P1_NT) void zs_k_pass1(zs_sargs a) {
     const uint32_t c = blockIdx.x, r = blockIdx.y;
     const zs_batch& b = a.b;
@@ -406,6 +523,7 @@ __global__ __launch_bounds__(ZS_P1_NT) void zs_k_pass1(zs_sargs a) {
     // 64-bit composites picks the larger value, then the larger index.
     unsigned long long best_all = 0, best_tail = 0;
     int tail_n = 0;
+    if (T <= 0.0f) {  // greedy rows only (uniform per workgroup)
     for (int e = 0; e < P1_EPT; e++) {
         if (!((vmask >> e) & 1u)) continue;
         float z = zv[e];
@@ -438,6 +556,63 @@ __global__ __launch_bounds__(ZS_P1_NT) void zs_k_pass1(zs_sargs a) {
         __syncthreads();
     }
     tail_n = (int)block_sum_u<ZS_P1_NT>((uint32_t)tail_n, sh.u);
+    }
+
+    // ---- approximate moments per 1024-logit sub-chunk (predictions for the
+    // exact-sum rounds): sub j of this chunk is the j-th float4 of every thread
+    {
+        const bool om = (P.flags & (ZS_ROW_LOGPROBS | ZS_ROW_UNCERTAINTY)) && omax > -INFINITY && omax < INFINITY;
+        const bool zm = T > 0.0f && zmax > -INFINITY && zmax < INFINITY;
+        __shared__ float msh[ZS_P1_NT / 64][ZS_SUBS_PER_CHUNK][3];
+        float m1[ZS_SUBS_PER_CHUNK], md[ZS_SUBS_PER_CHUNK], mz[ZS_SUBS_PER_CHUNK];
+        // bit 2j: sub j holds the chunk's observer max, bit 2j+1: its sampler max
+        uint32_t hasmax = 0;
+#pragma unroll
+        for (int j = 0; j < ZS_SUBS_PER_CHUNK; j++) {
+            m1[j] = md[j] = mz[j] = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int e = j * 4 + q;
+                if (!((vmask >> e) & 1u)) continue;
+                if (xo[e] == omax) hasmax |= 1u << (2 * j);
+                if (zv[e] == zmax) hasmax |= 2u << (2 * j);
+                if (om) {
+                    float d = xo[e] - omax;
+                    if (d > -INFINITY) { float ex = __expf(d); m1[j] += ex; md[j] += d * ex; }
+                }
+                if (zm) {
+                    float d = zv[e] - zmax;
+                    if (d > -INFINITY) mz[j] += __expf(d);
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < ZS_SUBS_PER_CHUNK; j++) {
+            for (int d = 32; d > 0; d >>= 1) {
+                m1[j] += __shfl_xor(m1[j], d, 64);
+                md[j] += __shfl_xor(md[j], d, 64);
+                mz[j] += __shfl_xor(mz[j], d, 64);
+            }
+            if (zs_lane() == 0) { msh[zs_wid()][j][0] = m1[j]; msh[zs_wid()][j][1] = md[j]; msh[zs_wid()][j][2] = mz[j]; }
+        }
+        for (int d = 32; d > 0; d >>= 1) hasmax |= __shfl_xor(hasmax, d, 64);
+        __shared__ uint32_t hsh[ZS_P1_NT / 64];
+        if (zs_lane() == 0) hsh[zs_wid()] = hasmax;
+        __syncthreads();
+        if (t < ZS_SUBS_PER_CHUNK) {
+            zs_sub_mom mm;
+            mm.e1 = mm.ed = mm.ez = 0.0f;
+            uint32_t hm = 0;
+            for (int w = 0; w < ZS_P1_NT / 64; w++) {
+                mm.e1 += msh[w][t][0]; mm.ed += msh[w][t][1]; mm.ez += msh[w][t][2];
+                hm |= hsh[w];
+            }
+            mm.pad = zs_u2f((hm >> (2 * t)) & 3u);
+            const uint32_t sub = c * ZS_SUBS_PER_CHUNK + t;
+            if (sub * ZS_SUB < V) a.sub_mom[(size_t)r * a.max_subs + sub] = mm;
+        }
+        __syncthreads();
+    }
 
     // ---- candidate lists
     uint32_t key[P1_EPT];
@@ -448,16 +623,20 @@ __global__ __launch_bounds__(ZS_P1_NT) void zs_k_pass1(zs_sargs a) {
 #pragma unroll
     for (int e = 0; e < P1_EPT; e++) key[e] = zs_total_key(zv[e]);
     uint32_t ns, s_kth, s_full;
-    p1_topk(key, vmask, Ks, base, a.cs_key + lofs * ZS_KS, a.cs_idx + lofs * ZS_KS, &ns, &s_kth,
-            &s_full, sh);
+    ns = s_kth = s_full = 0;
+    if (T > 0.0f)
+        p1_topk_fast(key, vmask, Ks, base, a.cs_key + lofs * ZS_KS, a.cs_idx + lofs * ZS_KS, &ns, &s_kth,
+                     &s_full, sh);
     uint32_t ntl = P.top_logprobs > 20 ? 20 : P.top_logprobs;
     uint32_t Ko = ntl + 8;
     if (Ko > ZS_KO) Ko = ZS_KO;
 #pragma unroll
     for (int e = 0; e < P1_EPT; e++) key[e] = zs_total_key(xo[e]);
     uint32_t no, o_kth, o_full;
-    p1_topk(key, vmask, Ko, base, a.co_key + lofs * ZS_KO, a.co_idx + lofs * ZS_KO, &no, &o_kth,
-            &o_full, sh);
+    no = o_kth = o_full = 0;
+    if (P.flags & (ZS_ROW_LOGPROBS | ZS_ROW_UNCERTAINTY))
+        p1_topk_fast(key, vmask, Ko, base, a.co_key + lofs * ZS_KO, a.co_idx + lofs * ZS_KO, &no, &o_kth,
+                     &o_full, sh);
 
     if (t == 0) {
         zs_chunk_stat cs;
@@ -484,6 +663,62 @@ __global__ __launch_bounds__(ZS_P1_NT) void zs_k_pass1(zs_sargs a) {
 // ===========================================================================
 // zs_k_combine
 // ===========================================================================
+
+// Predicted grid of a sequential sum at each sub-chunk start from approximate
+// sub-chunk sums A_j (one wave, 4 sub-chunks per lane). A sub-chunk is fragile
+// -- processed exactly by the stitch -- when the running sum may leave its
+// binade inside it or sits too close to a binade edge for the prediction to be
+// trusted (the f32 sum differs from the exact prefix by far less than 2^-8).
+// ONE(j) tells whether sub-chunk j holds the term exp(0) = 1 exactly: an f32
+// running sum of non-negative terms never decreases, so once that term is in,
+// the sum is >= 1 and the lower edge of [1, 2) cannot be crossed -- without
+// this, the common peaked rows (sum just above 1) would be fragile throughout.
+// A misprediction only costs an exact pass: the stitch checks every grid.
+template <class F, class G>
+__device__ void zs_predict_subs(zs_sub_sum* out, uint32_t nsub, const F& A, const G& ONE, bool all_fragile) {
+    const int lane = zs_lane();
+    double v[4], loc = 0.0;
+    int j1 = ZS_BIGI;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        uint32_t j = 4 * lane + q;
+        v[q] = j < nsub ? A(j) : 0.0;
+        loc += v[q];
+        if (j < nsub && j1 == ZS_BIGI && ONE(j)) j1 = (int)j;
+    }
+    j1 = wave_min_i(j1);
+    double inc = loc;
+    for (int d = 1; d < 64; d <<= 1) {
+        double y = __shfl_up(inc, d, 64);
+        if (lane >= d) inc += y;
+    }
+    double run = inc - loc;
+    const double delta = 1.0 / 256.0;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        uint32_t j = 4 * lane + q;
+        double lo = run, hi = run + v[q];
+        run = hi;
+        if (j >= nsub) continue;
+        zs_sub_sum e;
+        double lm = lo * (1.0 - delta), hm = hi * (1.0 + delta);
+        if ((int)j > j1) {
+            lm = fmax(lm, 1.0);
+            lo = fmax(lo, 1.0);
+        }
+        // every sum below 2^-125 lies on the finest grid (2^-149), so tiny
+        // prefixes share one binade
+        const int blo = lm < 0x1p-125 ? -125 : ilogb(lm);
+        const int bhi = hm < 0x1p-125 ? -125 : ilogb(hm);
+        bool fragile = all_fragile || !(lm >= 0.0) || blo != bhi || !(hm < 3.0e38);
+        e.eg = fragile ? 0 : zs_grid_exp((float)lo);
+        e.flags = fragile ? ZS_SF_FRAGILE : 0u;
+        e.total = 0;
+        e.pad = 0;
+        out[j] = e;
+    }
+}
+
 #define CB_NT 256
 #define ZS_SMALL_CAP 512
 
@@ -530,7 +765,7 @@ __device__ uint32_t small_path_sample(const zs_sargs& a, uint32_t r, const zs_ro
         float pm = 0.0f;
 #pragma unroll
         for (int j = 0; j < SP_EPT; j++) pm = fmaxf(pm, p[j]);
-        pm = block_max_f<CB_NT>(pm, reinterpret_cast<float*>(sq.scan));
+        pm = block_max_f<CB_NT>(pm, reinterpret_cast<float*>(sq.a));
         float cut = P.min_p * pm;
         float tv[SP_EPT];
 #pragma unroll
@@ -619,6 +854,7 @@ __global__ __launch_bounds__(CB_NT) void zs_k_combine(zs_sargs a) {
             st.mode = ZS_MODE_DONE;
             st.token = 0xffffffffu;
             st.obs_need = 0;
+            st.rounds = 0;
             st.n_cand = 0;
             a.rst[r] = st;
         }
@@ -671,7 +907,7 @@ __global__ __launch_bounds__(CB_NT) void zs_k_combine(zs_sargs a) {
         const uint32_t np = a.p_cnt[r];
         const uint32_t* pfl = a.p_flags + (size_t)r * ZS_MAX_PATCHES;
         for (uint32_t i = t; i < np; i += CB_NT) has_y |= (pfl[i] & ZS_PF_Y) ? 1u : 0u;
-        has_y = block_or_u<CB_NT>(has_y, reinterpret_cast<uint32_t*>(sq.scan));
+        has_y = block_or_u<CB_NT>(has_y, sq.a);
     }
     const uint32_t z_is_x = (P.temperature == 1.0f && !has_y) ? 1u : 0u;
 
@@ -777,7 +1013,42 @@ __global__ __launch_bounds__(CB_NT) void zs_k_combine(zs_sargs a) {
         }
         if (!small) mode = ZS_MODE_BIG;
     }
+    // ---- predictions for the parallel exact-sum rounds
+    uint32_t rounds = 0;
+    {
+        const uint32_t nsub = (V + ZS_SUB - 1) / ZS_SUB;
+        const zs_sub_mom* mom = a.sub_mom + (size_t)r * a.max_subs;
+        if (obs_need & ZS_OBS_S) {
+            rounds |= 1u << ZS_SUM_OBS_S;
+            if (t < 64)
+                zs_predict_subs(a.sub_sum + ((size_t)r * ZS_NSUM + ZS_SUM_OBS_S) * a.max_subs, nsub,
+                                [&](uint32_t j) {
+                                    float mc = cs[j / ZS_SUBS_PER_CHUNK].obs_max;
+                                    return (double)mom[j].e1 * exp((double)mc - (double)M);
+                                },
+                                [&](uint32_t j) {
+                                    return (zs_f2u(mom[j].pad) & 1u) && cs[j / ZS_SUBS_PER_CHUNK].obs_max == M;
+                                },
+                                false);
+        }
+        const bool reuse = z_is_x && !has_thr && (obs_need & ZS_OBS_S);
+        if (mode == ZS_MODE_BIG && !reuse && has_thr != 2) {  // has_thr 2: threshold found later
+            rounds |= 1u << ZS_SUM_SAMP_S;
+            if (t < 64)
+                zs_predict_subs(a.sub_sum + ((size_t)r * ZS_NSUM + ZS_SUM_SAMP_S) * a.max_subs, nsub,
+                                [&](uint32_t j) {
+                                    float mc = cs[j / ZS_SUBS_PER_CHUNK].z_max;
+                                    return mc > -INFINITY ? (double)mom[j].ez * exp((double)mc - (double)zmax) : 0.0;
+                                },
+                                [&](uint32_t j) {
+                                    return (zs_f2u(mom[j].pad) & 2u) && cs[j / ZS_SUBS_PER_CHUNK].z_max == zmax;
+                                },
+                                has_thr != 0);
+        }
+        if (obs_need & ZS_OBS_H) rounds |= 1u << ZS_SUM_OBS_H;
+    }
     if (t == 0) {
+        st.rounds = rounds;
         st.z_max = zmax;
         st.has_thr = has_thr;
         st.thr_key = thr_key;
@@ -791,6 +1062,358 @@ __global__ __launch_bounds__(CB_NT) void zs_k_combine(zs_sargs a) {
         for (uint32_t j = 0; j < n_cand; j++) { st.cand_id[j] = cid_sh[j]; st.cand_x[j] = cx_sh[j]; }
         st.z_is_x = z_is_x;
         a.rst[r] = st;
+    }
+}
+
+
+// ===========================================================================
+// Parallel exact-sum rounds. A round kernel gives every 1024-logit sub-chunk
+// its total increment on the predicted grid (one wave per sub-chunk, all CUs);
+// a stitch kernel walks a row's sub-chunks in order with the exact running sum,
+// accepting a total when the prediction holds and recomputing the sub-chunk
+// with the exact wave-level scan otherwise. Observer sums (tolerance outputs)
+// take increments from the fast exp; the sampler sum uses certified ones.
+// ===========================================================================
+struct sub_row {
+    const float* row;
+    const uint32_t* allow;
+    const uint32_t* pid;
+    const uint32_t* pfl;
+    const float* py;
+    const uint32_t* psub;
+    uint32_t V;
+    float T;
+    bool masked;
+};
+
+__device__ __forceinline__ sub_row make_sub_row(const zs_sargs& a, uint32_t r, const zs_row_params& P) {
+    const zs_batch& b = a.b;
+    sub_row R;
+    R.row = b.d_logits + (size_t)r * b.ld;
+    R.masked = (P.flags & ZS_ROW_MASKED) && b.d_allow_bits;
+    R.allow = R.masked ? b.d_allow_bits + (size_t)r * b.allow_words : nullptr;
+    R.pid = a.p_id + (size_t)r * ZS_MAX_PATCHES;
+    R.pfl = a.p_flags + (size_t)r * ZS_MAX_PATCHES;
+    R.py = a.p_y + (size_t)r * ZS_MAX_PATCHES;
+    R.psub = a.p_sub + (size_t)r * (a.max_subs + 1);
+    R.V = b.V;
+    R.T = P.temperature;
+    return R;
+}
+
+// thread t holds elements j*1024 + EPT*t .. +EPT-1 of sub-chunk j
+// (EPT * threads = 1024; EPT is 8 or 16)
+template <int EPT>
+__device__ __forceinline__ void sub_load_t(const sub_row& R, uint32_t j, uint32_t t, float (&x)[EPT], float (&z)[EPT]) {
+    const uint32_t base = j * ZS_SUB + (uint32_t)EPT * t;
+    uint32_t w = 0xffffffffu;
+    if (R.masked && base < R.V) w = R.allow[base >> 5] >> (base & 31);
+#pragma unroll
+    for (int k = 0; k < EPT / 4; k++) {
+        float4 v = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+        if (base + 4 * k < R.V) v = *reinterpret_cast<const float4*>(R.row + base + 4 * k);
+        x[4 * k] = v.x; x[4 * k + 1] = v.y; x[4 * k + 2] = v.z; x[4 * k + 3] = v.w;
+    }
+#pragma unroll
+    for (int q = 0; q < EPT; q++) {
+        if (base + q >= R.V || (R.masked && !((w >> q) & 1u))) x[q] = -INFINITY;
+        z[q] = x[q];
+    }
+    const uint32_t p0 = R.psub[j], p1 = R.psub[j + 1];
+    for (uint32_t p = p0; p < p1; p++) {
+        uint32_t off = R.pid[p] - base;
+        if (off < (uint32_t)EPT) {
+            uint32_t fl = R.pfl[p];
+            float py = R.py[p];
+#pragma unroll
+            for (int q = 0; q < EPT; q++) {
+                if ((uint32_t)q != off) continue;
+                if (fl & ZS_PF_BAN) { x[q] = -INFINITY; z[q] = -INFINITY; }
+                if (fl & ZS_PF_Y) z[q] = py;
+            }
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < EPT; q++) z[q] = zs_temper(z[q], R.T);
+}
+
+// lane l of the wave holds elements j*1024 + 16l .. +15 of sub-chunk j
+__device__ __forceinline__ void sub_load(const sub_row& R, uint32_t j, float (&x)[16], float (&z)[16]) {
+    sub_load_t<16>(R, j, (uint32_t)zs_lane(), x, z);
+}
+
+__device__ __forceinline__ uint32_t wave_sum_sat(uint32_t v) {
+    for (int d = 32; d > 0; d >>= 1) v = zs_sat_add(v, __shfl_xor(v, d, 64));
+    return v;
+}
+
+// approximate exp for the observer sums
+__device__ __forceinline__ float zs_exp_obs(float d) {
+    if (d >= ZS_EXP_FAST_MIN) return zs_exp_fast(d);
+    return d < ZS_EXP_ZERO ? 0.0f : zs_expf(d);
+}
+
+// observer terms with approximate values (tolerance outputs): the exact
+// machinery is still applied to these values, so only terms whose fast-exp
+// rounding differs move the sum, by a grid unit each
+template <int EPT>
+struct obs_exp_terms {
+    float a[EPT];
+    __device__ __forceinline__ void inc(int j, int eg, uint32_t* ie, uint32_t* io) const {
+        seq_pair p = seq_pair_of(zs_pick(a, j), eg);
+        *ie = p.e;
+        *io = p.o;
+    }
+    __device__ __forceinline__ float val(int j) const { return zs_pick(a, j); }
+};
+
+__global__ __launch_bounds__(256) void zs_k_roundA(zs_sargs a) {
+    const uint32_t r = blockIdx.y;
+    const uint32_t j = blockIdx.x * 4 + zs_wid();
+    const zs_row_state* st = a.rst + r;
+    const uint32_t rounds = st->rounds;
+    if (!(rounds & ((1u << ZS_SUM_OBS_S) | (1u << ZS_SUM_SAMP_S)))) return;
+    const uint32_t V = a.b.V;
+    const uint32_t nsub = (V + ZS_SUB - 1) / ZS_SUB;
+    if (j >= nsub) return;
+    const zs_row_params P = a.b.d_params[r];
+    sub_row R = make_sub_row(a, r, P);
+    zs_sub_sum* ss = a.sub_sum + (size_t)r * ZS_NSUM * a.max_subs;
+    const bool do_obs = (rounds >> ZS_SUM_OBS_S) & 1u;
+    const bool do_samp = (rounds >> ZS_SUM_SAMP_S) & 1u;
+    zs_sub_sum eo = ss[ZS_SUM_OBS_S * a.max_subs + j];
+    zs_sub_sum es = ss[ZS_SUM_SAMP_S * a.max_subs + j];
+    const bool need_o = do_obs && !(eo.flags & ZS_SF_FRAGILE);
+    const bool need_s = do_samp && !(es.flags & ZS_SF_FRAGILE);
+    if (!need_o && !need_s) return;
+    float x[16], z[16];
+    sub_load(R, j, x, z);
+    if (need_o) {
+        const float M = st->obs_max;
+        uint32_t tot = 0;
+#pragma unroll
+        for (int q = 0; q < 16; q++) {
+            uint32_t tie;
+            tot = zs_sat_add(tot, zs_seq_inc(zs_exp_obs(x[q] - M), eo.eg, &tie));
+        }
+        tot = wave_sum_sat(tot);
+        if (zs_lane() == 0) {
+            zs_sub_sum& o = ss[ZS_SUM_OBS_S * a.max_subs + j];
+            o.total = tot;
+            o.flags = eo.flags | ZS_SF_DONE;
+        }
+    }
+    if (need_s) {
+        const float m = st->z_max;
+        const bool use_thr = st->has_thr != 0;
+        const float thr = zs_key_to_float(st->thr_key);
+        exp_terms<16> f;
+#pragma unroll
+        for (int q = 0; q < 16; q++) f.set(q, (use_thr && z[q] < thr) ? -INFINITY : z[q] - m);
+        uint32_t tot = 0, tie = 0;
+#pragma unroll
+        for (int q = 0; q < 16; q++) {
+            uint32_t ie, io;
+            f.inc(q, es.eg, &ie, &io);
+            if (ie != io) tie = 1;
+            tot = zs_sat_add(tot, ie);
+        }
+        tot = wave_sum_sat(tot);
+        tie = wave_or_u(tie);
+        if (zs_lane() == 0) {
+            zs_sub_sum& o = ss[ZS_SUM_SAMP_S * a.max_subs + j];
+            o.total = tot;
+            o.flags = es.flags | ZS_SF_DONE | (tie ? ZS_SF_TIE : 0u);
+        }
+    }
+}
+
+// H = -sum p (d - ln S) terms with the fast exp (tolerance output)
+__device__ __forceinline__ float zs_ent_obs(float d, float inv, float lns) {
+    float p = zs_exp_obs(d) * inv;
+    if (!(p > 0.0f)) return 0.0f;
+    return -(p * (d - lns));
+}
+
+template <int EPT>
+struct obs_ent_terms {
+    float a[EPT];
+    __device__ __forceinline__ void inc(int j, int eg, uint32_t* ie, uint32_t* io) const {
+        seq_pair p = seq_pair_of(zs_pick(a, j), eg);
+        *ie = p.e;
+        *io = p.o;
+    }
+    __device__ __forceinline__ float val(int j) const { return zs_pick(a, j); }
+};
+
+__global__ __launch_bounds__(256) void zs_k_roundB(zs_sargs a) {
+    const uint32_t r = blockIdx.y;
+    const uint32_t j = blockIdx.x * 4 + zs_wid();
+    const zs_row_state* st = a.rst + r;
+    if (!((st->rounds >> ZS_SUM_OBS_H) & 1u)) return;
+    const uint32_t V = a.b.V;
+    const uint32_t nsub = (V + ZS_SUB - 1) / ZS_SUB;
+    if (j >= nsub) return;
+    zs_sub_sum* ss = a.sub_sum + ((size_t)r * ZS_NSUM + ZS_SUM_OBS_H) * a.max_subs;
+    zs_sub_sum e = ss[j];
+    if (e.flags & ZS_SF_FRAGILE) return;
+    const zs_row_params P = a.b.d_params[r];
+    sub_row R = make_sub_row(a, r, P);
+    float x[16], z[16];
+    sub_load(R, j, x, z);
+    const float M = st->obs_max, S = st->obs_S;
+    const float inv = 1.0f / S, lns = (float)log((double)S);
+    uint32_t tot = 0;
+#pragma unroll
+    for (int q = 0; q < 16; q++) {
+        uint32_t tie;
+        tot = zs_sat_add(tot, zs_seq_inc(zs_ent_obs(x[q] - M, inv, lns), e.eg, &tie));
+    }
+    tot = wave_sum_sat(tot);
+    if (zs_lane() == 0) {
+        ss[j].total = tot;
+        ss[j].flags = e.flags | ZS_SF_DONE;
+    }
+}
+
+#define ST_NT 128
+#define ST_EPT (ZS_SUB / ST_NT)
+
+struct st_sh {
+    seq_sh<ST_NT> seq;
+    float head[64];
+    zs_sub_sum rec[ZS_MAX_SUBS];
+};
+
+// Exact processing of one sub-chunk by the workgroup: the first 64 terms of a
+// sum that starts at zero are added serially by thread 0 (the running sum
+// crosses many binades there), the rest with the increment scan.
+template <class F>
+__device__ __forceinline__ void stitch_sub(const F& f, float& s, bool first, st_sh& sh) {
+    int start = 0;
+    if (first) {
+        const int t = threadIdx.x;
+        if (t < 64 / ST_EPT) {
+#pragma unroll
+            for (int q = 0; q < ST_EPT; q++) sh.head[ST_EPT * t + q] = f.val(q);
+        }
+        __syncthreads();
+        if (t == 0) {
+            float acc = s;
+            for (int i = 0; i < 64; i++) acc = acc + sh.head[i];
+            sh.seq.s = acc;
+        }
+        __syncthreads();
+        s = sh.seq.s;
+        __syncthreads();
+        start = 64;
+    }
+    seq_group_f<ST_NT, ST_EPT>(f, start, s, NAN, sh.seq);
+}
+
+// One workgroup per (row, sum): the exact running sum over the row's
+// sub-chunks, taking the rounds' totals where the predicted grid holds.
+template <int KIND>
+__global__ __launch_bounds__(ST_NT) void zs_k_stitch(zs_sargs a) {
+    const uint32_t r = blockIdx.x;
+    zs_row_state* st = a.rst + r;
+    const uint32_t rounds = st->rounds;
+    if (!((rounds >> KIND) & 1u)) return;
+    __shared__ st_sh sh;
+    const uint32_t t = threadIdx.x;
+    const uint32_t V = a.b.V;
+    const uint32_t nsub = (V + ZS_SUB - 1) / ZS_SUB;
+    const zs_row_params P = a.b.d_params[r];
+    sub_row R = make_sub_row(a, r, P);
+    const zs_sub_sum* ss = a.sub_sum + ((size_t)r * ZS_NSUM + KIND) * a.max_subs;
+    for (uint32_t j = t; j < nsub; j += ST_NT) sh.rec[j] = ss[j];
+    __syncthreads();
+    const float M = st->obs_max, m = st->z_max;
+    const bool use_thr = st->has_thr != 0;
+    const float thr = zs_key_to_float(st->thr_key);
+    float inv = 0.0f, lns = 0.0f;
+    if (KIND == ZS_SUM_OBS_H) {
+        inv = 1.0f / st->obs_S;
+        lns = (float)log((double)st->obs_S);
+    }
+    float s = KIND == ZS_SUM_OBS_H ? 0.0f : -0.0f;
+#ifdef ZS_DEBUG_STITCH
+    uint32_t nfr = 0, nmis = 0, novf = 0, ntie = 0;
+    long long c_load = 0, c_seq = 0, c_all = clock64();
+#endif
+    for (uint32_t j = 0; j < nsub; j++) {
+        const zs_sub_sum e = sh.rec[j];
+        const int eg = zs_grid_exp(s);
+        const uint32_t k0 = zs_grid_k(s);
+        if ((e.flags & ZS_SF_DONE) && !(e.flags & (ZS_SF_FRAGILE | ZS_SF_TIE)) && e.eg == eg &&
+            k0 + e.total < ZS_BINADE) {
+            s = zs_grid_value(k0 + e.total, eg);
+            continue;
+        }
+#ifdef ZS_DEBUG_STITCH
+        if (e.flags & ZS_SF_FRAGILE) nfr++;
+        else if (e.flags & ZS_SF_TIE) ntie++;
+        else if (e.eg != eg) nmis++;
+        else novf++;
+#endif
+        const bool first = (j == 0);
+        float x[ST_EPT], z[ST_EPT];
+#ifdef ZS_DEBUG_STITCH
+        long long c0 = clock64();
+#endif
+        sub_load_t<ST_EPT>(R, j, t, x, z);
+#ifdef ZS_DEBUG_STITCH
+        long long c1 = clock64();
+        c_load += c1 - c0;
+#endif
+        if (KIND == ZS_SUM_OBS_S) {
+            obs_exp_terms<ST_EPT> f;
+#pragma unroll
+            for (int q = 0; q < ST_EPT; q++) f.a[q] = zs_exp_obs(x[q] - M);
+            stitch_sub(f, s, first, sh);
+        } else if (KIND == ZS_SUM_SAMP_S) {
+            exp_terms<ST_EPT> f;
+#pragma unroll
+            for (int q = 0; q < ST_EPT; q++) f.set(q, (use_thr && z[q] < thr) ? -INFINITY : z[q] - m);
+            stitch_sub(f, s, first, sh);
+        } else {
+            obs_ent_terms<ST_EPT> f;
+#pragma unroll
+            for (int q = 0; q < ST_EPT; q++) f.a[q] = zs_ent_obs(x[q] - M, inv, lns);
+            stitch_sub(f, s, first, sh);
+        }
+#ifdef ZS_DEBUG_STITCH
+        c_seq += clock64() - c1;
+#endif
+    }
+#ifdef ZS_DEBUG_STITCH
+    c_all = clock64() - c_all;
+    if (t == 0) printf("stitch row %u kind %d nsub %u fragile %u tie %u mispred %u ovf %u  clk all %lld load %lld seq %lld M %g m %g s %a masked %d T %g\n", r, KIND, nsub, nfr, ntie, nmis, novf, c_all, c_load, c_seq, M, m, s, (int)R.masked, R.T);
+#endif
+    if (KIND == ZS_SUM_OBS_S) {
+        if (t == 0) st->obs_S = s;
+        if (((rounds >> ZS_SUM_OBS_H) & 1u) && t < 64) {
+            // predictions for the entropy sum: p = e * inv, term = p (ln S - d)
+            const float iv = 1.0f / s;
+            const double ls = log((double)s);
+            const zs_sub_mom* mom = a.sub_mom + (size_t)r * a.max_subs;
+            const zs_chunk_stat* cs = a.cst + (size_t)r * a.nch;
+            zs_predict_subs(a.sub_sum + ((size_t)r * ZS_NSUM + ZS_SUM_OBS_H) * a.max_subs, nsub,
+                            [&](uint32_t jj) {
+                                double mc = (double)cs[jj / ZS_SUBS_PER_CHUNK].obs_max;
+                                double sc = exp(mc - (double)M);
+                                double e1 = (double)mom[jj].e1 * sc;
+                                double ed = ((double)mom[jj].ed + (mc - (double)M) * (double)mom[jj].e1) * sc;
+                                double v = (double)iv * (ls * e1 - ed);
+                                return v > 0.0 ? v : 0.0;
+                            },
+                            [](uint32_t) { return false; },
+                            false);
+        }
+    } else if (KIND == ZS_SUM_SAMP_S) {
+        if (t == 0) st->samp_S = s;
+    } else {
+        if (t == 0) st->obs_H = s;
     }
 }
 
@@ -820,8 +1443,10 @@ struct big_row {
 };
 
 // z for the 4 elements idx0..idx0+3 of group g (patch cursor in sh.pc0/pc1).
-// obs = true: the observers' x~ (mask and bans only); false: the sampler's z.
-__device__ __forceinline__ void big_load(const big_row& R, uint32_t g, float (&z)[4], big_shared& sh, bool obs) {
+// x~ (observers: mask and bans) and z (sampler: patched y, divided by T) of the
+// 4 elements idx0..idx0+3 of group g; the patch cursor advances in sh.pc0/pc1.
+__device__ __forceinline__ void big_load2(const big_row& R, uint32_t g, float (&x)[4], float (&z)[4],
+                                          big_shared& sh) {
     const int t = threadIdx.x;
     const uint32_t g0 = g * ZS_BIG_G;
     if (t == 0) {
@@ -841,31 +1466,37 @@ __device__ __forceinline__ void big_load(const big_row& R, uint32_t g, float (&z
         v = *reinterpret_cast<const float4*>(R.row + idx0);
         if (R.masked) w = R.allow[idx0 >> 5] >> (idx0 & 31);
     }
-    z[0] = v.x; z[1] = v.y; z[2] = v.z; z[3] = v.w;
+    x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
 #pragma unroll
     for (int q = 0; q < 4; q++) {
-        if (idx0 + q >= R.V) z[q] = -INFINITY;
-        else if (R.masked && !((w >> q) & 1u)) z[q] = -INFINITY;
+        if (idx0 + q >= R.V) x[q] = -INFINITY;
+        else if (R.masked && !((w >> q) & 1u)) x[q] = -INFINITY;
+        z[q] = x[q];
     }
     for (uint32_t p = sh.pc0; p < sh.pc1; p++) {
         uint32_t off = R.pid[p] - idx0;
         if (off < 4) {
             uint32_t fl = R.pfl[p];
-            float nv = z[off];
-            if (fl & ZS_PF_BAN) nv = -INFINITY;
-            if (!obs && (fl & ZS_PF_Y)) nv = R.py[p];
+            float py = R.py[p];
 #pragma unroll
-            for (int q = 0; q < 4; q++) if ((uint32_t)q == off) z[q] = nv;
+            for (int q = 0; q < 4; q++) {
+                if ((uint32_t)q != off) continue;
+                if (fl & ZS_PF_BAN) { x[q] = -INFINITY; z[q] = -INFINITY; }
+                if (fl & ZS_PF_Y) z[q] = py;
+            }
         }
     }
-    if (!obs) {
 #pragma unroll
-        for (int q = 0; q < 4; q++) z[q] = zs_temper(z[q], R.T);
-    }
+    for (int q = 0; q < 4; q++) z[q] = zs_temper(z[q], R.T);
     __syncthreads();
 }
 __device__ __forceinline__ void big_load_z(const big_row& R, uint32_t g, float (&z)[4], big_shared& sh) {
-    big_load(R, g, z, sh, false);
+    float x[4];
+    big_load2(R, g, x, z, sh);
+}
+__device__ __forceinline__ void big_load(const big_row& R, uint32_t g, float (&x)[4], big_shared& sh, bool obs) {
+    float z[4];
+    big_load2(R, g, x, z, sh);
 }
 
 __device__ __forceinline__ float big_term_e(float z, bool has_thr, float thr, float m) {
@@ -877,7 +1508,7 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
     const uint32_t r = blockIdx.x;
     zs_row_state stt = a.rst[r];
     const bool run_samp = stt.mode == ZS_MODE_BIG;
-    if (!run_samp && !stt.obs_need) return;
+    if (!run_samp) return;
     __shared__ big_shared sh;
     const int t = threadIdx.x;
     const zs_batch& b = a.b;
@@ -897,43 +1528,6 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
     const float m = stt.z_max;
     if (t == 0) sh.pc1 = 0;
     __syncthreads();
-
-    // ---- observers: the reference's sequential sums over x~
-    //   sum     = sum exp(l - max)                  hallucination.rs:237-238, logprobs.rs:36
-    //   entropy -= p * ((l - max) - ln(sum)), p > 0 hallucination.rs:242-248
-    float S_obs = -0.0f, H_obs = 0.0f;
-    if (stt.obs_need & ZS_OBS_S) {
-        const float M = stt.obs_max;
-        for (uint32_t g = 0; g < ng; g++) {
-            float x[4], tv[4];
-            big_load(R, g, x, sh, true);
-#pragma unroll
-            for (int q = 0; q < 4; q++) tv[q] = zs_expf(x[q] - M);
-            seq_group<ZS_BIG_NT, 4>(tv, 0, S_obs, NAN, sh.q);
-        }
-        if (stt.obs_need & ZS_OBS_H) {
-            const float inv = 1.0f / S_obs;
-            const float lns = (float)log((double)S_obs);
-            for (uint32_t g = 0; g < ng; g++) {
-                float x[4], tv[4];
-                big_load(R, g, x, sh, true);
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    float d = x[q] - M;
-                    float p = zs_expf(d) * inv;
-                    float tt = d - lns;
-                    tv[q] = p > 0.0f ? -(p * tt) : 0.0f;
-                }
-                seq_group<ZS_BIG_NT, 4>(tv, 0, H_obs, NAN, sh.q);
-            }
-        }
-    }
-    stt.obs_S = S_obs;
-    stt.obs_H = H_obs;
-    if (!run_samp) {
-        if (t == 0) a.rst[r] = stt;
-        return;
-    }
 
     // ---- top-k threshold by radix select when the candidates could not give it
     uint32_t has_thr = stt.has_thr;
@@ -976,17 +1570,21 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
     const bool use_thr = has_thr != 0;
     const float thr = zs_key_to_float(thr_key);
 
-    // ---- S = sum exp(z - m) in index order (sampler.rs:67-68); identical to the
-    // observers' sum when z == x~ and no top-k cut applies
-    float S = -0.0f;
+    // ---- softmax denominators: computed by the parallel rounds (sampler S, or
+    // the observers' S when z == x~ and no top-k cut applies)
     const bool reuse = stt.z_is_x && !use_thr && (stt.obs_need & ZS_OBS_S);
-    if (reuse) S = S_obs;
-    for (uint32_t g = 0; g < (reuse ? 0u : ng); g++) {
-        float z[4], tv[4];
-        big_load_z(R, g, z, sh);
+    float S = reuse ? stt.obs_S : stt.samp_S;
+    if (!reuse && !((stt.rounds >> ZS_SUM_SAMP_S) & 1u)) {
+        // the top-k threshold was only found above: sum here
+        S = -0.0f;
+        for (uint32_t g = 0; g < ng; g++) {
+            float x[4], z[4];
+            big_load2(R, g, x, z, sh);
+            exp_terms<4> f;
 #pragma unroll
-        for (int q = 0; q < 4; q++) tv[q] = big_term_e(z[q], use_thr, thr, m);
-        seq_group<ZS_BIG_NT, 4>(tv, 0, S, NAN, sh.q);
+            for (int q = 0; q < 4; q++) f.set(q, (use_thr && z[q] < thr) ? -INFINITY : z[q] - m);
+            seq_group_f<ZS_BIG_NT, 4>(f, 0, S, NAN, sh.q);
+        }
     }
 
     // ---- min-p (sampler.rs:72-88)
@@ -1094,7 +1692,7 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
                     tv[q] = zs_u2f(bits[q]);
                 }
                 uint32_t excl[4];
-                seq_find_res F = seq_find<ZS_BIG_NT, 4>(tv, 0, s, P.top_p, excl, sh.q);
+                seq_find_res F = seq_find<ZS_BIG_NT, 4>(seq_terms<4>(tv), 0, s, P.top_p, excl, sh.q);
                 int first = min(F.ev, F.st);
                 // bucket open at the end of this group, and its start
                 uint32_t last = min(pos + ZS_BIG_G, nend) - 1;
@@ -1330,6 +1928,10 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
     a.pairs = ctx->pairs;
     a.nch = ctx->max_chunks;
     a.max_vocab = ctx->max_vocab;
+    a.sub_mom = ctx->sub_mom;
+    a.sub_sum = ctx->sub_sum;
+    a.p_sub = ctx->p_sub;
+    a.max_subs = ctx->max_subs;
     const uint32_t B = bt->B;
     const uint32_t nch = (bt->V + ZS_P1_CH - 1) / ZS_P1_CH;
     const bool prof = ctx->profiling != 0;
@@ -1347,6 +1949,16 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
     mark("zs_k_pass1");
     hipLaunchKernelGGL(zs_k_combine, dim3(B), dim3(CB_NT), 0, stream, a);
     mark("zs_k_combine");
+    const uint32_t nsub = (bt->V + ZS_SUB - 1) / ZS_SUB;
+    hipLaunchKernelGGL(zs_k_roundA, dim3((nsub + 3) / 4, B), dim3(256), 0, stream, a);
+    mark("zs_k_roundA");
+    hipLaunchKernelGGL(zs_k_stitch<ZS_SUM_OBS_S>, dim3(B), dim3(ST_NT), 0, stream, a);
+    hipLaunchKernelGGL(zs_k_stitch<ZS_SUM_SAMP_S>, dim3(B), dim3(ST_NT), 0, stream, a);
+    mark("zs_k_stitchA");
+    hipLaunchKernelGGL(zs_k_roundB, dim3((nsub + 3) / 4, B), dim3(256), 0, stream, a);
+    mark("zs_k_roundB");
+    hipLaunchKernelGGL(zs_k_stitch<ZS_SUM_OBS_H>, dim3(B), dim3(ST_NT), 0, stream, a);
+    mark("zs_k_stitchB");
     hipLaunchKernelGGL(zs_k_big, dim3(B), dim3(ZS_BIG_NT), 0, stream, a);
     mark("zs_k_big");
     hipLaunchKernelGGL(zs_k_final, dim3((B + 63) / 64), dim3(64), 0, stream, a);
