@@ -88,10 +88,15 @@ def compare(x, params_list, out, allow=None, check_stats=True):
         if tok != ref["token"]:
             errs.append(f"row {i}: token gpu={tok} ref={ref['token']} status={st:#x} params={ {k: v for k, v in p.items() if k != 'counts'} }")
             continue
-        if not close(out["logprob"][i], ref["logprob"]):
+        if not p.get("logprobs", True):
+            if int(out["top_n"][i]) != 0 or not np.isnan(out["logprob"][i]):
+                errs.append(f"row {i}: logprobs written although not requested")
+        elif not close(out["logprob"][i], ref["logprob"]):
             errs.append(f"row {i}: logprob {out['logprob'][i]} vs {ref['logprob']}")
         n = int(out["top_n"][i])
-        if n != len(ref["top_ids"]):
+        if not p.get("logprobs", True):
+            pass
+        elif n != len(ref["top_ids"]):
             errs.append(f"row {i}: top_n {n} vs {len(ref['top_ids'])}")
         elif not (st & 8):  # ZS_ST_TOPLP_AMBIG
             gi = [int(v) for v in out["top_ids"][i][:n]]
@@ -101,7 +106,10 @@ def compare(x, params_list, out, allow=None, check_stats=True):
                 if not close(a, b):
                     errs.append(f"row {i}: top lp {a} vs {b}")
                     break
-        if check_stats:
+        if check_stats and not p.get("detect_hallucination", True):
+            if not np.isnan(out["entropy"][i]):
+                errs.append(f"row {i}: uncertainty written although not requested")
+        elif check_stats:
             if not close(out["entropy"][i], ref["entropy"], 1e-5, 2e-5):
                 errs.append(f"row {i}: entropy {out['entropy'][i]} vs {ref['entropy']}")
             if not close(out["max_prob"][i], ref["max_prob"]):

@@ -105,3 +105,22 @@ def test_allow_bits_rows():
     params = [dict(temperature=0.9, top_k=0, top_p=0.9, seed=i, masked=True, top_logprobs=3) for i in range(B)]
     params[3]["top_k"] = 20
     _run(x, params, allow_bits=bits, allow=allow)
+
+
+@pytest.mark.parametrize("q", [0.5, 4.0])
+def test_tied_values_topk_lists(q):
+    """Quantized logits: many equal keys around each chunk's k-th value, so the
+    per-chunk candidate selection runs its wave-sort, workgroup-sort and
+    radix paths and the tie rule (key desc, index asc) decides membership."""
+    B, V = 12, 60000
+    x = np.round(synth.logits_powerlaw(B, V, 31) * q) / q
+    x = x.astype(np.float32)
+    rng = np.random.default_rng(31)
+    params = []
+    for i in range(B):
+        params.append(dict(temperature=float([0.7, 1.0, 1.3][i % 3]), top_k=[20, 50, 128, 0][i % 4],
+                           top_p=float([1.0, 0.9][i % 2]), seed=500 + i, top_logprobs=int(rng.integers(0, 21)),
+                           detect_hallucination=bool(i % 2)))
+    x[3, :] = 1.0                      # one value everywhere: every chunk ties completely
+    x[7, ::3] = -np.inf                # a third masked out
+    _run(x, params)

@@ -62,7 +62,7 @@ extern "C" void zs_ctx_destroy(zs_ctx* ctx) {
     for (int i = 0; i < 16; i++)
         if (ctx->events[i]) hipEventDestroy((hipEvent_t)ctx->events[i]);
     void* ptrs[] = {ctx->p_cnt, ctx->p_id, ctx->p_flags, ctx->p_y, ctx->cst, ctx->cs_key, ctx->cs_idx,
-                    ctx->co_key, ctx->co_idx, ctx->rst, ctx->pairs, ctx->mask_scratch, ctx->spec_chunks,
+                    ctx->co_key, ctx->co_idx, ctx->rst, ctx->pairs, ctx->pv, ctx->mask_scratch, ctx->spec_chunks,
                     ctx->spec_rows, ctx->sub_mom, ctx->sub_sum, ctx->p_sub};
     for (void* p : ptrs)
         if (p) hipFree(p);
@@ -105,6 +105,7 @@ extern "C" int zs_ctx_create(int device, uint32_t max_rows, uint32_t max_vocab, 
     if (!rc) rc = zs_alloc(ctx, &ctx->co_idx, R * C * ZS_KO);
     if (!rc) rc = zs_alloc(ctx, &ctx->rst, R);
     if (!rc) rc = zs_alloc(ctx, &ctx->pairs, R * (size_t)max_vocab * 2);
+    if (!rc) rc = zs_alloc(ctx, &ctx->pv, R * (size_t)max_vocab);
     if (!rc) rc = zs_alloc(ctx, (uint32_t**)&ctx->mask_scratch, R);
     if (!rc) rc = zs_alloc(ctx, &ctx->spec_chunks, R * (2 * ZS_SPEC_KMAX + 1) * C);
     if (!rc) rc = zs_alloc(ctx, &ctx->sub_mom, R * ctx->max_subs);

@@ -149,6 +149,35 @@ __device__ __forceinline__ uint32_t block_excl_scan_sat(uint32_t v, uint32_t* sh
 }
 
 // In-LDS bitonic sort, ascending, of n (power of two) 64-bit keys.
+// Ascending bitonic sort across the wave, one value per lane (lane i ends
+// with the i-th smallest).
+__device__ __forceinline__ uint32_t wave_sort_u32(uint32_t v) {
+    const int lane = zs_lane();
+#pragma unroll
+    for (int k = 2; k <= 64; k <<= 1) {
+#pragma unroll
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            uint32_t o = __shfl_xor(v, j, 64);
+            bool keep_min = ((lane & j) == 0) == ((lane & k) == 0 || k == 64);
+            v = keep_min ? min(v, o) : max(v, o);
+        }
+    }
+    return v;
+}
+__device__ __forceinline__ unsigned long long wave_sort_u64(unsigned long long v) {
+    const int lane = zs_lane();
+#pragma unroll
+    for (int k = 2; k <= 64; k <<= 1) {
+#pragma unroll
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            unsigned long long o = __shfl_xor(v, j, 64);
+            bool keep_min = ((lane & j) == 0) == ((lane & k) == 0 || k == 64);
+            v = keep_min ? (o < v ? o : v) : (o > v ? o : v);
+        }
+    }
+    return v;
+}
+
 template <int NT>
 __device__ void block_bitonic_u64(unsigned long long* a, int n) {
     for (int k = 2; k <= n; k <<= 1) {

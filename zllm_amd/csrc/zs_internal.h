@@ -18,7 +18,7 @@
 // Big-row engine: 1024 threads, 4 consecutive elements per thread.
 #define ZS_BIG_NT 1024
 #define ZS_BIG_G 4096
-#define ZS_SORT_CAP 8192
+#define ZS_SORT_CAP 32768
 
 // Patch flags (merged bias / count-map / ban list, one entry per token id).
 #define ZS_PF_BAN 1u
@@ -155,6 +155,7 @@ struct zs_ctx {
     uint32_t* co_idx;
     zs_row_state* rst;
     uint32_t* pairs;       // big-row gather area [rows][max_vocab][2]
+    uint32_t* pv;          // big-row probabilities (f32 bits) [rows][max_vocab]
     void* mask_scratch;    // DFA mask staging
     zs_sub_mom* sub_mom;         // [rows][max_subs]
     zs_sub_sum* sub_sum;         // [rows][ZS_NSUM][max_subs]

@@ -41,6 +41,7 @@ struct zs_sargs {
     uint32_t* co_idx;
     zs_row_state* rst;
     uint32_t* pairs;
+    uint32_t* pv;
     uint32_t nch;
     uint32_t max_vocab;
     zs_sub_mom* sub_mom;
@@ -191,6 +192,7 @@ __global__ __launch_bounds__(ZS_PREP_NT) void zs_k_prep(zs_sargs a) {
 #define P1_EPT 32
 
 #define P1_SUP 1024
+#define P1_SORT 256
 struct p1_shared {
     uint32_t hist[256];
     uint32_t u[8];
@@ -204,12 +206,13 @@ struct p1_shared {
     uint32_t skey[P1_SUP];
     uint32_t sidx[P1_SUP];
     uint32_t sel[4];
+    unsigned long long s64[P1_SORT];
 };
 
 // Exact top-K (key desc, index asc) of the chunk's valid keys; writes the
 // candidates (unordered) to out_key/out_idx. Element e = j*4+q of thread t has
 // index base + (j*256 + t)*4 + q.
-__device__ void p1_topk(const uint32_t (&key)[P1_EPT], uint32_t vmask, uint32_t K, uint32_t base,
+__device__ __forceinline__ void p1_topk(const uint32_t (&key)[P1_EPT], uint32_t vmask, uint32_t K, uint32_t base,
                         uint32_t* out_key, uint32_t* out_idx, uint32_t* n_out, uint32_t* kth,
                         uint32_t* full, p1_shared& sh) {
     const int t = threadIdx.x;
@@ -321,98 +324,108 @@ __device__ void p1_topk(const uint32_t (&key)[P1_EPT], uint32_t vmask, uint32_t 
 }
 
 
-// Fast exact top-K: the K-th largest of the 256 per-thread maxima is a lower
-// bound theta of the chunk's K-th largest key, so the elements >= theta (a
-// small superset) contain the top-K. One wave selects inside the superset by
-// binary search over key bits (ballot counts); degenerate chunks whose
-// superset exceeds P1_SUP fall back to the LDS radix select.
-__device__ __forceinline__ uint32_t p1_wave_count_ge(const uint32_t* a, uint32_t n, uint32_t v) {
-    uint32_t c = 0;
-    for (uint32_t i = zs_lane(); i < n; i += 64) c += a[i] >= v ? 1u : 0u;
-    return wave_sum_u(c);
-}
-__device__ void p1_topk_fast(const uint32_t (&key)[P1_EPT], uint32_t vmask, uint32_t K, uint32_t base,
+// Fast exact top-K. Every wave sorts its 64 per-thread maxima; the c-th largest
+// of them, c = ceil(K / 4), has at least c elements of its wave at or above
+// it, so theta = the smallest of the four waves' values has at least K
+// elements of the chunk at or above it: theta bounds the chunk's K-th largest
+// key from below. The elements >= theta (a small superset of the top-K, with
+// every element equal to the K-th key) are sorted by (key desc, index asc) --
+// one wave for up to 64 of them, the workgroup for up to P1_SORT -- and the
+// first K are the answer. Degenerate chunks (larger supersets) use the LDS
+// radix select.
+__device__ __forceinline__ void p1_topk_fast(const uint32_t (&key)[P1_EPT], uint32_t vmask, uint32_t K, uint32_t base,
                              uint32_t* out_key, uint32_t* out_idx, uint32_t* n_out, uint32_t* kth,
                              uint32_t* full, p1_shared& sh) {
     const int t = threadIdx.x;
     uint32_t tm = 0;
-    bool anyv = false;
 #pragma unroll
     for (int e = 0; e < P1_EPT; e++)
-        if ((vmask >> e) & 1u) { tm = max(tm, key[e]); anyv = true; }
+        if ((vmask >> e) & 1u) tm = max(tm, key[e]);
     uint32_t nvalid = block_sum_u<ZS_P1_NT>(__popc(vmask), sh.u);
-    if (nvalid <= K || K > ZS_P1_NT) {
+    const uint32_t c = (K + (ZS_P1_NT / 64) - 1) / (ZS_P1_NT / 64);
+    if (nvalid <= K || c > 64) {
         p1_topk(key, vmask, K, base, out_key, out_idx, n_out, kth, full, sh);
         return;
     }
-    sh.tmax[t] = anyv ? tm : 0u;
+    // threads without elements hold key 0, below every element
+    const uint32_t srt = wave_sort_u32(tm);
+    const uint32_t thw = __shfl(srt, 64 - (int)c, 64);
+    if (zs_lane() == 0) sh.sel[zs_wid()] = thw;
     __syncthreads();
-    if (t < 64) {
-        // theta = K-th largest thread maximum (threads without elements hold 0)
-        uint32_t pre = 0;
-        for (int bit = 31; bit >= 0; bit--) {
-            uint32_t cand = pre | (1u << bit);
-            if (p1_wave_count_ge(sh.tmax, ZS_P1_NT, cand) >= K) pre = cand;
-        }
-        if (t == 0) sh.sel[0] = pre;
-    }
-    __syncthreads();
-    const uint32_t theta = sh.sel[0];
-    uint32_t c = 0;
+    uint32_t theta = sh.sel[0];
 #pragma unroll
-    for (int e = 0; e < P1_EPT; e++) c += (((vmask >> e) & 1u) && key[e] >= theta) ? 1u : 0u;
+    for (int w = 1; w < ZS_P1_NT / 64; w++) theta = min(theta, sh.sel[w]);
+    uint32_t cnt = 0;
+#pragma unroll
+    for (int e = 0; e < P1_EPT; e++) cnt += (((vmask >> e) & 1u) && key[e] >= theta) ? 1u : 0u;
     uint32_t nsup;
-    uint32_t pos = block_excl_scan_u<ZS_P1_NT>(c, sh.u, &nsup);
-    if (nsup > P1_SUP) {
+    uint32_t pos = block_excl_scan_u<ZS_P1_NT>(cnt, sh.u, &nsup);
+    if (nsup > P1_SORT) {
         p1_topk(key, vmask, K, base, out_key, out_idx, n_out, kth, full, sh);
         return;
     }
+    // composite ((~key) << 32 | index): ascending order = key desc, index asc
 #pragma unroll
     for (int e = 0; e < P1_EPT; e++) {
         if (((vmask >> e) & 1u) && key[e] >= theta) {
-            sh.skey[pos] = key[e];
-            sh.sidx[pos] = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
+            const uint32_t idx = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
+            sh.s64[pos++] = ((unsigned long long)(~key[e]) << 32) | idx;
+        }
+    }
+    __syncthreads();
+    if (nsup <= 64) {
+        if (t < 64) {
+            unsigned long long v = (uint32_t)t < nsup ? sh.s64[t] : ~0ull;
+            v = wave_sort_u64(v);
+            const unsigned long long vk = __shfl(v, (int)K - 1, 64);
+            const unsigned long long vn = __shfl(v, min((int)K, 63), 64);
+            if ((uint32_t)t < K) { out_key[t] = ~(uint32_t)(v >> 32); out_idx[t] = (uint32_t)v; }
+            if (t == 0) {
+                sh.sel[0] = ~(uint32_t)(vk >> 32);
+                sh.sel[1] = (K < nsup && (uint32_t)(vn >> 32) == (uint32_t)(vk >> 32)) ? 2u : 1u;
+            }
+        }
+    } else {
+        for (uint32_t i = nsup + t; i < P1_SORT; i += ZS_P1_NT) sh.s64[i] = ~0ull;
+        __syncthreads();
+        block_bitonic_u64<ZS_P1_NT>(sh.s64, P1_SORT);
+        for (uint32_t i = t; i < K; i += ZS_P1_NT) {
+            const unsigned long long v = sh.s64[i];
+            out_key[i] = ~(uint32_t)(v >> 32);
+            out_idx[i] = (uint32_t)v;
+        }
+        if (t == 0) {
+            const uint32_t hk = (uint32_t)(sh.s64[K - 1] >> 32);
+            sh.sel[0] = ~hk;
+            sh.sel[1] = (K < nsup && (uint32_t)(sh.s64[K] >> 32) == hk) ? 2u : 1u;
+        }
+    }
+    __syncthreads();
+    *n_out = K;
+    *kth = sh.sel[0];
+    *full = sh.sel[1];
+    __syncthreads();
+}
+
+// Compaction of the chunk's finite sampler values (the list when the chunk has
+// at most K of them: then it holds every element a top-k or a small-survivor
+// path can keep).
+__device__ __forceinline__ void p1_finite(const uint32_t (&key)[P1_EPT], const float (&zv)[P1_EPT], uint32_t vmask,
+                          uint32_t base, uint32_t* out_key, uint32_t* out_idx, p1_shared& sh) {
+    const int t = threadIdx.x;
+    uint32_t cnt = 0;
+#pragma unroll
+    for (int e = 0; e < P1_EPT; e++) cnt += (((vmask >> e) & 1u) && zv[e] > -INFINITY) ? 1u : 0u;
+    uint32_t tot;
+    uint32_t pos = block_excl_scan_u<ZS_P1_NT>(cnt, sh.u, &tot);
+#pragma unroll
+    for (int e = 0; e < P1_EPT; e++) {
+        if (((vmask >> e) & 1u) && zv[e] > -INFINITY) {
+            out_key[pos] = key[e];
+            out_idx[pos] = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
             pos++;
         }
     }
-    __syncthreads();
-    if (t < 64) {
-        // K-th largest key of the superset, then the need-th smallest id among its ties
-        uint32_t kk = 0;
-        for (int bit = 31; bit >= 0; bit--) {
-            uint32_t cand = kk | (1u << bit);
-            if (p1_wave_count_ge(sh.skey, nsup, cand) >= K) kk = cand;
-        }
-        uint32_t gt = 0, eq = 0;
-        for (uint32_t i = t; i < nsup; i += 64) { gt += sh.skey[i] > kk; eq += sh.skey[i] == kk; }
-        gt = wave_sum_u(gt);
-        eq = wave_sum_u(eq);
-        uint32_t need = K - gt;
-        // smallest id I with #(key == kk && id <= I) >= need
-        uint32_t lo = 0;
-        for (int bit = 31; bit >= 0; bit--) {
-            uint32_t cand = lo | (1u << bit);  // test: count(id < cand) < need  => id bound >= cand
-            uint32_t cc = 0;
-            for (uint32_t i = t; i < nsup; i += 64) cc += (sh.skey[i] == kk && sh.sidx[i] < cand) ? 1u : 0u;
-            if (wave_sum_u(cc) < need) lo = cand;
-        }
-        if (t == 0) { sh.sel[1] = kk; sh.sel[2] = lo; sh.sel[3] = eq > need ? 2u : 1u; }
-    }
-    if (t == 0) sh.cnt = 0;
-    __syncthreads();
-    const uint32_t kk = sh.sel[1], ilim = sh.sel[2];
-    for (uint32_t i = t; i < nsup; i += ZS_P1_NT) {
-        uint32_t k = sh.skey[i], id = sh.sidx[i];
-        if (k > kk || (k == kk && id <= ilim)) {
-            uint32_t p = atomicAdd(&sh.cnt, 1u);
-            if (p < K) { out_key[p] = k; out_idx[p] = id; }
-        }
-    }
-    __syncthreads();
-    *n_out = min(sh.cnt, K);
-    *kth = kk;
-    *full = sh.sel[3];
-    __syncthreads();
 }
 
 __global__ __launch_bounds__(ZS_P1_NT) void zs_k_pass1(zs_sargs a) {
@@ -624,9 +637,17 @@ __global__ __launch_bounds__(ZS_P1_NT) void zs_k_pass1(zs_sargs a) {
     for (int e = 0; e < P1_EPT; e++) key[e] = zs_total_key(zv[e]);
     uint32_t ns, s_kth, s_full;
     ns = s_kth = s_full = 0;
-    if (T > 0.0f)
-        p1_topk_fast(key, vmask, Ks, base, a.cs_key + lofs * ZS_KS, a.cs_idx + lofs * ZS_KS, &ns, &s_kth,
-                     &s_full, sh);
+    // The list is read by a top-k cut within ZS_KS and by the small-survivor
+    // path, which needs every chunk to have at most ZS_KS finite values.
+    if (T > 0.0f) {
+        if (zfin <= Ks) {
+            p1_finite(key, zv, vmask, base, a.cs_key + lofs * ZS_KS, a.cs_idx + lofs * ZS_KS, sh);
+            ns = zfin;
+        } else if (has_topk && P.top_k <= ZS_KS) {
+            p1_topk_fast(key, vmask, Ks, base, a.cs_key + lofs * ZS_KS, a.cs_idx + lofs * ZS_KS, &ns, &s_kth,
+                         &s_full, sh);
+        }
+    }
     uint32_t ntl = P.top_logprobs > 20 ? 20 : P.top_logprobs;
     uint32_t Ko = ntl + 8;
     if (Ko > ZS_KO) Ko = ZS_KO;
@@ -968,7 +989,9 @@ __global__ __launch_bounds__(CB_NT) void zs_k_combine(zs_sargs a) {
         bool small = false;
         float thr = -INFINITY;
         if (has_topk && P.top_k <= ZS_KS) {
-            thr_key = ~(uint32_t)(sbuf[P.top_k - 1] >> 32);
+            // fewer listed values than k: every finite value is listed and the
+            // k-th largest of the row is -inf
+            thr_key = P.top_k <= ncs ? ~(uint32_t)(sbuf[P.top_k - 1] >> 32) : zs_total_key(-INFINITY);
             has_thr = 1;
             thr = zs_key_to_float(thr_key);
             bool complete = true;
@@ -1420,14 +1443,17 @@ __global__ __launch_bounds__(ST_NT) void zs_k_stitch(zs_sargs a) {
 // ===========================================================================
 // zs_k_big: exact emulation of the reference's sequential sums over a full row.
 // ===========================================================================
+#define BK_NB 2048   // buckets per level of the top-p walk
+
 struct big_shared {
     seq_sh<ZS_BIG_NT> q;
-    uint32_t u[4];
+    uint32_t u[8];
     float s;
     uint32_t pc0, pc1;
-    uint32_t hist[2048];
-    uint32_t cnt[2048];
-    unsigned long long sortbuf[ZS_SORT_CAP];
+    uint32_t hist[BK_NB + 1];    // level 0: bucket starts by rank (rank 0 = largest values)
+    uint32_t hist1[BK_NB + 1];   // level 1 (refinement of one oversize bucket)
+    uint32_t hist2[256];         // level 2: counts of single values
+    uint32_t sortbuf[ZS_SORT_CAP];
 };
 
 struct big_row {
@@ -1442,7 +1468,6 @@ struct big_row {
     float T;
 };
 
-// z for the 4 elements idx0..idx0+3 of group g (patch cursor in sh.pc0/pc1).
 // x~ (observers: mask and bans) and z (sampler: patched y, divided by T) of the
 // 4 elements idx0..idx0+3 of group g; the patch cursor advances in sh.pc0/pc1.
 __device__ __forceinline__ void big_load2(const big_row& R, uint32_t g, float (&x)[4], float (&z)[4],
@@ -1494,14 +1519,196 @@ __device__ __forceinline__ void big_load_z(const big_row& R, uint32_t g, float (
     float x[4];
     big_load2(R, g, x, z, sh);
 }
-__device__ __forceinline__ void big_load(const big_row& R, uint32_t g, float (&x)[4], big_shared& sh, bool obs) {
-    float z[4];
-    big_load2(R, g, x, z, sh);
-}
 
 __device__ __forceinline__ float big_term_e(float z, bool has_thr, float thr, float m) {
     if (has_thr && z < thr) return 0.0f;
     return zs_expf(z - m);
+}
+
+// ---------------------------------------------------------------------------
+// Exact top-p walk (sampler.rs:91-104): the running f32 sum over the
+// probabilities in (p desc, index asc) order, up to the first element after
+// which it reaches top_p. The sum depends on the order only through parity
+// ties and binade crossings (events): inside a binade, every non-tie term adds
+// a fixed integer number of grid units whatever its position. Values are
+// therefore bucketed by their high bits and visited bucket by bucket in
+// descending order, in any order inside a bucket; a bucket holding an event,
+// a tie or the stop is redone in exact descending order -- sorted in LDS, or,
+// when larger than the LDS, refined by the next 11 bits, and at the last level
+// (all values share their 24 high bits) walked as repeated values by count.
+// Equal values are adjacent in that order, and the stop is reported as
+// (value, rank among the equal values passed): the index order among equal
+// probabilities is resolved afterwards on the row.
+// ---------------------------------------------------------------------------
+struct walk_out {
+    bool stopped;
+    uint32_t v;      // stop value (f32 bits)
+    uint32_t rank;   // 0-based rank of the stop among the elements equal to v
+};
+
+// descending bitonic sort of n (power of two) u32 values in LDS
+__device__ void bk_sort_desc(uint32_t* a, int n) {
+    for (int k = 2; k <= n; k <<= 1) {
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            for (int i = threadIdx.x; i < n; i += ZS_BIG_NT) {
+                int ixj = i ^ j;
+                if (ixj > i) {
+                    uint32_t x = a[i], y = a[ixj];
+                    bool desc = (i & k) == 0;
+                    if ((x < y) == desc) { a[i] = y; a[ixj] = x; }
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// Walk n <= ZS_SORT_CAP values in exact descending order (sorted in LDS).
+__device__ walk_out bk_walk_sorted(const uint32_t* vals, uint32_t n, float& s, float thresh, big_shared& sh) {
+    walk_out o = {false, 0u, 0u};
+    uint32_t np2 = 1;
+    while (np2 < n) np2 <<= 1;
+    for (uint32_t i = threadIdx.x; i < np2; i += ZS_BIG_NT) sh.sortbuf[i] = i < n ? vals[i] : 0u;
+    __syncthreads();
+    if (np2 > 1) bk_sort_desc(sh.sortbuf, (int)np2);
+    for (uint32_t q0 = 0; q0 < n; q0 += ZS_BIG_G) {
+        float tv[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            uint32_t i = q0 + 4 * threadIdx.x + q;
+            tv[q] = i < n ? zs_u2f(sh.sortbuf[i]) : 0.0f;
+        }
+        int stp = seq_group<ZS_BIG_NT, 4>(tv, 0, s, thresh, sh.q);
+        if (stp >= 0) {
+            const uint32_t pos = q0 + (uint32_t)stp;
+            const uint32_t v = sh.sortbuf[pos];
+            // first position holding v (the sorted values are descending)
+            uint32_t lo = 0, hi = pos;
+            while (lo < hi) {
+                uint32_t mid = (lo + hi) >> 1;
+                if (sh.sortbuf[mid] > v) lo = mid + 1; else hi = mid;
+            }
+            o.stopped = true;
+            o.v = v;
+            o.rank = pos - lo;
+            break;
+        }
+    }
+    __syncthreads();
+    return o;
+}
+
+// Last level: all n values share bits 31..8 (`prefix`); count each of the 256
+// possible values and add them as repeated terms, largest first.
+__device__ walk_out bk_walk_counts(const uint32_t* vals, uint32_t n, uint32_t prefix, float& s, float thresh,
+                                   big_shared& sh) {
+    for (int i = threadIdx.x; i < 256; i += ZS_BIG_NT) sh.hist2[i] = 0;
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < n; i += ZS_BIG_NT) atomicAdd(&sh.hist2[vals[i] & 255u], 1u);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float ss = s;
+        uint32_t stopped = 0, v = 0, rank = 0;
+        for (int lo = 255; lo >= 0 && !stopped; lo--) {
+            const uint32_t c = sh.hist2[lo];
+            if (!c) continue;
+            const uint32_t bits = prefix | (uint32_t)lo;
+            long long k = seq_repeat(ss, zs_u2f(bits), c, thresh);
+            if (k >= 0) { stopped = 1; v = bits; rank = (uint32_t)k; }
+        }
+        sh.s = ss;
+        sh.u[4] = stopped;
+        sh.u[5] = v;
+        sh.u[6] = rank;
+    }
+    __syncthreads();
+    walk_out o;
+    s = sh.s;
+    o.stopped = sh.u[4] != 0;
+    o.v = sh.u[5];
+    o.rank = sh.u[6];
+    __syncthreads();
+    return o;
+}
+
+// Bucket index of value v at level L (0: bits 31..19, 1: bits 18..8), as a rank
+// (0 = the bucket of the largest values).
+template <int L>
+__device__ __forceinline__ uint32_t bk_rank(uint32_t v) {
+    return L == 0 ? (BK_NB - 1u) - min(v >> 19, (uint32_t)(BK_NB - 1)) : (BK_NB - 1u) - ((v >> 8) & (BK_NB - 1u));
+}
+
+template <int L>
+__device__ walk_out bk_exact(const uint32_t* vals, uint32_t n, float& s, float thresh, uint32_t* tmp, big_shared& sh);
+
+// Walk vals[from, to), laid out bucket by bucket (level L, starts in `start`),
+// from running sum s. The values of a bucket are in any order.
+template <int L>
+__device__ walk_out bk_walk(const uint32_t* vals, uint32_t from, uint32_t to, const uint32_t* start, float& s,
+                            float thresh, uint32_t* tmp, big_shared& sh) {
+    walk_out o = {false, 0u, 0u};
+    uint32_t pos = from;
+    float s_bstart = s;  // running sum at the start of the bucket open at pos
+    while (pos < to) {
+        float tv[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            uint32_t ps = pos + 4 * threadIdx.x + q;
+            tv[q] = ps < to ? zs_u2f(vals[ps]) : 0.0f;
+        }
+        uint32_t excl[4];
+        seq_find_res F = seq_find<ZS_BIG_NT, 4>(seq_terms<4>(tv), 0, s, thresh, excl, sh.q);
+        const int first = min(min(F.ev, F.st), F.tie);
+        if (first == ZS_BIGI) {
+            const uint32_t last = min(pos + ZS_BIG_G, to) - 1;
+            const uint32_t bst = start[bk_rank<L>(vals[last])];
+            if (bst >= pos) s_bstart = seq_value_at<ZS_BIG_NT, 4>(F, excl, (int)(bst - pos), sh.q);
+            s = zs_grid_value(F.k0 + F.total, F.eg);
+            pos += ZS_BIG_G;
+            continue;
+        }
+        // the bucket holding the first event / tie / stop is redone in exact order
+        const uint32_t rk = bk_rank<L>(vals[pos + (uint32_t)first]);
+        const uint32_t bst = start[rk], bend = start[rk + 1];
+        if (bst >= pos) s = seq_value_at<ZS_BIG_NT, 4>(F, excl, (int)(bst - pos), sh.q);
+        else s = s_bstart;
+        o = bk_exact<L + 1>(vals + bst, bend - bst, s, thresh, tmp, sh);
+        if (o.stopped) return o;
+        s_bstart = s;
+        pos = bend;
+    }
+    return o;
+}
+
+// Exact descending walk of one bucket of level L-1 (its values share the
+// bucket's high bits).
+template <int L>
+__device__ walk_out bk_exact(const uint32_t* vals, uint32_t n, float& s, float thresh, uint32_t* tmp, big_shared& sh) {
+    if (n <= ZS_SORT_CAP) return bk_walk_sorted(vals, n, s, thresh, sh);
+    if constexpr (L >= 2) {
+        return bk_walk_counts(vals, n, vals[0] & ~255u, s, thresh, sh);
+    } else {
+        // refine by bits 18..8 into tmp, bucket by bucket
+        for (int i = threadIdx.x; i <= BK_NB; i += ZS_BIG_NT) sh.hist1[i] = 0;
+        __syncthreads();
+        for (uint32_t i = threadIdx.x; i < n; i += ZS_BIG_NT) atomicAdd(&sh.hist1[bk_rank<1>(vals[i])], 1u);
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            uint32_t acc = 0;
+            for (int i = 0; i <= BK_NB; i++) { uint32_t c = i < BK_NB ? sh.hist1[i] : 0u; sh.hist1[i] = acc; acc += c; }
+        }
+        __syncthreads();
+        uint32_t* cur = sh.sortbuf;  // scatter cursors
+        for (int i = threadIdx.x; i < BK_NB; i += ZS_BIG_NT) cur[i] = sh.hist1[i];
+        __syncthreads();
+        for (uint32_t i = threadIdx.x; i < n; i += ZS_BIG_NT) {
+            const uint32_t v = vals[i];
+            tmp[atomicAdd(&cur[bk_rank<1>(v)], 1u)] = v;
+        }
+        __threadfence_block();
+        __syncthreads();
+        return bk_walk<1>(tmp, 0, n, sh.hist1, s, thresh, nullptr, sh);
+    }
 }
 
 __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
@@ -1526,6 +1733,7 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
     const uint32_t V = b.V;
     const uint32_t ng = (V + ZS_BIG_G - 1) / ZS_BIG_G;
     const float m = stt.z_max;
+    uint32_t* pv = a.pv + (size_t)r * a.max_vocab;
     if (t == 0) sh.pc1 = 0;
     __syncthreads();
 
@@ -1570,12 +1778,11 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
     const bool use_thr = has_thr != 0;
     const float thr = zs_key_to_float(thr_key);
 
-    // ---- softmax denominators: computed by the parallel rounds (sampler S, or
-    // the observers' S when z == x~ and no top-k cut applies)
+    // ---- softmax denominator: from the parallel rounds (sampler S, or the
+    // observers' S when z == x~ and no top-k cut applies), else summed here
     const bool reuse = stt.z_is_x && !use_thr && (stt.obs_need & ZS_OBS_S);
     float S = reuse ? stt.obs_S : stt.samp_S;
     if (!reuse && !((stt.rounds >> ZS_SUM_SAMP_S) & 1u)) {
-        // the top-k threshold was only found above: sum here
         S = -0.0f;
         for (uint32_t g = 0; g < ng; g++) {
             float x[4], z[4];
@@ -1587,184 +1794,156 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
         }
     }
 
-    // ---- min-p (sampler.rs:72-88)
+    // ---- probabilities p = exp(z - max) / S (sampler.rs:69), kept in pv for
+    // the later passes; min-p kept mass (sampler.rs:72-88) in the same pass
     const bool minp = P.min_p > 0.0f;
-    float cut = 0.0f, kept = 0.0f;
-    if (minp) {
-        float pmax = 1.0f / S;  // the max element has exp(0) = 1
-        cut = P.min_p * pmax;
-        for (uint32_t g = 0; g < ng; g++) {
-            float z[4], tv[4];
-            big_load_z(R, g, z, sh);
+    const float cut = minp ? P.min_p * (1.0f / S) : 0.0f;  // p_max: the max element has exp(0) = 1
+    float kept = 0.0f;
+    for (uint32_t g = 0; g < ng; g++) {
+        float z[4], tv[4];
+        big_load_z(R, g, z, sh);
+        const uint32_t idx0 = g * ZS_BIG_G + 4 * t;
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                float p = big_term_e(z[q], use_thr, thr, m) / S;
-                tv[q] = (p < cut) ? 0.0f : p;
-            }
-            seq_group<ZS_BIG_NT, 4>(tv, 0, kept, NAN, sh.q);
+        for (int q = 0; q < 4; q++) {
+            const float p = big_term_e(z[q], use_thr, thr, m) / S;
+            if (idx0 + q < V) pv[idx0 + q] = zs_f2u(p);
+            tv[q] = (p < cut) ? 0.0f : p;
         }
+        if (minp) seq_group<ZS_BIG_NT, 4>(tv, 0, kept, NAN, sh.q);
     }
-    auto p1_of = [&](float z) -> float {
-        float p = big_term_e(z, use_thr, thr, m) / S;
+    __threadfence_block();
+    __syncthreads();
+    auto p1_of = [&](uint32_t pb) -> float {
+        float p = zs_u2f(pb);
         if (minp) {
             if (p < cut) p = 0.0f;
             else if (kept > 0.0f) p = p / kept;
         }
         return p;
     };
+    auto load_p1 = [&](uint32_t g, float (&p)[4]) {
+        const uint32_t idx0 = g * ZS_BIG_G + 4 * t;
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if (idx0 < V) v = *reinterpret_cast<const uint4*>(pv + idx0);
+        p[0] = p1_of(v.x); p[1] = p1_of(v.y); p[2] = p1_of(v.z); p[3] = p1_of(v.w);
+#pragma unroll
+        for (int q = 0; q < 4; q++) if (idx0 + q >= V) p[q] = 0.0f;
+    };
 
     // ---- top-p (sampler.rs:91-115)
     const bool topp = P.top_p < 1.0f && P.top_p > 0.0f;
     uint32_t vstar = 0, istar = 0xffffffffu;  // kept: p1 > v* or (p1 == v* and idx <= i*)
     float sum2 = 0.0f;
-    bool stopped = false;
     if (topp) {
-        uint32_t* pairs = a.pairs + (size_t)r * a.max_vocab * 2;
-        for (int i = t; i < 2048; i += ZS_BIG_NT) sh.hist[i] = 0;
+        uint32_t* gv = a.pairs + (size_t)r * a.max_vocab * 2;  // level-0 layout
+        uint32_t* tmp = gv + a.max_vocab;                       // level-1 refinement
+        for (int i = t; i <= BK_NB; i += ZS_BIG_NT) sh.hist[i] = 0;
         __syncthreads();
         for (uint32_t g = 0; g < ng; g++) {
-            float z[4];
-            big_load_z(R, g, z, sh);
+            float p[4];
+            load_p1(g, p);
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                float p = p1_of(z[q]);
-                if (p > 0.0f) atomicAdd(&sh.hist[min(zs_f2u(p) >> 19, 2047u)], 1u);
-            }
+            for (int q = 0; q < 4; q++)
+                if (p[q] > 0.0f) atomicAdd(&sh.hist[bk_rank<0>(zs_f2u(p[q]))], 1u);
         }
         __syncthreads();
-        // offsets in descending bucket order, and the first candidate range:
-        // buckets whose guaranteed mass reaches 1.02 * top_p
+        // bucket starts by rank, and the first candidate range: buckets whose
+        // guaranteed mass (count * bucket floor) reaches 1.02 * top_p
         if (t == 0) {
-            uint32_t off = 0;
+            uint32_t acc = 0;
             double lb = 0.0;
-            int blo = 0;
+            uint32_t rlim = BK_NB - 1;
             bool found = false;
-            for (int bk = 2047; bk >= 0; bk--) {
-                uint32_t n = sh.hist[bk];
-                sh.cnt[bk] = n;
-                sh.hist[bk] = off;  // becomes the bucket start
-                off += n;
-                lb += (double)n * (double)zs_u2f((uint32_t)bk << 19);
-                if (!found && lb >= 1.02 * (double)P.top_p) { blo = bk; found = true; }
+            for (int rk = 0; rk <= BK_NB; rk++) {
+                const uint32_t c = rk < BK_NB ? sh.hist[rk] : 0u;
+                sh.hist[rk] = acc;
+                acc += c;
+                if (rk < BK_NB && !found) {
+                    lb += (double)c * (double)zs_u2f((uint32_t)(BK_NB - 1 - rk) << 19);
+                    if (lb >= 1.02 * (double)P.top_p) { rlim = (uint32_t)rk; found = true; }
+                }
             }
-            sh.u[0] = (uint32_t)blo;
+            sh.u[0] = rlim;
         }
         __syncthreads();
-        int blo = (int)sh.u[0];
-        int bhi = 2047;
-        float s = 0.0f, s_bstart = 0.0f;
-        uint32_t pos = 0;
-        for (int round = 0; round < 2 && !stopped; round++) {
-            // gather buckets [blo, bhi] into their slots
-            for (int i = t; i < 2048; i += ZS_BIG_NT) {
-                // cursor = bucket start (kept in hist); use the upper half of sortbuf as cursors
-                reinterpret_cast<uint32_t*>(sh.sortbuf)[i] = sh.hist[i];
-            }
+        const uint32_t rlim = sh.u[0];
+        float s = 0.0f;
+        walk_out wo = {false, 0u, 0u};
+        uint32_t done = 0;  // walked prefix of the level-0 layout
+        for (int round = 0; round < 2 && !wo.stopped; round++) {
+            const uint32_t rlo = round == 0 ? 0u : rlim + 1, rhi = round == 0 ? rlim : BK_NB - 1;
+            if (rlo > rhi) break;
+            uint32_t* cur = sh.sortbuf;  // gather cursors
+            for (int i = t; i < BK_NB; i += ZS_BIG_NT) cur[i] = sh.hist[i];
             __syncthreads();
-            uint32_t* cursor = reinterpret_cast<uint32_t*>(sh.sortbuf);
             for (uint32_t g = 0; g < ng; g++) {
-                float z[4];
-                big_load_z(R, g, z, sh);
+                float p[4];
+                load_p1(g, p);
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    float p = p1_of(z[q]);
-                    if (p > 0.0f) {
-                        int bk = (int)min(zs_f2u(p) >> 19, 2047u);
-                        if (bk >= blo && bk <= bhi) {
-                            uint32_t ps = atomicAdd(&cursor[bk], 1u);
-                            pairs[2 * ps] = zs_f2u(p);
-                            pairs[2 * ps + 1] = g * ZS_BIG_G + 4 * t + q;
-                        }
-                    }
+                    if (!(p[q] > 0.0f)) continue;
+                    const uint32_t pb = zs_f2u(p[q]);
+                    const uint32_t rk = bk_rank<0>(pb);
+                    if (rk >= rlo && rk <= rhi) gv[atomicAdd(&cur[rk], 1u)] = pb;
                 }
+            }
+            __threadfence_block();
+            __syncthreads();
+            const uint32_t upto = sh.hist[rhi + 1];
+            wo = bk_walk<0>(gv, done, upto, sh.hist, s, P.top_p, tmp, sh);
+            done = upto;
+        }
+        if (wo.stopped) {
+            // i*: the index of the (rank+1)-th element, in index order, whose
+            // probability is v* (sampler.rs:93: the sort is stable)
+            vstar = wo.v;
+            const uint32_t nbl = (V + 511) / 512;
+            for (uint32_t i = t; i < nbl; i += ZS_BIG_NT) sh.sortbuf[i] = 0;
+            __syncthreads();
+            for (uint32_t g = 0; g < ng; g++) {
+                float p[4];
+                load_p1(g, p);
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    if (zs_f2u(p[q]) == vstar && p[q] > 0.0f) atomicAdd(&sh.sortbuf[(g * ZS_BIG_G + 4 * t + q) >> 9], 1u);
             }
             __syncthreads();
-            __threadfence_block();
-            const uint32_t nend = sh.hist[blo] + sh.cnt[blo];
-            // walk pos .. nend in bucket-major order
-            while (pos < nend && !stopped) {
-                float tv[4];
-                uint32_t bits[4];
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    uint32_t ps = pos + 4 * t + q;
-                    bits[q] = ps < nend ? pairs[2 * ps] : 0u;
-                    tv[q] = zs_u2f(bits[q]);
+            if (t == 0) {
+                uint32_t acc = 0, blk = 0;
+                sh.u[7] = 0xffffffffu;
+                for (uint32_t i = 0; i < nbl; i++) {
+                    if (acc + sh.sortbuf[i] > wo.rank) { blk = i; break; }
+                    acc += sh.sortbuf[i];
                 }
-                uint32_t excl[4];
-                seq_find_res F = seq_find<ZS_BIG_NT, 4>(seq_terms<4>(tv), 0, s, P.top_p, excl, sh.q);
-                int first = min(F.ev, F.st);
-                // bucket open at the end of this group, and its start
-                uint32_t last = min(pos + ZS_BIG_G, nend) - 1;
-                if (first == ZS_BIGI) {
-                    uint32_t bl = min(pairs[2 * last] >> 19, 2047u);
-                    uint32_t bst = sh.hist[bl];
-                    if (bst >= pos) s_bstart = seq_value_at<ZS_BIG_NT, 4>(F, excl, (int)(bst - pos), sh.q);
-                    s = zs_grid_value(F.k0 + F.total, F.eg);
-                    pos += ZS_BIG_G;
-                    continue;
-                }
-                // an event or the stop lies in bucket bk: restart that bucket in
-                // exact (p desc, idx asc) order from the sum at its start
-                uint32_t bk = min(pairs[2 * min(pos + (uint32_t)first, nend - 1)] >> 19, 2047u);
-                uint32_t bst = sh.hist[bk], bn = sh.cnt[bk];
-                if (bst >= pos) s = seq_value_at<ZS_BIG_NT, 4>(F, excl, (int)(bst - pos), sh.q);
-                else s = s_bstart;
-                if (bn > ZS_SORT_CAP) {
-                    // not handled on chip: flag the row (the token stays invalid);
-                    // every thread takes this branch (bn is uniform)
-                    stt.status |= ZS_ST_FALLBACK;
-                    stopped = true;
-                    vstar = 0; istar = 0xffffffffu;
-                    break;
-                }
-                uint32_t np2 = 1;
-                while (np2 < bn) np2 <<= 1;
-                for (uint32_t i = t; i < np2; i += ZS_BIG_NT) {
-                    unsigned long long v = ~0ull;
-                    if (i < bn) v = ((unsigned long long)(~pairs[2 * (bst + i)]) << 32) | pairs[2 * (bst + i) + 1];
-                    sh.sortbuf[i] = v;
-                }
-                __syncthreads();
-                if (np2 > 1) block_bitonic_u64<ZS_BIG_NT>(sh.sortbuf, (int)np2);
-                for (uint32_t q0 = 0; q0 < bn && !stopped; q0 += ZS_BIG_G) {
-                    float tv2[4];
-#pragma unroll
-                    for (int q = 0; q < 4; q++) {
-                        uint32_t i = q0 + 4 * t + q;
-                        tv2[q] = i < bn ? zs_u2f(~(uint32_t)(sh.sortbuf[i] >> 32)) : 0.0f;
-                    }
-                    int stp = seq_group<ZS_BIG_NT, 4>(tv2, 0, s, P.top_p, sh.q);
-                    if (stp >= 0) {
-                        unsigned long long v = sh.sortbuf[q0 + stp];
-                        vstar = ~(uint32_t)(v >> 32);
-                        istar = (uint32_t)(v & 0xffffffffull);
-                        stopped = true;
-                    }
-                }
-                __syncthreads();
-                s_bstart = s;
-                pos = bst + bn;
+                sh.u[0] = blk;
+                sh.u[1] = wo.rank - acc;
             }
-            // extend to every remaining bucket once
-            if (!stopped) {
-                if (blo == 0) break;
-                bhi = blo - 1;
-                blo = 0;
-            }
+            __syncthreads();
+            const uint32_t blk = sh.u[0], want = sh.u[1];
+            const uint32_t idx = blk * 512 + (uint32_t)t;
+            uint32_t hit = 0;
+            if (t < 512 && idx < V) hit = (pv[idx] != 0u && zs_f2u(p1_of(pv[idx])) == vstar) ? 1u : 0u;
+            uint32_t tot;
+            const uint32_t ex = block_excl_scan_u<ZS_BIG_NT>(hit, sh.hist2, &tot);
+            __syncthreads();
+            if (hit && ex == want) sh.u[7] = idx;
+            __syncthreads();
+            istar = sh.u[7];
+            __syncthreads();
+        } else {
+            vstar = 0;
+            istar = 0xffffffffu;  // every positive p kept
         }
-        if (!stopped) { vstar = 0; istar = 0xffffffffu; }  // every positive p kept
         // ---- sum over the kept set in index order (sampler.rs:107)
         sum2 = -0.0f;
         for (uint32_t g = 0; g < ng; g++) {
-            float z[4], tv[4];
-            big_load_z(R, g, z, sh);
+            float p[4], tv[4];
+            load_p1(g, p);
 #pragma unroll
             for (int q = 0; q < 4; q++) {
-                float p = p1_of(z[q]);
-                uint32_t pb = zs_f2u(p), idx = g * ZS_BIG_G + 4 * t + q;
-                bool keep = pb > vstar || (pb == vstar && idx <= istar);
-                tv[q] = keep ? p : 0.0f;
+                const uint32_t pb = zs_f2u(p[q]), idx = g * ZS_BIG_G + 4 * t + q;
+                const bool keep = pb > vstar || (pb == vstar && idx <= istar);
+                tv[q] = keep ? p[q] : 0.0f;
             }
             seq_group<ZS_BIG_NT, 4>(tv, 0, sum2, NAN, sh.q);
         }
@@ -1772,31 +1951,27 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
     // ---- draw (sampler.rs:118-127)
     const float rr = zs_philox_uniform(b.d_seed[r], b.d_counter[r], 0u);
     uint32_t token = V - 1;
-    if (!(stt.status & ZS_ST_FALLBACK)) {
-        if (rr <= 0.0f) {
-            token = 0;
-        } else {
-            float cum = 0.0f;
-            const bool renorm = topp && sum2 > 0.0f;
-            for (uint32_t g = 0; g < ng; g++) {
-                float z[4], tv[4];
-                big_load_z(R, g, z, sh);
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    float p = p1_of(z[q]);
-                    if (renorm) {
-                        uint32_t pb = zs_f2u(p), idx = g * ZS_BIG_G + 4 * t + q;
-                        bool keep = pb > vstar || (pb == vstar && idx <= istar);
-                        p = keep ? p / sum2 : 0.0f;
-                    }
-                    tv[q] = p;
-                }
-                int stp = seq_group<ZS_BIG_NT, 4>(tv, 0, cum, rr, sh.q);
-                if (stp >= 0) { token = g * ZS_BIG_G + stp; break; }
-            }
-        }
+    if (rr <= 0.0f) {
+        token = 0;
     } else {
-        token = 0xffffffffu;
+        float cum = 0.0f;
+        const bool renorm = topp && sum2 > 0.0f;
+        for (uint32_t g = 0; g < ng; g++) {
+            float p[4], tv[4];
+            load_p1(g, p);
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                float pp = p[q];
+                if (renorm) {
+                    const uint32_t pb = zs_f2u(pp), idx = g * ZS_BIG_G + 4 * t + q;
+                    const bool keep = pb > vstar || (pb == vstar && idx <= istar);
+                    pp = keep ? pp / sum2 : 0.0f;
+                }
+                tv[q] = pp;
+            }
+            int stp = seq_group<ZS_BIG_NT, 4>(tv, 0, cum, rr, sh.q);
+            if (stp >= 0) { token = g * ZS_BIG_G + stp; break; }
+        }
     }
     if (t == 0) {
         stt.token = token;
@@ -1928,6 +2103,7 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
     a.pairs = ctx->pairs;
     a.nch = ctx->max_chunks;
     a.max_vocab = ctx->max_vocab;
+    a.pv = ctx->pv;
     a.sub_mom = ctx->sub_mom;
     a.sub_sum = ctx->sub_sum;
     a.p_sub = ctx->p_sub;

@@ -87,6 +87,7 @@ struct seq_terms {
 
 struct seq_find_res {
     int ev, st;    // first event / first element reaching thresh (ZS_BIGI if none)
+    int tie;       // first element whose increment depends on the sum's parity
     int eg;        // grid exponent of the running sum at group start
     uint32_t k0;   // running sum / grid at group start
     uint32_t total;  // increments of the whole group (actual path)
@@ -141,12 +142,13 @@ __device__ __forceinline__ seq_find_res seq_find(const F& f, int start, float s,
     }
     pre = seq_compose(pre, ex);
     uint32_t run = p0 ? pre.o : pre.e;
-    int my_ev = ZS_BIGI, my_st = ZS_BIGI;
+    int my_ev = ZS_BIGI, my_st = ZS_BIGI, my_tie = ZS_BIGI;
 #pragma unroll
     for (int j = 0; j < EPT; j++) {
         int e = EPT * t + j;
         excl[j] = run;
         if (e < start) continue;
+        if (my_tie == ZS_BIGI && ie[j] != io[j]) my_tie = e;
         uint32_t par = (R.k0 + run) & 1u;
         const uint32_t o = io[j], ev = ie[j];
         run = zs_sat_add(run, par ? o : ev);
@@ -157,14 +159,20 @@ __device__ __forceinline__ seq_find_res seq_find(const F& f, int start, float s,
     // first event / stop (the scan's LDS slots are free again after this sync)
     my_ev = wave_min_i(my_ev);
     my_st = wave_min_i(my_st);
+    my_tie = wave_min_i(my_tie);
     __syncthreads();
-    if (lane == 0) { sh.a[zs_wid()] = (uint32_t)my_ev; sh.b[zs_wid()] = (uint32_t)my_st; }
+    if (lane == 0) { sh.a[zs_wid()] = (uint32_t)my_ev; sh.b[zs_wid()] = (uint32_t)my_st; sh.imin[zs_wid()] = my_tie; }
     __syncthreads();
-    int ev = ZS_BIGI, st = ZS_BIGI;
-    for (int i = 0; i < NT / 64; i++) { ev = min(ev, (int)sh.a[i]); st = min(st, (int)sh.b[i]); }
+    int ev = ZS_BIGI, st = ZS_BIGI, tie = ZS_BIGI;
+    for (int i = 0; i < NT / 64; i++) {
+        ev = min(ev, (int)sh.a[i]);
+        st = min(st, (int)sh.b[i]);
+        tie = min(tie, sh.imin[i]);
+    }
     __syncthreads();
     R.ev = ev;
     R.st = st;
+    R.tie = tie;
     return R;
 }
 
@@ -220,4 +228,43 @@ __device__ __forceinline__ int seq_group(const float (&tv)[EPT], int start, floa
                                          seq_sh<NT>& sh) {
     seq_terms<EPT> f(tv);
     return seq_group_f<NT, EPT>(f, start, s, thresh, sh);
+}
+
+// Adds the same term t to the running sum s up to c times, one thread, in
+// closed form per binade: on a fixed grid the increment is constant once the
+// parity rule is settled (a tie term moves k to an even value on its first
+// addition and keeps it even). Returns the 0-based count of the addition
+// after which s >= thresh (s is then that sum), or -1 with s = the sum after
+// all c additions.
+__device__ __forceinline__ long long seq_repeat(float& s, float t, uint32_t c, float thresh) {
+    uint32_t done = 0;
+    while (done < c) {
+        const int eg = zs_grid_exp(s);
+        const uint32_t k = zs_grid_k(s);
+        seq_pair p = seq_pair_of(t, eg);
+        const uint32_t inc = (k & 1u) ? p.o : p.e;
+        const bool steady = (p.e == p.o) || !(inc & 1u);
+        if (inc == 0u) {
+            // the sum no longer moves: no further stop possible
+            return -1;
+        }
+        if (!steady || k + inc >= ZS_BINADE) {
+            s = s + t;
+            done++;
+            if (s >= thresh) return (long long)done - 1;
+            continue;
+        }
+        // additions that stay inside the binade: k + n*inc < 2^24
+        uint32_t n = (ZS_BINADE - 1u - k) / inc;
+        if (n > c - done) n = c - done;
+        const uint32_t kthr = zs_grid_thresh(thresh, eg);
+        if (kthr != 0xffffffffu && k + (unsigned long long)n * inc >= kthr) {
+            const uint32_t need = kthr <= k ? 1u : (kthr - k + inc - 1u) / inc;
+            s = zs_grid_value(k + need * inc, eg);
+            return (long long)done + need - 1;
+        }
+        s = zs_grid_value(k + n * inc, eg);
+        done += n;
+    }
+    return -1;
 }
