@@ -60,7 +60,10 @@ extern "C" void zs_ctx_destroy(zs_ctx* ctx) {
     hipGetDevice(&dev);
     hipSetDevice(ctx->device);
     for (int i = 0; i < 16; i++)
-        if (ctx->events[i]) hipEventDestroy((hipEvent_t)ctx->events[i]);
+        if (ctx->events[i]) (void)hipEventDestroy((hipEvent_t)ctx->events[i]);
+    if (ctx->fork_event) (void)hipEventDestroy((hipEvent_t)ctx->fork_event);
+    if (ctx->join_event) (void)hipEventDestroy((hipEvent_t)ctx->join_event);
+    if (ctx->side_stream) (void)hipStreamDestroy((hipStream_t)ctx->side_stream);
     void* ptrs[] = {ctx->p_cnt, ctx->p_id, ctx->p_flags, ctx->p_y, ctx->cst, ctx->cs_key, ctx->cs_idx,
                     ctx->co_key, ctx->co_idx, ctx->rst, ctx->pairs, ctx->pv, ctx->mask_scratch, ctx->spec_chunks,
                     ctx->spec_rows, ctx->sub_mom, ctx->sub_sum, ctx->p_sub};
@@ -105,13 +108,24 @@ extern "C" int zs_ctx_create(int device, uint32_t max_rows, uint32_t max_vocab, 
     if (!rc) rc = zs_alloc(ctx, &ctx->co_idx, R * C * ZS_KO);
     if (!rc) rc = zs_alloc(ctx, &ctx->rst, R);
     if (!rc) rc = zs_alloc(ctx, &ctx->pairs, R * (size_t)max_vocab * 2);
-    if (!rc) rc = zs_alloc(ctx, &ctx->pv, R * (size_t)max_vocab);
+    if (!rc) rc = zs_alloc(ctx, &ctx->pv, R * (size_t)max_vocab + 4);  // 16-byte loads at the tail
     if (!rc) rc = zs_alloc(ctx, (uint32_t**)&ctx->mask_scratch, R);
     if (!rc) rc = zs_alloc(ctx, &ctx->spec_chunks, R * (2 * ZS_SPEC_KMAX + 1) * C);
     if (!rc) rc = zs_alloc(ctx, &ctx->sub_mom, R * ctx->max_subs);
     if (!rc) rc = zs_alloc(ctx, &ctx->sub_sum, R * ZS_NSUM * ctx->max_subs);
     if (!rc) rc = zs_alloc(ctx, &ctx->p_sub, R * (ctx->max_subs + 1));
     if (!rc) rc = zs_alloc(ctx, &ctx->spec_rows, R);
+    if (!rc) {
+        hipStream_t s2 = nullptr;
+        hipEvent_t e1 = nullptr, e2 = nullptr;
+        if (hipStreamCreateWithFlags(&s2, hipStreamNonBlocking) != hipSuccess ||
+            hipEventCreateWithFlags(&e1, hipEventDisableTiming) != hipSuccess ||
+            hipEventCreateWithFlags(&e2, hipEventDisableTiming) != hipSuccess)
+            rc = ZS_EHIP;
+        ctx->side_stream = s2;
+        ctx->fork_event = e1;
+        ctx->join_event = e2;
+    }
     hipSetDevice(prev);
     if (rc) {
         zs_ctx_destroy(ctx);

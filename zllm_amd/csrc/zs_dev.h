@@ -129,6 +129,27 @@ __device__ __forceinline__ uint32_t block_excl_scan_u(uint32_t v, uint32_t* sh, 
     *total = tot;
     return pre + inc - v;
 }
+// Exclusive scan of doubles in thread order; sets *total.
+template <int NT>
+__device__ __forceinline__ double block_excl_scan_d(double v, double* sh, double* total) {
+    const int lane = zs_lane();
+    double inc = v;
+    for (int d = 1; d < 64; d <<= 1) {
+        double y = __shfl_up(inc, d, 64);
+        if (lane >= d) inc += y;
+    }
+    if (lane == 63) sh[zs_wid()] = inc;
+    __syncthreads();
+    double pre = 0.0, tot = 0.0;
+    for (int i = 0; i < NT / 64; i++) {
+        double w = sh[i];
+        if (i < zs_wid()) pre += w;
+        tot += w;
+    }
+    __syncthreads();
+    *total = tot;
+    return pre + (inc - v);
+}
 // Same with saturating add (exclusive value computed without subtraction).
 template <int NT>
 __device__ __forceinline__ uint32_t block_excl_scan_sat(uint32_t v, uint32_t* sh, uint32_t* total) {

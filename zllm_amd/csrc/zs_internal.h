@@ -163,6 +163,11 @@ struct zs_ctx {
     uint32_t max_subs;
     zs_spec_chunk* spec_chunks;  // [rows][2*ZS_SPEC_KMAX+1][max_chunks]
     zs_spec_row* spec_rows;      // [rows]
+    // side stream for the observers' entropy chain, which runs beside the big
+    // rows (fork / join by events on the caller's stream; default priority)
+    void* side_stream;     // hipStream_t
+    void* fork_event;      // hipEvent_t
+    void* join_event;      // hipEvent_t
     // profiling (zs_set_profiling)
     int profiling;
     int n_timed;

@@ -1337,7 +1337,7 @@ __device__ __forceinline__ void stitch_sub(const F& f, float& s, bool first, st_
 // One workgroup per (row, sum): the exact running sum over the row's
 // sub-chunks, taking the rounds' totals where the predicted grid holds.
 template <int KIND>
-__global__ __launch_bounds__(ST_NT) void zs_k_stitch(zs_sargs a) {
+__device__ __forceinline__ void stitch_body(const zs_sargs& a) {
     const uint32_t r = blockIdx.x;
     zs_row_state* st = a.rst + r;
     const uint32_t rounds = st->rounds;
@@ -1440,16 +1440,24 @@ __global__ __launch_bounds__(ST_NT) void zs_k_stitch(zs_sargs a) {
     }
 }
 
+// the observers' S (blockIdx.y 0) and the sampler's S (1) side by side
+__global__ __launch_bounds__(ST_NT) void zs_k_stitchA(zs_sargs a) {
+    if (blockIdx.y == 0) stitch_body<ZS_SUM_OBS_S>(a);
+    else stitch_body<ZS_SUM_SAMP_S>(a);
+}
+__global__ __launch_bounds__(ST_NT) void zs_k_stitchB(zs_sargs a) { stitch_body<ZS_SUM_OBS_H>(a); }
+
 // ===========================================================================
 // zs_k_big: exact emulation of the reference's sequential sums over a full row.
 // ===========================================================================
 #define BK_NB 2048   // buckets per level of the top-p walk
+#define BK_NC 16     // copies of each bucket counter (by lane)
+static_assert(BK_NB * BK_NC <= ZS_SORT_CAP, "per-copy bucket counters live in the sort buffer");
 
 struct big_shared {
     seq_sh<ZS_BIG_NT> q;
     uint32_t u[8];
     float s;
-    uint32_t pc0, pc1;
     uint32_t hist[BK_NB + 1];    // level 0: bucket starts by rank (rank 0 = largest values)
     uint32_t hist1[BK_NB + 1];   // level 1 (refinement of one oversize bucket)
     uint32_t hist2[256];         // level 2: counts of single values
@@ -1463,42 +1471,44 @@ struct big_row {
     const uint32_t* pid;
     const uint32_t* pfl;
     const float* py;
-    uint32_t np;
+    const uint32_t* psub;
+    uint32_t nsub;
     uint32_t V;
     float T;
 };
 
-// x~ (observers: mask and bans) and z (sampler: patched y, divided by T) of the
-// 4 elements idx0..idx0+3 of group g; the patch cursor advances in sh.pc0/pc1.
-__device__ __forceinline__ void big_load2(const big_row& R, uint32_t g, float (&x)[4], float (&z)[4],
-                                          big_shared& sh) {
-    const int t = threadIdx.x;
-    const uint32_t g0 = g * ZS_BIG_G;
-    if (t == 0) {
-        uint32_t p = sh.pc1;  // groups are visited in increasing order within a pass
-        if (g0 == 0) p = 0;
-        while (p < R.np && R.pid[p] < g0) p++;
-        uint32_t q = p;
-        while (q < R.np && R.pid[q] < g0 + ZS_BIG_G) q++;
-        sh.pc0 = p;
-        sh.pc1 = q;
-    }
-    __syncthreads();
-    const uint32_t idx0 = g0 + 4 * t;
-    float4 v = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
-    uint32_t w = 0xffffffffu;
+// Raw loads of group g for thread t: 4 logits and the allow word.
+struct big_raw {
+    float4 v;
+    uint32_t w;
+};
+__device__ __forceinline__ big_raw big_fetch(const big_row& R, uint32_t g) {
+    const uint32_t idx0 = g * ZS_BIG_G + 4 * threadIdx.x;
+    big_raw o;
+    o.v = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+    o.w = 0xffffffffu;
     if (idx0 < R.V) {
-        v = *reinterpret_cast<const float4*>(R.row + idx0);
-        if (R.masked) w = R.allow[idx0 >> 5] >> (idx0 & 31);
+        o.v = *reinterpret_cast<const float4*>(R.row + idx0);
+        if (R.masked) o.w = R.allow[idx0 >> 5] >> (idx0 & 31);
     }
-    x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+    return o;
+}
+// x~ (observers: mask and bans) and z (sampler: patched y, divided by T) of the
+// 4 elements idx0..idx0+3 of group g; the group's patches are those of its
+// ZS_BIG_G / ZS_SUB sub-chunks (per-sub-chunk patch offsets from zs_k_prep).
+__device__ __forceinline__ void big_finish(const big_row& R, uint32_t g, const big_raw& raw, float (&x)[4],
+                                           float (&z)[4]) {
+    const uint32_t idx0 = g * ZS_BIG_G + 4 * threadIdx.x;
+    x[0] = raw.v.x; x[1] = raw.v.y; x[2] = raw.v.z; x[3] = raw.v.w;
 #pragma unroll
     for (int q = 0; q < 4; q++) {
         if (idx0 + q >= R.V) x[q] = -INFINITY;
-        else if (R.masked && !((w >> q) & 1u)) x[q] = -INFINITY;
+        else if (R.masked && !((raw.w >> q) & 1u)) x[q] = -INFINITY;
         z[q] = x[q];
     }
-    for (uint32_t p = sh.pc0; p < sh.pc1; p++) {
+    const uint32_t s0 = g * (ZS_BIG_G / ZS_SUB);
+    const uint32_t p0 = R.psub[s0], p1 = R.psub[min(s0 + ZS_BIG_G / ZS_SUB, R.nsub)];
+    for (uint32_t p = p0; p < p1; p++) {
         uint32_t off = R.pid[p] - idx0;
         if (off < 4) {
             uint32_t fl = R.pfl[p];
@@ -1513,7 +1523,29 @@ __device__ __forceinline__ void big_load2(const big_row& R, uint32_t g, float (&
     }
 #pragma unroll
     for (int q = 0; q < 4; q++) z[q] = zs_temper(z[q], R.T);
-    __syncthreads();
+}
+__device__ __forceinline__ void big_load2(const big_row& R, uint32_t g, float (&x)[4], float (&z)[4],
+                                          big_shared& sh) {
+    big_finish(R, g, big_fetch(R, g), x, z);
+}
+// Calls f(g, z) for every group in order, with the loads of BK_U groups in
+// flight at once (a single 16-byte load per thread leaves a one-workgroup
+// stream latency-bound). f returns true to stop; it must be uniform.
+#define BK_U 8
+template <class F>
+__device__ __forceinline__ void big_stream_z(const big_row& R, uint32_t ng, const F& f) {
+    for (uint32_t g0 = 0; g0 < ng; g0 += BK_U) {
+        big_raw raw[BK_U];
+#pragma unroll
+        for (int u = 0; u < BK_U; u++) raw[u] = g0 + u < ng ? big_fetch(R, g0 + u) : big_raw{};
+#pragma unroll
+        for (int u = 0; u < BK_U; u++) {
+            if (g0 + u >= ng) break;
+            float x[4], z[4];
+            big_finish(R, g0 + u, raw[u], x, z);
+            if (f(g0 + u, z)) return;
+        }
+    }
 }
 __device__ __forceinline__ void big_load_z(const big_row& R, uint32_t g, float (&z)[4], big_shared& sh) {
     float x[4];
@@ -1540,6 +1572,12 @@ __device__ __forceinline__ float big_term_e(float z, bool has_thr, float thr, fl
 // (value, rank among the equal values passed): the index order among equal
 // probabilities is resolved afterwards on the row.
 // ---------------------------------------------------------------------------
+#ifdef ZS_DEBUG_WALK
+__device__ unsigned long long zs_dbg_walk[256][6];
+#define WALK_COUNT(k, v) do { if (threadIdx.x == 0) zs_dbg_walk[blockIdx.x][k] += (v); } while (0)
+#else
+#define WALK_COUNT(k, v) do {} while (0)
+#endif
 struct walk_out {
     bool stopped;
     uint32_t v;      // stop value (f32 bits)
@@ -1566,6 +1604,7 @@ __device__ void bk_sort_desc(uint32_t* a, int n) {
 // Walk n <= ZS_SORT_CAP values in exact descending order (sorted in LDS).
 __device__ walk_out bk_walk_sorted(const uint32_t* vals, uint32_t n, float& s, float thresh, big_shared& sh) {
     walk_out o = {false, 0u, 0u};
+    WALK_COUNT(0, 1); WALK_COUNT(1, n);
     uint32_t np2 = 1;
     while (np2 < n) np2 <<= 1;
     for (uint32_t i = threadIdx.x; i < np2; i += ZS_BIG_NT) sh.sortbuf[i] = i < n ? vals[i] : 0u;
@@ -1602,9 +1641,18 @@ __device__ walk_out bk_walk_sorted(const uint32_t* vals, uint32_t n, float& s, f
 // possible values and add them as repeated terms, largest first.
 __device__ walk_out bk_walk_counts(const uint32_t* vals, uint32_t n, uint32_t prefix, float& s, float thresh,
                                    big_shared& sh) {
-    for (int i = threadIdx.x; i < 256; i += ZS_BIG_NT) sh.hist2[i] = 0;
+    uint32_t* cc = sh.sortbuf;  // per (value, copy) counts
+    for (int i = threadIdx.x; i < 256 * BK_NC; i += ZS_BIG_NT) cc[i] = 0;
     __syncthreads();
-    for (uint32_t i = threadIdx.x; i < n; i += ZS_BIG_NT) atomicAdd(&sh.hist2[vals[i] & 255u], 1u);
+    const uint32_t cp = threadIdx.x & (BK_NC - 1);
+    for (uint32_t i = threadIdx.x; i < n; i += ZS_BIG_NT) atomicAdd(&cc[(vals[i] & 255u) * BK_NC + cp], 1u);
+    __syncthreads();
+    for (int i = threadIdx.x; i < 256; i += ZS_BIG_NT) {
+        uint32_t c = 0;
+#pragma unroll
+        for (int k = 0; k < BK_NC; k++) c += cc[i * BK_NC + k];
+        sh.hist2[i] = c;
+    }
     __syncthreads();
     if (threadIdx.x == 0) {
         float ss = s;
@@ -1659,6 +1707,7 @@ __device__ walk_out bk_walk(const uint32_t* vals, uint32_t from, uint32_t to, co
         uint32_t excl[4];
         seq_find_res F = seq_find<ZS_BIG_NT, 4>(seq_terms<4>(tv), 0, s, thresh, excl, sh.q);
         const int first = min(min(F.ev, F.st), F.tie);
+        WALK_COUNT(2, 1); WALK_COUNT(3, F.tie < min(F.ev, F.st) ? 1 : 0); WALK_COUNT(4, F.ev < F.st ? 1 : 0);
         if (first == ZS_BIGI) {
             const uint32_t last = min(pos + ZS_BIG_G, to) - 1;
             const uint32_t bst = start[bk_rank<L>(vals[last])];
@@ -1689,26 +1738,89 @@ __device__ walk_out bk_exact(const uint32_t* vals, uint32_t n, float& s, float t
         return bk_walk_counts(vals, n, vals[0] & ~255u, s, thresh, sh);
     } else {
         // refine by bits 18..8 into tmp, bucket by bucket
-        for (int i = threadIdx.x; i <= BK_NB; i += ZS_BIG_NT) sh.hist1[i] = 0;
+        uint32_t* cur = sh.sortbuf;  // counts, then cursors, per (rank, copy)
+        const uint32_t cp = threadIdx.x & (BK_NC - 1);
+        for (int i = threadIdx.x; i < BK_NB * BK_NC; i += ZS_BIG_NT) cur[i] = 0;
         __syncthreads();
-        for (uint32_t i = threadIdx.x; i < n; i += ZS_BIG_NT) atomicAdd(&sh.hist1[bk_rank<1>(vals[i])], 1u);
+        for (uint32_t i = threadIdx.x; i < n; i += ZS_BIG_NT) atomicAdd(&cur[bk_rank<1>(vals[i]) * BK_NC + cp], 1u);
         __syncthreads();
-        if (threadIdx.x == 0) {
-            uint32_t acc = 0;
-            for (int i = 0; i <= BK_NB; i++) { uint32_t c = i < BK_NB ? sh.hist1[i] : 0u; sh.hist1[i] = acc; acc += c; }
+        {
+            uint32_t c2[2];
+#pragma unroll
+            for (int k2 = 0; k2 < 2; k2++) {
+                const int rk = 2 * threadIdx.x + k2;
+                uint32_t c = 0;
+#pragma unroll
+                for (int k = 0; k < BK_NC; k++) c += cur[rk * BK_NC + k];
+                c2[k2] = c;
+            }
+            uint32_t ctot;
+            const uint32_t cex = block_excl_scan_u<ZS_BIG_NT>(c2[0] + c2[1], sh.hist2, &ctot);
+            sh.hist1[2 * threadIdx.x] = cex;
+            sh.hist1[2 * threadIdx.x + 1] = cex + c2[0];
+            if (threadIdx.x == 0) sh.hist1[BK_NB] = ctot;
         }
         __syncthreads();
-        uint32_t* cur = sh.sortbuf;  // scatter cursors
-        for (int i = threadIdx.x; i < BK_NB; i += ZS_BIG_NT) cur[i] = sh.hist1[i];
+        for (int i = threadIdx.x; i < BK_NB; i += ZS_BIG_NT) {
+            uint32_t acc = sh.hist1[i];
+#pragma unroll
+            for (int k = 0; k < BK_NC; k++) { uint32_t c = cur[i * BK_NC + k]; cur[i * BK_NC + k] = acc; acc += c; }
+        }
         __syncthreads();
         for (uint32_t i = threadIdx.x; i < n; i += ZS_BIG_NT) {
             const uint32_t v = vals[i];
-            tmp[atomicAdd(&cur[bk_rank<1>(v)], 1u)] = v;
+            tmp[atomicAdd(&cur[bk_rank<1>(v) * BK_NC + cp], 1u)] = v;
         }
         __threadfence_block();
         __syncthreads();
         return bk_walk<1>(tmp, 0, n, sh.hist1, s, thresh, nullptr, sh);
     }
+}
+
+// The sampler's softmax denominator of a big row is known before zs_k_big when
+// the rounds summed it (or the observers' S is the same sum: z == x~, no cut).
+__device__ __forceinline__ bool big_s_from_rounds(const zs_row_state& st) {
+    const bool reuse = st.z_is_x && !st.has_thr && (st.obs_need & ZS_OBS_S);
+    return reuse || ((st.rounds >> ZS_SUM_SAMP_S) & 1u);
+}
+__device__ __forceinline__ float big_s_value(const zs_row_state& st) {
+    const bool reuse = st.z_is_x && !st.has_thr && (st.obs_need & ZS_OBS_S);
+    return reuse ? st.obs_S : st.samp_S;
+}
+
+// Probabilities p = exp(z - max) / S (sampler.rs:68-69) of the big rows whose
+// S is known, one workgroup per (group of ZS_BIG_G elements, row): the exact
+// exponentials are the bulk of a big row's arithmetic, spread here over the
+// whole GPU instead of one workgroup per row.
+__global__ __launch_bounds__(ZS_BIG_NT) void zs_k_pv(zs_sargs a) {
+    const uint32_t g = blockIdx.x, r = blockIdx.y;
+    const zs_row_state& st = a.rst[r];
+    if (st.mode != ZS_MODE_BIG || !big_s_from_rounds(st)) return;
+    const zs_batch& b = a.b;
+    const uint32_t V = b.V;
+    const uint32_t idx0 = g * ZS_BIG_G + 4 * threadIdx.x;
+    if (idx0 >= V) return;
+    const zs_row_params P = b.d_params[r];
+    big_row R;
+    R.row = b.d_logits + (size_t)r * b.ld;
+    R.masked = (P.flags & ZS_ROW_MASKED) && b.d_allow_bits;
+    R.allow = R.masked ? b.d_allow_bits + (size_t)r * b.allow_words : nullptr;
+    R.pid = a.p_id + (size_t)r * ZS_MAX_PATCHES;
+    R.pfl = a.p_flags + (size_t)r * ZS_MAX_PATCHES;
+    R.py = a.p_y + (size_t)r * ZS_MAX_PATCHES;
+    R.psub = a.p_sub + (size_t)r * (a.max_subs + 1);
+    R.nsub = (V + ZS_SUB - 1) / ZS_SUB;
+    R.V = V;
+    R.T = P.temperature;
+    const bool use_thr = st.has_thr != 0;
+    const float thr = zs_key_to_float(st.thr_key), m = st.z_max, S = big_s_value(st);
+    float x[4], z[4];
+    big_finish(R, g, big_fetch(R, g), x, z);
+    uint4 o;
+    uint32_t* ob = reinterpret_cast<uint32_t*>(&o);
+#pragma unroll
+    for (int q = 0; q < 4; q++) ob[q] = zs_f2u(idx0 + q < V ? big_term_e(z[q], use_thr, thr, m) / S : 0.0f);
+    *reinterpret_cast<uint4*>(a.pv + (size_t)r * a.max_vocab + idx0) = o;
 }
 
 __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
@@ -1727,15 +1839,21 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
     R.pid = a.p_id + (size_t)r * ZS_MAX_PATCHES;
     R.pfl = a.p_flags + (size_t)r * ZS_MAX_PATCHES;
     R.py = a.p_y + (size_t)r * ZS_MAX_PATCHES;
-    R.np = a.p_cnt[r];
+    R.psub = a.p_sub + (size_t)r * (a.max_subs + 1);
+    R.nsub = (b.V + ZS_SUB - 1) / ZS_SUB;
     R.V = b.V;
     R.T = P.temperature;
     const uint32_t V = b.V;
     const uint32_t ng = (V + ZS_BIG_G - 1) / ZS_BIG_G;
     const float m = stt.z_max;
     uint32_t* pv = a.pv + (size_t)r * a.max_vocab;
-    if (t == 0) sh.pc1 = 0;
-    __syncthreads();
+#ifdef XB_STOP
+    int nck = 0;
+#define BIG_MARK() do { if (++nck == XB_STOP) { if (t == 0) { a.rst[r].token = 0; a.rst[r].mode = ZS_MODE_DONE; } return; } } while (0)
+#else
+#define BIG_MARK() do {} while (0)
+#endif
+#define BIG_REPORT(tag) do {} while (0)
 
     // ---- top-k threshold by radix select when the candidates could not give it
     uint32_t has_thr = stt.has_thr;
@@ -1796,23 +1914,40 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
 
     // ---- probabilities p = exp(z - max) / S (sampler.rs:69), kept in pv for
     // the later passes; min-p kept mass (sampler.rs:72-88) in the same pass
+    BIG_MARK();
     const bool minp = P.min_p > 0.0f;
     const float cut = minp ? P.min_p * (1.0f / S) : 0.0f;  // p_max: the max element has exp(0) = 1
     float kept = 0.0f;
-    for (uint32_t g = 0; g < ng; g++) {
-        float z[4], tv[4];
-        big_load_z(R, g, z, sh);
+    if (big_s_from_rounds(stt)) {
+        // pv was filled by zs_k_pv; min-p needs the kept mass
+        if (minp) {
+            for (uint32_t g = 0; g < ng; g++) {
+                const uint32_t idx0 = g * ZS_BIG_G + 4 * t;
+                uint4 v = idx0 < V ? *reinterpret_cast<const uint4*>(pv + idx0) : make_uint4(0u, 0u, 0u, 0u);
+                float tv[4] = {zs_u2f(v.x), zs_u2f(v.y), zs_u2f(v.z), zs_u2f(v.w)};
+#pragma unroll
+                for (int q = 0; q < 4; q++) tv[q] = (tv[q] < cut) ? 0.0f : tv[q];
+                seq_group<ZS_BIG_NT, 4>(tv, 0, kept, NAN, sh.q);
+            }
+        }
+    } else big_stream_z(R, ng, [&](uint32_t g, const float (&z)[4]) {
+        float tv[4];
         const uint32_t idx0 = g * ZS_BIG_G + 4 * t;
+        uint4 o;
+        uint32_t* ob = reinterpret_cast<uint32_t*>(&o);
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-            const float p = big_term_e(z[q], use_thr, thr, m) / S;
-            if (idx0 + q < V) pv[idx0 + q] = zs_f2u(p);
+            const float p = idx0 + q < V ? big_term_e(z[q], use_thr, thr, m) / S : 0.0f;
+            ob[q] = zs_f2u(p);
             tv[q] = (p < cut) ? 0.0f : p;
         }
+        if (idx0 < V) *reinterpret_cast<uint4*>(pv + idx0) = o;
         if (minp) seq_group<ZS_BIG_NT, 4>(tv, 0, kept, NAN, sh.q);
-    }
+        return false;
+    });
     __threadfence_block();
     __syncthreads();
+    BIG_MARK();
     auto p1_of = [&](uint32_t pb) -> float {
         float p = zs_u2f(pb);
         if (minp) {
@@ -1821,13 +1956,23 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
         }
         return p;
     };
-    auto load_p1 = [&](uint32_t g, float (&p)[4]) {
-        const uint32_t idx0 = g * ZS_BIG_G + 4 * t;
-        uint4 v = make_uint4(0u, 0u, 0u, 0u);
-        if (idx0 < V) v = *reinterpret_cast<const uint4*>(pv + idx0);
-        p[0] = p1_of(v.x); p[1] = p1_of(v.y); p[2] = p1_of(v.z); p[3] = p1_of(v.w);
+    // f(g, p1[4]) for every group in order, BK_U groups of loads in flight;
+    // elements past V read 0 (pv holds 0 there); f returns true to stop
+    auto stream_p1 = [&](auto&& f) {
+        for (uint32_t g0 = 0; g0 < ng; g0 += BK_U) {
+            uint4 v[BK_U];
 #pragma unroll
-        for (int q = 0; q < 4; q++) if (idx0 + q >= V) p[q] = 0.0f;
+            for (int u = 0; u < BK_U; u++) {
+                const uint32_t idx0 = (g0 + u) * ZS_BIG_G + 4 * t;
+                v[u] = (g0 + u < ng && idx0 < V) ? *reinterpret_cast<const uint4*>(pv + idx0) : make_uint4(0u, 0u, 0u, 0u);
+            }
+#pragma unroll
+            for (int u = 0; u < BK_U; u++) {
+                if (g0 + u >= ng) break;
+                float p[4] = {p1_of(v[u].x), p1_of(v[u].y), p1_of(v[u].z), p1_of(v[u].w)};
+                if (f(g0 + u, p)) return;
+            }
+        }
     };
 
     // ---- top-p (sampler.rs:91-115)
@@ -1837,115 +1982,202 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
     if (topp) {
         uint32_t* gv = a.pairs + (size_t)r * a.max_vocab * 2;  // level-0 layout
         uint32_t* tmp = gv + a.max_vocab;                       // level-1 refinement
-        for (int i = t; i <= BK_NB; i += ZS_BIG_NT) sh.hist[i] = 0;
+        // The largest probability is p1 of exp(0) / S. When it reaches top_p
+        // alone, the walk stops at the first element of the sorted order: the
+        // lowest index holding that value.
+        const uint32_t pmax1 = zs_f2u(p1_of(zs_f2u(1.0f / S)));
+        const bool peak = zs_u2f(pmax1) >= P.top_p;
+        // counts per (rank, copy): 16 copies by lane keep same-address LDS
+        // atomics (skewed histograms) at most 4-way
+        uint32_t* cc = sh.sortbuf;
+        for (int i = t; i < BK_NB * BK_NC; i += ZS_BIG_NT) cc[i] = 0;
         __syncthreads();
-        for (uint32_t g = 0; g < ng; g++) {
-            float p[4];
-            load_p1(g, p);
+        const uint32_t cp = (uint32_t)t & (BK_NC - 1);
+        if (!peak)
+            stream_p1([&](uint32_t, const float (&p)[4]) {
 #pragma unroll
-            for (int q = 0; q < 4; q++)
-                if (p[q] > 0.0f) atomicAdd(&sh.hist[bk_rank<0>(zs_f2u(p[q]))], 1u);
-        }
+                for (int q = 0; q < 4; q++)
+                    if (p[q] > 0.0f) atomicAdd(&cc[bk_rank<0>(zs_f2u(p[q])) * BK_NC + cp], 1u);
+                return false;
+            });
         __syncthreads();
-        // bucket starts by rank, and the first candidate range: buckets whose
+        // bucket starts by rank and the first candidate range: the ranks whose
         // guaranteed mass (count * bucket floor) reaches 1.02 * top_p
-        if (t == 0) {
-            uint32_t acc = 0;
-            double lb = 0.0;
-            uint32_t rlim = BK_NB - 1;
-            bool found = false;
-            for (int rk = 0; rk <= BK_NB; rk++) {
-                const uint32_t c = rk < BK_NB ? sh.hist[rk] : 0u;
-                sh.hist[rk] = acc;
-                acc += c;
-                if (rk < BK_NB && !found) {
-                    lb += (double)c * (double)zs_u2f((uint32_t)(BK_NB - 1 - rk) << 19);
-                    if (lb >= 1.02 * (double)P.top_p) { rlim = (uint32_t)rk; found = true; }
-                }
+        static_assert(BK_NB == 2 * ZS_BIG_NT, "two ranks per thread");
+        if (!peak) {
+            uint32_t c2[2];
+            double m2[2];
+#pragma unroll
+            for (int k2 = 0; k2 < 2; k2++) {
+                const int rk = 2 * t + k2;
+                uint32_t c = 0;
+#pragma unroll
+                for (int k = 0; k < BK_NC; k++) c += cc[rk * BK_NC + k];
+                c2[k2] = c;
+                m2[k2] = (double)c * (double)zs_u2f((uint32_t)(BK_NB - 1 - rk) << 19);
             }
-            sh.u[0] = rlim;
+            uint32_t ctot;
+            double mtot;
+            const uint32_t cex = block_excl_scan_u<ZS_BIG_NT>(c2[0] + c2[1], sh.hist2, &ctot);
+            const double mex = block_excl_scan_d<ZS_BIG_NT>(m2[0] + m2[1], reinterpret_cast<double*>(sh.hist2), &mtot);
+            sh.hist[2 * t] = cex;
+            sh.hist[2 * t + 1] = cex + c2[0];
+            if (t == 0) sh.hist[BK_NB] = ctot;
+            const double lim = 1.02 * (double)P.top_p;
+            int cand = ZS_BIGI;
+            if (mex + m2[0] >= lim) cand = 2 * t;
+            else if (mex + m2[0] + m2[1] >= lim) cand = 2 * t + 1;
+            cand = block_min_i<ZS_BIG_NT>(cand, reinterpret_cast<int*>(sh.hist2));
+            if (t == 0) sh.u[0] = cand == ZS_BIGI ? (uint32_t)(BK_NB - 1) : (uint32_t)cand;
         }
         __syncthreads();
+        BIG_MARK();
         const uint32_t rlim = sh.u[0];
         float s = 0.0f;
         walk_out wo = {false, 0u, 0u};
         uint32_t done = 0;  // walked prefix of the level-0 layout
-        for (int round = 0; round < 2 && !wo.stopped; round++) {
+        for (int round = 0; round < 2 && !wo.stopped && !peak; round++) {
             const uint32_t rlo = round == 0 ? 0u : rlim + 1, rhi = round == 0 ? rlim : BK_NB - 1;
             if (rlo > rhi) break;
-            uint32_t* cur = sh.sortbuf;  // gather cursors
-            for (int i = t; i < BK_NB; i += ZS_BIG_NT) cur[i] = sh.hist[i];
+            // per (rank, copy) counts of the ranks gathered now (round 0 has
+            // them from the histogram), turned into cursors inside each bucket
+            uint32_t* cur = sh.sortbuf;
+            if (round > 0) {
+                for (int i = t; i < BK_NB * BK_NC; i += ZS_BIG_NT) cur[i] = 0;
+                __syncthreads();
+                stream_p1([&](uint32_t, const float (&p)[4]) {
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const uint32_t rk = bk_rank<0>(zs_f2u(p[q]));
+                        if (p[q] > 0.0f && rk >= rlo && rk <= rhi) atomicAdd(&cur[rk * BK_NC + cp], 1u);
+                    }
+                    return false;
+                });
+                __syncthreads();
+            }
+            for (uint32_t i = rlo + t; i <= rhi; i += ZS_BIG_NT) {
+                uint32_t acc = sh.hist[i];
+#pragma unroll
+                for (int k = 0; k < BK_NC; k++) { uint32_t c = cur[i * BK_NC + k]; cur[i * BK_NC + k] = acc; acc += c; }
+            }
             __syncthreads();
-            for (uint32_t g = 0; g < ng; g++) {
-                float p[4];
-                load_p1(g, p);
+            stream_p1([&](uint32_t, const float (&p)[4]) {
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    if (!(p[q] > 0.0f)) continue;
                     const uint32_t pb = zs_f2u(p[q]);
                     const uint32_t rk = bk_rank<0>(pb);
-                    if (rk >= rlo && rk <= rhi) gv[atomicAdd(&cur[rk], 1u)] = pb;
+                    if (p[q] > 0.0f && rk >= rlo && rk <= rhi) gv[atomicAdd(&cur[rk * BK_NC + cp], 1u)] = pb;
                 }
-            }
+                return false;
+            });
             __threadfence_block();
             __syncthreads();
             const uint32_t upto = sh.hist[rhi + 1];
             wo = bk_walk<0>(gv, done, upto, sh.hist, s, P.top_p, tmp, sh);
             done = upto;
         }
+        BIG_MARK();
+        if (peak) wo = {true, pmax1, 0u};
         if (wo.stopped) {
-            // i*: the index of the (rank+1)-th element, in index order, whose
-            // probability is v* (sampler.rs:93: the sort is stable)
             vstar = wo.v;
-            const uint32_t nbl = (V + 511) / 512;
-            for (uint32_t i = t; i < nbl; i += ZS_BIG_NT) sh.sortbuf[i] = 0;
-            __syncthreads();
-            for (uint32_t g = 0; g < ng; g++) {
-                float p[4];
-                load_p1(g, p);
+            // The kept set is {p1 > v*} plus the first rank+1 elements equal to v*
+            // in index order (the sort is stable). Compact {p1 >= v*} in index
+            // order; sum2 and the draw only see these (the others are 0 and
+            // leave a running sum unchanged).
+            uint32_t* kp = gv;
+            uint32_t* ki = tmp;
+            uint32_t nk = 0;
+            stream_p1([&](uint32_t g, const float (&p)[4]) {
+                uint32_t c = 0;
 #pragma unroll
-                for (int q = 0; q < 4; q++)
-                    if (zs_f2u(p[q]) == vstar && p[q] > 0.0f) atomicAdd(&sh.sortbuf[(g * ZS_BIG_G + 4 * t + q) >> 9], 1u);
-            }
-            __syncthreads();
-            if (t == 0) {
-                uint32_t acc = 0, blk = 0;
-                sh.u[7] = 0xffffffffu;
-                for (uint32_t i = 0; i < nbl; i++) {
-                    if (acc + sh.sortbuf[i] > wo.rank) { blk = i; break; }
-                    acc += sh.sortbuf[i];
+                for (int q = 0; q < 4; q++) c += (p[q] > 0.0f && zs_f2u(p[q]) >= vstar) ? 1u : 0u;
+                uint32_t tot;
+                uint32_t pos = nk + block_excl_scan_u<ZS_BIG_NT>(c, sh.hist2, &tot);
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    if (p[q] > 0.0f && zs_f2u(p[q]) >= vstar) {
+                        kp[pos] = zs_f2u(p[q]);
+                        ki[pos] = g * ZS_BIG_G + 4 * t + q;
+                        pos++;
+                    }
                 }
-                sh.u[0] = blk;
-                sh.u[1] = wo.rank - acc;
+                nk += tot;
+                return false;
+            });
+            __threadfence_block();
+            __syncthreads();
+            BIG_MARK();
+            // i*: the (rank+1)-th list element equal to v*
+            if (t == 0) sh.u[7] = 0xffffffffu;
+            __syncthreads();
+            uint32_t seen = 0;
+            for (uint32_t q0 = 0; q0 < nk; q0 += ZS_BIG_NT) {
+                const uint32_t i = q0 + t;
+                const uint32_t hit = (i < nk && kp[i] == vstar) ? 1u : 0u;
+                uint32_t tot;
+                const uint32_t ex = block_excl_scan_u<ZS_BIG_NT>(hit, sh.hist2, &tot);
+                if (hit && seen + ex == wo.rank) sh.u[7] = ki[i];
+                seen += tot;
+                if (seen > wo.rank) break;
             }
-            __syncthreads();
-            const uint32_t blk = sh.u[0], want = sh.u[1];
-            const uint32_t idx = blk * 512 + (uint32_t)t;
-            uint32_t hit = 0;
-            if (t < 512 && idx < V) hit = (pv[idx] != 0u && zs_f2u(p1_of(pv[idx])) == vstar) ? 1u : 0u;
-            uint32_t tot;
-            const uint32_t ex = block_excl_scan_u<ZS_BIG_NT>(hit, sh.hist2, &tot);
-            __syncthreads();
-            if (hit && ex == want) sh.u[7] = idx;
             __syncthreads();
             istar = sh.u[7];
             __syncthreads();
-        } else {
-            vstar = 0;
-            istar = 0xffffffffu;  // every positive p kept
-        }
-        // ---- sum over the kept set in index order (sampler.rs:107)
-        sum2 = -0.0f;
-        for (uint32_t g = 0; g < ng; g++) {
-            float p[4], tv[4];
-            load_p1(g, p);
+            // ---- sum over the kept set in index order (sampler.rs:107)
+            auto kept_term = [&](uint32_t i) -> float {
+                if (i >= nk) return 0.0f;
+                const uint32_t pb = kp[i];
+                return (pb > vstar || ki[i] <= istar) ? zs_u2f(pb) : 0.0f;
+            };
+            sum2 = -0.0f;
+            for (uint32_t q0 = 0; q0 < nk; q0 += ZS_BIG_G) {
+                float tv[4];
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const uint32_t pb = zs_f2u(p[q]), idx = g * ZS_BIG_G + 4 * t + q;
-                const bool keep = pb > vstar || (pb == vstar && idx <= istar);
-                tv[q] = keep ? p[q] : 0.0f;
+                for (int q = 0; q < 4; q++) tv[q] = kept_term(q0 + 4 * t + q);
+                seq_group<ZS_BIG_NT, 4>(tv, 0, sum2, NAN, sh.q);
             }
-            seq_group<ZS_BIG_NT, 4>(tv, 0, sum2, NAN, sh.q);
+            BIG_MARK();
+            if (sum2 > 0.0f) {
+                // ---- draw (sampler.rs:118-127) over the renormalised kept set
+                const float rr = zs_philox_uniform(b.d_seed[r], b.d_counter[r], 0u);
+                uint32_t token = V - 1;
+                if (rr <= 0.0f) {
+                    token = 0;
+                } else {
+                    float cum = 0.0f;
+                    for (uint32_t q0 = 0; q0 < nk; q0 += ZS_BIG_G) {
+                        float tv[4];
+#pragma unroll
+                        for (int q = 0; q < 4; q++) {
+                            const float pp = kept_term(q0 + 4 * t + q);
+                            tv[q] = pp > 0.0f ? pp / sum2 : 0.0f;
+                        }
+                        int stp = seq_group<ZS_BIG_NT, 4>(tv, 0, cum, rr, sh.q);
+                        if (stp >= 0) { token = ki[q0 + (uint32_t)stp]; break; }
+                    }
+                }
+                BIG_MARK();
+#ifdef ZS_DEBUG_WALK
+                if (t == 0) printf("walk row %u peak %d nk %u sorts %llu sorted %llu finds %llu tiefirst %llu evfirst %llu\n", r, (int)peak, nk,
+                                   zs_dbg_walk[r][0], zs_dbg_walk[r][1], zs_dbg_walk[r][2], zs_dbg_walk[r][3], zs_dbg_walk[r][4]);
+#endif
+                if (t == 0) {
+                    // only the sampler's fields: the observers' entropy is written
+                    // concurrently by the side stream
+                    a.rst[r].token = token;
+                    a.rst[r].mode = ZS_MODE_DONE;
+                }
+                return;
+            }
+        } else {
+            // every positive p kept: sum over the whole row
+            vstar = 0;
+            istar = 0xffffffffu;
+            sum2 = -0.0f;
+            stream_p1([&](uint32_t, const float (&p)[4]) {
+                seq_group<ZS_BIG_NT, 4>(p, 0, sum2, NAN, sh.q);
+                return false;
+            });
         }
     }
     // ---- draw (sampler.rs:118-127)
@@ -1956,9 +2188,8 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
     } else {
         float cum = 0.0f;
         const bool renorm = topp && sum2 > 0.0f;
-        for (uint32_t g = 0; g < ng; g++) {
-            float p[4], tv[4];
-            load_p1(g, p);
+        stream_p1([&](uint32_t g, const float (&p)[4]) {
+            float tv[4];
 #pragma unroll
             for (int q = 0; q < 4; q++) {
                 float pp = p[q];
@@ -1970,13 +2201,13 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
                 tv[q] = pp;
             }
             int stp = seq_group<ZS_BIG_NT, 4>(tv, 0, cum, rr, sh.q);
-            if (stp >= 0) { token = g * ZS_BIG_G + stp; break; }
-        }
+            if (stp >= 0) { token = g * ZS_BIG_G + stp; return true; }
+            return false;
+        });
     }
     if (t == 0) {
-        stt.token = token;
-        stt.mode = ZS_MODE_DONE;
-        a.rst[r] = stt;
+        a.rst[r].token = token;
+        a.rst[r].mode = ZS_MODE_DONE;
     }
 }
 
@@ -2087,6 +2318,12 @@ __global__ void zs_k_final(zs_sargs a) {
 // ===========================================================================
 // host launcher
 // ===========================================================================
+#define ZS_LAUNCH_CHECK(call)                                                                   \
+    do {                                                                                        \
+        hipError_t e_ = (call);                                                                 \
+        if (e_ != hipSuccess) return zs_set_error(ctx, ZS_EHIP, "zs_sample: %s", hipGetErrorString(e_)); \
+    } while (0)
+
 extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t stream) {
     zs_sargs a;
     a.b = *bt;
@@ -2128,15 +2365,26 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
     const uint32_t nsub = (bt->V + ZS_SUB - 1) / ZS_SUB;
     hipLaunchKernelGGL(zs_k_roundA, dim3((nsub + 3) / 4, B), dim3(256), 0, stream, a);
     mark("zs_k_roundA");
-    hipLaunchKernelGGL(zs_k_stitch<ZS_SUM_OBS_S>, dim3(B), dim3(ST_NT), 0, stream, a);
-    hipLaunchKernelGGL(zs_k_stitch<ZS_SUM_SAMP_S>, dim3(B), dim3(ST_NT), 0, stream, a);
+    hipLaunchKernelGGL(zs_k_stitchA, dim3(B, 2), dim3(ST_NT), 0, stream, a);
     mark("zs_k_stitchA");
-    hipLaunchKernelGGL(zs_k_roundB, dim3((nsub + 3) / 4, B), dim3(256), 0, stream, a);
+    // The entropy chain (roundB, stitchB) depends on the observers' S only and
+    // runs on the side stream while the big rows run here; profiling keeps one
+    // stream so that every kernel has its own interval.
+    hipStream_t side = prof ? stream : (hipStream_t)ctx->side_stream;
+    if (!prof) {
+        ZS_LAUNCH_CHECK(hipEventRecord((hipEvent_t)ctx->fork_event, stream));
+        ZS_LAUNCH_CHECK(hipStreamWaitEvent(side, (hipEvent_t)ctx->fork_event, 0));
+    }
+    hipLaunchKernelGGL(zs_k_roundB, dim3((nsub + 3) / 4, B), dim3(256), 0, side, a);
     mark("zs_k_roundB");
-    hipLaunchKernelGGL(zs_k_stitch<ZS_SUM_OBS_H>, dim3(B), dim3(ST_NT), 0, stream, a);
+    hipLaunchKernelGGL(zs_k_stitchB, dim3(B), dim3(ST_NT), 0, side, a);
     mark("zs_k_stitchB");
+    if (!prof) ZS_LAUNCH_CHECK(hipEventRecord((hipEvent_t)ctx->join_event, side));
+    hipLaunchKernelGGL(zs_k_pv, dim3((bt->V + ZS_BIG_G - 1) / ZS_BIG_G, B), dim3(ZS_BIG_NT), 0, stream, a);
+    mark("zs_k_pv");
     hipLaunchKernelGGL(zs_k_big, dim3(B), dim3(ZS_BIG_NT), 0, stream, a);
     mark("zs_k_big");
+    if (!prof) ZS_LAUNCH_CHECK(hipStreamWaitEvent(stream, (hipEvent_t)ctx->join_event, 0));
     hipLaunchKernelGGL(zs_k_final, dim3((B + 63) / 64), dim3(64), 0, stream, a);
     mark("zs_k_final");
     if (prof) ctx->n_timed = ev - 1;
