@@ -66,13 +66,28 @@ def build_workload(B, V, S, seed):
         rq.detect_hallucination = True
         rows.append(rq)
     xs = torch.from_numpy(x).cuda()
+    # speculative decoding, k=4 draft positions per row: target logits at k+1
+    # positions and draft logits at k, both synthetic N(0, 2) plus a peak
+    # shared by draft and target so that drafts are often accepted
+    g = torch.Generator(device="cuda").manual_seed(seed + 99)
+    K = SPEC_K
+    peak_ids = torch.randint(0, V, (B, K + 1), device="cuda", generator=g)
+    tgt = torch.randn((B, K + 1, V), device="cuda", generator=g) * 2.0
+    tgt.scatter_add_(2, peak_ids[:, :, None], torch.full((B, K + 1, 1), 12.0, device="cuda"))
+    dft = tgt[:, :K, :] + torch.randn((B, K, V), device="cuda", generator=g) * 0.5
+    dft = dft.contiguous()
+    draft_ids = peak_ids[:, :K].to(torch.int32).contiguous()
+    spec_T = torch.tensor([float(p["temperature"]) for p in params], dtype=torch.float32, device="cuda")
+    spec_seed = torch.arange(B, dtype=torch.int64, device="cuda") + 5000
+    spec_ctr = torch.zeros(B, dtype=torch.int64, device="cuda")
     sampler = BatchSampler(ctx)
     bufs = sampler.pack(xs, rows)
     st = torch.from_numpy(states).cuda()
     bits = torch.empty((B, (V + 31) // 32), dtype=torch.int32, device="cuda")
     return dict(ctx=ctx, x=x, xs=xs, params=params, rows=rows, sampler=sampler, bufs=bufs, dfa=dfa, table=table,
                 states=states, st=st, bits=bits, masked=masked, trans=trans, dead=dead, acc=acc, offs=offs,
-                data=data, valid=valid)
+                data=data, valid=valid, tgt=tgt, dft=dft, draft_ids=draft_ids, spec_T=spec_T, spec_seed=spec_seed,
+                spec_ctr=spec_ctr)
 
 
 def algorithmic_bytes_per_row(V, H, masked):
@@ -82,6 +97,14 @@ def algorithmic_bytes_per_row(V, H, masked):
     if masked:
         b += 4 * ((V + 31) // 32)
     return b
+
+
+SPEC_K = 4
+
+
+def spec_bytes_per_row(V, k):
+    # target logits at k+1 positions + draft logits at k positions + ids/outputs
+    return 4 * V * (2 * k + 1) + 4 * k + 8
 
 
 def cpu_baseline(W, seconds, cores):
@@ -127,10 +150,14 @@ def main():
     ctx, sampler, bufs, xs, bits = W["ctx"], W["sampler"], W["bufs"], W["xs"], W["bits"]
     stream = torch.cuda.current_stream()
 
+    from zllm_amd.engine import verify_drafts
+
     def step(out=None):
         W["dfa"].mask(W["table"], W["st"], V, out=bits)
         out = sampler.run(xs, bufs, bits, top_stride=5, out=out)
+        verify_drafts(ctx, W["tgt"], W["draft_ids"], W["spec_T"], W["spec_seed"], W["spec_ctr"], W["dft"])
         bufs["counter"].add_(1)
+        W["spec_ctr"].add_(1)
         return out
 
     out = None
@@ -144,6 +171,15 @@ def main():
     e1.record(stream)
     torch.cuda.synchronize()
     ms_step = e0.elapsed_time(e1) / args.steps
+
+    # spec verify alone (separate, untimed loop)
+    s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s0.record(stream)
+    for _ in range(10):
+        verify_drafts(ctx, W["tgt"], W["draft_ids"], W["spec_T"], W["spec_seed"], W["spec_ctr"], W["dft"])
+    s1.record(stream)
+    torch.cuda.synchronize()
+    us_spec = s0.elapsed_time(s1) / 10 * 1000.0
 
     # DFA mask alone and per-kernel timings of zs_sample (separate, untimed loops)
     m0, m1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -167,7 +203,7 @@ def main():
     status = out["status"].cpu().numpy()
     H = [len(p["counts"]) for p in W["params"]]
     row_bytes = [algorithmic_bytes_per_row(V, H[i], W["masked"][i]) for i in range(B)]
-    step_bytes = float(sum(row_bytes))
+    step_bytes = float(sum(row_bytes)) + B * spec_bytes_per_row(V, SPEC_K)
     dom = max(acc, key=acc.get)
     dom_ms = acc[dom]
     # algorithmic bytes attributed to the dominant kernel: the rows it processes
@@ -199,9 +235,10 @@ def main():
         "data": "synthetic (seeded power-law logits, synthetic vocab and 512-state DFA)",
         "config": {"workload": "C5 full continuous-batching sampler step", "B": B, "V": V,
                    "masked_rows": int(W["masked"].sum()), "dfa_states": args.dfa_states, "top_logprobs": 5,
-                   "entropy": True},
+                   "entropy": True, "spec_k": SPEC_K},
         "step_hbm_frac": round(step_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "dfa_mask_us": round(us_mask, 2),
+        "spec_verify_us": round(us_spec, 2),
         "kernel_ms": {k: round(v, 4) for k, v in acc.items()},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},

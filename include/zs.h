@@ -169,9 +169,11 @@ int zs_sample(zs_ctx* ctx, const zs_batch* batch, void* stream);
  * (spec_decode.rs:241-279): d_accepted = accepted drafts, d_next = the bonus /
  * corrected token. temperature > 0 is rejection sampling against the draft
  * distributions (the reference has none, rest.rs:2639); probabilities are
- * exact integer weights rint(expf(z - max) * 2^24), uniforms are Philox words
+ * exact integer weights rint(2^24 * 2^((z - max) log2 e)) from a fixed f32
+ * operation sequence (0 below z - max = -17.5), uniforms are Philox words
  * of (seed, counter, tag) -- tag 1+i for the test of draft i, 1+k+i for the
- * replacement draw at a rejection at i, 1+2k for the bonus draw. */
+ * replacement draw at a rejection at i, 1+2k for the bonus draw. Rows are
+ * read with 16-byte loads: ld >= V, ld % 4 == 0, both bases 16-byte aligned. */
 #define ZS_SPEC_KMAX 16
 typedef struct zs_spec_batch {
     uint32_t B, V, k;

@@ -571,7 +571,9 @@ ZO_API float zo_philox_uniform(uint64_t seed, uint64_t counter, uint32_t tag) {
  * Speculative-decode verification. temperature <= 0: verify_drafts
  * (spec_decode.rs:241-267). temperature > 0: rejection sampling
  * (Leviathan et al. 2023, Chen et al. 2023) as libzs defines it with
- * integer weights W_v = rint(expf(z_v - max z) * 2^24), z = x / T; accept
+ * integer weights W_v = w(z_v - max z), z = x / T, where w(d) is 0 for
+ * d < -17.5 and otherwise rint(2^24 * 2^t) with t = d * log2(e) evaluated
+ * as a fixed sequence of f32 operations (zo_spec_w_of below); accept
  * draft d at step i iff U_i * Q_d * sum(P) <= P_d * sum(Q) * 2^32 (U_i the
  * 32-bit Philox word, tag 1+i); at the first rejection draw from
  * max(0, P sum(Q) - Q sum(P)) (P if that is all zero) with tag 1+k+i; after k
@@ -607,10 +609,26 @@ static int zo_spec_row_max(const float* x, uint32_t V, float T, float* m) {
     return bad;
 }
 
-static uint64_t zo_spec_w(float x, float T, float m) {
-    float e = expf(zo_spec_z(x, T) - m);
-    return (uint64_t)rint((double)e * 16777216.0);
+/* w(d): 2^t, t = d * log2(e) (f32 product), split t = n + f with n = floor(t),
+ * 2^f from the degree-7 Taylor polynomial of exp(f ln 2) by fmaf Horner, then
+ * rint(2^f * 2^(24 + n)). Every step is one correctly rounded f32 operation,
+ * so any IEEE implementation reproduces the integer exactly. */
+static uint64_t zo_spec_w_of(float d) {
+    if (!(d >= -17.5f)) return 0;
+    const float t = d * 1.44269502f;
+    const float n = floorf(t);
+    const float f = t - n;
+    float p = 1.52527338e-05f;
+    p = fmaf(p, f, 1.54035304e-04f);
+    p = fmaf(p, f, 1.33335581e-03f);
+    p = fmaf(p, f, 9.61812911e-03f);
+    p = fmaf(p, f, 5.55041087e-02f);
+    p = fmaf(p, f, 2.40226507e-01f);
+    p = fmaf(p, f, 6.93147182e-01f);
+    p = fmaf(p, f, 1.0f);
+    return (uint64_t)rintf(ldexpf(p, 24 + (int)n));
 }
+static uint64_t zo_spec_w(float x, float T, float m) { return zo_spec_w_of(zo_spec_z(x, T) - m); }
 
 ZO_API uint32_t zo_spec_verify(const float* target, const float* draft, const uint32_t* drafts, uint32_t k,
                                uint32_t V, float T, uint64_t seed, uint64_t counter, uint32_t* next) {

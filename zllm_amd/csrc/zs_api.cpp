@@ -472,7 +472,8 @@ extern "C" int zs_spec_verify(zs_ctx* ctx, const zs_spec_batch* b, void* stream)
     if (!b->d_target || (b->k && !b->d_draft_ids) || !b->d_temperature || !b->d_seed || !b->d_counter ||
         !b->d_accepted || !b->d_next)
         return zs_set_error(ctx, ZS_EINVAL, "zs_spec_verify: null required pointer");
-    if (b->ld < b->V) return zs_set_error(ctx, ZS_EINVAL, "zs_spec_verify: ld < V");
+    if (b->ld < b->V || (b->ld & 3u) || ((uintptr_t)b->d_target & 15u) || ((uintptr_t)b->d_draft & 15u))
+        return zs_set_error(ctx, ZS_EINVAL, "zs_spec_verify: ld must be >= V and a multiple of 4, logits 16-byte aligned");
     zs_spec_args a{};
     a.B = b->B; a.V = b->V; a.k = b->k; a.ld = b->ld;
     a.target = b->d_target; a.draft = b->k ? b->d_draft : nullptr; a.draft_ids = b->d_draft_ids;

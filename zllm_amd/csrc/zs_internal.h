@@ -116,6 +116,7 @@ struct zs_spec_chunk {
     float amax_val;
     uint32_t amax_idx;
     unsigned long long wsum;
+    unsigned long long rlo, rhi;  // residual weight sum (position slot 0 of a row)
 };
 struct zs_spec_row {
     uint32_t mode, pos, residual, word;

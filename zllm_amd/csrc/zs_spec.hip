@@ -7,9 +7,10 @@
 // temperature > 0: rejection sampling (Leviathan et al. 2023; Chen et al.
 // 2023), which the reference does not implement (rest.rs:2639). To make it
 // reproducible bit-for-bit on any reduction order, probabilities are integer
-// quantised: with z = x / T (f32, no division when T == 1), m = max z and
-// e = expf(z - m) (glibc-identical), the weight of id v is
-//   P_v = rint(e_v * 2^24)               (target),   Q_v likewise (draft).
+// quantised: with z = x / T (f32, no division when T == 1) and m = max z, the
+// weight of id v is
+//   P_v = rint(2^24 * 2^((z_v - m) log2 e))   (target),   Q_v likewise (draft),
+// from a fixed sequence of f32 operations (sp_weight_of), 0 below z - m = -17.5.
 // Draft i (token d) is accepted iff U_i * Q_d * sum(P) <= P_d * sum(Q) * 2^32,
 // U_i the 32-bit Philox word of (seed, counter, tag 1+i). At the first
 // rejection i the replacement token is drawn from R_v = max(0, P_v sum(Q) -
@@ -25,19 +26,51 @@
 
 #define SP_NT 256
 #define SP_CH 8192
+#define SP_EPT (SP_CH / SP_NT)   // 32 elements per thread, as 8 float4
 #define SP_BIG_NT 1024
+// weights are 0 below this log-ratio
+#define SP_ZERO_D (-17.5f)
 
 typedef unsigned __int128 u128;
-
 
 __device__ __forceinline__ const float* sp_row(const zs_spec_args& a, uint32_t r, uint32_t pos) {
     if (pos <= a.k) return a.target + ((size_t)r * (a.k + 1) + pos) * a.ld;
     return a.draft + ((size_t)r * a.k + (pos - a.k - 1)) * a.ld;
 }
 __device__ __forceinline__ float sp_z(float x, float T) { return (T > 0.0f && T != 1.0f) ? x / T : x; }
-__device__ __forceinline__ uint64_t sp_weight(float z, float m) {
-    float e = zs_expf(z - m);
-    return (uint64_t)rint((double)e * 16777216.0);
+// Integer weight of log-ratio d = z - max: rint(2^24 * 2^(d log2 e)) through a
+// fixed sequence of correctly rounded f32 operations (t = d * log2 e, t = n + f
+// with n = floor(t), 2^f by a degree-7 Taylor polynomial in fmaf Horner form,
+// exact scaling by 2^(24+n), rint), so the CPU restatement reproduces every
+// weight bit for bit; 0 below d = -17.5.
+__device__ __forceinline__ uint64_t sp_weight_of(float d) {
+    if (!(d >= SP_ZERO_D)) return 0;
+    const float t = __fmul_rn(d, 1.44269502f);
+    const float n = floorf(t);
+    const float f = __fsub_rn(t, n);
+    float p = 1.52527338e-05f;
+    p = fmaf(p, f, 1.54035304e-04f);
+    p = fmaf(p, f, 1.33335581e-03f);
+    p = fmaf(p, f, 9.61812911e-03f);
+    p = fmaf(p, f, 5.55041087e-02f);
+    p = fmaf(p, f, 2.40226507e-01f);
+    p = fmaf(p, f, 6.93147182e-01f);
+    p = fmaf(p, f, 1.0f);
+    return (uint64_t)rintf(ldexpf(p, 24 + (int)n));
+}
+__device__ __forceinline__ uint64_t sp_weight(float z, float m) { return sp_weight_of(z - m); }
+// the chunk's elements of thread t: float4 j covers ids base + (j*SP_NT + t)*4 .. +3
+__device__ __forceinline__ void sp_load(const float* row, uint32_t base, uint32_t V, float (&x)[SP_EPT]) {
+#pragma unroll
+    for (int j = 0; j < SP_EPT / 4; j++) {
+        const uint32_t id = base + (j * SP_NT + threadIdx.x) * 4;
+        float4 v = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+        if (id < V) v = *reinterpret_cast<const float4*>(row + id);
+        x[4 * j] = v.x; x[4 * j + 1] = v.y; x[4 * j + 2] = v.z; x[4 * j + 3] = v.w;
+    }
+}
+__device__ __forceinline__ uint32_t sp_id(uint32_t base, int e) {
+    return base + ((e >> 2) * SP_NT + threadIdx.x) * 4 + (e & 3);
 }
 
 // pass 1: per chunk max of z, flags, first-max argmax of x
@@ -51,19 +84,22 @@ __global__ __launch_bounds__(SP_NT) void zs_k_spec_stats(zs_spec_args a) {
     __shared__ uint32_t ush[SP_NT / 64];
     __shared__ unsigned long long gsh[SP_NT / 64];
     const float T = a.temperature[r];
-    const float* row = sp_row(a, r, pos);
+    float x[SP_EPT];
+    sp_load(sp_row(a, r, pos), base, a.V, x);
     float zmax = -INFINITY;
     uint32_t fl = 0;
     unsigned long long best = 0;  // (value key, ~idx): first strict max
-    for (uint32_t i = base + threadIdx.x; i < min(a.V, base + SP_CH); i += SP_NT) {
-        float x = row[i];
-        float z = sp_z(x, T);
+#pragma unroll
+    for (int e = 0; e < SP_EPT; e++) {
+        const uint32_t i = sp_id(base, e);
+        if (i >= a.V) continue;
+        const float z = sp_z(x[e], T);
         if (z != z) fl |= 1u;
         else if (z == INFINITY) fl |= 2u;
         zmax = fmaxf(zmax, z);
-        if (x > -INFINITY) {  // strict > over init -inf (NaN never wins)
-            float xx = (x == 0.0f) ? 0.0f : x;
-            unsigned long long k = ((unsigned long long)zs_total_key(xx) << 32) | (0xffffffffu - i);
+        if (x[e] > -INFINITY) {  // strict > over init -inf (NaN never wins)
+            const float xx = (x[e] == 0.0f) ? 0.0f : x[e];
+            const unsigned long long k = ((unsigned long long)zs_total_key(xx) << 32) | (0xffffffffu - i);
             best = k > best ? k : best;
         }
     }
@@ -93,16 +129,20 @@ __global__ __launch_bounds__(SP_NT) void zs_k_spec_sums(zs_spec_args a) {
     const uint32_t base = c * SP_CH;
     if (base >= a.V) return;
     const float T = a.temperature[r];
-    if (!(T > 0.0f)) return;
+    if (!(T > 0.0f) || !a.draft) return;  // greedy verification needs no weights
     __shared__ unsigned long long sh[SP_NT / 64];
     const uint32_t nch = (a.V + SP_CH - 1) / SP_CH;
     const zs_spec_chunk* cs = a.cst + ((size_t)r * a.npos_max + pos) * a.nch;
     float m = -INFINITY;
     for (uint32_t i = 0; i < nch; i++) m = fmaxf(m, cs[i].zmax);
-    const float* row = sp_row(a, r, pos);
     unsigned long long s = 0;
-    if (m > -INFINITY && m < INFINITY)
-        for (uint32_t i = base + threadIdx.x; i < min(a.V, base + SP_CH); i += SP_NT) s += sp_weight(sp_z(row[i], T), m);
+    if (m > -INFINITY && m < INFINITY && cs[c].zmax - m >= SP_ZERO_D) {
+        float x[SP_EPT];
+        sp_load(sp_row(a, r, pos), base, a.V, x);
+#pragma unroll
+        for (int e = 0; e < SP_EPT; e++)
+            if (sp_id(base, e) < a.V) s += sp_weight(sp_z(x[e], T), m);
+    }
     for (int d = 32; d > 0; d >>= 1) s += __shfl_xor(s, d, 64);
     if (zs_lane() == 0) sh[zs_wid()] = s;
     __syncthreads();
@@ -113,10 +153,10 @@ __global__ __launch_bounds__(SP_NT) void zs_k_spec_sums(zs_spec_args a) {
     }
 }
 
-// pass 3: one thread per row -- accept / reject decisions
-__global__ void zs_k_spec_decide(zs_spec_args a) {
-    const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
-    if (r >= a.B) return;
+// pass 3: one wave per row -- accept / reject decisions (lanes over chunks)
+__global__ __launch_bounds__(64) void zs_k_spec_decide(zs_spec_args a) {
+    const uint32_t r = blockIdx.x;
+    const int lane = zs_lane();
     const uint32_t k = a.k, V = a.V;
     const uint32_t nch = (V + SP_CH - 1) / SP_CH;
     const uint32_t npos = a.draft ? 2 * k + 1 : k + 1;
@@ -124,30 +164,38 @@ __global__ void zs_k_spec_decide(zs_spec_args a) {
     zs_spec_row out;
     out.m_t = out.m_d = 0.f;
     out.sum_t = out.sum_d = 0;
-    // per position: max, flags, first-max argmax, weight sum
     bool degenerate = !(T > 0.0f) || !a.draft;
     float mpos[2 * ZS_SPEC_KMAX + 1];
     unsigned long long spos[2 * ZS_SPEC_KMAX + 1];
     uint32_t apos[ZS_SPEC_KMAX + 1];
     for (uint32_t p = 0; p < npos; p++) {
         const zs_spec_chunk* cs = a.cst + ((size_t)r * a.npos_max + p) * a.nch;
-        float m = -INFINITY, bv = -INFINITY;
-        uint32_t fl = 0, bi = 0xffffffffu;
-        unsigned long long s = 0;
-        for (uint32_t c = 0; c < nch; c++) {
-            m = fmaxf(m, cs[c].zmax);
-            fl |= cs[c].flags;
-            if (cs[c].amax_idx != 0xffffffffu && (bi == 0xffffffffu || cs[c].amax_val > bv)) {
-                bv = cs[c].amax_val;
-                bi = cs[c].amax_idx;
+        float m = -INFINITY;
+        uint32_t fl = 0;
+        unsigned long long s = 0, best = 0;  // (value key, ~id) of the first maximum
+        for (uint32_t c = lane; c < nch; c += 64) {
+            const zs_spec_chunk q = cs[c];
+            m = fmaxf(m, q.zmax);
+            fl |= q.flags;
+            if (!degenerate) s += q.wsum;
+            if (q.amax_idx != 0xffffffffu) {
+                const unsigned long long key = ((unsigned long long)zs_total_key(q.amax_val) << 32) | (0xffffffffu - q.amax_idx);
+                best = key > best ? key : best;
             }
-            s += cs[c].wsum;
         }
-        if (p <= k) apos[p] = bi == 0xffffffffu ? 0u : bi;
+        m = wave_max_f(m);
+        fl = wave_or_u(fl);
+        for (int d = 32; d > 0; d >>= 1) {
+            s += __shfl_xor(s, d, 64);
+            unsigned long long o = __shfl_xor(best, d, 64);
+            best = o > best ? o : best;
+        }
         if (fl || m == -INFINITY) degenerate = true;
+        if (p <= k) apos[p] = best ? 0xffffffffu - (uint32_t)(best & 0xffffffffull) : 0u;
         mpos[p] = m;
         spos[p] = s;
     }
+    if (lane != 0) return;
     const uint32_t* drafts = a.draft_ids + (size_t)r * k;
     if (degenerate) {
         uint32_t acc = 0, bonus = apos[k];
@@ -208,82 +256,151 @@ __device__ __forceinline__ u128 shfl_xor_u128(u128 v, int d) {
     return u128_of(p);
 }
 
-struct spd_shared {
-    unsigned long long lo[SP_BIG_NT / 64], hi[SP_BIG_NT / 64];
-    int imin[SP_BIG_NT / 64];
-    unsigned long long tlo, thi;
-};
-
-__device__ __forceinline__ u128 spd_weight(const zs_spec_args& a, const zs_spec_row& s, uint32_t r, float T,
-                                           uint32_t v) {
-    if (v >= a.V) return 0;
-    uint64_t P = sp_weight(sp_z(sp_row(a, r, s.pos)[v], T), s.m_t);
+// Draw weight of id v (given its target / draft logits): P, or the residual
+// max(0, P sum(Q) - Q sum(P)).
+__device__ __forceinline__ u128 spd_weight2(const zs_spec_row& s, float T, float xt, float xd) {
+    uint64_t P = sp_weight(sp_z(xt, T), s.m_t);
     if (!s.residual) return P;
-    uint64_t Q = sp_weight(sp_z(sp_row(a, r, a.k + 1 + s.pos)[v], T), s.m_d);
+    uint64_t Q = sp_weight(sp_z(xd, T), s.m_d);
     u128 pp = (u128)P * s.sum_d, qq = (u128)Q * s.sum_t;
     return pp > qq ? pp - qq : 0;
 }
 
-// pass 4: one workgroup per row -- the replacement / bonus draw
+// pass 4: chunk sums of the residual weights (rows that rejected a draft)
+__global__ __launch_bounds__(SP_NT) void zs_k_spec_rsum(zs_spec_args a) {
+    const uint32_t c = blockIdx.x, r = blockIdx.y;
+    const uint32_t base = c * SP_CH;
+    if (base >= a.V) return;
+    const zs_spec_row s = a.rs[r];
+    if (s.mode != 1 || !s.residual) return;
+    __shared__ unsigned long long lo[SP_NT / 64], hi[SP_NT / 64];
+    const float T = a.temperature[r];
+    float xt[SP_EPT], xd[SP_EPT];
+    sp_load(sp_row(a, r, s.pos), base, a.V, xt);
+    sp_load(sp_row(a, r, a.k + 1 + s.pos), base, a.V, xd);
+    u128 acc = 0;
+#pragma unroll
+    for (int e = 0; e < SP_EPT; e++)
+        if (sp_id(base, e) < a.V) acc += spd_weight2(s, T, xt[e], xd[e]);
+    for (int d = 32; d > 0; d >>= 1) acc += shfl_xor_u128(acc, d);
+    if (zs_lane() == 0) { lo[zs_wid()] = (unsigned long long)acc; hi[zs_wid()] = (unsigned long long)(acc >> 64); }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        u128 t = 0;
+        for (int i = 0; i < SP_NT / 64; i++) t += ((u128)hi[i] << 64) | lo[i];
+        zs_spec_chunk& o = a.cst[((size_t)r * a.npos_max + 0) * a.nch + c];
+        o.rlo = (unsigned long long)t;
+        o.rhi = (unsigned long long)(t >> 64);
+    }
+}
+
+// pass 5: one workgroup per row -- the replacement / bonus draw: the chunk
+// holding the target from the chunk sums, then the first id of that chunk whose
+// inclusive prefix exceeds the target
 __global__ __launch_bounds__(SP_BIG_NT) void zs_k_spec_draw(zs_spec_args a) {
     const uint32_t r = blockIdx.x;
-    __shared__ spd_shared sh;
+    __shared__ unsigned long long lo[SP_BIG_NT / 64], hi[SP_BIG_NT / 64];
+    __shared__ int imin[SP_BIG_NT / 64];
+    __shared__ uint32_t csel;
+    __shared__ unsigned long long clo, chi, rzero;
     zs_spec_row s = a.rs[r];
     if (s.mode != 1) return;
     const float T = a.temperature[r];
     const int t = threadIdx.x;
     const uint32_t V = a.V;
-    // total weight (known for P; summed here for the residual)
-    u128 total = s.sum_t;
-    if (s.residual) {
-        u128 acc = 0;
-        for (uint32_t v = t; v < V; v += SP_BIG_NT) acc += spd_weight(a, s, r, T, v);
-        for (int d = 32; d > 0; d >>= 1) acc += shfl_xor_u128(acc, d);
-        if (zs_lane() == 0) { sh.lo[zs_wid()] = (unsigned long long)acc; sh.hi[zs_wid()] = (unsigned long long)(acc >> 64); }
-        __syncthreads();
-        total = 0;
-        for (int i = 0; i < SP_BIG_NT / 64; i++) total += ((u128)sh.hi[i] << 64) | sh.lo[i];
-        __syncthreads();
-        if (total == 0) {  // p == q exactly: draw from the target instead
-            s.residual = 0;
-            total = s.sum_t;
+    const uint32_t nch = (V + SP_CH - 1) / SP_CH;
+    const zs_spec_chunk* c0 = a.cst + ((size_t)r * a.npos_max + 0) * a.nch;                   // residual sums
+    const zs_spec_chunk* cp = a.cst + ((size_t)r * a.npos_max + (s.residual ? s.pos : a.k)) * a.nch;  // P sums
+    if (t < 64) {
+        // residual total; p == q exactly leaves no residual: draw from the target
+        u128 rt = 0;
+        if (s.residual)
+            for (uint32_t c = t; c < nch; c += 64) rt += ((u128)c0[c].rhi << 64) | c0[c].rlo;
+        for (int d = 32; d > 0; d >>= 1) rt += shfl_xor_u128(rt, d);
+        const bool resid = s.residual && rt != 0;
+        const u128 total = resid ? rt : (u128)s.sum_t;
+        const u128 target = ((u128)s.word * total) >> 32;
+        // chunk prefix over the lanes (nch <= 64 for the vocab limit)
+        u128 w = 0;
+        if ((uint32_t)t < nch) w = resid ? (((u128)c0[t].rhi << 64) | c0[t].rlo) : (u128)cp[t].wsum;
+        u128 inc = w;
+        for (int d = 1; d < 64; d <<= 1) {
+            u128 y = shfl_up_u128(inc, d);
+            if (t >= d) inc += y;
+        }
+        const bool hit = w > 0 && inc > target;
+        const unsigned long long bal = __ballot(hit);
+        const int first = bal ? __ffsll((long long)bal) - 1 : -1;
+        const u128 before = __shfl(first >= 0 ? (unsigned long long)(inc - w) : 0ull, first >= 0 ? first : 0, 64);
+        const u128 beforeh = __shfl(first >= 0 ? (unsigned long long)((inc - w) >> 64) : 0ull, first >= 0 ? first : 0, 64);
+        if (t == 0) {
+            csel = first >= 0 ? (uint32_t)first : 0xffffffffu;
+            const u128 rem = target - ((beforeh << 64) | (unsigned long long)before);
+            clo = (unsigned long long)rem;
+            chi = (unsigned long long)(rem >> 64);
+            rzero = resid ? 1ull : 0ull;
         }
     }
-    const u128 target = ((u128)s.word * total) >> 32;
-    // first id whose inclusive prefix exceeds target, groups of 4*1024 ids
-    u128 carry = 0;
-    uint32_t found = 0xffffffffu;
-    for (uint32_t g0 = 0; g0 < V && found == 0xffffffffu; g0 += 4 * SP_BIG_NT) {
-        u128 w[4], loc = 0;
+    __syncthreads();
+    const uint32_t c = csel;
+    if (c == 0xffffffffu) {
+        if (t == 0) a.next[r] = V - 1;
+        return;
+    }
+    if (!rzero) s.residual = 0;
+    const u128 rem = ((u128)chi << 64) | clo;  // target minus the weight of the chunks before
+    const uint32_t base = c * SP_CH;
+    // 8192 ids, 8 per thread in two float4 of each row
+    const float* rt = sp_row(a, r, s.pos);
+    const float* rd = s.residual ? sp_row(a, r, a.k + 1 + s.pos) : rt;
+    u128 w[8], loc = 0;
 #pragma unroll
-        for (int q = 0; q < 4; q++) { w[q] = spd_weight(a, s, r, T, g0 + 4 * t + q); loc += w[q]; }
-        // inclusive scan of loc over the workgroup
-        u128 inc = loc;
+    for (int h = 0; h < 2; h++) {
+        const uint32_t id = base + (h * SP_BIG_NT + t) * 4;
+        float4 vt = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY), vd = vt;
+        if (id < V) {
+            vt = *reinterpret_cast<const float4*>(rt + id);
+            vd = *reinterpret_cast<const float4*>(rd + id);
+        }
+        const float xt[4] = {vt.x, vt.y, vt.z, vt.w}, xd[4] = {vd.x, vd.y, vd.z, vd.w};
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            w[4 * h + q] = id + q < V ? spd_weight2(s, T, xt[q], xd[q]) : 0;
+        }
+    }
+    // inclusive prefix in id order: ids of thread t are base + 4t..4t+3 (h=0)
+    // and base + 4096 + 4t..+3 (h=1); scan the two halves one after the other
+    int found = ZS_BIGI;
+    u128 carry = 0;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        u128 l = w[4 * h] + w[4 * h + 1] + w[4 * h + 2] + w[4 * h + 3];
+        u128 inc = l;
         for (int d = 1; d < 64; d <<= 1) {
             u128 y = shfl_up_u128(inc, d);
             if (zs_lane() >= d) inc += y;
         }
-        if (zs_lane() == 63) { sh.lo[zs_wid()] = (unsigned long long)inc; sh.hi[zs_wid()] = (unsigned long long)(inc >> 64); }
+        if (zs_lane() == 63) { lo[zs_wid()] = (unsigned long long)inc; hi[zs_wid()] = (unsigned long long)(inc >> 64); }
         __syncthreads();
         u128 pre = 0, tot = 0;
         for (int i = 0; i < SP_BIG_NT / 64; i++) {
-            u128 wv = ((u128)sh.hi[i] << 64) | sh.lo[i];
+            u128 wv = ((u128)hi[i] << 64) | lo[i];
             if (i < zs_wid()) pre += wv;
             tot += wv;
         }
         __syncthreads();
-        u128 run = carry + pre + inc - loc;
+        u128 run = carry + pre + inc - l;
         int my = ZS_BIGI;
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-            run += w[q];
-            if (my == ZS_BIGI && w[q] > 0 && run > target) my = 4 * t + q;
+            run += w[4 * h + q];
+            if (my == ZS_BIGI && w[4 * h + q] > 0 && run > rem) my = h * 4 * SP_BIG_NT + 4 * t + q;
         }
-        int first = block_min_i<SP_BIG_NT>(my, sh.imin);
-        if (first != ZS_BIGI) found = g0 + (uint32_t)first;
+        const int f = block_min_i<SP_BIG_NT>(my, imin);
+        if (found == ZS_BIGI) found = f;
         carry += tot;
     }
-    if (t == 0) a.next[r] = found == 0xffffffffu ? V - 1 : found;
+    if (t == 0) a.next[r] = found == ZS_BIGI ? V - 1 : base + (uint32_t)found;
 }
 
 extern "C" int zs_spec_launch(const zs_spec_args& a, hipStream_t stream) {
@@ -292,7 +409,8 @@ extern "C" int zs_spec_launch(const zs_spec_args& a, hipStream_t stream) {
     dim3 grid(nch, npos, a.B);
     hipLaunchKernelGGL(zs_k_spec_stats, grid, dim3(SP_NT), 0, stream, a);
     hipLaunchKernelGGL(zs_k_spec_sums, grid, dim3(SP_NT), 0, stream, a);
-    hipLaunchKernelGGL(zs_k_spec_decide, dim3((a.B + 63) / 64), dim3(64), 0, stream, a);
+    hipLaunchKernelGGL(zs_k_spec_decide, dim3(a.B), dim3(64), 0, stream, a);
+    hipLaunchKernelGGL(zs_k_spec_rsum, dim3(nch, a.B), dim3(SP_NT), 0, stream, a);
     hipLaunchKernelGGL(zs_k_spec_draw, dim3(a.B), dim3(SP_BIG_NT), 0, stream, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

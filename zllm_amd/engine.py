@@ -383,6 +383,16 @@ def verify_drafts(ctx: Context, target: torch.Tensor, draft_ids: torch.Tensor, t
     B, kp1, V = target.shape
     k = kp1 - 1
     dev = target.device
+    if target.stride(1) % 4 or target.stride(2) != 1 or (draft is not None and draft.stride(1) != target.stride(1)):
+        # the ABI reads rows with 16-byte loads: pad the row stride to a multiple of 4
+        ld = (V + 3) // 4 * 4
+        t2 = torch.zeros((B, kp1, ld), dtype=target.dtype, device=dev)
+        t2[:, :, :V] = target
+        target = t2[:, :, :V]
+        if draft is not None:
+            d2 = torch.zeros((B, k, ld), dtype=draft.dtype, device=dev)
+            d2[:, :, :V] = draft
+            draft = d2[:, :, :V]
     acc = torch.empty(B, dtype=torch.int32, device=dev)
     nxt = torch.empty(B, dtype=torch.int32, device=dev)
     sb = SpecBatch()
