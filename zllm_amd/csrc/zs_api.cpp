@@ -5,6 +5,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <algorithm>
 #include <map>
 #include <vector>
 #include "zs_internal.h"
@@ -19,7 +20,7 @@ extern "C" int zs_lane_topk_launch(const float* logits, uint32_t B, uint32_t V, 
 extern "C" int zs_lane_sample_topk_launch(const float* vals, const uint32_t* idxs, uint32_t B, uint32_t K,
                                           const float* temp, const uint32_t* top_k, const float* top_p,
                                           const uint32_t* seed, uint32_t* out, hipStream_t stream);
-extern "C" int zs_dfa_mask_launch(const dm_args& a, bool lds, uint32_t* any_scratch, hipStream_t stream);
+extern "C" int zs_dfa_mask_launch(const dm_args& a, bool lds, uint32_t ncu, uint32_t* any_scratch, hipStream_t stream);
 
 int zs_set_error(zs_ctx* ctx, int code, const char* fmt, ...) {
     if (ctx) {
@@ -96,6 +97,9 @@ extern "C" int zs_ctx_create(int device, uint32_t max_rows, uint32_t max_vocab, 
     hipGetDevice(&prev);
     hipSetDevice(device);
     int rc = ZS_OK;
+    int ncu = 0;
+    if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || ncu <= 0) ncu = 256;
+    ctx->num_cus = (uint32_t)ncu;
     const size_t R = max_rows, C = ctx->max_chunks;
     if (!rc) rc = zs_alloc(ctx, &ctx->p_cnt, R);
     if (!rc) rc = zs_alloc(ctx, &ctx->p_id, R * ZS_MAX_PATCHES);
@@ -149,6 +153,8 @@ extern "C" void zs_vocab_destroy(zs_vocab* v) {
     hipFree(v->d_bytes);
     hipFree(v->d_valid);
     hipFree(v->d_packed);
+    hipFree(v->d_wbytes);
+    hipFree(v->d_wmeta);
     free(v->h_offsets);
     free(v->h_bytes);
     free(v->h_valid);
@@ -188,6 +194,20 @@ extern "C" int zs_vocab_create(zs_ctx* ctx, const uint32_t* h_offsets, const uin
         for (uint32_t i = 0; i < n && i < 16; i++) tok16[(size_t)t * 4 + i / 4] |= (uint32_t)v->h_bytes[o + i] << (8 * (i % 4));
     }
     v->maxlen = maxlen;
+    // walk order by length inside each tile (tokens never allowed: length 0)
+    v->nwtile = (ntab + ZS_WALK_TILE - 1) / ZS_WALK_TILE;
+    std::vector<uint32_t> wbytes((size_t)v->nwtile * ZS_WALK_TILE * 4, 0), wmeta((size_t)v->nwtile * ZS_WALK_TILE, 0xffffffffu);
+    for (uint32_t tl = 0; tl < v->nwtile; tl++) {
+        std::vector<uint32_t> ids;
+        for (uint32_t t = tl * ZS_WALK_TILE; t < ntab && t < (tl + 1) * ZS_WALK_TILE; t++) ids.push_back(t);
+        auto wlen = [&](uint32_t t) { return h_valid[t] ? (uint32_t)tlen[t] : 0u; };
+        std::stable_sort(ids.begin(), ids.end(), [&](uint32_t x, uint32_t y) { return wlen(x) < wlen(y); });
+        for (size_t k = 0; k < ids.size(); k++) {
+            const size_t slot = (size_t)tl * ZS_WALK_TILE + k;
+            wmeta[slot] = ids[k] | (wlen(ids[k]) << 18);
+            for (int q = 0; q < 4; q++) wbytes[slot * 4 + q] = tok16[(size_t)ids[k] * 4 + q];
+        }
+    }
     int prev = 0;
     hipGetDevice(&prev);
     hipSetDevice(ctx->device);
@@ -199,7 +219,11 @@ extern "C" int zs_vocab_create(zs_ctx* ctx, const uint32_t* h_offsets, const uin
     if (!rc) rc = zs_alloc(ctx, &v->d_bytes, v->nbytes + 1);
     if (!rc) rc = zs_alloc(ctx, &v->d_valid, ntab + 1);
     if (!rc) rc = zs_alloc(ctx, &v->d_packed, tok_words + len_words);
+    if (!rc) rc = zs_alloc(ctx, &v->d_wbytes, wbytes.size());
+    if (!rc) rc = zs_alloc(ctx, &v->d_wmeta, wmeta.size());
     if (!rc) {
+        hipMemcpy(v->d_wbytes, wbytes.data(), wbytes.size() * 4, hipMemcpyHostToDevice);
+        hipMemcpy(v->d_wmeta, wmeta.data(), wmeta.size() * 4, hipMemcpyHostToDevice);
         hipMemcpy(v->d_offsets, v->h_offsets, sizeof(uint32_t) * (ntab + 1), hipMemcpyHostToDevice);
         if (v->nbytes) hipMemcpy(v->d_bytes, v->h_bytes, v->nbytes, hipMemcpyHostToDevice);
         hipMemcpy(v->d_valid, v->h_valid, ntab, hipMemcpyHostToDevice);
@@ -225,6 +249,9 @@ extern "C" void zs_dfa_destroy(zs_dfa* d) {
     hipFree(d->d_cls);
     hipFree(d->d_bad);
     hipFree(d->d_accept);
+    hipFree(d->d_packed);
+    hipFree(d->d_clsinfo);
+    hipFree(d->d_remap);
     free(d->h_trans);
     free(d->h_dead);
     free(d->h_accept);
@@ -314,6 +341,30 @@ extern "C" int zs_dfa_create(zs_ctx* ctx, const uint32_t* h_trans, uint32_t nsta
     for (uint32_t c = 0; c < ncls; c++)
         for (uint32_t s = 0; s < nstates; s++) tab[(size_t)s * ncls + c] = cols[c][s];
     d->ncls = ncls;
+    // bit-packed copy over the good states only
+    std::vector<uint16_t> remap(nstates, 0xffffu);
+    uint32_t ngood = 0;
+    for (uint32_t s = 0; s < nstates; s++)
+        if (!bad[s]) remap[s] = (uint16_t)ngood++;
+    uint32_t bits = 1;
+    while ((1u << bits) - 1u < ngood) bits++;  // all ones is the fail value
+    const uint32_t per = 64 / bits, rw = (ncls + per - 1) / per;
+    std::vector<uint64_t> packed((size_t)(ngood ? ngood : 1) * rw, 0ull);
+    const uint64_t fail = (1ull << bits) - 1ull;
+    for (uint32_t s = 0; s < nstates; s++) {
+        if (bad[s]) continue;
+        for (uint32_t c = 0; c < ncls; c++) {
+            const uint16_t tgt = cols[c][s];
+            const uint64_t v = tgt == 0xffffu ? fail : (uint64_t)remap[tgt];
+            packed[(size_t)remap[s] * rw + c / per] |= v << ((c % per) * bits);
+        }
+    }
+    uint16_t clsinfo[256];
+    for (uint32_t b = 0; b < 256; b++) clsinfo[b] = (uint16_t)((cls[b] / per) | (((cls[b] % per) * bits) << 8));
+    d->ngood = ngood;
+    d->bits = bits;
+    d->rw = rw;
+    d->packed_lds = (size_t)ngood * rw * 8 <= ZS_DFA_LDS_BYTES ? 1 : 0;
     int prev = 0;
     hipGetDevice(&prev);
     hipSetDevice(ctx->device);
@@ -322,7 +373,13 @@ extern "C" int zs_dfa_create(zs_ctx* ctx, const uint32_t* h_trans, uint32_t nsta
     if (!rc) rc = zs_alloc(ctx, &d->d_cls, 256);
     if (!rc) rc = zs_alloc(ctx, &d->d_bad, nstates);
     if (!rc) rc = zs_alloc(ctx, &d->d_accept, nstates);
+    if (!rc) rc = zs_alloc(ctx, &d->d_packed, packed.size());
+    if (!rc) rc = zs_alloc(ctx, &d->d_clsinfo, 256);
+    if (!rc) rc = zs_alloc(ctx, &d->d_remap, nstates);
     if (!rc) {
+        hipMemcpy(d->d_packed, packed.data(), packed.size() * 8, hipMemcpyHostToDevice);
+        hipMemcpy(d->d_clsinfo, clsinfo, 256 * 2, hipMemcpyHostToDevice);
+        hipMemcpy(d->d_remap, remap.data(), nstates * 2, hipMemcpyHostToDevice);
         hipMemcpy(d->d_trans, tab.data(), tab.size() * 2, hipMemcpyHostToDevice);
         hipMemcpy(d->d_cls, cls, 256, hipMemcpyHostToDevice);
         hipMemcpy(d->d_bad, bad.data(), nstates, hipMemcpyHostToDevice);
@@ -383,14 +440,22 @@ extern "C" int zs_dfa_mask(zs_ctx* ctx, const zs_dfa* dfa, const zs_vocab* vocab
     a.eos = vocab->eos;
     a.nstates = dfa->nstates;
     a.ncls = dfa->ncls;
+    a.packed = dfa->d_packed;
+    a.wbytes = vocab->d_wbytes;
+    a.wmeta = vocab->d_wmeta;
+    a.nwtile = vocab->nwtile;
+    a.clsinfo = dfa->d_clsinfo;
+    a.remap = dfa->d_remap;
+    a.ngood = dfa->ngood;
+    a.bits = dfa->bits;
+    a.rw = dfa->rw;
     a.states = d_states;
     a.B = B;
     a.V = V;
     a.words = (V + 31) / 32;
     a.out = d_out_bits;
-    bool lds = (size_t)dfa->nstates * dfa->ncls <= 32768;
     uint32_t* any = d_any ? d_any : (uint32_t*)ctx->mask_scratch;
-    if (zs_dfa_mask_launch(a, lds, any, (hipStream_t)stream))
+    if (zs_dfa_mask_launch(a, dfa->packed_lds != 0, ctx->num_cus, any, (hipStream_t)stream))
         return zs_set_error(ctx, ZS_EHIP, "zs_dfa_mask: launch failed: %s", hipGetErrorString(hipGetLastError()));
     return ZS_OK;
 }

@@ -105,6 +105,141 @@ __global__ __launch_bounds__(DM_NT) void zs_k_dfa_mask(dm_args a) {
     }
 }
 
+// Persistent walk over the bit-packed table (good states only, `bits`-bit
+// entries, all ones = fail). One workgroup per CU stages the table in LDS once
+// and then takes items: a tile of ZS_WALK_TILE ids times a group of DL_RG
+// constrained rows. A thread walks DL_TPT tokens, each through all rows of the
+// group at once: the byte and its class are read once per step and the rows'
+// states advance side by side. Inside a tile the tokens come in length order
+// (the vocabulary's walk order), so the lanes of a wave walk tokens of nearly
+// equal length; allowed ids are set in an LDS bitmap of the tile and written
+// out as whole words. A step costs one LDS class read and one 64-bit LDS
+// table read per row.
+#define DL_NT 1024
+#define DL_TPT (ZS_WALK_TILE / DL_NT)
+#define DL_RG 8                  // rows walked together
+#define DL_TW (ZS_WALK_TILE / 32) // bitmap words per row and tile
+#define DL_WORDS (ZS_DFA_LDS_BYTES / 8)
+#define DL_MAXROWS 2048          // constrained-row list in LDS
+__global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
+    __shared__ uint64_t tab[DL_WORDS];
+    __shared__ uint16_t ci[256];
+    __shared__ uint32_t bm[DL_RG][DL_TW];
+    __shared__ uint16_t crow[DL_MAXROWS];  // constrained rows
+    __shared__ uint16_t cst[DL_MAXROWS];   // their good start state (0xffff: none allowed)
+    __shared__ uint32_t ncr;
+    const int t = threadIdx.x;
+    const uint32_t nw = a.ngood * a.rw;
+    for (uint32_t i = t; i < nw; i += DL_NT) tab[i] = a.packed[i];
+    for (int i = t; i < 256; i += DL_NT) ci[i] = a.clsinfo[i];
+    if (t == 0) ncr = 0;
+    __syncthreads();
+    // constrained rows in order (every workgroup builds the same list)
+    for (uint32_t r0 = 0; r0 < a.B; r0 += DL_NT) {
+        const uint32_t r = r0 + t;
+        const int32_t st = r < a.B ? a.states[r] : -1;
+        const bool c = st >= 0;
+        uint32_t tot;
+        const uint32_t pos = block_excl_scan_u<DL_NT>(c ? 1u : 0u, reinterpret_cast<uint32_t*>(bm), &tot);
+        if (c) {
+            crow[ncr + pos] = (uint16_t)r;
+            cst[ncr + pos] = a.remap[st];
+        }
+        __syncthreads();
+        if (t == 0) ncr += tot;
+        __syncthreads();
+    }
+    const uint32_t nc = ncr;
+    const uint32_t rw = a.rw;
+    const uint64_t fmask = (1ull << a.bits) - 1ull;
+    const uint32_t fail = (uint32_t)fmask;
+    const uint32_t ncover = a.V > a.ntab ? a.V : a.ntab;
+    const uint32_t ntt = (ncover + ZS_WALK_TILE - 1) / ZS_WALK_TILE, nrg = (nc + DL_RG - 1) / DL_RG;
+    for (uint32_t w = blockIdx.x; w < ntt * nrg; w += gridDim.x) {
+        const uint32_t tt = w % ntt, g0 = (w / ntt) * DL_RG;
+        const uint32_t nr = min((uint32_t)DL_RG, nc - g0);
+        const uint32_t tok0 = tt * ZS_WALK_TILE;
+        for (int i = t; i < DL_RG * DL_TW; i += DL_NT) (&bm[0][0])[i] = 0;
+        uint32_t s0[DL_RG];
+#pragma unroll
+        for (int rr = 0; rr < DL_RG; rr++) s0[rr] = (uint32_t)rr < nr ? cst[g0 + rr] : 0xffffu;
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < DL_TPT; j++) {
+            const uint32_t slot = tok0 + j * DL_NT + t;
+            if (tt >= a.nwtile) break;
+            const uint32_t meta = a.wmeta[slot];
+            if (meta == 0xffffffffu) continue;
+            const uint32_t id = meta & 0x3ffffu, L = meta >> 18;
+            if (L == 0) continue;  // no bytes or not a token: never allowed
+            const uint4 wb = reinterpret_cast<const uint4*>(a.wbytes)[slot];
+            const uint32_t bw[4] = {wb.x, wb.y, wb.z, wb.w};
+            uint32_t s[DL_RG], alive = 0;
+#pragma unroll
+            for (int rr = 0; rr < DL_RG; rr++) {
+                s[rr] = s0[rr];
+                if (s0[rr] != 0xffffu) alive |= 1u << rr;
+            }
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                if ((uint32_t)i >= L || !alive) break;
+                const uint32_t c = ci[(bw[i >> 2] >> (8 * (i & 3))) & 0xffu];
+                const uint32_t cw = c & 0xffu, sh = c >> 8;
+#pragma unroll
+                for (int rr = 0; rr < DL_RG; rr++) {
+                    if (!((alive >> rr) & 1u)) continue;
+                    s[rr] = (uint32_t)((tab[s[rr] * rw + cw] >> sh) & fmask);
+                    if (s[rr] == fail) alive &= ~(1u << rr);
+                }
+            }
+            if (L > 16 && alive) {
+                // bytes past the first 16 from the CSR copy (long tokens)
+                const uint32_t o0 = a.offsets[id], o1 = a.offsets[id + 1];
+                for (uint32_t i = o0 + 16; i < o1 && alive; i++) {
+                    const uint32_t c = ci[a.bytes[i]];
+#pragma unroll
+                    for (int rr = 0; rr < DL_RG; rr++) {
+                        if (!((alive >> rr) & 1u)) continue;
+                        s[rr] = (uint32_t)((tab[s[rr] * rw + (c & 0xffu)] >> (c >> 8)) & fmask);
+                        if (s[rr] == fail) alive &= ~(1u << rr);
+                    }
+                }
+            }
+            const uint32_t off = id - tok0;
+#pragma unroll
+            for (int rr = 0; rr < DL_RG; rr++)
+                if ((alive >> rr) & 1u) atomicOr(&bm[rr][off >> 5], 1u << (off & 31));
+        }
+        __syncthreads();
+        // whole words out; bits at ids >= V stay clear; viability counts every
+        // table id of the tile
+        for (int i = t; i < (int)(nr * DL_TW); i += DL_NT) {
+            const uint32_t rr = i / DL_TW, wi = i % DL_TW;
+            const uint32_t r = crow[g0 + rr];
+            const uint32_t word = bm[rr][wi];
+            const uint32_t gw = tok0 / 32 + wi;
+            if (gw < a.words) {
+                uint32_t v = word;
+                if (gw == a.words - 1 && (a.V & 31)) v &= (1u << (a.V & 31)) - 1u;
+                a.out[(size_t)r * a.words + gw] = v;
+            }
+            if (word) a.any[r] = 1u;  // every writer stores 1
+        }
+        __syncthreads();
+    }
+}
+
+// Unconstrained rows: every id below V allowed.
+__global__ void zs_k_dfa_free_rows(dm_args a) {
+    const uint32_t r = blockIdx.y;
+    if (a.states[r] >= 0) return;
+    for (uint32_t wi = blockIdx.x * blockDim.x + threadIdx.x; wi < a.words; wi += gridDim.x * blockDim.x) {
+        uint32_t v = 0xffffffffu;
+        if (wi == a.words - 1 && (a.V & 31)) v = (1u << (a.V & 31)) - 1u;
+        a.out[(size_t)r * a.words + wi] = v;
+    }
+}
+
 __global__ void zs_k_fill_u32(uint32_t* p, uint32_t n, uint32_t v) {
     uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) p[i] = v;
@@ -124,14 +259,20 @@ __global__ void zs_k_dfa_eos(dm_args a) {
     *o = ok ? (*o | bit) : (*o & ~bit);
 }
 
-extern "C" int zs_dfa_mask_launch(const dm_args& a, bool lds, uint32_t* any_scratch, hipStream_t stream) {
+extern "C" int zs_dfa_mask_launch(const dm_args& a, bool packed_lds, uint32_t ncu, uint32_t* any_scratch,
+                                  hipStream_t stream) {
     dm_args x = a;
     x.any = any_scratch;
     hipLaunchKernelGGL(zs_k_fill_u32, dim3((a.B + 255) / 256), dim3(256), 0, stream, any_scratch, a.B, 0u);
     uint32_t ncover = a.V > a.ntab ? a.V : a.ntab;
-    dim3 grid((ncover + DM_TOK - 1) / DM_TOK, (a.B + DM_ROWS - 1) / DM_ROWS);
-    if (lds) hipLaunchKernelGGL(zs_k_dfa_mask<true>, grid, dim3(DM_NT), 0, stream, x);
-    else hipLaunchKernelGGL(zs_k_dfa_mask<false>, grid, dim3(DM_NT), 0, stream, x);
+    if (packed_lds && a.B <= DL_MAXROWS) {
+        const uint32_t items = ((ncover + ZS_WALK_TILE - 1) / ZS_WALK_TILE) * ((a.B + DL_RG - 1) / DL_RG);
+        hipLaunchKernelGGL(zs_k_dfa_free_rows, dim3(4, a.B), dim3(256), 0, stream, x);
+        hipLaunchKernelGGL(zs_k_dfa_mask_packed, dim3(min(items, ncu)), dim3(DL_NT), 0, stream, x);
+    } else {
+        dim3 grid((ncover + DM_TOK - 1) / DM_TOK, (a.B + DM_ROWS - 1) / DM_ROWS);
+        hipLaunchKernelGGL(zs_k_dfa_mask<false>, grid, dim3(DM_NT), 0, stream, x);
+    }
     hipLaunchKernelGGL(zs_k_dfa_eos, dim3((a.B + 63) / 64), dim3(64), 0, stream, x);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

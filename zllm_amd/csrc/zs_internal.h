@@ -14,6 +14,8 @@
 // Largest vocabulary a context accepts (chunk lists of one row must fit the
 // combine kernel's on-chip sort: 32 chunks x 128).
 #define ZS_MAX_VOCAB 262144
+#define ZS_DFA_LDS_BYTES 152576  // packed DFA table budget in LDS (149 KB)
+#define ZS_WALK_TILE 2048        // ids per tile of the vocab-parallel DFA walk
 #define ZS_MAX_CHUNKS (ZS_MAX_VOCAB / ZS_P1_CH)
 // Big-row engine: 1024 threads, 4 consecutive elements per thread.
 #define ZS_BIG_NT 1024
@@ -142,6 +144,7 @@ struct zs_spec_args {
 
 struct zs_ctx {
     int device;
+    uint32_t num_cus;
     uint32_t max_rows, max_vocab, max_chunks;
     char err[512];
     // device scratch
@@ -184,6 +187,12 @@ struct zs_vocab {
     uint8_t* d_valid;
     uint32_t* d_packed;    // per token: (offset << 8) | len, len==0xff... see zs_dfa.hip
     uint32_t maxlen;
+    // walk order: inside every tile of ZS_WALK_TILE ids, the ids sorted by byte
+    // length, with their first 16 bytes and (id | walk length << 18); 0xffffffff
+    // marks a slot with no token and length 0 a token that is never allowed
+    uint32_t nwtile;
+    uint32_t* d_wbytes;    // [nwtile * ZS_WALK_TILE][4]
+    uint32_t* d_wmeta;     // [nwtile * ZS_WALK_TILE]
     // host copies for advance()
     uint32_t* h_offsets;
     uint8_t* h_bytes;
@@ -204,6 +213,14 @@ struct zs_dfa {
     uint8_t* d_cls;        // [256] byte -> class
     uint8_t* d_bad;        // [nstates] dead or not live
     uint8_t* d_accept;     // [nstates]
+    // bit-packed table for the LDS walk: good states renumbered 0..ngood-1,
+    // entries of `bits` bits (all ones = fail), 64 / bits per u64 word, each
+    // state row padded to `rw` words
+    uint64_t* d_packed;    // [ngood][rw]
+    uint16_t* d_clsinfo;   // [256] word in row | bit shift << 8
+    uint16_t* d_remap;     // [nstates] good id or 0xffff
+    uint32_t ngood, bits, rw;
+    int packed_lds;        // the packed table fits the LDS budget
 };
 
 // Arguments of the DFA mask kernels (zs_dfa.hip).
@@ -218,6 +235,13 @@ struct dm_args {
     const uint8_t* bytes;
     const uint8_t* valid;
     uint32_t ntab, eos, nstates, ncls;
+    const uint64_t* packed;
+    const uint32_t* wbytes;
+    const uint32_t* wmeta;
+    uint32_t nwtile;
+    const uint16_t* clsinfo;
+    const uint16_t* remap;
+    uint32_t ngood, bits, rw;
     const int32_t* states;
     uint32_t B, V, words;
     uint32_t* out;
