@@ -346,17 +346,20 @@ extern "C" int zs_dfa_create(zs_ctx* ctx, const uint32_t* h_trans, uint32_t nsta
     uint32_t ngood = 0;
     for (uint32_t s = 0; s < nstates; s++)
         if (!bad[s]) remap[s] = (uint16_t)ngood++;
+    // the fail value is ngood, a sink row whose entries all lead to itself, so a
+    // walk needs no liveness test per step
     uint32_t bits = 1;
-    while ((1u << bits) - 1u < ngood) bits++;  // all ones is the fail value
+    while ((1u << bits) - 1u < ngood) bits++;
     const uint32_t per = 64 / bits, rw = (ncls + per - 1) / per;
-    std::vector<uint64_t> packed((size_t)(ngood ? ngood : 1) * rw, 0ull);
-    const uint64_t fail = (1ull << bits) - 1ull;
-    for (uint32_t s = 0; s < nstates; s++) {
-        if (bad[s]) continue;
+    std::vector<uint64_t> packed(((size_t)(ngood + 1) * rw + 1) & ~(size_t)1, 0ull);  // whole 16-byte quads
+    const uint64_t fail = ngood;
+    for (uint32_t s = 0; s <= nstates; s++) {
+        if (s < nstates && bad[s]) continue;
+        const uint32_t row = s < nstates ? remap[s] : ngood;
         for (uint32_t c = 0; c < ncls; c++) {
-            const uint16_t tgt = cols[c][s];
+            const uint16_t tgt = s < nstates ? cols[c][s] : 0xffffu;
             const uint64_t v = tgt == 0xffffu ? fail : (uint64_t)remap[tgt];
-            packed[(size_t)remap[s] * rw + c / per] |= v << ((c % per) * bits);
+            packed[(size_t)row * rw + c / per] |= v << ((c % per) * bits);
         }
     }
     uint16_t clsinfo[256];
@@ -364,7 +367,7 @@ extern "C" int zs_dfa_create(zs_ctx* ctx, const uint32_t* h_trans, uint32_t nsta
     d->ngood = ngood;
     d->bits = bits;
     d->rw = rw;
-    d->packed_lds = (size_t)ngood * rw * 8 <= ZS_DFA_LDS_BYTES ? 1 : 0;
+    d->packed_lds = packed.size() * 8 <= ZS_DFA_LDS_BYTES ? 1 : 0;
     int prev = 0;
     hipGetDevice(&prev);
     hipSetDevice(ctx->device);

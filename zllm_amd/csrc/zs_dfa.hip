@@ -120,7 +120,7 @@ __global__ __launch_bounds__(DM_NT) void zs_k_dfa_mask(dm_args a) {
 #define DL_RG 8                  // rows walked together
 #define DL_TW (ZS_WALK_TILE / 32) // bitmap words per row and tile
 #define DL_WORDS (ZS_DFA_LDS_BYTES / 8)
-#define DL_MAXROWS 2048          // constrained-row list in LDS
+#define DL_MAXROWS 1024          // constrained-row list in LDS
 __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
     __shared__ uint64_t tab[DL_WORDS];
     __shared__ uint16_t ci[256];
@@ -129,8 +129,24 @@ __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
     __shared__ uint16_t cst[DL_MAXROWS];   // their good start state (0xffff: none allowed)
     __shared__ uint32_t ncr;
     const int t = threadIdx.x;
-    const uint32_t nw = a.ngood * a.rw;
-    for (uint32_t i = t; i < nw; i += DL_NT) tab[i] = a.packed[i];
+    // stage the table with many 16-byte loads in flight per thread
+    const uint32_t nw = (a.ngood + 1) * a.rw;
+    const uint32_t nq = (nw + 1) / 2;  // 16-byte quads (the table is allocated in whole words)
+    const uint4* src = reinterpret_cast<const uint4*>(a.packed);
+    uint4* dst = reinterpret_cast<uint4*>(tab);
+    for (uint32_t q0 = 0; q0 < nq; q0 += 8 * DL_NT) {
+        uint4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const uint32_t q = q0 + u * DL_NT + t;
+            if (q < nq) v[u] = src[q];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const uint32_t q = q0 + u * DL_NT + t;
+            if (q < nq) dst[q] = v[u];
+        }
+    }
     for (int i = t; i < 256; i += DL_NT) ci[i] = a.clsinfo[i];
     if (t == 0) ncr = 0;
     __syncthreads();
@@ -151,8 +167,8 @@ __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
     }
     const uint32_t nc = ncr;
     const uint32_t rw = a.rw;
-    const uint64_t fmask = (1ull << a.bits) - 1ull;
-    const uint32_t fail = (uint32_t)fmask;
+    const uint32_t fmask = (1u << a.bits) - 1u;
+    const uint32_t fail = a.ngood;  // the sink row
     const uint32_t ncover = a.V > a.ntab ? a.V : a.ntab;
     const uint32_t ntt = (ncover + ZS_WALK_TILE - 1) / ZS_WALK_TILE, nrg = (nc + DL_RG - 1) / DL_RG;
     for (uint32_t w = blockIdx.x; w < ntt * nrg; w += gridDim.x) {
@@ -162,53 +178,52 @@ __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
         for (int i = t; i < DL_RG * DL_TW; i += DL_NT) (&bm[0][0])[i] = 0;
         uint32_t s0[DL_RG];
 #pragma unroll
-        for (int rr = 0; rr < DL_RG; rr++) s0[rr] = (uint32_t)rr < nr ? cst[g0 + rr] : 0xffffu;
+        for (int rr = 0; rr < DL_RG; rr++) {
+            const uint32_t g = (uint32_t)rr < nr ? cst[g0 + rr] : 0xffffu;
+            s0[rr] = g == 0xffffu ? fail : g;
+        }
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < DL_TPT; j++) {
-            const uint32_t slot = tok0 + j * DL_NT + t;
+            // runs of 64 length-sorted slots: wave w takes runs w and 31 - w, so
+            // its lanes walk tokens of nearly one length and every wave gets a
+            // short and a long run (the item waits for its slowest wave)
+            static_assert(DL_TPT == 2 && ZS_WALK_TILE == 2048 && DL_NT == 1024, "run pairing");
+            const uint32_t wv = (uint32_t)t >> 6;
+            const uint32_t run = j == 0 ? wv : 31u - wv;
+            const uint32_t slot = tok0 + run * 64 + (uint32_t)zs_lane();
             if (tt >= a.nwtile) break;
             const uint32_t meta = a.wmeta[slot];
+            const uint4 wb = reinterpret_cast<const uint4*>(a.wbytes)[slot];  // issued with meta
             if (meta == 0xffffffffu) continue;
             const uint32_t id = meta & 0x3ffffu, L = meta >> 18;
             if (L == 0) continue;  // no bytes or not a token: never allowed
-            const uint4 wb = reinterpret_cast<const uint4*>(a.wbytes)[slot];
             const uint32_t bw[4] = {wb.x, wb.y, wb.z, wb.w};
-            uint32_t s[DL_RG], alive = 0;
+            uint32_t s[DL_RG];
 #pragma unroll
-            for (int rr = 0; rr < DL_RG; rr++) {
-                s[rr] = s0[rr];
-                if (s0[rr] != 0xffffu) alive |= 1u << rr;
-            }
+            for (int rr = 0; rr < DL_RG; rr++) s[rr] = s0[rr];
+            // failed walks sit in the sink row: every row steps unconditionally
 #pragma unroll
             for (int i = 0; i < 16; i++) {
-                if ((uint32_t)i >= L || !alive) break;
+                if ((uint32_t)i >= L) break;
                 const uint32_t c = ci[(bw[i >> 2] >> (8 * (i & 3))) & 0xffu];
                 const uint32_t cw = c & 0xffu, sh = c >> 8;
 #pragma unroll
-                for (int rr = 0; rr < DL_RG; rr++) {
-                    if (!((alive >> rr) & 1u)) continue;
-                    s[rr] = (uint32_t)((tab[s[rr] * rw + cw] >> sh) & fmask);
-                    if (s[rr] == fail) alive &= ~(1u << rr);
-                }
+                for (int rr = 0; rr < DL_RG; rr++) s[rr] = (uint32_t)(tab[s[rr] * rw + cw] >> sh) & fmask;
             }
-            if (L > 16 && alive) {
+            if (L > 16) {
                 // bytes past the first 16 from the CSR copy (long tokens)
                 const uint32_t o0 = a.offsets[id], o1 = a.offsets[id + 1];
-                for (uint32_t i = o0 + 16; i < o1 && alive; i++) {
+                for (uint32_t i = o0 + 16; i < o1; i++) {
                     const uint32_t c = ci[a.bytes[i]];
 #pragma unroll
-                    for (int rr = 0; rr < DL_RG; rr++) {
-                        if (!((alive >> rr) & 1u)) continue;
-                        s[rr] = (uint32_t)((tab[s[rr] * rw + (c & 0xffu)] >> (c >> 8)) & fmask);
-                        if (s[rr] == fail) alive &= ~(1u << rr);
-                    }
+                    for (int rr = 0; rr < DL_RG; rr++) s[rr] = (uint32_t)(tab[s[rr] * rw + (c & 0xffu)] >> (c >> 8)) & fmask;
                 }
             }
             const uint32_t off = id - tok0;
 #pragma unroll
             for (int rr = 0; rr < DL_RG; rr++)
-                if ((alive >> rr) & 1u) atomicOr(&bm[rr][off >> 5], 1u << (off & 31));
+                if (s[rr] != fail) atomicOr(&bm[rr][off >> 5], 1u << (off & 31));
         }
         __syncthreads();
         // whole words out; bits at ids >= V stay clear; viability counts every
@@ -229,9 +244,10 @@ __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
     }
 }
 
-// Unconstrained rows: every id below V allowed.
+// Unconstrained rows: every id below V allowed; clears the viability flags.
 __global__ void zs_k_dfa_free_rows(dm_args a) {
     const uint32_t r = blockIdx.y;
+    if (blockIdx.x == 0 && threadIdx.x == 0) a.any[r] = 0;
     if (a.states[r] >= 0) return;
     for (uint32_t wi = blockIdx.x * blockDim.x + threadIdx.x; wi < a.words; wi += gridDim.x * blockDim.x) {
         uint32_t v = 0xffffffffu;
@@ -263,13 +279,13 @@ extern "C" int zs_dfa_mask_launch(const dm_args& a, bool packed_lds, uint32_t nc
                                   hipStream_t stream) {
     dm_args x = a;
     x.any = any_scratch;
-    hipLaunchKernelGGL(zs_k_fill_u32, dim3((a.B + 255) / 256), dim3(256), 0, stream, any_scratch, a.B, 0u);
     uint32_t ncover = a.V > a.ntab ? a.V : a.ntab;
     if (packed_lds && a.B <= DL_MAXROWS) {
         const uint32_t items = ((ncover + ZS_WALK_TILE - 1) / ZS_WALK_TILE) * ((a.B + DL_RG - 1) / DL_RG);
         hipLaunchKernelGGL(zs_k_dfa_free_rows, dim3(4, a.B), dim3(256), 0, stream, x);
         hipLaunchKernelGGL(zs_k_dfa_mask_packed, dim3(min(items, ncu)), dim3(DL_NT), 0, stream, x);
     } else {
+        hipLaunchKernelGGL(zs_k_fill_u32, dim3((a.B + 255) / 256), dim3(256), 0, stream, any_scratch, a.B, 0u);
         dim3 grid((ncover + DM_TOK - 1) / DM_TOK, (a.B + DM_ROWS - 1) / DM_ROWS);
         hipLaunchKernelGGL(zs_k_dfa_mask<false>, grid, dim3(DM_NT), 0, stream, x);
     }

@@ -213,10 +213,10 @@ struct zs_dfa {
     uint8_t* d_cls;        // [256] byte -> class
     uint8_t* d_bad;        // [nstates] dead or not live
     uint8_t* d_accept;     // [nstates]
-    // bit-packed table for the LDS walk: good states renumbered 0..ngood-1,
-    // entries of `bits` bits (all ones = fail), 64 / bits per u64 word, each
-    // state row padded to `rw` words
-    uint64_t* d_packed;    // [ngood][rw]
+    // bit-packed table for the LDS walk: good states renumbered 0..ngood-1 and
+    // a sink row ngood (the fail value), entries of `bits` bits, 64 / bits per
+    // u64 word, each state row padded to `rw` words
+    uint64_t* d_packed;    // [ngood + 1][rw]
     uint16_t* d_clsinfo;   // [256] word in row | bit shift << 8
     uint16_t* d_remap;     // [nstates] good id or 0xffff
     uint32_t ngood, bits, rw;
