@@ -347,27 +347,32 @@ extern "C" int zs_dfa_create(zs_ctx* ctx, const uint32_t* h_trans, uint32_t nsta
     for (uint32_t s = 0; s < nstates; s++)
         if (!bad[s]) remap[s] = (uint16_t)ngood++;
     // the fail value is ngood, a sink row whose entries all lead to itself, so a
-    // walk needs no liveness test per step
+    // walk needs no liveness test per step; entries of `bits` bits packed back
+    // to back (row s, class c at bit (s * ncls + c) * bits)
     uint32_t bits = 1;
     while ((1u << bits) - 1u < ngood) bits++;
-    const uint32_t per = 64 / bits, rw = (ncls + per - 1) / per;
-    std::vector<uint64_t> packed(((size_t)(ngood + 1) * rw + 1) & ~(size_t)1, 0ull);  // whole 16-byte quads
-    const uint64_t fail = ngood;
+    const uint64_t nbits = (uint64_t)(ngood + 1) * ncls * bits;
+    // + slack for the two-word reads, rounded to whole 16-byte quads
+    std::vector<uint32_t> packed(((size_t)((nbits + 31) / 32 + 1) + 3) & ~(size_t)3, 0u);
+    const uint32_t fail = ngood;
     for (uint32_t s = 0; s <= nstates; s++) {
         if (s < nstates && bad[s]) continue;
         const uint32_t row = s < nstates ? remap[s] : ngood;
         for (uint32_t c = 0; c < ncls; c++) {
             const uint16_t tgt = s < nstates ? cols[c][s] : 0xffffu;
-            const uint64_t v = tgt == 0xffffu ? fail : (uint64_t)remap[tgt];
-            packed[(size_t)row * rw + c / per] |= v << ((c % per) * bits);
+            const uint64_t v = tgt == 0xffffu ? fail : remap[tgt];
+            const uint64_t off = ((uint64_t)row * ncls + c) * bits;
+            packed[off >> 5] |= (uint32_t)(v << (off & 31));
+            if ((off & 31) + bits > 32) packed[(off >> 5) + 1] |= (uint32_t)(v >> (32 - (off & 31)));
         }
     }
     uint16_t clsinfo[256];
-    for (uint32_t b = 0; b < 256; b++) clsinfo[b] = (uint16_t)((cls[b] / per) | (((cls[b] % per) * bits) << 8));
+    for (uint32_t b = 0; b < 256; b++) clsinfo[b] = (uint16_t)(cls[b] * bits);
+    const uint32_t rw = ncls * bits;  // bits per state row
     d->ngood = ngood;
     d->bits = bits;
     d->rw = rw;
-    d->packed_lds = packed.size() * 8 <= ZS_DFA_LDS_BYTES ? 1 : 0;
+    d->packed_lds = packed.size() * 4 <= ZS_DFA_LDS_BYTES && ncls * bits < 65536 ? 1 : 0;
     int prev = 0;
     hipGetDevice(&prev);
     hipSetDevice(ctx->device);
@@ -380,7 +385,8 @@ extern "C" int zs_dfa_create(zs_ctx* ctx, const uint32_t* h_trans, uint32_t nsta
     if (!rc) rc = zs_alloc(ctx, &d->d_clsinfo, 256);
     if (!rc) rc = zs_alloc(ctx, &d->d_remap, nstates);
     if (!rc) {
-        hipMemcpy(d->d_packed, packed.data(), packed.size() * 8, hipMemcpyHostToDevice);
+        hipMemcpy(d->d_packed, packed.data(), packed.size() * 4, hipMemcpyHostToDevice);
+        d->packed_words = (uint32_t)packed.size();
         hipMemcpy(d->d_clsinfo, clsinfo, 256 * 2, hipMemcpyHostToDevice);
         hipMemcpy(d->d_remap, remap.data(), nstates * 2, hipMemcpyHostToDevice);
         hipMemcpy(d->d_trans, tab.data(), tab.size() * 2, hipMemcpyHostToDevice);
@@ -444,6 +450,7 @@ extern "C" int zs_dfa_mask(zs_ctx* ctx, const zs_dfa* dfa, const zs_vocab* vocab
     a.nstates = dfa->nstates;
     a.ncls = dfa->ncls;
     a.packed = dfa->d_packed;
+    a.packed_words = dfa->packed_words;
     a.wbytes = vocab->d_wbytes;
     a.wmeta = vocab->d_wmeta;
     a.nwtile = vocab->nwtile;

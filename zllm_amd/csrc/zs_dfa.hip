@@ -119,10 +119,10 @@ __global__ __launch_bounds__(DM_NT) void zs_k_dfa_mask(dm_args a) {
 #define DL_TPT (ZS_WALK_TILE / DL_NT)
 #define DL_RG 8                  // rows walked together
 #define DL_TW (ZS_WALK_TILE / 32) // bitmap words per row and tile
-#define DL_WORDS (ZS_DFA_LDS_BYTES / 8)
+#define DL_WORDS (ZS_DFA_LDS_BYTES / 4)
 #define DL_MAXROWS 1024          // constrained-row list in LDS
 __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
-    __shared__ uint64_t tab[DL_WORDS];
+    __shared__ uint32_t tab[DL_WORDS];
     __shared__ uint16_t ci[256];
     __shared__ uint32_t bm[DL_RG][DL_TW];
     __shared__ uint16_t crow[DL_MAXROWS];  // constrained rows
@@ -130,23 +130,18 @@ __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
     __shared__ uint32_t ncr;
     const int t = threadIdx.x;
     // stage the table with many 16-byte loads in flight per thread
-    const uint32_t nw = (a.ngood + 1) * a.rw;
-    const uint32_t nq = (nw + 1) / 2;  // 16-byte quads (the table is allocated in whole words)
+    const uint32_t nq = a.packed_words / 4;  // the table is allocated in whole quads
     const uint4* src = reinterpret_cast<const uint4*>(a.packed);
     uint4* dst = reinterpret_cast<uint4*>(tab);
-    for (uint32_t q0 = 0; q0 < nq; q0 += 8 * DL_NT) {
+    uint32_t q0 = 0;
+    for (; q0 + 8 * DL_NT <= nq; q0 += 8 * DL_NT) {
         uint4 v[8];
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const uint32_t q = q0 + u * DL_NT + t;
-            if (q < nq) v[u] = src[q];
-        }
+        for (int u = 0; u < 8; u++) v[u] = src[q0 + u * DL_NT + t];
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const uint32_t q = q0 + u * DL_NT + t;
-            if (q < nq) dst[q] = v[u];
-        }
+        for (int u = 0; u < 8; u++) dst[q0 + u * DL_NT + t] = v[u];
     }
+    for (uint32_t q = q0 + t; q < nq; q += DL_NT) dst[q] = src[q];
     for (int i = t; i < 256; i += DL_NT) ci[i] = a.clsinfo[i];
     if (t == 0) ncr = 0;
     __syncthreads();
@@ -166,8 +161,14 @@ __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
         __syncthreads();
     }
     const uint32_t nc = ncr;
-    const uint32_t rw = a.rw;
+    const uint32_t rw = a.rw;  // bits per state row
     const uint32_t fmask = (1u << a.bits) - 1u;
+    // entry at bit offset o: the 32 bits from o of the two words holding it
+    auto step = [&](uint32_t st, uint32_t cb) -> uint32_t {
+        const uint32_t o = __umul24(st, rw) + cb;  // states < 2^16, row bits < 2^16
+        const uint32_t w = o >> 5;
+        return __builtin_amdgcn_alignbit(tab[w + 1], tab[w], o & 31u) & fmask;
+    };
     const uint32_t fail = a.ngood;  // the sink row
     const uint32_t ncover = a.V > a.ntab ? a.V : a.ntab;
     const uint32_t ntt = (ncover + ZS_WALK_TILE - 1) / ZS_WALK_TILE, nrg = (nc + DL_RG - 1) / DL_RG;
@@ -206,18 +207,17 @@ __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 if ((uint32_t)i >= L) break;
-                const uint32_t c = ci[(bw[i >> 2] >> (8 * (i & 3))) & 0xffu];
-                const uint32_t cw = c & 0xffu, sh = c >> 8;
+                const uint32_t cb = ci[(bw[i >> 2] >> (8 * (i & 3))) & 0xffu];
 #pragma unroll
-                for (int rr = 0; rr < DL_RG; rr++) s[rr] = (uint32_t)(tab[s[rr] * rw + cw] >> sh) & fmask;
+                for (int rr = 0; rr < DL_RG; rr++) s[rr] = step(s[rr], cb);
             }
             if (L > 16) {
                 // bytes past the first 16 from the CSR copy (long tokens)
                 const uint32_t o0 = a.offsets[id], o1 = a.offsets[id + 1];
                 for (uint32_t i = o0 + 16; i < o1; i++) {
-                    const uint32_t c = ci[a.bytes[i]];
+                    const uint32_t cb = ci[a.bytes[i]];
 #pragma unroll
-                    for (int rr = 0; rr < DL_RG; rr++) s[rr] = (uint32_t)(tab[s[rr] * rw + (c & 0xffu)] >> (c >> 8)) & fmask;
+                    for (int rr = 0; rr < DL_RG; rr++) s[rr] = step(s[rr], cb);
                 }
             }
             const uint32_t off = id - tok0;

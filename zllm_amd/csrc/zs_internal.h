@@ -214,12 +214,12 @@ struct zs_dfa {
     uint8_t* d_bad;        // [nstates] dead or not live
     uint8_t* d_accept;     // [nstates]
     // bit-packed table for the LDS walk: good states renumbered 0..ngood-1 and
-    // a sink row ngood (the fail value), entries of `bits` bits, 64 / bits per
-    // u64 word, each state row padded to `rw` words
-    uint64_t* d_packed;    // [ngood + 1][rw]
-    uint16_t* d_clsinfo;   // [256] word in row | bit shift << 8
+    // a sink row ngood (the fail value), entries of `bits` bits back to back,
+    // state s / class c at bit (s * ncls + c) * bits; rw = ncls * bits
+    uint32_t* d_packed;    // [packed_words]
+    uint16_t* d_clsinfo;   // [256] class * bits
     uint16_t* d_remap;     // [nstates] good id or 0xffff
-    uint32_t ngood, bits, rw;
+    uint32_t ngood, bits, rw, packed_words;
     int packed_lds;        // the packed table fits the LDS budget
 };
 
@@ -235,7 +235,8 @@ struct dm_args {
     const uint8_t* bytes;
     const uint8_t* valid;
     uint32_t ntab, eos, nstates, ncls;
-    const uint64_t* packed;
+    const uint32_t* packed;
+    uint32_t packed_words;
     const uint32_t* wbytes;
     const uint32_t* wmeta;
     uint32_t nwtile;

@@ -100,3 +100,142 @@ def random_dfa(S, seed, dead_rate=0.3, accept_rate=0.1):
     accept = (rng.random(S) < accept_rate).astype(np.uint8)
     accept[dead_id] = 0
     return trans, dead, accept
+
+
+# ---------------------------------------------------------------- JSON-schema DFA
+_NAME_CHARS = b"abcdefghijklmnopqrstuvwxyz_"
+_STR_CHARS = b"abcdefghijklmnopqrstuvwxyzABCDEFGHIJKLMNOPQRSTUVWXYZ0123456789 -_.,"
+
+
+class _DfaBuilder:
+    def __init__(self):
+        self.rows = []
+        self.accept = []
+        self.dead = self.new()          # state 0: dead sink
+
+    def new(self):
+        self.rows.append(np.zeros(256, np.int64))   # default -> dead (0)
+        self.accept.append(0)
+        return len(self.rows) - 1
+
+    def edge(self, s, byte, t):
+        self.rows[s][byte] = t
+
+    def literal(self, s, text):
+        for b in text:
+            t = self.new()
+            self.edge(s, b, t)
+            s = t
+        return s
+
+
+def json_dfa(target_states, seed, max_depth=2):
+    """Anchored byte DFA for a synthetic JSON schema: nested objects of 6-12
+    required properties in a fixed order (no whitespace), each property a
+    string, number, bool, enum or (up to `max_depth`) nested object, names drawn
+    from seed. Properties are added to the root object until the automaton has
+    at least `target_states` states. Returns (trans u32[S,256], dead u8[S],
+    accept u8[S]); state 0 is the dead state, state 1 the start."""
+    rng = np.random.default_rng(seed + 7777)
+    B = _DfaBuilder()
+    start = B.new()
+
+    def name():
+        n = int(rng.integers(3, 11))
+        return bytes(rng.choice(np.frombuffer(_NAME_CHARS, np.uint8), n).tolist())
+
+    def value(s, depth):
+        """Value from state s; returns the state after the value."""
+        kind = rng.choice(["string", "number", "bool", "enum", "object"] if depth < max_depth
+                          else ["string", "number", "bool", "enum"])
+        if kind == "string":
+            q = B.new()
+            B.edge(s, ord('"'), q)
+            for c in _STR_CHARS:
+                B.edge(q, c, q)
+            e = B.new()
+            B.edge(q, ord('"'), e)
+            return e
+        if kind == "number":
+            sign = B.new()
+            B.edge(s, ord("-"), sign)
+            ip = B.new()
+            for c in b"0123456789":
+                B.edge(s, c, ip)
+                B.edge(sign, c, ip)
+                B.edge(ip, c, ip)
+            dot = B.new()
+            B.edge(ip, ord("."), dot)
+            fp = B.new()
+            for c in b"0123456789":
+                B.edge(dot, c, fp)
+                B.edge(fp, c, fp)
+            # the number ends at the next structural byte: the caller's edges
+            # from the end state are copied onto ip and fp
+            return ("number", ip, fp)
+        if kind == "bool":
+            t = B.literal(s, b"true")
+            f_ = B.literal(s, b"fals")
+            e = B.new()
+            B.edge(f_, ord("e"), e)
+            B.rows[t] = B.rows[e]   # share the continuation row (same object)
+            return ("alias", e, t)
+        if kind == "enum":
+            e = B.new()
+            words = {bytes(rng.choice(np.frombuffer(_NAME_CHARS, np.uint8), int(rng.integers(2, 8))).tolist())
+                     for _ in range(int(rng.integers(2, 6)))}
+            q = B.new()
+            B.edge(s, ord('"'), q)
+            for w in sorted(words):   # a trie of quoted words
+                cur = q
+                for c in w:
+                    nxt = B.rows[cur][c]
+                    if nxt == 0:
+                        nxt = B.new()
+                        B.edge(cur, c, nxt)
+                    cur = nxt
+                B.edge(cur, ord('"'), e)
+            return e
+        return obj(s, depth + 1, int(rng.integers(6, 13)))
+
+    def close_value(v):
+        """Normalises a value result to (end state, extra end states that share its row)."""
+        if isinstance(v, tuple):
+            if v[0] == "number":
+                return v[1], [v[2]]
+            return v[1], [v[2]]
+        return v, []
+
+    def obj(s, depth, nprops, grow=False):
+        o = B.new()
+        B.edge(s, ord("{"), o)
+        cur, extra = o, []
+        i = 0
+        while True:
+            if i > 0:
+                c = B.new()
+                B.edge(cur, ord(","), c)
+                for x in extra:
+                    B.edge(x, ord(","), c)
+                cur, extra = c, []
+            k = B.literal(cur, b'"' + name() + b'":')
+            cur, extra = close_value(value(k, depth))
+            i += 1
+            if i >= nprops and (not grow or len(B.rows) >= target_states - 2):
+                break
+        end = B.new()
+        B.edge(cur, ord("}"), end)
+        for x in extra:
+            B.edge(x, ord("}"), end)
+        return end
+
+    root_end = obj(start, 0, 6, grow=True)
+    B.accept[root_end] = 1
+    S = len(B.rows)
+    trans = np.stack(B.rows).astype(np.uint32)
+    dead = np.zeros(S, np.uint8)
+    dead[0] = 1
+    accept = np.array(B.accept, np.uint8)
+    # anchored: renumber so that state 0 is the start (the reference walks
+    # from the caller's current state; the start is what a fresh request uses)
+    return trans, dead, accept
