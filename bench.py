@@ -46,7 +46,9 @@ def build_workload(B, V, S, seed):
     params = synth.mixed_params(B, V, seed, hist=256)
     offs, data = synth.synthetic_vocab(V, seed)
     valid = np.ones(V, np.uint8)
-    trans, dead, acc = synth.random_dfa(S, seed, dead_rate=0.3)
+    # C5's grammar: a structured (JSON-schema) automaton of about S states
+    trans, dead, acc = synth.json_dfa(S, seed)
+    S = trans.shape[0]
     table = TokenByteTable.from_csr(ctx, offs, data, valid, eos=V - 1)
     dfa = ByteDfa(ctx, trans, dead, acc)
     rng = np.random.default_rng(seed)
@@ -105,6 +107,36 @@ SPEC_K = 4
 def spec_bytes_per_row(V, k):
     # target logits at k+1 positions + draft logits at k positions + ids/outputs
     return 4 * V * (2 * k + 1) + 4 * k + 8
+
+
+def mask_config_us(ctx, V, rows, kind, S, seed):
+    """Mean time of zs_dfa_mask over `rows` constrained rows (random current
+    states) for one DFA config; synthetic vocabulary as in config C3."""
+    import numpy as np
+    import torch
+    from zllm_amd import synth
+    from zllm_amd.engine import ByteDfa, TokenByteTable
+    offs, data = synth.synthetic_vocab(V, seed + S)
+    table = TokenByteTable.from_csr(ctx, offs, data, np.ones(V, np.uint8), eos=V - 1)
+    if kind == "random":
+        trans, dead, acc = synth.random_dfa(S, seed + S, dead_rate=0.3)
+    else:
+        trans, dead, acc = synth.json_dfa(S, seed + S)
+    dfa = ByteDfa(ctx, trans, dead, acc)
+    rng = np.random.default_rng(seed + S + 1)
+    live = [s for s in range(trans.shape[0]) if dfa.is_live(s) and not dead[s]]
+    st = torch.tensor(rng.choice(live, rows).astype(np.int32), device="cuda")
+    bits = torch.empty((rows, (V + 31) // 32), dtype=torch.int32, device="cuda")
+    for _ in range(3):
+        dfa.mask(table, st, V, out=bits)
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(20):
+        dfa.mask(table, st, V, out=bits)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / 20 * 1000.0
 
 
 def cpu_baseline(W, seconds, cores):
@@ -172,6 +204,11 @@ def main():
     torch.cuda.synchronize()
     ms_step = e0.elapsed_time(e1) / args.steps
 
+    # DFA-mask configs C3 (64-state random DFA, 32 rows, V=128256) and C4
+    # (JSON-schema DFA of 2048 states, 128 rows, V=151936), untimed loops
+    dfa_cfg = {"c5_json512": None, "c3_random64": mask_config_us(ctx, 128256, 32, "random", 64, args.seed),
+               "c4_json2048": mask_config_us(ctx, 151936, 128, "json", 2048, args.seed)}
+
     # spec verify alone (separate, untimed loop)
     s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     s0.record(stream)
@@ -232,12 +269,14 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (seeded power-law logits, synthetic vocab and 512-state DFA)",
+        "data": "synthetic (seeded power-law logits, synthetic vocab, 512-state JSON-schema DFA, spec-decode logits)",
         "config": {"workload": "C5 full continuous-batching sampler step", "B": B, "V": V,
                    "masked_rows": int(W["masked"].sum()), "dfa_states": args.dfa_states, "top_logprobs": 5,
                    "entropy": True, "spec_k": SPEC_K},
         "step_hbm_frac": round(step_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "dfa_mask_us": round(us_mask, 2),
+        "dfa_mask_us_configs": {"c5_json512": round(us_mask, 2), "c3_random64": round(dfa_cfg["c3_random64"], 2),
+                                "c4_json2048": round(dfa_cfg["c4_json2048"], 2)},
         "spec_verify_us": round(us_spec, 2),
         "kernel_ms": {k: round(v, 4) for k, v in acc.items()},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,

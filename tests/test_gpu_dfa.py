@@ -88,3 +88,51 @@ def test_advance_matches_oracle():
     for s in range(trans.shape[0]):
         for tok in range(7):
             assert dfa.advance(table, s, tok)[0] == O.advance(od, ov, s, tok)
+
+
+@pytest.mark.parametrize("S,V,rows", [(512, 20000, 16), (2048, 30000, 12)])
+def test_json_schema_dfa_grammar_vocab(S, V, rows):
+    """Structured DFA (nested-object JSON schema, few byte classes) with a vocab
+    of grammar fragments, so that walks survive many steps; the 2048-state
+    automaton exercises the tightly packed LDS table at 12-bit entries."""
+    print(f"[case] json S={S} V={V}", flush=True)
+    trans, dead, acc = synth.json_dfa(S, S + 1)
+    offs, data = synth.grammar_vocab(trans, dead, V, S + 2)
+    valid = np.ones(V, np.uint8)
+    valid[5::101] = 0
+    eos = V - 1
+    rng = np.random.default_rng(S + 3)
+    good = np.nonzero(dead == 0)[0]
+    states = list(rng.choice(good, rows)) + [0, -1]  # + the dead state and a free row
+    bits, anyv, dfa, table = _gpu_bits(trans, dead, acc, (offs, data, valid), eos, states, V)
+    tokens = [None if not valid[t] else bytes(data[offs[t]:offs[t + 1]]) for t in range(V)]
+    od, ov = O.Dfa(trans, dead, acc), O.Vocab(tokens, eos)
+    nonzero = 0
+    for i, s in enumerate(states):
+        if s < 0:
+            want = O.pack_bits(np.ones(V, bool))
+        else:
+            want = O.mask_bits(V, dfa=od, vocab=ov, state=int(s))
+            allowed, a = O.dfa_allowed(od, ov, int(s))
+            assert bool(anyv[i]) == a
+            nonzero += int(np.count_nonzero(want))
+        assert np.array_equal(bits[i], want), (i, s)
+    assert nonzero > 0
+
+
+def test_large_random_dfa_through_l2():
+    """A table beyond the LDS budget (3000 states x 256 classes) takes the
+    L2-resident walk."""
+    S, V = 3000, 8000
+    print(f"[case] large S={S} V={V}", flush=True)
+    offs, data = synth.synthetic_vocab(V, 77)
+    valid = np.ones(V, np.uint8)
+    trans, dead, acc = synth.random_dfa(S, 78, dead_rate=0.3)
+    rng = np.random.default_rng(79)
+    states = list(rng.integers(0, S - 1, 8)) + [-1]
+    bits, anyv, dfa, table = _gpu_bits(trans, dead, acc, (offs, data, valid), V - 1, states, V)
+    tokens = [bytes(data[offs[t]:offs[t + 1]]) for t in range(V)]
+    od, ov = O.Dfa(trans, dead, acc), O.Vocab(tokens, V - 1)
+    for i, s in enumerate(states):
+        want = O.pack_bits(np.ones(V, bool)) if s < 0 else O.mask_bits(V, dfa=od, vocab=ov, state=int(s))
+        assert np.array_equal(bits[i], want), (i, s)

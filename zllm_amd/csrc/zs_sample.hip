@@ -347,14 +347,71 @@ __device__ __forceinline__ void p1_topk_fast(const uint32_t (&key)[P1_EPT], uint
         p1_topk(key, vmask, K, base, out_key, out_idx, n_out, kth, full, sh);
         return;
     }
-    // threads without elements hold key 0, below every element
+    // Fewer than K values above -inf (a masked chunk): all of them plus the
+    // lowest-index -inf elements make the top-K.
+    const uint32_t kninf = zs_total_key(-INFINITY);
+    uint32_t myfin = 0;
+#pragma unroll
+    for (int e = 0; e < P1_EPT; e++) myfin += (((vmask >> e) & 1u) && key[e] > kninf) ? 1u : 0u;
+    const uint32_t nfin = block_sum_u<ZS_P1_NT>(myfin, sh.u);
+    if (nfin < K) {
+        if (t == 0) sh.cnt = 0;
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < P1_EPT; e++) {
+            if (((vmask >> e) & 1u) && key[e] > kninf) {
+                const uint32_t p = atomicAdd(&sh.cnt, 1u);
+                out_key[p] = key[e];
+                out_idx[p] = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
+            }
+        }
+        // -inf elements in index order: ids base + (j * NT + t) * 4 + q
+        const uint32_t need = K - nfin;
+        uint32_t carry = 0, ninf = 0;
+        const uint32_t ninf_all = nvalid - nfin;
+#pragma unroll
+        for (int j = 0; j < P1_EPT / 4; j++) {
+            if (carry >= need) break;  // uniform: the lowest ids are taken
+            uint32_t cj = 0;
+#pragma unroll
+            for (int q = 0; q < 4; q++) cj += (((vmask >> (4 * j + q)) & 1u) && key[4 * j + q] == kninf) ? 1u : 0u;
+            uint32_t tot;
+            uint32_t rank = carry + block_excl_scan_u<ZS_P1_NT>(cj, sh.u, &tot);
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int e = 4 * j + q;
+                if (((vmask >> e) & 1u) && key[e] == kninf) {
+                    if (rank < need) {
+                        out_key[nfin + rank] = kninf;
+                        out_idx[nfin + rank] = base + (j * ZS_P1_NT + t) * 4 + q;
+                    }
+                    rank++;
+                }
+            }
+            carry += tot;
+            ninf += tot;
+        }
+        __syncthreads();
+        (void)ninf;
+        *n_out = min(K, nfin + ninf_all);
+        *kth = kninf;
+        *full = ninf_all > need ? 2u : 1u;
+        __syncthreads();
+        return;
+    }
+    // theta: a lower bound of the K-th largest key -- the c-th largest thread
+    // maximum of every wave (c * 4 >= K elements at or above the smallest of
+    // them), or one wave's K-th largest thread maximum; threads without
+    // elements hold key 0, below every element
     const uint32_t srt = wave_sort_u32(tm);
     const uint32_t thw = __shfl(srt, 64 - (int)c, 64);
-    if (zs_lane() == 0) sh.sel[zs_wid()] = thw;
+    const uint32_t thk = K <= 64 ? __shfl(srt, 64 - (int)K, 64) : 0u;
+    if (zs_lane() == 0) { sh.sel[zs_wid()] = thw; sh.hist[zs_wid()] = thk; }
     __syncthreads();
-    uint32_t theta = sh.sel[0];
+    uint32_t theta = sh.sel[0], theta2 = sh.hist[0];
 #pragma unroll
-    for (int w = 1; w < ZS_P1_NT / 64; w++) theta = min(theta, sh.sel[w]);
+    for (int w = 1; w < ZS_P1_NT / 64; w++) { theta = min(theta, sh.sel[w]); theta2 = max(theta2, sh.hist[w]); }
+    theta = max(theta, theta2);
     uint32_t cnt = 0;
 #pragma unroll
     for (int e = 0; e < P1_EPT; e++) cnt += (((vmask >> e) & 1u) && key[e] >= theta) ? 1u : 0u;

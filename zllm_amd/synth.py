@@ -239,3 +239,35 @@ def json_dfa(target_states, seed, max_depth=2):
     # anchored: renumber so that state 0 is the start (the reference walks
     # from the caller's current state; the start is what a fresh request uses)
     return trans, dead, accept
+
+
+def grammar_vocab(trans, dead, V, seed, frac=0.5):
+    """V tokens: a `frac` share are byte strings of random walks through the
+    DFA (lengths geometric with mean 4, capped at 16, from random non-dead
+    states along non-dead transitions), the rest as synthetic_vocab. Gives a
+    vocabulary whose tokens survive long walks. Returns (offsets, bytes)."""
+    rng = np.random.default_rng(seed + 3331)
+    offs0, data0 = synthetic_vocab(V, seed)
+    S = trans.shape[0]
+    good = np.nonzero(dead == 0)[0]
+    toks = []
+    for t in range(V):
+        if rng.random() < frac:
+            s = int(rng.choice(good))
+            n = int(min(rng.geometric(0.25), 16))
+            out = bytearray()
+            for _ in range(n):
+                nxt = np.nonzero(dead[trans[s]] == 0)[0]
+                if len(nxt) == 0:
+                    break
+                b = int(rng.choice(nxt))
+                out.append(b)
+                s = int(trans[s, b])
+            if not out:
+                out = bytearray(b"a")
+            toks.append(bytes(out))
+        else:
+            toks.append(bytes(data0[offs0[t]:offs0[t + 1]]))
+    offs = np.zeros(V + 1, np.uint32)
+    offs[1:] = np.cumsum([len(x) for x in toks])
+    return offs, np.frombuffer(b"".join(toks), np.uint8).copy()
