@@ -67,7 +67,7 @@ extern "C" void zs_ctx_destroy(zs_ctx* ctx) {
     if (ctx->side_stream) (void)hipStreamDestroy((hipStream_t)ctx->side_stream);
     void* ptrs[] = {ctx->p_cnt, ctx->p_id, ctx->p_flags, ctx->p_y, ctx->cst, ctx->cs_key, ctx->cs_idx,
                     ctx->co_key, ctx->co_idx, ctx->rst, ctx->pairs, ctx->pv, ctx->mask_scratch, ctx->spec_chunks,
-                    ctx->spec_rows, ctx->sub_mom, ctx->sub_sum, ctx->p_sub};
+                    ctx->spec_rows, ctx->sub_mom, ctx->sub_sum, ctx->p_sub, ctx->k_ap, ctx->k_sum};
     for (void* p : ptrs)
         if (p) hipFree(p);
     hipSetDevice(dev);
@@ -118,6 +118,8 @@ extern "C" int zs_ctx_create(int device, uint32_t max_rows, uint32_t max_vocab, 
     if (!rc) rc = zs_alloc(ctx, &ctx->sub_mom, R * ctx->max_subs);
     if (!rc) rc = zs_alloc(ctx, &ctx->sub_sum, R * ZS_NSUM * ctx->max_subs);
     if (!rc) rc = zs_alloc(ctx, &ctx->p_sub, R * (ctx->max_subs + 1));
+    if (!rc) rc = zs_alloc(ctx, &ctx->k_ap, R * ctx->max_subs);
+    if (!rc) rc = zs_alloc(ctx, &ctx->k_sum, R * 2 * ctx->max_subs);
     if (!rc) rc = zs_alloc(ctx, &ctx->spec_rows, R);
     if (!rc) {
         hipStream_t s2 = nullptr;

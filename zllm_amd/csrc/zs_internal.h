@@ -105,6 +105,12 @@ struct zs_row_state {
     float samp_S;         // sampler softmax denominator (sampler.rs:68) when computed by the rounds
     float obs_S;          // sequential f32 sum (hallucination.rs:237-238, logprobs.rs:36)
     float obs_H;          // sequential f32 entropy (hallucination.rs:242-248)
+    // big rows with a top-p cut: the kept set compacted in index order (zs_k_big)
+    // whose sum and draw run as parallel rounds (zs_k_roundK / zs_k_stitchK)
+    uint32_t klist;       // 1: list ready
+    uint32_t nk;          // list length
+    uint32_t vstar, istar;  // kept: p > v*, or p == v* and id <= i*
+    float sum2;           // sequential sum of the kept set (sampler.rs:107)
     uint32_t n_cand;      // observer candidates by (x~ desc, id asc)
     uint32_t cand_id[ZS_OBS_CAND];
     float cand_x[ZS_OBS_CAND];
@@ -163,6 +169,8 @@ struct zs_ctx {
     void* mask_scratch;    // DFA mask staging
     zs_sub_mom* sub_mom;         // [rows][max_subs]
     zs_sub_sum* sub_sum;         // [rows][ZS_NSUM][max_subs]
+    double* k_ap;                // [rows][max_subs] approximate sums of the kept list per sub-chunk
+    zs_sub_sum* k_sum;           // [rows][2][max_subs] kept-list rounds (sum2, draw)
     uint32_t* p_sub;             // [rows][max_subs+1] patch index range per sub-chunk
     uint32_t max_subs;
     zs_spec_chunk* spec_chunks;  // [rows][2*ZS_SPEC_KMAX+1][max_chunks]

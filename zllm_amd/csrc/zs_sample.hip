@@ -48,6 +48,8 @@ struct zs_sargs {
     zs_sub_sum* sub_sum;
     uint32_t* p_sub;
     uint32_t max_subs;
+    double* k_ap;
+    zs_sub_sum* k_sum;
 };
 
 #define ZS_ST_LIMIT 0x100u
@@ -934,6 +936,7 @@ __global__ __launch_bounds__(CB_NT) void zs_k_combine(zs_sargs a) {
             st.obs_need = 0;
             st.rounds = 0;
             st.n_cand = 0;
+            st.klist = 0;
             a.rst[r] = st;
         }
         return;
@@ -1141,6 +1144,7 @@ __global__ __launch_bounds__(CB_NT) void zs_k_combine(zs_sargs a) {
         st.n_cand = n_cand;
         for (uint32_t j = 0; j < n_cand; j++) { st.cand_id[j] = cid_sh[j]; st.cand_x[j] = cx_sh[j]; }
         st.z_is_x = z_is_x;
+        st.klist = 0;
         a.rst[r] = st;
     }
 }
@@ -2180,52 +2184,28 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
             __syncthreads();
             istar = sh.u[7];
             __syncthreads();
-            // ---- sum over the kept set in index order (sampler.rs:107)
-            auto kept_term = [&](uint32_t i) -> float {
-                if (i >= nk) return 0.0f;
-                const uint32_t pb = kp[i];
-                return (pb > vstar || ki[i] <= istar) ? zs_u2f(pb) : 0.0f;
-            };
-            sum2 = -0.0f;
-            for (uint32_t q0 = 0; q0 < nk; q0 += ZS_BIG_G) {
-                float tv[4];
+            // ---- the sum over the kept set (sampler.rs:107) and the draw run as
+            // parallel rounds over the list (zs_k_roundK / zs_k_stitchK): here the
+            // approximate sum of every 1024-entry sub-chunk, one wave per sub-chunk
+            const uint32_t nks = (nk + ZS_SUB - 1) / ZS_SUB;
+            double* ap = a.k_ap + (size_t)r * a.max_subs;
+            for (uint32_t j = zs_wid(); j < nks; j += ZS_BIG_NT / 64) {
+                double acc = 0.0;
 #pragma unroll
-                for (int q = 0; q < 4; q++) tv[q] = kept_term(q0 + 4 * t + q);
-                seq_group<ZS_BIG_NT, 4>(tv, 0, sum2, NAN, sh.q);
-            }
-            BIG_MARK();
-            if (sum2 > 0.0f) {
-                // ---- draw (sampler.rs:118-127) over the renormalised kept set
-                const float rr = zs_philox_uniform(b.d_seed[r], b.d_counter[r], 0u);
-                uint32_t token = V - 1;
-                if (rr <= 0.0f) {
-                    token = 0;
-                } else {
-                    float cum = 0.0f;
-                    for (uint32_t q0 = 0; q0 < nk; q0 += ZS_BIG_G) {
-                        float tv[4];
-#pragma unroll
-                        for (int q = 0; q < 4; q++) {
-                            const float pp = kept_term(q0 + 4 * t + q);
-                            tv[q] = pp > 0.0f ? pp / sum2 : 0.0f;
-                        }
-                        int stp = seq_group<ZS_BIG_NT, 4>(tv, 0, cum, rr, sh.q);
-                        if (stp >= 0) { token = ki[q0 + (uint32_t)stp]; break; }
-                    }
+                for (int q = 0; q < ZS_SUB / 64; q++) {
+                    const uint32_t i = j * ZS_SUB + q * 64 + zs_lane();
+                    if (i < nk && (kp[i] > vstar || ki[i] <= istar)) acc += (double)zs_u2f(kp[i]);
                 }
-                BIG_MARK();
-#ifdef ZS_DEBUG_WALK
-                if (t == 0) printf("walk row %u peak %d nk %u sorts %llu sorted %llu finds %llu tiefirst %llu evfirst %llu\n", r, (int)peak, nk,
-                                   zs_dbg_walk[r][0], zs_dbg_walk[r][1], zs_dbg_walk[r][2], zs_dbg_walk[r][3], zs_dbg_walk[r][4]);
-#endif
-                if (t == 0) {
-                    // only the sampler's fields: the observers' entropy is written
-                    // concurrently by the side stream
-                    a.rst[r].token = token;
-                    a.rst[r].mode = ZS_MODE_DONE;
-                }
-                return;
+                acc = wave_sum_d(acc);
+                if (zs_lane() == 0) ap[j] = acc;
             }
+            if (t == 0) {
+                a.rst[r].klist = 1;
+                a.rst[r].nk = nk;
+                a.rst[r].vstar = vstar;
+                a.rst[r].istar = istar;
+            }
+            return;
         } else {
             // every positive p kept: sum over the whole row
             vstar = 0;
@@ -2265,6 +2245,144 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
     if (t == 0) {
         a.rst[r].token = token;
         a.rst[r].mode = ZS_MODE_DONE;
+    }
+}
+
+// ===========================================================================
+// Kept-list rounds: the sequential sums of the kept set in index order --
+// sum2 (sampler.rs:107) and the draw's running sum of p / sum2 (:118-127) --
+// spread over the GPU like the row sums above: every 1024-entry sub-chunk of a
+// row's kept list adds its increments on the grid predicted from the
+// approximate prefix, and one workgroup per row stitches the totals, redoing
+// exactly the sub-chunks whose grid was not certain.
+// ===========================================================================
+struct klist_row {
+    const uint32_t* kp;
+    const uint32_t* ki;
+    uint32_t nk, vstar, istar;
+    float inv;  // 0: the kept p themselves (sum2), else p / sum2 (draw)
+    float sum2;
+};
+__device__ __forceinline__ klist_row make_klist(const zs_sargs& a, uint32_t r, const zs_row_state& st, int kind) {
+    klist_row L;
+    L.kp = a.pairs + (size_t)r * a.max_vocab * 2;
+    L.ki = L.kp + a.max_vocab;
+    L.nk = st.nk;
+    L.vstar = st.vstar;
+    L.istar = st.istar;
+    L.sum2 = kind ? st.sum2 : 1.0f;
+    L.inv = kind ? 1.0f : 0.0f;
+    return L;
+}
+// term i of the list: the kept p (0 for the equal values after i*), divided by
+// sum2 for the draw
+__device__ __forceinline__ float klist_term(const klist_row& L, uint32_t i) {
+    if (i >= L.nk) return 0.0f;
+    const uint32_t pb = L.kp[i];
+    if (!(pb > L.vstar || L.ki[i] <= L.istar)) return 0.0f;
+    const float p = zs_u2f(pb);
+    return L.inv != 0.0f ? p / L.sum2 : p;
+}
+
+// one wave per (sub-chunk, row)
+template <int KIND>
+__global__ __launch_bounds__(256) void zs_k_roundK(zs_sargs a) {
+    const uint32_t r = blockIdx.y;
+    const uint32_t j = blockIdx.x * 4 + zs_wid();
+    const zs_row_state& st = a.rst[r];
+    if (!st.klist) return;
+    const uint32_t nks = (st.nk + ZS_SUB - 1) / ZS_SUB;
+    if (j >= nks) return;
+    const klist_row L = make_klist(a, r, st, KIND);
+    const double* ap = a.k_ap + (size_t)r * a.max_subs;
+    // approximate prefix before sub-chunk j and after it
+    double pre = 0.0;
+    for (uint32_t i = zs_lane(); i < j; i += 64) pre += ap[i];
+    pre = wave_sum_d(pre);
+    const double scale = KIND ? 1.0 / (double)L.sum2 : 1.0;
+    const double lo = pre * scale, hi = (pre + ap[j]) * scale;
+    const double delta = 1.0 / 256.0;
+    const double lm = lo * (1.0 - delta), hm = hi * (1.0 + delta);
+    const int blo = lm < 0x1p-125 ? -125 : ilogb(lm);
+    const int bhi = hm < 0x1p-125 ? -125 : ilogb(hm);
+    zs_sub_sum e;
+    e.pad = 0;
+    if (j == 0 || blo != bhi || !(hm < 3.0e38)) {
+        e.eg = 0;
+        e.flags = ZS_SF_FRAGILE;
+        e.total = 0;
+    } else {
+        e.eg = zs_grid_exp((float)lo);
+        uint32_t tot = 0, tie = 0;
+#pragma unroll
+        for (int q = 0; q < ZS_SUB / 64; q++) {
+            uint32_t tq;
+            tot = zs_sat_add(tot, zs_seq_inc(klist_term(L, j * ZS_SUB + q * 64 + zs_lane()), e.eg, &tq));
+            tie |= tq;
+        }
+        tot = wave_sum_sat(tot);
+        tie = wave_or_u(tie);
+        e.total = tot;
+        e.flags = ZS_SF_DONE | (tie ? ZS_SF_TIE : 0u);
+    }
+    if (zs_lane() == 0) a.k_sum[((size_t)r * 2 + KIND) * a.max_subs + j] = e;
+}
+
+// one workgroup per row: sum2 (KIND 0), or the draw (KIND 1) -- the first
+// entry after which the running sum reaches the uniform
+#define SK_NT 128
+#define SK_EPT (ZS_SUB / SK_NT)
+template <int KIND>
+__global__ __launch_bounds__(SK_NT) void zs_k_stitchK(zs_sargs a) {
+    const uint32_t r = blockIdx.x;
+    zs_row_state* stp = a.rst + r;
+    if (!stp->klist) return;
+    const zs_row_state st = *stp;
+    __shared__ seq_sh<SK_NT> sh;
+    __shared__ zs_sub_sum rec[ZS_MAX_SUBS];
+    const int t = threadIdx.x;
+    const klist_row L = make_klist(a, r, st, KIND);
+    const uint32_t nks = (L.nk + ZS_SUB - 1) / ZS_SUB;
+    const zs_sub_sum* ks = a.k_sum + ((size_t)r * 2 + KIND) * a.max_subs;
+    for (uint32_t j = t; j < nks; j += SK_NT) rec[j] = ks[j];
+    __syncthreads();
+    float thresh = NAN;
+    uint32_t token = a.b.V - 1;
+    bool done = false;
+    if (KIND == 1) {
+        const float rr = zs_philox_uniform(a.b.d_seed[r], a.b.d_counter[r], 0u);
+        if (rr <= 0.0f) { token = 0; done = true; }  // cumsum >= r at the first id
+        thresh = rr;
+    }
+    float s = KIND ? 0.0f : -0.0f;
+    for (uint32_t j = 0; j < nks && !done; j++) {
+        const zs_sub_sum e = rec[j];
+        const int eg = zs_grid_exp(s);
+        const uint32_t k0 = zs_grid_k(s);
+        if ((e.flags & ZS_SF_DONE) && !(e.flags & (ZS_SF_FRAGILE | ZS_SF_TIE)) && e.eg == eg &&
+            k0 + e.total < ZS_BINADE) {
+            const uint32_t kthr = KIND ? zs_grid_thresh(thresh, eg) : 0xffffffffu;
+            if (kthr == 0xffffffffu || k0 + e.total < kthr) {
+                s = zs_grid_value(k0 + e.total, eg);
+                continue;
+            }
+        }
+        float tv[SK_EPT];
+#pragma unroll
+        for (int q = 0; q < SK_EPT; q++) tv[q] = klist_term(L, j * ZS_SUB + SK_EPT * t + q);
+        const int stop = seq_group<SK_NT, SK_EPT>(tv, 0, s, thresh, sh);
+        if (KIND == 1 && stop >= 0) {
+            token = L.ki[j * ZS_SUB + (uint32_t)stop];
+            done = true;
+        }
+    }
+    if (t == 0) {
+        if (KIND == 0) {
+            stp->sum2 = s;
+        } else {
+            stp->token = token;
+            stp->mode = ZS_MODE_DONE;
+        }
     }
 }
 
@@ -2402,6 +2520,8 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
     a.sub_sum = ctx->sub_sum;
     a.p_sub = ctx->p_sub;
     a.max_subs = ctx->max_subs;
+    a.k_ap = ctx->k_ap;
+    a.k_sum = ctx->k_sum;
     const uint32_t B = bt->B;
     const uint32_t nch = (bt->V + ZS_P1_CH - 1) / ZS_P1_CH;
     const bool prof = ctx->profiling != 0;
@@ -2441,6 +2561,12 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
     mark("zs_k_pv");
     hipLaunchKernelGGL(zs_k_big, dim3(B), dim3(ZS_BIG_NT), 0, stream, a);
     mark("zs_k_big");
+    const uint32_t nsubk = (bt->V + ZS_SUB - 1) / ZS_SUB;
+    hipLaunchKernelGGL(zs_k_roundK<0>, dim3((nsubk + 3) / 4, B), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(zs_k_stitchK<0>, dim3(B), dim3(SK_NT), 0, stream, a);
+    hipLaunchKernelGGL(zs_k_roundK<1>, dim3((nsubk + 3) / 4, B), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(zs_k_stitchK<1>, dim3(B), dim3(SK_NT), 0, stream, a);
+    mark("zs_k_kept");
     if (!prof) ZS_LAUNCH_CHECK(hipStreamWaitEvent(stream, (hipEvent_t)ctx->join_event, 0));
     hipLaunchKernelGGL(zs_k_final, dim3((B + 63) / 64), dim3(64), 0, stream, a);
     mark("zs_k_final");
