@@ -102,6 +102,9 @@ def algorithmic_bytes_per_row(V, H, masked):
 
 
 SPEC_K = 4
+# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
+# (profiles/), scaled by the copy-kernel calibration; None where not measured
+TRAFFIC = {}
 
 
 def spec_bytes_per_row(V, k):
@@ -243,12 +246,17 @@ def main():
     step_bytes = float(sum(row_bytes)) + B * spec_bytes_per_row(V, SPEC_K)
     dom = max(acc, key=acc.get)
     dom_ms = acc[dom]
-    # algorithmic bytes attributed to the dominant kernel: the rows it processes
-    if dom == "zs_k_big":
-        n_big = int(np.sum((status & 4) == 0))
-        dom_bytes = float(sum(row_bytes[i] for i in range(B) if not (status[i] & 4)))
-    else:
-        dom_bytes = step_bytes
+    # algorithmic bytes of one launch of the dominant kernel: the rows it
+    # processes times their per-row bytes (the logits it must read at least once)
+    big_rows = [i for i in range(B) if not (status[i] & (1 | 2 | 4))]  # not greedy / non-finite / small
+    per_kernel_bytes = {
+        "zs_k_pass1": float(sum(row_bytes)),
+        "zs_k_big": float(sum(row_bytes[i] for i in big_rows)),
+        "zs_k_pv": float(sum(4 * V + 4 * V for i in big_rows)),   # read logits, write p
+        "zs_k_spec_stats": float(B * 4 * V * (2 * SPEC_K + 1)),
+        "zs_k_spec_sums": float(B * 4 * V * (2 * SPEC_K + 1)),
+    }
+    dom_bytes = per_kernel_bytes.get(dom, step_bytes)
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
     cpu = None
     if not args.no_cpu:
@@ -280,7 +288,8 @@ def main():
         "spec_verify_us": round(us_spec, 2),
         "kernel_ms": {k: round(v, 4) for k, v in acc.items()},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC.get(dom),
+                     "algorithmic_bytes": dom_bytes, "ms": round(dom_ms, 4)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(res))

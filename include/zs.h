@@ -208,11 +208,12 @@ int zs_lane_sample_topk(zs_ctx* ctx, const float* d_vals, const uint32_t* d_idxs
 uint32_t zs_step_seed(uint32_t base, uint32_t gen_idx);
 
 /* ---- profiling ----------------------------------------------------------
- * When enabled, zs_sample records a HIP event around each of its kernel
- * launches (no synchronisation is added). zs_last_timings waits for the last
- * call's events and writes up to `cap` kernel names / durations (ms); returns
- * the number of kernels. Stands in for the reference's in-process timing
- * (Cargo feature `profile`, Cargo.toml:121-126). */
+ * When enabled, zs_sample and zs_spec_verify record a HIP event around their
+ * kernel launches (no synchronisation is added; zs_sample then runs every
+ * kernel on the caller's stream). zs_last_timings waits for the last calls'
+ * events and writes up to `cap` kernel names / durations (ms), zs_sample's
+ * first; returns the number written. Stands in for the reference's
+ * in-process timing (Cargo feature `profile`, Cargo.toml:121-126). */
 int zs_set_profiling(zs_ctx* ctx, int on);
 int zs_last_timings(zs_ctx* ctx, const char** names, float* ms, int cap);
 

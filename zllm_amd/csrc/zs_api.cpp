@@ -12,7 +12,7 @@
 
 // launchers (zs_sample.hip, zs_dfa.hip)
 extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t stream);
-extern "C" int zs_spec_launch(const zs_spec_args& a, hipStream_t stream);
+extern "C" int zs_spec_launch(const zs_spec_args& a, const zs_prof& prof, hipStream_t stream);
 extern "C" int zs_lane_argmax_launch(const float* logits, uint32_t B, uint32_t V, uint64_t ld, const float* temp,
                                      const uint32_t* seed, uint32_t* out, hipStream_t stream);
 extern "C" int zs_lane_topk_launch(const float* logits, uint32_t B, uint32_t V, uint64_t ld, uint32_t K,
@@ -509,25 +509,42 @@ extern "C" int zs_set_profiling(zs_ctx* ctx, int on) {
             ZS_HIP(ctx, hipEventCreate(&e));
             ctx->events[i] = e;
         }
+        for (int i = 0; i < 8; i++) {
+            hipEvent_t e;
+            ZS_HIP(ctx, hipEventCreate(&e));
+            ctx->spec_events[i] = e;
+        }
         hipSetDevice(prev);
     }
     ctx->profiling = on ? 1 : 0;
     ctx->n_timed = 0;
+    ctx->n_spec_timed = 0;
     return ZS_OK;
 }
 
 extern "C" int zs_last_timings(zs_ctx* ctx, const char** names, float* ms, int cap) {
     if (!ctx) return ZS_EINVAL;
-    int n = ctx->n_timed;
-    if (n <= 0) return 0;
-    ZS_HIP(ctx, hipEventSynchronize((hipEvent_t)ctx->events[n]));
-    for (int i = 0; i < n && i < cap; i++) {
-        float t = 0.f;
-        ZS_HIP(ctx, hipEventElapsedTime(&t, (hipEvent_t)ctx->events[i], (hipEvent_t)ctx->events[i + 1]));
-        if (names) names[i] = ctx->timed_names[i + 1];
-        if (ms) ms[i] = t;
+    int k = 0;
+    const int n = ctx->n_timed, m = ctx->n_spec_timed;
+    if (n > 0) {
+        ZS_HIP(ctx, hipEventSynchronize((hipEvent_t)ctx->events[n]));
+        for (int i = 0; i < n && k < cap; i++, k++) {
+            float t = 0.f;
+            ZS_HIP(ctx, hipEventElapsedTime(&t, (hipEvent_t)ctx->events[i], (hipEvent_t)ctx->events[i + 1]));
+            if (names) names[k] = ctx->timed_names[i + 1];
+            if (ms) ms[k] = t;
+        }
     }
-    return n;
+    if (m > 0) {
+        ZS_HIP(ctx, hipEventSynchronize((hipEvent_t)ctx->spec_events[m]));
+        for (int i = 0; i < m && k < cap; i++, k++) {
+            float t = 0.f;
+            ZS_HIP(ctx, hipEventElapsedTime(&t, (hipEvent_t)ctx->spec_events[i], (hipEvent_t)ctx->spec_events[i + 1]));
+            if (names) names[k] = ctx->spec_names[i + 1];
+            if (ms) ms[k] = t;
+        }
+    }
+    return k;
 }
 
 static int zs_device_guard_begin(zs_ctx* ctx) {
@@ -559,7 +576,8 @@ extern "C" int zs_spec_verify(zs_ctx* ctx, const zs_spec_batch* b, void* stream)
     a.cst = ctx->spec_chunks; a.rs = ctx->spec_rows;
     a.nch = ctx->max_chunks; a.npos_max = 2 * ZS_SPEC_KMAX + 1;
     int prev = zs_device_guard_begin(ctx);
-    int rc = zs_spec_launch(a, (hipStream_t)stream);
+    zs_prof prof{ctx->profiling, ctx->spec_events, ctx->spec_names, &ctx->n_spec_timed};
+    int rc = zs_spec_launch(a, prof, (hipStream_t)stream);
     zs_device_guard_end(ctx, prev);
     if (rc) return zs_set_error(ctx, ZS_EHIP, "zs_spec_verify: launch failed: %s", hipGetErrorString(hipGetLastError()));
     return ZS_OK;

@@ -185,6 +185,9 @@ struct zs_ctx {
     int n_timed;
     void* events[16];      // hipEvent_t
     const char* timed_names[16];
+    int n_spec_timed;      // the same for the last zs_spec_verify call
+    void* spec_events[8];
+    const char* spec_names[8];
 };
 
 struct zs_vocab {
@@ -255,6 +258,14 @@ struct dm_args {
     uint32_t B, V, words;
     uint32_t* out;
     uint32_t* any;
+};
+
+// Optional per-kernel event timing of a launch sequence (zs_set_profiling).
+struct zs_prof {
+    int on;
+    void** events;       // hipEvent_t[n + 1]
+    const char** names;
+    int* n;
 };
 
 // Error helper (host).

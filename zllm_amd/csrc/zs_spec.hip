@@ -403,14 +403,26 @@ __global__ __launch_bounds__(SP_BIG_NT) void zs_k_spec_draw(zs_spec_args a) {
     if (t == 0) a.next[r] = found == ZS_BIGI ? V - 1 : base + (uint32_t)found;
 }
 
-extern "C" int zs_spec_launch(const zs_spec_args& a, hipStream_t stream) {
+extern "C" int zs_spec_launch(const zs_spec_args& a, const zs_prof& prof, hipStream_t stream) {
     const uint32_t npos = a.draft ? 2 * a.k + 1 : a.k + 1;
     const uint32_t nch = (a.V + SP_CH - 1) / SP_CH;
+    int ev = 0;
+    auto mark = [&](const char* name) {
+        if (!prof.on) return;
+        prof.names[ev] = name;
+        (void)hipEventRecord((hipEvent_t)prof.events[ev], stream);
+        ev++;
+    };
     dim3 grid(nch, npos, a.B);
+    mark(nullptr);
     hipLaunchKernelGGL(zs_k_spec_stats, grid, dim3(SP_NT), 0, stream, a);
+    mark("zs_k_spec_stats");
     hipLaunchKernelGGL(zs_k_spec_sums, grid, dim3(SP_NT), 0, stream, a);
+    mark("zs_k_spec_sums");
     hipLaunchKernelGGL(zs_k_spec_decide, dim3(a.B), dim3(64), 0, stream, a);
     hipLaunchKernelGGL(zs_k_spec_rsum, dim3(nch, a.B), dim3(SP_NT), 0, stream, a);
     hipLaunchKernelGGL(zs_k_spec_draw, dim3(a.B), dim3(SP_BIG_NT), 0, stream, a);
+    mark("zs_k_spec_draw");
+    if (prof.on) *prof.n = ev - 1;
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

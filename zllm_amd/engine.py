@@ -49,10 +49,11 @@ class Context:
         _check(self.h, lib().zs_set_profiling(self.h, 1 if on else 0), "zs_set_profiling")
 
     def last_timings(self) -> Dict[str, float]:
-        """Per-kernel durations (ms) of the last zs_sample call (profiling on)."""
-        names = (C.c_char_p * 16)()
-        ms = (C.c_float * 16)()
-        n = lib().zs_last_timings(self.h, names, ms, 16)
+        """Per-kernel durations (ms) of the last zs_sample and zs_spec_verify
+        calls (profiling on)."""
+        names = (C.c_char_p * 32)()
+        ms = (C.c_float * 32)()
+        n = lib().zs_last_timings(self.h, names, ms, 32)
         if n < 0:
             _check(self.h, n, "zs_last_timings")
         return {names[i].decode(): float(ms[i]) for i in range(n)}
