@@ -32,6 +32,8 @@ def parse():
     ap.add_argument("--seed", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe", type=int, default=0,
+                    help="only copy this many MiB device-to-device (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
     return ap.parse_args()
 
 
@@ -103,8 +105,10 @@ def algorithmic_bytes_per_row(V, H, masked):
 
 SPEC_K = 4
 # HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
-# (profiles/), scaled by the copy-kernel calibration; None where not measured
-TRAFFIC = {}
+# (profiles/c5_traffic.md), scaled by the copy-kernel calibration there; None
+# where not measured
+TRAFFIC = {"zs_k_big": 51.5e6, "zs_k_pass1": 167.5e6, "zs_k_pv": 55.2e6,
+           "zs_k_spec_stats": 1402.1e6, "zs_k_spec_sums": 1426.7e6}
 
 
 def spec_bytes_per_row(V, k):
@@ -173,8 +177,24 @@ def cpu_baseline(W, seconds, cores):
     return done / el, done
 
 
+def copy_probe(mib):
+    """A plain device copy of known size: its FETCH_SIZE / WRITE_SIZE per
+    dispatch against mib * 1024 KiB gives the counter scale."""
+    import torch
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_mib": mib}))
+
+
 def main():
     args = parse()
+    if args.copy_probe:
+        copy_probe(args.copy_probe)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build targets one GPU: run with --gpus 1 (sharding is design-only)"}))
         sys.exit(2)
