@@ -86,23 +86,27 @@ __global__ __launch_bounds__(SP_NT) void zs_k_spec_stats(zs_spec_args a) {
     const float T = a.temperature[r];
     float x[SP_EPT];
     sp_load(sp_row(a, r, pos), base, a.V, x);
-    float zmax = -INFINITY;
+    // max z = (max x) / T: a correctly rounded division by T > 0 is monotone,
+    // so the per-element divisions are not needed here (z overflows to +inf
+    // somewhere iff it does at the max)
+    float xmax = -INFINITY;
     uint32_t fl = 0;
     unsigned long long best = 0;  // (value key, ~idx): first strict max
 #pragma unroll
     for (int e = 0; e < SP_EPT; e++) {
         const uint32_t i = sp_id(base, e);
         if (i >= a.V) continue;
-        const float z = sp_z(x[e], T);
-        if (z != z) fl |= 1u;
-        else if (z == INFINITY) fl |= 2u;
-        zmax = fmaxf(zmax, z);
-        if (x[e] > -INFINITY) {  // strict > over init -inf (NaN never wins)
-            const float xx = (x[e] == 0.0f) ? 0.0f : x[e];
+        const float xv = x[e];
+        if (xv != xv) fl |= 1u;
+        xmax = fmaxf(xmax, xv);
+        if (xv > -INFINITY) {  // strict > over init -inf (NaN never wins)
+            const float xx = (xv == 0.0f) ? 0.0f : xv;
             const unsigned long long k = ((unsigned long long)zs_total_key(xx) << 32) | (0xffffffffu - i);
             best = k > best ? k : best;
         }
     }
+    float zmax = sp_z(xmax, T);
+    if (zmax == INFINITY) fl |= 2u;
     zmax = block_max_f<SP_NT>(zmax, fsh);
     fl = block_or_u<SP_NT>(fl, ush);
     for (int d = 32; d > 0; d >>= 1) {
@@ -139,9 +143,12 @@ __global__ __launch_bounds__(SP_NT) void zs_k_spec_sums(zs_spec_args a) {
     if (m > -INFINITY && m < INFINITY && cs[c].zmax - m >= SP_ZERO_D) {
         float x[SP_EPT];
         sp_load(sp_row(a, r, pos), base, a.V, x);
+        // x below xl gives z - m < -17.5 whatever the rounding of x / T (the
+        // bound keeps a 0.05 margin): no division or weight needed
+        const float xl = (float)(((double)m + (double)SP_ZERO_D - 0.05) * (double)(T != 1.0f ? T : 1.0f));
 #pragma unroll
         for (int e = 0; e < SP_EPT; e++)
-            if (sp_id(base, e) < a.V) s += sp_weight(sp_z(x[e], T), m);
+            if (sp_id(base, e) < a.V && x[e] >= xl) s += sp_weight(sp_z(x[e], T), m);
     }
     for (int d = 32; d > 0; d >>= 1) s += __shfl_xor(s, d, 64);
     if (zs_lane() == 0) sh[zs_wid()] = s;
