@@ -58,8 +58,8 @@ extern "C" const char* zs_last_error(const zs_ctx* ctx) { return ctx ? ctx->err 
 extern "C" void zs_ctx_destroy(zs_ctx* ctx) {
     if (!ctx) return;
     int dev = 0;
-    hipGetDevice(&dev);
-    hipSetDevice(ctx->device);
+    (void)hipGetDevice(&dev);
+    (void)hipSetDevice(ctx->device);
     for (int i = 0; i < 16; i++)
         if (ctx->events[i]) (void)hipEventDestroy((hipEvent_t)ctx->events[i]);
     if (ctx->fork_event) (void)hipEventDestroy((hipEvent_t)ctx->fork_event);
@@ -69,8 +69,8 @@ extern "C" void zs_ctx_destroy(zs_ctx* ctx) {
                     ctx->co_key, ctx->co_idx, ctx->rst, ctx->pairs, ctx->pv, ctx->mask_scratch, ctx->spec_chunks,
                     ctx->spec_rows, ctx->sub_mom, ctx->sub_sum, ctx->p_sub, ctx->k_ap, ctx->k_sum};
     for (void* p : ptrs)
-        if (p) hipFree(p);
-    hipSetDevice(dev);
+        if (p) (void)hipFree(p);
+    (void)hipSetDevice(dev);
     free(ctx);
 }
 
@@ -94,8 +94,8 @@ extern "C" int zs_ctx_create(int device, uint32_t max_rows, uint32_t max_vocab, 
         return ZS_EHIP;
     }
     int prev = 0;
-    hipGetDevice(&prev);
-    hipSetDevice(device);
+    (void)hipGetDevice(&prev);
+    (void)hipSetDevice(device);
     int rc = ZS_OK;
     int ncu = 0;
     if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || ncu <= 0) ncu = 256;
@@ -132,7 +132,7 @@ extern "C" int zs_ctx_create(int device, uint32_t max_rows, uint32_t max_vocab, 
         ctx->fork_event = e1;
         ctx->join_event = e2;
     }
-    hipSetDevice(prev);
+    (void)hipSetDevice(prev);
     if (rc) {
         zs_ctx_destroy(ctx);
         return rc;
@@ -151,12 +151,12 @@ struct zs_vocab_dev {
 
 extern "C" void zs_vocab_destroy(zs_vocab* v) {
     if (!v) return;
-    hipFree(v->d_offsets);
-    hipFree(v->d_bytes);
-    hipFree(v->d_valid);
-    hipFree(v->d_packed);
-    hipFree(v->d_wbytes);
-    hipFree(v->d_wmeta);
+    (void)hipFree(v->d_offsets);
+    (void)hipFree(v->d_bytes);
+    (void)hipFree(v->d_valid);
+    (void)hipFree(v->d_packed);
+    (void)hipFree(v->d_wbytes);
+    (void)hipFree(v->d_wmeta);
     free(v->h_offsets);
     free(v->h_bytes);
     free(v->h_valid);
@@ -211,8 +211,8 @@ extern "C" int zs_vocab_create(zs_ctx* ctx, const uint32_t* h_offsets, const uin
         }
     }
     int prev = 0;
-    hipGetDevice(&prev);
-    hipSetDevice(ctx->device);
+    (void)hipGetDevice(&prev);
+    (void)hipSetDevice(ctx->device);
     int rc = ZS_OK;
     // d_packed holds tok16 followed by tlen (bytes)
     size_t tok_words = (size_t)ntab * 4 + 4;
@@ -224,16 +224,18 @@ extern "C" int zs_vocab_create(zs_ctx* ctx, const uint32_t* h_offsets, const uin
     if (!rc) rc = zs_alloc(ctx, &v->d_wbytes, wbytes.size());
     if (!rc) rc = zs_alloc(ctx, &v->d_wmeta, wmeta.size());
     if (!rc) {
-        hipMemcpy(v->d_wbytes, wbytes.data(), wbytes.size() * 4, hipMemcpyHostToDevice);
-        hipMemcpy(v->d_wmeta, wmeta.data(), wmeta.size() * 4, hipMemcpyHostToDevice);
-        hipMemcpy(v->d_offsets, v->h_offsets, sizeof(uint32_t) * (ntab + 1), hipMemcpyHostToDevice);
-        if (v->nbytes) hipMemcpy(v->d_bytes, v->h_bytes, v->nbytes, hipMemcpyHostToDevice);
-        hipMemcpy(v->d_valid, v->h_valid, ntab, hipMemcpyHostToDevice);
-        hipMemcpy(v->d_packed, tok16.data(), tok_words * 4, hipMemcpyHostToDevice);
-        hipError_t e = hipMemcpy((uint8_t*)(v->d_packed + tok_words), tlen.data(), ntab + 1, hipMemcpyHostToDevice);
+        hipError_t e = hipMemcpy(v->d_wbytes, wbytes.data(), wbytes.size() * 4, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemcpy(v->d_wmeta, wmeta.data(), wmeta.size() * 4, hipMemcpyHostToDevice);
+        if (e == hipSuccess)
+            e = hipMemcpy(v->d_offsets, v->h_offsets, sizeof(uint32_t) * (ntab + 1), hipMemcpyHostToDevice);
+        if (e == hipSuccess && v->nbytes) e = hipMemcpy(v->d_bytes, v->h_bytes, v->nbytes, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemcpy(v->d_valid, v->h_valid, ntab, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemcpy(v->d_packed, tok16.data(), tok_words * 4, hipMemcpyHostToDevice);
+        if (e == hipSuccess)
+            e = hipMemcpy((uint8_t*)(v->d_packed + tok_words), tlen.data(), ntab + 1, hipMemcpyHostToDevice);
         if (e != hipSuccess) rc = zs_set_error(ctx, ZS_EHIP, "zs_vocab_create: %s", hipGetErrorString(e));
     }
-    hipSetDevice(prev);
+    (void)hipSetDevice(prev);
     if (rc) {
         zs_vocab_destroy(v);
         return rc;
@@ -247,13 +249,13 @@ extern "C" int zs_vocab_create(zs_ctx* ctx, const uint32_t* h_offsets, const uin
 // ---------------------------------------------------------------------------
 extern "C" void zs_dfa_destroy(zs_dfa* d) {
     if (!d) return;
-    hipFree(d->d_trans);
-    hipFree(d->d_cls);
-    hipFree(d->d_bad);
-    hipFree(d->d_accept);
-    hipFree(d->d_packed);
-    hipFree(d->d_clsinfo);
-    hipFree(d->d_remap);
+    (void)hipFree(d->d_trans);
+    (void)hipFree(d->d_cls);
+    (void)hipFree(d->d_bad);
+    (void)hipFree(d->d_accept);
+    (void)hipFree(d->d_packed);
+    (void)hipFree(d->d_clsinfo);
+    (void)hipFree(d->d_remap);
     free(d->h_trans);
     free(d->h_dead);
     free(d->h_accept);
@@ -376,8 +378,8 @@ extern "C" int zs_dfa_create(zs_ctx* ctx, const uint32_t* h_trans, uint32_t nsta
     d->rw = rw;
     d->packed_lds = packed.size() * 4 <= ZS_DFA_LDS_BYTES && ncls * bits < 65536 ? 1 : 0;
     int prev = 0;
-    hipGetDevice(&prev);
-    hipSetDevice(ctx->device);
+    (void)hipGetDevice(&prev);
+    (void)hipSetDevice(ctx->device);
     int rc = ZS_OK;
     if (!rc) rc = zs_alloc(ctx, &d->d_trans, tab.size());
     if (!rc) rc = zs_alloc(ctx, &d->d_cls, 256);
@@ -387,17 +389,17 @@ extern "C" int zs_dfa_create(zs_ctx* ctx, const uint32_t* h_trans, uint32_t nsta
     if (!rc) rc = zs_alloc(ctx, &d->d_clsinfo, 256);
     if (!rc) rc = zs_alloc(ctx, &d->d_remap, nstates);
     if (!rc) {
-        hipMemcpy(d->d_packed, packed.data(), packed.size() * 4, hipMemcpyHostToDevice);
         d->packed_words = (uint32_t)packed.size();
-        hipMemcpy(d->d_clsinfo, clsinfo, 256 * 2, hipMemcpyHostToDevice);
-        hipMemcpy(d->d_remap, remap.data(), nstates * 2, hipMemcpyHostToDevice);
-        hipMemcpy(d->d_trans, tab.data(), tab.size() * 2, hipMemcpyHostToDevice);
-        hipMemcpy(d->d_cls, cls, 256, hipMemcpyHostToDevice);
-        hipMemcpy(d->d_bad, bad.data(), nstates, hipMemcpyHostToDevice);
-        hipError_t e = hipMemcpy(d->d_accept, d->h_accept, nstates, hipMemcpyHostToDevice);
+        hipError_t e = hipMemcpy(d->d_packed, packed.data(), packed.size() * 4, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemcpy(d->d_clsinfo, clsinfo, 256 * 2, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemcpy(d->d_remap, remap.data(), nstates * 2, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemcpy(d->d_trans, tab.data(), tab.size() * 2, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemcpy(d->d_cls, cls, 256, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemcpy(d->d_bad, bad.data(), nstates, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemcpy(d->d_accept, d->h_accept, nstates, hipMemcpyHostToDevice);
         if (e != hipSuccess) rc = zs_set_error(ctx, ZS_EHIP, "zs_dfa_create: %s", hipGetErrorString(e));
     }
-    hipSetDevice(prev);
+    (void)hipSetDevice(prev);
     if (rc) {
         zs_dfa_destroy(d);
         return rc;
@@ -491,10 +493,10 @@ extern "C" int zs_sample(zs_ctx* ctx, const zs_batch* b, void* stream) {
     if (b->d_allow_bits && b->allow_words < (b->V + 31) / 32)
         return zs_set_error(ctx, ZS_EINVAL, "zs_sample: allow_words < ceil(V/32)");
     int prev = 0;
-    hipGetDevice(&prev);
-    if (prev != ctx->device) hipSetDevice(ctx->device);
+    (void)hipGetDevice(&prev);
+    if (prev != ctx->device) (void)hipSetDevice(ctx->device);
     int rc = zs_sample_launch(ctx, b, (hipStream_t)stream);
-    if (prev != ctx->device) hipSetDevice(prev);
+    if (prev != ctx->device) (void)hipSetDevice(prev);
     return rc;
 }
 
@@ -502,8 +504,8 @@ extern "C" int zs_set_profiling(zs_ctx* ctx, int on) {
     if (!ctx) return ZS_EINVAL;
     if (on && !ctx->events[0]) {
         int prev = 0;
-        hipGetDevice(&prev);
-        hipSetDevice(ctx->device);
+        (void)hipGetDevice(&prev);
+        (void)hipSetDevice(ctx->device);
         for (int i = 0; i < 16; i++) {
             hipEvent_t e;
             ZS_HIP(ctx, hipEventCreate(&e));
@@ -514,7 +516,7 @@ extern "C" int zs_set_profiling(zs_ctx* ctx, int on) {
             ZS_HIP(ctx, hipEventCreate(&e));
             ctx->spec_events[i] = e;
         }
-        hipSetDevice(prev);
+        (void)hipSetDevice(prev);
     }
     ctx->profiling = on ? 1 : 0;
     ctx->n_timed = 0;
@@ -549,12 +551,12 @@ extern "C" int zs_last_timings(zs_ctx* ctx, const char** names, float* ms, int c
 
 static int zs_device_guard_begin(zs_ctx* ctx) {
     int prev = 0;
-    hipGetDevice(&prev);
-    if (prev != ctx->device) hipSetDevice(ctx->device);
+    (void)hipGetDevice(&prev);
+    if (prev != ctx->device) (void)hipSetDevice(ctx->device);
     return prev;
 }
 static void zs_device_guard_end(zs_ctx* ctx, int prev) {
-    if (prev != ctx->device) hipSetDevice(prev);
+    if (prev != ctx->device) (void)hipSetDevice(prev);
 }
 
 extern "C" int zs_spec_verify(zs_ctx* ctx, const zs_spec_batch* b, void* stream) {

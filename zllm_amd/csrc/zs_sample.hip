@@ -2529,7 +2529,7 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
     auto mark = [&](const char* name) {
         if (!prof) return;
         if (name) ctx->timed_names[ev] = name;
-        hipEventRecord((hipEvent_t)ctx->events[ev], stream);
+        (void)hipEventRecord((hipEvent_t)ctx->events[ev], stream);
         ev++;
     };
     mark(nullptr);
