@@ -1513,6 +1513,7 @@ __global__ __launch_bounds__(ST_NT) void zs_k_stitchB(zs_sargs a) { stitch_body<
 // ===========================================================================
 #define BK_NB 2048   // buckets per level of the top-p walk
 #define BK_NC 16     // copies of each bucket counter (by lane)
+#define BK_SERIAL 4096  // exact buckets up to this size are walked by one thread
 static_assert(BK_NB * BK_NC <= ZS_SORT_CAP, "per-copy bucket counters live in the sort buffer");
 
 struct big_shared {
@@ -1634,7 +1635,7 @@ __device__ __forceinline__ float big_term_e(float z, bool has_thr, float thr, fl
 // probabilities is resolved afterwards on the row.
 // ---------------------------------------------------------------------------
 #ifdef ZS_DEBUG_WALK
-__device__ unsigned long long zs_dbg_walk[256][6];
+__device__ unsigned long long zs_dbg_walk[256][8];
 #define WALK_COUNT(k, v) do { if (threadIdx.x == 0) zs_dbg_walk[blockIdx.x][k] += (v); } while (0)
 #else
 #define WALK_COUNT(k, v) do {} while (0)
@@ -1646,7 +1647,7 @@ struct walk_out {
 };
 
 // descending bitonic sort of n (power of two) u32 values in LDS
-__device__ void bk_sort_desc(uint32_t* a, int n) {
+__device__ __forceinline__ void bk_sort_desc(uint32_t* a, int n) {
     for (int k = 2; k <= n; k <<= 1) {
         for (int j = k >> 1; j > 0; j >>= 1) {
             for (int i = threadIdx.x; i < n; i += ZS_BIG_NT) {
@@ -1663,14 +1664,52 @@ __device__ void bk_sort_desc(uint32_t* a, int n) {
 }
 
 // Walk n <= ZS_SORT_CAP values in exact descending order (sorted in LDS).
-__device__ walk_out bk_walk_sorted(const uint32_t* vals, uint32_t n, float& s, float thresh, big_shared& sh) {
+__device__ __forceinline__ walk_out bk_walk_sorted(const uint32_t* vals, uint32_t n, float& s, float thresh, big_shared& sh) {
     walk_out o = {false, 0u, 0u};
-    WALK_COUNT(0, 1); WALK_COUNT(1, n);
+    WALK_COUNT(0, 1);
     uint32_t np2 = 1;
     while (np2 < n) np2 <<= 1;
     for (uint32_t i = threadIdx.x; i < np2; i += ZS_BIG_NT) sh.sortbuf[i] = i < n ? vals[i] : 0u;
     __syncthreads();
     if (np2 > 1) bk_sort_desc(sh.sortbuf, (int)np2);
+    if (n <= BK_SERIAL) {
+        // a bucket of this size is walked faster by one thread than by the
+        // workgroup scan (whose cost is its latency chain, not its width)
+        if (threadIdx.x == 0) {
+            float ss = s;
+            uint32_t stp = 0xffffffffu;
+            for (uint32_t i0 = 0; i0 < n && stp == 0xffffffffu; i0 += 8) {
+                float v8[8];
+#pragma unroll
+                for (int q = 0; q < 8; q++) v8[q] = i0 + q < n ? zs_u2f(sh.sortbuf[i0 + q]) : 0.0f;
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    if (stp != 0xffffffffu || i0 + q >= n) continue;
+                    ss = ss + v8[q];
+                    if (ss >= thresh) stp = i0 + q;
+                }
+            }
+            sh.s = ss;
+            sh.u[4] = stp;
+        }
+        __syncthreads();
+        s = sh.s;
+        const uint32_t stp = sh.u[4];
+        __syncthreads();
+        if (stp != 0xffffffffu) {
+            const uint32_t v = sh.sortbuf[stp];
+            uint32_t lo = 0, hi = stp;
+            while (lo < hi) {
+                uint32_t mid = (lo + hi) >> 1;
+                if (sh.sortbuf[mid] > v) lo = mid + 1; else hi = mid;
+            }
+            o.stopped = true;
+            o.v = v;
+            o.rank = stp - lo;
+        }
+        __syncthreads();
+        return o;
+    }
     for (uint32_t q0 = 0; q0 < n; q0 += ZS_BIG_G) {
         float tv[4];
 #pragma unroll
@@ -1700,7 +1739,7 @@ __device__ walk_out bk_walk_sorted(const uint32_t* vals, uint32_t n, float& s, f
 
 // Last level: all n values share bits 31..8 (`prefix`); count each of the 256
 // possible values and add them as repeated terms, largest first.
-__device__ walk_out bk_walk_counts(const uint32_t* vals, uint32_t n, uint32_t prefix, float& s, float thresh,
+__device__ __forceinline__ walk_out bk_walk_counts(const uint32_t* vals, uint32_t n, uint32_t prefix, float& s, float thresh,
                                    big_shared& sh) {
     uint32_t* cc = sh.sortbuf;  // per (value, copy) counts
     for (int i = threadIdx.x; i < 256 * BK_NC; i += ZS_BIG_NT) cc[i] = 0;
@@ -1748,17 +1787,20 @@ __device__ __forceinline__ uint32_t bk_rank(uint32_t v) {
 }
 
 template <int L>
-__device__ walk_out bk_exact(const uint32_t* vals, uint32_t n, float& s, float thresh, uint32_t* tmp, big_shared& sh);
+__device__ __forceinline__ walk_out bk_exact(const uint32_t* vals, uint32_t n, float& s, float thresh, uint32_t* tmp, big_shared& sh);
 
 // Walk vals[from, to), laid out bucket by bucket (level L, starts in `start`),
 // from running sum s. The values of a bucket are in any order.
 template <int L>
-__device__ walk_out bk_walk(const uint32_t* vals, uint32_t from, uint32_t to, const uint32_t* start, float& s,
+__device__ __forceinline__ walk_out bk_walk(const uint32_t* vals, uint32_t from, uint32_t to, const uint32_t* start, float& s,
                             float thresh, uint32_t* tmp, big_shared& sh) {
     walk_out o = {false, 0u, 0u};
     uint32_t pos = from;
     float s_bstart = s;  // running sum at the start of the bucket open at pos
     while (pos < to) {
+#ifdef ZS_DEBUG_WALK
+        long long cf0 = clock64();
+#endif
         float tv[4];
 #pragma unroll
         for (int q = 0; q < 4; q++) {
@@ -1767,8 +1809,14 @@ __device__ walk_out bk_walk(const uint32_t* vals, uint32_t from, uint32_t to, co
         }
         uint32_t excl[4];
         seq_find_res F = seq_find<ZS_BIG_NT, 4>(seq_terms<4>(tv), 0, s, thresh, excl, sh.q);
+#ifdef ZS_DEBUG_WALK
+        WALK_COUNT(1, clock64() - cf0);
+#endif
         const int first = min(min(F.ev, F.st), F.tie);
         WALK_COUNT(2, 1); WALK_COUNT(3, F.tie < min(F.ev, F.st) ? 1 : 0); WALK_COUNT(4, F.ev < F.st ? 1 : 0);
+#ifdef ZS_DEBUG_WALK
+        long long cw0 = clock64();
+#endif
         if (first == ZS_BIGI) {
             const uint32_t last = min(pos + ZS_BIG_G, to) - 1;
             const uint32_t bst = start[bk_rank<L>(vals[last])];
@@ -1783,6 +1831,9 @@ __device__ walk_out bk_walk(const uint32_t* vals, uint32_t from, uint32_t to, co
         if (bst >= pos) s = seq_value_at<ZS_BIG_NT, 4>(F, excl, (int)(bst - pos), sh.q);
         else s = s_bstart;
         o = bk_exact<L + 1>(vals + bst, bend - bst, s, thresh, tmp, sh);
+#ifdef ZS_DEBUG_WALK
+        WALK_COUNT(5, clock64() - cw0);
+#endif
         if (o.stopped) return o;
         s_bstart = s;
         pos = bend;
@@ -1793,7 +1844,7 @@ __device__ walk_out bk_walk(const uint32_t* vals, uint32_t from, uint32_t to, co
 // Exact descending walk of one bucket of level L-1 (its values share the
 // bucket's high bits).
 template <int L>
-__device__ walk_out bk_exact(const uint32_t* vals, uint32_t n, float& s, float thresh, uint32_t* tmp, big_shared& sh) {
+__device__ __forceinline__ walk_out bk_exact(const uint32_t* vals, uint32_t n, float& s, float thresh, uint32_t* tmp, big_shared& sh) {
     if (n <= ZS_SORT_CAP) return bk_walk_sorted(vals, n, s, thresh, sh);
     if constexpr (L >= 2) {
         return bk_walk_counts(vals, n, vals[0] & ~255u, s, thresh, sh);
@@ -2134,7 +2185,14 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
             __threadfence_block();
             __syncthreads();
             const uint32_t upto = sh.hist[rhi + 1];
+#ifdef ZS_DEBUG_WALK
+            long long cg = clock64();
+            WALK_COUNT(6, 1);
+#endif
             wo = bk_walk<0>(gv, done, upto, sh.hist, s, P.top_p, tmp, sh);
+#ifdef ZS_DEBUG_WALK
+            WALK_COUNT(7, clock64() - cg);
+#endif
             done = upto;
         }
         BIG_MARK();
@@ -2199,6 +2257,10 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
                 acc = wave_sum_d(acc);
                 if (zs_lane() == 0) ap[j] = acc;
             }
+#ifdef ZS_DEBUG_WALK
+            if (t == 0) printf("walk row %u peak %d nk %u sorts %llu sorted %llu finds %llu tiefirst %llu evfirst %llu exactclk %llu rounds %llu walkclk %llu\n", r, (int)peak, nk,
+                               zs_dbg_walk[r][0], zs_dbg_walk[r][1], zs_dbg_walk[r][2], zs_dbg_walk[r][3], zs_dbg_walk[r][4], zs_dbg_walk[r][5], zs_dbg_walk[r][6], zs_dbg_walk[r][7]);
+#endif
             if (t == 0) {
                 a.rst[r].klist = 1;
                 a.rst[r].nk = nk;
