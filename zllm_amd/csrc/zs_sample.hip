@@ -195,7 +195,13 @@ __global__ __launch_bounds__(ZS_PREP_NT) void zs_k_prep(zs_sargs a) {
 
 #define P1_SUP 1024
 #define P1_SORT 256
+struct p1_red {
+    float omax, zmax;
+    uint32_t fl, zfin, zabove, xabove;
+    int last_nan;
+};
 struct p1_shared {
+    p1_red red[ZS_P1_NT / 64];
     uint32_t hist[256];
     uint32_t u[8];
     int i[8];
@@ -214,11 +220,10 @@ struct p1_shared {
 // Exact top-K (key desc, index asc) of the chunk's valid keys; writes the
 // candidates (unordered) to out_key/out_idx. Element e = j*4+q of thread t has
 // index base + (j*256 + t)*4 + q.
-__device__ __forceinline__ void p1_topk(const uint32_t (&key)[P1_EPT], uint32_t vmask, uint32_t K, uint32_t base,
-                        uint32_t* out_key, uint32_t* out_idx, uint32_t* n_out, uint32_t* kth,
+__device__ __forceinline__ void p1_topk(const uint32_t (&key)[P1_EPT], uint32_t vmask, uint32_t nvalid, uint32_t K,
+                        uint32_t base, uint32_t* out_key, uint32_t* out_idx, uint32_t* n_out, uint32_t* kth,
                         uint32_t* full, p1_shared& sh) {
     const int t = threadIdx.x;
-    uint32_t nvalid = block_sum_u<ZS_P1_NT>(__popc(vmask), sh.u);
     if (t == 0) sh.cnt = 0;
     __syncthreads();
     if (nvalid <= K) {
@@ -335,7 +340,10 @@ __device__ __forceinline__ void p1_topk(const uint32_t (&key)[P1_EPT], uint32_t 
 // one wave for up to 64 of them, the workgroup for up to P1_SORT -- and the
 // first K are the answer. Degenerate chunks (larger supersets) use the LDS
 // radix select.
-__device__ __forceinline__ void p1_topk_fast(const uint32_t (&key)[P1_EPT], uint32_t vmask, uint32_t K, uint32_t base,
+// nvalid: valid elements of the chunk; nfin: valid elements whose key is above
+// that of -inf.
+__device__ __forceinline__ void p1_topk_fast(const uint32_t (&key)[P1_EPT], uint32_t vmask, uint32_t nvalid,
+                             uint32_t nfin, uint32_t K, uint32_t base,
                              uint32_t* out_key, uint32_t* out_idx, uint32_t* n_out, uint32_t* kth,
                              uint32_t* full, p1_shared& sh) {
     const int t = threadIdx.x;
@@ -343,19 +351,14 @@ __device__ __forceinline__ void p1_topk_fast(const uint32_t (&key)[P1_EPT], uint
 #pragma unroll
     for (int e = 0; e < P1_EPT; e++)
         if ((vmask >> e) & 1u) tm = max(tm, key[e]);
-    uint32_t nvalid = block_sum_u<ZS_P1_NT>(__popc(vmask), sh.u);
     const uint32_t c = (K + (ZS_P1_NT / 64) - 1) / (ZS_P1_NT / 64);
     if (nvalid <= K || c > 64) {
-        p1_topk(key, vmask, K, base, out_key, out_idx, n_out, kth, full, sh);
+        p1_topk(key, vmask, nvalid, K, base, out_key, out_idx, n_out, kth, full, sh);
         return;
     }
     // Fewer than K values above -inf (a masked chunk): all of them plus the
     // lowest-index -inf elements make the top-K.
     const uint32_t kninf = zs_total_key(-INFINITY);
-    uint32_t myfin = 0;
-#pragma unroll
-    for (int e = 0; e < P1_EPT; e++) myfin += (((vmask >> e) & 1u) && key[e] > kninf) ? 1u : 0u;
-    const uint32_t nfin = block_sum_u<ZS_P1_NT>(myfin, sh.u);
     if (nfin < K) {
         if (t == 0) sh.cnt = 0;
         __syncthreads();
@@ -401,26 +404,50 @@ __device__ __forceinline__ void p1_topk_fast(const uint32_t (&key)[P1_EPT], uint
         __syncthreads();
         return;
     }
-    // theta: a lower bound of the K-th largest key -- the c-th largest thread
-    // maximum of every wave (c * 4 >= K elements at or above the smallest of
-    // them), or one wave's K-th largest thread maximum; threads without
-    // elements hold key 0, below every element
+    // theta: a lower bound of the K-th largest key. Thread maxima belong to
+    // distinct elements, so the K-th largest of the workgroup's 256 thread
+    // maxima has at least K elements at or above it. Each wave sorts its 64;
+    // for K <= 64 wave 0 merges the four sorted lists (elementwise max of an
+    // ascending and a descending list keeps the larger half as a bitonic
+    // sequence, which six exchange steps sort). For K > 64: the c-th largest
+    // thread maximum of every wave, c = ceil(K / 4), and their minimum.
+    // Threads without elements hold key 0, below every element.
+    const int lane = zs_lane();
     const uint32_t srt = wave_sort_u32(tm);
-    const uint32_t thw = __shfl(srt, 64 - (int)c, 64);
-    const uint32_t thk = K <= 64 ? __shfl(srt, 64 - (int)K, 64) : 0u;
-    if (zs_lane() == 0) { sh.sel[zs_wid()] = thw; sh.hist[zs_wid()] = thk; }
-    __syncthreads();
-    uint32_t theta = sh.sel[0], theta2 = sh.hist[0];
+    uint32_t theta;
+    if (K <= 64) {
+        sh.tmax[zs_wid() * 64 + lane] = srt;
+        __syncthreads();
+        if (t < 64) {
+            uint32_t m = srt;
 #pragma unroll
-    for (int w = 1; w < ZS_P1_NT / 64; w++) { theta = min(theta, sh.sel[w]); theta2 = max(theta2, sh.hist[w]); }
-    theta = max(theta, theta2);
+            for (int w = 1; w < ZS_P1_NT / 64; w++) {
+                m = max(m, sh.tmax[w * 64 + 63 - lane]);
+#pragma unroll
+                for (int j = 32; j > 0; j >>= 1) {
+                    const uint32_t o = __shfl_xor(m, j, 64);
+                    m = (lane & j) ? max(m, o) : min(m, o);
+                }
+            }
+            if (lane == 64 - (int)K) sh.sel[0] = m;
+        }
+        __syncthreads();
+        theta = sh.sel[0];
+    } else {
+        const uint32_t thw = __shfl(srt, 64 - (int)c, 64);
+        if (lane == 0) sh.sel[zs_wid()] = thw;
+        __syncthreads();
+        theta = sh.sel[0];
+#pragma unroll
+        for (int w = 1; w < ZS_P1_NT / 64; w++) theta = min(theta, sh.sel[w]);
+    }
     uint32_t cnt = 0;
 #pragma unroll
     for (int e = 0; e < P1_EPT; e++) cnt += (((vmask >> e) & 1u) && key[e] >= theta) ? 1u : 0u;
     uint32_t nsup;
     uint32_t pos = block_excl_scan_u<ZS_P1_NT>(cnt, sh.u, &nsup);
     if (nsup > P1_SORT) {
-        p1_topk(key, vmask, K, base, out_key, out_idx, n_out, kth, full, sh);
+        p1_topk(key, vmask, nvalid, K, base, out_key, out_idx, n_out, kth, full, sh);
         return;
     }
     // composite ((~key) << 32 | index): ascending order = key desc, index asc
@@ -561,35 +588,53 @@ __global__ __launch_bounds__(ZS_P1_NT) void zs_k_pass1(zs_sargs a) {
 #pragma unroll
     for (int e = 0; e < P1_EPT; e++) zv[e] = zs_temper(zv[e], T);
 
-    // ---- observers over x~
-    float omax = -INFINITY;
-    uint32_t fl = 0;
+    // ---- chunk statistics of x~ (observers) and z (sampler), one workgroup
+    // reduction: maxima, NaN / +inf flags, the last NaN of z, and counts of
+    // finite z and of elements whose key is above that of -inf for the lists
+    static_assert(ZS_P1_NT == 256, "four waves per pass-1 workgroup");
+    const uint32_t kninf = zs_total_key(-INFINITY);
+    float omax = -INFINITY, zmax = -INFINITY;
+    uint32_t fl = 0, zfin = 0, zabove = 0, xabove = 0;
+    int last_nan = -1;
 #pragma unroll
     for (int e = 0; e < P1_EPT; e++) {
         if (!((vmask >> e) & 1u)) continue;
-        float x = xo[e];
+        const float x = xo[e], z = zv[e];
         if (x != x) fl |= ZS_CF_OBS_NAN;
         omax = fmaxf(omax, x);
-    }
-    omax = block_max_f<ZS_P1_NT>(omax, sh.f);
-
-    // ---- sampler over z
-    float zmax = -INFINITY;
-    uint32_t zfin = 0;
-    int last_nan = -1;
-    for (int e = 0; e < P1_EPT; e++) {
-        if (!((vmask >> e) & 1u)) continue;
-        float z = zv[e];
-        uint32_t idx = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
+        xabove += zs_total_key(x) > kninf ? 1u : 0u;
+        const uint32_t idx = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
         if (z != z) { fl |= ZS_CF_Z_NAN; last_nan = max(last_nan, (int)idx); }
         else if (z == INFINITY) fl |= ZS_CF_Z_PINF;
-        if (z == z && z > -INFINITY) zfin++;
+        zfin += (z == z && z > -INFINITY) ? 1u : 0u;
+        zabove += zs_total_key(z) > kninf ? 1u : 0u;
         zmax = fmaxf(zmax, z);
     }
-    zmax = block_max_f<ZS_P1_NT>(zmax, sh.f);
-    zfin = block_sum_u<ZS_P1_NT>(zfin, sh.u);
-    last_nan = block_max_i<ZS_P1_NT>(last_nan, sh.i);
-    fl = block_or_u<ZS_P1_NT>(fl, sh.u);
+    for (int d = 32; d > 0; d >>= 1) {
+        omax = fmaxf(omax, __shfl_xor(omax, d, 64));
+        zmax = fmaxf(zmax, __shfl_xor(zmax, d, 64));
+        fl |= __shfl_xor(fl, d, 64);
+        zfin += __shfl_xor(zfin, d, 64);
+        zabove += __shfl_xor(zabove, d, 64);
+        xabove += __shfl_xor(xabove, d, 64);
+        last_nan = max(last_nan, __shfl_xor(last_nan, d, 64));
+    }
+    if (zs_lane() == 0) {
+        p1_red& R = sh.red[zs_wid()];
+        R.omax = omax; R.zmax = zmax; R.fl = fl; R.zfin = zfin;
+        R.zabove = zabove; R.xabove = xabove; R.last_nan = last_nan;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < ZS_P1_NT / 64; w++) {
+        const p1_red& R = sh.red[w];
+        omax = fmaxf(omax, R.omax); zmax = fmaxf(zmax, R.zmax); fl |= R.fl;
+        last_nan = max(last_nan, R.last_nan);
+    }
+    zfin = sh.red[0].zfin + sh.red[1].zfin + sh.red[2].zfin + sh.red[3].zfin;
+    zabove = sh.red[0].zabove + sh.red[1].zabove + sh.red[2].zabove + sh.red[3].zabove;
+    xabove = sh.red[0].xabove + sh.red[1].xabove + sh.red[2].xabove + sh.red[3].xabove;
+    const uint32_t nvalid = min((uint32_t)ZS_P1_CH, V - base);
     // greedy: argmax-last (ties -> larger index) over all, and over the tail
     // after the chunk's last NaN. Encode (value key, index) so that a max over
     // 64-bit composites picks the larger value, then the larger index.
@@ -703,7 +748,7 @@ __global__ __launch_bounds__(ZS_P1_NT) void zs_k_pass1(zs_sargs a) {
             p1_finite(key, zv, vmask, base, a.cs_key + lofs * ZS_KS, a.cs_idx + lofs * ZS_KS, sh);
             ns = zfin;
         } else if (has_topk && P.top_k <= ZS_KS) {
-            p1_topk_fast(key, vmask, Ks, base, a.cs_key + lofs * ZS_KS, a.cs_idx + lofs * ZS_KS, &ns, &s_kth,
+            p1_topk_fast(key, vmask, nvalid, zabove, Ks, base, a.cs_key + lofs * ZS_KS, a.cs_idx + lofs * ZS_KS, &ns, &s_kth,
                          &s_full, sh);
         }
     }
@@ -715,7 +760,7 @@ __global__ __launch_bounds__(ZS_P1_NT) void zs_k_pass1(zs_sargs a) {
     uint32_t no, o_kth, o_full;
     no = o_kth = o_full = 0;
     if (P.flags & (ZS_ROW_LOGPROBS | ZS_ROW_UNCERTAINTY))
-        p1_topk_fast(key, vmask, Ko, base, a.co_key + lofs * ZS_KO, a.co_idx + lofs * ZS_KO, &no, &o_kth,
+        p1_topk_fast(key, vmask, nvalid, xabove, Ko, base, a.co_key + lofs * ZS_KO, a.co_idx + lofs * ZS_KO, &no, &o_kth,
                      &o_full, sh);
 
     if (t == 0) {
