@@ -191,7 +191,7 @@ __global__ __launch_bounds__(ZS_PREP_NT) void zs_k_prep(zs_sargs a) {
 // ===========================================================================
 // zs_k_pass1
 // ===========================================================================
-#define P1_EPT 32
+#define P1_EPT (ZS_P1_CH / ZS_P1_NT)
 
 #define P1_SUP 1024
 #define P1_SORT 256
@@ -244,7 +244,7 @@ __device__ __forceinline__ void p1_topk(const uint32_t (&key)[P1_EPT], uint32_t 
     }
     uint32_t prefix = 0, mask = 0, need = K;
     for (int shift = 24; shift >= 0; shift -= 8) {
-        sh.hist[t] = 0;  // 256 threads == 256 bins
+        if (t < 256) sh.hist[t] = 0;
         __syncthreads();
         for (int e = 0; e < P1_EPT; e++)
             if (((vmask >> e) & 1u) && (key[e] & mask) == prefix)
@@ -570,7 +570,7 @@ __global__ __launch_bounds__(ZS_P1_NT) void zs_k_pass1(zs_sargs a) {
         const float* py = a.p_y + (size_t)r * ZS_MAX_PATCHES;
         for (uint32_t p = sh.pcur0; p < sh.pcur1; p++) {
             uint32_t off = pid[p] - base;
-            uint32_t q = off & 3, tt = (off >> 2) % ZS_P1_NT, j = off >> 10;
+            uint32_t q = off & 3, tt = (off >> 2) % ZS_P1_NT, j = (off >> 2) / ZS_P1_NT;
             if ((int)tt == t) {
 #pragma unroll
                 for (int jj = 0; jj < P1_EPT / 4; jj++)
@@ -591,7 +591,6 @@ __global__ __launch_bounds__(ZS_P1_NT) void zs_k_pass1(zs_sargs a) {
     // ---- chunk statistics of x~ (observers) and z (sampler), one workgroup
     // reduction: maxima, NaN / +inf flags, the last NaN of z, and counts of
     // finite z and of elements whose key is above that of -inf for the lists
-    static_assert(ZS_P1_NT == 256, "four waves per pass-1 workgroup");
     const uint32_t kninf = zs_total_key(-INFINITY);
     float omax = -INFINITY, zmax = -INFINITY;
     uint32_t fl = 0, zfin = 0, zabove = 0, xabove = 0;
@@ -631,32 +630,35 @@ __global__ __launch_bounds__(ZS_P1_NT) void zs_k_pass1(zs_sargs a) {
         omax = fmaxf(omax, R.omax); zmax = fmaxf(zmax, R.zmax); fl |= R.fl;
         last_nan = max(last_nan, R.last_nan);
     }
-    zfin = sh.red[0].zfin + sh.red[1].zfin + sh.red[2].zfin + sh.red[3].zfin;
-    zabove = sh.red[0].zabove + sh.red[1].zabove + sh.red[2].zabove + sh.red[3].zabove;
-    xabove = sh.red[0].xabove + sh.red[1].xabove + sh.red[2].xabove + sh.red[3].xabove;
+    zfin = zabove = xabove = 0;
+#pragma unroll
+    for (int w = 0; w < ZS_P1_NT / 64; w++) {
+        zfin += sh.red[w].zfin; zabove += sh.red[w].zabove; xabove += sh.red[w].xabove;
+    }
     const uint32_t nvalid = min((uint32_t)ZS_P1_CH, V - base);
     // greedy: argmax-last (ties -> larger index) over all, and over the tail
-    // after the chunk's last NaN. Encode (value key, index) so that a max over
-    // 64-bit composites picks the larger value, then the larger index.
+    // after the chunk's last NaN (the whole chunk when it has no NaN). A pair
+    // (value key, index + 1) compares by key, then by index; 0 = none.
     unsigned long long best_all = 0, best_tail = 0;
     int tail_n = 0;
     if (T <= 0.0f) {  // greedy rows only (uniform per workgroup)
-    for (int e = 0; e < P1_EPT; e++) {
-        if (!((vmask >> e) & 1u)) continue;
-        float z = zv[e];
-        if (z != z) continue;
-        uint32_t idx = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
-        // -0.0 and +0.0 compare equal in the reference (partial_cmp): map both to +0
-        float zz = (z == 0.0f) ? 0.0f : z;
-        unsigned long long comp = ((unsigned long long)zs_total_key(zz) << 32) | (idx + 1);
-        if (comp > best_all) best_all = comp;
-        if ((int)idx > last_nan) {
-            tail_n++;
-            if (comp > best_tail) best_tail = comp;
+        uint32_t bk = 0, bi = 0, tk = 0, ti = 0;
+        uint32_t tn = 0;
+#pragma unroll
+        for (int e = 0; e < P1_EPT; e++) {
+            const float z = zv[e];
+            if (!((vmask >> e) & 1u) || z != z) continue;
+            const uint32_t idx = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
+            // -0.0 and +0.0 compare equal in the reference (partial_cmp): map both to +0
+            const uint32_t k = zs_total_key(z == 0.0f ? 0.0f : z);
+            if (k >= bk) { bk = k; bi = idx + 1; }  // ids ascend with e: ties -> later
+            if ((int)idx > last_nan) {
+                tn++;
+                if (k >= tk) { tk = k; ti = idx + 1; }
+            }
         }
-    }
-    {
-        // block max of two u64 via the double slots
+        best_all = ((unsigned long long)bk << 32) | bi;
+        best_tail = ((unsigned long long)tk << 32) | ti;
         __shared__ unsigned long long u64sh[2][ZS_P1_NT / 64];
         for (int d = 32; d > 0; d >>= 1) {
             unsigned long long o1 = __shfl_xor(best_all, d, 64);
@@ -671,28 +673,34 @@ __global__ __launch_bounds__(ZS_P1_NT) void zs_k_pass1(zs_sargs a) {
             best_tail = u64sh[1][i] > best_tail ? u64sh[1][i] : best_tail;
         }
         __syncthreads();
-    }
-    tail_n = (int)block_sum_u<ZS_P1_NT>((uint32_t)tail_n, sh.u);
+        tail_n = (int)block_sum_u<ZS_P1_NT>(tn, sh.u);
     }
 
     // ---- approximate moments per 1024-logit sub-chunk (predictions for the
-    // exact-sum rounds): sub j of this chunk is the j-th float4 of every thread
+    // exact-sum rounds). Float4 j of thread t holds ids base + (j*NT + t)*4..+3,
+    // so it lies in sub-chunk j*P1_SPF + t*4/1024 of the chunk: a wave's float4
+    // row lies inside one sub-chunk, and four waves make up a sub-chunk row.
     {
+        constexpr int P1_SPF = ZS_P1_NT * 4 / ZS_SUB;  // sub-chunks per float4 row
+        constexpr int P1_J = P1_EPT / 4;
+        static_assert(P1_SPF * P1_J == ZS_SUBS_PER_CHUNK, "float4 rows tile the sub-chunks");
+        const int wid = zs_wid(), wh = (wid * 256) / ZS_SUB;
         const bool om = (P.flags & (ZS_ROW_LOGPROBS | ZS_ROW_UNCERTAINTY)) && omax > -INFINITY && omax < INFINITY;
         const bool zm = T > 0.0f && zmax > -INFINITY && zmax < INFINITY;
-        __shared__ float msh[ZS_P1_NT / 64][ZS_SUBS_PER_CHUNK][3];
-        float m1[ZS_SUBS_PER_CHUNK], md[ZS_SUBS_PER_CHUNK], mz[ZS_SUBS_PER_CHUNK];
-        // bit 2j: sub j holds the chunk's observer max, bit 2j+1: its sampler max
+        __shared__ float msh[ZS_P1_NT / 64][P1_J][3];
+        float m1[P1_J], md[P1_J], mz[P1_J];
+        // bit 2s: sub-chunk s holds the chunk's observer max, bit 2s+1: its sampler max
         uint32_t hasmax = 0;
 #pragma unroll
-        for (int j = 0; j < ZS_SUBS_PER_CHUNK; j++) {
+        for (int j = 0; j < P1_J; j++) {
             m1[j] = md[j] = mz[j] = 0.0f;
+            const int sj = j * P1_SPF + wh;
 #pragma unroll
             for (int q = 0; q < 4; q++) {
                 const int e = j * 4 + q;
                 if (!((vmask >> e) & 1u)) continue;
-                if (xo[e] == omax) hasmax |= 1u << (2 * j);
-                if (zv[e] == zmax) hasmax |= 2u << (2 * j);
+                if (xo[e] == omax) hasmax |= 1u << (2 * sj);
+                if (zv[e] == zmax) hasmax |= 2u << (2 * sj);
                 if (om) {
                     float d = xo[e] - omax;
                     if (d > -INFINITY) { float ex = __expf(d); m1[j] += ex; md[j] += d * ex; }
@@ -704,25 +712,27 @@ __global__ __launch_bounds__(ZS_P1_NT) void zs_k_pass1(zs_sargs a) {
             }
         }
 #pragma unroll
-        for (int j = 0; j < ZS_SUBS_PER_CHUNK; j++) {
+        for (int j = 0; j < P1_J; j++) {
             for (int d = 32; d > 0; d >>= 1) {
                 m1[j] += __shfl_xor(m1[j], d, 64);
                 md[j] += __shfl_xor(md[j], d, 64);
                 mz[j] += __shfl_xor(mz[j], d, 64);
             }
-            if (zs_lane() == 0) { msh[zs_wid()][j][0] = m1[j]; msh[zs_wid()][j][1] = md[j]; msh[zs_wid()][j][2] = mz[j]; }
+            if (zs_lane() == 0) { msh[wid][j][0] = m1[j]; msh[wid][j][1] = md[j]; msh[wid][j][2] = mz[j]; }
         }
         for (int d = 32; d > 0; d >>= 1) hasmax |= __shfl_xor(hasmax, d, 64);
         __shared__ uint32_t hsh[ZS_P1_NT / 64];
-        if (zs_lane() == 0) hsh[zs_wid()] = hasmax;
+        if (zs_lane() == 0) hsh[wid] = hasmax;
         __syncthreads();
         if (t < ZS_SUBS_PER_CHUNK) {
+            const int j = t / P1_SPF, h = t % P1_SPF;
             zs_sub_mom mm;
             mm.e1 = mm.ed = mm.ez = 0.0f;
             uint32_t hm = 0;
             for (int w = 0; w < ZS_P1_NT / 64; w++) {
-                mm.e1 += msh[w][t][0]; mm.ed += msh[w][t][1]; mm.ez += msh[w][t][2];
                 hm |= hsh[w];
+                if ((w * 256) / ZS_SUB != h) continue;
+                mm.e1 += msh[w][j][0]; mm.ed += msh[w][j][1]; mm.ez += msh[w][j][2];
             }
             mm.pad = zs_u2f((hm >> (2 * t)) & 3u);
             const uint32_t sub = c * ZS_SUBS_PER_CHUNK + t;

@@ -42,8 +42,9 @@ __device__ __forceinline__ float sp_z(float x, float T) { return (T > 0.0f && T 
 // fixed sequence of correctly rounded f32 operations (t = d * log2 e, t = n + f
 // with n = floor(t), 2^f by a degree-7 Taylor polynomial in fmaf Horner form,
 // exact scaling by 2^(24+n), rint), so the CPU restatement reproduces every
-// weight bit for bit; 0 below d = -17.5.
-__device__ __forceinline__ uint64_t sp_weight_of(float d) {
+// weight bit for bit; 0 below d = -17.5. For d <= 0 the weight is at most
+// 2^24 * 2^f < 2^25, so 32 of them add up in 32 bits.
+__device__ __forceinline__ uint32_t sp_weight_of(float d) {
     if (!(d >= SP_ZERO_D)) return 0;
     const float t = __fmul_rn(d, 1.44269502f);
     const float n = floorf(t);
@@ -56,9 +57,10 @@ __device__ __forceinline__ uint64_t sp_weight_of(float d) {
     p = fmaf(p, f, 2.40226507e-01f);
     p = fmaf(p, f, 6.93147182e-01f);
     p = fmaf(p, f, 1.0f);
-    return (uint64_t)rintf(ldexpf(p, 24 + (int)n));
+    return (uint32_t)rintf(ldexpf(p, 24 + (int)n));
 }
 __device__ __forceinline__ uint64_t sp_weight(float z, float m) { return sp_weight_of(z - m); }
+__device__ __forceinline__ uint32_t sp_weight32(float z, float m) { return sp_weight_of(z - m); }
 // the chunk's elements of thread t: float4 j covers ids base + (j*SP_NT + t)*4 .. +3
 __device__ __forceinline__ void sp_load(const float* row, uint32_t base, uint32_t V, float (&x)[SP_EPT]) {
 #pragma unroll
@@ -139,7 +141,7 @@ __global__ __launch_bounds__(SP_NT) void zs_k_spec_sums(zs_spec_args a) {
     const zs_spec_chunk* cs = a.cst + ((size_t)r * a.npos_max + pos) * a.nch;
     float m = -INFINITY;
     for (uint32_t i = 0; i < nch; i++) m = fmaxf(m, cs[i].zmax);
-    unsigned long long s = 0;
+    uint32_t s32 = 0;  // at most 32 weights below 2^25 each
     if (m > -INFINITY && m < INFINITY && cs[c].zmax - m >= SP_ZERO_D) {
         float x[SP_EPT];
         sp_load(sp_row(a, r, pos), base, a.V, x);
@@ -148,8 +150,9 @@ __global__ __launch_bounds__(SP_NT) void zs_k_spec_sums(zs_spec_args a) {
         const float xl = (float)(((double)m + (double)SP_ZERO_D - 0.05) * (double)(T != 1.0f ? T : 1.0f));
 #pragma unroll
         for (int e = 0; e < SP_EPT; e++)
-            if (sp_id(base, e) < a.V && x[e] >= xl) s += sp_weight(sp_z(x[e], T), m);
+            if (sp_id(base, e) < a.V && x[e] >= xl) s32 += sp_weight32(sp_z(x[e], T), m);
     }
+    unsigned long long s = s32;
     for (int d = 32; d > 0; d >>= 1) s += __shfl_xor(s, d, 64);
     if (zs_lane() == 0) sh[zs_wid()] = s;
     __syncthreads();
