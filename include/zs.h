@@ -89,6 +89,35 @@ int zs_dfa_advance(const zs_dfa* dfa, const zs_vocab* vocab, uint32_t state, uin
 int zs_dfa_mask(zs_ctx* ctx, const zs_dfa* dfa, const zs_vocab* vocab, const int32_t* d_states,
                 uint32_t B, uint32_t V, uint32_t* d_out_bits, uint32_t* d_any, void* stream);
 
+/* ---- grammar compilers (host only: no context, no GPU) -----------------
+ * Replace regex-automata's dense::Builder (logit_fsm.rs:62-88: anchored start,
+ * MatchKind::All, minimised, 24 MB limit) and the schema compiler of
+ * json_schema.rs. The DFA recognises "the whole text matches the pattern";
+ * any DFA of that language yields the reference's masks, EOS rule and
+ * advance (liveness is recomputed by zs_dfa_create). Errors go to err
+ * (NUL-terminated, truncated to errcap) and return ZS_EINVAL. */
+typedef struct zs_grammar zs_grammar;
+/* RegexEngine::compile (logit_fsm.rs:62-91): pattern (len bytes, UTF-8) to a
+ * host DFA; state 0 is dead, zs_grammar_info gives the start state. Feed
+ * zs_grammar_trans / _dead / _accept to zs_dfa_create. */
+int zs_regex_compile(const char* pattern, size_t len, zs_grammar** out, char* err, size_t errcap);
+void zs_grammar_destroy(zs_grammar* g);
+int zs_grammar_info(const zs_grammar* g, uint32_t* nstates, uint32_t* start);
+const uint32_t* zs_grammar_trans(const zs_grammar* g);  /* [nstates * 256] */
+const uint8_t* zs_grammar_accept(const zs_grammar* g);  /* [nstates] */
+const uint8_t* zs_grammar_dead(const zs_grammar* g);    /* [nstates] */
+/* json_schema.rs:78-80 schema_to_regex: the schema (JSON text) to an anchored
+ * regex. String outputs: *need = length + 1; ZS_ELIMIT (nothing written) when
+ * cap is smaller. */
+int zs_json_schema_regex(const char* schema, size_t len, char* out, size_t cap, size_t* need, char* err,
+                         size_t errcap);
+/* json_schema.rs:84-91 any_json_regex(depth) (depth capped at 32; the
+ * reference's `json:` mode uses depth 5). */
+int zs_any_json_regex(uint32_t depth, char* out, size_t cap, size_t* need);
+/* json_schema.rs:99-112 tool_call_envelope_regex over n (name, schema JSON). */
+int zs_tool_call_envelope_regex(const char* const* names, const char* const* schemas, uint32_t n,
+                                char* out, size_t cap, size_t* need, char* err, size_t errcap);
+
 /* ---- sampler ------------------------------------------------------------
  * Per-row knobs: SamplerConfig (sampler.rs:3-22) + PenaltyConfig
  * (decode_ctrl.rs:21-43) + LogprobsCollector::top_n (logprobs.rs:27, clamped

@@ -136,3 +136,54 @@ def test_large_random_dfa_through_l2():
     for i, s in enumerate(states):
         want = O.pack_bits(np.ones(V, bool)) if s < 0 else O.mask_bits(V, dfa=od, vocab=ov, state=int(s))
         assert np.array_equal(bits[i], want), (i, s)
+
+
+COMPILED = {
+    "json": "json:",
+    "tool_schema": 'json_schema:{"type":"object","properties":{"location":{"type":"string"},'
+                   '"unit":{"enum":["celsius","fahrenheit"]},"days":{"type":"array","items":{"type":"integer"},'
+                   '"maxItems":3}}}',
+    "regex": r"regex:[A-Z][a-z]*( [a-z]+)*[.!?]( [A-Z][a-z]*( [a-z]+)*[.!?])*",
+}
+
+
+@pytest.mark.parametrize("name", list(COMPILED))
+def test_compiled_grammar_masks(name):
+    """Grammars compiled by the native regex / JSON-schema compiler
+    (LogitFSM.compile): GPU masks along a constrained walk equal the oracle's,
+    bit for bit."""
+    from tests.gpu_util import ctx
+    from zllm_amd import grammar as G
+    from zllm_amd.engine import LogitFSM, TokenByteTable
+    print(f"[case] compiled {name}", flush=True)
+    g = COMPILED[name]
+    pattern = (G.any_json_regex_default() if g == "json:" else
+               G.schema_to_regex(g[len("json_schema:"):]) if g.startswith("json_schema:") else g[len("regex:"):])
+    host = G.HostDfa(pattern)
+    V = 8192
+    offs, data = synth.grammar_vocab(host.trans, host.dead, V, 17)
+    valid = np.ones(V, np.uint8)
+    valid[::211] = 0
+    eos = V - 1
+    c = ctx()
+    table = TokenByteTable.from_csr(c, offs, data, valid, eos)
+    fsm = LogitFSM.compile(g, table)
+    assert fsm.state == host.start and fsm.dfa.nstates == host.nstates
+    tokens = [None if not valid[t] else bytes(data[offs[t]:offs[t + 1]]) for t in range(V)]
+    od, ov = O.Dfa(host.trans, host.dead, host.accept), O.Vocab(tokens, eos)
+    # states along a walk that always takes an allowed token
+    rng = np.random.default_rng(5)
+    states, s = [], host.start
+    for _ in range(24):
+        states.append(s)
+        allowed, _ = O.dfa_allowed(od, ov, s)
+        ids = np.nonzero(allowed)[0]
+        if len(ids) == 0:
+            break
+        s = O.advance(od, ov, s, int(rng.choice(ids)))
+    st = torch.tensor(np.asarray(states, np.int32), device="cuda")
+    bits = fsm.dfa.mask(table, st, V)
+    torch.cuda.synchronize()
+    bits = bits.cpu().numpy().view(np.uint32)
+    for i, s in enumerate(states):
+        assert np.array_equal(bits[i], O.mask_bits(V, dfa=od, vocab=ov, state=int(s))), (name, i, s)

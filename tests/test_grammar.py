@@ -1,0 +1,382 @@
+"""Host-side grammar compilers (CPU): regex -> anchored byte DFA and JSON
+schema -> regex.
+
+The cases of json_schema.rs:312-489 and logit_fsm.rs:330-536 are restated
+with the same inputs and expectations (the reference checks them on
+regex-automata's DFA; here they run on the native one, the masks through the
+oracle's apply_mask). The DFA's language is further pinned against an
+independent engine (Python's `re.fullmatch`) on many strings, and the regex
+text of a few schemas against the reference's format strings
+(json_schema.rs:44-53, 114-268) expanded by hand."""
+import json
+import random
+import re
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from zllm_amd import grammar as G
+
+
+def accepts(schema, text):
+    return G.HostDfa(G.schema_to_regex(schema)).full_match(text)
+
+
+def rejects(schema, text):
+    return not accepts(schema, text)
+
+
+# ------------------------------------------------------------ json_schema.rs tests
+def test_primitives():  # json_schema.rs:312-323
+    assert accepts({"type": "boolean"}, "true")
+    assert accepts({"type": "boolean"}, "false")
+    assert rejects({"type": "boolean"}, "True")
+    assert accepts({"type": "integer"}, "-42")
+    assert rejects({"type": "integer"}, "4.5")
+    assert accepts({"type": "number"}, "3.14")
+    assert accepts({"type": "number"}, "-1.2e10")
+    assert accepts({"type": "null"}, "null")
+    assert accepts({"type": "string"}, '"hi"')
+    assert rejects({"type": "string"}, "hi")
+
+
+def test_string_with_escapes():  # :325-330
+    assert accepts({"type": "string"}, r'"a\"b"')
+    assert accepts({"type": "string"}, r'"tab\tend"')
+    assert accepts({"type": "string"}, '"é"')
+
+
+def test_enums():  # :332-340
+    s = {"enum": ["red", "green", "blue"]}
+    assert accepts(s, '"green"')
+    assert rejects(s, '"yellow"')
+    n = {"enum": [1, 2, 3]}
+    assert accepts(n, "2")
+    assert rejects(n, "4")
+
+
+def test_const_literal():  # :342-347
+    assert accepts({"const": "yes"}, '"yes"')
+    assert rejects({"const": "yes"}, '"no"')
+
+
+def test_simple_object():  # :349-362
+    s = {"type": "object", "properties": {"name": {"type": "string"}, "age": {"type": "integer"}}}
+    assert accepts(s, '{"name":"Ada","age":36}')
+    assert accepts(s, '{"name": "Ada", "age": 36}')
+    assert rejects(s, '{"age":36,"name":"Ada"}')
+    assert rejects(s, '{"name":"Ada"}')
+    assert rejects(s, '{"name":"Ada","age":"36"}')
+
+
+def test_nested_object_and_array():  # :364-379
+    s = {"type": "object", "properties": {
+        "tags": {"type": "array", "items": {"type": "string"}},
+        "meta": {"type": "object", "properties": {"ok": {"type": "boolean"}}}}}
+    assert accepts(s, '{"tags":["a","b"],"meta":{"ok":true}}')
+    assert accepts(s, '{"tags":[],"meta":{"ok":false}}')
+    assert rejects(s, '{"tags":[1],"meta":{"ok":true}}')
+
+
+def test_array_bounds():  # :381-388
+    s = {"type": "array", "items": {"type": "integer"}, "minItems": 2, "maxItems": 3}
+    assert rejects(s, "[1]")
+    assert accepts(s, "[1,2]")
+    assert accepts(s, "[1,2,3]")
+    assert rejects(s, "[1,2,3,4]")
+
+
+def test_enum_with_regex_meta_in_value():  # :390-397
+    s = {"enum": ["a.b", "c+d"]}
+    assert accepts(s, '"a.b"')
+    assert rejects(s, '"axb"')
+    assert accepts(s, '"c+d"')
+
+
+def test_key_with_special_chars():  # :399-404
+    s = {"type": "object", "properties": {"a.b": {"type": "integer"}}}
+    assert accepts(s, '{"a.b":1}')
+    assert rejects(s, '{"axb":1}')
+
+
+def test_unsupported_constructs_error():  # :406-412
+    for bad in ({"$ref": "#/x"}, {"anyOf": [{"type": "string"}]}, {"type": "object", "properties": {"x": {}}}, 42):
+        with pytest.raises(G.GrammarError):
+            G.schema_to_regex(bad)
+
+
+def test_bare_object_type_is_object_only():  # :414-426
+    s = {"type": "object"}
+    assert accepts(s, "{}")
+    assert accepts(s, '{"a":1}')
+    assert accepts(s, '{"a":1,"b":[true,null,"x"]}')
+    assert rejects(s, '"just a string"')
+    assert rejects(s, "42")
+    assert rejects(s, "[1,2]")
+
+
+def test_pathologically_deep_schema_is_rejected_fast():  # :428-437
+    s = {"type": "boolean"}
+    for _ in range(32 + 8):
+        s = {"type": "object", "properties": {"x": s}}
+    with pytest.raises(G.GrammarError, match="nesting exceeds 32"):
+        G.schema_to_regex(s)
+
+
+def test_any_json_value():  # :439-449
+    d = G.HostDfa(G.any_json_regex_default())
+    for ok in ["true", "-3.5", '"hi"', '{"a":1,"b":[1,2,{"c":true}]}', "[]", "{}"]:
+        assert d.full_match(ok), ok
+    assert not d.full_match("{not json")
+
+
+def test_tool_call_envelope_selects_and_constrains():  # :451-471
+    tools = [("get_weather", {"type": "object", "properties": {"city": {"type": "string"}}}),
+             ("get_time", {"type": "object", "properties": {}})]
+    d = G.HostDfa(G.tool_call_envelope_regex(tools))
+    assert d.full_match('{"name":"get_weather","arguments":{"city":"Paris"}}')
+    assert d.full_match('{"name":"get_time","arguments":{}}')
+    assert not d.full_match('{"name":"get_weather","arguments":{}}')
+    assert not d.full_match('{"name":"nope","arguments":{}}')
+    assert not d.full_match('{"arguments":{},"name":"get_time"}')
+    with pytest.raises(G.GrammarError):
+        G.tool_call_envelope_regex([])
+
+
+def test_tool_call_shape_compiles():  # :473-488
+    s = {"type": "object", "properties": {"location": {"type": "string"},
+                                          "unit": {"enum": ["celsius", "fahrenheit"]}}}
+    assert accepts(s, '{"location":"Paris","unit":"celsius"}')
+    assert rejects(s, '{"location":"Paris","unit":"kelvin"}')
+
+
+# ------------------------------------------------------------ regex text of the compiler
+SP = " ?"
+STRING = r'"([^"\\]|\\(["\\/bfnrt]|u[0-9a-fA-F]{4}))*"'
+INTEGER = r"-?(0|[1-9][0-9]*)"
+
+
+def test_schema_regex_text():
+    """The reference's format strings (json_schema.rs:44-53, 177-268) expanded
+    by hand for a few schemas."""
+    assert G.schema_to_regex({"type": "string"}) == STRING
+    assert G.schema_to_regex({"type": "integer"}) == INTEGER
+    assert G.schema_to_regex({"type": "number"}) == r"-?(0|[1-9][0-9]*)(\.[0-9]+)?([eE][+-]?[0-9]+)?"
+    assert G.schema_to_regex({"type": "boolean"}) == "(true|false)"
+    assert G.schema_to_regex({"type": "null"}) == "null"
+    assert G.schema_to_regex({"type": "string", "pattern": "[a-z]+"}) == '"[a-z]+"'
+    obj = {"type": "object", "properties": {"name": {"type": "string"}, "age": {"type": "integer"}}}
+    assert G.schema_to_regex(obj) == (r"\{" + SP + '"name"' + SP + ":" + SP + STRING + SP + "," + SP + '"age"' + SP
+                                      + ":" + SP + INTEGER + SP + r"\}")
+    assert G.schema_to_regex({"type": "object", "properties": {}}) == r"\{" + SP + r"\}"
+    sep = SP + "," + SP
+    arr = {"type": "array", "items": {"type": "integer"}, "minItems": 2, "maxItems": 3}
+    two, three = INTEGER + sep + INTEGER, INTEGER + sep + INTEGER + sep + INTEGER
+    assert G.schema_to_regex(arr) == r"\[" + SP + "(" + two + "|" + three + ")" + SP + r"\]"
+    assert G.schema_to_regex({"type": "array", "items": {"type": "integer"}}) == \
+        r"\[" + SP + "(" + INTEGER + "(" + sep + INTEGER + ")*)?" + SP + r"\]"
+    assert G.schema_to_regex({"type": "array", "items": {"type": "integer"}, "minItems": 2}) == \
+        r"\[" + SP + two + "(" + sep + INTEGER + ")*" + SP + r"\]"
+    assert G.schema_to_regex({"type": "array", "items": {"type": "integer"}, "maxItems": 2}) == \
+        r"\[" + SP + "((" + INTEGER + "|" + two + "))?" + SP + r"\]"
+    assert G.schema_to_regex({"type": "array", "items": {"type": "integer"}, "maxItems": 0}) == \
+        r"\[" + SP + r"\]"
+    with pytest.raises(G.GrammarError, match="maxItems < minItems"):
+        G.schema_to_regex({"type": "array", "items": {"type": "integer"}, "minItems": 3, "maxItems": 2})
+    with pytest.raises(G.GrammarError, match="needs \"items\""):
+        G.schema_to_regex({"type": "array"})
+    # any_value(0): the four primitive shapes
+    assert G.any_json_regex(0) == "(" + "|".join([STRING, r"-?(0|[1-9][0-9]*)(\.[0-9]+)?([eE][+-]?[0-9]+)?",
+                                                  "(true|false)", "null"]) + ")"
+
+
+def test_schema_declaration_order_and_duplicate_keys():
+    """preserve_order (Cargo.toml:34): declaration order; a repeated key keeps
+    its first position with the last value."""
+    text = '{"type":"object","properties":{"b":{"type":"integer"},"a":{"type":"null"},"b":{"type":"boolean"}}}'
+    d = G.HostDfa(G.schema_to_regex(text))
+    assert d.full_match('{"b":true,"a":null}')
+    assert not d.full_match('{"b":1,"a":null}')
+    assert not d.full_match('{"a":null,"b":true}')
+
+
+@pytest.mark.parametrize("value,text", [
+    (100, "100"), (100.0, "100.0"), (1.5, "1.5"), (1e20, "1e20"), (1e16, "1e16"), (1e15, "1000000000000000.0"),
+    (0.0001, "0.0001"), (1e-5, "0.00001"), (1e-6, "1e-6"), (1.25e-7, "1.25e-7"), (-2.5, "-2.5"), (123456.789, "123456.789"),
+    ("a\nb", '"a\\nb"'), ("q\"x", '"q\\"x"'), ("\x01", '"\\u0001"'), ("é", '"é"'), (True, "true"), (None, "null"),
+    ([1, "x"], '[1,"x"]'), ({"k": [None]}, '{"k":[null]}'),
+])
+def test_literal_serialisation(value, text):
+    """const / enum literals are serde_json's compact output, regex-escaped
+    (json_schema.rs:70-73): float layout of ryu, string escapes of serde_json."""
+    d = G.HostDfa(G.schema_to_regex({"const": value}))
+    assert d.full_match(text), G.schema_to_regex({"const": value})
+
+
+def test_negative_zero_literal():
+    # serde_json reads "-0" as the float -0.0 and writes it back as "-0.0"
+    d = G.HostDfa(G.schema_to_regex('{"const": -0}'))
+    assert d.full_match("-0.0") and not d.full_match("0") and not d.full_match("-0")
+
+
+def test_invalid_schema_json_is_an_error():
+    for bad in ["{not json}", '{"type": "string",}', '{"type": "string"} x', '"\\ud800"']:
+        with pytest.raises(G.GrammarError):
+            G.schema_to_regex(bad)
+
+
+# ------------------------------------------------------------ regex compiler
+def test_bad_patterns_are_errors():  # logit_fsm.rs:418-421 and the parser's own cases
+    for bad in ["a(", "a)", "*a", "a{2,1}", "[a", "(?z)", "\\b", "\\1", "a{", "[z-a]"]:
+        with pytest.raises(G.GrammarError):
+            G.HostDfa(bad)
+
+
+def test_size_limit_is_an_error():
+    # (a|b)*a(a|b){n}: the DFA needs 2^(n+1) states
+    with pytest.raises(G.GrammarError, match="size limit"):
+        G.HostDfa("(a|b)*a(a|b){20}")
+
+
+def test_dfa_is_minimal_and_dead_is_the_only_non_live_state():
+    d = G.HostDfa("(ab|cd)*e(f|g)?")
+    dfa = O.Dfa(d.trans, d.dead, d.accept)
+    assert d.dead[0] == 1 and d.dead[1:].sum() == 0
+    assert all(dfa.live[s] for s in range(1, d.nstates))
+    # Moore equivalence over the final table: no two states merge
+    blk = d.accept.astype(np.int64) + 1
+    blk[0] = 0
+    for _ in range(d.nstates):
+        sig = {}
+        nb = np.array([sig.setdefault((blk[s],) + tuple(blk[d.trans[s]]), len(sig)) for s in range(d.nstates)])
+        if len(sig) == len(set(blk.tolist())):
+            break
+        blk = nb
+    assert len(set(blk.tolist())) == d.nstates
+
+
+PATTERNS = [
+    r"ab*c", r"ab?", r"(a|bc)*d", r"[a-c]{2,4}x?", r"(?:foo|bar)+baz", r"[^\"\\]*", r"\.\+\*\?\(\)\|\[\]\{\}\^\$",
+    r"(?i)hello", r"a.c", r"(?s)a.c", r"[0-9]+(\.[0-9]+)?", r"x{3}", r"x{2,}", r"(ab){0,2}c",
+    r"é+[à-ÿ]", r"[^a-z]", r"\x41é\U0001F600\u00e9", r"(a|)b", r"", r"a|b|", r"(?x) a b # comment",
+    r"[\d_]+", r"\D\S\W", r"[a-]+", r"[]a]+", r"[^]a]", r"^ab$", r"a^b", r"a$b", r"(a$|b)c?",
+]
+ALPHABET = ["a", "b", "c", "d", "x", "f", "o", "r", "z", "A", "H", "e", "l", "L", "O", ".", "\n", "é", "à", "ÿ",
+            "😀", "0", "5", "_", " ", '"', "\\", "]", "-", "^", "$", "+"]
+
+
+def _strings(rng, n):
+    out = [""]
+    for _ in range(n):
+        L = rng.randint(1, 7)
+        out.append("".join(rng.choice(ALPHABET) for _ in range(L)))
+    return out
+
+
+@pytest.mark.parametrize("pat", PATTERNS)
+def test_language_matches_python_re(pat):
+    """Whole-text match of the DFA agrees with re.fullmatch (an independent
+    engine) on random strings and on strings the DFA generates."""
+    d = G.HostDfa(pat)
+    py = re.compile(pat, re.ASCII if "\\d" in pat or "\\D" in pat else 0)
+    rng = random.Random(hash(pat) & 0xffff)
+    cases = _strings(rng, 400)
+    # strings accepted by the DFA, from random walks that end in an accepting state
+    for _ in range(200):
+        s, buf = d.start, bytearray()
+        for _ in range(rng.randint(0, 12)):
+            nxt = [b for b in range(256) if not d.dead[d.trans[s, b]]]
+            if not nxt:
+                break
+            b = rng.choice(nxt)
+            buf.append(b)
+            s = int(d.trans[s, b])
+        if d.accept[s]:
+            cases.append(bytes(buf).decode("utf-8"))  # accepted text is valid UTF-8
+    if "$" in pat or "^" in pat:
+        cases = [c for c in cases if "\n" not in c]  # Python's $ also matches before a final newline
+    for text in cases:
+        assert d.full_match(text) == bool(py.fullmatch(text)), (pat, text)
+
+
+def test_posix_classes():
+    d = G.HostDfa(r"[[:digit:]]+[[:^alpha:]]")
+    assert d.full_match("12-") and d.full_match("07") and not d.full_match("12a") and not d.full_match("a1")
+
+
+def test_invalid_utf8_is_rejected():
+    d = G.HostDfa(r"[^a]*")
+    assert d.full_match("é".encode("utf-8"))
+    for bad in [b"\xc3", b"\xff", b"\xed\xa0\x80", b"\xc0\xaf", b"\xf4\x90\x80\x80"]:
+        assert not d.full_match(bad)
+
+
+# ------------------------------------------------------------ logit_fsm.rs tests (masks by the oracle)
+TINY = [b"a", b"b", b"ab", b"c", None]
+EOS = 5
+
+
+def _fsm(pattern):
+    d = G.HostDfa(pattern)
+    return d, O.Dfa(d.trans, d.dead, d.accept), O.Vocab(TINY, EOS)
+
+
+def _masked(dfa, voc, state):
+    x = O.apply_mask(np.zeros(6, np.float32), dfa=dfa, vocab=voc, state=state)
+    return [bool(np.isneginf(v)) for v in x]
+
+
+def test_regex_masks_to_viable_prefixes():  # logit_fsm.rs:370-379
+    d, dfa, voc = _fsm("ab*c")
+    assert _masked(dfa, voc, d.start) == [False, True, False, True, True, True]
+
+
+def test_regex_advance_transitions_and_accepts():  # :381-396
+    d, dfa, voc = _fsm("ab*c")
+    s = O.advance(dfa, voc, d.start, 0)
+    assert _masked(dfa, voc, s) == [True, False, True, False, True, True]
+    s = O.advance(dfa, voc, s, 1)
+    s = O.advance(dfa, voc, s, 3)
+    assert _masked(dfa, voc, s) == [True, True, True, True, True, False]
+
+
+def test_regex_multibyte_token_walks_whole_surface():  # :398-406
+    d, dfa, voc = _fsm("abc")
+    s = O.advance(dfa, voc, d.start, 2)
+    assert _masked(dfa, voc, s) == [True, True, True, False, True, True]
+
+
+def test_regex_optional_suffix_allows_eos_and_continuation():  # :408-416
+    d, dfa, voc = _fsm("ab?")
+    s = O.advance(dfa, voc, d.start, 0)
+    assert _masked(dfa, voc, s) == [True, False, True, True, True, False]
+
+
+def test_regex_constrains_a_greedy_loop_end_to_end():  # :492-536
+    d, dfa, voc = _fsm("ab+c")
+    prefs = [[3, 1, 0, 2, 4, 5], [0, 2, 1, 3, 4, 5], [3, 1, 0, 2, 4, 5], [0, 1, 2, 3, 4, 5]]
+    out, s = [], d.start
+    for pref in prefs:
+        x = np.zeros(6, np.float32)
+        for rank, i in enumerate(pref):
+            x[i] = 10.0 - rank
+        x = O.apply_mask(x, dfa=dfa, vocab=voc, state=s)
+        pick = int(max(range(6), key=lambda i: (x[i], i)))
+        if pick == 5:
+            break
+        out.append(pick)
+        s = O.advance(dfa, voc, s, pick)
+    assert out == [0, 1, 3]
+
+
+def test_json_modes_compile_on_the_tiny_table():  # :430-451 (the compile step; masks need a GPU context)
+    for pattern in [G.any_json_regex_default(), G.schema_to_regex('{"type":"boolean"}')]:
+        d = G.HostDfa(pattern)
+        dfa, voc = O.Dfa(d.trans, d.dead, d.accept), O.Vocab(TINY, EOS)
+        # nothing of the tiny table starts JSON except nothing: only EOS stays open (forced stop)
+        assert _masked(dfa, voc, d.start)[:5] == [True] * 5
+
+
+def test_braced_escapes():
+    assert G.HostDfa(r"\u{1F600}\x{41}\x42").full_match("😀AB")

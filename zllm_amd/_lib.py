@@ -117,6 +117,17 @@ SIGNATURES = {
                                       C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),
     "zs_step_seed": (C.c_uint32, [C.c_uint32, C.c_uint32]),
     "zs_last_timings": (C.c_int, [C.c_void_p, C.POINTER(C.c_char_p), C.POINTER(C.c_float), C.c_int]),
+    "zs_regex_compile": (C.c_int, [C.c_char_p, C.c_size_t, C.POINTER(C.c_void_p), C.c_char_p, C.c_size_t]),
+    "zs_grammar_destroy": (None, [C.c_void_p]),
+    "zs_grammar_info": (C.c_int, [C.c_void_p, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)]),
+    "zs_grammar_trans": (C.c_void_p, [C.c_void_p]),
+    "zs_grammar_accept": (C.c_void_p, [C.c_void_p]),
+    "zs_grammar_dead": (C.c_void_p, [C.c_void_p]),
+    "zs_json_schema_regex": (C.c_int, [C.c_char_p, C.c_size_t, C.c_char_p, C.c_size_t, C.POINTER(C.c_size_t),
+                                       C.c_char_p, C.c_size_t]),
+    "zs_any_json_regex": (C.c_int, [C.c_uint32, C.c_char_p, C.c_size_t, C.POINTER(C.c_size_t)]),
+    "zs_tool_call_envelope_regex": (C.c_int, [C.POINTER(C.c_char_p), C.POINTER(C.c_char_p), C.c_uint32, C.c_char_p,
+                                              C.c_size_t, C.POINTER(C.c_size_t), C.c_char_p, C.c_size_t]),
 }
 
 _lib = None

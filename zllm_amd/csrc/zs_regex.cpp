@@ -1,0 +1,806 @@
+// zs_regex.cpp -- regex -> anchored byte DFA on the host.
+//
+// Replaces the dense DFA that logit_fsm.rs:62-88 builds with regex-automata
+// (anchored start, MatchKind::All, minimised, 24 MB size limit). Only the
+// language matters to the masks: a token is allowed iff its bytes keep the
+// text a prefix of some full match (logit_fsm.rs:166-182 with is_live
+// :121-161), and EOS needs the text itself to be a full match (:110-112), so
+// any DFA of the same language gives the same masks. The DFA here recognises
+// "the whole text matches the pattern": Thompson NFA over UTF-8 bytes, subset
+// construction over byte equivalence classes, Moore minimisation (which also
+// folds every state that cannot reach a match into the dead state 0).
+//
+// Syntax (the regex-syntax subset that patterns reach here): literals (UTF-8),
+// escapes of punctuation, \t \n \r \f \v \a, \xHH \x{H..} \uHHHH \u{H..}
+// \UHHHHHHHH, classes [..] with ranges, negation, nested classes and ASCII
+// POSIX names, the Perl classes \d \s \w (ASCII; regex-syntax uses their
+// Unicode tables), '.', groups ( ), (?: ), (?P<n> ), (?<n> ), flags
+// (?imsxU-imsxU) and (?flags: ), alternation, * + ? {n} {n,} {n,m} with lazy
+// forms (same language), and the anchors ^ $ \A \z. Case-insensitive mode
+// folds ASCII letters only.
+#include <stdint.h>
+#include <string.h>
+#include <algorithm>
+#include <string>
+#include <unordered_map>
+#include <vector>
+#include "zs_grammar.h"
+
+namespace {
+
+const uint32_t CP_MAX = 0x10FFFF;
+const uint32_t INF = 0xffffffffu;
+
+// ------------------------------------------------------------ codepoint sets
+struct CpSet {
+    std::vector<std::pair<uint32_t, uint32_t>> r;  // inclusive ranges
+    void add(uint32_t lo, uint32_t hi) { r.push_back({lo, hi}); }
+    void add(const CpSet& o) { r.insert(r.end(), o.r.begin(), o.r.end()); }
+    void canon() {
+        std::sort(r.begin(), r.end());
+        std::vector<std::pair<uint32_t, uint32_t>> o;
+        for (auto& x : r) {
+            if (!o.empty() && x.first <= o.back().second + 1) o.back().second = std::max(o.back().second, x.second);
+            else o.push_back(x);
+        }
+        r.swap(o);
+    }
+    // complement over the Unicode scalar values
+    void negate() {
+        canon();
+        std::vector<std::pair<uint32_t, uint32_t>> o;
+        uint32_t next = 0;
+        for (auto& x : r) {
+            if (x.first > next) o.push_back({next, x.first - 1});
+            next = x.second + 1;
+        }
+        if (next <= CP_MAX) o.push_back({next, CP_MAX});
+        r.swap(o);
+        remove_surrogates();
+    }
+    void remove_surrogates() {
+        std::vector<std::pair<uint32_t, uint32_t>> o;
+        for (auto& x : r) {
+            if (x.second < 0xD800 || x.first > 0xDFFF) { o.push_back(x); continue; }
+            if (x.first < 0xD800) o.push_back({x.first, 0xD7FF});
+            if (x.second > 0xDFFF) o.push_back({0xE000, x.second});
+        }
+        r.swap(o);
+    }
+    // ASCII simple case folding (case-insensitive flag)
+    void fold_ascii() {
+        std::vector<std::pair<uint32_t, uint32_t>> extra;
+        for (auto& x : r) {
+            uint32_t lo = std::max(x.first, (uint32_t)'a'), hi = std::min(x.second, (uint32_t)'z');
+            if (lo <= hi) extra.push_back({lo - 32, hi - 32});
+            lo = std::max(x.first, (uint32_t)'A');
+            hi = std::min(x.second, (uint32_t)'Z');
+            if (lo <= hi) extra.push_back({lo + 32, hi + 32});
+        }
+        r.insert(r.end(), extra.begin(), extra.end());
+    }
+};
+
+// ------------------------------------------------------------ syntax tree
+enum Kind { K_EMPTY, K_CLASS, K_CAT, K_ALT, K_REP, K_START, K_END };
+struct Node {
+    Kind k;
+    CpSet set;
+    std::vector<int> kids;
+    uint32_t mn = 0, mx = 0;
+};
+
+struct Flags {
+    bool i = false, s = false, x = false, m = false;
+};
+
+struct ParseError {
+    std::string msg;
+};
+
+class Parser {
+public:
+    Parser(const std::string& p, std::vector<Node>& ar) : p_(p), ar_(ar) {}
+    int parse() {
+        Flags f;
+        int n = parse_alt(f, 0);
+        if (pos_ < p_.size()) {
+            if (p_[pos_] == ')') fail("unopened group");
+            fail("unexpected character");
+        }
+        return n;
+    }
+
+private:
+    const std::string& p_;
+    std::vector<Node>& ar_;
+    size_t pos_ = 0;
+
+    [[noreturn]] void fail(const std::string& m) {
+        throw ParseError{m + " at offset " + std::to_string(pos_)};
+    }
+    bool eof() const { return pos_ >= p_.size(); }
+    char peek() const { return p_[pos_]; }
+    int node(Kind k) {
+        ar_.push_back(Node{});
+        ar_.back().k = k;
+        return (int)ar_.size() - 1;
+    }
+    // one UTF-8 encoded scalar of the pattern
+    uint32_t next_cp() {
+        const unsigned char c = (unsigned char)p_[pos_];
+        int n = c < 0x80 ? 1 : (c >> 5) == 6 ? 2 : (c >> 4) == 14 ? 3 : (c >> 3) == 30 ? 4 : 0;
+        if (!n || pos_ + n > p_.size()) fail("invalid UTF-8 in pattern");
+        uint32_t cp = n == 1 ? c : n == 2 ? (c & 0x1f) : n == 3 ? (c & 0x0f) : (c & 0x07);
+        for (int i = 1; i < n; i++) {
+            const unsigned char d = (unsigned char)p_[pos_ + i];
+            if ((d >> 6) != 2) fail("invalid UTF-8 in pattern");
+            cp = (cp << 6) | (d & 0x3f);
+        }
+        pos_ += n;
+        return cp;
+    }
+    void skip_verbose(const Flags& f) {
+        if (!f.x) return;
+        while (!eof()) {
+            char c = peek();
+            if (c == ' ' || c == '\t' || c == '\n' || c == '\r' || c == '\f' || c == '\v') { pos_++; continue; }
+            if (c == '#') {
+                while (!eof() && peek() != '\n') pos_++;
+                continue;
+            }
+            break;
+        }
+    }
+
+    int parse_alt(Flags& f, int depth) {
+        if (depth > 250) fail("exceeds the nesting limit");
+        std::vector<int> br;
+        br.push_back(parse_concat(f, depth));
+        while (!eof() && peek() == '|') {
+            pos_++;
+            br.push_back(parse_concat(f, depth));
+        }
+        if (br.size() == 1) return br[0];
+        int n = node(K_ALT);
+        ar_[n].kids = br;
+        return n;
+    }
+
+    int parse_concat(Flags& f, int depth) {
+        std::vector<int> items;
+        for (;;) {
+            skip_verbose(f);
+            if (eof() || peek() == '|' || peek() == ')') break;
+            const char c = peek();
+            if (c == '*' || c == '+' || c == '?' || c == '{') {
+                if (items.empty()) fail("repetition operator missing expression");
+                items.back() = parse_rep(items.back(), f);
+                continue;
+            }
+            int a = parse_atom(f, depth);
+            if (a >= 0) items.push_back(a);
+        }
+        if (items.empty()) return node(K_EMPTY);
+        if (items.size() == 1) return items[0];
+        int n = node(K_CAT);
+        ar_[n].kids = items;
+        return n;
+    }
+
+    bool parse_dec(uint32_t* v) {
+        size_t st = pos_;
+        uint64_t x = 0;
+        while (!eof() && peek() >= '0' && peek() <= '9') {
+            x = x * 10 + (uint64_t)(peek() - '0');
+            if (x > 100000) fail("repetition count too large");
+            pos_++;
+        }
+        *v = (uint32_t)x;
+        return pos_ > st;
+    }
+
+    int parse_rep(int atom, const Flags& f) {
+        uint32_t mn, mx;
+        const char c = peek();
+        pos_++;
+        if (c == '*') { mn = 0; mx = INF; }
+        else if (c == '+') { mn = 1; mx = INF; }
+        else if (c == '?') { mn = 0; mx = 1; }
+        else {
+            skip_verbose(f);
+            if (!parse_dec(&mn)) fail("repetition quantifier expects a valid decimal");
+            skip_verbose(f);
+            mx = mn;
+            if (!eof() && peek() == ',') {
+                pos_++;
+                skip_verbose(f);
+                if (!parse_dec(&mx)) mx = INF;
+                skip_verbose(f);
+            }
+            if (eof() || peek() != '}') fail("unclosed counted repetition");
+            pos_++;
+            if (mx != INF && mx < mn) fail("invalid repetition count range");
+        }
+        if (!eof() && peek() == '?') pos_++;  // lazy: same language
+        int n = node(K_REP);
+        ar_[n].kids = {atom};
+        ar_[n].mn = mn;
+        ar_[n].mx = mx;
+        return n;
+    }
+
+    int class_node(CpSet s, const Flags& f) {
+        if (f.i) s.fold_ascii();
+        s.remove_surrogates();
+        s.canon();
+        int n = node(K_CLASS);
+        ar_[n].set = s;
+        return n;
+    }
+
+    // flags like "i-sx"; returns true when the group continues with ':'
+    void parse_flags(Flags& f) {
+        bool neg = false;
+        for (;;) {
+            if (eof()) fail("unclosed group");
+            char c = peek();
+            if (c == ')' || c == ':') return;
+            pos_++;
+            switch (c) {
+                case '-': neg = true; break;
+                case 'i': f.i = !neg; break;
+                case 's': f.s = !neg; break;
+                case 'x': f.x = !neg; break;
+                case 'm': f.m = !neg; break;
+                case 'U': break;  // swaps greediness: same language
+                case 'u':
+                    if (neg) fail("Unicode mode cannot be disabled here");
+                    break;
+                case 'R': break;
+                default: fail("unrecognized flag");
+            }
+        }
+    }
+
+    int parse_atom(Flags& f, int depth) {
+        const char c = peek();
+        if (c == '(') {
+            pos_++;
+            Flags inner = f;
+            if (!eof() && peek() == '?') {
+                pos_++;
+                if (eof()) fail("unclosed group");
+                if (peek() == ':') {
+                    pos_++;
+                } else if (peek() == 'P' || peek() == '<') {
+                    if (peek() == 'P') pos_++;
+                    if (eof() || peek() != '<') fail("invalid capture group name");
+                    pos_++;
+                    size_t st = pos_;
+                    while (!eof() && peek() != '>') pos_++;
+                    if (eof() || pos_ == st) fail("invalid capture group name");
+                    pos_++;
+                } else {
+                    parse_flags(inner);
+                    if (peek() == ')') {  // (?flags): applies to the rest of the group
+                        pos_++;
+                        f = inner;
+                        return -1;
+                    }
+                    pos_++;  // ':'
+                }
+            }
+            int n = parse_alt(inner, depth + 1);
+            if (eof() || peek() != ')') fail("unclosed group");
+            pos_++;
+            return n;
+        }
+        if (c == ')') fail("unopened group");
+        if (c == '[') return class_node(parse_class(f), Flags{});  // folded inside
+        if (c == '.') {
+            pos_++;
+            CpSet s;
+            if (f.s) s.add(0, CP_MAX);
+            else { s.add(0, 9); s.add(11, CP_MAX); }
+            return class_node(s, Flags{});
+        }
+        if (c == '^' || c == '$') {
+            if (f.m) fail("multi-line anchors are not supported");
+            pos_++;
+            return node(c == '^' ? K_START : K_END);
+        }
+        if (c == '\\') {
+            pos_++;
+            if (eof()) fail("incomplete escape sequence");
+            const char e = peek();
+            if (e == 'A' || e == 'z') {
+                pos_++;
+                return node(e == 'A' ? K_START : K_END);
+            }
+            CpSet s;
+            if (perl_class(s)) return class_node(s, f);
+            const uint32_t cp = escape_cp();
+            s.add(cp, cp);
+            return class_node(s, f);
+        }
+        CpSet s;
+        uint32_t cp = next_cp();
+        s.add(cp, cp);
+        return class_node(s, f);
+    }
+
+    uint32_t hex_digits(int n_fixed) {
+        uint32_t v = 0;
+        int n = 0;
+        bool braced = !eof() && peek() == '{';
+        if (braced) pos_++;
+        while (!eof()) {
+            char c = peek();
+            int d = (c >= '0' && c <= '9') ? c - '0' : (c >= 'a' && c <= 'f') ? c - 'a' + 10
+                    : (c >= 'A' && c <= 'F') ? c - 'A' + 10 : -1;
+            if (d < 0) break;
+            v = v * 16 + (uint32_t)d;
+            if (v > CP_MAX) fail("invalid Unicode scalar value");
+            pos_++;
+            n++;
+            if (!braced && n == n_fixed) break;
+        }
+        if (braced) {
+            if (eof() || peek() != '}' || n == 0) fail("invalid hexadecimal escape");
+            pos_++;
+        } else if (n != n_fixed) {
+            fail("invalid hexadecimal escape");
+        }
+        if (v >= 0xD800 && v <= 0xDFFF) fail("invalid Unicode scalar value");
+        return v;
+    }
+
+    // the scalar denoted by an escape (pos_ at the character after '\')
+    uint32_t escape_cp() {
+        const char e = peek();
+        pos_++;
+        switch (e) {
+            case 'n': return '\n';
+            case 't': return '\t';
+            case 'r': return '\r';
+            case 'f': return 0x0C;
+            case 'v': return 0x0B;
+            case 'a': return 0x07;
+            case 'x': return hex_digits(2);
+            case 'u': return hex_digits(4);
+            case 'U': return hex_digits(8);
+            default: break;
+        }
+        const unsigned char u = (unsigned char)e;
+        if (u < 0x80 && !((e >= '0' && e <= '9') || (e >= 'a' && e <= 'z') || (e >= 'A' && e <= 'Z')))
+            return u;  // escaped punctuation or space
+        pos_--;
+        if (e == 'b' || e == 'B' || e == '<' || e == '>') fail("word boundary assertions are not supported");
+        if (e == 'p' || e == 'P') fail("Unicode property classes are not supported");
+        if (e >= '0' && e <= '9') fail("backreferences are not supported");
+        fail("unrecognized escape sequence");
+    }
+
+    // \d \D \s \S \w \W (ASCII); pos_ at the letter
+    bool perl_class(CpSet& s) {
+        const char e = peek();
+        CpSet b;
+        if (e == 'd' || e == 'D') b.add('0', '9');
+        else if (e == 's' || e == 'S') { b.add('\t', '\r'); b.add(' ', ' '); }
+        else if (e == 'w' || e == 'W') { b.add('0', '9'); b.add('A', 'Z'); b.add('_', '_'); b.add('a', 'z'); }
+        else return false;
+        pos_++;
+        if (e == 'D' || e == 'S' || e == 'W') b.negate();
+        s.add(b);
+        return true;
+    }
+
+    bool posix_class(CpSet& s) {
+        // pos_ at "[:"
+        size_t end = p_.find(":]", pos_ + 2);
+        if (end == std::string::npos) return false;
+        std::string name = p_.substr(pos_ + 2, end - pos_ - 2);
+        bool neg = !name.empty() && name[0] == '^';
+        if (neg) name = name.substr(1);
+        CpSet b;
+        if (name == "alnum") { b.add('0', '9'); b.add('A', 'Z'); b.add('a', 'z'); }
+        else if (name == "alpha") { b.add('A', 'Z'); b.add('a', 'z'); }
+        else if (name == "ascii") b.add(0, 0x7f);
+        else if (name == "blank") { b.add('\t', '\t'); b.add(' ', ' '); }
+        else if (name == "cntrl") { b.add(0, 0x1f); b.add(0x7f, 0x7f); }
+        else if (name == "digit") b.add('0', '9');
+        else if (name == "graph") b.add('!', '~');
+        else if (name == "lower") b.add('a', 'z');
+        else if (name == "print") b.add(' ', '~');
+        else if (name == "punct") { b.add('!', '/'); b.add(':', '@'); b.add('[', '`'); b.add('{', '~'); }
+        else if (name == "space") { b.add('\t', '\r'); b.add(' ', ' '); }
+        else if (name == "upper") b.add('A', 'Z');
+        else if (name == "word") { b.add('0', '9'); b.add('A', 'Z'); b.add('_', '_'); b.add('a', 'z'); }
+        else if (name == "xdigit") { b.add('0', '9'); b.add('A', 'F'); b.add('a', 'f'); }
+        else return false;
+        if (neg) b.negate();
+        s.add(b);
+        pos_ = end + 2;
+        return true;
+    }
+
+    // one class member that is a single scalar (for ranges); -1 if not
+    int64_t class_char(CpSet& into, bool* was_set) {
+        *was_set = false;
+        if (peek() == '\\') {
+            pos_++;
+            if (eof()) fail("incomplete escape sequence");
+            CpSet s;
+            if (perl_class(s)) {
+                into.add(s);
+                *was_set = true;
+                return -1;
+            }
+            return escape_cp();
+        }
+        return next_cp();
+    }
+
+    CpSet parse_class(const Flags& f) {
+        const size_t open = pos_;
+        pos_++;  // '['
+        bool neg = false;
+        if (!eof() && peek() == '^') { pos_++; neg = true; }
+        CpSet s;
+        bool first = true;
+        for (;;) {
+            if (eof()) { pos_ = open; fail("unclosed character class"); }
+            const char c = peek();
+            if (c == ']' && !first) { pos_++; break; }
+            first = false;
+            if (c == '[') {
+                if (pos_ + 1 < p_.size() && p_[pos_ + 1] == ':' && posix_class(s)) continue;
+                CpSet inner = parse_class(f);
+                s.add(inner);
+                continue;
+            }
+            if ((c == '&' || c == '-' || c == '~') && pos_ + 1 < p_.size() && p_[pos_ + 1] == c &&
+                !(c == '-' && pos_ + 2 < p_.size() && p_[pos_ + 2] == ']'))
+                fail("character class set operations are not supported");
+            bool was_set;
+            int64_t lo = class_char(s, &was_set);
+            if (was_set) continue;
+            if (!eof() && peek() == '-' && pos_ + 1 < p_.size() && p_[pos_ + 1] != ']') {
+                pos_++;
+                bool ws2;
+                CpSet dummy;
+                int64_t hi = class_char(dummy, &ws2);
+                if (ws2) fail("invalid character class range");
+                if (hi < lo) fail("invalid character class range");
+                s.add((uint32_t)lo, (uint32_t)hi);
+            } else {
+                s.add((uint32_t)lo, (uint32_t)lo);
+            }
+        }
+        if (f.i) s.fold_ascii();
+        if (neg) s.negate();
+        return s;
+    }
+};
+
+// ------------------------------------------------------------ Thompson NFA
+enum NKind : uint8_t { N_BYTE, N_SPLIT, N_EPS, N_MATCH, N_START, N_END };
+struct NState {
+    NKind k;
+    uint8_t lo, hi;
+    uint32_t a, b;
+};
+
+struct TooBig {};
+
+class NfaBuilder {
+public:
+    std::vector<NState> st;
+    explicit NfaBuilder(size_t limit) : limit_(limit) {}
+    uint32_t add(NKind k, uint32_t a = 0, uint32_t b = 0, uint8_t lo = 0, uint8_t hi = 0) {
+        if (st.size() >= limit_) throw TooBig{};
+        st.push_back(NState{k, lo, hi, a, b});
+        return (uint32_t)st.size() - 1;
+    }
+    uint32_t build(const std::vector<Node>& ar, int n, uint32_t next) {
+        const Node& nd = ar[n];
+        switch (nd.k) {
+            case K_EMPTY: return next;
+            case K_START: return add(N_START, next);
+            case K_END: return add(N_END, next);
+            case K_CLASS: return cls(nd.set, next);
+            case K_CAT: {
+                uint32_t s = next;
+                for (size_t i = nd.kids.size(); i-- > 0;) s = build(ar, nd.kids[i], s);
+                return s;
+            }
+            case K_ALT: {
+                uint32_t s = build(ar, nd.kids.back(), next);
+                for (size_t i = nd.kids.size() - 1; i-- > 0;) s = add(N_SPLIT, build(ar, nd.kids[i], next), s);
+                return s;
+            }
+            case K_REP: {
+                uint32_t s = next;
+                if (nd.mx == INF) {
+                    uint32_t loop = add(N_SPLIT, 0, next);
+                    uint32_t body = build(ar, nd.kids[0], loop);
+                    st[loop].a = body;
+                    s = loop;
+                } else {
+                    for (uint32_t i = nd.mn; i < nd.mx; i++) s = add(N_SPLIT, build(ar, nd.kids[0], s), next);
+                }
+                for (uint32_t i = 0; i < nd.mn; i++) s = build(ar, nd.kids[0], s);
+                return s;
+            }
+        }
+        return next;
+    }
+
+private:
+    size_t limit_;
+    // byte sequence [lo_i, hi_i]... then next
+    uint32_t seq(const std::vector<std::pair<uint8_t, uint8_t>>& bs, uint32_t next) {
+        uint32_t s = next;
+        for (size_t i = bs.size(); i-- > 0;) s = add(N_BYTE, s, 0, bs[i].first, bs[i].second);
+        return s;
+    }
+    static int enc(uint32_t cp, uint8_t* b) {
+        if (cp < 0x80) { b[0] = (uint8_t)cp; return 1; }
+        if (cp < 0x800) { b[0] = (uint8_t)(0xC0 | (cp >> 6)); b[1] = (uint8_t)(0x80 | (cp & 0x3f)); return 2; }
+        if (cp < 0x10000) {
+            b[0] = (uint8_t)(0xE0 | (cp >> 12)); b[1] = (uint8_t)(0x80 | ((cp >> 6) & 0x3f));
+            b[2] = (uint8_t)(0x80 | (cp & 0x3f));
+            return 3;
+        }
+        b[0] = (uint8_t)(0xF0 | (cp >> 18)); b[1] = (uint8_t)(0x80 | ((cp >> 12) & 0x3f));
+        b[2] = (uint8_t)(0x80 | ((cp >> 6) & 0x3f)); b[3] = (uint8_t)(0x80 | (cp & 0x3f));
+        return 4;
+    }
+    // split a scalar range into ranges whose UTF-8 forms are products of byte
+    // ranges (same length, differing only in a suffix of full continuation bytes)
+    void utf8_split(uint32_t lo, uint32_t hi, std::vector<std::vector<std::pair<uint8_t, uint8_t>>>& out) {
+        if (lo > hi) return;
+        static const uint32_t bounds[3] = {0x7F, 0x7FF, 0xFFFF};
+        for (uint32_t m : bounds)
+            if (lo <= m && hi > m) { utf8_split(lo, m, out); utf8_split(m + 1, hi, out); return; }
+        if (hi < 0x80) { out.push_back({{(uint8_t)lo, (uint8_t)hi}}); return; }
+        const int n = hi < 0x800 ? 2 : hi < 0x10000 ? 3 : 4;
+        for (int i = 1; i < n; i++) {
+            const uint32_t m = (1u << (6 * i)) - 1;
+            if ((lo & ~m) != (hi & ~m)) {
+                if ((lo & m) != 0) { utf8_split(lo, lo | m, out); utf8_split((lo | m) + 1, hi, out); return; }
+                if ((hi & m) != m) { utf8_split(lo, (hi & ~m) - 1, out); utf8_split(hi & ~m, hi, out); return; }
+            }
+        }
+        uint8_t a[4], b[4];
+        enc(lo, a);
+        enc(hi, b);
+        std::vector<std::pair<uint8_t, uint8_t>> v;
+        for (int i = 0; i < n; i++) v.push_back({a[i], b[i]});
+        out.push_back(v);
+    }
+    uint32_t cls(const CpSet& s, uint32_t next) {
+        std::vector<std::vector<std::pair<uint8_t, uint8_t>>> seqs;
+        for (auto& x : s.r) utf8_split(x.first, x.second, seqs);
+        if (seqs.empty()) return add(N_BYTE, next, 0, 1, 0);  // matches nothing (lo > hi)
+        uint32_t st0 = seq(seqs.back(), next);
+        for (size_t i = seqs.size() - 1; i-- > 0;) st0 = add(N_SPLIT, seq(seqs[i], next), st0);
+        return st0;
+    }
+};
+
+// ------------------------------------------------------------ subset construction
+struct VecHash {
+    size_t operator()(const std::vector<uint32_t>& v) const {
+        uint64_t h = 1469598103934665603ull;
+        for (uint32_t x : v) { h ^= x; h *= 1099511628211ull; }
+        return (size_t)h;
+    }
+};
+
+class Determinizer {
+public:
+    Determinizer(const std::vector<NState>& n, uint32_t start, size_t limit_bytes)
+        : n_(n), start_(start), limit_(limit_bytes), mark_(n.size(), 0) {}
+
+    bool run(zs_host_dfa& out, std::string& err) {
+        // byte equivalence classes from the NFA's byte ranges
+        std::vector<uint8_t> cut(257, 0);
+        for (auto& s : n_)
+            if (s.k == N_BYTE && s.lo <= s.hi) { cut[s.lo] = 1; cut[(size_t)s.hi + 1] = 1; }
+        uint8_t cls_of[256];
+        int nc = 0;
+        for (int b = 0; b < 256; b++) {
+            if (b > 0 && cut[b]) nc++;
+            cls_of[b] = (uint8_t)nc;
+        }
+        nc++;
+        std::vector<uint8_t> rep(nc);
+        for (int b = 255; b >= 0; b--) rep[cls_of[b]] = (uint8_t)b;
+        size_t stride = 1;
+        while (stride < (size_t)nc + 1) stride <<= 1;
+        const size_t max_states = limit_ / (stride * 4);
+
+        std::unordered_map<std::vector<uint32_t>, uint32_t, VecHash> ids;
+        std::vector<std::vector<uint32_t>> sets;
+        std::vector<uint8_t> acc;
+        std::vector<uint32_t> tr;  // [state][class]
+        auto intern = [&](std::vector<uint32_t>&& v, bool force_new) -> int64_t {
+            if (!force_new) {
+                auto it = ids.find(v);
+                if (it != ids.end()) return it->second;
+            }
+            if (sets.size() >= max_states) return -1;
+            uint32_t id = (uint32_t)sets.size();
+            acc.push_back(accepting(v, force_new) ? 1 : 0);
+            if (!force_new) ids.emplace(v, id);
+            sets.push_back(std::move(v));
+            return id;
+        };
+        intern(std::vector<uint32_t>{}, false);  // 0: dead (empty set)
+        std::vector<uint32_t> s0;
+        closure({start_}, true, s0);
+        intern(std::move(s0), true);  // 1: start (its closure may pass ^)
+        for (size_t i = 0; i < sets.size(); i++) {
+            tr.resize(sets.size() * nc, 0);
+            for (int c = 0; c < nc; c++) {
+                const uint8_t b = rep[c];
+                std::vector<uint32_t> tgt;
+                for (uint32_t q : sets[i]) {
+                    const NState& s = n_[q];
+                    if (s.k == N_BYTE && s.lo <= b && b <= s.hi) tgt.push_back(s.a);
+                }
+                std::vector<uint32_t> cl;
+                if (!tgt.empty()) closure(tgt, false, cl);
+                int64_t id = intern(std::move(cl), false);
+                if (id < 0) {
+                    err = "DFA exceeded the size limit (" + std::to_string(limit_) + " bytes)";
+                    return false;
+                }
+                tr.resize(sets.size() * nc, 0);
+                tr[i * nc + c] = (uint32_t)id;
+            }
+        }
+        minimize_and_emit(tr, acc, nc, cls_of, out);
+        return true;
+    }
+
+private:
+    const std::vector<NState>& n_;
+    uint32_t start_;
+    size_t limit_;
+    std::vector<uint32_t> mark_;
+    uint32_t epoch_ = 0;
+
+    // states reachable by empty moves; keeps byte, match and end-anchor states
+    void closure(const std::vector<uint32_t>& from, bool at_start, std::vector<uint32_t>& out) {
+        epoch_++;
+        std::vector<uint32_t> stack(from.rbegin(), from.rend());
+        while (!stack.empty()) {
+            uint32_t q = stack.back();
+            stack.pop_back();
+            if (mark_[q] == epoch_) continue;
+            mark_[q] = epoch_;
+            const NState& s = n_[q];
+            switch (s.k) {
+                case N_BYTE: case N_MATCH: case N_END: out.push_back(q); break;
+                case N_EPS: stack.push_back(s.a); break;
+                case N_SPLIT: stack.push_back(s.b); stack.push_back(s.a); break;
+                case N_START: if (at_start) stack.push_back(s.a); break;
+            }
+        }
+        std::sort(out.begin(), out.end());
+    }
+    // a match is reached at the end of the text from this set
+    bool accepting(const std::vector<uint32_t>& set, bool at_start) {
+        epoch_++;
+        std::vector<uint32_t> stack(set.begin(), set.end());
+        while (!stack.empty()) {
+            uint32_t q = stack.back();
+            stack.pop_back();
+            if (mark_[q] == epoch_) continue;
+            mark_[q] = epoch_;
+            const NState& s = n_[q];
+            switch (s.k) {
+                case N_MATCH: return true;
+                case N_END: case N_EPS: stack.push_back(s.a); break;
+                case N_SPLIT: stack.push_back(s.b); stack.push_back(s.a); break;
+                case N_START: if (at_start) stack.push_back(s.a); break;
+                default: break;
+            }
+        }
+        return false;
+    }
+
+    // Moore partition refinement; block of the empty set becomes state 0
+    static void minimize_and_emit(const std::vector<uint32_t>& tr, const std::vector<uint8_t>& acc, int nc,
+                                  const uint8_t* cls_of, zs_host_dfa& out) {
+        const size_t n = acc.size();
+        // states that reach an accepting state; all others share the dead block
+        std::vector<std::vector<uint32_t>> rev(n);
+        for (size_t s = 0; s < n; s++)
+            for (int c = 0; c < nc; c++) rev[tr[s * nc + c]].push_back((uint32_t)s);
+        std::vector<uint8_t> live(n, 0);
+        std::vector<uint32_t> stack;
+        for (size_t s = 0; s < n; s++) if (acc[s]) { live[s] = 1; stack.push_back((uint32_t)s); }
+        while (!stack.empty()) {
+            uint32_t s = stack.back();
+            stack.pop_back();
+            for (uint32_t p : rev[s]) if (!live[p]) { live[p] = 1; stack.push_back(p); }
+        }
+        std::vector<uint32_t> blk(n);
+        for (size_t s = 0; s < n; s++) blk[s] = !live[s] ? 0u : acc[s] ? 2u : 1u;
+        size_t nb = 0;
+        for (;;) {
+            std::unordered_map<std::vector<uint32_t>, uint32_t, VecHash> sig;
+            std::vector<uint32_t> nbk(n);
+            std::vector<uint32_t> key(nc + 1);
+            // the dead block keeps id 0
+            for (size_t s = 0; s < n; s++) {
+                key[0] = blk[s];
+                for (int c = 0; c < nc; c++) key[c + 1] = blk[tr[s * nc + c]];
+                if (blk[s] == 0) { nbk[s] = 0; continue; }
+                auto it = sig.find(key);
+                if (it == sig.end()) it = sig.emplace(key, (uint32_t)sig.size() + 1).first;
+                nbk[s] = it->second;
+            }
+            const size_t cnt = sig.size() + 1;
+            blk.swap(nbk);
+            if (cnt == nb) break;
+            nb = cnt;
+        }
+        // renumber: dead 0, start 1, then in discovery order
+        std::vector<int64_t> newid(nb, -1);
+        std::vector<uint32_t> order;
+        newid[0] = 0;
+        order.push_back(0);
+        auto visit = [&](uint32_t b) { if (newid[b] < 0) { newid[b] = (int64_t)order.size(); order.push_back(b); } };
+        std::vector<uint32_t> rep_of(nb, 0);
+        for (size_t s = n; s-- > 0;) rep_of[blk[s]] = (uint32_t)s;
+        visit(blk[1]);
+        for (size_t i = 1; i < order.size(); i++) {
+            const uint32_t s = rep_of[order[i]];
+            for (int c = 0; c < nc; c++) visit(blk[tr[s * nc + c]]);
+        }
+        const size_t m = order.size();
+        out.nstates = (uint32_t)m;
+        out.start = (uint32_t)newid[blk[1]];
+        out.trans.assign(m * 256, 0);
+        out.accept.assign(m, 0);
+        out.dead.assign(m, 0);
+        out.dead[0] = 1;
+        for (size_t i = 1; i < m; i++) {
+            const uint32_t s = rep_of[order[i]];
+            out.accept[i] = acc[s];
+            for (int b = 0; b < 256; b++) out.trans[i * 256 + b] = (uint32_t)newid[blk[tr[s * nc + cls_of[b]]]];
+        }
+    }
+};
+
+}  // namespace
+
+int zs_regex_build(const std::string& pattern, zs_host_dfa& out, std::string& err) {
+    std::vector<Node> ar;
+    int root;
+    try {
+        Parser p(pattern, ar);
+        root = p.parse();
+    } catch (const ParseError& e) {
+        err = "regex parse error: " + e.msg;
+        return -1;
+    }
+    const size_t limit = (size_t)ZS_REGEX_DFA_LIMIT;
+    NfaBuilder nb(limit / 4);
+    uint32_t start;
+    try {
+        uint32_t match = nb.add(N_MATCH);
+        start = nb.build(ar, root, match);
+    } catch (const TooBig&) {
+        err = "regex exceeds the size limit";
+        return -1;
+    }
+    Determinizer d(nb.st, start, limit);
+    if (!d.run(out, err)) return -1;
+    return 0;
+}

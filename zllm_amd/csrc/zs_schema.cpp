@@ -1,0 +1,511 @@
+// zs_schema.cpp -- JSON schema -> anchored regex (json_schema.rs:78-268), the
+// shapeless JSON value grammar (:84-91, :114-127) and the multi-tool call
+// envelope (:99-112), plus the small JSON reader / compact writer they need.
+//
+// The reader keeps object members in document order with a repeated key
+// replacing the value in its first position (serde_json with the
+// `preserve_order` feature, Cargo.toml:34, which the reference builds with:
+// properties are emitted in declaration order). Numbers are kept as serde_json
+// classifies them: unsigned / negative integers that fit 64 bits, everything
+// else (fractions, exponents, overflow, "-0") as f64; the writer prints f64 in
+// the shortest round-trip form with ryu's layout rules (what serde_json's
+// to_string prints), so `enum` / `const` literals match byte for byte.
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#include <charconv>
+#include <cmath>
+#include <string>
+#include <utility>
+#include <vector>
+#include "zs_grammar.h"
+
+namespace {
+
+struct JV {
+    enum T { NUL, BOOL, POS, NEG, F64, STR, ARR, OBJ } t = NUL;
+    bool b = false;
+    uint64_t u = 0;
+    int64_t i = 0;
+    double d = 0.0;
+    std::string s;
+    std::vector<JV> a;
+    std::vector<std::pair<std::string, JV>> o;
+    const JV* get(const char* k) const {
+        if (t != OBJ) return nullptr;
+        for (auto& m : o)
+            if (m.first == k) return &m.second;
+        return nullptr;
+    }
+};
+
+struct JsonError {
+    std::string msg;
+};
+
+class Reader {
+public:
+    explicit Reader(const std::string& s) : s_(s) {}
+    JV parse() {
+        JV v = value(0);
+        ws();
+        if (p_ < s_.size()) fail("trailing characters");
+        return v;
+    }
+
+private:
+    const std::string& s_;
+    size_t p_ = 0;
+
+    [[noreturn]] void fail(const std::string& m) {
+        // line / column like serde_json's messages
+        size_t line = 1, col = 0;
+        for (size_t i = 0; i < p_ && i < s_.size(); i++) {
+            if (s_[i] == '\n') { line++; col = 0; } else col++;
+        }
+        throw JsonError{m + " at line " + std::to_string(line) + " column " + std::to_string(col + 1)};
+    }
+    void ws() {
+        while (p_ < s_.size() && (s_[p_] == ' ' || s_[p_] == '\t' || s_[p_] == '\n' || s_[p_] == '\r')) p_++;
+    }
+    void lit(const char* w) {
+        size_t n = strlen(w);
+        if (s_.compare(p_, n, w) != 0) fail("expected value");
+        p_ += n;
+    }
+    JV value(int depth) {
+        ws();
+        if (p_ >= s_.size()) fail("EOF while parsing a value");
+        JV v;
+        const char c = s_[p_];
+        if (c == 'n') { lit("null"); return v; }
+        if (c == 't') { lit("true"); v.t = JV::BOOL; v.b = true; return v; }
+        if (c == 'f') { lit("false"); v.t = JV::BOOL; return v; }
+        if (c == '"') { v.t = JV::STR; v.s = str(); return v; }
+        if (c == '-' || (c >= '0' && c <= '9')) return number();
+        if (c == '[' || c == '{') {
+            if (depth >= 128) fail("recursion limit exceeded");
+            p_++;
+            const char close = c == '[' ? ']' : '}';
+            v.t = c == '[' ? JV::ARR : JV::OBJ;
+            ws();
+            if (p_ < s_.size() && s_[p_] == close) { p_++; return v; }
+            for (;;) {
+                if (v.t == JV::ARR) {
+                    v.a.push_back(value(depth + 1));
+                } else {
+                    ws();
+                    if (p_ >= s_.size() || s_[p_] != '"') fail("key must be a string");
+                    std::string k = str();
+                    ws();
+                    if (p_ >= s_.size() || s_[p_] != ':') fail("expected `:`");
+                    p_++;
+                    JV m = value(depth + 1);
+                    bool found = false;
+                    for (auto& e : v.o)
+                        if (e.first == k) { e.second = std::move(m); found = true; break; }
+                    if (!found) v.o.emplace_back(std::move(k), std::move(m));
+                }
+                ws();
+                if (p_ >= s_.size()) fail("EOF while parsing");
+                if (s_[p_] == ',') { p_++; continue; }
+                if (s_[p_] == close) { p_++; return v; }
+                fail(v.t == JV::ARR ? "expected `,` or `]`" : "expected `,` or `}`");
+            }
+        }
+        fail("expected value");
+    }
+    uint32_t hex4() {
+        if (p_ + 4 > s_.size()) fail("EOF while parsing a string");
+        uint32_t v = 0;
+        for (int i = 0; i < 4; i++) {
+            const char c = s_[p_++];
+            int d = (c >= '0' && c <= '9') ? c - '0' : (c >= 'a' && c <= 'f') ? c - 'a' + 10
+                    : (c >= 'A' && c <= 'F') ? c - 'A' + 10 : -1;
+            if (d < 0) fail("invalid escape");
+            v = v * 16 + (uint32_t)d;
+        }
+        return v;
+    }
+    static void put_utf8(std::string& o, uint32_t cp) {
+        if (cp < 0x80) o += (char)cp;
+        else if (cp < 0x800) { o += (char)(0xC0 | (cp >> 6)); o += (char)(0x80 | (cp & 0x3f)); }
+        else if (cp < 0x10000) {
+            o += (char)(0xE0 | (cp >> 12)); o += (char)(0x80 | ((cp >> 6) & 0x3f)); o += (char)(0x80 | (cp & 0x3f));
+        } else {
+            o += (char)(0xF0 | (cp >> 18)); o += (char)(0x80 | ((cp >> 12) & 0x3f));
+            o += (char)(0x80 | ((cp >> 6) & 0x3f)); o += (char)(0x80 | (cp & 0x3f));
+        }
+    }
+    std::string str() {
+        p_++;  // opening quote
+        std::string o;
+        for (;;) {
+            if (p_ >= s_.size()) fail("EOF while parsing a string");
+            const unsigned char c = (unsigned char)s_[p_];
+            if (c == '"') { p_++; return o; }
+            if (c < 0x20) fail("control character (\\u0000-\\u001F) found while parsing a string");
+            if (c != '\\') { o += (char)c; p_++; continue; }
+            p_++;
+            if (p_ >= s_.size()) fail("EOF while parsing a string");
+            const char e = s_[p_++];
+            switch (e) {
+                case '"': o += '"'; break;
+                case '\\': o += '\\'; break;
+                case '/': o += '/'; break;
+                case 'b': o += '\b'; break;
+                case 'f': o += '\f'; break;
+                case 'n': o += '\n'; break;
+                case 'r': o += '\r'; break;
+                case 't': o += '\t'; break;
+                case 'u': {
+                    uint32_t cp = hex4();
+                    if (cp >= 0xDC00 && cp <= 0xDFFF) fail("lone leading surrogate in hex escape");
+                    if (cp >= 0xD800 && cp <= 0xDBFF) {
+                        if (p_ + 2 > s_.size() || s_[p_] != '\\' || s_[p_ + 1] != 'u')
+                            fail("unexpected end of hex escape");
+                        p_ += 2;
+                        const uint32_t lo = hex4();
+                        if (lo < 0xDC00 || lo > 0xDFFF) fail("lone leading surrogate in hex escape");
+                        cp = 0x10000 + ((cp - 0xD800) << 10) + (lo - 0xDC00);
+                    }
+                    put_utf8(o, cp);
+                    break;
+                }
+                default: fail("invalid escape");
+            }
+        }
+    }
+    JV number() {
+        const size_t st = p_;
+        const bool neg = s_[p_] == '-';
+        if (neg) p_++;
+        if (p_ >= s_.size() || !(s_[p_] >= '0' && s_[p_] <= '9')) fail("invalid number");
+        if (s_[p_] == '0' && p_ + 1 < s_.size() && s_[p_ + 1] >= '0' && s_[p_ + 1] <= '9') fail("invalid number");
+        while (p_ < s_.size() && s_[p_] >= '0' && s_[p_] <= '9') p_++;
+        const size_t int_end = p_;
+        bool is_float = false;
+        if (p_ < s_.size() && s_[p_] == '.') {
+            is_float = true;
+            p_++;
+            if (p_ >= s_.size() || !(s_[p_] >= '0' && s_[p_] <= '9')) fail("invalid number");
+            while (p_ < s_.size() && s_[p_] >= '0' && s_[p_] <= '9') p_++;
+        }
+        if (p_ < s_.size() && (s_[p_] == 'e' || s_[p_] == 'E')) {
+            is_float = true;
+            p_++;
+            if (p_ < s_.size() && (s_[p_] == '+' || s_[p_] == '-')) p_++;
+            if (p_ >= s_.size() || !(s_[p_] >= '0' && s_[p_] <= '9')) fail("invalid number");
+            while (p_ < s_.size() && s_[p_] >= '0' && s_[p_] <= '9') p_++;
+        }
+        JV v;
+        if (!is_float) {
+            // integer: fits 64 bits as serde_json keeps it?
+            unsigned __int128 m = 0;
+            bool big = false;
+            for (size_t i = st + (neg ? 1 : 0); i < int_end; i++) {
+                m = m * 10 + (unsigned)(s_[i] - '0');
+                if (m > ((unsigned __int128)1 << 64)) { big = true; break; }
+            }
+            if (!big && !neg && m <= UINT64_MAX) { v.t = JV::POS; v.u = (uint64_t)m; return v; }
+            if (!big && neg && m != 0 && m <= ((unsigned __int128)1 << 63)) {
+                v.t = JV::NEG;
+                v.i = (int64_t)(0 - (uint64_t)m);
+                return v;
+            }
+        }
+        const std::string txt = s_.substr(st, p_ - st);
+        v.t = JV::F64;
+        v.d = strtod(txt.c_str(), nullptr);
+        if (std::isinf(v.d)) fail("number out of range");
+        return v;
+    }
+};
+
+// ryu's layout of the shortest round-trip digits (serde_json's f64 output)
+std::string f64_text(double d) {
+    if (d == 0.0) return std::signbit(d) ? "-0.0" : "0.0";
+    std::string out;
+    if (d < 0) { out += '-'; d = -d; }
+    char buf[64];
+    auto r = std::to_chars(buf, buf + sizeof buf, d, std::chars_format::scientific);
+    std::string sci(buf, r.ptr);
+    const size_t e = sci.find('e');
+    std::string digits;
+    for (size_t i = 0; i < e; i++)
+        if (sci[i] != '.') digits += sci[i];
+    const int sexp = atoi(sci.c_str() + e + 1);
+    const int length = (int)digits.size();
+    const int kk = sexp + 1;          // 10^(kk-1) <= v < 10^kk
+    const int k = kk - length;        // exponent of the last digit
+    if (k >= 0 && kk <= 16) {
+        out += digits;
+        out.append((size_t)(kk - length), '0');
+        out += ".0";
+    } else if (kk > 0 && kk <= 16) {
+        out += digits.substr(0, (size_t)kk);
+        out += '.';
+        out += digits.substr((size_t)kk);
+    } else if (kk > -5 && kk <= 0) {
+        out += "0.";
+        out.append((size_t)(-kk), '0');
+        out += digits;
+    } else if (length == 1) {
+        out += digits;
+        out += 'e';
+        out += std::to_string(kk - 1);
+    } else {
+        out += digits[0];
+        out += '.';
+        out += digits.substr(1);
+        out += 'e';
+        out += std::to_string(kk - 1);
+    }
+    return out;
+}
+
+void write_str(std::string& o, const std::string& s) {
+    static const char hex[] = "0123456789abcdef";
+    o += '"';
+    for (unsigned char c : s) {
+        switch (c) {
+            case '"': o += "\\\""; break;
+            case '\\': o += "\\\\"; break;
+            case '\b': o += "\\b"; break;
+            case '\f': o += "\\f"; break;
+            case '\n': o += "\\n"; break;
+            case '\r': o += "\\r"; break;
+            case '\t': o += "\\t"; break;
+            default:
+                if (c < 0x20) { o += "\\u00"; o += hex[c >> 4]; o += hex[c & 15]; }
+                else o += (char)c;
+        }
+    }
+    o += '"';
+}
+
+// compact serialization (serde_json::to_string)
+void write_json(std::string& o, const JV& v) {
+    switch (v.t) {
+        case JV::NUL: o += "null"; break;
+        case JV::BOOL: o += v.b ? "true" : "false"; break;
+        case JV::POS: o += std::to_string(v.u); break;
+        case JV::NEG: o += std::to_string(v.i); break;
+        case JV::F64: o += f64_text(v.d); break;
+        case JV::STR: write_str(o, v.s); break;
+        case JV::ARR:
+            o += '[';
+            for (size_t i = 0; i < v.a.size(); i++) { if (i) o += ','; write_json(o, v.a[i]); }
+            o += ']';
+            break;
+        case JV::OBJ:
+            o += '{';
+            for (size_t i = 0; i < v.o.size(); i++) {
+                if (i) o += ',';
+                write_str(o, v.o[i].first);
+                o += ':';
+                write_json(o, v.o[i].second);
+            }
+            o += '}';
+            break;
+    }
+}
+
+// Rust's `{:?}` of a str, for error messages
+std::string dbg(const std::string& s) {
+    std::string o = "\"";
+    for (unsigned char c : s) {
+        if (c == '"' || c == '\\') { o += '\\'; o += (char)c; }
+        else if (c == '\n') o += "\\n";
+        else if (c == '\r') o += "\\r";
+        else if (c == '\t') o += "\\t";
+        else if (c < 0x20 || c == 0x7f) { char b[16]; snprintf(b, sizeof b, "\\u{%x}", c); o += b; }
+        else o += (char)c;
+    }
+    return o + "\"";
+}
+
+// ---------------------------------------------------------------- regex pieces
+// JSON primitive shapes of json_schema.rs:44-53 (RFC 8259, compact) and the
+// optional single space after structural ':' and ','.
+const char* const RX_STRING = "\"([^\"\\\\]|\\\\([\"\\\\/bfnrt]|u[0-9a-fA-F]{4}))*\"";
+const char* const RX_NUMBER = "-?(0|[1-9][0-9]*)(\\.[0-9]+)?([eE][+-]?[0-9]+)?";
+const char* const RX_INTEGER = "-?(0|[1-9][0-9]*)";
+const char* const RX_BOOL = "(true|false)";
+const char* const RX_NULL = "null";
+const std::string SP = " ?";
+const int MAX_DEPTH = 32;
+const int ANY_DEPTH = 5;
+
+// regex metacharacters escaped so a literal matches itself (json_schema.rs:58-67)
+std::string esc(const std::string& s) {
+    std::string o;
+    for (char c : s) {
+        if (strchr("\\.+*?()|[]{}^$", c) && c != '\0') o += '\\';
+        o += c;
+    }
+    return o;
+}
+
+std::string literal(const JV& v) {
+    std::string j;
+    write_json(j, v);
+    return esc(j);
+}
+
+std::string join(const std::vector<std::string>& v, const std::string& sep) {
+    std::string o;
+    for (size_t i = 0; i < v.size(); i++) { if (i) o += sep; o += v[i]; }
+    return o;
+}
+
+std::string any_value(int depth) {
+    std::vector<std::string> alts = {RX_STRING, RX_NUMBER, RX_BOOL, RX_NULL};
+    if (depth > 0) {
+        const std::string in = any_value(depth - 1);
+        alts.push_back("\\[" + SP + "(" + in + "(" + SP + "," + SP + in + ")*)?" + SP + "\\]");
+        const std::string mem = std::string(RX_STRING) + SP + ":" + SP + in;
+        alts.push_back("\\{" + SP + "(" + mem + "(" + SP + "," + SP + mem + ")*)?" + SP + "\\}");
+    }
+    return "(" + join(alts, "|") + ")";
+}
+
+struct SchemaError {
+    std::string msg;
+};
+
+std::string compile(const JV& sc, int depth);
+
+std::string compile_array(const JV& sc, int depth) {
+    const JV* items = sc.get("items");
+    if (!items) throw SchemaError{"array schema needs \"items\""};
+    const std::string item = compile(*items, depth + 1);
+    const JV* jmin = sc.get("minItems");
+    const JV* jmax = sc.get("maxItems");
+    const uint64_t mn = (jmin && jmin->t == JV::POS) ? jmin->u : 0;
+    const bool has_max = jmax && jmax->t == JV::POS;
+    const uint64_t mx = has_max ? jmax->u : 0;
+    if (has_max) {
+        if (mx < mn) throw SchemaError{"maxItems < minItems"};
+        if (mx == 0) return "\\[" + SP + "\\]";
+    }
+    const std::string sep = SP + "," + SP;
+    auto times = [&](uint64_t n) {
+        if (n > 100000) throw SchemaError{"array bounds too large to unroll"};
+        std::vector<std::string> v((size_t)n, item);
+        return join(v, sep);
+    };
+    std::string body;
+    if (!has_max) {
+        if (mn == 0) body = "(" + item + "(" + sep + item + ")*)?";
+        else body = times(mn) + "(" + sep + item + ")*";
+    } else {
+        std::vector<std::string> parts;
+        for (uint64_t c = mn > 1 ? mn : 1; c <= mx; c++) parts.push_back(times(c));
+        body = "(" + join(parts, "|") + ")";
+        if (mn == 0) body = "(" + body + ")?";
+    }
+    return "\\[" + SP + body + SP + "\\]";
+}
+
+std::string compile_object(const JV& sc, int depth) {
+    const JV* props = sc.get("properties");
+    if (!props || props->t != JV::OBJ) {
+        int d = ANY_DEPTH - depth - 1;
+        if (d < 0) d = 0;
+        const std::string v = any_value(d);
+        const std::string mem = std::string(RX_STRING) + SP + ":" + SP + v;
+        return "\\{" + SP + "(" + mem + "(" + SP + "," + SP + mem + ")*)?" + SP + "\\}";
+    }
+    if (props->o.empty()) return "\\{" + SP + "\\}";
+    std::vector<std::string> pairs;
+    for (auto& m : props->o) {
+        const std::string val = compile(m.second, depth + 1);
+        pairs.push_back("\"" + esc(m.first) + "\"" + SP + ":" + SP + val);
+    }
+    return "\\{" + SP + join(pairs, SP + "," + SP) + SP + "\\}";
+}
+
+std::string compile(const JV& sc, int depth) {
+    if (depth > MAX_DEPTH)
+        throw SchemaError{"schema nesting exceeds " + std::to_string(MAX_DEPTH) + " \xE2\x80\x94 refusing to unroll"};
+    if (sc.t != JV::OBJ) throw SchemaError{"schema must be a JSON object"};
+    for (const char* k : {"$ref", "oneOf", "anyOf", "allOf", "not", "patternProperties", "if"})
+        if (sc.get(k)) throw SchemaError{"schema keyword " + dbg(k) + " is not supported by the regex compiler"};
+    if (const JV* c = sc.get("const")) return literal(*c);
+    if (const JV* e = sc.get("enum"); e && e->t == JV::ARR) {
+        if (e->a.empty()) throw SchemaError{"enum must be non-empty"};
+        std::vector<std::string> alts;
+        for (auto& v : e->a) alts.push_back(literal(v));
+        return "(" + join(alts, "|") + ")";
+    }
+    const JV* ty = sc.get("type");
+    if (!ty || ty->t != JV::STR)
+        throw SchemaError{"schema needs a \"type\" (or enum/const); unions via type-arrays are not supported"};
+    const std::string& t = ty->s;
+    if (t == "string") {
+        const JV* p = sc.get("pattern");
+        if (p && p->t == JV::STR) return "\"" + p->s + "\"";
+        return RX_STRING;
+    }
+    if (t == "integer") return RX_INTEGER;
+    if (t == "number") return RX_NUMBER;
+    if (t == "boolean") return RX_BOOL;
+    if (t == "null") return RX_NULL;
+    if (t == "array") return compile_array(sc, depth);
+    if (t == "object") return compile_object(sc, depth);
+    throw SchemaError{"unsupported schema type " + dbg(t)};
+}
+
+}  // namespace
+
+int zs_schema_regex(const std::string& schema_json, std::string& out, std::string& err) {
+    JV sc;
+    try {
+        sc = Reader(schema_json).parse();
+    } catch (const JsonError& e) {
+        err = "json_schema: invalid JSON schema: " + e.msg;
+        return -1;
+    }
+    try {
+        out = compile(sc, 0);
+    } catch (const SchemaError& e) {
+        err = e.msg;
+        return -1;
+    }
+    return 0;
+}
+
+std::string zs_any_json(uint32_t depth) { return any_value((int)(depth < (uint32_t)MAX_DEPTH ? depth : MAX_DEPTH)); }
+
+int zs_tool_envelope(const std::vector<std::string>& names, const std::vector<std::string>& schemas,
+                     std::string& out, std::string& err) {
+    if (names.empty()) {
+        err = "no tools to build a call envelope from";
+        return -1;
+    }
+    std::vector<std::string> alts;
+    for (size_t i = 0; i < names.size(); i++) {
+        JV name;
+        name.t = JV::STR;
+        name.s = names[i];
+        JV params;
+        try {
+            params = Reader(schemas[i]).parse();
+        } catch (const JsonError& e) {
+            err = "json_schema: invalid JSON schema: " + e.msg;
+            return -1;
+        }
+        std::string args;
+        try {
+            args = compile(params, 0);
+        } catch (const SchemaError& e) {
+            err = e.msg;
+            return -1;
+        }
+        alts.push_back("\\{" + SP + "\"name\"" + SP + ":" + SP + literal(name) + SP + "," + SP + "\"arguments\"" + SP +
+                       ":" + SP + args + SP + "\\}");
+    }
+    out = "(" + join(alts, "|") + ")";
+    return 0;
+}

@@ -213,8 +213,9 @@ class ByteDfa:
 
 class LogitFSM:
     """logit_fsm.rs:33-37: either a `ban:` list or a byte-DFA constraint with
-    its current state. Regex / JSON-schema compilation to a DFA is not part of
-    this build; pass the built DFA."""
+    its current state. `compile` builds the DFA of `regex:`, `json_schema:`
+    and `json:` grammars with the native compiler (zllm_amd.grammar) and
+    uploads it to the table's context."""
 
     def __init__(self, banned: Sequence[int] = (), dfa: Optional[ByteDfa] = None,
                  table: Optional[TokenByteTable] = None, state: int = 0):
@@ -235,11 +236,26 @@ class LogitFSM:
             return cls(banned=banned)
         if g == "":
             return cls()
-        for mode in ("regex", "json_schema", "json", "bnf"):
-            if g.startswith(mode + ":"):
-                raise NotImplementedError(f"grammar mode {mode!r} needs a compiled DFA: use LogitFSM(dfa=...)")
-        raise ValueError('grammar mode "unknown" is not implemented yet; supported: "ban:<id>,<id>,...", '
-                         '"regex:<pattern>", "json_schema:<schema>", "json:"')
+        from . import grammar as G
+        if g.startswith("regex:"):
+            if table is None:
+                raise G.GrammarError("regex grammar needs a tokenizer byte table")
+            pattern = g[len("regex:"):]
+        elif g.startswith("json_schema:"):
+            if table is None:
+                raise G.GrammarError("json_schema grammar needs a tokenizer byte table")
+            pattern = G.schema_to_regex(g[len("json_schema:"):].strip())
+        elif g.startswith("json:"):
+            if table is None:
+                raise G.GrammarError("json grammar needs a tokenizer byte table")
+            pattern = G.any_json_regex_default()
+        else:
+            mode = next((m for m in ("regex", "json_schema", "json", "bnf") if g.startswith(m + ":")), "unknown")
+            raise G.GrammarError(f'grammar mode "{mode}" is not implemented yet; supported: "ban:<id>,<id>,...", '
+                                 '"regex:<pattern>", "json_schema:<schema>", "json:"')
+        host = G.HostDfa(pattern)
+        dfa = ByteDfa(table.ctx, host.trans, host.dead, host.accept)
+        return cls(dfa=dfa, table=table, state=host.start)
 
     def is_active(self) -> bool:  # logit_fsm.rs:299-301
         return bool(self.banned) or self.dfa is not None
