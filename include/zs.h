@@ -118,6 +118,22 @@ int zs_any_json_regex(uint32_t depth, char* out, size_t cap, size_t* need);
 int zs_tool_call_envelope_regex(const char* const* names, const char* const* schemas, uint32_t n,
                                 char* out, size_t cap, size_t* need, char* err, size_t errcap);
 
+/* ---- grammar byte table of a real vocabulary (host only) ----------------
+ * LlamaTokenizer::token_bytes_table (tokenizer.rs:108-117): per id below
+ * get_vocab_size(true), the bytes of decode([id]) with special tokens
+ * skipped, or None (valid = 0) when that text is empty or holds U+FFFD. From
+ * a tokenizer.json document (len bytes) or from the vocab embedded in a GGUF
+ * file (gguf_vocab.rs:75-171, byte-level BPE only). The CSR arrays feed
+ * zs_vocab_create; eos is eos_token_id (tokenizer.rs:52-57) or -1. */
+typedef struct zs_token_table zs_token_table;
+int zs_token_table_from_json(const char* json, size_t len, zs_token_table** out, char* err, size_t errcap);
+int zs_token_table_from_gguf(const char* path, zs_token_table** out, char* err, size_t errcap);
+int zs_token_table_info(const zs_token_table* t, uint32_t* ntab, uint32_t* nbytes, int64_t* eos);
+const uint32_t* zs_token_table_offsets(const zs_token_table* t);  /* [ntab + 1] */
+const uint8_t* zs_token_table_bytes(const zs_token_table* t);     /* [nbytes] */
+const uint8_t* zs_token_table_valid(const zs_token_table* t);     /* [ntab] */
+void zs_token_table_destroy(zs_token_table* t);
+
 /* ---- sampler ------------------------------------------------------------
  * Per-row knobs: SamplerConfig (sampler.rs:3-22) + PenaltyConfig
  * (decode_ctrl.rs:21-43) + LogprobsCollector::top_n (logprobs.rs:27, clamped

@@ -187,3 +187,31 @@ def test_compiled_grammar_masks(name):
     bits = bits.cpu().numpy().view(np.uint32)
     for i, s in enumerate(states):
         assert np.array_equal(bits[i], O.mask_bits(V, dfa=od, vocab=ov, state=int(s))), (name, i, s)
+
+
+def test_real_vocab_table_and_json_grammar():
+    """A byte-level BPE vocabulary (HF tokenizers) -> zs_token_table ->
+    zs_vocab, with the `json:` grammar: GPU masks equal the oracle's."""
+    tk = pytest.importorskip("tokenizers")
+    from tests.gpu_util import ctx
+    from tests.test_vocab import byte_level_bpe
+    from zllm_amd.engine import LogitFSM, TokenByteTable
+    from zllm_amd.vocab import HostTokenTable
+    print("[case] real vocab json", flush=True)
+    host = HostTokenTable.from_tokenizer_json(byte_level_bpe(seed=7, vocab_size=3000).to_str())
+    c = ctx()
+    table = TokenByteTable.from_host_table(c, host)
+    fsm = LogitFSM.compile("json:", table)
+    V = host.ntab + 5  # logits wider than the table: the extra ids are never allowed
+    tokens = host.tokens()
+    d = fsm.dfa
+    from zllm_amd import grammar as G
+    g = G.HostDfa(G.any_json_regex_default())
+    od, ov = O.Dfa(g.trans, g.dead, g.accept), O.Vocab(tokens, host.eos)
+    states = [g.start] + [int(s) for s in np.random.default_rng(3).integers(1, g.nstates, 15)]
+    st = torch.tensor(np.asarray(states, np.int32), device="cuda")
+    bits = d.mask(table, st, V)
+    torch.cuda.synchronize()
+    bits = bits.cpu().numpy().view(np.uint32)
+    for i, s in enumerate(states):
+        assert np.array_equal(bits[i], O.mask_bits(V, dfa=od, vocab=ov, state=s)), (i, s)

@@ -126,6 +126,14 @@ SIGNATURES = {
     "zs_json_schema_regex": (C.c_int, [C.c_char_p, C.c_size_t, C.c_char_p, C.c_size_t, C.POINTER(C.c_size_t),
                                        C.c_char_p, C.c_size_t]),
     "zs_any_json_regex": (C.c_int, [C.c_uint32, C.c_char_p, C.c_size_t, C.POINTER(C.c_size_t)]),
+    "zs_token_table_from_json": (C.c_int, [C.c_char_p, C.c_size_t, C.POINTER(C.c_void_p), C.c_char_p, C.c_size_t]),
+    "zs_token_table_from_gguf": (C.c_int, [C.c_char_p, C.POINTER(C.c_void_p), C.c_char_p, C.c_size_t]),
+    "zs_token_table_info": (C.c_int, [C.c_void_p, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32),
+                                      C.POINTER(C.c_int64)]),
+    "zs_token_table_offsets": (C.c_void_p, [C.c_void_p]),
+    "zs_token_table_bytes": (C.c_void_p, [C.c_void_p]),
+    "zs_token_table_valid": (C.c_void_p, [C.c_void_p]),
+    "zs_token_table_destroy": (None, [C.c_void_p]),
     "zs_tool_call_envelope_regex": (C.c_int, [C.POINTER(C.c_char_p), C.POINTER(C.c_char_p), C.c_uint32, C.c_char_p,
                                               C.c_size_t, C.POINTER(C.c_size_t), C.c_char_p, C.c_size_t]),
 }

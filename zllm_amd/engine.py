@@ -136,6 +136,17 @@ class TokenByteTable:
         self.h = h
 
     @classmethod
+    def from_host_table(cls, ctx, host, eos=None):
+        """Upload a zllm_amd.vocab.HostTokenTable (tokenizer.json / GGUF vocab);
+        eos defaults to its eos_token_id (rest.rs:1331 refuses a grammar
+        without one)."""
+        eos = host.eos if eos is None else eos
+        if eos is None:
+            raise ValueError("tokenizer has no EOS token; regex grammar unavailable")
+        return cls.from_csr(ctx, host.offsets, host.data if host.data.size else np.zeros(1, np.uint8), host.valid,
+                            eos)
+
+    @classmethod
     def from_csr(cls, ctx, offsets, data, valid, eos):
         obj = cls.__new__(cls)
         obj.ctx = ctx
