@@ -132,7 +132,36 @@ int zs_token_table_info(const zs_token_table* t, uint32_t* ntab, uint32_t* nbyte
 const uint32_t* zs_token_table_offsets(const zs_token_table* t);  /* [ntab + 1] */
 const uint8_t* zs_token_table_bytes(const zs_token_table* t);     /* [nbytes] */
 const uint8_t* zs_token_table_valid(const zs_token_table* t);     /* [ntab] */
+/* decode([id]) text of every id (U+FFFD pieces and the "" of specials kept),
+ * for the logprobs JSON (rest.rs:1714): offsets [ntab + 1] into bytes. */
+int zs_token_table_text(const zs_token_table* t, const uint32_t** offsets, const uint8_t** bytes);
 void zs_token_table_destroy(zs_token_table* t);
+
+/* ---- OpenAI wire output (host only) ---------------------------------------
+ * Detector::report (hallucination.rs:101-125) over per-token entropy /
+ * max_prob (zs_sample's d_entropy / d_max_prob), vocab = row width, with the
+ * DetectorConfig thresholds (defaults 2.0 and 0.4, hallucination.rs:44-50).
+ * peak_token = -1 for an empty report. */
+typedef struct zs_halluc_report {
+    float risk_score, mean_entropy, normalized_entropy, risky_fraction;
+    int64_t peak_token;
+    uint64_t n_tokens;
+} zs_halluc_report;
+int zs_hallucination_report(const float* entropy, const float* max_prob, uint64_t n, uint64_t vocab,
+                            float entropy_threshold, float max_prob_threshold, zs_halluc_report* out);
+/* hallucination_json (rest.rs:1494-1503); `flagged` = risk_score >=
+ * risk_threshold (the server uses 0.5). String outputs as zs_json_schema_regex. */
+int zs_hallucination_json(const zs_halluc_report* r, float risk_threshold, char* out, size_t cap, size_t* need);
+/* chat_logprobs_json / legacy_logprobs_json (rest.rs:1710-1744) over n
+ * generated tokens: ids[i], logprobs[i] (zs_sample's d_token / d_logprob) and
+ * top_count[i] alternatives top_ids / top_logprobs [i * top_stride + k]
+ * (d_top_n / d_top_ids / d_top_lps), token texts from zs_token_table_text. */
+#define ZS_LOGPROBS_CHAT 0
+#define ZS_LOGPROBS_LEGACY 1
+int zs_logprobs_json(int kind, uint32_t n, const uint32_t* ids, const float* logprobs, const uint32_t* top_count,
+                     uint32_t top_stride, const uint32_t* top_ids, const float* top_logprobs,
+                     const uint32_t* text_offsets, const uint8_t* text, uint32_t ntext, char* out, size_t cap,
+                     size_t* need);
 
 /* ---- sampler ------------------------------------------------------------
  * Per-row knobs: SamplerConfig (sampler.rs:3-22) + PenaltyConfig
@@ -251,6 +280,31 @@ int zs_lane_sample_topk(zs_ctx* ctx, const float* d_vals, const uint32_t* d_idxs
                         const uint32_t* d_seed, uint32_t* d_out, void* stream);
 /* gpu/sampling.rs:9 step_seed: base + gen_idx * 0x9E3779B1 (wrapping). */
 uint32_t zs_step_seed(uint32_t base, uint32_t gen_idx);
+
+/* One active stream of the continuous batcher: SamplingParams
+ * (gpu/sampling.rs:14-21; temp <= 0 greedy, top_k 0 = none, top_p >= 1 or 0 =
+ * none) and its seeding (base seed, tokens generated so far). */
+typedef struct zs_lane_stream {
+    float temp;
+    uint32_t top_k;
+    float top_p;
+    uint32_t base_seed;
+    uint32_t gen_index;
+} zs_lane_stream;
+#define ZS_LANE_ARGMAX 0
+#define ZS_LANE_SAMPLE 1
+#define ZS_LANE_TOPK 2
+/* ContinuousBatcher::step's selection (gpu/batch.rs:176-192) for m streams
+ * over d_logits[m][ld]: the cheapest path serving every stream -- top-64
+ * pool + nucleus draw (step_slotted_topk, gpu/mod.rs:2213-2229) if any stream
+ * needs top-k / top-p, else Gumbel temperature sampling (BSAMPLE) if any temp
+ * > 0, else argmax (BARGMAX) -- with seeds step_seed(base_seed, gen_index),
+ * all on the device: writes d_out[m], reads nothing back (the reference reads
+ * m x 64 candidates back and samples on the CPU). h_streams is read before the
+ * call returns; *path (optional) receives the ZS_LANE_* path taken. Calls on
+ * one context must be issued in order on one stream. m <= max_rows. */
+int zs_lane_step(zs_ctx* ctx, const float* d_logits, uint32_t m, uint32_t V, uint64_t ld,
+                 const zs_lane_stream* h_streams, uint32_t* d_out, int* path, void* stream);
 
 /* ---- profiling ----------------------------------------------------------
  * When enabled, zs_sample and zs_spec_verify record a HIP event around their

@@ -109,3 +109,47 @@ def test_spec_verify_matches_oracle(k, V):
     for b in range(B):
         want = O.spec_verify(target[b], draft[b], ids[b].tolist(), float(temp[b]), int(seeds[b]), int(ctr[b]))
         assert (int(acc[b]), int(nxt[b])) == want, (b, (acc[b], nxt[b]), want)
+
+
+@pytest.mark.parametrize("mix", ["topk", "sample", "greedy"])
+def test_lane_batcher_steps(mix):
+    """LaneBatcher (ContinuousBatcher::step's selection, gpu/batch.rs:176-207)
+    over several steps: every id equals the reference lane's choice for the
+    path the batch takes (BTOPK + sample_topk, BSAMPLE or BARGMAX with
+    step_seed(base, gen_index)); streams retire at eos / max_tokens."""
+    from zllm_amd.engine import (ZS_LANE_ARGMAX, ZS_LANE_SAMPLE, ZS_LANE_TOPK, LaneBatcher, LaneSeq,
+                                 SamplingParams)
+    print(f"[case] lane batcher {mix}", flush=True)
+    rng = np.random.default_rng({"topk": 1, "sample": 2, "greedy": 3}[mix])
+    m, V = 24, 32000
+    lb = LaneBatcher(_c())
+    for i in range(m):
+        if mix == "topk":
+            sp = [SamplingParams(0.7, 40, 0.9), SamplingParams(1.0, 0, 0.8), SamplingParams.greedy(),
+                  SamplingParams(0.5, 10, 1.0)][i % 4]
+        elif mix == "sample":
+            sp = SamplingParams.temperature([0.8, 0.0, 1.3][i % 3])
+        else:
+            sp = SamplingParams.greedy()
+        lb.add(LaneSeq(i, sp, base_seed=1000 + 7 * i, eos=5, max_tokens=3 + i % 4, generated=[int(rng.integers(V))]))
+    want_path = {"topk": ZS_LANE_TOPK, "sample": ZS_LANE_SAMPLE, "greedy": ZS_LANE_ARGMAX}[mix]
+    for step in range(6):
+        if not lb.active:
+            break
+        act = list(lb.active)
+        x = (rng.standard_normal((len(act), V)) * 4).astype(np.float32)
+        x[:, 5] = -1e9 if step < 2 else x[:, 5]  # eos only possible later
+        seeds = [O.step_seed(s.base_seed, s.gen_index()) for s in act]
+        res = lb.step(torch.from_numpy(x).cuda())
+        assert lb.last_path == want_path
+        for r, (s, (sid, tok, done)) in enumerate(zip(act, res)):
+            if want_path == ZS_LANE_TOPK:
+                vals, idxs = O.btopk(x[r], 64)
+                want = O.sample_topk(vals, idxs, s.params.temp, s.params.top_k, s.params.top_p, seeds[r])
+            elif want_path == ZS_LANE_SAMPLE:
+                want = O.bsample(x[r], s.params.temp, seeds[r])
+            else:
+                want = O.bargmax(x[r])
+            assert (sid, tok) == (s.id, want), (step, r)
+            assert done == (tok == 5 or s.gen_index() >= s.max_tokens)
+        assert all(not (s.generated[-1] == 5 or s.gen_index() >= s.max_tokens) for s in lb.active)

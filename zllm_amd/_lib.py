@@ -87,6 +87,16 @@ class SpecBatch(C.Structure):
     ]
 
 
+class LaneStream(C.Structure):
+    _fields_ = [("temp", C.c_float), ("top_k", C.c_uint32), ("top_p", C.c_float), ("base_seed", C.c_uint32),
+                ("gen_index", C.c_uint32)]
+
+
+class HallucReport(C.Structure):
+    _fields_ = [("risk_score", C.c_float), ("mean_entropy", C.c_float), ("normalized_entropy", C.c_float),
+                ("risky_fraction", C.c_float), ("peak_token", C.c_int64), ("n_tokens", C.c_uint64)]
+
+
 # name -> (restype, argtypes); every symbol include/zs.h declares
 SIGNATURES = {
     "zs_abi_version": (C.c_int, []),
@@ -116,6 +126,8 @@ SIGNATURES = {
     "zs_lane_sample_topk": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p,
                                       C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),
     "zs_step_seed": (C.c_uint32, [C.c_uint32, C.c_uint32]),
+    "zs_lane_step": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint64, C.POINTER(LaneStream),
+                               C.c_void_p, C.POINTER(C.c_int), C.c_void_p]),
     "zs_last_timings": (C.c_int, [C.c_void_p, C.POINTER(C.c_char_p), C.POINTER(C.c_float), C.c_int]),
     "zs_regex_compile": (C.c_int, [C.c_char_p, C.c_size_t, C.POINTER(C.c_void_p), C.c_char_p, C.c_size_t]),
     "zs_grammar_destroy": (None, [C.c_void_p]),
@@ -134,6 +146,14 @@ SIGNATURES = {
     "zs_token_table_bytes": (C.c_void_p, [C.c_void_p]),
     "zs_token_table_valid": (C.c_void_p, [C.c_void_p]),
     "zs_token_table_destroy": (None, [C.c_void_p]),
+    "zs_token_table_text": (C.c_int, [C.c_void_p, C.POINTER(C.c_void_p), C.POINTER(C.c_void_p)]),
+    "zs_hallucination_report": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64, C.c_uint64, C.c_float, C.c_float,
+                                          C.POINTER(HallucReport)]),
+    "zs_hallucination_json": (C.c_int, [C.POINTER(HallucReport), C.c_float, C.c_char_p, C.c_size_t,
+                                        C.POINTER(C.c_size_t)]),
+    "zs_logprobs_json": (C.c_int, [C.c_int, C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p,
+                                   C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_char_p, C.c_size_t,
+                                   C.POINTER(C.c_size_t)]),
     "zs_tool_call_envelope_regex": (C.c_int, [C.POINTER(C.c_char_p), C.POINTER(C.c_char_p), C.c_uint32, C.c_char_p,
                                               C.c_size_t, C.POINTER(C.c_size_t), C.c_char_p, C.c_size_t]),
 }

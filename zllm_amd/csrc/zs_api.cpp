@@ -65,9 +65,16 @@ extern "C" void zs_ctx_destroy(zs_ctx* ctx) {
     if (ctx->fork_event) (void)hipEventDestroy((hipEvent_t)ctx->fork_event);
     if (ctx->join_event) (void)hipEventDestroy((hipEvent_t)ctx->join_event);
     if (ctx->side_stream) (void)hipStreamDestroy((hipStream_t)ctx->side_stream);
+    if (ctx->lane_event) {
+        (void)hipEventSynchronize((hipEvent_t)ctx->lane_event);
+        (void)hipEventDestroy((hipEvent_t)ctx->lane_event);
+    }
+    if (ctx->lane_host) (void)hipHostFree(ctx->lane_host);
     void* ptrs[] = {ctx->p_cnt, ctx->p_id, ctx->p_flags, ctx->p_y, ctx->cst, ctx->cs_key, ctx->cs_idx,
                     ctx->co_key, ctx->co_idx, ctx->rst, ctx->pairs, ctx->pv, ctx->mask_scratch, ctx->spec_chunks,
-                    ctx->spec_rows, ctx->sub_mom, ctx->sub_sum, ctx->p_sub, ctx->k_ap, ctx->k_sum};
+                    ctx->spec_rows, ctx->sub_mom, ctx->sub_sum, ctx->p_sub, ctx->k_ap, ctx->k_sum,
+                    ctx->lane_temp, ctx->lane_topk, ctx->lane_topp, ctx->lane_seed, ctx->lane_vals,
+                    ctx->lane_idxs};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
     (void)hipSetDevice(dev);
@@ -121,6 +128,21 @@ extern "C" int zs_ctx_create(int device, uint32_t max_rows, uint32_t max_vocab, 
     if (!rc) rc = zs_alloc(ctx, &ctx->k_ap, R * ctx->max_subs);
     if (!rc) rc = zs_alloc(ctx, &ctx->k_sum, R * 2 * ctx->max_subs);
     if (!rc) rc = zs_alloc(ctx, &ctx->spec_rows, R);
+    if (!rc) rc = zs_alloc(ctx, &ctx->lane_temp, R);
+    if (!rc) rc = zs_alloc(ctx, &ctx->lane_topk, R);
+    if (!rc) rc = zs_alloc(ctx, &ctx->lane_topp, R);
+    if (!rc) rc = zs_alloc(ctx, &ctx->lane_seed, R);
+    if (!rc) rc = zs_alloc(ctx, &ctx->lane_vals, R * ZS_LANE_K);
+    if (!rc) rc = zs_alloc(ctx, &ctx->lane_idxs, R * ZS_LANE_K);
+    if (!rc) {
+        void* h = nullptr;
+        hipEvent_t e = nullptr;
+        if (hipHostMalloc(&h, 4 * R * sizeof(uint32_t), hipHostMallocDefault) != hipSuccess ||
+            hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess)
+            rc = ZS_ENOMEM;
+        ctx->lane_host = (uint32_t*)h;
+        ctx->lane_event = e;
+    }
     if (!rc) {
         hipStream_t s2 = nullptr;
         hipEvent_t e1 = nullptr, e2 = nullptr;
@@ -644,3 +666,62 @@ extern "C" int zs_lane_sample_topk(zs_ctx* ctx, const float* d_vals, const uint3
 }
 
 extern "C" uint32_t zs_step_seed(uint32_t base, uint32_t gen_idx) { return base + gen_idx * 0x9E3779B1u; }
+
+// ContinuousBatcher::step's token selection (gpu/batch.rs:176-192) with the
+// CPU nucleus over the read-back top-64 pool (gpu/mod.rs:2213-2229) moved to
+// the device: one call, m ids out, nothing read back.
+extern "C" int zs_lane_step(zs_ctx* ctx, const float* d_logits, uint32_t m, uint32_t V, uint64_t ld,
+                            const zs_lane_stream* h_streams, uint32_t* d_out, int* path, void* stream) {
+    int rc = lane_check(ctx, m, V, ld, d_logits, "zs_lane_step");
+    if (rc) return rc;
+    if (!d_out || (m && !h_streams)) return zs_set_error(ctx, ZS_EINVAL, "zs_lane_step: null argument");
+    if (m > ctx->max_rows) return zs_set_error(ctx, ZS_ELIMIT, "zs_lane_step: m=%u > max_rows=%u", m, ctx->max_rows);
+    if (V == 0) return zs_set_error(ctx, ZS_EINVAL, "zs_lane_step: V == 0");
+    // the cheapest path that serves every stream: top-K > temperature > greedy
+    int p = ZS_LANE_ARGMAX;
+    for (uint32_t i = 0; i < m; i++) {
+        const zs_lane_stream& s = h_streams[i];
+        if (s.top_k > 0 || (s.top_p > 0.0f && s.top_p < 1.0f)) { p = ZS_LANE_TOPK; break; }  // needs_topk
+        if (s.temp > 0.0f) p = ZS_LANE_SAMPLE;
+    }
+    if (path) *path = p;
+    if (m == 0) return ZS_OK;
+    const hipStream_t st = (hipStream_t)stream;
+    const int prev = zs_device_guard_begin(ctx);
+    if (p != ZS_LANE_ARGMAX) {
+        // the staging area is reused: wait for the previous call's copy
+        if (hipEventSynchronize((hipEvent_t)ctx->lane_event) != hipSuccess) rc = ZS_EHIP;
+        const size_t R = ctx->max_rows;
+        float* ht = (float*)ctx->lane_host;
+        uint32_t* hk = ctx->lane_host + R;
+        float* hp = (float*)(ctx->lane_host + 2 * R);
+        uint32_t* hs = ctx->lane_host + 3 * R;
+        for (uint32_t i = 0; i < m; i++) {
+            ht[i] = h_streams[i].temp;
+            hk[i] = h_streams[i].top_k;
+            hp[i] = h_streams[i].top_p;
+            hs[i] = zs_step_seed(h_streams[i].base_seed, h_streams[i].gen_index);
+        }
+        if (!rc && (hipMemcpyAsync(ctx->lane_temp, ht, m * 4, hipMemcpyHostToDevice, st) != hipSuccess ||
+                    hipMemcpyAsync(ctx->lane_topk, hk, m * 4, hipMemcpyHostToDevice, st) != hipSuccess ||
+                    hipMemcpyAsync(ctx->lane_topp, hp, m * 4, hipMemcpyHostToDevice, st) != hipSuccess ||
+                    hipMemcpyAsync(ctx->lane_seed, hs, m * 4, hipMemcpyHostToDevice, st) != hipSuccess ||
+                    hipEventRecord((hipEvent_t)ctx->lane_event, st) != hipSuccess))
+            rc = ZS_EHIP;
+    }
+    if (!rc) {
+        if (p == ZS_LANE_ARGMAX)
+            rc = zs_lane_argmax_launch(d_logits, m, V, ld, nullptr, nullptr, d_out, st);
+        else if (p == ZS_LANE_SAMPLE)
+            rc = zs_lane_argmax_launch(d_logits, m, V, ld, ctx->lane_temp, ctx->lane_seed, d_out, st);
+        else {
+            rc = zs_lane_topk_launch(d_logits, m, V, ld, ZS_LANE_K, ctx->lane_vals, ctx->lane_idxs, st);
+            if (!rc)
+                rc = zs_lane_sample_topk_launch(ctx->lane_vals, ctx->lane_idxs, m, ZS_LANE_K, ctx->lane_temp,
+                                                ctx->lane_topk, ctx->lane_topp, ctx->lane_seed, d_out, st);
+        }
+        if (rc) rc = ZS_EHIP;
+    }
+    zs_device_guard_end(ctx, prev);
+    return rc ? zs_set_error(ctx, rc, "zs_lane_step: %s", hipGetErrorString(hipGetLastError())) : ZS_OK;
+}

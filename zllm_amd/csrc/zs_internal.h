@@ -21,6 +21,8 @@
 #define ZS_BIG_NT 1024
 #define ZS_BIG_G 4096
 #define ZS_SORT_CAP 32768
+// top-K pool of the batched lane (gpu/mod.rs:1846 TOPK_K)
+#define ZS_LANE_K 64
 
 // Patch flags (merged bias / count-map / ban list, one entry per token id).
 #define ZS_PF_BAN 1u
@@ -185,6 +187,16 @@ struct zs_ctx {
     int n_timed;
     void* events[16];      // hipEvent_t
     const char* timed_names[16];
+    // batched lane (zs_lane_step): per-stream knobs staged through pinned
+    // host memory, top-K pool of every stream
+    float* lane_temp;            // [rows]
+    uint32_t* lane_topk;         // [rows]
+    float* lane_topp;            // [rows]
+    uint32_t* lane_seed;         // [rows]
+    float* lane_vals;            // [rows][ZS_LANE_K]
+    uint32_t* lane_idxs;         // [rows][ZS_LANE_K]
+    uint32_t* lane_host;         // pinned [4][rows]: temp, top_k, top_p, seed
+    void* lane_event;            // hipEvent_t: staging copy of the last call done
     int n_spec_timed;      // the same for the last zs_spec_verify call
     void* spec_events[8];
     const char* spec_names[8];

@@ -1,5 +1,6 @@
-// zs_json.h -- a small strict JSON reader (RFC 8259) for the host-side
-// compilers (zs_schema.cpp, zs_tokens.cpp). Object members stay in document
+// zs_json.h -- a small strict JSON reader (RFC 8259) and the pieces of a
+// serde_json-compatible writer for the host-side code (zs_schema.cpp,
+// zs_tokens.cpp, zs_wire.cpp). Object members stay in document
 // order; a repeated key replaces the value in its first position (serde_json
 // with `preserve_order`, the reference's build, Cargo.toml:34). Numbers are
 // classified as serde_json does: non-negative / negative integers that fit 64
@@ -8,6 +9,7 @@
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
+#include <charconv>
 #include <cmath>
 #include <string>
 #include <utility>
@@ -214,5 +216,68 @@ private:
         return v;
     }
 };
+
+// ---------------------------------------------------------------- writer
+// ryu's layout of the shortest round-trip digits (serde_json's f64 output)
+inline std::string f64_text(double d) {
+    if (d == 0.0) return std::signbit(d) ? "-0.0" : "0.0";
+    std::string out;
+    if (d < 0) { out += '-'; d = -d; }
+    char buf[64];
+    auto r = std::to_chars(buf, buf + sizeof buf, d, std::chars_format::scientific);
+    std::string sci(buf, r.ptr);
+    const size_t e = sci.find('e');
+    std::string digits;
+    for (size_t i = 0; i < e; i++)
+        if (sci[i] != '.') digits += sci[i];
+    const int sexp = atoi(sci.c_str() + e + 1);
+    const int length = (int)digits.size();
+    const int kk = sexp + 1;          // 10^(kk-1) <= v < 10^kk
+    const int k = kk - length;        // exponent of the last digit
+    if (k >= 0 && kk <= 16) {
+        out += digits;
+        out.append((size_t)(kk - length), '0');
+        out += ".0";
+    } else if (kk > 0 && kk <= 16) {
+        out += digits.substr(0, (size_t)kk);
+        out += '.';
+        out += digits.substr((size_t)kk);
+    } else if (kk > -5 && kk <= 0) {
+        out += "0.";
+        out.append((size_t)(-kk), '0');
+        out += digits;
+    } else if (length == 1) {
+        out += digits;
+        out += 'e';
+        out += std::to_string(kk - 1);
+    } else {
+        out += digits[0];
+        out += '.';
+        out += digits.substr(1);
+        out += 'e';
+        out += std::to_string(kk - 1);
+    }
+    return out;
+}
+
+inline void write_str(std::string& o, const std::string& s) {
+    static const char hex[] = "0123456789abcdef";
+    o += '"';
+    for (unsigned char c : s) {
+        switch (c) {
+            case '"': o += "\\\""; break;
+            case '\\': o += "\\\\"; break;
+            case '\b': o += "\\b"; break;
+            case '\f': o += "\\f"; break;
+            case '\n': o += "\\n"; break;
+            case '\r': o += "\\r"; break;
+            case '\t': o += "\\t"; break;
+            default:
+                if (c < 0x20) { o += "\\u00"; o += hex[c >> 4]; o += hex[c & 15]; }
+                else o += (char)c;
+        }
+    }
+    o += '"';
+}
 
 }  // namespace zsj

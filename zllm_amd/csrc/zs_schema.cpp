@@ -10,7 +10,6 @@
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
-#include <charconv>
 #include <cmath>
 #include <string>
 #include <utility>
@@ -21,70 +20,10 @@
 using zsj::JV;
 using zsj::JsonError;
 using zsj::Reader;
+using zsj::f64_text;
+using zsj::write_str;
 
 namespace {
-
-// ryu's layout of the shortest round-trip digits (serde_json's f64 output)
-std::string f64_text(double d) {
-    if (d == 0.0) return std::signbit(d) ? "-0.0" : "0.0";
-    std::string out;
-    if (d < 0) { out += '-'; d = -d; }
-    char buf[64];
-    auto r = std::to_chars(buf, buf + sizeof buf, d, std::chars_format::scientific);
-    std::string sci(buf, r.ptr);
-    const size_t e = sci.find('e');
-    std::string digits;
-    for (size_t i = 0; i < e; i++)
-        if (sci[i] != '.') digits += sci[i];
-    const int sexp = atoi(sci.c_str() + e + 1);
-    const int length = (int)digits.size();
-    const int kk = sexp + 1;          // 10^(kk-1) <= v < 10^kk
-    const int k = kk - length;        // exponent of the last digit
-    if (k >= 0 && kk <= 16) {
-        out += digits;
-        out.append((size_t)(kk - length), '0');
-        out += ".0";
-    } else if (kk > 0 && kk <= 16) {
-        out += digits.substr(0, (size_t)kk);
-        out += '.';
-        out += digits.substr((size_t)kk);
-    } else if (kk > -5 && kk <= 0) {
-        out += "0.";
-        out.append((size_t)(-kk), '0');
-        out += digits;
-    } else if (length == 1) {
-        out += digits;
-        out += 'e';
-        out += std::to_string(kk - 1);
-    } else {
-        out += digits[0];
-        out += '.';
-        out += digits.substr(1);
-        out += 'e';
-        out += std::to_string(kk - 1);
-    }
-    return out;
-}
-
-void write_str(std::string& o, const std::string& s) {
-    static const char hex[] = "0123456789abcdef";
-    o += '"';
-    for (unsigned char c : s) {
-        switch (c) {
-            case '"': o += "\\\""; break;
-            case '\\': o += "\\\\"; break;
-            case '\b': o += "\\b"; break;
-            case '\f': o += "\\f"; break;
-            case '\n': o += "\\n"; break;
-            case '\r': o += "\\r"; break;
-            case '\t': o += "\\t"; break;
-            default:
-                if (c < 0x20) { o += "\\u00"; o += hex[c >> 4]; o += hex[c & 15]; }
-                else o += (char)c;
-        }
-    }
-    o += '"';
-}
 
 // compact serialization (serde_json::to_string)
 void write_json(std::string& o, const JV& v) {

@@ -33,6 +33,10 @@ struct zs_token_table {
     std::vector<uint8_t> bytes;
     std::vector<uint8_t> valid;
     int64_t eos = -1;
+    // decode([id]) text of every id, U+FFFD pieces and "" of specials
+    // included (what the logprobs JSON shows, rest.rs:1714)
+    std::vector<uint32_t> text_offsets;
+    std::vector<uint8_t> text;
 };
 
 namespace {
@@ -372,10 +376,13 @@ struct Vocab {
         for (auto& kv : added_tok_to_id)
             if (!model_tok_to_id.count(kv.first)) n++;
         tt.offsets.assign(1, 0);
+        tt.text_offsets.assign(1, 0);
         tt.valid.assign(n, 0);
         std::string s;
         for (size_t id = 0; id < n; id++) {
             decode((uint32_t)id, s);
+            tt.text.insert(tt.text.end(), s.begin(), s.end());
+            tt.text_offsets.push_back((uint32_t)tt.text.size());
             if (!s.empty() && s.find("\xEF\xBF\xBD") == std::string::npos) {
                 tt.valid[id] = 1;
                 tt.bytes.insert(tt.bytes.end(), s.begin(), s.end());
@@ -609,4 +616,10 @@ extern "C" int zs_token_table_info(const zs_token_table* t, uint32_t* ntab, uint
 extern "C" const uint32_t* zs_token_table_offsets(const zs_token_table* t) { return t ? t->offsets.data() : nullptr; }
 extern "C" const uint8_t* zs_token_table_bytes(const zs_token_table* t) { return t ? t->bytes.data() : nullptr; }
 extern "C" const uint8_t* zs_token_table_valid(const zs_token_table* t) { return t ? t->valid.data() : nullptr; }
+extern "C" int zs_token_table_text(const zs_token_table* t, const uint32_t** offsets, const uint8_t** bytes) {
+    if (!t || !offsets || !bytes) return ZS_EINVAL;
+    *offsets = t->text_offsets.data();
+    *bytes = t->text.data();
+    return ZS_OK;
+}
 extern "C" void zs_token_table_destroy(zs_token_table* t) { delete t; }

@@ -16,7 +16,7 @@ from typing import Dict, List, Optional, Sequence, Tuple
 import numpy as np
 import torch
 
-from ._lib import (Batch, RowParams, SpecBatch, ZS_OK, ZS_ROW_LOGPROBS, ZS_ROW_MASKED, ZS_ROW_UNCERTAINTY, ZsError, lib)
+from ._lib import (Batch, LaneStream, RowParams, SpecBatch, ZS_OK, ZS_ROW_LOGPROBS, ZS_ROW_MASKED, ZS_ROW_UNCERTAINTY, ZsError, lib)
 
 OPENAI_TOP_LOGPROBS_CAP = 20  # logprobs.rs:27-29
 
@@ -482,3 +482,87 @@ def lane_sample_topk(ctx: Context, vals: torch.Tensor, idxs: torch.Tensor, tempe
 def step_seed(base: int, gen_idx: int) -> int:
     """gpu/sampling.rs:9."""
     return int(lib().zs_step_seed(base & 0xFFFFFFFF, gen_idx & 0xFFFFFFFF))
+
+
+# ---------------------------------------------------------------- continuous-batching lane
+ZS_LANE_ARGMAX, ZS_LANE_SAMPLE, ZS_LANE_TOPK = 0, 1, 2
+
+
+@dataclass
+class SamplingParams:
+    """gpu/sampling.rs:14-21: temp <= 0 greedy; top_k 0 = no cap; top_p >= 1
+    (or 0) = no nucleus cut (both applied inside the top-64 pool)."""
+    temp: float = 0.0
+    top_k: int = 0
+    top_p: float = 1.0
+
+    @staticmethod
+    def greedy():
+        return SamplingParams(0.0, 0, 1.0)
+
+    @staticmethod
+    def temperature(temp: float):
+        return SamplingParams(temp, 0, 1.0)
+
+    def needs_topk(self) -> bool:  # gpu/sampling.rs:20
+        return self.top_k > 0 or (0.0 < self.top_p < 1.0)
+
+
+@dataclass
+class LaneSeq:
+    """The sampling state of CbSeq (gpu/batch.rs): tokens generated so far
+    (the prefill's first token included), limits and seeding."""
+    id: int
+    params: SamplingParams
+    base_seed: int
+    eos: int
+    max_tokens: int
+    generated: List[int] = field(default_factory=list)
+
+    def gen_index(self) -> int:
+        return len(self.generated)
+
+
+class LaneBatcher:
+    """ContinuousBatcher::step's token selection (gpu/batch.rs:176-207) on
+    libzs: the caller runs the model forward for the active streams (in
+    `active` order) and hands the logits [m, V] to step(), which picks every
+    stream's next token on the GPU with one zs_lane_step call (top-64 pool +
+    nucleus / Gumbel sampling / argmax, seeds step_seed(base, gen_index)),
+    reads back m ids and retires finished streams as the reference does."""
+
+    def __init__(self, ctx: Context):
+        self.ctx = ctx
+        self.active: List[LaneSeq] = []
+        self.last_path = None
+
+    def add(self, seq: LaneSeq):
+        self.active.append(seq)
+
+    def select(self, logits: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Device ids for the active streams (no host sync)."""
+        m, V = logits.shape
+        assert m == len(self.active) and logits.dtype == torch.float32 and logits.stride(1) == 1
+        if out is None:
+            out = torch.empty(m, dtype=torch.int32, device=logits.device)
+        st = (LaneStream * max(m, 1))()
+        for i, s in enumerate(self.active):
+            st[i].temp, st[i].top_k, st[i].top_p = s.params.temp, s.params.top_k, s.params.top_p
+            st[i].base_seed, st[i].gen_index = s.base_seed & 0xFFFFFFFF, s.gen_index() & 0xFFFFFFFF
+        path = C.c_int()
+        stream = torch.cuda.current_stream(logits.device).cuda_stream
+        rc = lib().zs_lane_step(self.ctx.h, logits.data_ptr(), m, V, logits.stride(0), st, out.data_ptr(),
+                                C.byref(path), stream)
+        _check(self.ctx.h, rc, "zs_lane_step")
+        self.last_path = path.value
+        return out
+
+    def step(self, logits: torch.Tensor) -> List[Tuple[int, int, bool]]:
+        """(id, token, done) per active stream; finished streams leave the batch."""
+        ids = self.select(logits).cpu().numpy().view(np.uint32)
+        res = []
+        for s, t in zip(self.active, ids):
+            s.generated.append(int(t))
+            res.append((s.id, int(t), int(t) == s.eos or s.gen_index() >= s.max_tokens))
+        self.active = [s for s in self.active if not (s.generated[-1] == s.eos or s.gen_index() >= s.max_tokens)]
+        return res

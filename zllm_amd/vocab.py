@@ -33,8 +33,18 @@ class HostTokenTable:
             self.data = arr(lib().zs_token_table_bytes(h), C.c_uint8, nb.value)
             self.valid = arr(lib().zs_token_table_valid(h), C.c_uint8, n.value)
             self.eos = None if eos.value < 0 else int(eos.value)
+            to, tb = C.c_void_p(), C.c_void_p()
+            lib().zs_token_table_text(h, C.byref(to), C.byref(tb))
+            self.text_offsets = arr(to.value, C.c_uint32, n.value + 1)
+            self.text = arr(tb.value, C.c_uint8, int(self.text_offsets[-1]))
         finally:
             lib().zs_token_table_destroy(h)
+
+    def decode_text(self, i: int) -> str:
+        """decode([i]) (special tokens skipped, lossy UTF-8), as shown in logprobs."""
+        if i >= self.ntab:
+            return ""
+        return bytes(self.text[self.text_offsets[i]:self.text_offsets[i + 1]]).decode("utf-8")
 
     def tokens(self) -> List[Optional[bytes]]:
         return [bytes(self.data[self.offsets[i]:self.offsets[i + 1]]) if self.valid[i] else None
