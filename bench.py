@@ -116,6 +116,42 @@ def spec_bytes_per_row(V, k):
     return 4 * V * (2 * k + 1) + 4 * k + 8
 
 
+def lane_step_us(ctx, xs, params):
+    """Mean time of one zs_lane_step over the C5 batch for each lane path:
+    top-64 pool + nucleus (the C5 knobs), Gumbel sampling (temperatures
+    only) and argmax (greedy)."""
+    import ctypes as C
+    import torch
+    from zllm_amd._lib import LaneStream, lib
+    B, V = xs.shape
+    out = torch.empty(B, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream()
+    res = {}
+    for name in ("topk", "sample", "argmax"):
+        st = (LaneStream * B)()
+        for i, p in enumerate(params):
+            st[i].temp = 0.0 if name == "argmax" else p["temperature"]
+            st[i].top_k = p["top_k"] if name == "topk" else 0
+            st[i].top_p = p["top_p"] if name == "topk" else 1.0
+            st[i].base_seed, st[i].gen_index = 1000 + i, 3
+        path = C.c_int()
+
+        def call():
+            rc = lib().zs_lane_step(ctx.h, xs.data_ptr(), B, V, xs.stride(0), st, out.data_ptr(), C.byref(path),
+                                    stream.cuda_stream)
+            assert rc == 0
+        for _ in range(3):
+            call()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(20):
+            call()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        res[name] = round(e0.elapsed_time(e1) / 20 * 1000.0, 2)
+    return res
+
+
 def mask_config_us(ctx, V, rows, kind, S, seed):
     """Mean time of zs_dfa_mask over `rows` constrained rows (random current
     states) for one DFA config; synthetic vocabulary as in config C3."""
@@ -127,6 +163,11 @@ def mask_config_us(ctx, V, rows, kind, S, seed):
     table = TokenByteTable.from_csr(ctx, offs, data, np.ones(V, np.uint8), eos=V - 1)
     if kind == "random":
         trans, dead, acc = synth.random_dfa(S, seed + S, dead_rate=0.3)
+    elif kind == "compiled":
+        # the `json:` grammar (any JSON value, depth 5) through the native compiler
+        from zllm_amd import grammar as G
+        g = G.HostDfa(G.any_json_regex_default())
+        trans, dead, acc = g.trans, g.dead, g.accept
     else:
         trans, dead, acc = synth.json_dfa(S, seed + S)
     dfa = ByteDfa(ctx, trans, dead, acc)
@@ -232,6 +273,9 @@ def main():
     dfa_cfg = {"c5_json512": None, "c3_random64": mask_config_us(ctx, 128256, 32, "random", 64, args.seed),
                "c4_json2048": mask_config_us(ctx, 151936, 128, "json", 2048, args.seed)}
 
+    dfa_cfg["json_any_compiled"] = mask_config_us(ctx, 151936, 128, "compiled", 0, args.seed)
+    lane_us = lane_step_us(ctx, xs, W["params"])
+
     # spec verify alone (separate, untimed loop)
     s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     s0.record(stream)
@@ -304,8 +348,10 @@ def main():
         "step_hbm_frac": round(step_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "dfa_mask_us": round(us_mask, 2),
         "dfa_mask_us_configs": {"c5_json512": round(us_mask, 2), "c3_random64": round(dfa_cfg["c3_random64"], 2),
-                                "c4_json2048": round(dfa_cfg["c4_json2048"], 2)},
+                                "c4_json2048": round(dfa_cfg["c4_json2048"], 2),
+                                "json_any_compiled": round(dfa_cfg["json_any_compiled"], 2)},
         "spec_verify_us": round(us_spec, 2),
+        "lane_step_us": lane_us,
         "kernel_ms": {k: round(v, 4) for k, v in acc.items()},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC.get(dom),

@@ -16,7 +16,8 @@ extern "C" int zs_spec_launch(const zs_spec_args& a, const zs_prof& prof, hipStr
 extern "C" int zs_lane_argmax_launch(const float* logits, uint32_t B, uint32_t V, uint64_t ld, const float* temp,
                                      const uint32_t* seed, uint32_t* out, hipStream_t stream);
 extern "C" int zs_lane_topk_launch(const float* logits, uint32_t B, uint32_t V, uint64_t ld, uint32_t K,
-                                   float* vals, uint32_t* idxs, hipStream_t stream);
+                                   float* vals, uint32_t* idxs, unsigned long long* ck, uint32_t* cn,
+                                   hipStream_t stream);
 extern "C" int zs_lane_sample_topk_launch(const float* vals, const uint32_t* idxs, uint32_t B, uint32_t K,
                                           const float* temp, const uint32_t* top_k, const float* top_p,
                                           const uint32_t* seed, uint32_t* out, hipStream_t stream);
@@ -74,7 +75,7 @@ extern "C" void zs_ctx_destroy(zs_ctx* ctx) {
                     ctx->co_key, ctx->co_idx, ctx->rst, ctx->pairs, ctx->pv, ctx->mask_scratch, ctx->spec_chunks,
                     ctx->spec_rows, ctx->sub_mom, ctx->sub_sum, ctx->p_sub, ctx->k_ap, ctx->k_sum,
                     ctx->lane_temp, ctx->lane_topk, ctx->lane_topp, ctx->lane_seed, ctx->lane_vals,
-                    ctx->lane_idxs};
+                    ctx->lane_idxs, ctx->lane_ck, ctx->lane_cn};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
     (void)hipSetDevice(dev);
@@ -134,6 +135,8 @@ extern "C" int zs_ctx_create(int device, uint32_t max_rows, uint32_t max_vocab, 
     if (!rc) rc = zs_alloc(ctx, &ctx->lane_seed, R);
     if (!rc) rc = zs_alloc(ctx, &ctx->lane_vals, R * ZS_LANE_K);
     if (!rc) rc = zs_alloc(ctx, &ctx->lane_idxs, R * ZS_LANE_K);
+    if (!rc) rc = zs_alloc(ctx, &ctx->lane_ck, R * C * ZS_LANE_K);
+    if (!rc) rc = zs_alloc(ctx, &ctx->lane_cn, R * C);
     if (!rc) {
         void* h = nullptr;
         hipEvent_t e = nullptr;
@@ -646,7 +649,9 @@ extern "C" int zs_lane_topk(zs_ctx* ctx, const float* d_logits, uint32_t B, uint
     if (K == 0 || K > 1024) return zs_set_error(ctx, ZS_ELIMIT, "zs_lane_topk: K=%u outside 1..1024", K);
     if (B == 0) return ZS_OK;
     int prev = zs_device_guard_begin(ctx);
-    rc = zs_lane_topk_launch(d_logits, B, V, ld, K, d_vals, d_idxs, (hipStream_t)stream);
+    const bool fits = B <= ctx->max_rows && V <= ctx->max_vocab;
+    rc = zs_lane_topk_launch(d_logits, B, V, ld, K, d_vals, d_idxs, fits ? ctx->lane_ck : nullptr,
+                             fits ? ctx->lane_cn : nullptr, (hipStream_t)stream);
     zs_device_guard_end(ctx, prev);
     return rc ? zs_set_error(ctx, ZS_EHIP, "zs_lane_topk: launch failed") : ZS_OK;
 }
@@ -715,7 +720,8 @@ extern "C" int zs_lane_step(zs_ctx* ctx, const float* d_logits, uint32_t m, uint
         else if (p == ZS_LANE_SAMPLE)
             rc = zs_lane_argmax_launch(d_logits, m, V, ld, ctx->lane_temp, ctx->lane_seed, d_out, st);
         else {
-            rc = zs_lane_topk_launch(d_logits, m, V, ld, ZS_LANE_K, ctx->lane_vals, ctx->lane_idxs, st);
+            rc = zs_lane_topk_launch(d_logits, m, V, ld, ZS_LANE_K, ctx->lane_vals, ctx->lane_idxs,
+                                     V <= ctx->max_vocab ? ctx->lane_ck : nullptr, ctx->lane_cn, st);
             if (!rc)
                 rc = zs_lane_sample_topk_launch(ctx->lane_vals, ctx->lane_idxs, m, ZS_LANE_K, ctx->lane_temp,
                                                 ctx->lane_topk, ctx->lane_topp, ctx->lane_seed, d_out, st);

@@ -195,6 +195,8 @@ struct zs_ctx {
     uint32_t* lane_seed;         // [rows]
     float* lane_vals;            // [rows][ZS_LANE_K]
     uint32_t* lane_idxs;         // [rows][ZS_LANE_K]
+    unsigned long long* lane_ck; // [rows][chunks][ZS_LANE_K] chunk top-K lists (two-phase BTOPK)
+    uint32_t* lane_cn;           // [rows][chunks]
     uint32_t* lane_host;         // pinned [4][rows]: temp, top_k, top_p, seed
     void* lane_event;            // hipEvent_t: staging copy of the last call done
     int n_spec_timed;      // the same for the last zs_spec_verify call

@@ -189,6 +189,196 @@ __global__ __launch_bounds__(LN_NT) void zs_k_btopk(const float* logits, uint32_
     }
 }
 
+// Two-phase BTOPK for K <= 64: every 8192-id chunk keeps its own top-K by
+// (key desc, id asc) -- a superset of the row's top-K restricted to the chunk
+// -- and one workgroup per row sorts the chunk lists. Same result as
+// zs_k_btopk; one read of the row over the whole chip instead of six passes
+// by one workgroup.
+#define TC_NT 256
+#define TC_CH 8192
+#define TC_EPT (TC_CH / TC_NT)
+#define TC_SORT 256
+#define TC_K 64
+#define TC_MAXCH 32
+__global__ __launch_bounds__(TC_NT) void zs_k_btopk_chunks(const float* logits, uint32_t V, uint64_t ld, uint32_t K,
+                                                            unsigned long long* ck, uint32_t* cn, uint32_t nch) {
+    __shared__ uint32_t tmax[TC_NT];
+    __shared__ unsigned long long s64[TC_SORT];
+    __shared__ uint32_t hist[256];
+    __shared__ uint32_t u[4];
+    __shared__ uint32_t scan_sh[TC_NT / 64];
+    const uint32_t c = blockIdx.x, r = blockIdx.y;
+    const int t = threadIdx.x, lane = zs_lane(), wid = zs_wid();
+    const uint32_t base = c * TC_CH;
+    const float* row = logits + (size_t)r * ld;
+    unsigned long long* out = ck + ((size_t)r * nch + c) * TC_K;
+    // keys of the thread's elements: float4 j covers ids base + (j*NT + t)*4 .. +3;
+    // 0 for ids past V and for non-candidates (below every candidate key)
+    uint32_t key[TC_EPT];
+#pragma unroll
+    for (int j = 0; j < TC_EPT / 4; j++) {
+        const uint32_t id = base + (j * TC_NT + t) * 4;
+        float4 v = make_float4(NAN, NAN, NAN, NAN);
+        if (id + 3 < V) v = *reinterpret_cast<const float4*>(row + id);
+        else {
+            if (id < V) v.x = row[id];
+            if (id + 1 < V) v.y = row[id + 1];
+            if (id + 2 < V) v.z = row[id + 2];
+        }
+        const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int q = 0; q < 4; q++) key[4 * j + q] = tk_cand(vv[q]) ? tk_key(vv[q]) : 0u;
+    }
+    auto idx_of = [&](int e) { return base + ((e >> 2) * TC_NT + t) * 4 + (e & 3); };
+    uint32_t tm = 0;
+#pragma unroll
+    for (int e = 0; e < TC_EPT; e++) tm = max(tm, key[e]);
+    // theta: the K-th largest of the 256 thread maxima (maxima of distinct
+    // elements, so at least K keys are >= theta when K threads hold one)
+    const uint32_t srt = wave_sort_u32(tm);
+    tmax[wid * 64 + lane] = srt;
+    __syncthreads();
+    if (t < 64) {
+        uint32_t m = srt;
+#pragma unroll
+        for (int w = 1; w < TC_NT / 64; w++) {
+            m = max(m, tmax[w * 64 + 63 - lane]);
+#pragma unroll
+            for (int j = 32; j > 0; j >>= 1) {
+                const uint32_t o = __shfl_xor(m, j, 64);
+                m = (lane & j) ? max(m, o) : min(m, o);
+            }
+        }
+        if (lane == 64 - (int)K) u[0] = m;
+    }
+    __syncthreads();
+    const uint32_t theta = max(u[0], 1u);
+    uint32_t cnt = 0;
+#pragma unroll
+    for (int e = 0; e < TC_EPT; e++) cnt += key[e] >= theta ? 1u : 0u;
+    uint32_t nsup;
+    uint32_t pos = block_excl_scan_u<TC_NT>(cnt, scan_sh, &nsup);
+    if (nsup <= TC_SORT) {
+#pragma unroll
+        for (int e = 0; e < TC_EPT; e++)
+            if (key[e] >= theta) s64[pos++] = ((unsigned long long)(~key[e]) << 32) | idx_of(e);
+        __syncthreads();
+        const uint32_t n = min(K, nsup);
+        if (nsup <= 64) {
+            if (t < 64) {
+                unsigned long long v = (uint32_t)t < nsup ? s64[t] : ~0ull;
+                v = wave_sort_u64(v);
+                if ((uint32_t)t < n) out[t] = v;
+            }
+        } else {
+            for (uint32_t i = nsup + t; i < TC_SORT; i += TC_NT) s64[i] = ~0ull;
+            __syncthreads();
+            block_bitonic_u64<TC_NT>(s64, TC_SORT);
+            if ((uint32_t)t < n) out[t] = s64[t];
+        }
+        if (t == 0) cn[(size_t)r * nch + c] = n;
+        return;
+    }
+    // many keys tie near theta: exact K-th key by an 8-bit radix select, then
+    // the keys above it and the lowest ids among the keys equal to it
+    uint32_t ncand = 0;
+#pragma unroll
+    for (int e = 0; e < TC_EPT; e++) ncand += key[e] ? 1u : 0u;
+    ncand = block_sum_u<TC_NT>(ncand, scan_sh);
+    const uint32_t KK = min(K, ncand);
+    uint32_t prefix = 0, mask = 0, need = KK;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        hist[t] = 0;
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < TC_EPT; e++)
+            if (key[e] && (key[e] & mask) == prefix) atomicAdd(&hist[(key[e] >> shift) & 255u], 1u);
+        __syncthreads();
+        if (t < 64) {
+            uint32_t cc[4], loc = 0;
+            for (int q = 0; q < 4; q++) { cc[q] = hist[255 - 4 * t - q]; loc += cc[q]; }
+            uint32_t inc = wave_incl_scan_u(loc);
+            uint32_t before = inc - loc;
+            for (int q = 0; q < 4; q++) {
+                if (before < need && need <= before + cc[q]) { u[1] = 255 - 4 * t - q; u[2] = need - before; }
+                before += cc[q];
+            }
+        }
+        __syncthreads();
+        prefix |= u[1] << shift;
+        mask |= 0xffu << shift;
+        need = u[2];
+        __syncthreads();
+    }
+    if (t == 0) u[3] = 0;
+    __syncthreads();
+    uint32_t carry = 0;  // the KK chosen keys are gathered in s64, then sorted
+#pragma unroll
+    for (int j = 0; j < TC_EPT / 4; j++) {  // ids ascend with j, then t, then q
+        uint32_t ce = 0;
+#pragma unroll
+        for (int q = 0; q < 4; q++) ce += key[4 * j + q] == prefix ? 1u : 0u;
+        uint32_t tot;
+        uint32_t rank = carry + block_excl_scan_u<TC_NT>(ce, scan_sh, &tot);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const uint32_t k = key[4 * j + q];
+            bool take = k && k > prefix;
+            if (k && k == prefix) { take = rank < need; rank++; }
+            if (take) {
+                const uint32_t p = atomicAdd(&u[3], 1u);
+                if (p < TC_K) s64[p] = ((unsigned long long)(~k) << 32) | idx_of(4 * j + q);
+            }
+        }
+        carry += tot;
+    }
+    __syncthreads();
+    if (t < 64) {
+        unsigned long long v = (uint32_t)t < KK ? s64[t] : ~0ull;
+        v = wave_sort_u64(v);
+        if ((uint32_t)t < KK) out[t] = v;
+    }
+    if (t == 0) cn[(size_t)r * nch + c] = KK;
+}
+
+// One wave per row: the chunk lists are sorted (best first), so the row's
+// best K is a running merge -- the elementwise min of the kept list and the
+// reversed next list holds the 64 best of both as a bitonic sequence, which
+// six exchange steps sort.
+#define TM_ROWS 4
+__global__ __launch_bounds__(64 * TM_ROWS) void zs_k_btopk_merge(const float* logits, uint32_t B, uint64_t ld,
+                                                                  uint32_t K, const unsigned long long* ck,
+                                                                  const uint32_t* cn, uint32_t nch, float* vals,
+                                                                  uint32_t* idxs) {
+    const uint32_t r = blockIdx.x * TM_ROWS + zs_wid();
+    if (r >= B) return;
+    const int lane = zs_lane();
+    unsigned long long cur = ~0ull;
+    for (uint32_t c = 0; c < nch; c++) {
+        const uint32_t n = cn[(size_t)r * nch + c];
+        unsigned long long b = (uint32_t)lane < n ? ck[((size_t)r * nch + c) * TC_K + lane] : ~0ull;
+        b = __shfl(b, 63 - lane, 64);
+        unsigned long long m = b < cur ? b : cur;
+#pragma unroll
+        for (int j = 32; j > 0; j >>= 1) {
+            const unsigned long long o = __shfl_xor(m, j, 64);
+            m = (lane & j) ? (o > m ? o : m) : (o < m ? o : m);
+        }
+        cur = m;
+    }
+    if ((uint32_t)lane < K) {
+        const float* row = logits + (size_t)r * ld;
+        if (cur != ~0ull) {
+            const uint32_t id = (uint32_t)(cur & 0xffffffffull);
+            vals[(size_t)r * K + lane] = row[id];
+            idxs[(size_t)r * K + lane] = id;
+        } else {
+            vals[(size_t)r * K + lane] = -3.0e38f;
+            idxs[(size_t)r * K + lane] = 0xffffffffu;
+        }
+    }
+}
+
 // gpu/sampling.rs:24-31
 __device__ __forceinline__ float zs_rng01(uint32_t seed) {
     uint64_t z = (uint64_t)seed * 0x9E3779B97F4A7C15ull + 0x9E3779B97F4A7C15ull;
@@ -235,20 +425,83 @@ __global__ void zs_k_sample_topk(const float* vals, const uint32_t* idxs, uint32
     out[r] = res;
 }
 
+// The same draw with one wave per row for pools of at most 64: the
+// exponentials in parallel, the sequential sums (sampler order, f32) as
+// broadcast chains.
+__global__ __launch_bounds__(64 * TM_ROWS) void zs_k_sample_topk64(const float* vals, const uint32_t* idxs,
+                                                                    uint32_t B, uint32_t K, const float* temp,
+                                                                    const uint32_t* top_k, const float* top_p,
+                                                                    const uint32_t* seed, uint32_t* out) {
+    const uint32_t r = blockIdx.x * TM_ROWS + zs_wid();
+    if (r >= B) return;
+    const int lane = zs_lane();
+    const float v = (uint32_t)lane < K ? vals[(size_t)r * K + lane] : -INFINITY;
+    const uint32_t id = (uint32_t)lane < K ? idxs[(size_t)r * K + lane] : 0u;
+    const uint32_t id0 = __shfl(id, 0, 64);
+    // n: length of the leading run of values above the sentinel
+    const unsigned long long fail = __ballot(!((uint32_t)lane < K && v > -3.0e37f));
+    const uint32_t n = fail ? (uint32_t)__ffsll((long long)fail) - 1u : 64u;
+    const float T = temp[r];
+    if (n == 0 || T <= 0.0f) {
+        if (lane == 0) out[r] = id0;
+        return;
+    }
+    const uint32_t kk = top_k[r] == 0 ? n : (top_k[r] < n ? top_k[r] : n);
+    const float maxv = __shfl(v, 0, 64);
+    const float e = (uint32_t)lane < kk ? zs_expf((v - maxv) / T) : 0.0f;
+    float z = -0.0f;
+    for (uint32_t i = 0; i < kk; i++) z = z + __shfl(e, (int)i, 64);
+    const float p = e / z;
+    uint32_t cut = kk;
+    const float tp = top_p[r];
+    if (tp > 0.0f && tp < 1.0f) {
+        float cum = 0.0f;
+        for (uint32_t i = 0; i < kk; i++) {
+            cum = cum + __shfl(p, (int)i, 64);
+            if (cum >= tp) { cut = i + 1; break; }
+        }
+    }
+    float zc = -0.0f;
+    for (uint32_t i = 0; i < cut; i++) zc = zc + __shfl(p, (int)i, 64);
+    const float target = zs_rng01(seed[r]) * zc;
+    float acc = 0.0f;
+    uint32_t pick = cut - 1;
+    for (uint32_t i = 0; i < cut; i++) {
+        acc = acc + __shfl(p, (int)i, 64);
+        if (acc >= target) { pick = i; break; }
+    }
+    const uint32_t res = __shfl(id, (int)pick, 64);
+    if (lane == 0) out[r] = res;
+}
+
 extern "C" int zs_lane_argmax_launch(const float* logits, uint32_t B, uint32_t V, uint64_t ld, const float* temp,
                                      const uint32_t* seed, uint32_t* out, hipStream_t stream) {
     hipLaunchKernelGGL(zs_k_bargmax, dim3(B), dim3(LN_NT), 0, stream, logits, V, ld, temp, seed, out);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
+// ck / cn: scratch of at least B * ceil(V / 8192) * 64 keys and B * ceil(V / 8192)
+// counts (two-phase path, K <= 64, V <= 32 * 8192); nullptr forces one pass
 extern "C" int zs_lane_topk_launch(const float* logits, uint32_t B, uint32_t V, uint64_t ld, uint32_t K,
-                                   float* vals, uint32_t* idxs, hipStream_t stream) {
-    hipLaunchKernelGGL(zs_k_btopk, dim3(B), dim3(LN_NT), 0, stream, logits, V, ld, K, vals, idxs);
+                                   float* vals, uint32_t* idxs, unsigned long long* ck, uint32_t* cn,
+                                   hipStream_t stream) {
+    const uint32_t nch = (V + TC_CH - 1) / TC_CH;
+    if (ck && cn && K <= TC_K && nch <= TC_MAXCH) {
+        hipLaunchKernelGGL(zs_k_btopk_chunks, dim3(nch, B), dim3(TC_NT), 0, stream, logits, V, ld, K, ck, cn, nch);
+        hipLaunchKernelGGL(zs_k_btopk_merge, dim3((B + TM_ROWS - 1) / TM_ROWS), dim3(64 * TM_ROWS), 0, stream,
+                           logits, B, ld, K, ck, cn, nch, vals, idxs);
+    } else {
+        hipLaunchKernelGGL(zs_k_btopk, dim3(B), dim3(LN_NT), 0, stream, logits, V, ld, K, vals, idxs);
+    }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 extern "C" int zs_lane_sample_topk_launch(const float* vals, const uint32_t* idxs, uint32_t B, uint32_t K,
                                           const float* temp, const uint32_t* top_k, const float* top_p,
                                           const uint32_t* seed, uint32_t* out, hipStream_t stream) {
-    hipLaunchKernelGGL(zs_k_sample_topk, dim3((B + 63) / 64), dim3(64), 0, stream, vals, idxs, B, K, temp, top_k,
-                       top_p, seed, out);
+    if (K <= 64)
+        hipLaunchKernelGGL(zs_k_sample_topk64, dim3((B + TM_ROWS - 1) / TM_ROWS), dim3(64 * TM_ROWS), 0, stream, vals,
+                           idxs, B, K, temp, top_k, top_p, seed, out);
+    else
+        hipLaunchKernelGGL(zs_k_sample_topk, dim3((B + 63) / 64), dim3(64), 0, stream, vals, idxs, B, K, temp, top_k,
+                           top_p, seed, out);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
