@@ -1569,6 +1569,10 @@ __global__ __launch_bounds__(ST_NT) void zs_k_stitchB(zs_sargs a) { stitch_body<
 #define BK_NB 2048   // buckets per level of the top-p walk
 #define BK_NC 16     // copies of each bucket counter (by lane)
 #define BK_SERIAL 4096  // exact buckets up to this size are walked by one thread
+#ifndef BK_WEPT
+#define BK_WEPT 4  // values per thread of one quick-walk group
+#endif
+#define BK_WG (ZS_BIG_NT * BK_WEPT)
 static_assert(BK_NB * BK_NC <= ZS_SORT_CAP, "per-copy bucket counters live in the sort buffer");
 
 struct big_shared {
@@ -1856,14 +1860,14 @@ __device__ __forceinline__ walk_out bk_walk(const uint32_t* vals, uint32_t from,
 #ifdef ZS_DEBUG_WALK
         long long cf0 = clock64();
 #endif
-        float tv[4];
+        float tv[BK_WEPT];
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            uint32_t ps = pos + 4 * threadIdx.x + q;
+        for (int q = 0; q < BK_WEPT; q++) {
+            uint32_t ps = pos + BK_WEPT * threadIdx.x + q;
             tv[q] = ps < to ? zs_u2f(vals[ps]) : 0.0f;
         }
-        uint32_t excl[4];
-        seq_find_res F = seq_find<ZS_BIG_NT, 4>(seq_terms<4>(tv), 0, s, thresh, excl, sh.q);
+        uint32_t excl[BK_WEPT];
+        seq_find_res F = seq_find<ZS_BIG_NT, BK_WEPT>(seq_terms<BK_WEPT>(tv), 0, s, thresh, excl, sh.q);
 #ifdef ZS_DEBUG_WALK
         WALK_COUNT(1, clock64() - cf0);
 #endif
@@ -1873,17 +1877,17 @@ __device__ __forceinline__ walk_out bk_walk(const uint32_t* vals, uint32_t from,
         long long cw0 = clock64();
 #endif
         if (first == ZS_BIGI) {
-            const uint32_t last = min(pos + ZS_BIG_G, to) - 1;
+            const uint32_t last = min(pos + BK_WG, to) - 1;
             const uint32_t bst = start[bk_rank<L>(vals[last])];
-            if (bst >= pos) s_bstart = seq_value_at<ZS_BIG_NT, 4>(F, excl, (int)(bst - pos), sh.q);
+            if (bst >= pos) s_bstart = seq_value_at<ZS_BIG_NT, BK_WEPT>(F, excl, (int)(bst - pos), sh.q);
             s = zs_grid_value(F.k0 + F.total, F.eg);
-            pos += ZS_BIG_G;
+            pos += BK_WG;
             continue;
         }
         // the bucket holding the first event / tie / stop is redone in exact order
         const uint32_t rk = bk_rank<L>(vals[pos + (uint32_t)first]);
         const uint32_t bst = start[rk], bend = start[rk + 1];
-        if (bst >= pos) s = seq_value_at<ZS_BIG_NT, 4>(F, excl, (int)(bst - pos), sh.q);
+        if (bst >= pos) s = seq_value_at<ZS_BIG_NT, BK_WEPT>(F, excl, (int)(bst - pos), sh.q);
         else s = s_bstart;
         o = bk_exact<L + 1>(vals + bst, bend - bst, s, thresh, tmp, sh);
 #ifdef ZS_DEBUG_WALK

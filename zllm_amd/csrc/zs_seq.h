@@ -21,8 +21,9 @@
 
 template <int NT>
 struct seq_sh {
-    uint32_t a[NT / 64], b[NT / 64];
-    int imin[NT / 64];
+    uint32_t a[NT / 64], b[NT / 64];     // wave totals, then wave prefixes
+    uint32_t te, to;                     // group total (even / odd start)
+    int ev, st, tie;                     // first event / stop / tie of the group
     float s;
     int stop;
 };
@@ -132,15 +133,33 @@ __device__ __forceinline__ seq_find_res seq_find(const F& f, int start, float s,
     ex.e = __shfl_up(inc.e, 1, 64);
     ex.o = __shfl_up(inc.o, 1, 64);
     if (lane == 0) ex.e = ex.o = 0u;
+    constexpr int NW = NT / 64;
     if (lane == 63) { sh.a[zs_wid()] = inc.e; sh.b[zs_wid()] = inc.o; }
     __syncthreads();
-    seq_pair pre = {0u, 0u}, tot = {0u, 0u};
-    for (int i = 0; i < NT / 64; i++) {
-        seq_pair w = {sh.a[i], sh.b[i]};
-        if (i < zs_wid()) pre = seq_compose(pre, w);
-        tot = seq_compose(tot, w);
+    // wave 0 scans the wave totals (lane w = wave w) and publishes each wave's
+    // exclusive prefix and the group total
+    if (zs_wid() == 0) {
+        seq_pair w = {0u, 0u};
+        if (lane < NW) { w.e = sh.a[lane]; w.o = sh.b[lane]; }
+        seq_pair wi = w;
+#pragma unroll
+        for (int d = 1; d < NW; d <<= 1) {
+            seq_pair y;
+            y.e = __shfl_up(wi.e, d, 64);
+            y.o = __shfl_up(wi.o, d, 64);
+            seq_pair c = seq_compose(y, wi);
+            if (lane >= d) wi = c;
+        }
+        seq_pair we;
+        we.e = __shfl_up(wi.e, 1, 64);
+        we.o = __shfl_up(wi.o, 1, 64);
+        if (lane == 0) we.e = we.o = 0u;
+        if (lane < NW) { sh.a[lane] = we.e; sh.b[lane] = we.o; }
+        if (lane == NW - 1) { sh.te = wi.e; sh.to = wi.o; }
+        if (lane == 0) { sh.ev = ZS_BIGI; sh.st = ZS_BIGI; sh.tie = ZS_BIGI; }
     }
-    pre = seq_compose(pre, ex);
+    __syncthreads();
+    const seq_pair pre = seq_compose(seq_pair{sh.a[zs_wid()], sh.b[zs_wid()]}, ex);
     uint32_t run = p0 ? pre.o : pre.e;
     int my_ev = ZS_BIGI, my_st = ZS_BIGI, my_tie = ZS_BIGI;
 #pragma unroll
@@ -155,20 +174,18 @@ __device__ __forceinline__ seq_find_res seq_find(const F& f, int start, float s,
         if (my_ev == ZS_BIGI && R.k0 + run >= ZS_BINADE) my_ev = e;
         if (my_st == ZS_BIGI && kthr != 0xffffffffu && R.k0 + run >= kthr) my_st = e;
     }
-    R.total = p0 ? tot.o : tot.e;
-    // first event / stop (the scan's LDS slots are free again after this sync)
+    R.total = p0 ? sh.to : sh.te;
+    // first event / stop / tie over the group
     my_ev = wave_min_i(my_ev);
     my_st = wave_min_i(my_st);
     my_tie = wave_min_i(my_tie);
-    __syncthreads();
-    if (lane == 0) { sh.a[zs_wid()] = (uint32_t)my_ev; sh.b[zs_wid()] = (uint32_t)my_st; sh.imin[zs_wid()] = my_tie; }
-    __syncthreads();
-    int ev = ZS_BIGI, st = ZS_BIGI, tie = ZS_BIGI;
-    for (int i = 0; i < NT / 64; i++) {
-        ev = min(ev, (int)sh.a[i]);
-        st = min(st, (int)sh.b[i]);
-        tie = min(tie, sh.imin[i]);
+    if (lane == 0) {
+        if (my_ev != ZS_BIGI) atomicMin(&sh.ev, my_ev);
+        if (my_st != ZS_BIGI) atomicMin(&sh.st, my_st);
+        if (my_tie != ZS_BIGI) atomicMin(&sh.tie, my_tie);
     }
+    __syncthreads();
+    const int ev = sh.ev, st = sh.st, tie = sh.tie;
     __syncthreads();
     R.ev = ev;
     R.st = st;
