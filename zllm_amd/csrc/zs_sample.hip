@@ -1568,7 +1568,7 @@ __global__ __launch_bounds__(ST_NT) void zs_k_stitchB(zs_sargs a) { stitch_body<
 // ===========================================================================
 #define BK_NB 2048   // buckets per level of the top-p walk
 #define BK_NC 16     // copies of each bucket counter (by lane)
-#define BK_SERIAL 4096  // exact buckets up to this size are walked by one thread
+#define BK_SERIAL 128   // exact buckets up to this size are walked by one thread
 #ifndef BK_WEPT
 #define BK_WEPT 4  // values per thread of one quick-walk group
 #endif
@@ -1696,8 +1696,10 @@ __device__ __forceinline__ float big_term_e(float z, bool has_thr, float thr, fl
 #ifdef ZS_DEBUG_WALK
 __device__ unsigned long long zs_dbg_walk[256][8];
 #define WALK_COUNT(k, v) do { if (threadIdx.x == 0) zs_dbg_walk[blockIdx.x][k] += (v); } while (0)
+#define WALK_MAX(k, v) do { if (threadIdx.x == 0 && zs_dbg_walk[blockIdx.x][k] < (unsigned long long)(v)) zs_dbg_walk[blockIdx.x][k] = (v); } while (0)
 #else
 #define WALK_COUNT(k, v) do {} while (0)
+#define WALK_MAX(k, v) do {} while (0)
 #endif
 struct walk_out {
     bool stopped;
@@ -1722,15 +1724,48 @@ __device__ __forceinline__ void bk_sort_desc(uint32_t* a, int n) {
     }
 }
 
+// The same for np2 <= ZS_BIG_NT, one value per thread: exchanges inside a
+// wave by shuffles, only the strides of 64 and more through LDS.
+__device__ __forceinline__ void bk_sort_desc_small(uint32_t* a, int np2) {
+    const int t = threadIdx.x;
+    uint32_t x = t < np2 ? a[t] : 0u;
+    for (int k = 2; k <= np2; k <<= 1) {
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            uint32_t y;
+            if (j >= 64) {
+                if (t < np2) a[t] = x;
+                __syncthreads();
+                y = t < np2 ? a[t ^ j] : 0u;
+                __syncthreads();
+            } else {
+                y = __shfl_xor(x, j, 64);
+            }
+            const bool desc = (t & k) == 0, lower = (t & j) == 0;
+            x = (lower == desc) ? max(x, y) : min(x, y);
+        }
+    }
+    if (t < np2) a[t] = x;
+    __syncthreads();
+}
+
 // Walk n <= ZS_SORT_CAP values in exact descending order (sorted in LDS).
 __device__ __forceinline__ walk_out bk_walk_sorted(const uint32_t* vals, uint32_t n, float& s, float thresh, big_shared& sh) {
     walk_out o = {false, 0u, 0u};
     WALK_COUNT(0, 1);
+    WALK_COUNT(1, n);
+    WALK_MAX(6, n);
+#ifdef ZS_DEBUG_WALK
+    long long cs0 = clock64();
+#endif
     uint32_t np2 = 1;
     while (np2 < n) np2 <<= 1;
     for (uint32_t i = threadIdx.x; i < np2; i += ZS_BIG_NT) sh.sortbuf[i] = i < n ? vals[i] : 0u;
     __syncthreads();
-    if (np2 > 1) bk_sort_desc(sh.sortbuf, (int)np2);
+    if (np2 > ZS_BIG_NT) bk_sort_desc(sh.sortbuf, (int)np2);
+    else if (np2 > 1) bk_sort_desc_small(sh.sortbuf, (int)np2);
+#ifdef ZS_DEBUG_WALK
+    WALK_COUNT(4, clock64() - cs0);
+#endif
     if (n <= BK_SERIAL) {
         // a bucket of this size is walked faster by one thread than by the
         // workgroup scan (whose cost is its latency chain, not its width)
@@ -1869,10 +1904,10 @@ __device__ __forceinline__ walk_out bk_walk(const uint32_t* vals, uint32_t from,
         uint32_t excl[BK_WEPT];
         seq_find_res F = seq_find<ZS_BIG_NT, BK_WEPT>(seq_terms<BK_WEPT>(tv), 0, s, thresh, excl, sh.q);
 #ifdef ZS_DEBUG_WALK
-        WALK_COUNT(1, clock64() - cf0);
+        WALK_COUNT(3, clock64() - cf0);
 #endif
         const int first = min(min(F.ev, F.st), F.tie);
-        WALK_COUNT(2, 1); WALK_COUNT(3, F.tie < min(F.ev, F.st) ? 1 : 0); WALK_COUNT(4, F.ev < F.st ? 1 : 0);
+        WALK_COUNT(2, 1);
 #ifdef ZS_DEBUG_WALK
         long long cw0 = clock64();
 #endif
@@ -2246,7 +2281,6 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
             const uint32_t upto = sh.hist[rhi + 1];
 #ifdef ZS_DEBUG_WALK
             long long cg = clock64();
-            WALK_COUNT(6, 1);
 #endif
             wo = bk_walk<0>(gv, done, upto, sh.hist, s, P.top_p, tmp, sh);
 #ifdef ZS_DEBUG_WALK
@@ -2317,7 +2351,7 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
                 if (zs_lane() == 0) ap[j] = acc;
             }
 #ifdef ZS_DEBUG_WALK
-            if (t == 0) printf("walk row %u peak %d nk %u sorts %llu sorted %llu finds %llu tiefirst %llu evfirst %llu exactclk %llu rounds %llu walkclk %llu\n", r, (int)peak, nk,
+            if (t == 0) printf("walk row %u peak %d nk %u sorts %llu sortn %llu finds %llu findclk %llu sortclk %llu exactclk %llu maxn %llu walkclk %llu\n", r, (int)peak, nk,
                                zs_dbg_walk[r][0], zs_dbg_walk[r][1], zs_dbg_walk[r][2], zs_dbg_walk[r][3], zs_dbg_walk[r][4], zs_dbg_walk[r][5], zs_dbg_walk[r][6], zs_dbg_walk[r][7]);
 #endif
             if (t == 0) {
