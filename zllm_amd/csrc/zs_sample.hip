@@ -220,7 +220,7 @@ struct p1_shared {
 // Exact top-K (key desc, index asc) of the chunk's valid keys; writes the
 // candidates (unordered) to out_key/out_idx. Element e = j*4+q of thread t has
 // index base + (j*256 + t)*4 + q.
-__device__ __forceinline__ void p1_topk(const uint32_t (&key)[P1_EPT], uint32_t vmask, uint32_t nvalid, uint32_t K,
+__device__ __forceinline__ void p1_topk(const float (&kv)[P1_EPT], uint32_t vmask, uint32_t nvalid, uint32_t K,
                         uint32_t base, uint32_t* out_key, uint32_t* out_idx, uint32_t* n_out, uint32_t* kth,
                         uint32_t* full, p1_shared& sh) {
     const int t = threadIdx.x;
@@ -231,7 +231,7 @@ __device__ __forceinline__ void p1_topk(const uint32_t (&key)[P1_EPT], uint32_t 
             if ((vmask >> e) & 1u) {
                 uint32_t pos = atomicAdd(&sh.cnt, 1u);
                 if (pos < K) {
-                    out_key[pos] = key[e];
+                    out_key[pos] = zs_total_key(kv[e]);
                     out_idx[pos] = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
                 }
             }
@@ -247,8 +247,8 @@ __device__ __forceinline__ void p1_topk(const uint32_t (&key)[P1_EPT], uint32_t 
         if (t < 256) sh.hist[t] = 0;
         __syncthreads();
         for (int e = 0; e < P1_EPT; e++)
-            if (((vmask >> e) & 1u) && (key[e] & mask) == prefix)
-                atomicAdd(&sh.hist[(key[e] >> shift) & 255u], 1u);
+            if (((vmask >> e) & 1u) && (zs_total_key(kv[e]) & mask) == prefix)
+                atomicAdd(&sh.hist[(zs_total_key(kv[e]) >> shift) & 255u], 1u);
         __syncthreads();
         if (t < 64) {
             // lane l owns bins 255-4l .. 252-4l (descending)
@@ -274,23 +274,23 @@ __device__ __forceinline__ void p1_topk(const uint32_t (&key)[P1_EPT], uint32_t 
     uint32_t my_eq = 0;
     for (int e = 0; e < P1_EPT; e++) {
         if (!((vmask >> e) & 1u)) continue;
-        if (key[e] > kk) {
+        if (zs_total_key(kv[e]) > kk) {
             uint32_t pos = atomicAdd(&sh.cnt, 1u);
             if (pos < K) {
-                out_key[pos] = key[e];
+                out_key[pos] = zs_total_key(kv[e]);
                 out_idx[pos] = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
             }
-        } else if (key[e] == kk) {
+        } else if (zs_total_key(kv[e]) == kk) {
             my_eq++;
         }
     }
     uint32_t n_eq = block_sum_u<ZS_P1_NT>(my_eq, sh.u);
     if (n_eq == need) {
         for (int e = 0; e < P1_EPT; e++) {
-            if (((vmask >> e) & 1u) && key[e] == kk) {
+            if (((vmask >> e) & 1u) && zs_total_key(kv[e]) == kk) {
                 uint32_t pos = atomicAdd(&sh.cnt, 1u);
                 if (pos < K) {
-                    out_key[pos] = key[e];
+                    out_key[pos] = zs_total_key(kv[e]);
                     out_idx[pos] = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
                 }
             }
@@ -302,18 +302,18 @@ __device__ __forceinline__ void p1_topk(const uint32_t (&key)[P1_EPT], uint32_t 
             uint32_t c = 0;
             for (int q = 0; q < 4; q++) {
                 int e = j * 4 + q;
-                c += (((vmask >> e) & 1u) && key[e] == kk) ? 1u : 0u;
+                c += (((vmask >> e) & 1u) && zs_total_key(kv[e]) == kk) ? 1u : 0u;
             }
             uint32_t tot;
             uint32_t ex = block_excl_scan_u<ZS_P1_NT>(c, sh.u, &tot);
             uint32_t rank = carry + ex;
             for (int q = 0; q < 4; q++) {
                 int e = j * 4 + q;
-                if (((vmask >> e) & 1u) && key[e] == kk) {
+                if (((vmask >> e) & 1u) && zs_total_key(kv[e]) == kk) {
                     if (rank < need) {
                         uint32_t pos = atomicAdd(&sh.cnt, 1u);
                         if (pos < K) {
-                            out_key[pos] = key[e];
+                            out_key[pos] = zs_total_key(kv[e]);
                             out_idx[pos] = base + (j * ZS_P1_NT + t) * 4 + q;
                         }
                     }
@@ -342,7 +342,7 @@ __device__ __forceinline__ void p1_topk(const uint32_t (&key)[P1_EPT], uint32_t 
 // radix select.
 // nvalid: valid elements of the chunk; nfin: valid elements whose key is above
 // that of -inf.
-__device__ __forceinline__ void p1_topk_fast(const uint32_t (&key)[P1_EPT], uint32_t vmask, uint32_t nvalid,
+__device__ __forceinline__ void p1_topk_fast(const float (&kv)[P1_EPT], uint32_t vmask, uint32_t nvalid,
                              uint32_t nfin, uint32_t K, uint32_t base,
                              uint32_t* out_key, uint32_t* out_idx, uint32_t* n_out, uint32_t* kth,
                              uint32_t* full, p1_shared& sh) {
@@ -350,10 +350,10 @@ __device__ __forceinline__ void p1_topk_fast(const uint32_t (&key)[P1_EPT], uint
     uint32_t tm = 0;
 #pragma unroll
     for (int e = 0; e < P1_EPT; e++)
-        if ((vmask >> e) & 1u) tm = max(tm, key[e]);
+        if ((vmask >> e) & 1u) tm = max(tm, zs_total_key(kv[e]));
     const uint32_t c = (K + (ZS_P1_NT / 64) - 1) / (ZS_P1_NT / 64);
     if (nvalid <= K || c > 64) {
-        p1_topk(key, vmask, nvalid, K, base, out_key, out_idx, n_out, kth, full, sh);
+        p1_topk(kv, vmask, nvalid, K, base, out_key, out_idx, n_out, kth, full, sh);
         return;
     }
     // Fewer than K values above -inf (a masked chunk): all of them plus the
@@ -364,9 +364,9 @@ __device__ __forceinline__ void p1_topk_fast(const uint32_t (&key)[P1_EPT], uint
         __syncthreads();
 #pragma unroll
         for (int e = 0; e < P1_EPT; e++) {
-            if (((vmask >> e) & 1u) && key[e] > kninf) {
+            if (((vmask >> e) & 1u) && zs_total_key(kv[e]) > kninf) {
                 const uint32_t p = atomicAdd(&sh.cnt, 1u);
-                out_key[p] = key[e];
+                out_key[p] = zs_total_key(kv[e]);
                 out_idx[p] = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
             }
         }
@@ -379,13 +379,13 @@ __device__ __forceinline__ void p1_topk_fast(const uint32_t (&key)[P1_EPT], uint
             if (carry >= need) break;  // uniform: the lowest ids are taken
             uint32_t cj = 0;
 #pragma unroll
-            for (int q = 0; q < 4; q++) cj += (((vmask >> (4 * j + q)) & 1u) && key[4 * j + q] == kninf) ? 1u : 0u;
+            for (int q = 0; q < 4; q++) cj += (((vmask >> (4 * j + q)) & 1u) && zs_total_key(kv[4 * j + q]) == kninf) ? 1u : 0u;
             uint32_t tot;
             uint32_t rank = carry + block_excl_scan_u<ZS_P1_NT>(cj, sh.u, &tot);
 #pragma unroll
             for (int q = 0; q < 4; q++) {
                 const int e = 4 * j + q;
-                if (((vmask >> e) & 1u) && key[e] == kninf) {
+                if (((vmask >> e) & 1u) && zs_total_key(kv[e]) == kninf) {
                     if (rank < need) {
                         out_key[nfin + rank] = kninf;
                         out_idx[nfin + rank] = base + (j * ZS_P1_NT + t) * 4 + q;
@@ -443,19 +443,19 @@ __device__ __forceinline__ void p1_topk_fast(const uint32_t (&key)[P1_EPT], uint
     }
     uint32_t cnt = 0;
 #pragma unroll
-    for (int e = 0; e < P1_EPT; e++) cnt += (((vmask >> e) & 1u) && key[e] >= theta) ? 1u : 0u;
+    for (int e = 0; e < P1_EPT; e++) cnt += (((vmask >> e) & 1u) && zs_total_key(kv[e]) >= theta) ? 1u : 0u;
     uint32_t nsup;
     uint32_t pos = block_excl_scan_u<ZS_P1_NT>(cnt, sh.u, &nsup);
     if (nsup > P1_SORT) {
-        p1_topk(key, vmask, nvalid, K, base, out_key, out_idx, n_out, kth, full, sh);
+        p1_topk(kv, vmask, nvalid, K, base, out_key, out_idx, n_out, kth, full, sh);
         return;
     }
     // composite ((~key) << 32 | index): ascending order = key desc, index asc
 #pragma unroll
     for (int e = 0; e < P1_EPT; e++) {
-        if (((vmask >> e) & 1u) && key[e] >= theta) {
+        if (((vmask >> e) & 1u) && zs_total_key(kv[e]) >= theta) {
             const uint32_t idx = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
-            sh.s64[pos++] = ((unsigned long long)(~key[e]) << 32) | idx;
+            sh.s64[pos++] = ((unsigned long long)(~zs_total_key(kv[e])) << 32) | idx;
         }
     }
     __syncthreads();
@@ -493,10 +493,59 @@ __device__ __forceinline__ void p1_topk_fast(const uint32_t (&key)[P1_EPT], uint
     __syncthreads();
 }
 
+// Observer candidates without the exact cut: every element whose key is at
+// least theta, the K-th largest thread maximum (K <= 64), when at most `cap`
+// of them exist. The list then holds the chunk's top K (and possibly more), in
+// any order -- what the combine kernel's merge needs. Returns false (nothing
+// written) when more than `cap` elements reach theta.
+__device__ __forceinline__ bool p1_superset(const float (&kv)[P1_EPT], uint32_t vmask, uint32_t K, uint32_t cap,
+                                            uint32_t base, uint32_t* out_key, uint32_t* out_idx, uint32_t* n_out,
+                                            p1_shared& sh) {
+    const int t = threadIdx.x, lane = zs_lane();
+    uint32_t tm = 0;
+#pragma unroll
+    for (int e = 0; e < P1_EPT; e++)
+        if ((vmask >> e) & 1u) tm = max(tm, zs_total_key(kv[e]));
+    const uint32_t srt = wave_sort_u32(tm);
+    sh.tmax[zs_wid() * 64 + lane] = srt;
+    if (t == 0) sh.cnt = 0;
+    __syncthreads();
+    if (t < 64) {
+        uint32_t m = srt;
+#pragma unroll
+        for (int w = 1; w < ZS_P1_NT / 64; w++) {
+            m = max(m, sh.tmax[w * 64 + 63 - lane]);
+#pragma unroll
+            for (int j = 32; j > 0; j >>= 1) {
+                const uint32_t o = __shfl_xor(m, j, 64);
+                m = (lane & j) ? max(m, o) : min(m, o);
+            }
+        }
+        if (lane == 64 - (int)K) sh.sel[2] = m;
+    }
+    __syncthreads();
+    const uint32_t theta = max(sh.sel[2], 1u);
+    uint32_t cnt = 0;
+#pragma unroll
+    for (int e = 0; e < P1_EPT; e++) cnt += (((vmask >> e) & 1u) && zs_total_key(kv[e]) >= theta) ? 1u : 0u;
+    const uint32_t nsup = block_sum_u<ZS_P1_NT>(cnt, sh.u);
+    if (nsup > cap) return false;
+#pragma unroll
+    for (int e = 0; e < P1_EPT; e++) {
+        if (((vmask >> e) & 1u) && zs_total_key(kv[e]) >= theta) {
+            const uint32_t p = atomicAdd(&sh.cnt, 1u);
+            out_key[p] = zs_total_key(kv[e]);
+            out_idx[p] = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
+        }
+    }
+    *n_out = nsup;
+    return true;
+}
+
 // Compaction of the chunk's finite sampler values (the list when the chunk has
 // at most K of them: then it holds every element a top-k or a small-survivor
 // path can keep).
-__device__ __forceinline__ void p1_finite(const uint32_t (&key)[P1_EPT], const float (&zv)[P1_EPT], uint32_t vmask,
+__device__ __forceinline__ void p1_finite(const float (&zv)[P1_EPT], uint32_t vmask,
                           uint32_t base, uint32_t* out_key, uint32_t* out_idx, p1_shared& sh) {
     const int t = threadIdx.x;
     uint32_t cnt = 0;
@@ -507,14 +556,20 @@ __device__ __forceinline__ void p1_finite(const uint32_t (&key)[P1_EPT], const f
 #pragma unroll
     for (int e = 0; e < P1_EPT; e++) {
         if (((vmask >> e) & 1u) && zv[e] > -INFINITY) {
-            out_key[pos] = key[e];
+            out_key[pos] = zs_total_key(zv[e]);
             out_idx[pos] = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
             pos++;
         }
     }
 }
 
-__global__ __launch_bounds__(ZS_P1_NT) void zs_k_pass1(zs_sargs a) {
+// element e of the calling thread in a [P1_EPT][ZS_P1_NT] LDS array
+struct p1_lds_arr {
+    float* p;
+    __device__ __forceinline__ float& operator[](int e) const { return p[e * ZS_P1_NT]; }
+};
+
+__global__ __launch_bounds__(ZS_P1_NT) __attribute__((amdgpu_waves_per_eu(3))) void zs_k_pass1(zs_sargs a) {
     const uint32_t c = blockIdx.x, r = blockIdx.y;
     const zs_batch& b = a.b;
     const uint32_t V = b.V;
@@ -540,7 +595,11 @@ __global__ __launch_bounds__(ZS_P1_NT) void zs_k_pass1(zs_sargs a) {
         sh.pcur1 = lo;
     }
 
-    float xo[P1_EPT], zv[P1_EPT];
+    // x~ lives in LDS (thread t's element e at xsh[e][t]) until the observer
+    // list, z in registers: both arrays in registers would halve occupancy
+    __shared__ float xsh[P1_EPT][ZS_P1_NT];
+    const p1_lds_arr xo{&xsh[0][t]};
+    float zv[P1_EPT];
     uint32_t vmask = 0;
 #pragma unroll
     for (int j = 0; j < P1_EPT / 4; j++) {
@@ -688,12 +747,11 @@ __global__ __launch_bounds__(ZS_P1_NT) void zs_k_pass1(zs_sargs a) {
         const bool om = (P.flags & (ZS_ROW_LOGPROBS | ZS_ROW_UNCERTAINTY)) && omax > -INFINITY && omax < INFINITY;
         const bool zm = T > 0.0f && zmax > -INFINITY && zmax < INFINITY;
         __shared__ float msh[ZS_P1_NT / 64][P1_J][3];
-        float m1[P1_J], md[P1_J], mz[P1_J];
         // bit 2s: sub-chunk s holds the chunk's observer max, bit 2s+1: its sampler max
         uint32_t hasmax = 0;
 #pragma unroll
         for (int j = 0; j < P1_J; j++) {
-            m1[j] = md[j] = mz[j] = 0.0f;
+            float m1 = 0.0f, md = 0.0f, mz = 0.0f;
             const int sj = j * P1_SPF + wh;
 #pragma unroll
             for (int q = 0; q < 4; q++) {
@@ -703,22 +761,19 @@ __global__ __launch_bounds__(ZS_P1_NT) void zs_k_pass1(zs_sargs a) {
                 if (zv[e] == zmax) hasmax |= 2u << (2 * sj);
                 if (om) {
                     float d = xo[e] - omax;
-                    if (d > -INFINITY) { float ex = __expf(d); m1[j] += ex; md[j] += d * ex; }
+                    if (d > -INFINITY) { float ex = __expf(d); m1 += ex; md += d * ex; }
                 }
                 if (zm) {
                     float d = zv[e] - zmax;
-                    if (d > -INFINITY) mz[j] += __expf(d);
+                    if (d > -INFINITY) mz += __expf(d);
                 }
             }
-        }
-#pragma unroll
-        for (int j = 0; j < P1_J; j++) {
             for (int d = 32; d > 0; d >>= 1) {
-                m1[j] += __shfl_xor(m1[j], d, 64);
-                md[j] += __shfl_xor(md[j], d, 64);
-                mz[j] += __shfl_xor(mz[j], d, 64);
+                m1 += __shfl_xor(m1, d, 64);
+                md += __shfl_xor(md, d, 64);
+                mz += __shfl_xor(mz, d, 64);
             }
-            if (zs_lane() == 0) { msh[wid][j][0] = m1[j]; msh[wid][j][1] = md[j]; msh[wid][j][2] = mz[j]; }
+            if (zs_lane() == 0) { msh[wid][j][0] = m1; msh[wid][j][1] = md; msh[wid][j][2] = mz; }
         }
         for (int d = 32; d > 0; d >>= 1) hasmax |= __shfl_xor(hasmax, d, 64);
         __shared__ uint32_t hsh[ZS_P1_NT / 64];
@@ -741,36 +796,36 @@ __global__ __launch_bounds__(ZS_P1_NT) void zs_k_pass1(zs_sargs a) {
         __syncthreads();
     }
 
-    // ---- candidate lists
-    uint32_t key[P1_EPT];
+    // ---- candidate lists (keys recomputed from the values where needed)
     const size_t lofs = ((size_t)r * a.nch + c);
     // sampler list size: top_k when the row has a top-k cut within range
     const bool has_topk = P.top_k > 0 && P.top_k < V;
     const uint32_t Ks = (has_topk && P.top_k <= ZS_KS) ? P.top_k : ZS_KS;
-#pragma unroll
-    for (int e = 0; e < P1_EPT; e++) key[e] = zs_total_key(zv[e]);
     uint32_t ns, s_kth, s_full;
     ns = s_kth = s_full = 0;
     // The list is read by a top-k cut within ZS_KS and by the small-survivor
     // path, which needs every chunk to have at most ZS_KS finite values.
     if (T > 0.0f) {
         if (zfin <= Ks) {
-            p1_finite(key, zv, vmask, base, a.cs_key + lofs * ZS_KS, a.cs_idx + lofs * ZS_KS, sh);
+            p1_finite(zv, vmask, base, a.cs_key + lofs * ZS_KS, a.cs_idx + lofs * ZS_KS, sh);
             ns = zfin;
         } else if (has_topk && P.top_k <= ZS_KS) {
-            p1_topk_fast(key, vmask, nvalid, zabove, Ks, base, a.cs_key + lofs * ZS_KS, a.cs_idx + lofs * ZS_KS, &ns, &s_kth,
+            p1_topk_fast(zv, vmask, nvalid, zabove, Ks, base, a.cs_key + lofs * ZS_KS, a.cs_idx + lofs * ZS_KS, &ns, &s_kth,
                          &s_full, sh);
         }
     }
     uint32_t ntl = P.top_logprobs > 20 ? 20 : P.top_logprobs;
     uint32_t Ko = ntl + 8;
     if (Ko > ZS_KO) Ko = ZS_KO;
-#pragma unroll
-    for (int e = 0; e < P1_EPT; e++) key[e] = zs_total_key(xo[e]);
     uint32_t no, o_kth, o_full;
     no = o_kth = o_full = 0;
-    if (P.flags & (ZS_ROW_LOGPROBS | ZS_ROW_UNCERTAINTY))
-        p1_topk_fast(key, vmask, nvalid, xabove, Ko, base, a.co_key + lofs * ZS_KO, a.co_idx + lofs * ZS_KO, &no, &o_kth,
+    float xr[P1_EPT];  // z is dead here: x~ back in registers for the list
+#pragma unroll
+    for (int e = 0; e < P1_EPT; e++) xr[e] = xo[e];
+    if ((P.flags & (ZS_ROW_LOGPROBS | ZS_ROW_UNCERTAINTY)) &&
+        !(nvalid > Ko && p1_superset(xr, vmask, Ko, ZS_KO, base, a.co_key + lofs * ZS_KO, a.co_idx + lofs * ZS_KO,
+                                     &no, sh)))
+        p1_topk_fast(xr, vmask, nvalid, xabove, Ko, base, a.co_key + lofs * ZS_KO, a.co_idx + lofs * ZS_KO, &no, &o_kth,
                      &o_full, sh);
 
     if (t == 0) {
