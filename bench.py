@@ -248,12 +248,25 @@ def main():
 
     from zllm_amd.engine import verify_drafts
 
-    def step(out=None):
+    # The draft verification is independent of this step's sampling: it runs on
+    # a second stream (default priority) and fills the CUs that the sampler's
+    # latency-bound row kernels leave idle; the step ends when both are done.
+    spec_stream = torch.cuda.Stream()
+
+    def step(out=None, overlap=True):
+        if overlap:
+            spec_stream.wait_stream(stream)
+            with torch.cuda.stream(spec_stream):
+                verify_drafts(ctx, W["tgt"], W["draft_ids"], W["spec_T"], W["spec_seed"], W["spec_ctr"], W["dft"])
+                W["spec_ctr"].add_(1)
         W["dfa"].mask(W["table"], W["st"], V, out=bits)
         out = sampler.run(xs, bufs, bits, top_stride=5, out=out)
-        verify_drafts(ctx, W["tgt"], W["draft_ids"], W["spec_T"], W["spec_seed"], W["spec_ctr"], W["dft"])
         bufs["counter"].add_(1)
-        W["spec_ctr"].add_(1)
+        if overlap:
+            stream.wait_stream(spec_stream)
+        else:
+            verify_drafts(ctx, W["tgt"], W["draft_ids"], W["spec_T"], W["spec_seed"], W["spec_ctr"], W["dft"])
+            W["spec_ctr"].add_(1)
         return out
 
     out = None
@@ -298,7 +311,7 @@ def main():
     acc = {}
     n_prof = 10
     for _ in range(n_prof):
-        out = step(out)
+        out = step(out, overlap=False)  # one stream: events bracket single kernels
         for k, v in ctx.last_timings().items():
             acc[k] = acc.get(k, 0.0) + v / n_prof
     ctx.set_profiling(False)
