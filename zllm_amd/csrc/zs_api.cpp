@@ -122,6 +122,11 @@ extern "C" int zs_ctx_create(int device, uint32_t max_rows, uint32_t max_vocab, 
     if (!rc) rc = zs_alloc(ctx, &ctx->pairs, R * (size_t)max_vocab * 2);
     if (!rc) rc = zs_alloc(ctx, &ctx->pv, R * (size_t)max_vocab + 4);  // 16-byte loads at the tail
     if (!rc) rc = zs_alloc(ctx, (uint32_t**)&ctx->mask_scratch, R);
+    // epochs start at 1 over zeroed flags (set-up only, outside any stream
+    // work a caller could capture)
+    if (!rc && (hipMemset(ctx->mask_scratch, 0, R * sizeof(uint32_t)) != hipSuccess ||
+                hipDeviceSynchronize() != hipSuccess))
+        rc = ZS_EHIP;
     if (!rc) rc = zs_alloc(ctx, &ctx->spec_chunks, R * (2 * ZS_SPEC_KMAX + 1) * C);
     if (!rc) rc = zs_alloc(ctx, &ctx->sub_mom, R * ctx->max_subs);
     if (!rc) rc = zs_alloc(ctx, &ctx->sub_sum, R * ZS_NSUM * ctx->max_subs);
@@ -493,8 +498,15 @@ extern "C" int zs_dfa_mask(zs_ctx* ctx, const zs_dfa* dfa, const zs_vocab* vocab
     a.V = V;
     a.words = (V + 31) / 32;
     a.out = d_out_bits;
+    const bool packed = dfa->packed_lds != 0 && B <= ZS_DFA_MAXROWS;
     uint32_t* any = d_any ? d_any : (uint32_t*)ctx->mask_scratch;
-    if (zs_dfa_mask_launch(a, dfa->packed_lds != 0, ctx->num_cus, any, (hipStream_t)stream))
+    if (packed) {
+        if (++ctx->mask_epoch == 0) ctx->mask_epoch = 1;  // 0 is what the flags start as
+        a.epoch = ctx->mask_epoch;
+        a.any_user = d_any;
+        any = (uint32_t*)ctx->mask_scratch;
+    }
+    if (zs_dfa_mask_launch(a, packed, ctx->num_cus, any, (hipStream_t)stream))
         return zs_set_error(ctx, ZS_EHIP, "zs_dfa_mask: launch failed: %s", hipGetErrorString(hipGetLastError()));
     return ZS_OK;
 }

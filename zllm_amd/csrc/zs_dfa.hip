@@ -120,14 +120,15 @@ __global__ __launch_bounds__(DM_NT) void zs_k_dfa_mask(dm_args a) {
 #define DL_RG 8                  // rows walked together
 #define DL_TW (ZS_WALK_TILE / 32) // bitmap words per row and tile
 #define DL_WORDS (ZS_DFA_LDS_BYTES / 4)
-#define DL_MAXROWS 1024          // constrained-row list in LDS
+#define DL_MAXROWS ZS_DFA_MAXROWS
 __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
     __shared__ uint32_t tab[DL_WORDS];
     __shared__ uint16_t ci[256];
     __shared__ uint32_t bm[DL_RG][DL_TW];
     __shared__ uint16_t crow[DL_MAXROWS];  // constrained rows
     __shared__ uint16_t cst[DL_MAXROWS];   // their good start state (0xffff: none allowed)
-    __shared__ uint32_t ncr;
+    __shared__ uint16_t frow[DL_MAXROWS];  // unconstrained rows
+    __shared__ uint32_t ncr, nfr;
     const int t = threadIdx.x;
     // stage the table with many 16-byte loads in flight per thread
     const uint32_t nq = a.packed_words / 4;  // the table is allocated in whole quads
@@ -143,21 +144,25 @@ __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
     }
     for (uint32_t q = q0 + t; q < nq; q += DL_NT) dst[q] = src[q];
     for (int i = t; i < 256; i += DL_NT) ci[i] = a.clsinfo[i];
-    if (t == 0) ncr = 0;
+    if (t == 0) ncr = nfr = 0;
     __syncthreads();
-    // constrained rows in order (every workgroup builds the same list)
+    // constrained and unconstrained rows in order (every workgroup builds the
+    // same lists)
     for (uint32_t r0 = 0; r0 < a.B; r0 += DL_NT) {
         const uint32_t r = r0 + t;
-        const int32_t st = r < a.B ? a.states[r] : -1;
-        const bool c = st >= 0;
+        const int32_t st = r < a.B ? a.states[r] : 0;
+        const bool c = r < a.B && st >= 0, f = r < a.B && st < 0;
         uint32_t tot;
         const uint32_t pos = block_excl_scan_u<DL_NT>(c ? 1u : 0u, reinterpret_cast<uint32_t*>(bm), &tot);
         if (c) {
             crow[ncr + pos] = (uint16_t)r;
             cst[ncr + pos] = a.remap[st];
         }
+        uint32_t ftot;
+        const uint32_t fpos = block_excl_scan_u<DL_NT>(f ? 1u : 0u, reinterpret_cast<uint32_t*>(bm), &ftot);
+        if (f) frow[nfr + fpos] = (uint16_t)r;
         __syncthreads();
-        if (t == 0) ncr += tot;
+        if (t == 0) { ncr += tot; nfr += ftot; }
         __syncthreads();
     }
     const uint32_t nc = ncr;
@@ -238,9 +243,17 @@ __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
                 if (gw == a.words - 1 && (a.V & 31)) v &= (1u << (a.V & 31)) - 1u;
                 a.out[(size_t)r * a.words + gw] = v;
             }
-            if (word) a.any[r] = 1u;  // every writer stores 1
+            if (word) a.any[r] = a.epoch;  // every writer stores the same value
         }
         __syncthreads();
+    }
+    // unconstrained rows: every id below V (the workgroups split the words)
+    const uint32_t nfw = nfr * a.words;
+    for (uint32_t i = blockIdx.x * DL_NT + t; i < nfw; i += gridDim.x * DL_NT) {
+        const uint32_t k = i / a.words, wi = i - k * a.words;
+        uint32_t v = 0xffffffffu;
+        if (wi == a.words - 1 && (a.V & 31)) v = (1u << (a.V & 31)) - 1u;
+        a.out[(size_t)frow[k] * a.words + wi] = v;
     }
 }
 
@@ -262,14 +275,18 @@ __global__ void zs_k_fill_u32(uint32_t* p, uint32_t n, uint32_t v) {
 }
 
 // EOS rule (logit_fsm.rs:258-262): eos allowed iff is_accept(s) or no token is
-// viable; ids >= ntab other than eos stay disallowed.
+// viable; ids >= ntab other than eos stay disallowed. With epoch != 0 the
+// viability flags hold the epoch of the call that found a viable token (the
+// packed walk: no clearing pass), and the caller's 0/1 flags are written here.
 __global__ void zs_k_dfa_eos(dm_args a) {
     uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
     if (r >= a.B) return;
     int32_t st = a.states[r];
     if (st < 0) return;
+    const bool anyv = a.epoch ? a.any[r] == a.epoch : a.any[r] != 0;
+    if (a.epoch && a.any_user) a.any_user[r] = anyv ? 1u : 0u;
     if (a.eos >= a.V) return;
-    bool ok = a.accept[st] || a.any[r] == 0;
+    bool ok = a.accept[st] || !anyv;
     uint32_t* o = a.out + (size_t)r * a.words + (a.eos >> 5);
     uint32_t bit = 1u << (a.eos & 31);
     *o = ok ? (*o | bit) : (*o & ~bit);
@@ -282,9 +299,9 @@ extern "C" int zs_dfa_mask_launch(const dm_args& a, bool packed_lds, uint32_t nc
     uint32_t ncover = a.V > a.ntab ? a.V : a.ntab;
     if (packed_lds && a.B <= DL_MAXROWS) {
         const uint32_t items = ((ncover + ZS_WALK_TILE - 1) / ZS_WALK_TILE) * ((a.B + DL_RG - 1) / DL_RG);
-        hipLaunchKernelGGL(zs_k_dfa_free_rows, dim3(4, a.B), dim3(256), 0, stream, x);
         hipLaunchKernelGGL(zs_k_dfa_mask_packed, dim3(min(items, ncu)), dim3(DL_NT), 0, stream, x);
     } else {
+        x.epoch = 0;
         hipLaunchKernelGGL(zs_k_fill_u32, dim3((a.B + 255) / 256), dim3(256), 0, stream, any_scratch, a.B, 0u);
         dim3 grid((ncover + DM_TOK - 1) / DM_TOK, (a.B + DM_ROWS - 1) / DM_ROWS);
         hipLaunchKernelGGL(zs_k_dfa_mask<false>, grid, dim3(DM_NT), 0, stream, x);

@@ -16,6 +16,7 @@
 #define ZS_MAX_VOCAB 262144
 #define ZS_DFA_LDS_BYTES 152576  // packed DFA table budget in LDS (149 KB)
 #define ZS_WALK_TILE 2048        // ids per tile of the vocab-parallel DFA walk
+#define ZS_DFA_MAXROWS 1024      // rows of the LDS-table DFA walk (constrained-row list in LDS)
 #define ZS_MAX_CHUNKS (ZS_MAX_VOCAB / ZS_P1_CH)
 // Big-row engine: 1024 threads, 4 consecutive elements per thread.
 #define ZS_BIG_NT 1024
@@ -168,7 +169,8 @@ struct zs_ctx {
     zs_row_state* rst;
     uint32_t* pairs;       // big-row gather area [rows][max_vocab][2]
     uint32_t* pv;          // big-row probabilities (f32 bits) [rows][max_vocab]
-    void* mask_scratch;    // DFA mask staging
+    void* mask_scratch;    // DFA mask viability flags [rows]
+    uint32_t mask_epoch;   // last epoch handed to the packed DFA mask
     zs_sub_mom* sub_mom;         // [rows][max_subs]
     zs_sub_sum* sub_sum;         // [rows][ZS_NSUM][max_subs]
     double* k_ap;                // [rows][max_subs] approximate sums of the kept list per sub-chunk
@@ -272,6 +274,10 @@ struct dm_args {
     uint32_t B, V, words;
     uint32_t* out;
     uint32_t* any;
+    // packed path: viability flags hold the call's epoch (no clearing pass);
+    // the EOS kernel writes the caller's 0/1 flags (any_user, optional)
+    uint32_t epoch;
+    uint32_t* any_user;
 };
 
 // Optional per-kernel event timing of a launch sequence (zs_set_profiling).
