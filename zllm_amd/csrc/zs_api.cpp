@@ -407,6 +407,38 @@ extern "C" int zs_dfa_create(zs_ctx* ctx, const uint32_t* h_trans, uint32_t nsta
     d->bits = bits;
     d->rw = rw;
     d->packed_lds = packed.size() * 4 <= ZS_DFA_LDS_BYTES && ncls * bits < 65536 ? 1 : 0;
+    if (!d->packed_lds && ncls <= 64) {
+        // Sparse rows for tables past the LDS budget (large grammars are
+        // mostly fail entries): per good state {class mask lo, hi, first
+        // target, 0}, the sink last with an empty mask, then the u16 targets
+        // of the set classes in class order.
+        std::vector<uint32_t> rec((size_t)(ngood + 1) * 4, 0u);
+        std::vector<uint16_t> tgts;
+        for (uint32_t s = 0; s < nstates; s++) {
+            if (bad[s]) continue;
+            const uint32_t row = remap[s];
+            uint64_t mask = 0;
+            rec[(size_t)row * 4 + 2] = (uint32_t)tgts.size();
+            for (uint32_t c = 0; c < ncls; c++) {
+                const uint16_t tgt = cols[c][s];
+                if (tgt == 0xffffu) continue;
+                mask |= 1ull << c;
+                tgts.push_back(remap[tgt]);
+            }
+            rec[(size_t)row * 4] = (uint32_t)mask;
+            rec[(size_t)row * 4 + 1] = (uint32_t)(mask >> 32);
+        }
+        std::vector<uint32_t> sp(rec);
+        sp.resize(rec.size() + (tgts.size() + 1) / 2, 0u);
+        if (!tgts.empty()) memcpy(sp.data() + rec.size(), tgts.data(), tgts.size() * 2);
+        sp.resize((sp.size() + 3) & ~(size_t)3, 0u);
+        if (sp.size() * 4 <= ZS_DFA_LDS_BYTES) {
+            packed.swap(sp);
+            for (uint32_t b = 0; b < 256; b++) clsinfo[b] = cls[b];
+            d->sparse = 1;
+            d->packed_lds = 1;
+        }
+    }
     int prev = 0;
     (void)hipGetDevice(&prev);
     (void)hipSetDevice(ctx->device);
@@ -491,6 +523,7 @@ extern "C" int zs_dfa_mask(zs_ctx* ctx, const zs_dfa* dfa, const zs_vocab* vocab
     a.clsinfo = dfa->d_clsinfo;
     a.remap = dfa->d_remap;
     a.ngood = dfa->ngood;
+    a.sparse = dfa->sparse;
     a.bits = dfa->bits;
     a.rw = dfa->rw;
     a.states = d_states;

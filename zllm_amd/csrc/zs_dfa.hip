@@ -121,6 +121,7 @@ __global__ __launch_bounds__(DM_NT) void zs_k_dfa_mask(dm_args a) {
 #define DL_TW (ZS_WALK_TILE / 32) // bitmap words per row and tile
 #define DL_WORDS (ZS_DFA_LDS_BYTES / 4)
 #define DL_MAXROWS ZS_DFA_MAXROWS
+template <bool SPARSE>
 __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
     __shared__ uint32_t tab[DL_WORDS];
     __shared__ uint16_t ci[256];
@@ -169,7 +170,15 @@ __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
     const uint32_t rw = a.rw;  // bits per state row
     const uint32_t fmask = (1u << a.bits) - 1u;
     // entry at bit offset o: the 32 bits from o of the two words holding it
+    const uint16_t* tgt16 = reinterpret_cast<const uint16_t*>(tab + 4 * (a.ngood + 1));
     auto step = [&](uint32_t st, uint32_t cb) -> uint32_t {
+        if (SPARSE) {
+            // class mask of the state, then the target at the rank of its class
+            const uint4 rec = reinterpret_cast<const uint4*>(tab)[st];
+            const unsigned long long mask = ((unsigned long long)rec.y << 32) | rec.x;
+            if (!((mask >> cb) & 1ull)) return a.ngood;
+            return tgt16[rec.z + (uint32_t)__popcll(mask & ((1ull << cb) - 1ull))];
+        }
         const uint32_t o = __umul24(st, rw) + cb;  // states < 2^16, row bits < 2^16
         const uint32_t w = o >> 5;
         return __builtin_amdgcn_alignbit(tab[w + 1], tab[w], o & 31u) & fmask;
@@ -299,7 +308,10 @@ extern "C" int zs_dfa_mask_launch(const dm_args& a, bool packed_lds, uint32_t nc
     uint32_t ncover = a.V > a.ntab ? a.V : a.ntab;
     if (packed_lds && a.B <= DL_MAXROWS) {
         const uint32_t items = ((ncover + ZS_WALK_TILE - 1) / ZS_WALK_TILE) * ((a.B + DL_RG - 1) / DL_RG);
-        hipLaunchKernelGGL(zs_k_dfa_mask_packed, dim3(min(items, ncu)), dim3(DL_NT), 0, stream, x);
+        if (a.sparse)
+            hipLaunchKernelGGL(zs_k_dfa_mask_packed<true>, dim3(min(items, ncu)), dim3(DL_NT), 0, stream, x);
+        else
+            hipLaunchKernelGGL(zs_k_dfa_mask_packed<false>, dim3(min(items, ncu)), dim3(DL_NT), 0, stream, x);
     } else {
         x.epoch = 0;
         hipLaunchKernelGGL(zs_k_fill_u32, dim3((a.B + 255) / 256), dim3(256), 0, stream, any_scratch, a.B, 0u);

@@ -248,6 +248,10 @@ struct zs_dfa {
     uint16_t* d_remap;     // [nstates] good id or 0xffff
     uint32_t ngood, bits, rw, packed_words;
     int packed_lds;        // the packed table fits the LDS budget
+    // sparse form instead (tables past the budget with at most 64 classes):
+    // d_packed = {mask lo, mask hi, first target, 0} per good state + sink,
+    // then u16 targets; d_clsinfo = class index
+    uint32_t sparse;
 };
 
 // Arguments of the DFA mask kernels (zs_dfa.hip).
@@ -270,6 +274,7 @@ struct dm_args {
     const uint16_t* clsinfo;
     const uint16_t* remap;
     uint32_t ngood, bits, rw;
+    uint32_t sparse;          // packed table in the sparse row form
     const int32_t* states;
     uint32_t B, V, words;
     uint32_t* out;
