@@ -251,18 +251,23 @@ def main():
     # The draft verification is independent of this step's sampling: it runs on
     # a second stream (default priority) and fills the CUs that the sampler's
     # latency-bound row kernels leave idle; the step ends when both are done.
+    # It starts once the sampler's first full pass over the logits is done
+    # (zs_batch.pass_event), beside the latency-bound per-row kernels.
     spec_stream = torch.cuda.Stream()
+    pass_ev = torch.cuda.Event()
+    pass_ev.record(stream)  # creates the event
 
     def step(out=None, overlap=True):
         if overlap:
             spec_stream.wait_stream(stream)
-            with torch.cuda.stream(spec_stream):
-                verify_drafts(ctx, W["tgt"], W["draft_ids"], W["spec_T"], W["spec_seed"], W["spec_ctr"], W["dft"])
-                W["spec_ctr"].add_(1)
         W["dfa"].mask(W["table"], W["st"], V, out=bits)
-        out = sampler.run(xs, bufs, bits, top_stride=5, out=out)
+        out = sampler.run(xs, bufs, bits, top_stride=5, out=out, pass_event=pass_ev if overlap else None)
         bufs["counter"].add_(1)
         if overlap:
+            with torch.cuda.stream(spec_stream):
+                spec_stream.wait_event(pass_ev)
+                verify_drafts(ctx, W["tgt"], W["draft_ids"], W["spec_T"], W["spec_seed"], W["spec_ctr"], W["dft"])
+                W["spec_ctr"].add_(1)
             stream.wait_stream(spec_stream)
         else:
             verify_drafts(ctx, W["tgt"], W["draft_ids"], W["spec_T"], W["spec_seed"], W["spec_ctr"], W["dft"])

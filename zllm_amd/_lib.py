@@ -74,6 +74,7 @@ class Batch(C.Structure):
         ("d_margin", C.c_void_p),
         ("d_chosen_lp", C.c_void_p),
         ("d_status", C.c_void_p),
+        ("pass_event", C.c_void_p),
     ]
 
 

@@ -348,7 +348,10 @@ class BatchSampler:
         return bufs
 
     def run(self, logits: torch.Tensor, bufs: dict, allow_bits: Optional[torch.Tensor] = None,
-            top_stride: int = OPENAI_TOP_LOGPROBS_CAP, out: Optional[dict] = None):
+            top_stride: int = OPENAI_TOP_LOGPROBS_CAP, out: Optional[dict] = None,
+            pass_event: Optional[torch.cuda.Event] = None):
+        """pass_event (optional, already recorded once so that it exists) is
+        recorded after the first full pass over the logits (zs_batch.pass_event)."""
         B, V = logits.shape
         dev = logits.device
         assert logits.dtype == torch.float32 and logits.stride(1) == 1
@@ -379,6 +382,8 @@ class BatchSampler:
             b.allow_words = allow_bits.shape[1]
         b.top_stride = top_stride
         b.d_seed, b.d_counter = bufs["seed"].data_ptr(), bufs["counter"].data_ptr()
+        if pass_event is not None:
+            b.pass_event = pass_event.cuda_event
         for k in ("token", "logprob", "top_ids", "top_lps", "top_n", "entropy", "max_prob", "margin", "chosen_lp",
                   "status"):
             setattr(b, "d_" + k, out[k].data_ptr())
