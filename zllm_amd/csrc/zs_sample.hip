@@ -1051,7 +1051,18 @@ __global__ __launch_bounds__(CB_NT) void zs_k_combine(zs_sargs a) {
         }
         return;
     }
-    const zs_chunk_stat* cs = a.cst + (size_t)r * a.nch;
+    // the row's chunk statistics in LDS (one parallel load; the loops over
+    // chunks below would otherwise wait on one global load per chunk)
+    __shared__ zs_chunk_stat cs_sh[ZS_MAX_CHUNKS];
+    {
+        static_assert(sizeof(zs_chunk_stat) % 4 == 0, "word copy");
+        constexpr uint32_t W = sizeof(zs_chunk_stat) / 4;
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(a.cst + (size_t)r * a.nch);
+        uint32_t* dst = reinterpret_cast<uint32_t*>(cs_sh);
+        for (uint32_t i = t; i < nch * W; i += CB_NT) dst[i] = src[i];
+    }
+    __syncthreads();
+    const zs_chunk_stat* cs = cs_sh;
 
     // ---------------- observers: max, special rows, top candidates ----------------
     float M = -INFINITY;
@@ -1069,11 +1080,12 @@ __global__ __launch_bounds__(CB_NT) void zs_k_combine(zs_sargs a) {
     if (want_lp || want_unc) {
         if (t == 0) n_sh = 0;
         __syncthreads();
-        for (uint32_t c = 0; c < nch; c++) {
-            uint32_t no = cs[c].no;
-            const uint32_t* kk = a.co_key + ((size_t)r * a.nch + c) * ZS_KO;
-            const uint32_t* ii = a.co_idx + ((size_t)r * a.nch + c) * ZS_KO;
-            for (uint32_t i = t; i < no; i += CB_NT) {
+        {
+            // all chunks' lists at once (their order in sbuf does not matter: sorted next)
+            const uint32_t* kk = a.co_key + (size_t)r * a.nch * ZS_KO;
+            const uint32_t* ii = a.co_idx + (size_t)r * a.nch * ZS_KO;
+            for (uint32_t i = t; i < nch * ZS_KO; i += CB_NT) {
+                if (i % ZS_KO >= cs[i / ZS_KO].no) continue;
                 uint32_t pos = atomicAdd(&n_sh, 1u);
                 sbuf[pos] = ((unsigned long long)(~kk[i]) << 32) | ii[i];
             }
@@ -1140,11 +1152,12 @@ __global__ __launch_bounds__(CB_NT) void zs_k_combine(zs_sargs a) {
         // gather sampler candidates
         if (t == 0) n_sh = 0;
         __syncthreads();
-        for (uint32_t c = 0; c < nch; c++) {
-            uint32_t ns = cs[c].ns;
-            const uint32_t* kk = a.cs_key + ((size_t)r * a.nch + c) * ZS_KS;
-            const uint32_t* ii = a.cs_idx + ((size_t)r * a.nch + c) * ZS_KS;
-            for (uint32_t i = t; i < ns; i += CB_NT) {
+        {
+            const uint32_t* kk = a.cs_key + (size_t)r * a.nch * ZS_KS;
+            const uint32_t* ii = a.cs_idx + (size_t)r * a.nch * ZS_KS;
+#pragma unroll 4
+            for (uint32_t i = t; i < nch * ZS_KS; i += CB_NT) {
+                if (i % ZS_KS >= cs[i / ZS_KS].ns) continue;
                 uint32_t pos = atomicAdd(&n_sh, 1u);
                 sbuf[pos] = ((unsigned long long)(~kk[i]) << 32) | ii[i];
             }
