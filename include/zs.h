@@ -232,7 +232,8 @@ typedef struct zs_batch {
     uint32_t* d_status;               /* [B] ZS_ST_* */
     /* optional hipEvent_t, recorded on `stream` once the bandwidth-bound
      * passes over the logits are done (the first pass with its candidate
-     * lists and moments, and the parallel rounds of the softmax sums):
+     * lists and moments, the parallel rounds of the softmax sums and the
+     * probabilities of the rows that take the top-p walk):
      * independent bandwidth-bound work (draft verification of the same step)
      * made to wait on it runs beside the latency-bound per-row kernels that
      * follow instead of slowing those passes. NULL: no event. */

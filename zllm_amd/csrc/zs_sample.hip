@@ -2765,7 +2765,6 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
     const uint32_t nsub = (bt->V + ZS_SUB - 1) / ZS_SUB;
     hipLaunchKernelGGL(zs_k_roundA, dim3((nsub + 3) / 4, B), dim3(256), 0, stream, a);
     mark("zs_k_roundA");
-    if (a.b.pass_event && hipEventRecord((hipEvent_t)a.b.pass_event, stream) != hipSuccess) return -1;
     hipLaunchKernelGGL(zs_k_stitchA, dim3(B, 2), dim3(ST_NT), 0, stream, a);
     mark("zs_k_stitchA");
     // The entropy chain (roundB, stitchB) depends on the observers' S only and
@@ -2783,6 +2782,7 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
     if (!prof) ZS_LAUNCH_CHECK(hipEventRecord((hipEvent_t)ctx->join_event, side));
     hipLaunchKernelGGL(zs_k_pv, dim3((bt->V + ZS_BIG_G - 1) / ZS_BIG_G, B), dim3(ZS_BIG_NT), 0, stream, a);
     mark("zs_k_pv");
+    if (a.b.pass_event && hipEventRecord((hipEvent_t)a.b.pass_event, stream) != hipSuccess) return -1;
     hipLaunchKernelGGL(zs_k_big, dim3(B), dim3(ZS_BIG_NT), 0, stream, a);
     mark("zs_k_big");
     const uint32_t nsubk = (bt->V + ZS_SUB - 1) / ZS_SUB;
