@@ -231,28 +231,20 @@ def copy_probe(mib):
     print(json.dumps({"copy_probe_mib": mib}))
 
 
-def main():
-    args = parse()
-    if args.copy_probe:
-        copy_probe(args.copy_probe)
-        return
-    if args.gpus != 1:
-        print(json.dumps({"error": "this build targets one GPU: run with --gpus 1 (sharding is design-only)"}))
-        sys.exit(2)
-    import numpy as np
+def make_step(W, V):
+    """The timed step over workload W: DFA mask of the grammar rows, the
+    sampler over all rows, draft verification. Returns (step, spec_stream);
+    step(out=None, overlap=True) -> (sampler outputs, (accepted, next)).
+
+    The draft verification is independent of this step's sampling: it runs on
+    a second stream (default priority) and fills the CUs that the sampler's
+    latency-bound row kernels leave idle; the step ends when both are done. It
+    starts once the sampler's bandwidth-bound passes over the logits are done
+    (zs_batch.pass_event), beside the latency-bound per-row kernels."""
     import torch
-    B, V = args.B, args.V
-    W = build_workload(B, V, args.dfa_states, args.seed)
+    from zllm_amd.engine import verify_drafts
     ctx, sampler, bufs, xs, bits = W["ctx"], W["sampler"], W["bufs"], W["xs"], W["bits"]
     stream = torch.cuda.current_stream()
-
-    from zllm_amd.engine import verify_drafts
-
-    # The draft verification is independent of this step's sampling: it runs on
-    # a second stream (default priority) and fills the CUs that the sampler's
-    # latency-bound row kernels leave idle; the step ends when both are done.
-    # It starts once the sampler's first full pass over the logits is done
-    # (zs_batch.pass_event), beside the latency-bound per-row kernels.
     spec_stream = torch.cuda.Stream()
     pass_ev = torch.cuda.Event()
     pass_ev.record(stream)  # creates the event
@@ -266,22 +258,45 @@ def main():
         if overlap:
             with torch.cuda.stream(spec_stream):
                 spec_stream.wait_event(pass_ev)
-                verify_drafts(ctx, W["tgt"], W["draft_ids"], W["spec_T"], W["spec_seed"], W["spec_ctr"], W["dft"])
+                spec = verify_drafts(ctx, W["tgt"], W["draft_ids"], W["spec_T"], W["spec_seed"], W["spec_ctr"],
+                                     W["dft"])
                 W["spec_ctr"].add_(1)
             stream.wait_stream(spec_stream)
         else:
-            verify_drafts(ctx, W["tgt"], W["draft_ids"], W["spec_T"], W["spec_seed"], W["spec_ctr"], W["dft"])
+            spec = verify_drafts(ctx, W["tgt"], W["draft_ids"], W["spec_T"], W["spec_seed"], W["spec_ctr"], W["dft"])
             W["spec_ctr"].add_(1)
-        return out
+        return out, spec
+
+    return step, spec_stream
+
+
+def main():
+    args = parse()
+    if args.copy_probe:
+        copy_probe(args.copy_probe)
+        return
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build targets one GPU: run with --gpus 1 (sharding is design-only)"}))
+        sys.exit(2)
+    import numpy as np
+    import torch
+    B, V = args.B, args.V
+    W = build_workload(B, V, args.dfa_states, args.seed)
+    ctx, xs, bits = W["ctx"], W["xs"], W["bits"]
+    stream = torch.cuda.current_stream()
+
+    from zllm_amd.engine import verify_drafts
+
+    step, spec_stream = make_step(W, V)
 
     out = None
     for _ in range(args.warmup):
-        out = step(out)
+        out, _ = step(out)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
     for _ in range(args.steps):
-        out = step(out)
+        out, _ = step(out)
     e1.record(stream)
     torch.cuda.synchronize()
     ms_step = e0.elapsed_time(e1) / args.steps
@@ -316,7 +331,7 @@ def main():
     acc = {}
     n_prof = 10
     for _ in range(n_prof):
-        out = step(out, overlap=False)  # one stream: events bracket single kernels
+        out, _ = step(out, overlap=False)  # one stream: events bracket single kernels
         for k, v in ctx.last_timings().items():
             acc[k] = acc.get(k, 0.0) + v / n_prof
     ctx.set_profiling(False)
