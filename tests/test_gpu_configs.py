@@ -96,3 +96,62 @@ def test_config5_bench_step():
     assert not bad, bad[:10]
     # the workload exercises acceptance, rejection and the bonus draw
     assert len({a for a, _ in got}) > 1
+
+
+def _grammar_case(V, trans, dead, acc, nrows, seed):
+    """Synthetic vocabulary of V tokens, GPU allow bitsets from random live
+    states, and the oracle's bitsets for the same states."""
+    import torch
+
+    from oracle import oracle as O
+    from tests.gpu_util import ctx
+    from zllm_amd.engine import ByteDfa, TokenByteTable
+    c = ctx(max(64, nrows), 151936)
+    offs, data = synth.synthetic_vocab(V, seed)
+    table = TokenByteTable.from_csr(c, offs, data, np.ones(V, np.uint8), eos=V - 1)
+    dfa = ByteDfa(c, trans, dead, acc)
+    rng = np.random.default_rng(seed)
+    live = [s for s in range(trans.shape[0]) if dfa.is_live(s) and not dead[s]]
+    states = rng.choice(live, nrows).astype(np.int32)
+    bits = dfa.mask(table, torch.tensor(states, device="cuda"), V)
+    torch.cuda.synchronize()
+    got = bits.cpu().numpy().view(np.uint32)
+    ov = O.Vocab([bytes(data[offs[t]:offs[t + 1]]) for t in range(V)], V - 1)
+    od = O.Dfa(trans, dead, acc)
+    with ThreadPoolExecutor(WORKERS) as ex:
+        want = list(ex.map(lambda s: O.mask_bits(V, dfa=od, vocab=ov, state=int(s)), states))
+    bad = [i for i in range(nrows) if not np.array_equal(got[i], want[i])]
+    assert not bad, f"allow bitsets differ on rows {bad[:10]} (states {states[bad[:10]]})"
+    allow = np.stack([np.unpackbits(w.view(np.uint8), bitorder="little")[:V].astype(bool) for w in want])
+    return got, allow
+
+
+def _sample_masked(x, params, bits, allow):
+    from tests.gpu_util import compare, oracle_row, run_gpu
+    out = run_gpu(x, params, allow_bits=bits)
+    with ThreadPoolExecutor(WORKERS) as ex:
+        refs = list(ex.map(lambda i: oracle_row(x[i], params[i], allow[i]), range(len(params))))
+    errs = compare(x, params, out, allow, refs=refs)
+    assert not errs, "\n".join(errs[:20])
+
+
+def test_config3_regex_mask_and_sample():
+    B, V = 32, 128256
+    print(f"[case] config 3 B={B} V={V} dfa=64", flush=True)
+    trans, dead, acc = synth.random_dfa(64, 3, dead_rate=0.3)
+    bits, allow = _grammar_case(V, trans, dead, acc, B, 3)
+    x = synth.logits_powerlaw(B, V, 3)
+    params = [dict(temperature=1.0, top_k=0, top_p=1.0, seed=700 + i, masked=True, top_logprobs=5) for i in range(B)]
+    _sample_masked(x, params, bits, allow)
+
+
+def test_config4_json_schema_mask_ban_and_sample():
+    B, V = 128, 151936
+    print(f"[case] config 4 B={B} V={V} dfa=2048", flush=True)
+    trans, dead, acc = synth.json_dfa(2048, 4)
+    bits, allow = _grammar_case(V, trans, dead, acc, B, 4)
+    x = synth.logits_powerlaw(B, V, 4)
+    rng = np.random.default_rng(4)
+    params = [dict(temperature=0.7, top_k=0, top_p=0.9, seed=900 + i, masked=True, top_logprobs=5,
+                   ban=[int(v) for v in rng.choice(V, 500, replace=False)]) for i in range(B)]
+    _sample_masked(x, params, bits, allow)
