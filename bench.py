@@ -259,7 +259,7 @@ def make_step(W, V):
             with torch.cuda.stream(spec_stream):
                 spec_stream.wait_event(pass_ev)
                 spec = verify_drafts(ctx, W["tgt"], W["draft_ids"], W["spec_T"], W["spec_seed"], W["spec_ctr"],
-                                     W["dft"])
+                                     W["dft"], background=True)
                 W["spec_ctr"].add_(1)
             stream.wait_stream(spec_stream)
         else:

@@ -268,7 +268,16 @@ typedef struct zs_spec_batch {
     const uint64_t* d_counter;      /* [B] */
     uint32_t* d_accepted;           /* [B] */
     uint32_t* d_next;               /* [B] */
+    uint32_t flags;                 /* 0 or ZS_SPEC_BACKGROUND */
 } zs_spec_batch;
+/* ZS_SPEC_BACKGROUND: for a verification that runs on its own stream beside
+ * other GPU work (e.g. after zs_batch.pass_event). The statistics and weight
+ * sums over the target / draft rows then run as one workgroup per (row,
+ * position) and at most one per CU: slower alone, but the second read of each
+ * row comes from the memory-side cache and the other work keeps more of the
+ * memory system. Results are identical. (No reference counterpart: a
+ * scheduling hint of this implementation.) */
+#define ZS_SPEC_BACKGROUND 1u
 int zs_spec_verify(zs_ctx* ctx, const zs_spec_batch* batch, void* stream);
 
 /* ---- batched lane (continuous batching, gpu/batch.rs:176-192) --------------

@@ -88,10 +88,11 @@ def test_sample_topk_on_device():
         assert int(out[s]) == want, s
 
 
+@pytest.mark.parametrize("background", [False, True])
 @pytest.mark.parametrize("k,V", [(4, 3000), (4, 151936), (1, 50)])
-def test_spec_verify_matches_oracle(k, V):
+def test_spec_verify_matches_oracle(k, V, background):
     from zllm_amd.engine import verify_drafts
-    print(f"[case] spec k={k} V={V}", flush=True)
+    print(f"[case] spec k={k} V={V} background={background}", flush=True)
     B = 8
     rng = np.random.default_rng(k + V)
     target = synth.logits_powerlaw(B * (k + 1), V, 7).reshape(B, k + 1, V)
@@ -104,7 +105,7 @@ def test_spec_verify_matches_oracle(k, V):
     ctr = np.full(B, 3, np.uint64)
     t = lambda a, dt=None: torch.from_numpy(np.ascontiguousarray(a)).cuda()
     acc, nxt = verify_drafts(_c(), t(target), t(ids.view(np.int32)), t(temp), t(seeds.view(np.int64)),
-                             t(ctr.view(np.int64)), t(draft))
+                             t(ctr.view(np.int64)), t(draft), background=background)
     acc, nxt = acc.cpu().numpy(), nxt.cpu().numpy().view(np.uint32)
     for b in range(B):
         want = O.spec_verify(target[b], draft[b], ids[b].tolist(), float(temp[b]), int(seeds[b]), int(ctr[b]))

@@ -19,6 +19,8 @@ ZS_ROW_MASKED = 1
 ZS_ROW_LOGPROBS = 2
 ZS_ROW_UNCERTAINTY = 4
 
+ZS_SPEC_BACKGROUND = 1
+
 ZS_ST_GREEDY = 1
 ZS_ST_NONFINITE = 2
 ZS_ST_SMALL = 4
@@ -84,7 +86,7 @@ class SpecBatch(C.Structure):
         ("ld", C.c_uint64),
         ("d_target", C.c_void_p), ("d_draft", C.c_void_p), ("d_draft_ids", C.c_void_p),
         ("d_temperature", C.c_void_p), ("d_seed", C.c_void_p), ("d_counter", C.c_void_p),
-        ("d_accepted", C.c_void_p), ("d_next", C.c_void_p),
+        ("d_accepted", C.c_void_p), ("d_next", C.c_void_p), ("flags", C.c_uint32),
     ]
 
 

@@ -647,6 +647,9 @@ extern "C" int zs_spec_verify(zs_ctx* ctx, const zs_spec_batch* b, void* stream)
     a.accepted = b->d_accepted; a.next = b->d_next;
     a.cst = ctx->spec_chunks; a.rs = ctx->spec_rows;
     a.nch = ctx->max_chunks; a.npos_max = 2 * ZS_SPEC_KMAX + 1;
+    if (b->flags & ~(uint32_t)ZS_SPEC_BACKGROUND)
+        return zs_set_error(ctx, ZS_EINVAL, "zs_spec_verify: unknown flags %#x", b->flags);
+    a.background = (b->flags & ZS_SPEC_BACKGROUND) ? 1u : 0u;
     int prev = zs_device_guard_begin(ctx);
     zs_prof prof{ctx->profiling, ctx->spec_events, ctx->spec_names, &ctx->n_spec_timed};
     int rc = zs_spec_launch(a, prof, (hipStream_t)stream);

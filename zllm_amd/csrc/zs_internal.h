@@ -149,6 +149,7 @@ struct zs_spec_args {
     zs_spec_chunk* cst;         // scratch [B][npos_max][nch]
     zs_spec_row* rs;            // scratch [B]
     uint32_t nch, npos_max;
+    uint32_t background;        // ZS_SPEC_BACKGROUND: the fused one-workgroup-per-CU passes
 };
 
 struct zs_ctx {

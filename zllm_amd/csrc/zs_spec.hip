@@ -163,6 +163,137 @@ __global__ __launch_bounds__(SP_NT) void zs_k_spec_sums(zs_spec_args a) {
     }
 }
 
+// passes 1 + 2 fused: one workgroup per (row, position) walks the row's chunks
+// twice -- the chunk statistics, then (with the row maximum known) the chunk
+// weight sums. One workgroup per CU (its LDS request keeps a second one out):
+// the rows in flight then fit the memory-side cache, and the second walk of a
+// row reads it from there instead of HBM. Writes the same zs_spec_chunk
+// fields as zs_k_spec_stats / zs_k_spec_sums.
+#define SR_NT 1024
+#define SR_NW (SR_NT / 64)
+#define SR_EPT (SP_CH / SR_NT)  // 8 elements per thread, as 2 float4
+#define SR_PAIR 2               // chunks loaded together
+#define SR_LDS_HOLD 90000       // bytes of LDS requested to keep occupancy at one workgroup per CU
+__device__ __forceinline__ void sr_load(const float* row, uint32_t base, uint32_t V, float* x) {
+#pragma unroll
+    for (int j = 0; j < SR_EPT / 4; j++) {
+        const uint32_t id = base + (j * SR_NT + threadIdx.x) * 4;
+        float4 v = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+        if (id < V) v = *reinterpret_cast<const float4*>(row + id);
+        x[4 * j] = v.x; x[4 * j + 1] = v.y; x[4 * j + 2] = v.z; x[4 * j + 3] = v.w;
+    }
+}
+__device__ __forceinline__ uint32_t sr_id(uint32_t base, int e) {
+    return base + ((e >> 2) * SR_NT + threadIdx.x) * 4 + (e & 3);
+}
+
+__global__ __launch_bounds__(SR_NT) void zs_k_spec_row(zs_spec_args a) {
+    extern __shared__ uint32_t hold[];  // occupancy limiter only
+    const uint32_t pos = blockIdx.x, r = blockIdx.y;
+    const uint32_t V = a.V;
+    const uint32_t nch = (V + SP_CH - 1) / SP_CH;
+    __shared__ float wz[ZS_MAX_CHUNKS][SR_NW];
+    __shared__ uint32_t wf[ZS_MAX_CHUNKS][SR_NW];
+    __shared__ unsigned long long wb[ZS_MAX_CHUNKS][SR_NW];
+    __shared__ float cz[ZS_MAX_CHUNKS];
+    if (threadIdx.x == 0) hold[0] = 0;  // the request is used, so it is kept
+    const float T = a.temperature[r];
+    const float* row = sp_row(a, r, pos);
+    const int lane = zs_lane(), wid = zs_wid();
+    zs_spec_chunk* cs = a.cst + ((size_t)r * a.npos_max + pos) * a.nch;
+    for (uint32_t c0 = 0; c0 < nch; c0 += SR_PAIR) {
+        float x[SR_PAIR][SR_EPT];
+#pragma unroll
+        for (int h = 0; h < SR_PAIR; h++) sr_load(row, (c0 + h) * SP_CH, V, x[h]);
+#pragma unroll
+        for (int h = 0; h < SR_PAIR; h++) {
+            const uint32_t c = c0 + h;
+            if (c >= nch) break;
+            const uint32_t base = c * SP_CH;
+            float xmax = -INFINITY;
+            uint32_t fl = 0;
+            unsigned long long best = 0;  // (value key, ~idx): first strict max
+#pragma unroll
+            for (int e = 0; e < SR_EPT; e++) {
+                const uint32_t i = sr_id(base, e);
+                if (i >= V) continue;
+                const float xv = x[h][e];
+                if (xv != xv) fl |= 1u;
+                xmax = fmaxf(xmax, xv);
+                if (xv > -INFINITY) {
+                    const float xx = (xv == 0.0f) ? 0.0f : xv;
+                    const unsigned long long k = ((unsigned long long)zs_total_key(xx) << 32) | (0xffffffffu - i);
+                    best = k > best ? k : best;
+                }
+            }
+            xmax = wave_max_f(xmax);
+            fl = wave_or_u(fl);
+            for (int d = 32; d > 0; d >>= 1) {
+                unsigned long long o = __shfl_xor(best, d, 64);
+                best = o > best ? o : best;
+            }
+            if (lane == 0) { wz[c][wid] = xmax; wf[c][wid] = fl; wb[c][wid] = best; }
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < nch) {
+        const uint32_t c = threadIdx.x;
+        float xmax = -INFINITY;
+        uint32_t fl = 0;
+        unsigned long long best = 0;
+        for (int w = 0; w < SR_NW; w++) {
+            xmax = fmaxf(xmax, wz[c][w]);
+            fl |= wf[c][w];
+            best = wb[c][w] > best ? wb[c][w] : best;
+        }
+        // max z = (max x) / T: division by T > 0 is monotone
+        const float zmax = sp_z(xmax, T);
+        if (zmax == INFINITY) fl |= 2u;
+        cz[c] = zmax;
+        zs_spec_chunk& o = cs[c];
+        o.zmax = zmax;
+        o.flags = fl;
+        o.amax_val = best ? zs_key_to_float((uint32_t)(best >> 32)) : -INFINITY;
+        o.amax_idx = best ? 0xffffffffu - (uint32_t)(best & 0xffffffffull) : 0xffffffffu;
+    }
+    if (!(T > 0.0f) || !a.draft) return;  // greedy verification needs no weights
+    __syncthreads();
+    float m = -INFINITY;
+    for (uint32_t c = 0; c < nch; c++) m = fmaxf(m, cz[c]);
+    const bool fin = m > -INFINITY && m < INFINITY;
+    // x below xl gives z - m < -17.5 whatever the rounding of x / T (0.05 margin)
+    const float xl = (float)(((double)m + (double)SP_ZERO_D - 0.05) * (double)(T != 1.0f ? T : 1.0f));
+    for (uint32_t c0 = 0; c0 < nch; c0 += SR_PAIR) {
+        float x[SR_PAIR][SR_EPT];
+#pragma unroll
+        for (int h = 0; h < SR_PAIR; h++) {
+            const uint32_t c = c0 + h;
+            if (fin && c < nch && cz[c] - m >= SP_ZERO_D) sr_load(row, c * SP_CH, V, x[h]);
+            else
+#pragma unroll
+                for (int e = 0; e < SR_EPT; e++) x[h][e] = -INFINITY;
+        }
+#pragma unroll
+        for (int h = 0; h < SR_PAIR; h++) {
+            const uint32_t c = c0 + h;
+            if (c >= nch) break;
+            uint32_t s32 = 0;  // at most 8 weights below 2^25 each
+#pragma unroll
+            for (int e = 0; e < SR_EPT; e++)
+                if (sr_id(c * SP_CH, e) < V && x[h][e] >= xl) s32 += sp_weight32(sp_z(x[h][e], T), m);
+            unsigned long long s = s32;
+            for (int d = 32; d > 0; d >>= 1) s += __shfl_xor(s, d, 64);
+            if (lane == 0) wb[c][wid] = s;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < nch) {
+        unsigned long long t = 0;
+        for (int w = 0; w < SR_NW; w++) t += wb[threadIdx.x][w];
+        cs[threadIdx.x].wsum = t;
+    }
+}
+
 // pass 3: one wave per row -- accept / reject decisions (lanes over chunks)
 __global__ __launch_bounds__(64) void zs_k_spec_decide(zs_spec_args a) {
     const uint32_t r = blockIdx.x;
@@ -425,10 +556,15 @@ extern "C" int zs_spec_launch(const zs_spec_args& a, const zs_prof& prof, hipStr
     };
     dim3 grid(nch, npos, a.B);
     mark(nullptr);
+    if (a.background) {
+        hipLaunchKernelGGL(zs_k_spec_row, dim3(npos, a.B), dim3(SR_NT), SR_LDS_HOLD, stream, a);
+        mark("zs_k_spec_row");
+    } else {
     hipLaunchKernelGGL(zs_k_spec_stats, grid, dim3(SP_NT), 0, stream, a);
     mark("zs_k_spec_stats");
     hipLaunchKernelGGL(zs_k_spec_sums, grid, dim3(SP_NT), 0, stream, a);
     mark("zs_k_spec_sums");
+    }
     hipLaunchKernelGGL(zs_k_spec_decide, dim3(a.B), dim3(64), 0, stream, a);
     hipLaunchKernelGGL(zs_k_spec_rsum, dim3(nch, a.B), dim3(SP_NT), 0, stream, a);
     hipLaunchKernelGGL(zs_k_spec_draw, dim3(a.B), dim3(SP_BIG_NT), 0, stream, a);

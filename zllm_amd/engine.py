@@ -16,7 +16,8 @@ from typing import Dict, List, Optional, Sequence, Tuple
 import numpy as np
 import torch
 
-from ._lib import (Batch, LaneStream, RowParams, SpecBatch, ZS_OK, ZS_ROW_LOGPROBS, ZS_ROW_MASKED, ZS_ROW_UNCERTAINTY, ZsError, lib)
+from ._lib import (Batch, LaneStream, RowParams, SpecBatch, ZS_OK, ZS_ROW_LOGPROBS, ZS_ROW_MASKED, ZS_ROW_UNCERTAINTY,
+                   ZS_SPEC_BACKGROUND, ZsError, lib)
 
 OPENAI_TOP_LOGPROBS_CAP = 20  # logprobs.rs:27-29
 
@@ -409,10 +410,13 @@ class BatchSampler:
 
 # ---------------------------------------------------------------- spec decode
 def verify_drafts(ctx: Context, target: torch.Tensor, draft_ids: torch.Tensor, temperature: torch.Tensor,
-                  seed: torch.Tensor, counter: torch.Tensor, draft: Optional[torch.Tensor] = None):
+                  seed: torch.Tensor, counter: torch.Tensor, draft: Optional[torch.Tensor] = None,
+                  background: bool = False):
     """Batched spec_decode::verify_drafts (spec_decode.rs:241-267) and, for
     temperature > 0 with draft logits, rejection sampling. target [B, k+1, V],
-    draft [B, k, V], draft_ids [B, k] (int32). Returns (accepted, next)."""
+    draft [B, k, V], draft_ids [B, k] (int32). Returns (accepted, next).
+    background: ZS_SPEC_BACKGROUND, for a call overlapped with other GPU work
+    on another stream (same results)."""
     B, kp1, V = target.shape
     k = kp1 - 1
     dev = target.device
@@ -435,6 +439,7 @@ def verify_drafts(ctx: Context, target: torch.Tensor, draft_ids: torch.Tensor, t
     sb.d_draft_ids = draft_ids.data_ptr()
     sb.d_temperature, sb.d_seed, sb.d_counter = temperature.data_ptr(), seed.data_ptr(), counter.data_ptr()
     sb.d_accepted, sb.d_next = acc.data_ptr(), nxt.data_ptr()
+    sb.flags = ZS_SPEC_BACKGROUND if background else 0
     rc = lib().zs_spec_verify(ctx.h, C.byref(sb), torch.cuda.current_stream(dev).cuda_stream)
     _check(ctx.h, rc, "zs_spec_verify")
     return acc, nxt
