@@ -1309,17 +1309,25 @@ __device__ __forceinline__ sub_row make_sub_row(const zs_sargs& a, uint32_t r, c
 }
 
 // thread t holds elements j*1024 + EPT*t .. +EPT-1 of sub-chunk j
-// (EPT * threads = 1024; EPT is 8 or 16)
+// (EPT * threads = 1024)
 template <int EPT>
 __device__ __forceinline__ void sub_load_t(const sub_row& R, uint32_t j, uint32_t t, float (&x)[EPT], float (&z)[EPT]) {
     const uint32_t base = j * ZS_SUB + (uint32_t)EPT * t;
     uint32_t w = 0xffffffffu;
     if (R.masked && base < R.V) w = R.allow[base >> 5] >> (base & 31);
+    if constexpr (EPT >= 4) {
 #pragma unroll
-    for (int k = 0; k < EPT / 4; k++) {
-        float4 v = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
-        if (base + 4 * k < R.V) v = *reinterpret_cast<const float4*>(R.row + base + 4 * k);
-        x[4 * k] = v.x; x[4 * k + 1] = v.y; x[4 * k + 2] = v.z; x[4 * k + 3] = v.w;
+        for (int k = 0; k < EPT / 4; k++) {
+            float4 v = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+            if (base + 4 * k < R.V) v = *reinterpret_cast<const float4*>(R.row + base + 4 * k);
+            x[4 * k] = v.x; x[4 * k + 1] = v.y; x[4 * k + 2] = v.z; x[4 * k + 3] = v.w;
+        }
+    } else if constexpr (EPT == 2) {
+        float2 v = make_float2(-INFINITY, -INFINITY);
+        if (base < R.V) v = *reinterpret_cast<const float2*>(R.row + base);  // V is a multiple of 4 or row padded
+        x[0] = v.x; x[1] = v.y;
+    } else {
+        x[0] = base < R.V ? R.row[base] : -INFINITY;
     }
 #pragma unroll
     for (int q = 0; q < EPT; q++) {
@@ -1483,7 +1491,7 @@ __global__ __launch_bounds__(256) void zs_k_roundB(zs_sargs a) {
     }
 }
 
-#define ST_NT 128
+#define ST_NT 512
 #define ST_EPT (ZS_SUB / ST_NT)
 
 struct st_sh {
@@ -2553,7 +2561,7 @@ __global__ __launch_bounds__(256) void zs_k_roundK(zs_sargs a) {
 
 // one workgroup per row: sum2 (KIND 0), or the draw (KIND 1) -- the first
 // entry after which the running sum reaches the uniform
-#define SK_NT 128
+#define SK_NT 512
 #define SK_EPT (ZS_SUB / SK_NT)
 template <int KIND>
 __global__ __launch_bounds__(SK_NT) void zs_k_stitchK(zs_sargs a) {
