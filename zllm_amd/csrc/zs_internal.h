@@ -119,6 +119,21 @@ struct zs_row_state {
     float cand_x[ZS_OBS_CAND];
 };
 
+// Top-p walk on bucket totals: the probabilities of a row bucketed by their
+// 13 high bits (rank 0 = the largest values). Per bucket: element count,
+// approximate mass, start / gather cursor in the row's bucket layout, the
+// predicted grid exponent of the running sum and flags (meta), and the total
+// integer increment of its elements on that grid.
+#define ZS_TP_NB 2048
+#define ZS_TP_CAND 64
+#define ZS_TP_CL (2 + ZS_TP_CAND)
+struct zs_tp_bucket {
+    uint32_t cnt;
+    float mass;
+    uint32_t start, cur, meta, pad;
+    unsigned long long tot;
+};
+
 // Speculative-decode verification scratch (zs_spec.hip).
 #define ZS_SPEC_KMAX 16
 struct zs_spec_chunk {
@@ -176,6 +191,9 @@ struct zs_ctx {
     zs_sub_sum* sub_sum;         // [rows][ZS_NSUM][max_subs]
     double* k_ap;                // [rows][max_subs] approximate sums of the kept list per sub-chunk
     zs_sub_sum* k_sum;           // [rows][2][max_subs] kept-list rounds (sum2, draw)
+    zs_tp_bucket* tp_bk;         // [rows][ZS_TP_NB] top-p buckets (zs_k_tp_*)
+    uint32_t* tp_cl;             // [rows][ZS_TP_CL] row flags, candidate count, candidate buckets
+    uint32_t* tp_pre;            // [rows][2][max_vocab] increment prefixes of presorted buckets
     uint32_t* p_sub;             // [rows][max_subs+1] patch index range per sub-chunk
     uint32_t max_subs;
     zs_spec_chunk* spec_chunks;  // [rows][2*ZS_SPEC_KMAX+1][max_chunks]

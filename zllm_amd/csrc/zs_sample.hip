@@ -50,6 +50,9 @@ struct zs_sargs {
     uint32_t max_subs;
     double* k_ap;
     zs_sub_sum* k_sum;
+    zs_tp_bucket* tp_bk;
+    uint32_t* tp_cl;
+    uint32_t* tp_pre;
 };
 
 #define ZS_ST_LIMIT 0x100u
@@ -1270,6 +1273,11 @@ __global__ __launch_bounds__(CB_NT) void zs_k_combine(zs_sargs a) {
         st.klist = 0;
         a.rst[r] = st;
     }
+    if (mode == ZS_MODE_BIG) {
+        // bucket counts and masses of the top-p walk, accumulated by zs_k_pv
+        zs_tp_bucket* bk = a.tp_bk + (size_t)r * ZS_TP_NB;
+        for (uint32_t i = t; i < ZS_TP_NB; i += CB_NT) { bk[i].cnt = 0u; bk[i].mass = 0.0f; }
+    }
 }
 
 
@@ -2070,10 +2078,21 @@ __device__ __forceinline__ float big_s_value(const zs_row_state& st) {
     return reuse ? st.obs_S : st.samp_S;
 }
 
+// Rows whose top-p walk runs on bucket totals (zs_k_tp_*): p comes from
+// zs_k_pv, no min-p (the walked values are the p themselves), the top-k
+// threshold is known, and the largest p alone stays below top_p (else the walk
+// stops at its first element).
+__device__ __forceinline__ bool tp_fast_row(const zs_row_state& st, const zs_row_params& P) {
+    if (st.mode != ZS_MODE_BIG || !big_s_from_rounds(st) || st.has_thr == 2) return false;
+    if (P.min_p > 0.0f || !(P.top_p < 1.0f && P.top_p > 0.0f)) return false;
+    return !(1.0f / big_s_value(st) >= P.top_p);
+}
+
 // Probabilities p = exp(z - max) / S (sampler.rs:68-69) of the big rows whose
 // S is known, one workgroup per (group of ZS_BIG_G elements, row): the exact
 // exponentials are the bulk of a big row's arithmetic, spread here over the
-// whole GPU instead of one workgroup per row.
+// whole GPU instead of one workgroup per row. Rows of the bucket-total walk
+// also add their positive p to the per-bucket counts and masses.
 __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_pv(zs_sargs a) {
     const uint32_t g = blockIdx.x, r = blockIdx.y;
     const zs_row_state& st = a.rst[r];
@@ -2081,28 +2100,493 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_pv(zs_sargs a) {
     const zs_batch& b = a.b;
     const uint32_t V = b.V;
     const uint32_t idx0 = g * ZS_BIG_G + 4 * threadIdx.x;
-    if (idx0 >= V) return;
     const zs_row_params P = b.d_params[r];
-    big_row R;
-    R.row = b.d_logits + (size_t)r * b.ld;
-    R.masked = (P.flags & ZS_ROW_MASKED) && b.d_allow_bits;
-    R.allow = R.masked ? b.d_allow_bits + (size_t)r * b.allow_words : nullptr;
-    R.pid = a.p_id + (size_t)r * ZS_MAX_PATCHES;
-    R.pfl = a.p_flags + (size_t)r * ZS_MAX_PATCHES;
-    R.py = a.p_y + (size_t)r * ZS_MAX_PATCHES;
-    R.psub = a.p_sub + (size_t)r * (a.max_subs + 1);
-    R.nsub = (V + ZS_SUB - 1) / ZS_SUB;
-    R.V = V;
-    R.T = P.temperature;
-    const bool use_thr = st.has_thr != 0;
-    const float thr = zs_key_to_float(st.thr_key), m = st.z_max, S = big_s_value(st);
-    float x[4], z[4];
-    big_finish(R, g, big_fetch(R, g), x, z);
-    uint4 o;
-    uint32_t* ob = reinterpret_cast<uint32_t*>(&o);
+    const bool hist = tp_fast_row(st, P);
+    __shared__ uint32_t hc[ZS_TP_NB];
+    __shared__ float hm[ZS_TP_NB];
+    if (hist) {
+        for (uint32_t i = threadIdx.x; i < ZS_TP_NB; i += ZS_BIG_NT) { hc[i] = 0u; hm[i] = 0.0f; }
+        __syncthreads();
+    }
+    if (idx0 < V) {
+        big_row R;
+        R.row = b.d_logits + (size_t)r * b.ld;
+        R.masked = (P.flags & ZS_ROW_MASKED) && b.d_allow_bits;
+        R.allow = R.masked ? b.d_allow_bits + (size_t)r * b.allow_words : nullptr;
+        R.pid = a.p_id + (size_t)r * ZS_MAX_PATCHES;
+        R.pfl = a.p_flags + (size_t)r * ZS_MAX_PATCHES;
+        R.py = a.p_y + (size_t)r * ZS_MAX_PATCHES;
+        R.psub = a.p_sub + (size_t)r * (a.max_subs + 1);
+        R.nsub = (V + ZS_SUB - 1) / ZS_SUB;
+        R.V = V;
+        R.T = P.temperature;
+        const bool use_thr = st.has_thr != 0;
+        const float thr = zs_key_to_float(st.thr_key), m = st.z_max, S = big_s_value(st);
+        float x[4], z[4];
+        big_finish(R, g, big_fetch(R, g), x, z);
+        uint4 o;
+        uint32_t* ob = reinterpret_cast<uint32_t*>(&o);
 #pragma unroll
-    for (int q = 0; q < 4; q++) ob[q] = zs_f2u(idx0 + q < V ? big_term_e(z[q], use_thr, thr, m) / S : 0.0f);
-    *reinterpret_cast<uint4*>(a.pv + (size_t)r * a.max_vocab + idx0) = o;
+        for (int q = 0; q < 4; q++) ob[q] = zs_f2u(idx0 + q < V ? big_term_e(z[q], use_thr, thr, m) / S : 0.0f);
+        *reinterpret_cast<uint4*>(a.pv + (size_t)r * a.max_vocab + idx0) = o;
+        if (hist) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const float p = zs_u2f(ob[q]);
+                if (p > 0.0f) {
+                    const uint32_t rk = bk_rank<0>(ob[q]);
+                    atomicAdd(&hc[rk], 1u);
+                    atomicAdd(&hm[rk], p);
+                }
+            }
+        }
+    }
+    if (hist) {
+        __syncthreads();
+        zs_tp_bucket* bk = a.tp_bk + (size_t)r * ZS_TP_NB;
+        for (uint32_t i = threadIdx.x; i < ZS_TP_NB; i += ZS_BIG_NT) {
+            if (hc[i]) {
+                atomicAdd(&bk[i].cnt, hc[i]);
+                atomicAdd(&bk[i].mass, hm[i]);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Top-p walk on bucket totals (sampler.rs:91-104), for the rows of
+// tp_fast_row. The running f32 sum over the p in descending order is fixed by
+// integer increments inside each binade of the sum (zs_math.h), so a bucket
+// the sum crosses without an event adds the total of its elements' increments
+// on the grid of that binade, whatever their order. The kernels below
+//   zs_k_tp_plan  (one workgroup per row): bucket starts, the predicted grid of
+//                 every bucket from the approximate prefix masses, and the
+//                 candidate buckets that may hold an event (the prefix range,
+//                 widened by a bound on the f32 rounding error, crosses a
+//                 power of two or top_p; the first bucket);
+//   zs_k_tp_inc   (all CUs): per-bucket increment totals on the predicted grid
+//                 and the exact-half (tie) flags; every positive p is gathered
+//                 into the bucket layout; buckets with ties become candidates;
+//   zs_k_tp_sort  (one workgroup per candidate): sorts the bucket in
+//                 descending order and stores the prefix of its increment
+//                 maps on the predicted grid (a parity pair, so ties are
+//                 exact) and the prefix of its increments on the next grid;
+// leave the walk itself to one wave in zs_k_big (tp_walk), which adds bucket
+// totals with wave scans and resolves a bucket with an event by binary
+// searches on the stored prefixes (or by adding its sorted values one by one).
+// A walk that meets anything it cannot resolve exactly (an event in a bucket
+// that was not presorted, a grid other than the two prepared) reports failure
+// and the row takes the workgroup walk below.
+// ---------------------------------------------------------------------------
+#define TP_M_EG 0xffu
+#define TP_M_CAND 0x100u
+#define TP_M_TIE0 0x200u
+#define TP_M_TIE1 0x400u
+#define TP_M_SORTED 0x800u
+#define TP_ROW_FAST 1u
+#define TP_SORT_MAX 4096
+#define TP_SORT_NT 1024
+#define TP_SERIAL_N 512
+
+__global__ __launch_bounds__(ZS_BIG_NT) void zs_k_tp_plan(zs_sargs a) {
+    const uint32_t r = blockIdx.x;
+    const int t = threadIdx.x;
+    uint32_t* cl = a.tp_cl + (size_t)r * ZS_TP_CL;
+    const zs_row_state& st = a.rst[r];
+    const zs_row_params P = a.b.d_params[r];
+    if (!tp_fast_row(st, P)) {
+        if (t == 0) cl[0] = 0u;
+        return;
+    }
+    __shared__ uint32_t su[ZS_BIG_NT / 64];
+    __shared__ double sd[ZS_BIG_NT / 64];
+    zs_tp_bucket* bk = a.tp_bk + (size_t)r * ZS_TP_NB;
+    static_assert(ZS_TP_NB == 2 * ZS_BIG_NT, "two buckets per thread");
+    uint32_t c[2];
+    double m[2];
+#pragma unroll
+    for (int k2 = 0; k2 < 2; k2++) {
+        c[k2] = bk[2 * t + k2].cnt;
+        m[k2] = (double)bk[2 * t + k2].mass;
+    }
+    uint32_t ctot;
+    double mtot;
+    const uint32_t cex = block_excl_scan_u<ZS_BIG_NT>(c[0] + c[1], su, &ctot);
+    const double mex = block_excl_scan_d<ZS_BIG_NT>(m[0] + m[1], sd, &mtot);
+    const double top_p = (double)P.top_p;
+    uint32_t cand[2], meta[2];
+#pragma unroll
+    for (int k2 = 0; k2 < 2; k2++) {
+        const uint32_t start = cex + (k2 ? c[0] : 0u);
+        const double P0 = k2 ? mex + m[0] : mex, P1 = P0 + m[k2];
+        // margin for |f32 running sum - prefix mass| (rounding of the additions
+        // and of the float mass accumulation); a wrong prediction is caught by
+        // the walk, so this is a typical bound, not a worst case
+        const double delta = ldexp(P1 * (16.0 * sqrt((double)(start + c[k2])) + 64.0), -24) + 1e-30;
+        const double lo = P0 - delta > 0.0 ? P0 - delta : 0.0, hi = P1 + delta;
+        // the sum stops at top_p: buckets past it are never walked, and a
+        // binade above top_p is never entered
+        const int e0 = zs_grid_exp((float)lo), e1 = zs_grid_exp((float)fmin(hi, top_p));
+        const bool cd = c[k2] != 0u && lo < top_p && (P0 == 0.0 || e0 != e1 || hi >= top_p);
+        cand[k2] = cd ? 1u : 0u;
+        meta[k2] = (uint32_t)(cd ? e0 : e1) | (cd ? TP_M_CAND : 0u);
+        zs_tp_bucket& B = bk[2 * t + k2];
+        B.start = start;
+        B.cur = start;
+        B.meta = meta[k2];
+        B.tot = 0ull;
+    }
+    uint32_t ntot;
+    const uint32_t pos = block_excl_scan_u<ZS_BIG_NT>(cand[0] + cand[1], su, &ntot);
+    if (ntot > ZS_TP_CAND) {
+        if (t == 0) cl[0] = 0u;
+        return;
+    }
+    uint32_t q = pos;
+#pragma unroll
+    for (int k2 = 0; k2 < 2; k2++)
+        if (cand[k2]) cl[2 + q++] = 2 * t + k2;
+    if (t == 0) {
+        cl[0] = TP_ROW_FAST;
+        cl[1] = ntot;
+    }
+}
+
+__global__ __launch_bounds__(ZS_BIG_NT) void zs_k_tp_inc(zs_sargs a) {
+    const uint32_t g = blockIdx.x, r = blockIdx.y;
+    uint32_t* cl = a.tp_cl + (size_t)r * ZS_TP_CL;
+    if (!(cl[0] & TP_ROW_FAST)) return;
+    const uint32_t V = a.b.V;
+    const int t = threadIdx.x;
+    __shared__ uint32_t lc[ZS_TP_NB];
+    __shared__ unsigned long long lt[ZS_TP_NB];
+    __shared__ uint32_t lf[ZS_TP_NB];
+#ifdef ZS_DEBUG_TPT
+    const unsigned long long w0 = wall_clock64();
+#endif
+    for (uint32_t i = t; i < ZS_TP_NB; i += ZS_BIG_NT) { lc[i] = 0u; lt[i] = 0ull; lf[i] = 0u; }
+    __syncthreads();
+    zs_tp_bucket* bk = a.tp_bk + (size_t)r * ZS_TP_NB;
+    const uint32_t idx0 = g * ZS_BIG_G + 4 * t;
+    uint4 v = idx0 < V ? *reinterpret_cast<const uint4*>(a.pv + (size_t)r * a.max_vocab + idx0) : make_uint4(0u, 0u, 0u, 0u);
+    const uint32_t pb[4] = {v.x, v.y, v.z, v.w};
+    uint32_t off[4], rk[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        rk[q] = bk_rank<0>(pb[q]);
+        off[q] = 0u;
+        if (zs_u2f(pb[q]) > 0.0f) {
+            const int eg = (int)(bk[rk[q]].meta & TP_M_EG);
+            const seq_pair pr = seq_pair_of(zs_u2f(pb[q]), eg);
+            off[q] = atomicAdd(&lc[rk[q]], 1u);
+            atomicAdd(&lt[rk[q]], (unsigned long long)pr.e);
+            if (pr.e != pr.o) lf[rk[q]] = 1u;
+        }
+    }
+    __syncthreads();
+    for (uint32_t i = t; i < ZS_TP_NB; i += ZS_BIG_NT) {
+        if (!lc[i]) continue;
+        lc[i] = atomicAdd(&bk[i].cur, lc[i]);  // this group's base in the bucket
+        atomicAdd(&bk[i].tot, lt[i]);
+        if (lf[i]) {
+            const uint32_t old = atomicOr(&bk[i].meta, TP_M_TIE0);
+            if (!(old & (TP_M_TIE0 | TP_M_CAND))) {
+                const uint32_t j = atomicAdd(&cl[1], 1u);
+                if (j < ZS_TP_CAND) cl[2 + j] = i;
+            }
+        }
+    }
+    __syncthreads();
+    uint32_t* gv = a.pairs + (size_t)r * a.max_vocab * 2;
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+        if (zs_u2f(pb[q]) > 0.0f) gv[lc[rk[q]] + off[q]] = pb[q];
+#ifdef ZS_DEBUG_TPT
+    if (t == 0) printf("tpinc %u %u start %llu dur %llu\n", r, g, w0, wall_clock64() - w0);
+#endif
+}
+
+// Composition of increment maps over a workgroup, in thread order: exclusive
+// prefix of the thread maps (and of plain saturating sums alongside).
+template <int NT>
+__device__ __forceinline__ seq_pair tp_block_excl_pairs(seq_pair v, uint32_t& sv, uint32_t* sh, uint32_t* tot_s) {
+    const int lane = zs_lane(), w = zs_wid();
+    seq_pair inc = v;
+    uint32_t sinc = sv;
+    for (int d = 1; d < 64; d <<= 1) {
+        seq_pair y;
+        y.e = __shfl_up(inc.e, d, 64);
+        y.o = __shfl_up(inc.o, d, 64);
+        const uint32_t ys = __shfl_up(sinc, d, 64);
+        if (lane >= d) { inc = seq_compose(y, inc); sinc = zs_sat_add(ys, sinc); }
+    }
+    seq_pair ex;
+    ex.e = __shfl_up(inc.e, 1, 64);
+    ex.o = __shfl_up(inc.o, 1, 64);
+    uint32_t sex = __shfl_up(sinc, 1, 64);
+    if (lane == 0) { ex.e = ex.o = 0u; sex = 0u; }
+    if (lane == 63) { sh[3 * w] = inc.e; sh[3 * w + 1] = inc.o; sh[3 * w + 2] = sinc; }
+    __syncthreads();
+    seq_pair pre = {0u, 0u};
+    uint32_t spre = 0u, stot = 0u;
+    for (int i = 0; i < NT / 64; i++) {
+        const seq_pair wi = {sh[3 * i], sh[3 * i + 1]};
+        if (i < w) { pre = seq_compose(pre, wi); spre = zs_sat_add(spre, sh[3 * i + 2]); }
+        stot = zs_sat_add(stot, sh[3 * i + 2]);
+    }
+    __syncthreads();
+    *tot_s = stot;
+    sv = zs_sat_add(spre, sex);
+    return seq_compose(pre, ex);
+}
+
+// Bitonic compare-exchange step (k, j) over 4 values per thread, element i =
+// 4 * thread + e, descending: strides 1 and 2 inside the thread, 4..255 by
+// lane exchanges, larger ones through LDS.
+__device__ __forceinline__ void tp_bitonic_step(uint32_t (&v)[4], uint32_t k, uint32_t j, uint32_t* sb) {
+    const uint32_t t = threadIdx.x;
+    if (j < 4u) {
+#pragma unroll
+        for (uint32_t e = 0; e < 4u; e++) {
+            const uint32_t pe = e ^ j;
+            if (pe > e) {
+                const uint32_t i = 4u * t + e;
+                const bool desc = (i & k) == 0u;
+                const uint32_t x = v[e], y = v[pe];
+                if ((x < y) == desc) { v[e] = y; v[pe] = x; }
+            }
+        }
+        return;
+    }
+    uint32_t w[4];
+    if (j < 256u) {
+#pragma unroll
+        for (uint32_t e = 0; e < 4u; e++) w[e] = __shfl_xor(v[e], (int)(j >> 2), 64);
+    } else {
+#pragma unroll
+        for (uint32_t e = 0; e < 4u; e++) sb[4u * t + e] = v[e];
+        __syncthreads();
+#pragma unroll
+        for (uint32_t e = 0; e < 4u; e++) w[e] = sb[(4u * t + e) ^ j];
+        __syncthreads();
+    }
+#pragma unroll
+    for (uint32_t e = 0; e < 4u; e++) {
+        const uint32_t i = 4u * t + e;
+        const bool desc = (i & k) == 0u, lower = (i & j) == 0u;
+        v[e] = (lower == desc) ? max(v[e], w[e]) : min(v[e], w[e]);
+    }
+}
+
+__global__ __launch_bounds__(TP_SORT_NT) void zs_k_tp_sort(zs_sargs a) {
+    const uint32_t c = blockIdx.x, r = blockIdx.y;
+    const uint32_t t = threadIdx.x;
+    const uint32_t* cl = a.tp_cl + (size_t)r * ZS_TP_CL;
+    if (!(cl[0] & TP_ROW_FAST) || c >= min(cl[1], (uint32_t)ZS_TP_CAND)) return;
+    const uint32_t bi = cl[2 + c];
+    zs_tp_bucket* B = a.tp_bk + (size_t)r * ZS_TP_NB + bi;
+    const uint32_t n = B->cnt, st0 = B->start;
+    if (n == 0u || n > TP_SORT_MAX) return;
+    __shared__ uint32_t sb[TP_SORT_MAX];
+    __shared__ uint32_t sh[3 * TP_SORT_NT / 64];
+    uint32_t* gv = a.pairs + (size_t)r * a.max_vocab * 2 + st0;
+    uint32_t* q1 = gv + a.max_vocab;
+    uint32_t* pe = a.tp_pre + (size_t)r * a.max_vocab * 2 + st0;
+    uint32_t* po = pe + a.max_vocab;
+#ifdef ZS_DEBUG_TPT
+    const unsigned long long w0 = wall_clock64();
+#endif
+    uint32_t np2 = 256;
+    while (np2 < n) np2 <<= 1;
+    uint32_t v[4];
+#pragma unroll
+    for (uint32_t e = 0; e < 4u; e++) {
+        const uint32_t i = 4u * t + e;
+        v[e] = i < n ? gv[i] : 0u;   // 0 (p = 0) sorts last
+    }
+#ifdef ZS_DEBUG_TPT
+    const unsigned long long w1 = wall_clock64();
+#endif
+    for (uint32_t k = 2; k <= np2; k <<= 1)
+        for (uint32_t j = k >> 1; j > 0; j >>= 1) tp_bitonic_step(v, k, j, sb);
+#ifdef ZS_DEBUG_TPT
+    const unsigned long long w2 = wall_clock64();
+#endif
+    // prefixes over the sorted order: thread t owns elements 4t..4t+3
+    const int eg0 = (int)(B->meta & TP_M_EG), eg1 = eg0 + 1;
+    seq_pair loc = {0u, 0u};
+    uint32_t s1 = 0u, tie1 = 0u;
+    seq_pair pr[4];
+    uint32_t i1[4];
+#pragma unroll
+    for (uint32_t e = 0; e < 4u; e++) {
+        const uint32_t i = 4u * t + e;
+        const float x = i < n ? zs_u2f(v[e]) : 0.0f;
+        pr[e] = seq_pair_of(x, eg0);
+        uint32_t tie;
+        i1[e] = zs_seq_inc(x, eg1, &tie);
+        tie1 |= tie;
+        loc = seq_compose(loc, pr[e]);
+        s1 = zs_sat_add(s1, i1[e]);
+    }
+    uint32_t stot;
+    seq_pair run = tp_block_excl_pairs<TP_SORT_NT>(loc, s1, sh, &stot);
+    uint32_t srun = s1;
+#pragma unroll
+    for (uint32_t e = 0; e < 4u; e++) {
+        const uint32_t i = 4u * t + e;
+        run = seq_compose(run, pr[e]);
+        srun = zs_sat_add(srun, i1[e]);
+        if (i < n) {
+            gv[i] = v[e];
+            pe[i] = run.e;
+            po[i] = run.o;
+            q1[i] = srun;
+        }
+    }
+    tie1 = __syncthreads_or(tie1);
+    if (t == 0) atomicOr(&B->meta, TP_M_SORTED | (tie1 ? TP_M_TIE1 : 0u));
+#ifdef ZS_DEBUG_TPT
+    if (t == 0) printf("tpsort %u %u n %u start %llu load %llu sort %llu end %llu\n", r, c, n, w0, w1 - w0, w2 - w1, wall_clock64() - w2);
+#endif
+}
+
+// First j in [lo, hi) with pred(j) (pred monotone: false then true), or hi;
+// one wave, every lane calls it with the same arguments.
+template <class F>
+__device__ __forceinline__ uint32_t tp_first(uint32_t lo, uint32_t hi, const F& pred) {
+    const uint32_t lane = (uint32_t)zs_lane();
+    const uint32_t hi0 = hi;
+    while (hi - lo > 64u) {
+        const uint32_t seg = (hi - lo + 63u) / 64u;
+        const uint32_t s0 = lo + lane * seg;
+        const uint32_t j = min(s0 + seg, hi) - 1u;
+        const unsigned long long m = __ballot(s0 < hi && pred(j));
+        if (!m) return hi0;
+        const uint32_t f = (uint32_t)__ffsll((long long)m) - 1u;
+        const uint32_t nhi = min(lo + (f + 1u) * seg, hi);
+        lo = lo + f * seg;
+        hi = nhi;
+    }
+    const unsigned long long m = __ballot(lo + lane < hi && pred(lo + lane));
+    return m ? lo + (uint32_t)__ffsll((long long)m) - 1u : hi0;
+}
+
+// The walk itself, by one wave (tp_fast_row rows): returns 1 with the stop
+// (value, rank among equal values) in *wo, 2 when the sum never reaches top_p,
+// 0 when the row must take the workgroup walk.
+__device__ __forceinline__ int tp_walk(const zs_sargs& a, uint32_t r, float top_p, walk_out* wo) {
+    const uint32_t lane = (uint32_t)zs_lane();
+    const zs_tp_bucket* bk = a.tp_bk + (size_t)r * ZS_TP_NB;
+    const uint32_t* gv = a.pairs + (size_t)r * a.max_vocab * 2;
+    const uint32_t* q1 = gv + a.max_vocab;
+    const uint32_t* pe = a.tp_pre + (size_t)r * a.max_vocab * 2;
+    const uint32_t* po = pe + a.max_vocab;
+    float s = 0.0f;
+    int eg = zs_grid_exp(s);
+    unsigned long long k = 0ull;
+    uint32_t kthr = zs_grid_thresh(top_p, eg);
+    auto set_sum = [&](float ns) {
+        s = ns;
+        eg = zs_grid_exp(s);
+        k = zs_grid_k(s);
+        kthr = zs_grid_thresh(top_p, eg);
+    };
+    uint32_t b0 = 0;
+    while (b0 < ZS_TP_NB) {
+        const uint32_t bb = b0 + lane;
+        uint32_t cnt = 0u, meta = 0u;
+        unsigned long long tot = 0ull;
+        if (bb < ZS_TP_NB) { cnt = bk[bb].cnt; meta = bk[bb].meta; tot = bk[bb].tot; }
+        const bool special = cnt && ((int)(meta & TP_M_EG) != eg || (meta & TP_M_TIE0));
+        const unsigned long long inc = (cnt && !special) ? tot : 0ull;
+        unsigned long long incl = inc;
+        for (int d = 1; d < 64; d <<= 1) {
+            const unsigned long long y = __shfl_up(incl, d, 64);
+            if (lane >= (uint32_t)d) incl += y;
+        }
+        const unsigned long long lim = min((unsigned long long)ZS_BINADE, (unsigned long long)kthr);
+        const unsigned long long hm = __ballot(cnt && (special || k + incl >= lim));
+        if (!hm) {
+            k += __shfl(incl, 63, 64);
+            b0 += 64;
+            continue;
+        }
+        const uint32_t f = (uint32_t)__ffsll((long long)hm) - 1u;
+        k += __shfl(incl - inc, (int)f, 64);
+        const uint32_t b = b0 + f;
+        b0 = b + 1;
+        const uint32_t n = __shfl(cnt, (int)f, 64), bm = __shfl(meta, (int)f, 64);
+        if (!(bm & TP_M_SORTED)) {
+#ifdef ZS_DEBUG_TP
+            if (lane == 0) printf("tp fail row %u bucket %u n %u meta %x eg %d k %llu kthr %u\n", r, b, n, bm, eg, k, kthr);
+#endif
+            return 0;
+        }
+        const uint32_t st0 = bk[b].start;
+        // the bucket in exact descending order, from the exact sum k * grid
+        uint32_t pos = 0;
+        bool done = false, stop = false;
+        uint32_t at = 0;
+        const int G0 = (int)(bm & TP_M_EG);
+        if (n > TP_SERIAL_N && eg == G0) {
+            const uint32_t* P = ((k & 1ull) ? po : pe) + st0;
+            const unsigned long long lm = min((unsigned long long)ZS_BINADE, (unsigned long long)kthr);
+            const uint32_t i = tp_first(0u, n, [&](uint32_t j) { return k + P[j] >= lm; });
+            if (i == n) {
+                k += P[n - 1];
+                done = true;
+            } else if (k + P[i] < ZS_BINADE) {
+                stop = true;
+                at = i;
+            } else {
+                const unsigned long long prev = k + (i ? P[i - 1] : 0u);
+                const float ns = zs_grid_value((uint32_t)prev, eg) + zs_u2f(gv[st0 + i]);
+                if (ns >= top_p) { stop = true; at = i; }
+                else { set_sum(ns); pos = i + 1; }
+            }
+        }
+        if (!done && !stop && n > TP_SERIAL_N && pos < n && eg == G0 + 1 && !(bm & TP_M_TIE1) &&
+            q1[st0 + n - 1] < ZS_INC_CAP) {
+            const uint32_t base = pos ? q1[st0 + pos - 1] : 0u;
+            const unsigned long long lm = min((unsigned long long)ZS_BINADE, (unsigned long long)kthr);
+            const uint32_t j = tp_first(pos, n, [&](uint32_t jj) { return k + (q1[st0 + jj] - base) >= lm; });
+            if (j == n) {
+                k += q1[st0 + n - 1] - base;
+                done = true;
+            } else if (k + (q1[st0 + j] - base) < ZS_BINADE) {
+                stop = true;
+                at = j;
+            } else {
+                const unsigned long long prev = k + (j > pos ? q1[st0 + j - 1] - base : 0u);
+                const float ns = zs_grid_value((uint32_t)prev, eg) + zs_u2f(gv[st0 + j]);
+                if (ns >= top_p) { stop = true; at = j; }
+                else { set_sum(ns); pos = j + 1; }
+            }
+        }
+        if (!done && !stop) {
+            // one addition at a time (sampler.rs:103)
+            float ss = zs_grid_value((uint32_t)k, eg);
+            for (uint32_t i = pos; i < n && !stop; i += 64) {
+                const float v = i + lane < n ? zs_u2f(gv[st0 + i + lane]) : 0.0f;
+                const uint32_t m = min(64u, n - i);
+                for (uint32_t j = 0; j < m; j++) {
+                    ss = ss + __shfl(v, (int)j, 64);
+                    if (ss >= top_p) { stop = true; at = i + j; break; }
+                }
+            }
+            if (!stop) set_sum(ss);
+        }
+        if (stop) {
+            const uint32_t vs = gv[st0 + at];
+            const uint32_t first = tp_first(0u, at + 1, [&](uint32_t j) { return gv[st0 + j] <= vs; });
+            wo->stopped = true;
+            wo->v = vs;
+            wo->rank = at - first;
+            return 1;
+        }
+    }
+    return 2;
 }
 
 __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
@@ -2269,6 +2753,24 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
         // lowest index holding that value.
         const uint32_t pmax1 = zs_f2u(p1_of(zs_f2u(1.0f / S)));
         const bool peak = zs_u2f(pmax1) >= P.top_p;
+        // the walk on bucket totals (one wave) when zs_k_tp_* prepared it
+        walk_out wo = {false, 0u, 0u};
+        int fw = 0;
+        if (!peak && (a.tp_cl[(size_t)r * ZS_TP_CL] & TP_ROW_FAST)) {
+            if (t < 64) {
+                walk_out w = {false, 0u, 0u};
+                const int res = tp_walk(a, r, P.top_p, &w);
+                if (t == 0) { sh.u[0] = (uint32_t)res; sh.u[1] = w.v; sh.u[2] = w.rank; }
+            }
+            __syncthreads();
+            fw = (int)sh.u[0];
+            wo = {fw == 1, sh.u[1], sh.u[2]};
+            __syncthreads();
+        }
+#ifdef ZS_DEBUG_TP
+        if (t == 0) printf("tp row %u peak %d fast %u ncand %u fw %d\n", r, (int)peak, a.tp_cl[(size_t)r * ZS_TP_CL], a.tp_cl[(size_t)r * ZS_TP_CL + 1], fw);
+#endif
+        if (fw == 0) {
         // counts per (rank, copy): 16 copies by lane keep same-address LDS
         // atomics (skewed histograms) at most 4-way
         uint32_t* cc = sh.sortbuf;
@@ -2316,7 +2818,6 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
         BIG_MARK();
         const uint32_t rlim = sh.u[0];
         float s = 0.0f;
-        walk_out wo = {false, 0u, 0u};
         uint32_t done = 0;  // walked prefix of the level-0 layout
         for (int round = 0; round < 2 && !wo.stopped && !peak; round++) {
             const uint32_t rlo = round == 0 ? 0u : rlim + 1, rhi = round == 0 ? rlim : BK_NB - 1;
@@ -2364,6 +2865,7 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
 #endif
             done = upto;
         }
+        }  // fw == 0
         BIG_MARK();
         if (peak) wo = {true, pmax1, 0u};
         if (wo.stopped) {
@@ -2753,6 +3255,9 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
     a.max_subs = ctx->max_subs;
     a.k_ap = ctx->k_ap;
     a.k_sum = ctx->k_sum;
+    a.tp_bk = ctx->tp_bk;
+    a.tp_cl = ctx->tp_cl;
+    a.tp_pre = ctx->tp_pre;
     const uint32_t B = bt->B;
     const uint32_t nch = (bt->V + ZS_P1_CH - 1) / ZS_P1_CH;
     const bool prof = ctx->profiling != 0;
@@ -2791,6 +3296,12 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
     hipLaunchKernelGGL(zs_k_pv, dim3((bt->V + ZS_BIG_G - 1) / ZS_BIG_G, B), dim3(ZS_BIG_NT), 0, stream, a);
     mark("zs_k_pv");
     if (a.b.pass_event && hipEventRecord((hipEvent_t)a.b.pass_event, stream) != hipSuccess) return -1;
+    hipLaunchKernelGGL(zs_k_tp_plan, dim3(B), dim3(ZS_BIG_NT), 0, stream, a);
+    mark("zs_k_tp_plan");
+    hipLaunchKernelGGL(zs_k_tp_inc, dim3((bt->V + ZS_BIG_G - 1) / ZS_BIG_G, B), dim3(ZS_BIG_NT), 0, stream, a);
+    mark("zs_k_tp_inc");
+    hipLaunchKernelGGL(zs_k_tp_sort, dim3(ZS_TP_CAND, B), dim3(TP_SORT_NT), 0, stream, a);
+    mark("zs_k_tp_sort");
     hipLaunchKernelGGL(zs_k_big, dim3(B), dim3(ZS_BIG_NT), 0, stream, a);
     mark("zs_k_big");
     const uint32_t nsubk = (bt->V + ZS_SUB - 1) / ZS_SUB;
