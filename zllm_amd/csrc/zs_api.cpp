@@ -73,7 +73,7 @@ extern "C" void zs_ctx_destroy(zs_ctx* ctx) {
     if (ctx->lane_host) (void)hipHostFree(ctx->lane_host);
     void* ptrs[] = {ctx->p_cnt, ctx->p_id, ctx->p_flags, ctx->p_y, ctx->cst, ctx->cs_key, ctx->cs_idx,
                     ctx->co_key, ctx->co_idx, ctx->rst, ctx->pairs, ctx->pv, ctx->mask_scratch, ctx->spec_chunks,
-                    ctx->spec_rows, ctx->sub_mom, ctx->sub_sum, ctx->p_sub, ctx->k_ap, ctx->k_sum, ctx->tp_bk, ctx->tp_cl, ctx->tp_pre,
+                    ctx->spec_rows, ctx->sub_mom, ctx->sub_sum, ctx->p_sub, ctx->k_ap, ctx->k_sum, ctx->tp_bk, ctx->tp_cl, ctx->tp_pre, ctx->kcnt,
                     ctx->lane_temp, ctx->lane_topk, ctx->lane_topp, ctx->lane_seed, ctx->lane_vals,
                     ctx->lane_idxs, ctx->lane_ck, ctx->lane_cn};
     for (void* p : ptrs)
@@ -136,6 +136,7 @@ extern "C" int zs_ctx_create(int device, uint32_t max_rows, uint32_t max_vocab, 
     if (!rc) rc = zs_alloc(ctx, &ctx->tp_bk, R * ZS_TP_NB);
     if (!rc) rc = zs_alloc(ctx, &ctx->tp_cl, R * ZS_TP_CL);
     if (!rc) rc = zs_alloc(ctx, &ctx->tp_pre, R * (size_t)max_vocab * 2);
+    if (!rc) rc = zs_alloc(ctx, &ctx->kcnt, R * C * 2);
     if (!rc) rc = zs_alloc(ctx, &ctx->spec_rows, R);
     if (!rc) rc = zs_alloc(ctx, &ctx->lane_temp, R);
     if (!rc) rc = zs_alloc(ctx, &ctx->lane_topk, R);

@@ -113,6 +113,10 @@ struct zs_row_state {
     uint32_t klist;       // 1: list ready
     uint32_t nk;          // list length
     uint32_t vstar, istar;  // kept: p > v*, or p == v* and id <= i*
+    uint32_t kpend;       // 1: the kept list is compacted by zs_k_kcount / zs_k_kwrite
+    uint32_t krank;       // rank of the top-p stop among the values equal to v*
+    uint32_t kminp;       // min-p applies: p1 = p < kcut ? 0 : p / kkept
+    float kcut, kkept;
     float sum2;           // sequential sum of the kept set (sampler.rs:107)
     uint32_t n_cand;      // observer candidates by (x~ desc, id asc)
     uint32_t cand_id[ZS_OBS_CAND];
@@ -194,6 +198,7 @@ struct zs_ctx {
     zs_tp_bucket* tp_bk;         // [rows][ZS_TP_NB] top-p buckets (zs_k_tp_*)
     uint32_t* tp_cl;             // [rows][ZS_TP_CL] row flags, candidate count, candidate buckets
     uint32_t* tp_pre;            // [rows][2][max_vocab] increment prefixes of presorted buckets
+    uint32_t* kcnt;              // [rows][2 * max_chunks] kept-set counts per 4096-id group
     uint32_t* p_sub;             // [rows][max_subs+1] patch index range per sub-chunk
     uint32_t max_subs;
     zs_spec_chunk* spec_chunks;  // [rows][2*ZS_SPEC_KMAX+1][max_chunks]

@@ -53,6 +53,7 @@ struct zs_sargs {
     zs_tp_bucket* tp_bk;
     uint32_t* tp_cl;
     uint32_t* tp_pre;
+    uint32_t* kcnt;
 };
 
 #define ZS_ST_LIMIT 0x100u
@@ -1271,6 +1272,7 @@ __global__ __launch_bounds__(CB_NT) void zs_k_combine(zs_sargs a) {
         for (uint32_t j = 0; j < n_cand; j++) { st.cand_id[j] = cid_sh[j]; st.cand_x[j] = cx_sh[j]; }
         st.z_is_x = z_is_x;
         st.klist = 0;
+        st.kpend = 0;
         a.rst[r] = st;
     }
     if (mode == ZS_MODE_BIG) {
@@ -2869,74 +2871,19 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
         BIG_MARK();
         if (peak) wo = {true, pmax1, 0u};
         if (wo.stopped) {
-            vstar = wo.v;
-            // The kept set is {p1 > v*} plus the first rank+1 elements equal to v*
-            // in index order (the sort is stable). Compact {p1 >= v*} in index
-            // order; sum2 and the draw only see these (the others are 0 and
-            // leave a running sum unchanged).
-            uint32_t* kp = gv;
-            uint32_t* ki = tmp;
-            uint32_t nk = 0;
-            stream_p1([&](uint32_t g, const float (&p)[4]) {
-                uint32_t c = 0;
-#pragma unroll
-                for (int q = 0; q < 4; q++) c += (p[q] > 0.0f && zs_f2u(p[q]) >= vstar) ? 1u : 0u;
-                uint32_t tot;
-                uint32_t pos = nk + block_excl_scan_u<ZS_BIG_NT>(c, sh.hist2, &tot);
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    if (p[q] > 0.0f && zs_f2u(p[q]) >= vstar) {
-                        kp[pos] = zs_f2u(p[q]);
-                        ki[pos] = g * ZS_BIG_G + 4 * t + q;
-                        pos++;
-                    }
-                }
-                nk += tot;
-                return false;
-            });
-            __threadfence_block();
-            __syncthreads();
-            BIG_MARK();
-            // i*: the (rank+1)-th list element equal to v*
-            if (t == 0) sh.u[7] = 0xffffffffu;
-            __syncthreads();
-            uint32_t seen = 0;
-            for (uint32_t q0 = 0; q0 < nk; q0 += ZS_BIG_NT) {
-                const uint32_t i = q0 + t;
-                const uint32_t hit = (i < nk && kp[i] == vstar) ? 1u : 0u;
-                uint32_t tot;
-                const uint32_t ex = block_excl_scan_u<ZS_BIG_NT>(hit, sh.hist2, &tot);
-                if (hit && seen + ex == wo.rank) sh.u[7] = ki[i];
-                seen += tot;
-                if (seen > wo.rank) break;
-            }
-            __syncthreads();
-            istar = sh.u[7];
-            __syncthreads();
-            // ---- the sum over the kept set (sampler.rs:107) and the draw run as
-            // parallel rounds over the list (zs_k_roundK / zs_k_stitchK): here the
-            // approximate sum of every 1024-entry sub-chunk, one wave per sub-chunk
-            const uint32_t nks = (nk + ZS_SUB - 1) / ZS_SUB;
-            double* ap = a.k_ap + (size_t)r * a.max_subs;
-            for (uint32_t j = zs_wid(); j < nks; j += ZS_BIG_NT / 64) {
-                double acc = 0.0;
-#pragma unroll
-                for (int q = 0; q < ZS_SUB / 64; q++) {
-                    const uint32_t i = j * ZS_SUB + q * 64 + zs_lane();
-                    if (i < nk && (kp[i] > vstar || ki[i] <= istar)) acc += (double)zs_u2f(kp[i]);
-                }
-                acc = wave_sum_d(acc);
-                if (zs_lane() == 0) ap[j] = acc;
-            }
-#ifdef ZS_DEBUG_WALK
-            if (t == 0) printf("walk row %u peak %d nk %u sorts %llu sortn %llu finds %llu findclk %llu sortclk %llu exactclk %llu maxn %llu walkclk %llu\n", r, (int)peak, nk,
-                               zs_dbg_walk[r][0], zs_dbg_walk[r][1], zs_dbg_walk[r][2], zs_dbg_walk[r][3], zs_dbg_walk[r][4], zs_dbg_walk[r][5], zs_dbg_walk[r][6], zs_dbg_walk[r][7]);
-#endif
+            // The kept set is {p1 > v*} plus the first rank+1 elements equal to
+            // v* in index order (the sort is stable); zs_k_kcount / zs_k_kwrite
+            // compact {p1 >= v*} in index order over all CUs, and sum2 and the
+            // draw run as rounds over that list.
             if (t == 0) {
-                a.rst[r].klist = 1;
-                a.rst[r].nk = nk;
-                a.rst[r].vstar = vstar;
-                a.rst[r].istar = istar;
+                zs_row_state& o = a.rst[r];
+                o.vstar = wo.v;
+                o.krank = wo.rank;
+                o.istar = 0xffffffffu;
+                o.kminp = minp ? 1u : 0u;
+                o.kcut = cut;
+                o.kkept = kept;
+                o.kpend = 1;
             }
             return;
         } else {
@@ -2978,6 +2925,120 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
     if (t == 0) {
         a.rst[r].token = token;
         a.rst[r].mode = ZS_MODE_DONE;
+    }
+}
+
+// ===========================================================================
+// Compaction of the kept set {p1 >= v*} in index order (rows with a top-p
+// stop), over all CUs: zs_k_kcount counts per 4096-id group the values above
+// and equal to v*; zs_k_kwrite places each group's elements after the groups
+// before it, finds i* (the (rank+1)-th element equal to v*) and adds the
+// approximate sums of the kept list per 1024-entry sub-chunk (the predictions
+// of the kept-list rounds).
+// ===========================================================================
+__device__ __forceinline__ float kc_p1(const zs_row_state& st, uint32_t pb) {
+    float p = zs_u2f(pb);
+    if (st.kminp) {
+        if (p < st.kcut) p = 0.0f;
+        else if (st.kkept > 0.0f) p = p / st.kkept;
+    }
+    return p;
+}
+
+__global__ __launch_bounds__(ZS_BIG_NT) void zs_k_kcount(zs_sargs a) {
+    const uint32_t g = blockIdx.x, r = blockIdx.y;
+    const zs_row_state& st = a.rst[r];
+    if (!st.kpend) return;
+    const uint32_t t = threadIdx.x, V = a.b.V;
+    const uint32_t idx0 = g * ZS_BIG_G + 4 * t;
+    const uint4 v = idx0 < V ? *reinterpret_cast<const uint4*>(a.pv + (size_t)r * a.max_vocab + idx0) : make_uint4(0u, 0u, 0u, 0u);
+    const uint32_t pb[4] = {v.x, v.y, v.z, v.w};
+    const uint32_t vs = st.vstar;
+    uint32_t c = 0;  // (above << 16) | equal
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const float p = kc_p1(st, pb[q]);
+        const uint32_t b = zs_f2u(p);
+        if (p > 0.0f && b >= vs) c += b > vs ? 0x10000u : 1u;
+    }
+    __shared__ uint32_t sh[ZS_BIG_NT / 64];
+    c = wave_sum_u(c);
+    if (zs_lane() == 0) sh[zs_wid()] = c;
+    __syncthreads();
+    if (t == 0) {
+        uint32_t tot = 0;
+        for (int i = 0; i < ZS_BIG_NT / 64; i++) tot += sh[i];
+        a.kcnt[(size_t)r * a.nch * 2 + g] = tot;
+    }
+    // the kept-list sub-chunk sums are added by zs_k_kwrite
+    if (t < ZS_BIG_G / ZS_SUB) a.k_ap[(size_t)r * a.max_subs + g * (ZS_BIG_G / ZS_SUB) + t] = 0.0;
+}
+
+__global__ __launch_bounds__(ZS_BIG_NT) void zs_k_kwrite(zs_sargs a) {
+    const uint32_t g = blockIdx.x, r = blockIdx.y;
+    zs_row_state& st = a.rst[r];
+    if (!st.kpend) return;
+    const uint32_t t = threadIdx.x, V = a.b.V;
+    const uint32_t ng = (V + ZS_BIG_G - 1) / ZS_BIG_G;
+    __shared__ uint32_t sh[ZS_BIG_NT / 64];
+    __shared__ uint32_t base_sh[3];
+    __shared__ double lap[ZS_BIG_G / ZS_SUB + 1];
+    const uint32_t* kc = a.kcnt + (size_t)r * a.nch * 2;
+    if (t < 64) {
+        // elements and equal elements before this group, and the totals
+        uint32_t pre_all = 0, pre_eq = 0, tot_all = 0;
+        for (uint32_t i = t; i < ng; i += 64) {
+            const uint32_t c = kc[i];
+            const uint32_t n = (c >> 16) + (c & 0xffffu);
+            if (i < g) { pre_all += n; pre_eq += c & 0xffffu; }
+            tot_all += n;
+        }
+        pre_all = wave_sum_u(pre_all);
+        pre_eq = wave_sum_u(pre_eq);
+        tot_all = wave_sum_u(tot_all);
+        if (t == 0) { base_sh[0] = pre_all; base_sh[1] = pre_eq; base_sh[2] = tot_all; }
+    }
+    if (t <= ZS_BIG_G / ZS_SUB) lap[t] = 0.0;
+    __syncthreads();
+    const uint32_t base = base_sh[0], eq0 = base_sh[1];
+    const uint32_t idx0 = g * ZS_BIG_G + 4 * t;
+    const uint4 v = idx0 < V ? *reinterpret_cast<const uint4*>(a.pv + (size_t)r * a.max_vocab + idx0) : make_uint4(0u, 0u, 0u, 0u);
+    const uint32_t pb[4] = {v.x, v.y, v.z, v.w};
+    const uint32_t vs = st.vstar, rank = st.krank;
+    uint32_t kb[4];
+    uint32_t c = 0;  // (kept << 16) | equal
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const float p = kc_p1(st, pb[q]);
+        kb[q] = zs_f2u(p);
+        if (p > 0.0f && kb[q] >= vs) c += 0x10000u + (kb[q] == vs ? 1u : 0u);
+    }
+    uint32_t tot;
+    uint32_t ex = block_excl_scan_u<ZS_BIG_NT>(c, sh, &tot);
+    uint32_t pos = base + (ex >> 16), eq = eq0 + (ex & 0xffffu);
+    uint32_t* kp = a.pairs + (size_t)r * a.max_vocab * 2;
+    uint32_t* ki = kp + a.max_vocab;
+    const uint32_t sub0 = base / ZS_SUB;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        if (!(zs_u2f(kb[q]) > 0.0f && kb[q] >= vs)) continue;
+        const uint32_t idx = idx0 + q;
+        kp[pos] = kb[q];
+        ki[pos] = idx;
+        bool in = true;
+        if (kb[q] == vs) {
+            if (eq == rank) st.istar = idx;
+            in = eq <= rank;
+            eq++;
+        }
+        if (in) atomicAdd(&lap[pos / ZS_SUB - sub0], (double)zs_u2f(kb[q]));
+        pos++;
+    }
+    __syncthreads();
+    if (t <= ZS_BIG_G / ZS_SUB && lap[t] != 0.0) atomicAdd(&a.k_ap[(size_t)r * a.max_subs + sub0 + t], lap[t]);
+    if (g == 0 && t == 0) {
+        st.nk = base_sh[2];
+        st.klist = 1;
     }
 }
 
@@ -3258,6 +3319,7 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
     a.tp_bk = ctx->tp_bk;
     a.tp_cl = ctx->tp_cl;
     a.tp_pre = ctx->tp_pre;
+    a.kcnt = ctx->kcnt;
     const uint32_t B = bt->B;
     const uint32_t nch = (bt->V + ZS_P1_CH - 1) / ZS_P1_CH;
     const bool prof = ctx->profiling != 0;
@@ -3304,6 +3366,9 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
     mark("zs_k_tp_sort");
     hipLaunchKernelGGL(zs_k_big, dim3(B), dim3(ZS_BIG_NT), 0, stream, a);
     mark("zs_k_big");
+    hipLaunchKernelGGL(zs_k_kcount, dim3((bt->V + ZS_BIG_G - 1) / ZS_BIG_G, B), dim3(ZS_BIG_NT), 0, stream, a);
+    hipLaunchKernelGGL(zs_k_kwrite, dim3((bt->V + ZS_BIG_G - 1) / ZS_BIG_G, B), dim3(ZS_BIG_NT), 0, stream, a);
+    mark("zs_k_kcompact");
     const uint32_t nsubk = (bt->V + ZS_SUB - 1) / ZS_SUB;
     hipLaunchKernelGGL(zs_k_roundK<0>, dim3((nsubk + 3) / 4, B), dim3(256), 0, stream, a);
     hipLaunchKernelGGL(zs_k_stitchK<0>, dim3(B), dim3(SK_NT), 0, stream, a);
