@@ -571,9 +571,9 @@ ZO_API float zo_philox_uniform(uint64_t seed, uint64_t counter, uint32_t tag) {
  * Speculative-decode verification. temperature <= 0: verify_drafts
  * (spec_decode.rs:241-267). temperature > 0: rejection sampling
  * (Leviathan et al. 2023, Chen et al. 2023) as libzs defines it with
- * integer weights W_v = w(z_v - max z), z = x / T, where w(d) is 0 for
- * d < -17.5 and otherwise rint(2^24 * 2^t) with t = d * log2(e) evaluated
- * as a fixed sequence of f32 operations (zo_spec_w_of below); accept
+ * integer weights W_v = rint(2^24 * 2^t), t = (x_v - max x) * c, c = the f32
+ * quotient log2(e) / T, evaluated as a fixed sequence of f32 operations
+ * (zo_spec_w below; 0 for t < -25, where the formula rounds to 0); accept
  * draft d at step i iff U_i * Q_d * sum(P) <= P_d * sum(Q) * 2^32 (U_i the
  * 32-bit Philox word, tag 1+i); at the first rejection draw from
  * max(0, P sum(Q) - Q sum(P)) (P if that is all zero) with tag 1+k+i; after k
@@ -593,29 +593,26 @@ static uint32_t zo_philox_u32(uint64_t seed, uint64_t counter, uint32_t tag) {
     return o[0];
 }
 
-static float zo_spec_z(float x, float T) { return (T > 0.0f && T != 1.0f) ? x / T : x; }
-
-/* row stats: max z (NaN ignored), degenerate flag */
-static int zo_spec_row_max(const float* x, uint32_t V, float T, float* m) {
+/* row stats: max x (NaN ignored), degenerate flag (NaN, +inf, all -inf) */
+static int zo_spec_row_max(const float* x, uint32_t V, float* m) {
     float mm = -INFINITY;
     int bad = 0;
     for (uint32_t v = 0; v < V; v++) {
-        float z = zo_spec_z(x[v], T);
-        if (z != z || z == INFINITY) bad = 1;
-        mm = rmax(mm, z);
+        if (x[v] != x[v] || x[v] == INFINITY) bad = 1;
+        mm = rmax(mm, x[v]);
     }
     if (mm == -INFINITY) bad = 1;
     *m = mm;
     return bad;
 }
 
-/* w(d): 2^t, t = d * log2(e) (f32 product), split t = n + f with n = floor(t),
+/* w: t = (x - m) * c (two f32 operations), split t = n + f with n = floor(t),
  * 2^f from the degree-7 Taylor polynomial of exp(f ln 2) by fmaf Horner, then
  * rint(2^f * 2^(24 + n)). Every step is one correctly rounded f32 operation,
  * so any IEEE implementation reproduces the integer exactly. */
-static uint64_t zo_spec_w_of(float d) {
-    if (!(d >= -17.5f)) return 0;
-    const float t = d * 1.44269502f;
+static uint64_t zo_spec_w(float x, float c, float m) {
+    const float t = (x - m) * c;
+    if (!(t >= -25.0f)) return 0;
     const float n = floorf(t);
     const float f = t - n;
     float p = 1.52527338e-05f;
@@ -628,7 +625,6 @@ static uint64_t zo_spec_w_of(float d) {
     p = fmaf(p, f, 1.0f);
     return (uint64_t)rintf(ldexpf(p, 24 + (int)n));
 }
-static uint64_t zo_spec_w(float x, float T, float m) { return zo_spec_w_of(zo_spec_z(x, T) - m); }
 
 ZO_API uint32_t zo_spec_verify(const float* target, const float* draft, const uint32_t* drafts, uint32_t k,
                                uint32_t V, float T, uint64_t seed, uint64_t counter, uint32_t* next) {
@@ -637,27 +633,28 @@ ZO_API uint32_t zo_spec_verify(const float* target, const float* draft, const ui
     uint64_t st[64], sd[64];
     if (!greedy) {
         for (uint32_t p = 0; p <= k && !greedy; p++)
-            if (zo_spec_row_max(target + (size_t)p * V, V, T, &mt[p])) greedy = 1;
+            if (zo_spec_row_max(target + (size_t)p * V, V, &mt[p])) greedy = 1;
         for (uint32_t p = 0; p < k && !greedy; p++)
-            if (zo_spec_row_max(draft + (size_t)p * V, V, T, &md[p])) greedy = 1;
+            if (zo_spec_row_max(draft + (size_t)p * V, V, &md[p])) greedy = 1;
     }
     if (greedy) return zo_verify_drafts(drafts, k, target, k + 1, V, next);
+    const float c = 1.44269502f / T;
     for (uint32_t p = 0; p <= k; p++) {
         uint64_t s = 0;
-        for (uint32_t v = 0; v < V; v++) s += zo_spec_w(target[(size_t)p * V + v], T, mt[p]);
+        for (uint32_t v = 0; v < V; v++) s += zo_spec_w(target[(size_t)p * V + v], c, mt[p]);
         st[p] = s;
     }
     for (uint32_t p = 0; p < k; p++) {
         uint64_t s = 0;
-        for (uint32_t v = 0; v < V; v++) s += zo_spec_w(draft[(size_t)p * V + v], T, md[p]);
+        for (uint32_t v = 0; v < V; v++) s += zo_spec_w(draft[(size_t)p * V + v], c, md[p]);
         sd[p] = s;
     }
     uint32_t i = 0;
     for (; i < k; i++) {
         uint32_t d = drafts[i];
         if (d >= V) break;
-        uint64_t P = zo_spec_w(target[(size_t)i * V + d], T, mt[i]);
-        uint64_t Q = zo_spec_w(draft[(size_t)i * V + d], T, md[i]);
+        uint64_t P = zo_spec_w(target[(size_t)i * V + d], c, mt[i]);
+        uint64_t Q = zo_spec_w(draft[(size_t)i * V + d], c, md[i]);
         uint32_t U = zo_philox_u32(seed, counter, 1u + i);
         zo_u128 lhs = (zo_u128)U * Q * st[i];
         zo_u128 rhs = ((zo_u128)P * sd[i]) << 32;
@@ -672,8 +669,8 @@ ZO_API uint32_t zo_spec_verify(const float* target, const float* draft, const ui
     uint32_t word;
     if (residual) {
         for (uint32_t v = 0; v < V; v++) {
-            zo_u128 pp = (zo_u128)zo_spec_w(trow[v], T, mt[i]) * sd[i];
-            zo_u128 qq = (zo_u128)zo_spec_w(drow[v], T, md[i]) * st[i];
+            zo_u128 pp = (zo_u128)zo_spec_w(trow[v], c, mt[i]) * sd[i];
+            zo_u128 qq = (zo_u128)zo_spec_w(drow[v], c, md[i]) * st[i];
             total += pp > qq ? pp - qq : 0;
         }
         word = zo_philox_u32(seed, counter, 1u + k + i);
@@ -688,11 +685,11 @@ ZO_API uint32_t zo_spec_verify(const float* target, const float* draft, const ui
     for (uint32_t v = 0; v < V; v++) {
         zo_u128 w;
         if (residual) {
-            zo_u128 pp = (zo_u128)zo_spec_w(trow[v], T, mt[i]) * sd[i];
-            zo_u128 qq = (zo_u128)zo_spec_w(drow[v], T, md[i]) * st[i];
+            zo_u128 pp = (zo_u128)zo_spec_w(trow[v], c, mt[i]) * sd[i];
+            zo_u128 qq = (zo_u128)zo_spec_w(drow[v], c, md[i]) * st[i];
             w = pp > qq ? pp - qq : 0;
         } else {
-            w = zo_spec_w(trow[v], T, mt[pos]);
+            w = zo_spec_w(trow[v], c, mt[pos]);
         }
         run += w;
         if (w > 0 && run > thr) { *next = v; break; }

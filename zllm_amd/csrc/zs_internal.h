@@ -141,7 +141,7 @@ struct zs_tp_bucket {
 // Speculative-decode verification scratch (zs_spec.hip).
 #define ZS_SPEC_KMAX 16
 struct zs_spec_chunk {
-    float zmax;
+    float xmax;           // chunk maximum of x (NaN ignored)
     uint32_t flags;
     float amax_val;
     uint32_t amax_idx;

@@ -573,7 +573,16 @@ struct p1_lds_arr {
     __device__ __forceinline__ float& operator[](int e) const { return p[e * ZS_P1_NT]; }
 };
 
+#ifdef ZS_DEBUG_P1
+__device__ unsigned long long zs_dbg_p1[10];
+#define P1_MARK(k) do { if (threadIdx.x == 0) { const long long c1_ = clock64(); atomicAdd(&zs_dbg_p1[k], (unsigned long long)(c1_ - p1c0)); p1c0 = c1_; } } while (0)
+#else
+#define P1_MARK(k) do {} while (0)
+#endif
 __global__ __launch_bounds__(ZS_P1_NT) __attribute__((amdgpu_waves_per_eu(3))) void zs_k_pass1(zs_sargs a) {
+#ifdef ZS_DEBUG_P1
+    long long p1c0 = clock64();
+#endif
     const uint32_t c = blockIdx.x, r = blockIdx.y;
     const zs_batch& b = a.b;
     const uint32_t V = b.V;
@@ -586,18 +595,13 @@ __global__ __launch_bounds__(ZS_P1_NT) __attribute__((amdgpu_waves_per_eu(3))) v
     const bool masked = (P.flags & ZS_ROW_MASKED) && b.d_allow_bits;
     const float* row = b.d_logits + (size_t)r * b.ld;
 
-    // patch range of this chunk (patch ids are sorted)
-    const uint32_t np = a.p_cnt[r];
+    // patch range of this chunk (patch ids are sorted; zs_k_prep stored the
+    // first patch of every 1024-id sub-chunk)
     const uint32_t* pid = a.p_id + (size_t)r * ZS_MAX_PATCHES;
-    if (t == 0) {
-        uint32_t lo = 0, hi = np;
-        while (lo < hi) { uint32_t mid = (lo + hi) >> 1; if (pid[mid] < base) lo = mid + 1; else hi = mid; }
-        uint32_t p0 = lo;
-        hi = np;
-        while (lo < hi) { uint32_t mid = (lo + hi) >> 1; if (pid[mid] < base + ZS_P1_CH) lo = mid + 1; else hi = mid; }
-        sh.pcur0 = p0;
-        sh.pcur1 = lo;
-    }
+    const uint32_t* psub = a.p_sub + (size_t)r * (a.max_subs + 1);
+    const uint32_t nsub_row = (V + ZS_SUB - 1) / ZS_SUB;
+    const uint32_t pc0 = psub[c * ZS_SUBS_PER_CHUNK];
+    const uint32_t pc1 = psub[min((c + 1) * ZS_SUBS_PER_CHUNK, nsub_row)];
 
     // x~ lives in LDS (thread t's element e at xsh[e][t]) until the observer
     // list, z in registers: both arrays in registers would halve occupancy
@@ -627,30 +631,44 @@ __global__ __launch_bounds__(ZS_P1_NT) __attribute__((amdgpu_waves_per_eu(3))) v
         }
     }
     __syncthreads();
-    // patches: bans change x~, bias/penalty set y
+    P1_MARK(1);
+    // patches: bans change x~, bias/penalty set y. Staged through LDS a
+    // batch at a time (one load per thread), then each thread applies those
+    // that fall on its elements.
     {
         const uint32_t* pfl = a.p_flags + (size_t)r * ZS_MAX_PATCHES;
         const float* py = a.p_y + (size_t)r * ZS_MAX_PATCHES;
-        for (uint32_t p = sh.pcur0; p < sh.pcur1; p++) {
-            uint32_t off = pid[p] - base;
-            uint32_t q = off & 3, tt = (off >> 2) % ZS_P1_NT, j = (off >> 2) / ZS_P1_NT;
-            if ((int)tt == t) {
+        for (uint32_t pb = pc0; pb < pc1; pb += ZS_P1_NT) {
+            const uint32_t n = min((uint32_t)ZS_P1_NT, pc1 - pb);
+            if ((uint32_t)t < n) {
+                sh.skey[t] = pid[pb + t] - base;
+                sh.sidx[t] = pfl[pb + t];
+                sh.tmax[t] = zs_f2u(py[pb + t]);
+            }
+            __syncthreads();
+            for (uint32_t i = 0; i < n; i++) {
+                const uint32_t off = sh.skey[i];
+                const uint32_t q = off & 3, tt = (off >> 2) % ZS_P1_NT, j = (off >> 2) / ZS_P1_NT;
+                if ((int)tt != t) continue;
+                const uint32_t fl = sh.sidx[i];
+                const float y = zs_u2f(sh.tmax[i]);
 #pragma unroll
                 for (int jj = 0; jj < P1_EPT / 4; jj++)
 #pragma unroll
                     for (int qq = 0; qq < 4; qq++)
                         if (jj == (int)j && qq == (int)q) {
-                            uint32_t fl = pfl[p];
                             if (fl & ZS_PF_BAN) { xo[jj * 4 + qq] = -INFINITY; zv[jj * 4 + qq] = -INFINITY; }
-                            if (fl & ZS_PF_Y) zv[jj * 4 + qq] = py[p];
+                            if (fl & ZS_PF_Y) zv[jj * 4 + qq] = y;
                         }
             }
+            __syncthreads();
         }
     }
     // z = y / T
 #pragma unroll
     for (int e = 0; e < P1_EPT; e++) zv[e] = zs_temper(zv[e], T);
 
+    P1_MARK(3);
     // ---- chunk statistics of x~ (observers) and z (sampler), one workgroup
     // reduction: maxima, NaN / +inf flags, the last NaN of z, and counts of
     // finite z and of elements whose key is above that of -inf for the lists
@@ -698,6 +716,7 @@ __global__ __launch_bounds__(ZS_P1_NT) __attribute__((amdgpu_waves_per_eu(3))) v
     for (int w = 0; w < ZS_P1_NT / 64; w++) {
         zfin += sh.red[w].zfin; zabove += sh.red[w].zabove; xabove += sh.red[w].xabove;
     }
+    P1_MARK(4);
     const uint32_t nvalid = min((uint32_t)ZS_P1_CH, V - base);
     // greedy: argmax-last (ties -> larger index) over all, and over the tail
     // after the chunk's last NaN (the whole chunk when it has no NaN). A pair
@@ -739,6 +758,7 @@ __global__ __launch_bounds__(ZS_P1_NT) __attribute__((amdgpu_waves_per_eu(3))) v
         tail_n = (int)block_sum_u<ZS_P1_NT>(tn, sh.u);
     }
 
+    P1_MARK(5);
     // ---- approximate moments per 1024-logit sub-chunk (predictions for the
     // exact-sum rounds). Float4 j of thread t holds ids base + (j*NT + t)*4..+3,
     // so it lies in sub-chunk j*P1_SPF + t*4/1024 of the chunk: a wave's float4
@@ -800,6 +820,7 @@ __global__ __launch_bounds__(ZS_P1_NT) __attribute__((amdgpu_waves_per_eu(3))) v
         __syncthreads();
     }
 
+    P1_MARK(6);
     // ---- candidate lists (keys recomputed from the values where needed)
     const size_t lofs = ((size_t)r * a.nch + c);
     // sampler list size: top_k when the row has a top-k cut within range
@@ -818,6 +839,7 @@ __global__ __launch_bounds__(ZS_P1_NT) __attribute__((amdgpu_waves_per_eu(3))) v
                          &s_full, sh);
         }
     }
+    P1_MARK(7);
     uint32_t ntl = P.top_logprobs > 20 ? 20 : P.top_logprobs;
     uint32_t Ko = ntl + 8;
     if (Ko > ZS_KO) Ko = ZS_KO;
@@ -832,6 +854,7 @@ __global__ __launch_bounds__(ZS_P1_NT) __attribute__((amdgpu_waves_per_eu(3))) v
         p1_topk_fast(xr, vmask, nvalid, xabove, Ko, base, a.co_key + lofs * ZS_KO, a.co_idx + lofs * ZS_KO, &no, &o_kth,
                      &o_full, sh);
 
+    P1_MARK(8);
     if (t == 0) {
         zs_chunk_stat cs;
         cs.obs_max = omax;
@@ -852,6 +875,7 @@ __global__ __launch_bounds__(ZS_P1_NT) __attribute__((amdgpu_waves_per_eu(3))) v
         cs.o_full = o_full;
         a.cst[lofs] = cs;
     }
+    P1_MARK(9);
 }
 
 // ===========================================================================
@@ -3184,6 +3208,13 @@ __global__ __launch_bounds__(SK_NT) void zs_k_stitchK(zs_sargs a) {
 // zs_k_final: per-row outputs (logprobs.rs:34-54, hallucination.rs:232-257)
 // ===========================================================================
 __global__ void zs_k_final(zs_sargs a) {
+#ifdef ZS_DEBUG_P1
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        printf("p1 phases:");
+        for (int k = 1; k < 10; k++) { printf(" %d:%llu", k, zs_dbg_p1[k]); zs_dbg_p1[k] = 0; }
+        printf("\n");
+    }
+#endif
     const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
     const zs_batch& b = a.b;
     if (r >= b.B) return;

@@ -7,10 +7,11 @@
 // temperature > 0: rejection sampling (Leviathan et al. 2023; Chen et al.
 // 2023), which the reference does not implement (rest.rs:2639). To make it
 // reproducible bit-for-bit on any reduction order, probabilities are integer
-// quantised: with z = x / T (f32, no division when T == 1) and m = max z, the
-// weight of id v is
-//   P_v = rint(2^24 * 2^((z_v - m) log2 e))   (target),   Q_v likewise (draft),
-// from a fixed sequence of f32 operations (sp_weight_of), 0 below z - m = -17.5.
+// quantised: with m = max x (NaN ignored) and c = log2(e) / T (one f32
+// division per row), the weight of id v is
+//   P_v = rint(2^24 * 2^t),  t = (x_v - m) * c   (target),   Q_v likewise (draft),
+// from a fixed sequence of f32 operations (sp_weight), 0 below t = -25 (where
+// the formula itself rounds to 0). No per-element division by T is needed.
 // Draft i (token d) is accepted iff U_i * Q_d * sum(P) <= P_d * sum(Q) * 2^32,
 // U_i the 32-bit Philox word of (seed, counter, tag 1+i). At the first
 // rejection i the replacement token is drawn from R_v = max(0, P_v sum(Q) -
@@ -29,7 +30,7 @@
 #define SP_EPT (SP_CH / SP_NT)   // 32 elements per thread, as 8 float4
 #define SP_BIG_NT 1024
 // weights are 0 below this log-ratio
-#define SP_ZERO_D (-17.5f)
+#define SP_ZERO_T (-25.0f)
 
 typedef unsigned __int128 u128;
 
@@ -37,16 +38,16 @@ __device__ __forceinline__ const float* sp_row(const zs_spec_args& a, uint32_t r
     if (pos <= a.k) return a.target + ((size_t)r * (a.k + 1) + pos) * a.ld;
     return a.draft + ((size_t)r * a.k + (pos - a.k - 1)) * a.ld;
 }
-__device__ __forceinline__ float sp_z(float x, float T) { return (T > 0.0f && T != 1.0f) ? x / T : x; }
-// Integer weight of log-ratio d = z - max: rint(2^24 * 2^(d log2 e)) through a
-// fixed sequence of correctly rounded f32 operations (t = d * log2 e, t = n + f
-// with n = floor(t), 2^f by a degree-7 Taylor polynomial in fmaf Horner form,
-// exact scaling by 2^(24+n), rint), so the CPU restatement reproduces every
-// weight bit for bit; 0 below d = -17.5. For d <= 0 the weight is at most
-// 2^24 * 2^f < 2^25, so 32 of them add up in 32 bits.
-__device__ __forceinline__ uint32_t sp_weight_of(float d) {
-    if (!(d >= SP_ZERO_D)) return 0;
-    const float t = __fmul_rn(d, 1.44269502f);
+// c = log2(e) / T, the factor of the exponent (T > 0)
+__device__ __forceinline__ float sp_c(float T) { return __fdiv_rn(1.44269502f, T); }
+// Integer weight rint(2^24 * 2^t), t = (x - m) * c, through a fixed sequence of
+// correctly rounded f32 operations (t = n + f with n = floor(t), 2^f by a
+// degree-7 Taylor polynomial in fmaf Horner form, exact scaling by 2^(24+n),
+// rint), so the CPU restatement reproduces every weight bit for bit. t < -25
+// gives 2^f * 2^(24+n) < 0.5, i.e. 0. For x <= m the weight is below 2^25, so
+// 32 of them add up in 32 bits.
+__device__ __forceinline__ uint32_t sp_weight(float x, float m, float c) {
+    const float t = __fmul_rn(__fsub_rn(x, m), c);
     const float n = floorf(t);
     const float f = __fsub_rn(t, n);
     float p = 1.52527338e-05f;
@@ -57,10 +58,13 @@ __device__ __forceinline__ uint32_t sp_weight_of(float d) {
     p = fmaf(p, f, 2.40226507e-01f);
     p = fmaf(p, f, 6.93147182e-01f);
     p = fmaf(p, f, 1.0f);
-    return (uint32_t)rintf(ldexpf(p, 24 + (int)n));
+    const uint32_t w = (uint32_t)rintf(ldexpf(p, 24 + (int)n));
+    return t >= SP_ZERO_T ? w : 0u;
 }
-__device__ __forceinline__ uint64_t sp_weight(float z, float m) { return sp_weight_of(z - m); }
-__device__ __forceinline__ uint32_t sp_weight32(float z, float m) { return sp_weight_of(z - m); }
+// whether any x <= xc can have a positive weight
+__device__ __forceinline__ bool sp_live(float xc, float m, float c) {
+    return __fmul_rn(__fsub_rn(xc, m), c) >= SP_ZERO_T;
+}
 // the chunk's elements of thread t: float4 j covers ids base + (j*SP_NT + t)*4 .. +3
 __device__ __forceinline__ void sp_load(const float* row, uint32_t base, uint32_t V, float (&x)[SP_EPT]) {
 #pragma unroll
@@ -69,6 +73,11 @@ __device__ __forceinline__ void sp_load(const float* row, uint32_t base, uint32_
         float4 v = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
         if (id < V) v = *reinterpret_cast<const float4*>(row + id);
         x[4 * j] = v.x; x[4 * j + 1] = v.y; x[4 * j + 2] = v.z; x[4 * j + 3] = v.w;
+    }
+    if (base + SP_CH > V) {  // ids past V read as -inf (neutral in every pass)
+#pragma unroll
+        for (int e = 0; e < SP_EPT; e++)
+            if (base + ((e >> 2) * SP_NT + threadIdx.x) * 4 + (e & 3) >= V) x[e] = -INFINITY;
     }
 }
 __device__ __forceinline__ uint32_t sp_id(uint32_t base, int e) {
@@ -85,31 +94,25 @@ __global__ __launch_bounds__(SP_NT) void zs_k_spec_stats(zs_spec_args a) {
     __shared__ float fsh[SP_NT / 64];
     __shared__ uint32_t ush[SP_NT / 64];
     __shared__ unsigned long long gsh[SP_NT / 64];
-    const float T = a.temperature[r];
     float x[SP_EPT];
     sp_load(sp_row(a, r, pos), base, a.V, x);
-    // max z = (max x) / T: a correctly rounded division by T > 0 is monotone,
-    // so the per-element divisions are not needed here (z overflows to +inf
-    // somewhere iff it does at the max)
-    float xmax = -INFINITY;
-    uint32_t fl = 0;
-    unsigned long long best = 0;  // (value key, ~idx): first strict max
+    // first strict maximum (init -inf, NaN never wins) in index order: the
+    // elements of a thread ascend with e; it is also the NaN-ignoring max
+    float bv = -INFINITY;
+    int be = -1;
+    bool nan = false;
 #pragma unroll
     for (int e = 0; e < SP_EPT; e++) {
-        const uint32_t i = sp_id(base, e);
-        if (i >= a.V) continue;
         const float xv = x[e];
-        if (xv != xv) fl |= 1u;
-        xmax = fmaxf(xmax, xv);
-        if (xv > -INFINITY) {  // strict > over init -inf (NaN never wins)
-            const float xx = (xv == 0.0f) ? 0.0f : xv;
-            const unsigned long long k = ((unsigned long long)zs_total_key(xx) << 32) | (0xffffffffu - i);
-            best = k > best ? k : best;
-        }
+        nan |= xv != xv;
+        if (xv > bv) { bv = xv; be = e; }
     }
-    float zmax = sp_z(xmax, T);
-    if (zmax == INFINITY) fl |= 2u;
-    zmax = block_max_f<SP_NT>(zmax, fsh);
+    uint32_t fl = nan ? 1u : 0u;
+    if (bv == INFINITY) fl |= 2u;
+    // (value key, ~idx): larger value first, then the lower id; -0 == +0
+    unsigned long long best = be < 0 ? 0ull
+        : ((unsigned long long)zs_total_key(bv == 0.0f ? 0.0f : bv) << 32) | (0xffffffffu - sp_id(base, be));
+    const float xmax = block_max_f<SP_NT>(bv, fsh);
     fl = block_or_u<SP_NT>(fl, ush);
     for (int d = 32; d > 0; d >>= 1) {
         unsigned long long o = __shfl_xor(best, d, 64);
@@ -120,7 +123,7 @@ __global__ __launch_bounds__(SP_NT) void zs_k_spec_stats(zs_spec_args a) {
     if (threadIdx.x == 0) {
         for (int i = 0; i < SP_NT / 64; i++) best = gsh[i] > best ? gsh[i] : best;
         zs_spec_chunk& o = a.cst[((size_t)r * a.npos_max + pos) * a.nch + c];
-        o.zmax = zmax;
+        o.xmax = xmax;
         o.flags = fl;
         o.amax_val = best ? zs_key_to_float((uint32_t)(best >> 32)) : -INFINITY;
         o.amax_idx = best ? 0xffffffffu - (uint32_t)(best & 0xffffffffull) : 0xffffffffu;
@@ -140,17 +143,14 @@ __global__ __launch_bounds__(SP_NT) void zs_k_spec_sums(zs_spec_args a) {
     const uint32_t nch = (a.V + SP_CH - 1) / SP_CH;
     const zs_spec_chunk* cs = a.cst + ((size_t)r * a.npos_max + pos) * a.nch;
     float m = -INFINITY;
-    for (uint32_t i = 0; i < nch; i++) m = fmaxf(m, cs[i].zmax);
+    for (uint32_t i = 0; i < nch; i++) m = fmaxf(m, cs[i].xmax);
+    const float cT = sp_c(T);
     uint32_t s32 = 0;  // at most 32 weights below 2^25 each
-    if (m > -INFINITY && m < INFINITY && cs[c].zmax - m >= SP_ZERO_D) {
+    if (m > -INFINITY && m < INFINITY && sp_live(cs[c].xmax, m, cT)) {
         float x[SP_EPT];
         sp_load(sp_row(a, r, pos), base, a.V, x);
-        // x below xl gives z - m < -17.5 whatever the rounding of x / T (the
-        // bound keeps a 0.05 margin): no division or weight needed
-        const float xl = (float)(((double)m + (double)SP_ZERO_D - 0.05) * (double)(T != 1.0f ? T : 1.0f));
 #pragma unroll
-        for (int e = 0; e < SP_EPT; e++)
-            if (sp_id(base, e) < a.V && x[e] >= xl) s32 += sp_weight32(sp_z(x[e], T), m);
+        for (int e = 0; e < SP_EPT; e++) s32 += sp_weight(x[e], m, cT);
     }
     unsigned long long s = s32;
     for (int d = 32; d > 0; d >>= 1) s += __shfl_xor(s, d, 64);
@@ -182,6 +182,11 @@ __device__ __forceinline__ void sr_load(const float* row, uint32_t base, uint32_
         if (id < V) v = *reinterpret_cast<const float4*>(row + id);
         x[4 * j] = v.x; x[4 * j + 1] = v.y; x[4 * j + 2] = v.z; x[4 * j + 3] = v.w;
     }
+    if (base + SP_CH > V) {  // ids past V read as -inf
+#pragma unroll
+        for (int e = 0; e < SR_EPT; e++)
+            if (base + ((e >> 2) * SR_NT + threadIdx.x) * 4 + (e & 3) >= V) x[e] = -INFINITY;
+    }
 }
 __device__ __forceinline__ uint32_t sr_id(uint32_t base, int e) {
     return base + ((e >> 2) * SR_NT + threadIdx.x) * 4 + (e & 3);
@@ -210,22 +215,19 @@ __global__ __launch_bounds__(SR_NT) void zs_k_spec_row(zs_spec_args a) {
             const uint32_t c = c0 + h;
             if (c >= nch) break;
             const uint32_t base = c * SP_CH;
-            float xmax = -INFINITY;
-            uint32_t fl = 0;
-            unsigned long long best = 0;  // (value key, ~idx): first strict max
+            float bv = -INFINITY;
+            int be = -1;
+            bool nan = false;
 #pragma unroll
             for (int e = 0; e < SR_EPT; e++) {
-                const uint32_t i = sr_id(base, e);
-                if (i >= V) continue;
                 const float xv = x[h][e];
-                if (xv != xv) fl |= 1u;
-                xmax = fmaxf(xmax, xv);
-                if (xv > -INFINITY) {
-                    const float xx = (xv == 0.0f) ? 0.0f : xv;
-                    const unsigned long long k = ((unsigned long long)zs_total_key(xx) << 32) | (0xffffffffu - i);
-                    best = k > best ? k : best;
-                }
+                nan |= xv != xv;
+                if (xv > bv) { bv = xv; be = e; }
             }
+            float xmax = bv;
+            uint32_t fl = nan ? 1u : 0u;
+            unsigned long long best = be < 0 ? 0ull
+                : ((unsigned long long)zs_total_key(bv == 0.0f ? 0.0f : bv) << 32) | (0xffffffffu - sr_id(base, be));
             xmax = wave_max_f(xmax);
             fl = wave_or_u(fl);
             for (int d = 32; d > 0; d >>= 1) {
@@ -246,12 +248,10 @@ __global__ __launch_bounds__(SR_NT) void zs_k_spec_row(zs_spec_args a) {
             fl |= wf[c][w];
             best = wb[c][w] > best ? wb[c][w] : best;
         }
-        // max z = (max x) / T: division by T > 0 is monotone
-        const float zmax = sp_z(xmax, T);
-        if (zmax == INFINITY) fl |= 2u;
-        cz[c] = zmax;
+        if (xmax == INFINITY) fl |= 2u;
+        cz[c] = xmax;
         zs_spec_chunk& o = cs[c];
-        o.zmax = zmax;
+        o.xmax = xmax;
         o.flags = fl;
         o.amax_val = best ? zs_key_to_float((uint32_t)(best >> 32)) : -INFINITY;
         o.amax_idx = best ? 0xffffffffu - (uint32_t)(best & 0xffffffffull) : 0xffffffffu;
@@ -261,14 +261,13 @@ __global__ __launch_bounds__(SR_NT) void zs_k_spec_row(zs_spec_args a) {
     float m = -INFINITY;
     for (uint32_t c = 0; c < nch; c++) m = fmaxf(m, cz[c]);
     const bool fin = m > -INFINITY && m < INFINITY;
-    // x below xl gives z - m < -17.5 whatever the rounding of x / T (0.05 margin)
-    const float xl = (float)(((double)m + (double)SP_ZERO_D - 0.05) * (double)(T != 1.0f ? T : 1.0f));
+    const float cT = sp_c(T);
     for (uint32_t c0 = 0; c0 < nch; c0 += SR_PAIR) {
         float x[SR_PAIR][SR_EPT];
 #pragma unroll
         for (int h = 0; h < SR_PAIR; h++) {
             const uint32_t c = c0 + h;
-            if (fin && c < nch && cz[c] - m >= SP_ZERO_D) sr_load(row, c * SP_CH, V, x[h]);
+            if (fin && c < nch && sp_live(cz[c], m, cT)) sr_load(row, c * SP_CH, V, x[h]);
             else
 #pragma unroll
                 for (int e = 0; e < SR_EPT; e++) x[h][e] = -INFINITY;
@@ -280,7 +279,7 @@ __global__ __launch_bounds__(SR_NT) void zs_k_spec_row(zs_spec_args a) {
             uint32_t s32 = 0;  // at most 8 weights below 2^25 each
 #pragma unroll
             for (int e = 0; e < SR_EPT; e++)
-                if (sr_id(c * SP_CH, e) < V && x[h][e] >= xl) s32 += sp_weight32(sp_z(x[h][e], T), m);
+                s32 += sp_weight(x[h][e], m, cT);
             unsigned long long s = s32;
             for (int d = 32; d > 0; d >>= 1) s += __shfl_xor(s, d, 64);
             if (lane == 0) wb[c][wid] = s;
@@ -316,7 +315,7 @@ __global__ __launch_bounds__(64) void zs_k_spec_decide(zs_spec_args a) {
         unsigned long long s = 0, best = 0;  // (value key, ~id) of the first maximum
         for (uint32_t c = lane; c < nch; c += 64) {
             const zs_spec_chunk q = cs[c];
-            m = fmaxf(m, q.zmax);
+            m = fmaxf(m, q.xmax);
             fl |= q.flags;
             if (!degenerate) s += q.wsum;
             if (q.amax_idx != 0xffffffffu) {
@@ -350,12 +349,13 @@ __global__ __launch_bounds__(64) void zs_k_spec_decide(zs_spec_args a) {
         a.rs[r] = out;
         return;
     }
+    const float cT = sp_c(T);
     uint32_t i = 0;
     for (; i < k; i++) {
         uint32_t d = drafts[i];
         if (d >= V) break;
-        uint64_t P = sp_weight(sp_z(sp_row(a, r, i)[d], T), mpos[i]);
-        uint64_t Q = sp_weight(sp_z(sp_row(a, r, k + 1 + i)[d], T), mpos[k + 1 + i]);
+        uint64_t P = sp_weight(sp_row(a, r, i)[d], mpos[i], cT);
+        uint64_t Q = sp_weight(sp_row(a, r, k + 1 + i)[d], mpos[k + 1 + i], cT);
         uint32_t U = zs_philox_u32(a.seed[r], a.counter[r], 1u + i);
         u128 lhs = (u128)U * Q * spos[i];
         u128 rhs = ((u128)P * spos[k + 1 + i]) << 32;
@@ -399,10 +399,10 @@ __device__ __forceinline__ u128 shfl_xor_u128(u128 v, int d) {
 
 // Draw weight of id v (given its target / draft logits): P, or the residual
 // max(0, P sum(Q) - Q sum(P)).
-__device__ __forceinline__ u128 spd_weight2(const zs_spec_row& s, float T, float xt, float xd) {
-    uint64_t P = sp_weight(sp_z(xt, T), s.m_t);
+__device__ __forceinline__ u128 spd_weight2(const zs_spec_row& s, float cT, float xt, float xd) {
+    uint64_t P = sp_weight(xt, s.m_t, cT);
     if (!s.residual) return P;
-    uint64_t Q = sp_weight(sp_z(xd, T), s.m_d);
+    uint64_t Q = sp_weight(xd, s.m_d, cT);
     u128 pp = (u128)P * s.sum_d, qq = (u128)Q * s.sum_t;
     return pp > qq ? pp - qq : 0;
 }
@@ -415,14 +415,14 @@ __global__ __launch_bounds__(SP_NT) void zs_k_spec_rsum(zs_spec_args a) {
     const zs_spec_row s = a.rs[r];
     if (s.mode != 1 || !s.residual) return;
     __shared__ unsigned long long lo[SP_NT / 64], hi[SP_NT / 64];
-    const float T = a.temperature[r];
+    const float cT = sp_c(a.temperature[r]);
     float xt[SP_EPT], xd[SP_EPT];
     sp_load(sp_row(a, r, s.pos), base, a.V, xt);
     sp_load(sp_row(a, r, a.k + 1 + s.pos), base, a.V, xd);
     u128 acc = 0;
 #pragma unroll
     for (int e = 0; e < SP_EPT; e++)
-        if (sp_id(base, e) < a.V) acc += spd_weight2(s, T, xt[e], xd[e]);
+        acc += spd_weight2(s, cT, xt[e], xd[e]);
     for (int d = 32; d > 0; d >>= 1) acc += shfl_xor_u128(acc, d);
     if (zs_lane() == 0) { lo[zs_wid()] = (unsigned long long)acc; hi[zs_wid()] = (unsigned long long)(acc >> 64); }
     __syncthreads();
@@ -446,7 +446,7 @@ __global__ __launch_bounds__(SP_BIG_NT) void zs_k_spec_draw(zs_spec_args a) {
     __shared__ unsigned long long clo, chi, rzero;
     zs_spec_row s = a.rs[r];
     if (s.mode != 1) return;
-    const float T = a.temperature[r];
+    const float cT = sp_c(a.temperature[r]);
     const int t = threadIdx.x;
     const uint32_t V = a.V;
     const uint32_t nch = (V + SP_CH - 1) / SP_CH;
@@ -506,7 +506,7 @@ __global__ __launch_bounds__(SP_BIG_NT) void zs_k_spec_draw(zs_spec_args a) {
         const float xt[4] = {vt.x, vt.y, vt.z, vt.w}, xd[4] = {vd.x, vd.y, vd.z, vd.w};
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-            w[4 * h + q] = id + q < V ? spd_weight2(s, T, xt[q], xd[q]) : 0;
+            w[4 * h + q] = id + q < V ? spd_weight2(s, cT, xt[q], xd[q]) : 0;
         }
     }
     // inclusive prefix in id order: ids of thread t are base + 4t..4t+3 (h=0)
