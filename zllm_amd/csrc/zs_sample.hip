@@ -669,6 +669,9 @@ __global__ __launch_bounds__(ZS_P1_NT) __attribute__((amdgpu_waves_per_eu(3))) v
     for (int e = 0; e < P1_EPT; e++) zv[e] = zs_temper(zv[e], T);
 
     P1_MARK(3);
+#ifdef XP_NOSTAT
+    if (T > -1e30f) return;
+#endif
     // ---- chunk statistics of x~ (observers) and z (sampler), one workgroup
     // reduction: maxima, NaN / +inf flags, the last NaN of z, and counts of
     // finite z and of elements whose key is above that of -inf for the lists
@@ -770,6 +773,9 @@ __global__ __launch_bounds__(ZS_P1_NT) __attribute__((amdgpu_waves_per_eu(3))) v
         const int wid = zs_wid(), wh = (wid * 256) / ZS_SUB;
         const bool om = (P.flags & (ZS_ROW_LOGPROBS | ZS_ROW_UNCERTAINTY)) && omax > -INFINITY && omax < INFINITY;
         const bool zm = T > 0.0f && zmax > -INFINITY && zmax < INFINITY;
+#ifdef XP_NOMOM
+        if (T > -1e30f) return;
+#endif
         __shared__ float msh[ZS_P1_NT / 64][P1_J][3];
         // bit 2s: sub-chunk s holds the chunk's observer max, bit 2s+1: its sampler max
         uint32_t hasmax = 0;
@@ -822,6 +828,9 @@ __global__ __launch_bounds__(ZS_P1_NT) __attribute__((amdgpu_waves_per_eu(3))) v
 
     P1_MARK(6);
     // ---- candidate lists (keys recomputed from the values where needed)
+#ifdef XP_NOLIST
+    if (T > -1e30f) return;
+#endif
     const size_t lofs = ((size_t)r * a.nch + c);
     // sampler list size: top_k when the row has a top-k cut within range
     const bool has_topk = P.top_k > 0 && P.top_k < V;
@@ -3207,7 +3216,7 @@ __global__ __launch_bounds__(SK_NT) void zs_k_stitchK(zs_sargs a) {
 // ===========================================================================
 // zs_k_final: per-row outputs (logprobs.rs:34-54, hallucination.rs:232-257)
 // ===========================================================================
-__global__ void zs_k_final(zs_sargs a) {
+__global__ __launch_bounds__(64) void zs_k_final(zs_sargs a) {
 #ifdef ZS_DEBUG_P1
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         printf("p1 phases:");
@@ -3215,37 +3224,45 @@ __global__ void zs_k_final(zs_sargs a) {
         printf("\n");
     }
 #endif
-    const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
+    // one wave per row; lane j handles observer candidate j
+    const uint32_t r = blockIdx.x;
+    const uint32_t lane = threadIdx.x;
     const zs_batch& b = a.b;
     if (r >= b.B) return;
     const zs_row_state& st = a.rst[r];
     const uint32_t tok = st.token;
     uint32_t status = st.status;
-    b.d_token[r] = tok;
     const zs_row_params P = b.d_params[r];
     const bool want_lp = (P.flags & ZS_ROW_LOGPROBS) != 0;
     const bool want_unc = (P.flags & ZS_ROW_UNCERTAINTY) != 0;
-    b.d_top_n[r] = 0;
-    b.d_logprob[r] = NAN;
-    b.d_entropy[r] = NAN;
-    b.d_max_prob[r] = NAN;
-    b.d_margin[r] = NAN;
-    b.d_chosen_lp[r] = NAN;
+    if (lane == 0) {
+        b.d_token[r] = tok;
+        b.d_top_n[r] = 0;
+        b.d_logprob[r] = NAN;
+        b.d_entropy[r] = NAN;
+        b.d_max_prob[r] = NAN;
+        b.d_margin[r] = NAN;
+        b.d_chosen_lp[r] = NAN;
+    }
     if (status & ZS_ST_LIMIT) {
-        b.d_status[r] = status;
+        if (lane == 0) b.d_status[r] = status;
         return;
     }
-    // x~ of the chosen token
+    // x~ of the chosen token: the logit, the mask bit and a ban among the
+    // patches of its 1024-id sub-chunk (lanes check them in parallel)
     float xc = -INFINITY;
     const bool in_range = tok < b.V;
     if (in_range) {
         xc = b.d_logits[(size_t)r * b.ld + tok];
         if ((P.flags & ZS_ROW_MASKED) && b.d_allow_bits && !zs_allowed_bit(b, r, tok)) xc = -INFINITY;
         const uint32_t* pid = a.p_id + (size_t)r * ZS_MAX_PATCHES;
-        uint32_t lo = 0, hi = a.p_cnt[r];
-        while (lo < hi) { uint32_t mid = (lo + hi) >> 1; if (pid[mid] < tok) lo = mid + 1; else hi = mid; }
-        if (lo < a.p_cnt[r] && pid[lo] == tok && (a.p_flags[(size_t)r * ZS_MAX_PATCHES + lo] & ZS_PF_BAN))
-            xc = -INFINITY;
+        const uint32_t* psub = a.p_sub + (size_t)r * (a.max_subs + 1);
+        const uint32_t nsub = (b.V + ZS_SUB - 1) / ZS_SUB;
+        const uint32_t p0 = psub[tok / ZS_SUB], p1 = psub[min(tok / ZS_SUB + 1, nsub)];
+        bool ban = false;
+        for (uint32_t p = p0 + lane; p < p1; p += 64)
+            if (pid[p] == tok && (a.p_flags[(size_t)r * ZS_MAX_PATCHES + p] & ZS_PF_BAN)) ban = true;
+        if (__ballot(ban)) xc = -INFINITY;
     }
     const float M = st.obs_max;
     if (want_lp) {
@@ -3256,44 +3273,51 @@ __global__ void zs_k_final(zs_sargs a) {
         if (st.obs_special) {
             // lse is NaN: every lp is NaN and partition_point(x >= NaN) == 0 inserts
             // each entry first, leaving ids n-1 .. 0 (logprobs.rs:41-51)
-            uint32_t n = ntl < b.V ? ntl : b.V;
-            for (uint32_t j = 0; j < n; j++) { tid[j] = n - 1 - j; tlp[j] = NAN; }
-            b.d_top_n[r] = n;
-            b.d_logprob[r] = in_range ? NAN : -INFINITY;
+            const uint32_t n = ntl < b.V ? ntl : b.V;
+            for (uint32_t j = lane; j < n; j += 64) { tid[j] = n - 1 - j; tlp[j] = NAN; }
+            if (lane == 0) {
+                b.d_top_n[r] = n;
+                b.d_logprob[r] = in_range ? NAN : -INFINITY;
+            }
         } else {
             const float lse = M + (float)log((double)st.obs_S);  // logprobs.rs:36
-            b.d_logprob[r] = in_range ? xc - lse : -INFINITY;
-            uint32_t nc = st.n_cand;
-            uint32_t ids[ZS_OBS_CAND];
-            float xs[ZS_OBS_CAND], lps[ZS_OBS_CAND];
-            for (uint32_t j = 0; j < nc; j++) { ids[j] = st.cand_id[j]; xs[j] = st.cand_x[j]; lps[j] = xs[j] - lse; }
-            // candidates arrive by (x~ desc, id asc); equal lp values keep id order
-            for (uint32_t j = 1; j < nc; j++) {
-                uint32_t id = ids[j];
-                float lp = lps[j], xv = xs[j];
-                int k = (int)j - 1;
-                while (k >= 0 && (lps[k] < lp || (lps[k] == lp && ids[k] > id))) {
-                    ids[k + 1] = ids[k]; lps[k + 1] = lps[k]; xs[k + 1] = xs[k];
-                    k--;
-                }
-                ids[k + 1] = id; lps[k + 1] = lp; xs[k + 1] = xv;
+            if (lane == 0) b.d_logprob[r] = in_range ? xc - lse : -INFINITY;
+            // the list the reference keeps by insertion (logprobs.rs:41-51):
+            // lp desc, equal lp in id order; rank of candidate j in it
+            const uint32_t nc = st.n_cand;
+            const bool mine = lane < nc;
+            const uint32_t id = mine ? st.cand_id[lane] : 0xffffffffu;
+            const float xv = mine ? st.cand_x[lane] : -INFINITY;
+            const float lp = xv - lse;
+            uint32_t rank = 0;
+            for (uint32_t i = 0; i < nc; i++) {
+                const float li = __shfl(lp, (int)i, 64);
+                const uint32_t ii = __shfl(id, (int)i, 64);
+                rank += (li > lp || (li == lp && ii < id)) ? 1u : 0u;
             }
+            // sorted x~ by rank, for the check below
+            __shared__ float xs_sh[64];
+            if (mine) xs_sh[rank] = xv;
+            __syncthreads();
             // the order must not hinge on the last bit of lse (its logf may differ
             // from glibc's by one ulp)
-            float lo = nextafterf(lse, -INFINITY), hi = nextafterf(lse, INFINITY);
-            uint32_t lim = nc < ntl + 1 ? nc : ntl + 1;
-            for (uint32_t j = 0; j + 1 < lim; j++) {
-                bool e0 = (xs[j] - lse) == (xs[j + 1] - lse);
-                bool e1 = (xs[j] - lo) == (xs[j + 1] - lo);
-                bool e2 = (xs[j] - hi) == (xs[j + 1] - hi);
-                if (e0 != e1 || e0 != e2) status |= ZS_ST_TOPLP_AMBIG;
+            const float lo = nextafterf(lse, -INFINITY), hi = nextafterf(lse, INFINITY);
+            const uint32_t lim = nc < ntl + 1 ? nc : ntl + 1;
+            bool amb = false;
+            if (lane + 1 < lim) {
+                const float x0 = xs_sh[lane], x1 = xs_sh[lane + 1];
+                const bool e0 = (x0 - lse) == (x1 - lse);
+                const bool e1 = (x0 - lo) == (x1 - lo);
+                const bool e2 = (x0 - hi) == (x1 - hi);
+                amb = e0 != e1 || e0 != e2;
             }
-            uint32_t n = ntl < nc ? ntl : nc;
-            for (uint32_t j = 0; j < n; j++) { tid[j] = ids[j]; tlp[j] = lps[j]; }
-            b.d_top_n[r] = n;
+            if (__ballot(amb)) status |= ZS_ST_TOPLP_AMBIG;
+            const uint32_t n = ntl < nc ? ntl : nc;
+            if (mine && rank < n) { tid[rank] = id; tlp[rank] = lp; }
+            if (lane == 0) b.d_top_n[r] = n;
         }
     }
-    if (want_unc) {
+    if (want_unc && lane == 0) {
         if (st.obs_special) {
             // sum is NaN: no p > 0, top1 stays -inf (hallucination.rs:243-256)
             b.d_entropy[r] = 0.0f;
@@ -3312,7 +3336,7 @@ __global__ void zs_k_final(zs_sargs a) {
             b.d_chosen_lp[r] = pc > 0.0f ? (float)log((double)pc) : -INFINITY;
         }
     }
-    b.d_status[r] = status;
+    if (lane == 0) b.d_status[r] = status;
 }
 
 // ===========================================================================
@@ -3407,7 +3431,7 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
     hipLaunchKernelGGL(zs_k_stitchK<1>, dim3(B), dim3(SK_NT), 0, stream, a);
     mark("zs_k_kept");
     if (!prof) ZS_LAUNCH_CHECK(hipStreamWaitEvent(stream, (hipEvent_t)ctx->join_event, 0));
-    hipLaunchKernelGGL(zs_k_final, dim3((B + 63) / 64), dim3(64), 0, stream, a);
+    hipLaunchKernelGGL(zs_k_final, dim3(B), dim3(64), 0, stream, a);
     mark("zs_k_final");
     if (prof) ctx->n_timed = ev - 1;
     hipError_t e = hipGetLastError();
