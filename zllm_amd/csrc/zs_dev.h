@@ -199,6 +199,85 @@ __device__ __forceinline__ unsigned long long wave_sort_u64(unsigned long long v
     return v;
 }
 
+// Value of lane l (uniform over the wave) read into a scalar register:
+// unlike __shfl with a uniform source (an LDS permute), no LDS round trip.
+__device__ __forceinline__ float zs_readlane_f(float v, uint32_t l) {
+    return __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(v), (int)l));
+}
+__device__ __forceinline__ uint32_t zs_readlane_u(uint32_t v, uint32_t l) {
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)l);
+}
+__device__ __forceinline__ unsigned long long zs_readlane_u64(unsigned long long v, uint32_t l) {
+    return ((unsigned long long)zs_readlane_u((uint32_t)(v >> 32), l) << 32) | zs_readlane_u((uint32_t)v, l);
+}
+
+// Ascending bitonic sort of n (power of two, n <= NT * E) u64 keys in LDS,
+// held in registers while sorted: element i = thread * E + e. Strides below E
+// stay inside a thread, strides below 64 * E are lane exchanges, larger ones
+// go through `a`. Every thread of the block must call it.
+template <int NT, int E>
+__device__ void block_sort_reg_u64(unsigned long long* a, uint32_t n) {
+    const uint32_t t = threadIdx.x, lane = (uint32_t)zs_lane();
+    unsigned long long v[E];
+#pragma unroll
+    for (int e = 0; e < E; e++) {
+        const uint32_t i = t * E + e;
+        v[e] = i < n ? a[i] : ~0ull;
+    }
+    for (uint32_t k = 2; k <= n; k <<= 1) {
+        for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+            if (j < (uint32_t)E) {
+                // compile-time strides keep the register indices static
+#pragma unroll
+                for (uint32_t jj = E / 2; jj > 0; jj >>= 1) {
+                    if (jj != j) continue;
+#pragma unroll
+                    for (uint32_t e = 0; e < (uint32_t)E; e++) {
+                        const uint32_t pe = e ^ jj;
+                        if (pe > e) {
+                            const bool asc = ((t * E + e) & k) == 0u;
+                            const unsigned long long x = v[e], y = v[pe];
+                            if ((x > y) == asc) { v[e] = y; v[pe] = x; }
+                        }
+                    }
+                }
+            } else {
+                unsigned long long o[E];
+                if (j < 64u * E) {
+#pragma unroll
+                    for (int e = 0; e < E; e++) o[e] = __shfl_xor(v[e], (int)(j / E), 64);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < E; e++) if (t * E + e < n) a[t * E + e] = v[e];
+                    __syncthreads();
+#pragma unroll
+                    for (int e = 0; e < E; e++) o[e] = t * E + e < n ? a[(t * E + e) ^ j] : ~0ull;
+                    __syncthreads();
+                }
+#pragma unroll
+                for (uint32_t e = 0; e < (uint32_t)E; e++) {
+                    const uint32_t i = t * E + e;
+                    const bool asc = (i & k) == 0u, lower = (i & j) == 0u;
+                    v[e] = (lower == asc) ? (o[e] < v[e] ? o[e] : v[e]) : (o[e] > v[e] ? o[e] : v[e]);
+                }
+            }
+        }
+    }
+    (void)lane;
+#pragma unroll
+    for (int e = 0; e < E; e++) if (t * E + e < n) a[t * E + e] = v[e];
+    __syncthreads();
+}
+// block_sort_reg_u64 with E chosen from n (n <= 16 * NT)
+template <int NT>
+__device__ void block_sort_u64(unsigned long long* a, uint32_t n) {
+    if (n <= NT) block_sort_reg_u64<NT, 1>(a, n);
+    else if (n <= 2 * NT) block_sort_reg_u64<NT, 2>(a, n);
+    else if (n <= 4 * NT) block_sort_reg_u64<NT, 4>(a, n);
+    else if (n <= 8 * NT) block_sort_reg_u64<NT, 8>(a, n);
+    else block_sort_reg_u64<NT, 16>(a, n);
+}
+
 template <int NT>
 __device__ void block_bitonic_u64(unsigned long long* a, int n) {
     for (int k = 2; k <= n; k <<= 1) {

@@ -950,118 +950,163 @@ __device__ void zs_predict_subs(zs_sub_sum* out, uint32_t nsub, const F& A, cons
 #define ZS_SMALL_CAP 512
 
 
-// Exact sampler over a small survivor set (n <= ZS_SMALL_CAP, all other
-// logits are -inf after top-k / mask): every sequential sum of sampler.rs is
-// reproduced with seq_group over survivors in index order; zero terms of the
+// Small survivor sets (n <= ZS_SMALL_CAP, all other logits are -inf after
+// top-k / mask) are sampled exactly in zs_k_combine: zero terms of the
 // reference's full-vocabulary loops do not change a running sum.
-#define SP_EPT (ZS_SMALL_CAP / CB_NT)
-__device__ uint32_t small_path_sample(const zs_sargs& a, uint32_t r, const zs_row_params& P, uint32_t n,
-                                      float m, float* sval, uint32_t* sidx, unsigned long long* sbuf,
-                                      seq_sh<CB_NT>& sq) {
-    const int t = threadIdx.x;
-    const zs_batch& b = a.b;
-    const uint32_t V = b.V;
-    // order survivors by index: composite (idx << 32 | value bits)
-    uint32_t np = 1;
-    while (np < n) np <<= 1;
-    for (uint32_t i = t; i < np; i += CB_NT)
-        sbuf[i] = i < n ? (((unsigned long long)sidx[i] << 32) | zs_f2u(sval[i])) : ~0ull;
-    __syncthreads();
-    if (np > 1) block_bitonic_u64<CB_NT>(sbuf, (int)np);
-    float p[SP_EPT];
-    uint32_t id[SP_EPT];
+// Ascending bitonic sort of 64*E u64 keys by one wave, element i = lane*E + e
+// in register e of lane i / E: strides below E inside the lane, the others by
+// lane exchanges.
+template <int E>
+__device__ __forceinline__ void wave_sort_u64_e(unsigned long long (&v)[E]) {
+    const uint32_t lane = (uint32_t)zs_lane();
 #pragma unroll
-    for (int j = 0; j < SP_EPT; j++) {
-        uint32_t i = SP_EPT * t + j;
-        if (i < n) {
-            id[j] = (uint32_t)(sbuf[i] >> 32);
-            p[j] = zs_expf(zs_u2f((uint32_t)(sbuf[i] & 0xffffffffull)) - m);
-        } else {
-            id[j] = 0xffffffffu;
-            p[j] = 0.0f;
+    for (uint32_t k = 2; k <= 64u * E; k <<= 1) {
+#pragma unroll
+        for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+            if (j < (uint32_t)E) {
+#pragma unroll
+                for (uint32_t e = 0; e < (uint32_t)E; e++) {
+                    const uint32_t pe = e ^ j;
+                    if (pe > e) {
+                        const bool asc = ((lane * E + e) & k) == 0u;
+                        const unsigned long long x = v[e], y = v[pe];
+                        if ((x > y) == asc) { v[e] = y; v[pe] = x; }
+                    }
+                }
+            } else {
+#pragma unroll
+                for (uint32_t e = 0; e < (uint32_t)E; e++) {
+                    const unsigned long long o = __shfl_xor(v[e], (int)(j / E), 64);
+                    const uint32_t i = lane * E + e;
+                    const bool asc = (i & k) == 0u, lower = (i & j) == 0u;
+                    v[e] = (lower == asc) ? (o < v[e] ? o : v[e]) : (o > v[e] ? o : v[e]);
+                }
+            }
         }
     }
-    __syncthreads();
-    // softmax (sampler.rs:67-69)
-    float S = -0.0f;
-    seq_group<CB_NT, SP_EPT>(p, 0, S, NAN, sq);
+}
+
+// Exact sampler over a small survivor set (n <= 64 * E, every other element
+// below the top-k threshold, masked or -inf), by one wave: the reference's
+// sequential f32 sums are done literally, one addition at a time in the
+// reference's order, with no workgroup synchronisation (sampler.rs:46-127).
+// Called by the 64 lanes of one wave; returns the token on every lane.
+template <int E>
+__device__ uint32_t small_path_wave(const zs_sargs& a, uint32_t r, const zs_row_params& P, uint32_t n, float m,
+                                    const float* sval, const uint32_t* sidx) {
+    const zs_batch& b = a.b;
+    const uint32_t lane = (uint32_t)zs_lane();
+    // survivors by index: element i (sorted) in register i % E of lane i / E
+    unsigned long long key[E];
 #pragma unroll
-    for (int j = 0; j < SP_EPT; j++) p[j] = p[j] / S;
+    for (int e = 0; e < E; e++) {
+        const uint32_t i = lane * E + e;
+        key[e] = i < n ? (((unsigned long long)sidx[i] << 32) | zs_f2u(sval[i])) : ~0ull;
+    }
+    wave_sort_u64_e<E>(key);
+    uint32_t id[E];
+    float p[E];
+#pragma unroll
+    for (int e = 0; e < E; e++) {
+        const bool live = lane * E + e < n;
+        id[e] = (uint32_t)(key[e] >> 32);
+        p[e] = live ? zs_expf(zs_u2f((uint32_t)key[e]) - m) : 0.0f;
+    }
+    // s0 + v[0] + v[1] + ... in order (sampler.rs:68, 80, 107)
+    auto seq_sum = [&](const float (&v)[E], float s0) {
+        float s = s0;
+        for (uint32_t L = 0; L * E < n; L++)
+#pragma unroll
+            for (int e = 0; e < E; e++)
+                if (L * E + e < n) s = s + zs_readlane_f(v[e], L);
+        return s;
+    };
+    // softmax (sampler.rs:67-69)
+    const float S = seq_sum(p, -0.0f);
+#pragma unroll
+    for (int e = 0; e < E; e++) p[e] = p[e] / S;
     // min-p (sampler.rs:72-88)
     if (P.min_p > 0.0f) {
         float pm = 0.0f;
 #pragma unroll
-        for (int j = 0; j < SP_EPT; j++) pm = fmaxf(pm, p[j]);
-        pm = block_max_f<CB_NT>(pm, reinterpret_cast<float*>(sq.a));
-        float cut = P.min_p * pm;
-        float tv[SP_EPT];
+        for (int e = 0; e < E; e++) if (lane * E + e < n) pm = fmaxf(pm, p[e]);
+        pm = wave_max_f(pm);
+        const float cut = P.min_p * pm;
 #pragma unroll
-        for (int j = 0; j < SP_EPT; j++) { if (p[j] < cut) p[j] = 0.0f; tv[j] = p[j]; }
-        float kept = 0.0f;
-        seq_group<CB_NT, SP_EPT>(tv, 0, kept, NAN, sq);
+        for (int e = 0; e < E; e++) if (p[e] < cut) p[e] = 0.0f;
+        const float kept = seq_sum(p, 0.0f);
         if (kept > 0.0f)
 #pragma unroll
-            for (int j = 0; j < SP_EPT; j++) p[j] = p[j] / kept;
+            for (int e = 0; e < E; e++) p[e] = p[e] / kept;
     }
     // top-p (sampler.rs:91-115): cumsum in (p desc, idx asc) order
     if (P.top_p < 1.0f) {
         uint32_t vstar = 0, istar = 0xffffffffu;
-        bool none = !(P.top_p > 0.0f);  // cumsum 0 >= top_p: nothing kept
+        const bool none = !(P.top_p > 0.0f);  // cumsum 0 >= top_p: nothing kept
         if (!none) {
+            unsigned long long k2[E];
 #pragma unroll
-            for (int j = 0; j < SP_EPT; j++) {
-                uint32_t i = SP_EPT * t + j;
-                if (i < np) sbuf[i] = i < n ? (((unsigned long long)(~zs_f2u(p[j])) << 32) | id[j]) : ~0ull;
-            }
-            __syncthreads();
-            if (np > 1) block_bitonic_u64<CB_NT>(sbuf, (int)np);
-            float tv[SP_EPT];
-#pragma unroll
-            for (int j = 0; j < SP_EPT; j++) {
-                uint32_t i = SP_EPT * t + j;
-                tv[j] = i < n ? zs_u2f(~(uint32_t)(sbuf[i] >> 32)) : 0.0f;
-            }
+            for (int e = 0; e < E; e++)
+                k2[e] = lane * E + e < n ? (((unsigned long long)(~zs_f2u(p[e])) << 32) | id[e]) : ~0ull;
+            wave_sort_u64_e<E>(k2);
             float cum = 0.0f;
-            int stp = seq_group<CB_NT, SP_EPT>(tv, 0, cum, P.top_p, sq);
-            if (stp >= 0) {
-                vstar = ~(uint32_t)(sbuf[stp] >> 32);
-                istar = (uint32_t)(sbuf[stp] & 0xffffffffull);
-            }
-            __syncthreads();
-        }
-        float f[SP_EPT];
+            bool found = false;
+            for (uint32_t L = 0; L * E < n && !found; L++) {
 #pragma unroll
-        for (int j = 0; j < SP_EPT; j++) {
-            uint32_t pb = zs_f2u(p[j]);
-            bool keep = !none && (pb > vstar || (pb == vstar && id[j] <= istar));
-            f[j] = keep ? p[j] : 0.0f;
+                for (int e = 0; e < E; e++) {
+                    if (found || L * E + e >= n) continue;
+                    const unsigned long long ks = zs_readlane_u64(k2[e], L);
+                    cum = cum + zs_u2f(~(uint32_t)(ks >> 32));
+                    if (cum >= P.top_p) {
+                        vstar = ~(uint32_t)(ks >> 32);
+                        istar = (uint32_t)ks;
+                        found = true;
+                    }
+                }
+            }
         }
-        float sum = -0.0f;
-        seq_group<CB_NT, SP_EPT>(f, 0, sum, NAN, sq);
+        float f[E];
+#pragma unroll
+        for (int e = 0; e < E; e++) {
+            const uint32_t pb = zs_f2u(p[e]);
+            const bool keep = !none && (pb > vstar || (pb == vstar && id[e] <= istar));
+            f[e] = keep ? p[e] : 0.0f;
+        }
+        const float sum = seq_sum(f, -0.0f);
         if (sum > 0.0f)
 #pragma unroll
-            for (int j = 0; j < SP_EPT; j++) p[j] = f[j] / sum;
+            for (int e = 0; e < E; e++) p[e] = f[e] / sum;
     }
     // draw (sampler.rs:118-127); r == 0 stops at index 0 whatever its p
     const float rr = zs_philox_uniform(b.d_seed[r], b.d_counter[r], 0u);
     if (rr <= 0.0f) return 0;
     float cum = 0.0f;
-    int stp = seq_group<CB_NT, SP_EPT>(p, 0, cum, rr, sq);
-    uint32_t tok = V - 1;
-    if (stp >= 0) {
-        __syncthreads();
-        if (t == stp / SP_EPT) {
+    for (uint32_t L = 0; L * E < n; L++) {
 #pragma unroll
-            for (int j = 0; j < SP_EPT; j++) if (j == stp % SP_EPT) sq.stop = (int)id[j];
+        for (int e = 0; e < E; e++) {
+            if (L * E + e >= n) continue;
+            cum = cum + zs_readlane_f(p[e], L);
+            if (cum >= rr) return zs_readlane_u(id[e], L);
         }
-        __syncthreads();
-        tok = (uint32_t)sq.stop;
-        __syncthreads();
     }
-    return tok;
+    return b.V - 1;
 }
 
+#ifdef ZS_DEBUG_CB
+__device__ unsigned long long zs_dbg_cb[10];
+#define CB_MARK(k) do { if (threadIdx.x == 0) { const long long c1_ = clock64(); cbd[k] = c1_ - cbc0; atomicAdd(&zs_dbg_cb[k], (unsigned long long)(c1_ - cbc0)); atomicMax(&zs_dbg_cb[9], (unsigned long long)(c1_ - cbs)); cbc0 = c1_; } } while (0)
+__device__ long long zs_dbg_cbrow[512][8];
+#define CB_PRINT() do { if (threadIdx.x == 0) { for (int q_ = 1; q_ < 7; q_++) zs_dbg_cbrow[r][q_] = cbd[q_]; zs_dbg_cbrow[r][0] = cbc0 - cbs; zs_dbg_cbrow[r][7] = (long long)status | ((long long)mode << 16) | ((long long)P.top_k << 24); } } while (0)
+#else
+#define CB_MARK(k) do {} while (0)
+#define CB_PRINT() do {} while (0)
+#endif
 __global__ __launch_bounds__(CB_NT) void zs_k_combine(zs_sargs a) {
+#ifdef ZS_DEBUG_CB
+    long long cbc0 = clock64();
+    const long long cbs = cbc0;
+    long long cbd[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#endif
     const uint32_t r = blockIdx.x;
     const zs_batch& b = a.b;
     const uint32_t V = b.V;
@@ -1075,7 +1120,9 @@ __global__ __launch_bounds__(CB_NT) void zs_k_combine(zs_sargs a) {
     __shared__ uint32_t cid_sh[ZS_OBS_CAND];
     __shared__ float cx_sh[ZS_OBS_CAND];
     const zs_row_params P = b.d_params[r];
-    zs_row_state st = a.rst[r];
+    // the row state is written field by field by thread 0 (a private copy of
+    // the whole struct per thread would live in scratch memory)
+    zs_row_state& st = a.rst[r];
     if (st.status & ZS_ST_LIMIT) {
         if (t == 0) {
             st.mode = ZS_MODE_DONE;
@@ -1084,7 +1131,7 @@ __global__ __launch_bounds__(CB_NT) void zs_k_combine(zs_sargs a) {
             st.rounds = 0;
             st.n_cand = 0;
             st.klist = 0;
-            a.rst[r] = st;
+            st.kpend = 0;
         }
         return;
     }
@@ -1100,6 +1147,7 @@ __global__ __launch_bounds__(CB_NT) void zs_k_combine(zs_sargs a) {
     }
     __syncthreads();
     const zs_chunk_stat* cs = cs_sh;
+    CB_MARK(1);
 
     // ---------------- observers: max, special rows, top candidates ----------------
     float M = -INFINITY;
@@ -1133,7 +1181,7 @@ __global__ __launch_bounds__(CB_NT) void zs_k_combine(zs_sargs a) {
         while (np2 < nco) np2 <<= 1;
         for (uint32_t i = nco + t; i < np2; i += CB_NT) sbuf[i] = ~0ull;
         __syncthreads();
-        if (np2 > 1) block_bitonic_u64<CB_NT>(sbuf, (int)np2);
+        if (np2 > 1) block_sort_u64<CB_NT>(sbuf, np2);
         n_cand = nco < ZS_OBS_CAND ? nco : ZS_OBS_CAND;
         if (t < (int)n_cand) {
             cid_sh[t] = (uint32_t)(sbuf[t] & 0xffffffffull);
@@ -1141,6 +1189,7 @@ __global__ __launch_bounds__(CB_NT) void zs_k_combine(zs_sargs a) {
         }
         __syncthreads();
     }
+    CB_MARK(2);
     // the sampler sees x~ itself when T == 1 and no bias / penalty applies
     uint32_t has_y = 0;
     {
@@ -1151,6 +1200,7 @@ __global__ __launch_bounds__(CB_NT) void zs_k_combine(zs_sargs a) {
     }
     const uint32_t z_is_x = (P.temperature == 1.0f && !has_y) ? 1u : 0u;
 
+    CB_MARK(3);
     // ---------------- sampler ----------------
     const float T = P.temperature;
     uint32_t token = 0;
@@ -1205,7 +1255,8 @@ __global__ __launch_bounds__(CB_NT) void zs_k_combine(zs_sargs a) {
         while (np2 < ncs) np2 <<= 1;
         for (uint32_t i = ncs + t; i < np2; i += CB_NT) sbuf[i] = ~0ull;
         __syncthreads();
-        if (np2 > 1) block_bitonic_u64<CB_NT>(sbuf, (int)np2);
+        if (np2 > 1) block_sort_u64<CB_NT>(sbuf, np2);
+        CB_MARK(4);
         bool small = false;
         float thr = -INFINITY;
         if (has_topk && P.top_k <= ZS_KS) {
@@ -1250,12 +1301,19 @@ __global__ __launch_bounds__(CB_NT) void zs_k_combine(zs_sargs a) {
             if (n > ZS_SMALL_CAP) {
                 small = false;
             } else {
-                token = small_path_sample(a, r, P, n, zmax, sval, sidx, sbuf, sq);
+                if (t < 64) {
+                    const uint32_t tk = n <= 64 ? small_path_wave<1>(a, r, P, n, zmax, sval, sidx)
+                                                : small_path_wave<ZS_SMALL_CAP / 64>(a, r, P, n, zmax, sval, sidx);
+                    if (t == 0) n_sh = tk;
+                }
+                __syncthreads();
+                token = n_sh;
                 status |= ZS_ST_SMALL;
             }
         }
         if (!small) mode = ZS_MODE_BIG;
     }
+    CB_MARK(5);
     // ---- predictions for the parallel exact-sum rounds
     uint32_t rounds = 0;
     {
@@ -1290,6 +1348,8 @@ __global__ __launch_bounds__(CB_NT) void zs_k_combine(zs_sargs a) {
         }
         if (obs_need & ZS_OBS_H) rounds |= 1u << ZS_SUM_OBS_H;
     }
+    CB_MARK(6);
+    CB_PRINT();
     if (t == 0) {
         st.rounds = rounds;
         st.z_max = zmax;
@@ -1306,7 +1366,6 @@ __global__ __launch_bounds__(CB_NT) void zs_k_combine(zs_sargs a) {
         st.z_is_x = z_is_x;
         st.klist = 0;
         st.kpend = 0;
-        a.rst[r] = st;
     }
     if (mode == ZS_MODE_BIG) {
         // bucket counts and masses of the top-p walk, accumulated by zs_k_pv
@@ -2606,7 +2665,7 @@ __device__ __forceinline__ int tp_walk(const zs_sargs& a, uint32_t r, float top_
                 const float v = i + lane < n ? zs_u2f(gv[st0 + i + lane]) : 0.0f;
                 const uint32_t m = min(64u, n - i);
                 for (uint32_t j = 0; j < m; j++) {
-                    ss = ss + __shfl(v, (int)j, 64);
+                    ss = ss + zs_readlane_f(v, j);
                     if (ss >= top_p) { stop = true; at = i + j; break; }
                 }
             }
@@ -3217,6 +3276,19 @@ __global__ __launch_bounds__(SK_NT) void zs_k_stitchK(zs_sargs a) {
 // zs_k_final: per-row outputs (logprobs.rs:34-54, hallucination.rs:232-257)
 // ===========================================================================
 __global__ __launch_bounds__(64) void zs_k_final(zs_sargs a) {
+#ifdef ZS_DEBUG_CB
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        printf("cb phases:");
+        for (int k = 1; k < 10; k++) { printf(" %d:%llu", k, zs_dbg_cb[k]); zs_dbg_cb[k] = 0; }
+        printf("\n");
+        for (int q = 0; q < 10; q++) {
+            int bi = 0;
+            for (uint32_t i = 1; i < a.b.B; i++) if (zs_dbg_cbrow[i][0] > zs_dbg_cbrow[bi][0]) bi = (int)i;
+            printf("cbrow %d tot %lld flags %llx: %lld %lld %lld %lld %lld %lld\n", bi, zs_dbg_cbrow[bi][0], zs_dbg_cbrow[bi][7], zs_dbg_cbrow[bi][1], zs_dbg_cbrow[bi][2], zs_dbg_cbrow[bi][3], zs_dbg_cbrow[bi][4], zs_dbg_cbrow[bi][5], zs_dbg_cbrow[bi][6]);
+            zs_dbg_cbrow[bi][0] = -1;
+        }
+    }
+#endif
 #ifdef ZS_DEBUG_P1
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         printf("p1 phases:");
@@ -3291,8 +3363,8 @@ __global__ __launch_bounds__(64) void zs_k_final(zs_sargs a) {
             const float lp = xv - lse;
             uint32_t rank = 0;
             for (uint32_t i = 0; i < nc; i++) {
-                const float li = __shfl(lp, (int)i, 64);
-                const uint32_t ii = __shfl(id, (int)i, 64);
+                const float li = zs_readlane_f(lp, i);
+                const uint32_t ii = zs_readlane_u(id, i);
                 rank += (li > lp || (li == lp && ii < id)) ? 1u : 0u;
             }
             // sorted x~ by rank, for the check below
