@@ -107,8 +107,8 @@ SPEC_K = 4
 # HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
 # (profiles/c5_traffic.md), scaled by the copy-kernel calibration there; None
 # where not measured
-TRAFFIC = {"zs_k_big": 41.4e6, "zs_k_pass1": 168.6e6, "zs_k_pv": 55.2e6,
-           "zs_k_spec_stats": 1402.0e6, "zs_k_spec_sums": 1426.7e6}
+TRAFFIC = {"zs_k_pass1": 167.0e6, "zs_k_pv": 64.1e6, "zs_k_tp_inc": 36.4e6, "zs_k_big": 0.5e6,
+           "zs_k_spec_stats": 1401.8e6, "zs_k_spec_sums": 1426.5e6}
 
 
 def spec_bytes_per_row(V, k):
