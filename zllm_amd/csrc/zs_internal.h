@@ -21,7 +21,7 @@
 // Big-row engine: 1024 threads, 4 consecutive elements per thread.
 #define ZS_BIG_NT 1024
 #define ZS_BIG_G 4096
-#define ZS_SORT_CAP 32768
+#define ZS_SORT_CAP 8192
 // top-K pool of the batched lane (gpu/mod.rs:1846 TOPK_K)
 #define ZS_LANE_K 64
 

@@ -1745,7 +1745,7 @@ __global__ __launch_bounds__(ST_NT) void zs_k_stitchB(zs_sargs a) { stitch_body<
 // zs_k_big: exact emulation of the reference's sequential sums over a full row.
 // ===========================================================================
 #define BK_NB 2048   // buckets per level of the top-p walk
-#define BK_NC 16     // copies of each bucket counter (by lane)
+#define BK_NC 4      // copies of each bucket counter (by lane)
 #define BK_SERIAL 128   // exact buckets up to this size are walked by one thread
 #ifndef BK_WEPT
 #define BK_WEPT 4  // values per thread of one quick-walk group
