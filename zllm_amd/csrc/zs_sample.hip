@@ -224,7 +224,7 @@ struct p1_shared {
 // Exact top-K (key desc, index asc) of the chunk's valid keys; writes the
 // candidates (unordered) to out_key/out_idx. Element e = j*4+q of thread t has
 // index base + (j*256 + t)*4 + q.
-__device__ __forceinline__ void p1_topk(const float (&kv)[P1_EPT], uint32_t vmask, uint32_t nvalid, uint32_t K,
+__device__ __forceinline__ void p1_topk(const uint32_t (&kv)[P1_EPT], uint32_t vmask, uint32_t nvalid, uint32_t K,
                         uint32_t base, uint32_t* out_key, uint32_t* out_idx, uint32_t* n_out, uint32_t* kth,
                         uint32_t* full, p1_shared& sh) {
     const int t = threadIdx.x;
@@ -235,7 +235,7 @@ __device__ __forceinline__ void p1_topk(const float (&kv)[P1_EPT], uint32_t vmas
             if ((vmask >> e) & 1u) {
                 uint32_t pos = atomicAdd(&sh.cnt, 1u);
                 if (pos < K) {
-                    out_key[pos] = zs_total_key(kv[e]);
+                    out_key[pos] = kv[e];
                     out_idx[pos] = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
                 }
             }
@@ -251,8 +251,8 @@ __device__ __forceinline__ void p1_topk(const float (&kv)[P1_EPT], uint32_t vmas
         if (t < 256) sh.hist[t] = 0;
         __syncthreads();
         for (int e = 0; e < P1_EPT; e++)
-            if (((vmask >> e) & 1u) && (zs_total_key(kv[e]) & mask) == prefix)
-                atomicAdd(&sh.hist[(zs_total_key(kv[e]) >> shift) & 255u], 1u);
+            if (((vmask >> e) & 1u) && (kv[e] & mask) == prefix)
+                atomicAdd(&sh.hist[(kv[e] >> shift) & 255u], 1u);
         __syncthreads();
         if (t < 64) {
             // lane l owns bins 255-4l .. 252-4l (descending)
@@ -278,23 +278,23 @@ __device__ __forceinline__ void p1_topk(const float (&kv)[P1_EPT], uint32_t vmas
     uint32_t my_eq = 0;
     for (int e = 0; e < P1_EPT; e++) {
         if (!((vmask >> e) & 1u)) continue;
-        if (zs_total_key(kv[e]) > kk) {
+        if (kv[e] > kk) {
             uint32_t pos = atomicAdd(&sh.cnt, 1u);
             if (pos < K) {
-                out_key[pos] = zs_total_key(kv[e]);
+                out_key[pos] = kv[e];
                 out_idx[pos] = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
             }
-        } else if (zs_total_key(kv[e]) == kk) {
+        } else if (kv[e] == kk) {
             my_eq++;
         }
     }
     uint32_t n_eq = block_sum_u<ZS_P1_NT>(my_eq, sh.u);
     if (n_eq == need) {
         for (int e = 0; e < P1_EPT; e++) {
-            if (((vmask >> e) & 1u) && zs_total_key(kv[e]) == kk) {
+            if (((vmask >> e) & 1u) && kv[e] == kk) {
                 uint32_t pos = atomicAdd(&sh.cnt, 1u);
                 if (pos < K) {
-                    out_key[pos] = zs_total_key(kv[e]);
+                    out_key[pos] = kv[e];
                     out_idx[pos] = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
                 }
             }
@@ -306,18 +306,18 @@ __device__ __forceinline__ void p1_topk(const float (&kv)[P1_EPT], uint32_t vmas
             uint32_t c = 0;
             for (int q = 0; q < 4; q++) {
                 int e = j * 4 + q;
-                c += (((vmask >> e) & 1u) && zs_total_key(kv[e]) == kk) ? 1u : 0u;
+                c += (((vmask >> e) & 1u) && kv[e] == kk) ? 1u : 0u;
             }
             uint32_t tot;
             uint32_t ex = block_excl_scan_u<ZS_P1_NT>(c, sh.u, &tot);
             uint32_t rank = carry + ex;
             for (int q = 0; q < 4; q++) {
                 int e = j * 4 + q;
-                if (((vmask >> e) & 1u) && zs_total_key(kv[e]) == kk) {
+                if (((vmask >> e) & 1u) && kv[e] == kk) {
                     if (rank < need) {
                         uint32_t pos = atomicAdd(&sh.cnt, 1u);
                         if (pos < K) {
-                            out_key[pos] = zs_total_key(kv[e]);
+                            out_key[pos] = kv[e];
                             out_idx[pos] = base + (j * ZS_P1_NT + t) * 4 + q;
                         }
                     }
@@ -346,7 +346,7 @@ __device__ __forceinline__ void p1_topk(const float (&kv)[P1_EPT], uint32_t vmas
 // radix select.
 // nvalid: valid elements of the chunk; nfin: valid elements whose key is above
 // that of -inf.
-__device__ __forceinline__ void p1_topk_fast(const float (&kv)[P1_EPT], uint32_t vmask, uint32_t nvalid,
+__device__ __forceinline__ void p1_topk_fast(const uint32_t (&kv)[P1_EPT], uint32_t vmask, uint32_t nvalid,
                              uint32_t nfin, uint32_t K, uint32_t base,
                              uint32_t* out_key, uint32_t* out_idx, uint32_t* n_out, uint32_t* kth,
                              uint32_t* full, p1_shared& sh) {
@@ -354,7 +354,7 @@ __device__ __forceinline__ void p1_topk_fast(const float (&kv)[P1_EPT], uint32_t
     uint32_t tm = 0;
 #pragma unroll
     for (int e = 0; e < P1_EPT; e++)
-        if ((vmask >> e) & 1u) tm = max(tm, zs_total_key(kv[e]));
+        if ((vmask >> e) & 1u) tm = max(tm, kv[e]);
     const uint32_t c = (K + (ZS_P1_NT / 64) - 1) / (ZS_P1_NT / 64);
     if (nvalid <= K || c > 64) {
         p1_topk(kv, vmask, nvalid, K, base, out_key, out_idx, n_out, kth, full, sh);
@@ -368,9 +368,9 @@ __device__ __forceinline__ void p1_topk_fast(const float (&kv)[P1_EPT], uint32_t
         __syncthreads();
 #pragma unroll
         for (int e = 0; e < P1_EPT; e++) {
-            if (((vmask >> e) & 1u) && zs_total_key(kv[e]) > kninf) {
+            if (((vmask >> e) & 1u) && kv[e] > kninf) {
                 const uint32_t p = atomicAdd(&sh.cnt, 1u);
-                out_key[p] = zs_total_key(kv[e]);
+                out_key[p] = kv[e];
                 out_idx[p] = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
             }
         }
@@ -383,13 +383,13 @@ __device__ __forceinline__ void p1_topk_fast(const float (&kv)[P1_EPT], uint32_t
             if (carry >= need) break;  // uniform: the lowest ids are taken
             uint32_t cj = 0;
 #pragma unroll
-            for (int q = 0; q < 4; q++) cj += (((vmask >> (4 * j + q)) & 1u) && zs_total_key(kv[4 * j + q]) == kninf) ? 1u : 0u;
+            for (int q = 0; q < 4; q++) cj += (((vmask >> (4 * j + q)) & 1u) && kv[4 * j + q] == kninf) ? 1u : 0u;
             uint32_t tot;
             uint32_t rank = carry + block_excl_scan_u<ZS_P1_NT>(cj, sh.u, &tot);
 #pragma unroll
             for (int q = 0; q < 4; q++) {
                 const int e = 4 * j + q;
-                if (((vmask >> e) & 1u) && zs_total_key(kv[e]) == kninf) {
+                if (((vmask >> e) & 1u) && kv[e] == kninf) {
                     if (rank < need) {
                         out_key[nfin + rank] = kninf;
                         out_idx[nfin + rank] = base + (j * ZS_P1_NT + t) * 4 + q;
@@ -447,7 +447,7 @@ __device__ __forceinline__ void p1_topk_fast(const float (&kv)[P1_EPT], uint32_t
     }
     uint32_t cnt = 0;
 #pragma unroll
-    for (int e = 0; e < P1_EPT; e++) cnt += (((vmask >> e) & 1u) && zs_total_key(kv[e]) >= theta) ? 1u : 0u;
+    for (int e = 0; e < P1_EPT; e++) cnt += (((vmask >> e) & 1u) && kv[e] >= theta) ? 1u : 0u;
     uint32_t nsup;
     uint32_t pos = block_excl_scan_u<ZS_P1_NT>(cnt, sh.u, &nsup);
     if (nsup > P1_SORT) {
@@ -457,9 +457,9 @@ __device__ __forceinline__ void p1_topk_fast(const float (&kv)[P1_EPT], uint32_t
     // composite ((~key) << 32 | index): ascending order = key desc, index asc
 #pragma unroll
     for (int e = 0; e < P1_EPT; e++) {
-        if (((vmask >> e) & 1u) && zs_total_key(kv[e]) >= theta) {
+        if (((vmask >> e) & 1u) && kv[e] >= theta) {
             const uint32_t idx = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
-            sh.s64[pos++] = ((unsigned long long)(~zs_total_key(kv[e])) << 32) | idx;
+            sh.s64[pos++] = ((unsigned long long)(~kv[e]) << 32) | idx;
         }
     }
     __syncthreads();
@@ -502,14 +502,14 @@ __device__ __forceinline__ void p1_topk_fast(const float (&kv)[P1_EPT], uint32_t
 // of them exist. The list then holds the chunk's top K (and possibly more), in
 // any order -- what the combine kernel's merge needs. Returns false (nothing
 // written) when more than `cap` elements reach theta.
-__device__ __forceinline__ bool p1_superset(const float (&kv)[P1_EPT], uint32_t vmask, uint32_t K, uint32_t cap,
+__device__ __forceinline__ bool p1_superset(const uint32_t (&kv)[P1_EPT], uint32_t vmask, uint32_t K, uint32_t cap,
                                             uint32_t base, uint32_t* out_key, uint32_t* out_idx, uint32_t* n_out,
                                             p1_shared& sh) {
     const int t = threadIdx.x, lane = zs_lane();
     uint32_t tm = 0;
 #pragma unroll
     for (int e = 0; e < P1_EPT; e++)
-        if ((vmask >> e) & 1u) tm = max(tm, zs_total_key(kv[e]));
+        if ((vmask >> e) & 1u) tm = max(tm, kv[e]);
     const uint32_t srt = wave_sort_u32(tm);
     sh.tmax[zs_wid() * 64 + lane] = srt;
     if (t == 0) sh.cnt = 0;
@@ -531,14 +531,14 @@ __device__ __forceinline__ bool p1_superset(const float (&kv)[P1_EPT], uint32_t 
     const uint32_t theta = max(sh.sel[2], 1u);
     uint32_t cnt = 0;
 #pragma unroll
-    for (int e = 0; e < P1_EPT; e++) cnt += (((vmask >> e) & 1u) && zs_total_key(kv[e]) >= theta) ? 1u : 0u;
+    for (int e = 0; e < P1_EPT; e++) cnt += (((vmask >> e) & 1u) && kv[e] >= theta) ? 1u : 0u;
     const uint32_t nsup = block_sum_u<ZS_P1_NT>(cnt, sh.u);
     if (nsup > cap) return false;
 #pragma unroll
     for (int e = 0; e < P1_EPT; e++) {
-        if (((vmask >> e) & 1u) && zs_total_key(kv[e]) >= theta) {
+        if (((vmask >> e) & 1u) && kv[e] >= theta) {
             const uint32_t p = atomicAdd(&sh.cnt, 1u);
-            out_key[p] = zs_total_key(kv[e]);
+            out_key[p] = kv[e];
             out_idx[p] = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
         }
     }
@@ -549,18 +549,20 @@ __device__ __forceinline__ bool p1_superset(const float (&kv)[P1_EPT], uint32_t 
 // Compaction of the chunk's finite sampler values (the list when the chunk has
 // at most K of them: then it holds every element a top-k or a small-survivor
 // path can keep).
-__device__ __forceinline__ void p1_finite(const float (&zv)[P1_EPT], uint32_t vmask,
+__device__ __forceinline__ void p1_finite(const uint32_t (&zv)[P1_EPT], uint32_t vmask,
                           uint32_t base, uint32_t* out_key, uint32_t* out_idx, p1_shared& sh) {
     const int t = threadIdx.x;
     uint32_t cnt = 0;
+    const uint32_t kninf = zs_total_key(-INFINITY), kpinf = zs_total_key(INFINITY);
+    // z > -inf: keys above that of -inf, NaN (above +inf) excluded
 #pragma unroll
-    for (int e = 0; e < P1_EPT; e++) cnt += (((vmask >> e) & 1u) && zv[e] > -INFINITY) ? 1u : 0u;
+    for (int e = 0; e < P1_EPT; e++) cnt += (((vmask >> e) & 1u) && zv[e] > kninf && zv[e] <= kpinf) ? 1u : 0u;
     uint32_t tot;
     uint32_t pos = block_excl_scan_u<ZS_P1_NT>(cnt, sh.u, &tot);
 #pragma unroll
     for (int e = 0; e < P1_EPT; e++) {
-        if (((vmask >> e) & 1u) && zv[e] > -INFINITY) {
-            out_key[pos] = zs_total_key(zv[e]);
+        if (((vmask >> e) & 1u) && zv[e] > kninf && zv[e] <= kpinf) {
+            out_key[pos] = zv[e];
             out_idx[pos] = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
             pos++;
         }
@@ -569,8 +571,8 @@ __device__ __forceinline__ void p1_finite(const float (&zv)[P1_EPT], uint32_t vm
 
 // element e of the calling thread in a [P1_EPT][ZS_P1_NT] LDS array
 struct p1_lds_arr {
-    float* p;
-    __device__ __forceinline__ float& operator[](int e) const { return p[e * ZS_P1_NT]; }
+    uint32_t* p;
+    __device__ __forceinline__ uint32_t& operator[](int e) const { return p[e * ZS_P1_NT]; }
 };
 
 #ifdef ZS_DEBUG_P1
@@ -603,10 +605,13 @@ __global__ __launch_bounds__(ZS_P1_NT) __attribute__((amdgpu_waves_per_eu(3))) v
     const uint32_t pc0 = psub[c * ZS_SUBS_PER_CHUNK];
     const uint32_t pc1 = psub[min((c + 1) * ZS_SUBS_PER_CHUNK, nsub_row)];
 
-    // x~ lives in LDS (thread t's element e at xsh[e][t]) until the observer
-    // list, z in registers: both arrays in registers would halve occupancy
-    __shared__ float xsh[P1_EPT][ZS_P1_NT];
+    // x~ lives in LDS as total-order keys (thread t's element e at xsh[e][t])
+    // until the observer list, z in registers (keys after the temperature):
+    // both arrays in registers would halve occupancy. Every later use compares
+    // keys; the float is recovered where arithmetic needs it.
+    __shared__ uint32_t xsh[P1_EPT][ZS_P1_NT];
     const p1_lds_arr xo{&xsh[0][t]};
+    const uint32_t kninf = zs_total_key(-INFINITY), kpinf = zs_total_key(INFINITY);
     float zv[P1_EPT];
     uint32_t vmask = 0;
 #pragma unroll
@@ -625,7 +630,8 @@ __global__ __launch_bounds__(ZS_P1_NT) __attribute__((amdgpu_waves_per_eu(3))) v
             bool valid = idx + q < V;
             float x = vv[q];
             if (masked && !((w >> q) & 1u)) x = -INFINITY;
-            xo[e] = x;
+            if (!valid) x = -INFINITY;  // neutral in every statistic
+            xo[e] = zs_total_key(x);
             zv[e] = x;
             if (valid) vmask |= 1u << e;
         }
@@ -657,16 +663,17 @@ __global__ __launch_bounds__(ZS_P1_NT) __attribute__((amdgpu_waves_per_eu(3))) v
 #pragma unroll
                     for (int qq = 0; qq < 4; qq++)
                         if (jj == (int)j && qq == (int)q) {
-                            if (fl & ZS_PF_BAN) { xo[jj * 4 + qq] = -INFINITY; zv[jj * 4 + qq] = -INFINITY; }
+                            if (fl & ZS_PF_BAN) { xo[jj * 4 + qq] = kninf; zv[jj * 4 + qq] = -INFINITY; }
                             if (fl & ZS_PF_Y) zv[jj * 4 + qq] = y;
                         }
             }
             __syncthreads();
         }
     }
-    // z = y / T
+    // z = y / T, kept as keys
+    uint32_t kz[P1_EPT];
 #pragma unroll
-    for (int e = 0; e < P1_EPT; e++) zv[e] = zs_temper(zv[e], T);
+    for (int e = 0; e < P1_EPT; e++) kz[e] = zs_total_key(zs_temper(zv[e], T));
 
     P1_MARK(3);
 #ifdef XP_NOSTAT
@@ -675,24 +682,40 @@ __global__ __launch_bounds__(ZS_P1_NT) __attribute__((amdgpu_waves_per_eu(3))) v
     // ---- chunk statistics of x~ (observers) and z (sampler), one workgroup
     // reduction: maxima, NaN / +inf flags, the last NaN of z, and counts of
     // finite z and of elements whose key is above that of -inf for the lists
-    const uint32_t kninf = zs_total_key(-INFINITY);
-    float omax = -INFINITY, zmax = -INFINITY;
-    uint32_t fl = 0, zfin = 0, zabove = 0, xabove = 0;
+    // branch-free on keys: NaN keys lie above +inf's (positive) or below
+    // -inf's (negative); the maxima skip them (fmaxf semantics); the rare
+    // waves with a NaN z redo their elements for the last NaN and the finite
+    // count (+inf counts as finite there: the test is z > -inf)
+    uint32_t okm = kninf, zkm = kninf;
+    uint32_t fl = 0, zfin, zabove = 0, xabove = 0;
+    bool xnan = false, znan = false;
     int last_nan = -1;
 #pragma unroll
     for (int e = 0; e < P1_EPT; e++) {
-        if (!((vmask >> e) & 1u)) continue;
-        const float x = xo[e], z = zv[e];
-        if (x != x) fl |= ZS_CF_OBS_NAN;
-        omax = fmaxf(omax, x);
-        xabove += zs_total_key(x) > kninf ? 1u : 0u;
-        const uint32_t idx = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
-        if (z != z) { fl |= ZS_CF_Z_NAN; last_nan = max(last_nan, (int)idx); }
-        else if (z == INFINITY) fl |= ZS_CF_Z_PINF;
-        zfin += (z == z && z > -INFINITY) ? 1u : 0u;
-        zabove += zs_total_key(z) > kninf ? 1u : 0u;
-        zmax = fmaxf(zmax, z);
+        const uint32_t kx = xo[e], k = kz[e];
+        xnan |= (kx > kpinf) | (kx < kninf);
+        znan |= (k > kpinf) | (k < kninf);
+        okm = max(okm, kx <= kpinf ? kx : kninf);
+        zkm = max(zkm, k <= kpinf ? k : kninf);
+        xabove += kx > kninf ? 1u : 0u;
+        zabove += k > kninf ? 1u : 0u;
     }
+    zfin = zabove;
+    if (__ballot(znan)) {
+        zfin = 0;
+#pragma unroll
+        for (int e = 0; e < P1_EPT; e++) {
+            if (!((vmask >> e) & 1u)) continue;
+            const uint32_t k = kz[e];
+            const uint32_t idx = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
+            if (k > kpinf || k < kninf) last_nan = max(last_nan, (int)idx);
+            zfin += (k > kninf && k <= kpinf) ? 1u : 0u;
+        }
+    }
+    if (xnan) fl |= ZS_CF_OBS_NAN;
+    if (znan) fl |= ZS_CF_Z_NAN;
+    if (zkm == kpinf) fl |= ZS_CF_Z_PINF;
+    float omax = zs_key_to_float(okm), zmax = zs_key_to_float(zkm);
     for (int d = 32; d > 0; d >>= 1) {
         omax = fmaxf(omax, __shfl_xor(omax, d, 64));
         zmax = fmaxf(zmax, __shfl_xor(zmax, d, 64));
@@ -731,7 +754,7 @@ __global__ __launch_bounds__(ZS_P1_NT) __attribute__((amdgpu_waves_per_eu(3))) v
         uint32_t tn = 0;
 #pragma unroll
         for (int e = 0; e < P1_EPT; e++) {
-            const float z = zv[e];
+            const float z = zs_key_to_float(kz[e]);
             if (!((vmask >> e) & 1u) || z != z) continue;
             const uint32_t idx = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
             // -0.0 and +0.0 compare equal in the reference (partial_cmp): map both to +0
@@ -787,14 +810,15 @@ __global__ __launch_bounds__(ZS_P1_NT) __attribute__((amdgpu_waves_per_eu(3))) v
             for (int q = 0; q < 4; q++) {
                 const int e = j * 4 + q;
                 if (!((vmask >> e) & 1u)) continue;
-                if (xo[e] == omax) hasmax |= 1u << (2 * sj);
-                if (zv[e] == zmax) hasmax |= 2u << (2 * sj);
+                const float xe = zs_key_to_float(xo[e]), ze = zs_key_to_float(kz[e]);
+                if (xe == omax) hasmax |= 1u << (2 * sj);
+                if (ze == zmax) hasmax |= 2u << (2 * sj);
                 if (om) {
-                    float d = xo[e] - omax;
+                    float d = xe - omax;
                     if (d > -INFINITY) { float ex = __expf(d); m1 += ex; md += d * ex; }
                 }
                 if (zm) {
-                    float d = zv[e] - zmax;
+                    float d = ze - zmax;
                     if (d > -INFINITY) mz += __expf(d);
                 }
             }
@@ -841,10 +865,10 @@ __global__ __launch_bounds__(ZS_P1_NT) __attribute__((amdgpu_waves_per_eu(3))) v
     // path, which needs every chunk to have at most ZS_KS finite values.
     if (T > 0.0f) {
         if (zfin <= Ks) {
-            p1_finite(zv, vmask, base, a.cs_key + lofs * ZS_KS, a.cs_idx + lofs * ZS_KS, sh);
+            p1_finite(kz, vmask, base, a.cs_key + lofs * ZS_KS, a.cs_idx + lofs * ZS_KS, sh);
             ns = zfin;
         } else if (has_topk && P.top_k <= ZS_KS) {
-            p1_topk_fast(zv, vmask, nvalid, zabove, Ks, base, a.cs_key + lofs * ZS_KS, a.cs_idx + lofs * ZS_KS, &ns, &s_kth,
+            p1_topk_fast(kz, vmask, nvalid, zabove, Ks, base, a.cs_key + lofs * ZS_KS, a.cs_idx + lofs * ZS_KS, &ns, &s_kth,
                          &s_full, sh);
         }
     }
@@ -854,7 +878,7 @@ __global__ __launch_bounds__(ZS_P1_NT) __attribute__((amdgpu_waves_per_eu(3))) v
     if (Ko > ZS_KO) Ko = ZS_KO;
     uint32_t no, o_kth, o_full;
     no = o_kth = o_full = 0;
-    float xr[P1_EPT];  // z is dead here: x~ back in registers for the list
+    uint32_t xr[P1_EPT];  // z is dead here: x~ keys back in registers for the list
 #pragma unroll
     for (int e = 0; e < P1_EPT; e++) xr[e] = xo[e];
     if ((P.flags & (ZS_ROW_LOGPROBS | ZS_ROW_UNCERTAINTY)) &&
