@@ -802,6 +802,8 @@ __global__ __launch_bounds__(ZS_P1_NT) __attribute__((amdgpu_waves_per_eu(3))) v
         __shared__ float msh[ZS_P1_NT / 64][P1_J][3];
         // bit 2s: sub-chunk s holds the chunk's observer max, bit 2s+1: its sampler max
         uint32_t hasmax = 0;
+        static_assert(P1_J == 8, "the reduce-scatter below splits 8 rows over 3 lane bits");
+        float mv[3][P1_J];
 #pragma unroll
         for (int j = 0; j < P1_J; j++) {
             float m1 = 0.0f, md = 0.0f, mz = 0.0f;
@@ -822,12 +824,33 @@ __global__ __launch_bounds__(ZS_P1_NT) __attribute__((amdgpu_waves_per_eu(3))) v
                     if (d > -INFINITY) mz += __expf(d);
                 }
             }
-            for (int d = 32; d > 0; d >>= 1) {
-                m1 += __shfl_xor(m1, d, 64);
-                md += __shfl_xor(md, d, 64);
-                mz += __shfl_xor(mz, d, 64);
+            mv[0][j] = m1; mv[1][j] = md; mv[2][j] = mz;
+        }
+        // reduce-scatter over the wave: each exchange halves the rows a lane
+        // keeps (lane bits 5, 4, 3 pick them), then 8-lane sums; lane 8j ends
+        // with row j's totals
+        {
+            const uint32_t lane = (uint32_t)zs_lane();
+#pragma unroll
+            for (int u = 0; u < 3; u++) {
+                float v4[4], v2[2];
+                const bool h5 = (lane & 32u) != 0, h4 = (lane & 16u) != 0, h3 = (lane & 8u) != 0;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const float send = h5 ? mv[u][k] : mv[u][k + 4];
+                    v4[k] = (h5 ? mv[u][k + 4] : mv[u][k]) + __shfl_xor(send, 32, 64);
+                }
+#pragma unroll
+                for (int k = 0; k < 2; k++) {
+                    const float send = h4 ? v4[k] : v4[k + 2];
+                    v2[k] = (h4 ? v4[k + 2] : v4[k]) + __shfl_xor(send, 16, 64);
+                }
+                float v1 = (h3 ? v2[1] : v2[0]) + __shfl_xor(h3 ? v2[0] : v2[1], 8, 64);
+                v1 += __shfl_xor(v1, 4, 64);
+                v1 += __shfl_xor(v1, 2, 64);
+                v1 += __shfl_xor(v1, 1, 64);
+                if ((lane & 7u) == 0) msh[wid][lane >> 3][u] = v1;
             }
-            if (zs_lane() == 0) { msh[wid][j][0] = m1; msh[wid][j][1] = md; msh[wid][j][2] = mz; }
         }
         for (int d = 32; d > 0; d >>= 1) hasmax |= __shfl_xor(hasmax, d, 64);
         __shared__ uint32_t hsh[ZS_P1_NT / 64];
