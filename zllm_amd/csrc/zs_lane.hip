@@ -176,7 +176,7 @@ __global__ __launch_bounds__(LN_NT) void zs_k_btopk(const float* logits, uint32_
     while (np2 < n) np2 <<= 1;
     for (uint32_t i = n + t; i < np2; i += LN_NT) buf[i] = ~0ull;
     __syncthreads();
-    if (np2 > 1) block_bitonic_u64<LN_NT>(buf, (int)np2);
+    if (np2 > 1) block_sort_u64<LN_NT>(buf, np2);
     for (uint32_t j = t; j < K; j += LN_NT) {
         if (j < n) {
             uint32_t id = (uint32_t)(buf[j] & 0xffffffffull);
@@ -273,7 +273,7 @@ __global__ __launch_bounds__(TC_NT) void zs_k_btopk_chunks(const float* logits, 
         } else {
             for (uint32_t i = nsup + t; i < TC_SORT; i += TC_NT) s64[i] = ~0ull;
             __syncthreads();
-            block_bitonic_u64<TC_NT>(s64, TC_SORT);
+            block_sort_u64<TC_NT>(s64, TC_SORT);
             if ((uint32_t)t < n) out[t] = s64[t];
         }
         if (t == 0) cn[(size_t)r * nch + c] = n;

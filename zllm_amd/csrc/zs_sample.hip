@@ -121,7 +121,7 @@ __global__ __launch_bounds__(ZS_PREP_NT) void zs_k_prep(zs_sargs a) {
     while (np2 < n) np2 <<= 1;
     for (uint32_t i = n + threadIdx.x; i < np2; i += ZS_PREP_NT) ent[i] = ~0ull;
     __syncthreads();
-    if (np2 > 1) block_bitonic_u64<ZS_PREP_NT>(ent, (int)np2);
+    if (np2 > 1) block_sort_u64<ZS_PREP_NT>(ent, np2);
     // segment starts -> output slots
     uint32_t* out_id = a.p_id + (size_t)r * ZS_MAX_PATCHES;
     uint32_t* out_fl = a.p_flags + (size_t)r * ZS_MAX_PATCHES;
@@ -478,7 +478,7 @@ __device__ __forceinline__ void p1_topk_fast(const uint32_t (&kv)[P1_EPT], uint3
     } else {
         for (uint32_t i = nsup + t; i < P1_SORT; i += ZS_P1_NT) sh.s64[i] = ~0ull;
         __syncthreads();
-        block_bitonic_u64<ZS_P1_NT>(sh.s64, P1_SORT);
+        block_sort_reg_u64<ZS_P1_NT, P1_SORT / ZS_P1_NT>(sh.s64, P1_SORT);
         for (uint32_t i = t; i < K; i += ZS_P1_NT) {
             const unsigned long long v = sh.s64[i];
             out_key[i] = ~(uint32_t)(v >> 32);
