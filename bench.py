@@ -107,8 +107,7 @@ SPEC_K = 4
 # HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
 # (profiles/c5_traffic.md), scaled by the copy-kernel calibration there; None
 # where not measured
-TRAFFIC = {"zs_k_pass1": 167.0e6, "zs_k_pv": 64.1e6, "zs_k_tp_inc": 36.4e6, "zs_k_big": 0.5e6,
-           "zs_k_spec_stats": 1401.8e6, "zs_k_spec_sums": 1426.5e6}
+TRAFFIC = {"zs_k_pass1": 167.0e6, "zs_k_pv": 64.1e6, "zs_k_tp_inc": 36.4e6, "zs_k_big": 0.5e6}
 
 
 def spec_bytes_per_row(V, k):
@@ -237,30 +236,27 @@ def make_step(W, V):
     step(out=None, overlap=True) -> (sampler outputs, (accepted, next)).
 
     The draft verification is independent of this step's sampling: it runs on
-    a second stream (default priority) and fills the CUs that the sampler's
-    latency-bound row kernels leave idle; the step ends when both are done. It
-    starts once the sampler's bandwidth-bound passes over the logits are done
-    (zs_batch.pass_event), beside the latency-bound per-row kernels."""
+    a second stream (default priority) from the start of the step. It reads
+    its logits once (bandwidth-bound) and fills the CUs that the sampler's
+    latency-bound per-row kernels leave idle; the step ends when both are
+    done."""
     import torch
     from zllm_amd.engine import verify_drafts
     ctx, sampler, bufs, xs, bits = W["ctx"], W["sampler"], W["bufs"], W["xs"], W["bits"]
     stream = torch.cuda.current_stream()
     spec_stream = torch.cuda.Stream()
-    pass_ev = torch.cuda.Event()
-    pass_ev.record(stream)  # creates the event
 
     def step(out=None, overlap=True):
         if overlap:
             spec_stream.wait_stream(stream)
+            with torch.cuda.stream(spec_stream):
+                spec = verify_drafts(ctx, W["tgt"], W["draft_ids"], W["spec_T"], W["spec_seed"], W["spec_ctr"],
+                                     W["dft"])
+                W["spec_ctr"].add_(1)
         W["dfa"].mask(W["table"], W["st"], V, out=bits)
-        out = sampler.run(xs, bufs, bits, top_stride=5, out=out, pass_event=pass_ev if overlap else None)
+        out = sampler.run(xs, bufs, bits, top_stride=5, out=out)
         bufs["counter"].add_(1)
         if overlap:
-            with torch.cuda.stream(spec_stream):
-                spec_stream.wait_event(pass_ev)
-                spec = verify_drafts(ctx, W["tgt"], W["draft_ids"], W["spec_T"], W["spec_seed"], W["spec_ctr"],
-                                     W["dft"], background=True)
-                W["spec_ctr"].add_(1)
             stream.wait_stream(spec_stream)
         else:
             spec = verify_drafts(ctx, W["tgt"], W["draft_ids"], W["spec_T"], W["spec_seed"], W["spec_ctr"], W["dft"])
@@ -350,8 +346,7 @@ def main():
         "zs_k_pass1": float(sum(row_bytes)),
         "zs_k_big": float(sum(row_bytes[i] for i in big_rows)),
         "zs_k_pv": float(sum(4 * V + 4 * V for i in big_rows)),   # read logits, write p
-        "zs_k_spec_stats": float(B * 4 * V * (2 * SPEC_K + 1)),
-        "zs_k_spec_sums": float(B * 4 * V * (2 * SPEC_K + 1)),
+        "zs_k_spec_chunk": float(B * 4 * V * (2 * SPEC_K + 1)),
     }
     dom_bytes = per_kernel_bytes.get(dom, step_bytes)
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9

@@ -570,13 +570,16 @@ ZO_API float zo_philox_uniform(uint64_t seed, uint64_t counter, uint32_t tag) {
 /* -------------------------------------------------------------------------
  * Speculative-decode verification. temperature <= 0: verify_drafts
  * (spec_decode.rs:241-267). temperature > 0: rejection sampling
- * (Leviathan et al. 2023, Chen et al. 2023) as libzs defines it with
- * integer weights W_v = rint(2^24 * 2^t), t = (x_v - max x) * c, c = the f32
- * quotient log2(e) / T, evaluated as a fixed sequence of f32 operations
- * (zo_spec_w below; 0 for t < -25, where the formula rounds to 0); accept
- * draft d at step i iff U_i * Q_d * sum(P) <= P_d * sum(Q) * 2^32 (U_i the
+ * (Leviathan et al. 2023, Chen et al. 2023) as libzs defines it with integer
+ * weights computed chunk by chunk: ids in chunks of 8192, m_c the chunk's
+ * maximum of x (NaN ignored), M the row's, c = the f32 quotient log2(e) / T,
+ * W(t) = rint(2^24 * 2^t) as a fixed sequence of f32 operations (zo_spec_w
+ * below; 0 for t < -25, where the formula rounds to 0), and
+ *   P_v = W((x_v - m_c) c) * W((m_c - M) c)   (target; Q likewise, draft).
+ * With s = max(0, bitlen(sum P | sum Q) - 40), Ps = sum(P) >> s, Qs = sum(Q) >> s:
+ * accept draft d at step i iff U_i * Q_d * Ps <= P_d * Qs * 2^32 (U_i the
  * 32-bit Philox word, tag 1+i); at the first rejection draw from
- * max(0, P sum(Q) - Q sum(P)) (P if that is all zero) with tag 1+k+i; after k
+ * max(0, P_v Qs - Q_v Ps) (P if that is all zero) with tag 1+k+i; after k
  * acceptances draw from target row k with tag 1+2k. A draw returns the first
  * id whose inclusive prefix exceeds floor(U * total / 2^32). Rows with NaN /
  * +inf / all -inf logits are verified greedily; draft ids >= V are rejected.
@@ -593,13 +596,20 @@ static uint32_t zo_philox_u32(uint64_t seed, uint64_t counter, uint32_t tag) {
     return o[0];
 }
 
-/* row stats: max x (NaN ignored), degenerate flag (NaN, +inf, all -inf) */
-static int zo_spec_row_max(const float* x, uint32_t V, float* m) {
+#define ZO_SP_CH 8192u
+/* row stats: chunk maxima and the row maximum of x (NaN ignored); returns the
+ * degenerate flag (NaN, +inf, all -inf) */
+static int zo_spec_row_max(const float* x, uint32_t V, float* mc, float* m) {
     float mm = -INFINITY;
     int bad = 0;
-    for (uint32_t v = 0; v < V; v++) {
-        if (x[v] != x[v] || x[v] == INFINITY) bad = 1;
-        mm = rmax(mm, x[v]);
+    for (uint32_t c0 = 0; c0 < V; c0 += ZO_SP_CH) {
+        float cm = -INFINITY;
+        for (uint32_t v = c0; v < V && v < c0 + ZO_SP_CH; v++) {
+            if (x[v] != x[v] || x[v] == INFINITY) bad = 1;
+            cm = rmax(cm, x[v]);
+        }
+        mc[c0 / ZO_SP_CH] = cm;
+        mm = rmax(mm, cm);
     }
     if (mm == -INFINITY) bad = 1;
     *m = mm;
@@ -626,73 +636,106 @@ static uint64_t zo_spec_w(float x, float c, float m) {
     return (uint64_t)rintf(ldexpf(p, 24 + (int)n));
 }
 
+/* P_v = W((x_v - m_c) c) * W((m_c - M) c) */
+static uint64_t zo_spec_p(const float* x, uint32_t v, const float* mc, float M, float c) {
+    const float m = mc[v / ZO_SP_CH];
+    return zo_spec_w(x[v], c, m) * zo_spec_w(m, c, M);
+}
+/* sum of P over the row, chunk by chunk: sum_c W((m_c - M) c) * sum_{v in c} W((x_v - m_c) c) */
+static zo_u128 zo_spec_sum(const float* x, uint32_t V, const float* mc, float M, float c) {
+    zo_u128 s = 0;
+    for (uint32_t c0 = 0; c0 < V; c0 += ZO_SP_CH) {
+        const float m = mc[c0 / ZO_SP_CH];
+        uint64_t sc = 0;
+        for (uint32_t v = c0; v < V && v < c0 + ZO_SP_CH; v++) sc += zo_spec_w(x[v], c, m);
+        s += (zo_u128)(zo_spec_w(m, c, M) * sc);
+    }
+    return s;
+}
+static int zo_bitlen128(zo_u128 v) {
+    int n = 0;
+    while (v) { n++; v >>= 1; }
+    return n;
+}
+
 ZO_API uint32_t zo_spec_verify(const float* target, const float* draft, const uint32_t* drafts, uint32_t k,
                                uint32_t V, float T, uint64_t seed, uint64_t counter, uint32_t* next) {
     int greedy = !(T > 0.0f) || draft == 0;
+    const uint32_t nch = (V + ZO_SP_CH - 1) / ZO_SP_CH;
     float mt[64], md[64];
-    uint64_t st[64], sd[64];
+    float* mct = (float*)malloc(sizeof(float) * (size_t)(k + 1) * nch);
+    float* mcd = (float*)malloc(sizeof(float) * (size_t)(k + 1) * nch);
     if (!greedy) {
         for (uint32_t p = 0; p <= k && !greedy; p++)
-            if (zo_spec_row_max(target + (size_t)p * V, V, &mt[p])) greedy = 1;
+            if (zo_spec_row_max(target + (size_t)p * V, V, mct + (size_t)p * nch, &mt[p])) greedy = 1;
         for (uint32_t p = 0; p < k && !greedy; p++)
-            if (zo_spec_row_max(draft + (size_t)p * V, V, &md[p])) greedy = 1;
+            if (zo_spec_row_max(draft + (size_t)p * V, V, mcd + (size_t)p * nch, &md[p])) greedy = 1;
     }
-    if (greedy) return zo_verify_drafts(drafts, k, target, k + 1, V, next);
+    if (greedy) {
+        free(mct);
+        free(mcd);
+        return zo_verify_drafts(drafts, k, target, k + 1, V, next);
+    }
     const float c = 1.44269502f / T;
-    for (uint32_t p = 0; p <= k; p++) {
-        uint64_t s = 0;
-        for (uint32_t v = 0; v < V; v++) s += zo_spec_w(target[(size_t)p * V + v], c, mt[p]);
-        st[p] = s;
-    }
-    for (uint32_t p = 0; p < k; p++) {
-        uint64_t s = 0;
-        for (uint32_t v = 0; v < V; v++) s += zo_spec_w(draft[(size_t)p * V + v], c, md[p]);
-        sd[p] = s;
-    }
     uint32_t i = 0;
+    zo_u128 sp = 0, sq = 0;
+    uint64_t Ps = 0, Qs = 0;
     for (; i < k; i++) {
-        uint32_t d = drafts[i];
+        const float* trow = target + (size_t)i * V;
+        const float* drow = draft + (size_t)i * V;
+        sp = zo_spec_sum(trow, V, mct + (size_t)i * nch, mt[i], c);
+        sq = zo_spec_sum(drow, V, mcd + (size_t)i * nch, md[i], c);
+        int sh = zo_bitlen128(sp | sq) - 40;
+        if (sh < 0) sh = 0;
+        Ps = (uint64_t)(sp >> sh);
+        Qs = (uint64_t)(sq >> sh);
+        const uint32_t d = drafts[i];
         if (d >= V) break;
-        uint64_t P = zo_spec_w(target[(size_t)i * V + d], c, mt[i]);
-        uint64_t Q = zo_spec_w(draft[(size_t)i * V + d], c, md[i]);
-        uint32_t U = zo_philox_u32(seed, counter, 1u + i);
-        zo_u128 lhs = (zo_u128)U * Q * st[i];
-        zo_u128 rhs = ((zo_u128)P * sd[i]) << 32;
+        const uint64_t P = zo_spec_p(trow, d, mct + (size_t)i * nch, mt[i], c);
+        const uint64_t Q = zo_spec_p(drow, d, mcd + (size_t)i * nch, md[i], c);
+        const uint32_t U = zo_philox_u32(seed, counter, 1u + i);
+        const zo_u128 lhs = ((zo_u128)U * Q) * Ps; /* < 2^122 */
+        const zo_u128 rhs = ((zo_u128)P * Qs) << 32;
         if (!(lhs <= rhs)) break;
     }
     /* weights of the final draw */
     const uint32_t pos = i < k ? i : k;
     const float* trow = target + (size_t)pos * V;
     const float* drow = i < k ? draft + (size_t)i * V : 0;
+    const float* tmc = mct + (size_t)pos * nch;
+    const float* dmc = i < k ? mcd + (size_t)i * nch : 0;
     int residual = i < k;
     zo_u128 total = 0;
     uint32_t word;
     if (residual) {
         for (uint32_t v = 0; v < V; v++) {
-            zo_u128 pp = (zo_u128)zo_spec_w(trow[v], c, mt[i]) * sd[i];
-            zo_u128 qq = (zo_u128)zo_spec_w(drow[v], c, md[i]) * st[i];
+            const zo_u128 pp = (zo_u128)zo_spec_p(trow, v, tmc, mt[i], c) * Qs;
+            const zo_u128 qq = (zo_u128)zo_spec_p(drow, v, dmc, md[i], c) * Ps;
             total += pp > qq ? pp - qq : 0;
         }
         word = zo_philox_u32(seed, counter, 1u + k + i);
-        if (total == 0) { residual = 0; total = st[i]; }
+        if (total == 0) { residual = 0; total = sp; }
     } else {
-        total = st[k];
+        total = zo_spec_sum(trow, V, tmc, mt[k], c);
         word = zo_philox_u32(seed, counter, 1u + 2 * k);
     }
-    const zo_u128 thr = ((zo_u128)word * total) >> 32;
+    /* floor(word * total / 2^32), total < 2^108 */
+    const zo_u128 thr = (((zo_u128)word * (uint64_t)(total >> 64)) << 32) + (((zo_u128)word * (uint64_t)total) >> 32);
     zo_u128 run = 0;
     *next = V - 1;
     for (uint32_t v = 0; v < V; v++) {
         zo_u128 w;
         if (residual) {
-            zo_u128 pp = (zo_u128)zo_spec_w(trow[v], c, mt[i]) * sd[i];
-            zo_u128 qq = (zo_u128)zo_spec_w(drow[v], c, md[i]) * st[i];
+            const zo_u128 pp = (zo_u128)zo_spec_p(trow, v, tmc, mt[i], c) * Qs;
+            const zo_u128 qq = (zo_u128)zo_spec_p(drow, v, dmc, md[i], c) * Ps;
             w = pp > qq ? pp - qq : 0;
         } else {
-            w = zo_spec_w(trow[v], c, mt[pos]);
+            w = zo_spec_p(trow, v, tmc, mt[pos], c);
         }
         run += w;
         if (w > 0 && run > thr) { *next = v; break; }
     }
+    free(mct);
+    free(mcd);
     return i;
 }

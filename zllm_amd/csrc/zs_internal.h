@@ -145,13 +145,14 @@ struct zs_spec_chunk {
     uint32_t flags;
     float amax_val;
     uint32_t amax_idx;
-    unsigned long long wsum;
+    unsigned long long wsum;      // sum of the weights relative to the chunk maximum
     unsigned long long rlo, rhi;  // residual weight sum (position slot 0 of a row)
 };
 struct zs_spec_row {
     uint32_t mode, pos, residual, word;
-    float m_t, m_d;
-    unsigned long long sum_t, sum_d;
+    float m_t, m_d;                     // row maxima of the draw's target / draft positions
+    unsigned long long ps, qs;          // their weight sums shifted to 40 bits (residual draw)
+    unsigned long long sum_lo, sum_hi;  // the target's weight sum (draw from P)
 };
 
 struct zs_spec_args {

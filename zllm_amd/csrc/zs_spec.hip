@@ -84,8 +84,10 @@ __device__ __forceinline__ uint32_t sp_id(uint32_t base, int e) {
     return base + ((e >> 2) * SP_NT + threadIdx.x) * 4 + (e & 3);
 }
 
-// pass 1: per chunk max of z, flags, first-max argmax of x
-__global__ __launch_bounds__(SP_NT) void zs_k_spec_stats(zs_spec_args a) {
+// One pass per chunk: the chunk maximum, flags, the first strict maximum of x
+// (greedy verification) and, once the chunk maximum is known, the chunk sum of
+// the weights w_v = W((x_v - m_c) c).
+__global__ __launch_bounds__(SP_NT) void zs_k_spec_chunk(zs_spec_args a) {
     const uint32_t c = blockIdx.x, pos = blockIdx.y, r = blockIdx.z;
     const uint32_t npos = a.draft ? 2 * a.k + 1 : a.k + 1;
     if (pos >= npos) return;
@@ -93,7 +95,7 @@ __global__ __launch_bounds__(SP_NT) void zs_k_spec_stats(zs_spec_args a) {
     if (base >= a.V) return;
     __shared__ float fsh[SP_NT / 64];
     __shared__ uint32_t ush[SP_NT / 64];
-    __shared__ unsigned long long gsh[SP_NT / 64];
+    __shared__ unsigned long long gsh[SP_NT / 64], wsh[SP_NT / 64];
     float x[SP_EPT];
     sp_load(sp_row(a, r, pos), base, a.V, x);
     // first strict maximum (init -inf, NaN never wins) in index order: the
@@ -118,57 +120,36 @@ __global__ __launch_bounds__(SP_NT) void zs_k_spec_stats(zs_spec_args a) {
         unsigned long long o = __shfl_xor(best, d, 64);
         best = o > best ? o : best;
     }
-    if (zs_lane() == 0) gsh[zs_wid()] = best;
+    // chunk sum of the weights relative to the chunk maximum (at most 32
+    // weights below 2^25 each per thread)
+    const float T = a.temperature[r];
+    unsigned long long wsum = 0;
+    if (T > 0.0f && a.draft && xmax > -INFINITY && xmax < INFINITY) {
+        const float cT = sp_c(T);
+        uint32_t s32 = 0;
+#pragma unroll
+        for (int e = 0; e < SP_EPT; e++) s32 += sp_weight(x[e], xmax, cT);
+        wsum = s32;
+        for (int d = 32; d > 0; d >>= 1) wsum += __shfl_xor(wsum, d, 64);
+    }
+    if (zs_lane() == 0) { gsh[zs_wid()] = best; wsh[zs_wid()] = wsum; }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int i = 0; i < SP_NT / 64; i++) best = gsh[i] > best ? gsh[i] : best;
+        unsigned long long ws = 0;
+        for (int i = 0; i < SP_NT / 64; i++) { best = gsh[i] > best ? gsh[i] : best; ws += wsh[i]; }
         zs_spec_chunk& o = a.cst[((size_t)r * a.npos_max + pos) * a.nch + c];
         o.xmax = xmax;
         o.flags = fl;
         o.amax_val = best ? zs_key_to_float((uint32_t)(best >> 32)) : -INFINITY;
         o.amax_idx = best ? 0xffffffffu - (uint32_t)(best & 0xffffffffull) : 0xffffffffu;
+        o.wsum = ws;
     }
 }
 
-// pass 2: chunk sums of the integer weights
-__global__ __launch_bounds__(SP_NT) void zs_k_spec_sums(zs_spec_args a) {
-    const uint32_t c = blockIdx.x, pos = blockIdx.y, r = blockIdx.z;
-    const uint32_t npos = a.draft ? 2 * a.k + 1 : a.k + 1;
-    if (pos >= npos) return;
-    const uint32_t base = c * SP_CH;
-    if (base >= a.V) return;
-    const float T = a.temperature[r];
-    if (!(T > 0.0f) || !a.draft) return;  // greedy verification needs no weights
-    __shared__ unsigned long long sh[SP_NT / 64];
-    const uint32_t nch = (a.V + SP_CH - 1) / SP_CH;
-    const zs_spec_chunk* cs = a.cst + ((size_t)r * a.npos_max + pos) * a.nch;
-    float m = -INFINITY;
-    for (uint32_t i = 0; i < nch; i++) m = fmaxf(m, cs[i].xmax);
-    const float cT = sp_c(T);
-    uint32_t s32 = 0;  // at most 32 weights below 2^25 each
-    if (m > -INFINITY && m < INFINITY && sp_live(cs[c].xmax, m, cT)) {
-        float x[SP_EPT];
-        sp_load(sp_row(a, r, pos), base, a.V, x);
-#pragma unroll
-        for (int e = 0; e < SP_EPT; e++) s32 += sp_weight(x[e], m, cT);
-    }
-    unsigned long long s = s32;
-    for (int d = 32; d > 0; d >>= 1) s += __shfl_xor(s, d, 64);
-    if (zs_lane() == 0) sh[zs_wid()] = s;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        unsigned long long t = 0;
-        for (int i = 0; i < SP_NT / 64; i++) t += sh[i];
-        a.cst[((size_t)r * a.npos_max + pos) * a.nch + c].wsum = t;
-    }
-}
-
-// passes 1 + 2 fused: one workgroup per (row, position) walks the row's chunks
-// twice -- the chunk statistics, then (with the row maximum known) the chunk
-// weight sums. One workgroup per CU (its LDS request keeps a second one out):
-// the rows in flight then fit the memory-side cache, and the second walk of a
-// row reads it from there instead of HBM. Writes the same zs_spec_chunk
-// fields as zs_k_spec_stats / zs_k_spec_sums.
+// The same per (row, position) by one workgroup walking the row's chunks once,
+// two at a time. One workgroup per CU (its LDS request keeps a second one out):
+// the verification then leaves most of each CU to the sampler's kernels when
+// the two run side by side.
 #define SR_NT 1024
 #define SR_NW (SR_NT / 64)
 #define SR_EPT (SP_CH / SR_NT)  // 8 elements per thread, as 2 float4
@@ -197,12 +178,15 @@ __global__ __launch_bounds__(SR_NT) void zs_k_spec_row(zs_spec_args a) {
     const uint32_t pos = blockIdx.x, r = blockIdx.y;
     const uint32_t V = a.V;
     const uint32_t nch = (V + SP_CH - 1) / SP_CH;
-    __shared__ float wz[ZS_MAX_CHUNKS][SR_NW];
+    __shared__ float wz[SR_PAIR][SR_NW];
     __shared__ uint32_t wf[ZS_MAX_CHUNKS][SR_NW];
     __shared__ unsigned long long wb[ZS_MAX_CHUNKS][SR_NW];
+    __shared__ unsigned long long ws[ZS_MAX_CHUNKS][SR_NW];
     __shared__ float cz[ZS_MAX_CHUNKS];
     if (threadIdx.x == 0) hold[0] = 0;  // the request is used, so it is kept
     const float T = a.temperature[r];
+    const bool weights = T > 0.0f && a.draft;
+    const float cT = weights ? sp_c(T) : 1.0f;
     const float* row = sp_row(a, r, pos);
     const int lane = zs_lane(), wid = zs_wid();
     zs_spec_chunk* cs = a.cst + ((size_t)r * a.npos_max + pos) * a.nch;
@@ -224,76 +208,78 @@ __global__ __launch_bounds__(SR_NT) void zs_k_spec_row(zs_spec_args a) {
                 nan |= xv != xv;
                 if (xv > bv) { bv = xv; be = e; }
             }
-            float xmax = bv;
             uint32_t fl = nan ? 1u : 0u;
             unsigned long long best = be < 0 ? 0ull
                 : ((unsigned long long)zs_total_key(bv == 0.0f ? 0.0f : bv) << 32) | (0xffffffffu - sr_id(base, be));
-            xmax = wave_max_f(xmax);
+            const float xmax = wave_max_f(bv);
             fl = wave_or_u(fl);
             for (int d = 32; d > 0; d >>= 1) {
                 unsigned long long o = __shfl_xor(best, d, 64);
                 best = o > best ? o : best;
             }
-            if (lane == 0) { wz[c][wid] = xmax; wf[c][wid] = fl; wb[c][wid] = best; }
+            if (lane == 0) { wz[h][wid] = xmax; wf[c][wid] = fl; wb[c][wid] = best; }
         }
-    }
-    __syncthreads();
-    if (threadIdx.x < nch) {
-        const uint32_t c = threadIdx.x;
-        float xmax = -INFINITY;
-        uint32_t fl = 0;
-        unsigned long long best = 0;
-        for (int w = 0; w < SR_NW; w++) {
-            xmax = fmaxf(xmax, wz[c][w]);
-            fl |= wf[c][w];
-            best = wb[c][w] > best ? wb[c][w] : best;
-        }
-        if (xmax == INFINITY) fl |= 2u;
-        cz[c] = xmax;
-        zs_spec_chunk& o = cs[c];
-        o.xmax = xmax;
-        o.flags = fl;
-        o.amax_val = best ? zs_key_to_float((uint32_t)(best >> 32)) : -INFINITY;
-        o.amax_idx = best ? 0xffffffffu - (uint32_t)(best & 0xffffffffull) : 0xffffffffu;
-    }
-    if (!(T > 0.0f) || !a.draft) return;  // greedy verification needs no weights
-    __syncthreads();
-    float m = -INFINITY;
-    for (uint32_t c = 0; c < nch; c++) m = fmaxf(m, cz[c]);
-    const bool fin = m > -INFINITY && m < INFINITY;
-    const float cT = sp_c(T);
-    for (uint32_t c0 = 0; c0 < nch; c0 += SR_PAIR) {
-        float x[SR_PAIR][SR_EPT];
-#pragma unroll
-        for (int h = 0; h < SR_PAIR; h++) {
-            const uint32_t c = c0 + h;
-            if (fin && c < nch && sp_live(cz[c], m, cT)) sr_load(row, c * SP_CH, V, x[h]);
-            else
-#pragma unroll
-                for (int e = 0; e < SR_EPT; e++) x[h][e] = -INFINITY;
-        }
+        __syncthreads();
+        // chunk maxima, then the chunk weight sums from the registers
 #pragma unroll
         for (int h = 0; h < SR_PAIR; h++) {
             const uint32_t c = c0 + h;
             if (c >= nch) break;
-            uint32_t s32 = 0;  // at most 8 weights below 2^25 each
+            float m = -INFINITY;
+            for (int w = 0; w < SR_NW; w++) m = fmaxf(m, wz[h][w]);
+            if (threadIdx.x == 0) cz[c] = m;
+            unsigned long long s = 0;
+            if (weights && m > -INFINITY && m < INFINITY) {
+                uint32_t s32 = 0;  // at most 8 weights below 2^25 each
 #pragma unroll
-            for (int e = 0; e < SR_EPT; e++)
-                s32 += sp_weight(x[h][e], m, cT);
-            unsigned long long s = s32;
-            for (int d = 32; d > 0; d >>= 1) s += __shfl_xor(s, d, 64);
-            if (lane == 0) wb[c][wid] = s;
+                for (int e = 0; e < SR_EPT; e++) s32 += sp_weight(x[h][e], m, cT);
+                s = s32;
+                for (int d = 32; d > 0; d >>= 1) s += __shfl_xor(s, d, 64);
+            }
+            if (lane == 0) ws[c][wid] = s;
         }
+        __syncthreads();
     }
-    __syncthreads();
     if (threadIdx.x < nch) {
-        unsigned long long t = 0;
-        for (int w = 0; w < SR_NW; w++) t += wb[threadIdx.x][w];
-        cs[threadIdx.x].wsum = t;
+        const uint32_t c = threadIdx.x;
+        uint32_t fl = 0;
+        unsigned long long best = 0, s = 0;
+        for (int w = 0; w < SR_NW; w++) {
+            fl |= wf[c][w];
+            best = wb[c][w] > best ? wb[c][w] : best;
+            s += ws[c][w];
+        }
+        if (cz[c] == INFINITY) fl |= 2u;
+        zs_spec_chunk& o = cs[c];
+        o.xmax = cz[c];
+        o.flags = fl;
+        o.amax_val = best ? zs_key_to_float((uint32_t)(best >> 32)) : -INFINITY;
+        o.amax_idx = best ? 0xffffffffu - (uint32_t)(best & 0xffffffffull) : 0xffffffffu;
+        o.wsum = s;
     }
 }
 
-// pass 3: one wave per row -- accept / reject decisions (lanes over chunks)
+// bit length of a u128
+__device__ __forceinline__ int sp_bitlen(u128 v) {
+    const unsigned long long hi = (unsigned long long)(v >> 64), lo = (unsigned long long)v;
+    return hi ? 128 - __clzll((long long)hi) : (lo ? 64 - __clzll((long long)lo) : 0);
+}
+// sum of a row's weights, sum_c F_c * S_c, by one wave (lanes over chunks);
+// every lane gets it
+__device__ __forceinline__ u128 sp_row_sum(const zs_spec_chunk* cs, uint32_t nch, float M, float cT) {
+    u128 s = 0;
+    for (uint32_t c = (uint32_t)zs_lane(); c < nch; c += 64)
+        s += (u128)((unsigned long long)sp_weight(cs[c].xmax, M, cT) * cs[c].wsum);
+    for (int d = 32; d > 0; d >>= 1) {
+        const unsigned long long lo = __shfl_xor((unsigned long long)s, d, 64);
+        const unsigned long long hi = __shfl_xor((unsigned long long)(s >> 64), d, 64);
+        s += ((u128)hi << 64) | lo;
+    }
+    return s;
+}
+
+// pass 2: one wave per row -- accept / reject decisions (lanes over chunks)
+// and the sums of the final draw
 __global__ __launch_bounds__(64) void zs_k_spec_decide(zs_spec_args a) {
     const uint32_t r = blockIdx.x;
     const int lane = zs_lane();
@@ -303,21 +289,21 @@ __global__ __launch_bounds__(64) void zs_k_spec_decide(zs_spec_args a) {
     const float T = a.temperature[r];
     zs_spec_row out;
     out.m_t = out.m_d = 0.f;
-    out.sum_t = out.sum_d = 0;
+    out.ps = out.qs = 0;
+    out.sum_lo = out.sum_hi = 0;
     bool degenerate = !(T > 0.0f) || !a.draft;
     float mpos[2 * ZS_SPEC_KMAX + 1];
-    unsigned long long spos[2 * ZS_SPEC_KMAX + 1];
     uint32_t apos[ZS_SPEC_KMAX + 1];
+    auto cst = [&](uint32_t p) { return a.cst + ((size_t)r * a.npos_max + p) * a.nch; };
     for (uint32_t p = 0; p < npos; p++) {
-        const zs_spec_chunk* cs = a.cst + ((size_t)r * a.npos_max + p) * a.nch;
+        const zs_spec_chunk* cs = cst(p);
         float m = -INFINITY;
         uint32_t fl = 0;
-        unsigned long long s = 0, best = 0;  // (value key, ~id) of the first maximum
+        unsigned long long best = 0;  // (value key, ~id) of the first maximum
         for (uint32_t c = lane; c < nch; c += 64) {
             const zs_spec_chunk q = cs[c];
             m = fmaxf(m, q.xmax);
             fl |= q.flags;
-            if (!degenerate) s += q.wsum;
             if (q.amax_idx != 0xffffffffu) {
                 const unsigned long long key = ((unsigned long long)zs_total_key(q.amax_val) << 32) | (0xffffffffu - q.amax_idx);
                 best = key > best ? key : best;
@@ -326,18 +312,16 @@ __global__ __launch_bounds__(64) void zs_k_spec_decide(zs_spec_args a) {
         m = wave_max_f(m);
         fl = wave_or_u(fl);
         for (int d = 32; d > 0; d >>= 1) {
-            s += __shfl_xor(s, d, 64);
             unsigned long long o = __shfl_xor(best, d, 64);
             best = o > best ? o : best;
         }
         if (fl || m == -INFINITY) degenerate = true;
         if (p <= k) apos[p] = best ? 0xffffffffu - (uint32_t)(best & 0xffffffffull) : 0u;
         mpos[p] = m;
-        spos[p] = s;
     }
-    if (lane != 0) return;
     const uint32_t* drafts = a.draft_ids + (size_t)r * k;
     if (degenerate) {
+        if (lane != 0) return;
         uint32_t acc = 0, bonus = apos[k];
         for (uint32_t i = 0; i < k; i++) {
             if (apos[i] == drafts[i]) acc++;
@@ -350,33 +334,48 @@ __global__ __launch_bounds__(64) void zs_k_spec_decide(zs_spec_args a) {
         return;
     }
     const float cT = sp_c(T);
+    // P_d = w_d * F_c of the chunk holding d
+    auto weight_at = [&](uint32_t p, uint32_t d) -> unsigned long long {
+        const float mc = cst(p)[d / SP_CH].xmax;
+        return (unsigned long long)sp_weight(sp_row(a, r, p)[d], mc, cT) * sp_weight(mc, mpos[p], cT);
+    };
     uint32_t i = 0;
+    u128 sp = 0, sq = 0;
+    int sh = 0;
     for (; i < k; i++) {
-        uint32_t d = drafts[i];
+        sp = sp_row_sum(cst(i), nch, mpos[i], cT);
+        sq = sp_row_sum(cst(k + 1 + i), nch, mpos[k + 1 + i], cT);
+        sh = max(0, sp_bitlen(sp | sq) - 40);
+        const uint32_t d = drafts[i];
         if (d >= V) break;
-        uint64_t P = sp_weight(sp_row(a, r, i)[d], mpos[i], cT);
-        uint64_t Q = sp_weight(sp_row(a, r, k + 1 + i)[d], mpos[k + 1 + i], cT);
-        uint32_t U = zs_philox_u32(a.seed[r], a.counter[r], 1u + i);
-        u128 lhs = (u128)U * Q * spos[i];
-        u128 rhs = ((u128)P * spos[k + 1 + i]) << 32;
+        const unsigned long long Ps = (unsigned long long)(sp >> sh), Qs = (unsigned long long)(sq >> sh);
+        const unsigned long long P = weight_at(i, d), Q = weight_at(k + 1 + i, d);
+        const uint32_t U = zs_philox_u32(a.seed[r], a.counter[r], 1u + i);
+        const u128 lhs = ((u128)U * Q) * Ps;  // < 2^122
+        const u128 rhs = ((u128)P * Qs) << 32;                      // < 2^122
         if (!(lhs <= rhs)) break;
     }
-    a.accepted[r] = i;
     out.mode = 1;
     out.pos = i;
     if (i == k) {
+        const u128 st = sp_row_sum(cst(k), nch, mpos[k], cT);
         out.residual = 0;
         out.m_t = mpos[k];
-        out.sum_t = spos[k];
+        out.sum_lo = (unsigned long long)st;
+        out.sum_hi = (unsigned long long)(st >> 64);
         out.word = zs_philox_u32(a.seed[r], a.counter[r], 1u + 2 * k);
     } else {
         out.residual = 1;
         out.m_t = mpos[i];
         out.m_d = mpos[k + 1 + i];
-        out.sum_t = spos[i];
-        out.sum_d = spos[k + 1 + i];
+        out.ps = (unsigned long long)(sp >> sh);
+        out.qs = (unsigned long long)(sq >> sh);
+        out.sum_lo = (unsigned long long)sp;  // the target's sum: the draw when R is all 0
+        out.sum_hi = (unsigned long long)(sp >> 64);
         out.word = zs_philox_u32(a.seed[r], a.counter[r], 1u + k + i);
     }
+    if (lane != 0) return;
+    a.accepted[r] = i;
     a.rs[r] = out;
 }
 
@@ -397,17 +396,36 @@ __device__ __forceinline__ u128 shfl_xor_u128(u128 v, int d) {
     return u128_of(p);
 }
 
-// Draw weight of id v (given its target / draft logits): P, or the residual
-// max(0, P sum(Q) - Q sum(P)).
-__device__ __forceinline__ u128 spd_weight2(const zs_spec_row& s, float cT, float xt, float xd) {
-    uint64_t P = sp_weight(xt, s.m_t, cT);
+// Draw weight of id v (given its target / draft logits and its chunk's maxima
+// and scales): P, or the residual max(0, P Qs - Q Ps) (below 2^90).
+struct sp_chunk_w {
+    float mt, md;
+    unsigned long long ft, fd;
+};
+// tpos: the target position the draw's P comes from (pos after a rejection,
+// k after k acceptances)
+__device__ __forceinline__ sp_chunk_w sp_chunk_scales(const zs_spec_args& a, uint32_t r, const zs_spec_row& s, uint32_t c,
+                                                      float cT, uint32_t tpos) {
+    sp_chunk_w w;
+    w.mt = a.cst[((size_t)r * a.npos_max + tpos) * a.nch + c].xmax;
+    w.ft = sp_weight(w.mt, s.m_t, cT);
+    w.md = 0.0f;
+    w.fd = 0;
+    if (s.residual) {
+        w.md = a.cst[((size_t)r * a.npos_max + a.k + 1 + s.pos) * a.nch + c].xmax;
+        w.fd = sp_weight(w.md, s.m_d, cT);
+    }
+    return w;
+}
+__device__ __forceinline__ u128 spd_weight2(const zs_spec_row& s, const sp_chunk_w& cw, float cT, float xt, float xd) {
+    const unsigned long long P = (unsigned long long)sp_weight(xt, cw.mt, cT) * cw.ft;
     if (!s.residual) return P;
-    uint64_t Q = sp_weight(xd, s.m_d, cT);
-    u128 pp = (u128)P * s.sum_d, qq = (u128)Q * s.sum_t;
+    const unsigned long long Q = (unsigned long long)sp_weight(xd, cw.md, cT) * cw.fd;
+    const u128 pp = (u128)P * s.qs, qq = (u128)Q * s.ps;
     return pp > qq ? pp - qq : 0;
 }
 
-// pass 4: chunk sums of the residual weights (rows that rejected a draft)
+// pass 3: chunk sums of the residual weights (rows that rejected a draft)
 __global__ __launch_bounds__(SP_NT) void zs_k_spec_rsum(zs_spec_args a) {
     const uint32_t c = blockIdx.x, r = blockIdx.y;
     const uint32_t base = c * SP_CH;
@@ -416,13 +434,14 @@ __global__ __launch_bounds__(SP_NT) void zs_k_spec_rsum(zs_spec_args a) {
     if (s.mode != 1 || !s.residual) return;
     __shared__ unsigned long long lo[SP_NT / 64], hi[SP_NT / 64];
     const float cT = sp_c(a.temperature[r]);
+    const sp_chunk_w cw = sp_chunk_scales(a, r, s, c, cT, s.pos);
     float xt[SP_EPT], xd[SP_EPT];
     sp_load(sp_row(a, r, s.pos), base, a.V, xt);
     sp_load(sp_row(a, r, a.k + 1 + s.pos), base, a.V, xd);
     u128 acc = 0;
 #pragma unroll
     for (int e = 0; e < SP_EPT; e++)
-        acc += spd_weight2(s, cT, xt[e], xd[e]);
+        acc += spd_weight2(s, cw, cT, xt[e], xd[e]);
     for (int d = 32; d > 0; d >>= 1) acc += shfl_xor_u128(acc, d);
     if (zs_lane() == 0) { lo[zs_wid()] = (unsigned long long)acc; hi[zs_wid()] = (unsigned long long)(acc >> 64); }
     __syncthreads();
@@ -435,7 +454,7 @@ __global__ __launch_bounds__(SP_NT) void zs_k_spec_rsum(zs_spec_args a) {
     }
 }
 
-// pass 5: one workgroup per row -- the replacement / bonus draw: the chunk
+// pass 4: one workgroup per row -- the replacement / bonus draw: the chunk
 // holding the target from the chunk sums, then the first id of that chunk whose
 // inclusive prefix exceeds the target
 __global__ __launch_bounds__(SP_BIG_NT) void zs_k_spec_draw(zs_spec_args a) {
@@ -459,11 +478,15 @@ __global__ __launch_bounds__(SP_BIG_NT) void zs_k_spec_draw(zs_spec_args a) {
             for (uint32_t c = t; c < nch; c += 64) rt += ((u128)c0[c].rhi << 64) | c0[c].rlo;
         for (int d = 32; d > 0; d >>= 1) rt += shfl_xor_u128(rt, d);
         const bool resid = s.residual && rt != 0;
-        const u128 total = resid ? rt : (u128)s.sum_t;
-        const u128 target = ((u128)s.word * total) >> 32;
+        const u128 total = resid ? rt : (((u128)s.sum_hi << 64) | s.sum_lo);
+        // floor(word * total / 2^32) without overflow: total < 2^108
+        const u128 target = (((u128)s.word * (unsigned long long)(total >> 64)) << 32) +
+                            (((u128)s.word * (unsigned long long)total) >> 32);
         // chunk prefix over the lanes (nch <= 64 for the vocab limit)
         u128 w = 0;
-        if ((uint32_t)t < nch) w = resid ? (((u128)c0[t].rhi << 64) | c0[t].rlo) : (u128)cp[t].wsum;
+        if ((uint32_t)t < nch)
+            w = resid ? (((u128)c0[t].rhi << 64) | c0[t].rlo)
+                      : (u128)((unsigned long long)sp_weight(cp[t].xmax, s.m_t, cT) * cp[t].wsum);
         u128 inc = w;
         for (int d = 1; d < 64; d <<= 1) {
             u128 y = shfl_up_u128(inc, d);
@@ -488,9 +511,11 @@ __global__ __launch_bounds__(SP_BIG_NT) void zs_k_spec_draw(zs_spec_args a) {
         if (t == 0) a.next[r] = V - 1;
         return;
     }
+    const uint32_t tpos = s.residual ? s.pos : a.k;
     if (!rzero) s.residual = 0;
     const u128 rem = ((u128)chi << 64) | clo;  // target minus the weight of the chunks before
     const uint32_t base = c * SP_CH;
+    const sp_chunk_w cw = sp_chunk_scales(a, r, s, c, cT, tpos);
     // 8192 ids, 8 per thread in two float4 of each row
     const float* rt = sp_row(a, r, s.pos);
     const float* rd = s.residual ? sp_row(a, r, a.k + 1 + s.pos) : rt;
@@ -506,7 +531,7 @@ __global__ __launch_bounds__(SP_BIG_NT) void zs_k_spec_draw(zs_spec_args a) {
         const float xt[4] = {vt.x, vt.y, vt.z, vt.w}, xd[4] = {vd.x, vd.y, vd.z, vd.w};
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-            w[4 * h + q] = id + q < V ? spd_weight2(s, cT, xt[q], xd[q]) : 0;
+            w[4 * h + q] = id + q < V ? spd_weight2(s, cw, cT, xt[q], xd[q]) : 0;
         }
     }
     // inclusive prefix in id order: ids of thread t are base + 4t..4t+3 (h=0)
@@ -560,10 +585,8 @@ extern "C" int zs_spec_launch(const zs_spec_args& a, const zs_prof& prof, hipStr
         hipLaunchKernelGGL(zs_k_spec_row, dim3(npos, a.B), dim3(SR_NT), SR_LDS_HOLD, stream, a);
         mark("zs_k_spec_row");
     } else {
-    hipLaunchKernelGGL(zs_k_spec_stats, grid, dim3(SP_NT), 0, stream, a);
-    mark("zs_k_spec_stats");
-    hipLaunchKernelGGL(zs_k_spec_sums, grid, dim3(SP_NT), 0, stream, a);
-    mark("zs_k_spec_sums");
+    hipLaunchKernelGGL(zs_k_spec_chunk, grid, dim3(SP_NT), 0, stream, a);
+    mark("zs_k_spec_chunk");
     }
     hipLaunchKernelGGL(zs_k_spec_decide, dim3(a.B), dim3(64), 0, stream, a);
     hipLaunchKernelGGL(zs_k_spec_rsum, dim3(nch, a.B), dim3(SP_NT), 0, stream, a);
