@@ -575,16 +575,7 @@ struct p1_lds_arr {
     __device__ __forceinline__ uint32_t& operator[](int e) const { return p[e * ZS_P1_NT]; }
 };
 
-#ifdef ZS_DEBUG_P1
-__device__ unsigned long long zs_dbg_p1[10];
-#define P1_MARK(k) do { if (threadIdx.x == 0) { const long long c1_ = clock64(); atomicAdd(&zs_dbg_p1[k], (unsigned long long)(c1_ - p1c0)); p1c0 = c1_; } } while (0)
-#else
-#define P1_MARK(k) do {} while (0)
-#endif
 __global__ __launch_bounds__(ZS_P1_NT) __attribute__((amdgpu_waves_per_eu(3))) void zs_k_pass1(zs_sargs a) {
-#ifdef ZS_DEBUG_P1
-    long long p1c0 = clock64();
-#endif
     const uint32_t c = blockIdx.x, r = blockIdx.y;
     const zs_batch& b = a.b;
     const uint32_t V = b.V;
@@ -637,7 +628,6 @@ __global__ __launch_bounds__(ZS_P1_NT) __attribute__((amdgpu_waves_per_eu(3))) v
         }
     }
     __syncthreads();
-    P1_MARK(1);
     // patches: bans change x~, bias/penalty set y. Staged through LDS a
     // batch at a time (one load per thread), then each thread applies those
     // that fall on its elements.
@@ -675,10 +665,6 @@ __global__ __launch_bounds__(ZS_P1_NT) __attribute__((amdgpu_waves_per_eu(3))) v
 #pragma unroll
     for (int e = 0; e < P1_EPT; e++) kz[e] = zs_total_key(zs_temper(zv[e], T));
 
-    P1_MARK(3);
-#ifdef XP_NOSTAT
-    if (T > -1e30f) return;
-#endif
     // ---- chunk statistics of x~ (observers) and z (sampler), one workgroup
     // reduction: maxima, NaN / +inf flags, the last NaN of z, and counts of
     // finite z and of elements whose key is above that of -inf for the lists
@@ -742,7 +728,6 @@ __global__ __launch_bounds__(ZS_P1_NT) __attribute__((amdgpu_waves_per_eu(3))) v
     for (int w = 0; w < ZS_P1_NT / 64; w++) {
         zfin += sh.red[w].zfin; zabove += sh.red[w].zabove; xabove += sh.red[w].xabove;
     }
-    P1_MARK(4);
     const uint32_t nvalid = min((uint32_t)ZS_P1_CH, V - base);
     // greedy: argmax-last (ties -> larger index) over all, and over the tail
     // after the chunk's last NaN (the whole chunk when it has no NaN). A pair
@@ -784,7 +769,6 @@ __global__ __launch_bounds__(ZS_P1_NT) __attribute__((amdgpu_waves_per_eu(3))) v
         tail_n = (int)block_sum_u<ZS_P1_NT>(tn, sh.u);
     }
 
-    P1_MARK(5);
     // ---- approximate moments per 1024-logit sub-chunk (predictions for the
     // exact-sum rounds). Float4 j of thread t holds ids base + (j*NT + t)*4..+3,
     // so it lies in sub-chunk j*P1_SPF + t*4/1024 of the chunk: a wave's float4
@@ -796,9 +780,6 @@ __global__ __launch_bounds__(ZS_P1_NT) __attribute__((amdgpu_waves_per_eu(3))) v
         const int wid = zs_wid(), wh = (wid * 256) / ZS_SUB;
         const bool om = (P.flags & (ZS_ROW_LOGPROBS | ZS_ROW_UNCERTAINTY)) && omax > -INFINITY && omax < INFINITY;
         const bool zm = T > 0.0f && zmax > -INFINITY && zmax < INFINITY;
-#ifdef XP_NOMOM
-        if (T > -1e30f) return;
-#endif
         __shared__ float msh[ZS_P1_NT / 64][P1_J][3];
         // bit 2s: sub-chunk s holds the chunk's observer max, bit 2s+1: its sampler max
         uint32_t hasmax = 0;
@@ -873,11 +854,7 @@ __global__ __launch_bounds__(ZS_P1_NT) __attribute__((amdgpu_waves_per_eu(3))) v
         __syncthreads();
     }
 
-    P1_MARK(6);
     // ---- candidate lists (keys recomputed from the values where needed)
-#ifdef XP_NOLIST
-    if (T > -1e30f) return;
-#endif
     const size_t lofs = ((size_t)r * a.nch + c);
     // sampler list size: top_k when the row has a top-k cut within range
     const bool has_topk = P.top_k > 0 && P.top_k < V;
@@ -895,7 +872,6 @@ __global__ __launch_bounds__(ZS_P1_NT) __attribute__((amdgpu_waves_per_eu(3))) v
                          &s_full, sh);
         }
     }
-    P1_MARK(7);
     uint32_t ntl = P.top_logprobs > 20 ? 20 : P.top_logprobs;
     uint32_t Ko = ntl + 8;
     if (Ko > ZS_KO) Ko = ZS_KO;
@@ -910,7 +886,6 @@ __global__ __launch_bounds__(ZS_P1_NT) __attribute__((amdgpu_waves_per_eu(3))) v
         p1_topk_fast(xr, vmask, nvalid, xabove, Ko, base, a.co_key + lofs * ZS_KO, a.co_idx + lofs * ZS_KO, &no, &o_kth,
                      &o_full, sh);
 
-    P1_MARK(8);
     if (t == 0) {
         zs_chunk_stat cs;
         cs.obs_max = omax;
@@ -931,7 +906,6 @@ __global__ __launch_bounds__(ZS_P1_NT) __attribute__((amdgpu_waves_per_eu(3))) v
         cs.o_full = o_full;
         a.cst[lofs] = cs;
     }
-    P1_MARK(9);
 }
 
 // ===========================================================================
@@ -1139,21 +1113,7 @@ __device__ uint32_t small_path_wave(const zs_sargs& a, uint32_t r, const zs_row_
     return b.V - 1;
 }
 
-#ifdef ZS_DEBUG_CB
-__device__ unsigned long long zs_dbg_cb[10];
-#define CB_MARK(k) do { if (threadIdx.x == 0) { const long long c1_ = clock64(); cbd[k] = c1_ - cbc0; atomicAdd(&zs_dbg_cb[k], (unsigned long long)(c1_ - cbc0)); atomicMax(&zs_dbg_cb[9], (unsigned long long)(c1_ - cbs)); cbc0 = c1_; } } while (0)
-__device__ long long zs_dbg_cbrow[512][8];
-#define CB_PRINT() do { if (threadIdx.x == 0) { for (int q_ = 1; q_ < 7; q_++) zs_dbg_cbrow[r][q_] = cbd[q_]; zs_dbg_cbrow[r][0] = cbc0 - cbs; zs_dbg_cbrow[r][7] = (long long)status | ((long long)mode << 16) | ((long long)P.top_k << 24); } } while (0)
-#else
-#define CB_MARK(k) do {} while (0)
-#define CB_PRINT() do {} while (0)
-#endif
 __global__ __launch_bounds__(CB_NT) void zs_k_combine(zs_sargs a) {
-#ifdef ZS_DEBUG_CB
-    long long cbc0 = clock64();
-    const long long cbs = cbc0;
-    long long cbd[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-#endif
     const uint32_t r = blockIdx.x;
     const zs_batch& b = a.b;
     const uint32_t V = b.V;
@@ -1194,7 +1154,6 @@ __global__ __launch_bounds__(CB_NT) void zs_k_combine(zs_sargs a) {
     }
     __syncthreads();
     const zs_chunk_stat* cs = cs_sh;
-    CB_MARK(1);
 
     // ---------------- observers: max, special rows, top candidates ----------------
     float M = -INFINITY;
@@ -1236,7 +1195,6 @@ __global__ __launch_bounds__(CB_NT) void zs_k_combine(zs_sargs a) {
         }
         __syncthreads();
     }
-    CB_MARK(2);
     // the sampler sees x~ itself when T == 1 and no bias / penalty applies
     uint32_t has_y = 0;
     {
@@ -1247,7 +1205,6 @@ __global__ __launch_bounds__(CB_NT) void zs_k_combine(zs_sargs a) {
     }
     const uint32_t z_is_x = (P.temperature == 1.0f && !has_y) ? 1u : 0u;
 
-    CB_MARK(3);
     // ---------------- sampler ----------------
     const float T = P.temperature;
     uint32_t token = 0;
@@ -1303,7 +1260,6 @@ __global__ __launch_bounds__(CB_NT) void zs_k_combine(zs_sargs a) {
         for (uint32_t i = ncs + t; i < np2; i += CB_NT) sbuf[i] = ~0ull;
         __syncthreads();
         if (np2 > 1) block_sort_u64<CB_NT>(sbuf, np2);
-        CB_MARK(4);
         bool small = false;
         float thr = -INFINITY;
         if (has_topk && P.top_k <= ZS_KS) {
@@ -1360,7 +1316,6 @@ __global__ __launch_bounds__(CB_NT) void zs_k_combine(zs_sargs a) {
         }
         if (!small) mode = ZS_MODE_BIG;
     }
-    CB_MARK(5);
     // ---- predictions for the parallel exact-sum rounds
     uint32_t rounds = 0;
     {
@@ -1395,8 +1350,6 @@ __global__ __launch_bounds__(CB_NT) void zs_k_combine(zs_sargs a) {
         }
         if (obs_need & ZS_OBS_H) rounds |= 1u << ZS_SUM_OBS_H;
     }
-    CB_MARK(6);
-    CB_PRINT();
     if (t == 0) {
         st.rounds = rounds;
         st.z_max = zmax;
@@ -2402,9 +2355,6 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_tp_inc(zs_sargs a) {
     __shared__ uint32_t lc[ZS_TP_NB];
     __shared__ unsigned long long lt[ZS_TP_NB];
     __shared__ uint32_t lf[ZS_TP_NB];
-#ifdef ZS_DEBUG_TPT
-    const unsigned long long w0 = wall_clock64();
-#endif
     for (uint32_t i = t; i < ZS_TP_NB; i += ZS_BIG_NT) { lc[i] = 0u; lt[i] = 0ull; lf[i] = 0u; }
     __syncthreads();
     zs_tp_bucket* bk = a.tp_bk + (size_t)r * ZS_TP_NB;
@@ -2442,9 +2392,6 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_tp_inc(zs_sargs a) {
 #pragma unroll
     for (int q = 0; q < 4; q++)
         if (zs_u2f(pb[q]) > 0.0f) gv[lc[rk[q]] + off[q]] = pb[q];
-#ifdef ZS_DEBUG_TPT
-    if (t == 0) printf("tpinc %u %u start %llu dur %llu\n", r, g, w0, wall_clock64() - w0);
-#endif
 }
 
 // Composition of increment maps over a workgroup, in thread order: exclusive
@@ -2534,9 +2481,6 @@ __global__ __launch_bounds__(TP_SORT_NT) void zs_k_tp_sort(zs_sargs a) {
     uint32_t* q1 = gv + a.max_vocab;
     uint32_t* pe = a.tp_pre + (size_t)r * a.max_vocab * 2 + st0;
     uint32_t* po = pe + a.max_vocab;
-#ifdef ZS_DEBUG_TPT
-    const unsigned long long w0 = wall_clock64();
-#endif
     uint32_t np2 = 256;
     while (np2 < n) np2 <<= 1;
     uint32_t v[4];
@@ -2545,14 +2489,8 @@ __global__ __launch_bounds__(TP_SORT_NT) void zs_k_tp_sort(zs_sargs a) {
         const uint32_t i = 4u * t + e;
         v[e] = i < n ? gv[i] : 0u;   // 0 (p = 0) sorts last
     }
-#ifdef ZS_DEBUG_TPT
-    const unsigned long long w1 = wall_clock64();
-#endif
     for (uint32_t k = 2; k <= np2; k <<= 1)
         for (uint32_t j = k >> 1; j > 0; j >>= 1) tp_bitonic_step(v, k, j, sb);
-#ifdef ZS_DEBUG_TPT
-    const unsigned long long w2 = wall_clock64();
-#endif
     // prefixes over the sorted order: thread t owns elements 4t..4t+3
     const int eg0 = (int)(B->meta & TP_M_EG), eg1 = eg0 + 1;
     seq_pair loc = {0u, 0u};
@@ -2587,9 +2525,6 @@ __global__ __launch_bounds__(TP_SORT_NT) void zs_k_tp_sort(zs_sargs a) {
     }
     tie1 = __syncthreads_or(tie1);
     if (t == 0) atomicOr(&B->meta, TP_M_SORTED | (tie1 ? TP_M_TIE1 : 0u));
-#ifdef ZS_DEBUG_TPT
-    if (t == 0) printf("tpsort %u %u n %u start %llu load %llu sort %llu end %llu\n", r, c, n, w0, w1 - w0, w2 - w1, wall_clock64() - w2);
-#endif
 }
 
 // First j in [lo, hi) with pred(j) (pred monotone: false then true), or hi;
@@ -2659,9 +2594,6 @@ __device__ __forceinline__ int tp_walk(const zs_sargs& a, uint32_t r, float top_
         b0 = b + 1;
         const uint32_t n = __shfl(cnt, (int)f, 64), bm = __shfl(meta, (int)f, 64);
         if (!(bm & TP_M_SORTED)) {
-#ifdef ZS_DEBUG_TP
-            if (lane == 0) printf("tp fail row %u bucket %u n %u meta %x eg %d k %llu kthr %u\n", r, b, n, bm, eg, k, kthr);
-#endif
             return 0;
         }
         const uint32_t st0 = bk[b].start;
@@ -2754,13 +2686,6 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
     const uint32_t ng = (V + ZS_BIG_G - 1) / ZS_BIG_G;
     const float m = stt.z_max;
     uint32_t* pv = a.pv + (size_t)r * a.max_vocab;
-#ifdef XB_STOP
-    int nck = 0;
-#define BIG_MARK() do { if (++nck == XB_STOP) { if (t == 0) { a.rst[r].token = 0; a.rst[r].mode = ZS_MODE_DONE; } return; } } while (0)
-#else
-#define BIG_MARK() do {} while (0)
-#endif
-#define BIG_REPORT(tag) do {} while (0)
 
     // ---- top-k threshold by radix select when the candidates could not give it
     uint32_t has_thr = stt.has_thr;
@@ -2821,7 +2746,6 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
 
     // ---- probabilities p = exp(z - max) / S (sampler.rs:69), kept in pv for
     // the later passes; min-p kept mass (sampler.rs:72-88) in the same pass
-    BIG_MARK();
     const bool minp = P.min_p > 0.0f;
     const float cut = minp ? P.min_p * (1.0f / S) : 0.0f;  // p_max: the max element has exp(0) = 1
     float kept = 0.0f;
@@ -2854,7 +2778,6 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
     });
     __threadfence_block();
     __syncthreads();
-    BIG_MARK();
     auto p1_of = [&](uint32_t pb) -> float {
         float p = zs_u2f(pb);
         if (minp) {
@@ -2908,9 +2831,6 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
             wo = {fw == 1, sh.u[1], sh.u[2]};
             __syncthreads();
         }
-#ifdef ZS_DEBUG_TP
-        if (t == 0) printf("tp row %u peak %d fast %u ncand %u fw %d\n", r, (int)peak, a.tp_cl[(size_t)r * ZS_TP_CL], a.tp_cl[(size_t)r * ZS_TP_CL + 1], fw);
-#endif
         if (fw == 0) {
         // counts per (rank, copy): 16 copies by lane keep same-address LDS
         // atomics (skewed histograms) at most 4-way
@@ -2956,7 +2876,6 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
             if (t == 0) sh.u[0] = cand == ZS_BIGI ? (uint32_t)(BK_NB - 1) : (uint32_t)cand;
         }
         __syncthreads();
-        BIG_MARK();
         const uint32_t rlim = sh.u[0];
         float s = 0.0f;
         uint32_t done = 0;  // walked prefix of the level-0 layout
@@ -3007,7 +2926,6 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
             done = upto;
         }
         }  // fw == 0
-        BIG_MARK();
         if (peak) wo = {true, pmax1, 0u};
         if (wo.stopped) {
             // The kept set is {p1 > v*} plus the first rank+1 elements equal to
@@ -3323,26 +3241,6 @@ __global__ __launch_bounds__(SK_NT) void zs_k_stitchK(zs_sargs a) {
 // zs_k_final: per-row outputs (logprobs.rs:34-54, hallucination.rs:232-257)
 // ===========================================================================
 __global__ __launch_bounds__(64) void zs_k_final(zs_sargs a) {
-#ifdef ZS_DEBUG_CB
-    if (blockIdx.x == 0 && threadIdx.x == 0) {
-        printf("cb phases:");
-        for (int k = 1; k < 10; k++) { printf(" %d:%llu", k, zs_dbg_cb[k]); zs_dbg_cb[k] = 0; }
-        printf("\n");
-        for (int q = 0; q < 10; q++) {
-            int bi = 0;
-            for (uint32_t i = 1; i < a.b.B; i++) if (zs_dbg_cbrow[i][0] > zs_dbg_cbrow[bi][0]) bi = (int)i;
-            printf("cbrow %d tot %lld flags %llx: %lld %lld %lld %lld %lld %lld\n", bi, zs_dbg_cbrow[bi][0], zs_dbg_cbrow[bi][7], zs_dbg_cbrow[bi][1], zs_dbg_cbrow[bi][2], zs_dbg_cbrow[bi][3], zs_dbg_cbrow[bi][4], zs_dbg_cbrow[bi][5], zs_dbg_cbrow[bi][6]);
-            zs_dbg_cbrow[bi][0] = -1;
-        }
-    }
-#endif
-#ifdef ZS_DEBUG_P1
-    if (blockIdx.x == 0 && threadIdx.x == 0) {
-        printf("p1 phases:");
-        for (int k = 1; k < 10; k++) { printf(" %d:%llu", k, zs_dbg_p1[k]); zs_dbg_p1[k] = 0; }
-        printf("\n");
-    }
-#endif
     // one wave per row; lane j handles observer candidate j
     const uint32_t r = blockIdx.x;
     const uint32_t lane = threadIdx.x;
