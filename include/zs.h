@@ -251,11 +251,15 @@ int zs_sample(zs_ctx* ctx, const zs_batch* batch, void* stream);
  * (spec_decode.rs:241-279): d_accepted = accepted drafts, d_next = the bonus /
  * corrected token. temperature > 0 is rejection sampling against the draft
  * distributions (the reference has none, rest.rs:2639); probabilities are
- * exact integer weights rint(2^24 * 2^((z - max) log2 e)) from a fixed f32
- * operation sequence (0 below z - max = -17.5), uniforms are Philox words
- * of (seed, counter, tag) -- tag 1+i for the test of draft i, 1+k+i for the
- * replacement draw at a rejection at i, 1+2k for the bonus draw. Rows are
- * read with 16-byte loads: ld >= V, ld % 4 == 0, both bases 16-byte aligned. */
+ * exact integer weights, computed in one read of the logits: with chunks of
+ * 8192 ids, chunk maxima m_c, row maximum M, c = log2(e) / T and
+ * W(t) = rint(2^24 * 2^t) from a fixed f32 operation sequence (0 below
+ * t = -25), P_v = W((x_v - m_c) c) * W((m_c - M) c); the accept test and the
+ * residual use the row sums shifted to 40 significant bits. Uniforms are
+ * Philox words of (seed, counter, tag) -- tag 1+i for the test of draft i,
+ * 1+k+i for the replacement draw at a rejection at i, 1+2k for the bonus
+ * draw. Rows are read with 16-byte loads: ld >= V, ld % 4 == 0, both bases
+ * 16-byte aligned. */
 #define ZS_SPEC_KMAX 16
 typedef struct zs_spec_batch {
     uint32_t B, V, k;
@@ -270,13 +274,10 @@ typedef struct zs_spec_batch {
     uint32_t* d_next;               /* [B] */
     uint32_t flags;                 /* 0 or ZS_SPEC_BACKGROUND */
 } zs_spec_batch;
-/* ZS_SPEC_BACKGROUND: for a verification that runs on its own stream beside
- * other GPU work (e.g. after zs_batch.pass_event). The statistics and weight
- * sums over the target / draft rows then run as one workgroup per (row,
- * position) and at most one per CU: slower alone, but the second read of each
- * row comes from the memory-side cache and the other work keeps more of the
- * memory system. Results are identical. (No reference counterpart: a
- * scheduling hint of this implementation.) */
+/* ZS_SPEC_BACKGROUND: the chunk statistics and weight sums run as one
+ * workgroup per (row, position) and at most one per CU, leaving most of each
+ * CU to other work on other streams; slower alone. Results are identical.
+ * (No reference counterpart: a scheduling hint of this implementation.) */
 #define ZS_SPEC_BACKGROUND 1u
 int zs_spec_verify(zs_ctx* ctx, const zs_spec_batch* batch, void* stream);
 
