@@ -237,27 +237,30 @@ def make_step(W, V):
     step(out=None, overlap=True) -> (sampler outputs, (accepted, next)).
 
     The draft verification is independent of this step's sampling: it runs on
-    a second stream (default priority) from the start of the step. It reads
-    its logits once (bandwidth-bound) and fills the CUs that the sampler's
-    latency-bound per-row kernels leave idle; the step ends when both are
-    done."""
+    a second stream (default priority) once the sampler's first pass over the
+    logits is done (zs_batch.pass_event). It reads its logits once
+    (bandwidth-bound) and fills the CUs that the sampler's latency-bound
+    per-row kernels leave idle; the step ends when both are done."""
     import torch
     from zllm_amd.engine import verify_drafts
     ctx, sampler, bufs, xs, bits = W["ctx"], W["sampler"], W["bufs"], W["xs"], W["bits"]
     stream = torch.cuda.current_stream()
     spec_stream = torch.cuda.Stream()
+    pass_ev = torch.cuda.Event()
+    pass_ev.record(stream)  # creates the event
 
     def step(out=None, overlap=True):
         if overlap:
             spec_stream.wait_stream(stream)
+        W["dfa"].mask(W["table"], W["st"], V, out=bits)
+        out = sampler.run(xs, bufs, bits, top_stride=5, out=out, pass_event=pass_ev if overlap else None)
+        bufs["counter"].add_(1)
+        if overlap:
             with torch.cuda.stream(spec_stream):
+                spec_stream.wait_event(pass_ev)
                 spec = verify_drafts(ctx, W["tgt"], W["draft_ids"], W["spec_T"], W["spec_seed"], W["spec_ctr"],
                                      W["dft"])
                 W["spec_ctr"].add_(1)
-        W["dfa"].mask(W["table"], W["st"], V, out=bits)
-        out = sampler.run(xs, bufs, bits, top_stride=5, out=out)
-        bufs["counter"].add_(1)
-        if overlap:
             stream.wait_stream(spec_stream)
         else:
             spec = verify_drafts(ctx, W["tgt"], W["draft_ids"], W["spec_T"], W["spec_seed"], W["spec_ctr"], W["dft"])

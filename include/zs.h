@@ -230,13 +230,12 @@ typedef struct zs_batch {
     float* d_margin;
     float* d_chosen_lp;               /* [B] token_uncertainty.chosen_logprob */
     uint32_t* d_status;               /* [B] ZS_ST_* */
-    /* optional hipEvent_t, recorded on `stream` once the bandwidth-bound
-     * passes over the logits are done (the first pass with its candidate
-     * lists and moments, the parallel rounds of the softmax sums and the
-     * probabilities of the rows that take the top-p walk):
+    /* optional hipEvent_t, recorded on `stream` once the first full pass
+     * over the logits (with its candidate lists and moments) is done:
      * independent bandwidth-bound work (draft verification of the same step)
-     * made to wait on it runs beside the latency-bound per-row kernels that
-     * follow instead of slowing those passes. NULL: no event. */
+     * made to wait on it runs beside the mostly latency-bound per-row kernels
+     * that follow instead of holding back the start of the sampler. NULL: no
+     * event. */
     void* pass_event;
 } zs_batch;
 

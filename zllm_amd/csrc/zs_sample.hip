@@ -3407,6 +3407,7 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
     mark("zs_k_prep");
     hipLaunchKernelGGL(zs_k_pass1, dim3(nch, B), dim3(ZS_P1_NT), 0, stream, a);
     mark("zs_k_pass1");
+    if (a.b.pass_event && hipEventRecord((hipEvent_t)a.b.pass_event, stream) != hipSuccess) return -1;
     hipLaunchKernelGGL(zs_k_combine, dim3(B), dim3(CB_NT), 0, stream, a);
     mark("zs_k_combine");
     const uint32_t nsub = (bt->V + ZS_SUB - 1) / ZS_SUB;
@@ -3429,7 +3430,6 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
     if (!prof) ZS_LAUNCH_CHECK(hipEventRecord((hipEvent_t)ctx->join_event, side));
     hipLaunchKernelGGL(zs_k_pv, dim3((bt->V + ZS_BIG_G - 1) / ZS_BIG_G, B), dim3(ZS_BIG_NT), 0, stream, a);
     mark("zs_k_pv");
-    if (a.b.pass_event && hipEventRecord((hipEvent_t)a.b.pass_event, stream) != hipSuccess) return -1;
     hipLaunchKernelGGL(zs_k_tp_plan, dim3(B), dim3(ZS_BIG_NT), 0, stream, a);
     mark("zs_k_tp_plan");
     hipLaunchKernelGGL(zs_k_tp_inc, dim3((bt->V + ZS_BIG_G - 1) / ZS_BIG_G, B), dim3(ZS_BIG_NT), 0, stream, a);
