@@ -386,10 +386,13 @@ extern "C" int zs_dfa_create(zs_ctx* ctx, const uint32_t* h_trans, uint32_t nsta
         if (!bad[s]) remap[s] = (uint16_t)ngood++;
     // the fail value is ngood, a sink row whose entries all lead to itself, so a
     // walk needs no liveness test per step; entries of `bits` bits packed back
-    // to back (row s, class c at bit (s * ncls + c) * bits)
+    // to back inside a row, each row padded to whole 32-bit words (row s, class
+    // c at bit s * rw + c * bits, rw = 32 * ceil(ncls * bits / 32)), so that the
+    // walk finds an entry's first word with one multiply-add
     uint32_t bits = 1;
     while ((1u << bits) - 1u < ngood) bits++;
-    const uint64_t nbits = (uint64_t)(ngood + 1) * ncls * bits;
+    const uint32_t rw = (ncls * bits + 31u) & ~31u;  // bits per state row
+    const uint64_t nbits = (uint64_t)(ngood + 1) * rw;
     // + slack for the two-word reads, rounded to whole 16-byte quads
     std::vector<uint32_t> packed(((size_t)((nbits + 31) / 32 + 1) + 3) & ~(size_t)3, 0u);
     const uint32_t fail = ngood;
@@ -399,18 +402,17 @@ extern "C" int zs_dfa_create(zs_ctx* ctx, const uint32_t* h_trans, uint32_t nsta
         for (uint32_t c = 0; c < ncls; c++) {
             const uint16_t tgt = s < nstates ? cols[c][s] : 0xffffu;
             const uint64_t v = tgt == 0xffffu ? fail : remap[tgt];
-            const uint64_t off = ((uint64_t)row * ncls + c) * bits;
+            const uint64_t off = (uint64_t)row * rw + (uint64_t)c * bits;
             packed[off >> 5] |= (uint32_t)(v << (off & 31));
             if ((off & 31) + bits > 32) packed[(off >> 5) + 1] |= (uint32_t)(v >> (32 - (off & 31)));
         }
     }
     uint16_t clsinfo[256];
     for (uint32_t b = 0; b < 256; b++) clsinfo[b] = (uint16_t)(cls[b] * bits);
-    const uint32_t rw = ncls * bits;  // bits per state row
     d->ngood = ngood;
     d->bits = bits;
     d->rw = rw;
-    d->packed_lds = packed.size() * 4 <= ZS_DFA_LDS_BYTES && ncls * bits < 65536 ? 1 : 0;
+    d->packed_lds = packed.size() * 4 <= ZS_DFA_LDS_BYTES && rw < 65536 ? 1 : 0;
     if (!d->packed_lds && ncls <= 64) {
         // Sparse rows for tables past the LDS budget (large grammars are
         // mostly fail entries): per good state {class mask lo, hi, first

@@ -167,11 +167,13 @@ __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
         __syncthreads();
     }
     const uint32_t nc = ncr;
-    const uint32_t rw = a.rw;  // bits per state row
+    const uint32_t rwb = a.rw >> 3;  // bytes per state row (whole words)
     const uint32_t fmask = (1u << a.bits) - 1u;
-    // entry at bit offset o: the 32 bits from o of the two words holding it
+    // entry of class bit offset cb in row st: the 32 bits from bit cb & 31 of
+    // the two words from byte st * rwb + cbw, cbw = the byte offset of the word
+    // holding bit cb (computed once per byte, shared by the rows)
     const uint16_t* tgt16 = reinterpret_cast<const uint16_t*>(tab + 4 * (a.ngood + 1));
-    auto step = [&](uint32_t st, uint32_t cb) -> uint32_t {
+    auto step = [&](uint32_t st, uint32_t cb, uint32_t cbw) -> uint32_t {
         if (SPARSE) {
             // class mask of the state, then the target at the rank of its class
             const uint4 rec = reinterpret_cast<const uint4*>(tab)[st];
@@ -179,9 +181,10 @@ __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
             if (!((mask >> cb) & 1ull)) return a.ngood;
             return tgt16[rec.z + (uint32_t)__popcll(mask & ((1ull << cb) - 1ull))];
         }
-        const uint32_t o = __umul24(st, rw) + cb;  // states < 2^16, row bits < 2^16
-        const uint32_t w = o >> 5;
-        return __builtin_amdgcn_alignbit(tab[w + 1], tab[w], o & 31u) & fmask;
+        // states < 2^16, row bytes < 2^13: the byte address fits 24 bits
+        const uint32_t ba = __umul24(st, rwb) + cbw;
+        const uint32_t* w = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint8_t*>(tab) + ba);
+        return __builtin_amdgcn_alignbit(w[1], w[0], cb) & fmask;
     };
     const uint32_t fail = a.ngood;  // the sink row
     const uint32_t ncover = a.V > a.ntab ? a.V : a.ntab;
@@ -222,16 +225,18 @@ __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
             for (int i = 0; i < 16; i++) {
                 if ((uint32_t)i >= L) break;
                 const uint32_t cb = ci[(bw[i >> 2] >> (8 * (i & 3))) & 0xffu];
+                const uint32_t cbw = (cb >> 3) & ~3u;
 #pragma unroll
-                for (int rr = 0; rr < DL_RG; rr++) s[rr] = step(s[rr], cb);
+                for (int rr = 0; rr < DL_RG; rr++) s[rr] = step(s[rr], cb, cbw);
             }
             if (L > 16) {
                 // bytes past the first 16 from the CSR copy (long tokens)
                 const uint32_t o0 = a.offsets[id], o1 = a.offsets[id + 1];
                 for (uint32_t i = o0 + 16; i < o1; i++) {
                     const uint32_t cb = ci[a.bytes[i]];
+                    const uint32_t cbw = (cb >> 3) & ~3u;
 #pragma unroll
-                    for (int rr = 0; rr < DL_RG; rr++) s[rr] = step(s[rr], cb);
+                    for (int rr = 0; rr < DL_RG; rr++) s[rr] = step(s[rr], cb, cbw);
                 }
             }
             const uint32_t off = id - tok0;

@@ -267,7 +267,7 @@ struct zs_dfa {
     uint8_t* d_accept;     // [nstates]
     // bit-packed table for the LDS walk: good states renumbered 0..ngood-1 and
     // a sink row ngood (the fail value), entries of `bits` bits back to back,
-    // state s / class c at bit (s * ncls + c) * bits; rw = ncls * bits
+    // state s / class c at bit s * rw + c * bits; rw = ncls * bits rounded up to 32
     uint32_t* d_packed;    // [packed_words]
     uint16_t* d_clsinfo;   // [256] class * bits
     uint16_t* d_remap;     // [nstates] good id or 0xffff
