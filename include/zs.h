@@ -182,13 +182,15 @@ typedef struct zs_row_params {
 
 #define ZS_ROW_MASKED 1u       /* apply the row's allow bitset (grammar mask) */
 #define ZS_ROW_LOGPROBS 2u     /* logprob of the token + top_logprobs list (logprobs.rs:34-54) */
-#define ZS_ROW_UNCERTAINTY 4u  /* entropy / max_prob / margin / chosen_lp (hallucination.rs:232-257) */
+#define ZS_ROW_UNCERTAINTY 4u  /* entropy / max_prob / margin / chosen_lp (hallucination.rs:129-154) */
 
 /* Output status bits per row (d_status). */
 #define ZS_ST_GREEDY 1u        /* temperature <= 0: argmax path */
 #define ZS_ST_NONFINITE 2u     /* NaN/+inf/all -inf after adjustment: id V-1 (sampler.rs:127) */
 #define ZS_ST_SMALL 4u         /* survivors fit the on-chip exact path */
 #define ZS_ST_TOPLP_AMBIG 8u   /* top_logprobs order depends on the last bit of lse */
+#define ZS_ST_LIMIT 0x100u     /* the row exceeded ZS_MAX_PATCHES: nothing was sampled,
+                                  d_token = 0xffffffff; callers must check it */
 
 /* One step over B rows (the decode loop order of rest.rs:2594-2624):
  *   mask (bans, then the allow bitset)  -> x~        (observers see x~)
@@ -215,8 +217,15 @@ typedef struct zs_batch {
     const uint32_t* d_allow_bits;     /* [B][allow_words] or NULL */
     uint32_t allow_words;
     uint32_t top_stride;              /* >= max top_logprobs */
+    /* Philox key per row. The reference seeds StdRng from the request seed
+     * and falls back to the thread RNG when there is none (sampler.rs:26-29,
+     * decode_ctrl.rs:73); libzs has no entropy source of its own, so for an
+     * unseeded request the caller passes a fresh random 64-bit seed (drawn
+     * from the OS entropy source once per request, distinct per row) and
+     * keeps it for the request's later steps. Rows sharing a seed and a
+     * counter draw the same uniform. */
     const uint64_t* d_seed;           /* [B] */
-    const uint64_t* d_counter;        /* [B] */
+    const uint64_t* d_counter;        /* [B] step index of the row's request */
     /* outputs */
     uint32_t* d_token;                /* [B] */
     /* observer outputs are written for rows that request them (ZS_ROW_LOGPROBS
@@ -225,7 +234,7 @@ typedef struct zs_batch {
     uint32_t* d_top_ids;              /* [B][top_stride] */
     float* d_top_lps;                 /* [B][top_stride] */
     uint32_t* d_top_n;                /* [B] entries written */
-    float* d_entropy;                 /* [B] hallucination.rs:232-257 */
+    float* d_entropy;                 /* [B] hallucination.rs:129-154 */
     float* d_max_prob;
     float* d_margin;
     float* d_chosen_lp;               /* [B] token_uncertainty.chosen_logprob */

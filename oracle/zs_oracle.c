@@ -337,7 +337,7 @@ ZO_API uint32_t zo_logprobs_observe(const float* x, uint32_t V, uint32_t chosen,
 }
 
 /* -------------------------------------------------------------------------
- * hallucination.rs:232-257 token_uncertainty -> out[4] = entropy, max_prob,
+ * hallucination.rs:129-154 token_uncertainty -> out[4] = entropy, max_prob,
  * margin, chosen_logprob.
  * Parity: pinned by hallucination.rs tests (:162-202) and closed forms.
  * ------------------------------------------------------------------------- */
@@ -362,7 +362,7 @@ ZO_API void zo_token_uncertainty(const float* x, uint32_t V, uint32_t chosen, fl
     out[3] = cp > 0.0f ? logf(cp) : -INFINITY;
 }
 
-/* hallucination.rs:204-227 Detector::report over per-token (entropy,
+/* hallucination.rs:101-125 Detector::report over per-token (entropy,
  * max_prob) pairs. out[4] = risk_score, mean_entropy, normalized_entropy,
  * risky_fraction; returns peak index (-1 if none). thr_ent/thr_p =
  * DetectorConfig (defaults 2.0, 0.4 at :147-152). */

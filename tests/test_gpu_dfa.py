@@ -215,3 +215,39 @@ def test_real_vocab_table_and_json_grammar():
     bits = bits.cpu().numpy().view(np.uint32)
     for i, s in enumerate(states):
         assert np.array_equal(bits[i], O.mask_bits(V, dfa=od, vocab=ov, state=s)), (i, s)
+
+
+def test_viability_flags_across_kernel_paths():
+    """A call on the L2-table path (more rows than the LDS walk takes) followed
+    by one on the LDS path, on one context with the context's own viability
+    flags: a flag left by the first call must not make a dead-end row's EOS
+    disallowed in the second (logit_fsm.rs:258-262: EOS is allowed when no
+    token is viable)."""
+    from tests.tiny import build_dfa
+    from zllm_amd.engine import ByteDfa, Context, TokenByteTable
+    print("[case] fallback then packed DFA mask on one context", flush=True)
+    # 0 -a-> 1 -z-> 2 (accepting); no token of the table starts with 'z', so
+    # state 1 is live, not accepting, and has no viable token
+    trans, dead, acc = build_dfa({0: {"a": 1}, 1: {"z": 2}}, [2], 3)
+    V = 6
+    c = Context(0, 1100, 64)
+    offs, data, valid = _csr(TINY_TOKENS)
+    table = TokenByteTable.from_csr(c, offs, data, valid, TINY_EOS)
+    dfa = ByteDfa(c, trans, dead, acc)
+    od, ov = O.Dfa(trans, dead, acc), O.Vocab(TINY_TOKENS, TINY_EOS)
+    big = torch.zeros(1100, dtype=torch.int32, device="cuda")        # > ZS_DFA_MAXROWS rows: L2 path
+    bits_big = dfa.mask(table, big, V)
+    small = torch.tensor([1, 0], dtype=torch.int32, device="cuda")  # LDS path
+    bits_small = dfa.mask(table, small, V)
+    torch.cuda.synchronize()
+    bb = bits_big.cpu().numpy().view(np.uint32)
+    bs = bits_small.cpu().numpy().view(np.uint32)
+    want0 = O.mask_bits(V, dfa=od, vocab=ov, state=0)
+    want1 = O.mask_bits(V, dfa=od, vocab=ov, state=1)
+    assert all(np.array_equal(bb[i], want0) for i in (0, 1, 1099))
+    assert np.array_equal(bs[0], want1), (bs[0], want1)
+    assert np.array_equal(bs[1], want0), (bs[1], want0)
+    # and back on the L2 path after the LDS path
+    bits_big2 = dfa.mask(table, torch.ones(1100, dtype=torch.int32, device="cuda"), V)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits_big2.cpu().numpy().view(np.uint32)[7], want1)

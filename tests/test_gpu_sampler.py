@@ -124,3 +124,36 @@ def test_tied_values_topk_lists(q):
     x[3, :] = 1.0                      # one value everywhere: every chunk ties completely
     x[7, ::3] = -np.inf                # a third masked out
     _run(x, params)
+
+
+def test_unseeded_rows_draw_independently():
+    """Unseeded requests (sampler.rs:26-29 draws from the thread RNG) get a
+    fresh OS-entropy key each: 64 unseeded rows with identical logits draw
+    independently, while rows with one explicit seed draw one token; every row
+    matches the oracle under the key it was given."""
+    from tests.gpu_util import compare, ctx, make_rows
+    from zllm_amd.engine import BatchSampler
+    import torch
+    B, V = 64, 1000
+    print(f"[case] unseeded B={B} V={V}", flush=True)
+    x = np.zeros((B, V), np.float32)           # uniform: every draw is a fresh index
+    unseeded = [dict(temperature=1.0, top_k=0, top_p=1.0, seed=None, logprobs=False,
+                     detect_hallucination=False) for _ in range(B // 2)]
+    seeded = [dict(temperature=1.0, top_k=0, top_p=1.0, seed=77, logprobs=False,
+                   detect_hallucination=False) for _ in range(B // 2)]
+    params = unseeded + seeded
+    rows = make_rows(params)
+    keys = [r.ctrl.seed for r in rows]
+    assert len(set(keys[:B // 2])) == B // 2 and set(keys[B // 2:]) == {77}
+    xs = torch.from_numpy(x).cuda()
+    bs = BatchSampler(ctx())
+    out = bs.run(xs, bs.pack(xs, rows))
+    torch.cuda.synchronize()
+    tok = out["token"].cpu().numpy().view(np.uint32)
+    assert len(set(tok[:B // 2].tolist())) >= 24, tok[:B // 2]    # 32 draws from 1000 ids
+    assert len(set(tok[B // 2:].tolist())) == 1
+    for p, k in zip(params, keys):
+        p["seed"] = k
+    res = {k: v.cpu().numpy() for k, v in out.items()}
+    errs = compare(x, params, res, check_stats=False)
+    assert not errs, "\n".join(errs[:10])

@@ -364,25 +364,25 @@ def test_uniform_logprob_closed_form():
 
 
 # ---------------------------------------------------------------- hallucination.rs
-def test_one_hot_is_certain():  # hallucination.rs:165-175
+def test_one_hot_is_certain():  # hallucination.rs:163-172
     l = np.zeros(64, np.float32)
     l[7] = 50.0
     H, mp, mg, clp = O.token_uncertainty(l, 7)
     assert H < 1e-3 and abs(mp - 1) < 1e-3 and abs(mg - 1) < 1e-3 and clp > -1e-3
 
 
-def test_uniform_is_maximally_uncertain():  # hallucination.rs:177-186
+def test_uniform_is_maximally_uncertain():  # hallucination.rs:175-183
     H, mp, mg, clp = O.token_uncertainty(np.zeros(64), 0)
     assert abs(H - math.log(64)) < 1e-3 and abs(mp - 1 / 64) < 1e-4 and mg < 1e-4
 
 
-def test_sharper_distribution_is_less_risky():  # hallucination.rs:188-197
+def test_sharper_distribution_is_less_risky():  # hallucination.rs:186-194
     ud = O.token_uncertainty([0.0, 0.1, 0.2, 0.0], 2)
     up = O.token_uncertainty([0.0, 0.1, 6.0, 0.0], 2)
     assert up[0] < ud[0] and up[1] > ud[1]
 
 
-def test_chosen_logprob_tracks_choice():  # hallucination.rs:199-205
+def test_chosen_logprob_tracks_choice():  # hallucination.rs:197-202
     assert O.token_uncertainty([3.0, 1.0, 0.0], 0)[3] > O.token_uncertainty([3.0, 1.0, 0.0], 2)[3]
 
 
@@ -396,7 +396,7 @@ def test_entropy_closed_form_two_level():
     assert abs(O.token_uncertainty(x, 0)[0] - H) < 1e-5
 
 
-def test_report_aggregates_and_flags():  # hallucination.rs:207-224
+def test_report_aggregates_and_flags():  # hallucination.rs:205-221
     sharp = np.zeros(32, np.float32)
     sharp[1] = 40.0
     us = [O.token_uncertainty(sharp, 1), O.token_uncertainty(sharp, 1), O.token_uncertainty(np.zeros(32), 0)]
@@ -406,7 +406,7 @@ def test_report_aggregates_and_flags():  # hallucination.rs:207-224
     assert risk >= 0.1 and not risk >= 0.99
 
 
-def test_empty_report_is_zero():  # hallucination.rs:226-232
+def test_empty_report_is_zero():  # hallucination.rs:224-231
     out, peak = O.report([], [], 0)
     assert list(out) == [0, 0, 0, 0] and peak is None
 

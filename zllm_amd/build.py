@@ -34,21 +34,6 @@ FLAGS = [
 ]
 
 
-CALIB_SRC = os.path.join(ROOT, "tests", "c", "calib_exp.hip")
-CALIB_BIN = os.path.join(ROOT, "tests", "c", "calib_exp")
-
-
-def build_calibration(verbose=False):
-    """Test helper: the fast-exp calibration sweep (run by a GPU test)."""
-    flags = [f for f in FLAGS if f not in ("-fPIC", "-shared")]
-    cmd = [HIPCC] + flags + [CALIB_SRC, "-o", CALIB_BIN]
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        sys.stderr.write(r.stdout + r.stderr)
-        raise RuntimeError("hipcc failed building the calibration sweep")
-    return CALIB_BIN
-
-
 def build(verbose=False):
     srcs = [os.path.join(CSRC, s) for s in SOURCES if os.path.exists(os.path.join(CSRC, s))]
     cmd = [HIPCC] + FLAGS + srcs + ["-o", LIB + ".tmp"]
@@ -59,8 +44,6 @@ def build(verbose=False):
         sys.stderr.write(r.stdout + r.stderr)
         raise RuntimeError("hipcc failed building libzs.so")
     os.replace(LIB + ".tmp", LIB)
-    if os.path.exists(CALIB_SRC):
-        build_calibration(verbose)
     return LIB
 
 

@@ -538,8 +538,14 @@ extern "C" int zs_dfa_mask(zs_ctx* ctx, const zs_dfa* dfa, const zs_vocab* vocab
     a.words = (V + 31) / 32;
     a.out = d_out_bits;
     const bool packed = dfa->packed_lds != 0 && B <= ZS_DFA_MAXROWS;
-    uint32_t* any = d_any ? d_any : (uint32_t*)ctx->mask_scratch;
-    if (packed) {
+    // Viability flags: the context's flags hold the epoch of the call that
+    // found a viable token, on both kernel paths (no clearing pass, and a flag
+    // left by an earlier call on the other path never reads as viable); the
+    // caller's d_any then receives 0/1 from the EOS kernel. Only the
+    // L2-table path with a caller-supplied d_any uses plain cleared flags.
+    uint32_t* any = d_any;
+    a.epoch = 0;
+    if (packed || !d_any) {
         if (++ctx->mask_epoch == 0) ctx->mask_epoch = 1;  // 0 is what the flags start as
         a.epoch = ctx->mask_epoch;
         a.any_user = d_any;

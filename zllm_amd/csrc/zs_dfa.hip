@@ -100,7 +100,7 @@ __global__ __launch_bounds__(DM_NT) void zs_k_dfa_mask(dm_args a) {
         }
         if (st >= 0) {
             anyv = wave_or_u(anyv);
-            if (zs_lane() == 0 && anyv) atomicOr(&a.any[r], 1u);
+            if (zs_lane() == 0 && anyv) a.any[r] = a.epoch ? a.epoch : 1u;  // same value from every writer
         }
     }
 }
@@ -271,18 +271,6 @@ __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
     }
 }
 
-// Unconstrained rows: every id below V allowed; clears the viability flags.
-__global__ void zs_k_dfa_free_rows(dm_args a) {
-    const uint32_t r = blockIdx.y;
-    if (blockIdx.x == 0 && threadIdx.x == 0) a.any[r] = 0;
-    if (a.states[r] >= 0) return;
-    for (uint32_t wi = blockIdx.x * blockDim.x + threadIdx.x; wi < a.words; wi += gridDim.x * blockDim.x) {
-        uint32_t v = 0xffffffffu;
-        if (wi == a.words - 1 && (a.V & 31)) v = (1u << (a.V & 31)) - 1u;
-        a.out[(size_t)r * a.words + wi] = v;
-    }
-}
-
 __global__ void zs_k_fill_u32(uint32_t* p, uint32_t n, uint32_t v) {
     uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) p[i] = v;
@@ -318,8 +306,9 @@ extern "C" int zs_dfa_mask_launch(const dm_args& a, bool packed_lds, uint32_t nc
         else
             hipLaunchKernelGGL(zs_k_dfa_mask_packed<false>, dim3(min(items, ncu)), dim3(DL_NT), 0, stream, x);
     } else {
-        x.epoch = 0;
-        hipLaunchKernelGGL(zs_k_fill_u32, dim3((a.B + 255) / 256), dim3(256), 0, stream, any_scratch, a.B, 0u);
+        // epoch 0: the caller's own 0/1 flags, cleared first; otherwise the
+        // context's flags, compared with the epoch as in the packed walk
+        if (!x.epoch) hipLaunchKernelGGL(zs_k_fill_u32, dim3((a.B + 255) / 256), dim3(256), 0, stream, any_scratch, a.B, 0u);
         dim3 grid((ncover + DM_TOK - 1) / DM_TOK, (a.B + DM_ROWS - 1) / DM_ROWS);
         hipLaunchKernelGGL(zs_k_dfa_mask<false>, grid, dim3(DM_NT), 0, stream, x);
     }

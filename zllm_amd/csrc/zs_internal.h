@@ -106,8 +106,8 @@ struct zs_row_state {
     uint32_t obs_need;
     uint32_t rounds;      // ZS_SUM_* bits computed by the parallel rounds
     float samp_S;         // sampler softmax denominator (sampler.rs:68) when computed by the rounds
-    float obs_S;          // sequential f32 sum (hallucination.rs:237-238, logprobs.rs:36)
-    float obs_H;          // sequential f32 entropy (hallucination.rs:242-248)
+    float obs_S;          // sequential f32 sum (hallucination.rs:134-135, logprobs.rs:36)
+    float obs_H;          // sequential f32 entropy (hallucination.rs:139-144)
     // big rows with a top-p cut: the kept set compacted in index order (zs_k_big)
     // whose sum and draw run as parallel rounds (zs_k_roundK / zs_k_stitchK)
     uint32_t klist;       // 1: list ready

@@ -4,7 +4,7 @@
 //   x~ = apply_mask(x)                    logit_fsm.rs:247-270 (bans, allow bits)
 //   y  = adjust_logits(x~)                decode_ctrl.rs:107-126
 //   token = sample_with_rng(y, cfg, r)    sampler.rs:31-128
-//   logprobs / token_uncertainty on x~    logprobs.rs:34-54, hallucination.rs:232-257
+//   logprobs / token_uncertainty on x~    logprobs.rs:34-54, hallucination.rs:129-154
 //
 // Kernels (one launch each, in stream order):
 //   zs_k_prep     one workgroup per row: merge ban / bias / count-map lists into a
@@ -56,7 +56,6 @@ struct zs_sargs {
     uint32_t* kcnt;
 };
 
-#define ZS_ST_LIMIT 0x100u
 #define ZS_ST_FALLBACK 0x200u
 
 __device__ __forceinline__ bool zs_penalty_active(const zs_row_params& P) {
@@ -1654,10 +1653,6 @@ __device__ __forceinline__ void stitch_body(const zs_sargs& a) {
         lns = (float)log((double)st->obs_S);
     }
     float s = KIND == ZS_SUM_OBS_H ? 0.0f : -0.0f;
-#ifdef ZS_DEBUG_STITCH
-    uint32_t nfr = 0, nmis = 0, novf = 0, ntie = 0;
-    long long c_load = 0, c_seq = 0, c_all = clock64();
-#endif
     for (uint32_t j = 0; j < nsub; j++) {
         const zs_sub_sum e = sh.rec[j];
         const int eg = zs_grid_exp(s);
@@ -1667,22 +1662,9 @@ __device__ __forceinline__ void stitch_body(const zs_sargs& a) {
             s = zs_grid_value(k0 + e.total, eg);
             continue;
         }
-#ifdef ZS_DEBUG_STITCH
-        if (e.flags & ZS_SF_FRAGILE) nfr++;
-        else if (e.flags & ZS_SF_TIE) ntie++;
-        else if (e.eg != eg) nmis++;
-        else novf++;
-#endif
         const bool first = (j == 0);
         float x[ST_EPT], z[ST_EPT];
-#ifdef ZS_DEBUG_STITCH
-        long long c0 = clock64();
-#endif
         sub_load_t<ST_EPT>(R, j, t, x, z);
-#ifdef ZS_DEBUG_STITCH
-        long long c1 = clock64();
-        c_load += c1 - c0;
-#endif
         if (KIND == ZS_SUM_OBS_S) {
             obs_exp_terms<ST_EPT> f;
 #pragma unroll
@@ -1699,14 +1681,7 @@ __device__ __forceinline__ void stitch_body(const zs_sargs& a) {
             for (int q = 0; q < ST_EPT; q++) f.a[q] = zs_ent_obs(x[q] - M, inv, lns);
             stitch_sub(f, s, first, sh);
         }
-#ifdef ZS_DEBUG_STITCH
-        c_seq += clock64() - c1;
-#endif
     }
-#ifdef ZS_DEBUG_STITCH
-    c_all = clock64() - c_all;
-    if (t == 0) printf("stitch row %u kind %d nsub %u fragile %u tie %u mispred %u ovf %u  clk all %lld load %lld seq %lld M %g m %g s %a masked %d T %g\n", r, KIND, nsub, nfr, ntie, nmis, novf, c_all, c_load, c_seq, M, m, s, (int)R.masked, R.T);
-#endif
     if (KIND == ZS_SUM_OBS_S) {
         if (t == 0) st->obs_S = s;
         if (((rounds >> ZS_SUM_OBS_H) & 1u) && t < 64) {
@@ -1871,14 +1846,6 @@ __device__ __forceinline__ float big_term_e(float z, bool has_thr, float thr, fl
 // (value, rank among the equal values passed): the index order among equal
 // probabilities is resolved afterwards on the row.
 // ---------------------------------------------------------------------------
-#ifdef ZS_DEBUG_WALK
-__device__ unsigned long long zs_dbg_walk[256][8];
-#define WALK_COUNT(k, v) do { if (threadIdx.x == 0) zs_dbg_walk[blockIdx.x][k] += (v); } while (0)
-#define WALK_MAX(k, v) do { if (threadIdx.x == 0 && zs_dbg_walk[blockIdx.x][k] < (unsigned long long)(v)) zs_dbg_walk[blockIdx.x][k] = (v); } while (0)
-#else
-#define WALK_COUNT(k, v) do {} while (0)
-#define WALK_MAX(k, v) do {} while (0)
-#endif
 struct walk_out {
     bool stopped;
     uint32_t v;      // stop value (f32 bits)
@@ -1929,21 +1896,12 @@ __device__ __forceinline__ void bk_sort_desc_small(uint32_t* a, int np2) {
 // Walk n <= ZS_SORT_CAP values in exact descending order (sorted in LDS).
 __device__ __forceinline__ walk_out bk_walk_sorted(const uint32_t* vals, uint32_t n, float& s, float thresh, big_shared& sh) {
     walk_out o = {false, 0u, 0u};
-    WALK_COUNT(0, 1);
-    WALK_COUNT(1, n);
-    WALK_MAX(6, n);
-#ifdef ZS_DEBUG_WALK
-    long long cs0 = clock64();
-#endif
     uint32_t np2 = 1;
     while (np2 < n) np2 <<= 1;
     for (uint32_t i = threadIdx.x; i < np2; i += ZS_BIG_NT) sh.sortbuf[i] = i < n ? vals[i] : 0u;
     __syncthreads();
     if (np2 > ZS_BIG_NT) bk_sort_desc(sh.sortbuf, (int)np2);
     else if (np2 > 1) bk_sort_desc_small(sh.sortbuf, (int)np2);
-#ifdef ZS_DEBUG_WALK
-    WALK_COUNT(4, clock64() - cs0);
-#endif
     if (n <= BK_SERIAL) {
         // a bucket of this size is walked faster by one thread than by the
         // workgroup scan (whose cost is its latency chain, not its width)
@@ -2070,9 +2028,6 @@ __device__ __forceinline__ walk_out bk_walk(const uint32_t* vals, uint32_t from,
     uint32_t pos = from;
     float s_bstart = s;  // running sum at the start of the bucket open at pos
     while (pos < to) {
-#ifdef ZS_DEBUG_WALK
-        long long cf0 = clock64();
-#endif
         float tv[BK_WEPT];
 #pragma unroll
         for (int q = 0; q < BK_WEPT; q++) {
@@ -2081,14 +2036,7 @@ __device__ __forceinline__ walk_out bk_walk(const uint32_t* vals, uint32_t from,
         }
         uint32_t excl[BK_WEPT];
         seq_find_res F = seq_find<ZS_BIG_NT, BK_WEPT>(seq_terms<BK_WEPT>(tv), 0, s, thresh, excl, sh.q);
-#ifdef ZS_DEBUG_WALK
-        WALK_COUNT(3, clock64() - cf0);
-#endif
         const int first = min(min(F.ev, F.st), F.tie);
-        WALK_COUNT(2, 1);
-#ifdef ZS_DEBUG_WALK
-        long long cw0 = clock64();
-#endif
         if (first == ZS_BIGI) {
             const uint32_t last = min(pos + BK_WG, to) - 1;
             const uint32_t bst = start[bk_rank<L>(vals[last])];
@@ -2103,9 +2051,6 @@ __device__ __forceinline__ walk_out bk_walk(const uint32_t* vals, uint32_t from,
         if (bst >= pos) s = seq_value_at<ZS_BIG_NT, BK_WEPT>(F, excl, (int)(bst - pos), sh.q);
         else s = s_bstart;
         o = bk_exact<L + 1>(vals + bst, bend - bst, s, thresh, tmp, sh);
-#ifdef ZS_DEBUG_WALK
-        WALK_COUNT(5, clock64() - cw0);
-#endif
         if (o.stopped) return o;
         s_bstart = s;
         pos = bend;
@@ -2916,13 +2861,7 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
             __threadfence_block();
             __syncthreads();
             const uint32_t upto = sh.hist[rhi + 1];
-#ifdef ZS_DEBUG_WALK
-            long long cg = clock64();
-#endif
             wo = bk_walk<0>(gv, done, upto, sh.hist, s, P.top_p, tmp, sh);
-#ifdef ZS_DEBUG_WALK
-            WALK_COUNT(7, clock64() - cg);
-#endif
             done = upto;
         }
         }  // fw == 0
@@ -3238,7 +3177,7 @@ __global__ __launch_bounds__(SK_NT) void zs_k_stitchK(zs_sargs a) {
 }
 
 // ===========================================================================
-// zs_k_final: per-row outputs (logprobs.rs:34-54, hallucination.rs:232-257)
+// zs_k_final: per-row outputs (logprobs.rs:34-54, hallucination.rs:129-154)
 // ===========================================================================
 __global__ __launch_bounds__(64) void zs_k_final(zs_sargs a) {
     // one wave per row; lane j handles observer candidate j
@@ -3336,7 +3275,7 @@ __global__ __launch_bounds__(64) void zs_k_final(zs_sargs a) {
     }
     if (want_unc && lane == 0) {
         if (st.obs_special) {
-            // sum is NaN: no p > 0, top1 stays -inf (hallucination.rs:243-256)
+            // sum is NaN: no p > 0, top1 stays -inf (hallucination.rs:140-153)
             b.d_entropy[r] = 0.0f;
             b.d_max_prob[r] = 0.0f;
             b.d_margin[r] = 0.0f;

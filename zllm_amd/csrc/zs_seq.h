@@ -1,6 +1,6 @@
 // zs_seq.h -- workgroup-parallel exact reproduction of a sequential f32 sum of
 // non-negative terms (the `sum()` / `cumsum +=` loops of sampler.rs:68, 80,
-// 103, 107, 121, logprobs.rs:36, hallucination.rs:238, 246).
+// 103, 107, 121, logprobs.rs:36, hallucination.rs:135, 143).
 //
 // While the running sum s = k*g stays inside one binade (grid g = ulp(s),
 // k < 2^24), adding a term t gives k' = k + round_half_even(k + t/g) - k: an

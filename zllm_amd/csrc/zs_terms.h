@@ -40,7 +40,7 @@ __device__ __forceinline__ bool zs_cert_inc(float a, int eg, uint32_t* inc) {
 template <int EPT>
 __device__ __forceinline__ float zs_pick(const float (&v)[EPT], int j) { return seq_pick_f(v, j); }
 
-// term = expf(d) (softmax numerators: sampler.rs:68, logprobs.rs:36, hallucination.rs:238)
+// term = expf(d) (softmax numerators: sampler.rs:68, logprobs.rs:36, hallucination.rs:135)
 template <int EPT>
 struct exp_terms {
     float d[EPT], a[EPT];
@@ -62,7 +62,7 @@ struct exp_terms {
 };
 
 // term = -(p * ((l - max) - ln_sum)) with p = expf(l - max) * inv, 0 unless p > 0
-// (hallucination.rs:244-246: `entropy -= p * ((l - max) - ln_sum)`).
+// (hallucination.rs:143: `entropy -= p * ((l - max) - ln_sum)`).
 template <int EPT>
 struct ent_terms {
     float d[EPT], a[EPT];

@@ -10,13 +10,14 @@ torch is used only for device memory and the stream; every computation runs
 in libzs's HIP kernels.
 """
 import ctypes as C
+import secrets
 from dataclasses import dataclass, field
 from typing import Dict, List, Optional, Sequence, Tuple
 
 import numpy as np
 import torch
 
-from ._lib import (Batch, LaneStream, RowParams, SpecBatch, ZS_OK, ZS_ROW_LOGPROBS, ZS_ROW_MASKED, ZS_ROW_UNCERTAINTY,
+from ._lib import (Batch, LaneStream, RowParams, SpecBatch, ZS_OK, ZS_ST_LIMIT, ZS_ROW_LOGPROBS, ZS_ROW_MASKED, ZS_ROW_UNCERTAINTY,
                    ZS_SPEC_BACKGROUND, ZsError, lib)
 
 OPENAI_TOP_LOGPROBS_CAP = 20  # logprobs.rs:27-29
@@ -89,14 +90,18 @@ class PenaltyConfig:
 class DecodeControl:
     """decode_ctrl.rs:45-153: penalties, logit_bias, the per-request RNG and the
     count map. The RNG is Philox4x32-10 keyed by `seed` with a per-step counter
-    (the reference uses StdRng)."""
+    (the reference uses StdRng). Without a seed the reference draws from the
+    thread RNG (sampler.rs:26-29, decode_ctrl.rs:73); here an unseeded request
+    gets a fresh 64-bit key from the OS entropy source, so unseeded requests
+    (and rows) draw independently of each other."""
 
     def __init__(self, penalties: Optional[PenaltyConfig] = None, logit_bias: Sequence[Tuple[int, float]] = (),
                  seed: Optional[int] = None):
         self.penalties = penalties or PenaltyConfig()
         self.logit_bias = [(int(t), float(b)) for t, b in logit_bias]
         self.counts: Dict[int, int] = {}
-        self.seed = 0 if seed is None else int(seed) & (2**64 - 1)
+        self.seeded = seed is not None
+        self.seed = secrets.randbits(64) if seed is None else int(seed) & (2**64 - 1)
         self.counter = 0
 
     def observe_prompt_tail(self, prompt: Sequence[int], last_n: int):  # decode_ctrl.rs:90-97
@@ -400,6 +405,10 @@ class BatchSampler:
         out = self.run(logits, bufs, allow_bits)
         torch.cuda.current_stream(logits.device).synchronize()
         toks = out["token"].cpu().numpy().view(np.uint32)
+        st = out["status"].cpu().numpy().view(np.uint32)
+        bad = np.nonzero(st & ZS_ST_LIMIT)[0]
+        if len(bad):
+            raise RuntimeError(f"zs_sample: rows {bad.tolist()} exceed the per-row patch limit (ZS_ST_LIMIT)")
         for rq, tok in zip(rows, toks):
             rq.ctrl.counter += 1
             if rq.fsm is not None:

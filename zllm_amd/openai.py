@@ -1,5 +1,5 @@
 """OpenAI wire output fed from the sampler's per-token outputs (host side):
-LogprobsCollector (logprobs.rs:20-31) and Detector (hallucination.rs:71-126)
+LogprobsCollector (logprobs.rs:20-31) and Detector (hallucination.rs:77-125)
 accumulate zs_sample's per-row outputs step by step; the JSON views are
 produced by libzs (chat_logprobs_json / legacy_logprobs_json,
 rest.rs:1710-1744; hallucination_json, rest.rs:1494-1503) with serde_json's
@@ -76,7 +76,7 @@ class LogprobsCollector:
 
 
 @dataclass
-class HallucinationReport:  # hallucination.rs:53-70 (summary fields)
+class HallucinationReport:  # hallucination.rs:54-67 (summary fields)
     risk_score: float
     mean_entropy: float
     normalized_entropy: float
@@ -94,7 +94,7 @@ class HallucinationReport:  # hallucination.rs:53-70 (summary fields)
 
 
 class Detector:
-    """hallucination.rs:71-126 over zs_sample's per-token entropy / max_prob."""
+    """hallucination.rs:77-125 over zs_sample's per-token entropy / max_prob."""
 
     def __init__(self, entropy_threshold: float = 2.0, max_prob_threshold: float = 0.4):
         self.entropy_threshold = entropy_threshold
