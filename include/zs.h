@@ -289,6 +289,22 @@ typedef struct zs_spec_batch {
 #define ZS_SPEC_BACKGROUND 1u
 int zs_spec_verify(zs_ctx* ctx, const zs_spec_batch* batch, void* stream);
 
+/* zs_spec_verify without a context and without any allocation: the same
+ * kernels and results, with their scratch (per-chunk records and per-row
+ * state) in a fixed device array of the library, one per GPU, held until the
+ * process ends. No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops
+ * that forbid hipMalloc). Runs on the current device. Limits: B <=
+ * ZS_SPEC_STATIC_MAX_ROWS and B * npos * ceil(V / 8192) <=
+ * ZS_SPEC_STATIC_MAX_RECORDS (npos = 2k+1 with draft logits, else k+1);
+ * beyond them ZS_ELIMIT and nothing runs. Returns ZS_EINVAL for the argument
+ * errors zs_spec_verify reports (no error string: there is no context), and
+ * ZS_EHIP for a launch failure. Calls that overlap on one GPU (other streams,
+ * other host threads) share the array and race: serialise them. */
+#define ZS_SPEC_STATIC_MAX_ROWS 4096
+#define ZS_SPEC_STATIC_MAX_RECORDS 65536   /* 40 bytes each: 2.5 MiB per GPU */
+int zs_spec_verify_static(const zs_spec_batch* batch, void* stream);
+
 /* ---- batched lane (continuous batching, gpu/batch.rs:176-192) --------------
  * Device-side versions of the WGSL sampling kernels with their exact
  * semantics: BARGMAX (shaders.rs:761-789), BSAMPLE Gumbel-max (:796-850; WGSL

@@ -121,6 +121,7 @@ SIGNATURES = {
     "zs_sample": (C.c_int, [C.c_void_p, C.POINTER(Batch), C.c_void_p]),
     "zs_set_profiling": (C.c_int, [C.c_void_p, C.c_int]),
     "zs_spec_verify": (C.c_int, [C.c_void_p, C.POINTER(SpecBatch), C.c_void_p]),
+    "zs_spec_verify_static": (C.c_int, [C.POINTER(SpecBatch), C.c_void_p]),
     "zs_lane_argmax": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint64, C.c_void_p, C.c_void_p]),
     "zs_lane_sample": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint64, C.c_void_p, C.c_void_p,
                                  C.c_void_p, C.c_void_p]),

@@ -24,6 +24,7 @@
 #include <hip/hip_runtime.h>
 #include "zs_internal.h"
 #include "zs_dev.h"
+#include <mutex>
 
 #define SP_NT 256
 #define SP_CH 8192
@@ -594,4 +595,71 @@ extern "C" int zs_spec_launch(const zs_spec_args& a, const zs_prof& prof, hipStr
     mark("zs_k_spec_draw");
     if (prof.on) *prof.n = ev - 1;
     return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// ---------------------------------------------------------------------------
+// zs_spec_verify_static: the same verification without a context, for callers
+// that cannot allocate (HIP graph capture, serving loops that forbid
+// hipMalloc). The chunk records and per-row state live in `scratch`, one copy
+// per GPU for the life of the process. The host never passes the array's own
+// name to a kernel (in host code it is only a stand-in for the symbol): the
+// device address of each GPU's copy is looked up once with
+// hipGetSymbolAddress, with that GPU current, and kept per device.
+// Every kernel writes the records it later reads, so nothing needs clearing.
+// Calls that overlap on one GPU share the array and race.
+// ---------------------------------------------------------------------------
+struct zs_spec_static_area {
+    zs_spec_chunk cst[ZS_SPEC_STATIC_MAX_RECORDS];
+    zs_spec_row rs[ZS_SPEC_STATIC_MAX_ROWS];
+};
+static __device__ __align__(256) zs_spec_static_area scratch;
+
+#define ZS_STATIC_MAX_DEVICES 64
+static zs_spec_static_area* g_static_area[ZS_STATIC_MAX_DEVICES];
+static std::mutex g_static_mu;
+
+// Device address of the current GPU's copy of `scratch` (looked up once per
+// device), or null when the lookup fails.
+static zs_spec_static_area* zs_spec_static_area_of(int dev) {
+    if (dev < 0 || dev >= ZS_STATIC_MAX_DEVICES) return nullptr;
+    std::lock_guard<std::mutex> lk(g_static_mu);
+    if (!g_static_area[dev]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return nullptr;
+        g_static_area[dev] = static_cast<zs_spec_static_area*>(p);
+    }
+    return g_static_area[dev];
+}
+
+extern "C" int zs_spec_verify_static(const zs_spec_batch* b, void* stream) {
+    if (!b) return ZS_EINVAL;
+    if (b->B == 0) return ZS_OK;
+    if (b->V == 0 || b->k > ZS_SPEC_KMAX || b->B > ZS_SPEC_STATIC_MAX_ROWS) return ZS_ELIMIT;
+    if (!b->d_target || (b->k && !b->d_draft_ids) || !b->d_temperature || !b->d_seed || !b->d_counter ||
+        !b->d_accepted || !b->d_next)
+        return ZS_EINVAL;
+    if (b->ld < b->V || (b->ld & 3u) || ((uintptr_t)b->d_target & 15u) || ((uintptr_t)b->d_draft & 15u))
+        return ZS_EINVAL;
+    if (b->flags & ~(uint32_t)ZS_SPEC_BACKGROUND) return ZS_EINVAL;
+    const uint32_t k = b->k;
+    const bool draft = k && b->d_draft;
+    const uint64_t npos = draft ? 2ull * k + 1 : (uint64_t)k + 1;
+    const uint64_t nch = (b->V + SP_CH - 1) / SP_CH;
+    if ((uint64_t)b->B * npos * nch > ZS_SPEC_STATIC_MAX_RECORDS) return ZS_ELIMIT;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return ZS_EHIP;
+    zs_spec_static_area* area = zs_spec_static_area_of(dev);
+    if (!area) return ZS_EHIP;
+    zs_spec_args a{};
+    a.B = b->B; a.V = b->V; a.k = k; a.ld = b->ld;
+    a.target = b->d_target; a.draft = k ? b->d_draft : nullptr; a.draft_ids = b->d_draft_ids;
+    a.temperature = b->d_temperature; a.seed = b->d_seed; a.counter = b->d_counter;
+    a.accepted = b->d_accepted; a.next = b->d_next;
+    a.cst = area->cst;        // device address of this GPU's copy
+    a.rs = area->rs;
+    a.nch = (uint32_t)nch;
+    a.npos_max = (uint32_t)npos;
+    a.background = (b->flags & ZS_SPEC_BACKGROUND) ? 1u : 0u;
+    zs_prof prof{0, nullptr, nullptr, nullptr};
+    return zs_spec_launch(a, prof, (hipStream_t)stream) ? ZS_EHIP : ZS_OK;
 }
