@@ -1,0 +1,1621 @@
+// zs_row.hip -- the front of the sampler step, one 1024-thread workgroup per
+// row: everything of a row that needs the whole row, with no other workgroup
+// involved and therefore no device-scope synchronisation and no launch
+// boundary between the phases.
+//
+// Reference semantics (per row, in the order of rest.rs:2594-2624):
+//   x~ = apply_mask(x)                    logit_fsm.rs:247-270 (bans, allow bits)
+//   y  = adjust_logits(x~)                decode_ctrl.rs:107-126
+//   token = sample_with_rng(y, cfg, r)    sampler.rs:31-128
+//   logprobs / token_uncertainty on x~    logprobs.rs:34-54, hallucination.rs:129-154
+//
+// Phases of zs_k_row (row r = blockIdx.x):
+//   P0  patches: the row's ban / bias / count-map entries merged into one list
+//       sorted by id with the exact patched y of every listed id
+//       (decode_ctrl.rs:107-126 operation order), kept in LDS with a bitmap of
+//       the patched ids, and stored for the later kernels;
+//   P1  one read of the logits: observer maximum / NaN / +inf, sampler maximum,
+//       finite count and flags, greedy argmax (last maximal element, a NaN
+//       restarts the fold: sampler.rs:35-43), and candidate lists kept in LDS
+//       behind a rising threshold: the observers' top entries by (x~ desc, id
+//       asc) for top_logprobs / margin, the sampler's top-k by (z desc, id asc)
+//       (sampler.rs:53-64: its k-th key is the threshold), or every finite z
+//       when no top-k applies and at most ZS_SMALL_CAP are finite;
+//   decisions: greedy / non-finite rows get their token; rows whose survivors
+//       fit ZS_SMALL_CAP are sampled exactly by one wave (small_path_wave);
+//       other rows are "big" and continue in zs_sample.hip;
+//   P2  the sequential f32 sums S = sum exp(x~ - max) (observers) and, for big
+//       rows, S = sum exp(z - max) of the sampler (sampler.rs:68), exactly;
+//   P3  the entropy sum of token_uncertainty (hallucination.rs:139-144).
+//
+// Exact sequential sums (P2, P3). The row is walked in tiles of 4096 ids in
+// index order with the exact running sum s known at every tile start: each
+// thread adds its terms' integer increments on the grid of s (zs_math.h), one
+// workgroup reduction gives the tile's total, and s moves by total * grid
+// unless a term of the tile was an exact half-way case (its increment depends
+// on the sum's parity) or the sum leaves its binade inside the tile; such a
+// tile is redone with the exact ordered scan of zs_seq.h. No prediction and
+// no second pass is needed: the grid is always that of the true running sum.
+#include <hip/hip_runtime.h>
+#include "zs_sampler.h"
+
+#define RW_NT 1024
+#define RW_NW (RW_NT / 64)
+#define RW_G 4096          // ids per tile: one float4 per thread
+#define RW_BUF 2048        // candidate buffer entries (per list)
+#define RW_KEEP 256        // a list above this is compacted to its top K
+
+struct rw_shared {
+    uint32_t pid[ZS_MAX_PATCHES];   // patched ids (sorted) | flags << 30
+    float py[ZS_MAX_PATCHES];       // their y
+    union {
+        unsigned long long ent[ZS_MAX_PATCHES];   // P0: merge sort
+        struct {
+            unsigned long long o[RW_BUF];         // P1: observer candidates
+            unsigned long long s[RW_BUF];         // P1: sampler candidates
+        } b;
+        seq_sh<RW_NT> seq;                        // P2 / P3: exact scans
+    } u;
+    float sval[ZS_SMALL_CAP];
+    uint32_t sidx[ZS_SMALL_CAP];
+    uint32_t cand_id[ZS_OBS_CAND];
+    float cand_x[ZS_OBS_CAND];
+    uint32_t ru[6][RW_NW];
+    float rf[3][RW_NW];
+    float fthr[2];                  // candidate thresholds as values
+    float fcut[2];                  // largest values cut from the lists
+    unsigned long long rl[RW_NW];
+    uint32_t grp[2][RW_NW][8];      // P2 / P3: per-wave tile totals (double buffered)
+    uint32_t gsum[2][RW_NW];        // P2 / P3: per-wave group totals (double buffered)
+    uint32_t cross[3][RW_NW];       // crossing path: per-wave prefix totals (RW_NG grids)
+    float head[256];
+    uint32_t n_ent, n_surv, tok;
+    uint32_t ovf[3];                // first tile that lost a list entry, per group slot
+    uint32_t thr_o, thr_s;          // candidate admission thresholds (keys)
+    float fsh;
+    uint32_t pass_g;                // sum passes: the tile left to the ordered scan (or ng)
+    int pass_start;                 // and the first element of it still to add
+};
+// Bitmap of the row's patched ids, ceil(V / 32) words, followed by the number
+// of patched ids before each word (dynamic LDS).
+extern __shared__ uint32_t rw_pbits[];
+
+#define RW_PF_SHIFT 30u
+
+// A value every lane holds equally (read from LDS after a barrier), moved to
+// a scalar register so that the compiler branches on it without exec masks.
+__device__ __forceinline__ uint32_t rw_uni(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ float rw_unif(float v) { return __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(v))); }
+// Sum of a u32 over the wave (no overflow check), uniform: pairs, quads,
+// eights and rows of 16 by DPP permutations, then the rows by broadcasts;
+// lane 63 ends with the total.
+__device__ __forceinline__ uint32_t rw_wave_sum(uint32_t v) {
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xf, 0xf, false);    // quad_perm [1,0,3,2]
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xf, 0xf, false);    // quad_perm [2,3,0,1]
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xf, 0xf, false);   // row_half_mirror
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xf, 0xf, false);   // row_mirror
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false);   // row_bcast:15
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false);   // row_bcast:31
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+// Workgroup barrier that orders LDS accesses only. __syncthreads() also waits
+// for every outstanding global load of the calling wave, which would drain the
+// loads the tile loops keep in flight ahead of the tile being processed.
+__device__ __forceinline__ void rw_bar() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+#ifdef RW_PROF
+__device__ unsigned long long rw_prof[1024][16];
+#define RW_MARK(i) do { if (threadIdx.x == 0) rw_prof[blockIdx.x][i] = wall_clock64(); } while (0)
+#define RW_COUNT(i) do { if (threadIdx.x == 0) rw_prof[blockIdx.x][i]++; } while (0)
+extern "C" int zs_row_prof_read(void* out) { return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(rw_prof), sizeof(rw_prof)); }
+extern "C" int zs_row_prof_clear() { static unsigned long long z[1024][16]; return (int)hipMemcpyToSymbol(HIP_SYMBOL(rw_prof), z, sizeof(z)); }
+#else
+#define RW_MARK(i) do {} while (0)
+#define RW_COUNT(i) do {} while (0)
+#endif
+
+// ---------------------------------------------------------------------------
+// P0: merged patch list (the entries of zs_k_prep's format, plus LDS copies)
+// Entries are (id << 32) | (kind << 28) | order with kind 0 = ban, 1 = bias,
+// 2 = count; sorting groups them by id with bans first and biases in list
+// order, which reproduces the reference's per-token operation sequence.
+// Returns the number of patched ids, or -1 when the row has more entries than
+// ZS_MAX_PATCHES.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int rw_patches(const zs_sargs& a, uint32_t r, const zs_row_params& P, uint32_t& has_y, rw_shared& sh) {
+    const zs_batch& b = a.b;
+    const uint32_t t = threadIdx.x, V = b.V;
+    const uint32_t words = (V + 31) / 32;
+    for (uint32_t i = t; i < words; i += RW_NT) rw_pbits[i] = 0u;
+    const uint32_t ban0 = b.d_ban_off ? b.d_ban_off[r] : 0, ban1 = b.d_ban_off ? b.d_ban_off[r + 1] : 0;
+    const uint32_t bi0 = b.d_bias_off ? b.d_bias_off[r] : 0, bi1 = b.d_bias_off ? b.d_bias_off[r + 1] : 0;
+    uint32_t c0 = b.d_cnt_off ? b.d_cnt_off[r] : 0, c1 = b.d_cnt_off ? b.d_cnt_off[r + 1] : 0;
+    if (!zs_penalty_active(P)) c1 = c0;  // counts only matter when penalties are active
+    const uint32_t nb = ban1 - ban0, nbi = bi1 - bi0, nc = c1 - c0;
+    const uint32_t total = nb + nbi + nc;
+    const uint32_t nsub = (V + ZS_SUB - 1) / ZS_SUB;
+    uint32_t* psub = a.p_sub + (size_t)r * (a.max_subs + 1);
+    if (t == 0) sh.n_ent = 0;
+    __syncthreads();
+    if (total > ZS_MAX_PATCHES) {
+        if (t == 0) a.p_cnt[r] = 0;
+        for (uint32_t j = t; j <= nsub; j += RW_NT) psub[j] = 0;
+        has_y = 0;
+        return -1;
+    }
+    for (uint32_t i = t; i < total; i += RW_NT) {
+        uint32_t id, kind, ord;
+        if (i < nb) { id = b.d_ban_ids[ban0 + i]; kind = 0; ord = i; }
+        else if (i < nb + nbi) { ord = i - nb; id = b.d_bias_ids[bi0 + ord]; kind = 1; }
+        else { ord = i - nb - nbi; id = b.d_cnt_ids[c0 + ord]; kind = 2; }
+        if (id < V) {
+            const uint32_t pos = atomicAdd(&sh.n_ent, 1u);
+            sh.u.ent[pos] = ((unsigned long long)id << 32) | ((unsigned long long)kind << 28) | ord;
+        }
+    }
+    __syncthreads();
+    const uint32_t n = sh.n_ent;
+    uint32_t np2 = 1;
+    while (np2 < n) np2 <<= 1;
+    for (uint32_t i = n + t; i < np2; i += RW_NT) sh.u.ent[i] = ~0ull;
+    __syncthreads();
+    if (np2 > 2 * RW_NT) block_sort_reg_u64<RW_NT, 4>(sh.u.ent, np2);
+    else if (np2 > 1) block_sort_reg_u64<RW_NT, 2>(sh.u.ent, np2);
+    uint32_t* out_id = a.p_id + (size_t)r * ZS_MAX_PATCHES;
+    uint32_t* out_fl = a.p_flags + (size_t)r * ZS_MAX_PATCHES;
+    float* out_y = a.p_y + (size_t)r * ZS_MAX_PATCHES;
+    uint32_t base_out = 0, hy = 0;
+    for (uint32_t s0 = 0; s0 < n; s0 += RW_NT) {
+        const uint32_t i = s0 + t;
+        uint32_t is_start = 0;
+        if (i < n) {
+            const uint32_t id = (uint32_t)(sh.u.ent[i] >> 32);
+            is_start = (i == 0) || ((uint32_t)(sh.u.ent[i - 1] >> 32) != id);
+        }
+        uint32_t tot;
+        const uint32_t ex = block_excl_scan_u<RW_NT>(is_start, sh.ru[0], &tot);
+        if (is_start) {
+            const uint32_t id = (uint32_t)(sh.u.ent[i] >> 32);
+            float x = b.d_logits[(size_t)r * b.ld + id];
+            if ((P.flags & ZS_ROW_MASKED) && b.d_allow_bits && !zs_allowed_bit(b, r, id)) x = -INFINITY;
+            uint32_t fl = 0;
+            uint32_t j = i;
+            // bans (logit_fsm.rs:248-252)
+            while (j < n && (uint32_t)(sh.u.ent[j] >> 32) == id && ((sh.u.ent[j] >> 28) & 3ull) == 0) {
+                fl |= ZS_PF_BAN;
+                j++;
+            }
+            if (fl & ZS_PF_BAN) x = -INFINITY;
+            float y = x;
+            // logit_bias in list order (decode_ctrl.rs:108-112)
+            while (j < n && (uint32_t)(sh.u.ent[j] >> 32) == id && ((sh.u.ent[j] >> 28) & 3ull) == 1) {
+                const uint32_t ord = (uint32_t)(sh.u.ent[j] & 0x0fffffffull);
+                y = y + b.d_bias_vals[bi0 + ord];
+                fl |= ZS_PF_Y;
+                j++;
+            }
+            // penalty (decode_ctrl.rs:113-125): repeat, then frequency * count + presence
+            if (j < n && (uint32_t)(sh.u.ent[j] >> 32) == id && ((sh.u.ent[j] >> 28) & 3ull) == 2) {
+                const uint32_t ord = (uint32_t)(sh.u.ent[j] & 0x0fffffffull);
+                const uint32_t cnt = b.d_cnt_vals[c0 + ord];
+                if (P.repeat != 1.0f) {
+                    if (y > 0.0f) y = y / P.repeat;
+                    else y = y * P.repeat;
+                }
+                float pen_v = __fmul_rn(P.frequency, (float)cnt);
+                pen_v = __fadd_rn(pen_v, P.presence);
+                y = __fsub_rn(y, pen_v);
+                fl |= ZS_PF_Y;
+            }
+            const uint32_t o = base_out + ex;
+            out_id[o] = id;
+            out_fl[o] = fl;
+            out_y[o] = y;
+            sh.pid[o] = id | (fl << RW_PF_SHIFT);
+            sh.py[o] = y;
+            atomicOr(&rw_pbits[id >> 5], 1u << (id & 31));
+            hy |= (fl & ZS_PF_Y) ? 1u : 0u;
+        }
+        base_out += tot;
+    }
+    has_y = block_or_u<RW_NT>(hy, sh.ru[1]);
+    if (t == 0) a.p_cnt[r] = base_out;
+    // per-word prefix counts of the bitmap (words / RW_NT words per thread at most 8)
+    {
+        const uint32_t per = (words + RW_NT - 1) / RW_NT;
+        const uint32_t w0 = t * per;
+        uint32_t c = 0;
+        for (uint32_t w = w0; w < min(w0 + per, words); w++) c += __popc(rw_pbits[w]);
+        uint32_t tot;
+        uint32_t run = block_excl_scan_u<RW_NT>(c, sh.ru[2], &tot);
+        for (uint32_t w = w0; w < min(w0 + per, words); w++) {
+            rw_pbits[words + w] = run;
+            run += __popc(rw_pbits[w]);
+        }
+    }
+    // first patch of every 1024-id sub-chunk (read by zs_k_big / zs_k_final)
+    for (uint32_t j = t; j <= nsub; j += RW_NT) {
+        uint32_t lo = 0, hi = base_out;
+        const uint32_t key = j * ZS_SUB;
+        while (lo < hi) {
+            const uint32_t mid = (lo + hi) >> 1;
+            if ((sh.pid[mid] & ((1u << RW_PF_SHIFT) - 1u)) < key) lo = mid + 1; else hi = mid;
+        }
+        psub[j] = lo;
+    }
+    __syncthreads();
+    return (int)base_out;
+}
+
+// ---------------------------------------------------------------------------
+// Element access: x~ (observers: mask and bans) and z (sampler: patched y,
+// divided by T) of the 4 ids g*RW_G + 4t .. +3.
+// ---------------------------------------------------------------------------
+struct rw_row {
+    const float* row;
+    const uint32_t* allow;
+    const uint32_t* allow_or_row;   // allow bits, or any readable words when unmasked
+    uint32_t V, np, words;
+    uint32_t ldm4, wmax;            // last float4 of the row, last readable word
+    uint32_t amask;                 // 15 for an unmasked row, else 0
+    uint32_t glast;                 // the row's last tile
+};
+struct rw_raw {
+    float4 v;
+    uint32_t w;   // the allow word holding the 4 ids
+};
+// A load through a global-address-space pointer (the host pass of the
+// compiler only parses device code, and has no such address space).
+template <class T>
+__device__ __forceinline__ T rw_gload(const T* p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    return *(const __attribute__((address_space(1))) T*)p;
+#else
+    return *p;
+#endif
+}
+// Loads of tile g for this thread, as global-memory loads (a generic pointer
+// would be loaded with flat instructions, whose completion every LDS wait
+// also waits for). Unconditional, from addresses clamped into the row (rows
+// are ld >= V floats, ld a multiple of 4) and into the allow bitset, so that
+// nothing waits for them before their data is used.
+__device__ __forceinline__ rw_raw rw_fetch(const rw_row& R, uint32_t g) {
+    const uint32_t idx0 = min(g * RW_G + 4 * threadIdx.x, R.ldm4);
+    rw_raw o;
+    typedef float rw_f4 __attribute__((ext_vector_type(4)));
+    const rw_f4 v = rw_gload(reinterpret_cast<const rw_f4*>(R.row + idx0));
+    o.v = make_float4(v.x, v.y, v.z, v.w);
+    o.w = rw_gload(R.allow_or_row + min(idx0 >> 5, R.wmax));
+    return o;
+}
+// The patched ids among the 4 ids from idx0 (bits of pb): bans set x~ and
+// y to -inf, biased or counted ids take their y from the patch list. Their
+// rank in the sorted list is the number of bitmap bits before them (per-word
+// prefix counts follow the bitmap).
+__device__ __forceinline__ void rw_patch4(uint32_t idx0, uint32_t pb, uint32_t words, uint32_t wd, float (&x)[4], float (&y)[4],
+                                       const rw_shared& sh) {
+    uint32_t rank = rw_pbits[words + (idx0 >> 5)] + __popc(wd & ((1u << (idx0 & 31)) - 1u));
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        if (!((pb >> q) & 1u)) continue;
+        const uint32_t fl = sh.pid[rank] >> RW_PF_SHIFT;
+        if (fl & ZS_PF_BAN) { x[q] = -INFINITY; y[q] = -INFINITY; }
+        if (fl & ZS_PF_Y) y[q] = sh.py[rank];
+        rank++;
+    }
+}
+// x~ (observers: mask and bans) and y (sampler: patched, before the
+// temperature) of the 4 ids g*RW_G + 4t .. +3; ids >= V read -inf. Branch
+// free but for two uniform tests (the row's last tile, patches in the row)
+// and the rare threads holding a patched id.
+__device__ __forceinline__ void rw_elems(const rw_row& R, uint32_t g, const rw_raw& raw, float (&x)[4], float (&y)[4],
+                                         const rw_shared& sh) {
+    const uint32_t idx0 = g * RW_G + 4 * threadIdx.x;
+    const uint32_t aw = (raw.w >> (idx0 & 31)) | R.amask;   // amask: 15 when unmasked
+    x[0] = (aw & 1u) ? raw.v.x : -INFINITY;
+    x[1] = (aw & 2u) ? raw.v.y : -INFINITY;
+    x[2] = (aw & 4u) ? raw.v.z : -INFINITY;
+    x[3] = (aw & 8u) ? raw.v.w : -INFINITY;
+    const bool last = g >= R.glast;   // uniform
+    if (last) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) x[q] = idx0 + q < R.V ? x[q] : -INFINITY;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; q++) y[q] = x[q];
+    if (R.np) {
+        const uint32_t wi = min(idx0 >> 5, R.words - 1);
+        const uint32_t wd = rw_pbits[wi];
+        uint32_t pb = (wd >> (idx0 & 31)) & 15u;
+        if (last) pb = idx0 < R.V ? pb : 0u;
+        if (pb) rw_patch4(idx0, pb, R.words, wd, x, y, sh);
+    }
+}
+
+// Calls f(g, u, x, y) for the tiles from g_begin in order, in groups of four
+// (u = 0..3, a constant in each unrolled copy: per-tile state of a group can
+// live in registers indexed by u), with four tiles of loads in flight:
+// unrolled by four so that each load stays in its own registers until used
+// (copying a register whose load is outstanding waits for every load). f
+// returns true (uniformly) to stop; rw_stream then returns that tile's index,
+// else ng. The last group is padded with tiles past the row (ids >= V only),
+// which f must treat as neutral. f must not call functions: a call inside the
+// loop saves the registers of the loads in flight, which waits for them.
+template <class F>
+__device__ __forceinline__ uint32_t rw_stream(const rw_row& R, const rw_shared& sh, uint32_t g_begin, const F& f) {
+    const uint32_t ng = (R.V + RW_G - 1) / RW_G;
+    rw_raw raw[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) raw[u] = rw_fetch(R, min(g_begin + (uint32_t)u, ng - 1));
+    for (uint32_t g0 = g_begin; g0 < ng; g0 += 4) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const uint32_t g = g0 + u;
+            float x[4], y[4];
+            rw_elems(R, g, raw[u], x, y, sh);
+            raw[u] = rw_fetch(R, min(g + 4, ng - 1));
+            __asm__ volatile("" ::: "memory");   // keep the loads issued here, ahead of their use
+            if (rw_uni(f(g, u, x, y) ? 1u : 0u)) return g;
+        }
+    }
+    return ng;
+}
+
+// The elements of one tile (the tile a stream stopped at).
+__device__ __forceinline__ void rw_tile(const rw_row& R, const rw_shared& sh, uint32_t g, float (&x)[4], float (&y)[4]) {
+    const rw_raw raw = rw_fetch(R, g);
+    rw_elems(R, g, raw, x, y, sh);
+}
+
+// ---------------------------------------------------------------------------
+// Candidate lists (P1). Entries are ((~key) << 32) | id: ascending order is
+// key descending, id ascending (Rust's stable descending sort on total_cmp).
+// A list admits the elements whose key exceeds its threshold (the key of its
+// K-th entry once known); when it holds more than RW_KEEP entries it is
+// sorted and cut to its first K, raising the threshold. Elements equal to the
+// threshold that arrive later have larger ids than the K entries at or above
+// it, so they can never enter the first K.
+// ---------------------------------------------------------------------------
+struct rw_list {
+    unsigned long long* buf;
+    uint32_t* cnt;      // [3] per-tile reservation counters (rotating)
+    long long* thr;     // admission threshold: keys > thr enter
+    uint32_t* flag;     // bit 0: the last compaction cut entries equal to its K-th key
+};
+
+// Sort the n entries of a list, dropping those of ids >= idlim (their tiles
+// are streamed again), and keep the first K; the K-th key becomes the
+// threshold (below K entries: every id is admitted). Also records the value
+// of the threshold, whether entries equal to the K-th key were cut, and the
+// largest value cut (into *cutmax).
+// Returns the new entry count. Called by every thread.
+__device__ __noinline__ uint32_t rw_compact(const rw_list& L, uint32_t n, uint32_t K, uint32_t idlim, float* fthr,
+                                            float* cutmax) {
+    RW_COUNT(10);
+    uint32_t np2 = 1;
+    while (np2 < n) np2 <<= 1;
+    for (uint32_t i = threadIdx.x; i < np2; i += RW_NT)
+        if (i >= n || (uint32_t)L.buf[i] >= idlim) L.buf[i] = ~0ull;
+    __syncthreads();
+    block_sort_reg_u64<RW_NT, 2>(L.buf, np2);
+    // entries that remain: those before the first ~0
+    uint32_t c = 0;
+    for (uint32_t i = threadIdx.x; i < np2; i += RW_NT) c += L.buf[i] != ~0ull ? 1u : 0u;
+    __shared__ uint32_t cs[RW_NW];
+    c = block_sum_u<RW_NT>(c, cs);
+    const uint32_t keep = min(c, K);
+    if (threadIdx.x == 0) {
+        if (c >= K) {
+            const uint32_t kk = ~(uint32_t)(L.buf[K - 1] >> 32);
+            *L.thr = (long long)kk;
+            *fthr = zs_key_to_float(kk);
+            *L.flag = (c > K && ~(uint32_t)(L.buf[K] >> 32) == kk) ? 1u : 0u;
+            if (c > K) *cutmax = fmaxf(*cutmax, zs_key_to_float(~(uint32_t)(L.buf[K] >> 32)));
+        } else {
+            *L.thr = -1;
+            *fthr = -INFINITY;
+            *L.flag = 0u;
+        }
+    }
+    __syncthreads();
+    return keep;
+}
+
+// Writes the admitted elements (bit q of m = element q: key kk[q], id idx0 +
+// q) at base + their reservation on counter ctr; an element whose place is
+// past the buffer is not written and its tile is reported in *ovf (the lowest
+// such tile is streamed again after a compaction).
+__device__ __forceinline__ void rw_admit(const rw_list& L, uint32_t* ctr, uint32_t base, uint32_t m,
+                                         const uint32_t (&kk)[4], uint32_t idx0, uint32_t g, uint32_t* ovf) {
+    const uint32_t n = __popc(m);
+    uint32_t p = base + atomicAdd(ctr, n);
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        if (!((m >> q) & 1u)) continue;
+        if (p < RW_BUF) L.buf[p] = ((unsigned long long)(~kk[q]) << 32) | (idx0 + q);
+        else atomicMin(ovf, g);
+        p++;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Exact sequential sums (P2, P3)
+//
+// A tile's terms are added to the running sum s on the grid g = ulp(s) of its
+// binade: each adds the integer round_half_even(t / g) (zs_math.h). Fast
+// path: every thread sums its four increments, one reduction gives the tile
+// total, and s moves by total * g when the sum stays in its binade. A tile
+// where the sum leaves its binade takes the crossing path (rw_cross): the
+// increments on RW_NG consecutive grids are prefix-scanned at once, each
+// crossing is located in the prefix of its grid and added as a real f32
+// addition, and the walk continues on the next grid. Terms with an exact
+// half-way increment (whose rounding depends on the sum's parity), and sums
+// still below 2^-126, take the ordered scan of zs_seq.h (rw_slow).
+// ---------------------------------------------------------------------------
+#define RW_NG 3
+#define RW_QCAP 33554432.0f   // increments are clamped to 2^25 (any larger one crosses the binade)
+#define RW_QFLAG (1u << 28)   // a tile total that forces the crossing path
+
+// 2^(150-eg) = 1 / grid as an exact f32, or 0 when the grid is finer than
+// f32 scaling reaches (sums below 2^-126).
+__device__ __forceinline__ float rw_scale(int eg) {
+    return (eg >= 24 && eg <= 276) ? __uint_as_float((uint32_t)(277 - eg) << 23) : 0.0f;
+}
+
+// exp(d) from the fast exp (relative error below ZS_EXP_EPS), 0 below the
+// fast range; `sub` is set where the exact result is subnormal or the
+// argument is in the fast exp's excluded range (those terms need zs_expf).
+__device__ __forceinline__ float rw_fexp(float d, uint32_t& sub) {
+    const float e = zs_exp_fast(fmaxf(d, ZS_EXP_FAST_MIN));
+    sub |= (d < ZS_EXP_FAST_MIN && d >= ZS_EXP_ZERO) ? 1u : 0u;
+    return d >= ZS_EXP_FAST_MIN ? e : 0.0f;
+}
+
+// H term -(p * ((l - max) - ln S)), p = exp(l - max) * inv, 0 unless p > 0
+// (hallucination.rs:142-143), with the fast exp (a tolerance output) and
+// glibc's exp where the fast exp does not cover the argument.
+__device__ __forceinline__ float rw_hterm_exact(float d, float inv, float lns) {
+    uint32_t sub = 0;
+    float e = rw_fexp(d, sub);
+    if (sub) e = zs_expf(d);
+    const float p = e * inv;
+    return p > 0.0f ? -(p * (d - lns)) : 0.0f;
+}
+
+// Ordered exact scan of a tile of values from running sum s (elements >=
+// start), zs_seq.h. A sum that is still zero starts at its first nonzero
+// term, and its next 256 terms are added serially by one thread (the sum
+// climbs through many binades there).
+__device__ __noinline__ float rw_slow(float v0, float v1, float v2, float v3, int start, float s, rw_shared& sh) {
+    const float v[4] = {v0, v1, v2, v3};
+    const int t = (int)threadIdx.x;
+    if (s == 0.0f) {
+        int first = ZS_BIGI;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (first == ZS_BIGI && 4 * t + j >= start && v[j] != 0.0f) first = 4 * t + j;
+        first = block_min_i<RW_NT>(first, reinterpret_cast<int*>(sh.ru[5]));
+        if (first == ZS_BIGI) return s + 0.0f;  // only zero terms: the sum is +0
+        const int e0 = first, e1 = min(first + 256, RW_G);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int e = 4 * t + j;
+            if (e >= e0 && e < e1) sh.head[e - e0] = v[j];
+        }
+        __syncthreads();
+        if (t == 0) {
+            float acc = s;
+            for (int i = 0; i < e1 - e0; i++) acc = acc + sh.head[i];
+            sh.fsh = acc;
+        }
+        __syncthreads();
+        s = sh.fsh;
+        __syncthreads();
+        start = e1;
+    }
+    if (start < RW_G) {
+        seq_terms<4> f(v);
+        seq_group_f<RW_NT, 4>(f, start, s, NAN, sh.u.seq);
+    }
+    return s;
+}
+
+// Saturating add for the crossing path's prefixes: increments are at most
+// 2^25, so a thread's four stay below 2^27, and a cap of 2^30 keeps every
+// prefix a crossing search compares exact up to the crossing (a prefix is
+// only ever subtracted from a larger one on the same grid, and the prefix at
+// a crossing is below 2^27).
+__device__ __forceinline__ uint32_t rw_sat(uint32_t a, uint32_t b) {
+    const uint32_t c = a + b;
+    return c > (1u << 30) ? (1u << 30) : c;
+}
+
+// Crossing path: the tile's values from running sum s (elements >= start),
+// with the increments on RW_NG grids prefix-scanned at once. Exact sums
+// (`ties` = 1) go to the ordered scan when a term is an exact half-way case.
+__device__ __forceinline__ float rw_cross(const float (&v)[4], int& start, float s, uint32_t ties, bool& slow,
+                                          rw_shared& sh) {
+    const int t = (int)threadIdx.x, lane = zs_lane(), wid = zs_wid();
+    slow = false;
+    while (start < RW_G) {
+        if (s == 0.0f) {
+            // a zero sum takes the first nonzero term as it is (zero terms
+            // before it leave a zero; -0 + +0 = +0 is restored at the end)
+            int first = ZS_BIGI;
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                if (first == ZS_BIGI && 4 * t + q >= start && v[q] != 0.0f) first = 4 * t + q;
+            first = block_min_i<RW_NT>(first, reinterpret_cast<int*>(sh.ru[5]));
+            if (first == ZS_BIGI) return s + 0.0f;
+            if (t == first / 4) {
+                float ve = v[0];
+#pragma unroll
+                for (int q = 1; q < 4; q++) ve = q == first % 4 ? v[q] : ve;
+                sh.fsh = ve;
+            }
+            __syncthreads();
+            s = (s + 0.0f) + sh.fsh;
+            __syncthreads();
+            start = first + 1;
+            continue;
+        }
+        const int eg0 = zs_grid_exp(s);
+        if (rw_scale(eg0) == 0.0f) { slow = true; return s; }
+        // per-thread increments on grids eg0 .. eg0 + RW_NG - 1
+        uint32_t inc[RW_NG][4], tot[RW_NG];
+        uint32_t tie = 0;
+#pragma unroll
+        for (int j = 0; j < RW_NG; j++) {
+            const float sc = rw_scale(eg0 + j);
+            tot[j] = 0;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const float qv = (4 * t + q >= start) ? fminf(v[q] * sc, RW_QCAP) : 0.0f;
+                const float rq = rintf(qv);
+                tie |= (fabsf(qv - rq) == 0.5f) ? 1u : 0u;
+                inc[j][q] = (uint32_t)rq;
+                tot[j] = rw_sat(tot[j], inc[j][q]);
+            }
+        }
+        if (ties && __syncthreads_or(tie)) { slow = true; return s; }
+        // exclusive prefix of the thread totals over the workgroup, per grid
+        uint32_t pre[RW_NG];
+#pragma unroll
+        for (int j = 0; j < RW_NG; j++) {
+            uint32_t x = tot[j];
+            for (int d = 1; d < 64; d <<= 1) {
+                const uint32_t y = __shfl_up(x, d, 64);
+                if (lane >= d) x = rw_sat(x, y);
+            }
+            pre[j] = x;   // inclusive within the wave for now
+            if (lane == 63) sh.cross[j][wid] = x;
+        }
+        __syncthreads();
+        uint32_t wtot[RW_NG];
+#pragma unroll
+        for (int j = 0; j < RW_NG; j++) {
+            uint32_t before = 0, all = 0;
+            for (int w = 0; w < RW_NW; w++) {
+                const uint32_t c = sh.cross[j][w];
+                if (w < wid) before = rw_sat(before, c);
+                all = rw_sat(all, c);
+            }
+            pre[j] = rw_sat(before, pre[j] - tot[j]);   // exclusive prefix of this thread
+            wtot[j] = all;
+        }
+        __syncthreads();
+        // walk: running sum k on grid eg0 + j from element position P (the
+        // prefix of grid j before P is base); the grid index is a
+        // compile-time constant in every step, so the increments stay in
+        // registers
+        uint32_t k = zs_grid_k(s), base = 0;
+        int P = start;
+        bool done = false, next = true;
+#pragma unroll
+        for (int j = 0; j < RW_NG; j++) {
+            if (!next) break;
+            next = false;
+            // first element e >= P whose inclusive prefix reaches the binade end
+            int my = ZS_BIGI;
+            uint32_t run = pre[j];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                run = rw_sat(run, inc[j][q]);
+                if (my == ZS_BIGI && 4 * t + q >= P && (uint64_t)k + (run - base) >= ZS_BINADE) my = 4 * t + q;
+            }
+            const int e = block_min_i<RW_NT>(my, reinterpret_cast<int*>(sh.ru[5]));
+            if (e == ZS_BIGI) {
+                s = zs_grid_value(k + (wtot[j] - base), eg0 + j);
+                done = true;
+                break;
+            }
+            // the crossing term as a real f32 addition (its owner)
+            if (t == e / 4) {
+                const int eq = e % 4;
+                uint32_t ex = pre[j];
+                uint32_t nb = pre[j + 1 < RW_NG ? j + 1 : j];
+                float ve = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    if (q < eq) ex = rw_sat(ex, inc[j][q]);
+                    if (q <= eq && j + 1 < RW_NG) nb = rw_sat(nb, inc[j + 1 < RW_NG ? j + 1 : j][q]);
+                    ve = q == eq ? v[q] : ve;
+                }
+                sh.fsh = zs_grid_value(k + (ex - base), eg0 + j) + ve;
+                sh.ru[4][0] = nb;   // prefix of grid j + 1 through e
+            }
+            __syncthreads();
+            s = sh.fsh;
+            const uint32_t nb = sh.ru[4][0];
+            __syncthreads();
+            P = e + 1;
+            if (j + 1 < RW_NG && zs_grid_exp(s) == eg0 + j + 1) {
+                k = zs_grid_k(s);
+                base = nb;
+                next = true;
+            }
+            // otherwise past the prepared grids (or a jump over a binade):
+            // rescan from P
+        }
+        if (done) return s;
+        start = P;
+    }
+    return s;
+}
+
+// End of a group of four tiles: per-thread per-tile increment totals q[u]
+// and flag bits (bit u: tile u needs the ordered path) in; the workgroup
+// totals per tile and the OR'ed flags out (a slot that alternates between
+// groups, so one LDS-only barrier suffices).
+__device__ __forceinline__ void rw_group_reduce(uint32_t (&q)[4], uint32_t& f, uint32_t parity, rw_shared& sh) {
+    for (int d = 32; d > 0; d >>= 1) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) q[u] = zs_sat_add(q[u], __shfl_xor(q[u], d, 64));
+        f |= __shfl_xor(f, d, 64);
+    }
+    uint4* R4 = reinterpret_cast<uint4*>(&sh.grp[parity][0][0]);
+    if (zs_lane() == 0) {
+        R4[2 * zs_wid() + 0] = make_uint4(q[0], q[1], q[2], q[3]);
+        R4[2 * zs_wid() + 1] = make_uint4(f, 0u, 0u, 0u);
+    }
+    rw_bar();
+#pragma unroll
+    for (int u = 0; u < 4; u++) q[u] = 0;
+    f = 0;
+#pragma unroll
+    for (int w = 0; w < RW_NW; w++) {
+        const uint4 A = R4[2 * w + 0];
+        q[0] = zs_sat_add(q[0], A.x); q[1] = zs_sat_add(q[1], A.y);
+        q[2] = zs_sat_add(q[2], A.z); q[3] = zs_sat_add(q[3], A.w);
+        f |= R4[2 * w + 1].x;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) q[u] = rw_uni(q[u]);
+    f = rw_uni(f);
+}
+
+// First tile of a group whose totals carry the sum k out of its binade or
+// that is flagged (4: none); *pre = the increments of the tiles before it.
+__device__ __forceinline__ int rw_group_first(const uint32_t (&q)[4], uint32_t f, uint32_t k, uint32_t* pre) {
+    uint32_t run = 0;
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        if (((f >> u) & 1u) || k + zs_sat_add(run, q[u]) >= ZS_BINADE) { *pre = run; return u; }
+        run = zs_sat_add(run, q[u]);
+    }
+    *pre = run;
+    return 4;
+}
+
+// Increments of four values on the grid of scale sc (a positive scale: the
+// sum pass sends tiles on finer grids to the crossing path). Each is at most
+// 2^25, so the total does not overflow.
+__device__ __forceinline__ uint32_t rw_inc4(const float (&v)[4], float sc) {
+    uint32_t sum = 0;
+#pragma unroll
+    for (int q = 0; q < 4; q++) sum += (uint32_t)rintf(fminf(v[q] * sc, RW_QCAP));
+    return sum;
+}
+
+// Certified increments of exact terms exp(d) from their fast-exp values a
+// (relative error below ZS_EXP_EPS): where |q - rint(q)| is within q * eps of
+// one half the term is recomputed with glibc's algorithm; an exact half-way
+// increment sets fl (its rounding depends on the sum's parity: the ordered
+// path). Arguments below the fast exp's range were clamped to it: the sum
+// pass only takes this path on grids where such terms round to 0 either way.
+__device__ __forceinline__ uint32_t rw_inc4_cert(const float (&a)[4], const float (&d)[4], float sc, uint32_t& fl) {
+    uint32_t unc = 0;
+    float qv[4], rq[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        qv[q] = fminf(a[q] * sc, RW_QCAP);
+        rq[q] = rintf(qv[q]);
+        const bool u = fmaf(qv[q], (float)ZS_EXP_EPS, fabsf(qv[q] - rq[q])) >= 0.5f && qv[q] < RW_QCAP;
+        unc |= u ? (1u << q) : 0u;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        if (unc & (1u << q)) {   // rare
+            const float qe = fminf(zs_expf(d[q]) * sc, RW_QCAP);
+            rq[q] = rintf(qe);
+            if (fabsf(qe - rq[q]) == 0.5f) fl |= 1u;
+        }
+    }
+    uint32_t sum = 0;
+#pragma unroll
+    for (int q = 0; q < 4; q++) sum += (uint32_t)rq[q];
+    return sum;
+}
+
+// One exact sequential sum over the row (P2, P3): F gives the terms of a
+// tile (values and per-tile flags, for the fast path) and the terms of the
+// crossing path. Tiles are added in groups of four on the grid of the sum at
+// the group start; a group whose tile carries the sum out of its binade (or
+// is flagged) stops the stream at that tile, adds the tiles before it, and
+// that tile takes the crossing path (rw_cross).
+template <class F>
+__device__ __forceinline__ float rw_sum_pass(const rw_row& R, rw_shared& sh, float s, uint32_t ties, const F& f,
+                                             uint32_t g) {
+    uint32_t stop = 0, gpar = 0;
+    bool stopped = false;
+    const uint32_t ng = (R.V + RW_G - 1) / RW_G;
+    uint32_t qt[4] = {0u, 0u, 0u, 0u};
+    int eg = 0;
+    float sc = 0.0f;
+    while (g < ng) {
+        g = rw_stream(R, sh, g, [&](uint32_t g, int u, const float (&x)[4], const float (&y)[4]) {
+            if (u == 0) {
+                eg = zs_grid_exp(s);
+                sc = rw_scale(eg);
+            }
+            uint32_t tf = 0;
+            qt[u] = f.fast(x, y, sc, tf);
+            if (tf) qt[u] = RW_QFLAG;   // a flagged tile reads as a crossing
+            if (u != 3) return false;
+            // the group's total first (one value per thread); the tiles'
+            // totals only when the sum leaves its binade in the group
+            const uint32_t k = zs_grid_k(s);
+            const uint32_t w = min(rw_wave_sum(min(qt[0] + qt[1] + qt[2] + qt[3], ZS_BINADE)), ZS_BINADE);
+            if (zs_lane() == 0) sh.gsum[gpar][zs_wid()] = w;
+            rw_bar();
+            uint32_t tot = 0;
+#pragma unroll
+            for (int v = 0; v < RW_NW; v++) tot += sh.gsum[gpar][v];
+            tot = rw_uni(tot);
+            // grids finer than f32 scaling reaches, or on which terms below
+            // the fast exp's range could round up: the crossing path
+            const bool fine = sc == 0.0f || sc >= F::sc_max;
+            if (!fine && k + tot < ZS_BINADE) {
+                s = zs_grid_value(k + tot, eg);
+                gpar ^= 1u;
+                return false;
+            }
+            uint32_t pre = 0, fl = 0;
+            int c = 0;
+            if (!fine) {
+                rw_group_reduce(qt, fl, gpar, sh);
+                c = rw_group_first(qt, fl, k, &pre);
+            }
+            gpar ^= 1u;
+            s = zs_grid_value(k + pre, eg);
+            stop = g - 3 + (uint32_t)c;
+            stopped = true;
+            return true;
+        });
+        // (the stop tile is below ng even when the group's last tile is not)
+        if (!stopped) break;
+        stopped = false;
+        g = rw_uni(stop);
+        RW_COUNT(8);
+        float x[4], y[4];
+        rw_tile(R, sh, g, x, y);
+        float v[4];
+        f.exact(x, y, v);
+        int start = 0;
+        bool slow = false;
+#ifdef RW_PROF
+        const unsigned long long c0 = wall_clock64();
+#endif
+        s = rw_cross(v, start, s, ties, slow, sh);
+#ifdef RW_PROF
+        if (threadIdx.x == 0) rw_prof[blockIdx.x][13] += wall_clock64() - c0;
+#endif
+        if (slow) {
+            // the ordered scan (zs_seq.h) finishes this tile outside
+            if (threadIdx.x == 0) { sh.pass_g = g; sh.pass_start = start; }
+            __syncthreads();
+            return s;
+        }
+        g++;
+    }
+    if (threadIdx.x == 0) sh.pass_g = ng;
+    __syncthreads();
+    return s;
+}
+
+// Terms of the observers' S: exp(x~ - max) with the fast exp (a tolerance
+// output), glibc's exp for arguments the fast exp does not cover.
+struct rw_obs_terms {
+    float M;
+    // grids on which the fast path holds: a term below the fast exp's range
+    // (below 2^-125) then rounds to 0
+    static constexpr float sc_max = 0x1p123f;
+    __device__ __forceinline__ uint32_t fast(const float (&x)[4], const float (&)[4], float sc, uint32_t&) const {
+        float v[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) v[q] = zs_exp_fast(fmaxf(x[q] - M, ZS_EXP_FAST_MIN));
+        return rw_inc4(v, sc);
+    }
+    __device__ __forceinline__ void exact(const float (&x)[4], const float (&)[4], float (&v)[4]) const {
+        uint32_t sub = 0;
+#pragma unroll
+        for (int q = 0; q < 4; q++) v[q] = rw_fexp(x[q] - M, sub);
+        if (sub) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) v[q] = zs_expf(x[q] - M);
+        }
+    }
+};
+
+// Terms of the sampler's S (sampler.rs:68): expf(z - max) exactly, z = y / T,
+// 0 below the top-k threshold.
+struct rw_samp_terms {
+    float T, rT, zmax, thr;
+    bool use_thr;
+    uint32_t div;   // 0: T = 1 (no division), 1: Markstein's division, 2: IEEE division
+    // z = y / T correctly rounded (sampler.rs:47-51). With rT = RN(1 / T),
+    // q0 = RN(y * rT) is within an ulp of y / T, the remainder y - q0 * T is
+    // exact in one fma, and RN(q0 + r * rT) is RN(y / T) (Markstein's
+    // theorem) while nothing underflows or overflows: for 2^-100 <= |y| <=
+    // 2^100 and 2^-20 <= T <= 2^20. Zeros and infinities divide exactly as
+    // y * rT; other y divide the IEEE way.
+    __device__ __forceinline__ float temper(float y) const {
+        if (div == 0u) return y;
+        if (div == 2u) return y / T;
+        const float q0 = y * rT;
+        const float q1 = fmaf(fmaf(-q0, T, y), rT, q0);
+        const float a = fabsf(y);
+        const bool mid = a >= 0x1p-100f && a <= 0x1p100f;
+        float z = mid ? q1 : q0;
+        if (!mid && a != 0.0f && a != INFINITY) z = y / T;   // rare
+        return z;
+    }
+    __device__ __forceinline__ void args(const float (&y)[4], float (&d)[4]) const {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            float z = temper(y[q]);
+            if (use_thr && z < thr) z = -INFINITY;
+            d[q] = z - zmax;
+        }
+    }
+    static constexpr float sc_max = 0x1p123f;
+    __device__ __forceinline__ uint32_t fast(const float (&)[4], const float (&y)[4], float sc, uint32_t& fl) const {
+        float d[4], a[4];
+        args(y, d);
+#pragma unroll
+        for (int q = 0; q < 4; q++) a[q] = zs_exp_fast(fmaxf(d[q], ZS_EXP_FAST_MIN));
+        return rw_inc4_cert(a, d, sc, fl);
+    }
+    __device__ __forceinline__ void exact(const float (&)[4], const float (&y)[4], float (&v)[4]) const {
+        float d[4];
+        args(y, d);
+#pragma unroll
+        for (int q = 0; q < 4; q++) v[q] = zs_expf(d[q]);
+    }
+};
+
+// Terms of the entropy (hallucination.rs:139-144), fast exp (a tolerance output).
+struct rw_ent_terms {
+    float M, inv, lns;
+    // a term with an argument below the fast exp's range is below
+    // 2^-125.5 * (104 + ln S) < 2^-118 (S >= 1, ln S < 13): 0 on these grids
+    static constexpr float sc_max = 0x1p116f;
+    __device__ __forceinline__ uint32_t fast(const float (&x)[4], const float (&)[4], float sc, uint32_t&) const {
+        float v[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float d = fmaxf(x[q] - M, ZS_EXP_FAST_MIN);
+            const float p = zs_exp_fast(d) * inv;
+            v[q] = p > 0.0f ? -(p * (d - lns)) : 0.0f;
+        }
+        return rw_inc4(v, sc);
+    }
+    __device__ __forceinline__ void exact(const float (&x)[4], const float (&)[4], float (&v)[4]) const {
+#pragma unroll
+        for (int q = 0; q < 4; q++) v[q] = rw_hterm_exact(x[q] - M, inv, lns);
+    }
+};
+
+// The workgroup's LDS (one object, so that functions outside the kernel
+// address it directly).
+__shared__ rw_shared rw_sh;
+
+// The sum passes as functions of their own: a pass's loop then holds only
+// its own values (the kernel's live values are saved once around the call,
+// not reloaded in every tile). Arguments arrive in vector registers and are
+// made uniform first.
+__device__ __forceinline__ const float* rw_uni_ptr(const float* p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    return reinterpret_cast<const float*>(((uint64_t)rw_uni((uint32_t)(v >> 32)) << 32) | rw_uni((uint32_t)v));
+}
+__device__ __forceinline__ rw_row rw_row_of(const float* row, const float* allow, uint32_t V, uint32_t np, uint32_t ldm4) {
+    rw_row R;
+    R.row = rw_uni_ptr(row);
+    R.allow = reinterpret_cast<const uint32_t*>(rw_uni_ptr(allow));
+    R.V = rw_uni(V);
+    R.np = rw_uni(np);
+    R.words = (R.V + 31) / 32;
+    R.ldm4 = rw_uni(ldm4);
+    R.allow_or_row = R.allow ? R.allow : reinterpret_cast<const uint32_t*>(R.row);
+    R.wmax = R.allow ? R.words - 1 : R.ldm4;
+    R.amask = R.allow ? 0u : 15u;
+    R.glast = (R.V - 1) / RW_G;
+    return R;
+}
+// The ordered scan of one tile (a sum pass stopped there): the tile's
+// exact terms from element `start`, from running sum s.
+template <class F>
+__device__ __forceinline__ float rw_slow_tile(const rw_row& R, const F& f, uint32_t g, int start, float s) {
+    float x[4], y[4], v[4];
+    rw_tile(R, rw_sh, g, x, y);
+    f.exact(x, y, v);
+    return rw_slow(v[0], v[1], v[2], v[3], start, s, rw_sh);
+}
+// One sum pass from tile g with running sum s: the streaming pass, or
+// (slow != 0) the ordered scan of tile g from the element the pass left in
+// the shared state. The pass leaves in pass_g the tile it could not finish
+// (ng: none).
+template <class F>
+__device__ __forceinline__ float rw_pass(const rw_row& R, const F& f, float s, uint32_t g, uint32_t slow,
+                                         uint32_t ties) {
+#ifdef RW_PROF
+    if (rw_uni(slow)) {
+        const unsigned long long c0 = wall_clock64();
+        const float r = rw_slow_tile(R, f, rw_uni(g), rw_sh.pass_start, rw_unif(s));
+        if (threadIdx.x == 0) { rw_prof[blockIdx.x][14] += wall_clock64() - c0; rw_prof[blockIdx.x][9]++; }
+        return r;
+    }
+#else
+    if (rw_uni(slow)) return rw_slow_tile(R, f, rw_uni(g), rw_sh.pass_start, rw_unif(s));
+#endif
+    return rw_sum_pass(R, rw_sh, rw_unif(s), ties, f, rw_uni(g));
+}
+__device__ __noinline__ float rw_pass_obs(const float* row, const float* allow, uint32_t V, uint32_t np, uint32_t ldm4,
+                                          float M, float s, uint32_t g, uint32_t slow) {
+    rw_obs_terms f;
+    f.M = rw_unif(M);
+    return rw_pass(rw_row_of(row, allow, V, np, ldm4), f, s, g, slow, 0u);
+}
+__device__ __noinline__ float rw_pass_samp(const float* row, const float* allow, uint32_t V, uint32_t np, uint32_t ldm4,
+                                           float T, float zmax, float thr, uint32_t use_thr, float s, uint32_t g,
+                                           uint32_t slow) {
+    rw_samp_terms f;
+    f.T = rw_unif(T);
+    f.rT = 1.0f / f.T;
+    f.div = !(f.T > 0.0f && f.T != 1.0f) ? 0u : ((f.T >= 0x1p-20f && f.T <= 0x1p20f) ? 1u : 2u);
+    f.zmax = rw_unif(zmax);
+    f.thr = rw_unif(thr);
+    f.use_thr = rw_uni(use_thr) != 0u;
+    return rw_pass(rw_row_of(row, allow, V, np, ldm4), f, s, g, slow, 1u);
+}
+__device__ __noinline__ float rw_pass_ent(const float* row, const float* allow, uint32_t V, uint32_t np, uint32_t ldm4,
+                                          float M, float inv, float lns, float s, uint32_t g, uint32_t slow) {
+    rw_ent_terms f;
+    f.M = rw_unif(M);
+    f.inv = rw_unif(inv);
+    f.lns = rw_unif(lns);
+    return rw_pass(rw_row_of(row, allow, V, np, ldm4), f, s, g, slow, 0u);
+}
+
+// Exact sampling of a small survivor set by wave 0 (token to sh.tok).
+__device__ __noinline__ void rw_small(uint64_t seed, uint64_t counter, uint32_t V, const zs_row_params& P, uint32_t nsv,
+                                      float zmax, rw_shared& sh) {
+    const uint32_t tk = nsv <= 64 ? small_path_wave<1>(seed, counter, V, P, nsv, zmax, sh.sval, sh.sidx)
+                                  : small_path_wave<ZS_SMALL_CAP / 64>(seed, counter, V, P, nsv, zmax, sh.sval, sh.sidx);
+    if (threadIdx.x == 0) sh.tok = tk;
+}
+
+// ---------------------------------------------------------------------------
+// zs_k_row
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
+    const uint32_t r = blockIdx.x;
+    const uint32_t t = threadIdx.x;
+    const zs_batch& b = a.b;
+    const uint32_t V = b.V;
+    rw_shared& sh = rw_sh;
+    __shared__ uint32_t cnt_o[3], cnt_s[3], flag_o, flag_s;
+    __shared__ long long thr_o, thr_s;
+    const zs_row_params P = b.d_params[r];
+    zs_row_state& st = a.rst[r];
+    const float T = P.temperature;
+    const bool want_lp = (P.flags & ZS_ROW_LOGPROBS) != 0;
+    const bool want_unc = (P.flags & ZS_ROW_UNCERTAINTY) != 0;
+    const bool want_obs = want_lp || want_unc;
+    RW_MARK(0);
+
+    // ---------------- P0: patches
+    uint32_t has_y = 0;
+    const int np = rw_patches(a, r, P, has_y, sh);
+    if (np < 0) {
+        if (t == 0) {
+            st.status = ZS_ST_LIMIT;
+            st.mode = ZS_MODE_DONE;
+            st.token = 0xffffffffu;
+            st.obs_need = 0;
+            st.rounds = 0;
+            st.n_cand = 0;
+            st.klist = 0;
+            st.kpend = 0;
+        }
+        return;
+    }
+    RW_MARK(5);
+    rw_row R;
+    R.row = b.d_logits + (size_t)r * b.ld;
+    R.allow = ((P.flags & ZS_ROW_MASKED) && b.d_allow_bits) ? b.d_allow_bits + (size_t)r * b.allow_words : nullptr;
+    R.V = V;
+    R.np = rw_uni((uint32_t)np);
+    R.words = (V + 31) / 32;
+    R.ldm4 = (uint32_t)min((uint64_t)b.ld - 4, (uint64_t)0xfffffff0u);
+    R.allow_or_row = R.allow ? R.allow : reinterpret_cast<const uint32_t*>(R.row);
+    R.wmax = R.allow ? R.words - 1 : R.ldm4;
+    R.amask = R.allow ? 0u : 15u;
+    R.glast = (V - 1) / RW_G;
+
+    // ---------------- P1: statistics and candidate lists
+    // The sampler's z = y / T (sampler.rs:47-51) is not formed per element
+    // here: division by T > 0 is monotone, so the maximum, the order and the
+    // top-k of z follow from those of y (ties created by the rounding are
+    // checked when the threshold is set).
+    const bool greedy = T <= 0.0f;
+    const bool tinf = T == INFINITY;   // y / inf is NaN for y = +-inf: checked per element
+    const bool has_topk = P.top_k > 0 && P.top_k < V;
+    // sampler list: 1 = top-k by y (k <= ZS_KS), 2 = every y > -inf (the
+    // small-survivor check when no top-k applies), 0 = none
+    const uint32_t smode = greedy ? 0u : (has_topk ? (P.top_k <= ZS_KS ? 1u : 0u) : 2u);
+    const uint32_t Ks = smode == 1 ? P.top_k : 0u;
+    const uint32_t Ko = want_obs ? (ZS_OBS_CAND < V ? ZS_OBS_CAND : V) : 0u;
+    rw_list LO, LS;
+    LO.buf = sh.u.b.o; LO.cnt = cnt_o; LO.thr = &thr_o; LO.flag = &flag_o;
+    LS.buf = sh.u.b.s; LS.cnt = cnt_s; LS.thr = &thr_s; LS.flag = &flag_s;
+    if (t < 3) { cnt_o[t] = 0; cnt_s[t] = 0; }
+    if (t == 0) { thr_o = -1; thr_s = -1; flag_o = 0; flag_s = 0; }
+    float omax = -INFINITY, ymax = -INFINITY;
+    uint32_t fl = 0;                // ZS_CF_OBS_NAN, ZS_CF_Z_NAN
+    float rejf = -INFINITY;         // largest y turned away from the top-k list
+    int last_nan = -1;
+    unsigned long long gbest = 0;   // greedy: (key << 32) | (id + 1); ties -> larger id
+    uint32_t n_o = 0, n_s = 0;      // entries in the lists (uniform)
+    bool s_over = false;            // smode 2: more than ZS_SMALL_CAP values above -inf
+    __syncthreads();
+    // keys of one element set (observers: -0 and +0 share one key, as equal
+    // logprobs rank by id, logprobs.rs:41-51)
+    auto keys = [&](const float (&x)[4], const float (&y)[4], uint32_t (&kx)[4], uint32_t (&ky)[4]) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            kx[q] = zs_total_key(x[q] + 0.0f);
+            ky[q] = zs_total_key(y[q]);
+        }
+    };
+    // The lists are synchronised once per group of four tiles: admissions
+    // reserve places with a counter slot that rotates over three groups, so a
+    // single barrier per group separates its use, its read and its reset.
+    uint32_t grp = 0, lastslot = 0;
+    bool thr_init = false, p1stop = false;
+    if (t < 3) sh.ovf[t] = 0xffffffffu;
+    if (t == 0) {
+        sh.fthr[0] = sh.fthr[1] = -INFINITY;
+        sh.fcut[0] = sh.fcut[1] = -INFINITY;
+    }
+    __syncthreads();
+    uint32_t g = 0;
+    const uint32_t ng = (V + RW_G - 1) / RW_G;
+    while (g < ng) {
+        g = rw_stream(R, sh, g, [&](uint32_t g, int u, const float (&x)[4], const float (&y)[4]) {
+            const uint32_t idx0 = g * RW_G + 4 * t;
+            // branch-free statistics (ids >= V read -inf: neutral here)
+            omax = fmaxf(omax, fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])));
+            ymax = fmaxf(ymax, fmaxf(fmaxf(y[0], y[1]), fmaxf(y[2], y[3])));
+            uint32_t nx = 0, ny = 0;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                nx |= (x[q] != x[q]) ? 1u : 0u;
+                ny |= (y[q] != y[q]) ? (1u << q) : 0u;
+            }
+            if (nx) fl |= ZS_CF_OBS_NAN;
+            if (ny) {
+                fl |= ZS_CF_Z_NAN;
+                last_nan = max(last_nan, (int)(idx0 + 31 - __clz(ny)));
+            }
+            if (tinf) {
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    if (y[q] == INFINITY || y[q] == -INFINITY) fl |= ZS_CF_Z_NAN;
+            }
+            if (greedy) {
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    if (y[q] != y[q] || idx0 + q >= V) continue;
+                    // -0.0 and +0.0 compare equal in the reference (partial_cmp)
+                    const uint32_t k = zs_total_key(y[q] == 0.0f ? 0.0f : y[q]);
+                    const unsigned long long c = ((unsigned long long)k << 32) | (idx0 + q + 1);
+                    gbest = c > gbest ? c : gbest;
+                }
+            }
+            // valid ids of the thread (the last tile only is partial)
+            const uint32_t vm = idx0 + 4 <= V ? 15u : (idx0 >= V ? 0u : (1u << (V - idx0)) - 1u);
+            if (!thr_init) {
+                // initial thresholds (first tile): in every wave the c-th largest
+                // thread maximum has at least c elements of that wave at or above
+                // it, so the smallest of the waves' values, with c = ceil(K / 16),
+                // has at least K elements of this tile at or above it (ids >= V
+                // hold key 0)
+                thr_init = true;
+                if (Ko || Ks) {
+                    uint32_t kx[4], ky[4];
+                    keys(x, y, kx, ky);
+                    uint32_t mo = 0, ms = 0;
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        if (!((vm >> q) & 1u)) continue;
+                        mo = max(mo, kx[q]);
+                        ms = max(ms, ky[q]);
+                    }
+                    const uint32_t so = wave_sort_u32(mo), ss = wave_sort_u32(ms);
+                    const int co = max((int)((Ko + RW_NW - 1) / RW_NW), 1), cs = max((int)((Ks + RW_NW - 1) / RW_NW), 1);
+                    const uint32_t wo = __shfl(so, 64 - co, 64), ws = __shfl(ss, 64 - cs, 64);
+                    if (zs_lane() == 0) { sh.ru[2][zs_wid()] = wo; sh.ru[3][zs_wid()] = ws; }
+                    rw_bar();
+                    uint32_t a0 = 0xffffffffu, a1 = 0xffffffffu;
+#pragma unroll
+                    for (int w = 0; w < RW_NW; w++) { a0 = min(a0, sh.ru[2][w]); a1 = min(a1, sh.ru[3][w]); }
+                    rw_bar();
+                    if (t == 0) {
+                        // observers: a bound at or below the key of -inf admits
+                        // every id (equal -inf logprobs rank by id). Sampler:
+                        // the values above -inf (a k-th value of -inf makes
+                        // every finite value a survivor; -inf ids never are)
+                        const uint32_t kmin = zs_total_key(-INFINITY);
+                        thr_o = a0 > kmin ? (long long)a0 - 1 : -1;
+                        thr_s = a1 > kmin ? (long long)a1 - 1 : (long long)kmin;
+                        sh.fthr[0] = a0 > kmin ? zs_key_to_float(a0 - 1u) : -INFINITY;
+                        sh.fthr[1] = a1 > kmin ? zs_key_to_float(a1 - 1u) : -INFINITY;
+                    }
+                    rw_bar();
+                }
+            }
+            // admissions, compared as values: a key above the threshold key is a
+            // value above the threshold value, -0 and +0 aside (they compare
+            // equal: only the value of the k-th entry matters, and observers
+            // rank equal values by id) and NaN aside (a NaN row takes no list);
+            // a threshold below every key (-1) admits every valid id
+            const uint32_t slot = grp % 3;
+            uint32_t po = 0, ps = 0;
+            {
+                const float tfo = rw_unif(sh.fthr[0]), tfs = rw_unif(sh.fthr[1]);
+                const bool allo = rw_uni(thr_o < 0 ? 1u : 0u) != 0u, alls = rw_uni(thr_s < 0 ? 1u : 0u) != 0u;
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    po |= (x[q] > tfo || allo) ? (1u << q) : 0u;
+                    if (smode == 1) {
+                        const bool in = y[q] > tfs || alls;
+                        ps |= in ? (1u << q) : 0u;
+                        if (!in) rejf = fmaxf(rejf, y[q]);
+                    }
+                }
+                po &= Ko ? vm : 0u;
+                ps &= vm;
+            }
+            if (smode == 2 && !s_over) {
+                // every value above -inf: one reservation per wave (places past
+                // ZS_SMALL_CAP are not written; the count ends the list)
+                uint32_t m = 0;
+#pragma unroll
+                for (int q = 0; q < 4; q++) m |= (y[q] > -INFINITY) ? (1u << q) : 0u;
+                m &= vm;
+                const uint32_t c = __popc(m);
+                uint32_t inc = c;
+                for (int d = 1; d < 64; d <<= 1) {
+                    const uint32_t o = __shfl_up(inc, d, 64);
+                    if (zs_lane() >= d) inc += o;
+                }
+                const uint32_t wtot = __shfl(inc, 63, 64);
+                uint32_t base = 0;
+                if (wtot) {
+                    if (zs_lane() == 0) base = atomicAdd(&cnt_s[slot], wtot);
+                    base = __shfl(base, 0, 64);
+                }
+                uint32_t p = n_s + base + inc - c;
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    if (!((m >> q) & 1u)) continue;
+                    if (p < ZS_SMALL_CAP) LS.buf[p] = ((unsigned long long)(~zs_total_key(y[q])) << 32) | (idx0 + q);
+                    p++;
+                }
+            }
+            if (po | ps) {
+                uint32_t kx[4], ky[4];
+                keys(x, y, kx, ky);
+                if (po) rw_admit(LO, &cnt_o[slot], n_o, po, kx, idx0, g, &sh.ovf[slot]);
+                if (ps) rw_admit(LS, &cnt_s[slot], n_s, ps, ky, idx0, g, &sh.ovf[slot]);
+            }
+            if (u != 3) return false;
+            // end of the group: counts, overflow, compaction need
+            if (t == 0) {
+                const uint32_t nx = (grp + 1) % 3;
+                cnt_o[nx] = 0;
+                cnt_s[nx] = 0;
+                sh.ovf[nx] = 0xffffffffu;
+            }
+            rw_bar();
+            n_o += rw_uni(cnt_o[slot]);
+            n_s += rw_uni(cnt_s[slot]);
+            const uint32_t ovf = rw_uni(sh.ovf[slot]);
+            lastslot = slot;
+            grp++;
+            p1stop = ovf != 0xffffffffu || n_o > RW_KEEP || (smode == 1 && n_s > RW_KEEP) ||
+                     (smode == 2 && !s_over && n_s > ZS_SMALL_CAP);
+            return p1stop;
+        });
+        if (!p1stop) break;
+        p1stop = false;
+        // compactions (rare): a list past RW_KEEP is cut to its first K. After
+        // an overflow, the entries of the tiles from the first one that lost
+        // an entry are dropped; that tile is admitted again element by element
+        // with compactions as needed (every round places at least
+        // RW_BUF - RW_KEEP entries), and the stream resumes after it (the
+        // statistics are maxima and flags, which a second visit does not
+        // change).
+        __syncthreads();
+        const uint32_t ovf = sh.ovf[lastslot];
+        const uint32_t idlim = ovf != 0xffffffffu ? ovf * RW_G : 0xffffffffu;
+        if (smode == 2 && !s_over && (n_s > ZS_SMALL_CAP || ovf != 0xffffffffu)) s_over = true;
+        auto compact_lists = [&](uint32_t lim) {
+            if (Ko && (n_o > RW_KEEP || lim != 0xffffffffu))
+                n_o = rw_compact(LO, min(n_o, (uint32_t)RW_BUF), Ko, lim, &sh.fthr[0], &sh.fcut[0]);
+            if (smode == 1 && (n_s > RW_KEEP || lim != 0xffffffffu)) {
+                n_s = rw_compact(LS, min(n_s, (uint32_t)RW_BUF), Ks, lim, &sh.fthr[1], &sh.fcut[1]);
+                rejf = fmaxf(rejf, sh.fcut[1]);   // entries cut count as turned away
+            }
+        };
+        compact_lists(idlim);
+        if (t < 3) { cnt_o[t] = 0; cnt_s[t] = 0; sh.ovf[t] = 0xffffffffu; }
+        __syncthreads();
+        if (ovf != 0xffffffffu && ovf < ng) {
+            float x[4], y[4];
+            rw_tile(R, sh, ovf, x, y);
+            uint32_t kx[4], ky[4];
+            keys(x, y, kx, ky);
+            const uint32_t idx0 = ovf * RW_G + 4 * t;
+            const uint32_t vm = idx0 + 4 <= V ? 15u : (idx0 >= V ? 0u : (1u << (V - idx0)) - 1u);
+            uint32_t po = 0, ps = 0;
+            for (int round = 0; ; round++) {
+                // the tile's elements above the current thresholds, minus those placed
+                const float tfo = sh.fthr[0], tfs = sh.fthr[1];
+                const bool allo = thr_o < 0, alls = thr_s < 0;
+                uint32_t wo = 0, ws = 0;
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    wo |= (x[q] > tfo || allo) ? (1u << q) : 0u;
+                    if (smode == 1) {
+                        const bool in = y[q] > tfs || alls;
+                        ws |= in ? (1u << q) : 0u;
+                        if (!in) rejf = fmaxf(rejf, y[q]);
+                    }
+                }
+                wo &= Ko ? vm : 0u;
+                ws &= vm;
+                if (round == 0) { po = wo; ps = ws; }
+                else { po &= wo; ps &= ws; }
+                // place what fits (the rest stays in po / ps)
+                uint32_t lo = 0, ls = 0;
+                {
+                    const uint32_t n1 = __popc(po), n2 = __popc(ps);
+                    uint32_t p1 = n_o + (n1 ? atomicAdd(&cnt_o[0], n1) : 0u);
+                    uint32_t p2 = n_s + (n2 ? atomicAdd(&cnt_s[0], n2) : 0u);
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        if ((po >> q) & 1u) {
+                            if (p1 < RW_BUF) LO.buf[p1] = ((unsigned long long)(~kx[q]) << 32) | (idx0 + q);
+                            else lo |= 1u << q;
+                            p1++;
+                        }
+                        if ((ps >> q) & 1u) {
+                            if (p2 < RW_BUF) LS.buf[p2] = ((unsigned long long)(~ky[q]) << 32) | (idx0 + q);
+                            else ls |= 1u << q;
+                            p2++;
+                        }
+                    }
+                }
+                po = lo;
+                ps = ls;
+                __syncthreads();
+                n_o = min(n_o + cnt_o[0], (uint32_t)RW_BUF);
+                n_s = min(n_s + cnt_s[0], (uint32_t)RW_BUF);
+                const bool more = __syncthreads_or((po | ps) != 0u);
+                if (t == 0) { cnt_o[0] = 0; cnt_s[0] = 0; }
+                if (!more) break;
+                compact_lists(0xffffffffu);
+                __syncthreads();
+            }
+            compact_lists(0xffffffffu);   // back below RW_KEEP for the stream
+            __syncthreads();
+            grp = 0;
+            g = ovf + 1;
+        } else {
+            grp = 0;
+            g = g + 1;
+        }
+    }
+    RW_MARK(1);
+#ifdef RW_STOP_AFTER_P1
+    if (t == 0) { st.mode = ZS_MODE_DONE; st.token = 0; st.status = 0; st.obs_need = 0; st.rounds = 0; st.n_cand = 0; st.klist = 0; st.kpend = 0; st.obs_special = 1; }
+    return;
+#endif
+    // ---- row statistics (one workgroup reduction)
+    {
+        for (int d = 32; d > 0; d >>= 1) {
+            omax = fmaxf(omax, __shfl_xor(omax, d, 64));
+            ymax = fmaxf(ymax, __shfl_xor(ymax, d, 64));
+            fl |= __shfl_xor(fl, d, 64);
+            last_nan = max(last_nan, __shfl_xor(last_nan, d, 64));
+            rejf = fmaxf(rejf, __shfl_xor(rejf, d, 64));
+            const unsigned long long og = __shfl_xor(gbest, d, 64);
+            gbest = og > gbest ? og : gbest;
+        }
+        if (zs_lane() == 0) {
+            sh.rf[0][zs_wid()] = omax; sh.rf[1][zs_wid()] = ymax;
+            sh.ru[0][zs_wid()] = fl; sh.rf[2][zs_wid()] = rejf;
+            sh.ru[2][zs_wid()] = (uint32_t)last_nan;
+            sh.rl[zs_wid()] = gbest;
+        }
+        __syncthreads();
+        omax = -INFINITY; ymax = -INFINITY; fl = 0; rejf = -INFINITY; last_nan = -1; gbest = 0;
+#pragma unroll
+        for (int w = 0; w < RW_NW; w++) {
+            omax = fmaxf(omax, sh.rf[0][w]); ymax = fmaxf(ymax, sh.rf[1][w]);
+            fl |= sh.ru[0][w]; rejf = fmaxf(rejf, sh.rf[2][w]);
+            last_nan = max(last_nan, (int)sh.ru[2][w]);
+            gbest = sh.rl[w] > gbest ? sh.rl[w] : gbest;
+        }
+        __syncthreads();
+    }
+    const float M = rw_unif(omax);
+    const float zmax = rw_unif(zs_temper(ymax, T));   // max z = temper(max y): monotone
+    const bool special = (fl & ZS_CF_OBS_NAN) || M == INFINITY || M == -INFINITY;
+    uint32_t obs_need = 0;
+    if (!special && want_obs) obs_need |= ZS_OBS_S;
+    if (!special && want_unc) obs_need |= ZS_OBS_H;
+    // observer candidates: the first Ko entries of the sorted list
+    uint32_t n_cand = 0;
+    if (Ko) {
+        const uint32_t n = min(n_o, (uint32_t)RW_BUF);
+        uint32_t np2 = 1;
+        while (np2 < n) np2 <<= 1;
+        for (uint32_t i = n + t; i < np2; i += RW_NT) sh.u.b.o[i] = ~0ull;
+        __syncthreads();
+        if (np2 > 1) block_sort_reg_u64<RW_NT, 2>(sh.u.b.o, np2);
+        n_cand = min(n, Ko);
+        if (t < n_cand) {
+            sh.cand_id[t] = (uint32_t)sh.u.b.o[t];
+            sh.cand_x[t] = zs_key_to_float(~(uint32_t)(sh.u.b.o[t] >> 32));
+        }
+    }
+    const uint32_t z_is_x = (T == 1.0f && !has_y) ? 1u : 0u;
+
+    // ---------------- sampler decisions
+    uint32_t token = 0, mode = ZS_MODE_DONE, status = 0, has_thr = 0, thr_key = 0;
+    float thr = -INFINITY;
+    if (greedy) {
+        // sampler.rs:35-42, max_by over partial_cmp: the last maximal element;
+        // a NaN compares Equal, so the fold restarts after the last NaN
+        status |= ZS_ST_GREEDY;
+        if (last_nan < 0) {
+            token = gbest ? (uint32_t)(gbest & 0xffffffffull) - 1u : 0u;
+        } else {
+            const uint32_t L = (uint32_t)last_nan;
+            unsigned long long gb = 0;
+            rw_stream(R, sh, 0, [&](uint32_t g, int, const float (&x)[4], const float (&y)[4]) {
+                const uint32_t idx0 = g * RW_G + 4 * t;
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const uint32_t id = idx0 + q;
+                    if (id >= V || id <= L || y[q] != y[q]) continue;
+                    const uint32_t k = zs_total_key(y[q] == 0.0f ? 0.0f : y[q]);
+                    const unsigned long long c = ((unsigned long long)k << 32) | (id + 1);
+                    gb = c > gb ? c : gb;
+                }
+                return false;
+            });
+            for (int d = 32; d > 0; d >>= 1) {
+                const unsigned long long o = __shfl_xor(gb, d, 64);
+                gb = o > gb ? o : gb;
+            }
+            if (zs_lane() == 0) sh.rl[zs_wid()] = gb;
+            __syncthreads();
+            gb = 0;
+#pragma unroll
+            for (int w = 0; w < RW_NW; w++) gb = sh.rl[w] > gb ? sh.rl[w] : gb;
+            __syncthreads();
+            token = gb ? (uint32_t)(gb & 0xffffffffull) - 1u : L;
+        }
+    } else if ((fl & ZS_CF_Z_NAN) || zmax == INFINITY || zmax == -INFINITY) {
+        // exp_sum is NaN: every comparison in the draw fails -> V-1 (sampler.rs:127)
+        status |= ZS_ST_NONFINITE;
+        token = V - 1;
+    } else {
+        bool small = false;
+        uint32_t nsv = 0;
+        if (smode == 1) {
+            const uint32_t n = min(n_s, (uint32_t)RW_BUF);
+            uint32_t np2 = 1;
+            while (np2 < n) np2 <<= 1;
+            for (uint32_t i = n + t; i < np2; i += RW_NT) sh.u.b.s[i] = ~0ull;
+            __syncthreads();
+            if (np2 > 1) block_sort_reg_u64<RW_NT, 2>(sh.u.b.s, np2);
+            // the k-th largest z is temper(the k-th largest y)
+            const float yk = zs_key_to_float(~(uint32_t)(sh.u.b.s[Ks - 1] >> 32));
+            thr = zs_temper(yk, T);
+            thr_key = zs_total_key(thr);
+            has_thr = 1;
+            // every element at the threshold must be listed: after the first
+            // k, the next listed y and the largest y turned away must map
+            // below it (or the threshold is -inf: every finite value listed)
+            bool complete = thr == -INFINITY;
+            if (!complete) {
+                const float ynext = n > Ks ? zs_key_to_float(~(uint32_t)(sh.u.b.s[Ks] >> 32)) : -INFINITY;
+                const float yrej = rejf;
+                complete = zs_temper(ynext, T) < thr && zs_temper(yrej, T) < thr;
+            }
+            if (thr == 0.0f) complete = false;  // the other zero also survives
+            if (complete) {
+                // survivors: !(z < thr) (sampler.rs:59-63) and above -inf
+                if (t < 64) {
+                    uint32_t c = 0;
+                    for (uint32_t i0 = 0; i0 < Ks; i0 += 64) {
+                        const uint32_t i = i0 + t;
+                        float zi = -INFINITY;
+                        if (i < Ks) zi = zs_temper(zs_key_to_float(~(uint32_t)(sh.u.b.s[i] >> 32)), T);
+                        const bool sv = zi > -INFINITY;
+                        const unsigned long long m = __ballot(sv);
+                        if (sv) {
+                            const uint32_t p = c + __popcll(m & ((1ull << t) - 1ull));
+                            sh.sval[p] = zi;
+                            sh.sidx[p] = (uint32_t)sh.u.b.s[i];
+                        }
+                        c += __popcll(m);
+                    }
+                    if (t == 0) sh.n_surv = c;
+                }
+                __syncthreads();
+                nsv = sh.n_surv;
+                small = true;
+            }
+        } else if (smode == 2 && !s_over) {
+            // every y above -inf, unordered (<= ZS_SMALL_CAP); their z
+            if (t < 64) {
+                uint32_t c = 0;
+                for (uint32_t i0 = 0; i0 < n_s; i0 += 64) {
+                    const uint32_t i = i0 + t;
+                    float zi = -INFINITY;
+                    if (i < n_s) zi = zs_temper(zs_key_to_float(~(uint32_t)(sh.u.b.s[i] >> 32)), T);
+                    const bool sv = zi > -INFINITY;
+                    const unsigned long long m = __ballot(sv);
+                    if (sv) {
+                        const uint32_t p = c + __popcll(m & ((1ull << t) - 1ull));
+                        sh.sval[p] = zi;
+                        sh.sidx[p] = (uint32_t)sh.u.b.s[i];
+                    }
+                    c += __popcll(m);
+                }
+                if (t == 0) sh.n_surv = c;
+            }
+            __syncthreads();
+            nsv = sh.n_surv;
+            small = true;
+        } else if (has_topk) {
+            has_thr = 2;   // top_k > ZS_KS: zs_k_big selects the threshold
+        }
+        if (small) {
+            __syncthreads();
+            if (t < 64) rw_small(b.d_seed[r], b.d_counter[r], V, P, nsv, zmax, sh);
+            __syncthreads();
+            token = sh.tok;
+            status |= ZS_ST_SMALL;
+        } else {
+            mode = ZS_MODE_BIG;
+        }
+    }
+    __syncthreads();
+    RW_MARK(2);
+
+    // ---------------- P2: observers' S (fast-exp terms: a tolerance output)
+    // and the big rows' sampler S = sum expf(z - max) (sampler.rs:68, exact)
+    const bool doA = (obs_need & ZS_OBS_S) != 0;
+    const bool doB = mode == ZS_MODE_BIG && has_thr != 2;
+    float SA = -0.0f, SB = -0.0f;
+    const float* allow_f = reinterpret_cast<const float*>(R.allow);
+    // a pass alternates between its streaming function and the ordered scan
+    // of the tiles that need it, until the row is done
+    if (doA) {
+        uint32_t g = 0, slow = 0;
+        while (true) {
+            SA = rw_pass_obs(R.row, allow_f, V, R.np, R.ldm4, M, SA, g, slow);
+            if (slow) { g++; slow = 0; continue; }
+            g = rw_uni(sh.pass_g);
+            if (g >= ng) break;
+            slow = 1;
+        }
+    }
+    if (doB) {
+        const uint32_t use_thr = has_thr != 0 ? 1u : 0u;
+        uint32_t g = 0, slow = 0;
+        while (true) {
+            SB = rw_pass_samp(R.row, allow_f, V, R.np, R.ldm4, T, zmax, thr, use_thr, SB, g, slow);
+            if (slow) { g++; slow = 0; continue; }
+            g = rw_uni(sh.pass_g);
+            if (g >= ng) break;
+            slow = 1;
+        }
+    }
+    RW_MARK(3);
+#ifdef RW_PROF
+    if (t == 0) rw_prof[r][12] = rw_prof[r][8];
+#endif
+    // ---------------- P3: entropy (hallucination.rs:139-144; fast-exp terms)
+    float H = 0.0f;
+    if (obs_need & ZS_OBS_H) {
+        const float inv = 1.0f / SA, lns = (float)log((double)SA);
+        uint32_t g = 0, slow = 0;
+        while (true) {
+            H = rw_pass_ent(R.row, allow_f, V, R.np, R.ldm4, M, inv, lns, H, g, slow);
+            if (slow) { g++; slow = 0; continue; }
+            g = rw_uni(sh.pass_g);
+            if (g >= ng) break;
+            slow = 1;
+        }
+    }
+    RW_MARK(4);
+
+    // ---------------- row state for the big-row kernels and zs_k_final
+    if (t == 0) {
+        st.rounds = (doB ? (1u << ZS_SUM_SAMP_S) : 0u) | (doA ? (1u << ZS_SUM_OBS_S) : 0u) |
+                    ((obs_need & ZS_OBS_H) ? (1u << ZS_SUM_OBS_H) : 0u);
+        st.z_max = zmax;
+        st.has_thr = has_thr;
+        st.thr_key = thr_key;
+        st.mode = mode;
+        st.token = token;
+        st.status = status;
+        st.obs_max = M;
+        st.obs_special = special ? 1u : 0u;
+        st.obs_need = obs_need;
+        st.n_cand = n_cand;
+        // the sampler's S always comes from the exact sum above: the observers'
+        // S uses fast-exp terms
+        st.z_is_x = 0;
+        st.klist = 0;
+        st.kpend = 0;
+        st.samp_S = SB;
+        st.obs_S = SA;
+        st.obs_H = H;
+    }
+    if (t < n_cand) { st.cand_id[t] = sh.cand_id[t]; st.cand_x[t] = sh.cand_x[t]; }
+    if (mode == ZS_MODE_BIG) {
+        // bucket counts and masses of the top-p walk, accumulated by zs_k_pv
+        zs_tp_bucket* bk = a.tp_bk + (size_t)r * ZS_TP_NB;
+        for (uint32_t i = t; i < ZS_TP_NB; i += RW_NT) { bk[i].cnt = 0u; bk[i].mass = 0.0f; }
+    }
+    (void)z_is_x;
+}
+
+extern "C" int zs_row_launch(const zs_sargs& a, hipStream_t stream) {
+    const size_t dyn = 2 * ((a.b.V + 31) / 32) * sizeof(uint32_t);
+    hipLaunchKernelGGL(zs_k_row, dim3(a.b.B), dim3(RW_NT), dyn, stream, a);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}

@@ -27,48 +27,7 @@
 #include "zs_dev.h"
 #include "zs_seq.h"
 #include "zs_terms.h"
-
-struct zs_sargs {
-    zs_batch b;
-    uint32_t* p_cnt;
-    uint32_t* p_id;
-    uint32_t* p_flags;
-    float* p_y;
-    zs_chunk_stat* cst;
-    uint32_t* cs_key;
-    uint32_t* cs_idx;
-    uint32_t* co_key;
-    uint32_t* co_idx;
-    zs_row_state* rst;
-    uint32_t* pairs;
-    uint32_t* pv;
-    uint32_t nch;
-    uint32_t max_vocab;
-    zs_sub_mom* sub_mom;
-    zs_sub_sum* sub_sum;
-    uint32_t* p_sub;
-    uint32_t max_subs;
-    double* k_ap;
-    zs_sub_sum* k_sum;
-    zs_tp_bucket* tp_bk;
-    uint32_t* tp_cl;
-    uint32_t* tp_pre;
-    uint32_t* kcnt;
-};
-
-#define ZS_ST_FALLBACK 0x200u
-
-__device__ __forceinline__ bool zs_penalty_active(const zs_row_params& P) {
-    return P.repeat != 1.0f || P.presence != 0.0f || P.frequency != 0.0f;
-}
-__device__ __forceinline__ float zs_temper(float y, float T) {
-    // sampler.rs:47-51: divide only when T != 1 (T > 0 here)
-    return (T > 0.0f && T != 1.0f) ? y / T : y;
-}
-__device__ __forceinline__ bool zs_allowed_bit(const zs_batch& b, uint32_t r, uint32_t idx) {
-    uint32_t w = b.d_allow_bits[(size_t)r * b.allow_words + (idx >> 5)];
-    return (w >> (idx & 31)) & 1u;
-}
+#include "zs_sampler.h"
 
 // ===========================================================================
 // zs_k_prep: per-row patch list.
@@ -967,151 +926,6 @@ __device__ void zs_predict_subs(zs_sub_sum* out, uint32_t nsub, const F& A, cons
 }
 
 #define CB_NT 256
-#define ZS_SMALL_CAP 512
-
-
-// Small survivor sets (n <= ZS_SMALL_CAP, all other logits are -inf after
-// top-k / mask) are sampled exactly in zs_k_combine: zero terms of the
-// reference's full-vocabulary loops do not change a running sum.
-// Ascending bitonic sort of 64*E u64 keys by one wave, element i = lane*E + e
-// in register e of lane i / E: strides below E inside the lane, the others by
-// lane exchanges.
-template <int E>
-__device__ __forceinline__ void wave_sort_u64_e(unsigned long long (&v)[E]) {
-    const uint32_t lane = (uint32_t)zs_lane();
-#pragma unroll
-    for (uint32_t k = 2; k <= 64u * E; k <<= 1) {
-#pragma unroll
-        for (uint32_t j = k >> 1; j > 0; j >>= 1) {
-            if (j < (uint32_t)E) {
-#pragma unroll
-                for (uint32_t e = 0; e < (uint32_t)E; e++) {
-                    const uint32_t pe = e ^ j;
-                    if (pe > e) {
-                        const bool asc = ((lane * E + e) & k) == 0u;
-                        const unsigned long long x = v[e], y = v[pe];
-                        if ((x > y) == asc) { v[e] = y; v[pe] = x; }
-                    }
-                }
-            } else {
-#pragma unroll
-                for (uint32_t e = 0; e < (uint32_t)E; e++) {
-                    const unsigned long long o = __shfl_xor(v[e], (int)(j / E), 64);
-                    const uint32_t i = lane * E + e;
-                    const bool asc = (i & k) == 0u, lower = (i & j) == 0u;
-                    v[e] = (lower == asc) ? (o < v[e] ? o : v[e]) : (o > v[e] ? o : v[e]);
-                }
-            }
-        }
-    }
-}
-
-// Exact sampler over a small survivor set (n <= 64 * E, every other element
-// below the top-k threshold, masked or -inf), by one wave: the reference's
-// sequential f32 sums are done literally, one addition at a time in the
-// reference's order, with no workgroup synchronisation (sampler.rs:46-127).
-// Called by the 64 lanes of one wave; returns the token on every lane.
-template <int E>
-__device__ uint32_t small_path_wave(const zs_sargs& a, uint32_t r, const zs_row_params& P, uint32_t n, float m,
-                                    const float* sval, const uint32_t* sidx) {
-    const zs_batch& b = a.b;
-    const uint32_t lane = (uint32_t)zs_lane();
-    // survivors by index: element i (sorted) in register i % E of lane i / E
-    unsigned long long key[E];
-#pragma unroll
-    for (int e = 0; e < E; e++) {
-        const uint32_t i = lane * E + e;
-        key[e] = i < n ? (((unsigned long long)sidx[i] << 32) | zs_f2u(sval[i])) : ~0ull;
-    }
-    wave_sort_u64_e<E>(key);
-    uint32_t id[E];
-    float p[E];
-#pragma unroll
-    for (int e = 0; e < E; e++) {
-        const bool live = lane * E + e < n;
-        id[e] = (uint32_t)(key[e] >> 32);
-        p[e] = live ? zs_expf(zs_u2f((uint32_t)key[e]) - m) : 0.0f;
-    }
-    // s0 + v[0] + v[1] + ... in order (sampler.rs:68, 80, 107)
-    auto seq_sum = [&](const float (&v)[E], float s0) {
-        float s = s0;
-        for (uint32_t L = 0; L * E < n; L++)
-#pragma unroll
-            for (int e = 0; e < E; e++)
-                if (L * E + e < n) s = s + zs_readlane_f(v[e], L);
-        return s;
-    };
-    // softmax (sampler.rs:67-69)
-    const float S = seq_sum(p, -0.0f);
-#pragma unroll
-    for (int e = 0; e < E; e++) p[e] = p[e] / S;
-    // min-p (sampler.rs:72-88)
-    if (P.min_p > 0.0f) {
-        float pm = 0.0f;
-#pragma unroll
-        for (int e = 0; e < E; e++) if (lane * E + e < n) pm = fmaxf(pm, p[e]);
-        pm = wave_max_f(pm);
-        const float cut = P.min_p * pm;
-#pragma unroll
-        for (int e = 0; e < E; e++) if (p[e] < cut) p[e] = 0.0f;
-        const float kept = seq_sum(p, 0.0f);
-        if (kept > 0.0f)
-#pragma unroll
-            for (int e = 0; e < E; e++) p[e] = p[e] / kept;
-    }
-    // top-p (sampler.rs:91-115): cumsum in (p desc, idx asc) order
-    if (P.top_p < 1.0f) {
-        uint32_t vstar = 0, istar = 0xffffffffu;
-        const bool none = !(P.top_p > 0.0f);  // cumsum 0 >= top_p: nothing kept
-        if (!none) {
-            unsigned long long k2[E];
-#pragma unroll
-            for (int e = 0; e < E; e++)
-                k2[e] = lane * E + e < n ? (((unsigned long long)(~zs_f2u(p[e])) << 32) | id[e]) : ~0ull;
-            wave_sort_u64_e<E>(k2);
-            float cum = 0.0f;
-            bool found = false;
-            for (uint32_t L = 0; L * E < n && !found; L++) {
-#pragma unroll
-                for (int e = 0; e < E; e++) {
-                    if (found || L * E + e >= n) continue;
-                    const unsigned long long ks = zs_readlane_u64(k2[e], L);
-                    cum = cum + zs_u2f(~(uint32_t)(ks >> 32));
-                    if (cum >= P.top_p) {
-                        vstar = ~(uint32_t)(ks >> 32);
-                        istar = (uint32_t)ks;
-                        found = true;
-                    }
-                }
-            }
-        }
-        float f[E];
-#pragma unroll
-        for (int e = 0; e < E; e++) {
-            const uint32_t pb = zs_f2u(p[e]);
-            const bool keep = !none && (pb > vstar || (pb == vstar && id[e] <= istar));
-            f[e] = keep ? p[e] : 0.0f;
-        }
-        const float sum = seq_sum(f, -0.0f);
-        if (sum > 0.0f)
-#pragma unroll
-            for (int e = 0; e < E; e++) p[e] = f[e] / sum;
-    }
-    // draw (sampler.rs:118-127); r == 0 stops at index 0 whatever its p
-    const float rr = zs_philox_uniform(b.d_seed[r], b.d_counter[r], 0u);
-    if (rr <= 0.0f) return 0;
-    float cum = 0.0f;
-    for (uint32_t L = 0; L * E < n; L++) {
-#pragma unroll
-        for (int e = 0; e < E; e++) {
-            if (L * E + e >= n) continue;
-            cum = cum + zs_readlane_f(p[e], L);
-            if (cum >= rr) return zs_readlane_u(id[e], L);
-        }
-    }
-    return b.V - 1;
-}
-
 __global__ __launch_bounds__(CB_NT) void zs_k_combine(zs_sargs a) {
     const uint32_t r = blockIdx.x;
     const zs_batch& b = a.b;
@@ -1304,8 +1118,8 @@ __global__ __launch_bounds__(CB_NT) void zs_k_combine(zs_sargs a) {
                 small = false;
             } else {
                 if (t < 64) {
-                    const uint32_t tk = n <= 64 ? small_path_wave<1>(a, r, P, n, zmax, sval, sidx)
-                                                : small_path_wave<ZS_SMALL_CAP / 64>(a, r, P, n, zmax, sval, sidx);
+                    const uint32_t tk = n <= 64 ? small_path_wave<1>(b.d_seed[r], b.d_counter[r], V, P, n, zmax, sval, sidx)
+                                                : small_path_wave<ZS_SMALL_CAP / 64>(b.d_seed[r], b.d_counter[r], V, P, n, zmax, sval, sidx);
                     if (t == 0) n_sh = tk;
                 }
                 __syncthreads();
@@ -3342,31 +3156,9 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
         ev++;
     };
     mark(nullptr);
-    hipLaunchKernelGGL(zs_k_prep, dim3(B), dim3(ZS_PREP_NT), 0, stream, a);
-    mark("zs_k_prep");
-    hipLaunchKernelGGL(zs_k_pass1, dim3(nch, B), dim3(ZS_P1_NT), 0, stream, a);
-    mark("zs_k_pass1");
+    if (zs_row_launch(a, stream)) return zs_set_error(ctx, ZS_EHIP, "zs_sample: zs_k_row launch failed");
+    mark("zs_k_row");
     if (a.b.pass_event && hipEventRecord((hipEvent_t)a.b.pass_event, stream) != hipSuccess) return -1;
-    hipLaunchKernelGGL(zs_k_combine, dim3(B), dim3(CB_NT), 0, stream, a);
-    mark("zs_k_combine");
-    const uint32_t nsub = (bt->V + ZS_SUB - 1) / ZS_SUB;
-    hipLaunchKernelGGL(zs_k_roundA, dim3((nsub + 3) / 4, B), dim3(256), 0, stream, a);
-    mark("zs_k_roundA");
-    hipLaunchKernelGGL(zs_k_stitchA, dim3(B, 2), dim3(ST_NT), 0, stream, a);
-    mark("zs_k_stitchA");
-    // The entropy chain (roundB, stitchB) depends on the observers' S only and
-    // runs on the side stream while the big rows run here; profiling keeps one
-    // stream so that every kernel has its own interval.
-    hipStream_t side = prof ? stream : (hipStream_t)ctx->side_stream;
-    if (!prof) {
-        ZS_LAUNCH_CHECK(hipEventRecord((hipEvent_t)ctx->fork_event, stream));
-        ZS_LAUNCH_CHECK(hipStreamWaitEvent(side, (hipEvent_t)ctx->fork_event, 0));
-    }
-    hipLaunchKernelGGL(zs_k_roundB, dim3((nsub + 3) / 4, B), dim3(256), 0, side, a);
-    mark("zs_k_roundB");
-    hipLaunchKernelGGL(zs_k_stitchB, dim3(B), dim3(ST_NT), 0, side, a);
-    mark("zs_k_stitchB");
-    if (!prof) ZS_LAUNCH_CHECK(hipEventRecord((hipEvent_t)ctx->join_event, side));
     hipLaunchKernelGGL(zs_k_pv, dim3((bt->V + ZS_BIG_G - 1) / ZS_BIG_G, B), dim3(ZS_BIG_NT), 0, stream, a);
     mark("zs_k_pv");
     hipLaunchKernelGGL(zs_k_tp_plan, dim3(B), dim3(ZS_BIG_NT), 0, stream, a);
@@ -3386,7 +3178,6 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
     hipLaunchKernelGGL(zs_k_roundK<1>, dim3((nsubk + 3) / 4, B), dim3(256), 0, stream, a);
     hipLaunchKernelGGL(zs_k_stitchK<1>, dim3(B), dim3(SK_NT), 0, stream, a);
     mark("zs_k_kept");
-    if (!prof) ZS_LAUNCH_CHECK(hipStreamWaitEvent(stream, (hipEvent_t)ctx->join_event, 0));
     hipLaunchKernelGGL(zs_k_final, dim3(B), dim3(64), 0, stream, a);
     mark("zs_k_final");
     if (prof) ctx->n_timed = ev - 1;
