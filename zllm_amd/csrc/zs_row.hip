@@ -68,6 +68,9 @@ struct rw_shared {
     uint32_t grp[2][RW_NW][8];      // P2 / P3: per-wave tile totals (double buffered)
     uint32_t gsum[2][RW_NW];        // P2 / P3: per-wave group totals (double buffered)
     uint32_t cross[3][RW_NW];       // crossing path: per-wave prefix totals (RW_NG grids)
+    int cr_first[2][RW_NW];         // crossing path: per-wave first event (double buffered)
+    float cr_s[2];                  // crossing path: the sum after an event
+    uint32_t cr_nb[2][2];           // crossing path: prefixes through the event
     float head[256];
     uint32_t n_ent, n_surv, tok;
     uint32_t ovf[3];                // first tile that lost a list entry, per group slot
@@ -534,84 +537,123 @@ __device__ __forceinline__ uint32_t rw_sat(uint32_t a, uint32_t b) {
     return c > (1u << 30) ? (1u << 30) : c;
 }
 
-// Crossing path: the tile's values from running sum s (elements >= start),
-// with the increments on RW_NG grids prefix-scanned at once. Exact sums
-// (`ties` = 1) go to the ordered scan when a term is an exact half-way case.
+// Inclusive prefix sum of a u32 over the wave (no overflow check): shifts by
+// 1, 2, 4, 8 within each row of 16 lanes, then the rows by broadcasts.
+__device__ __forceinline__ uint32_t rw_wave_scan(uint32_t v) {
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, true);   // row_shr:1
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, true);   // row_shr:2
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, true);   // row_shr:4
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, true);   // row_shr:8
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false);  // row_bcast:15
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false);  // row_bcast:31
+    return v;
+}
+
+// Crossing path: the tile's values from running sum s (elements >= start).
+// The increments on RW_NG consecutive grids are prefix-scanned at once; a
+// walk then finds the events in order: an element whose prefix carries the
+// sum out of its binade, and (exact sums, `ties`) an element whose increment
+// is an exact half-way case (its rounding follows the sum's parity). Each
+// event is added as a real f32 addition, and the walk continues on the grid
+// of the new sum. A thread's total is capped at 2^25: any larger one holds
+// a crossing, so the prefixes are exact up to the first crossing. Sums below
+// 2^-103 (no f32 scale reaches their grid) are left to the ordered scan
+// (slow: from element `start`).
 __device__ __forceinline__ float rw_cross(const float (&v)[4], int& start, float s, uint32_t ties, bool& slow,
                                           rw_shared& sh) {
     const int t = (int)threadIdx.x, lane = zs_lane(), wid = zs_wid();
+    uint32_t par = 0;
     slow = false;
+    // the first element of the workgroup with an event (uniform)
+    auto first_of = [&](int my) -> int {
+        // (read by every lane: a lane's value exists only where it was
+        // computed, so the read must not sit inside the lane-0 branch)
+        const unsigned long long m = __ballot(my != ZS_BIGI);
+        const int mv = m ? __builtin_amdgcn_readlane(my, __ffsll((long long)m) - 1) : ZS_BIGI;
+        if (lane == 0) sh.cr_first[par][wid] = mv;
+        rw_bar();
+        int e = ZS_BIGI;
+#pragma unroll
+        for (int w = 0; w < RW_NW; w++) e = min(e, sh.cr_first[par][w]);
+        par ^= 1u;
+        return (int)rw_uni((uint32_t)e);
+    };
     while (start < RW_G) {
         if (s == 0.0f) {
             // a zero sum takes the first nonzero term as it is (zero terms
-            // before it leave a zero; -0 + +0 = +0 is restored at the end)
-            int first = ZS_BIGI;
+            // before it leave a zero; -0 + +0 = +0 is restored here)
+            int my = ZS_BIGI;
 #pragma unroll
             for (int q = 0; q < 4; q++)
-                if (first == ZS_BIGI && 4 * t + q >= start && v[q] != 0.0f) first = 4 * t + q;
-            first = block_min_i<RW_NT>(first, reinterpret_cast<int*>(sh.ru[5]));
+                if (my == ZS_BIGI && 4 * t + q >= start && v[q] != 0.0f) my = 4 * t + q;
+            const int first = first_of(my);
+#ifdef RW_PROF
+            if (threadIdx.x == 0) rw_prof[blockIdx.x][7]++;
+#endif
             if (first == ZS_BIGI) return s + 0.0f;
             if (t == first / 4) {
                 float ve = v[0];
 #pragma unroll
                 for (int q = 1; q < 4; q++) ve = q == first % 4 ? v[q] : ve;
-                sh.fsh = ve;
+                sh.cr_s[par] = ve;
             }
-            __syncthreads();
-            s = (s + 0.0f) + sh.fsh;
-            __syncthreads();
+            rw_bar();
+            s = (s + 0.0f) + sh.cr_s[par];
+            par ^= 1u;
             start = first + 1;
             continue;
         }
         const int eg0 = zs_grid_exp(s);
         if (rw_scale(eg0) == 0.0f) { slow = true; return s; }
-        // per-thread increments on grids eg0 .. eg0 + RW_NG - 1
-        uint32_t inc[RW_NG][4], tot[RW_NG];
-        uint32_t tie = 0;
+#ifdef RW_PROF
+        const unsigned long long cs0 = wall_clock64();
+        if (threadIdx.x == 0) rw_prof[blockIdx.x][6]++;
+#endif
+        // per-thread increments and half-way flags on grids eg0 .. eg0 + RW_NG - 1
+        uint32_t inc[RW_NG][4], tot[RW_NG], tb[RW_NG];
 #pragma unroll
         for (int j = 0; j < RW_NG; j++) {
             const float sc = rw_scale(eg0 + j);
             tot[j] = 0;
+            tb[j] = 0;
 #pragma unroll
             for (int q = 0; q < 4; q++) {
                 const float qv = (4 * t + q >= start) ? fminf(v[q] * sc, RW_QCAP) : 0.0f;
                 const float rq = rintf(qv);
-                tie |= (fabsf(qv - rq) == 0.5f) ? 1u : 0u;
+                if (ties && fabsf(qv - rq) == 0.5f) tb[j] |= 1u << q;
                 inc[j][q] = (uint32_t)rq;
-                tot[j] = rw_sat(tot[j], inc[j][q]);
+                tot[j] += inc[j][q];
             }
+            tot[j] = min(tot[j], 1u << 25);
         }
-        if (ties && __syncthreads_or(tie)) { slow = true; return s; }
         // exclusive prefix of the thread totals over the workgroup, per grid
-        uint32_t pre[RW_NG];
+        uint32_t pre[RW_NG], wtot[RW_NG];
 #pragma unroll
         for (int j = 0; j < RW_NG; j++) {
-            uint32_t x = tot[j];
-            for (int d = 1; d < 64; d <<= 1) {
-                const uint32_t y = __shfl_up(x, d, 64);
-                if (lane >= d) x = rw_sat(x, y);
-            }
-            pre[j] = x;   // inclusive within the wave for now
-            if (lane == 63) sh.cross[j][wid] = x;
+            const uint32_t x = rw_wave_scan(tot[j]);
+            pre[j] = x - tot[j];
+            if (lane == 63) sh.cross[j][wid] = min(x, 1u << 25);
         }
-        __syncthreads();
-        uint32_t wtot[RW_NG];
+        rw_bar();
 #pragma unroll
         for (int j = 0; j < RW_NG; j++) {
             uint32_t before = 0, all = 0;
+#pragma unroll
             for (int w = 0; w < RW_NW; w++) {
                 const uint32_t c = sh.cross[j][w];
-                if (w < wid) before = rw_sat(before, c);
-                all = rw_sat(all, c);
+                before += w < wid ? c : 0u;
+                all += c;
             }
-            pre[j] = rw_sat(before, pre[j] - tot[j]);   // exclusive prefix of this thread
+            pre[j] += before;
             wtot[j] = all;
         }
-        __syncthreads();
+#ifdef RW_PROF
+        if (threadIdx.x == 0) rw_prof[blockIdx.x][11] += wall_clock64() - cs0;
+#endif
         // walk: running sum k on grid eg0 + j from element position P (the
-        // prefix of grid j before P is base); the grid index is a
-        // compile-time constant in every step, so the increments stay in
-        // registers
+        // prefix of grid j through the last event is base); the grid index
+        // is a compile-time constant in every step, so the increments stay
+        // in registers
         uint32_t k = zs_grid_k(s), base = 0;
         int P = start;
         bool done = false, next = true;
@@ -619,47 +661,61 @@ __device__ __forceinline__ float rw_cross(const float (&v)[4], int& start, float
         for (int j = 0; j < RW_NG; j++) {
             if (!next) break;
             next = false;
-            // first element e >= P whose inclusive prefix reaches the binade end
-            int my = ZS_BIGI;
-            uint32_t run = pre[j];
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                run = rw_sat(run, inc[j][q]);
-                if (my == ZS_BIGI && 4 * t + q >= P && (uint64_t)k + (run - base) >= ZS_BINADE) my = 4 * t + q;
-            }
-            const int e = block_min_i<RW_NT>(my, reinterpret_cast<int*>(sh.ru[5]));
-            if (e == ZS_BIGI) {
-                s = zs_grid_value(k + (wtot[j] - base), eg0 + j);
-                done = true;
-                break;
-            }
-            // the crossing term as a real f32 addition (its owner)
-            if (t == e / 4) {
-                const int eq = e % 4;
-                uint32_t ex = pre[j];
-                uint32_t nb = pre[j + 1 < RW_NG ? j + 1 : j];
-                float ve = 0.0f;
+            const int jn = j + 1 < RW_NG ? j + 1 : j;
+            while (true) {
+                int my = ZS_BIGI;
+                uint32_t run = pre[j];
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    if (q < eq) ex = rw_sat(ex, inc[j][q]);
-                    if (q <= eq && j + 1 < RW_NG) nb = rw_sat(nb, inc[j + 1 < RW_NG ? j + 1 : j][q]);
-                    ve = q == eq ? v[q] : ve;
+                    run += inc[j][q];
+                    if (my == ZS_BIGI && 4 * t + q >= P &&
+                        ((uint64_t)k + (run - base) >= ZS_BINADE || ((tb[j] >> q) & 1u)))
+                        my = 4 * t + q;
                 }
-                sh.fsh = zs_grid_value(k + (ex - base), eg0 + j) + ve;
-                sh.ru[4][0] = nb;   // prefix of grid j + 1 through e
+                const int e = first_of(my);
+#ifdef RW_PROF
+                if (threadIdx.x == 0 && e != ZS_BIGI) rw_prof[blockIdx.x][15]++;
+#endif
+                if (e == ZS_BIGI) {
+                    s = zs_grid_value(k + (wtot[j] - base), eg0 + j);
+                    done = true;
+                    break;
+                }
+                // the event as a real f32 addition (its owner), with the
+                // prefixes of grids j and j + 1 through it
+                if (t == e / 4) {
+                    const int eq = e % 4;
+                    uint32_t ex = pre[j], nbj = pre[j], nbn = pre[jn];
+                    float ve = 0.0f;
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        if (q < eq) ex += inc[j][q];
+                        if (q <= eq) { nbj += inc[j][q]; nbn += inc[jn][q]; }
+                        ve = q == eq ? v[q] : ve;
+                    }
+                    sh.cr_s[par] = zs_grid_value(k + (ex - base), eg0 + j) + ve;
+                    sh.cr_nb[par][0] = nbj;
+                    sh.cr_nb[par][1] = nbn;
+                }
+                rw_bar();
+                s = sh.cr_s[par];
+                const uint32_t nbj = sh.cr_nb[par][0], nbn = sh.cr_nb[par][1];
+                par ^= 1u;
+                P = e + 1;
+                const int ge = zs_grid_exp(s);
+                if (ge == eg0 + j) {   // a half-way event: the same grid
+                    k = zs_grid_k(s);
+                    base = nbj;
+                    continue;
+                }
+                if (j + 1 < RW_NG && ge == eg0 + j + 1) {
+                    k = zs_grid_k(s);
+                    base = nbn;
+                    next = true;
+                }
+                break;   // otherwise past the prepared grids: rescan from P
             }
-            __syncthreads();
-            s = sh.fsh;
-            const uint32_t nb = sh.ru[4][0];
-            __syncthreads();
-            P = e + 1;
-            if (j + 1 < RW_NG && zs_grid_exp(s) == eg0 + j + 1) {
-                k = zs_grid_k(s);
-                base = nb;
-                next = true;
-            }
-            // otherwise past the prepared grids (or a jump over a binade):
-            // rescan from P
+            if (done) break;
         }
         if (done) return s;
         start = P;
@@ -772,8 +828,12 @@ __device__ __forceinline__ float rw_sum_pass(const rw_row& R, rw_shared& sh, flo
                 eg = zs_grid_exp(s);
                 sc = rw_scale(eg);
             }
+            // a zero sum only needs to know whether a term may be nonzero
+            // (rows whose terms are all zero up to some tile: masked rows)
+            const bool zero = s == 0.0f;
             uint32_t tf = 0;
-            qt[u] = f.fast(x, y, sc, tf);
+            if (zero) qt[u] = f.nonzero(x, y) ? RW_QFLAG : 0u;
+            else qt[u] = f.fast(x, y, sc, tf);
             if (tf) qt[u] = RW_QFLAG;   // a flagged tile reads as a crossing
             if (u != 3) return false;
             // the group's total first (one value per thread); the tiles'
@@ -789,6 +849,11 @@ __device__ __forceinline__ float rw_sum_pass(const rw_row& R, rw_shared& sh, flo
             // grids finer than f32 scaling reaches, or on which terms below
             // the fast exp's range could round up: the crossing path
             const bool fine = sc == 0.0f || sc >= F::sc_max;
+            if (zero && tot == 0) {   // zero terms only: the sum stays a zero
+                s = s + 0.0f;
+                gpar ^= 1u;
+                return false;
+            }
             if (!fine && k + tot < ZS_BINADE) {
                 s = zs_grid_value(k + tot, eg);
                 gpar ^= 1u;
@@ -796,7 +861,7 @@ __device__ __forceinline__ float rw_sum_pass(const rw_row& R, rw_shared& sh, flo
             }
             uint32_t pre = 0, fl = 0;
             int c = 0;
-            if (!fine) {
+            if (!fine || zero) {
                 rw_group_reduce(qt, fl, gpar, sh);
                 c = rw_group_first(qt, fl, k, &pre);
             }
@@ -841,6 +906,10 @@ __device__ __forceinline__ float rw_sum_pass(const rw_row& R, rw_shared& sh, flo
 // output), glibc's exp for arguments the fast exp does not cover.
 struct rw_obs_terms {
     float M;
+    // whether a term of the four may be nonzero (glibc's expf is 0 below -104)
+    __device__ __forceinline__ bool nonzero(const float (&x)[4], const float (&)[4]) const {
+        return fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])) - M >= ZS_EXP_ZERO;
+    }
     // grids on which the fast path holds: a term below the fast exp's range
     // (below 2^-125) then rounds to 0
     static constexpr float sc_max = 0x1p123f;
@@ -892,6 +961,11 @@ struct rw_samp_terms {
             d[q] = z - zmax;
         }
     }
+    __device__ __forceinline__ bool nonzero(const float (&)[4], const float (&y)[4]) const {
+        float d[4];
+        args(y, d);
+        return fmaxf(fmaxf(d[0], d[1]), fmaxf(d[2], d[3])) >= ZS_EXP_ZERO;
+    }
     static constexpr float sc_max = 0x1p123f;
     __device__ __forceinline__ uint32_t fast(const float (&)[4], const float (&y)[4], float sc, uint32_t& fl) const {
         float d[4], a[4];
@@ -911,6 +985,9 @@ struct rw_samp_terms {
 // Terms of the entropy (hallucination.rs:139-144), fast exp (a tolerance output).
 struct rw_ent_terms {
     float M, inv, lns;
+    __device__ __forceinline__ bool nonzero(const float (&x)[4], const float (&)[4]) const {
+        return fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])) - M >= ZS_EXP_ZERO;
+    }
     // a term with an argument below the fast exp's range is below
     // 2^-125.5 * (104 + ln S) < 2^-118 (S >= 1, ln S < 13): 0 on these grids
     static constexpr float sc_max = 0x1p116f;

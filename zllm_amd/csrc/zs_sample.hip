@@ -3156,9 +3156,9 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
         ev++;
     };
     mark(nullptr);
+    if (a.b.pass_event && hipEventRecord((hipEvent_t)a.b.pass_event, stream) != hipSuccess) return -1;
     if (zs_row_launch(a, stream)) return zs_set_error(ctx, ZS_EHIP, "zs_sample: zs_k_row launch failed");
     mark("zs_k_row");
-    if (a.b.pass_event && hipEventRecord((hipEvent_t)a.b.pass_event, stream) != hipSuccess) return -1;
     hipLaunchKernelGGL(zs_k_pv, dim3((bt->V + ZS_BIG_G - 1) / ZS_BIG_G, B), dim3(ZS_BIG_NT), 0, stream, a);
     mark("zs_k_pv");
     hipLaunchKernelGGL(zs_k_tp_plan, dim3(B), dim3(ZS_BIG_NT), 0, stream, a);
