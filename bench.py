@@ -237,10 +237,10 @@ def make_step(W, V):
     step(out=None, overlap=True) -> (sampler outputs, (accepted, next)).
 
     The draft verification is independent of this step's sampling: it runs on
-    a second stream (default priority) once the sampler's first pass over the
-    logits is done (zs_batch.pass_event). It reads its logits once
-    (bandwidth-bound) and fills the CUs that the sampler's latency-bound
-    per-row kernels leave idle; the step ends when both are done."""
+    a second stream (default priority) from the point where the sampler's
+    kernels begin (zs_batch.pass_event). The sampler's row kernel holds one
+    workgroup per row and its rows finish at different times; the
+    verification fills the CUs that frees. The step ends when both are done."""
     import torch
     from zllm_amd.engine import verify_drafts
     ctx, sampler, bufs, xs, bits = W["ctx"], W["sampler"], W["bufs"], W["xs"], W["bits"]

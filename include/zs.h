@@ -239,12 +239,11 @@ typedef struct zs_batch {
     float* d_margin;
     float* d_chosen_lp;               /* [B] token_uncertainty.chosen_logprob */
     uint32_t* d_status;               /* [B] ZS_ST_* */
-    /* optional hipEvent_t, recorded on `stream` once the first full pass
-     * over the logits (with its candidate lists and moments) is done:
-     * independent bandwidth-bound work (draft verification of the same step)
-     * made to wait on it runs beside the mostly latency-bound per-row kernels
-     * that follow instead of holding back the start of the sampler. NULL: no
-     * event. */
+    /* optional hipEvent_t, recorded on `stream` where the sampler's kernels
+     * begin: independent work (draft verification of the same step) made to
+     * wait on it runs beside the sampler, on the CUs its per-row workgroups
+     * leave idle (rows finish at different times), instead of after it.
+     * NULL: no event. */
     void* pass_event;
 } zs_batch;
 

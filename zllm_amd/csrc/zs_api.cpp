@@ -71,9 +71,8 @@ extern "C" void zs_ctx_destroy(zs_ctx* ctx) {
         (void)hipEventDestroy((hipEvent_t)ctx->lane_event);
     }
     if (ctx->lane_host) (void)hipHostFree(ctx->lane_host);
-    void* ptrs[] = {ctx->p_cnt, ctx->p_id, ctx->p_flags, ctx->p_y, ctx->cst, ctx->cs_key, ctx->cs_idx,
-                    ctx->co_key, ctx->co_idx, ctx->rst, ctx->pairs, ctx->pv, ctx->mask_scratch, ctx->spec_chunks,
-                    ctx->spec_rows, ctx->sub_mom, ctx->sub_sum, ctx->p_sub, ctx->k_ap, ctx->k_sum, ctx->tp_bk, ctx->tp_cl, ctx->tp_pre, ctx->kcnt,
+    void* ptrs[] = {ctx->p_cnt, ctx->p_id, ctx->p_flags, ctx->p_y, ctx->rst, ctx->pairs, ctx->pv, ctx->mask_scratch, ctx->spec_chunks,
+                    ctx->spec_rows, ctx->p_sub, ctx->k_ap, ctx->k_sum, ctx->tp_bk, ctx->tp_cl, ctx->tp_pre, ctx->kcnt,
                     ctx->lane_temp, ctx->lane_topk, ctx->lane_topp, ctx->lane_seed, ctx->lane_vals,
                     ctx->lane_idxs, ctx->lane_ck, ctx->lane_cn};
     for (void* p : ptrs)
@@ -113,11 +112,6 @@ extern "C" int zs_ctx_create(int device, uint32_t max_rows, uint32_t max_vocab, 
     if (!rc) rc = zs_alloc(ctx, &ctx->p_id, R * ZS_MAX_PATCHES);
     if (!rc) rc = zs_alloc(ctx, &ctx->p_flags, R * ZS_MAX_PATCHES);
     if (!rc) rc = zs_alloc(ctx, &ctx->p_y, R * ZS_MAX_PATCHES);
-    if (!rc) rc = zs_alloc(ctx, &ctx->cst, R * C);
-    if (!rc) rc = zs_alloc(ctx, &ctx->cs_key, R * C * ZS_KS);
-    if (!rc) rc = zs_alloc(ctx, &ctx->cs_idx, R * C * ZS_KS);
-    if (!rc) rc = zs_alloc(ctx, &ctx->co_key, R * C * ZS_KO);
-    if (!rc) rc = zs_alloc(ctx, &ctx->co_idx, R * C * ZS_KO);
     if (!rc) rc = zs_alloc(ctx, &ctx->rst, R);
     if (!rc) rc = zs_alloc(ctx, &ctx->pairs, R * (size_t)max_vocab * 2);
     if (!rc) rc = zs_alloc(ctx, &ctx->pv, R * (size_t)max_vocab + 4);  // 16-byte loads at the tail
@@ -128,8 +122,6 @@ extern "C" int zs_ctx_create(int device, uint32_t max_rows, uint32_t max_vocab, 
                 hipDeviceSynchronize() != hipSuccess))
         rc = ZS_EHIP;
     if (!rc) rc = zs_alloc(ctx, &ctx->spec_chunks, R * (2 * ZS_SPEC_KMAX + 1) * C);
-    if (!rc) rc = zs_alloc(ctx, &ctx->sub_mom, R * ctx->max_subs);
-    if (!rc) rc = zs_alloc(ctx, &ctx->sub_sum, R * ZS_NSUM * ctx->max_subs);
     if (!rc) rc = zs_alloc(ctx, &ctx->p_sub, R * (ctx->max_subs + 1));
     if (!rc) rc = zs_alloc(ctx, &ctx->k_ap, R * ctx->max_subs);
     if (!rc) rc = zs_alloc(ctx, &ctx->k_sum, R * 2 * ctx->max_subs);

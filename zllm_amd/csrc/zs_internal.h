@@ -4,15 +4,14 @@
 #include <stdint.h>
 #include "../../include/zs.h"
 
-// Pass-1 chunking: 256 threads x 32 elements (8 float4 loads per thread).
-#define ZS_P1_NT 256
+// Chunks of 8192 ids: the granularity of per-row scratch records (kept-set
+// counts, draft-verification and batched-lane chunk records).
 #define ZS_P1_CH 8192
-// Candidate lists kept per chunk: sampler (top-k threshold / small-survivor
-// detection) and observers (top_logprobs + margin).
+// Largest top-k the row kernel selects by its sorted candidate list (above
+// it the big-row engine selects the threshold).
 #define ZS_KS 128
-#define ZS_KO 32
-// Largest vocabulary a context accepts (chunk lists of one row must fit the
-// combine kernel's on-chip sort: 32 chunks x 128).
+// Largest vocabulary a context accepts (the row kernel's patch bitmap and
+// the per-row chunk records are sized for it).
 #define ZS_MAX_VOCAB 262144
 #define ZS_DFA_LDS_BYTES 152576  // packed DFA table budget in LDS (149 KB)
 #define ZS_WALK_TILE 2048        // ids per tile of the vocab-parallel DFA walk
@@ -35,21 +34,6 @@
 #define ZS_CF_Z_PINF 4u
 #define ZS_CF_OBS_PINF 8u
 
-struct zs_chunk_stat {
-    float obs_max;       // NaN-ignoring max of x~
-    float z_max;         // NaN-ignoring max of z
-    uint32_t flags;
-    uint32_t z_finite;   // count of z that are not -inf and not NaN
-    int32_t g_last_nan;  // last index with NaN z (row index) or -1
-    uint32_t g_arg_all;  // argmax-last of z over the chunk (ties -> later)
-    float g_val_all;
-    uint32_t g_arg_tail; // argmax-last over elements after g_last_nan
-    float g_val_tail;
-    int32_t g_tail_n;    // number of elements after g_last_nan in the chunk
-    uint32_t ns, no;     // candidates written
-    uint32_t s_kth, o_kth; // key of the last (K-th) candidate when the list is full
-    uint32_t s_full, o_full;
-};
 
 // Sub-chunks of 1024 logits: the unit of the parallel exact-sum rounds.
 // Sub-chunk j of pass-1 chunk c is the j-th float4 of every pass-1 thread.
@@ -57,12 +41,6 @@ struct zs_chunk_stat {
 #define ZS_SUBS_PER_CHUNK (ZS_P1_CH / ZS_SUB)
 #define ZS_MAX_SUBS (ZS_MAX_VOCAB / ZS_SUB)
 
-// Approximate moments of a sub-chunk relative to its chunk's maxima (pass 1):
-// e1 = sum exp(x~ - obs_max_c), ed = sum (x~ - obs_max_c) exp(x~ - obs_max_c),
-// ez = sum exp(z - z_max_c).
-struct zs_sub_mom {
-    float e1, ed, ez, pad;
-};
 
 // Sums reproduced by the rounds.
 #define ZS_SUM_OBS_S 0
@@ -82,7 +60,7 @@ struct zs_sub_sum {
     uint32_t pad;
 };
 
-// Row modes decided by the combine kernel.
+// Row modes decided by the row kernel.
 #define ZS_MODE_DONE 1u   // token final (greedy / non-finite / small path)
 #define ZS_MODE_BIG 2u    // big-row engine must run
 
@@ -182,18 +160,11 @@ struct zs_ctx {
     uint32_t* p_id;
     uint32_t* p_flags;
     float* p_y;
-    zs_chunk_stat* cst;
-    uint32_t* cs_key;
-    uint32_t* cs_idx;
-    uint32_t* co_key;
-    uint32_t* co_idx;
     zs_row_state* rst;
     uint32_t* pairs;       // big-row gather area [rows][max_vocab][2]
     uint32_t* pv;          // big-row probabilities (f32 bits) [rows][max_vocab]
     void* mask_scratch;    // DFA mask viability flags [rows]
     uint32_t mask_epoch;   // last epoch handed to the packed DFA mask
-    zs_sub_mom* sub_mom;         // [rows][max_subs]
-    zs_sub_sum* sub_sum;         // [rows][ZS_NSUM][max_subs]
     double* k_ap;                // [rows][max_subs] approximate sums of the kept list per sub-chunk
     zs_sub_sum* k_sum;           // [rows][2][max_subs] kept-list rounds (sum2, draw)
     zs_tp_bucket* tp_bk;         // [rows][ZS_TP_NB] top-p buckets (zs_k_tp_*)

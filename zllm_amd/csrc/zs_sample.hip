@@ -7,15 +7,14 @@
 //   logprobs / token_uncertainty on x~    logprobs.rs:34-54, hallucination.rs:129-154
 //
 // Kernels (one launch each, in stream order):
-//   zs_k_prep     one workgroup per row: merge ban / bias / count-map lists into a
-//                 per-row list of patched token ids (y values computed exactly).
-//   zs_k_pass1    one workgroup per 8192-logit chunk: the only full HBM read.
-//                 Observer statistics, sampler max / greedy argmax / flags, and
-//                 exact top-K candidate lists (LDS radix select on total-order keys).
-//   zs_k_combine  one workgroup per row: merges chunk results; finishes greedy,
-//                 non-finite and small-survivor rows exactly on chip.
-//   zs_k_big      one 1024-thread workgroup per remaining row: exact emulation of
-//                 the reference's sequential f32 sums (S, min-p, top-p, draw).
+//   zs_k_row      (zs_row.hip) one workgroup per row: patch list, candidate
+//                 lists, the sampler's decisions (greedy, non-finite, top-k and
+//                 small survivor sets sampled on chip), the observers' S and
+//                 entropy, and the sampler's S of the remaining ("big") rows.
+//   zs_k_pv .. zs_k_tp_sort   big rows: survivor values and the top-p bucket plan.
+//   zs_k_big      one 1024-thread workgroup per big row: exact emulation of the
+//                 reference's sequential f32 sums (min-p, top-p, draw).
+//   zs_k_kcount, zs_k_kwrite, zs_k_roundK, zs_k_stitchK   the kept list's sums.
 //   zs_k_final    chosen-token outputs.
 //
 // Exactness: every value that decides the sampled id is computed with the same
@@ -29,1506 +28,11 @@
 #include "zs_terms.h"
 #include "zs_sampler.h"
 
-// ===========================================================================
-// zs_k_prep: per-row patch list.
-// Entries are (id << 32) | (kind << 28) | order with kind 0 = ban, 1 = bias,
-// 2 = count; sorting groups them by id with bans first and biases in list
-// order, which reproduces the reference's per-token operation sequence.
-// ===========================================================================
-#define ZS_PREP_NT 256
-__global__ __launch_bounds__(ZS_PREP_NT) void zs_k_prep(zs_sargs a) {
-    const uint32_t r = blockIdx.x;
-    const zs_batch& b = a.b;
-    __shared__ unsigned long long ent[ZS_MAX_PATCHES];
-    __shared__ uint32_t scan_sh[ZS_PREP_NT / 64];
-    __shared__ uint32_t n_sh;
-    const zs_row_params P = b.d_params[r];
-    const uint32_t V = b.V;
-    uint32_t ban0 = b.d_ban_off ? b.d_ban_off[r] : 0, ban1 = b.d_ban_off ? b.d_ban_off[r + 1] : 0;
-    uint32_t bi0 = b.d_bias_off ? b.d_bias_off[r] : 0, bi1 = b.d_bias_off ? b.d_bias_off[r + 1] : 0;
-    uint32_t c0 = b.d_cnt_off ? b.d_cnt_off[r] : 0, c1 = b.d_cnt_off ? b.d_cnt_off[r + 1] : 0;
-    const bool pen = zs_penalty_active(P);
-    if (!pen) { c1 = c0; }  // counts only matter when penalties are active
-    uint32_t nb = ban1 - ban0, nbi = bi1 - bi0, nc = c1 - c0;
-    uint32_t total = nb + nbi + nc;
-    if (threadIdx.x == 0) n_sh = 0;
-    __syncthreads();
-    if (total > ZS_MAX_PATCHES) {
-        if (threadIdx.x == 0) {
-            a.p_cnt[r] = 0;
-            a.rst[r].status = ZS_ST_LIMIT;
-        }
-        const uint32_t nsub = (V + ZS_SUB - 1) / ZS_SUB;
-        for (uint32_t j = threadIdx.x; j <= nsub; j += ZS_PREP_NT) a.p_sub[(size_t)r * (a.max_subs + 1) + j] = 0;
-        return;
-    }
-    // gather entries with id < V
-    for (uint32_t i = threadIdx.x; i < total; i += ZS_PREP_NT) {
-        uint32_t id, kind, ord;
-        if (i < nb) { id = b.d_ban_ids[ban0 + i]; kind = 0; ord = i; }
-        else if (i < nb + nbi) { ord = i - nb; id = b.d_bias_ids[bi0 + ord]; kind = 1; }
-        else { ord = i - nb - nbi; id = b.d_cnt_ids[c0 + ord]; kind = 2; }
-        if (id < V) {
-            uint32_t pos = atomicAdd(&n_sh, 1u);
-            ent[pos] = ((unsigned long long)id << 32) | ((unsigned long long)kind << 28) | ord;
-        }
-    }
-    __syncthreads();
-    uint32_t n = n_sh;
-    uint32_t np2 = 1;
-    while (np2 < n) np2 <<= 1;
-    for (uint32_t i = n + threadIdx.x; i < np2; i += ZS_PREP_NT) ent[i] = ~0ull;
-    __syncthreads();
-    if (np2 > 1) block_sort_u64<ZS_PREP_NT>(ent, np2);
-    // segment starts -> output slots
-    uint32_t* out_id = a.p_id + (size_t)r * ZS_MAX_PATCHES;
-    uint32_t* out_fl = a.p_flags + (size_t)r * ZS_MAX_PATCHES;
-    float* out_y = a.p_y + (size_t)r * ZS_MAX_PATCHES;
-    uint32_t base_out = 0;
-    for (uint32_t s0 = 0; s0 < n; s0 += ZS_PREP_NT) {
-        uint32_t i = s0 + threadIdx.x;
-        uint32_t is_start = 0;
-        if (i < n) {
-            uint32_t id = (uint32_t)(ent[i] >> 32);
-            is_start = (i == 0) || ((uint32_t)(ent[i - 1] >> 32) != id);
-        }
-        uint32_t tot;
-        uint32_t ex = block_excl_scan_u<ZS_PREP_NT>(is_start, scan_sh, &tot);
-        if (is_start) {
-            uint32_t id = (uint32_t)(ent[i] >> 32);
-            float x = b.d_logits[(size_t)r * b.ld + id];
-            if ((P.flags & ZS_ROW_MASKED) && b.d_allow_bits && !zs_allowed_bit(b, r, id)) x = -INFINITY;
-            uint32_t fl = 0;
-            float y;
-            uint32_t j = i;
-            // bans (logit_fsm.rs:248-252)
-            while (j < n && (uint32_t)(ent[j] >> 32) == id && ((ent[j] >> 28) & 3ull) == 0) {
-                fl |= ZS_PF_BAN;
-                j++;
-            }
-            if (fl & ZS_PF_BAN) x = -INFINITY;
-            y = x;
-            // logit_bias in list order (decode_ctrl.rs:108-112)
-            while (j < n && (uint32_t)(ent[j] >> 32) == id && ((ent[j] >> 28) & 3ull) == 1) {
-                uint32_t ord = (uint32_t)(ent[j] & 0x0fffffffull);
-                y = y + b.d_bias_vals[bi0 + ord];
-                fl |= ZS_PF_Y;
-                j++;
-            }
-            // penalty (decode_ctrl.rs:113-125)
-            if (j < n && (uint32_t)(ent[j] >> 32) == id && ((ent[j] >> 28) & 3ull) == 2) {
-                uint32_t ord = (uint32_t)(ent[j] & 0x0fffffffull);
-                uint32_t cnt = b.d_cnt_vals[c0 + ord];
-                if (P.repeat != 1.0f) {
-                    if (y > 0.0f) y = y / P.repeat;
-                    else y = y * P.repeat;
-                }
-                float pen_v = __fmul_rn(P.frequency, (float)cnt);
-                pen_v = __fadd_rn(pen_v, P.presence);
-                y = __fsub_rn(y, pen_v);
-                fl |= ZS_PF_Y;
-            }
-            out_id[base_out + ex] = id;
-            out_fl[base_out + ex] = fl;
-            out_y[base_out + ex] = y;
-        }
-        base_out += tot;
-    }
-    if (threadIdx.x == 0) {
-        a.p_cnt[r] = base_out;
-        a.rst[r].status = 0;
-    }
-    // first patch of every sub-chunk (patch ids are sorted and unique)
-    __threadfence_block();
-    __syncthreads();
-    const uint32_t nsub = (V + ZS_SUB - 1) / ZS_SUB;
-    uint32_t* psub = a.p_sub + (size_t)r * (a.max_subs + 1);
-    for (uint32_t j = threadIdx.x; j <= nsub; j += ZS_PREP_NT) {
-        uint32_t lo = 0, hi = base_out, key = j * ZS_SUB;
-        while (lo < hi) { uint32_t mid = (lo + hi) >> 1; if (out_id[mid] < key) lo = mid + 1; else hi = mid; }
-        psub[j] = lo;
-    }
-}
-
-// ===========================================================================
-// zs_k_pass1
-// ===========================================================================
-#define P1_EPT (ZS_P1_CH / ZS_P1_NT)
-
-#define P1_SUP 1024
-#define P1_SORT 256
-struct p1_red {
-    float omax, zmax;
-    uint32_t fl, zfin, zabove, xabove;
-    int last_nan;
-};
-struct p1_shared {
-    p1_red red[ZS_P1_NT / 64];
-    uint32_t hist[256];
-    uint32_t u[8];
-    int i[8];
-    float f[8];
-    double d[8];
-    uint32_t cnt;
-    uint32_t prefix, need, found;
-    uint32_t pcur0, pcur1;
-    uint32_t tmax[ZS_P1_NT];
-    uint32_t skey[P1_SUP];
-    uint32_t sidx[P1_SUP];
-    uint32_t sel[4];
-    unsigned long long s64[P1_SORT];
-};
-
-// Exact top-K (key desc, index asc) of the chunk's valid keys; writes the
-// candidates (unordered) to out_key/out_idx. Element e = j*4+q of thread t has
-// index base + (j*256 + t)*4 + q.
-__device__ __forceinline__ void p1_topk(const uint32_t (&kv)[P1_EPT], uint32_t vmask, uint32_t nvalid, uint32_t K,
-                        uint32_t base, uint32_t* out_key, uint32_t* out_idx, uint32_t* n_out, uint32_t* kth,
-                        uint32_t* full, p1_shared& sh) {
-    const int t = threadIdx.x;
-    if (t == 0) sh.cnt = 0;
-    __syncthreads();
-    if (nvalid <= K) {
-        for (int e = 0; e < P1_EPT; e++) {
-            if ((vmask >> e) & 1u) {
-                uint32_t pos = atomicAdd(&sh.cnt, 1u);
-                if (pos < K) {
-                    out_key[pos] = kv[e];
-                    out_idx[pos] = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
-                }
-            }
-        }
-        __syncthreads();
-        *n_out = min(sh.cnt, K);
-        *kth = 0;
-        *full = 0;
-        return;
-    }
-    uint32_t prefix = 0, mask = 0, need = K;
-    for (int shift = 24; shift >= 0; shift -= 8) {
-        if (t < 256) sh.hist[t] = 0;
-        __syncthreads();
-        for (int e = 0; e < P1_EPT; e++)
-            if (((vmask >> e) & 1u) && (kv[e] & mask) == prefix)
-                atomicAdd(&sh.hist[(kv[e] >> shift) & 255u], 1u);
-        __syncthreads();
-        if (t < 64) {
-            // lane l owns bins 255-4l .. 252-4l (descending)
-            uint32_t c[4], loc = 0;
-            for (int q = 0; q < 4; q++) { c[q] = sh.hist[255 - 4 * t - q]; loc += c[q]; }
-            uint32_t inc = wave_incl_scan_u(loc);
-            uint32_t before = inc - loc;
-            for (int q = 0; q < 4; q++) {
-                if (before < need && need <= before + c[q]) {
-                    sh.found = 255 - 4 * t - q;
-                    sh.need = need - before;
-                }
-                before += c[q];
-            }
-        }
-        __syncthreads();
-        prefix |= sh.found << shift;
-        mask |= 0xffu << shift;
-        need = sh.need;
-        __syncthreads();
-    }
-    const uint32_t kk = prefix;
-    uint32_t my_eq = 0;
-    for (int e = 0; e < P1_EPT; e++) {
-        if (!((vmask >> e) & 1u)) continue;
-        if (kv[e] > kk) {
-            uint32_t pos = atomicAdd(&sh.cnt, 1u);
-            if (pos < K) {
-                out_key[pos] = kv[e];
-                out_idx[pos] = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
-            }
-        } else if (kv[e] == kk) {
-            my_eq++;
-        }
-    }
-    uint32_t n_eq = block_sum_u<ZS_P1_NT>(my_eq, sh.u);
-    if (n_eq == need) {
-        for (int e = 0; e < P1_EPT; e++) {
-            if (((vmask >> e) & 1u) && kv[e] == kk) {
-                uint32_t pos = atomicAdd(&sh.cnt, 1u);
-                if (pos < K) {
-                    out_key[pos] = kv[e];
-                    out_idx[pos] = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
-                }
-            }
-        }
-    } else {
-        // lowest-index `need` elements among the equal ones, in index order
-        uint32_t carry = 0;
-        for (int j = 0; j < P1_EPT / 4; j++) {
-            uint32_t c = 0;
-            for (int q = 0; q < 4; q++) {
-                int e = j * 4 + q;
-                c += (((vmask >> e) & 1u) && kv[e] == kk) ? 1u : 0u;
-            }
-            uint32_t tot;
-            uint32_t ex = block_excl_scan_u<ZS_P1_NT>(c, sh.u, &tot);
-            uint32_t rank = carry + ex;
-            for (int q = 0; q < 4; q++) {
-                int e = j * 4 + q;
-                if (((vmask >> e) & 1u) && kv[e] == kk) {
-                    if (rank < need) {
-                        uint32_t pos = atomicAdd(&sh.cnt, 1u);
-                        if (pos < K) {
-                            out_key[pos] = kv[e];
-                            out_idx[pos] = base + (j * ZS_P1_NT + t) * 4 + q;
-                        }
-                    }
-                    rank++;
-                }
-            }
-            carry += tot;
-        }
-    }
-    __syncthreads();
-    *n_out = min(sh.cnt, K);
-    *kth = kk;
-    *full = (n_eq > need) ? 2u : 1u;  // 2: equal keys were left out
-    __syncthreads();
-}
-
-
-// Fast exact top-K. Every wave sorts its 64 per-thread maxima; the c-th largest
-// of them, c = ceil(K / 4), has at least c elements of its wave at or above
-// it, so theta = the smallest of the four waves' values has at least K
-// elements of the chunk at or above it: theta bounds the chunk's K-th largest
-// key from below. The elements >= theta (a small superset of the top-K, with
-// every element equal to the K-th key) are sorted by (key desc, index asc) --
-// one wave for up to 64 of them, the workgroup for up to P1_SORT -- and the
-// first K are the answer. Degenerate chunks (larger supersets) use the LDS
-// radix select.
-// nvalid: valid elements of the chunk; nfin: valid elements whose key is above
-// that of -inf.
-__device__ __forceinline__ void p1_topk_fast(const uint32_t (&kv)[P1_EPT], uint32_t vmask, uint32_t nvalid,
-                             uint32_t nfin, uint32_t K, uint32_t base,
-                             uint32_t* out_key, uint32_t* out_idx, uint32_t* n_out, uint32_t* kth,
-                             uint32_t* full, p1_shared& sh) {
-    const int t = threadIdx.x;
-    uint32_t tm = 0;
-#pragma unroll
-    for (int e = 0; e < P1_EPT; e++)
-        if ((vmask >> e) & 1u) tm = max(tm, kv[e]);
-    const uint32_t c = (K + (ZS_P1_NT / 64) - 1) / (ZS_P1_NT / 64);
-    if (nvalid <= K || c > 64) {
-        p1_topk(kv, vmask, nvalid, K, base, out_key, out_idx, n_out, kth, full, sh);
-        return;
-    }
-    // Fewer than K values above -inf (a masked chunk): all of them plus the
-    // lowest-index -inf elements make the top-K.
-    const uint32_t kninf = zs_total_key(-INFINITY);
-    if (nfin < K) {
-        if (t == 0) sh.cnt = 0;
-        __syncthreads();
-#pragma unroll
-        for (int e = 0; e < P1_EPT; e++) {
-            if (((vmask >> e) & 1u) && kv[e] > kninf) {
-                const uint32_t p = atomicAdd(&sh.cnt, 1u);
-                out_key[p] = kv[e];
-                out_idx[p] = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
-            }
-        }
-        // -inf elements in index order: ids base + (j * NT + t) * 4 + q
-        const uint32_t need = K - nfin;
-        uint32_t carry = 0, ninf = 0;
-        const uint32_t ninf_all = nvalid - nfin;
-#pragma unroll
-        for (int j = 0; j < P1_EPT / 4; j++) {
-            if (carry >= need) break;  // uniform: the lowest ids are taken
-            uint32_t cj = 0;
-#pragma unroll
-            for (int q = 0; q < 4; q++) cj += (((vmask >> (4 * j + q)) & 1u) && kv[4 * j + q] == kninf) ? 1u : 0u;
-            uint32_t tot;
-            uint32_t rank = carry + block_excl_scan_u<ZS_P1_NT>(cj, sh.u, &tot);
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const int e = 4 * j + q;
-                if (((vmask >> e) & 1u) && kv[e] == kninf) {
-                    if (rank < need) {
-                        out_key[nfin + rank] = kninf;
-                        out_idx[nfin + rank] = base + (j * ZS_P1_NT + t) * 4 + q;
-                    }
-                    rank++;
-                }
-            }
-            carry += tot;
-            ninf += tot;
-        }
-        __syncthreads();
-        (void)ninf;
-        *n_out = min(K, nfin + ninf_all);
-        *kth = kninf;
-        *full = ninf_all > need ? 2u : 1u;
-        __syncthreads();
-        return;
-    }
-    // theta: a lower bound of the K-th largest key. Thread maxima belong to
-    // distinct elements, so the K-th largest of the workgroup's 256 thread
-    // maxima has at least K elements at or above it. Each wave sorts its 64;
-    // for K <= 64 wave 0 merges the four sorted lists (elementwise max of an
-    // ascending and a descending list keeps the larger half as a bitonic
-    // sequence, which six exchange steps sort). For K > 64: the c-th largest
-    // thread maximum of every wave, c = ceil(K / 4), and their minimum.
-    // Threads without elements hold key 0, below every element.
-    const int lane = zs_lane();
-    const uint32_t srt = wave_sort_u32(tm);
-    uint32_t theta;
-    if (K <= 64) {
-        sh.tmax[zs_wid() * 64 + lane] = srt;
-        __syncthreads();
-        if (t < 64) {
-            uint32_t m = srt;
-#pragma unroll
-            for (int w = 1; w < ZS_P1_NT / 64; w++) {
-                m = max(m, sh.tmax[w * 64 + 63 - lane]);
-#pragma unroll
-                for (int j = 32; j > 0; j >>= 1) {
-                    const uint32_t o = __shfl_xor(m, j, 64);
-                    m = (lane & j) ? max(m, o) : min(m, o);
-                }
-            }
-            if (lane == 64 - (int)K) sh.sel[0] = m;
-        }
-        __syncthreads();
-        theta = sh.sel[0];
-    } else {
-        const uint32_t thw = __shfl(srt, 64 - (int)c, 64);
-        if (lane == 0) sh.sel[zs_wid()] = thw;
-        __syncthreads();
-        theta = sh.sel[0];
-#pragma unroll
-        for (int w = 1; w < ZS_P1_NT / 64; w++) theta = min(theta, sh.sel[w]);
-    }
-    uint32_t cnt = 0;
-#pragma unroll
-    for (int e = 0; e < P1_EPT; e++) cnt += (((vmask >> e) & 1u) && kv[e] >= theta) ? 1u : 0u;
-    uint32_t nsup;
-    uint32_t pos = block_excl_scan_u<ZS_P1_NT>(cnt, sh.u, &nsup);
-    if (nsup > P1_SORT) {
-        p1_topk(kv, vmask, nvalid, K, base, out_key, out_idx, n_out, kth, full, sh);
-        return;
-    }
-    // composite ((~key) << 32 | index): ascending order = key desc, index asc
-#pragma unroll
-    for (int e = 0; e < P1_EPT; e++) {
-        if (((vmask >> e) & 1u) && kv[e] >= theta) {
-            const uint32_t idx = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
-            sh.s64[pos++] = ((unsigned long long)(~kv[e]) << 32) | idx;
-        }
-    }
-    __syncthreads();
-    if (nsup <= 64) {
-        if (t < 64) {
-            unsigned long long v = (uint32_t)t < nsup ? sh.s64[t] : ~0ull;
-            v = wave_sort_u64(v);
-            const unsigned long long vk = __shfl(v, (int)K - 1, 64);
-            const unsigned long long vn = __shfl(v, min((int)K, 63), 64);
-            if ((uint32_t)t < K) { out_key[t] = ~(uint32_t)(v >> 32); out_idx[t] = (uint32_t)v; }
-            if (t == 0) {
-                sh.sel[0] = ~(uint32_t)(vk >> 32);
-                sh.sel[1] = (K < nsup && (uint32_t)(vn >> 32) == (uint32_t)(vk >> 32)) ? 2u : 1u;
-            }
-        }
-    } else {
-        for (uint32_t i = nsup + t; i < P1_SORT; i += ZS_P1_NT) sh.s64[i] = ~0ull;
-        __syncthreads();
-        block_sort_reg_u64<ZS_P1_NT, P1_SORT / ZS_P1_NT>(sh.s64, P1_SORT);
-        for (uint32_t i = t; i < K; i += ZS_P1_NT) {
-            const unsigned long long v = sh.s64[i];
-            out_key[i] = ~(uint32_t)(v >> 32);
-            out_idx[i] = (uint32_t)v;
-        }
-        if (t == 0) {
-            const uint32_t hk = (uint32_t)(sh.s64[K - 1] >> 32);
-            sh.sel[0] = ~hk;
-            sh.sel[1] = (K < nsup && (uint32_t)(sh.s64[K] >> 32) == hk) ? 2u : 1u;
-        }
-    }
-    __syncthreads();
-    *n_out = K;
-    *kth = sh.sel[0];
-    *full = sh.sel[1];
-    __syncthreads();
-}
-
-// Observer candidates without the exact cut: every element whose key is at
-// least theta, the K-th largest thread maximum (K <= 64), when at most `cap`
-// of them exist. The list then holds the chunk's top K (and possibly more), in
-// any order -- what the combine kernel's merge needs. Returns false (nothing
-// written) when more than `cap` elements reach theta.
-__device__ __forceinline__ bool p1_superset(const uint32_t (&kv)[P1_EPT], uint32_t vmask, uint32_t K, uint32_t cap,
-                                            uint32_t base, uint32_t* out_key, uint32_t* out_idx, uint32_t* n_out,
-                                            p1_shared& sh) {
-    const int t = threadIdx.x, lane = zs_lane();
-    uint32_t tm = 0;
-#pragma unroll
-    for (int e = 0; e < P1_EPT; e++)
-        if ((vmask >> e) & 1u) tm = max(tm, kv[e]);
-    const uint32_t srt = wave_sort_u32(tm);
-    sh.tmax[zs_wid() * 64 + lane] = srt;
-    if (t == 0) sh.cnt = 0;
-    __syncthreads();
-    if (t < 64) {
-        uint32_t m = srt;
-#pragma unroll
-        for (int w = 1; w < ZS_P1_NT / 64; w++) {
-            m = max(m, sh.tmax[w * 64 + 63 - lane]);
-#pragma unroll
-            for (int j = 32; j > 0; j >>= 1) {
-                const uint32_t o = __shfl_xor(m, j, 64);
-                m = (lane & j) ? max(m, o) : min(m, o);
-            }
-        }
-        if (lane == 64 - (int)K) sh.sel[2] = m;
-    }
-    __syncthreads();
-    const uint32_t theta = max(sh.sel[2], 1u);
-    uint32_t cnt = 0;
-#pragma unroll
-    for (int e = 0; e < P1_EPT; e++) cnt += (((vmask >> e) & 1u) && kv[e] >= theta) ? 1u : 0u;
-    const uint32_t nsup = block_sum_u<ZS_P1_NT>(cnt, sh.u);
-    if (nsup > cap) return false;
-#pragma unroll
-    for (int e = 0; e < P1_EPT; e++) {
-        if (((vmask >> e) & 1u) && kv[e] >= theta) {
-            const uint32_t p = atomicAdd(&sh.cnt, 1u);
-            out_key[p] = kv[e];
-            out_idx[p] = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
-        }
-    }
-    *n_out = nsup;
-    return true;
-}
-
-// Compaction of the chunk's finite sampler values (the list when the chunk has
-// at most K of them: then it holds every element a top-k or a small-survivor
-// path can keep).
-__device__ __forceinline__ void p1_finite(const uint32_t (&zv)[P1_EPT], uint32_t vmask,
-                          uint32_t base, uint32_t* out_key, uint32_t* out_idx, p1_shared& sh) {
-    const int t = threadIdx.x;
-    uint32_t cnt = 0;
-    const uint32_t kninf = zs_total_key(-INFINITY), kpinf = zs_total_key(INFINITY);
-    // z > -inf: keys above that of -inf, NaN (above +inf) excluded
-#pragma unroll
-    for (int e = 0; e < P1_EPT; e++) cnt += (((vmask >> e) & 1u) && zv[e] > kninf && zv[e] <= kpinf) ? 1u : 0u;
-    uint32_t tot;
-    uint32_t pos = block_excl_scan_u<ZS_P1_NT>(cnt, sh.u, &tot);
-#pragma unroll
-    for (int e = 0; e < P1_EPT; e++) {
-        if (((vmask >> e) & 1u) && zv[e] > kninf && zv[e] <= kpinf) {
-            out_key[pos] = zv[e];
-            out_idx[pos] = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
-            pos++;
-        }
-    }
-}
-
-// element e of the calling thread in a [P1_EPT][ZS_P1_NT] LDS array
-struct p1_lds_arr {
-    uint32_t* p;
-    __device__ __forceinline__ uint32_t& operator[](int e) const { return p[e * ZS_P1_NT]; }
-};
-
-__global__ __launch_bounds__(ZS_P1_NT) __attribute__((amdgpu_waves_per_eu(3))) void zs_k_pass1(zs_sargs a) {
-    const uint32_t c = blockIdx.x, r = blockIdx.y;
-    const zs_batch& b = a.b;
-    const uint32_t V = b.V;
-    const uint32_t base = c * ZS_P1_CH;
-    if (base >= V) return;
-    __shared__ p1_shared sh;
-    const int t = threadIdx.x;
-    const zs_row_params P = b.d_params[r];
-    const float T = P.temperature;
-    const bool masked = (P.flags & ZS_ROW_MASKED) && b.d_allow_bits;
-    const float* row = b.d_logits + (size_t)r * b.ld;
-
-    // patch range of this chunk (patch ids are sorted; zs_k_prep stored the
-    // first patch of every 1024-id sub-chunk)
-    const uint32_t* pid = a.p_id + (size_t)r * ZS_MAX_PATCHES;
-    const uint32_t* psub = a.p_sub + (size_t)r * (a.max_subs + 1);
-    const uint32_t nsub_row = (V + ZS_SUB - 1) / ZS_SUB;
-    const uint32_t pc0 = psub[c * ZS_SUBS_PER_CHUNK];
-    const uint32_t pc1 = psub[min((c + 1) * ZS_SUBS_PER_CHUNK, nsub_row)];
-
-    // x~ lives in LDS as total-order keys (thread t's element e at xsh[e][t])
-    // until the observer list, z in registers (keys after the temperature):
-    // both arrays in registers would halve occupancy. Every later use compares
-    // keys; the float is recovered where arithmetic needs it.
-    __shared__ uint32_t xsh[P1_EPT][ZS_P1_NT];
-    const p1_lds_arr xo{&xsh[0][t]};
-    const uint32_t kninf = zs_total_key(-INFINITY), kpinf = zs_total_key(INFINITY);
-    float zv[P1_EPT];
-    uint32_t vmask = 0;
-#pragma unroll
-    for (int j = 0; j < P1_EPT / 4; j++) {
-        uint32_t idx = base + (j * ZS_P1_NT + t) * 4;
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        uint32_t w = 0xffffffffu;
-        if (idx < V) {
-            v = *reinterpret_cast<const float4*>(row + idx);
-            if (masked) w = b.d_allow_bits[(size_t)r * b.allow_words + (idx >> 5)] >> (idx & 31);
-        }
-        float vv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            int e = j * 4 + q;
-            bool valid = idx + q < V;
-            float x = vv[q];
-            if (masked && !((w >> q) & 1u)) x = -INFINITY;
-            if (!valid) x = -INFINITY;  // neutral in every statistic
-            xo[e] = zs_total_key(x);
-            zv[e] = x;
-            if (valid) vmask |= 1u << e;
-        }
-    }
-    __syncthreads();
-    // patches: bans change x~, bias/penalty set y. Staged through LDS a
-    // batch at a time (one load per thread), then each thread applies those
-    // that fall on its elements.
-    {
-        const uint32_t* pfl = a.p_flags + (size_t)r * ZS_MAX_PATCHES;
-        const float* py = a.p_y + (size_t)r * ZS_MAX_PATCHES;
-        for (uint32_t pb = pc0; pb < pc1; pb += ZS_P1_NT) {
-            const uint32_t n = min((uint32_t)ZS_P1_NT, pc1 - pb);
-            if ((uint32_t)t < n) {
-                sh.skey[t] = pid[pb + t] - base;
-                sh.sidx[t] = pfl[pb + t];
-                sh.tmax[t] = zs_f2u(py[pb + t]);
-            }
-            __syncthreads();
-            for (uint32_t i = 0; i < n; i++) {
-                const uint32_t off = sh.skey[i];
-                const uint32_t q = off & 3, tt = (off >> 2) % ZS_P1_NT, j = (off >> 2) / ZS_P1_NT;
-                if ((int)tt != t) continue;
-                const uint32_t fl = sh.sidx[i];
-                const float y = zs_u2f(sh.tmax[i]);
-#pragma unroll
-                for (int jj = 0; jj < P1_EPT / 4; jj++)
-#pragma unroll
-                    for (int qq = 0; qq < 4; qq++)
-                        if (jj == (int)j && qq == (int)q) {
-                            if (fl & ZS_PF_BAN) { xo[jj * 4 + qq] = kninf; zv[jj * 4 + qq] = -INFINITY; }
-                            if (fl & ZS_PF_Y) zv[jj * 4 + qq] = y;
-                        }
-            }
-            __syncthreads();
-        }
-    }
-    // z = y / T, kept as keys
-    uint32_t kz[P1_EPT];
-#pragma unroll
-    for (int e = 0; e < P1_EPT; e++) kz[e] = zs_total_key(zs_temper(zv[e], T));
-
-    // ---- chunk statistics of x~ (observers) and z (sampler), one workgroup
-    // reduction: maxima, NaN / +inf flags, the last NaN of z, and counts of
-    // finite z and of elements whose key is above that of -inf for the lists
-    // branch-free on keys: NaN keys lie above +inf's (positive) or below
-    // -inf's (negative); the maxima skip them (fmaxf semantics); the rare
-    // waves with a NaN z redo their elements for the last NaN and the finite
-    // count (+inf counts as finite there: the test is z > -inf)
-    uint32_t okm = kninf, zkm = kninf;
-    uint32_t fl = 0, zfin, zabove = 0, xabove = 0;
-    bool xnan = false, znan = false;
-    int last_nan = -1;
-#pragma unroll
-    for (int e = 0; e < P1_EPT; e++) {
-        const uint32_t kx = xo[e], k = kz[e];
-        xnan |= (kx > kpinf) | (kx < kninf);
-        znan |= (k > kpinf) | (k < kninf);
-        okm = max(okm, kx <= kpinf ? kx : kninf);
-        zkm = max(zkm, k <= kpinf ? k : kninf);
-        xabove += kx > kninf ? 1u : 0u;
-        zabove += k > kninf ? 1u : 0u;
-    }
-    zfin = zabove;
-    if (__ballot(znan)) {
-        zfin = 0;
-#pragma unroll
-        for (int e = 0; e < P1_EPT; e++) {
-            if (!((vmask >> e) & 1u)) continue;
-            const uint32_t k = kz[e];
-            const uint32_t idx = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
-            if (k > kpinf || k < kninf) last_nan = max(last_nan, (int)idx);
-            zfin += (k > kninf && k <= kpinf) ? 1u : 0u;
-        }
-    }
-    if (xnan) fl |= ZS_CF_OBS_NAN;
-    if (znan) fl |= ZS_CF_Z_NAN;
-    if (zkm == kpinf) fl |= ZS_CF_Z_PINF;
-    float omax = zs_key_to_float(okm), zmax = zs_key_to_float(zkm);
-    for (int d = 32; d > 0; d >>= 1) {
-        omax = fmaxf(omax, __shfl_xor(omax, d, 64));
-        zmax = fmaxf(zmax, __shfl_xor(zmax, d, 64));
-        fl |= __shfl_xor(fl, d, 64);
-        zfin += __shfl_xor(zfin, d, 64);
-        zabove += __shfl_xor(zabove, d, 64);
-        xabove += __shfl_xor(xabove, d, 64);
-        last_nan = max(last_nan, __shfl_xor(last_nan, d, 64));
-    }
-    if (zs_lane() == 0) {
-        p1_red& R = sh.red[zs_wid()];
-        R.omax = omax; R.zmax = zmax; R.fl = fl; R.zfin = zfin;
-        R.zabove = zabove; R.xabove = xabove; R.last_nan = last_nan;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int w = 0; w < ZS_P1_NT / 64; w++) {
-        const p1_red& R = sh.red[w];
-        omax = fmaxf(omax, R.omax); zmax = fmaxf(zmax, R.zmax); fl |= R.fl;
-        last_nan = max(last_nan, R.last_nan);
-    }
-    zfin = zabove = xabove = 0;
-#pragma unroll
-    for (int w = 0; w < ZS_P1_NT / 64; w++) {
-        zfin += sh.red[w].zfin; zabove += sh.red[w].zabove; xabove += sh.red[w].xabove;
-    }
-    const uint32_t nvalid = min((uint32_t)ZS_P1_CH, V - base);
-    // greedy: argmax-last (ties -> larger index) over all, and over the tail
-    // after the chunk's last NaN (the whole chunk when it has no NaN). A pair
-    // (value key, index + 1) compares by key, then by index; 0 = none.
-    unsigned long long best_all = 0, best_tail = 0;
-    int tail_n = 0;
-    if (T <= 0.0f) {  // greedy rows only (uniform per workgroup)
-        uint32_t bk = 0, bi = 0, tk = 0, ti = 0;
-        uint32_t tn = 0;
-#pragma unroll
-        for (int e = 0; e < P1_EPT; e++) {
-            const float z = zs_key_to_float(kz[e]);
-            if (!((vmask >> e) & 1u) || z != z) continue;
-            const uint32_t idx = base + ((e >> 2) * ZS_P1_NT + t) * 4 + (e & 3);
-            // -0.0 and +0.0 compare equal in the reference (partial_cmp): map both to +0
-            const uint32_t k = zs_total_key(z == 0.0f ? 0.0f : z);
-            if (k >= bk) { bk = k; bi = idx + 1; }  // ids ascend with e: ties -> later
-            if ((int)idx > last_nan) {
-                tn++;
-                if (k >= tk) { tk = k; ti = idx + 1; }
-            }
-        }
-        best_all = ((unsigned long long)bk << 32) | bi;
-        best_tail = ((unsigned long long)tk << 32) | ti;
-        __shared__ unsigned long long u64sh[2][ZS_P1_NT / 64];
-        for (int d = 32; d > 0; d >>= 1) {
-            unsigned long long o1 = __shfl_xor(best_all, d, 64);
-            unsigned long long o2 = __shfl_xor(best_tail, d, 64);
-            best_all = o1 > best_all ? o1 : best_all;
-            best_tail = o2 > best_tail ? o2 : best_tail;
-        }
-        if (zs_lane() == 0) { u64sh[0][zs_wid()] = best_all; u64sh[1][zs_wid()] = best_tail; }
-        __syncthreads();
-        for (int i = 0; i < ZS_P1_NT / 64; i++) {
-            best_all = u64sh[0][i] > best_all ? u64sh[0][i] : best_all;
-            best_tail = u64sh[1][i] > best_tail ? u64sh[1][i] : best_tail;
-        }
-        __syncthreads();
-        tail_n = (int)block_sum_u<ZS_P1_NT>(tn, sh.u);
-    }
-
-    // ---- approximate moments per 1024-logit sub-chunk (predictions for the
-    // exact-sum rounds). Float4 j of thread t holds ids base + (j*NT + t)*4..+3,
-    // so it lies in sub-chunk j*P1_SPF + t*4/1024 of the chunk: a wave's float4
-    // row lies inside one sub-chunk, and four waves make up a sub-chunk row.
-    {
-        constexpr int P1_SPF = ZS_P1_NT * 4 / ZS_SUB;  // sub-chunks per float4 row
-        constexpr int P1_J = P1_EPT / 4;
-        static_assert(P1_SPF * P1_J == ZS_SUBS_PER_CHUNK, "float4 rows tile the sub-chunks");
-        const int wid = zs_wid(), wh = (wid * 256) / ZS_SUB;
-        const bool om = (P.flags & (ZS_ROW_LOGPROBS | ZS_ROW_UNCERTAINTY)) && omax > -INFINITY && omax < INFINITY;
-        const bool zm = T > 0.0f && zmax > -INFINITY && zmax < INFINITY;
-        __shared__ float msh[ZS_P1_NT / 64][P1_J][3];
-        // bit 2s: sub-chunk s holds the chunk's observer max, bit 2s+1: its sampler max
-        uint32_t hasmax = 0;
-        static_assert(P1_J == 8, "the reduce-scatter below splits 8 rows over 3 lane bits");
-        float mv[3][P1_J];
-#pragma unroll
-        for (int j = 0; j < P1_J; j++) {
-            float m1 = 0.0f, md = 0.0f, mz = 0.0f;
-            const int sj = j * P1_SPF + wh;
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const int e = j * 4 + q;
-                if (!((vmask >> e) & 1u)) continue;
-                const float xe = zs_key_to_float(xo[e]), ze = zs_key_to_float(kz[e]);
-                if (xe == omax) hasmax |= 1u << (2 * sj);
-                if (ze == zmax) hasmax |= 2u << (2 * sj);
-                if (om) {
-                    float d = xe - omax;
-                    if (d > -INFINITY) { float ex = __expf(d); m1 += ex; md += d * ex; }
-                }
-                if (zm) {
-                    float d = ze - zmax;
-                    if (d > -INFINITY) mz += __expf(d);
-                }
-            }
-            mv[0][j] = m1; mv[1][j] = md; mv[2][j] = mz;
-        }
-        // reduce-scatter over the wave: each exchange halves the rows a lane
-        // keeps (lane bits 5, 4, 3 pick them), then 8-lane sums; lane 8j ends
-        // with row j's totals
-        {
-            const uint32_t lane = (uint32_t)zs_lane();
-#pragma unroll
-            for (int u = 0; u < 3; u++) {
-                float v4[4], v2[2];
-                const bool h5 = (lane & 32u) != 0, h4 = (lane & 16u) != 0, h3 = (lane & 8u) != 0;
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    const float send = h5 ? mv[u][k] : mv[u][k + 4];
-                    v4[k] = (h5 ? mv[u][k + 4] : mv[u][k]) + __shfl_xor(send, 32, 64);
-                }
-#pragma unroll
-                for (int k = 0; k < 2; k++) {
-                    const float send = h4 ? v4[k] : v4[k + 2];
-                    v2[k] = (h4 ? v4[k + 2] : v4[k]) + __shfl_xor(send, 16, 64);
-                }
-                float v1 = (h3 ? v2[1] : v2[0]) + __shfl_xor(h3 ? v2[0] : v2[1], 8, 64);
-                v1 += __shfl_xor(v1, 4, 64);
-                v1 += __shfl_xor(v1, 2, 64);
-                v1 += __shfl_xor(v1, 1, 64);
-                if ((lane & 7u) == 0) msh[wid][lane >> 3][u] = v1;
-            }
-        }
-        for (int d = 32; d > 0; d >>= 1) hasmax |= __shfl_xor(hasmax, d, 64);
-        __shared__ uint32_t hsh[ZS_P1_NT / 64];
-        if (zs_lane() == 0) hsh[wid] = hasmax;
-        __syncthreads();
-        if (t < ZS_SUBS_PER_CHUNK) {
-            const int j = t / P1_SPF, h = t % P1_SPF;
-            zs_sub_mom mm;
-            mm.e1 = mm.ed = mm.ez = 0.0f;
-            uint32_t hm = 0;
-            for (int w = 0; w < ZS_P1_NT / 64; w++) {
-                hm |= hsh[w];
-                if ((w * 256) / ZS_SUB != h) continue;
-                mm.e1 += msh[w][j][0]; mm.ed += msh[w][j][1]; mm.ez += msh[w][j][2];
-            }
-            mm.pad = zs_u2f((hm >> (2 * t)) & 3u);
-            const uint32_t sub = c * ZS_SUBS_PER_CHUNK + t;
-            if (sub * ZS_SUB < V) a.sub_mom[(size_t)r * a.max_subs + sub] = mm;
-        }
-        __syncthreads();
-    }
-
-    // ---- candidate lists (keys recomputed from the values where needed)
-    const size_t lofs = ((size_t)r * a.nch + c);
-    // sampler list size: top_k when the row has a top-k cut within range
-    const bool has_topk = P.top_k > 0 && P.top_k < V;
-    const uint32_t Ks = (has_topk && P.top_k <= ZS_KS) ? P.top_k : ZS_KS;
-    uint32_t ns, s_kth, s_full;
-    ns = s_kth = s_full = 0;
-    // The list is read by a top-k cut within ZS_KS and by the small-survivor
-    // path, which needs every chunk to have at most ZS_KS finite values.
-    if (T > 0.0f) {
-        if (zfin <= Ks) {
-            p1_finite(kz, vmask, base, a.cs_key + lofs * ZS_KS, a.cs_idx + lofs * ZS_KS, sh);
-            ns = zfin;
-        } else if (has_topk && P.top_k <= ZS_KS) {
-            p1_topk_fast(kz, vmask, nvalid, zabove, Ks, base, a.cs_key + lofs * ZS_KS, a.cs_idx + lofs * ZS_KS, &ns, &s_kth,
-                         &s_full, sh);
-        }
-    }
-    uint32_t ntl = P.top_logprobs > 20 ? 20 : P.top_logprobs;
-    uint32_t Ko = ntl + 8;
-    if (Ko > ZS_KO) Ko = ZS_KO;
-    uint32_t no, o_kth, o_full;
-    no = o_kth = o_full = 0;
-    uint32_t xr[P1_EPT];  // z is dead here: x~ keys back in registers for the list
-#pragma unroll
-    for (int e = 0; e < P1_EPT; e++) xr[e] = xo[e];
-    if ((P.flags & (ZS_ROW_LOGPROBS | ZS_ROW_UNCERTAINTY)) &&
-        !(nvalid > Ko && p1_superset(xr, vmask, Ko, ZS_KO, base, a.co_key + lofs * ZS_KO, a.co_idx + lofs * ZS_KO,
-                                     &no, sh)))
-        p1_topk_fast(xr, vmask, nvalid, xabove, Ko, base, a.co_key + lofs * ZS_KO, a.co_idx + lofs * ZS_KO, &no, &o_kth,
-                     &o_full, sh);
-
-    if (t == 0) {
-        zs_chunk_stat cs;
-        cs.obs_max = omax;
-        cs.z_max = zmax;
-        cs.flags = fl;
-        cs.z_finite = zfin;
-        cs.g_last_nan = last_nan;
-        cs.g_arg_all = best_all ? (uint32_t)(best_all & 0xffffffffull) - 1u : 0xffffffffu;
-        cs.g_val_all = best_all ? zs_key_to_float((uint32_t)(best_all >> 32)) : -INFINITY;
-        cs.g_arg_tail = best_tail ? (uint32_t)(best_tail & 0xffffffffull) - 1u : 0xffffffffu;
-        cs.g_val_tail = best_tail ? zs_key_to_float((uint32_t)(best_tail >> 32)) : -INFINITY;
-        cs.g_tail_n = tail_n;
-        cs.ns = ns;
-        cs.no = no;
-        cs.s_kth = s_kth;
-        cs.o_kth = o_kth;
-        cs.s_full = s_full;
-        cs.o_full = o_full;
-        a.cst[lofs] = cs;
-    }
-}
-
-// ===========================================================================
-// zs_k_combine
-// ===========================================================================
-
-// Predicted grid of a sequential sum at each sub-chunk start from approximate
-// sub-chunk sums A_j (one wave, 4 sub-chunks per lane). A sub-chunk is fragile
-// -- processed exactly by the stitch -- when the running sum may leave its
-// binade inside it or sits too close to a binade edge for the prediction to be
-// trusted (the f32 sum differs from the exact prefix by far less than 2^-8).
-// ONE(j) tells whether sub-chunk j holds the term exp(0) = 1 exactly: an f32
-// running sum of non-negative terms never decreases, so once that term is in,
-// the sum is >= 1 and the lower edge of [1, 2) cannot be crossed -- without
-// this, the common peaked rows (sum just above 1) would be fragile throughout.
-// A misprediction only costs an exact pass: the stitch checks every grid.
-template <class F, class G>
-__device__ void zs_predict_subs(zs_sub_sum* out, uint32_t nsub, const F& A, const G& ONE, bool all_fragile) {
-    const int lane = zs_lane();
-    double v[4], loc = 0.0;
-    int j1 = ZS_BIGI;
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-        uint32_t j = 4 * lane + q;
-        v[q] = j < nsub ? A(j) : 0.0;
-        loc += v[q];
-        if (j < nsub && j1 == ZS_BIGI && ONE(j)) j1 = (int)j;
-    }
-    j1 = wave_min_i(j1);
-    double inc = loc;
-    for (int d = 1; d < 64; d <<= 1) {
-        double y = __shfl_up(inc, d, 64);
-        if (lane >= d) inc += y;
-    }
-    double run = inc - loc;
-    const double delta = 1.0 / 256.0;
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-        uint32_t j = 4 * lane + q;
-        double lo = run, hi = run + v[q];
-        run = hi;
-        if (j >= nsub) continue;
-        zs_sub_sum e;
-        double lm = lo * (1.0 - delta), hm = hi * (1.0 + delta);
-        if ((int)j > j1) {
-            lm = fmax(lm, 1.0);
-            lo = fmax(lo, 1.0);
-        }
-        // every sum below 2^-125 lies on the finest grid (2^-149), so tiny
-        // prefixes share one binade
-        const int blo = lm < 0x1p-125 ? -125 : ilogb(lm);
-        const int bhi = hm < 0x1p-125 ? -125 : ilogb(hm);
-        bool fragile = all_fragile || !(lm >= 0.0) || blo != bhi || !(hm < 3.0e38);
-        e.eg = fragile ? 0 : zs_grid_exp((float)lo);
-        e.flags = fragile ? ZS_SF_FRAGILE : 0u;
-        e.total = 0;
-        e.pad = 0;
-        out[j] = e;
-    }
-}
-
-#define CB_NT 256
-__global__ __launch_bounds__(CB_NT) void zs_k_combine(zs_sargs a) {
-    const uint32_t r = blockIdx.x;
-    const zs_batch& b = a.b;
-    const uint32_t V = b.V;
-    const int t = threadIdx.x;
-    const uint32_t nch = (V + ZS_P1_CH - 1) / ZS_P1_CH;
-    __shared__ unsigned long long sbuf[ZS_MAX_CHUNKS * ZS_KS];
-    __shared__ float sval[ZS_SMALL_CAP];
-    __shared__ uint32_t sidx[ZS_SMALL_CAP];
-    __shared__ seq_sh<CB_NT> sq;
-    __shared__ uint32_t n_sh;
-    __shared__ uint32_t cid_sh[ZS_OBS_CAND];
-    __shared__ float cx_sh[ZS_OBS_CAND];
-    const zs_row_params P = b.d_params[r];
-    // the row state is written field by field by thread 0 (a private copy of
-    // the whole struct per thread would live in scratch memory)
-    zs_row_state& st = a.rst[r];
-    if (st.status & ZS_ST_LIMIT) {
-        if (t == 0) {
-            st.mode = ZS_MODE_DONE;
-            st.token = 0xffffffffu;
-            st.obs_need = 0;
-            st.rounds = 0;
-            st.n_cand = 0;
-            st.klist = 0;
-            st.kpend = 0;
-        }
-        return;
-    }
-    // the row's chunk statistics in LDS (one parallel load; the loops over
-    // chunks below would otherwise wait on one global load per chunk)
-    __shared__ zs_chunk_stat cs_sh[ZS_MAX_CHUNKS];
-    {
-        static_assert(sizeof(zs_chunk_stat) % 4 == 0, "word copy");
-        constexpr uint32_t W = sizeof(zs_chunk_stat) / 4;
-        const uint32_t* src = reinterpret_cast<const uint32_t*>(a.cst + (size_t)r * a.nch);
-        uint32_t* dst = reinterpret_cast<uint32_t*>(cs_sh);
-        for (uint32_t i = t; i < nch * W; i += CB_NT) dst[i] = src[i];
-    }
-    __syncthreads();
-    const zs_chunk_stat* cs = cs_sh;
-
-    // ---------------- observers: max, special rows, top candidates ----------------
-    float M = -INFINITY;
-    uint32_t fl = 0;
-    for (uint32_t c = 0; c < nch; c++) { M = fmaxf(M, cs[c].obs_max); fl |= cs[c].flags; }
-    // lse = max + ln(sum) is NaN for a NaN, a +inf or an all -inf row
-    const bool special = (fl & ZS_CF_OBS_NAN) || M == INFINITY || M == -INFINITY;
-    const bool want_lp = (P.flags & ZS_ROW_LOGPROBS) != 0;
-    const bool want_unc = (P.flags & ZS_ROW_UNCERTAINTY) != 0;
-    uint32_t status = 0;
-    uint32_t obs_need = 0;
-    if (!special && (want_lp || want_unc)) obs_need |= ZS_OBS_S;
-    if (!special && want_unc) obs_need |= ZS_OBS_H;
-    uint32_t n_cand = 0;
-    if (want_lp || want_unc) {
-        if (t == 0) n_sh = 0;
-        __syncthreads();
-        {
-            // all chunks' lists at once (their order in sbuf does not matter: sorted next)
-            const uint32_t* kk = a.co_key + (size_t)r * a.nch * ZS_KO;
-            const uint32_t* ii = a.co_idx + (size_t)r * a.nch * ZS_KO;
-            for (uint32_t i = t; i < nch * ZS_KO; i += CB_NT) {
-                if (i % ZS_KO >= cs[i / ZS_KO].no) continue;
-                uint32_t pos = atomicAdd(&n_sh, 1u);
-                sbuf[pos] = ((unsigned long long)(~kk[i]) << 32) | ii[i];
-            }
-        }
-        __syncthreads();
-        uint32_t nco = n_sh;
-        uint32_t np2 = 1;
-        while (np2 < nco) np2 <<= 1;
-        for (uint32_t i = nco + t; i < np2; i += CB_NT) sbuf[i] = ~0ull;
-        __syncthreads();
-        if (np2 > 1) block_sort_u64<CB_NT>(sbuf, np2);
-        n_cand = nco < ZS_OBS_CAND ? nco : ZS_OBS_CAND;
-        if (t < (int)n_cand) {
-            cid_sh[t] = (uint32_t)(sbuf[t] & 0xffffffffull);
-            cx_sh[t] = zs_key_to_float(~(uint32_t)(sbuf[t] >> 32));
-        }
-        __syncthreads();
-    }
-    // the sampler sees x~ itself when T == 1 and no bias / penalty applies
-    uint32_t has_y = 0;
-    {
-        const uint32_t np = a.p_cnt[r];
-        const uint32_t* pfl = a.p_flags + (size_t)r * ZS_MAX_PATCHES;
-        for (uint32_t i = t; i < np; i += CB_NT) has_y |= (pfl[i] & ZS_PF_Y) ? 1u : 0u;
-        has_y = block_or_u<CB_NT>(has_y, sq.a);
-    }
-    const uint32_t z_is_x = (P.temperature == 1.0f && !has_y) ? 1u : 0u;
-
-    // ---------------- sampler ----------------
-    const float T = P.temperature;
-    uint32_t token = 0;
-    uint32_t mode = ZS_MODE_DONE;
-    uint32_t has_thr = 0, thr_key = 0;
-    float zmax = -INFINITY;
-    for (uint32_t c = 0; c < nch; c++) zmax = fmaxf(zmax, cs[c].z_max);
-    if (T <= 0.0f) {
-        // sampler.rs:35-42, max_by over partial_cmp: the last maximal element,
-        // and a NaN restarts the fold (partial_cmp -> Equal keeps the later one).
-        status |= ZS_ST_GREEDY;
-        int L = -1;
-        for (uint32_t c = 0; c < nch; c++) L = max(L, cs[c].g_last_nan);
-        float bv = 0.f;
-        uint32_t bi = 0xffffffffu;
-        bool any = false;
-        uint32_t cstart = 0;
-        if (L >= 0) {
-            uint32_t cl = (uint32_t)L / ZS_P1_CH;
-            if (cs[cl].g_tail_n > 0) { bv = cs[cl].g_val_tail; bi = cs[cl].g_arg_tail; any = true; }
-            cstart = cl + 1;
-        }
-        for (uint32_t c = cstart; c < nch; c++) {
-            if (cs[c].g_arg_all == 0xffffffffu) continue;
-            float v = cs[c].g_val_all;
-            if (!any || !(bv > v)) { bv = v; bi = cs[c].g_arg_all; any = true; }
-        }
-        token = any ? bi : (uint32_t)L;
-        if (!any && L < 0) token = 0;
-    } else if ((fl & (ZS_CF_Z_NAN | ZS_CF_Z_PINF)) || zmax == -INFINITY) {
-        // exp_sum is NaN: every comparison in the draw fails -> V-1 (sampler.rs:127)
-        status |= ZS_ST_NONFINITE;
-        token = V - 1;
-    } else {
-        const bool has_topk = P.top_k > 0 && P.top_k < V;
-        // gather sampler candidates
-        if (t == 0) n_sh = 0;
-        __syncthreads();
-        {
-            const uint32_t* kk = a.cs_key + (size_t)r * a.nch * ZS_KS;
-            const uint32_t* ii = a.cs_idx + (size_t)r * a.nch * ZS_KS;
-#pragma unroll 4
-            for (uint32_t i = t; i < nch * ZS_KS; i += CB_NT) {
-                if (i % ZS_KS >= cs[i / ZS_KS].ns) continue;
-                uint32_t pos = atomicAdd(&n_sh, 1u);
-                sbuf[pos] = ((unsigned long long)(~kk[i]) << 32) | ii[i];
-            }
-        }
-        __syncthreads();
-        uint32_t ncs = n_sh;
-        uint32_t np2 = 1;
-        while (np2 < ncs) np2 <<= 1;
-        for (uint32_t i = ncs + t; i < np2; i += CB_NT) sbuf[i] = ~0ull;
-        __syncthreads();
-        if (np2 > 1) block_sort_u64<CB_NT>(sbuf, np2);
-        bool small = false;
-        float thr = -INFINITY;
-        if (has_topk && P.top_k <= ZS_KS) {
-            // fewer listed values than k: every finite value is listed and the
-            // k-th largest of the row is -inf
-            thr_key = P.top_k <= ncs ? ~(uint32_t)(sbuf[P.top_k - 1] >> 32) : zs_total_key(-INFINITY);
-            has_thr = 1;
-            thr = zs_key_to_float(thr_key);
-            bool complete = true;
-            for (uint32_t c = 0; c < nch; c++) {
-                if (!cs[c].s_full) continue;
-                if (cs[c].s_kth == thr_key && cs[c].s_full == 2) complete = false;
-                if (thr == 0.0f) complete = false;  // the other zero also survives
-            }
-            small = complete;
-        } else if (has_topk) {
-            has_thr = 2;
-        } else {
-            uint32_t fin = 0;
-            bool ok = true;
-            for (uint32_t c = 0; c < nch; c++) {
-                fin += cs[c].z_finite;
-                if (cs[c].z_finite > ZS_KS) ok = false;
-            }
-            small = ok && fin <= ZS_SMALL_CAP;
-        }
-        if (small) {
-            // survivors: !(z < thr) (sampler.rs:59-63) and finite, gathered by index
-            if (t == 0) n_sh = 0;
-            __syncthreads();
-            for (uint32_t i = t; i < ncs; i += CB_NT) {
-                float z = zs_key_to_float(~(uint32_t)(sbuf[i] >> 32));
-                bool surv = !(z < thr) && z > -INFINITY;
-                if (surv) {
-                    uint32_t pos = atomicAdd(&n_sh, 1u);
-                    if (pos < ZS_SMALL_CAP) { sval[pos] = z; sidx[pos] = (uint32_t)(sbuf[i] & 0xffffffffull); }
-                }
-            }
-            __syncthreads();
-            uint32_t n = n_sh;
-            __syncthreads();
-            if (n > ZS_SMALL_CAP) {
-                small = false;
-            } else {
-                if (t < 64) {
-                    const uint32_t tk = n <= 64 ? small_path_wave<1>(b.d_seed[r], b.d_counter[r], V, P, n, zmax, sval, sidx)
-                                                : small_path_wave<ZS_SMALL_CAP / 64>(b.d_seed[r], b.d_counter[r], V, P, n, zmax, sval, sidx);
-                    if (t == 0) n_sh = tk;
-                }
-                __syncthreads();
-                token = n_sh;
-                status |= ZS_ST_SMALL;
-            }
-        }
-        if (!small) mode = ZS_MODE_BIG;
-    }
-    // ---- predictions for the parallel exact-sum rounds
-    uint32_t rounds = 0;
-    {
-        const uint32_t nsub = (V + ZS_SUB - 1) / ZS_SUB;
-        const zs_sub_mom* mom = a.sub_mom + (size_t)r * a.max_subs;
-        if (obs_need & ZS_OBS_S) {
-            rounds |= 1u << ZS_SUM_OBS_S;
-            if (t < 64)
-                zs_predict_subs(a.sub_sum + ((size_t)r * ZS_NSUM + ZS_SUM_OBS_S) * a.max_subs, nsub,
-                                [&](uint32_t j) {
-                                    float mc = cs[j / ZS_SUBS_PER_CHUNK].obs_max;
-                                    return (double)mom[j].e1 * exp((double)mc - (double)M);
-                                },
-                                [&](uint32_t j) {
-                                    return (zs_f2u(mom[j].pad) & 1u) && cs[j / ZS_SUBS_PER_CHUNK].obs_max == M;
-                                },
-                                false);
-        }
-        const bool reuse = z_is_x && !has_thr && (obs_need & ZS_OBS_S);
-        if (mode == ZS_MODE_BIG && !reuse && has_thr != 2) {  // has_thr 2: threshold found later
-            rounds |= 1u << ZS_SUM_SAMP_S;
-            if (t < 64)
-                zs_predict_subs(a.sub_sum + ((size_t)r * ZS_NSUM + ZS_SUM_SAMP_S) * a.max_subs, nsub,
-                                [&](uint32_t j) {
-                                    float mc = cs[j / ZS_SUBS_PER_CHUNK].z_max;
-                                    return mc > -INFINITY ? (double)mom[j].ez * exp((double)mc - (double)zmax) : 0.0;
-                                },
-                                [&](uint32_t j) {
-                                    return (zs_f2u(mom[j].pad) & 2u) && cs[j / ZS_SUBS_PER_CHUNK].z_max == zmax;
-                                },
-                                has_thr != 0);
-        }
-        if (obs_need & ZS_OBS_H) rounds |= 1u << ZS_SUM_OBS_H;
-    }
-    if (t == 0) {
-        st.rounds = rounds;
-        st.z_max = zmax;
-        st.has_thr = has_thr;
-        st.thr_key = thr_key;
-        st.mode = mode;
-        st.token = token;
-        st.status = status;
-        st.obs_max = M;
-        st.obs_special = special ? 1u : 0u;
-        st.obs_need = obs_need;
-        st.n_cand = n_cand;
-        for (uint32_t j = 0; j < n_cand; j++) { st.cand_id[j] = cid_sh[j]; st.cand_x[j] = cx_sh[j]; }
-        st.z_is_x = z_is_x;
-        st.klist = 0;
-        st.kpend = 0;
-    }
-    if (mode == ZS_MODE_BIG) {
-        // bucket counts and masses of the top-p walk, accumulated by zs_k_pv
-        zs_tp_bucket* bk = a.tp_bk + (size_t)r * ZS_TP_NB;
-        for (uint32_t i = t; i < ZS_TP_NB; i += CB_NT) { bk[i].cnt = 0u; bk[i].mass = 0.0f; }
-    }
-}
-
-
-// ===========================================================================
-// Parallel exact-sum rounds. A round kernel gives every 1024-logit sub-chunk
-// its total increment on the predicted grid (one wave per sub-chunk, all CUs);
-// a stitch kernel walks a row's sub-chunks in order with the exact running sum,
-// accepting a total when the prediction holds and recomputing the sub-chunk
-// with the exact wave-level scan otherwise. Observer sums (tolerance outputs)
-// take increments from the fast exp; the sampler sum uses certified ones.
-// ===========================================================================
-struct sub_row {
-    const float* row;
-    const uint32_t* allow;
-    const uint32_t* pid;
-    const uint32_t* pfl;
-    const float* py;
-    const uint32_t* psub;
-    uint32_t V;
-    float T;
-    bool masked;
-};
-
-__device__ __forceinline__ sub_row make_sub_row(const zs_sargs& a, uint32_t r, const zs_row_params& P) {
-    const zs_batch& b = a.b;
-    sub_row R;
-    R.row = b.d_logits + (size_t)r * b.ld;
-    R.masked = (P.flags & ZS_ROW_MASKED) && b.d_allow_bits;
-    R.allow = R.masked ? b.d_allow_bits + (size_t)r * b.allow_words : nullptr;
-    R.pid = a.p_id + (size_t)r * ZS_MAX_PATCHES;
-    R.pfl = a.p_flags + (size_t)r * ZS_MAX_PATCHES;
-    R.py = a.p_y + (size_t)r * ZS_MAX_PATCHES;
-    R.psub = a.p_sub + (size_t)r * (a.max_subs + 1);
-    R.V = b.V;
-    R.T = P.temperature;
-    return R;
-}
-
-// thread t holds elements j*1024 + EPT*t .. +EPT-1 of sub-chunk j
-// (EPT * threads = 1024)
-template <int EPT>
-__device__ __forceinline__ void sub_load_t(const sub_row& R, uint32_t j, uint32_t t, float (&x)[EPT], float (&z)[EPT]) {
-    const uint32_t base = j * ZS_SUB + (uint32_t)EPT * t;
-    uint32_t w = 0xffffffffu;
-    if (R.masked && base < R.V) w = R.allow[base >> 5] >> (base & 31);
-    if constexpr (EPT >= 4) {
-#pragma unroll
-        for (int k = 0; k < EPT / 4; k++) {
-            float4 v = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
-            if (base + 4 * k < R.V) v = *reinterpret_cast<const float4*>(R.row + base + 4 * k);
-            x[4 * k] = v.x; x[4 * k + 1] = v.y; x[4 * k + 2] = v.z; x[4 * k + 3] = v.w;
-        }
-    } else if constexpr (EPT == 2) {
-        float2 v = make_float2(-INFINITY, -INFINITY);
-        if (base < R.V) v = *reinterpret_cast<const float2*>(R.row + base);  // V is a multiple of 4 or row padded
-        x[0] = v.x; x[1] = v.y;
-    } else {
-        x[0] = base < R.V ? R.row[base] : -INFINITY;
-    }
-#pragma unroll
-    for (int q = 0; q < EPT; q++) {
-        if (base + q >= R.V || (R.masked && !((w >> q) & 1u))) x[q] = -INFINITY;
-        z[q] = x[q];
-    }
-    const uint32_t p0 = R.psub[j], p1 = R.psub[j + 1];
-    for (uint32_t p = p0; p < p1; p++) {
-        uint32_t off = R.pid[p] - base;
-        if (off < (uint32_t)EPT) {
-            uint32_t fl = R.pfl[p];
-            float py = R.py[p];
-#pragma unroll
-            for (int q = 0; q < EPT; q++) {
-                if ((uint32_t)q != off) continue;
-                if (fl & ZS_PF_BAN) { x[q] = -INFINITY; z[q] = -INFINITY; }
-                if (fl & ZS_PF_Y) z[q] = py;
-            }
-        }
-    }
-#pragma unroll
-    for (int q = 0; q < EPT; q++) z[q] = zs_temper(z[q], R.T);
-}
-
-// lane l of the wave holds elements j*1024 + 16l .. +15 of sub-chunk j
-__device__ __forceinline__ void sub_load(const sub_row& R, uint32_t j, float (&x)[16], float (&z)[16]) {
-    sub_load_t<16>(R, j, (uint32_t)zs_lane(), x, z);
-}
-
+// Saturating sum over the wave (the kept-list sums' per-wave totals).
 __device__ __forceinline__ uint32_t wave_sum_sat(uint32_t v) {
     for (int d = 32; d > 0; d >>= 1) v = zs_sat_add(v, __shfl_xor(v, d, 64));
     return v;
 }
-
-// approximate exp for the observer sums
-__device__ __forceinline__ float zs_exp_obs(float d) {
-    if (d >= ZS_EXP_FAST_MIN) return zs_exp_fast(d);
-    return d < ZS_EXP_ZERO ? 0.0f : zs_expf(d);
-}
-
-// observer terms with approximate values (tolerance outputs): the exact
-// machinery is still applied to these values, so only terms whose fast-exp
-// rounding differs move the sum, by a grid unit each
-template <int EPT>
-struct obs_exp_terms {
-    float a[EPT];
-    __device__ __forceinline__ void inc(int j, int eg, uint32_t* ie, uint32_t* io) const {
-        seq_pair p = seq_pair_of(zs_pick(a, j), eg);
-        *ie = p.e;
-        *io = p.o;
-    }
-    __device__ __forceinline__ float val(int j) const { return zs_pick(a, j); }
-};
-
-__global__ __launch_bounds__(256) void zs_k_roundA(zs_sargs a) {
-    const uint32_t r = blockIdx.y;
-    const uint32_t j = blockIdx.x * 4 + zs_wid();
-    const zs_row_state* st = a.rst + r;
-    const uint32_t rounds = st->rounds;
-    if (!(rounds & ((1u << ZS_SUM_OBS_S) | (1u << ZS_SUM_SAMP_S)))) return;
-    const uint32_t V = a.b.V;
-    const uint32_t nsub = (V + ZS_SUB - 1) / ZS_SUB;
-    if (j >= nsub) return;
-    const zs_row_params P = a.b.d_params[r];
-    sub_row R = make_sub_row(a, r, P);
-    zs_sub_sum* ss = a.sub_sum + (size_t)r * ZS_NSUM * a.max_subs;
-    const bool do_obs = (rounds >> ZS_SUM_OBS_S) & 1u;
-    const bool do_samp = (rounds >> ZS_SUM_SAMP_S) & 1u;
-    zs_sub_sum eo = ss[ZS_SUM_OBS_S * a.max_subs + j];
-    zs_sub_sum es = ss[ZS_SUM_SAMP_S * a.max_subs + j];
-    const bool need_o = do_obs && !(eo.flags & ZS_SF_FRAGILE);
-    const bool need_s = do_samp && !(es.flags & ZS_SF_FRAGILE);
-    if (!need_o && !need_s) return;
-    float x[16], z[16];
-    sub_load(R, j, x, z);
-    if (need_o) {
-        const float M = st->obs_max;
-        uint32_t tot = 0;
-#pragma unroll
-        for (int q = 0; q < 16; q++) {
-            uint32_t tie;
-            tot = zs_sat_add(tot, zs_seq_inc(zs_exp_obs(x[q] - M), eo.eg, &tie));
-        }
-        tot = wave_sum_sat(tot);
-        if (zs_lane() == 0) {
-            zs_sub_sum& o = ss[ZS_SUM_OBS_S * a.max_subs + j];
-            o.total = tot;
-            o.flags = eo.flags | ZS_SF_DONE;
-        }
-    }
-    if (need_s) {
-        const float m = st->z_max;
-        const bool use_thr = st->has_thr != 0;
-        const float thr = zs_key_to_float(st->thr_key);
-        exp_terms<16> f;
-#pragma unroll
-        for (int q = 0; q < 16; q++) f.set(q, (use_thr && z[q] < thr) ? -INFINITY : z[q] - m);
-        uint32_t tot = 0, tie = 0;
-#pragma unroll
-        for (int q = 0; q < 16; q++) {
-            uint32_t ie, io;
-            f.inc(q, es.eg, &ie, &io);
-            if (ie != io) tie = 1;
-            tot = zs_sat_add(tot, ie);
-        }
-        tot = wave_sum_sat(tot);
-        tie = wave_or_u(tie);
-        if (zs_lane() == 0) {
-            zs_sub_sum& o = ss[ZS_SUM_SAMP_S * a.max_subs + j];
-            o.total = tot;
-            o.flags = es.flags | ZS_SF_DONE | (tie ? ZS_SF_TIE : 0u);
-        }
-    }
-}
-
-// H = -sum p (d - ln S) terms with the fast exp (tolerance output)
-__device__ __forceinline__ float zs_ent_obs(float d, float inv, float lns) {
-    float p = zs_exp_obs(d) * inv;
-    if (!(p > 0.0f)) return 0.0f;
-    return -(p * (d - lns));
-}
-
-template <int EPT>
-struct obs_ent_terms {
-    float a[EPT];
-    __device__ __forceinline__ void inc(int j, int eg, uint32_t* ie, uint32_t* io) const {
-        seq_pair p = seq_pair_of(zs_pick(a, j), eg);
-        *ie = p.e;
-        *io = p.o;
-    }
-    __device__ __forceinline__ float val(int j) const { return zs_pick(a, j); }
-};
-
-__global__ __launch_bounds__(256) void zs_k_roundB(zs_sargs a) {
-    const uint32_t r = blockIdx.y;
-    const uint32_t j = blockIdx.x * 4 + zs_wid();
-    const zs_row_state* st = a.rst + r;
-    if (!((st->rounds >> ZS_SUM_OBS_H) & 1u)) return;
-    const uint32_t V = a.b.V;
-    const uint32_t nsub = (V + ZS_SUB - 1) / ZS_SUB;
-    if (j >= nsub) return;
-    zs_sub_sum* ss = a.sub_sum + ((size_t)r * ZS_NSUM + ZS_SUM_OBS_H) * a.max_subs;
-    zs_sub_sum e = ss[j];
-    if (e.flags & ZS_SF_FRAGILE) return;
-    const zs_row_params P = a.b.d_params[r];
-    sub_row R = make_sub_row(a, r, P);
-    float x[16], z[16];
-    sub_load(R, j, x, z);
-    const float M = st->obs_max, S = st->obs_S;
-    const float inv = 1.0f / S, lns = (float)log((double)S);
-    uint32_t tot = 0;
-#pragma unroll
-    for (int q = 0; q < 16; q++) {
-        uint32_t tie;
-        tot = zs_sat_add(tot, zs_seq_inc(zs_ent_obs(x[q] - M, inv, lns), e.eg, &tie));
-    }
-    tot = wave_sum_sat(tot);
-    if (zs_lane() == 0) {
-        ss[j].total = tot;
-        ss[j].flags = e.flags | ZS_SF_DONE;
-    }
-}
-
-#define ST_NT 512
-#define ST_EPT (ZS_SUB / ST_NT)
-
-struct st_sh {
-    seq_sh<ST_NT> seq;
-    float head[64];
-    zs_sub_sum rec[ZS_MAX_SUBS];
-};
-
-// Exact processing of one sub-chunk by the workgroup: the first 64 terms of a
-// sum that starts at zero are added serially by thread 0 (the running sum
-// crosses many binades there), the rest with the increment scan.
-template <class F>
-__device__ __forceinline__ void stitch_sub(const F& f, float& s, bool first, st_sh& sh) {
-    int start = 0;
-    if (first) {
-        const int t = threadIdx.x;
-        if (t < 64 / ST_EPT) {
-#pragma unroll
-            for (int q = 0; q < ST_EPT; q++) sh.head[ST_EPT * t + q] = f.val(q);
-        }
-        __syncthreads();
-        if (t == 0) {
-            float acc = s;
-            for (int i = 0; i < 64; i++) acc = acc + sh.head[i];
-            sh.seq.s = acc;
-        }
-        __syncthreads();
-        s = sh.seq.s;
-        __syncthreads();
-        start = 64;
-    }
-    seq_group_f<ST_NT, ST_EPT>(f, start, s, NAN, sh.seq);
-}
-
-// One workgroup per (row, sum): the exact running sum over the row's
-// sub-chunks, taking the rounds' totals where the predicted grid holds.
-template <int KIND>
-__device__ __forceinline__ void stitch_body(const zs_sargs& a) {
-    const uint32_t r = blockIdx.x;
-    zs_row_state* st = a.rst + r;
-    const uint32_t rounds = st->rounds;
-    if (!((rounds >> KIND) & 1u)) return;
-    __shared__ st_sh sh;
-    const uint32_t t = threadIdx.x;
-    const uint32_t V = a.b.V;
-    const uint32_t nsub = (V + ZS_SUB - 1) / ZS_SUB;
-    const zs_row_params P = a.b.d_params[r];
-    sub_row R = make_sub_row(a, r, P);
-    const zs_sub_sum* ss = a.sub_sum + ((size_t)r * ZS_NSUM + KIND) * a.max_subs;
-    for (uint32_t j = t; j < nsub; j += ST_NT) sh.rec[j] = ss[j];
-    __syncthreads();
-    const float M = st->obs_max, m = st->z_max;
-    const bool use_thr = st->has_thr != 0;
-    const float thr = zs_key_to_float(st->thr_key);
-    float inv = 0.0f, lns = 0.0f;
-    if (KIND == ZS_SUM_OBS_H) {
-        inv = 1.0f / st->obs_S;
-        lns = (float)log((double)st->obs_S);
-    }
-    float s = KIND == ZS_SUM_OBS_H ? 0.0f : -0.0f;
-    for (uint32_t j = 0; j < nsub; j++) {
-        const zs_sub_sum e = sh.rec[j];
-        const int eg = zs_grid_exp(s);
-        const uint32_t k0 = zs_grid_k(s);
-        if ((e.flags & ZS_SF_DONE) && !(e.flags & (ZS_SF_FRAGILE | ZS_SF_TIE)) && e.eg == eg &&
-            k0 + e.total < ZS_BINADE) {
-            s = zs_grid_value(k0 + e.total, eg);
-            continue;
-        }
-        const bool first = (j == 0);
-        float x[ST_EPT], z[ST_EPT];
-        sub_load_t<ST_EPT>(R, j, t, x, z);
-        if (KIND == ZS_SUM_OBS_S) {
-            obs_exp_terms<ST_EPT> f;
-#pragma unroll
-            for (int q = 0; q < ST_EPT; q++) f.a[q] = zs_exp_obs(x[q] - M);
-            stitch_sub(f, s, first, sh);
-        } else if (KIND == ZS_SUM_SAMP_S) {
-            exp_terms<ST_EPT> f;
-#pragma unroll
-            for (int q = 0; q < ST_EPT; q++) f.set(q, (use_thr && z[q] < thr) ? -INFINITY : z[q] - m);
-            stitch_sub(f, s, first, sh);
-        } else {
-            obs_ent_terms<ST_EPT> f;
-#pragma unroll
-            for (int q = 0; q < ST_EPT; q++) f.a[q] = zs_ent_obs(x[q] - M, inv, lns);
-            stitch_sub(f, s, first, sh);
-        }
-    }
-    if (KIND == ZS_SUM_OBS_S) {
-        if (t == 0) st->obs_S = s;
-        if (((rounds >> ZS_SUM_OBS_H) & 1u) && t < 64) {
-            // predictions for the entropy sum: p = e * inv, term = p (ln S - d)
-            const float iv = 1.0f / s;
-            const double ls = log((double)s);
-            const zs_sub_mom* mom = a.sub_mom + (size_t)r * a.max_subs;
-            const zs_chunk_stat* cs = a.cst + (size_t)r * a.nch;
-            zs_predict_subs(a.sub_sum + ((size_t)r * ZS_NSUM + ZS_SUM_OBS_H) * a.max_subs, nsub,
-                            [&](uint32_t jj) {
-                                double mc = (double)cs[jj / ZS_SUBS_PER_CHUNK].obs_max;
-                                double sc = exp(mc - (double)M);
-                                double e1 = (double)mom[jj].e1 * sc;
-                                double ed = ((double)mom[jj].ed + (mc - (double)M) * (double)mom[jj].e1) * sc;
-                                double v = (double)iv * (ls * e1 - ed);
-                                return v > 0.0 ? v : 0.0;
-                            },
-                            [](uint32_t) { return false; },
-                            false);
-        }
-    } else if (KIND == ZS_SUM_SAMP_S) {
-        if (t == 0) st->samp_S = s;
-    } else {
-        if (t == 0) st->obs_H = s;
-    }
-}
-
-// the observers' S (blockIdx.y 0) and the sampler's S (1) side by side
-__global__ __launch_bounds__(ST_NT) void zs_k_stitchA(zs_sargs a) {
-    if (blockIdx.y == 0) stitch_body<ZS_SUM_OBS_S>(a);
-    else stitch_body<ZS_SUM_SAMP_S>(a);
-}
-__global__ __launch_bounds__(ST_NT) void zs_k_stitchB(zs_sargs a) { stitch_body<ZS_SUM_OBS_H>(a); }
 
 // ===========================================================================
 // zs_k_big: exact emulation of the reference's sequential sums over a full row.
@@ -3125,18 +1629,11 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
     a.p_id = ctx->p_id;
     a.p_flags = ctx->p_flags;
     a.p_y = ctx->p_y;
-    a.cst = ctx->cst;
-    a.cs_key = ctx->cs_key;
-    a.cs_idx = ctx->cs_idx;
-    a.co_key = ctx->co_key;
-    a.co_idx = ctx->co_idx;
     a.rst = ctx->rst;
     a.pairs = ctx->pairs;
     a.nch = ctx->max_chunks;
     a.max_vocab = ctx->max_vocab;
     a.pv = ctx->pv;
-    a.sub_mom = ctx->sub_mom;
-    a.sub_sum = ctx->sub_sum;
     a.p_sub = ctx->p_sub;
     a.max_subs = ctx->max_subs;
     a.k_ap = ctx->k_ap;

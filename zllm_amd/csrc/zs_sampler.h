@@ -13,18 +13,11 @@ struct zs_sargs {
     uint32_t* p_id;
     uint32_t* p_flags;
     float* p_y;
-    zs_chunk_stat* cst;
-    uint32_t* cs_key;
-    uint32_t* cs_idx;
-    uint32_t* co_key;
-    uint32_t* co_idx;
     zs_row_state* rst;
     uint32_t* pairs;
     uint32_t* pv;
     uint32_t nch;
     uint32_t max_vocab;
-    zs_sub_mom* sub_mom;
-    zs_sub_sum* sub_sum;
     uint32_t* p_sub;
     uint32_t max_subs;
     double* k_ap;
@@ -53,12 +46,11 @@ __device__ __forceinline__ bool zs_allowed_bit(const zs_batch& b, uint32_t r, ui
     return (w >> (idx & 31)) & 1u;
 }
 
+// Small survivor sets (n <= ZS_SMALL_CAP, all other logits are -inf after
+// top-k / mask) are sampled exactly by one wave of the row kernel: zero terms
+// of the reference's full-vocabulary loops do not change a running sum.
 #define ZS_SMALL_CAP 512
 
-
-// Small survivor sets (n <= ZS_SMALL_CAP, all other logits are -inf after
-// top-k / mask) are sampled exactly in zs_k_combine: zero terms of the
-// reference's full-vocabulary loops do not change a running sum.
 // Ascending bitonic sort of 64*E u64 keys by one wave, element i = lane*E + e
 // in register e of lane i / E: strides below E inside the lane, the others by
 // lane exchanges.

@@ -357,7 +357,7 @@ class BatchSampler:
             top_stride: int = OPENAI_TOP_LOGPROBS_CAP, out: Optional[dict] = None,
             pass_event: Optional[torch.cuda.Event] = None):
         """pass_event (optional, already recorded once so that it exists) is
-        recorded after the first full pass over the logits (zs_batch.pass_event)."""
+        recorded where the sampler's kernels begin (zs_batch.pass_event)."""
         B, V = logits.shape
         dev = logits.device
         assert logits.dtype == torch.float32 and logits.stride(1) == 1
