@@ -11,6 +11,7 @@ text of a few schemas against the reference's format strings
 import json
 import random
 import re
+import unicodedata
 
 import numpy as np
 import pytest
@@ -256,6 +257,9 @@ def test_dfa_is_minimal_and_dead_is_the_only_non_live_state():
     assert len(set(blk.tolist())) == d.nstates
 
 
+_WHITE_SPACE = set(range(0x09, 0x0E)) | {0x20, 0x85, 0xA0, 0x1680, 0x2028, 0x2029, 0x202F, 0x205F, 0x3000} | \
+    set(range(0x2000, 0x200B))   # PropList.txt White_Space
+
 PATTERNS = [
     r"ab*c", r"ab?", r"(a|bc)*d", r"[a-c]{2,4}x?", r"(?:foo|bar)+baz", r"[^\"\\]*", r"\.\+\*\?\(\)\|\[\]\{\}\^\$",
     r"(?i)hello", r"a.c", r"(?s)a.c", r"[0-9]+(\.[0-9]+)?", r"x{3}", r"x{2,}", r"(ab){0,2}c",
@@ -274,12 +278,26 @@ def _strings(rng, n):
     return out
 
 
+_WORD_CATS = {"Lu", "Ll", "Lt", "Lm", "Lo", "Nl", "Mn", "Mc", "Me", "Nd", "Pc"}
+
+
+def _uts_word(ch):
+    c = ord(ch)
+    return unicodedata.category(ch) in _WORD_CATS or c in (0x200C, 0x200D) or 0x24B6 <= c <= 0x24E9 or \
+        0x1F130 <= c <= 0x1F149 or 0x1F150 <= c <= 0x1F169 or 0x1F170 <= c <= 0x1F189
+
+
+def _py_agrees(ch):
+    return (bool(re.fullmatch(r"\s", ch)) == (ord(ch) in _WHITE_SPACE)) and \
+        (bool(re.fullmatch(r"\w", ch)) == _uts_word(ch))
+
+
 @pytest.mark.parametrize("pat", PATTERNS)
 def test_language_matches_python_re(pat):
     """Whole-text match of the DFA agrees with re.fullmatch (an independent
     engine) on random strings and on strings the DFA generates."""
     d = G.HostDfa(pat)
-    py = re.compile(pat, re.ASCII if "\\d" in pat or "\\D" in pat else 0)
+    py = re.compile(pat)   # Unicode classes: on ALPHABET Python's \d \s \w agree with UTS #18
     rng = random.Random(hash(pat) & 0xffff)
     cases = _strings(rng, 400)
     # strings accepted by the DFA, from random walks that end in an accepting state
@@ -296,6 +314,10 @@ def test_language_matches_python_re(pat):
             cases.append(bytes(buf).decode("utf-8"))  # accepted text is valid UTF-8
     if "$" in pat or "^" in pat:
         cases = [c for c in cases if "\n" not in c]  # Python's $ also matches before a final newline
+    # Python's \s and \w differ from UTS #18 on a few scalars (U+001C..U+001F
+    # are Python spaces, No digits are Python word characters): those are
+    # pinned by the Unicode-class tests below instead
+    cases = [c for c in cases if all(_py_agrees(ch) for ch in c)]
     for text in cases:
         assert d.full_match(text) == bool(py.fullmatch(text)), (pat, text)
 
@@ -380,3 +402,90 @@ def test_json_modes_compile_on_the_tiny_table():  # :430-451 (the compile step; 
 
 def test_braced_escapes():
     assert G.HostDfa(r"\u{1F600}\x{41}\x42").full_match("😀AB")
+
+
+# ------------------------------------------------------------ Unicode classes
+# regex-syntax's Unicode mode (logit_fsm.rs:73-86 builds with the defaults):
+# \d = \p{Nd}, \s = White_Space, \w = UTS #18 Annex C word characters,
+# \p{..} general categories, simple case folding. Expected sets come from
+# unicodedata's categories directly (an engine-independent restatement) and
+# from Python's re where its semantics coincide.
+
+
+def _bmp():
+    return [c for c in range(0x10000) if not 0xD800 <= c <= 0xDFFF]
+
+
+def _single_char_language(pat):
+    """The BMP scalars c for which the DFA of `pat` fully matches chr(c)."""
+    d = G.HostDfa(pat)
+    out = set()
+    for c in _bmp():
+        s = d.start
+        for b in chr(c).encode("utf-8"):
+            s = int(d.trans[s, b])
+        if not d.dead[s] and d.accept[s]:
+            out.add(c)
+    return out
+
+
+def test_unicode_digit_class_is_nd():
+    want = {c for c in _bmp() if unicodedata.category(chr(c)) == "Nd"}
+    assert _single_char_language(r"\d") == want
+    assert _single_char_language(r"\p{Nd}") == want
+    d = G.HostDfa(r"\d+")
+    assert d.full_match("٣١٤") and d.full_match("१२") and not d.full_match("²") and not d.full_match("Ⅳ")
+
+
+def test_unicode_space_class_is_white_space():
+    assert _single_char_language(r"\s") == {c for c in _WHITE_SPACE if c < 0x10000}
+    d = G.HostDfa(r"a\sb")
+    assert d.full_match("a\u3000b") and d.full_match("a\u00a0b") and not d.full_match("a\u001cb")
+
+
+def test_unicode_word_class():
+    L = {"Lu", "Ll", "Lt", "Lm", "Lo", "Nl", "Mn", "Mc", "Me", "Nd", "Pc"}
+    want = {c for c in _bmp() if unicodedata.category(chr(c)) in L} | {0x200C, 0x200D} | set(range(0x24B6, 0x24EA))
+    got = _single_char_language(r"\w")
+    assert got == want
+    assert 0x00B2 not in got          # superscript two (No): not a word character
+    assert ord("‿") in got and ord("é") in got and ord("中") in got
+
+
+def test_unicode_general_categories():
+    for pat, cats in [(r"\p{L}", {"Lu", "Ll", "Lt", "Lm", "Lo"}), (r"\pN", {"Nd", "Nl", "No"}),
+                      (r"\p{Lu}", {"Lu"}), (r"\p{Uppercase_Letter}", {"Lu"}), (r"\p{gc=Sc}", {"Sc"}),
+                      (r"[\p{Zs}\p{Pd}]", {"Zs", "Pd"})]:
+        want = {c for c in _bmp() if unicodedata.category(chr(c)) in cats}
+        assert _single_char_language(pat) == want, pat
+    notn = _single_char_language(r"\P{N}")
+    assert ord("a") in notn and ord("٣") not in notn and ord("²") not in notn
+    for bad in [r"\p{Greek}", r"\p{Alphabetic}", r"\p{", r"\bword\b"]:
+        with pytest.raises(G.GrammarError):
+            G.HostDfa(bad)
+
+
+def test_unicode_case_folding():
+    d = G.HostDfa(r"(?i)k")
+    assert d.full_match("k") and d.full_match("K") and d.full_match("\u212a")   # Kelvin sign folds to k
+    d = G.HostDfa(r"(?i)s")
+    assert d.full_match("S") and d.full_match("\u017f")                       # long s
+    d = G.HostDfa(r"(?i)σ+")
+    assert d.full_match("Σσς")
+    d = G.HostDfa(r"(?i)µ")
+    assert d.full_match("μ") and d.full_match("Μ")
+    d = G.HostDfa(r"(?i)ß")
+    assert d.full_match("ẞ")
+    d = G.HostDfa(r"(?i)i")
+    assert d.full_match("I") and not d.full_match("ı") and not d.full_match("İ")  # no Turkic folds
+    # letters of Latin-1, Greek and Cyrillic: case-insensitive single-letter
+    # languages agree with Python's re.IGNORECASE
+    block = list(range(0x41, 0x5B)) + list(range(0x61, 0x7B)) + list(range(0xC0, 0xFF)) + \
+        list(range(0x391, 0x3AA)) + list(range(0x3B1, 0x3CA)) + list(range(0x410, 0x450))
+    block = [c for c in block if c not in (0xD7, 0xF7)]
+    for c in block[::3]:
+        pat = "(?i)" + re.escape(chr(c))
+        d = G.HostDfa(pat)
+        py = re.compile(pat)
+        for o in block:
+            assert d.full_match(chr(o)) == bool(py.fullmatch(chr(o))), (hex(c), hex(o))

@@ -13,18 +13,28 @@
 // Syntax (the regex-syntax subset that patterns reach here): literals (UTF-8),
 // escapes of punctuation, \t \n \r \f \v \a, \xHH \x{H..} \uHHHH \u{H..}
 // \UHHHHHHHH, classes [..] with ranges, negation, nested classes and ASCII
-// POSIX names, the Perl classes \d \s \w (ASCII; regex-syntax uses their
-// Unicode tables), '.', groups ( ), (?: ), (?P<n> ), (?<n> ), flags
+// POSIX names, '.', groups ( ), (?: ), (?P<n> ), (?<n> ), flags
 // (?imsxU-imsxU) and (?flags: ), alternation, * + ? {n} {n,} {n,m} with lazy
-// forms (same language), and the anchors ^ $ \A \z. Case-insensitive mode
-// folds ASCII letters only.
+// forms (same language), and the anchors ^ $ \A \z. Unicode mode, as
+// regex-syntax's default: \d is \p{Nd}, \s is White_Space, \w is
+// [\p{Alphabetic}\p{M}\p{Nd}\p{Pc}\p{Join_Control}] (UTS #18 Annex C),
+// \p{..} / \P{..} take general categories (short or long names, one-letter
+// groups, gc= forms) and Any / ASCII / Assigned, and case-insensitive mode
+// uses simple case folding. The tables (zs_unicode.h) are generated from
+// Python's unicodedata (Unicode 13.0 in this image; regex-syntax 0.8.10 has
+// 16.0: scalars assigned after 13.0 are outside \w \d \p{..} here). Refused
+// with an error, as regex-syntax would accept them: word boundaries \b \B,
+// script and binary properties other than the above (\p{Greek}), class set
+// operations (&& -- ~~), multi-line anchors.
 #include <stdint.h>
 #include <string.h>
 #include <algorithm>
+#include <initializer_list>
 #include <string>
 #include <unordered_map>
 #include <vector>
 #include "zs_grammar.h"
+#include "zs_unicode.h"
 
 namespace {
 
@@ -67,17 +77,27 @@ struct CpSet {
         }
         r.swap(o);
     }
-    // ASCII simple case folding (case-insensitive flag)
-    void fold_ascii() {
-        std::vector<std::pair<uint32_t, uint32_t>> extra;
-        for (auto& x : r) {
-            uint32_t lo = std::max(x.first, (uint32_t)'a'), hi = std::min(x.second, (uint32_t)'z');
-            if (lo <= hi) extra.push_back({lo - 32, hi - 32});
-            lo = std::max(x.first, (uint32_t)'A');
-            hi = std::min(x.second, (uint32_t)'Z');
-            if (lo <= hi) extra.push_back({lo + 32, hi + 32});
+    bool contains(uint32_t c) const {   // canonical ranges
+        size_t lo = 0, hi = r.size();
+        while (lo < hi) {
+            const size_t mid = (lo + hi) / 2;
+            if (r[mid].second < c) lo = mid + 1;
+            else hi = mid;
         }
-        r.insert(r.end(), extra.begin(), extra.end());
+        return lo < r.size() && r[lo].first <= c;
+    }
+    // simple case folding (case-insensitive flag): adds every scalar that
+    // folds like a member (classes are cycles in zs_uc_fold)
+    void fold() {
+        canon();
+        for (;;) {
+            std::vector<std::pair<uint32_t, uint32_t>> extra;
+            for (const auto& e : zs_uc_fold)
+                if (contains(e[0]) && !contains(e[1])) extra.push_back({e[1], e[1]});
+            if (extra.empty()) return;
+            r.insert(r.end(), extra.begin(), extra.end());
+            canon();
+        }
     }
 };
 
@@ -231,7 +251,7 @@ private:
     }
 
     int class_node(CpSet s, const Flags& f) {
-        if (f.i) s.fold_ascii();
+        if (f.i) s.fold();
         s.remove_surrogates();
         s.canon();
         int n = node(K_CLASS);
@@ -377,23 +397,136 @@ private:
             return u;  // escaped punctuation or space
         pos_--;
         if (e == 'b' || e == 'B' || e == '<' || e == '>') fail("word boundary assertions are not supported");
-        if (e == 'p' || e == 'P') fail("Unicode property classes are not supported");
         if (e >= '0' && e <= '9') fail("backreferences are not supported");
         fail("unrecognized escape sequence");
     }
 
-    // \d \D \s \S \w \W (ASCII); pos_ at the letter
+    // the scalars of general categories (bit k of mask: zs_uc_cat_names[k])
+    static void add_cats(CpSet& s, uint32_t mask) {
+        for (const auto& g : zs_uc_cats)
+            if ((mask >> g.cat) & 1u) s.add(g.lo, g.hi);
+    }
+    static uint32_t cat_bit(const char* n) {
+        for (int k = 0; k < ZS_UC_NCATS; k++)
+            if (!strcmp(zs_uc_cat_names[k], n)) return 1u << k;
+        return 0;
+    }
+    static uint32_t cats(std::initializer_list<const char*> ns) {
+        uint32_t m = 0;
+        for (const char* n : ns) m |= cat_bit(n);
+        return m;
+    }
+    // PropList.txt White_Space
+    static void add_white_space(CpSet& s) {
+        s.add(0x09, 0x0D); s.add(0x20, 0x20); s.add(0x85, 0x85); s.add(0xA0, 0xA0); s.add(0x1680, 0x1680);
+        s.add(0x2000, 0x200A); s.add(0x2028, 0x2029); s.add(0x202F, 0x202F); s.add(0x205F, 0x205F);
+        s.add(0x3000, 0x3000);
+    }
+    // \w: Alphabetic (letters, Nl and Other_Alphabetic), marks, Nd, Pc and
+    // Join_Control; the Other_Alphabetic scalars outside the marks are the
+    // circled and squared Latin letters (category So)
+    static void add_word(CpSet& s) {
+        add_cats(s, cats({"Lu", "Ll", "Lt", "Lm", "Lo", "Nl", "Mn", "Mc", "Me", "Nd", "Pc"}));
+        s.add(0x200C, 0x200D);
+        s.add(0x24B6, 0x24E9);
+        s.add(0x1F130, 0x1F149);
+        s.add(0x1F150, 0x1F169);
+        s.add(0x1F170, 0x1F189);
+    }
+
+    // \d \D \s \S \w \W \p{..} \P{..} (Unicode); pos_ at the letter
     bool perl_class(CpSet& s) {
         const char e = peek();
         CpSet b;
-        if (e == 'd' || e == 'D') b.add('0', '9');
-        else if (e == 's' || e == 'S') { b.add('\t', '\r'); b.add(' ', ' '); }
-        else if (e == 'w' || e == 'W') { b.add('0', '9'); b.add('A', 'Z'); b.add('_', '_'); b.add('a', 'z'); }
-        else return false;
+        if (e == 'd' || e == 'D') add_cats(b, cats({"Nd"}));
+        else if (e == 's' || e == 'S') add_white_space(b);
+        else if (e == 'w' || e == 'W') add_word(b);
+        else if (e == 'p' || e == 'P') {
+            pos_++;
+            std::string name;
+            if (!eof() && peek() == '{') {
+                const size_t end = p_.find('}', pos_);
+                if (end == std::string::npos) fail("unclosed Unicode class");
+                name = p_.substr(pos_ + 1, end - pos_ - 1);
+                pos_ = end + 1;
+            } else {
+                if (eof()) fail("incomplete escape sequence");
+                name = std::string(1, peek());
+                pos_++;
+            }
+            unicode_class(name, b);
+            if (e == 'P') b.negate();
+            s.add(b);
+            return true;
+        } else {
+            return false;
+        }
         pos_++;
         if (e == 'D' || e == 'S' || e == 'W') b.negate();
         s.add(b);
         return true;
+    }
+
+    // \p{name}: general categories, Any, ASCII, Assigned (UAX #44 loose
+    // matching: case, spaces, '_' and '-' ignored; "gc=" prefixes allowed)
+    void unicode_class(const std::string& raw, CpSet& b) {
+        std::string n;
+        bool neg = false;
+        for (char c : raw) {
+            if (c == ' ' || c == '_' || c == '-') continue;
+            n += (char)((c >= 'A' && c <= 'Z') ? c - 'A' + 'a' : c);
+        }
+        if (!n.empty() && n[0] == '^') { neg = true; n = n.substr(1); }
+        for (const char* pre : {"generalcategory=", "generalcategory:", "gc=", "gc:"}) {
+            const size_t L = strlen(pre);
+            if (n.compare(0, L, pre) == 0) { n = n.substr(L); break; }
+        }
+        static const struct { const char* name; const char* cats; } T[] = {
+            {"l", "Lu Ll Lt Lm Lo"}, {"letter", "Lu Ll Lt Lm Lo"}, {"lc", "Lu Ll Lt"}, {"l&", "Lu Ll Lt"},
+            {"casedletter", "Lu Ll Lt"}, {"lu", "Lu"}, {"uppercaseletter", "Lu"}, {"ll", "Ll"},
+            {"lowercaseletter", "Ll"}, {"lt", "Lt"}, {"titlecaseletter", "Lt"}, {"lm", "Lm"},
+            {"modifierletter", "Lm"}, {"lo", "Lo"}, {"otherletter", "Lo"}, {"m", "Mn Mc Me"},
+            {"mark", "Mn Mc Me"}, {"combiningmark", "Mn Mc Me"}, {"mn", "Mn"}, {"nonspacingmark", "Mn"},
+            {"mc", "Mc"}, {"spacingmark", "Mc"}, {"me", "Me"}, {"enclosingmark", "Me"}, {"n", "Nd Nl No"},
+            {"number", "Nd Nl No"}, {"nd", "Nd"}, {"decimalnumber", "Nd"}, {"digit", "Nd"}, {"nl", "Nl"},
+            {"letternumber", "Nl"}, {"no", "No"}, {"othernumber", "No"}, {"p", "Pc Pd Ps Pe Pi Pf Po"},
+            {"punctuation", "Pc Pd Ps Pe Pi Pf Po"}, {"punct", "Pc Pd Ps Pe Pi Pf Po"}, {"pc", "Pc"},
+            {"connectorpunctuation", "Pc"}, {"pd", "Pd"}, {"dashpunctuation", "Pd"}, {"ps", "Ps"},
+            {"openpunctuation", "Ps"}, {"pe", "Pe"}, {"closepunctuation", "Pe"}, {"pi", "Pi"},
+            {"initialpunctuation", "Pi"}, {"pf", "Pf"}, {"finalpunctuation", "Pf"}, {"po", "Po"},
+            {"otherpunctuation", "Po"}, {"s", "Sm Sc Sk So"}, {"symbol", "Sm Sc Sk So"}, {"sm", "Sm"},
+            {"mathsymbol", "Sm"}, {"sc", "Sc"}, {"currencysymbol", "Sc"}, {"sk", "Sk"},
+            {"modifiersymbol", "Sk"}, {"so", "So"}, {"othersymbol", "So"}, {"z", "Zs Zl Zp"},
+            {"separator", "Zs Zl Zp"}, {"zs", "Zs"}, {"spaceseparator", "Zs"}, {"zl", "Zl"},
+            {"lineseparator", "Zl"}, {"zp", "Zp"}, {"paragraphseparator", "Zp"}, {"cc", "Cc"},
+            {"control", "Cc"}, {"cntrl", "Cc"}, {"cf", "Cf"}, {"format", "Cf"}, {"co", "Co"},
+            {"privateuse", "Co"}, {"cs", "Cs"}, {"surrogate", "Cs"},
+        };
+        bool found = false;
+        for (const auto& t : T) {
+            if (n != t.name) continue;
+            uint32_t m = 0;
+            std::string cs = t.cats;
+            for (size_t i = 0; i < cs.size(); i += 3) m |= cat_bit(cs.substr(i, 2).c_str());
+            add_cats(b, m);
+            found = true;
+            break;
+        }
+        if (!found) {
+            if (n == "any") b.add(0, CP_MAX);
+            else if (n == "ascii") b.add(0, 0x7F);
+            else if (n == "assigned") add_cats(b, 0xffffffffu);
+            else if (n == "cn" || n == "unassigned") { add_cats(b, 0xffffffffu); b.negate(); }
+            else if (n == "c" || n == "other") {   // Cc Cf Cs Co and the unassigned
+                CpSet a;
+                add_cats(a, ~cats({"Cc", "Cf", "Cs", "Co"}));
+                a.negate();
+                b.add(a);
+            } else {
+                fail("Unicode property not supported (general categories, Any, ASCII and Assigned only)");
+            }
+        }
+        if (neg) b.negate();
     }
 
     bool posix_class(CpSet& s) {
@@ -478,7 +611,7 @@ private:
                 s.add((uint32_t)lo, (uint32_t)lo);
             }
         }
-        if (f.i) s.fold_ascii();
+        if (f.i) s.fold();
         if (neg) s.negate();
         return s;
     }
