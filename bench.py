@@ -218,6 +218,166 @@ def cpu_baseline(W, seconds, cores):
     return done / el, done
 
 
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def build_config(ctx, name, seed):
+    """Inputs of BASELINE.json configs 1-4 (the sampler part; C3 / C4 with
+    their grammar masks): dict(x, rows, params, bits, dfa, table, states,
+    masked, hist)."""
+    import numpy as np
+    import torch
+    from zllm_amd import synth
+    from zllm_amd.engine import (ByteDfa, DecodeControl, LogitFSM, PenaltyConfig, RowRequest, SamplerConfig,
+                                 TokenByteTable)
+    rng = np.random.default_rng(seed + 101)
+    C = {"name": name, "dfa": None, "table": None, "states": None}
+    if name == "c1":
+        x = synth.logits_c1(0)
+        V = x.shape[1]
+        hist = rng.integers(0, V, 64)
+        ids, cnt = np.unique(hist, return_counts=True)
+        params = [dict(temperature=0.8, top_k=40, top_p=0.95, min_p=0.0, repeat=1.1, presence=0.0, frequency=0.0,
+                       counts=list(zip(ids.tolist(), cnt.tolist())))]
+    elif name == "c2":
+        B, V = 64, 128256
+        x = synth.logits_powerlaw(B, V, 2)
+        params = synth.mixed_params(B, V, 2, hist=256)
+    elif name == "c3":
+        B, V = 32, 128256
+        x = synth.logits_powerlaw(B, V, 3)
+        params = [dict(temperature=1.0, top_k=0, top_p=1.0, min_p=0.0, repeat=1.0, presence=0.0, frequency=0.0,
+                       counts=[]) for _ in range(B)]
+        trans, dead, acc = synth.random_dfa(64, seed + 64, dead_rate=0.3)
+    else:   # c4
+        B, V = 128, 151936
+        x = synth.logits_powerlaw(B, V, 4)
+        params = [dict(temperature=0.7, top_k=0, top_p=0.9, min_p=0.0, repeat=1.0, presence=0.0, frequency=0.0,
+                       counts=[], ban=[int(t) for t in rng.choice(V, 500, replace=False)]) for _ in range(B)]
+        trans, dead, acc = synth.json_dfa(2048, seed + 2048)
+    B, V = x.shape
+    if name in ("c3", "c4"):
+        offs, data = synth.synthetic_vocab(V, seed + V)
+        C["table"] = TokenByteTable.from_csr(ctx, offs, data, np.ones(V, np.uint8), eos=V - 1)
+        C["dfa"] = ByteDfa(ctx, trans, dead, acc)
+        live = [q for q in range(trans.shape[0]) if C["dfa"].is_live(q) and not dead[q]]
+        C["states"] = torch.tensor(rng.choice(live, B).astype(np.int32), device="cuda")
+        C["trans"], C["dead"], C["acc"], C["offs"], C["data"] = trans, dead, acc, offs, data
+    rows = []
+    for i, p in enumerate(params):
+        ctrl = DecodeControl(PenaltyConfig(p["repeat"], p["presence"], p["frequency"]), (), seed=900 + i)
+        for t, c in p["counts"]:
+            ctrl.counts[int(t)] = int(c)
+        fsm = LogitFSM(banned=p["ban"]) if p.get("ban") else None
+        rq = RowRequest(SamplerConfig(p["temperature"], p["top_k"], p["top_p"], p["min_p"]), ctrl, fsm, 5)
+        rq.masked = C["dfa"] is not None
+        rq.logprobs = True
+        rq.detect_hallucination = True
+        rows.append(rq)
+    C.update(x=x, xs=torch.from_numpy(x).cuda(), params=params, rows=rows,
+             bits=torch.zeros((B, (V + 31) // 32), dtype=torch.int32, device="cuda"),
+             hist=[len(p["counts"]) + len(p.get("ban", ())) for p in params])
+    return C
+
+
+def config_measure(ctx, C, iters=20):
+    """GPU: sampler us per step over the config's batch (the grammar mask
+    separately), rows/s and the sampler's HBM fraction."""
+    import torch
+    from zllm_amd.engine import BatchSampler
+    xs, bits = C["xs"], C["bits"]
+    B, V = xs.shape
+    sampler = BatchSampler(ctx)
+    bufs = sampler.pack(xs, C["rows"], bits if C["dfa"] is not None else None)
+    ab = bits if C["dfa"] is not None else None
+    if C["dfa"] is not None:
+        C["dfa"].mask(C["table"], C["states"], V, out=bits)
+    out = None
+    for _ in range(3):
+        out = sampler.run(xs, bufs, ab, top_stride=5, out=out)
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(iters):
+        out = sampler.run(xs, bufs, ab, top_stride=5, out=out)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) / iters * 1000.0
+    res = {"B": B, "V": V, "sampler_us": round(us, 2), "rows_per_s": round(B / (us * 1e-6), 1)}
+    masked = C["dfa"] is not None
+    nbytes = sum(algorithmic_bytes_per_row(V, C["hist"][i], masked) for i in range(B))
+    res["sampler_hbm_frac"] = round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+    if masked:
+        m0, m1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        m0.record(stream)
+        for _ in range(iters):
+            C["dfa"].mask(C["table"], C["states"], V, out=bits)
+        m1.record(stream)
+        torch.cuda.synchronize()
+        res["mask_us"] = round(m0.elapsed_time(m1) / iters * 1000.0, 2)
+    res["toplp_ambig_rows"] = int(((out["status"].cpu().numpy().view("uint32") & 8) != 0).sum())
+    return res
+
+
+def config_cpu(C, seconds, cores):
+    """CPU oracle on the same rows: rows/s on one core and on `cores` threads
+    (bounded samples of about `seconds` each), and for grammar configs the
+    CPU mask per row: cold (the DFA walk over every token) and warm (the
+    per-state memo of logit_fsm.rs:166-182 hit: the cached mask applied)."""
+    import numpy as np
+    from concurrent.futures import ThreadPoolExecutor
+    from oracle import oracle as O
+    x = C["x"]
+    B, V = x.shape
+    od = ov = None
+    st = None
+    if C["dfa"] is not None:
+        ov = O.Vocab([bytes(C["data"][C["offs"][t]:C["offs"][t + 1]]) for t in range(V)], V - 1)
+        od = O.Dfa(C["trans"], C["dead"], C["acc"])
+        st = C["states"].cpu().numpy()
+
+    def one(i):
+        p = dict(C["params"][i % B])
+        p["top_logprobs"] = 5
+        return O.reference_step(x[i % B], p, ban=p.get("ban", ()), counts=p["counts"], dfa=od,
+                                vocab=ov, state=int(st[i % B]) if st is not None else -1, seed=900 + i,
+                                counter=0)["token"]
+
+    res = {}
+    for n in (1, cores):
+        done, t0 = 0, time.time()
+        with ThreadPoolExecutor(n) as ex:
+            while time.time() - t0 < seconds / 2 and done < 8 * B:
+                list(ex.map(one, range(done, done + n)))
+                done += n
+        res[f"rows_per_s_{n}core" if n == 1 else "rows_per_s_ncore"] = round(done / (time.time() - t0), 2)
+    if od is not None:
+        t0 = time.time()
+        k = 0
+        cache = {}
+        while time.time() - t0 < seconds / 4 and k < B:
+            allowed, _ = O.dfa_allowed(od, ov, int(st[k]))
+            cache[int(st[k])] = allowed.astype(bool)
+            k += 1
+        cold = (time.time() - t0) / k
+        t0 = time.time()
+        for j in range(k):
+            xm = x[j].copy()
+            xm[~cache[int(st[j])]] = -np.inf
+        warm = (time.time() - t0) / k
+        res["mask_cold_ms_per_row"] = round(cold * 1e3, 3)
+        res["mask_warm_ms_per_row"] = round(warm * 1e3, 3)
+    return res
+
+
 def copy_probe(mib):
     """A plain device copy of known size: its FETCH_SIZE / WRITE_SIZE per
     dispatch against mib * 1024 KiB gives the counter scale."""
@@ -347,13 +507,27 @@ def main():
     # processes times their per-row bytes (the logits it must read at least once)
     big_rows = [i for i in range(B) if not (status[i] & (1 | 2 | 4))]  # not greedy / non-finite / small
     per_kernel_bytes = {
-        "zs_k_pass1": float(sum(row_bytes)),
+        "zs_k_row": float(sum(row_bytes)),
         "zs_k_big": float(sum(row_bytes[i] for i in big_rows)),
         "zs_k_pv": float(sum(4 * V + 4 * V for i in big_rows)),   # read logits, write p
         "zs_k_spec_chunk": float(B * 4 * V * (2 * SPEC_K + 1)),
     }
     dom_bytes = per_kernel_bytes.get(dom, step_bytes)
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
+    # the sampler chain alone (one stream): every sampler kernel's time, against
+    # the bytes every row must read once
+    samp_ms = sum(v for k, v in acc.items() if not k.startswith("zs_k_spec") and not k.startswith("zs_k_dfa"))
+    samp_bytes = float(sum(row_bytes))
+    samp_gbs = samp_bytes / (samp_ms * 1e-3) / 1e9
+    ambig = int(((status.view("uint32") & 8) != 0).sum())
+    cores = min(16, len(os.sched_getaffinity(0)))
+    configs = {}
+    for name in ("c1", "c2", "c3", "c4"):
+        Cf = build_config(ctx, name, args.seed)
+        configs[name] = config_measure(ctx, Cf)
+        if not args.no_cpu:
+            configs[name]["cpu"] = config_cpu(Cf, args.cpu_seconds / 4, cores)
+        del Cf
     cpu = None
     if not args.no_cpu:
         cores = min(16, len(os.sched_getaffinity(0)))
@@ -388,6 +562,13 @@ def main():
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC.get(dom),
                      "algorithmic_bytes": dom_bytes, "ms": round(dom_ms, 4)},
+        "roofline_sampler": {"bound": "hbm", "kernels": "zs_sample (all its kernels, one stream)",
+                             "achieved": round(samp_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                             "frac": round(samp_gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": samp_bytes,
+                             "ms": round(samp_ms, 4)},
+        "toplp_ambig_rows": ambig,
+        "configs": configs,
+        "cpu_model": cpu_model(),
         "cpu_baseline": cpu,
     }
     print(json.dumps(res))

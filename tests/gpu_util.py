@@ -78,10 +78,23 @@ def close(a, b, rel=1e-5, abs_=1e-5):
     return abs(a - b) <= max(abs_, rel * abs(b))
 
 
+AMBIG_FRAC = 0.02   # rows whose top_logprobs ids may be compared as a set at most
+
+
 def compare(x, params_list, out, allow=None, check_stats=True, refs=None):
     """Asserts bit-exact tokens and top ids; tolerance on float outputs.
-    refs: the oracle's results per row when the caller computed them."""
+    refs: the oracle's results per row when the caller computed them.
+
+    Rows flagged ZS_ST_TOPLP_AMBIG (their top_logprobs order depends on the
+    last bit of lse, so the ranking is left unchecked) are counted
+    and printed; more than AMBIG_FRAC of the rows (at least one allowed) is an
+    error."""
     errs = []
+    n_amb = int(np.count_nonzero(np.asarray(out["status"]).view(np.uint32) & 8))
+    lim = max(1, int(np.ceil(AMBIG_FRAC * len(params_list))))
+    print(f"[toplp-ambig] {n_amb} of {len(params_list)} rows", flush=True)
+    if n_amb > lim:
+        errs.append(f"{n_amb} rows flagged ZS_ST_TOPLP_AMBIG (limit {lim})")
     for i, p in enumerate(params_list):
         ref = refs[i] if refs is not None else oracle_row(x[i], p, None if allow is None else allow[i])
         tok = int(out["token"][i]) & 0xFFFFFFFF

@@ -586,3 +586,47 @@ def test_spec_rejection_sampling_preserves_target_distribution():
         counts[d if acc == 1 else nxt] += 1
     chi2 = (((counts - N * p) ** 2) / (N * p)).sum()
     assert chi2 < 25.0, (chi2, counts / N, p)  # 5 dof: p(chi2 > 25) ~ 1e-4
+
+
+def test_spec_rejection_sampling_k3_acceptance_and_bonus():
+    """k = 3 drafts: the joint law of (accepted, next) over N trials against
+    its closed form (Leviathan et al. 2023, Thm 1 applied position by
+    position): with a_i = sum_x min(p_i, q_i), P(accepted = j, next = x) is
+    prod_{i<j} a_i * (1 - a_j) * r_j(x) for j < 3, r_j = norm(max(0, p_j - q_j)),
+    and prod_i a_i * p_3(x) for the all-accepted bonus draw from row k."""
+    rng = np.random.default_rng(3)
+    V, k = 4, 3
+    tl = np.array([[1.0, 0.2, -1.0, 2.0], [0.0, 1.0, 0.5, -0.5], [0.3, 0.3, 1.2, 0.0], [2.0, 0.0, 0.5, 1.0]],
+                  np.float32)
+    dl = np.array([[0.0, 1.5, 0.3, -0.5], [0.5, 0.0, 1.0, 0.2], [0.0, 0.8, 0.6, -1.0]], np.float32)
+
+    def weights(x):
+        e = np.array([np.float32(np.exp(np.float32(v - x.max()))) for v in x], np.float64)
+        return np.rint(e * 2 ** 24)
+
+    p = [weights(r) / weights(r).sum() for r in tl]
+    q = [weights(r) / weights(r).sum() for r in dl]
+    a = [np.minimum(p[i], q[i]).sum() for i in range(k)]
+    expect = np.zeros((k + 1, V))
+    reach = 1.0
+    for j in range(k):
+        r = np.maximum(p[j] - q[j], 0.0)
+        expect[j] = reach * (1.0 - a[j]) * r / r.sum()
+        reach *= a[j]
+    expect[k] = reach * p[k]
+    assert abs(expect.sum() - 1.0) < 1e-9
+    N = 40000
+    counts = np.zeros((k + 1, V))
+    for c in range(N):
+        drafts = [int(rng.choice(V, p=q[i])) for i in range(k)]
+        acc, nxt = O.spec_verify(tl, dl, drafts, 1.0, seed=5, counter=c)
+        counts[acc, nxt] += 1
+    m = expect > 0
+    chi2 = (((counts[m] - N * expect[m]) ** 2) / (N * expect[m])).sum()
+    assert counts[~m].sum() == 0
+    dof = int(m.sum()) - 1
+    assert chi2 < dof + 6.0 * np.sqrt(2.0 * dof), (chi2, dof, counts / N, expect)  # ~4.2 sigma
+    # per-position acceptance (the marginal of `accepted`)
+    acc_emp = counts.sum(1) / N
+    acc_exp = expect.sum(1)
+    assert np.all(np.abs(acc_emp - acc_exp) < 5 * np.sqrt(acc_exp * (1 - acc_exp) / N) + 1e-9), (acc_emp, acc_exp)
