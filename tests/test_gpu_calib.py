@@ -1,9 +1,10 @@
-"""Calibration of the fast f32 exp behind the certified increments: its
-relative error over every input of its domain must stay far below the band
-ZS_EXP_EPS = 2^-18 the kernels assume.
+"""Calibrations of the fast approximations behind certified results: the
+fast f32 exp of the exact sums (relative error far below ZS_EXP_EPS = 2^-18
+over every input of its domain) and the fast Gumbel term of the lane's
+BSAMPLE (within ZS_GUMBEL_EPS / 4 of the exact term for all 2^24 uniforms).
 
-The sweep is a test program (tests/c/calib_exp.hip), not part of the
-library: this test compiles it with the library's flags when the binary is
+The sweeps are test programs (tests/c/calib_*.hip), not part of the
+library: this test compiles each with the library's flags when the binary is
 missing or older than its source."""
 import os
 import subprocess
@@ -12,23 +13,31 @@ import pytest
 
 pytestmark = pytest.mark.gpu
 HERE = os.path.dirname(os.path.abspath(__file__))
-SRC = os.path.join(HERE, "c", "calib_exp.hip")
-EXE = os.path.join(HERE, "c", "calib_exp")
 
 
-def build_calibration():
+def build_calibration(name="calib_exp"):
     from zllm_amd.build import FLAGS, HIPCC
-    if os.path.exists(EXE) and os.path.getmtime(EXE) >= os.path.getmtime(SRC):
-        return EXE
+    src = os.path.join(HERE, "c", name + ".hip")
+    exe = os.path.join(HERE, "c", name)
+    if os.path.exists(exe) and os.path.getmtime(exe) >= os.path.getmtime(src):
+        return exe
     flags = [f for f in FLAGS if f not in ("-fPIC", "-shared")]
-    r = subprocess.run([HIPCC] + flags + [SRC, "-o", EXE], capture_output=True, text=True)
+    r = subprocess.run([HIPCC] + flags + [src, "-o", exe], capture_output=True, text=True)
     assert r.returncode == 0, "hipcc failed building the calibration sweep:\n" + r.stdout + r.stderr
-    return EXE
+    return exe
 
 
 def test_fast_exp_error_bound():
     exe = build_calibration()
     print("[case] fast exp sweep", flush=True)
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout + r.stderr
+
+
+def test_fast_gumbel_error_bound():
+    exe = build_calibration("calib_gumbel")
+    print("[case] fast gumbel sweep", flush=True)
     r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
     print(r.stdout)
     assert r.returncode == 0, r.stdout + r.stderr

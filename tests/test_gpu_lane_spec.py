@@ -55,6 +55,11 @@ def test_bargmax_and_bsample():
     x[0, [300, 5, 7000]] = 2.0
     x[1, :] = -2e30
     x[2, 11] = np.nan
+    x[3, :] = -np.inf            # two finite ids only
+    x[3, [10, 20]] = 1.0
+    x[4, 77] = np.inf
+    x[5, :] = 1e33               # beyond the fast Gumbel bands: every id exact
+    x[6, :] = 1.0                # only the Gumbel terms differ
     xs = torch.from_numpy(x).cuda()
     a = lane_argmax(_c(), xs).cpu().numpy()
     for s in range(B):

@@ -14,7 +14,9 @@
 extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t stream);
 extern "C" int zs_spec_launch(const zs_spec_args& a, const zs_prof& prof, hipStream_t stream);
 extern "C" int zs_lane_argmax_launch(const float* logits, uint32_t B, uint32_t V, uint64_t ld, const float* temp,
-                                     const uint32_t* seed, uint32_t* out, hipStream_t stream);
+                                     const uint32_t* seed, const uint32_t* ih, unsigned long long* keys,
+                                     uint32_t* out, hipStream_t stream);
+extern "C" int zs_lane_hash_fill(uint32_t* ih, uint32_t n, hipStream_t stream);
 extern "C" int zs_lane_topk_launch(const float* logits, uint32_t B, uint32_t V, uint64_t ld, uint32_t K,
                                    float* vals, uint32_t* idxs, unsigned long long* ck, uint32_t* cn,
                                    hipStream_t stream);
@@ -66,14 +68,15 @@ extern "C" void zs_ctx_destroy(zs_ctx* ctx) {
     if (ctx->fork_event) (void)hipEventDestroy((hipEvent_t)ctx->fork_event);
     if (ctx->join_event) (void)hipEventDestroy((hipEvent_t)ctx->join_event);
     if (ctx->side_stream) (void)hipStreamDestroy((hipStream_t)ctx->side_stream);
-    if (ctx->lane_event) {
-        (void)hipEventSynchronize((hipEvent_t)ctx->lane_event);
-        (void)hipEventDestroy((hipEvent_t)ctx->lane_event);
-    }
+    for (int i = 0; i < 2; i++)
+        if (ctx->lane_event[i]) {
+            (void)hipEventSynchronize((hipEvent_t)ctx->lane_event[i]);
+            (void)hipEventDestroy((hipEvent_t)ctx->lane_event[i]);
+        }
     if (ctx->lane_host) (void)hipHostFree(ctx->lane_host);
     void* ptrs[] = {ctx->p_cnt, ctx->p_id, ctx->p_flags, ctx->p_y, ctx->rst, ctx->pairs, ctx->pv, ctx->mask_scratch, ctx->spec_chunks,
                     ctx->spec_rows, ctx->p_sub, ctx->k_ap, ctx->k_sum, ctx->tp_bk, ctx->tp_cl, ctx->tp_pre, ctx->kcnt,
-                    ctx->lane_temp, ctx->lane_topk, ctx->lane_topp, ctx->lane_seed, ctx->lane_vals,
+                    ctx->lane_temp, ctx->lane_topk, ctx->lane_topp, ctx->lane_seed, ctx->lane_vals, ctx->lane_ih, ctx->lane_keys,
                     ctx->lane_idxs, ctx->lane_ck, ctx->lane_cn};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
@@ -138,14 +141,22 @@ extern "C" int zs_ctx_create(int device, uint32_t max_rows, uint32_t max_vocab, 
     if (!rc) rc = zs_alloc(ctx, &ctx->lane_idxs, R * ZS_LANE_K);
     if (!rc) rc = zs_alloc(ctx, &ctx->lane_ck, R * C * ZS_LANE_K);
     if (!rc) rc = zs_alloc(ctx, &ctx->lane_cn, R * C);
+    if (!rc) rc = zs_alloc(ctx, &ctx->lane_ih, (size_t)ctx->max_vocab + 4);
+    if (!rc) rc = zs_alloc(ctx, &ctx->lane_keys, R);
+    if (!rc && hipMemset(ctx->lane_keys, 0, R * sizeof(unsigned long long)) != hipSuccess) rc = ZS_EHIP;
+    if (!rc && (zs_lane_hash_fill(ctx->lane_ih, ctx->max_vocab + 4, nullptr) || hipDeviceSynchronize() != hipSuccess))
+        rc = ZS_EHIP;
     if (!rc) {
         void* h = nullptr;
-        hipEvent_t e = nullptr;
-        if (hipHostMalloc(&h, 4 * R * sizeof(uint32_t), hipHostMallocDefault) != hipSuccess ||
-            hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess)
+        hipEvent_t e0 = nullptr, e1 = nullptr;
+        if (hipHostMalloc(&h, 8 * R * sizeof(uint32_t), hipHostMallocDefault) != hipSuccess ||
+            hipEventCreateWithFlags(&e0, hipEventDisableTiming) != hipSuccess ||
+            hipEventCreateWithFlags(&e1, hipEventDisableTiming) != hipSuccess)
             rc = ZS_ENOMEM;
         ctx->lane_host = (uint32_t*)h;
-        ctx->lane_event = e;
+        ctx->lane_event[0] = e0;
+        ctx->lane_event[1] = e1;
+        ctx->lane_slot = 0;
     }
     if (!rc) {
         hipStream_t s2 = nullptr;
@@ -676,7 +687,7 @@ extern "C" int zs_lane_argmax(zs_ctx* ctx, const float* d_logits, uint32_t B, ui
     if (!d_out) return zs_set_error(ctx, ZS_EINVAL, "zs_lane_argmax: null output");
     if (B == 0) return ZS_OK;
     int prev = zs_device_guard_begin(ctx);
-    rc = zs_lane_argmax_launch(d_logits, B, V, ld, nullptr, nullptr, d_out, (hipStream_t)stream);
+    rc = zs_lane_argmax_launch(d_logits, B, V, ld, nullptr, nullptr, nullptr, nullptr, d_out, (hipStream_t)stream);
     zs_device_guard_end(ctx, prev);
     return rc ? zs_set_error(ctx, ZS_EHIP, "zs_lane_argmax: launch failed") : ZS_OK;
 }
@@ -688,7 +699,7 @@ extern "C" int zs_lane_sample(zs_ctx* ctx, const float* d_logits, uint32_t B, ui
     if (!d_out || !d_temperature || !d_seed) return zs_set_error(ctx, ZS_EINVAL, "zs_lane_sample: null argument");
     if (B == 0) return ZS_OK;
     int prev = zs_device_guard_begin(ctx);
-    rc = zs_lane_argmax_launch(d_logits, B, V, ld, d_temperature, d_seed, d_out, (hipStream_t)stream);
+    rc = zs_lane_argmax_launch(d_logits, B, V, ld, d_temperature, d_seed, ctx->lane_ih, ctx->lane_keys, d_out, (hipStream_t)stream);
     zs_device_guard_end(ctx, prev);
     return rc ? zs_set_error(ctx, ZS_EHIP, "zs_lane_sample: launch failed") : ZS_OK;
 }
@@ -746,13 +757,17 @@ extern "C" int zs_lane_step(zs_ctx* ctx, const float* d_logits, uint32_t m, uint
     const hipStream_t st = (hipStream_t)stream;
     const int prev = zs_device_guard_begin(ctx);
     if (p != ZS_LANE_ARGMAX) {
-        // the staging area is reused: wait for the previous call's copy
-        if (hipEventSynchronize((hipEvent_t)ctx->lane_event) != hipSuccess) rc = ZS_EHIP;
+        // two staging areas, alternating: wait for the copy made from this
+        // one two calls ago (the call before it keeps running meanwhile)
+        const uint32_t slot = ctx->lane_slot;
+        ctx->lane_slot ^= 1u;
+        if (hipEventSynchronize((hipEvent_t)ctx->lane_event[slot]) != hipSuccess) rc = ZS_EHIP;
         const size_t R = ctx->max_rows;
-        float* ht = (float*)ctx->lane_host;
-        uint32_t* hk = ctx->lane_host + R;
-        float* hp = (float*)(ctx->lane_host + 2 * R);
-        uint32_t* hs = ctx->lane_host + 3 * R;
+        uint32_t* area = ctx->lane_host + (size_t)slot * 4 * R;
+        float* ht = (float*)area;
+        uint32_t* hk = area + R;
+        float* hp = (float*)(area + 2 * R);
+        uint32_t* hs = area + 3 * R;
         for (uint32_t i = 0; i < m; i++) {
             ht[i] = h_streams[i].temp;
             hk[i] = h_streams[i].top_k;
@@ -763,14 +778,14 @@ extern "C" int zs_lane_step(zs_ctx* ctx, const float* d_logits, uint32_t m, uint
                     hipMemcpyAsync(ctx->lane_topk, hk, m * 4, hipMemcpyHostToDevice, st) != hipSuccess ||
                     hipMemcpyAsync(ctx->lane_topp, hp, m * 4, hipMemcpyHostToDevice, st) != hipSuccess ||
                     hipMemcpyAsync(ctx->lane_seed, hs, m * 4, hipMemcpyHostToDevice, st) != hipSuccess ||
-                    hipEventRecord((hipEvent_t)ctx->lane_event, st) != hipSuccess))
+                    hipEventRecord((hipEvent_t)ctx->lane_event[slot], st) != hipSuccess))
             rc = ZS_EHIP;
     }
     if (!rc) {
         if (p == ZS_LANE_ARGMAX)
-            rc = zs_lane_argmax_launch(d_logits, m, V, ld, nullptr, nullptr, d_out, st);
+            rc = zs_lane_argmax_launch(d_logits, m, V, ld, nullptr, nullptr, nullptr, nullptr, d_out, st);
         else if (p == ZS_LANE_SAMPLE)
-            rc = zs_lane_argmax_launch(d_logits, m, V, ld, ctx->lane_temp, ctx->lane_seed, d_out, st);
+            rc = zs_lane_argmax_launch(d_logits, m, V, ld, ctx->lane_temp, ctx->lane_seed, ctx->lane_ih, ctx->lane_keys, d_out, st);
         else {
             rc = zs_lane_topk_launch(d_logits, m, V, ld, ZS_LANE_K, ctx->lane_vals, ctx->lane_idxs,
                                      V <= ctx->max_vocab ? ctx->lane_ck : nullptr, ctx->lane_cn, st);

@@ -195,8 +195,11 @@ struct zs_ctx {
     uint32_t* lane_idxs;         // [rows][ZS_LANE_K]
     unsigned long long* lane_ck; // [rows][chunks][ZS_LANE_K] chunk top-K lists (two-phase BTOPK)
     uint32_t* lane_cn;           // [rows][chunks]
-    uint32_t* lane_host;         // pinned [4][rows]: temp, top_k, top_p, seed
-    void* lane_event;            // hipEvent_t: staging copy of the last call done
+    uint32_t* lane_ih;           // [max_vocab + 4] hash of every id (the id half of BSAMPLE's uniforms)
+    unsigned long long* lane_keys;  // [rows] BSAMPLE's per-row best key (zero between calls)
+    uint32_t* lane_host;         // pinned [2][4][rows]: temp, top_k, top_p, seed (two areas, alternating)
+    void* lane_event[2];         // hipEvent_t: the staging copy from each area done
+    uint32_t lane_slot;          // the area the next call fills
     int n_spec_timed;      // the same for the last zs_spec_verify call
     void* spec_events[8];
     const char* spec_names[8];

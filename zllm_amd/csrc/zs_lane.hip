@@ -54,50 +54,217 @@ __device__ __forceinline__ uint32_t zs_hash_u32(uint32_t x) {
     h ^= h >> 16;
     return h;
 }
-__device__ __forceinline__ float zs_rand01(uint32_t s, uint32_t i) {
-    uint32_t r = zs_hash_u32(s ^ zs_hash_u32(i));
+// rand01 from the id's half of the hash, hi = zs_hash_u32(i)
+__device__ __forceinline__ float zs_rand01_h(uint32_t s, uint32_t hi) {
+    uint32_t r = zs_hash_u32(s ^ hi);
     return ((float)(r >> 8) + 0.5f) / 16777216.0f;
 }
-// WGSL `log` has no precision contract; this build fixes it as the correctly
-// rounded f32 log (double log rounded once).
-__device__ __forceinline__ float zs_log_cr(float x) { return (float)log((double)x); }
+__device__ __forceinline__ float zs_rand01(uint32_t s, uint32_t i) { return zs_rand01_h(s, zs_hash_u32(i)); }
 
-// BARGMAX (shaders.rs:761-789) and BSAMPLE (:796-850): temp == nullptr -> argmax.
-__global__ __launch_bounds__(LN_NT) void zs_k_bargmax(const float* logits, uint32_t V, uint64_t ld,
-                                                       const float* temp, const uint32_t* seed, uint32_t* out) {
+// ih[i] = zs_hash_u32(i): the id half of every row's uniforms, computed once
+// per context (BSAMPLE reads it instead of hashing each id again)
+__global__ void zs_k_lane_hash_fill(uint32_t* ih, uint32_t n) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) ih[i] = zs_hash_u32(i);
+}
+extern "C" int zs_lane_hash_fill(uint32_t* ih, uint32_t n, hipStream_t stream) {
+    hipLaunchKernelGGL(zs_k_lane_hash_fill, dim3((n + 255) / 256), dim3(256), 0, stream, ih, n);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+// WGSL `log` has no precision contract; this build fixes it as the f32
+// rounding of the double log. Fast path: ln x in double from the atanh series
+// of m in [sqrt(1/2), sqrt(2)) (x = m 2^e), relative error below 2^-44.7
+// over every positive normal float up to 18 (the arguments here: u in (0, 1)
+// and -ln u <= 17.33); its f32 rounding is certain unless the value lies
+// within 2^-40 (relative) of a midpoint between floats (about 2e-5 of the
+// inputs), where the double log is evaluated as the reference does; so are
+// arguments outside that range.
+__device__ __forceinline__ double zs_log_series(float x) {
+    const uint32_t ix = __float_as_uint(x);
+    int e = (int)(ix >> 23) - 127;
+    float m = __uint_as_float((ix & 0x7fffffu) | 0x3f800000u);
+    if (m > 1.41421356f) { m *= 0.5f; e += 1; }
+    const double md = (double)m, num = md - 1.0, den = md + 1.0;
+    double r = __builtin_amdgcn_rcp(den);
+    r = fma(fma(-den, r, 1.0), r, r);
+    r = fma(fma(-den, r, 1.0), r, r);
+    const double f = num * r, f2 = f * f;
+    double p = 1.0 / 15;
+    p = fma(p, f2, 1.0 / 13);
+    p = fma(p, f2, 1.0 / 11);
+    p = fma(p, f2, 1.0 / 9);
+    p = fma(p, f2, 1.0 / 7);
+    p = fma(p, f2, 1.0 / 5);
+    p = fma(p, f2, 1.0 / 3);
+    p = fma(p, f2, 1.0);
+    return fma((double)e, 0.6931471805599453, 2.0 * f * p);
+}
+__device__ __forceinline__ float zs_log_cr(float x) {
+    // zeros (u = 1 gives -ln u = -0, whose log is -inf), infinities, NaN and
+    // subnormals take the double log
+    if (!(x >= 0x1p-126f && x <= 18.0f)) return (float)log((double)x);   // rare
+    const double a = zs_log_series(x);
+    const float r = (float)a;
+    const double rd = (double)r, err = fabs(a) * 0x1p-40;
+    const double up = (double)__uint_as_float(__float_as_uint(r) + (r >= 0.0f ? 1u : 0xffffffffu));
+    const double dn = (double)__uint_as_float(__float_as_uint(r) + (r >= 0.0f ? 0xffffffffu : 1u));
+    if (fabs(a - 0.5 * (rd + up)) <= err || fabs(a - 0.5 * (rd + dn)) <= err) return (float)log((double)x);  // rare
+    return r;
+}
+
+// Gumbel term -ln(-ln u) with v_log_f32: within ZS_GUMBEL_EPS of the exact
+// term for every u the hash can give (2^24 values, checked by
+// tests/c/calib_gumbel.hip: the largest difference is 2^-19).
+#define ZS_GUMBEL_EPS 0x1p-16f
+__device__ __forceinline__ float zs_gumbel_fast(float u) {
+    const float w = -(__builtin_amdgcn_logf(u) * 0.693147180559945309f);
+    return -(__builtin_amdgcn_logf(w) * 0.693147180559945309f);
+}
+// Largest distance between an approximate Gumbel value a = RN(x/T) + g~ and
+// its exact b (both rounded sums): the term's error plus an ulp each way.
+__device__ __forceinline__ float zs_gumbel_band(float a) { return ZS_GUMBEL_EPS + fabsf(a) * 0x1p-22f; }
+__device__ __forceinline__ float zs_gumbel_exact(float x, float inv_t, uint32_t sd, uint32_t i) {
+    const float u = zs_rand01(sd, i);
+    const float g = -zs_log_cr(-zs_log_cr(u));
+    float v = x * inv_t;
+    return v + g;
+}
+
+// BARGMAX (shaders.rs:761-789): one workgroup per row.
+__global__ __launch_bounds__(LN_NT) void zs_k_bargmax(const float* logits, uint32_t V, uint64_t ld, uint32_t* out) {
     __shared__ unsigned long long sh[LN_NT / 64];
     const uint32_t r = blockIdx.x;
     const float* row = logits + (size_t)r * ld;
-    bool greedy = true;
-    float inv_t = 1.0f;
-    uint32_t sd = 0;
-    if (temp) {
-        float ts = temp[r];
-        greedy = ts <= 0.0f;
-        inv_t = greedy ? 1.0f : 1.0f / ts;
-        sd = seed[r];
-    }
     unsigned long long best = 0;
     for (uint32_t i0 = threadIdx.x * 4; i0 < V; i0 += LN_NT * 4) {
         float4 v4 = *reinterpret_cast<const float4*>(row + i0);
         float vv[4] = {v4.x, v4.y, v4.z, v4.w};
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-            uint32_t i = i0 + q;
+            const uint32_t i = i0 + q;
             if (i >= V) continue;
-            float v = vv[q];
-            if (!greedy) {
-                float u = zs_rand01(sd, i);
-                float g = -zs_log_cr(-zs_log_cr(u));
-                v = v * inv_t;
-                v = v + g;
-            }
-            unsigned long long k = wg_key(v, i);
+            const unsigned long long k = wg_key(vv[q], i);
             best = k > best ? k : best;
         }
     }
     best = block_max_u64(best, sh);
     if (threadIdx.x == 0) out[r] = best ? wg_key_idx(best) : 0u;
+}
+
+// BSAMPLE (shaders.rs:796-850; rows with temperature <= 0 take the argmax)
+// over segments of BS_SEG ids, one workgroup each (rows x segments fill the
+// GPU). Two steps: every id's value with the fast Gumbel term, then the exact
+// values (correctly rounded logs) only for the ids whose fast value lies
+// within two bands of the segment's fast maximum -- the row's exact winner is
+// among them, any other id being strictly below it. The segment's best exact
+// key is merged into keys[row] with a 64-bit atomic max; zs_k_bsample_fin
+// turns the keys into ids and clears them for the next call.
+#define BS_NT 256
+#define BS_SEG (BS_NT * 32)
+__global__ __launch_bounds__(BS_NT) void zs_k_bsample(const float* logits, uint32_t V, uint64_t ld, const float* temp,
+                                                      const uint32_t* seed, const uint32_t* ih,
+                                                      unsigned long long* keys) {
+    __shared__ unsigned long long shk[BS_NT / 64];
+    __shared__ float shf[BS_NT / 64];
+    const uint32_t r = blockIdx.y;
+    const uint32_t s0 = blockIdx.x * BS_SEG, s1 = min(s0 + BS_SEG, V);
+    const float* row = logits + (size_t)r * ld;
+    const float ts = temp[r];
+    const bool greedy = ts <= 0.0f;
+    const float inv_t = greedy ? 1.0f : 1.0f / ts;
+    const uint32_t sd = seed[r];
+    const uint32_t last4 = (V - 1) & ~3u;
+    unsigned long long best = 0;
+    // exact keys of the thread's ids of the segment (greedy rows; threads
+    // whose fast values cannot decide)
+    auto exact_all = [&]() {
+        for (uint32_t i0 = s0 + threadIdx.x * 4; i0 < s1; i0 += BS_NT * 4) {
+            const float4 v4 = *reinterpret_cast<const float4*>(row + min(i0, last4));
+            const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const uint32_t i = i0 + q;
+                if (i >= s1) continue;
+                const float v = greedy ? vv[q] : zs_gumbel_exact(vv[q], inv_t, sd, i);
+                const unsigned long long k = wg_key(v, i);
+                best = k > best ? k : best;
+            }
+        }
+    };
+    if (greedy) {
+        exact_all();
+    } else {
+        float ba = -INFINITY, bb = -INFINITY, bx = 0.0f;
+        uint32_t bi = 0;
+        bool exact = false;
+        for (uint32_t i0 = s0 + threadIdx.x * 4; i0 < s1; i0 += BS_NT * 16) {
+            float4 v4[4];
+            uint4 h4[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const uint32_t j = min(i0 + (uint32_t)u * BS_NT * 4, last4);
+                v4[u] = *reinterpret_cast<const float4*>(row + j);
+                h4[u] = *reinterpret_cast<const uint4*>(ih + j);
+            }
+            float va[16], xs[16];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const float vv[4] = {v4[u].x, v4[u].y, v4[u].z, v4[u].w};
+                const uint32_t hh[4] = {h4[u].x, h4[u].y, h4[u].z, h4[u].w};
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const uint32_t i = i0 + (uint32_t)u * BS_NT * 4 + q;
+                    xs[4 * u + q] = i < s1 ? vv[q] : -INFINITY;
+                    const float v = xs[4 * u + q] * inv_t;
+                    va[4 * u + q] = v + zs_gumbel_fast(zs_rand01_h(sd, hh[q]));
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const float a = va[e];
+                const bool fin = fabsf(a) < 1e29f;
+                exact = exact | ((!fin) & (a == a) & (a != -INFINITY));   // -inf and NaN never win
+                const float vf = fin ? a : -INFINITY;
+                const bool gt = vf > ba;
+                bb = fmaxf(bb, fminf(vf, ba));
+                bx = gt ? xs[e] : bx;
+                bi = gt ? i0 + (uint32_t)(e >> 2) * BS_NT * 4 + (uint32_t)(e & 3) : bi;
+                ba = fmaxf(ba, vf);
+            }
+        }
+        const bool near = bb > -INFINITY && ba - bb <= 2.0f * zs_gumbel_band(fmaxf(fabsf(ba), fabsf(bb)));
+        float m = ba;
+        for (int d = 32; d > 0; d >>= 1) m = fmaxf(m, __shfl_xor(m, d, 64));
+        if (zs_lane() == 0) shf[zs_wid()] = m;
+        __syncthreads();
+        m = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < BS_NT / 64; w++) m = fmaxf(m, shf[w]);
+        const bool cand = exact || (ba > -INFINITY && ba >= m - 2.0f * zs_gumbel_band(fmaxf(fabsf(m), fabsf(ba))));
+        if (cand) {
+            if (exact || near) exact_all();   // rare
+            else best = wg_key(zs_gumbel_exact(bx, inv_t, sd, bi), bi);
+        }
+    }
+    for (int d = 32; d > 0; d >>= 1) {
+        const unsigned long long o = __shfl_xor(best, d, 64);
+        best = o > best ? o : best;
+    }
+    if (zs_lane() == 0) shk[zs_wid()] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long b = 0;
+#pragma unroll
+        for (int w = 0; w < BS_NT / 64; w++) b = shk[w] > b ? shk[w] : b;
+        if (b) atomicMax(&keys[r], b);
+    }
+}
+__global__ void zs_k_bsample_fin(unsigned long long* keys, uint32_t B, uint32_t* out) {
+    const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= B) return;
+    const unsigned long long k = keys[r];
+    out[r] = k ? wg_key_idx(k) : 0u;
+    keys[r] = 0ull;
 }
 
 // BTOPK (shaders.rs:859-905): the K largest (value desc, id asc) among values in
@@ -474,9 +641,18 @@ __global__ __launch_bounds__(64 * TM_ROWS) void zs_k_sample_topk64(const float* 
     if (lane == 0) out[r] = res;
 }
 
+// ih: zs_lane_hash_fill of at least round_up(V, 4) ids; keys: B zeroed u64
+// (left zeroed) -- both used when temp is set
 extern "C" int zs_lane_argmax_launch(const float* logits, uint32_t B, uint32_t V, uint64_t ld, const float* temp,
-                                     const uint32_t* seed, uint32_t* out, hipStream_t stream) {
-    hipLaunchKernelGGL(zs_k_bargmax, dim3(B), dim3(LN_NT), 0, stream, logits, V, ld, temp, seed, out);
+                                     const uint32_t* seed, const uint32_t* ih, unsigned long long* keys,
+                                     uint32_t* out, hipStream_t stream) {
+    if (temp) {
+        hipLaunchKernelGGL(zs_k_bsample, dim3((V + BS_SEG - 1) / BS_SEG, B), dim3(BS_NT), 0, stream, logits, V, ld,
+                           temp, seed, ih, keys);
+        hipLaunchKernelGGL(zs_k_bsample_fin, dim3((B + 255) / 256), dim3(256), 0, stream, keys, B, out);
+        return hipGetLastError() == hipSuccess ? 0 : -1;
+    }
+    hipLaunchKernelGGL(zs_k_bargmax, dim3(B), dim3(LN_NT), 0, stream, logits, V, ld, out);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 // ck / cn: scratch of at least B * ceil(V / 8192) * 64 keys and B * ceil(V / 8192)
