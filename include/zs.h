@@ -85,9 +85,20 @@ int zs_dfa_advance(const zs_dfa* dfa, const zs_vocab* vocab, uint32_t state, uin
  * packed allow bitset d_out_bits[r*words + w] (bit i of word w = id 32w+i is
  * allowed, words = ceil(V/32)), with the EOS rule applied: eos is allowed iff
  * is_accept(state) or no table token is viable. Ids >= ntab other than eos
- * are disallowed. d_any (optional, uint32[B]) receives any(allowed). */
+ * are disallowed. d_any (optional, uint32[B]) receives any(allowed).
+ * Like the reference's per-state cache (logit_fsm.rs:166-182, the HashMap
+ * that allowed_mask fills), the DFA keeps a device memo of walked bitsets per
+ * state for the last (vocab, V) pair used with it: a row whose state was
+ * walked by an earlier call copies the stored bitset, and rows sharing a state
+ * in one call share one walk. Calls on one DFA must be ordered on one stream
+ * (or synchronised); two calls that overlap on different streams with
+ * different vocabularies or V race on the memo. */
 int zs_dfa_mask(zs_ctx* ctx, const zs_dfa* dfa, const zs_vocab* vocab, const int32_t* d_states,
                 uint32_t B, uint32_t V, uint32_t* d_out_bits, uint32_t* d_any, void* stream);
+/* Drops every memoised bitset of the DFA (host only, no GPU work): the next
+ * zs_dfa_mask walks all its rows. The reference has no call for this (its
+ * cache lives as long as the engine); it is for timing the walk. */
+void zs_dfa_memo_clear(zs_dfa* dfa);
 
 /* ---- grammar compilers (host only: no context, no GPU) -----------------
  * Replace regex-automata's dense::Builder (logit_fsm.rs:62-88: anchored start,

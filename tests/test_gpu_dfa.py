@@ -251,3 +251,61 @@ def test_viability_flags_across_kernel_paths():
     bits_big2 = dfa.mask(table, torch.ones(1100, dtype=torch.int32, device="cuda"), V)
     torch.cuda.synchronize()
     assert np.array_equal(bits_big2.cpu().numpy().view(np.uint32)[7], want1)
+
+
+def test_memo_hits_equal_fresh_walks():
+    """The per-state memo (logit_fsm.rs:166-182's cache): masks served from it
+    are bit-identical, with the same viability flags and EOS rule, to the
+    masks of a DFA with an empty memo; rows that share a state in one call
+    share one walk; another vocabulary or V invalidates the memo."""
+    from tests.gpu_util import ctx
+    from zllm_amd.engine import ByteDfa, TokenByteTable
+    S, V = 512, 20000
+    print(f"[case] memo json S={S} V={V}", flush=True)
+    c = ctx()
+    trans, dead, acc = synth.json_dfa(S, 41)
+    offs, data = synth.grammar_vocab(trans, dead, V, 42)
+    valid = np.ones(V, np.uint8)
+    valid[3::89] = 0
+    table = TokenByteTable.from_csr(c, offs, data, valid, V - 1)
+    offs2, data2 = synth.grammar_vocab(trans, dead, V, 43)
+    table2 = TokenByteTable.from_csr(c, offs2, data2, np.ones(V, np.uint8), V - 1)
+    dfa = ByteDfa(c, trans, dead, acc)
+    rng = np.random.default_rng(44)
+    good = np.nonzero(dead == 0)[0]
+    pool = rng.choice(good, 40, replace=False)
+
+    def run(d, tab, states, v):
+        st = torch.tensor(np.asarray(states, np.int32), device="cuda")
+        anyv = torch.zeros(len(states), dtype=torch.int32, device="cuda")
+        bits = d.mask(tab, st, v, any_out=anyv)
+        torch.cuda.synchronize()
+        return bits.cpu().numpy().view(np.uint32).copy(), anyv.cpu().numpy().copy()
+
+    def fresh(tab, states, v):
+        return run(ByteDfa(c, trans, dead, acc), tab, states, v)
+
+    def same(got, want, what):
+        assert np.array_equal(got[0], want[0]), what
+        assert np.array_equal(got[1], want[1]), what
+
+    # cold: repeated states in one call, the dead state, a free row
+    s1 = [int(x) for x in pool[:20]] + [int(pool[0]), int(pool[3]), int(pool[3]), 0, -1]
+    first = run(dfa, table, s1, V)
+    tokens = [None if not valid[t] else bytes(data[offs[t]:offs[t + 1]]) for t in range(V)]
+    od, ov = O.Dfa(trans, dead, acc), O.Vocab(tokens, V - 1)
+    for i in (0, 3, 20, 21, 22, 23):
+        assert np.array_equal(first[0][i], O.mask_bits(V, dfa=od, vocab=ov, state=s1[i])), i
+    same(first, fresh(table, s1, V), "cold call")
+    # all hits, twice; then a smaller call mixing hits and new states
+    same(run(dfa, table, s1, V), first, "all hits")
+    same(run(dfa, table, s1[::-1], V), (first[0][::-1], first[1][::-1]), "all hits, reversed")
+    s2 = [int(x) for x in pool[15:35]] + [-1, int(pool[16])]
+    same(run(dfa, table, s2, V), fresh(table, s2, V), "hits and misses")
+    # another vocabulary, another V, then back: never a stale slot
+    same(run(dfa, table2, s1, V), fresh(table2, s1, V), "other vocabulary")
+    same(run(dfa, table, s1, V - 37), fresh(table, s1, V - 37), "other V")
+    same(run(dfa, table, s1, V), first, "back to the first pair")
+    # cleared memo: every row walked again
+    dfa.memo_clear()
+    same(run(dfa, table, s2, V), fresh(table, s2, V), "after memo_clear")

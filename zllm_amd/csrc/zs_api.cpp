@@ -215,6 +215,7 @@ extern "C" int zs_vocab_create(zs_ctx* ctx, const uint32_t* h_offsets, const uin
     v->ctx = ctx;
     v->ntab = ntab;
     v->eos = eos;
+    v->serial = ++ctx->vocab_serial;
     v->nbytes = h_offsets[ntab] - h_offsets[0];
     v->h_offsets = (uint32_t*)malloc(sizeof(uint32_t) * (ntab + 1));
     v->h_bytes = (uint8_t*)malloc(v->nbytes + 1);
@@ -293,6 +294,9 @@ extern "C" void zs_dfa_destroy(zs_dfa* d) {
     (void)hipFree(d->d_packed);
     (void)hipFree(d->d_clsinfo);
     (void)hipFree(d->d_remap);
+    (void)hipFree(d->d_memo);
+    (void)hipFree(d->d_memo_key);
+    (void)hipFree(d->d_memo_any);
     free(d->h_trans);
     free(d->h_dead);
     free(d->h_accept);
@@ -459,6 +463,16 @@ extern "C" int zs_dfa_create(zs_ctx* ctx, const uint32_t* h_trans, uint32_t nsta
     if (!rc) rc = zs_alloc(ctx, &d->d_packed, packed.size());
     if (!rc) rc = zs_alloc(ctx, &d->d_clsinfo, 256);
     if (!rc) rc = zs_alloc(ctx, &d->d_remap, nstates);
+    // the memo: one slot of ceil(max_vocab / 32) words per good state, up to
+    // ZS_DFA_MEMO_BYTES (states past the cap are walked on every call)
+    d->memo_words = (ctx->max_vocab + 31) / 32;
+    d->memo_slots = (uint32_t)std::min<uint64_t>(ngood, ZS_DFA_MEMO_BYTES / ((uint64_t)d->memo_words * 4));
+    d->memo_tag = 1;   // the keys start at 0: tag 0 is never used
+    if (!rc && d->memo_slots) rc = zs_alloc(ctx, &d->d_memo, (size_t)d->memo_slots * d->memo_words);
+    if (!rc && d->memo_slots) rc = zs_alloc(ctx, &d->d_memo_key, d->memo_slots);
+    if (!rc && d->memo_slots) rc = zs_alloc(ctx, &d->d_memo_any, d->memo_slots);
+    if (!rc && d->memo_slots && hipMemset(d->d_memo_key, 0, (size_t)d->memo_slots * 8) != hipSuccess)
+        rc = zs_set_error(ctx, ZS_EHIP, "zs_dfa_create: memo clear failed");
     if (!rc) {
         d->packed_words = (uint32_t)packed.size();
         hipError_t e = hipMemcpy(d->d_packed, packed.data(), packed.size() * 4, hipMemcpyHostToDevice);
@@ -503,6 +517,17 @@ extern "C" int zs_dfa_advance(const zs_dfa* d, const zs_vocab* v, uint32_t state
     return ZS_OK;
 }
 
+extern "C" void zs_dfa_memo_clear(zs_dfa* dfa) {
+    if (!dfa) return;
+    // a slot is valid only while its word equals the tag; the words are
+    // zeroed at creation, so tag 0 is skipped (after 2^32 - 1 clears a slot
+    // could hold a stale tag: the memo is then dropped for this DFA)
+    if (++dfa->memo_tag == 0) {
+        dfa->memo_tag = 1;
+        dfa->memo_slots = 0;
+    }
+}
+
 extern "C" int zs_dfa_mask(zs_ctx* ctx, const zs_dfa* dfa, const zs_vocab* vocab, const int32_t* d_states,
                            uint32_t B, uint32_t V, uint32_t* d_out_bits, uint32_t* d_any, void* stream) {
     if (!ctx || !dfa || !vocab || !d_states || !d_out_bits)
@@ -541,6 +566,20 @@ extern "C" int zs_dfa_mask(zs_ctx* ctx, const zs_dfa* dfa, const zs_vocab* vocab
     a.words = (V + 31) / 32;
     a.out = d_out_bits;
     const bool packed = dfa->packed_lds != 0 && B <= ZS_DFA_MAXROWS;
+    // the memo holds masks of one (vocabulary, V): another pair invalidates it
+    if (dfa->memo_serial != vocab->serial || dfa->memo_V != V) {
+        dfa->memo_serial = vocab->serial;
+        dfa->memo_V = V;
+        zs_dfa_memo_clear(const_cast<zs_dfa*>(dfa));
+    }
+    a.memo = dfa->d_memo;
+    a.memo_key = dfa->d_memo_key;
+    a.memo_any = dfa->d_memo_any;
+    a.memo_seq = ++dfa->memo_seq;
+    a.memo_slots = V <= ctx->max_vocab ? dfa->memo_slots : 0u;
+    a.memo_words = dfa->memo_words;
+    a.memo_tag = dfa->memo_tag;
+    a.rg = 0;   // the kernel's default group size
     // Viability flags: the context's flags hold the epoch of the call that
     // found a viable token, on both kernel paths (no clearing pass, and a flag
     // left by an earlier call on the other path never reads as viable); the

@@ -106,31 +106,59 @@ __global__ __launch_bounds__(DM_NT) void zs_k_dfa_mask(dm_args a) {
 }
 
 // Persistent walk over the bit-packed table (good states only, `bits`-bit
-// entries, all ones = fail). One workgroup per CU stages the table in LDS once
-// and then takes items: a tile of ZS_WALK_TILE ids times a group of DL_RG
-// constrained rows. A thread walks DL_TPT tokens, each through all rows of the
-// group at once: the byte and its class are read once per step and the rows'
-// states advance side by side. Inside a tile the tokens come in length order
-// (the vocabulary's walk order), so the lanes of a wave walk tokens of nearly
-// equal length; allowed ids are set in an LDS bitmap of the tile and written
-// out as whole words. A step costs one LDS class read and one 64-bit LDS
-// table read per row.
+// entries, all ones = fail), with the per-state memo. One workgroup per CU
+// stages the table in LDS once and plans the call (every workgroup builds the
+// same plan): each constrained row is either a memo hit (its state's slot is
+// valid) or a walk, and rows sharing a state share one walk, whose result
+// goes to all of them and to the state's memo slot. The walks are taken as
+// items: a tile of ZS_WALK_TILE ids times a group of up to rg (<= 32)
+// distinct states. Per item the workgroup first tabulates, for every byte,
+// which of the item's states survive that byte as a first byte (one bit per
+// state); a token reads its first byte's word and walks its remaining bytes
+// only from the states whose bits are set, which is a small fraction of the
+// pairs. Inside a tile the tokens come in length order (the vocabulary's walk
+// order), so the lanes of a wave walk tokens of nearly equal length; allowed
+// ids are set in an LDS bitmap of the tile and written out as whole words.
+// Memo hits and unconstrained rows are written last, their words split over
+// the workgroups.
 #define DL_NT 1024
 #define DL_TPT (ZS_WALK_TILE / DL_NT)
-#define DL_RG 8                  // rows walked together
-#define DL_TW (ZS_WALK_TILE / 32) // bitmap words per row and tile
+#define DL_RG 32                  // distinct states per item (bits of a first-byte word)
+#define DL_TW (ZS_WALK_TILE / 32) // bitmap words per state and tile
+#define DL_SIDE 4                 // surviving states walked side by side
+#define DL_FREE 0xffffu           // row modes: unconstrained
+#define DL_WALKED 0xfffeu         //            walked in this call (else: its memo slot)
+
+// Workgroup barrier that orders LDS accesses only (__syncthreads() would also
+// wait for the next item's token loads, issued ahead on purpose)
+__device__ __forceinline__ void dl_bar() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 #define DL_WORDS (ZS_DFA_LDS_BYTES / 4)
 #define DL_MAXROWS ZS_DFA_MAXROWS
+#define DL_HASH (2 * DL_MAXROWS)  // plan hash table (state -> first row)
+static_assert(DL_HASH <= DL_RG * DL_TW, "the plan's hash table lives in the bitmap");
+static_assert(DL_MAXROWS <= DL_NT, "one row per thread in the plan");
+
+__device__ __forceinline__ uint32_t dl_hash(uint32_t g) { return (g * 2654435761u) >> (32 - 11); }
+static_assert(DL_HASH == 2048, "dl_hash yields 11 bits");
+
 template <bool SPARSE>
 __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
     __shared__ uint32_t tab[DL_WORDS];
     __shared__ uint16_t ci[256];
-    __shared__ uint32_t bm[DL_RG][DL_TW];
-    __shared__ uint16_t crow[DL_MAXROWS];  // constrained rows
-    __shared__ uint16_t cst[DL_MAXROWS];   // their good start state (0xffff: none allowed)
-    __shared__ uint16_t frow[DL_MAXROWS];  // unconstrained rows
-    __shared__ uint32_t ncr, nfr;
+    __shared__ uint32_t bm[DL_RG][DL_TW];   // the plan's hash table first
+    __shared__ uint32_t fb[256];            // per byte: the item's states alive after it
+    __shared__ uint32_t wl[DL_MAXROWS];     // walks: good state << 16 | first row
+    __shared__ uint32_t link[DL_MAXROWS];   // row -> next row of its state (0xffff: end)
+    __shared__ uint32_t s0r[DL_RG];         // the item's start states (packed ids)
+    __shared__ uint16_t rmode[DL_MAXROWS];  // row: memo slot (hit), DL_WALKED or DL_FREE
+    __shared__ uint32_t nwl;
     const int t = threadIdx.x;
+    const uint32_t r = (uint32_t)t;
+    const int32_t st = r < a.B ? a.states[r] : -1;   // issued before the table loads
     // stage the table with many 16-byte loads in flight per thread
     const uint32_t nq = a.packed_words / 4;  // the table is allocated in whole quads
     const uint4* src = reinterpret_cast<const uint4*>(a.packed);
@@ -145,129 +173,228 @@ __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
     }
     for (uint32_t q = q0 + t; q < nq; q += DL_NT) dst[q] = src[q];
     for (int i = t; i < 256; i += DL_NT) ci[i] = a.clsinfo[i];
-    if (t == 0) ncr = nfr = 0;
+    // ---- plan: row t (B <= DL_MAXROWS <= DL_NT)
+    uint32_t* hs = &bm[0][0];
+    for (int i = t; i < DL_HASH; i += DL_NT) hs[i] = 0xffffffffu;
+    if (t < DL_MAXROWS) link[t] = 0xffffu;
+    if (t == 0) nwl = 0;
+    const uint32_t g = st >= 0 ? a.remap[st] : 0xffffu;   // 0xffff: allows nothing
+    // a hit needs this tag; the key also names the call that filled the slot
+    // (never this one: keys are written by the EOS kernel after the walk, so
+    // every workgroup builds the same plan)
+    const unsigned long long key = g < a.memo_slots ? a.memo_key[g] : 0ull;
+    const bool hit = st >= 0 && g < a.memo_slots && (uint32_t)(key >> 32) == a.memo_tag && (uint32_t)key != a.memo_seq;
+    const bool walk = st >= 0 && !hit;
+    if (t < DL_MAXROWS) rmode[t] = st < 0 ? DL_FREE : (hit ? (uint16_t)g : DL_WALKED);
     __syncthreads();
-    // constrained and unconstrained rows in order (every workgroup builds the
-    // same lists)
-    for (uint32_t r0 = 0; r0 < a.B; r0 += DL_NT) {
-        const uint32_t r = r0 + t;
-        const int32_t st = r < a.B ? a.states[r] : 0;
-        const bool c = r < a.B && st >= 0, f = r < a.B && st < 0;
-        uint32_t tot;
-        const uint32_t pos = block_excl_scan_u<DL_NT>(c ? 1u : 0u, reinterpret_cast<uint32_t*>(bm), &tot);
-        if (c) {
-            crow[ncr + pos] = (uint16_t)r;
-            cst[ncr + pos] = a.remap[st];
+    // the first row of every walked state: insert g << 16 | row, keep the least
+    uint32_t hpos = 0;
+    if (walk) {
+        const uint32_t hk = g << 16 | r;
+        hpos = dl_hash(g);
+        while (true) {
+            const uint32_t old = atomicCAS(&hs[hpos], 0xffffffffu, hk);
+            if (old == 0xffffffffu || (old >> 16) == g) {
+                if (old != 0xffffffffu) atomicMin(&hs[hpos], hk);
+                break;
+            }
+            hpos = (hpos + 1) & (DL_HASH - 1);
         }
-        uint32_t ftot;
-        const uint32_t fpos = block_excl_scan_u<DL_NT>(f ? 1u : 0u, reinterpret_cast<uint32_t*>(bm), &ftot);
-        if (f) frow[nfr + fpos] = (uint16_t)r;
-        __syncthreads();
-        if (t == 0) { ncr += tot; nfr += ftot; }
-        __syncthreads();
     }
-    const uint32_t nc = ncr;
+    __syncthreads();
+    const uint32_t first = walk ? (hs[hpos] & 0xffffu) : 0u;
+    const bool lead = walk && first == r;
+    // the other rows of the state chain behind the first one
+    if (walk && !lead) link[r] = atomicExch(&link[first], r);
+    {
+        uint32_t tot;
+        const uint32_t pos = block_excl_scan_u<DL_NT>(lead ? 1u : 0u, fb, &tot);
+        if (lead) wl[pos] = g << 16 | r;
+        if (t == 0) nwl = tot;
+    }
+    for (int i = t; i < DL_RG * DL_TW; i += DL_NT) (&bm[0][0])[i] = 0;
+    __syncthreads();
+    const uint32_t nc = nwl;
     const uint32_t rwb = a.rw >> 3;  // bytes per state row (whole words)
     const uint32_t fmask = (1u << a.bits) - 1u;
     // entry of class bit offset cb in row st: the 32 bits from bit cb & 31 of
     // the two words from byte st * rwb + cbw, cbw = the byte offset of the word
-    // holding bit cb (computed once per byte, shared by the rows)
+    // holding bit cb
     const uint16_t* tgt16 = reinterpret_cast<const uint16_t*>(tab + 4 * (a.ngood + 1));
-    auto step = [&](uint32_t st, uint32_t cb, uint32_t cbw) -> uint32_t {
+    auto step = [&](uint32_t s, uint32_t cb) -> uint32_t {
         if (SPARSE) {
             // class mask of the state, then the target at the rank of its class
-            const uint4 rec = reinterpret_cast<const uint4*>(tab)[st];
+            const uint4 rec = reinterpret_cast<const uint4*>(tab)[s];
             const unsigned long long mask = ((unsigned long long)rec.y << 32) | rec.x;
             if (!((mask >> cb) & 1ull)) return a.ngood;
             return tgt16[rec.z + (uint32_t)__popcll(mask & ((1ull << cb) - 1ull))];
         }
         // states < 2^16, row bytes < 2^13: the byte address fits 24 bits
-        const uint32_t ba = __umul24(st, rwb) + cbw;
+        const uint32_t ba = __umul24(s, rwb) + ((cb >> 3) & ~3u);
         const uint32_t* w = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint8_t*>(tab) + ba);
         return __builtin_amdgcn_alignbit(w[1], w[0], cb) & fmask;
     };
     const uint32_t fail = a.ngood;  // the sink row
     const uint32_t ncover = a.V > a.ntab ? a.V : a.ntab;
-    const uint32_t ntt = (ncover + ZS_WALK_TILE - 1) / ZS_WALK_TILE, nrg = (nc + DL_RG - 1) / DL_RG;
-    for (uint32_t w = blockIdx.x; w < ntt * nrg; w += gridDim.x) {
-        const uint32_t tt = w % ntt, g0 = (w / ntt) * DL_RG;
-        const uint32_t nr = min((uint32_t)DL_RG, nc - g0);
-        const uint32_t tok0 = tt * ZS_WALK_TILE;
-        for (int i = t; i < DL_RG * DL_TW; i += DL_NT) (&bm[0][0])[i] = 0;
-        uint32_t s0[DL_RG];
+    const uint32_t rg = a.rg;
+    const uint32_t ntt = (ncover + ZS_WALK_TILE - 1) / ZS_WALK_TILE, nrg = (nc + rg - 1) / rg;
+    static_assert(DL_TPT == 2 && ZS_WALK_TILE == 2048 && DL_NT == 1024, "run pairing");
+    // the thread's two slots of an item's tile: runs of 64 length-sorted
+    // slots, wave w takes runs w and 31 - w (a short and a long run)
+    const uint32_t wv = (uint32_t)t >> 6;
+    const uint32_t sl_off[2] = {wv * 64 + (uint32_t)zs_lane(), (31u - wv) * 64 + (uint32_t)zs_lane()};
+    auto fetch = [&](uint32_t w, uint32_t (&meta)[2], uint4 (&wb)[2]) {
+        const uint32_t tt = w % ntt;
 #pragma unroll
-        for (int rr = 0; rr < DL_RG; rr++) {
-            const uint32_t g = (uint32_t)rr < nr ? cst[g0 + rr] : 0xffffu;
-            s0[rr] = g == 0xffffu ? fail : g;
+        for (int j = 0; j < 2; j++) {
+            const bool ok = w < ntt * nrg && tt < a.nwtile;
+            const uint32_t sl = tt * ZS_WALK_TILE + sl_off[j];
+            meta[j] = ok ? a.wmeta[sl] : 0xffffffffu;
+            wb[j] = ok ? reinterpret_cast<const uint4*>(a.wbytes)[sl] : make_uint4(0, 0, 0, 0);
         }
-        __syncthreads();
+    };
+    uint32_t meta[2];
+    uint4 wb[2];
+    fetch(blockIdx.x, meta, wb);
+    for (uint32_t w = blockIdx.x; w < ntt * nrg; w += gridDim.x) {
+        const uint32_t tt = w % ntt, g0 = (w / ntt) * rg;
+        const uint32_t nr = min(rg, nc - g0);
+        const uint32_t tok0 = tt * ZS_WALK_TILE;
+        // the item's start states, then the first-byte words: thread t takes
+        // byte t & 255 for the states 8 * (t >> 8) .. + 7
+        if (t < DL_RG) {
+            const uint32_t gg = (uint32_t)t < nr ? wl[g0 + t] >> 16 : 0xffffu;
+            s0r[t] = gg == 0xffffu ? fail : gg;
+        }
+        dl_bar();
+        {
+            const uint32_t b = (uint32_t)t & 255u, q = (uint32_t)t >> 8;
+            const uint32_t cb = ci[b];
+            uint32_t m = 0;
 #pragma unroll
-        for (int j = 0; j < DL_TPT; j++) {
-            // runs of 64 length-sorted slots: wave w takes runs w and 31 - w, so
-            // its lanes walk tokens of nearly one length and every wave gets a
-            // short and a long run (the item waits for its slowest wave)
-            static_assert(DL_TPT == 2 && ZS_WALK_TILE == 2048 && DL_NT == 1024, "run pairing");
-            const uint32_t wv = (uint32_t)t >> 6;
-            const uint32_t run = j == 0 ? wv : 31u - wv;
-            const uint32_t slot = tok0 + run * 64 + (uint32_t)zs_lane();
-            if (tt >= a.nwtile) break;
-            const uint32_t meta = a.wmeta[slot];
-            const uint4 wb = reinterpret_cast<const uint4*>(a.wbytes)[slot];  // issued with meta
-            if (meta == 0xffffffffu) continue;
-            const uint32_t id = meta & 0x3ffffu, L = meta >> 18;
-            if (L == 0) continue;  // no bytes or not a token: never allowed
-            const uint32_t bw[4] = {wb.x, wb.y, wb.z, wb.w};
-            uint32_t s[DL_RG];
-#pragma unroll
-            for (int rr = 0; rr < DL_RG; rr++) s[rr] = s0[rr];
-            // failed walks sit in the sink row: every row steps unconditionally
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                if ((uint32_t)i >= L) break;
-                const uint32_t cb = ci[(bw[i >> 2] >> (8 * (i & 3))) & 0xffu];
-                const uint32_t cbw = (cb >> 3) & ~3u;
-#pragma unroll
-                for (int rr = 0; rr < DL_RG; rr++) s[rr] = step(s[rr], cb, cbw);
+            for (uint32_t k = 0; k < 8; k++) {
+                const uint32_t rr = q * 8 + k;
+                if (rr < nr && step(s0r[rr], cb) != fail) m |= 1u << k;
             }
-            if (L > 16) {
-                // bytes past the first 16 from the CSR copy (long tokens)
-                const uint32_t o0 = a.offsets[id], o1 = a.offsets[id + 1];
-                for (uint32_t i = o0 + 16; i < o1; i++) {
-                    const uint32_t cb = ci[a.bytes[i]];
-                    const uint32_t cbw = (cb >> 3) & ~3u;
+            reinterpret_cast<uint8_t*>(fb)[b * 4 + q] = (uint8_t)m;
+        }
+        // this item's tokens (fetched during the previous item), the next
+        // item's fetched now
+        uint32_t cm[2] = {meta[0], meta[1]};
+        uint4 cw[2] = {wb[0], wb[1]};
+        fetch(w + gridDim.x, meta, wb);
+        dl_bar();
+        // both tokens' surviving states, DL_SIDE of each token at a time,
+        // walked side by side (independent chains hide the LDS latency)
+        uint32_t L[2], m[2], id[2], cb0[2];
 #pragma unroll
-                    for (int rr = 0; rr < DL_RG; rr++) s[rr] = step(s[rr], cb, cbw);
+        for (int j = 0; j < 2; j++) {
+            L[j] = cm[j] == 0xffffffffu ? 0u : cm[j] >> 18;   // 0: never allowed
+            id[j] = cm[j] & 0x3ffffu;
+            m[j] = L[j] ? fb[cw[j].x & 0xffu] : 0u;           // most tokens end here
+            cb0[j] = ci[cw[j].x & 0xffu];
+        }
+        while (m[0] | m[1]) {
+            // up to DL_SIDE states of each token; the ones taken leave m
+            uint32_t sv[2][DL_SIDE], taken[2];
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                uint32_t mm = m[j];
+#pragma unroll
+                for (int k = 0; k < DL_SIDE; k++) {
+                    sv[j][k] = mm ? step(s0r[__builtin_ctz(mm)], cb0[j]) : fail;
+                    mm &= mm - 1u;
+                }
+                taken[j] = m[j] & ~mm;
+                m[j] = mm;
+            }
+            // the class of the next byte is read while the current step's
+            // table reads are in flight
+            uint32_t cb[2] = {ci[(cw[0].x >> 8) & 0xffu], ci[(cw[1].x >> 8) & 0xffu]};
+#pragma unroll
+            for (int i = 1; i < 16; i++) {
+                bool go[2];
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    bool live = false;
+#pragma unroll
+                    for (int k = 0; k < DL_SIDE; k++) live |= sv[j][k] != fail;
+                    go[j] = live && (uint32_t)i < L[j];
+                }
+                if (!go[0] && !go[1]) break;
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    if (!go[j]) continue;
+                    uint32_t cbn = 0;
+                    if (i < 15) {
+                        const int n = i + 1;
+                        const uint32_t bw = n < 4 ? cw[j].x : n < 8 ? cw[j].y : n < 12 ? cw[j].z : cw[j].w;
+                        cbn = ci[(bw >> (8 * (n & 3))) & 0xffu];
+                    }
+#pragma unroll
+                    for (int k = 0; k < DL_SIDE; k++) sv[j][k] = step(sv[j][k], cb[j]);
+                    cb[j] = cbn;
                 }
             }
-            const uint32_t off = id - tok0;
 #pragma unroll
-            for (int rr = 0; rr < DL_RG; rr++)
-                if (s[rr] != fail) atomicOr(&bm[rr][off >> 5], 1u << (off & 31));
+            for (int j = 0; j < 2; j++) {
+                bool live = false;
+#pragma unroll
+                for (int k = 0; k < DL_SIDE; k++) live |= sv[j][k] != fail;
+                if (L[j] > 16 && live) {
+                    // bytes past the first 16 from the CSR copy (long tokens)
+                    const uint32_t o0 = a.offsets[id[j]], o1 = a.offsets[id[j] + 1];
+                    for (uint32_t i = o0 + 16; i < o1; i++) {
+                        const uint32_t c = ci[a.bytes[i]];
+#pragma unroll
+                        for (int k = 0; k < DL_SIDE; k++) sv[j][k] = step(sv[j][k], c);
+                    }
+                }
+                const uint32_t off = id[j] - tok0;
+                uint32_t tk = taken[j];
+#pragma unroll
+                for (int k = 0; k < DL_SIDE; k++) {
+                    if (tk && sv[j][k] != fail) atomicOr(&bm[__builtin_ctz(tk)][off >> 5], 1u << (off & 31));
+                    tk &= tk - 1u;
+                }
+            }
         }
-        __syncthreads();
-        // whole words out; bits at ids >= V stay clear; viability counts every
-        // table id of the tile
+        dl_bar();
+        // whole words out to every row of the state and its memo slot (and
+        // cleared for the next item); bits at ids >= V stay clear; viability
+        // counts every table id of the tile
         for (int i = t; i < (int)(nr * DL_TW); i += DL_NT) {
             const uint32_t rr = i / DL_TW, wi = i % DL_TW;
-            const uint32_t r = crow[g0 + rr];
+            const uint32_t e = wl[g0 + rr];
+            const uint32_t gg = e >> 16;
             const uint32_t word = bm[rr][wi];
+            bm[rr][wi] = 0;
             const uint32_t gw = tok0 / 32 + wi;
-            if (gw < a.words) {
-                uint32_t v = word;
-                if (gw == a.words - 1 && (a.V & 31)) v &= (1u << (a.V & 31)) - 1u;
-                a.out[(size_t)r * a.words + gw] = v;
+            uint32_t v = word;
+            if (gw == a.words - 1 && (a.V & 31)) v &= (1u << (a.V & 31)) - 1u;
+            for (uint32_t rw = e & 0xffffu; rw != 0xffffu; rw = link[rw]) {
+                if (gw < a.words) a.out[(size_t)rw * a.words + gw] = v;
+                if (word) a.any[rw] = a.epoch;  // every writer stores the same value
             }
-            if (word) a.any[r] = a.epoch;  // every writer stores the same value
+            if (gg < a.memo_slots && gw < a.words) a.memo[(size_t)gg * a.memo_words + gw] = v;
         }
-        __syncthreads();
     }
-    // unconstrained rows: every id below V (the workgroups split the words)
-    const uint32_t nfw = nfr * a.words;
-    for (uint32_t i = blockIdx.x * DL_NT + t; i < nfw; i += gridDim.x * DL_NT) {
-        const uint32_t k = i / a.words, wi = i - k * a.words;
-        uint32_t v = 0xffffffffu;
-        if (wi == a.words - 1 && (a.V & 31)) v = (1u << (a.V & 31)) - 1u;
-        a.out[(size_t)frow[k] * a.words + wi] = v;
+    // memo hits and unconstrained rows (the workgroups split the rows' words)
+    const uint32_t nall = a.B * a.words;
+    for (uint32_t i = blockIdx.x * DL_NT + t; i < nall; i += gridDim.x * DL_NT) {
+        const uint32_t rr = i / a.words, wi = i - rr * a.words;
+        const uint32_t mode = rmode[rr];
+        if (mode == DL_WALKED) continue;
+        uint32_t v;
+        if (mode == DL_FREE) {
+            v = 0xffffffffu;
+            if (wi == a.words - 1 && (a.V & 31)) v = (1u << (a.V & 31)) - 1u;
+        } else {
+            // the stored walk and its viability (the EOS kernel follows)
+            v = a.memo[(size_t)mode * a.memo_words + wi];
+            if (wi == 0 && a.memo_any[mode]) a.any[rr] = a.epoch;
+        }
+        a.out[(size_t)rr * a.words + wi] = v;
     }
 }
 
@@ -287,6 +414,13 @@ __global__ void zs_k_dfa_eos(dm_args a) {
     if (st < 0) return;
     const bool anyv = a.epoch ? a.any[r] == a.epoch : a.any[r] != 0;
     if (a.epoch && a.any_user) a.any_user[r] = anyv ? 1u : 0u;
+    // the walk of this call is complete: the state's memo slot is valid from
+    // the next call on (rows of one state store the same values)
+    const uint32_t g = a.remap[st];
+    if (g < a.memo_slots) {
+        a.memo_any[g] = anyv ? 1u : 0u;
+        a.memo_key[g] = ((unsigned long long)a.memo_tag << 32) | a.memo_seq;
+    }
     if (a.eos >= a.V) return;
     bool ok = a.accept[st] || !anyv;
     uint32_t* o = a.out + (size_t)r * a.words + (a.eos >> 5);
@@ -299,8 +433,14 @@ extern "C" int zs_dfa_mask_launch(const dm_args& a, bool packed_lds, uint32_t nc
     dm_args x = a;
     x.any = any_scratch;
     uint32_t ncover = a.V > a.ntab ? a.V : a.ntab;
+    if (!packed_lds || a.B > DL_MAXROWS) x.memo_slots = 0;  // the memo is the packed walk's
     if (packed_lds && a.B <= DL_MAXROWS) {
-        const uint32_t items = ((ncover + ZS_WALK_TILE - 1) / ZS_WALK_TILE) * ((a.B + DL_RG - 1) / DL_RG);
+        // states per item: enough items to give every CU one when B rows are
+        // walked (B bounds the distinct states), at most DL_RG
+        const uint32_t ntt = (ncover + ZS_WALK_TILE - 1) / ZS_WALK_TILE;
+        if (x.rg == 0) x.rg = (a.B * ntt + ncu - 1) / ncu;
+        x.rg = x.rg < 1 ? 1 : (x.rg > DL_RG ? DL_RG : x.rg);
+        const uint32_t items = ntt * ((a.B + x.rg - 1) / x.rg);
         if (a.sparse)
             hipLaunchKernelGGL(zs_k_dfa_mask_packed<true>, dim3(min(items, ncu)), dim3(DL_NT), 0, stream, x);
         else

@@ -13,7 +13,8 @@
 // Largest vocabulary a context accepts (the row kernel's patch bitmap and
 // the per-row chunk records are sized for it).
 #define ZS_MAX_VOCAB 262144
-#define ZS_DFA_LDS_BYTES 152576  // packed DFA table budget in LDS (149 KB)
+#define ZS_DFA_LDS_BYTES 143360  // packed DFA table budget in LDS (140 KB)
+#define ZS_DFA_MEMO_BYTES (256ull << 20)  // per-DFA device memo of allow bitsets (cap)
 #define ZS_WALK_TILE 2048        // ids per tile of the vocab-parallel DFA walk
 #define ZS_DFA_MAXROWS 1024      // rows of the LDS-table DFA walk (constrained-row list in LDS)
 #define ZS_MAX_CHUNKS (ZS_MAX_VOCAB / ZS_P1_CH)
@@ -165,6 +166,7 @@ struct zs_ctx {
     uint32_t* pv;          // big-row probabilities (f32 bits) [rows][max_vocab]
     void* mask_scratch;    // DFA mask viability flags [rows]
     uint32_t mask_epoch;   // last epoch handed to the packed DFA mask
+    uint32_t vocab_serial; // serial number of the last zs_vocab created
     double* k_ap;                // [rows][max_subs] approximate sums of the kept list per sub-chunk
     zs_sub_sum* k_sum;           // [rows][2][max_subs] kept-list rounds (sum2, draw)
     zs_tp_bucket* tp_bk;         // [rows][ZS_TP_NB] top-p buckets (zs_k_tp_*)
@@ -207,6 +209,7 @@ struct zs_ctx {
 
 struct zs_vocab {
     zs_ctx* ctx;
+    uint32_t serial;       // unique per context: keys the DFA memo
     uint32_t ntab, eos, nbytes;
     uint32_t* d_offsets;   // [ntab+1]
     uint8_t* d_bytes;
@@ -251,6 +254,19 @@ struct zs_dfa {
     // d_packed = {mask lo, mask hi, first target, 0} per good state + sink,
     // then u16 targets; d_clsinfo = class index
     uint32_t sparse;
+    // memo of allow bitsets per good state (logit_fsm.rs:166-182's cache):
+    // slot g holds the walk's bitset for good state g (before the EOS rule)
+    // and d_memo_any[g] = a token is viable; it is valid when
+    // d_memo_key[g] == memo_tag << 32 | seq with seq not the current call's
+    // (the EOS kernel fills the key after the walk; a slot is used from the
+    // next call on, so every workgroup of a walk builds the same plan). The tag
+    // is bumped when the vocabulary or V changes (or on zs_dfa_memo_clear),
+    // which invalidates every slot at once.
+    uint32_t* d_memo;                 // [memo_slots][memo_words]
+    unsigned long long* d_memo_key;   // [memo_slots]
+    uint32_t* d_memo_any;             // [memo_slots]
+    uint32_t memo_slots, memo_words;
+    mutable uint32_t memo_tag, memo_seq, memo_serial, memo_V;
 };
 
 // Arguments of the DFA mask kernels (zs_dfa.hip).
@@ -282,6 +298,14 @@ struct dm_args {
     // the EOS kernel writes the caller's 0/1 flags (any_user, optional)
     uint32_t epoch;
     uint32_t* any_user;
+    // memo (packed path; memo_slots = 0 disables it): a constrained row whose
+    // good state g < memo_slots has a valid slot copies it; the others are
+    // walked, once per distinct state, and fill their slot
+    uint32_t* memo;
+    unsigned long long* memo_key;
+    uint32_t* memo_any;
+    uint32_t memo_slots, memo_words, memo_tag, memo_seq;
+    uint32_t rg;              // distinct states walked together (<= 32)
 };
 
 // Optional per-kernel event timing of a launch sequence (zs_set_profiling).

@@ -110,16 +110,6 @@ __device__ __forceinline__ void rw_bar() {
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
-#ifdef RW_PROF
-__device__ unsigned long long rw_prof[1024][16];
-#define RW_MARK(i) do { if (threadIdx.x == 0) rw_prof[blockIdx.x][i] = wall_clock64(); } while (0)
-#define RW_COUNT(i) do { if (threadIdx.x == 0) rw_prof[blockIdx.x][i]++; } while (0)
-extern "C" int zs_row_prof_read(void* out) { return (int)hipMemcpyFromSymbol(out, HIP_SYMBOL(rw_prof), sizeof(rw_prof)); }
-extern "C" int zs_row_prof_clear() { static unsigned long long z[1024][16]; return (int)hipMemcpyToSymbol(HIP_SYMBOL(rw_prof), z, sizeof(z)); }
-#else
-#define RW_MARK(i) do {} while (0)
-#define RW_COUNT(i) do {} while (0)
-#endif
 
 // ---------------------------------------------------------------------------
 // P0: merged patch list (the entries of zs_k_prep's format, plus LDS copies)
@@ -398,7 +388,6 @@ struct rw_list {
 // Returns the new entry count. Called by every thread.
 __device__ __noinline__ uint32_t rw_compact(const rw_list& L, uint32_t n, uint32_t K, uint32_t idlim, float* fthr,
                                             float* cutmax) {
-    RW_COUNT(10);
     uint32_t np2 = 1;
     while (np2 < n) np2 <<= 1;
     for (uint32_t i = threadIdx.x; i < np2; i += RW_NT)
@@ -587,9 +576,6 @@ __device__ __forceinline__ float rw_cross(const float (&v)[4], int& start, float
             for (int q = 0; q < 4; q++)
                 if (my == ZS_BIGI && 4 * t + q >= start && v[q] != 0.0f) my = 4 * t + q;
             const int first = first_of(my);
-#ifdef RW_PROF
-            if (threadIdx.x == 0) rw_prof[blockIdx.x][7]++;
-#endif
             if (first == ZS_BIGI) return s + 0.0f;
             if (t == first / 4) {
                 float ve = v[0];
@@ -605,10 +591,6 @@ __device__ __forceinline__ float rw_cross(const float (&v)[4], int& start, float
         }
         const int eg0 = zs_grid_exp(s);
         if (rw_scale(eg0) == 0.0f) { slow = true; return s; }
-#ifdef RW_PROF
-        const unsigned long long cs0 = wall_clock64();
-        if (threadIdx.x == 0) rw_prof[blockIdx.x][6]++;
-#endif
         // per-thread increments and half-way flags on grids eg0 .. eg0 + RW_NG - 1
         uint32_t inc[RW_NG][4], tot[RW_NG], tb[RW_NG];
 #pragma unroll
@@ -647,9 +629,6 @@ __device__ __forceinline__ float rw_cross(const float (&v)[4], int& start, float
             pre[j] += before;
             wtot[j] = all;
         }
-#ifdef RW_PROF
-        if (threadIdx.x == 0) rw_prof[blockIdx.x][11] += wall_clock64() - cs0;
-#endif
         // walk: running sum k on grid eg0 + j from element position P (the
         // prefix of grid j through the last event is base); the grid index
         // is a compile-time constant in every step, so the increments stay
@@ -673,9 +652,6 @@ __device__ __forceinline__ float rw_cross(const float (&v)[4], int& start, float
                         my = 4 * t + q;
                 }
                 const int e = first_of(my);
-#ifdef RW_PROF
-                if (threadIdx.x == 0 && e != ZS_BIGI) rw_prof[blockIdx.x][15]++;
-#endif
                 if (e == ZS_BIGI) {
                     s = zs_grid_value(k + (wtot[j] - base), eg0 + j);
                     done = true;
@@ -875,20 +851,13 @@ __device__ __forceinline__ float rw_sum_pass(const rw_row& R, rw_shared& sh, flo
         if (!stopped) break;
         stopped = false;
         g = rw_uni(stop);
-        RW_COUNT(8);
         float x[4], y[4];
         rw_tile(R, sh, g, x, y);
         float v[4];
         f.exact(x, y, v);
         int start = 0;
         bool slow = false;
-#ifdef RW_PROF
-        const unsigned long long c0 = wall_clock64();
-#endif
         s = rw_cross(v, start, s, ties, slow, sh);
-#ifdef RW_PROF
-        if (threadIdx.x == 0) rw_prof[blockIdx.x][13] += wall_clock64() - c0;
-#endif
         if (slow) {
             // the ordered scan (zs_seq.h) finishes this tile outside
             if (threadIdx.x == 0) { sh.pass_g = g; sh.pass_start = start; }
@@ -1049,16 +1018,7 @@ __device__ __forceinline__ float rw_slow_tile(const rw_row& R, const F& f, uint3
 template <class F>
 __device__ __forceinline__ float rw_pass(const rw_row& R, const F& f, float s, uint32_t g, uint32_t slow,
                                          uint32_t ties) {
-#ifdef RW_PROF
-    if (rw_uni(slow)) {
-        const unsigned long long c0 = wall_clock64();
-        const float r = rw_slow_tile(R, f, rw_uni(g), rw_sh.pass_start, rw_unif(s));
-        if (threadIdx.x == 0) { rw_prof[blockIdx.x][14] += wall_clock64() - c0; rw_prof[blockIdx.x][9]++; }
-        return r;
-    }
-#else
     if (rw_uni(slow)) return rw_slow_tile(R, f, rw_uni(g), rw_sh.pass_start, rw_unif(s));
-#endif
     return rw_sum_pass(R, rw_sh, rw_unif(s), ties, f, rw_uni(g));
 }
 __device__ __noinline__ float rw_pass_obs(const float* row, const float* allow, uint32_t V, uint32_t np, uint32_t ldm4,
@@ -1113,7 +1073,6 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
     const bool want_lp = (P.flags & ZS_ROW_LOGPROBS) != 0;
     const bool want_unc = (P.flags & ZS_ROW_UNCERTAINTY) != 0;
     const bool want_obs = want_lp || want_unc;
-    RW_MARK(0);
 
     // ---------------- P0: patches
     uint32_t has_y = 0;
@@ -1131,7 +1090,6 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
         }
         return;
     }
-    RW_MARK(5);
     rw_row R;
     R.row = b.d_logits + (size_t)r * b.ld;
     R.allow = ((P.flags & ZS_ROW_MASKED) && b.d_allow_bits) ? b.d_allow_bits + (size_t)r * b.allow_words : nullptr;
@@ -1429,11 +1387,6 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
             g = g + 1;
         }
     }
-    RW_MARK(1);
-#ifdef RW_STOP_AFTER_P1
-    if (t == 0) { st.mode = ZS_MODE_DONE; st.token = 0; st.status = 0; st.obs_need = 0; st.rounds = 0; st.n_cand = 0; st.klist = 0; st.kpend = 0; st.obs_special = 1; }
-    return;
-#endif
     // ---- row statistics (one workgroup reduction)
     {
         for (int d = 32; d > 0; d >>= 1) {
@@ -1609,7 +1562,6 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
         }
     }
     __syncthreads();
-    RW_MARK(2);
 
     // ---------------- P2: observers' S (fast-exp terms: a tolerance output)
     // and the big rows' sampler S = sum expf(z - max) (sampler.rs:68, exact)
@@ -1640,10 +1592,6 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
             slow = 1;
         }
     }
-    RW_MARK(3);
-#ifdef RW_PROF
-    if (t == 0) rw_prof[r][12] = rw_prof[r][8];
-#endif
     // ---------------- P3: entropy (hallucination.rs:139-144; fast-exp terms)
     float H = 0.0f;
     if (obs_need & ZS_OBS_H) {
@@ -1657,7 +1605,6 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
             slow = 1;
         }
     }
-    RW_MARK(4);
 
     // ---------------- row state for the big-row kernels and zs_k_final
     if (t == 0) {

@@ -220,6 +220,10 @@ class ByteDfa:
         _check(self.ctx.h, rc, "zs_dfa_mask")
         return out
 
+    def memo_clear(self) -> None:
+        """Drop the memoised per-state bitsets: the next mask() walks every row."""
+        lib().zs_dfa_memo_clear(self.h)
+
     def __del__(self):
         try:
             if self.h:
