@@ -579,7 +579,6 @@ extern "C" int zs_dfa_mask(zs_ctx* ctx, const zs_dfa* dfa, const zs_vocab* vocab
     a.memo_slots = V <= ctx->max_vocab ? dfa->memo_slots : 0u;
     a.memo_words = dfa->memo_words;
     a.memo_tag = dfa->memo_tag;
-    a.rg = 0;   // the kernel's default group size
     // Viability flags: the context's flags hold the epoch of the call that
     // found a viable token, on both kernel paths (no clearing pass, and a flag
     // left by an earlier call on the other path never reads as viable); the

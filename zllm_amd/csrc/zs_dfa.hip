@@ -111,7 +111,7 @@ __global__ __launch_bounds__(DM_NT) void zs_k_dfa_mask(dm_args a) {
 // same plan): each constrained row is either a memo hit (its state's slot is
 // valid) or a walk, and rows sharing a state share one walk, whose result
 // goes to all of them and to the state's memo slot. The walks are taken as
-// items: a tile of ZS_WALK_TILE ids times a group of up to rg (<= 32)
+// items: a tile of ZS_WALK_TILE ids times a group of up to rg (<= 48)
 // distinct states. Per item the workgroup first tabulates, for every byte,
 // which of the item's states survive that byte as a first byte (one bit per
 // state); a token reads its first byte's word and walks its remaining bytes
@@ -123,7 +123,7 @@ __global__ __launch_bounds__(DM_NT) void zs_k_dfa_mask(dm_args a) {
 // the workgroups.
 #define DL_NT 1024
 #define DL_TPT (ZS_WALK_TILE / DL_NT)
-#define DL_RG 32                  // distinct states per item (bits of a first-byte word)
+#define DL_RG 48                  // distinct states per item (bits of a first-byte word)
 #define DL_TW (ZS_WALK_TILE / 32) // bitmap words per state and tile
 #define DL_SIDE 4                 // surviving states walked side by side
 #define DL_FREE 0xffffu           // row modes: unconstrained
@@ -150,10 +150,10 @@ __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
     __shared__ uint32_t tab[DL_WORDS];
     __shared__ uint16_t ci[256];
     __shared__ uint32_t bm[DL_RG][DL_TW];   // the plan's hash table first
-    __shared__ uint32_t fb[256];            // per byte: the item's states alive after it
+    __shared__ unsigned long long fb[256];  // per byte: the item's states alive after it
     __shared__ uint32_t wl[DL_MAXROWS];     // walks: good state << 16 | first row
     __shared__ uint32_t link[DL_MAXROWS];   // row -> next row of its state (0xffff: end)
-    __shared__ uint32_t s0r[DL_RG];         // the item's start states (packed ids)
+    __shared__ uint32_t s0r[DL_RG + 1];     // the item's start states (packed ids); [DL_RG] = fail
     __shared__ uint16_t rmode[DL_MAXROWS];  // row: memo slot (hit), DL_WALKED or DL_FREE
     __shared__ uint32_t nwl;
     const int t = threadIdx.x;
@@ -208,7 +208,7 @@ __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
     if (walk && !lead) link[r] = atomicExch(&link[first], r);
     {
         uint32_t tot;
-        const uint32_t pos = block_excl_scan_u<DL_NT>(lead ? 1u : 0u, fb, &tot);
+        const uint32_t pos = block_excl_scan_u<DL_NT>(lead ? 1u : 0u, reinterpret_cast<uint32_t*>(fb), &tot);
         if (lead) wl[pos] = g << 16 | r;
         if (t == 0) nwl = tot;
     }
@@ -236,8 +236,12 @@ __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
     };
     const uint32_t fail = a.ngood;  // the sink row
     const uint32_t ncover = a.V > a.ntab ? a.V : a.ntab;
-    const uint32_t rg = a.rg;
-    const uint32_t ntt = (ncover + ZS_WALK_TILE - 1) / ZS_WALK_TILE, nrg = (nc + rg - 1) / rg;
+    // states per item: as few groups as fill the grid once (every workgroup
+    // builds the same nc, so the same split), at most DL_RG states a group
+    const uint32_t ntt = (ncover + ZS_WALK_TILE - 1) / ZS_WALK_TILE;
+    const uint32_t ngrp = gridDim.x / ntt > 1u ? gridDim.x / ntt : 1u;
+    const uint32_t rg = min((uint32_t)DL_RG, max(1u, (nc + ngrp - 1) / ngrp));
+    const uint32_t nrg = (nc + rg - 1) / rg;
     static_assert(DL_TPT == 2 && ZS_WALK_TILE == 2048 && DL_NT == 1024, "run pairing");
     // the thread's two slots of an item's tile: runs of 64 length-sorted
     // slots, wave w takes runs w and 31 - w (a short and a long run)
@@ -261,22 +265,27 @@ __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
         const uint32_t nr = min(rg, nc - g0);
         const uint32_t tok0 = tt * ZS_WALK_TILE;
         // the item's start states, then the first-byte words: thread t takes
-        // byte t & 255 for the states 8 * (t >> 8) .. + 7
-        if (t < DL_RG) {
+        // byte t & 255 for the states 16 * (t >> 8) .. + 15
+        if (t <= DL_RG) {
             const uint32_t gg = (uint32_t)t < nr ? wl[g0 + t] >> 16 : 0xffffu;
             s0r[t] = gg == 0xffffu ? fail : gg;
         }
         dl_bar();
         {
             const uint32_t b = (uint32_t)t & 255u, q = (uint32_t)t >> 8;
-            const uint32_t cb = ci[b];
-            uint32_t m = 0;
+            static_assert(DL_RG <= 64 && DL_NT == 1024, "four 16-state quarters per byte");
+            if (q * 16 < nr) {
+                // states past nr start in the sink row: no branches, so the
+                // 16 reads of each kind are in flight together
+                const uint32_t cb = ci[b];
+                uint32_t m = 0;
 #pragma unroll
-            for (uint32_t k = 0; k < 8; k++) {
-                const uint32_t rr = q * 8 + k;
-                if (rr < nr && step(s0r[rr], cb) != fail) m |= 1u << k;
+                for (uint32_t k = 0; k < 16; k++)
+                    if (step(s0r[q * 16 + k], cb) != fail) m |= 1u << k;
+                reinterpret_cast<uint16_t*>(fb)[b * 4 + q] = (uint16_t)m;
+            } else {
+                reinterpret_cast<uint16_t*>(fb)[b * 4 + q] = 0;
             }
-            reinterpret_cast<uint8_t*>(fb)[b * 4 + q] = (uint8_t)m;
         }
         // this item's tokens (fetched during the previous item), the next
         // item's fetched now
@@ -286,24 +295,27 @@ __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
         dl_bar();
         // both tokens' surviving states, DL_SIDE of each token at a time,
         // walked side by side (independent chains hide the LDS latency)
-        uint32_t L[2], m[2], id[2], cb0[2];
+        uint32_t L[2], id[2], cb0[2];
+        unsigned long long m[2];
 #pragma unroll
         for (int j = 0; j < 2; j++) {
             L[j] = cm[j] == 0xffffffffu ? 0u : cm[j] >> 18;   // 0: never allowed
             id[j] = cm[j] & 0x3ffffu;
-            m[j] = L[j] ? fb[cw[j].x & 0xffu] : 0u;           // most tokens end here
+            m[j] = L[j] ? fb[cw[j].x & 0xffu] : 0ull;         // most tokens end here
             cb0[j] = ci[cw[j].x & 0xffu];
         }
         while (m[0] | m[1]) {
             // up to DL_SIDE states of each token; the ones taken leave m
-            uint32_t sv[2][DL_SIDE], taken[2];
+            uint32_t sv[2][DL_SIDE];
+            unsigned long long taken[2];
 #pragma unroll
             for (int j = 0; j < 2; j++) {
-                uint32_t mm = m[j];
+                unsigned long long mm = m[j];
 #pragma unroll
                 for (int k = 0; k < DL_SIDE; k++) {
-                    sv[j][k] = mm ? step(s0r[__builtin_ctz(mm)], cb0[j]) : fail;
-                    mm &= mm - 1u;
+                    // no state left: the sink entry (no branch per state)
+                    sv[j][k] = step(s0r[mm ? (uint32_t)__builtin_ctzll(mm) : (uint32_t)DL_RG], cb0[j]);
+                    mm &= mm - 1ull;
                 }
                 taken[j] = m[j] & ~mm;
                 m[j] = mm;
@@ -351,11 +363,11 @@ __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
                     }
                 }
                 const uint32_t off = id[j] - tok0;
-                uint32_t tk = taken[j];
+                unsigned long long tk = taken[j];
 #pragma unroll
                 for (int k = 0; k < DL_SIDE; k++) {
-                    if (tk && sv[j][k] != fail) atomicOr(&bm[__builtin_ctz(tk)][off >> 5], 1u << (off & 31));
-                    tk &= tk - 1u;
+                    if (tk && sv[j][k] != fail) atomicOr(&bm[__builtin_ctzll(tk)][off >> 5], 1u << (off & 31));
+                    tk &= tk - 1ull;
                 }
             }
         }
@@ -435,12 +447,10 @@ extern "C" int zs_dfa_mask_launch(const dm_args& a, bool packed_lds, uint32_t nc
     uint32_t ncover = a.V > a.ntab ? a.V : a.ntab;
     if (!packed_lds || a.B > DL_MAXROWS) x.memo_slots = 0;  // the memo is the packed walk's
     if (packed_lds && a.B <= DL_MAXROWS) {
-        // states per item: enough items to give every CU one when B rows are
-        // walked (B bounds the distinct states), at most DL_RG
+        // one workgroup per CU, fewer when there are fewer (tile, state)
+        // pairs (B bounds the distinct states; the kernel splits them)
         const uint32_t ntt = (ncover + ZS_WALK_TILE - 1) / ZS_WALK_TILE;
-        if (x.rg == 0) x.rg = (a.B * ntt + ncu - 1) / ncu;
-        x.rg = x.rg < 1 ? 1 : (x.rg > DL_RG ? DL_RG : x.rg);
-        const uint32_t items = ntt * ((a.B + x.rg - 1) / x.rg);
+        const uint32_t items = ntt * a.B;
         if (a.sparse)
             hipLaunchKernelGGL(zs_k_dfa_mask_packed<true>, dim3(min(items, ncu)), dim3(DL_NT), 0, stream, x);
         else

@@ -13,7 +13,7 @@
 // Largest vocabulary a context accepts (the row kernel's patch bitmap and
 // the per-row chunk records are sized for it).
 #define ZS_MAX_VOCAB 262144
-#define ZS_DFA_LDS_BYTES 143360  // packed DFA table budget in LDS (140 KB)
+#define ZS_DFA_LDS_BYTES 138544  // packed DFA table budget in LDS (135.3 KB)
 #define ZS_DFA_MEMO_BYTES (256ull << 20)  // per-DFA device memo of allow bitsets (cap)
 #define ZS_WALK_TILE 2048        // ids per tile of the vocab-parallel DFA walk
 #define ZS_DFA_MAXROWS 1024      // rows of the LDS-table DFA walk (constrained-row list in LDS)
@@ -305,7 +305,6 @@ struct dm_args {
     unsigned long long* memo_key;
     uint32_t* memo_any;
     uint32_t memo_slots, memo_words, memo_tag, memo_seq;
-    uint32_t rg;              // distinct states walked together (<= 32)
 };
 
 // Optional per-kernel event timing of a launch sequence (zs_set_profiling).
