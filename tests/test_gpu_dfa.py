@@ -309,3 +309,38 @@ def test_memo_hits_equal_fresh_walks():
     # cleared memo: every row walked again
     dfa.memo_clear()
     same(run(dfa, table, s2, V), fresh(table, s2, V), "after memo_clear")
+
+
+@pytest.mark.parametrize("mk", [dfa_ab_star_c, dfa_ab_plus_c])
+def test_empty_token_and_direct_eos_rule(mk):
+    """A valid token with no bytes is allowed from every live state (its walk
+    ends where it starts, logit_fsm.rs:170-178), so every live state has a
+    viable token and the EOS rule reduces to is_accept(s); the mask kernel
+    then applies it without the separate EOS pass. Masks and viability flags
+    equal the oracle's for every state, twice (the second call from the memo)."""
+    trans, dead, acc = mk()
+    S = trans.shape[0]
+    tokens = [b"a", b"", b"b", b"ab", None, b"c", b"zz"]
+    eos = 4
+    V = 8
+    print(f"[case] empty token {mk.__name__}", flush=True)
+    od, ov = O.Dfa(trans, dead, acc), O.Vocab(tokens, eos)
+    states = list(range(S)) + [-1, 1, 0]
+    from tests.gpu_util import ctx
+    from zllm_amd.engine import ByteDfa, TokenByteTable
+    c = ctx()
+    offs, data, valid = _csr(tokens)
+    table = TokenByteTable.from_csr(c, offs, data, valid, eos)
+    dfa = ByteDfa(c, trans, dead, acc)
+    st = torch.tensor(np.asarray(states, np.int32), device="cuda")
+    for _ in range(2):
+        anyv = torch.full((len(states),), 7, dtype=torch.int32, device="cuda")
+        bits = dfa.mask(table, st, V, any_out=anyv)
+        torch.cuda.synchronize()
+        b, a = bits.cpu().numpy().view(np.uint32), anyv.cpu().numpy()
+        for i, s in enumerate(states):
+            if s < 0:
+                assert b[i].tolist() == O.pack_bits(np.ones(V, bool)).tolist()
+                continue
+            assert b[i].tolist() == O.mask_bits(V, dfa=od, vocab=ov, state=s).tolist(), (i, s)
+            assert bool(a[i]) == O.dfa_allowed(od, ov, s)[1], (i, s)

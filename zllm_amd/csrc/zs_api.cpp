@@ -240,7 +240,8 @@ extern "C" int zs_vocab_create(zs_ctx* ctx, const uint32_t* h_offsets, const uin
     for (uint32_t tl = 0; tl < v->nwtile; tl++) {
         std::vector<uint32_t> ids;
         for (uint32_t t = tl * ZS_WALK_TILE; t < ntab && t < (tl + 1) * ZS_WALK_TILE; t++) ids.push_back(t);
-        auto wlen = [&](uint32_t t) { return h_valid[t] ? (uint32_t)tlen[t] : 0u; };
+        // walk length: 0 = never allowed (not valid), 0x3fff = valid with no bytes
+        auto wlen = [&](uint32_t t) { return h_valid[t] ? (tlen[t] ? (uint32_t)tlen[t] : 0x3fffu) : 0u; };
         std::stable_sort(ids.begin(), ids.end(), [&](uint32_t x, uint32_t y) { return wlen(x) < wlen(y); });
         for (size_t k = 0; k < ids.size(); k++) {
             const size_t slot = (size_t)tl * ZS_WALK_TILE + k;
@@ -296,6 +297,9 @@ extern "C" void zs_dfa_destroy(zs_dfa* d) {
     (void)hipFree(d->d_remap);
     (void)hipFree(d->d_memo);
     (void)hipFree(d->d_memo_key);
+    (void)hipFree(d->d_viable);
+    free(d->h_viable);
+    free(d->h_remap);
     (void)hipFree(d->d_memo_any);
     free(d->h_trans);
     free(d->h_dead);
@@ -391,6 +395,9 @@ extern "C" int zs_dfa_create(zs_ctx* ctx, const uint32_t* h_trans, uint32_t nsta
     uint32_t ngood = 0;
     for (uint32_t s = 0; s < nstates; s++)
         if (!bad[s]) remap[s] = (uint16_t)ngood++;
+    d->h_remap = (uint16_t*)malloc(sizeof(uint16_t) * nstates);
+    memcpy(d->h_remap, remap.data(), sizeof(uint16_t) * nstates);
+    d->h_viable = (uint8_t*)calloc(ngood + 1, 1);
     // the fail value is ngood, a sink row whose entries all lead to itself, so a
     // walk needs no liveness test per step; entries of `bits` bits packed back
     // to back inside a row, each row padded to whole 32-bit words (row s, class
@@ -466,10 +473,12 @@ extern "C" int zs_dfa_create(zs_ctx* ctx, const uint32_t* h_trans, uint32_t nsta
     // the memo: one slot of ceil(max_vocab / 32) words per good state, up to
     // ZS_DFA_MEMO_BYTES (states past the cap are walked on every call)
     d->memo_words = (ctx->max_vocab + 31) / 32;
-    d->memo_slots = (uint32_t)std::min<uint64_t>(ngood, ZS_DFA_MEMO_BYTES / ((uint64_t)d->memo_words * 4));
+    d->memo_slots = (uint32_t)std::min<uint64_t>(std::min<uint64_t>(ngood, 0xfff0u),
+                                                  ZS_DFA_MEMO_BYTES / ((uint64_t)d->memo_words * 4));
     d->memo_tag = 1;   // the keys start at 0: tag 0 is never used
     if (!rc && d->memo_slots) rc = zs_alloc(ctx, &d->d_memo, (size_t)d->memo_slots * d->memo_words);
     if (!rc && d->memo_slots) rc = zs_alloc(ctx, &d->d_memo_key, d->memo_slots);
+    if (!rc) rc = zs_alloc(ctx, &d->d_viable, ngood + 1);
     if (!rc && d->memo_slots) rc = zs_alloc(ctx, &d->d_memo_any, d->memo_slots);
     if (!rc && d->memo_slots && hipMemset(d->d_memo_key, 0, (size_t)d->memo_slots * 8) != hipSuccess)
         rc = zs_set_error(ctx, ZS_EHIP, "zs_dfa_create: memo clear failed");
@@ -515,6 +524,40 @@ extern "C" int zs_dfa_advance(const zs_dfa* d, const zs_vocab* v, uint32_t state
     }
     *out_state = s;
     return ZS_OK;
+}
+
+// Is the viability of every good state (some token of the vocabulary is
+// allowed, logit_fsm.rs:258-262) known without walking the vocabulary? A
+// state is viable when the vocabulary has a valid empty token (allowed from
+// every live state) or a single-byte token b with trans(s, b) neither dead
+// nor non-live (logit_fsm.rs:170-178); it is not viable when no byte leads to
+// such a state and there is no empty token (every walk of one byte or more
+// fails at its first byte). Otherwise it stays open and the mask kernel's
+// walk decides. Fills d->h_viable per good state; returns 1 when no state is
+// open. Host, once per (DFA, vocabulary): nstates * 256 steps.
+static uint32_t zs_dfa_all_quick(const zs_dfa* d, const zs_vocab* v) {
+    bool has1[256] = {false}, empty = false;
+    for (uint32_t t = 0; t < v->ntab; t++) {
+        if (!v->h_valid[t]) continue;
+        const uint32_t n = v->h_offsets[t + 1] - v->h_offsets[t];
+        if (n == 0) empty = true;
+        if (n == 1) has1[v->h_bytes[v->h_offsets[t]]] = true;
+    }
+    uint32_t all = 1;
+    for (uint32_t s = 0; s < d->nstates; s++) {
+        if (d->h_dead[s] || !d->h_live[s]) continue;
+        bool one = false, any_good = false;
+        for (uint32_t b = 0; b < 256 && !one; b++) {
+            const uint32_t u = d->h_trans[(size_t)s * 256 + b];
+            const bool good = !d->h_dead[u] && d->h_live[u];
+            any_good |= good;
+            one = good && has1[b];
+        }
+        const uint32_t g = d->h_remap[s];
+        d->h_viable[g] = (empty || one) ? 1 : 0;
+        if (!empty && !one && any_good) all = 0;
+    }
+    return all;
 }
 
 extern "C" void zs_dfa_memo_clear(zs_dfa* dfa) {
@@ -568,10 +611,19 @@ extern "C" int zs_dfa_mask(zs_ctx* ctx, const zs_dfa* dfa, const zs_vocab* vocab
     const bool packed = dfa->packed_lds != 0 && B <= ZS_DFA_MAXROWS;
     // the memo holds masks of one (vocabulary, V): another pair invalidates it
     if (dfa->memo_serial != vocab->serial || dfa->memo_V != V) {
+        if (dfa->memo_serial != vocab->serial) {
+            dfa->all_quick = zs_dfa_all_quick(dfa, vocab);
+            if (dfa->all_quick &&
+                hipMemcpyAsync(dfa->d_viable, dfa->h_viable, dfa->ngood ? dfa->ngood : 1, hipMemcpyHostToDevice,
+                               (hipStream_t)stream) != hipSuccess)
+                dfa->all_quick = 0;
+        }
         dfa->memo_serial = vocab->serial;
         dfa->memo_V = V;
         zs_dfa_memo_clear(const_cast<zs_dfa*>(dfa));
     }
+    a.eos_direct = dfa->all_quick;
+    a.viable = dfa->d_viable;
     a.memo = dfa->d_memo;
     a.memo_key = dfa->d_memo_key;
     a.memo_any = dfa->d_memo_any;

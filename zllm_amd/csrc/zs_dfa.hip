@@ -127,7 +127,8 @@ __global__ __launch_bounds__(DM_NT) void zs_k_dfa_mask(dm_args a) {
 #define DL_TW (ZS_WALK_TILE / 32) // bitmap words per state and tile
 #define DL_SIDE 4                 // surviving states walked side by side
 #define DL_FREE 0xffffu           // row modes: unconstrained
-#define DL_WALKED 0xfffeu         //            walked in this call (else: its memo slot)
+#define DL_WALKED 0xfffcu         //            walked in this call, | 1: eos allowed (else: its memo slot)
+#define DL_EMPTY 0x3fffu          // walk length of a valid token with no bytes
 
 // Workgroup barrier that orders LDS accesses only (__syncthreads() would also
 // wait for the next item's token loads, issued ahead on purpose)
@@ -185,7 +186,22 @@ __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
     const unsigned long long key = g < a.memo_slots ? a.memo_key[g] : 0ull;
     const bool hit = st >= 0 && g < a.memo_slots && (uint32_t)(key >> 32) == a.memo_tag && (uint32_t)key != a.memo_seq;
     const bool walk = st >= 0 && !hit;
-    if (t < DL_MAXROWS) rmode[t] = st < 0 ? DL_FREE : (hit ? (uint16_t)g : DL_WALKED);
+    // the EOS bit of a walked row when the state's viability is known without
+    // the walk (eos_direct, viable[g]); a bad start state allows nothing, so
+    // eos is allowed
+    const uint32_t viab = a.eos_direct && g != 0xffffu ? a.viable[g] : 0u;
+    const uint32_t eos_ok = g == 0xffffu ? 1u : (a.eos_direct && (a.accept[st] || !viab) ? 1u : 0u);
+    if (t < DL_MAXROWS) rmode[t] = st < 0 ? DL_FREE : (hit ? (uint16_t)g : (uint16_t)(DL_WALKED | eos_ok));
+    if (a.eos_direct && blockIdx.x == 0 && walk) {
+        // viability is known now: the caller's flags, and the state's memo
+        // slot (keyed with this call's sequence number: no workgroup of this
+        // call takes it as a hit)
+        if (a.any_user) a.any_user[r] = viab;
+        if (g < a.memo_slots) {
+            a.memo_any[g] = viab;
+            a.memo_key[g] = ((unsigned long long)a.memo_tag << 32) | a.memo_seq;
+        }
+    }
     __syncthreads();
     // the first row of every walked state: insert g << 16 | row, keep the least
     uint32_t hpos = 0;
@@ -303,6 +319,13 @@ __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
             id[j] = cm[j] & 0x3ffffu;
             m[j] = L[j] ? fb[cw[j].x & 0xffu] : 0ull;         // most tokens end here
             cb0[j] = ci[cw[j].x & 0xffu];
+            if (L[j] == DL_EMPTY) {
+                // no bytes: allowed from every (live) start state
+                m[j] = 0ull;
+                const uint32_t off = id[j] - tok0;
+                for (uint32_t rr = 0; rr < nr; rr++)
+                    if (s0r[rr] != fail) atomicOr(&bm[rr][off >> 5], 1u << (off & 31));
+            }
         }
         while (m[0] | m[1]) {
             // up to DL_SIDE states of each token; the ones taken leave m
@@ -384,11 +407,16 @@ __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
             const uint32_t gw = tok0 / 32 + wi;
             uint32_t v = word;
             if (gw == a.words - 1 && (a.V & 31)) v &= (1u << (a.V & 31)) - 1u;
+            if (gg < a.memo_slots && gw < a.words) a.memo[(size_t)gg * a.memo_words + gw] = v;
+            if (a.eos_direct && gw == (a.eos >> 5) && a.eos < a.V) {
+                // the EOS rule here (the same for every row of the state)
+                const uint32_t bit = 1u << (a.eos & 31);
+                v = (rmode[e & 0xffffu] & 1u) ? (v | bit) : (v & ~bit);
+            }
             for (uint32_t rw = e & 0xffffu; rw != 0xffffu; rw = link[rw]) {
                 if (gw < a.words) a.out[(size_t)rw * a.words + gw] = v;
-                if (word) a.any[rw] = a.epoch;  // every writer stores the same value
+                if (word && !a.eos_direct) a.any[rw] = a.epoch;  // every writer stores the same value
             }
-            if (gg < a.memo_slots && gw < a.words) a.memo[(size_t)gg * a.memo_words + gw] = v;
         }
     }
     // memo hits and unconstrained rows (the workgroups split the rows' words)
@@ -396,15 +424,24 @@ __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
     for (uint32_t i = blockIdx.x * DL_NT + t; i < nall; i += gridDim.x * DL_NT) {
         const uint32_t rr = i / a.words, wi = i - rr * a.words;
         const uint32_t mode = rmode[rr];
-        if (mode == DL_WALKED) continue;
+        if ((mode & ~1u) == DL_WALKED) continue;
         uint32_t v;
         if (mode == DL_FREE) {
             v = 0xffffffffu;
             if (wi == a.words - 1 && (a.V & 31)) v = (1u << (a.V & 31)) - 1u;
         } else {
-            // the stored walk and its viability (the EOS kernel follows)
+            // the stored walk and its viability, then the EOS rule (here, or
+            // by the EOS kernel)
             v = a.memo[(size_t)mode * a.memo_words + wi];
-            if (wi == 0 && a.memo_any[mode]) a.any[rr] = a.epoch;
+            if (a.eos_direct) {
+                if (wi == 0 && a.any_user) a.any_user[rr] = a.memo_any[mode];
+                if (a.eos < a.V && wi == (a.eos >> 5)) {
+                    const uint32_t bit = 1u << (a.eos & 31);
+                    v = (a.accept[a.states[rr]] || !a.memo_any[mode]) ? (v | bit) : (v & ~bit);
+                }
+            } else if (wi == 0 && a.memo_any[mode]) {
+                a.any[rr] = a.epoch;
+            }
         }
         a.out[(size_t)rr * a.words + wi] = v;
     }
@@ -445,7 +482,10 @@ extern "C" int zs_dfa_mask_launch(const dm_args& a, bool packed_lds, uint32_t nc
     dm_args x = a;
     x.any = any_scratch;
     uint32_t ncover = a.V > a.ntab ? a.V : a.ntab;
-    if (!packed_lds || a.B > DL_MAXROWS) x.memo_slots = 0;  // the memo is the packed walk's
+    if (!packed_lds || a.B > DL_MAXROWS) {
+        x.memo_slots = 0;      // the memo and the direct EOS rule are the packed walk's
+        x.eos_direct = 0;
+    }
     if (packed_lds && a.B <= DL_MAXROWS) {
         // one workgroup per CU, fewer when there are fewer (tile, state)
         // pairs (B bounds the distinct states; the kernel splits them)
@@ -455,6 +495,7 @@ extern "C" int zs_dfa_mask_launch(const dm_args& a, bool packed_lds, uint32_t nc
             hipLaunchKernelGGL(zs_k_dfa_mask_packed<true>, dim3(min(items, ncu)), dim3(DL_NT), 0, stream, x);
         else
             hipLaunchKernelGGL(zs_k_dfa_mask_packed<false>, dim3(min(items, ncu)), dim3(DL_NT), 0, stream, x);
+        if (x.eos_direct) return hipGetLastError() == hipSuccess ? 0 : -1;   // the walk applied the EOS rule
     } else {
         // epoch 0: the caller's own 0/1 flags, cleared first; otherwise the
         // context's flags, compared with the epoch as in the packed walk

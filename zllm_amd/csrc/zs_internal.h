@@ -218,7 +218,8 @@ struct zs_vocab {
     uint32_t maxlen;
     // walk order: inside every tile of ZS_WALK_TILE ids, the ids sorted by byte
     // length, with their first 16 bytes and (id | walk length << 18); 0xffffffff
-    // marks a slot with no token and length 0 a token that is never allowed
+    // marks a slot with no token, length 0 a token that is never allowed and
+    // length 0x3fff a valid token with no bytes
     uint32_t nwtile;
     uint32_t* d_wbytes;    // [nwtile * ZS_WALK_TILE][4]
     uint32_t* d_wmeta;     // [nwtile * ZS_WALK_TILE]
@@ -267,6 +268,12 @@ struct zs_dfa {
     uint32_t* d_memo_any;             // [memo_slots]
     uint32_t memo_slots, memo_words;
     mutable uint32_t memo_tag, memo_seq, memo_serial, memo_V;
+    // for the vocabulary memo_serial: every good state's viability known
+    // without the walk (all_quick), and that viability per good state
+    mutable uint32_t all_quick;
+    uint8_t* h_viable;                // [ngood]
+    uint16_t* h_remap;                // [nstates] good id or 0xffff (host copy)
+    uint8_t* d_viable;                // [ngood]
 };
 
 // Arguments of the DFA mask kernels (zs_dfa.hip).
@@ -305,6 +312,10 @@ struct dm_args {
     unsigned long long* memo_key;
     uint32_t* memo_any;
     uint32_t memo_slots, memo_words, memo_tag, memo_seq;
+    // the viability of every good state is known without the walk
+    // (viable[g], 0/1): the walk applies the EOS rule itself
+    uint32_t eos_direct;
+    const uint8_t* viable;
 };
 
 // Optional per-kernel event timing of a launch sequence (zs_set_profiling).
