@@ -425,6 +425,13 @@ extern "C" int zs_dfa_create(zs_ctx* ctx, const uint32_t* h_trans, uint32_t nsta
     for (uint32_t b = 0; b < 256; b++) clsinfo[b] = (uint16_t)(cls[b] * bits);
     d->ngood = ngood;
     d->bits = bits;
+    {
+        uint64_t goodt = 0;
+        for (uint32_t s = 0; s < nstates; s++)
+            if (!bad[s])
+                for (uint32_t b = 0; b < 256; b++) goodt += bad[d->h_trans[(size_t)s * 256 + b]] ? 0 : 1;
+        d->dense = goodt * 10 > (uint64_t)ngood * 256 * 3 ? 1 : 0;
+    }
     d->rw = rw;
     d->packed_lds = packed.size() * 4 <= ZS_DFA_LDS_BYTES && rw < 65536 ? 1 : 0;
     if (!d->packed_lds && ncls <= 64) {
@@ -601,6 +608,7 @@ extern "C" int zs_dfa_mask(zs_ctx* ctx, const zs_dfa* dfa, const zs_vocab* vocab
     a.remap = dfa->d_remap;
     a.ngood = dfa->ngood;
     a.sparse = dfa->sparse;
+    a.dense = dfa->dense;
     a.bits = dfa->bits;
     a.rw = dfa->rw;
     a.states = d_states;

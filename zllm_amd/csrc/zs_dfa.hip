@@ -125,7 +125,6 @@ __global__ __launch_bounds__(DM_NT) void zs_k_dfa_mask(dm_args a) {
 #define DL_TPT (ZS_WALK_TILE / DL_NT)
 #define DL_RG 48                  // distinct states per item (bits of a first-byte word)
 #define DL_TW (ZS_WALK_TILE / 32) // bitmap words per state and tile
-#define DL_SIDE 4                 // surviving states walked side by side
 #define DL_FREE 0xffffu           // row modes: unconstrained
 #define DL_WALKED 0xfffcu         //            walked in this call, | 1: eos allowed (else: its memo slot)
 #define DL_EMPTY 0x3fffu          // walk length of a valid token with no bytes
@@ -146,7 +145,9 @@ static_assert(DL_MAXROWS <= DL_NT, "one row per thread in the plan");
 __device__ __forceinline__ uint32_t dl_hash(uint32_t g) { return (g * 2654435761u) >> (32 - 11); }
 static_assert(DL_HASH == 2048, "dl_hash yields 11 bits");
 
-template <bool SPARSE>
+// SIDE states per token walked side by side, TG tokens together: 4 x 2 when
+// few states survive a first byte, 8 x 1 for dense automata
+template <bool SPARSE, int SIDE, int TG>
 __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
     __shared__ uint32_t tab[DL_WORDS];
     __shared__ uint16_t ci[256];
@@ -327,70 +328,86 @@ __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
                     if (s0r[rr] != fail) atomicOr(&bm[rr][off >> 5], 1u << (off & 31));
             }
         }
-        while (m[0] | m[1]) {
-            // up to DL_SIDE states of each token; the ones taken leave m
-            uint32_t sv[2][DL_SIDE];
-            unsigned long long taken[2];
 #pragma unroll
-            for (int j = 0; j < 2; j++) {
-                unsigned long long mm = m[j];
+        for (int j0 = 0; j0 < 2; j0 += TG) {
+            // tokens j0 .. j0 + TG - 1 together: up to SIDE states of each
+            // (the ones taken leave m), walked side by side
+            auto left = [&]() {
+                unsigned long long x = 0ull;
 #pragma unroll
-                for (int k = 0; k < DL_SIDE; k++) {
-                    // no state left: the sink entry (no branch per state)
-                    sv[j][k] = step(s0r[mm ? (uint32_t)__builtin_ctzll(mm) : (uint32_t)DL_RG], cb0[j]);
-                    mm &= mm - 1ull;
+                for (int jj = 0; jj < TG; jj++) x |= m[j0 + jj];
+                return x;
+            };
+            while (left()) {
+                uint32_t sv[TG][SIDE];
+                unsigned long long taken[TG];
+#pragma unroll
+                for (int jj = 0; jj < TG; jj++) {
+                    const int j = j0 + jj;
+                    unsigned long long mm = m[j];
+#pragma unroll
+                    for (int k = 0; k < SIDE; k++) {
+                        // no state left: the sink entry (no branch per state)
+                        sv[jj][k] = step(s0r[mm ? (uint32_t)__builtin_ctzll(mm) : (uint32_t)DL_RG], cb0[j]);
+                        mm &= mm - 1ull;
+                    }
+                    taken[jj] = m[j] & ~mm;
+                    m[j] = mm;
                 }
-                taken[j] = m[j] & ~mm;
-                m[j] = mm;
-            }
-            // the class of the next byte is read while the current step's
-            // table reads are in flight
-            uint32_t cb[2] = {ci[(cw[0].x >> 8) & 0xffu], ci[(cw[1].x >> 8) & 0xffu]};
+                // the class of the next byte is read while the current step's
+                // table reads are in flight
+                uint32_t cb[TG];
 #pragma unroll
-            for (int i = 1; i < 16; i++) {
-                bool go[2];
+                for (int jj = 0; jj < TG; jj++) cb[jj] = ci[(cw[j0 + jj].x >> 8) & 0xffu];
 #pragma unroll
-                for (int j = 0; j < 2; j++) {
+                for (int i = 1; i < 16; i++) {
+                    bool go[TG], any = false;
+#pragma unroll
+                    for (int jj = 0; jj < TG; jj++) {
+                        bool live = false;
+#pragma unroll
+                        for (int k = 0; k < SIDE; k++) live |= sv[jj][k] != fail;
+                        go[jj] = live && (uint32_t)i < L[j0 + jj];
+                        any |= go[jj];
+                    }
+                    if (!any) break;
+#pragma unroll
+                    for (int jj = 0; jj < TG; jj++) {
+                        if (!go[jj]) continue;
+                        const uint4 w4 = cw[j0 + jj];
+                        uint32_t cbn = 0;
+                        if (i < 15) {
+                            const int n = i + 1;
+                            const uint32_t bw = n < 4 ? w4.x : n < 8 ? w4.y : n < 12 ? w4.z : w4.w;
+                            cbn = ci[(bw >> (8 * (n & 3))) & 0xffu];
+                        }
+#pragma unroll
+                        for (int k = 0; k < SIDE; k++) sv[jj][k] = step(sv[jj][k], cb[jj]);
+                        cb[jj] = cbn;
+                    }
+                }
+#pragma unroll
+                for (int jj = 0; jj < TG; jj++) {
+                    const int j = j0 + jj;
                     bool live = false;
 #pragma unroll
-                    for (int k = 0; k < DL_SIDE; k++) live |= sv[j][k] != fail;
-                    go[j] = live && (uint32_t)i < L[j];
-                }
-                if (!go[0] && !go[1]) break;
+                    for (int k = 0; k < SIDE; k++) live |= sv[jj][k] != fail;
+                    if (L[j] > 16 && live) {
+                        // bytes past the first 16 from the CSR copy (long tokens)
+                        const uint32_t o0 = a.offsets[id[j]], o1 = a.offsets[id[j] + 1];
+                        for (uint32_t i = o0 + 16; i < o1; i++) {
+                            const uint32_t c = ci[a.bytes[i]];
 #pragma unroll
-                for (int j = 0; j < 2; j++) {
-                    if (!go[j]) continue;
-                    uint32_t cbn = 0;
-                    if (i < 15) {
-                        const int n = i + 1;
-                        const uint32_t bw = n < 4 ? cw[j].x : n < 8 ? cw[j].y : n < 12 ? cw[j].z : cw[j].w;
-                        cbn = ci[(bw >> (8 * (n & 3))) & 0xffu];
+                            for (int k = 0; k < SIDE; k++) sv[jj][k] = step(sv[jj][k], c);
+                        }
                     }
+                    const uint32_t off = id[j] - tok0;
+                    unsigned long long tk = taken[jj];
 #pragma unroll
-                    for (int k = 0; k < DL_SIDE; k++) sv[j][k] = step(sv[j][k], cb[j]);
-                    cb[j] = cbn;
-                }
-            }
-#pragma unroll
-            for (int j = 0; j < 2; j++) {
-                bool live = false;
-#pragma unroll
-                for (int k = 0; k < DL_SIDE; k++) live |= sv[j][k] != fail;
-                if (L[j] > 16 && live) {
-                    // bytes past the first 16 from the CSR copy (long tokens)
-                    const uint32_t o0 = a.offsets[id[j]], o1 = a.offsets[id[j] + 1];
-                    for (uint32_t i = o0 + 16; i < o1; i++) {
-                        const uint32_t c = ci[a.bytes[i]];
-#pragma unroll
-                        for (int k = 0; k < DL_SIDE; k++) sv[j][k] = step(sv[j][k], c);
+                    for (int k = 0; k < SIDE; k++) {
+                        if (tk && sv[jj][k] != fail) atomicOr(&bm[__builtin_ctzll(tk)][off >> 5], 1u << (off & 31));
+                        tk &= tk - 1ull;
                     }
-                }
-                const uint32_t off = id[j] - tok0;
-                unsigned long long tk = taken[j];
-#pragma unroll
-                for (int k = 0; k < DL_SIDE; k++) {
-                    if (tk && sv[j][k] != fail) atomicOr(&bm[__builtin_ctzll(tk)][off >> 5], 1u << (off & 31));
-                    tk &= tk - 1ull;
                 }
             }
         }
@@ -491,10 +508,13 @@ extern "C" int zs_dfa_mask_launch(const dm_args& a, bool packed_lds, uint32_t nc
         // pairs (B bounds the distinct states; the kernel splits them)
         const uint32_t ntt = (ncover + ZS_WALK_TILE - 1) / ZS_WALK_TILE;
         const uint32_t items = ntt * a.B;
+        const dim3 grid(min(items, ncu));
         if (a.sparse)
-            hipLaunchKernelGGL(zs_k_dfa_mask_packed<true>, dim3(min(items, ncu)), dim3(DL_NT), 0, stream, x);
+            hipLaunchKernelGGL((zs_k_dfa_mask_packed<true, 4, 2>), grid, dim3(DL_NT), 0, stream, x);
+        else if (a.dense)
+            hipLaunchKernelGGL((zs_k_dfa_mask_packed<false, 8, 1>), grid, dim3(DL_NT), 0, stream, x);
         else
-            hipLaunchKernelGGL(zs_k_dfa_mask_packed<false>, dim3(min(items, ncu)), dim3(DL_NT), 0, stream, x);
+            hipLaunchKernelGGL((zs_k_dfa_mask_packed<false, 4, 2>), grid, dim3(DL_NT), 0, stream, x);
         if (x.eos_direct) return hipGetLastError() == hipSuccess ? 0 : -1;   // the walk applied the EOS rule
     } else {
         // epoch 0: the caller's own 0/1 flags, cleared first; otherwise the

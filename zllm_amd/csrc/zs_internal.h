@@ -255,6 +255,7 @@ struct zs_dfa {
     // d_packed = {mask lo, mask hi, first target, 0} per good state + sink,
     // then u16 targets; d_clsinfo = class index
     uint32_t sparse;
+    uint32_t dense;        // over 30% of (good state, byte) transitions reach a good state
     // memo of allow bitsets per good state (logit_fsm.rs:166-182's cache):
     // slot g holds the walk's bitset for good state g (before the EOS rule)
     // and d_memo_any[g] = a token is viable; it is valid when
@@ -297,6 +298,7 @@ struct dm_args {
     const uint16_t* remap;
     uint32_t ngood, bits, rw;
     uint32_t sparse;          // packed table in the sparse row form
+    uint32_t dense;           // most (good state, byte) pairs lead to a good state
     const int32_t* states;
     uint32_t B, V, words;
     uint32_t* out;
