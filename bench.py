@@ -32,6 +32,8 @@ def parse():
     ap.add_argument("--seed", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--dfa-only", action="store_true",
+                    help="only time zs_dfa_mask (cold and warm) on the DFA configs and print one JSON line")
     ap.add_argument("--copy-probe", type=int, default=0,
                     help="only copy this many MiB device-to-device (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
     return ap.parse_args()
@@ -441,6 +443,20 @@ def make_step(W, V):
     return step, spec_stream
 
 
+DFA_CONFIGS = [("c5_json512", 151936, 128, "json", 512), ("c4_json2048", 151936, 128, "json", 2048),
+               ("c3_random64", 128256, 32, "random", 64), ("json_any_compiled", 151936, 128, "compiled", 0)]
+
+
+def dfa_only(seed):
+    """zs_dfa_mask alone over the DFA configs (in this order: 23 cold calls,
+    then 23 warm calls each): {config: [cold us, warm us]}."""
+    from zllm_amd.engine import Context
+    ctx = Context(0, 256, 151936)
+    res = {name: [round(v, 2) for v in mask_config_us(ctx, V, rows, kind, S, seed)]
+           for name, V, rows, kind, S in DFA_CONFIGS}
+    print(json.dumps({"dfa_mask_us_cold_warm": res}))
+
+
 def main():
     args = parse()
     if args.copy_probe:
@@ -449,6 +465,9 @@ def main():
     if args.gpus != 1:
         print(json.dumps({"error": "this build targets one GPU: run with --gpus 1 (sharding is design-only)"}))
         sys.exit(2)
+    if args.dfa_only:
+        dfa_only(args.seed)
+        return
     import numpy as np
     import torch
     B, V = args.B, args.V
