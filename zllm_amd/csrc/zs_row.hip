@@ -549,10 +549,28 @@ __device__ __forceinline__ uint32_t rw_wave_scan(uint32_t v) {
 // 2^-103 (no f32 scale reaches their grid) are left to the ordered scan
 // (slow: from element `start`).
 __device__ __forceinline__ float rw_cross(const float (&v)[4], int& start, float s, uint32_t ties, bool& slow,
-                                          rw_shared& sh) {
+                                          rw_shared& sh, bool first_tile) {
     const int t = (int)threadIdx.x, lane = zs_lane(), wid = zs_wid();
     uint32_t par = 0;
     slow = false;
+    if (first_tile && start == 0) {
+        // the row's first 256 terms, where the sum leaves a binade at almost
+        // every doubling of the number of terms: wave 0 adds them one by one
+        // in index order (the reference's own additions; a sum that is still
+        // zero counts as +0, as the reference's sum starts)
+        if (wid == 0) {
+            float ss = s + 0.0f;
+            for (int L = 0; L < 64; L++) {
+#pragma unroll
+                for (int q = 0; q < 4; q++) ss = ss + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v[q]), L));
+            }
+            if (lane == 0) sh.cr_s[par] = ss;
+        }
+        rw_bar();
+        s = sh.cr_s[par];
+        par ^= 1u;
+        start = 4 * 64;
+    }
     // the first element of the workgroup with an event (uniform)
     auto first_of = [&](int my) -> int {
         // (read by every lane: a lane's value exists only where it was
@@ -857,7 +875,7 @@ __device__ __forceinline__ float rw_sum_pass(const rw_row& R, rw_shared& sh, flo
         f.exact(x, y, v);
         int start = 0;
         bool slow = false;
-        s = rw_cross(v, start, s, ties, slow, sh);
+        s = rw_cross(v, start, s, ties, slow, sh, g == 0);
         if (slow) {
             // the ordered scan (zs_seq.h) finishes this tile outside
             if (threadIdx.x == 0) { sh.pass_g = g; sh.pass_start = start; }
@@ -1046,6 +1064,55 @@ __device__ __noinline__ float rw_pass_ent(const float* row, const float* allow, 
     f.inv = rw_unif(inv);
     f.lns = rw_unif(lns);
     return rw_pass(rw_row_of(row, allow, V, np, ldm4), f, s, g, slow, 0u);
+}
+
+// A masked row's allowed ids in index order, with their x~ (cx) and y (cy)
+// written to row scratch: the sums then run over these values only (a
+// masked id's term is zero, which leaves a running sum unchanged). cx, cy
+// hold round_up(n, 4) values each (the tail padded with -inf); cy = cx +
+// round_up(n, 4). Returns n, or 0 when no id or more than a quarter of the
+// row is allowed (then the sums run over the whole row). Uniform.
+__device__ __noinline__ uint32_t rw_gather_allowed(const float* row, const uint32_t* allow, uint32_t V, uint32_t np,
+                                                   float* cx) {
+    rw_shared& sh = rw_sh;
+    const uint32_t t = threadIdx.x, words = (V + 31) / 32;
+    const uint32_t per = (words + RW_NT - 1) / RW_NT, w0 = t * per, w1 = min(w0 + per, words);
+    auto word = [&](uint32_t w) {
+        uint32_t a = allow[w];
+        if (w == words - 1 && (V & 31)) a &= (1u << (V & 31)) - 1u;
+        return a;
+    };
+    uint32_t c = 0;
+    for (uint32_t w = w0; w < w1; w++) c += __popc(word(w));
+    uint32_t n;
+    uint32_t pos = block_excl_scan_u<RW_NT>(c, sh.ru[4], &n);
+    n = rw_uni(n);
+    if (n == 0 || n > V / 4) return 0;
+    const uint32_t n4 = (n + 3) & ~3u;
+    float* cy = cx + n4;
+    for (uint32_t w = w0; w < w1; w++) {
+        uint32_t a = word(w);
+        while (a) {
+            const uint32_t id = w * 32 + (uint32_t)__builtin_ctz(a);
+            a &= a - 1u;
+            float x = row[id], y = x;
+            if (np) {
+                const uint32_t wd = rw_pbits[id >> 5];
+                if ((wd >> (id & 31)) & 1u) {
+                    const uint32_t rank = rw_pbits[words + (id >> 5)] + __popc(wd & ((1u << (id & 31)) - 1u));
+                    const uint32_t fl = sh.pid[rank] >> RW_PF_SHIFT;
+                    if (fl & ZS_PF_BAN) { x = -INFINITY; y = -INFINITY; }
+                    if (fl & ZS_PF_Y) y = sh.py[rank];
+                }
+            }
+            cx[pos] = x;
+            cy[pos] = y;
+            pos++;
+        }
+    }
+    if (t < n4 - n) { cx[n + t] = -INFINITY; cy[n + t] = -INFINITY; }
+    __syncthreads();
+    return n;
 }
 
 // Exact sampling of a small survivor set by wave 0 (token to sh.tok).
@@ -1569,15 +1636,36 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
     const bool doB = mode == ZS_MODE_BIG && has_thr != 2;
     float SA = -0.0f, SB = -0.0f;
     const float* allow_f = reinterpret_cast<const float*>(R.allow);
+    // the sums' view of the row: the whole row, or a masked row's allowed ids
+    const float* px = R.row;
+    const float* py = R.row;
+    uint32_t pV = V, pnp = R.np, pldm4 = R.ldm4;
+    if (R.allow && (doA || doB || (obs_need & ZS_OBS_H))) {
+        // row scratch of the big-row kernels (not in use before they run),
+        // 16-byte aligned
+        float* cx = reinterpret_cast<float*>(a.pairs + (size_t)r * a.max_vocab * 2);
+        cx += (4u - (uint32_t)((reinterpret_cast<uintptr_t>(cx) >> 2) & 3u)) & 3u;
+        const uint32_t n = rw_gather_allowed(R.row, R.allow, V, R.np, cx);
+        if (n) {
+            const uint32_t n4 = (n + 3) & ~3u;
+            px = cx;
+            py = cx + n4;
+            allow_f = nullptr;
+            pV = n;
+            pnp = 0;
+            pldm4 = n4 - 4;
+        }
+    }
+    const uint32_t ngp = (pV + RW_G - 1) / RW_G;
     // a pass alternates between its streaming function and the ordered scan
     // of the tiles that need it, until the row is done
     if (doA) {
         uint32_t g = 0, slow = 0;
         while (true) {
-            SA = rw_pass_obs(R.row, allow_f, V, R.np, R.ldm4, M, SA, g, slow);
+            SA = rw_pass_obs(px, allow_f, pV, pnp, pldm4, M, SA, g, slow);
             if (slow) { g++; slow = 0; continue; }
             g = rw_uni(sh.pass_g);
-            if (g >= ng) break;
+            if (g >= ngp) break;
             slow = 1;
         }
     }
@@ -1585,10 +1673,10 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
         const uint32_t use_thr = has_thr != 0 ? 1u : 0u;
         uint32_t g = 0, slow = 0;
         while (true) {
-            SB = rw_pass_samp(R.row, allow_f, V, R.np, R.ldm4, T, zmax, thr, use_thr, SB, g, slow);
+            SB = rw_pass_samp(py, allow_f, pV, pnp, pldm4, T, zmax, thr, use_thr, SB, g, slow);
             if (slow) { g++; slow = 0; continue; }
             g = rw_uni(sh.pass_g);
-            if (g >= ng) break;
+            if (g >= ngp) break;
             slow = 1;
         }
     }
@@ -1598,10 +1686,10 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
         const float inv = 1.0f / SA, lns = (float)log((double)SA);
         uint32_t g = 0, slow = 0;
         while (true) {
-            H = rw_pass_ent(R.row, allow_f, V, R.np, R.ldm4, M, inv, lns, H, g, slow);
+            H = rw_pass_ent(px, allow_f, pV, pnp, pldm4, M, inv, lns, H, g, slow);
             if (slow) { g++; slow = 0; continue; }
             g = rw_uni(sh.pass_g);
-            if (g >= ng) break;
+            if (g >= ngp) break;
             slow = 1;
         }
     }
