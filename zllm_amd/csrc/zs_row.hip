@@ -787,12 +787,14 @@ __device__ __forceinline__ uint32_t rw_inc4_cert(const float (&a)[4], const floa
         const bool u = fmaf(qv[q], (float)ZS_EXP_EPS, fabsf(qv[q] - rq[q])) >= 0.5f && qv[q] < RW_QCAP;
         unc |= u ? (1u << q) : 0u;
     }
+    if (unc) {   // rare: one branch per thread
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-        if (unc & (1u << q)) {   // rare
-            const float qe = fminf(zs_expf(d[q]) * sc, RW_QCAP);
-            rq[q] = rintf(qe);
-            if (fabsf(qe - rq[q]) == 0.5f) fl |= 1u;
+        for (int q = 0; q < 4; q++) {
+            if (unc & (1u << q)) {
+                const float qe = fminf(zs_expf(d[q]) * sc, RW_QCAP);
+                rq[q] = rintf(qe);
+                if (fabsf(qe - rq[q]) == 0.5f) fl |= 1u;
+            }
         }
     }
     uint32_t sum = 0;
@@ -918,34 +920,55 @@ struct rw_obs_terms {
 };
 
 // Terms of the sampler's S (sampler.rs:68): expf(z - max) exactly, z = y / T,
-// 0 below the top-k threshold.
+// 0 below the top-k threshold. DIV: 0 = T is 1 (no division), 1 = Markstein's
+// division, 2 = IEEE division (a compile-time choice, so that the four
+// elements' code stays free of branches).
+template <uint32_t DIV>
 struct rw_samp_terms {
     float T, rT, zmax, thr;
     bool use_thr;
-    uint32_t div;   // 0: T = 1 (no division), 1: Markstein's division, 2: IEEE division
     // z = y / T correctly rounded (sampler.rs:47-51). With rT = RN(1 / T),
     // q0 = RN(y * rT) is within an ulp of y / T, the remainder y - q0 * T is
     // exact in one fma, and RN(q0 + r * rT) is RN(y / T) (Markstein's
     // theorem) while nothing underflows or overflows: for 2^-100 <= |y| <=
     // 2^100 and 2^-20 <= T <= 2^20. Zeros and infinities divide exactly as
-    // y * rT; other y divide the IEEE way.
-    __device__ __forceinline__ float temper(float y) const {
-        if (div == 0u) return y;
-        if (div == 2u) return y / T;
-        const float q0 = y * rT;
-        const float q1 = fmaf(fmaf(-q0, T, y), rT, q0);
-        const float a = fabsf(y);
-        const bool mid = a >= 0x1p-100f && a <= 0x1p100f;
-        float z = mid ? q1 : q0;
-        if (!mid && a != 0.0f && a != INFINITY) z = y / T;   // rare
-        return z;
-    }
-    __device__ __forceinline__ void args(const float (&y)[4], float (&d)[4]) const {
+    // y * rT; other y divide the IEEE way (rare: one branch per thread).
+    __device__ __forceinline__ void temper4(const float (&y)[4], float (&z)[4]) const {
+        if (DIV == 0u) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) z[q] = y[q];
+            return;
+        }
+        if (DIV == 2u) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) z[q] = y[q] / T;
+            return;
+        }
+        bool odd = false;
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-            float z = temper(y[q]);
-            if (use_thr && z < thr) z = -INFINITY;
-            d[q] = z - zmax;
+            const float q0 = y[q] * rT;
+            const float q1 = fmaf(fmaf(-q0, T, y[q]), rT, q0);
+            const float a = fabsf(y[q]);
+            const bool mid = a >= 0x1p-100f && a <= 0x1p100f;
+            z[q] = mid ? q1 : q0;
+            odd |= !mid && a != 0.0f && a != INFINITY;
+        }
+        if (odd) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const float a = fabsf(y[q]);
+                if (!(a >= 0x1p-100f && a <= 0x1p100f) && a != 0.0f && a != INFINITY) z[q] = y[q] / T;
+            }
+        }
+    }
+    __device__ __forceinline__ void args(const float (&y)[4], float (&d)[4]) const {
+        float z[4];
+        temper4(y, z);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            if (use_thr && z[q] < thr) z[q] = -INFINITY;
+            d[q] = z[q] - zmax;
         }
     }
     __device__ __forceinline__ bool nonzero(const float (&)[4], const float (&y)[4]) const {
@@ -1048,14 +1071,19 @@ __device__ __noinline__ float rw_pass_obs(const float* row, const float* allow, 
 __device__ __noinline__ float rw_pass_samp(const float* row, const float* allow, uint32_t V, uint32_t np, uint32_t ldm4,
                                            float T, float zmax, float thr, uint32_t use_thr, float s, uint32_t g,
                                            uint32_t slow) {
-    rw_samp_terms f;
-    f.T = rw_unif(T);
-    f.rT = 1.0f / f.T;
-    f.div = !(f.T > 0.0f && f.T != 1.0f) ? 0u : ((f.T >= 0x1p-20f && f.T <= 0x1p20f) ? 1u : 2u);
-    f.zmax = rw_unif(zmax);
-    f.thr = rw_unif(thr);
-    f.use_thr = rw_uni(use_thr) != 0u;
-    return rw_pass(rw_row_of(row, allow, V, np, ldm4), f, s, g, slow, 1u);
+    const float Tu = rw_unif(T);
+    const uint32_t div = !(Tu > 0.0f && Tu != 1.0f) ? 0u : ((Tu >= 0x1p-20f && Tu <= 0x1p20f) ? 1u : 2u);
+    auto run = [&](auto f) {
+        f.T = Tu;
+        f.rT = 1.0f / Tu;
+        f.zmax = rw_unif(zmax);
+        f.thr = rw_unif(thr);
+        f.use_thr = rw_uni(use_thr) != 0u;
+        return rw_pass(rw_row_of(row, allow, V, np, ldm4), f, s, g, slow, 1u);
+    };
+    if (rw_uni(div) == 1u) return run(rw_samp_terms<1>{});
+    if (rw_uni(div) == 0u) return run(rw_samp_terms<0>{});
+    return run(rw_samp_terms<2>{});
 }
 __device__ __noinline__ float rw_pass_ent(const float* row, const float* allow, uint32_t V, uint32_t np, uint32_t ldm4,
                                           float M, float inv, float lns, float s, uint32_t g, uint32_t slow) {
