@@ -1664,7 +1664,13 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
     const bool doB = mode == ZS_MODE_BIG && has_thr != 2;
     float SA = -0.0f, SB = -0.0f;
     const float* allow_f = reinterpret_cast<const float*>(R.allow);
-    // the sums' view of the row: the whole row, or a masked row's allowed ids
+    // the sums' view of the row: the whole row, or a masked row's allowed ids.
+    // The observers' terms see only the bans among the patches (biases and
+    // counts change y, not x~): without a ban their passes skip the patch
+    // list.
+    bool any_ban = false;
+    for (uint32_t i = t; i < (uint32_t)np; i += RW_NT) any_ban |= ((sh.pid[i] >> RW_PF_SHIFT) & ZS_PF_BAN) != 0u;
+    any_ban = __syncthreads_or(any_ban) != 0;
     const float* px = R.row;
     const float* py = R.row;
     uint32_t pV = V, pnp = R.np, pldm4 = R.ldm4;
@@ -1690,7 +1696,7 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
     if (doA) {
         uint32_t g = 0, slow = 0;
         while (true) {
-            SA = rw_pass_obs(px, allow_f, pV, pnp, pldm4, M, SA, g, slow);
+            SA = rw_pass_obs(px, allow_f, pV, any_ban ? pnp : 0u, pldm4, M, SA, g, slow);
             if (slow) { g++; slow = 0; continue; }
             g = rw_uni(sh.pass_g);
             if (g >= ngp) break;
@@ -1714,7 +1720,7 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
         const float inv = 1.0f / SA, lns = (float)log((double)SA);
         uint32_t g = 0, slow = 0;
         while (true) {
-            H = rw_pass_ent(px, allow_f, pV, pnp, pldm4, M, inv, lns, H, g, slow);
+            H = rw_pass_ent(px, allow_f, pV, any_ban ? pnp : 0u, pldm4, M, inv, lns, H, g, slow);
             if (slow) { g++; slow = 0; continue; }
             g = rw_uni(sh.pass_g);
             if (g >= ngp) break;
