@@ -109,8 +109,8 @@ SPEC_K = 4
 # HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
 # (profiles/c5_traffic.md), scaled by the copy-kernel calibration there; None
 # where not measured
-TRAFFIC = {"zs_k_spec_chunk": 1402.3e6, "zs_k_pass1": 166.4e6, "zs_k_pv": 64.1e6, "zs_k_tp_inc": 36.4e6,
-           "zs_k_big": 0.5e6}
+TRAFFIC = {"zs_k_spec_chunk": 1402.3e6, "zs_k_row": 711.7e6, "zs_k_pv": 106.5e6, "zs_k_tp_inc": 55.8e6,
+           "zs_k_big": 0.8e6}
 
 
 def spec_bytes_per_row(V, k):
@@ -491,6 +491,8 @@ def main():
     torch.cuda.synchronize()
     ms_step = e0.elapsed_time(e1) / args.steps
 
+    # the step's DFA mask alone (C5: 128 grammar rows of 256), cold and warm
+    us_mask, us_mask_warm = mask_cold_warm_us(W["dfa"], W["table"], W["st"], V, bits)
     # DFA-mask configs C3 (64-state random DFA, 32 rows, V=128256) and C4
     # (JSON-schema DFA of 2048 states, 128 rows, V=151936), untimed loops
     dfa_cfg = {"c5_json512": None, "c3_random64": mask_config_us(ctx, 128256, 32, "random", 64, args.seed),
@@ -509,7 +511,6 @@ def main():
     us_spec = s0.elapsed_time(s1) / 10 * 1000.0
 
     # DFA mask alone and per-kernel timings of zs_sample (separate, untimed loops)
-    us_mask, us_mask_warm = mask_cold_warm_us(W["dfa"], W["table"], W["st"], V, bits)
     ctx.set_profiling(True)
     acc = {}
     n_prof = 10
