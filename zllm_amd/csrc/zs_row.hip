@@ -43,7 +43,7 @@
 #define RW_NW (RW_NT / 64)
 #define RW_G 4096          // ids per tile: one float4 per thread
 #define RW_BUF 2048        // candidate buffer entries (per list)
-#define RW_KEEP 256        // a list above this is compacted to its top K
+#define RW_KEEP 1024       // a list above this is compacted to its top K
 
 struct rw_shared {
     uint32_t pid[ZS_MAX_PATCHES];   // patched ids (sorted) | flags << 30
@@ -343,7 +343,12 @@ __device__ __forceinline__ uint32_t rw_stream(const rw_row& R, const rw_shared& 
     const uint32_t ng = (R.V + RW_G - 1) / RW_G;
     rw_raw raw[4];
 #pragma unroll
-    for (int u = 0; u < 4; u++) raw[u] = rw_fetch(R, min(g_begin + (uint32_t)u, ng - 1));
+    for (int u = 0; u < 4; u++) {
+        raw[u] = rw_fetch(R, min(g_begin + (uint32_t)u, ng - 1));
+        // issued in slot order, as in the loop: the wait before a slot's use
+        // then covers only that slot's loads
+        __asm__ volatile("" ::: "memory");
+    }
     for (uint32_t g0 = g_begin; g0 < ng; g0 += 4) {
 #pragma unroll
         for (int u = 0; u < 4; u++) {
@@ -771,7 +776,7 @@ __device__ __forceinline__ uint32_t rw_inc4(const float (&v)[4], float sc) {
     return sum;
 }
 
-// Certified increments of exact terms exp(d) from their fast-exp values a
+// Certified increments of exact terms exp(d) from their zs_exp_fast values a
 // (relative error below ZS_EXP_EPS): where |q - rint(q)| is within q * eps of
 // one half the term is recomputed with glibc's algorithm; an exact half-way
 // increment sets fl (its rounding depends on the sum's parity: the ordered
@@ -905,7 +910,7 @@ struct rw_obs_terms {
     __device__ __forceinline__ uint32_t fast(const float (&x)[4], const float (&)[4], float sc, uint32_t&) const {
         float v[4];
 #pragma unroll
-        for (int q = 0; q < 4; q++) v[q] = zs_exp_fast(fmaxf(x[q] - M, ZS_EXP_FAST_MIN));
+        for (int q = 0; q < 4; q++) v[q] = zs_exp_hw(fmaxf(x[q] - M, ZS_EXP_FAST_MIN));
         return rw_inc4(v, sc);
     }
     __device__ __forceinline__ void exact(const float (&x)[4], const float (&)[4], float (&v)[4]) const {
@@ -1006,7 +1011,7 @@ struct rw_ent_terms {
 #pragma unroll
         for (int q = 0; q < 4; q++) {
             const float d = fmaxf(x[q] - M, ZS_EXP_FAST_MIN);
-            const float p = zs_exp_fast(d) * inv;
+            const float p = zs_exp_hw(d) * inv;
             v[q] = p > 0.0f ? -(p * (d - lns)) : 0.0f;
         }
         return rw_inc4(v, sc);
