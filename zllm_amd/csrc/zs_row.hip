@@ -1393,8 +1393,10 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
             const uint32_t ovf = rw_uni(sh.ovf[slot]);
             lastslot = slot;
             grp++;
-            p1stop = ovf != 0xffffffffu || n_o > RW_KEEP || (smode == 1 && n_s > RW_KEEP) ||
-                     (smode == 2 && !s_over && n_s > ZS_SMALL_CAP);
+            // more than ZS_SMALL_CAP finite values: the small-survivor list
+            // is dropped (its count ended it; nothing to compact)
+            if (smode == 2 && !s_over && n_s > ZS_SMALL_CAP) s_over = true;
+            p1stop = ovf != 0xffffffffu || n_o > RW_KEEP || (smode == 1 && n_s > RW_KEEP);
             return p1stop;
         });
         if (!p1stop) break;
