@@ -1478,7 +1478,38 @@ __global__ __launch_bounds__(SK_NT) void zs_k_stitchK(zs_sargs a) {
         float tv[SK_EPT];
 #pragma unroll
         for (int q = 0; q < SK_EPT; q++) tv[q] = klist_term(L, j * ZS_SUB + SK_EPT * t + q);
-        const int stop = seq_group<SK_NT, SK_EPT>(tv, 0, s, thresh, sh);
+        int start = 0;
+        if (j == 0) {
+            // the list's first SK_EPT * 64 terms, where the sum leaves a binade
+            // at almost every doubling of the number of terms: wave 0 adds
+            // them one by one (the reference's own additions, and its stop)
+            __shared__ float s0;
+            __shared__ int stop0;
+            if (t < 64) {
+                float ss = s;
+                int sp = -1;
+                for (int Lq = 0; Lq < 64 && sp < 0; Lq++) {
+#pragma unroll
+                    for (int q = 0; q < SK_EPT; q++) {
+                        if (sp >= 0) break;
+                        ss = ss + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, tv[q]), Lq));
+                        if (KIND == 1 && ss >= thresh) sp = SK_EPT * Lq + q;
+                    }
+                }
+                if (t == 0) { s0 = ss; stop0 = sp; }
+            }
+            __syncthreads();
+            s = s0;
+            const int sp = stop0;
+            __syncthreads();
+            if (sp >= 0) {
+                token = L.ki[(uint32_t)sp];
+                done = true;
+                continue;
+            }
+            start = SK_EPT * 64;
+        }
+        const int stop = seq_group<SK_NT, SK_EPT>(tv, start, s, thresh, sh);
         if (KIND == 1 && stop >= 0) {
             token = L.ki[j * ZS_SUB + (uint32_t)stop];
             done = true;
