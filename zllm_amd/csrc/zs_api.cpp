@@ -76,7 +76,7 @@ extern "C" void zs_ctx_destroy(zs_ctx* ctx) {
     if (ctx->lane_host) (void)hipHostFree(ctx->lane_host);
     void* ptrs[] = {ctx->p_cnt, ctx->p_id, ctx->p_flags, ctx->p_y, ctx->rst, ctx->pairs, ctx->pv, ctx->mask_scratch, ctx->spec_chunks,
                     ctx->spec_rows, ctx->p_sub, ctx->k_ap, ctx->k_sum, ctx->tp_bk, ctx->tp_cl, ctx->tp_pre, ctx->kcnt,
-                    ctx->lane_temp, ctx->lane_topk, ctx->lane_topp, ctx->lane_seed, ctx->lane_vals, ctx->lane_ih, ctx->lane_keys,
+                    ctx->lane_temp, ctx->lane_vals, ctx->lane_ih, ctx->lane_keys,
                     ctx->lane_idxs, ctx->lane_ck, ctx->lane_cn};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
@@ -133,10 +133,14 @@ extern "C" int zs_ctx_create(int device, uint32_t max_rows, uint32_t max_vocab, 
     if (!rc) rc = zs_alloc(ctx, &ctx->tp_pre, R * (size_t)max_vocab * 2);
     if (!rc) rc = zs_alloc(ctx, &ctx->kcnt, R * C * 2);
     if (!rc) rc = zs_alloc(ctx, &ctx->spec_rows, R);
-    if (!rc) rc = zs_alloc(ctx, &ctx->lane_temp, R);
-    if (!rc) rc = zs_alloc(ctx, &ctx->lane_topk, R);
-    if (!rc) rc = zs_alloc(ctx, &ctx->lane_topp, R);
-    if (!rc) rc = zs_alloc(ctx, &ctx->lane_seed, R);
+    // the lane knobs in one block laid out as the staging areas (temp, top_k,
+    // top_p, seed; R each): one copy per call
+    if (!rc) rc = zs_alloc(ctx, &ctx->lane_temp, 4 * (size_t)R);
+    if (!rc) {
+        ctx->lane_topk = reinterpret_cast<uint32_t*>(ctx->lane_temp + R);
+        ctx->lane_topp = ctx->lane_temp + 2 * (size_t)R;
+        ctx->lane_seed = reinterpret_cast<uint32_t*>(ctx->lane_temp + 3 * (size_t)R);
+    }
     if (!rc) rc = zs_alloc(ctx, &ctx->lane_vals, R * ZS_LANE_K);
     if (!rc) rc = zs_alloc(ctx, &ctx->lane_idxs, R * ZS_LANE_K);
     if (!rc) rc = zs_alloc(ctx, &ctx->lane_ck, R * C * ZS_LANE_K);
@@ -872,10 +876,9 @@ extern "C" int zs_lane_step(zs_ctx* ctx, const float* d_logits, uint32_t m, uint
             hp[i] = h_streams[i].top_p;
             hs[i] = zs_step_seed(h_streams[i].base_seed, h_streams[i].gen_index);
         }
-        if (!rc && (hipMemcpyAsync(ctx->lane_temp, ht, m * 4, hipMemcpyHostToDevice, st) != hipSuccess ||
-                    hipMemcpyAsync(ctx->lane_topk, hk, m * 4, hipMemcpyHostToDevice, st) != hipSuccess ||
-                    hipMemcpyAsync(ctx->lane_topp, hp, m * 4, hipMemcpyHostToDevice, st) != hipSuccess ||
-                    hipMemcpyAsync(ctx->lane_seed, hs, m * 4, hipMemcpyHostToDevice, st) != hipSuccess ||
+        // one copy of the whole area (the four knob arrays; entries past m unused)
+        const size_t nb = (3 * R + m) * 4;
+        if (!rc && (hipMemcpyAsync(ctx->lane_temp, area, nb, hipMemcpyHostToDevice, st) != hipSuccess ||
                     hipEventRecord((hipEvent_t)ctx->lane_event[slot], st) != hipSuccess))
             rc = ZS_EHIP;
     }

@@ -189,7 +189,7 @@ struct zs_ctx {
     const char* timed_names[16];
     // batched lane (zs_lane_step): per-stream knobs staged through pinned
     // host memory, top-K pool of every stream
-    float* lane_temp;            // [rows]
+    float* lane_temp;            // [4][rows] block: temp, then top_k, top_p, seed (below point into it)
     uint32_t* lane_topk;         // [rows]
     float* lane_topp;            // [rows]
     uint32_t* lane_seed;         // [rows]
