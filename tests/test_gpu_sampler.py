@@ -104,6 +104,8 @@ def test_allow_bits_rows():
     bits = np.stack([O.pack_bits(a) for a in allow])
     params = [dict(temperature=0.9, top_k=0, top_p=0.9, seed=i, masked=True, top_logprobs=3) for i in range(B)]
     params[3]["top_k"] = 20
+    params[2]["top_k"] = 100   # about 40 ids allowed: fewer than k
+    params[5]["top_k"] = 3
     _run(x, params, allow_bits=bits, allow=allow)
 
 

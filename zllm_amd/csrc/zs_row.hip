@@ -78,7 +78,14 @@ struct rw_shared {
     float fsh;
     uint32_t pass_g;                // sum passes: the tile left to the ordered scan (or ng)
     int pass_start;                 // and the first element of it still to add
+    uint32_t sel_hist[2][256];      // list selection: digit histogram (double buffered)
+    uint32_t sel_mm[3][RW_NW];      // list selection: per-wave member count, key min / max
+    uint32_t sel_n;                 // list selection: places taken by the gather
+    uint32_t sel_st[4];             // list selection: chosen digit, count before it, its count, places
 };
+// The workgroup's LDS (one object, so that functions outside the kernel
+// address it directly).
+__shared__ rw_shared rw_sh;
 // Bitmap of the row's patched ids, ceil(V / 32) words, followed by the number
 // of patched ids before each word (dynamic LDS).
 extern __shared__ uint32_t rw_pbits[];
@@ -385,25 +392,153 @@ struct rw_list {
     uint32_t* flag;     // bit 0: the last compaction cut entries equal to its K-th key
 };
 
-// Sort the n entries of a list, dropping those of ids >= idlim (their tiles
-// are streamed again), and keep the first K; the K-th key becomes the
-// threshold (below K entries: every id is admitted). Also records the value
+// Selection on a list (list 0: observers, 1: sampler): of its first n
+// entries, those of ids < idlim are the list's members; the K1 smallest
+// members (all of them when fewer) are brought to the front of the buffer in
+// ascending order. Returns the number of members. Called by every thread.
+//
+// An MSB radix selection on the 64-bit entries, 8-bit digits: the digits
+// above the first bit where the members' keys differ are skipped; each pass
+// histograms one digit of the members that share the bits above it with the
+// K1-th smallest, and one wave picks the digit where the count reaches K1. It stops once the members up to and including the chosen digit
+// number at most RW_SEL_CAP (always by the last digit: entries are
+// distinct); those are gathered to the front and sorted by one wave.
+#define RW_SEL_CAP 256
+__device__ __noinline__ uint32_t rw_select(int which, uint32_t n, uint32_t K1, uint32_t idlim) {
+    rw_shared& sh = rw_sh;
+    unsigned long long* buf = which ? sh.u.b.s : sh.u.b.o;
+    const uint32_t t = threadIdx.x, lane = (uint32_t)zs_lane(), wid = (uint32_t)zs_wid();
+    const unsigned long long NONE = ~0ull;   // no member: ids are below 2^32 - 1
+    unsigned long long v[2];
+    uint32_t lo = 0xffffffffu, hi = 0;       // keys (high words) of the members
+    uint32_t c = 0;
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+        const uint32_t i = t + (uint32_t)e * RW_NT;
+        v[e] = NONE;
+        if (i < n) {
+            const unsigned long long w = buf[i];
+            if ((uint32_t)w < idlim) v[e] = w;
+        }
+        const bool mem = v[e] != NONE;
+        c += (uint32_t)__popcll(__ballot(mem));
+        if (mem) {
+            lo = min(lo, (uint32_t)(v[e] >> 32));
+            hi = max(hi, (uint32_t)(v[e] >> 32));
+        }
+    }
+    for (int d = 32; d > 0; d >>= 1) {
+        lo = min(lo, (uint32_t)__shfl_xor(lo, d, 64));
+        hi = max(hi, (uint32_t)__shfl_xor(hi, d, 64));
+    }
+    if (lane == 0) { sh.sel_mm[0][wid] = c; sh.sel_mm[1][wid] = lo; sh.sel_mm[2][wid] = hi; }
+    __syncthreads();
+    c = 0; lo = 0xffffffffu; hi = 0;
+#pragma unroll
+    for (int w = 0; w < RW_NW; w++) {
+        c += sh.sel_mm[0][w];
+        lo = min(lo, sh.sel_mm[1][w]);
+        hi = max(hi, sh.sel_mm[2][w]);
+    }
+    c = rw_uni(c);
+    if (c == 0) return 0;   // every thread read buf before the barrier above
+    const uint32_t need = min(c, K1);
+    // the selected members: (v >> shift) <= (pre >> shift)
+    int shift = 0;
+    unsigned long long pre = NONE - 1ull;   // every member (ids < 2^32 - 1)
+    if (c > RW_SEL_CAP) {
+        lo = rw_uni(lo); hi = rw_uni(hi);
+        shift = lo != hi ? 32 + ((31 - __clz(lo ^ hi)) & ~7) : 24;
+        pre = ((unsigned long long)lo << 32) & ~((2ull << (shift + 7)) - 1ull);   // the bits above the digit
+        uint32_t below = 0;   // members with a smaller prefix
+        if (t < 256) sh.sel_hist[0][t] = 0;
+        for (int pass = 0;; pass ^= 1) {
+            // histogram pass-parity buffer; the other one is cleared for the
+            // next pass (its last reader finished before this pass's first barrier)
+            if (t < 256) sh.sel_hist[pass ^ 1][t] = 0;
+            __syncthreads();
+            const int up = shift + 8;
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const bool in = v[e] != NONE && (up >= 64 || (v[e] >> up) == (pre >> up));
+                const uint32_t dg = (uint32_t)(v[e] >> shift) & 255u;
+                if (in) atomicAdd(&sh.sel_hist[pass][dg], 1u);
+            }
+            __syncthreads();
+            if (wid == 0) {
+                // the digit where the running count reaches need
+                uint32_t h[4], s4 = 0;
+#pragma unroll
+                for (int q = 0; q < 4; q++) { h[q] = sh.sel_hist[pass][lane * 4 + q]; s4 += h[q]; }
+                const uint32_t inc = wave_incl_scan_u(s4);
+                const unsigned long long hit = __ballot(below + inc >= need);
+                const uint32_t L = (uint32_t)__ffsll((long long)hit) - 1u;   // one exists
+                if (lane == L) {
+                    uint32_t run = below + inc - s4;
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        if (run + h[q] >= need) {
+                            sh.sel_mm[0][0] = lane * 4 + q;
+                            sh.sel_mm[1][0] = run;
+                            sh.sel_mm[2][0] = h[q];
+                            break;
+                        }
+                        run += h[q];
+                    }
+                }
+            }
+            __syncthreads();
+            const uint32_t dg = rw_uni(sh.sel_mm[0][0]), cb = rw_uni(sh.sel_mm[2][0]);
+            below = rw_uni(sh.sel_mm[1][0]);
+            pre |= (unsigned long long)dg << shift;
+            if (below + cb <= RW_SEL_CAP || shift == 0) break;
+            shift -= 8;
+        }
+    }
+    // gather the selected members to the front (every read of buf is done)
+    if (t == 0) sh.sel_n = 0;
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+        if (v[e] == NONE || (v[e] >> shift) > (pre >> shift)) continue;
+        buf[atomicAdd(&sh.sel_n, 1u)] = v[e];
+    }
+    __syncthreads();
+    const uint32_t m = rw_uni(sh.sel_n);
+    if (wid == 0) {
+        if (m <= 64) {
+            unsigned long long k[1];
+            k[0] = lane < m ? buf[lane] : NONE;
+            wave_sort_u64_e<1>(k);
+            if (lane < m) buf[lane] = k[0];
+        } else if (m <= 128) {
+            unsigned long long k[2];
+#pragma unroll
+            for (int e = 0; e < 2; e++) k[e] = lane * 2 + e < m ? buf[lane * 2 + e] : NONE;
+            wave_sort_u64_e<2>(k);
+#pragma unroll
+            for (int e = 0; e < 2; e++) if (lane * 2 + e < m) buf[lane * 2 + e] = k[e];
+        } else {
+            unsigned long long k[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) k[e] = lane * 4 + e < m ? buf[lane * 4 + e] : NONE;
+            wave_sort_u64_e<4>(k);
+#pragma unroll
+            for (int e = 0; e < 4; e++) if (lane * 4 + e < m) buf[lane * 4 + e] = k[e];
+        }
+    }
+    __syncthreads();
+    return c;
+}
+
+// Cuts a list to its K smallest members (rw_select); the K-th key becomes the
+// threshold (below K members: every id is admitted). Also records the value
 // of the threshold, whether entries equal to the K-th key were cut, and the
 // largest value cut (into *cutmax).
 // Returns the new entry count. Called by every thread.
-__device__ __noinline__ uint32_t rw_compact(const rw_list& L, uint32_t n, uint32_t K, uint32_t idlim, float* fthr,
-                                            float* cutmax) {
-    uint32_t np2 = 1;
-    while (np2 < n) np2 <<= 1;
-    for (uint32_t i = threadIdx.x; i < np2; i += RW_NT)
-        if (i >= n || (uint32_t)L.buf[i] >= idlim) L.buf[i] = ~0ull;
-    __syncthreads();
-    block_sort_reg_u64<RW_NT, 2>(L.buf, np2);
-    // entries that remain: those before the first ~0
-    uint32_t c = 0;
-    for (uint32_t i = threadIdx.x; i < np2; i += RW_NT) c += L.buf[i] != ~0ull ? 1u : 0u;
-    __shared__ uint32_t cs[RW_NW];
-    c = block_sum_u<RW_NT>(c, cs);
+__device__ uint32_t rw_compact(int which, const rw_list& L, uint32_t n, uint32_t K, uint32_t idlim, float* fthr,
+                               float* cutmax) {
+    const uint32_t c = rw_select(which, n, K + 1, idlim);
     const uint32_t keep = min(c, K);
     if (threadIdx.x == 0) {
         if (c >= K) {
@@ -1022,9 +1157,6 @@ struct rw_ent_terms {
     }
 };
 
-// The workgroup's LDS (one object, so that functions outside the kernel
-// address it directly).
-__shared__ rw_shared rw_sh;
 
 // The sum passes as functions of their own: a pass's loop then holds only
 // its own values (the kernel's live values are saved once around the call,
@@ -1414,9 +1546,9 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
         if (smode == 2 && !s_over && (n_s > ZS_SMALL_CAP || ovf != 0xffffffffu)) s_over = true;
         auto compact_lists = [&](uint32_t lim) {
             if (Ko && (n_o > RW_KEEP || lim != 0xffffffffu))
-                n_o = rw_compact(LO, min(n_o, (uint32_t)RW_BUF), Ko, lim, &sh.fthr[0], &sh.fcut[0]);
+                n_o = rw_compact(0, LO, min(n_o, (uint32_t)RW_BUF), Ko, lim, &sh.fthr[0], &sh.fcut[0]);
             if (smode == 1 && (n_s > RW_KEEP || lim != 0xffffffffu)) {
-                n_s = rw_compact(LS, min(n_s, (uint32_t)RW_BUF), Ks, lim, &sh.fthr[1], &sh.fcut[1]);
+                n_s = rw_compact(1, LS, min(n_s, (uint32_t)RW_BUF), Ks, lim, &sh.fthr[1], &sh.fcut[1]);
                 rejf = fmaxf(rejf, sh.fcut[1]);   // entries cut count as turned away
             }
         };
@@ -1526,12 +1658,7 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
     // observer candidates: the first Ko entries of the sorted list
     uint32_t n_cand = 0;
     if (Ko) {
-        const uint32_t n = min(n_o, (uint32_t)RW_BUF);
-        uint32_t np2 = 1;
-        while (np2 < n) np2 <<= 1;
-        for (uint32_t i = n + t; i < np2; i += RW_NT) sh.u.b.o[i] = ~0ull;
-        __syncthreads();
-        if (np2 > 1) block_sort_reg_u64<RW_NT, 2>(sh.u.b.o, np2);
+        const uint32_t n = rw_select(0, min(n_o, (uint32_t)RW_BUF), Ko, 0xffffffffu);
         n_cand = min(n, Ko);
         if (t < n_cand) {
             sh.cand_id[t] = (uint32_t)sh.u.b.o[t];
@@ -1584,14 +1711,10 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
         bool small = false;
         uint32_t nsv = 0;
         if (smode == 1) {
-            const uint32_t n = min(n_s, (uint32_t)RW_BUF);
-            uint32_t np2 = 1;
-            while (np2 < n) np2 <<= 1;
-            for (uint32_t i = n + t; i < np2; i += RW_NT) sh.u.b.s[i] = ~0ull;
-            __syncthreads();
-            if (np2 > 1) block_sort_reg_u64<RW_NT, 2>(sh.u.b.s, np2);
-            // the k-th largest z is temper(the k-th largest y)
-            const float yk = zs_key_to_float(~(uint32_t)(sh.u.b.s[Ks - 1] >> 32));
+            const uint32_t n = rw_select(1, min(n_s, (uint32_t)RW_BUF), Ks + 1, 0xffffffffu);
+            // the k-th largest z is temper(the k-th largest y); a list of
+            // fewer than k holds every y above -inf, so the k-th is -inf
+            const float yk = n >= Ks ? zs_key_to_float(~(uint32_t)(sh.u.b.s[Ks - 1] >> 32)) : -INFINITY;
             thr = zs_temper(yk, T);
             thr_key = zs_total_key(thr);
             has_thr = 1;
@@ -1612,7 +1735,7 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
                     for (uint32_t i0 = 0; i0 < Ks; i0 += 64) {
                         const uint32_t i = i0 + t;
                         float zi = -INFINITY;
-                        if (i < Ks) zi = zs_temper(zs_key_to_float(~(uint32_t)(sh.u.b.s[i] >> 32)), T);
+                        if (i < Ks && i < n) zi = zs_temper(zs_key_to_float(~(uint32_t)(sh.u.b.s[i] >> 32)), T);
                         const bool sv = zi > -INFINITY;
                         const unsigned long long m = __ballot(sv);
                         if (sv) {
