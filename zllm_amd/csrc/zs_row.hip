@@ -81,6 +81,7 @@ struct rw_shared {
     uint32_t sel_hist[2][256];      // list selection: digit histogram (double buffered)
     uint32_t sel_mm[3][RW_NW];      // list selection: per-wave member count, key min / max
     uint32_t sel_n;                 // list selection: places taken by the gather
+    uint32_t inf_lim;               // observers: largest id whose -inf can enter the list
     uint32_t sel_st[4];             // list selection: chosen digit, count before it, its count, places
 };
 // The workgroup's LDS (one object, so that functions outside the kernel
@@ -116,6 +117,24 @@ __device__ __forceinline__ void rw_bar() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Ascending sort of the m <= 256 entries at buf by one wave (called by the 64
+// lanes of one wave; no barrier).
+template <int E>
+__device__ __forceinline__ void rw_wave_sort_e(unsigned long long* buf, uint32_t m) {
+    const uint32_t lane = (uint32_t)zs_lane();
+    unsigned long long k[E];
+#pragma unroll
+    for (int e = 0; e < E; e++) k[e] = lane * E + e < m ? buf[lane * E + e] : ~0ull;
+    wave_sort_u64_e<E>(k);
+#pragma unroll
+    for (int e = 0; e < E; e++) if (lane * E + e < m) buf[lane * E + e] = k[e];
+}
+__device__ __forceinline__ void rw_wave_sort(unsigned long long* buf, uint32_t m) {
+    if (m <= 64) rw_wave_sort_e<1>(buf, m);
+    else if (m <= 128) rw_wave_sort_e<2>(buf, m);
+    else rw_wave_sort_e<4>(buf, m);
 }
 
 // ---------------------------------------------------------------------------
@@ -159,12 +178,18 @@ __device__ __forceinline__ int rw_patches(const zs_sargs& a, uint32_t r, const z
     }
     __syncthreads();
     const uint32_t n = sh.n_ent;
-    uint32_t np2 = 1;
-    while (np2 < n) np2 <<= 1;
-    for (uint32_t i = n + t; i < np2; i += RW_NT) sh.u.ent[i] = ~0ull;
-    __syncthreads();
-    if (np2 > 2 * RW_NT) block_sort_reg_u64<RW_NT, 4>(sh.u.ent, np2);
-    else if (np2 > 1) block_sort_reg_u64<RW_NT, 2>(sh.u.ent, np2);
+    if (n <= 256) {
+        // a few hundred entries: one wave, no barriers between the stages
+        if (zs_wid() == 0 && n > 1) rw_wave_sort(sh.u.ent, n);
+        __syncthreads();
+    } else {
+        uint32_t np2 = 1;
+        while (np2 < n) np2 <<= 1;
+        for (uint32_t i = n + t; i < np2; i += RW_NT) sh.u.ent[i] = ~0ull;
+        __syncthreads();
+        if (np2 > 2 * RW_NT) block_sort_reg_u64<RW_NT, 4>(sh.u.ent, np2);
+        else block_sort_reg_u64<RW_NT, 2>(sh.u.ent, np2);
+    }
     uint32_t* out_id = a.p_id + (size_t)r * ZS_MAX_PATCHES;
     uint32_t* out_fl = a.p_flags + (size_t)r * ZS_MAX_PATCHES;
     float* out_y = a.p_y + (size_t)r * ZS_MAX_PATCHES;
@@ -404,6 +429,7 @@ struct rw_list {
 // number at most RW_SEL_CAP (always by the last digit: entries are
 // distinct); those are gathered to the front and sorted by one wave.
 #define RW_SEL_CAP 256
+
 __device__ __noinline__ uint32_t rw_select(int which, uint32_t n, uint32_t K1, uint32_t idlim) {
     rw_shared& sh = rw_sh;
     unsigned long long* buf = which ? sh.u.b.s : sh.u.b.o;
@@ -505,28 +531,7 @@ __device__ __noinline__ uint32_t rw_select(int which, uint32_t n, uint32_t K1, u
     }
     __syncthreads();
     const uint32_t m = rw_uni(sh.sel_n);
-    if (wid == 0) {
-        if (m <= 64) {
-            unsigned long long k[1];
-            k[0] = lane < m ? buf[lane] : NONE;
-            wave_sort_u64_e<1>(k);
-            if (lane < m) buf[lane] = k[0];
-        } else if (m <= 128) {
-            unsigned long long k[2];
-#pragma unroll
-            for (int e = 0; e < 2; e++) k[e] = lane * 2 + e < m ? buf[lane * 2 + e] : NONE;
-            wave_sort_u64_e<2>(k);
-#pragma unroll
-            for (int e = 0; e < 2; e++) if (lane * 2 + e < m) buf[lane * 2 + e] = k[e];
-        } else {
-            unsigned long long k[4];
-#pragma unroll
-            for (int e = 0; e < 4; e++) k[e] = lane * 4 + e < m ? buf[lane * 4 + e] : NONE;
-            wave_sort_u64_e<4>(k);
-#pragma unroll
-            for (int e = 0; e < 4; e++) if (lane * 4 + e < m) buf[lane * 4 + e] = k[e];
-        }
-    }
+    if (wid == 0) rw_wave_sort(buf, m);
     __syncthreads();
     return c;
 }
@@ -1378,6 +1383,7 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
     if (t == 0) {
         sh.fthr[0] = sh.fthr[1] = -INFINITY;
         sh.fcut[0] = sh.fcut[1] = -INFINITY;
+        sh.inf_lim = 0xffffffffu;
     }
     __syncthreads();
     uint32_t g = 0;
@@ -1436,11 +1442,29 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
                     const uint32_t so = wave_sort_u32(mo), ss = wave_sort_u32(ms);
                     const int co = max((int)((Ko + RW_NW - 1) / RW_NW), 1), cs = max((int)((Ks + RW_NW - 1) / RW_NW), 1);
                     const uint32_t wo = __shfl(so, 64 - co, 64), ws = __shfl(ss, 64 - cs, 64);
+                    // observers: -inf values rank by id, so once this tile holds
+                    // Ko of them, a -inf of a larger id than the Ko-th can never
+                    // be among the first Ko (masked rows are mostly -inf)
+                    uint32_t minf = 0;
+#pragma unroll
+                    for (int q = 0; q < 4; q++) minf |= (((vm >> q) & 1u) && x[q] == -INFINITY) ? (1u << q) : 0u;
+                    const uint32_t ninf = (uint32_t)__popc(minf), winf = wave_incl_scan_u(ninf);
+                    if (zs_lane() == 63) sh.ru[4][zs_wid()] = winf;
                     if (zs_lane() == 0) { sh.ru[2][zs_wid()] = wo; sh.ru[3][zs_wid()] = ws; }
                     rw_bar();
-                    uint32_t a0 = 0xffffffffu, a1 = 0xffffffffu;
+                    uint32_t a0 = 0xffffffffu, a1 = 0xffffffffu, ibefore = 0;
 #pragma unroll
-                    for (int w = 0; w < RW_NW; w++) { a0 = min(a0, sh.ru[2][w]); a1 = min(a1, sh.ru[3][w]); }
+                    for (int w = 0; w < RW_NW; w++) {
+                        a0 = min(a0, sh.ru[2][w]); a1 = min(a1, sh.ru[3][w]);
+                        ibefore += (uint32_t)w < (uint32_t)zs_wid() ? sh.ru[4][w] : 0u;
+                    }
+                    ibefore += winf - ninf;
+                    if (Ko && ibefore < Ko && Ko <= ibefore + ninf) {
+                        // the (Ko - ibefore)-th set bit of minf
+                        uint32_t mm = minf;
+                        for (uint32_t k = Ko - ibefore; k > 1; k--) mm &= mm - 1u;
+                        sh.inf_lim = idx0 + (uint32_t)(__ffs(mm) - 1);
+                    }
                     rw_bar();
                     if (t == 0) {
                         // observers: a bound at or below the key of -inf admits
@@ -1466,9 +1490,10 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
             {
                 const float tfo = rw_unif(sh.fthr[0]), tfs = rw_unif(sh.fthr[1]);
                 const bool allo = rw_uni(thr_o < 0 ? 1u : 0u) != 0u, alls = rw_uni(thr_s < 0 ? 1u : 0u) != 0u;
+                const uint32_t ilim = rw_uni(sh.inf_lim);
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    po |= (x[q] > tfo || allo) ? (1u << q) : 0u;
+                    po |= ((x[q] > tfo || allo) && (x[q] != -INFINITY || idx0 + q <= ilim)) ? (1u << q) : 0u;
                     if (smode == 1) {
                         const bool in = y[q] > tfs || alls;
                         ps |= in ? (1u << q) : 0u;
@@ -1570,7 +1595,7 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
                 uint32_t wo = 0, ws = 0;
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    wo |= (x[q] > tfo || allo) ? (1u << q) : 0u;
+                    wo |= ((x[q] > tfo || allo) && (x[q] != -INFINITY || idx0 + q <= sh.inf_lim)) ? (1u << q) : 0u;
                     if (smode == 1) {
                         const bool in = y[q] > tfs || alls;
                         ws |= in ? (1u << q) : 0u;
