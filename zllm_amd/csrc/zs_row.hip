@@ -9,7 +9,8 @@
 //   token = sample_with_rng(y, cfg, r)    sampler.rs:31-128
 //   logprobs / token_uncertainty on x~    logprobs.rs:34-54, hallucination.rs:129-154
 //
-// Phases of zs_k_row (row r = blockIdx.x):
+// Phases of zs_k_row (one row workgroup per row; the sampler's S of unmasked
+// rows without top-k in a helper workgroup beside it, see rw_helper):
 //   P0  patches: the row's ban / bias / count-map entries merged into one list
 //       sorted by id with the exact patched y of every listed id
 //       (decode_ctrl.rs:107-126 operation order), kept in LDS with a bitmap of
@@ -145,7 +146,8 @@ __device__ __forceinline__ void rw_wave_sort(unsigned long long* buf, uint32_t m
 // Returns the number of patched ids, or -1 when the row has more entries than
 // ZS_MAX_PATCHES.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ int rw_patches(const zs_sargs& a, uint32_t r, const zs_row_params& P, uint32_t& has_y, rw_shared& sh) {
+__device__ __forceinline__ int rw_patches(const zs_sargs& a, uint32_t r, const zs_row_params& P, uint32_t& has_y, rw_shared& sh,
+                                          bool wr = true) {
     const zs_batch& b = a.b;
     const uint32_t t = threadIdx.x, V = b.V;
     const uint32_t words = (V + 31) / 32;
@@ -161,8 +163,8 @@ __device__ __forceinline__ int rw_patches(const zs_sargs& a, uint32_t r, const z
     if (t == 0) sh.n_ent = 0;
     __syncthreads();
     if (total > ZS_MAX_PATCHES) {
-        if (t == 0) a.p_cnt[r] = 0;
-        for (uint32_t j = t; j <= nsub; j += RW_NT) psub[j] = 0;
+        if (wr && t == 0) a.p_cnt[r] = 0;
+        for (uint32_t j = t; wr && j <= nsub; j += RW_NT) psub[j] = 0;
         has_y = 0;
         return -1;
     }
@@ -237,9 +239,11 @@ __device__ __forceinline__ int rw_patches(const zs_sargs& a, uint32_t r, const z
                 fl |= ZS_PF_Y;
             }
             const uint32_t o = base_out + ex;
-            out_id[o] = id;
-            out_fl[o] = fl;
-            out_y[o] = y;
+            if (wr) {
+                out_id[o] = id;
+                out_fl[o] = fl;
+                out_y[o] = y;
+            }
             sh.pid[o] = id | (fl << RW_PF_SHIFT);
             sh.py[o] = y;
             atomicOr(&rw_pbits[id >> 5], 1u << (id & 31));
@@ -248,7 +252,7 @@ __device__ __forceinline__ int rw_patches(const zs_sargs& a, uint32_t r, const z
         base_out += tot;
     }
     has_y = block_or_u<RW_NT>(hy, sh.ru[1]);
-    if (t == 0) a.p_cnt[r] = base_out;
+    if (wr && t == 0) a.p_cnt[r] = base_out;
     // per-word prefix counts of the bitmap (words / RW_NT words per thread at most 8)
     {
         const uint32_t per = (words + RW_NT - 1) / RW_NT;
@@ -263,7 +267,7 @@ __device__ __forceinline__ int rw_patches(const zs_sargs& a, uint32_t r, const z
         }
     }
     // first patch of every 1024-id sub-chunk (read by zs_k_big / zs_k_final)
-    for (uint32_t j = t; j <= nsub; j += RW_NT) {
+    for (uint32_t j = t; wr && j <= nsub; j += RW_NT) {
         uint32_t lo = 0, hi = base_out;
         const uint32_t key = j * ZS_SUB;
         while (lo < hi) {
@@ -1240,8 +1244,9 @@ __device__ __noinline__ float rw_pass_ent(const float* row, const float* allow, 
 // written to row scratch: the sums then run over these values only (a
 // masked id's term is zero, which leaves a running sum unchanged). cx, cy
 // hold round_up(n, 4) values each (the tail padded with -inf); cy = cx +
-// round_up(n, 4). Returns n, or 0 when no id or more than a quarter of the
-// row is allowed (then the sums run over the whole row). Uniform.
+// round_up(n, 4); the ids follow at cy + round_up(n, 4). Returns n, or 0
+// when no id or more than a quarter of the row is allowed (then the sums run
+// over the whole row). Uniform.
 __device__ __noinline__ uint32_t rw_gather_allowed(const float* row, const uint32_t* allow, uint32_t V, uint32_t np,
                                                    float* cx) {
     rw_shared& sh = rw_sh;
@@ -1257,7 +1262,7 @@ __device__ __noinline__ uint32_t rw_gather_allowed(const float* row, const uint3
     uint32_t n;
     uint32_t pos = block_excl_scan_u<RW_NT>(c, sh.ru[4], &n);
     n = rw_uni(n);
-    if (n == 0 || n > V / 4) return 0;
+    if (n == 0 || n > V / 4 || V < 16) return 0;   // V >= 16: 3 round_up(n, 4) + 3 values fit 2 V
     const uint32_t n4 = (n + 3) & ~3u;
     float* cy = cx + n4;
     for (uint32_t w = w0; w < w1; w++) {
@@ -1277,6 +1282,7 @@ __device__ __noinline__ uint32_t rw_gather_allowed(const float* row, const uint3
             }
             cx[pos] = x;
             cy[pos] = y;
+            reinterpret_cast<uint32_t*>(cy + n4)[pos] = id;
             pos++;
         }
     }
@@ -1294,12 +1300,140 @@ __device__ __noinline__ void rw_small(uint64_t seed, uint64_t counter, uint32_t 
 }
 
 // ---------------------------------------------------------------------------
+// The sampler's S of an unmasked row without a top-k cut (the longest of a
+// row's sums) runs in a workgroup of its own, beside the workgroup that does
+// the row's other phases: zs_k_row is launched with 2B workgroups, the first
+// B taking the rows (unmasked rows first: theirs are the long sums), the
+// other B being these helpers (a row that does not qualify ends its helper
+// at once). Workgroups start in index order, so the helpers take the CUs of
+// the first rows to finish (masked rows with few allowed ids) while the
+// unmasked rows are still running.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ bool rw_helped(const zs_batch& b, const zs_row_params& P) {
+    const float T = P.temperature;
+    const bool masked = (P.flags & ZS_ROW_MASKED) && b.d_allow_bits;
+    const bool has_topk = P.top_k > 0 && P.top_k < b.V;
+    return !masked && T > 0.0f && T != INFINITY && !has_topk;
+}
+
+// The row of the j-th row workgroup: the unmasked rows in index order, then
+// the masked ones. Uniform.
+__device__ __noinline__ uint32_t rw_block_row(const zs_batch& b, uint32_t j) {
+    if (!b.d_allow_bits || b.B > 4 * RW_NT) return j;
+    rw_shared& sh = rw_sh;
+    const uint32_t t = threadIdx.x, lane = (uint32_t)zs_lane(), wid = (uint32_t)zs_wid();
+    const uint32_t nchunk = (b.B + RW_NT - 1) / RW_NT;
+    uint32_t rank[4], um = 0;      // rank among the rows of its kind; bit c: unmasked
+    uint32_t carry = 0;            // unmasked rows in the chunks before
+#pragma unroll
+    for (uint32_t c = 0; c < 4; c++) {
+        rank[c] = 0;
+        if (c >= nchunk) continue;
+        const uint32_t i = c * RW_NT + t;
+        const bool in = i < b.B;
+        const bool u = in && !(b.d_params[i].flags & ZS_ROW_MASKED);
+        const unsigned long long m = __ballot(u);
+        if (lane == 0) sh.sel_mm[0][wid] = (uint32_t)__popcll(m);
+        __syncthreads();
+        uint32_t before = carry, tot = 0;
+#pragma unroll
+        for (int w = 0; w < RW_NW; w++) {
+            const uint32_t k = sh.sel_mm[0][w];
+            before += (uint32_t)w < wid ? k : 0u;
+            tot += k;
+        }
+        __syncthreads();
+        before += (uint32_t)__popcll(m & ((1ull << lane) - 1ull));
+        rank[c] = u ? before : i - before;   // masked: rows before it minus unmasked before it
+        um |= u ? (1u << c) : 0u;
+        carry += tot;
+    }
+    const uint32_t nu = carry;
+    if (t == 0) sh.sel_n = j;   // fallback (not reached: every j < B has a row)
+    __syncthreads();
+#pragma unroll
+    for (uint32_t c = 0; c < 4; c++) {
+        const uint32_t i = c * RW_NT + t;
+        if (c >= nchunk || i >= b.B) continue;
+        const uint32_t pos = ((um >> c) & 1u) ? rank[c] : nu + rank[c];
+        if (pos == j) sh.sel_n = i;
+    }
+    __syncthreads();
+    const uint32_t r = rw_uni(sh.sel_n);
+    __syncthreads();
+    return r;
+}
+
+// The helper: patches (LDS only), the maximum of y, then the sampler's S
+// into the row state (zs_k_row's row workgroup skips that pass and leaves
+// samp_S alone). A row whose y holds a NaN, or whose maximum z is infinite,
+// is not sampled from S (non-finite rows): the helper stops.
+__device__ __noinline__ void rw_helper(const zs_sargs& a, uint32_t r) {
+    const zs_batch& b = a.b;
+    const zs_row_params P = b.d_params[r];
+    if (!rw_helped(b, P)) return;
+    rw_shared& sh = rw_sh;
+    const uint32_t t = threadIdx.x, V = b.V;
+    const float T = P.temperature;
+    uint32_t has_y = 0;
+    const int np = rw_patches(a, r, P, has_y, sh, false);
+    if (np < 0) return;
+    rw_row R;
+    R.row = b.d_logits + (size_t)r * b.ld;
+    R.allow = nullptr;
+    R.V = V;
+    R.np = rw_uni((uint32_t)np);
+    R.words = (V + 31) / 32;
+    R.ldm4 = (uint32_t)min((uint64_t)b.ld - 4, (uint64_t)0xfffffff0u);
+    R.allow_or_row = reinterpret_cast<const uint32_t*>(R.row);
+    R.wmax = R.ldm4;
+    R.amask = 15u;
+    R.glast = (V - 1) / RW_G;
+    float ymax = -INFINITY;
+    uint32_t nan = 0;
+    rw_stream(R, sh, 0, [&](uint32_t, int, const float (&x)[4], const float (&y)[4]) {
+        ymax = fmaxf(ymax, fmaxf(fmaxf(y[0], y[1]), fmaxf(y[2], y[3])));
+#pragma unroll
+        for (int q = 0; q < 4; q++) nan |= (y[q] != y[q]) ? 1u : 0u;
+        (void)x;
+        return false;
+    });
+    for (int d = 32; d > 0; d >>= 1) {
+        ymax = fmaxf(ymax, __shfl_xor(ymax, d, 64));
+        nan |= __shfl_xor(nan, d, 64);
+    }
+    if (zs_lane() == 0) { sh.rf[0][zs_wid()] = ymax; sh.ru[0][zs_wid()] = nan; }
+    __syncthreads();
+    ymax = -INFINITY; nan = 0;
+#pragma unroll
+    for (int w = 0; w < RW_NW; w++) { ymax = fmaxf(ymax, sh.rf[0][w]); nan |= sh.ru[0][w]; }
+    __syncthreads();
+    const float zmax = rw_unif(zs_temper(ymax, T));
+    if (rw_uni(nan) || zmax == INFINITY || zmax == -INFINITY) return;
+    const uint32_t ng = (V + RW_G - 1) / RW_G;
+    float SB = -0.0f;
+    uint32_t g = 0, slow = 0;
+    while (true) {
+        SB = rw_pass_samp(R.row, nullptr, V, R.np, R.ldm4, T, zmax, -INFINITY, 0u, SB, g, slow);
+        if (slow) { g++; slow = 0; continue; }
+        g = rw_uni(sh.pass_g);
+        if (g >= ng) break;
+        slow = 1;
+    }
+    if (t == 0) a.rst[r].samp_S = SB;
+}
+
+// ---------------------------------------------------------------------------
 // zs_k_row
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
-    const uint32_t r = blockIdx.x;
-    const uint32_t t = threadIdx.x;
     const zs_batch& b = a.b;
+    if (blockIdx.x >= b.B) {
+        rw_helper(a, blockIdx.x - b.B);
+        return;
+    }
+    const uint32_t r = rw_block_row(b, blockIdx.x);
+    const uint32_t t = threadIdx.x;
     const uint32_t V = b.V;
     rw_shared& sh = rw_sh;
     __shared__ uint32_t cnt_o[3], cnt_s[3], flag_o, flag_s;
@@ -1386,8 +1520,58 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
         sh.inf_lim = 0xffffffffu;
     }
     __syncthreads();
+    // A masked row with at most RW_BUF allowed ids (every other x~ and y is
+    // -inf) takes its statistics and lists from the allowed ids alone,
+    // gathered in index order to row scratch (which the sums reuse): the
+    // lists then hold every allowed id (observers) and every y above -inf
+    // (sampler), of which the selections take the same first entries as from
+    // the whole row. Not for greedy rows (the last maximal element may be a
+    // masked -inf), T = inf (a masked y / T is NaN) or rows with fewer than
+    // Ko finite x~ (their observers' list ends with -inf ids of the whole
+    // row).
+    // row scratch of the big-row kernels (not in use before they run),
+    // 16-byte aligned
+    float* gcx = reinterpret_cast<float*>(a.pairs + (size_t)r * a.max_vocab * 2);
+    gcx += (4u - (uint32_t)((reinterpret_cast<uintptr_t>(gcx) >> 2) & 3u)) & 3u;
+    uint32_t gn = 0;
+    bool gdone = false, gath = false;
+    if (R.allow && !greedy && !tinf) {
+        gn = rw_gather_allowed(R.row, R.allow, V, R.np, gcx);
+        gdone = true;
+        if (gn && gn <= RW_BUF) {
+            uint32_t nf = 0;
+            for (uint32_t i = t; i < gn; i += RW_NT) nf += gcx[i] > -INFINITY ? 1u : 0u;
+            nf = block_sum_u<RW_NT>(nf, sh.ru[4]);
+            gath = rw_uni(nf) >= Ko;
+        }
+    }
     uint32_t g = 0;
-    const uint32_t ng = (V + RW_G - 1) / RW_G;
+    const uint32_t ng = gath ? 0u : (V + RW_G - 1) / RW_G;
+    if (gath) {
+        const uint32_t gn4 = (gn + 3) & ~3u;
+        const float* gy = gcx + gn4;
+        const uint32_t* gid = reinterpret_cast<const uint32_t*>(gy + gn4);
+        for (uint32_t i = t; i < gn; i += RW_NT) {
+            const float x = gcx[i], y = gy[i];
+            const uint32_t id = gid[i];
+            omax = fmaxf(omax, x);
+            ymax = fmaxf(ymax, y);
+            if (x != x) fl |= ZS_CF_OBS_NAN;
+            if (y != y) {
+                fl |= ZS_CF_Z_NAN;
+                last_nan = max(last_nan, (int)id);
+            }
+            if (Ko) LO.buf[i] = ((unsigned long long)(~zs_total_key(x + 0.0f)) << 32) | id;
+            if (smode != 0 && y > -INFINITY) {
+                const uint32_t p = atomicAdd(&cnt_s[0], 1u);
+                if (smode == 1 || p < ZS_SMALL_CAP) LS.buf[p] = ((unsigned long long)(~zs_total_key(y)) << 32) | id;
+            }
+        }
+        __syncthreads();
+        n_o = Ko ? gn : 0u;
+        n_s = rw_uni(cnt_s[0]);
+        if (smode == 2 && n_s > ZS_SMALL_CAP) s_over = true;
+    }
     while (g < ng) {
         g = rw_stream(R, sh, g, [&](uint32_t g, int u, const float (&x)[4], const float (&y)[4]) {
             const uint32_t idx0 = g * RW_G + 4 * t;
@@ -1830,11 +2014,8 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
     const float* py = R.row;
     uint32_t pV = V, pnp = R.np, pldm4 = R.ldm4;
     if (R.allow && (doA || doB || (obs_need & ZS_OBS_H))) {
-        // row scratch of the big-row kernels (not in use before they run),
-        // 16-byte aligned
-        float* cx = reinterpret_cast<float*>(a.pairs + (size_t)r * a.max_vocab * 2);
-        cx += (4u - (uint32_t)((reinterpret_cast<uintptr_t>(cx) >> 2) & 3u)) & 3u;
-        const uint32_t n = rw_gather_allowed(R.row, R.allow, V, R.np, cx);
+        float* cx = gcx;
+        const uint32_t n = gdone ? gn : rw_gather_allowed(R.row, R.allow, V, R.np, cx);
         if (n) {
             const uint32_t n4 = (n + 3) & ~3u;
             px = cx;
@@ -1858,7 +2039,8 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
             slow = 1;
         }
     }
-    if (doB) {
+    const bool helped = rw_helped(b, P);   // the helper workgroup sums S (same rule, same inputs)
+    if (doB && !helped) {
         const uint32_t use_thr = has_thr != 0 ? 1u : 0u;
         uint32_t g = 0, slow = 0;
         while (true) {
@@ -1902,7 +2084,7 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
         st.z_is_x = 0;
         st.klist = 0;
         st.kpend = 0;
-        st.samp_S = SB;
+        if (!helped) st.samp_S = SB;
         st.obs_S = SA;
         st.obs_H = H;
     }
@@ -1917,6 +2099,6 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
 
 extern "C" int zs_row_launch(const zs_sargs& a, hipStream_t stream) {
     const size_t dyn = 2 * ((a.b.V + 31) / 32) * sizeof(uint32_t);
-    hipLaunchKernelGGL(zs_k_row, dim3(a.b.B), dim3(RW_NT), dyn, stream, a);
+    hipLaunchKernelGGL(zs_k_row, dim3(2 * a.b.B), dim3(RW_NT), dyn, stream, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
