@@ -1302,18 +1302,19 @@ __device__ __noinline__ void rw_small(uint64_t seed, uint64_t counter, uint32_t 
 // ---------------------------------------------------------------------------
 // The sampler's S of an unmasked row without a top-k cut (the longest of a
 // row's sums) runs in a workgroup of its own, beside the workgroup that does
-// the row's other phases: zs_k_row is launched with 2B workgroups, the first
-// B taking the rows (unmasked rows first: theirs are the long sums), the
+// the row's other phases (when zs_sargs.helpers is set): zs_k_row is launched
+// with 2B workgroups, the first B taking the rows (unmasked rows first: theirs are the long sums), the
 // other B being these helpers (a row that does not qualify ends its helper
 // at once). Workgroups start in index order, so the helpers take the CUs of
 // the first rows to finish (masked rows with few allowed ids) while the
 // unmasked rows are still running.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ bool rw_helped(const zs_batch& b, const zs_row_params& P) {
+__device__ __forceinline__ bool rw_helped(const zs_sargs& a, const zs_row_params& P) {
+    const zs_batch& b = a.b;
     const float T = P.temperature;
     const bool masked = (P.flags & ZS_ROW_MASKED) && b.d_allow_bits;
     const bool has_topk = P.top_k > 0 && P.top_k < b.V;
-    return !masked && T > 0.0f && T != INFINITY && !has_topk;
+    return a.helpers && !masked && T > 0.0f && T != INFINITY && !has_topk;
 }
 
 // The row of the j-th row workgroup: the unmasked rows in index order, then
@@ -1371,7 +1372,7 @@ __device__ __noinline__ uint32_t rw_block_row(const zs_batch& b, uint32_t j) {
 __device__ __noinline__ void rw_helper(const zs_sargs& a, uint32_t r) {
     const zs_batch& b = a.b;
     const zs_row_params P = b.d_params[r];
-    if (!rw_helped(b, P)) return;
+    if (!rw_helped(a, P)) return;
     rw_shared& sh = rw_sh;
     const uint32_t t = threadIdx.x, V = b.V;
     const float T = P.temperature;
@@ -2039,7 +2040,7 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
             slow = 1;
         }
     }
-    const bool helped = rw_helped(b, P);   // the helper workgroup sums S (same rule, same inputs)
+    const bool helped = rw_helped(a, P);   // the helper workgroup sums S (same rule, same inputs)
     if (doB && !helped) {
         const uint32_t use_thr = has_thr != 0 ? 1u : 0u;
         uint32_t g = 0, slow = 0;
@@ -2099,6 +2100,6 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
 
 extern "C" int zs_row_launch(const zs_sargs& a, hipStream_t stream) {
     const size_t dyn = 2 * ((a.b.V + 31) / 32) * sizeof(uint32_t);
-    hipLaunchKernelGGL(zs_k_row, dim3(2 * a.b.B), dim3(RW_NT), dyn, stream, a);
+    hipLaunchKernelGGL(zs_k_row, dim3(a.helpers ? 2 * a.b.B : a.b.B), dim3(RW_NT), dyn, stream, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

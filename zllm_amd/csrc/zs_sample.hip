@@ -1673,6 +1673,10 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
     a.tp_cl = ctx->tp_cl;
     a.tp_pre = ctx->tp_pre;
     a.kcnt = ctx->kcnt;
+    // helper workgroups shorten the row kernel but add work (each repeats its
+    // row's patches and maximum): worth it when the sampler has the GPU to
+    // itself, not when the caller runs other work beside it (pass_event)
+    a.helpers = bt->pass_event ? 0u : 1u;
     const uint32_t B = bt->B;
     const uint32_t nch = (bt->V + ZS_P1_CH - 1) / ZS_P1_CH;
     const bool prof = ctx->profiling != 0;

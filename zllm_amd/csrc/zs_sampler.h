@@ -26,6 +26,7 @@ struct zs_sargs {
     uint32_t* tp_cl;
     uint32_t* tp_pre;
     uint32_t* kcnt;
+    uint32_t helpers;   // zs_k_row: helper workgroups for the longest sums (0 / 1)
 };
 
 #define ZS_ST_FALLBACK 0x200u
