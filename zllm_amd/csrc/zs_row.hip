@@ -83,6 +83,7 @@ struct rw_shared {
     uint32_t sel_mm[3][RW_NW];      // list selection: per-wave member count, key min / max
     uint32_t sel_n;                 // list selection: places taken by the gather
     uint32_t inf_lim;               // observers: largest id whose -inf can enter the list
+    uint32_t g_n, g_done;           // masked rows: allowed ids gathered to row scratch, gather done
     uint32_t sel_st[4];             // list selection: chosen digit, count before it, its count, places
 };
 // The workgroup's LDS (one object, so that functions outside the kernel
@@ -1240,6 +1241,13 @@ __device__ __noinline__ float rw_pass_ent(const float* row, const float* allow, 
     return rw_pass(rw_row_of(row, allow, V, np, ldm4), f, s, g, slow, 0u);
 }
 
+// Row scratch of the big-row kernels (not in use before they run), 16-byte
+// aligned: a masked row's gathered values.
+__device__ __forceinline__ float* rw_scratch(const zs_sargs& a, uint32_t r) {
+    float* cx = reinterpret_cast<float*>(a.pairs + (size_t)r * a.max_vocab * 2);
+    return cx + ((4u - (uint32_t)((reinterpret_cast<uintptr_t>(cx) >> 2) & 3u)) & 3u);
+}
+
 // A masked row's allowed ids in index order, with their x~ (cx) and y (cy)
 // written to row scratch: the sums then run over these values only (a
 // masked id's term is zero, which leaves a running sum unchanged). cx, cy
@@ -1319,7 +1327,7 @@ __device__ __forceinline__ bool rw_helped(const zs_sargs& a, const zs_row_params
 
 // The row of the j-th row workgroup: the unmasked rows in index order, then
 // the masked ones. Uniform.
-__device__ __noinline__ uint32_t rw_block_row(const zs_batch& b, uint32_t j) {
+__device__ __forceinline__ uint32_t rw_block_row(const zs_batch& b, uint32_t j) {
     if (!b.d_allow_bits || b.B > 4 * RW_NT) return j;
     rw_shared& sh = rw_sh;
     const uint32_t t = threadIdx.x, lane = (uint32_t)zs_lane(), wid = (uint32_t)zs_wid();
@@ -1369,7 +1377,7 @@ __device__ __noinline__ uint32_t rw_block_row(const zs_batch& b, uint32_t j) {
 // into the row state (zs_k_row's row workgroup skips that pass and leaves
 // samp_S alone). A row whose y holds a NaN, or whose maximum z is infinite,
 // is not sampled from S (non-finite rows): the helper stops.
-__device__ __noinline__ void rw_helper(const zs_sargs& a, uint32_t r) {
+__device__ __forceinline__ void rw_helper(const zs_sargs& a, uint32_t r) {
     const zs_batch& b = a.b;
     const zs_row_params P = b.d_params[r];
     if (!rw_helped(a, P)) return;
@@ -1530,15 +1538,14 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
     // masked -inf), T = inf (a masked y / T is NaN) or rows with fewer than
     // Ko finite x~ (their observers' list ends with -inf ids of the whole
     // row).
-    // row scratch of the big-row kernels (not in use before they run),
-    // 16-byte aligned
-    float* gcx = reinterpret_cast<float*>(a.pairs + (size_t)r * a.max_vocab * 2);
-    gcx += (4u - (uint32_t)((reinterpret_cast<uintptr_t>(gcx) >> 2) & 3u)) & 3u;
-    uint32_t gn = 0;
-    bool gdone = false, gath = false;
+    // (the gathered count and whether the gather ran are kept in LDS: few
+    // values stay live across the stream below)
+    bool gath = false;
+    if (t == 0) { sh.g_n = 0; sh.g_done = 0; }
     if (R.allow && !greedy && !tinf) {
-        gn = rw_gather_allowed(R.row, R.allow, V, R.np, gcx);
-        gdone = true;
+        const float* gcx = rw_scratch(a, r);
+        const uint32_t gn = rw_gather_allowed(R.row, R.allow, V, R.np, rw_scratch(a, r));
+        if (t == 0) { sh.g_n = gn; sh.g_done = 1; }
         if (gn && gn <= RW_BUF) {
             uint32_t nf = 0;
             for (uint32_t i = t; i < gn; i += RW_NT) nf += gcx[i] > -INFINITY ? 1u : 0u;
@@ -1549,6 +1556,8 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
     uint32_t g = 0;
     const uint32_t ng = gath ? 0u : (V + RW_G - 1) / RW_G;
     if (gath) {
+        const float* gcx = rw_scratch(a, r);
+        const uint32_t gn = rw_uni(sh.g_n);
         const uint32_t gn4 = (gn + 3) & ~3u;
         const float* gy = gcx + gn4;
         const uint32_t* gid = reinterpret_cast<const uint32_t*>(gy + gn4);
@@ -2015,8 +2024,8 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
     const float* py = R.row;
     uint32_t pV = V, pnp = R.np, pldm4 = R.ldm4;
     if (R.allow && (doA || doB || (obs_need & ZS_OBS_H))) {
-        float* cx = gcx;
-        const uint32_t n = gdone ? gn : rw_gather_allowed(R.row, R.allow, V, R.np, cx);
+        float* cx = rw_scratch(a, r);
+        const uint32_t n = rw_uni(sh.g_done) ? rw_uni(sh.g_n) : rw_gather_allowed(R.row, R.allow, V, R.np, cx);
         if (n) {
             const uint32_t n4 = (n + 3) & ~3u;
             px = cx;
