@@ -109,8 +109,8 @@ SPEC_K = 4
 # HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
 # (profiles/c5_traffic.md), scaled by the copy-kernel calibration there; None
 # where not measured
-TRAFFIC = {"zs_k_spec_chunk": 1402.3e6, "zs_k_row": 706.2e6, "zs_k_pv": 106.5e6, "zs_k_tp_inc": 55.9e6,
-           "zs_k_big": 0.8e6}
+TRAFFIC = {"zs_k_spec_chunk": 1402.3e6, "zs_k_row": 572.3e6, "zs_k_pv": 64.1e6, "zs_k_tp_inc": 36.3e6,
+           "zs_k_big": 0.5e6}
 
 
 def spec_bytes_per_row(V, k):
