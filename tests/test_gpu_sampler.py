@@ -196,3 +196,63 @@ def test_patch_limit_fails_cleanly():
     bs = BatchSampler(ctx(max(64, B), 151936))
     with pytest.raises(RuntimeError, match="ZS_ST_LIMIT"):
         bs.step(torch.from_numpy(x).cuda(), make_rows(params))
+
+
+def test_masked_rows_gathered_p1():
+    """Masked rows with at most 2048 allowed ids take their statistics and
+    lists from the gathered allowed ids; rows with fewer than 28 finite
+    allowed values (the observers' list then ends with -inf ids of the whole
+    row), more than 2048 allowed ids, greedy rows and NaN rows take the
+    whole-row path. Bans, biases and counts on allowed and masked ids."""
+    from oracle import oracle as O
+    V = 30000
+    rng = np.random.default_rng(41)
+    x = synth.logits_powerlaw(10, V, 41)
+    counts_allowed = [20, 500, 1500, 300, 2048, 2049, 100, 600, 30, 1200]
+    allow = np.zeros((10, V), bool)
+    for i, c in enumerate(counts_allowed):
+        allow[i, rng.choice(V, c, replace=False)] = True
+    ids1 = np.nonzero(allow[1])[0]
+    x[1, ids1[7]] = np.nan                         # a NaN among the allowed ids
+    ids8 = np.nonzero(allow[8])[0]
+    x[8, ids8[:10]] = -np.inf                      # 20 finite allowed values: fewer than 28
+    ids2 = np.nonzero(allow[2])[0]
+    bits = np.stack([O.pack_bits(a) for a in allow])
+    base = dict(temperature=0.9, top_k=0, top_p=0.95, masked=True, top_logprobs=5)
+    params = [dict(base, seed=700 + i) for i in range(10)]
+    params[2].update(ban=[int(v) for v in ids2[:40:3]], bias=[(int(ids2[5]), 2.5), (int(ids2[50]), -1.0), (3, 9.0)],
+                     counts=[(int(v), 2) for v in ids2[100:140]], presence=0.3, frequency=0.2)
+    params[3].update(temperature=0.0)
+    params[4].update(top_k=50)
+    params[5].update(top_k=20, top_p=0.8)
+    params[6].update(top_k=200)
+    params[7].update(min_p=0.05, top_p=1.0)
+    params[9].update(counts=[(int(v), 1) for v in rng.choice(V, 64, replace=False)], repeat=1.3)
+    _run(x, params, allow_bits=bits, allow=allow)
+
+
+def test_helper_workgroups_match_one_per_row():
+    """The sampler with helper workgroups (no pass_event) and with one
+    workgroup per row (pass_event given) gives identical outputs."""
+    import torch
+    from tests.gpu_util import ctx, make_rows
+    from zllm_amd.engine import BatchSampler
+    B, V = 8, 151936
+    x = synth.logits_powerlaw(B, V, 43)
+    params = [dict(temperature=[0.7, 1.0, 1.3, 1.0][i % 4], top_k=0, top_p=[1.0, 0.9][i % 2], seed=800 + i,
+                   top_logprobs=5, counts=[(i * 97 + j * 13, 1 + j % 3) for j in range(50)], presence=0.2)
+              for i in range(B)]
+    c = ctx(64, V)
+    xs = torch.from_numpy(x).cuda()
+    bs = BatchSampler(c)
+    bufs = bs.pack(xs, make_rows(params))
+    a = bs.run(xs, bufs)
+    ev = torch.cuda.Event()
+    ev.record()
+    b = bs.run(xs, bufs, pass_event=ev)
+    torch.cuda.synchronize()
+    for k in a:
+        assert np.array_equal(a[k].cpu().numpy().view(np.uint8), b[k].cpu().numpy().view(np.uint8)), k
+    from tests.gpu_util import compare
+    errs = compare(x, params, {k: v.cpu().numpy() for k, v in a.items()})
+    assert not errs, "\n".join(errs[:20])
