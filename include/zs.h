@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define ZS_ABI_VERSION 1
+#define ZS_ABI_VERSION 2   /* 2: zs_batch gained pass_event */
 
 #define ZS_OK 0
 #define ZS_EINVAL (-1)   /* bad argument (null pointer, size out of range) */
@@ -44,6 +44,20 @@ typedef struct zs_dfa zs_dfa;
  * the reference has no FFI (docs/PLUGIN_PLAN.md:93-136 sketches a versioned
  * C ABI that was never implemented). */
 int zs_abi_version(void);
+
+/* Layout of the ABI's structs as this library was compiled: `which` is one of
+ * ZS_LAYOUT_*; writes sizeof into *size and the offset of each field, in
+ * declaration order, into offsets[0 .. min(cap, nfields)); returns the number
+ * of fields, or ZS_EINVAL for an unknown `which`. A binding (Rust, ctypes)
+ * checks its own #[repr(C)] / Structure layout against it once at load time.
+ * New entry point; no counterpart in the reference (docs/PLUGIN_PLAN.md:101-131
+ * asks for a versioned ABI). */
+#define ZS_LAYOUT_BATCH 0
+#define ZS_LAYOUT_ROW_PARAMS 1
+#define ZS_LAYOUT_SPEC_BATCH 2
+#define ZS_LAYOUT_LANE_STREAM 3
+#define ZS_LAYOUT_HALLUC_REPORT 4
+int zs_struct_layout(int which, size_t* size, size_t* offsets, size_t cap);
 
 /* Context on HIP device `device`, with scratch sized for batches of up to
  * max_rows rows of up to max_vocab logits. */

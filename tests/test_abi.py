@@ -43,7 +43,25 @@ def test_library_exports_every_declared_symbol(libzs):
 
 def test_abi_version(libzs):
     libzs.zs_abi_version.restype = ctypes.c_int
-    assert libzs.zs_abi_version() == 1
+    assert libzs.zs_abi_version() == 2
+
+
+def test_struct_layouts_match_binding(libzs):
+    """sizeof and every field offset of the ABI structs, as compiled into the
+    library, equal the ctypes binding's (the Rust binding in INTEGRATION.md
+    mirrors the same field lists)."""
+    from zllm_amd import _lib
+    fn = libzs.zs_struct_layout
+    fn.restype = ctypes.c_int
+    fn.argtypes = _lib.SIGNATURES["zs_struct_layout"][1]
+    assert _lib.layout_mismatches(libzs) == []
+    # the batch ends with the pass_event pointer that ABI 2 added
+    size = ctypes.c_size_t()
+    offs = (ctypes.c_size_t * 64)()
+    n = fn(0, ctypes.byref(size), offs, 64)
+    assert n == len(_lib.Batch._fields_) and _lib.Batch._fields_[-1][0] == "pass_event"
+    assert offs[n - 1] + 8 == size.value
+    assert fn(99, ctypes.byref(size), offs, 64) == -1
 
 
 def test_python_binding_covers_header():

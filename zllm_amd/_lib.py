@@ -103,6 +103,7 @@ class HallucReport(C.Structure):
 # name -> (restype, argtypes); every symbol include/zs.h declares
 SIGNATURES = {
     "zs_abi_version": (C.c_int, []),
+    "zs_struct_layout": (C.c_int, [C.c_int, C.POINTER(C.c_size_t), C.POINTER(C.c_size_t), C.c_size_t]),
     "zs_ctx_create": (C.c_int, [C.c_int, C.c_uint32, C.c_uint32, C.POINTER(C.c_void_p)]),
     "zs_ctx_destroy": (None, [C.c_void_p]),
     "zs_last_error": (C.c_char_p, [C.c_void_p]),
@@ -163,6 +164,33 @@ SIGNATURES = {
                                               C.c_size_t, C.POINTER(C.c_size_t), C.c_char_p, C.c_size_t]),
 }
 
+# ABI version the Structures above describe (include/zs.h ZS_ABI_VERSION)
+ABI_VERSION = 2
+
+# zs_struct_layout ids (ZS_LAYOUT_*) of the Structures above
+LAYOUTS = {0: Batch, 1: RowParams, 2: SpecBatch, 3: LaneStream, 4: HallucReport}
+
+
+def layout_mismatches(lib_):
+    """Differences between each ctypes Structure and the library's own layout
+    of the struct (size and every field offset), as text; empty when equal."""
+    out = []
+    for which, cls in LAYOUTS.items():
+        size = C.c_size_t()
+        offs = (C.c_size_t * 64)()
+        n = lib_.zs_struct_layout(which, C.byref(size), offs, 64)
+        fields = [f[0] for f in cls._fields_]
+        if n != len(fields):
+            out.append(f"{cls.__name__}: {n} fields in the library, {len(fields)} here")
+            continue
+        if size.value != C.sizeof(cls):
+            out.append(f"{cls.__name__}: size {size.value} != {C.sizeof(cls)}")
+        for i, f in enumerate(fields):
+            if offs[i] != getattr(cls, f).offset:
+                out.append(f"{cls.__name__}.{f}: offset {offs[i]} != {getattr(cls, f).offset}")
+    return out
+
+
 _lib = None
 
 
@@ -181,5 +209,10 @@ def lib():
             fn = getattr(lib_, name)
             fn.restype = res
             fn.argtypes = args
+        if lib_.zs_abi_version() != ABI_VERSION:
+            raise ZsError(f"libzs ABI {lib_.zs_abi_version()} != binding ABI {ABI_VERSION}")
+        bad = layout_mismatches(lib_)
+        if bad:
+            raise ZsError("libzs struct layout differs from the ctypes binding: " + "; ".join(bad))
         _lib = lib_
     return _lib

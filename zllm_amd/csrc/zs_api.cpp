@@ -1,3 +1,4 @@
+#include <stddef.h>
 // zs_api.cpp -- host side of libzs: contexts, token tables, DFAs (liveness on
 // the host), argument validation, and the C entry points of include/zs.h.
 #include <hip/hip_runtime.h>
@@ -55,6 +56,52 @@ static int zs_alloc(zs_ctx* ctx, T** p, size_t n) {
 }
 
 extern "C" int zs_abi_version(void) { return ZS_ABI_VERSION; }
+
+// Field offsets of the ABI structs, in declaration order.
+#define ZS_OFF(T, f) offsetof(T, f)
+extern "C" int zs_struct_layout(int which, size_t* size, size_t* offsets, size_t cap) {
+    static const size_t batch[] = {
+        ZS_OFF(zs_batch, B), ZS_OFF(zs_batch, V), ZS_OFF(zs_batch, ld), ZS_OFF(zs_batch, d_logits),
+        ZS_OFF(zs_batch, d_params), ZS_OFF(zs_batch, d_cnt_off), ZS_OFF(zs_batch, d_cnt_ids),
+        ZS_OFF(zs_batch, d_cnt_vals), ZS_OFF(zs_batch, d_bias_off), ZS_OFF(zs_batch, d_bias_ids),
+        ZS_OFF(zs_batch, d_bias_vals), ZS_OFF(zs_batch, d_ban_off), ZS_OFF(zs_batch, d_ban_ids),
+        ZS_OFF(zs_batch, d_allow_bits), ZS_OFF(zs_batch, allow_words), ZS_OFF(zs_batch, top_stride),
+        ZS_OFF(zs_batch, d_seed), ZS_OFF(zs_batch, d_counter), ZS_OFF(zs_batch, d_token),
+        ZS_OFF(zs_batch, d_logprob), ZS_OFF(zs_batch, d_top_ids), ZS_OFF(zs_batch, d_top_lps),
+        ZS_OFF(zs_batch, d_top_n), ZS_OFF(zs_batch, d_entropy), ZS_OFF(zs_batch, d_max_prob),
+        ZS_OFF(zs_batch, d_margin), ZS_OFF(zs_batch, d_chosen_lp), ZS_OFF(zs_batch, d_status),
+        ZS_OFF(zs_batch, pass_event)};
+    static const size_t params[] = {
+        ZS_OFF(zs_row_params, temperature), ZS_OFF(zs_row_params, top_k), ZS_OFF(zs_row_params, top_p),
+        ZS_OFF(zs_row_params, min_p), ZS_OFF(zs_row_params, repeat), ZS_OFF(zs_row_params, presence),
+        ZS_OFF(zs_row_params, frequency), ZS_OFF(zs_row_params, top_logprobs), ZS_OFF(zs_row_params, flags),
+        ZS_OFF(zs_row_params, pad)};
+    static const size_t spec[] = {
+        ZS_OFF(zs_spec_batch, B), ZS_OFF(zs_spec_batch, V), ZS_OFF(zs_spec_batch, k), ZS_OFF(zs_spec_batch, ld),
+        ZS_OFF(zs_spec_batch, d_target), ZS_OFF(zs_spec_batch, d_draft), ZS_OFF(zs_spec_batch, d_draft_ids),
+        ZS_OFF(zs_spec_batch, d_temperature), ZS_OFF(zs_spec_batch, d_seed), ZS_OFF(zs_spec_batch, d_counter),
+        ZS_OFF(zs_spec_batch, d_accepted), ZS_OFF(zs_spec_batch, d_next), ZS_OFF(zs_spec_batch, flags)};
+    static const size_t lane[] = {
+        ZS_OFF(zs_lane_stream, temp), ZS_OFF(zs_lane_stream, top_k), ZS_OFF(zs_lane_stream, top_p),
+        ZS_OFF(zs_lane_stream, base_seed), ZS_OFF(zs_lane_stream, gen_index)};
+    static const size_t rep[] = {
+        ZS_OFF(zs_halluc_report, risk_score), ZS_OFF(zs_halluc_report, mean_entropy),
+        ZS_OFF(zs_halluc_report, normalized_entropy), ZS_OFF(zs_halluc_report, risky_fraction),
+        ZS_OFF(zs_halluc_report, peak_token), ZS_OFF(zs_halluc_report, n_tokens)};
+    const size_t* f;
+    size_t n, sz;
+    switch (which) {
+        case ZS_LAYOUT_BATCH: f = batch; n = sizeof(batch) / sizeof(size_t); sz = sizeof(zs_batch); break;
+        case ZS_LAYOUT_ROW_PARAMS: f = params; n = sizeof(params) / sizeof(size_t); sz = sizeof(zs_row_params); break;
+        case ZS_LAYOUT_SPEC_BATCH: f = spec; n = sizeof(spec) / sizeof(size_t); sz = sizeof(zs_spec_batch); break;
+        case ZS_LAYOUT_LANE_STREAM: f = lane; n = sizeof(lane) / sizeof(size_t); sz = sizeof(zs_lane_stream); break;
+        case ZS_LAYOUT_HALLUC_REPORT: f = rep; n = sizeof(rep) / sizeof(size_t); sz = sizeof(zs_halluc_report); break;
+        default: return ZS_EINVAL;
+    }
+    if (size) *size = sz;
+    for (size_t i = 0; offsets && i < n && i < cap; i++) offsets[i] = f[i];
+    return (int)n;
+}
 
 extern "C" const char* zs_last_error(const zs_ctx* ctx) { return ctx ? ctx->err : "null context"; }
 
