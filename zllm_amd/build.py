@@ -13,7 +13,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libzs.so")
 
-SOURCES = ["zs_api.cpp", "zs_grammar.cpp", "zs_regex.cpp", "zs_schema.cpp", "zs_tokens.cpp", "zs_wire.cpp", "zs_sample.hip", "zs_row.hip", "zs_dfa.hip", "zs_lane.hip", "zs_spec.hip"]
+SOURCES = ["zs_api.cpp", "zs_grammar.cpp", "zs_regex.cpp", "zs_schema.cpp", "zs_tokens.cpp", "zs_wire.cpp", "zs_sample.hip", "zs_row.hip", "zs_sums.hip", "zs_dfa.hip", "zs_lane.hip", "zs_spec.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 

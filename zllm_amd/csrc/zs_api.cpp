@@ -122,7 +122,7 @@ extern "C" void zs_ctx_destroy(zs_ctx* ctx) {
         }
     if (ctx->lane_host) (void)hipHostFree(ctx->lane_host);
     void* ptrs[] = {ctx->p_cnt, ctx->p_id, ctx->p_flags, ctx->p_y, ctx->rst, ctx->pairs, ctx->pv, ctx->mask_scratch, ctx->spec_chunks,
-                    ctx->spec_rows, ctx->p_sub, ctx->k_ap, ctx->k_sum, ctx->tp_bk, ctx->tp_cl, ctx->tp_pre, ctx->kcnt,
+                    ctx->spec_rows, ctx->p_sub, ctx->k_ap, ctx->k_sum, ctx->s_rec, ctx->s_apx, ctx->gath, ctx->s_hterm, ctx->tp_bk, ctx->tp_cl, ctx->tp_pre, ctx->kcnt,
                     ctx->lane_temp, ctx->lane_vals, ctx->lane_ih, ctx->lane_keys,
                     ctx->lane_idxs, ctx->lane_ck, ctx->lane_cn};
     for (void* p : ptrs)
@@ -175,9 +175,13 @@ extern "C" int zs_ctx_create(int device, uint32_t max_rows, uint32_t max_vocab, 
     if (!rc) rc = zs_alloc(ctx, &ctx->p_sub, R * (ctx->max_subs + 1));
     if (!rc) rc = zs_alloc(ctx, &ctx->k_ap, R * ctx->max_subs);
     if (!rc) rc = zs_alloc(ctx, &ctx->k_sum, R * 2 * ctx->max_subs);
+    if (!rc) rc = zs_alloc(ctx, &ctx->s_rec, R * ZS_NSUM * ctx->max_subs);
+    if (!rc) rc = zs_alloc(ctx, &ctx->s_apx, R * 8 * ctx->max_subs);
+    if (!rc) rc = zs_alloc(ctx, &ctx->gath, R * (2 * (size_t)max_vocab + 16));
+    if (!rc) rc = zs_alloc(ctx, &ctx->s_hterm, R * ((size_t)max_vocab + 8));
     if (!rc) rc = zs_alloc(ctx, &ctx->tp_bk, R * ZS_TP_NB);
     if (!rc) rc = zs_alloc(ctx, &ctx->tp_cl, R * ZS_TP_CL);
-    if (!rc) rc = zs_alloc(ctx, &ctx->tp_pre, R * (size_t)max_vocab * 2);
+    if (!rc) rc = zs_alloc(ctx, &ctx->tp_pre, R * (size_t)max_vocab * 2 + 8);  // 16-byte loads at the tail
     if (!rc) rc = zs_alloc(ctx, &ctx->kcnt, R * C * 2);
     if (!rc) rc = zs_alloc(ctx, &ctx->spec_rows, R);
     // the lane knobs in one block laid out as the staging areas (temp, top_k,

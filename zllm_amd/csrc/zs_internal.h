@@ -83,7 +83,8 @@ struct zs_row_state {
     float obs_max;
     uint32_t obs_special; // lse is NaN (NaN / +inf / all -inf row)
     uint32_t obs_need;
-    uint32_t rounds;      // ZS_SUM_* bits computed by the parallel rounds
+    uint32_t rounds;      // ZS_SUM_* bits: the sums zs_sums.hip computes for the row
+    uint32_t g_n;         // masked rows: allowed ids gathered to row scratch (0: none, the sums read the row)
     float samp_S;         // sampler softmax denominator (sampler.rs:68) when computed by the rounds
     float obs_S;          // sequential f32 sum (hallucination.rs:134-135, logprobs.rs:36)
     float obs_H;          // sequential f32 entropy (hallucination.rs:139-144)
@@ -169,6 +170,10 @@ struct zs_ctx {
     uint32_t vocab_serial; // serial number of the last zs_vocab created
     double* k_ap;                // [rows][max_subs] approximate sums of the kept list per sub-chunk
     zs_sub_sum* k_sum;           // [rows][2][max_subs] kept-list rounds (sum2, draw)
+    zs_sub_sum* s_rec;           // [rows][ZS_NSUM][max_subs] row-sum sub-chunk totals (zs_k_sround)
+    float* gath;                 // [rows][2 * max_vocab + 16] masked rows' gathered allowed ids (x~, y, ids)
+    float* s_hterm;              // [rows][max_vocab + 8] entropy terms of the sub-chunks its stitch walks
+    float* s_apx;                // [rows][max_subs][8] approximate row-sum parts per sub-chunk (zs_k_sapx)
     zs_tp_bucket* tp_bk;         // [rows][ZS_TP_NB] top-p buckets (zs_k_tp_*)
     uint32_t* tp_cl;             // [rows][ZS_TP_CL] row flags, candidate count, candidate buckets
     uint32_t* tp_pre;            // [rows][2][max_vocab] increment prefixes of presorted buckets

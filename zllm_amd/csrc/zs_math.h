@@ -50,7 +50,8 @@ static const uint64_t zs_exp2f_tab_host[32] = ZS_EXP2F_TAB;
 #define ZS_EXP2F_TABLE zs_exp2f_tab_host
 #endif
 
-ZS_HD float zs_expf(float x) {
+// (the table is an argument so that a kernel can read it from LDS)
+ZS_HD float zs_expf_tab(float x, const uint64_t* tab) {
     const double InvLn2N = 0x1.71547652b82fep+0 * 32;
     const double SHIFT = 0x1.8p+52;
     const double C0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32;
@@ -70,7 +71,7 @@ ZS_HD float zs_expf(float x) {
     uint64_t ki = zs_d2u(kd);
     kd -= SHIFT;
     double r = fma(InvLn2N, xd, -kd);
-    uint64_t t = ZS_EXP2F_TABLE[ki & 31] + (ki << 47);
+    uint64_t t = tab[ki & 31] + (ki << 47);
     double s = zs_u2d(t);
     double zz = fma(C0, r, C1);
     double r2 = r * r;
@@ -79,6 +80,7 @@ ZS_HD float zs_expf(float x) {
     y = y * s;
     return (float)y;
 }
+ZS_HD float zs_expf(float x) { return zs_expf_tab(x, ZS_EXP2F_TABLE); }
 
 // Rust f32::total_cmp order as an unsigned key: ascending key == ascending
 // total order (-NaN < -inf < ... < -0 < +0 < ... < +inf < +NaN).

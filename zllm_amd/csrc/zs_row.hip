@@ -55,7 +55,6 @@ struct rw_shared {
             unsigned long long o[RW_BUF];         // P1: observer candidates
             unsigned long long s[RW_BUF];         // P1: sampler candidates
         } b;
-        seq_sh<RW_NT> seq;                        // P2 / P3: exact scans
     } u;
     float sval[ZS_SMALL_CAP];
     uint32_t sidx[ZS_SMALL_CAP];
@@ -66,19 +65,10 @@ struct rw_shared {
     float fthr[2];                  // candidate thresholds as values
     float fcut[2];                  // largest values cut from the lists
     unsigned long long rl[RW_NW];
-    uint32_t grp[2][RW_NW][8];      // P2 / P3: per-wave tile totals (double buffered)
-    uint32_t gsum[2][RW_NW];        // P2 / P3: per-wave group totals (double buffered)
-    uint32_t cross[3][RW_NW];       // crossing path: per-wave prefix totals (RW_NG grids)
-    int cr_first[2][RW_NW];         // crossing path: per-wave first event (double buffered)
-    float cr_s[2];                  // crossing path: the sum after an event
-    uint32_t cr_nb[2][2];           // crossing path: prefixes through the event
-    float head[256];
     uint32_t n_ent, n_surv, tok;
     uint32_t ovf[3];                // first tile that lost a list entry, per group slot
     uint32_t thr_o, thr_s;          // candidate admission thresholds (keys)
     float fsh;
-    uint32_t pass_g;                // sum passes: the tile left to the ordered scan (or ng)
-    int pass_start;                 // and the first element of it still to add
     uint32_t sel_hist[2][256];      // list selection: digit histogram (double buffered)
     uint32_t sel_mm[3][RW_NW];      // list selection: per-wave member count, key min / max
     uint32_t sel_n;                 // list selection: places taken by the gather
@@ -584,667 +574,9 @@ __device__ __forceinline__ void rw_admit(const rw_list& L, uint32_t* ctr, uint32
     }
 }
 
-// ---------------------------------------------------------------------------
-// Exact sequential sums (P2, P3)
-//
-// A tile's terms are added to the running sum s on the grid g = ulp(s) of its
-// binade: each adds the integer round_half_even(t / g) (zs_math.h). Fast
-// path: every thread sums its four increments, one reduction gives the tile
-// total, and s moves by total * g when the sum stays in its binade. A tile
-// where the sum leaves its binade takes the crossing path (rw_cross): the
-// increments on RW_NG consecutive grids are prefix-scanned at once, each
-// crossing is located in the prefix of its grid and added as a real f32
-// addition, and the walk continues on the next grid. Terms with an exact
-// half-way increment (whose rounding depends on the sum's parity), and sums
-// still below 2^-126, take the ordered scan of zs_seq.h (rw_slow).
-// ---------------------------------------------------------------------------
-#define RW_NG 3
-#define RW_QCAP 33554432.0f   // increments are clamped to 2^25 (any larger one crosses the binade)
-#define RW_QFLAG (1u << 28)   // a tile total that forces the crossing path
-
-// 2^(150-eg) = 1 / grid as an exact f32, or 0 when the grid is finer than
-// f32 scaling reaches (sums below 2^-126).
-__device__ __forceinline__ float rw_scale(int eg) {
-    return (eg >= 24 && eg <= 276) ? __uint_as_float((uint32_t)(277 - eg) << 23) : 0.0f;
-}
-
-// exp(d) from the fast exp (relative error below ZS_EXP_EPS), 0 below the
-// fast range; `sub` is set where the exact result is subnormal or the
-// argument is in the fast exp's excluded range (those terms need zs_expf).
-__device__ __forceinline__ float rw_fexp(float d, uint32_t& sub) {
-    const float e = zs_exp_fast(fmaxf(d, ZS_EXP_FAST_MIN));
-    sub |= (d < ZS_EXP_FAST_MIN && d >= ZS_EXP_ZERO) ? 1u : 0u;
-    return d >= ZS_EXP_FAST_MIN ? e : 0.0f;
-}
-
-// H term -(p * ((l - max) - ln S)), p = exp(l - max) * inv, 0 unless p > 0
-// (hallucination.rs:142-143), with the fast exp (a tolerance output) and
-// glibc's exp where the fast exp does not cover the argument.
-__device__ __forceinline__ float rw_hterm_exact(float d, float inv, float lns) {
-    uint32_t sub = 0;
-    float e = rw_fexp(d, sub);
-    if (sub) e = zs_expf(d);
-    const float p = e * inv;
-    return p > 0.0f ? -(p * (d - lns)) : 0.0f;
-}
-
-// Ordered exact scan of a tile of values from running sum s (elements >=
-// start), zs_seq.h. A sum that is still zero starts at its first nonzero
-// term, and its next 256 terms are added serially by one thread (the sum
-// climbs through many binades there).
-__device__ __noinline__ float rw_slow(float v0, float v1, float v2, float v3, int start, float s, rw_shared& sh) {
-    const float v[4] = {v0, v1, v2, v3};
-    const int t = (int)threadIdx.x;
-    if (s == 0.0f) {
-        int first = ZS_BIGI;
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-            if (first == ZS_BIGI && 4 * t + j >= start && v[j] != 0.0f) first = 4 * t + j;
-        first = block_min_i<RW_NT>(first, reinterpret_cast<int*>(sh.ru[5]));
-        if (first == ZS_BIGI) return s + 0.0f;  // only zero terms: the sum is +0
-        const int e0 = first, e1 = min(first + 256, RW_G);
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int e = 4 * t + j;
-            if (e >= e0 && e < e1) sh.head[e - e0] = v[j];
-        }
-        __syncthreads();
-        if (t == 0) {
-            float acc = s;
-            for (int i = 0; i < e1 - e0; i++) acc = acc + sh.head[i];
-            sh.fsh = acc;
-        }
-        __syncthreads();
-        s = sh.fsh;
-        __syncthreads();
-        start = e1;
-    }
-    if (start < RW_G) {
-        seq_terms<4> f(v);
-        seq_group_f<RW_NT, 4>(f, start, s, NAN, sh.u.seq);
-    }
-    return s;
-}
-
-// Saturating add for the crossing path's prefixes: increments are at most
-// 2^25, so a thread's four stay below 2^27, and a cap of 2^30 keeps every
-// prefix a crossing search compares exact up to the crossing (a prefix is
-// only ever subtracted from a larger one on the same grid, and the prefix at
-// a crossing is below 2^27).
-__device__ __forceinline__ uint32_t rw_sat(uint32_t a, uint32_t b) {
-    const uint32_t c = a + b;
-    return c > (1u << 30) ? (1u << 30) : c;
-}
-
-// Inclusive prefix sum of a u32 over the wave (no overflow check): shifts by
-// 1, 2, 4, 8 within each row of 16 lanes, then the rows by broadcasts.
-__device__ __forceinline__ uint32_t rw_wave_scan(uint32_t v) {
-    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, true);   // row_shr:1
-    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, true);   // row_shr:2
-    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, true);   // row_shr:4
-    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, true);   // row_shr:8
-    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false);  // row_bcast:15
-    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false);  // row_bcast:31
-    return v;
-}
-
-// Crossing path: the tile's values from running sum s (elements >= start).
-// The increments on RW_NG consecutive grids are prefix-scanned at once; a
-// walk then finds the events in order: an element whose prefix carries the
-// sum out of its binade, and (exact sums, `ties`) an element whose increment
-// is an exact half-way case (its rounding follows the sum's parity). Each
-// event is added as a real f32 addition, and the walk continues on the grid
-// of the new sum. A thread's total is capped at 2^25: any larger one holds
-// a crossing, so the prefixes are exact up to the first crossing. Sums below
-// 2^-103 (no f32 scale reaches their grid) are left to the ordered scan
-// (slow: from element `start`).
-__device__ __forceinline__ float rw_cross(const float (&v)[4], int& start, float s, uint32_t ties, bool& slow,
-                                          rw_shared& sh, bool first_tile) {
-    const int t = (int)threadIdx.x, lane = zs_lane(), wid = zs_wid();
-    uint32_t par = 0;
-    slow = false;
-    if (first_tile && start == 0) {
-        // the row's first 256 terms, where the sum leaves a binade at almost
-        // every doubling of the number of terms: wave 0 adds them one by one
-        // in index order (the reference's own additions; a sum that is still
-        // zero counts as +0, as the reference's sum starts)
-        if (wid == 0) {
-            float ss = s + 0.0f;
-            for (int L = 0; L < 64; L++) {
-#pragma unroll
-                for (int q = 0; q < 4; q++) ss = ss + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v[q]), L));
-            }
-            if (lane == 0) sh.cr_s[par] = ss;
-        }
-        rw_bar();
-        s = sh.cr_s[par];
-        par ^= 1u;
-        start = 4 * 64;
-    }
-    // the first element of the workgroup with an event (uniform)
-    auto first_of = [&](int my) -> int {
-        // (read by every lane: a lane's value exists only where it was
-        // computed, so the read must not sit inside the lane-0 branch)
-        const unsigned long long m = __ballot(my != ZS_BIGI);
-        const int mv = m ? __builtin_amdgcn_readlane(my, __ffsll((long long)m) - 1) : ZS_BIGI;
-        if (lane == 0) sh.cr_first[par][wid] = mv;
-        rw_bar();
-        int e = ZS_BIGI;
-#pragma unroll
-        for (int w = 0; w < RW_NW; w++) e = min(e, sh.cr_first[par][w]);
-        par ^= 1u;
-        return (int)rw_uni((uint32_t)e);
-    };
-    while (start < RW_G) {
-        if (s == 0.0f) {
-            // a zero sum takes the first nonzero term as it is (zero terms
-            // before it leave a zero; -0 + +0 = +0 is restored here)
-            int my = ZS_BIGI;
-#pragma unroll
-            for (int q = 0; q < 4; q++)
-                if (my == ZS_BIGI && 4 * t + q >= start && v[q] != 0.0f) my = 4 * t + q;
-            const int first = first_of(my);
-            if (first == ZS_BIGI) return s + 0.0f;
-            if (t == first / 4) {
-                float ve = v[0];
-#pragma unroll
-                for (int q = 1; q < 4; q++) ve = q == first % 4 ? v[q] : ve;
-                sh.cr_s[par] = ve;
-            }
-            rw_bar();
-            s = (s + 0.0f) + sh.cr_s[par];
-            par ^= 1u;
-            start = first + 1;
-            continue;
-        }
-        const int eg0 = zs_grid_exp(s);
-        if (rw_scale(eg0) == 0.0f) { slow = true; return s; }
-        // per-thread increments and half-way flags on grids eg0 .. eg0 + RW_NG - 1
-        uint32_t inc[RW_NG][4], tot[RW_NG], tb[RW_NG];
-#pragma unroll
-        for (int j = 0; j < RW_NG; j++) {
-            const float sc = rw_scale(eg0 + j);
-            tot[j] = 0;
-            tb[j] = 0;
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const float qv = (4 * t + q >= start) ? fminf(v[q] * sc, RW_QCAP) : 0.0f;
-                const float rq = rintf(qv);
-                if (ties && fabsf(qv - rq) == 0.5f) tb[j] |= 1u << q;
-                inc[j][q] = (uint32_t)rq;
-                tot[j] += inc[j][q];
-            }
-            tot[j] = min(tot[j], 1u << 25);
-        }
-        // exclusive prefix of the thread totals over the workgroup, per grid
-        uint32_t pre[RW_NG], wtot[RW_NG];
-#pragma unroll
-        for (int j = 0; j < RW_NG; j++) {
-            const uint32_t x = rw_wave_scan(tot[j]);
-            pre[j] = x - tot[j];
-            if (lane == 63) sh.cross[j][wid] = min(x, 1u << 25);
-        }
-        rw_bar();
-#pragma unroll
-        for (int j = 0; j < RW_NG; j++) {
-            uint32_t before = 0, all = 0;
-#pragma unroll
-            for (int w = 0; w < RW_NW; w++) {
-                const uint32_t c = sh.cross[j][w];
-                before += w < wid ? c : 0u;
-                all += c;
-            }
-            pre[j] += before;
-            wtot[j] = all;
-        }
-        // walk: running sum k on grid eg0 + j from element position P (the
-        // prefix of grid j through the last event is base); the grid index
-        // is a compile-time constant in every step, so the increments stay
-        // in registers
-        uint32_t k = zs_grid_k(s), base = 0;
-        int P = start;
-        bool done = false, next = true;
-#pragma unroll
-        for (int j = 0; j < RW_NG; j++) {
-            if (!next) break;
-            next = false;
-            const int jn = j + 1 < RW_NG ? j + 1 : j;
-            while (true) {
-                int my = ZS_BIGI;
-                uint32_t run = pre[j];
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    run += inc[j][q];
-                    if (my == ZS_BIGI && 4 * t + q >= P &&
-                        ((uint64_t)k + (run - base) >= ZS_BINADE || ((tb[j] >> q) & 1u)))
-                        my = 4 * t + q;
-                }
-                const int e = first_of(my);
-                if (e == ZS_BIGI) {
-                    s = zs_grid_value(k + (wtot[j] - base), eg0 + j);
-                    done = true;
-                    break;
-                }
-                // the event as a real f32 addition (its owner), with the
-                // prefixes of grids j and j + 1 through it
-                if (t == e / 4) {
-                    const int eq = e % 4;
-                    uint32_t ex = pre[j], nbj = pre[j], nbn = pre[jn];
-                    float ve = 0.0f;
-#pragma unroll
-                    for (int q = 0; q < 4; q++) {
-                        if (q < eq) ex += inc[j][q];
-                        if (q <= eq) { nbj += inc[j][q]; nbn += inc[jn][q]; }
-                        ve = q == eq ? v[q] : ve;
-                    }
-                    sh.cr_s[par] = zs_grid_value(k + (ex - base), eg0 + j) + ve;
-                    sh.cr_nb[par][0] = nbj;
-                    sh.cr_nb[par][1] = nbn;
-                }
-                rw_bar();
-                s = sh.cr_s[par];
-                const uint32_t nbj = sh.cr_nb[par][0], nbn = sh.cr_nb[par][1];
-                par ^= 1u;
-                P = e + 1;
-                const int ge = zs_grid_exp(s);
-                if (ge == eg0 + j) {   // a half-way event: the same grid
-                    k = zs_grid_k(s);
-                    base = nbj;
-                    continue;
-                }
-                if (j + 1 < RW_NG && ge == eg0 + j + 1) {
-                    k = zs_grid_k(s);
-                    base = nbn;
-                    next = true;
-                }
-                break;   // otherwise past the prepared grids: rescan from P
-            }
-            if (done) break;
-        }
-        if (done) return s;
-        start = P;
-    }
-    return s;
-}
-
-// End of a group of four tiles: per-thread per-tile increment totals q[u]
-// and flag bits (bit u: tile u needs the ordered path) in; the workgroup
-// totals per tile and the OR'ed flags out (a slot that alternates between
-// groups, so one LDS-only barrier suffices).
-__device__ __forceinline__ void rw_group_reduce(uint32_t (&q)[4], uint32_t& f, uint32_t parity, rw_shared& sh) {
-    for (int d = 32; d > 0; d >>= 1) {
-#pragma unroll
-        for (int u = 0; u < 4; u++) q[u] = zs_sat_add(q[u], __shfl_xor(q[u], d, 64));
-        f |= __shfl_xor(f, d, 64);
-    }
-    uint4* R4 = reinterpret_cast<uint4*>(&sh.grp[parity][0][0]);
-    if (zs_lane() == 0) {
-        R4[2 * zs_wid() + 0] = make_uint4(q[0], q[1], q[2], q[3]);
-        R4[2 * zs_wid() + 1] = make_uint4(f, 0u, 0u, 0u);
-    }
-    rw_bar();
-#pragma unroll
-    for (int u = 0; u < 4; u++) q[u] = 0;
-    f = 0;
-#pragma unroll
-    for (int w = 0; w < RW_NW; w++) {
-        const uint4 A = R4[2 * w + 0];
-        q[0] = zs_sat_add(q[0], A.x); q[1] = zs_sat_add(q[1], A.y);
-        q[2] = zs_sat_add(q[2], A.z); q[3] = zs_sat_add(q[3], A.w);
-        f |= R4[2 * w + 1].x;
-    }
-#pragma unroll
-    for (int u = 0; u < 4; u++) q[u] = rw_uni(q[u]);
-    f = rw_uni(f);
-}
-
-// First tile of a group whose totals carry the sum k out of its binade or
-// that is flagged (4: none); *pre = the increments of the tiles before it.
-__device__ __forceinline__ int rw_group_first(const uint32_t (&q)[4], uint32_t f, uint32_t k, uint32_t* pre) {
-    uint32_t run = 0;
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-        if (((f >> u) & 1u) || k + zs_sat_add(run, q[u]) >= ZS_BINADE) { *pre = run; return u; }
-        run = zs_sat_add(run, q[u]);
-    }
-    *pre = run;
-    return 4;
-}
-
-// Increments of four values on the grid of scale sc (a positive scale: the
-// sum pass sends tiles on finer grids to the crossing path). Each is at most
-// 2^25, so the total does not overflow.
-__device__ __forceinline__ uint32_t rw_inc4(const float (&v)[4], float sc) {
-    uint32_t sum = 0;
-#pragma unroll
-    for (int q = 0; q < 4; q++) sum += (uint32_t)rintf(fminf(v[q] * sc, RW_QCAP));
-    return sum;
-}
-
-// Certified increments of exact terms exp(d) from their zs_exp_fast values a
-// (relative error below ZS_EXP_EPS): where |q - rint(q)| is within q * eps of
-// one half the term is recomputed with glibc's algorithm; an exact half-way
-// increment sets fl (its rounding depends on the sum's parity: the ordered
-// path). Arguments below the fast exp's range were clamped to it: the sum
-// pass only takes this path on grids where such terms round to 0 either way.
-__device__ __forceinline__ uint32_t rw_inc4_cert(const float (&a)[4], const float (&d)[4], float sc, uint32_t& fl) {
-    uint32_t unc = 0;
-    float qv[4], rq[4];
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-        qv[q] = fminf(a[q] * sc, RW_QCAP);
-        rq[q] = rintf(qv[q]);
-        const bool u = fmaf(qv[q], (float)ZS_EXP_EPS, fabsf(qv[q] - rq[q])) >= 0.5f && qv[q] < RW_QCAP;
-        unc |= u ? (1u << q) : 0u;
-    }
-    if (unc) {   // rare: one branch per thread
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            if (unc & (1u << q)) {
-                const float qe = fminf(zs_expf(d[q]) * sc, RW_QCAP);
-                rq[q] = rintf(qe);
-                if (fabsf(qe - rq[q]) == 0.5f) fl |= 1u;
-            }
-        }
-    }
-    uint32_t sum = 0;
-#pragma unroll
-    for (int q = 0; q < 4; q++) sum += (uint32_t)rq[q];
-    return sum;
-}
-
-// One exact sequential sum over the row (P2, P3): F gives the terms of a
-// tile (values and per-tile flags, for the fast path) and the terms of the
-// crossing path. Tiles are added in groups of four on the grid of the sum at
-// the group start; a group whose tile carries the sum out of its binade (or
-// is flagged) stops the stream at that tile, adds the tiles before it, and
-// that tile takes the crossing path (rw_cross).
-template <class F>
-__device__ __forceinline__ float rw_sum_pass(const rw_row& R, rw_shared& sh, float s, uint32_t ties, const F& f,
-                                             uint32_t g) {
-    uint32_t stop = 0, gpar = 0;
-    bool stopped = false;
-    const uint32_t ng = (R.V + RW_G - 1) / RW_G;
-    uint32_t qt[4] = {0u, 0u, 0u, 0u};
-    int eg = 0;
-    float sc = 0.0f;
-    while (g < ng) {
-        g = rw_stream(R, sh, g, [&](uint32_t g, int u, const float (&x)[4], const float (&y)[4]) {
-            if (u == 0) {
-                eg = zs_grid_exp(s);
-                sc = rw_scale(eg);
-            }
-            // a zero sum only needs to know whether a term may be nonzero
-            // (rows whose terms are all zero up to some tile: masked rows)
-            const bool zero = s == 0.0f;
-            uint32_t tf = 0;
-            if (zero) qt[u] = f.nonzero(x, y) ? RW_QFLAG : 0u;
-            else qt[u] = f.fast(x, y, sc, tf);
-            if (tf) qt[u] = RW_QFLAG;   // a flagged tile reads as a crossing
-            if (u != 3) return false;
-            // the group's total first (one value per thread); the tiles'
-            // totals only when the sum leaves its binade in the group
-            const uint32_t k = zs_grid_k(s);
-            const uint32_t w = min(rw_wave_sum(min(qt[0] + qt[1] + qt[2] + qt[3], ZS_BINADE)), ZS_BINADE);
-            if (zs_lane() == 0) sh.gsum[gpar][zs_wid()] = w;
-            rw_bar();
-            uint32_t tot = 0;
-#pragma unroll
-            for (int v = 0; v < RW_NW; v++) tot += sh.gsum[gpar][v];
-            tot = rw_uni(tot);
-            // grids finer than f32 scaling reaches, or on which terms below
-            // the fast exp's range could round up: the crossing path
-            const bool fine = sc == 0.0f || sc >= F::sc_max;
-            if (zero && tot == 0) {   // zero terms only: the sum stays a zero
-                s = s + 0.0f;
-                gpar ^= 1u;
-                return false;
-            }
-            if (!fine && k + tot < ZS_BINADE) {
-                s = zs_grid_value(k + tot, eg);
-                gpar ^= 1u;
-                return false;
-            }
-            uint32_t pre = 0, fl = 0;
-            int c = 0;
-            if (!fine || zero) {
-                rw_group_reduce(qt, fl, gpar, sh);
-                c = rw_group_first(qt, fl, k, &pre);
-            }
-            gpar ^= 1u;
-            s = zs_grid_value(k + pre, eg);
-            stop = g - 3 + (uint32_t)c;
-            stopped = true;
-            return true;
-        });
-        // (the stop tile is below ng even when the group's last tile is not)
-        if (!stopped) break;
-        stopped = false;
-        g = rw_uni(stop);
-        float x[4], y[4];
-        rw_tile(R, sh, g, x, y);
-        float v[4];
-        f.exact(x, y, v);
-        int start = 0;
-        bool slow = false;
-        s = rw_cross(v, start, s, ties, slow, sh, g == 0);
-        if (slow) {
-            // the ordered scan (zs_seq.h) finishes this tile outside
-            if (threadIdx.x == 0) { sh.pass_g = g; sh.pass_start = start; }
-            __syncthreads();
-            return s;
-        }
-        g++;
-    }
-    if (threadIdx.x == 0) sh.pass_g = ng;
-    __syncthreads();
-    return s;
-}
-
-// Terms of the observers' S: exp(x~ - max) with the fast exp (a tolerance
-// output), glibc's exp for arguments the fast exp does not cover.
-struct rw_obs_terms {
-    float M;
-    // whether a term of the four may be nonzero (glibc's expf is 0 below -104)
-    __device__ __forceinline__ bool nonzero(const float (&x)[4], const float (&)[4]) const {
-        return fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])) - M >= ZS_EXP_ZERO;
-    }
-    // grids on which the fast path holds: a term below the fast exp's range
-    // (below 2^-125) then rounds to 0
-    static constexpr float sc_max = 0x1p123f;
-    __device__ __forceinline__ uint32_t fast(const float (&x)[4], const float (&)[4], float sc, uint32_t&) const {
-        float v[4];
-#pragma unroll
-        for (int q = 0; q < 4; q++) v[q] = zs_exp_hw(fmaxf(x[q] - M, ZS_EXP_FAST_MIN));
-        return rw_inc4(v, sc);
-    }
-    __device__ __forceinline__ void exact(const float (&x)[4], const float (&)[4], float (&v)[4]) const {
-        uint32_t sub = 0;
-#pragma unroll
-        for (int q = 0; q < 4; q++) v[q] = rw_fexp(x[q] - M, sub);
-        if (sub) {
-#pragma unroll
-            for (int q = 0; q < 4; q++) v[q] = zs_expf(x[q] - M);
-        }
-    }
-};
-
-// Terms of the sampler's S (sampler.rs:68): expf(z - max) exactly, z = y / T,
-// 0 below the top-k threshold. DIV: 0 = T is 1 (no division), 1 = Markstein's
-// division, 2 = IEEE division (a compile-time choice, so that the four
-// elements' code stays free of branches).
-template <uint32_t DIV>
-struct rw_samp_terms {
-    float T, rT, zmax, thr;
-    bool use_thr;
-    // z = y / T correctly rounded (sampler.rs:47-51). With rT = RN(1 / T),
-    // q0 = RN(y * rT) is within an ulp of y / T, the remainder y - q0 * T is
-    // exact in one fma, and RN(q0 + r * rT) is RN(y / T) (Markstein's
-    // theorem) while nothing underflows or overflows: for 2^-100 <= |y| <=
-    // 2^100 and 2^-20 <= T <= 2^20. Zeros and infinities divide exactly as
-    // y * rT; other y divide the IEEE way (rare: one branch per thread).
-    __device__ __forceinline__ void temper4(const float (&y)[4], float (&z)[4]) const {
-        if (DIV == 0u) {
-#pragma unroll
-            for (int q = 0; q < 4; q++) z[q] = y[q];
-            return;
-        }
-        if (DIV == 2u) {
-#pragma unroll
-            for (int q = 0; q < 4; q++) z[q] = y[q] / T;
-            return;
-        }
-        bool odd = false;
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const float q0 = y[q] * rT;
-            const float q1 = fmaf(fmaf(-q0, T, y[q]), rT, q0);
-            const float a = fabsf(y[q]);
-            const bool mid = a >= 0x1p-100f && a <= 0x1p100f;
-            z[q] = mid ? q1 : q0;
-            odd |= !mid && a != 0.0f && a != INFINITY;
-        }
-        if (odd) {
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const float a = fabsf(y[q]);
-                if (!(a >= 0x1p-100f && a <= 0x1p100f) && a != 0.0f && a != INFINITY) z[q] = y[q] / T;
-            }
-        }
-    }
-    __device__ __forceinline__ void args(const float (&y)[4], float (&d)[4]) const {
-        float z[4];
-        temper4(y, z);
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            if (use_thr && z[q] < thr) z[q] = -INFINITY;
-            d[q] = z[q] - zmax;
-        }
-    }
-    __device__ __forceinline__ bool nonzero(const float (&)[4], const float (&y)[4]) const {
-        float d[4];
-        args(y, d);
-        return fmaxf(fmaxf(d[0], d[1]), fmaxf(d[2], d[3])) >= ZS_EXP_ZERO;
-    }
-    static constexpr float sc_max = 0x1p123f;
-    __device__ __forceinline__ uint32_t fast(const float (&)[4], const float (&y)[4], float sc, uint32_t& fl) const {
-        float d[4], a[4];
-        args(y, d);
-#pragma unroll
-        for (int q = 0; q < 4; q++) a[q] = zs_exp_fast(fmaxf(d[q], ZS_EXP_FAST_MIN));
-        return rw_inc4_cert(a, d, sc, fl);
-    }
-    __device__ __forceinline__ void exact(const float (&)[4], const float (&y)[4], float (&v)[4]) const {
-        float d[4];
-        args(y, d);
-#pragma unroll
-        for (int q = 0; q < 4; q++) v[q] = zs_expf(d[q]);
-    }
-};
-
-// Terms of the entropy (hallucination.rs:139-144), fast exp (a tolerance output).
-struct rw_ent_terms {
-    float M, inv, lns;
-    __device__ __forceinline__ bool nonzero(const float (&x)[4], const float (&)[4]) const {
-        return fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])) - M >= ZS_EXP_ZERO;
-    }
-    // a term with an argument below the fast exp's range is below
-    // 2^-125.5 * (104 + ln S) < 2^-118 (S >= 1, ln S < 13): 0 on these grids
-    static constexpr float sc_max = 0x1p116f;
-    __device__ __forceinline__ uint32_t fast(const float (&x)[4], const float (&)[4], float sc, uint32_t&) const {
-        float v[4];
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const float d = fmaxf(x[q] - M, ZS_EXP_FAST_MIN);
-            const float p = zs_exp_hw(d) * inv;
-            v[q] = p > 0.0f ? -(p * (d - lns)) : 0.0f;
-        }
-        return rw_inc4(v, sc);
-    }
-    __device__ __forceinline__ void exact(const float (&x)[4], const float (&)[4], float (&v)[4]) const {
-#pragma unroll
-        for (int q = 0; q < 4; q++) v[q] = rw_hterm_exact(x[q] - M, inv, lns);
-    }
-};
-
-
-// The sum passes as functions of their own: a pass's loop then holds only
-// its own values (the kernel's live values are saved once around the call,
-// not reloaded in every tile). Arguments arrive in vector registers and are
-// made uniform first.
-__device__ __forceinline__ const float* rw_uni_ptr(const float* p) {
-    const uint64_t v = reinterpret_cast<uint64_t>(p);
-    return reinterpret_cast<const float*>(((uint64_t)rw_uni((uint32_t)(v >> 32)) << 32) | rw_uni((uint32_t)v));
-}
-__device__ __forceinline__ rw_row rw_row_of(const float* row, const float* allow, uint32_t V, uint32_t np, uint32_t ldm4) {
-    rw_row R;
-    R.row = rw_uni_ptr(row);
-    R.allow = reinterpret_cast<const uint32_t*>(rw_uni_ptr(allow));
-    R.V = rw_uni(V);
-    R.np = rw_uni(np);
-    R.words = (R.V + 31) / 32;
-    R.ldm4 = rw_uni(ldm4);
-    R.allow_or_row = R.allow ? R.allow : reinterpret_cast<const uint32_t*>(R.row);
-    R.wmax = R.allow ? R.words - 1 : R.ldm4;
-    R.amask = R.allow ? 0u : 15u;
-    R.glast = (R.V - 1) / RW_G;
-    return R;
-}
-// The ordered scan of one tile (a sum pass stopped there): the tile's
-// exact terms from element `start`, from running sum s.
-template <class F>
-__device__ __forceinline__ float rw_slow_tile(const rw_row& R, const F& f, uint32_t g, int start, float s) {
-    float x[4], y[4], v[4];
-    rw_tile(R, rw_sh, g, x, y);
-    f.exact(x, y, v);
-    return rw_slow(v[0], v[1], v[2], v[3], start, s, rw_sh);
-}
-// One sum pass from tile g with running sum s: the streaming pass, or
-// (slow != 0) the ordered scan of tile g from the element the pass left in
-// the shared state. The pass leaves in pass_g the tile it could not finish
-// (ng: none).
-template <class F>
-__device__ __forceinline__ float rw_pass(const rw_row& R, const F& f, float s, uint32_t g, uint32_t slow,
-                                         uint32_t ties) {
-    if (rw_uni(slow)) return rw_slow_tile(R, f, rw_uni(g), rw_sh.pass_start, rw_unif(s));
-    return rw_sum_pass(R, rw_sh, rw_unif(s), ties, f, rw_uni(g));
-}
-__device__ __noinline__ float rw_pass_obs(const float* row, const float* allow, uint32_t V, uint32_t np, uint32_t ldm4,
-                                          float M, float s, uint32_t g, uint32_t slow) {
-    rw_obs_terms f;
-    f.M = rw_unif(M);
-    return rw_pass(rw_row_of(row, allow, V, np, ldm4), f, s, g, slow, 0u);
-}
-__device__ __noinline__ float rw_pass_samp(const float* row, const float* allow, uint32_t V, uint32_t np, uint32_t ldm4,
-                                           float T, float zmax, float thr, uint32_t use_thr, float s, uint32_t g,
-                                           uint32_t slow) {
-    const float Tu = rw_unif(T);
-    const uint32_t div = !(Tu > 0.0f && Tu != 1.0f) ? 0u : ((Tu >= 0x1p-20f && Tu <= 0x1p20f) ? 1u : 2u);
-    auto run = [&](auto f) {
-        f.T = Tu;
-        f.rT = 1.0f / Tu;
-        f.zmax = rw_unif(zmax);
-        f.thr = rw_unif(thr);
-        f.use_thr = rw_uni(use_thr) != 0u;
-        return rw_pass(rw_row_of(row, allow, V, np, ldm4), f, s, g, slow, 1u);
-    };
-    if (rw_uni(div) == 1u) return run(rw_samp_terms<1>{});
-    if (rw_uni(div) == 0u) return run(rw_samp_terms<0>{});
-    return run(rw_samp_terms<2>{});
-}
-__device__ __noinline__ float rw_pass_ent(const float* row, const float* allow, uint32_t V, uint32_t np, uint32_t ldm4,
-                                          float M, float inv, float lns, float s, uint32_t g, uint32_t slow) {
-    rw_ent_terms f;
-    f.M = rw_unif(M);
-    f.inv = rw_unif(inv);
-    f.lns = rw_unif(lns);
-    return rw_pass(rw_row_of(row, allow, V, np, ldm4), f, s, g, slow, 0u);
-}
-
-// Row scratch of the big-row kernels (not in use before they run), 16-byte
-// aligned: a masked row's gathered values.
+// Row scratch of a masked row's gathered values, 16-byte aligned.
 __device__ __forceinline__ float* rw_scratch(const zs_sargs& a, uint32_t r) {
-    float* cx = reinterpret_cast<float*>(a.pairs + (size_t)r * a.max_vocab * 2);
+    float* cx = a.gath + (size_t)r * (2 * (size_t)a.max_vocab + 16);
     return cx + ((4u - (uint32_t)((reinterpret_cast<uintptr_t>(cx) >> 2) & 3u)) & 3u);
 }
 
@@ -1307,24 +639,6 @@ __device__ __noinline__ void rw_small(uint64_t seed, uint64_t counter, uint32_t 
     if (threadIdx.x == 0) sh.tok = tk;
 }
 
-// ---------------------------------------------------------------------------
-// The sampler's S of an unmasked row without a top-k cut (the longest of a
-// row's sums) runs in a workgroup of its own, beside the workgroup that does
-// the row's other phases (when zs_sargs.helpers is set): zs_k_row is launched
-// with 2B workgroups, the first B taking the rows (unmasked rows first: theirs are the long sums), the
-// other B being these helpers (a row that does not qualify ends its helper
-// at once). Workgroups start in index order, so the helpers take the CUs of
-// the first rows to finish (masked rows with few allowed ids) while the
-// unmasked rows are still running.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ bool rw_helped(const zs_sargs& a, const zs_row_params& P) {
-    const zs_batch& b = a.b;
-    const float T = P.temperature;
-    const bool masked = (P.flags & ZS_ROW_MASKED) && b.d_allow_bits;
-    const bool has_topk = P.top_k > 0 && P.top_k < b.V;
-    return a.helpers && !masked && T > 0.0f && T != INFINITY && !has_topk;
-}
-
 // The row of the j-th row workgroup: the unmasked rows in index order, then
 // the masked ones. Uniform.
 __device__ __forceinline__ uint32_t rw_block_row(const zs_batch& b, uint32_t j) {
@@ -1373,74 +687,11 @@ __device__ __forceinline__ uint32_t rw_block_row(const zs_batch& b, uint32_t j) 
     return r;
 }
 
-// The helper: patches (LDS only), the maximum of y, then the sampler's S
-// into the row state (zs_k_row's row workgroup skips that pass and leaves
-// samp_S alone). A row whose y holds a NaN, or whose maximum z is infinite,
-// is not sampled from S (non-finite rows): the helper stops.
-__device__ __forceinline__ void rw_helper(const zs_sargs& a, uint32_t r) {
-    const zs_batch& b = a.b;
-    const zs_row_params P = b.d_params[r];
-    if (!rw_helped(a, P)) return;
-    rw_shared& sh = rw_sh;
-    const uint32_t t = threadIdx.x, V = b.V;
-    const float T = P.temperature;
-    uint32_t has_y = 0;
-    const int np = rw_patches(a, r, P, has_y, sh, false);
-    if (np < 0) return;
-    rw_row R;
-    R.row = b.d_logits + (size_t)r * b.ld;
-    R.allow = nullptr;
-    R.V = V;
-    R.np = rw_uni((uint32_t)np);
-    R.words = (V + 31) / 32;
-    R.ldm4 = (uint32_t)min((uint64_t)b.ld - 4, (uint64_t)0xfffffff0u);
-    R.allow_or_row = reinterpret_cast<const uint32_t*>(R.row);
-    R.wmax = R.ldm4;
-    R.amask = 15u;
-    R.glast = (V - 1) / RW_G;
-    float ymax = -INFINITY;
-    uint32_t nan = 0;
-    rw_stream(R, sh, 0, [&](uint32_t, int, const float (&x)[4], const float (&y)[4]) {
-        ymax = fmaxf(ymax, fmaxf(fmaxf(y[0], y[1]), fmaxf(y[2], y[3])));
-#pragma unroll
-        for (int q = 0; q < 4; q++) nan |= (y[q] != y[q]) ? 1u : 0u;
-        (void)x;
-        return false;
-    });
-    for (int d = 32; d > 0; d >>= 1) {
-        ymax = fmaxf(ymax, __shfl_xor(ymax, d, 64));
-        nan |= __shfl_xor(nan, d, 64);
-    }
-    if (zs_lane() == 0) { sh.rf[0][zs_wid()] = ymax; sh.ru[0][zs_wid()] = nan; }
-    __syncthreads();
-    ymax = -INFINITY; nan = 0;
-#pragma unroll
-    for (int w = 0; w < RW_NW; w++) { ymax = fmaxf(ymax, sh.rf[0][w]); nan |= sh.ru[0][w]; }
-    __syncthreads();
-    const float zmax = rw_unif(zs_temper(ymax, T));
-    if (rw_uni(nan) || zmax == INFINITY || zmax == -INFINITY) return;
-    const uint32_t ng = (V + RW_G - 1) / RW_G;
-    float SB = -0.0f;
-    uint32_t g = 0, slow = 0;
-    while (true) {
-        SB = rw_pass_samp(R.row, nullptr, V, R.np, R.ldm4, T, zmax, -INFINITY, 0u, SB, g, slow);
-        if (slow) { g++; slow = 0; continue; }
-        g = rw_uni(sh.pass_g);
-        if (g >= ng) break;
-        slow = 1;
-    }
-    if (t == 0) a.rst[r].samp_S = SB;
-}
-
 // ---------------------------------------------------------------------------
 // zs_k_row
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
     const zs_batch& b = a.b;
-    if (blockIdx.x >= b.B) {
-        rw_helper(a, blockIdx.x - b.B);
-        return;
-    }
     const uint32_t r = rw_block_row(b, blockIdx.x);
     const uint32_t t = threadIdx.x;
     const uint32_t V = b.V;
@@ -2007,78 +1258,24 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
     }
     __syncthreads();
 
-    // ---------------- P2: observers' S (fast-exp terms: a tolerance output)
-    // and the big rows' sampler S = sum expf(z - max) (sampler.rs:68, exact)
+    // ---------------- the row sums, left to zs_sums.hip: S_obs (logprobs and
+    // uncertainty), the sampler's S of a big row (unless it equals S_obs: z is
+    // x~ and no top-k cut applies), the entropy. A masked row's sums run over
+    // its allowed ids, gathered to row scratch (when at most a quarter of the
+    // row is allowed), else over the whole row with its allow bits.
     const bool doA = (obs_need & ZS_OBS_S) != 0;
-    const bool doB = mode == ZS_MODE_BIG && has_thr != 2;
-    float SA = -0.0f, SB = -0.0f;
-    const float* allow_f = reinterpret_cast<const float*>(R.allow);
-    // the sums' view of the row: the whole row, or a masked row's allowed ids.
-    // The observers' terms see only the bans among the patches (biases and
-    // counts change y, not x~): without a ban their passes skip the patch
-    // list.
-    bool any_ban = false;
-    for (uint32_t i = t; i < (uint32_t)np; i += RW_NT) any_ban |= ((sh.pid[i] >> RW_PF_SHIFT) & ZS_PF_BAN) != 0u;
-    any_ban = __syncthreads_or(any_ban) != 0;
-    const float* px = R.row;
-    const float* py = R.row;
-    uint32_t pV = V, pnp = R.np, pldm4 = R.ldm4;
-    if (R.allow && (doA || doB || (obs_need & ZS_OBS_H))) {
-        float* cx = rw_scratch(a, r);
-        const uint32_t n = rw_uni(sh.g_done) ? rw_uni(sh.g_n) : rw_gather_allowed(R.row, R.allow, V, R.np, cx);
-        if (n) {
-            const uint32_t n4 = (n + 3) & ~3u;
-            px = cx;
-            py = cx + n4;
-            allow_f = nullptr;
-            pV = n;
-            pnp = 0;
-            pldm4 = n4 - 4;
-        }
-    }
-    const uint32_t ngp = (pV + RW_G - 1) / RW_G;
-    // a pass alternates between its streaming function and the ordered scan
-    // of the tiles that need it, until the row is done
-    if (doA) {
-        uint32_t g = 0, slow = 0;
-        while (true) {
-            SA = rw_pass_obs(px, allow_f, pV, any_ban ? pnp : 0u, pldm4, M, SA, g, slow);
-            if (slow) { g++; slow = 0; continue; }
-            g = rw_uni(sh.pass_g);
-            if (g >= ngp) break;
-            slow = 1;
-        }
-    }
-    const bool helped = rw_helped(a, P);   // the helper workgroup sums S (same rule, same inputs)
-    if (doB && !helped) {
-        const uint32_t use_thr = has_thr != 0 ? 1u : 0u;
-        uint32_t g = 0, slow = 0;
-        while (true) {
-            SB = rw_pass_samp(py, allow_f, pV, pnp, pldm4, T, zmax, thr, use_thr, SB, g, slow);
-            if (slow) { g++; slow = 0; continue; }
-            g = rw_uni(sh.pass_g);
-            if (g >= ngp) break;
-            slow = 1;
-        }
-    }
-    // ---------------- P3: entropy (hallucination.rs:139-144; fast-exp terms)
-    float H = 0.0f;
-    if (obs_need & ZS_OBS_H) {
-        const float inv = 1.0f / SA, lns = (float)log((double)SA);
-        uint32_t g = 0, slow = 0;
-        while (true) {
-            H = rw_pass_ent(px, allow_f, pV, any_ban ? pnp : 0u, pldm4, M, inv, lns, H, g, slow);
-            if (slow) { g++; slow = 0; continue; }
-            g = rw_uni(sh.pass_g);
-            if (g >= ngp) break;
-            slow = 1;
-        }
-    }
+    const bool reuse = z_is_x && has_thr == 0 && doA;
+    const bool doB = mode == ZS_MODE_BIG && has_thr != 2 && !reuse;
+    const bool doH = (obs_need & ZS_OBS_H) != 0;
+    uint32_t gn = 0;
+    if (R.allow && (doA || doB || doH))
+        gn = rw_uni(sh.g_done) ? rw_uni(sh.g_n) : rw_gather_allowed(R.row, R.allow, V, R.np, rw_scratch(a, r));
 
-    // ---------------- row state for the big-row kernels and zs_k_final
+    // ---------------- row state for the sums, the big-row kernels and zs_k_final
     if (t == 0) {
         st.rounds = (doB ? (1u << ZS_SUM_SAMP_S) : 0u) | (doA ? (1u << ZS_SUM_OBS_S) : 0u) |
-                    ((obs_need & ZS_OBS_H) ? (1u << ZS_SUM_OBS_H) : 0u);
+                    (doH ? (1u << ZS_SUM_OBS_H) : 0u);
+        st.g_n = gn;
         st.z_max = zmax;
         st.has_thr = has_thr;
         st.thr_key = thr_key;
@@ -2089,14 +1286,12 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
         st.obs_special = special ? 1u : 0u;
         st.obs_need = obs_need;
         st.n_cand = n_cand;
-        // the sampler's S always comes from the exact sum above: the observers'
-        // S uses fast-exp terms
-        st.z_is_x = 0;
+        st.z_is_x = reuse ? 1u : 0u;
         st.klist = 0;
         st.kpend = 0;
-        if (!helped) st.samp_S = SB;
-        st.obs_S = SA;
-        st.obs_H = H;
+        st.samp_S = -0.0f;
+        st.obs_S = -0.0f;
+        st.obs_H = 0.0f;
     }
     if (t < n_cand) { st.cand_id[t] = sh.cand_id[t]; st.cand_x[t] = sh.cand_x[t]; }
     if (mode == ZS_MODE_BIG) {
@@ -2104,11 +1299,10 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
         zs_tp_bucket* bk = a.tp_bk + (size_t)r * ZS_TP_NB;
         for (uint32_t i = t; i < ZS_TP_NB; i += RW_NT) { bk[i].cnt = 0u; bk[i].mass = 0.0f; }
     }
-    (void)z_is_x;
 }
 
 extern "C" int zs_row_launch(const zs_sargs& a, hipStream_t stream) {
     const size_t dyn = 2 * ((a.b.V + 31) / 32) * sizeof(uint32_t);
-    hipLaunchKernelGGL(zs_k_row, dim3(a.helpers ? 2 * a.b.B : a.b.B), dim3(RW_NT), dyn, stream, a);
+    hipLaunchKernelGGL(zs_k_row, dim3(a.b.B), dim3(RW_NT), dyn, stream, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

@@ -1673,10 +1673,10 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
     a.tp_cl = ctx->tp_cl;
     a.tp_pre = ctx->tp_pre;
     a.kcnt = ctx->kcnt;
-    // helper workgroups shorten the row kernel but add work (each repeats its
-    // row's patches and maximum): worth it when the sampler has the GPU to
-    // itself, not when the caller runs other work beside it (pass_event)
-    a.helpers = bt->pass_event ? 0u : 1u;
+    a.s_rec = ctx->s_rec;
+    a.s_apx = ctx->s_apx;
+    a.gath = ctx->gath;
+    a.s_hterm = ctx->s_hterm;
     const uint32_t B = bt->B;
     const uint32_t nch = (bt->V + ZS_P1_CH - 1) / ZS_P1_CH;
     const bool prof = ctx->profiling != 0;
@@ -1691,6 +1691,28 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
     if (a.b.pass_event && hipEventRecord((hipEvent_t)a.b.pass_event, stream) != hipSuccess) return -1;
     if (zs_row_launch(a, stream)) return zs_set_error(ctx, ZS_EHIP, "zs_sample: zs_k_row launch failed");
     mark("zs_k_row");
+    // the row sums: S_obs and the sampler's S here; the entropy (needed only
+    // by zs_k_final) on the context's side stream beside the big-row kernels,
+    // unless profiling, which keeps every kernel on the caller's stream
+    {
+        static const char* const names[5] = {"zs_k_sapx", "zs_k_sround1", "zs_k_sstitch1", "zs_k_sround2",
+                                             "zs_k_sstitch2"};
+        for (uint32_t w = 0; w < 3; w++) {
+            if (zs_sums_launch(a, w, stream)) return zs_set_error(ctx, ZS_EHIP, "zs_sample: row sums launch failed");
+            mark(names[w]);
+        }
+        hipStream_t hs = stream;
+        if (!prof) {
+            hs = (hipStream_t)ctx->side_stream;
+            ZS_LAUNCH_CHECK(hipEventRecord((hipEvent_t)ctx->fork_event, stream));
+            ZS_LAUNCH_CHECK(hipStreamWaitEvent(hs, (hipEvent_t)ctx->fork_event, 0));
+        }
+        for (uint32_t w = 3; w < 5; w++) {
+            if (zs_sums_launch(a, w, hs)) return zs_set_error(ctx, ZS_EHIP, "zs_sample: entropy launch failed");
+            mark(names[w]);
+        }
+        if (!prof) ZS_LAUNCH_CHECK(hipEventRecord((hipEvent_t)ctx->join_event, hs));
+    }
     hipLaunchKernelGGL(zs_k_pv, dim3((bt->V + ZS_BIG_G - 1) / ZS_BIG_G, B), dim3(ZS_BIG_NT), 0, stream, a);
     mark("zs_k_pv");
     hipLaunchKernelGGL(zs_k_tp_plan, dim3(B), dim3(ZS_BIG_NT), 0, stream, a);
@@ -1710,6 +1732,7 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
     hipLaunchKernelGGL(zs_k_roundK<1>, dim3((nsubk + 3) / 4, B), dim3(256), 0, stream, a);
     hipLaunchKernelGGL(zs_k_stitchK<1>, dim3(B), dim3(SK_NT), 0, stream, a);
     mark("zs_k_kept");
+    if (!prof) ZS_LAUNCH_CHECK(hipStreamWaitEvent(stream, (hipEvent_t)ctx->join_event, 0));
     hipLaunchKernelGGL(zs_k_final, dim3(B), dim3(64), 0, stream, a);
     mark("zs_k_final");
     if (prof) ctx->n_timed = ev - 1;

@@ -26,7 +26,10 @@ struct zs_sargs {
     uint32_t* tp_cl;
     uint32_t* tp_pre;
     uint32_t* kcnt;
-    uint32_t helpers;   // zs_k_row: helper workgroups for the longest sums (0 / 1)
+    zs_sub_sum* s_rec;
+    float* s_apx;
+    float* gath;
+    float* s_hterm;
 };
 
 #define ZS_ST_FALLBACK 0x200u
@@ -34,6 +37,9 @@ struct zs_sargs {
 // zs_row.hip: the one-workgroup-per-row front of the step (patches, row
 // statistics, candidates, greedy / small rows, the exact S and entropy sums)
 extern "C" int zs_row_launch(const zs_sargs& a, hipStream_t stream);
+// zs_sums.hip: the row sums S_obs and the sampler's S, then the entropy,
+// spread over the GPU (one kernel per call, `which` 0..4 in launch order)
+extern "C" int zs_sums_launch(const zs_sargs& a, uint32_t which, hipStream_t stream);
 
 __device__ __forceinline__ bool zs_penalty_active(const zs_row_params& P) {
     return P.repeat != 1.0f || P.presence != 0.0f || P.frequency != 0.0f;

@@ -1,0 +1,1063 @@
+// zs_sums.hip -- the row sums of the sampler step, spread over the whole GPU.
+//
+// Three sequential f32 sums per row are reproduced exactly, in index order:
+//   S_obs = sum expf(x~ - M)                 logprobs.rs:36, hallucination.rs:134-135
+//   S     = sum expf(z - zmax), z = y / T    sampler.rs:68 (0 below a top-k cut)
+//   H     = sum -(p ((x~ - M) - ln S_obs)),  p = expf(x~ - M) / S_obs, p > 0
+//                                            hallucination.rs:139-144
+// Inside one binade of the running sum s its values lie on the grid g = ulp(s)
+// and adding a term t moves s by the integer round_half_even(t / g) (zs_math.h),
+// except for an exact half-way term (its rounding follows the parity of s / g)
+// and for the term that carries s out of its binade. A row is cut into
+// sub-chunks of ZS_SUB ids, each taken by one wave:
+//   zs_k_sapx    approximate sums of every sub-chunk (v_exp_f32 terms), from
+//                which the grid of the running sum at each sub-chunk is
+//                predicted (prefix sums, with a margin for the f32 rounding);
+//   zs_k_sround  every sub-chunk whose predicted interval stays inside one
+//                binade adds its increments on that grid: a pair (total from
+//                an even start, total from an odd start), which makes the
+//                half-way terms exact whatever the start;
+//   zs_k_sstitch one wave per (row, sum) walks the sub-chunks in order from
+//                the exact running sum: a sub-chunk whose grid was predicted
+//                right and whose total stays inside the binade moves the sum
+//                by its total; any other (a crossing, a wrong prediction) is
+//                added exactly from its terms: per-lane increment pairs
+//                prefix-scanned over the wave locate the lane where the sum
+//                leaves its binade, whose terms are added as real f32
+//                additions, and the walk resumes on the new grid.
+// A wrong prediction costs time, never exactness: the stitch checks the grid
+// and the binade end of every sub-chunk total it applies.
+//
+// Terms of S_obs and S are exact glibc expf values: a fast exp (relative
+// error below ZS_EXP_EPS) decides an increment unless its scaled value lies
+// within the error band of a half-integer, where zs_expf recomputes it
+// (certified increments); H's terms are certified the same way with a band
+// that covers the two extra f32 roundings of p and of the product.
+#include <hip/hip_runtime.h>
+#include "zs_sampler.h"
+
+#define SM_EPT 16                       // terms per lane of a sub-chunk
+#define SM_NT 256                       // threads of the approx / round kernels (4 sub-chunks)
+#define SM_QCAP 33554432.0f             // increments clamp at 2^25 (any larger one leaves the binade)
+#define SM_EG_MIN 28                    // grids from 2^-122 up take the float-scaled increments
+#define SM_BAND_S 0x1p-21f              // certification band of the exp terms (ZS_EXP_EPS)
+#define SM_BAND_H 0x1p-19f              // of the entropy terms (ZS_EXP_EPS + two roundings)
+#define SM_MARGIN 0x1p-9                // relative margin of the grid prediction
+#define SM_HEAD 128                     // terms added one by one from a sum's first nonzero term
+
+static_assert(ZS_SUB == SM_EPT * 64, "one wave per sub-chunk");
+
+#ifdef ZS_SM_DEBUG
+// working diagnostics: per (row, sum) sub-chunks applied from totals, walks,
+// walk iterations, clock cycles
+__device__ uint32_t sm_dbg[4096 * 3 * 16];
+#define SM_DBG(r, k, i, v) atomicAdd(&sm_dbg[((r) * 3 + (k)) * 16 + (i)], (uint32_t)(v))
+extern "C" int zs_dbg_sum_stats(uint32_t* out, uint32_t n) {
+    if (hipMemcpyFromSymbol(out, HIP_SYMBOL(sm_dbg), n * sizeof(uint32_t)) != hipSuccess) return -1;
+    static uint32_t zero[4096 * 3 * 16];
+    return hipMemcpyToSymbol(HIP_SYMBOL(sm_dbg), zero, sizeof(zero)) == hipSuccess ? 0 : -1;
+}
+#else
+#define SM_DBG(r, k, i, v) ((void)0)
+#endif
+
+// Per (row, sum, sub-chunk) record of zs_k_sround.
+#define SM_SAFE 1u
+struct sm_rec {
+    int32_t eg;       // grid exponent the totals are on
+    uint32_t flags;   // SM_SAFE: totals valid
+    uint32_t d0, d1;  // increments from an even / odd start (saturated at ZS_INC_CAP)
+};
+static_assert(sizeof(sm_rec) == sizeof(zs_sub_sum), "sm_rec lives in the zs_sub_sum scratch");
+
+// ---------------------------------------------------------------------------
+// The terms' source: the row's logits (with the allow bits of a masked row and
+// the merged patch list of zs_k_row), or the allowed ids a masked row gathered
+// to row scratch (x~ and y already patched).
+// ---------------------------------------------------------------------------
+struct sm_src {
+    const float* px;
+    const float* py;
+    const uint32_t* allow;   // row source of a masked row, else null
+    const uint32_t* pid;     // patches (row source), else null
+    const uint32_t* pfl;
+    const float* pyv;
+    const uint32_t* psub;
+    uint32_t n;              // terms
+    uint32_t lim4;           // last float4 start inside px / py
+};
+
+__device__ __forceinline__ const float* sm_gather_base(const zs_sargs& a, uint32_t r) {
+    const float* cx = a.gath + (size_t)r * (2 * (size_t)a.max_vocab + 16);
+    return cx + ((4u - (uint32_t)((reinterpret_cast<uintptr_t>(cx) >> 2) & 3u)) & 3u);
+}
+
+__device__ __forceinline__ sm_src sm_src_of(const zs_sargs& a, uint32_t r, const zs_row_state& st,
+                                            const zs_row_params& P) {
+    const zs_batch& b = a.b;
+    sm_src s;
+    if (st.g_n) {
+        const uint32_t n4 = (st.g_n + 3u) & ~3u;
+        s.px = sm_gather_base(a, r);
+        s.py = s.px + n4;
+        s.allow = nullptr;
+        s.pid = nullptr;
+        s.pfl = nullptr;
+        s.pyv = nullptr;
+        s.psub = nullptr;
+        s.n = st.g_n;
+        s.lim4 = n4 - 4u;
+    } else {
+        s.px = b.d_logits + (size_t)r * b.ld;
+        s.py = s.px;
+        s.allow = ((P.flags & ZS_ROW_MASKED) && b.d_allow_bits) ? b.d_allow_bits + (size_t)r * b.allow_words : nullptr;
+        const bool patched = a.p_cnt[r] != 0u;
+        s.pid = patched ? a.p_id + (size_t)r * ZS_MAX_PATCHES : nullptr;
+        s.pfl = a.p_flags + (size_t)r * ZS_MAX_PATCHES;
+        s.pyv = a.p_y + (size_t)r * ZS_MAX_PATCHES;
+        s.psub = a.p_sub + (size_t)r * (a.max_subs + 1);
+        s.n = b.V;
+        s.lim4 = (uint32_t)min((uint64_t)b.ld - 4u, (uint64_t)0xfffffff0u);
+    }
+    return s;
+}
+
+// Exact terms of the sub-chunks that are not safe, per (row, sum), max_vocab
+// floats: for the two S sums scratch the big-row kernels only use after them
+// (the probability array and the top-p prefix area); the entropy, which runs
+// beside the big-row kernels, has an area of its own.
+__device__ __forceinline__ float* sm_darea(const zs_sargs& a, uint32_t r, int kind) {
+    if (kind == ZS_SUM_OBS_S) return reinterpret_cast<float*>(a.pv + (size_t)r * a.max_vocab);
+    if (kind == ZS_SUM_SAMP_S) return reinterpret_cast<float*>(a.tp_pre + (size_t)r * a.max_vocab * 2);
+    return a.s_hterm + (size_t)r * ((size_t)a.max_vocab + 8);
+}
+
+// Position (in the sub-chunk) of term e of float4 i of this lane: interleaved
+// (i-th quarter of the sub-chunk, coalesced loads: the approx and round
+// kernels) or contiguous (the lane's 16 consecutive terms: the stitch, which
+// needs each lane's terms in summation order).
+template <bool CONTIG>
+__device__ __forceinline__ uint32_t sm_pos(uint32_t lane, int i) {
+    return CONTIG ? 16u * lane + 4u * (uint32_t)i : 256u * (uint32_t)i + 4u * lane;
+}
+
+// A sub-chunk's loads for this lane, issued ahead of their use: the logits
+// (or a masked row's gathered x~), the allow words and up to 64 of the
+// sub-chunk's patches, one per lane.
+typedef float sm_f4 __attribute__((ext_vector_type(4)));
+struct sm_raw {
+    sm_f4 vx[4];
+    uint32_t w[4];
+    uint32_t pid, pfl;
+    float pyv;
+    uint32_t p0, p1;    // the sub-chunk's patch range (uniform)
+};
+
+template <bool CONTIG>
+__device__ __forceinline__ void sm_fetch(const sm_src& S, uint32_t j, sm_raw& R) {
+    const uint32_t lane = (uint32_t)zs_lane();
+    const uint32_t base = j * ZS_SUB;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t id0 = base + sm_pos<CONTIG>(lane, i);
+        const uint32_t ia = min(id0, S.lim4);
+        R.vx[i] = *reinterpret_cast<const sm_f4*>(S.px + ia);
+        R.w[i] = S.allow ? S.allow[min(id0, S.n - 1u) >> 5] : 0xffffffffu;
+    }
+    R.p0 = R.p1 = 0u;
+    if (S.pid) {
+        R.p0 = S.psub[j];
+        R.p1 = S.psub[j + 1];
+        const uint32_t p = R.p0 + lane;
+        if (p < R.p1) {
+            R.pid = S.pid[p];
+            R.pfl = S.pfl[p];
+            R.pyv = S.pyv[p];
+        }
+    }
+}
+
+// x~ and y of the lane's terms from the fetched data: masked-out ids and
+// terms past n read -inf (a zero term); bans set x~ and y to -inf, biased /
+// counted ids take their y from the patch list.
+template <bool CONTIG>
+__device__ __forceinline__ void sm_finish(const sm_src& S, uint32_t j, const sm_raw& R, float (&x)[SM_EPT],
+                                          float (&y)[SM_EPT]) {
+    const uint32_t lane = (uint32_t)zs_lane();
+    const uint32_t base = j * ZS_SUB;
+    const bool gy = S.py != S.px;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t id0 = base + sm_pos<CONTIG>(lane, i);
+        const uint32_t w = R.w[i] >> (id0 & 31u);
+        const float xv[4] = {R.vx[i].x, R.vx[i].y, R.vx[i].z, R.vx[i].w};
+        float yv[4] = {xv[0], xv[1], xv[2], xv[3]};
+        if (gy) {
+            // (gathered rows: y follows the x values; loaded here, not ahead)
+            const sm_f4 vy = *reinterpret_cast<const sm_f4*>(S.py + min(id0, S.lim4));
+            yv[0] = vy.x; yv[1] = vy.y; yv[2] = vy.z; yv[3] = vy.w;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const bool in = ((w >> e) & 1u) && id0 + e < S.n;
+            x[4 * i + e] = in ? xv[e] : -INFINITY;
+            y[4 * i + e] = in ? yv[e] : -INFINITY;
+        }
+    }
+    // patches: each lane holds one of the first 64 (the rest are loaded here)
+    for (uint32_t pb = R.p0; pb < R.p1; pb += 64) {
+        uint32_t pid = R.pid, pfl = R.pfl;
+        float pyv = R.pyv;
+        if (pb != R.p0 && pb + lane < R.p1) {
+            pid = S.pid[pb + lane];
+            pfl = S.pfl[pb + lane];
+            pyv = S.pyv[pb + lane];
+        }
+        const uint32_t cnt = min(R.p1 - pb, 64u);
+        for (uint32_t u = 0; u < cnt; u++) {
+            const uint32_t loc = (uint32_t)__builtin_amdgcn_readlane((int)pid, (int)u) - base;
+            const uint32_t fl = (uint32_t)__builtin_amdgcn_readlane((int)pfl, (int)u);
+            const float yp = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pyv), (int)u));
+            const uint32_t owner = CONTIG ? (loc >> 4) : ((loc >> 2) & 63u);
+            const int slot = CONTIG ? (int)(loc & 15u) : (int)(4u * (loc >> 8) + (loc & 3u));
+            if (owner == lane) {
+#pragma unroll
+                for (int q = 0; q < SM_EPT; q++) {
+                    if (q != slot) continue;
+                    if (fl & ZS_PF_BAN) { x[q] = -INFINITY; y[q] = -INFINITY; }
+                    if (fl & ZS_PF_Y) y[q] = yp;
+                }
+            }
+        }
+    }
+}
+
+template <bool CONTIG>
+__device__ __forceinline__ void sm_load(const sm_src& S, uint32_t j, float (&x)[SM_EPT], float (&y)[SM_EPT]) {
+    sm_raw R;
+    sm_fetch<CONTIG>(S, j, R);
+    sm_finish<CONTIG>(S, j, R, x, y);
+}
+
+// The glibc expf table in LDS (zs_expf_tab): the exact recomputations read it
+// with a short LDS latency instead of a constant-memory load. File-scope LDS
+// objects, so that every access is an LDS instruction (a generic pointer
+// would give flat loads, which also wait for the outstanding global loads).
+__shared__ uint64_t sm_tab[32];
+__device__ __forceinline__ void sm_tab_fill() {
+    const uint64_t T[32] = ZS_EXP2F_TAB;
+    if (threadIdx.x < 32) {
+#pragma unroll
+        for (int i = 0; i < 32; i++)
+            if ((int)threadIdx.x == i) sm_tab[i] = T[i];
+    }
+    __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// Terms of the three sums: the argument d, a fast approximate value (-1: use
+// the exact value) and the exact value.
+// ---------------------------------------------------------------------------
+struct sm_terms {
+    int kind;            // ZS_SUM_*
+    float M;             // observers: the row maximum of x~
+    float T, rT, zmax, thr;
+    uint32_t div;        // sampler: 0 no division, 1 Markstein, 2 IEEE
+    bool use_thr;
+    float inv, lns;      // entropy: 1 / S_obs, ln S_obs
+};
+
+__device__ __forceinline__ sm_terms sm_terms_of(int kind, const zs_row_state& st, const zs_row_params& P) {
+    sm_terms f;
+    f.kind = kind;
+    f.M = st.obs_max;
+    const float T = P.temperature;
+    f.T = T;
+    f.rT = 1.0f / T;
+    f.div = !(T > 0.0f && T != 1.0f) ? 0u : ((T >= 0x1p-20f && T <= 0x1p20f) ? 1u : 2u);
+    f.zmax = st.z_max;
+    f.use_thr = st.has_thr != 0u;
+    f.thr = zs_key_to_float(st.thr_key);
+    f.inv = 1.0f / st.obs_S;
+    f.lns = (float)log((double)st.obs_S);
+    return f;
+}
+
+// z = y / T correctly rounded (sampler.rs:47-51): Markstein's sequence
+// q0 = RN(y rT), q1 = RN(q0 + RN(y - q0 T) rT) is RN(y / T) for 2^-100 <= |y|
+// <= 2^100 and 2^-20 <= T <= 2^20; zeros and infinities divide exactly as
+// y rT; other y (and other T) divide the IEEE way.
+__device__ __forceinline__ float sm_temper(const sm_terms& f, float y) {
+    if (f.div == 0u) return y;
+    if (f.div == 2u) return y / f.T;
+    const float q0 = y * f.rT;
+    const float q1 = fmaf(fmaf(-q0, f.T, y), f.rT, q0);
+    const float a = fabsf(y);
+    if (a >= 0x1p-100f && a <= 0x1p100f) return q1;
+    if (a == 0.0f || a == INFINITY) return q0;
+    return y / f.T;
+}
+
+__device__ __forceinline__ float sm_arg(const sm_terms& f, float x, float y) {
+    if (f.kind == ZS_SUM_SAMP_S) {
+        float z = sm_temper(f, y);
+        if (f.use_thr && z < f.thr) z = -INFINITY;
+        return z - f.zmax;
+    }
+    return x - f.M;
+}
+
+__device__ __forceinline__ float sm_exact(const sm_terms& f, float d) {
+    const float e = zs_expf_tab(d, sm_tab);
+    if (f.kind != ZS_SUM_OBS_H) return e;
+    const float p = e * f.inv;
+    return p > 0.0f ? -(p * (d - f.lns)) : 0.0f;
+}
+
+// -1 where only the exact value decides (subnormal results)
+__device__ __forceinline__ float sm_fast(const sm_terms& f, float d) {
+    const float e = zs_exp_fast(fmaxf(d, ZS_EXP_FAST_MIN));
+    float v = e;
+    if (f.kind == ZS_SUM_OBS_H) v = -((e * f.inv) * (d - f.lns));
+    return d >= ZS_EXP_FAST_MIN ? v : (d < ZS_EXP_ZERO ? 0.0f : -1.0f);
+}
+
+// Increments of the lane's 16 terms on the grid of scale sc = 2^(150 - eg),
+// eg >= SM_EG_MIN, from their fast values a, certified: where the band
+// around a scaled value reaches a half-integer (or a is -1) the exact value
+// decides (the recomputation is a branch taken only by the lanes that need
+// it, skipped by the wave when none does). Terms outside `valid` count 0.
+// *tie: bit q set for an exact half-way increment (then inc[q] is
+// floor(t / g)).
+__device__ __forceinline__ void sm_incs(const sm_terms& f, const float (&a)[SM_EPT], const float (&d)[SM_EPT], float sc,
+                                        uint32_t valid, uint32_t (&inc)[SM_EPT], uint32_t* tie) {
+    const float band = f.kind == ZS_SUM_OBS_H ? SM_BAND_H : SM_BAND_S;
+    uint32_t unc = 0u;
+#pragma unroll
+    for (int q = 0; q < SM_EPT; q++) {
+        const float qv = fminf(a[q] * sc, SM_QCAP);
+        const float rq = rintf(qv);
+        inc[q] = ((valid >> q) & 1u) ? (uint32_t)rq : 0u;
+        const bool u = a[q] < 0.0f || (fmaf(qv, band, fabsf(qv - rq)) >= 0.5f && qv < SM_QCAP);
+        unc |= (u ? 1u : 0u) << q;
+    }
+    unc &= valid;
+    *tie = 0u;
+    if (__builtin_amdgcn_readfirstlane((int)(__ballot(unc != 0u) != 0ull))) {
+#ifdef ZS_SM_DEBUG
+        if (zs_lane() == 0) atomicAdd(&sm_dbg[7], 1u);
+#endif
+        if (unc) {
+            uint32_t tb = 0u;
+#pragma unroll
+            for (int q = 0; q < SM_EPT; q++) {
+                if (!((unc >> q) & 1u)) continue;
+                const float qe = fminf(sm_exact(f, d[q]) * sc, SM_QCAP);
+                float rq = rintf(qe);
+                if (fabsf(qe - rq) == 0.5f) {
+                    tb |= 1u << q;
+                    rq = floorf(qe);
+                }
+                inc[q] = (uint32_t)rq;
+            }
+            *tie = tb;
+        }
+    }
+}
+
+__device__ __forceinline__ float sm_scale(int eg) { return __uint_as_float((uint32_t)(277 - eg) << 23); }
+
+// ---------------------------------------------------------------------------
+// Increment pairs: (total from an even start, total from an odd start).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ seq_pair sm_pair_tie(uint32_t m) {
+    // a half-way term m + 1/2: k + m goes to the even neighbour
+    seq_pair p;
+    p.e = m + (m & 1u);
+    p.o = m + ((m + 1u) & 1u);
+    return p;
+}
+
+// Ordered reduction of pairs over the wave (lane 0 holds the whole wave's
+// pair, lanes in increasing order).
+__device__ __forceinline__ seq_pair sm_wave_pair_reduce(seq_pair p) {
+    const uint32_t lane = (uint32_t)zs_lane();
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        seq_pair o;
+        o.e = (uint32_t)__shfl_down((int)p.e, d, 64);
+        o.o = (uint32_t)__shfl_down((int)p.o, d, 64);
+        if ((lane & (2u * d - 1u)) == 0u && lane + d < 64u) p = seq_compose(p, o);
+    }
+    p.e = (uint32_t)__builtin_amdgcn_readfirstlane((int)p.e);
+    p.o = (uint32_t)__builtin_amdgcn_readfirstlane((int)p.o);
+    return p;
+}
+
+// Inclusive ordered scan of pairs over the wave: shifts by 1, 2, 4, 8 inside
+// each row of 16 lanes, then the rows by broadcasts (DPP moves; a lane
+// without a source receives the identity pair (0, 0)).
+template <int CTRL, int ROWS, bool BC>
+__device__ __forceinline__ seq_pair sm_pair_step(seq_pair p) {
+    seq_pair o;
+    o.e = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)p.e, CTRL, ROWS, 0xf, BC);
+    o.o = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)p.o, CTRL, ROWS, 0xf, BC);
+    // rows outside ROWS keep their value: combine with the identity there
+    return seq_compose(o, p);
+}
+__device__ __forceinline__ seq_pair sm_wave_pair_scan(seq_pair p) {
+    p = sm_pair_step<0x111, 0xf, true>(p);    // row_shr:1
+    p = sm_pair_step<0x112, 0xf, true>(p);    // row_shr:2
+    p = sm_pair_step<0x114, 0xf, true>(p);    // row_shr:4
+    p = sm_pair_step<0x118, 0xf, true>(p);    // row_shr:8
+    p = sm_pair_step<0x142, 0xa, false>(p);   // row_bcast:15
+    p = sm_pair_step<0x143, 0xc, false>(p);   // row_bcast:31
+    return p;
+}
+
+__device__ __forceinline__ uint32_t sm_wave_sum_sat(uint32_t v) {
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) v = zs_sat_add(v, (uint32_t)__shfl_xor((int)v, d, 64));
+    return (uint32_t)__builtin_amdgcn_readfirstlane((int)v);
+}
+
+__device__ __forceinline__ float sm_wave_sum_f(float v) {
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) v += __shfl_xor(v, d, 64);
+    return __uint_as_float((uint32_t)__builtin_amdgcn_readfirstlane((int)__float_as_uint(v)));
+}
+
+// ---------------------------------------------------------------------------
+// zs_k_sapx / zs_k_sround: each wave takes SM_SPW sub-chunks of one row (a
+// workgroup SM_SPB consecutive ones), with the row's set-up done once and the
+// next sub-chunk's loads issued before the current one is computed.
+// ---------------------------------------------------------------------------
+#define SM_SPW 1
+#define SM_SPB (SM_SPW * (SM_NT / 64))
+
+// Sub-chunk i of this wave in its workgroup's range.
+__device__ __forceinline__ uint32_t sm_sub_of(uint32_t i) {
+    return blockIdx.x * SM_SPB + (uint32_t)zs_wid() + (SM_NT / 64) * i;
+}
+
+// ---------------------------------------------------------------------------
+// zs_k_sapx: approximate sums per sub-chunk. Record per sub-chunk: S_obs
+// part, sampler S part, sum of e (x~ - M) for the entropy (v_exp_f32 terms),
+// the largest x~ and the largest y.
+// ---------------------------------------------------------------------------
+#define SM_APX 8   // floats per sub-chunk record
+__global__ __launch_bounds__(SM_NT) void zs_k_sapx(zs_sargs a) {
+    const uint32_t r = blockIdx.y;
+    const zs_row_state& st = a.rst[r];
+    const uint32_t jobs = st.rounds;
+    if (!jobs) return;
+    const zs_row_params P = a.b.d_params[r];
+    const sm_src S = sm_src_of(a, r, st, P);
+    const uint32_t nsub = (S.n + ZS_SUB - 1) / ZS_SUB;
+    if (sm_sub_of(0) >= nsub) return;
+    const float M = st.obs_max, zmax = st.z_max;
+    const float T = P.temperature, rT = 1.0f / T;
+    const bool divide = T > 0.0f && T != 1.0f;
+    const bool use_thr = st.has_thr != 0u;
+    const float thr = zs_key_to_float(st.thr_key);
+    const bool obs = (jobs & ((1u << ZS_SUM_OBS_S) | (1u << ZS_SUM_OBS_H))) != 0u;
+    const bool samp = (jobs & (1u << ZS_SUM_SAMP_S)) != 0u;
+    // (a rolled loop: the copy of the next sub-chunk's loads at its end waits
+    // for them after this sub-chunk's arithmetic)
+    sm_raw Rc, Rn;
+    sm_fetch<false>(S, sm_sub_of(0), Rc);
+#pragma unroll 1
+    for (int i = 0; i < SM_SPW; i++) {
+        const uint32_t j = sm_sub_of(i);
+        if (j >= nsub) break;
+        const bool more = i + 1 < SM_SPW && sm_sub_of(i + 1) < nsub;
+        if (more) sm_fetch<false>(S, sm_sub_of(i + 1), Rn);
+        float x[SM_EPT], y[SM_EPT];
+        sm_finish<false>(S, j, Rc, x, y);
+        float so = 0.0f, ss = 0.0f, sd = 0.0f, mo = -INFINITY, ms = -INFINITY;
+#pragma unroll
+        for (int q = 0; q < SM_EPT; q++) {
+            if (obs) {
+                const float d = x[q] - M;
+                const float e = d >= ZS_EXP_FAST_MIN ? zs_exp_hw(d) : 0.0f;
+                so += e;
+                mo = fmaxf(mo, x[q]);
+                sd += d >= ZS_EXP_FAST_MIN ? e * d : 0.0f;
+            }
+            if (samp) {
+                float z = divide ? y[q] * rT : y[q];
+                if (use_thr && z < thr) z = -INFINITY;
+                const float d = z - zmax;
+                const float e = d >= ZS_EXP_FAST_MIN ? zs_exp_hw(d) : 0.0f;
+                ss += e;
+                ms = fmaxf(ms, y[q]);
+            }
+        }
+        so = sm_wave_sum_f(so);
+        ss = sm_wave_sum_f(ss);
+        sd = sm_wave_sum_f(sd);
+        mo = wave_max_f(mo);
+        ms = wave_max_f(ms);
+        if (zs_lane() == 0) {
+            float4* o = reinterpret_cast<float4*>(a.s_apx + ((size_t)r * a.max_subs + j) * SM_APX);
+            o[0] = make_float4(so, ss, sd, mo);
+            o[1] = make_float4(ms, 0.0f, 0.0f, 0.0f);
+        }
+        if (more) Rc = Rn;
+    }
+}
+
+// Prefix data of the predictions of sub-chunk j (uniform): the sums of the
+// approximate S_obs, sampler S and entropy parts of the sub-chunks before j
+// and the largest x~ and y there.
+struct sm_pre {
+    double so, ss, sd;
+    float mo, ms;
+};
+__device__ __forceinline__ sm_pre sm_pre_of(const zs_sargs& a, uint32_t r, uint32_t j) {
+    const float* ap = a.s_apx + (size_t)r * a.max_subs * SM_APX;
+    sm_pre P = {0.0, 0.0, 0.0, -INFINITY, -INFINITY};
+    for (uint32_t i = (uint32_t)zs_lane(); i < j; i += 64) {
+        const float4 v0 = *reinterpret_cast<const float4*>(ap + (size_t)i * SM_APX);
+        const float v4 = ap[(size_t)i * SM_APX + 4];
+        P.so += (double)v0.x;
+        P.ss += (double)v0.y;
+        P.sd += (double)v0.z;
+        P.mo = fmaxf(P.mo, v0.w);
+        P.ms = fmaxf(P.ms, v4);
+    }
+    P.so = wave_sum_d(P.so);
+    P.ss = wave_sum_d(P.ss);
+    P.sd = wave_sum_d(P.sd);
+    P.mo = wave_max_f(P.mo);
+    P.ms = wave_max_f(P.ms);
+    return P;
+}
+
+// Predicted grid of sub-chunk j of sum `kind` from the approximate prefix
+// sums: the sub-chunk's range [before, after] widened by the margin must stay
+// in one binade of grids >= SM_EG_MIN. The running sum is never below the
+// largest term added so far (the f32 additions of non-negative terms are
+// monotone), which bounds it from below where the margin would reach under
+// a power of two (a sum resting just above one after its largest term).
+// Returns the grid exponent, or 0.
+__device__ __forceinline__ int sm_predict(const zs_sargs& a, uint32_t r, uint32_t j, int kind, const sm_terms& f,
+                                          const sm_pre& P) {
+    const float* own = a.s_apx + ((size_t)r * a.max_subs + j) * SM_APX;
+    double lo, hi;
+    if (kind == ZS_SUM_OBS_H) {
+        const double inv = (double)f.inv, lns = (double)f.lns;
+        lo = inv * (lns * P.so - P.sd);
+        hi = inv * (lns * (P.so + (double)own[0]) - (P.sd + (double)own[2]));
+        lo *= 1.0 - SM_MARGIN;
+    } else {
+        // the largest term before j, exactly: expf(max x~ - M), or expf(z -
+        // zmax) of the largest y (z = y / T is monotone in y; not under a
+        // top-k cut, which the approximate sums apply only approximately)
+        const double pre = kind == ZS_SUM_SAMP_S ? P.ss : P.so;
+        float tmax = 0.0f;
+        if (kind == ZS_SUM_OBS_S) tmax = sm_exact(f, P.mo - f.M);
+        else if (!f.use_thr) tmax = sm_exact(f, sm_temper(f, P.ms) - f.zmax);
+        lo = fmax(pre * (1.0 - SM_MARGIN), (double)tmax);
+        hi = pre + (double)(kind == ZS_SUM_SAMP_S ? own[1] : own[0]);
+    }
+    hi *= 1.0 + SM_MARGIN;
+    if (j == 0 || !(lo > 0x1p-99) || !(hi < 0x1p100)) return 0;
+    const int blo = ilogb(lo), bhi = ilogb(hi);
+    if (blo != bhi) return 0;
+    return blo + 127;   // zs_grid_exp of a normal float in that binade
+}
+
+// Sub-chunk total on grid eg (uniform): the increment pair of the wave's
+// terms in summation order (interleaved layout: quarter i, lane, element).
+__device__ __forceinline__ seq_pair sm_total(const sm_terms& f, const float (&x)[SM_EPT], const float (&y)[SM_EPT],
+                                             int eg) {
+    float dd[SM_EPT], av[SM_EPT];
+#pragma unroll
+    for (int q = 0; q < SM_EPT; q++) {
+        dd[q] = sm_arg(f, x[q], y[q]);
+        av[q] = sm_fast(f, dd[q]);
+    }
+    uint32_t inc[SM_EPT], tie, tot = 0u;
+    sm_incs(f, av, dd, sm_scale(eg), 0xffffu, inc, &tie);
+#pragma unroll
+    for (int q = 0; q < SM_EPT; q++) tot = zs_sat_add(tot, inc[q]);
+    if (!__builtin_amdgcn_readfirstlane((int)(__ballot(tie != 0u) != 0ull))) {
+        const uint32_t s = sm_wave_sum_sat(tot);
+        return seq_pair{s, s};
+    }
+    // half-way terms: ordered pairs, quarter by quarter
+    seq_pair all = {0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        seq_pair lp = {0u, 0u};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int q = 4 * i + e;
+            const seq_pair t = ((tie >> q) & 1u) ? sm_pair_tie(inc[q]) : seq_pair{inc[q], inc[q]};
+            lp = seq_compose(lp, t);
+        }
+        all = seq_compose(all, sm_wave_pair_reduce(lp));
+    }
+    return all;
+}
+
+// ---------------------------------------------------------------------------
+// zs_k_sround<STAGE>: stage 1 the two S sums, stage 2 the entropy (which
+// needs the exact S_obs of stage 1).
+// ---------------------------------------------------------------------------
+template <int STAGE>
+__global__ __launch_bounds__(SM_NT) void zs_k_sround(zs_sargs a) {
+    const uint32_t r = blockIdx.y;
+    const zs_row_state& st = a.rst[r];
+    const uint32_t mine = STAGE == 1 ? ((1u << ZS_SUM_OBS_S) | (1u << ZS_SUM_SAMP_S)) : (1u << ZS_SUM_OBS_H);
+    const uint32_t jobs = st.rounds & mine;
+    if (!jobs) return;
+    const zs_row_params P = a.b.d_params[r];
+    const sm_src S = sm_src_of(a, r, st, P);
+    const uint32_t nsub = (S.n + ZS_SUB - 1) / ZS_SUB;
+    if (blockIdx.x * SM_SPB >= nsub) return;
+    sm_tab_fill();
+    const int kinds[2] = {STAGE == 1 ? ZS_SUM_OBS_S : ZS_SUM_OBS_H, ZS_SUM_SAMP_S};
+    constexpr int NK = STAGE == 1 ? 2 : 1;
+    sm_terms F[NK];
+#pragma unroll
+    for (int u = 0; u < NK; u++) F[u] = sm_terms_of(kinds[u], st, P);
+    if (sm_sub_of(0) >= nsub) return;
+    sm_raw Rc, Rn;
+    sm_fetch<false>(S, sm_sub_of(0), Rc);
+#pragma unroll 1
+    for (int i = 0; i < SM_SPW; i++) {
+        const uint32_t j = sm_sub_of(i);
+        if (j >= nsub) break;
+        const bool more = i + 1 < SM_SPW && sm_sub_of(i + 1) < nsub;
+        if (more) sm_fetch<false>(S, sm_sub_of(i + 1), Rn);
+        float x[SM_EPT], y[SM_EPT];
+        sm_finish<false>(S, j, Rc, x, y);
+        sm_rec* rec = reinterpret_cast<sm_rec*>(a.s_rec) + (size_t)r * ZS_NSUM * a.max_subs + j;
+#pragma unroll
+        for (int u = 0; u < NK; u++) {
+            if (!((jobs >> kinds[u]) & 1u)) continue;
+            const sm_terms& f = F[u];
+            const int eg = sm_predict(a, r, j, kinds[u], f, sm_pre_of(a, r, j));
+            if (eg) {
+                const seq_pair t = sm_total(f, x, y, eg);
+                if (zs_lane() == 0) rec[(size_t)kinds[u] * a.max_subs] = sm_rec{eg, SM_SAFE, t.e, t.o};
+            } else {
+                // the stitch walks this sub-chunk from its exact terms
+                if (zs_lane() == 0) rec[(size_t)kinds[u] * a.max_subs] = sm_rec{0, 0u, 0u, 0u};
+                float* da = sm_darea(a, r, kinds[u]) + (size_t)j * ZS_SUB;
+                // (a rolled loop over the quarters: sixteen inlined exact
+                // exponentials would hold too many registers)
+#pragma unroll 1
+                for (int qi = 0; qi < 4; qi++) {
+                    float xv[4], yv[4];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        xv[e] = qi == 0 ? x[e] : (qi == 1 ? x[4 + e] : (qi == 2 ? x[8 + e] : x[12 + e]));
+                        yv[e] = qi == 0 ? y[e] : (qi == 1 ? y[4 + e] : (qi == 2 ? y[8 + e] : y[12 + e]));
+                    }
+                    const uint32_t p = sm_pos<false>((uint32_t)zs_lane(), qi);
+                    float dv[4];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) dv[e] = sm_exact(f, sm_arg(f, xv[e], yv[e]));
+                    if (j * ZS_SUB + p + 4 <= S.n) {
+                        *reinterpret_cast<sm_f4*>(da + p) = sm_f4{dv[0], dv[1], dv[2], dv[3]};
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; e++)
+                            if (j * ZS_SUB + p + e < S.n) da[p + e] = dv[e];
+                    }
+                }
+            }
+        }
+        if (more) Rc = Rn;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// The exact walk of one sub-chunk by one 256-thread workgroup: thread t holds
+// terms 4t .. 4t+3 of the sub-chunk, in order, from running sum s. Each step
+// takes the terms from `pos` on the grid of s: per-thread increment pairs,
+// prefix-scanned over the workgroup (wave scans, then the wave totals), give
+// the running sum after every thread's terms; the first thread where it
+// leaves the binade walks its terms one by one (increments with the parity of
+// the sum at each half-way term) up to the term that leaves the binade, which
+// it adds as a real f32 addition of the exact value; the next step resumes
+// after that term on the new grid.
+// ---------------------------------------------------------------------------
+#define SW_NT 256
+#define SW_NW (SW_NT / 64)
+#define SW_TPT 4          // terms per thread
+static_assert(SW_NT * SW_TPT == ZS_SUB, "one workgroup per sub-chunk walk");
+
+struct sm_wsh {
+    uint32_t we[2][SW_NW], wo[2][SW_NW];   // per-wave pair totals on the grid (double buffered by step)
+    uint32_t w2[2][SW_NW];                 // per-wave totals on the next grid
+    uint32_t wt2[2][SW_NW];                // per wave: a half-way term on the next grid
+    uint32_t cross[2][SW_NW];              // per wave: a thread of it leaves the binade
+    float s_new[2][SW_NW];
+    uint32_t pos_new[2][SW_NW];
+    float tot_s[2];                        // the sum after the last thread (no crossing)
+    uint32_t first[SW_NW];                 // zero sums: first nonzero term per wave
+    float hs;
+};
+__shared__ sm_wsh sm_sh;
+
+// Workgroup barrier that orders LDS accesses only: __syncthreads() also waits
+// for every outstanding global load of the calling wave, which would drain
+// the loads the stitch keeps in flight for its next walks.
+__device__ __forceinline__ void sm_bar() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+__device__ __forceinline__ float sm_lane_f(float v, uint32_t l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), (int)l));
+}
+
+// Increments of a thread's 4 exact terms (those in `valid`) on grid eg, the
+// half-way flags, and their pair.
+__device__ __forceinline__ seq_pair sm_incs4(const float (&v)[SW_TPT], int eg, uint32_t valid,
+                                             uint32_t (&inc)[SW_TPT], uint32_t& tie) {
+    tie = 0u;
+    if (eg >= SM_EG_MIN) {
+        const float sc = sm_scale(eg);
+#pragma unroll
+        for (int q = 0; q < SW_TPT; q++) {
+            const float qv = fminf(v[q] * sc, SM_QCAP);
+            float rq = rintf(qv);
+            const bool h = fabsf(qv - rq) == 0.5f && ((valid >> q) & 1u);
+            if (h) rq = floorf(qv);
+            tie |= (h ? 1u : 0u) << q;
+            inc[q] = ((valid >> q) & 1u) ? (uint32_t)rq : 0u;
+        }
+    } else {
+        // sums below 2^-99: integer increments
+#pragma unroll
+        for (int q = 0; q < SW_TPT; q++) {
+            uint32_t tq = 0u;
+            inc[q] = ((valid >> q) & 1u) ? zs_seq_inc(v[q], eg, &tq) : 0u;
+            tie |= tq << q;
+        }
+    }
+    seq_pair lp = {0u, 0u};
+    if (tie) {
+#pragma unroll
+        for (int q = 0; q < SW_TPT; q++)
+            lp = seq_compose(lp, ((tie >> q) & 1u) ? sm_pair_tie(inc[q]) : seq_pair{inc[q], inc[q]});
+    } else {
+        uint32_t tot = 0u;
+#pragma unroll
+        for (int q = 0; q < SW_TPT; q++) tot = zs_sat_add(tot, inc[q]);
+        lp = seq_pair{tot, tot};
+    }
+    return lp;
+}
+
+// The walk over the exact terms v (thread t: terms 4t .. 4t+3) from s.
+__device__ __forceinline__ float sm_walk(int kind, const float (&v)[SW_TPT], float s, uint32_t dbg_r) {
+    sm_wsh& sh = sm_sh;
+    const uint32_t t = threadIdx.x, lane = (uint32_t)zs_lane(), wid = (uint32_t)zs_wid();
+    uint32_t pos = 0, par = 0;   // first term not yet added; LDS slot of this step
+    while (pos < ZS_SUB) {
+        if (t == 0) SM_DBG(dbg_r, kind, 2, 1);
+        if (s == 0.0f) {
+            // a zero sum takes its first nonzero term as it is (zero terms
+            // before it leave a +0: -0 + +0 = +0); from there the sum climbs
+            // through a binade at almost every doubling of the number of
+            // terms: the next SM_HEAD terms are added one by one, in order
+            uint32_t my = 0xffffffffu;
+#pragma unroll
+            for (int q = SW_TPT - 1; q >= 0; q--)
+                if (SW_TPT * t + (uint32_t)q >= pos && v[q] != 0.0f) my = SW_TPT * t + (uint32_t)q;
+            const unsigned long long m = __ballot(my != 0xffffffffu);
+            if (lane == 0) sh.first[wid] = m ? (uint32_t)__builtin_amdgcn_readlane((int)my, __ffsll((long long)m) - 1) : 0xffffffffu;
+            sm_bar();
+            uint32_t first = 0xffffffffu;
+#pragma unroll
+            for (int w = 0; w < SW_NW; w++) first = min(first, sh.first[w]);
+            s = s + 0.0f;
+            if (first == 0xffffffffu) return s;
+            const uint32_t end = min(first + SM_HEAD, (uint32_t)ZS_SUB);
+            // the head's terms lie in at most two waves: each wave adds the
+            // ones it holds, in order, the first wave's before the second's
+            const uint32_t w0 = first / (SW_TPT * 64), w1 = (end - 1) / (SW_TPT * 64);
+            float ss = s;
+            for (uint32_t w = w0; w <= w1; w++) {
+                if (wid == w) {
+                    if (w != w0) ss = sh.hs;
+                    for (uint32_t L = 0; L < 64; L++) {
+#pragma unroll
+                        for (int q = 0; q < SW_TPT; q++) {
+                            const uint32_t e = SW_TPT * (64 * w + L) + (uint32_t)q;
+                            if (e >= first && e < end) ss = ss + sm_lane_f(v[q], L);
+                        }
+                    }
+                    if (lane == 0) sh.hs = ss;
+                }
+                sm_bar();
+            }
+            s = sh.hs;
+            pos = end;
+            sm_bar();
+            continue;
+        }
+        const int eg = zs_grid_exp(s);
+        const uint32_t k = zs_grid_k(s);
+        uint32_t valid = 0u;
+#pragma unroll
+        for (int q = 0; q < SW_TPT; q++) valid |= (SW_TPT * t + (uint32_t)q >= pos ? 1u : 0u) << q;
+        uint32_t inc[SW_TPT], tie, inc2[SW_TPT], tie2;
+        const seq_pair lp = sm_incs4(v, eg, valid, inc, tie);
+        // the next grid as well: after a crossing the rest of the sub-chunk
+        // usually stays on it
+        const bool two = eg >= SM_EG_MIN && eg + 1 < 254;
+        uint32_t tot2 = 0u;
+        if (two) {
+            sm_incs4(v, eg + 1, valid, inc2, tie2);
+#pragma unroll
+            for (int q = 0; q < SW_TPT; q++) tot2 = zs_sat_add(tot2, inc2[q]);
+        } else {
+            tie2 = 1u;
+#pragma unroll
+            for (int q = 0; q < SW_TPT; q++) inc2[q] = 0u;
+        }
+        const seq_pair wp = sm_wave_pair_scan(lp);   // inclusive, in the wave
+        const uint32_t w2 = wave_incl_scan_sat(tot2);
+        const bool anyt2w = __ballot(tie2 != 0u) != 0ull;
+        if (lane == 63) {
+            sh.we[par][wid] = wp.e;
+            sh.wo[par][wid] = wp.o;
+            sh.w2[par][wid] = w2;
+            sh.wt2[par][wid] = anyt2w ? 1u : 0u;
+        }
+        sm_bar();
+        seq_pair pre = {0u, 0u};   // the waves before this one
+        uint32_t pre2 = 0u, all2 = 0u, anyt2 = 0u;
+#pragma unroll
+        for (int w = 0; w < SW_NW; w++) {
+            if ((uint32_t)w < wid) {
+                pre = seq_compose(pre, seq_pair{sh.we[par][w], sh.wo[par][w]});
+                pre2 = zs_sat_add(pre2, sh.w2[par][w]);
+            }
+            all2 = zs_sat_add(all2, sh.w2[par][w]);
+            anyt2 |= sh.wt2[par][w];
+        }
+        const seq_pair incl = seq_compose(pre, wp);
+        const uint32_t kend = zs_sat_add(k, (k & 1u) ? incl.o : incl.e);
+        const unsigned long long bad = __ballot(kend >= ZS_BINADE);
+        // the exclusive prefix of the first thread that leaves the binade
+        seq_pair ex;
+        ex.e = (uint32_t)__shfl_up((int)wp.e, 1, 64);
+        ex.o = (uint32_t)__shfl_up((int)wp.o, 1, 64);
+        if (lane == 0) ex = seq_pair{0u, 0u};
+        ex = seq_compose(pre, ex);
+        const uint32_t L = bad ? (uint32_t)(__ffsll((long long)bad) - 1) : 64u;
+        if (lane == L) {
+            uint32_t kk = zs_sat_add(k, (k & 1u) ? ex.o : ex.e);
+            int qx = SW_TPT - 1;
+            bool found = false;
+#pragma unroll
+            for (int q = 0; q < SW_TPT; q++) {
+                if (found || !((valid >> q) & 1u)) continue;
+                const uint32_t kn = zs_sat_add(kk, ((tie >> q) & 1u) ? inc[q] + ((kk + inc[q]) & 1u) : inc[q]);
+                if (kn >= ZS_BINADE) { qx = q; found = true; }
+                else kk = kn;
+            }
+            float vx = 0.0f;
+            uint32_t after2 = 0u;   // this thread's next-grid increments after the crossing term
+#pragma unroll
+            for (int q = 0; q < SW_TPT; q++) {
+                if (q == qx) vx = v[q];
+                if (q > qx) after2 = zs_sat_add(after2, inc2[q]);
+            }
+            const float sx = zs_grid_value(kk, eg) + vx;   // the term that leaves the binade
+            float sn = sx;
+            uint32_t pn = SW_TPT * t + (uint32_t)qx + 1u;
+            if (two && !anyt2 && zs_grid_exp(sx) == eg + 1) {
+                // the rest on the next grid: its total minus the terms through
+                // the crossing (no half-way term there, so plain sums)
+                const uint32_t rest = zs_sat_add(all2 - min(all2, zs_sat_add(pre2, w2)), after2);
+                const uint32_t k2 = zs_sat_add(zs_grid_k(sx), rest);
+                if (all2 < ZS_INC_CAP && k2 < ZS_BINADE) {
+                    sn = zs_grid_value(k2, eg + 1);
+                    pn = ZS_SUB;
+                }
+            }
+            sh.s_new[par][wid] = sn;
+            sh.pos_new[par][wid] = pn;
+        }
+        if (lane == 0) sh.cross[par][wid] = bad ? 1u : 0u;
+        if (t == SW_NT - 1) sh.tot_s[par] = kend < ZS_BINADE ? zs_grid_value(kend, eg) : 0.0f;
+        sm_bar();
+        int cw = -1;
+#pragma unroll
+        for (int w = SW_NW - 1; w >= 0; w--)
+            if (sh.cross[par][w]) cw = w;
+        if (cw < 0) return sh.tot_s[par];
+        s = sh.s_new[par][cw];
+        pos = sh.pos_new[par][cw];
+        par ^= 1u;
+    }
+    return s;
+}
+
+// ---------------------------------------------------------------------------
+// zs_k_sstitch<STAGE>: one 256-thread workgroup per (row, sum). Runs of
+// sub-chunks whose totals apply (safe, on the grid of the running sum, inside
+// its binade) are taken 64 at a time with a pair scan (every wave the same);
+// the others are walked exactly from the term arguments the round kernel
+// stored for them (loaded two walks ahead), or from the source for a safe
+// sub-chunk whose total did not apply.
+// ---------------------------------------------------------------------------
+// First sub-chunk from j whose record is not safe (nsub: none); uniform.
+__device__ __forceinline__ uint32_t sm_next_fragile(const sm_rec* R, uint32_t j, uint32_t nsub) {
+    for (uint32_t i0 = j; i0 < nsub; i0 += 64) {
+        const uint32_t i = i0 + (uint32_t)zs_lane();
+        const unsigned long long m = __ballot(i < nsub && !(R[i].flags & SM_SAFE));
+        if (m) return i0 + (uint32_t)(__ffsll((long long)m) - 1);
+    }
+    return nsub;
+}
+
+// A thread's 4 exact terms of sub-chunk j straight from the source (x~ / y
+// with mask and patches): the rare safe sub-chunk whose total did not apply.
+__device__ __forceinline__ void sm_terms_src(const sm_src& S, const sm_terms& f, uint32_t j, float (&d)[SW_TPT]) {
+    const uint32_t id0 = j * ZS_SUB + SW_TPT * threadIdx.x;
+    const uint32_t ia = min(id0, S.lim4);
+    const sm_f4 vx = *reinterpret_cast<const sm_f4*>(S.px + ia);
+    const sm_f4 vy = *reinterpret_cast<const sm_f4*>(S.py + ia);
+    float x[4] = {vx.x, vx.y, vx.z, vx.w}, y[4] = {vy.x, vy.y, vy.z, vy.w};
+    const uint32_t w = S.allow ? S.allow[min(id0, S.n - 1u) >> 5] >> (id0 & 31u) : 0xffffffffu;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        if (!((w >> e) & 1u) || id0 + e >= S.n) { x[e] = -INFINITY; y[e] = -INFINITY; }
+    }
+    if (S.pid) {
+        for (uint32_t p = S.psub[j]; p < S.psub[j + 1]; p++) {
+            const uint32_t id = S.pid[p];
+            if (id < id0 || id >= id0 + 4) continue;
+            const uint32_t fl = S.pfl[p];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                if (id != id0 + e) continue;
+                if (fl & ZS_PF_BAN) { x[e] = -INFINITY; y[e] = -INFINITY; }
+                if (fl & ZS_PF_Y) y[e] = S.pyv[p];
+            }
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e++) d[e] = sm_exact(f, sm_arg(f, x[e], y[e]));
+}
+
+template <int STAGE>
+__global__ __launch_bounds__(SW_NT) void zs_k_sstitch(zs_sargs a) {
+    __shared__ sm_rec R[ZS_MAX_SUBS];
+    const uint32_t r = blockIdx.x;
+    zs_row_state* stp = a.rst + r;
+    const int kind = STAGE == 1 ? (blockIdx.y == 0 ? ZS_SUM_OBS_S : ZS_SUM_SAMP_S) : ZS_SUM_OBS_H;
+    if (!((stp->rounds >> kind) & 1u)) return;
+    sm_tab_fill();
+    const zs_row_state& st = *stp;
+    const zs_row_params P = a.b.d_params[r];
+    const sm_src S = sm_src_of(a, r, st, P);
+    const sm_terms f = sm_terms_of(kind, st, P);
+    const uint32_t nsub = (S.n + ZS_SUB - 1) / ZS_SUB;
+    const uint32_t t = threadIdx.x, lane = (uint32_t)zs_lane();
+    const sm_rec* rec = reinterpret_cast<const sm_rec*>(a.s_rec) + ((size_t)r * ZS_NSUM + kind) * a.max_subs;
+    for (uint32_t i = t; i < nsub; i += SW_NT) R[i] = rec[i];
+    __syncthreads();
+    const float* darea = sm_darea(a, r, kind);
+    float s = kind == ZS_SUM_OBS_H ? 0.0f : -0.0f;
+#ifdef ZS_SM_DEBUG
+    const uint64_t t0 = wall_clock64();
+#endif
+    // the next two sub-chunks to walk and their argument loads
+    uint32_t nf0 = sm_next_fragile(R, 0, nsub);
+    uint32_t nf1 = nf0 < nsub ? sm_next_fragile(R, nf0 + 1, nsub) : nsub;
+    auto ld = [&](uint32_t jj) -> sm_f4 {
+        return *reinterpret_cast<const sm_f4*>(darea + min(jj * ZS_SUB + SW_TPT * t, S.n - 1u & ~3u));
+    };
+    sm_f4 q0 = {0.0f, 0.0f, 0.0f, 0.0f}, q1 = q0;
+    if (nf0 < nsub) q0 = ld(nf0);
+    if (nf1 < nsub) q1 = ld(nf1);
+    uint32_t j = 0;
+    while (j < nsub) {
+#ifdef ZS_SM_DEBUG
+        uint64_t c0 = clock64();
+#endif
+        if (s != 0.0f) {
+            // sub-chunks j .. j+63 on the grid of s, applied up to the first
+            // one that is not safe, is on another grid or leaves the binade
+            const int eg = zs_grid_exp(s);
+            const uint32_t k = zs_grid_k(s);
+            const uint32_t i = j + lane;
+            const sm_rec e = i < nsub ? R[i] : sm_rec{0, 0u, 0u, 0u};
+            const bool ok = (e.flags & SM_SAFE) && e.eg == eg;
+            const seq_pair p = sm_wave_pair_scan(ok ? seq_pair{e.d0, e.d1} : seq_pair{ZS_INC_CAP, ZS_INC_CAP});
+            const uint32_t kend = zs_sat_add(k, (k & 1u) ? p.o : p.e);
+            const unsigned long long bad = __ballot(!(ok && kend < ZS_BINADE));
+            const uint32_t n_ok = bad ? (uint32_t)(__ffsll((long long)bad) - 1) : 64u;
+            if (n_ok) {
+                if (t == 0) SM_DBG(r, kind, 0, n_ok);
+#ifdef ZS_SM_DEBUG
+                if (t == 0) SM_DBG(r, kind, 4, (clock64() - c0) / 16);
+#endif
+                s = zs_grid_value((uint32_t)__builtin_amdgcn_readlane((int)kend, (int)n_ok - 1), eg);
+                j += n_ok;
+                continue;
+            }
+        }
+        if (t == 0) SM_DBG(r, kind, 1, (R[j].flags & SM_SAFE) ? 1 : 0x10000);
+        float d[SW_TPT];
+        if (j == nf0) {
+            d[0] = q0.x; d[1] = q0.y; d[2] = q0.z; d[3] = q0.w;
+            nf0 = nf1;
+            q0 = q1;
+            nf1 = nf0 < nsub ? sm_next_fragile(R, nf0 + 1, nsub) : nsub;
+            if (nf1 < nsub) q1 = ld(nf1);
+            const uint32_t id0 = j * ZS_SUB + SW_TPT * t;
+#pragma unroll
+            for (int e = 0; e < SW_TPT; e++)
+                if (id0 + e >= S.n) d[e] = 0.0f;
+        } else {
+            sm_terms_src(S, f, j, d);
+        }
+#ifdef ZS_SM_DEBUG
+        uint64_t c1 = clock64();
+        if (t == 0) SM_DBG(r, kind, 5, (c1 - c0) / 16);
+#endif
+        s = sm_walk(kind, d, s, r);
+        sm_bar();
+#ifdef ZS_SM_DEBUG
+        if (t == 0) SM_DBG(r, kind, 6, (clock64() - c1) / 16);
+#endif
+        j++;
+    }
+#ifdef ZS_SM_DEBUG
+    if (t == 0) SM_DBG(r, kind, 3, wall_clock64() - t0);
+#endif
+    if (t == 0) {
+        if (kind == ZS_SUM_OBS_S) stp->obs_S = s;
+        else if (kind == ZS_SUM_SAMP_S) stp->samp_S = s;
+        else stp->obs_H = s;
+    }
+}
+
+// Launches one kernel of the row sums: 0 zs_k_sapx, 1 zs_k_sround<1>,
+// 2 zs_k_sstitch<1>, 3 zs_k_sround<2>, 4 zs_k_sstitch<2>.
+extern "C" int zs_sums_launch(const zs_sargs& a, uint32_t which, hipStream_t stream) {
+    const uint32_t nsub = (a.b.V + ZS_SUB - 1) / ZS_SUB;
+    const dim3 grid((nsub + SM_SPB - 1) / SM_SPB, a.b.B);
+    switch (which) {
+        case 0: hipLaunchKernelGGL(zs_k_sapx, grid, dim3(SM_NT), 0, stream, a); break;
+        case 1: hipLaunchKernelGGL(zs_k_sround<1>, grid, dim3(SM_NT), 0, stream, a); break;
+        case 2: hipLaunchKernelGGL(zs_k_sstitch<1>, dim3(a.b.B, 2), dim3(SW_NT), 0, stream, a); break;
+        case 3: hipLaunchKernelGGL(zs_k_sround<2>, grid, dim3(SM_NT), 0, stream, a); break;
+        case 4: hipLaunchKernelGGL(zs_k_sstitch<2>, dim3(a.b.B, 1), dim3(SW_NT), 0, stream, a); break;
+        default: return -1;
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
