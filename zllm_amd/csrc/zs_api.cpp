@@ -163,7 +163,7 @@ extern "C" int zs_ctx_create(int device, uint32_t max_rows, uint32_t max_vocab, 
     if (!rc) rc = zs_alloc(ctx, &ctx->p_flags, R * ZS_MAX_PATCHES);
     if (!rc) rc = zs_alloc(ctx, &ctx->p_y, R * ZS_MAX_PATCHES);
     if (!rc) rc = zs_alloc(ctx, &ctx->rst, R);
-    if (!rc) rc = zs_alloc(ctx, &ctx->pairs, R * (size_t)max_vocab * 2);
+    if (!rc) rc = zs_alloc(ctx, &ctx->pairs, R * (size_t)max_vocab * 2 + 8);  // 16-byte loads at the tail
     if (!rc) rc = zs_alloc(ctx, &ctx->pv, R * (size_t)max_vocab + 4);  // 16-byte loads at the tail
     if (!rc) rc = zs_alloc(ctx, (uint32_t**)&ctx->mask_scratch, R);
     // epochs start at 1 over zeroed flags (set-up only, outside any stream

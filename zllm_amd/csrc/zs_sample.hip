@@ -27,6 +27,7 @@
 #include "zs_seq.h"
 #include "zs_terms.h"
 #include "zs_sampler.h"
+#include "zs_walk.h"
 
 // Saturating sum over the wave (the kept-list sums' per-wave totals).
 __device__ __forceinline__ uint32_t wave_sum_sat(uint32_t v) {
@@ -1392,7 +1393,9 @@ __device__ __forceinline__ float klist_term(const klist_row& L, uint32_t i) {
     return L.inv != 0.0f ? p / L.sum2 : p;
 }
 
-// one wave per (sub-chunk, row)
+// one wave per (sub-chunk, row): the increment pair of the sub-chunk on the
+// grid predicted from the approximate prefix (terms in order: the q-th 64
+// entries, lanes in order)
 template <int KIND>
 __global__ __launch_bounds__(256) void zs_k_roundK(zs_sargs a) {
     const uint32_t r = blockIdx.y;
@@ -1411,115 +1414,107 @@ __global__ __launch_bounds__(256) void zs_k_roundK(zs_sargs a) {
     const double lo = pre * scale, hi = (pre + ap[j]) * scale;
     const double delta = 1.0 / 256.0;
     const double lm = lo * (1.0 - delta), hm = hi * (1.0 + delta);
-    const int blo = lm < 0x1p-125 ? -125 : ilogb(lm);
-    const int bhi = hm < 0x1p-125 ? -125 : ilogb(hm);
-    zs_sub_sum e;
-    e.pad = 0;
-    if (j == 0 || blo != bhi || !(hm < 3.0e38)) {
-        e.eg = 0;
-        e.flags = ZS_SF_FRAGILE;
-        e.total = 0;
-    } else {
-        e.eg = zs_grid_exp((float)lo);
-        uint32_t tot = 0, tie = 0;
+    sm_rec e = {0, 0u, 0u, 0u};
+    if (j != 0 && lm > 0x1p-99 && hm < 0x1p100 && ilogb(lm) == ilogb(hm)) {
+        e.eg = ilogb(lm) + 127;
+        const float sc = sm_scale(e.eg);
+        uint32_t inc[ZS_SUB / 64], tie = 0u, tot = 0u;
 #pragma unroll
         for (int q = 0; q < ZS_SUB / 64; q++) {
-            uint32_t tq;
-            tot = zs_sat_add(tot, zs_seq_inc(klist_term(L, j * ZS_SUB + q * 64 + zs_lane()), e.eg, &tq));
-            tie |= tq;
+            const float qv = fminf(klist_term(L, j * ZS_SUB + q * 64 + zs_lane()) * sc, SM_QCAP);
+            float rq = rintf(qv);
+            if (fabsf(qv - rq) == 0.5f) {
+                tie |= 1u << q;
+                rq = floorf(qv);
+            }
+            inc[q] = (uint32_t)rq;
+            tot = zs_sat_add(tot, inc[q]);
         }
-        tot = wave_sum_sat(tot);
-        tie = wave_or_u(tie);
-        e.total = tot;
-        e.flags = ZS_SF_DONE | (tie ? ZS_SF_TIE : 0u);
+        seq_pair all;
+        if (!__builtin_amdgcn_readfirstlane((int)(__ballot(tie != 0u) != 0ull))) {
+            const uint32_t t = sm_wave_sum_sat(tot);
+            all = seq_pair{t, t};
+        } else {
+            all = seq_pair{0u, 0u};
+#pragma unroll
+            for (int q = 0; q < ZS_SUB / 64; q++)
+                all = seq_compose(all, sm_wave_pair_reduce(((tie >> q) & 1u) ? sm_pair_tie(inc[q])
+                                                                              : seq_pair{inc[q], inc[q]}));
+        }
+        e.flags = SM_SAFE;
+        e.d0 = all.e;
+        e.d1 = all.o;
     }
-    if (zs_lane() == 0) a.k_sum[((size_t)r * 2 + KIND) * a.max_subs + j] = e;
+    if (zs_lane() == 0) reinterpret_cast<sm_rec*>(a.k_sum)[((size_t)r * 2 + KIND) * a.max_subs + j] = e;
 }
 
+// Kept-list terms for sm_stitch: thread t's 4 consecutive entries.
+struct klist_raw {
+    uint4 p, i;
+};
+struct klist_tp {
+    const klist_row& L;
+    __device__ __forceinline__ uint32_t at(uint32_t j) const {
+        return min(j * ZS_SUB + SW_TPT * threadIdx.x, (L.nk - 1u) & ~3u);
+    }
+    __device__ __forceinline__ void fetch(uint32_t j, klist_raw& raw) const {
+        const uint32_t i = at(j);
+        raw.p = *reinterpret_cast<const uint4*>(L.kp + i);
+        raw.i = *reinterpret_cast<const uint4*>(L.ki + i);
+    }
+    __device__ __forceinline__ void take(uint32_t j, const klist_raw& raw, float (&v)[SW_TPT]) const {
+        const uint32_t i0 = j * ZS_SUB + SW_TPT * threadIdx.x;
+        const uint32_t pb[4] = {raw.p.x, raw.p.y, raw.p.z, raw.p.w}, id[4] = {raw.i.x, raw.i.y, raw.i.z, raw.i.w};
+#pragma unroll
+        for (int e = 0; e < SW_TPT; e++) {
+            float p = 0.0f;
+            if (i0 + e < L.nk && (pb[e] > L.vstar || id[e] <= L.istar)) {
+                p = zs_u2f(pb[e]);
+                if (L.inv != 0.0f) p = p / L.sum2;
+            }
+            v[e] = p;
+        }
+    }
+    __device__ __forceinline__ void direct(uint32_t j, float (&v)[SW_TPT]) const {
+        klist_raw raw;
+        fetch(j, raw);
+        take(j, raw, v);
+    }
+};
+
 // one workgroup per row: sum2 (KIND 0), or the draw (KIND 1) -- the first
-// entry after which the running sum reaches the uniform
-#define SK_NT 512
-#define SK_EPT (ZS_SUB / SK_NT)
+// entry after which the running sum reaches the uniform (zs_walk.h)
 template <int KIND>
-__global__ __launch_bounds__(SK_NT) void zs_k_stitchK(zs_sargs a) {
+__global__ __launch_bounds__(SW_NT) void zs_k_stitchK(zs_sargs a) {
     const uint32_t r = blockIdx.x;
     zs_row_state* stp = a.rst + r;
     if (!stp->klist) return;
     const zs_row_state st = *stp;
-    __shared__ seq_sh<SK_NT> sh;
-    __shared__ zs_sub_sum rec[ZS_MAX_SUBS];
-    const int t = threadIdx.x;
     const klist_row L = make_klist(a, r, st, KIND);
     const uint32_t nks = (L.nk + ZS_SUB - 1) / ZS_SUB;
-    const zs_sub_sum* ks = a.k_sum + ((size_t)r * 2 + KIND) * a.max_subs;
-    for (uint32_t j = t; j < nks; j += SK_NT) rec[j] = ks[j];
+    const sm_rec* ks = reinterpret_cast<const sm_rec*>(a.k_sum) + ((size_t)r * 2 + KIND) * a.max_subs;
+    for (uint32_t j = threadIdx.x; j < nks; j += SW_NT) sm_sh.rec[j] = ks[j];
     __syncthreads();
     float thresh = NAN;
-    uint32_t token = a.b.V - 1;
-    bool done = false;
     if (KIND == 1) {
         const float rr = zs_philox_uniform(a.b.d_seed[r], a.b.d_counter[r], 0u);
-        if (rr <= 0.0f) { token = 0; done = true; }  // cumsum >= r at the first id
+        if (rr <= 0.0f) {  // cumsum >= r at id 0 (sampler.rs:118-127)
+            if (threadIdx.x == 0) {
+                stp->token = 0;
+                stp->mode = ZS_MODE_DONE;
+            }
+            return;
+        }
         thresh = rr;
     }
-    float s = KIND ? 0.0f : -0.0f;
-    for (uint32_t j = 0; j < nks && !done; j++) {
-        const zs_sub_sum e = rec[j];
-        const int eg = zs_grid_exp(s);
-        const uint32_t k0 = zs_grid_k(s);
-        if ((e.flags & ZS_SF_DONE) && !(e.flags & (ZS_SF_FRAGILE | ZS_SF_TIE)) && e.eg == eg &&
-            k0 + e.total < ZS_BINADE) {
-            const uint32_t kthr = KIND ? zs_grid_thresh(thresh, eg) : 0xffffffffu;
-            if (kthr == 0xffffffffu || k0 + e.total < kthr) {
-                s = zs_grid_value(k0 + e.total, eg);
-                continue;
-            }
-        }
-        float tv[SK_EPT];
-#pragma unroll
-        for (int q = 0; q < SK_EPT; q++) tv[q] = klist_term(L, j * ZS_SUB + SK_EPT * t + q);
-        int start = 0;
-        if (j == 0) {
-            // the list's first SK_EPT * 64 terms, where the sum leaves a binade
-            // at almost every doubling of the number of terms: wave 0 adds
-            // them one by one (the reference's own additions, and its stop)
-            __shared__ float s0;
-            __shared__ int stop0;
-            if (t < 64) {
-                float ss = s;
-                int sp = -1;
-                for (int Lq = 0; Lq < 64 && sp < 0; Lq++) {
-#pragma unroll
-                    for (int q = 0; q < SK_EPT; q++) {
-                        if (sp >= 0) break;
-                        ss = ss + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, tv[q]), Lq));
-                        if (KIND == 1 && ss >= thresh) sp = SK_EPT * Lq + q;
-                    }
-                }
-                if (t == 0) { s0 = ss; stop0 = sp; }
-            }
-            __syncthreads();
-            s = s0;
-            const int sp = stop0;
-            __syncthreads();
-            if (sp >= 0) {
-                token = L.ki[(uint32_t)sp];
-                done = true;
-                continue;
-            }
-            start = SK_EPT * 64;
-        }
-        const int stop = seq_group<SK_NT, SK_EPT>(tv, start, s, thresh, sh);
-        if (KIND == 1 && stop >= 0) {
-            token = L.ki[j * ZS_SUB + (uint32_t)stop];
-            done = true;
-        }
-    }
-    if (t == 0) {
+    klist_tp tp{L};
+    uint32_t stop;
+    const float s = sm_stitch<klist_tp, klist_raw>(tp, nks, KIND ? 0.0f : -0.0f, thresh, &stop);
+    if (threadIdx.x == 0) {
         if (KIND == 0) {
             stp->sum2 = s;
         } else {
-            stp->token = token;
+            stp->token = stop != 0xffffffffu ? L.ki[stop] : a.b.V - 1;
             stp->mode = ZS_MODE_DONE;
         }
     }
@@ -1728,9 +1723,9 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
     mark("zs_k_kcompact");
     const uint32_t nsubk = (bt->V + ZS_SUB - 1) / ZS_SUB;
     hipLaunchKernelGGL(zs_k_roundK<0>, dim3((nsubk + 3) / 4, B), dim3(256), 0, stream, a);
-    hipLaunchKernelGGL(zs_k_stitchK<0>, dim3(B), dim3(SK_NT), 0, stream, a);
+    hipLaunchKernelGGL(zs_k_stitchK<0>, dim3(B), dim3(SW_NT), 0, stream, a);
     hipLaunchKernelGGL(zs_k_roundK<1>, dim3((nsubk + 3) / 4, B), dim3(256), 0, stream, a);
-    hipLaunchKernelGGL(zs_k_stitchK<1>, dim3(B), dim3(SK_NT), 0, stream, a);
+    hipLaunchKernelGGL(zs_k_stitchK<1>, dim3(B), dim3(SW_NT), 0, stream, a);
     mark("zs_k_kept");
     if (!prof) ZS_LAUNCH_CHECK(hipStreamWaitEvent(stream, (hipEvent_t)ctx->join_event, 0));
     hipLaunchKernelGGL(zs_k_final, dim3(B), dim3(64), 0, stream, a);

@@ -35,39 +35,17 @@
 // that covers the two extra f32 roundings of p and of the product.
 #include <hip/hip_runtime.h>
 #include "zs_sampler.h"
+#include "zs_walk.h"
 
 #define SM_EPT 16                       // terms per lane of a sub-chunk
 #define SM_NT 256                       // threads of the approx / round kernels (4 sub-chunks)
-#define SM_QCAP 33554432.0f             // increments clamp at 2^25 (any larger one leaves the binade)
-#define SM_EG_MIN 28                    // grids from 2^-122 up take the float-scaled increments
 #define SM_BAND_S 0x1p-21f              // certification band of the exp terms (ZS_EXP_EPS)
 #define SM_BAND_H 0x1p-19f              // of the entropy terms (ZS_EXP_EPS + two roundings)
 #define SM_MARGIN 0x1p-9                // relative margin of the grid prediction
-#define SM_HEAD 128                     // terms added one by one from a sum's first nonzero term
 
 static_assert(ZS_SUB == SM_EPT * 64, "one wave per sub-chunk");
 
-#ifdef ZS_SM_DEBUG
-// working diagnostics: per (row, sum) sub-chunks applied from totals, walks,
-// walk iterations, clock cycles
-__device__ uint32_t sm_dbg[4096 * 3 * 16];
-#define SM_DBG(r, k, i, v) atomicAdd(&sm_dbg[((r) * 3 + (k)) * 16 + (i)], (uint32_t)(v))
-extern "C" int zs_dbg_sum_stats(uint32_t* out, uint32_t n) {
-    if (hipMemcpyFromSymbol(out, HIP_SYMBOL(sm_dbg), n * sizeof(uint32_t)) != hipSuccess) return -1;
-    static uint32_t zero[4096 * 3 * 16];
-    return hipMemcpyToSymbol(HIP_SYMBOL(sm_dbg), zero, sizeof(zero)) == hipSuccess ? 0 : -1;
-}
-#else
-#define SM_DBG(r, k, i, v) ((void)0)
-#endif
 
-// Per (row, sum, sub-chunk) record of zs_k_sround.
-#define SM_SAFE 1u
-struct sm_rec {
-    int32_t eg;       // grid exponent the totals are on
-    uint32_t flags;   // SM_SAFE: totals valid
-    uint32_t d0, d1;  // increments from an even / odd start (saturated at ZS_INC_CAP)
-};
 static_assert(sizeof(sm_rec) == sizeof(zs_sub_sum), "sm_rec lives in the zs_sub_sum scratch");
 
 // ---------------------------------------------------------------------------
@@ -344,9 +322,6 @@ __device__ __forceinline__ void sm_incs(const sm_terms& f, const float (&a)[SM_E
     unc &= valid;
     *tie = 0u;
     if (__builtin_amdgcn_readfirstlane((int)(__ballot(unc != 0u) != 0ull))) {
-#ifdef ZS_SM_DEBUG
-        if (zs_lane() == 0) atomicAdd(&sm_dbg[7], 1u);
-#endif
         if (unc) {
             uint32_t tb = 0u;
 #pragma unroll
@@ -363,62 +338,6 @@ __device__ __forceinline__ void sm_incs(const sm_terms& f, const float (&a)[SM_E
             *tie = tb;
         }
     }
-}
-
-__device__ __forceinline__ float sm_scale(int eg) { return __uint_as_float((uint32_t)(277 - eg) << 23); }
-
-// ---------------------------------------------------------------------------
-// Increment pairs: (total from an even start, total from an odd start).
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ seq_pair sm_pair_tie(uint32_t m) {
-    // a half-way term m + 1/2: k + m goes to the even neighbour
-    seq_pair p;
-    p.e = m + (m & 1u);
-    p.o = m + ((m + 1u) & 1u);
-    return p;
-}
-
-// Ordered reduction of pairs over the wave (lane 0 holds the whole wave's
-// pair, lanes in increasing order).
-__device__ __forceinline__ seq_pair sm_wave_pair_reduce(seq_pair p) {
-    const uint32_t lane = (uint32_t)zs_lane();
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        seq_pair o;
-        o.e = (uint32_t)__shfl_down((int)p.e, d, 64);
-        o.o = (uint32_t)__shfl_down((int)p.o, d, 64);
-        if ((lane & (2u * d - 1u)) == 0u && lane + d < 64u) p = seq_compose(p, o);
-    }
-    p.e = (uint32_t)__builtin_amdgcn_readfirstlane((int)p.e);
-    p.o = (uint32_t)__builtin_amdgcn_readfirstlane((int)p.o);
-    return p;
-}
-
-// Inclusive ordered scan of pairs over the wave: shifts by 1, 2, 4, 8 inside
-// each row of 16 lanes, then the rows by broadcasts (DPP moves; a lane
-// without a source receives the identity pair (0, 0)).
-template <int CTRL, int ROWS, bool BC>
-__device__ __forceinline__ seq_pair sm_pair_step(seq_pair p) {
-    seq_pair o;
-    o.e = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)p.e, CTRL, ROWS, 0xf, BC);
-    o.o = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)p.o, CTRL, ROWS, 0xf, BC);
-    // rows outside ROWS keep their value: combine with the identity there
-    return seq_compose(o, p);
-}
-__device__ __forceinline__ seq_pair sm_wave_pair_scan(seq_pair p) {
-    p = sm_pair_step<0x111, 0xf, true>(p);    // row_shr:1
-    p = sm_pair_step<0x112, 0xf, true>(p);    // row_shr:2
-    p = sm_pair_step<0x114, 0xf, true>(p);    // row_shr:4
-    p = sm_pair_step<0x118, 0xf, true>(p);    // row_shr:8
-    p = sm_pair_step<0x142, 0xa, false>(p);   // row_bcast:15
-    p = sm_pair_step<0x143, 0xc, false>(p);   // row_bcast:31
-    return p;
-}
-
-__device__ __forceinline__ uint32_t sm_wave_sum_sat(uint32_t v) {
-#pragma unroll
-    for (int d = 32; d > 0; d >>= 1) v = zs_sat_add(v, (uint32_t)__shfl_xor((int)v, d, 64));
-    return (uint32_t)__builtin_amdgcn_readfirstlane((int)v);
 }
 
 __device__ __forceinline__ float sm_wave_sum_f(float v) {
@@ -676,252 +595,10 @@ __global__ __launch_bounds__(SM_NT) void zs_k_sround(zs_sargs a) {
 }
 
 // ---------------------------------------------------------------------------
-// The exact walk of one sub-chunk by one 256-thread workgroup: thread t holds
-// terms 4t .. 4t+3 of the sub-chunk, in order, from running sum s. Each step
-// takes the terms from `pos` on the grid of s: per-thread increment pairs,
-// prefix-scanned over the workgroup (wave scans, then the wave totals), give
-// the running sum after every thread's terms; the first thread where it
-// leaves the binade walks its terms one by one (increments with the parity of
-// the sum at each half-way term) up to the term that leaves the binade, which
-// it adds as a real f32 addition of the exact value; the next step resumes
-// after that term on the new grid.
+// zs_k_sstitch<STAGE>: one 256-thread workgroup per (row, sum) (zs_walk.h):
+// the sub-chunks the round kernel left unsafe are walked from the exact terms
+// it stored for them, a safe one whose total did not apply from the source.
 // ---------------------------------------------------------------------------
-#define SW_NT 256
-#define SW_NW (SW_NT / 64)
-#define SW_TPT 4          // terms per thread
-static_assert(SW_NT * SW_TPT == ZS_SUB, "one workgroup per sub-chunk walk");
-
-struct sm_wsh {
-    uint32_t we[2][SW_NW], wo[2][SW_NW];   // per-wave pair totals on the grid (double buffered by step)
-    uint32_t w2[2][SW_NW];                 // per-wave totals on the next grid
-    uint32_t wt2[2][SW_NW];                // per wave: a half-way term on the next grid
-    uint32_t cross[2][SW_NW];              // per wave: a thread of it leaves the binade
-    float s_new[2][SW_NW];
-    uint32_t pos_new[2][SW_NW];
-    float tot_s[2];                        // the sum after the last thread (no crossing)
-    uint32_t first[SW_NW];                 // zero sums: first nonzero term per wave
-    float hs;
-};
-__shared__ sm_wsh sm_sh;
-
-// Workgroup barrier that orders LDS accesses only: __syncthreads() also waits
-// for every outstanding global load of the calling wave, which would drain
-// the loads the stitch keeps in flight for its next walks.
-__device__ __forceinline__ void sm_bar() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
-__device__ __forceinline__ float sm_lane_f(float v, uint32_t l) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), (int)l));
-}
-
-// Increments of a thread's 4 exact terms (those in `valid`) on grid eg, the
-// half-way flags, and their pair.
-__device__ __forceinline__ seq_pair sm_incs4(const float (&v)[SW_TPT], int eg, uint32_t valid,
-                                             uint32_t (&inc)[SW_TPT], uint32_t& tie) {
-    tie = 0u;
-    if (eg >= SM_EG_MIN) {
-        const float sc = sm_scale(eg);
-#pragma unroll
-        for (int q = 0; q < SW_TPT; q++) {
-            const float qv = fminf(v[q] * sc, SM_QCAP);
-            float rq = rintf(qv);
-            const bool h = fabsf(qv - rq) == 0.5f && ((valid >> q) & 1u);
-            if (h) rq = floorf(qv);
-            tie |= (h ? 1u : 0u) << q;
-            inc[q] = ((valid >> q) & 1u) ? (uint32_t)rq : 0u;
-        }
-    } else {
-        // sums below 2^-99: integer increments
-#pragma unroll
-        for (int q = 0; q < SW_TPT; q++) {
-            uint32_t tq = 0u;
-            inc[q] = ((valid >> q) & 1u) ? zs_seq_inc(v[q], eg, &tq) : 0u;
-            tie |= tq << q;
-        }
-    }
-    seq_pair lp = {0u, 0u};
-    if (tie) {
-#pragma unroll
-        for (int q = 0; q < SW_TPT; q++)
-            lp = seq_compose(lp, ((tie >> q) & 1u) ? sm_pair_tie(inc[q]) : seq_pair{inc[q], inc[q]});
-    } else {
-        uint32_t tot = 0u;
-#pragma unroll
-        for (int q = 0; q < SW_TPT; q++) tot = zs_sat_add(tot, inc[q]);
-        lp = seq_pair{tot, tot};
-    }
-    return lp;
-}
-
-// The walk over the exact terms v (thread t: terms 4t .. 4t+3) from s.
-__device__ __forceinline__ float sm_walk(int kind, const float (&v)[SW_TPT], float s, uint32_t dbg_r) {
-    sm_wsh& sh = sm_sh;
-    const uint32_t t = threadIdx.x, lane = (uint32_t)zs_lane(), wid = (uint32_t)zs_wid();
-    uint32_t pos = 0, par = 0;   // first term not yet added; LDS slot of this step
-    while (pos < ZS_SUB) {
-        if (t == 0) SM_DBG(dbg_r, kind, 2, 1);
-        if (s == 0.0f) {
-            // a zero sum takes its first nonzero term as it is (zero terms
-            // before it leave a +0: -0 + +0 = +0); from there the sum climbs
-            // through a binade at almost every doubling of the number of
-            // terms: the next SM_HEAD terms are added one by one, in order
-            uint32_t my = 0xffffffffu;
-#pragma unroll
-            for (int q = SW_TPT - 1; q >= 0; q--)
-                if (SW_TPT * t + (uint32_t)q >= pos && v[q] != 0.0f) my = SW_TPT * t + (uint32_t)q;
-            const unsigned long long m = __ballot(my != 0xffffffffu);
-            if (lane == 0) sh.first[wid] = m ? (uint32_t)__builtin_amdgcn_readlane((int)my, __ffsll((long long)m) - 1) : 0xffffffffu;
-            sm_bar();
-            uint32_t first = 0xffffffffu;
-#pragma unroll
-            for (int w = 0; w < SW_NW; w++) first = min(first, sh.first[w]);
-            s = s + 0.0f;
-            if (first == 0xffffffffu) return s;
-            const uint32_t end = min(first + SM_HEAD, (uint32_t)ZS_SUB);
-            // the head's terms lie in at most two waves: each wave adds the
-            // ones it holds, in order, the first wave's before the second's
-            const uint32_t w0 = first / (SW_TPT * 64), w1 = (end - 1) / (SW_TPT * 64);
-            float ss = s;
-            for (uint32_t w = w0; w <= w1; w++) {
-                if (wid == w) {
-                    if (w != w0) ss = sh.hs;
-                    for (uint32_t L = 0; L < 64; L++) {
-#pragma unroll
-                        for (int q = 0; q < SW_TPT; q++) {
-                            const uint32_t e = SW_TPT * (64 * w + L) + (uint32_t)q;
-                            if (e >= first && e < end) ss = ss + sm_lane_f(v[q], L);
-                        }
-                    }
-                    if (lane == 0) sh.hs = ss;
-                }
-                sm_bar();
-            }
-            s = sh.hs;
-            pos = end;
-            sm_bar();
-            continue;
-        }
-        const int eg = zs_grid_exp(s);
-        const uint32_t k = zs_grid_k(s);
-        uint32_t valid = 0u;
-#pragma unroll
-        for (int q = 0; q < SW_TPT; q++) valid |= (SW_TPT * t + (uint32_t)q >= pos ? 1u : 0u) << q;
-        uint32_t inc[SW_TPT], tie, inc2[SW_TPT], tie2;
-        const seq_pair lp = sm_incs4(v, eg, valid, inc, tie);
-        // the next grid as well: after a crossing the rest of the sub-chunk
-        // usually stays on it
-        const bool two = eg >= SM_EG_MIN && eg + 1 < 254;
-        uint32_t tot2 = 0u;
-        if (two) {
-            sm_incs4(v, eg + 1, valid, inc2, tie2);
-#pragma unroll
-            for (int q = 0; q < SW_TPT; q++) tot2 = zs_sat_add(tot2, inc2[q]);
-        } else {
-            tie2 = 1u;
-#pragma unroll
-            for (int q = 0; q < SW_TPT; q++) inc2[q] = 0u;
-        }
-        const seq_pair wp = sm_wave_pair_scan(lp);   // inclusive, in the wave
-        const uint32_t w2 = wave_incl_scan_sat(tot2);
-        const bool anyt2w = __ballot(tie2 != 0u) != 0ull;
-        if (lane == 63) {
-            sh.we[par][wid] = wp.e;
-            sh.wo[par][wid] = wp.o;
-            sh.w2[par][wid] = w2;
-            sh.wt2[par][wid] = anyt2w ? 1u : 0u;
-        }
-        sm_bar();
-        seq_pair pre = {0u, 0u};   // the waves before this one
-        uint32_t pre2 = 0u, all2 = 0u, anyt2 = 0u;
-#pragma unroll
-        for (int w = 0; w < SW_NW; w++) {
-            if ((uint32_t)w < wid) {
-                pre = seq_compose(pre, seq_pair{sh.we[par][w], sh.wo[par][w]});
-                pre2 = zs_sat_add(pre2, sh.w2[par][w]);
-            }
-            all2 = zs_sat_add(all2, sh.w2[par][w]);
-            anyt2 |= sh.wt2[par][w];
-        }
-        const seq_pair incl = seq_compose(pre, wp);
-        const uint32_t kend = zs_sat_add(k, (k & 1u) ? incl.o : incl.e);
-        const unsigned long long bad = __ballot(kend >= ZS_BINADE);
-        // the exclusive prefix of the first thread that leaves the binade
-        seq_pair ex;
-        ex.e = (uint32_t)__shfl_up((int)wp.e, 1, 64);
-        ex.o = (uint32_t)__shfl_up((int)wp.o, 1, 64);
-        if (lane == 0) ex = seq_pair{0u, 0u};
-        ex = seq_compose(pre, ex);
-        const uint32_t L = bad ? (uint32_t)(__ffsll((long long)bad) - 1) : 64u;
-        if (lane == L) {
-            uint32_t kk = zs_sat_add(k, (k & 1u) ? ex.o : ex.e);
-            int qx = SW_TPT - 1;
-            bool found = false;
-#pragma unroll
-            for (int q = 0; q < SW_TPT; q++) {
-                if (found || !((valid >> q) & 1u)) continue;
-                const uint32_t kn = zs_sat_add(kk, ((tie >> q) & 1u) ? inc[q] + ((kk + inc[q]) & 1u) : inc[q]);
-                if (kn >= ZS_BINADE) { qx = q; found = true; }
-                else kk = kn;
-            }
-            float vx = 0.0f;
-            uint32_t after2 = 0u;   // this thread's next-grid increments after the crossing term
-#pragma unroll
-            for (int q = 0; q < SW_TPT; q++) {
-                if (q == qx) vx = v[q];
-                if (q > qx) after2 = zs_sat_add(after2, inc2[q]);
-            }
-            const float sx = zs_grid_value(kk, eg) + vx;   // the term that leaves the binade
-            float sn = sx;
-            uint32_t pn = SW_TPT * t + (uint32_t)qx + 1u;
-            if (two && !anyt2 && zs_grid_exp(sx) == eg + 1) {
-                // the rest on the next grid: its total minus the terms through
-                // the crossing (no half-way term there, so plain sums)
-                const uint32_t rest = zs_sat_add(all2 - min(all2, zs_sat_add(pre2, w2)), after2);
-                const uint32_t k2 = zs_sat_add(zs_grid_k(sx), rest);
-                if (all2 < ZS_INC_CAP && k2 < ZS_BINADE) {
-                    sn = zs_grid_value(k2, eg + 1);
-                    pn = ZS_SUB;
-                }
-            }
-            sh.s_new[par][wid] = sn;
-            sh.pos_new[par][wid] = pn;
-        }
-        if (lane == 0) sh.cross[par][wid] = bad ? 1u : 0u;
-        if (t == SW_NT - 1) sh.tot_s[par] = kend < ZS_BINADE ? zs_grid_value(kend, eg) : 0.0f;
-        sm_bar();
-        int cw = -1;
-#pragma unroll
-        for (int w = SW_NW - 1; w >= 0; w--)
-            if (sh.cross[par][w]) cw = w;
-        if (cw < 0) return sh.tot_s[par];
-        s = sh.s_new[par][cw];
-        pos = sh.pos_new[par][cw];
-        par ^= 1u;
-    }
-    return s;
-}
-
-// ---------------------------------------------------------------------------
-// zs_k_sstitch<STAGE>: one 256-thread workgroup per (row, sum). Runs of
-// sub-chunks whose totals apply (safe, on the grid of the running sum, inside
-// its binade) are taken 64 at a time with a pair scan (every wave the same);
-// the others are walked exactly from the term arguments the round kernel
-// stored for them (loaded two walks ahead), or from the source for a safe
-// sub-chunk whose total did not apply.
-// ---------------------------------------------------------------------------
-// First sub-chunk from j whose record is not safe (nsub: none); uniform.
-__device__ __forceinline__ uint32_t sm_next_fragile(const sm_rec* R, uint32_t j, uint32_t nsub) {
-    for (uint32_t i0 = j; i0 < nsub; i0 += 64) {
-        const uint32_t i = i0 + (uint32_t)zs_lane();
-        const unsigned long long m = __ballot(i < nsub && !(R[i].flags & SM_SAFE));
-        if (m) return i0 + (uint32_t)(__ffsll((long long)m) - 1);
-    }
-    return nsub;
-}
-
 // A thread's 4 exact terms of sub-chunk j straight from the source (x~ / y
 // with mask and patches): the rare safe sub-chunk whose total did not apply.
 __device__ __forceinline__ void sm_terms_src(const sm_src& S, const sm_terms& f, uint32_t j, float (&d)[SW_TPT]) {
@@ -952,9 +629,26 @@ __device__ __forceinline__ void sm_terms_src(const sm_src& S, const sm_terms& f,
     for (int e = 0; e < 4; e++) d[e] = sm_exact(f, sm_arg(f, x[e], y[e]));
 }
 
+// Terms of a row sum for sm_stitch.
+struct sm_row_tp {
+    const sm_src& S;
+    const sm_terms& f;
+    const float* darea;
+    __device__ __forceinline__ void fetch(uint32_t j, sm_f4& raw) const {
+        raw = *reinterpret_cast<const sm_f4*>(darea + min(j * ZS_SUB + SW_TPT * threadIdx.x, (S.n - 1u) & ~3u));
+    }
+    __device__ __forceinline__ void take(uint32_t j, const sm_f4& raw, float (&v)[SW_TPT]) const {
+        const uint32_t id0 = j * ZS_SUB + SW_TPT * threadIdx.x;
+        v[0] = raw.x; v[1] = raw.y; v[2] = raw.z; v[3] = raw.w;
+#pragma unroll
+        for (int e = 0; e < SW_TPT; e++)
+            if (id0 + e >= S.n) v[e] = 0.0f;
+    }
+    __device__ __forceinline__ void direct(uint32_t j, float (&v)[SW_TPT]) const { sm_terms_src(S, f, j, v); }
+};
+
 template <int STAGE>
 __global__ __launch_bounds__(SW_NT) void zs_k_sstitch(zs_sargs a) {
-    __shared__ sm_rec R[ZS_MAX_SUBS];
     const uint32_t r = blockIdx.x;
     zs_row_state* stp = a.rst + r;
     const int kind = STAGE == 1 ? (blockIdx.y == 0 ? ZS_SUM_OBS_S : ZS_SUM_SAMP_S) : ZS_SUM_OBS_H;
@@ -965,81 +659,13 @@ __global__ __launch_bounds__(SW_NT) void zs_k_sstitch(zs_sargs a) {
     const sm_src S = sm_src_of(a, r, st, P);
     const sm_terms f = sm_terms_of(kind, st, P);
     const uint32_t nsub = (S.n + ZS_SUB - 1) / ZS_SUB;
-    const uint32_t t = threadIdx.x, lane = (uint32_t)zs_lane();
     const sm_rec* rec = reinterpret_cast<const sm_rec*>(a.s_rec) + ((size_t)r * ZS_NSUM + kind) * a.max_subs;
-    for (uint32_t i = t; i < nsub; i += SW_NT) R[i] = rec[i];
+    for (uint32_t i = threadIdx.x; i < nsub; i += SW_NT) sm_sh.rec[i] = rec[i];
     __syncthreads();
-    const float* darea = sm_darea(a, r, kind);
-    float s = kind == ZS_SUM_OBS_H ? 0.0f : -0.0f;
-#ifdef ZS_SM_DEBUG
-    const uint64_t t0 = wall_clock64();
-#endif
-    // the next two sub-chunks to walk and their argument loads
-    uint32_t nf0 = sm_next_fragile(R, 0, nsub);
-    uint32_t nf1 = nf0 < nsub ? sm_next_fragile(R, nf0 + 1, nsub) : nsub;
-    auto ld = [&](uint32_t jj) -> sm_f4 {
-        return *reinterpret_cast<const sm_f4*>(darea + min(jj * ZS_SUB + SW_TPT * t, S.n - 1u & ~3u));
-    };
-    sm_f4 q0 = {0.0f, 0.0f, 0.0f, 0.0f}, q1 = q0;
-    if (nf0 < nsub) q0 = ld(nf0);
-    if (nf1 < nsub) q1 = ld(nf1);
-    uint32_t j = 0;
-    while (j < nsub) {
-#ifdef ZS_SM_DEBUG
-        uint64_t c0 = clock64();
-#endif
-        if (s != 0.0f) {
-            // sub-chunks j .. j+63 on the grid of s, applied up to the first
-            // one that is not safe, is on another grid or leaves the binade
-            const int eg = zs_grid_exp(s);
-            const uint32_t k = zs_grid_k(s);
-            const uint32_t i = j + lane;
-            const sm_rec e = i < nsub ? R[i] : sm_rec{0, 0u, 0u, 0u};
-            const bool ok = (e.flags & SM_SAFE) && e.eg == eg;
-            const seq_pair p = sm_wave_pair_scan(ok ? seq_pair{e.d0, e.d1} : seq_pair{ZS_INC_CAP, ZS_INC_CAP});
-            const uint32_t kend = zs_sat_add(k, (k & 1u) ? p.o : p.e);
-            const unsigned long long bad = __ballot(!(ok && kend < ZS_BINADE));
-            const uint32_t n_ok = bad ? (uint32_t)(__ffsll((long long)bad) - 1) : 64u;
-            if (n_ok) {
-                if (t == 0) SM_DBG(r, kind, 0, n_ok);
-#ifdef ZS_SM_DEBUG
-                if (t == 0) SM_DBG(r, kind, 4, (clock64() - c0) / 16);
-#endif
-                s = zs_grid_value((uint32_t)__builtin_amdgcn_readlane((int)kend, (int)n_ok - 1), eg);
-                j += n_ok;
-                continue;
-            }
-        }
-        if (t == 0) SM_DBG(r, kind, 1, (R[j].flags & SM_SAFE) ? 1 : 0x10000);
-        float d[SW_TPT];
-        if (j == nf0) {
-            d[0] = q0.x; d[1] = q0.y; d[2] = q0.z; d[3] = q0.w;
-            nf0 = nf1;
-            q0 = q1;
-            nf1 = nf0 < nsub ? sm_next_fragile(R, nf0 + 1, nsub) : nsub;
-            if (nf1 < nsub) q1 = ld(nf1);
-            const uint32_t id0 = j * ZS_SUB + SW_TPT * t;
-#pragma unroll
-            for (int e = 0; e < SW_TPT; e++)
-                if (id0 + e >= S.n) d[e] = 0.0f;
-        } else {
-            sm_terms_src(S, f, j, d);
-        }
-#ifdef ZS_SM_DEBUG
-        uint64_t c1 = clock64();
-        if (t == 0) SM_DBG(r, kind, 5, (c1 - c0) / 16);
-#endif
-        s = sm_walk(kind, d, s, r);
-        sm_bar();
-#ifdef ZS_SM_DEBUG
-        if (t == 0) SM_DBG(r, kind, 6, (clock64() - c1) / 16);
-#endif
-        j++;
-    }
-#ifdef ZS_SM_DEBUG
-    if (t == 0) SM_DBG(r, kind, 3, wall_clock64() - t0);
-#endif
-    if (t == 0) {
+    sm_row_tp tp{S, f, sm_darea(a, r, kind)};
+    uint32_t stop;
+    const float s = sm_stitch<sm_row_tp, sm_f4>(tp, nsub, kind == ZS_SUM_OBS_H ? 0.0f : -0.0f, NAN, &stop);
+    if (threadIdx.x == 0) {
         if (kind == ZS_SUM_OBS_S) stp->obs_S = s;
         else if (kind == ZS_SUM_SAMP_S) stp->samp_S = s;
         else stp->obs_H = s;
