@@ -672,6 +672,14 @@ __global__ __launch_bounds__(SW_NT) void zs_k_sstitch(zs_sargs a) {
     }
 }
 
+#ifdef ZS_WALK_DEBUG
+extern "C" int zs_dbg_walk_stats(unsigned long long* out) {
+    if (hipMemcpyFromSymbol(out, HIP_SYMBOL(sw_dbg), 16 * sizeof(unsigned long long)) != hipSuccess) return -1;
+    static unsigned long long zero[16];
+    return hipMemcpyToSymbol(HIP_SYMBOL(sw_dbg), zero, sizeof(zero)) == hipSuccess ? 0 : -1;
+}
+#endif
+
 // Launches one kernel of the row sums: 0 zs_k_sapx, 1 zs_k_sround<1>,
 // 2 zs_k_sstitch<1>, 3 zs_k_sround<2>, 4 zs_k_sstitch<2>.
 extern "C" int zs_sums_launch(const zs_sargs& a, uint32_t which, hipStream_t stream) {

@@ -72,6 +72,21 @@ __device__ __forceinline__ seq_pair sm_wave_pair_scan(seq_pair p) {
     return p;
 }
 
+// Inclusive saturating scan of a u32 over the wave, with the same DPP moves.
+template <int CTRL, int ROWS, bool BC>
+__device__ __forceinline__ uint32_t sm_sat_step(uint32_t x) {
+    return zs_sat_add(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, ROWS, 0xf, BC));
+}
+__device__ __forceinline__ uint32_t sm_wave_scan_sat(uint32_t x) {
+    x = sm_sat_step<0x111, 0xf, true>(x);
+    x = sm_sat_step<0x112, 0xf, true>(x);
+    x = sm_sat_step<0x114, 0xf, true>(x);
+    x = sm_sat_step<0x118, 0xf, true>(x);
+    x = sm_sat_step<0x142, 0xa, false>(x);
+    x = sm_sat_step<0x143, 0xc, false>(x);
+    return x;
+}
+
 // Ordered reduction of pairs over the wave (lanes in increasing order; the
 // result is uniform).
 __device__ __forceinline__ seq_pair sm_wave_pair_reduce(seq_pair p) {
@@ -124,6 +139,17 @@ struct sm_wsh {
 };
 __shared__ sm_wsh sm_sh;
 #define SW_STOP 0x80000000u
+
+#ifdef ZS_WALK_DEBUG
+// working diagnostics: cycles per walk phase (summed over workgroups)
+__device__ unsigned long long sw_dbg[16];
+__shared__ unsigned long long sw_acc[16];
+#define SW_T(i, c) do { if (threadIdx.x == 0) sw_acc[i] += (unsigned long long)(c); } while (0)
+#define SW_CLK() clock64()
+#else
+#define SW_T(i, c) ((void)0)
+#define SW_CLK() 0ull
+#endif
 
 // Increments of a thread's 4 exact terms (those in `valid`) on grid eg, the
 // half-way flags, and their pair.
@@ -195,21 +221,26 @@ __device__ __forceinline__ float sm_walk(const float (&v)[SW_TPT], float s, floa
             s = s + 0.0f;
             if (first == 0xffffffffu) return s;
             const uint32_t end = min(first + SM_HEAD, (uint32_t)ZS_SUB);
+            const unsigned long long h0 = SW_CLK();
             // the head's terms lie in at most two waves: each wave adds the
             // ones it holds, in order, the first wave's before the second's
             const uint32_t w0 = first / (SW_TPT * 64), w1 = (end - 1) / (SW_TPT * 64);
+            const bool thr = thresh == thresh;
             for (uint32_t w = w0; w <= w1; w++) {
                 if (wid == w) {
                     float ss = w != w0 ? sh.hs : s;
                     uint32_t sp = w != w0 ? sh.hstop : 0xffffffffu;
-                    for (uint32_t L = 0; L < 64 && sp == 0xffffffffu; L++) {
+                    const uint32_t base = SW_TPT * 64 * w;
+                    const uint32_t Lb = first > base ? (first - base) / SW_TPT : 0u;
+                    const uint32_t Le = min(64u, (end - base + SW_TPT - 1) / SW_TPT);
+                    for (uint32_t L = Lb; L < Le && sp == 0xffffffffu; L++) {
 #pragma unroll
                         for (int q = 0; q < SW_TPT; q++) {
-                            const uint32_t e = SW_TPT * (64 * w + L) + (uint32_t)q;
-                            if (e >= first && e < end && sp == 0xffffffffu) {
-                                ss = ss + sm_lane_f(v[q], L);
-                                if (ss >= thresh) sp = e;
-                            }
+                            const uint32_t e = base + SW_TPT * L + (uint32_t)q;
+                            const bool in = e >= first && e < end && sp == 0xffffffffu;
+                            const float nv = ss + sm_lane_f(v[q], L);
+                            ss = in ? nv : ss;
+                            if (thr && in && nv >= thresh) sp = e;
                         }
                     }
                     if (lane == 0) { sh.hs = ss; sh.hstop = sp; }
@@ -220,32 +251,67 @@ __device__ __forceinline__ float sm_walk(const float (&v)[SW_TPT], float s, floa
             const uint32_t sp = sh.hstop;
             pos = end;
             sm_bar();
+            SW_T(6, SW_CLK() - h0); SW_T(7, 1);
             if (sp != 0xffffffffu) { *stop = sp; return s; }
             continue;
         }
+        const unsigned long long c0 = SW_CLK();
         const int eg = zs_grid_exp(s);
         const uint32_t k = zs_grid_k(s);
         const uint32_t kthr = zs_grid_thresh(thresh, eg);
         uint32_t valid = 0u;
 #pragma unroll
         for (int q = 0; q < SW_TPT; q++) valid |= (SW_TPT * t + (uint32_t)q >= pos ? 1u : 0u) << q;
-        uint32_t inc[SW_TPT], tie, inc2[SW_TPT], tie2;
-        const seq_pair lp = sm_incs4(v, eg, valid, inc, tie);
+        uint32_t inc[SW_TPT], tie = 0u, inc2[SW_TPT], tie2 = 0u, tot = 0u, tot2 = 0u;
         // the next grid as well: after a crossing the rest of the sub-chunk
-        // usually stays on it
+        // usually stays on it (its increments halve the scaled terms exactly)
         const bool two = eg >= SM_EG_MIN && eg + 1 < 254;
-        uint32_t tot2 = 0u;
-        if (two) {
-            sm_incs4(v, eg + 1, valid, inc2, tie2);
+        if (eg >= SM_EG_MIN) {
+            const float sc = sm_scale(eg);
 #pragma unroll
-            for (int q = 0; q < SW_TPT; q++) tot2 = zs_sat_add(tot2, inc2[q]);
+            for (int q = 0; q < SW_TPT; q++) {
+                const bool in = (valid >> q) & 1u;
+                const float qv = fminf(v[q] * sc, SM_QCAP);
+                float rq = rintf(qv);
+                const bool h = fabsf(qv - rq) == 0.5f && in;
+                if (h) rq = floorf(qv);
+                tie |= (h ? 1u : 0u) << q;
+                inc[q] = in ? (uint32_t)rq : 0u;
+                const float qv2 = qv * 0.5f;
+                const float rq2 = rintf(qv2);
+                tie2 |= (fabsf(qv2 - rq2) == 0.5f && in ? 1u : 0u) << q;
+                inc2[q] = in ? (uint32_t)rq2 : 0u;
+                tot = zs_sat_add(tot, inc[q]);
+                tot2 = zs_sat_add(tot2, inc2[q]);
+            }
         } else {
-            tie2 = 1u;
+            // sums below 2^-99: integer increments
 #pragma unroll
-            for (int q = 0; q < SW_TPT; q++) inc2[q] = 0u;
+            for (int q = 0; q < SW_TPT; q++) {
+                uint32_t tq = 0u;
+                inc[q] = ((valid >> q) & 1u) ? zs_seq_inc(v[q], eg, &tq) : 0u;
+                tie |= tq << q;
+                tot = zs_sat_add(tot, inc[q]);
+                inc2[q] = 0u;
+            }
+            tie2 = 1u;
         }
-        const seq_pair wp = sm_wave_pair_scan(lp);   // inclusive, in the wave
-        const uint32_t w2 = wave_incl_scan_sat(tot2);
+        const unsigned long long c1 = SW_CLK();
+        // inclusive scans over the wave: plain sums unless a half-way term
+        // makes the increments depend on the parity
+        const bool wtie = __builtin_amdgcn_readfirstlane((int)(__ballot(tie != 0u) != 0ull)) != 0;
+        seq_pair wp;
+        if (!wtie) {
+            const uint32_t x = sm_wave_scan_sat(tot);
+            wp = seq_pair{x, x};
+        } else {
+            seq_pair own = {0u, 0u};
+#pragma unroll
+            for (int q = 0; q < SW_TPT; q++)
+                own = seq_compose(own, ((tie >> q) & 1u) ? sm_pair_tie(inc[q]) : seq_pair{inc[q], inc[q]});
+            wp = sm_wave_pair_scan(own);
+        }
+        const uint32_t w2 = sm_wave_scan_sat(tot2);
         const bool anyt2w = __ballot(tie2 != 0u) != 0ull;
         if (lane == 63) {
             sh.we[par][wid] = wp.e;
@@ -253,7 +319,9 @@ __device__ __forceinline__ float sm_walk(const float (&v)[SW_TPT], float s, floa
             sh.w2[par][wid] = w2;
             sh.wt2[par][wid] = anyt2w ? 1u : 0u;
         }
+        const unsigned long long c2 = SW_CLK();
         sm_bar();
+        const unsigned long long c3 = SW_CLK();
         seq_pair pre = {0u, 0u};   // the waves before this one
         uint32_t pre2 = 0u, all2 = 0u, anyt2 = 0u;
 #pragma unroll
@@ -272,7 +340,7 @@ __device__ __forceinline__ float sm_walk(const float (&v)[SW_TPT], float s, floa
         // reaches the threshold
         seq_pair ex;
         ex.e = (uint32_t)__shfl_up((int)wp.e, 1, 64);
-        ex.o = (uint32_t)__shfl_up((int)wp.o, 1, 64);
+        ex.o = wtie ? (uint32_t)__shfl_up((int)wp.o, 1, 64) : ex.e;
         if (lane == 0) ex = seq_pair{0u, 0u};
         ex = seq_compose(pre, ex);
         const uint32_t L = bad ? (uint32_t)(__ffsll((long long)bad) - 1) : 64u;
@@ -321,7 +389,10 @@ __device__ __forceinline__ float sm_walk(const float (&v)[SW_TPT], float s, floa
         }
         if (lane == 0) sh.cross[par][wid] = bad ? 1u : 0u;
         if (t == SW_NT - 1) sh.tot_s[par] = (kend < ZS_BINADE && kend < kthr) ? zs_grid_value(kend, eg) : 0.0f;
+        const unsigned long long c4 = SW_CLK();
         sm_bar();
+        const unsigned long long c5 = SW_CLK();
+        SW_T(0, c1 - c0); SW_T(1, c2 - c1); SW_T(2, c3 - c2); SW_T(3, c4 - c3); SW_T(4, c5 - c4); SW_T(5, 1);
         int cw = -1;
 #pragma unroll
         for (int w = SW_NW - 1; w >= 0; w--)
@@ -362,6 +433,9 @@ __device__ __forceinline__ float sm_stitch(TP& tp, uint32_t nsub, float s, float
     uint32_t nf0 = sm_next_fragile(0, nsub);
     uint32_t nf1 = nf0 < nsub ? sm_next_fragile(nf0 + 1, nsub) : nsub;
     RAW q0, q1;
+#ifdef ZS_WALK_DEBUG
+    if (threadIdx.x < 16) sw_acc[threadIdx.x] = 0ull;
+#endif
     if (nf0 < nsub) tp.fetch(nf0, q0);
     if (nf1 < nsub) tp.fetch(nf1, q1);
     uint32_t j = 0;
@@ -381,12 +455,14 @@ __device__ __forceinline__ float sm_stitch(TP& tp, uint32_t nsub, float s, float
             const unsigned long long bad = __ballot(!(ok && kend < ZS_BINADE && kend < kthr));
             const uint32_t n_ok = bad ? (uint32_t)(__ffsll((long long)bad) - 1) : 64u;
             if (n_ok) {
+                SW_T(11, 1);
                 s = zs_grid_value((uint32_t)__builtin_amdgcn_readlane((int)kend, (int)n_ok - 1), eg);
                 j += n_ok;
                 continue;
             }
         }
         float v[SW_TPT];
+        const unsigned long long l0 = SW_CLK();
         if (j == nf0) {
             tp.take(j, q0, v);
             nf0 = nf1;
@@ -397,13 +473,19 @@ __device__ __forceinline__ float sm_stitch(TP& tp, uint32_t nsub, float s, float
             tp.direct(j, v);
         }
         uint32_t sp;
+        const unsigned long long l1 = SW_CLK();
+        SW_T(8, l1 - l0); SW_T(9, 1);
         s = sm_walk(v, s, thresh, &sp);
         sm_bar();
+        SW_T(10, SW_CLK() - l1);
         if (sp != 0xffffffffu) {
             *stop = j * ZS_SUB + sp;
-            return s;
+            break;
         }
         j++;
     }
+#ifdef ZS_WALK_DEBUG
+    if (threadIdx.x < 16) atomicAdd(&sw_dbg[threadIdx.x], sw_acc[threadIdx.x]);
+#endif
     return s;
 }
