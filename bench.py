@@ -454,7 +454,8 @@ def dfa_only(seed):
     ctx = Context(0, 256, 151936)
     res = {name: [round(v, 2) for v in mask_config_us(ctx, V, rows, kind, S, seed)]
            for name, V, rows, kind, S in DFA_CONFIGS}
-    print(json.dumps({"dfa_mask_us_cold_warm": res}))
+    print(json.dumps({"dfa_mask_us_cold_warm": res}), flush=True)
+    ctx.close()
 
 
 def main():
@@ -596,7 +597,10 @@ def main():
         "cpu_model": cpu_model(),
         "cpu_baseline": cpu,
     }
-    print(json.dumps(res))
+    print(json.dumps(res), flush=True)
+    # release the device objects before the interpreter shuts down
+    torch.cuda.synchronize()
+    ctx.close()
 
 
 if __name__ == "__main__":

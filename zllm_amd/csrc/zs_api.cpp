@@ -1,3 +1,4 @@
+#include <atomic>
 #include <stddef.h>
 // zs_api.cpp -- host side of libzs: contexts, token tables, DFAs (liveness on
 // the host), argument validation, and the C entry points of include/zs.h.
@@ -270,7 +271,10 @@ extern "C" int zs_vocab_create(zs_ctx* ctx, const uint32_t* h_offsets, const uin
     v->ctx = ctx;
     v->ntab = ntab;
     v->eos = eos;
-    v->serial = ++ctx->vocab_serial;
+    // serials are unique in the process (a DFA's memo may meet vocabularies
+    // of several contexts): 0 is never handed out
+    static std::atomic<uint32_t> next_serial{0};
+    v->serial = next_serial.fetch_add(1u, std::memory_order_relaxed) + 1u;
     v->nbytes = h_offsets[ntab] - h_offsets[0];
     v->h_offsets = (uint32_t*)malloc(sizeof(uint32_t) * (ntab + 1));
     v->h_bytes = (uint8_t*)malloc(v->nbytes + 1);

@@ -167,7 +167,6 @@ struct zs_ctx {
     uint32_t* pv;          // big-row probabilities (f32 bits) [rows][max_vocab]
     void* mask_scratch;    // DFA mask viability flags [rows]
     uint32_t mask_epoch;   // last epoch handed to the packed DFA mask
-    uint32_t vocab_serial; // serial number of the last zs_vocab created
     double* k_ap;                // [rows][max_subs] approximate sums of the kept list per sub-chunk
     zs_sub_sum* k_sum;           // [rows][2][max_subs] kept-list rounds (sum2, draw)
     zs_sub_sum* s_rec;           // [rows][ZS_NSUM][max_subs] row-sum sub-chunk totals (zs_k_sround)

@@ -26,11 +26,11 @@ __device__ __forceinline__ float zs_exp_fast(float d) {
     return ldexpf(y, (int)n);
 }
 
-// A cheaper exp for the row kernel's streaming sums: 2^(d * f32(log2 e)) by
-// v_exp_f32 alone, for d in [ZS_EXP_FAST_MIN, 1]. Its relative error against
-// the glibc-identical zs_expf (the argument's rounding, at most |d log2 e|
-// 2^-24, dominates) stays below ZS_EXP_HW_EPS / 2 over that whole domain
-// (tests/test_gpu_calib.py sweeps every input).
+// A cheaper exp for approximate sums only (the grid predictions of the row
+// sums, zs_k_sapx: a wrong prediction costs time, never exactness): 2^(d *
+// f32(log2 e)) by v_exp_f32 alone, for d in [ZS_EXP_FAST_MIN, 1]. Its relative
+// error against zs_expf (the argument's rounding, at most |d log2 e| 2^-24,
+// dominates) is measured by tests/test_gpu_calib.py over every input.
 #define ZS_EXP_HW_EPS 0x1p-16
 __device__ __forceinline__ float zs_exp_hw(float d) {
     return __builtin_amdgcn_exp2f(d * 1.44269502162933349609375f);

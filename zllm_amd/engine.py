@@ -10,6 +10,8 @@ torch is used only for device memory and the stream; every computation runs
 in libzs's HIP kernels.
 """
 import ctypes as C
+import sys
+import weakref
 import secrets
 from dataclasses import dataclass, field
 from typing import Dict, List, Optional, Sequence, Tuple
@@ -29,21 +31,38 @@ def _check(ctx_handle, rc, what):
         raise ZsError(f"{what} failed ({rc}): {msg.decode() if msg else ''}")
 
 
+def _finalizing() -> bool:
+    """True during interpreter shutdown: destructors then leave device
+    objects to the process exit instead of calling into the HIP runtime,
+    which torch may already have begun to tear down."""
+    return sys is None or sys.is_finalizing()
+
+
 class Context:
-    """One libzs context (device scratch sized for max_rows x max_vocab)."""
+    """One libzs context (device scratch sized for max_rows x max_vocab).
+
+    close() releases the vocabularies and DFAs created on it, then the
+    context; callers that own a context call it when done (the destructor
+    does the same outside interpreter shutdown)."""
 
     def __init__(self, device: int = 0, max_rows: int = 256, max_vocab: int = 151936):
         self.device = device
         self.max_rows = max_rows
         self.max_vocab = max_vocab
+        self._children = weakref.WeakSet()
         h = C.c_void_p()
         rc = lib().zs_ctx_create(device, max_rows, max_vocab, C.byref(h))
         if rc != ZS_OK:
             raise ZsError(f"zs_ctx_create failed ({rc})")
         self.h = h
 
+    def _adopt(self, obj) -> None:
+        self._children.add(obj)
+
     def close(self):
         if self.h:
+            for child in list(self._children):
+                child.close()
             lib().zs_ctx_destroy(self.h)
             self.h = None
 
@@ -61,6 +80,8 @@ class Context:
         return {names[i].decode(): float(ms[i]) for i in range(n)}
 
     def __del__(self):
+        if _finalizing():
+            return
         try:
             self.close()
         except Exception:
@@ -140,6 +161,7 @@ class TokenByteTable:
                                    self.eos, C.byref(h))
         _check(ctx.h, rc, "zs_vocab_create")
         self.h = h
+        ctx._adopt(self)
 
     @classmethod
     def from_host_table(cls, ctx, host, eos=None):
@@ -168,12 +190,19 @@ class TokenByteTable:
                                    obj.eos, C.byref(h))
         _check(ctx.h, rc, "zs_vocab_create")
         obj.h = h
+        ctx._adopt(obj)
         return obj
 
+    def close(self):
+        if getattr(self, "h", None):
+            lib().zs_vocab_destroy(self.h)
+            self.h = None
+
     def __del__(self):
+        if _finalizing():
+            return
         try:
-            if self.h:
-                lib().zs_vocab_destroy(self.h)
+            self.close()
         except Exception:
             pass
 
@@ -193,6 +222,12 @@ class ByteDfa:
                                  C.byref(h))
         _check(ctx.h, rc, "zs_dfa_create")
         self.h = h
+        ctx._adopt(self)
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().zs_dfa_destroy(self.h)
+            self.h = None
 
     def is_live(self, s: int) -> bool:
         return bool(lib().zs_dfa_is_live(self.h, s))
@@ -225,9 +260,10 @@ class ByteDfa:
         lib().zs_dfa_memo_clear(self.h)
 
     def __del__(self):
+        if _finalizing():
+            return
         try:
-            if self.h:
-                lib().zs_dfa_destroy(self.h)
+            self.close()
         except Exception:
             pass
 
