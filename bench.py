@@ -106,11 +106,11 @@ def algorithmic_bytes_per_row(V, H, masked):
 
 
 SPEC_K = 4
-# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
-# (profiles/c5_traffic.md), scaled by the copy-kernel calibration there; None
-# where not measured
-TRAFFIC = {"zs_k_spec_chunk": 1402.3e6, "zs_k_row": 572.3e6, "zs_k_pv": 64.1e6, "zs_k_tp_inc": 36.3e6,
-           "zs_k_big": 0.5e6}
+# HBM bytes per launch of the C5 batch's dispatches, measured with rocprofv3
+# --pmc FETCH_SIZE / WRITE_SIZE and scaled by the copy-kernel calibration
+# (profiles/c5_kernels_counters.md, the tree of the commit that added it)
+TRAFFIC = {"zs_k_spec_chunk": 1402.4e6, "zs_k_row": 118.7e6, "zs_k_sapx": 83.0e6, "zs_k_sround1": 94.2e6,
+           "zs_k_sround2": 91.6e6, "zs_k_pv": 64.1e6, "zs_k_tp_inc": 36.3e6, "zs_k_big": 0.5e6}
 
 
 def spec_bytes_per_row(V, k):
@@ -537,6 +537,13 @@ def main():
         "zs_k_pv": float(sum(4 * V + 4 * V for i in big_rows)),   # read logits, write p
         "zs_k_spec_chunk": float(B * 4 * V * (2 * SPEC_K + 1)),
     }
+    # the row sums read every unmasked row's logits once per pass and a masked
+    # row's gathered allowed values (x~ and y)
+    nb = bits.cpu().numpy().view(np.uint32)
+    allowed = [int(np.unpackbits(nb[i].view(np.uint8)).sum()) if W["masked"][i] else 0 for i in range(B)]
+    sum_bytes = float(sum(4 * V if not W["masked"][i] else 8 * allowed[i] for i in range(B)))
+    for k in ("zs_k_sapx", "zs_k_sround1", "zs_k_sround2"):
+        per_kernel_bytes[k] = sum_bytes
     dom_bytes = per_kernel_bytes.get(dom, step_bytes)
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
     # the sampler chain alone (one stream): every sampler kernel's time, against
@@ -588,6 +595,12 @@ def main():
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": TRAFFIC.get(dom),
                      "algorithmic_bytes": dom_bytes, "ms": round(dom_ms, 4)},
+        "roofline_kernels": {k: {"ms": round(acc[k], 4), "algorithmic_bytes": per_kernel_bytes[k],
+                                 "achieved": round(per_kernel_bytes[k] / (acc[k] * 1e-3) / 1e9, 1),
+                                 "frac": round(per_kernel_bytes[k] / (acc[k] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                 "traffic": TRAFFIC.get(k)}
+                             for k in ("zs_k_row", "zs_k_sapx", "zs_k_sround1", "zs_k_sround2", "zs_k_pv")
+                             if k in acc and k in per_kernel_bytes},
         "roofline_sampler": {"bound": "hbm", "kernels": "zs_sample (all its kernels, one stream)",
                              "achieved": round(samp_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                              "frac": round(samp_gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": samp_bytes,
