@@ -832,30 +832,37 @@ __device__ __forceinline__ int tp_walk(const zs_sargs& a, uint32_t r, float top_
         k = zs_grid_k(s);
         kthr = zs_grid_thresh(top_p, eg);
     };
+    // the bucket records of the next two groups of 64 are loaded ahead
+    struct grp_ld { uint32_t cnt, meta; unsigned long long tot; };
+    auto load = [&](uint32_t b) {
+        grp_ld g = {0u, 0u, 0ull};
+        if (b + lane < ZS_TP_NB) { g.cnt = bk[b + lane].cnt; g.meta = bk[b + lane].meta; g.tot = bk[b + lane].tot; }
+        return g;
+    };
     uint32_t b0 = 0;
+    grp_ld cur = load(0), nxt = load(64);
     while (b0 < ZS_TP_NB) {
-        const uint32_t bb = b0 + lane;
-        uint32_t cnt = 0u, meta = 0u;
-        unsigned long long tot = 0ull;
-        if (bb < ZS_TP_NB) { cnt = bk[bb].cnt; meta = bk[bb].meta; tot = bk[bb].tot; }
+        const uint32_t cnt = cur.cnt, meta = cur.meta;
         const bool special = cnt && ((int)(meta & TP_M_EG) != eg || (meta & TP_M_TIE0));
-        const unsigned long long inc = (cnt && !special) ? tot : 0ull;
-        unsigned long long incl = inc;
-        for (int d = 1; d < 64; d <<= 1) {
-            const unsigned long long y = __shfl_up(incl, d, 64);
-            if (lane >= (uint32_t)d) incl += y;
-        }
+        // totals on the grid, saturated: a group is only added whole while the
+        // sum stays below the binade end
+        const uint32_t inc = (cnt && !special) ? (uint32_t)min(cur.tot, (unsigned long long)ZS_INC_CAP) : 0u;
+        const uint32_t incl = sm_wave_scan_sat(inc);
         const unsigned long long lim = min((unsigned long long)ZS_BINADE, (unsigned long long)kthr);
         const unsigned long long hm = __ballot(cnt && (special || k + incl >= lim));
         if (!hm) {
-            k += __shfl(incl, 63, 64);
+            k += (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
             b0 += 64;
+            cur = nxt;
+            nxt = load(b0 + 64);
             continue;
         }
         const uint32_t f = (uint32_t)__ffsll((long long)hm) - 1u;
-        k += __shfl(incl - inc, (int)f, 64);
+        k += f ? (uint32_t)__builtin_amdgcn_readlane((int)incl, (int)f - 1) : 0u;
         const uint32_t b = b0 + f;
         b0 = b + 1;
+        cur = load(b0);
+        nxt = load(b0 + 64);
         const uint32_t n = __shfl(cnt, (int)f, 64), bm = __shfl(meta, (int)f, 64);
         if (!(bm & TP_M_SORTED)) {
             return 0;
@@ -1088,6 +1095,7 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
             if (t < 64) {
                 walk_out w = {false, 0u, 0u};
                 const int res = tp_walk(a, r, P.top_p, &w);
+
                 if (t == 0) { sh.u[0] = (uint32_t)res; sh.u[1] = w.v; sh.u[2] = w.rank; }
             }
             __syncthreads();
