@@ -214,8 +214,8 @@ typedef struct zs_row_params {
 #define ZS_ST_NONFINITE 2u     /* NaN/+inf/all -inf after adjustment: id V-1 (sampler.rs:127) */
 #define ZS_ST_SMALL 4u         /* survivors fit the on-chip exact path */
 #define ZS_ST_TOPLP_AMBIG 8u   /* top_logprobs order depends on the last bit of lse */
-#define ZS_ST_LIMIT 0x100u     /* the row exceeded ZS_MAX_PATCHES: nothing was sampled,
-                                  d_token = 0xffffffff; callers must check it */
+#define ZS_ST_LIMIT 0x100u     /* reserved (ABI 1 refused rows with over 4096 merged
+                                  ban / bias / count entries; every row is served now) */
 
 /* One step over B rows (the decode loop order of rest.rs:2594-2624):
  *   mask (bans, then the allow bitset)  -> x~        (observers see x~)
@@ -274,8 +274,9 @@ typedef struct zs_batch {
     void* pass_event;
 } zs_batch;
 
-/* Maximum entries per row in the merged bias+count+ban list. */
-#define ZS_MAX_PATCHES 4096
+/* The ban, bias and count lists of a row may hold any number of entries (ids
+ * >= V are ignored); a bias list may name an id more than once, its entries
+ * then add in list order (decode_ctrl.rs:108-112). */
 
 int zs_sample(zs_ctx* ctx, const zs_batch* batch, void* stream);
 

@@ -161,19 +161,19 @@ def test_unseeded_rows_draw_independently():
     assert not errs, "\n".join(errs[:10])
 
 
-def test_patch_limit_fails_cleanly():
-    """A row whose merged ban + bias + count list exceeds ZS_MAX_PATCHES (4096
-    entries; here 6000 counted ids and 2000 bans) is refused with
-    ZS_ST_LIMIT and token 0xffffffff, never sampled from a truncated list;
-    the other rows of the batch still match the oracle, and
-    BatchSampler.step raises on it. A row at exactly the limit is sampled."""
+def test_long_patch_lists_match_oracle():
+    """Ban, bias and count lists of any length (decode_ctrl.rs:107-126,
+    logit_fsm.rs:248-252): 6000 counted ids plus 2000 bans, a row past the
+    4096-entry head the row kernel keeps on chip, and 5000 biases whose ids
+    repeat (their adds happen in list order, where f32 rounding tells the
+    orders apart) are sampled and observed exactly as the oracle does, and
+    BatchSampler.step accepts them."""
     import torch
 
     from tests.gpu_util import compare, ctx, make_rows, run_gpu
-    from zllm_amd._lib import ZS_MAX_PATCHES, ZS_ST_LIMIT
     from zllm_amd.engine import BatchSampler
-    B, V = 4, 32000
-    print(f"[case] patch limit B={B} V={V}", flush=True)
+    B, V = 5, 32000
+    print(f"[case] long patch lists B={B} V={V}", flush=True)
     rng = np.random.default_rng(7)
     x = synth.logits_powerlaw(B, V, 7)
     params = synth.mixed_params(B, V, 7, hist=64)
@@ -183,19 +183,20 @@ def test_patch_limit_fails_cleanly():
     ids = rng.permutation(V)
     params[1]["counts"] = [(int(t), 1 + int(t) % 3) for t in ids[:6000]]
     params[1]["ban"] = [int(t) for t in ids[6000:8000]]
-    # exactly at the limit: 3096 counted ids + 1000 bans
-    params[2]["counts"] = [(int(t), 2) for t in ids[:ZS_MAX_PATCHES - 1000]]
-    params[2]["ban"] = [int(t) for t in ids[ZS_MAX_PATCHES - 1000:ZS_MAX_PATCHES]]
+    params[2]["counts"] = [(int(t), 2) for t in ids[:3096]]
+    params[2]["ban"] = [int(t) for t in ids[3096:4096]]
+    params[3]["counts"] = [(int(t), 1) for t in ids[:4500]]
+    # 5000 biases on 1200 ids (most ids biased several times, magnitudes apart)
+    bid = rng.choice(ids[4000:5200], 5000)
+    params[3]["bias"] = [(int(t), float(np.float32(rng.normal(0, 4) * 10.0 ** rng.integers(-3, 2)))) for t in bid]
+    params[3]["ban"] = [int(t) for t in bid[:300:7]]
+    params[4]["bias"] = [(int(t), float(np.float32(rng.normal(0, 2)))) for t in ids[:4200]]
+    params[4]["top_k"] = 0
     out = run_gpu(x, params)
-    st = out["status"].view(np.uint32)
-    assert st[1] & ZS_ST_LIMIT and out["token"].view(np.uint32)[1] == 0xFFFFFFFF
-    assert not any(st[i] & ZS_ST_LIMIT for i in (0, 2, 3))
-    keep = [0, 2, 3]
-    errs = compare(x[keep], [params[i] for i in keep], {k: v[keep] for k, v in out.items()})
+    errs = compare(x, params, out)
     assert not errs, "\n".join(errs[:20])
     bs = BatchSampler(ctx(max(64, B), 151936))
-    with pytest.raises(RuntimeError, match="ZS_ST_LIMIT"):
-        bs.step(torch.from_numpy(x).cuda(), make_rows(params))
+    bs.step(torch.from_numpy(x).cuda(), make_rows(params))
 
 
 def test_masked_rows_gathered_p1():

@@ -28,7 +28,6 @@ ZS_ST_TOPLP_AMBIG = 8
 ZS_ST_LIMIT = 0x100
 ZS_ST_FALLBACK = 0x200
 
-ZS_MAX_PATCHES = 4096
 
 
 class RowParams(C.Structure):

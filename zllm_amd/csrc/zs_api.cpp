@@ -160,9 +160,10 @@ extern "C" int zs_ctx_create(int device, uint32_t max_rows, uint32_t max_vocab, 
     ctx->num_cus = (uint32_t)ncu;
     const size_t R = max_rows, C = ctx->max_chunks;
     if (!rc) rc = zs_alloc(ctx, &ctx->p_cnt, R);
-    if (!rc) rc = zs_alloc(ctx, &ctx->p_id, R * ZS_MAX_PATCHES);
-    if (!rc) rc = zs_alloc(ctx, &ctx->p_flags, R * ZS_MAX_PATCHES);
-    if (!rc) rc = zs_alloc(ctx, &ctx->p_y, R * ZS_MAX_PATCHES);
+    // the merged patch list: at most one entry per id of a row
+    if (!rc) rc = zs_alloc(ctx, &ctx->p_id, R * (size_t)max_vocab);
+    if (!rc) rc = zs_alloc(ctx, &ctx->p_flags, R * (size_t)max_vocab);
+    if (!rc) rc = zs_alloc(ctx, &ctx->p_y, R * (size_t)max_vocab);
     if (!rc) rc = zs_alloc(ctx, &ctx->rst, R);
     if (!rc) rc = zs_alloc(ctx, &ctx->pairs, R * (size_t)max_vocab * 2 + 8);  // 16-byte loads at the tail
     if (!rc) rc = zs_alloc(ctx, &ctx->pv, R * (size_t)max_vocab + 4);  // 16-byte loads at the tail

@@ -47,10 +47,9 @@
 #define RW_KEEP 1024       // a list above this is compacted to its top K
 
 struct rw_shared {
-    uint32_t pid[ZS_MAX_PATCHES];   // patched ids (sorted) | flags << 30
-    float py[ZS_MAX_PATCHES];       // their y
+    uint32_t pid[4096];             // the patch list's head (ZS_PATCH_LDS): ids (sorted) | flags << 30
+    float py[4096];                 // their y
     union {
-        unsigned long long ent[ZS_MAX_PATCHES];   // P0: merge sort
         struct {
             unsigned long long o[RW_BUF];         // P1: observer candidates
             unsigned long long s[RW_BUF];         // P1: sampler candidates
@@ -65,7 +64,7 @@ struct rw_shared {
     float fthr[2];                  // candidate thresholds as values
     float fcut[2];                  // largest values cut from the lists
     unsigned long long rl[RW_NW];
-    uint32_t n_ent, n_surv, tok;
+    uint32_t n_surv, tok;
     uint32_t ovf[3];                // first tile that lost a list entry, per group slot
     uint32_t thr_o, thr_s;          // candidate admission thresholds (keys)
     float fsh;
@@ -130,145 +129,165 @@ __device__ __forceinline__ void rw_wave_sort(unsigned long long* buf, uint32_t m
 }
 
 // ---------------------------------------------------------------------------
-// P0: merged patch list (the entries of zs_k_prep's format, plus LDS copies)
-// Entries are (id << 32) | (kind << 28) | order with kind 0 = ban, 1 = bias,
-// 2 = count; sorting groups them by id with bans first and biases in list
-// order, which reproduces the reference's per-token operation sequence.
-// Returns the number of patched ids, or -1 when the row has more entries than
-// ZS_MAX_PATCHES.
+// P0: merged patch list. The row's ban / bias / count entries (any number)
+// are merged into one entry per patched id, in id order, with the exact
+// patched y of the reference's per-token operation sequence: bans first
+// (logit_fsm.rs:248-252), then the logit_bias entries in list order, then the
+// penalty of the count map (decode_ctrl.rs:107-126). The ids' bitmap and its
+// per-word prefix counts (dynamic LDS) give every patched id its rank in the
+// list; the list itself is in row scratch (a.pstride entries per row), its
+// first ZS_PATCH_LDS entries also in LDS for the row kernel's phases.
+// Returns the number of patched ids.
 // ---------------------------------------------------------------------------
+#define ZS_PATCH_LDS 4096
+__device__ __forceinline__ uint32_t rw_rank(uint32_t id, uint32_t words) {
+    const uint32_t wd = rw_pbits[id >> 5];
+    return rw_pbits[words + (id >> 5)] + __popc(wd & ((1u << (id & 31)) - 1u));
+}
+
 __device__ __forceinline__ int rw_patches(const zs_sargs& a, uint32_t r, const zs_row_params& P, uint32_t& has_y, rw_shared& sh,
                                           bool wr = true) {
     const zs_batch& b = a.b;
     const uint32_t t = threadIdx.x, V = b.V;
     const uint32_t words = (V + 31) / 32;
-    for (uint32_t i = t; i < words; i += RW_NT) rw_pbits[i] = 0u;
+    uint32_t* seen = rw_pbits + 2 * words;   // bias ids met once, and more than once
+    uint32_t* dup = rw_pbits + 3 * words;
     const uint32_t ban0 = b.d_ban_off ? b.d_ban_off[r] : 0, ban1 = b.d_ban_off ? b.d_ban_off[r + 1] : 0;
     const uint32_t bi0 = b.d_bias_off ? b.d_bias_off[r] : 0, bi1 = b.d_bias_off ? b.d_bias_off[r + 1] : 0;
+    for (uint32_t i = t; i < words; i += RW_NT) {
+        rw_pbits[i] = 0u;
+        if (bi1 != bi0) { seen[i] = 0u; dup[i] = 0u; }
+    }
     uint32_t c0 = b.d_cnt_off ? b.d_cnt_off[r] : 0, c1 = b.d_cnt_off ? b.d_cnt_off[r + 1] : 0;
     if (!zs_penalty_active(P)) c1 = c0;  // counts only matter when penalties are active
     const uint32_t nb = ban1 - ban0, nbi = bi1 - bi0, nc = c1 - c0;
-    const uint32_t total = nb + nbi + nc;
     const uint32_t nsub = (V + ZS_SUB - 1) / ZS_SUB;
     uint32_t* psub = a.p_sub + (size_t)r * (a.max_subs + 1);
-    if (t == 0) sh.n_ent = 0;
+    uint32_t* out_id = a.p_id + (size_t)r * a.pstride;
+    uint32_t* out_fl = a.p_flags + (size_t)r * a.pstride;
+    float* out_y = a.p_y + (size_t)r * a.pstride;
+    // entry k: in LDS (ids and flags in sh.pid, y in sh.py) for the list's
+    // head, in row scratch past it; the head is copied out at the end
+    auto FL = [&](uint32_t k) -> uint32_t { return k < ZS_PATCH_LDS ? sh.pid[k] >> RW_PF_SHIFT : out_fl[k]; };
+    auto SET_FL = [&](uint32_t k, uint32_t f) {
+        if (k < ZS_PATCH_LDS) sh.pid[k] = (sh.pid[k] & ((1u << RW_PF_SHIFT) - 1u)) | (f << RW_PF_SHIFT);
+        else out_fl[k] = f;
+    };
+    auto Y = [&](uint32_t k) -> float { return k < ZS_PATCH_LDS ? sh.py[k] : out_y[k]; };
+    auto SET_Y = [&](uint32_t k, float y) {
+        if (k < ZS_PATCH_LDS) sh.py[k] = y;
+        else out_y[k] = y;
+    };
     __syncthreads();
-    if (total > ZS_MAX_PATCHES) {
-        if (wr && t == 0) a.p_cnt[r] = 0;
-        for (uint32_t j = t; wr && j <= nsub; j += RW_NT) psub[j] = 0;
-        has_y = 0;
-        return -1;
-    }
-    for (uint32_t i = t; i < total; i += RW_NT) {
-        uint32_t id, kind, ord;
-        if (i < nb) { id = b.d_ban_ids[ban0 + i]; kind = 0; ord = i; }
-        else if (i < nb + nbi) { ord = i - nb; id = b.d_bias_ids[bi0 + ord]; kind = 1; }
-        else { ord = i - nb - nbi; id = b.d_cnt_ids[c0 + ord]; kind = 2; }
-        if (id < V) {
-            const uint32_t pos = atomicAdd(&sh.n_ent, 1u);
-            sh.u.ent[pos] = ((unsigned long long)id << 32) | ((unsigned long long)kind << 28) | ord;
-        }
+    // the patched ids, and the bias ids that occur more than once
+    for (uint32_t i = t; i < nb + nbi + nc; i += RW_NT) {
+        uint32_t id;
+        if (i < nb) id = b.d_ban_ids[ban0 + i];
+        else if (i < nb + nbi) id = b.d_bias_ids[bi0 + i - nb];
+        else id = b.d_cnt_ids[c0 + i - nb - nbi];
+        if (id >= V) continue;
+        const uint32_t bit = 1u << (id & 31);
+        atomicOr(&rw_pbits[id >> 5], bit);
+        if (i >= nb && i < nb + nbi && (atomicOr(&seen[id >> 5], bit) & bit)) atomicOr(&dup[id >> 5], bit);
     }
     __syncthreads();
-    const uint32_t n = sh.n_ent;
-    if (n <= 256) {
-        // a few hundred entries: one wave, no barriers between the stages
-        if (zs_wid() == 0 && n > 1) rw_wave_sort(sh.u.ent, n);
-        __syncthreads();
-    } else {
-        uint32_t np2 = 1;
-        while (np2 < n) np2 <<= 1;
-        for (uint32_t i = n + t; i < np2; i += RW_NT) sh.u.ent[i] = ~0ull;
-        __syncthreads();
-        if (np2 > 2 * RW_NT) block_sort_reg_u64<RW_NT, 4>(sh.u.ent, np2);
-        else block_sort_reg_u64<RW_NT, 2>(sh.u.ent, np2);
-    }
-    uint32_t* out_id = a.p_id + (size_t)r * ZS_MAX_PATCHES;
-    uint32_t* out_fl = a.p_flags + (size_t)r * ZS_MAX_PATCHES;
-    float* out_y = a.p_y + (size_t)r * ZS_MAX_PATCHES;
-    uint32_t base_out = 0, hy = 0;
-    for (uint32_t s0 = 0; s0 < n; s0 += RW_NT) {
-        const uint32_t i = s0 + t;
-        uint32_t is_start = 0;
-        if (i < n) {
-            const uint32_t id = (uint32_t)(sh.u.ent[i] >> 32);
-            is_start = (i == 0) || ((uint32_t)(sh.u.ent[i - 1] >> 32) != id);
-        }
-        uint32_t tot;
-        const uint32_t ex = block_excl_scan_u<RW_NT>(is_start, sh.ru[0], &tot);
-        if (is_start) {
-            const uint32_t id = (uint32_t)(sh.u.ent[i] >> 32);
-            float x = b.d_logits[(size_t)r * b.ld + id];
-            if ((P.flags & ZS_ROW_MASKED) && b.d_allow_bits && !zs_allowed_bit(b, r, id)) x = -INFINITY;
-            uint32_t fl = 0;
-            uint32_t j = i;
-            // bans (logit_fsm.rs:248-252)
-            while (j < n && (uint32_t)(sh.u.ent[j] >> 32) == id && ((sh.u.ent[j] >> 28) & 3ull) == 0) {
-                fl |= ZS_PF_BAN;
-                j++;
-            }
-            if (fl & ZS_PF_BAN) x = -INFINITY;
-            float y = x;
-            // logit_bias in list order (decode_ctrl.rs:108-112)
-            while (j < n && (uint32_t)(sh.u.ent[j] >> 32) == id && ((sh.u.ent[j] >> 28) & 3ull) == 1) {
-                const uint32_t ord = (uint32_t)(sh.u.ent[j] & 0x0fffffffull);
-                y = y + b.d_bias_vals[bi0 + ord];
-                fl |= ZS_PF_Y;
-                j++;
-            }
-            // penalty (decode_ctrl.rs:113-125): repeat, then frequency * count + presence
-            if (j < n && (uint32_t)(sh.u.ent[j] >> 32) == id && ((sh.u.ent[j] >> 28) & 3ull) == 2) {
-                const uint32_t ord = (uint32_t)(sh.u.ent[j] & 0x0fffffffull);
-                const uint32_t cnt = b.d_cnt_vals[c0 + ord];
-                if (P.repeat != 1.0f) {
-                    if (y > 0.0f) y = y / P.repeat;
-                    else y = y * P.repeat;
-                }
-                float pen_v = __fmul_rn(P.frequency, (float)cnt);
-                pen_v = __fadd_rn(pen_v, P.presence);
-                y = __fsub_rn(y, pen_v);
-                fl |= ZS_PF_Y;
-            }
-            const uint32_t o = base_out + ex;
-            if (wr) {
-                out_id[o] = id;
-                out_fl[o] = fl;
-                out_y[o] = y;
-            }
-            sh.pid[o] = id | (fl << RW_PF_SHIFT);
-            sh.py[o] = y;
-            atomicOr(&rw_pbits[id >> 5], 1u << (id & 31));
-            hy |= (fl & ZS_PF_Y) ? 1u : 0u;
-        }
-        base_out += tot;
-    }
-    has_y = block_or_u<RW_NT>(hy, sh.ru[1]);
-    if (wr && t == 0) a.p_cnt[r] = base_out;
     // per-word prefix counts of the bitmap (words / RW_NT words per thread at most 8)
+    uint32_t np;
     {
         const uint32_t per = (words + RW_NT - 1) / RW_NT;
         const uint32_t w0 = t * per;
         uint32_t c = 0;
         for (uint32_t w = w0; w < min(w0 + per, words); w++) c += __popc(rw_pbits[w]);
-        uint32_t tot;
-        uint32_t run = block_excl_scan_u<RW_NT>(c, sh.ru[2], &tot);
+        uint32_t run = block_excl_scan_u<RW_NT>(c, sh.ru[2], &np);
         for (uint32_t w = w0; w < min(w0 + per, words); w++) {
             rw_pbits[words + w] = run;
-            run += __popc(rw_pbits[w]);
+            // the list in id order: every patched id with its masked logit
+            uint32_t m = rw_pbits[w];
+            while (m) {
+                const uint32_t id = w * 32 + (uint32_t)__builtin_ctz(m);
+                m &= m - 1u;
+                float x = b.d_logits[(size_t)r * b.ld + id];
+                if ((P.flags & ZS_ROW_MASKED) && b.d_allow_bits && !zs_allowed_bit(b, r, id)) x = -INFINITY;
+                if (run < ZS_PATCH_LDS) {
+                    sh.pid[run] = id;
+                    sh.py[run] = x;
+                } else {
+                    out_id[run] = id;
+                    out_fl[run] = 0u;
+                    out_y[run] = x;
+                }
+                run++;
+            }
         }
     }
-    // first patch of every 1024-id sub-chunk (read by zs_k_big / zs_k_final)
-    for (uint32_t j = t; wr && j <= nsub; j += RW_NT) {
-        uint32_t lo = 0, hi = base_out;
-        const uint32_t key = j * ZS_SUB;
-        while (lo < hi) {
-            const uint32_t mid = (lo + hi) >> 1;
-            if ((sh.pid[mid] & ((1u << RW_PF_SHIFT) - 1u)) < key) lo = mid + 1; else hi = mid;
-        }
-        psub[j] = lo;
+    np = rw_uni(np);
+    __syncthreads();
+    // bans (a banned x~ and y are -inf)
+    for (uint32_t i = t; i < nb; i += RW_NT) {
+        const uint32_t id = b.d_ban_ids[ban0 + i];
+        if (id >= V) continue;
+        const uint32_t k = rw_rank(id, words);
+        SET_FL(k, ZS_PF_BAN);
+        SET_Y(k, -INFINITY);
     }
     __syncthreads();
-    return (int)base_out;
+    // logit_bias (decode_ctrl.rs:108-112): an id met once takes its bias in
+    // parallel; the entries of an id met more than once are added by one
+    // thread in list order
+    for (uint32_t i = t; i < nbi; i += RW_NT) {
+        const uint32_t id = b.d_bias_ids[bi0 + i];
+        if (id >= V || ((dup[id >> 5] >> (id & 31)) & 1u)) continue;
+        const uint32_t k = rw_rank(id, words);
+        SET_Y(k, Y(k) + b.d_bias_vals[bi0 + i]);
+        SET_FL(k, FL(k) | ZS_PF_Y);
+    }
+    if (t == 0) {
+        for (uint32_t i = 0; i < nbi; i++) {
+            const uint32_t id = b.d_bias_ids[bi0 + i];
+            if (id >= V || !((dup[id >> 5] >> (id & 31)) & 1u)) continue;
+            const uint32_t k = rw_rank(id, words);
+            SET_Y(k, Y(k) + b.d_bias_vals[bi0 + i]);
+            SET_FL(k, FL(k) | ZS_PF_Y);
+        }
+    }
+    __syncthreads();
+    // penalty (decode_ctrl.rs:113-125): repeat, then frequency * count + presence
+    // (the count map holds each id once)
+    for (uint32_t i = t; i < nc; i += RW_NT) {
+        const uint32_t id = b.d_cnt_ids[c0 + i];
+        if (id >= V) continue;
+        const uint32_t k = rw_rank(id, words);
+        const uint32_t cnt = b.d_cnt_vals[c0 + i];
+        float y = Y(k);
+        if (P.repeat != 1.0f) {
+            if (y > 0.0f) y = y / P.repeat;
+            else y = y * P.repeat;
+        }
+        float pen_v = __fmul_rn(P.frequency, (float)cnt);
+        pen_v = __fadd_rn(pen_v, P.presence);
+        y = __fsub_rn(y, pen_v);
+        SET_Y(k, y);
+        SET_FL(k, FL(k) | ZS_PF_Y);
+    }
+    __syncthreads();
+    // the list's head out to row scratch (the later kernels read it there)
+    uint32_t hy = 0;
+    for (uint32_t k = t; k < np; k += RW_NT) {
+        const uint32_t fl = FL(k);
+        hy |= (fl & ZS_PF_Y) ? 1u : 0u;
+        if (wr && k < ZS_PATCH_LDS) {
+            out_id[k] = sh.pid[k] & ((1u << RW_PF_SHIFT) - 1u);
+            out_fl[k] = fl;
+            out_y[k] = sh.py[k];
+        }
+    }
+    has_y = block_or_u<RW_NT>(hy, sh.ru[1]);
+    if (wr && t == 0) a.p_cnt[r] = np;
+    // first patch of every 1024-id sub-chunk (read by the sum, big-row and
+    // output kernels): the bitmap's prefix count at the sub-chunk start
+    for (uint32_t j = t; wr && j <= nsub; j += RW_NT) psub[j] = j * (ZS_SUB / 32) < words ? rw_pbits[words + j * (ZS_SUB / 32)] : np;
+    __syncthreads();
+    return (int)np;
 }
 
 // ---------------------------------------------------------------------------
@@ -276,6 +295,8 @@ __device__ __forceinline__ int rw_patches(const zs_sargs& a, uint32_t r, const z
 // divided by T) of the 4 ids g*RW_G + 4t .. +3.
 // ---------------------------------------------------------------------------
 struct rw_row {
+    const uint32_t* gfl;            // the patch list in row scratch (entries past its LDS head)
+    const float* gy;
     const float* row;
     const uint32_t* allow;
     const uint32_t* allow_or_row;   // allow bits, or any readable words when unmasked
@@ -316,15 +337,18 @@ __device__ __forceinline__ rw_raw rw_fetch(const rw_row& R, uint32_t g) {
 // y to -inf, biased or counted ids take their y from the patch list. Their
 // rank in the sorted list is the number of bitmap bits before them (per-word
 // prefix counts follow the bitmap).
-__device__ __forceinline__ void rw_patch4(uint32_t idx0, uint32_t pb, uint32_t words, uint32_t wd, float (&x)[4], float (&y)[4],
-                                       const rw_shared& sh) {
-    uint32_t rank = rw_pbits[words + (idx0 >> 5)] + __popc(wd & ((1u << (idx0 & 31)) - 1u));
+__device__ __forceinline__ void rw_patch4(const rw_row& R, uint32_t idx0, uint32_t pb, uint32_t wd, float (&x)[4],
+                                          float (&y)[4], const rw_shared& sh) {
+    uint32_t rank = rw_pbits[R.words + (idx0 >> 5)] + __popc(wd & ((1u << (idx0 & 31)) - 1u));
 #pragma unroll
     for (int q = 0; q < 4; q++) {
         if (!((pb >> q) & 1u)) continue;
-        const uint32_t fl = sh.pid[rank] >> RW_PF_SHIFT;
+        uint32_t fl;
+        float py;
+        if (rank < ZS_PATCH_LDS) { fl = sh.pid[rank] >> RW_PF_SHIFT; py = sh.py[rank]; }
+        else { fl = R.gfl[rank]; py = R.gy[rank]; }
         if (fl & ZS_PF_BAN) { x[q] = -INFINITY; y[q] = -INFINITY; }
-        if (fl & ZS_PF_Y) y[q] = sh.py[rank];
+        if (fl & ZS_PF_Y) y[q] = py;
         rank++;
     }
 }
@@ -352,7 +376,7 @@ __device__ __forceinline__ void rw_elems(const rw_row& R, uint32_t g, const rw_r
         const uint32_t wd = rw_pbits[wi];
         uint32_t pb = (wd >> (idx0 & 31)) & 15u;
         if (last) pb = idx0 < R.V ? pb : 0u;
-        if (pb) rw_patch4(idx0, pb, R.words, wd, x, y, sh);
+        if (pb) rw_patch4(R, idx0, pb, wd, x, y, sh);
     }
 }
 
@@ -588,7 +612,7 @@ __device__ __forceinline__ float* rw_scratch(const zs_sargs& a, uint32_t r) {
 // when no id or more than a quarter of the row is allowed (then the sums run
 // over the whole row). Uniform.
 __device__ __noinline__ uint32_t rw_gather_allowed(const float* row, const uint32_t* allow, uint32_t V, uint32_t np,
-                                                   float* cx) {
+                                                   float* cx, const uint32_t* gfl, const float* gy) {
     rw_shared& sh = rw_sh;
     const uint32_t t = threadIdx.x, words = (V + 31) / 32;
     const uint32_t per = (words + RW_NT - 1) / RW_NT, w0 = t * per, w1 = min(w0 + per, words);
@@ -615,9 +639,9 @@ __device__ __noinline__ uint32_t rw_gather_allowed(const float* row, const uint3
                 const uint32_t wd = rw_pbits[id >> 5];
                 if ((wd >> (id & 31)) & 1u) {
                     const uint32_t rank = rw_pbits[words + (id >> 5)] + __popc(wd & ((1u << (id & 31)) - 1u));
-                    const uint32_t fl = sh.pid[rank] >> RW_PF_SHIFT;
+                    const uint32_t fl = rank < ZS_PATCH_LDS ? sh.pid[rank] >> RW_PF_SHIFT : gfl[rank];
                     if (fl & ZS_PF_BAN) { x = -INFINITY; y = -INFINITY; }
-                    if (fl & ZS_PF_Y) y = sh.py[rank];
+                    if (fl & ZS_PF_Y) y = rank < ZS_PATCH_LDS ? sh.py[rank] : gy[rank];
                 }
             }
             cx[pos] = x;
@@ -708,20 +732,9 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
     // ---------------- P0: patches
     uint32_t has_y = 0;
     const int np = rw_patches(a, r, P, has_y, sh);
-    if (np < 0) {
-        if (t == 0) {
-            st.status = ZS_ST_LIMIT;
-            st.mode = ZS_MODE_DONE;
-            st.token = 0xffffffffu;
-            st.obs_need = 0;
-            st.rounds = 0;
-            st.n_cand = 0;
-            st.klist = 0;
-            st.kpend = 0;
-        }
-        return;
-    }
     rw_row R;
+    R.gfl = a.p_flags + (size_t)r * a.pstride;
+    R.gy = a.p_y + (size_t)r * a.pstride;
     R.row = b.d_logits + (size_t)r * b.ld;
     R.allow = ((P.flags & ZS_ROW_MASKED) && b.d_allow_bits) ? b.d_allow_bits + (size_t)r * b.allow_words : nullptr;
     R.V = V;
@@ -795,7 +808,7 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
     if (t == 0) { sh.g_n = 0; sh.g_done = 0; }
     if (R.allow && !greedy && !tinf) {
         const float* gcx = rw_scratch(a, r);
-        const uint32_t gn = rw_gather_allowed(R.row, R.allow, V, R.np, rw_scratch(a, r));
+        const uint32_t gn = rw_gather_allowed(R.row, R.allow, V, R.np, rw_scratch(a, r), R.gfl, R.gy);
         if (t == 0) { sh.g_n = gn; sh.g_done = 1; }
         if (gn && gn <= RW_BUF) {
             uint32_t nf = 0;
@@ -1269,7 +1282,7 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
     const bool doH = (obs_need & ZS_OBS_H) != 0;
     uint32_t gn = 0;
     if (R.allow && (doA || doB || doH))
-        gn = rw_uni(sh.g_done) ? rw_uni(sh.g_n) : rw_gather_allowed(R.row, R.allow, V, R.np, rw_scratch(a, r));
+        gn = rw_uni(sh.g_done) ? rw_uni(sh.g_n) : rw_gather_allowed(R.row, R.allow, V, R.np, rw_scratch(a, r), R.gfl, R.gy);
 
     // ---------------- row state for the sums, the big-row kernels and zs_k_final
     if (t == 0) {
@@ -1302,7 +1315,7 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
 }
 
 extern "C" int zs_row_launch(const zs_sargs& a, hipStream_t stream) {
-    const size_t dyn = 2 * ((a.b.V + 31) / 32) * sizeof(uint32_t);
+    const size_t dyn = 4 * ((a.b.V + 31) / 32) * sizeof(uint32_t);
     hipLaunchKernelGGL(zs_k_row, dim3(a.b.B), dim3(RW_NT), dyn, stream, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

@@ -471,9 +471,9 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_pv(zs_sargs a) {
         R.row = b.d_logits + (size_t)r * b.ld;
         R.masked = (P.flags & ZS_ROW_MASKED) && b.d_allow_bits;
         R.allow = R.masked ? b.d_allow_bits + (size_t)r * b.allow_words : nullptr;
-        R.pid = a.p_id + (size_t)r * ZS_MAX_PATCHES;
-        R.pfl = a.p_flags + (size_t)r * ZS_MAX_PATCHES;
-        R.py = a.p_y + (size_t)r * ZS_MAX_PATCHES;
+        R.pid = a.p_id + (size_t)r * a.pstride;
+        R.pfl = a.p_flags + (size_t)r * a.pstride;
+        R.py = a.p_y + (size_t)r * a.pstride;
         R.psub = a.p_sub + (size_t)r * (a.max_subs + 1);
         R.nsub = (V + ZS_SUB - 1) / ZS_SUB;
         R.V = V;
@@ -946,9 +946,9 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
     R.row = b.d_logits + (size_t)r * b.ld;
     R.masked = (P.flags & ZS_ROW_MASKED) && b.d_allow_bits;
     R.allow = R.masked ? b.d_allow_bits + (size_t)r * b.allow_words : nullptr;
-    R.pid = a.p_id + (size_t)r * ZS_MAX_PATCHES;
-    R.pfl = a.p_flags + (size_t)r * ZS_MAX_PATCHES;
-    R.py = a.p_y + (size_t)r * ZS_MAX_PATCHES;
+    R.pid = a.p_id + (size_t)r * a.pstride;
+    R.pfl = a.p_flags + (size_t)r * a.pstride;
+    R.py = a.p_y + (size_t)r * a.pstride;
     R.psub = a.p_sub + (size_t)r * (a.max_subs + 1);
     R.nsub = (b.V + ZS_SUB - 1) / ZS_SUB;
     R.V = b.V;
@@ -1563,13 +1563,13 @@ __global__ __launch_bounds__(64) void zs_k_final(zs_sargs a) {
     if (in_range) {
         xc = b.d_logits[(size_t)r * b.ld + tok];
         if ((P.flags & ZS_ROW_MASKED) && b.d_allow_bits && !zs_allowed_bit(b, r, tok)) xc = -INFINITY;
-        const uint32_t* pid = a.p_id + (size_t)r * ZS_MAX_PATCHES;
+        const uint32_t* pid = a.p_id + (size_t)r * a.pstride;
         const uint32_t* psub = a.p_sub + (size_t)r * (a.max_subs + 1);
         const uint32_t nsub = (b.V + ZS_SUB - 1) / ZS_SUB;
         const uint32_t p0 = psub[tok / ZS_SUB], p1 = psub[min(tok / ZS_SUB + 1, nsub)];
         bool ban = false;
         for (uint32_t p = p0 + lane; p < p1; p += 64)
-            if (pid[p] == tok && (a.p_flags[(size_t)r * ZS_MAX_PATCHES + p] & ZS_PF_BAN)) ban = true;
+            if (pid[p] == tok && (a.p_flags[(size_t)r * a.pstride + p] & ZS_PF_BAN)) ban = true;
         if (__ballot(ban)) xc = -INFINITY;
     }
     const float M = st.obs_max;
@@ -1679,6 +1679,7 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
     a.s_rec = ctx->s_rec;
     a.s_apx = ctx->s_apx;
     a.gath = ctx->gath;
+    a.pstride = ctx->max_vocab;
     a.s_hterm = ctx->s_hterm;
     const uint32_t B = bt->B;
     const uint32_t nch = (bt->V + ZS_P1_CH - 1) / ZS_P1_CH;

@@ -30,6 +30,7 @@ struct zs_sargs {
     float* s_apx;
     float* gath;
     float* s_hterm;
+    uint32_t pstride;   // entries per row of the merged patch list (p_id, p_flags, p_y): max_vocab
 };
 
 #define ZS_ST_FALLBACK 0x200u

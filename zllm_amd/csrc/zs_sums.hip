@@ -90,9 +90,9 @@ __device__ __forceinline__ sm_src sm_src_of(const zs_sargs& a, uint32_t r, const
         s.py = s.px;
         s.allow = ((P.flags & ZS_ROW_MASKED) && b.d_allow_bits) ? b.d_allow_bits + (size_t)r * b.allow_words : nullptr;
         const bool patched = a.p_cnt[r] != 0u;
-        s.pid = patched ? a.p_id + (size_t)r * ZS_MAX_PATCHES : nullptr;
-        s.pfl = a.p_flags + (size_t)r * ZS_MAX_PATCHES;
-        s.pyv = a.p_y + (size_t)r * ZS_MAX_PATCHES;
+        s.pid = patched ? a.p_id + (size_t)r * a.pstride : nullptr;
+        s.pfl = a.p_flags + (size_t)r * a.pstride;
+        s.pyv = a.p_y + (size_t)r * a.pstride;
         s.psub = a.p_sub + (size_t)r * (a.max_subs + 1);
         s.n = b.V;
         s.lim4 = (uint32_t)min((uint64_t)b.ld - 4u, (uint64_t)0xfffffff0u);

@@ -19,7 +19,7 @@ from typing import Dict, List, Optional, Sequence, Tuple
 import numpy as np
 import torch
 
-from ._lib import (Batch, LaneStream, RowParams, SpecBatch, ZS_OK, ZS_ST_LIMIT, ZS_ROW_LOGPROBS, ZS_ROW_MASKED, ZS_ROW_UNCERTAINTY,
+from ._lib import (Batch, LaneStream, RowParams, SpecBatch, ZS_OK, ZS_ROW_LOGPROBS, ZS_ROW_MASKED, ZS_ROW_UNCERTAINTY,
                    ZS_SPEC_BACKGROUND, ZsError, lib)
 
 OPENAI_TOP_LOGPROBS_CAP = 20  # logprobs.rs:27-29
@@ -445,10 +445,6 @@ class BatchSampler:
         out = self.run(logits, bufs, allow_bits)
         torch.cuda.current_stream(logits.device).synchronize()
         toks = out["token"].cpu().numpy().view(np.uint32)
-        st = out["status"].cpu().numpy().view(np.uint32)
-        bad = np.nonzero(st & ZS_ST_LIMIT)[0]
-        if len(bad):
-            raise RuntimeError(f"zs_sample: rows {bad.tolist()} exceed the per-row patch limit (ZS_ST_LIMIT)")
         for rq, tok in zip(rows, toks):
             rq.ctrl.counter += 1
             if rq.fsm is not None:
