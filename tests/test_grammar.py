@@ -489,3 +489,137 @@ def test_unicode_case_folding():
         py = re.compile(pat)
         for o in block:
             assert d.full_match(chr(o)) == bool(py.fullmatch(chr(o))), (hex(c), hex(o))
+
+
+# ------------------------------------------------------------ look-around and (?-u)
+# regex-automata's dense DFA (logit_fsm.rs:73-86) supports the line anchors of
+# (?m) / (?mR) and ASCII word boundaries, and refuses Unicode ones at build
+# time. Languages are pinned by brute force: every string of up to 5 symbols
+# over a small alphabet, whole-text match against Python's re on bytes (its
+# \b \w \s on bytes are the ASCII ones, its (?m) ^ $ are regex-syntax's
+# StartLF / EndLF); the forms Python lacks are written with its look-around.
+_LOOK_ALPHABET = [b"a", b"Z", b"1", b"_", b" ", b"\n", b"\r", "é".encode("utf-8"), b"-"]
+
+_PY_CRLF_START = rb"(?:(?<![\s\S])|(?<=\n)|(?<=\r)(?!\n))"
+_PY_CRLF_END = rb"(?:(?![\s\S])|(?=\r)|(?<!\r)(?=\n))"
+
+LOOK_PATTERNS = [
+    (r"(?-u)(?:\b\w+\b|\s|-)*", rb"(?:\b\w+\b|\s|-)*"),
+    (r"(?-u)(?:a|\B|_| |\n|\b1)*", rb"(?:a|\B|_| |\n|\b1)*"),
+    (r"(?-u)\<\w+\>(?: \<\w+\>)*", rb"(?<!\w)(?=\w)\w+(?<=\w)(?!\w)(?: (?<!\w)(?=\w)\w+(?<=\w)(?!\w))*"),
+    (r"(?-u)(?:\b{start}a|\b{end}-|\s)*", rb"(?:(?<!\w)(?=\w)a|(?<=\w)(?!\w)-|\s)*"),
+    (r"(?-u)\b{start-half}[a_ ]*\b{end-half}", rb"(?<!\w)[a_ ]*(?!\w)"),
+    (r"(?-u)(?:a\>|\<1|_| )*", rb"(?:a(?<=\w)(?!\w)|(?<!\w)(?=\w)1|_| )*"),
+    (r"(?-u)(?:a\b{end}|\b{start}1|_| )*", rb"(?:a(?<=\w)(?!\w)|(?<!\w)(?=\w)1|_| )*"),
+    (r"(?-u)(?:a\b{end-half}|\b{start-half}1| |_)*", rb"(?:a(?!\w)|(?<!\w)1| |_)*"),
+    (r"(?-u:\b)(?:é|a|1)+", rb"\b(?:\xc3\xa9|a|1)+"),
+    (r"(?m)^a*$(?:\n^a*$)*", rb"(?m)^a*$(?:\n^a*$)*"),
+    (r"(?m)(?:^|a|\n|\r|$|_$)*", rb"(?m)(?:^|a|\n|\r|$|_$)*"),
+    (r"(?m)(?:^_|a$|\n|\r|é)*", rb"(?m)(?:^_|a$|\n|\r|\xc3\xa9)*"),
+    (r"(?mR)(?:^a|_$|\n|\r)*", rb"(?:" + _PY_CRLF_START + rb"a|_" + _PY_CRLF_END + rb"|\n|\r)*"),
+    (r"(?mR)(?:^|$|\r|\n|a)*", rb"(?:" + _PY_CRLF_START + rb"|" + _PY_CRLF_END + rb"|\r|\n|a)*"),
+    (r"(?m:^a)\n(?-m:^a)", rb"(?m:^a)\n(?<![\s\S])a"),
+    (r"\Aa\z|(?m)^b$", rb"(?m)(?<![\s\S])a(?![\s\S])|^b$"),
+    (r"(?i-u)[k-m]+\w", rb"(?i)[k-m]+\w"),
+    (r"(?-u)[\w--\d]+ \s", rb"[A-Za-z_]+ \s"),
+]
+
+
+def _all_strings(alphabet, n):
+    out, layer = [b""], [b""]
+    for _ in range(n):
+        layer = [s + a for s in layer for a in alphabet]
+        out += layer
+    return out
+
+
+@pytest.mark.parametrize("pat,py", LOOK_PATTERNS)
+def test_look_around_matches_python_re(pat, py):
+    d = G.HostDfa(pat)
+    rx = re.compile(py)
+    texts = _all_strings(_LOOK_ALPHABET, 4) + [b"ab 1_\n", b"a\r\na", b"a\n\r_", b"Za -a\r"]
+    for t in texts:
+        assert d.full_match(t) == bool(rx.fullmatch(t)), (pat, t)
+
+
+def test_look_around_known_answers():
+    # (?mR): '\r' and '\n' both end lines, and ^ / $ never match between "\r\n"
+    d = G.HostDfa(r"(?mR)a$\r\n^b")
+    assert d.full_match("a\r\nb")
+    assert not G.HostDfa(r"(?mR)a\r^\nb").full_match("a\r\nb")
+    assert not G.HostDfa(r"(?mR)a\r$\nb").full_match("a\r\nb")
+    assert G.HostDfa(r"(?mR)a\r^b").full_match("a\rb")
+    assert G.HostDfa(r"(?m)a\r^\nb").full_match("a\r\nb") is False      # (?m) alone: only '\n' starts a line
+    assert G.HostDfa(r"(?m)a\n^\nb").full_match("a\n\nb")
+    # without (?m), ^ $ are \A \z
+    assert not G.HostDfa(r"a\n^b").full_match("a\nb")
+    assert not G.HostDfa(r"a$\nb").full_match("a\nb")
+    # ASCII word boundaries: bytes above 0x7F are not word bytes
+    assert G.HostDfa(r"(?-u:\b)é").full_match("é") is False
+    assert G.HostDfa(r"a(?-u:\b)é").full_match("aé")
+    assert G.HostDfa(r"(?-u:\B)").full_match("") and not G.HostDfa(r"(?-u:\b)").full_match("")
+    # the masks see the assertions: after "a", "b" may not follow a \b
+    d = G.HostDfa(r"(?-u)a\b[a-z ]*")
+    s = d.walk(d.start, b"a")
+    assert d.walk(s, b"b") is None and d.walk(s, b" ") is not None
+
+
+def test_unicode_mode_off():
+    d = G.HostDfa(r"(?-u)\w+")
+    assert d.full_match("ab_9") and not d.full_match("é")
+    assert G.HostDfa(r"(?-u)\d").full_match("5") and not G.HostDfa(r"(?-u)\d").full_match("٣")
+    assert G.HostDfa(r"(?-u)\s").full_match("\x0b") and not G.HostDfa(r"(?-u)\s").full_match("\u3000")
+    d = G.HostDfa(r"(?i-u)k")
+    assert d.full_match("k") and d.full_match("K") and not d.full_match("\u212a")
+    d = G.HostDfa(r"(?i)k(?-u:k)")
+    assert d.full_match("\u212ak") and not d.full_match("k\u212a")
+    assert G.HostDfa(r"(?-u)é\x{e9}\u00e9").full_match("ééé")   # literals outside classes stay scalars
+    assert G.HostDfa(r"(?-u)(?u:.)").full_match("é")
+    assert G.HostDfa(r"(?-u:[[:^alpha:]&&[0-9]])").full_match("5")
+
+
+@pytest.mark.parametrize("bad", [
+    r"\b", r"\B", r"\<", r"\>", r"\b{start}", r"(?-u:\b{foo})", r"(?-u:\b{start)",   # Unicode boundaries, bad names
+    r"(?-u).", r"(?s-u).", r"(?-u)\W", r"(?-u)\D", r"(?-u)[^a]", r"(?-u)[\S]", r"(?-u)\xFF", r"(?-u)[\x80]",
+    r"(?-u)[é]", r"(?-u)\pL", r"(?-u:[[:^alpha:]])", r"(?-u)[[^a]&&b]", r"[\b]",
+])
+def test_look_and_byte_mode_errors(bad):
+    with pytest.raises(G.GrammarError):
+        G.HostDfa(bad)
+
+
+# ------------------------------------------------------------ class set operations
+# [A&&B] [A--B] [A~~B]: equal precedence, left to right, looser than union;
+# negation applies to the result. Expected sets come from Python set
+# arithmetic over the single-scalar languages of the operands.
+_SET_UNIVERSE = [chr(c) for c in list(range(0x20, 0x250)) + [0x391, 0x3B1, 0x3C3, 0x3C2, 0x410, 0x430, 0x212A,
+                                                              0x17F, 0x660, 0x966, 0x3000]]
+
+
+def _lang(pat):
+    d = G.HostDfa(pat)
+    return {c for c in _SET_UNIVERSE if d.full_match(c)}
+
+
+@pytest.mark.parametrize("a,op,b", [
+    (r"\w", "&&", r"\d"), (r"\p{L}", "--", r"[a-z]"), (r"[a-g]", "~~", r"[c-z]"), (r"\pL", "&&", r"\p{Lu}"),
+    (r"[\x20-\x7e]", "--", r"\w"), (r"\s", "~~", r"[\t-\r]"), (r"[^a-z]", "&&", r"[\x20-\x7a]"),
+])
+def test_class_set_operations(a, op, b):
+    A, B = _lang(a), _lang(b)
+    want = {"&&": A & B, "--": A - B, "~~": A ^ B}[op]
+    assert _lang("[" + a + op + b + "]") == want
+    assert _lang("[^" + a + op + b + "]") == set(_SET_UNIVERSE) - want
+
+
+def test_class_set_operation_precedence():
+    # union binds tighter: [ab&&bc] == [[ab]&&[bc]]; operators go left to right
+    assert _lang(r"[ab&&bc]") == {"b"}
+    assert _lang(r"[a-z--b&&c-e]") == {"c", "d", "e"}
+    assert _lang(r"[a-z&&c-e--d]") == {"c", "e"}
+    assert _lang(r"[a-c~~b-d~~c]") == {"a", "c", "d"}
+    assert _lang(r"[[a-c]--[b]]") == {"a", "c"}
+    assert _lang(r"[a-]") == {"a", "-"}
+    # case folding applies to each operand before the operation
+    assert _lang(r"(?i)[a-z--k]") == _lang(r"(?i)[a-jl-z]")
+    assert "\u212a" not in _lang(r"(?i)[a-z--k]") and "\u017f" in _lang(r"(?i)[a-z--k]")

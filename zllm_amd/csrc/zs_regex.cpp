@@ -12,20 +12,34 @@
 //
 // Syntax (the regex-syntax subset that patterns reach here): literals (UTF-8),
 // escapes of punctuation, \t \n \r \f \v \a, \xHH \x{H..} \uHHHH \u{H..}
-// \UHHHHHHHH, classes [..] with ranges, negation, nested classes and ASCII
-// POSIX names, '.', groups ( ), (?: ), (?P<n> ), (?<n> ), flags
-// (?imsxU-imsxU) and (?flags: ), alternation, * + ? {n} {n,} {n,m} with lazy
-// forms (same language), and the anchors ^ $ \A \z. Unicode mode, as
-// regex-syntax's default: \d is \p{Nd}, \s is White_Space, \w is
-// [\p{Alphabetic}\p{M}\p{Nd}\p{Pc}\p{Join_Control}] (UTS #18 Annex C),
-// \p{..} / \P{..} take general categories (short or long names, one-letter
-// groups, gc= forms) and Any / ASCII / Assigned, and case-insensitive mode
-// uses simple case folding. The tables (zs_unicode.h) are generated from
-// Python's unicodedata (Unicode 13.0 in this image; regex-syntax 0.8.10 has
-// 16.0: scalars assigned after 13.0 are outside \w \d \p{..} here). Refused
-// with an error, as regex-syntax would accept them: word boundaries \b \B,
-// script and binary properties other than the above (\p{Greek}), class set
-// operations (&& -- ~~), multi-line anchors.
+// \UHHHHHHHH, classes [..] with ranges, negation, nested classes, ASCII
+// POSIX names and the set operations && -- ~~ (equal precedence, left to
+// right, binding looser than union), '.', groups ( ), (?: ), (?P<n> ),
+// (?<n> ), flags (?imsxuUR-imsxuUR) and (?flags: ), alternation, * + ? {n}
+// {n,} {n,m} with lazy forms (same language), the anchors ^ $ \A \z, with
+// (?m) the line anchors ^ $ (after / before '\n'; with (?mR) '\r' and '\n'
+// both end lines and ^ $ never match between "\r\n"), and the ASCII word
+// boundaries \b \B \< \> \b{start} \b{end} \b{start-half} \b{end-half}
+// under (?-u). Unicode mode, as regex-syntax's default: \d is \p{Nd}, \s is
+// White_Space, \w is [\p{Alphabetic}\p{M}\p{Nd}\p{Pc}\p{Join_Control}]
+// (UTS #18 Annex C), \p{..} / \P{..} take general categories (short or long
+// names, one-letter groups, gc= forms) and Any / ASCII / Assigned, and
+// case-insensitive mode uses simple case folding. The tables (zs_unicode.h)
+// are generated from Python's unicodedata (Unicode 13.0 in this image;
+// regex-syntax 0.8.10 has 16.0: scalars assigned after 13.0 are outside \w
+// \d \p{..} here). (?-u) makes \d \s \w ASCII and case folding ASCII-only,
+// and, as regex-syntax does with UTF-8 mode on, refuses what could match
+// bytes that are not UTF-8 ('.', negated byte classes, \x80-\xFF) and
+// non-ASCII class members. Errors as in regex-automata's dense DFA builder:
+// Unicode word boundaries (\b and friends without (?-u)). Refused with an
+// error although regex-syntax accepts them: script and binary properties
+// other than the above (\p{Greek}).
+//
+// Look-around (anchors, line anchors, word boundaries) is resolved during
+// subset construction: a DFA state is a set of NFA states plus the class of
+// the byte before the position (start of text, ASCII word byte, '\n', '\r',
+// other). Assertions in a set stay pending until the next byte, or the end of
+// the text, is known; then each holds or fails from (previous, next).
 #include <stdint.h>
 #include <string.h>
 #include <algorithm>
@@ -99,10 +113,58 @@ struct CpSet {
             canon();
         }
     }
+    // ASCII-only case folding (regex-syntax's byte classes)
+    void fold_ascii() {
+        canon();
+        std::vector<std::pair<uint32_t, uint32_t>> extra;
+        for (auto& x : r) {
+            const uint32_t lo = x.first, hi = std::min(x.second, 0x7Fu);
+            if (lo > hi) continue;
+            const uint32_t a = std::max(lo, (uint32_t)'a'), b = std::min(hi, (uint32_t)'z');
+            if (a <= b) extra.push_back({a - 32, b - 32});
+            const uint32_t A = std::max(lo, (uint32_t)'A'), B = std::min(hi, (uint32_t)'Z');
+            if (A <= B) extra.push_back({A + 32, B + 32});
+        }
+        r.insert(r.end(), extra.begin(), extra.end());
+        canon();
+    }
+    bool is_ascii() const {
+        for (auto& x : r) if (x.second > 0x7F) return false;
+        return true;
+    }
+    // set operations of classes (canonical operands)
+    static CpSet meet(const CpSet& a, const CpSet& b) {
+        CpSet o;
+        size_t i = 0, j = 0;
+        while (i < a.r.size() && j < b.r.size()) {
+            const uint32_t lo = std::max(a.r[i].first, b.r[j].first), hi = std::min(a.r[i].second, b.r[j].second);
+            if (lo <= hi) o.add(lo, hi);
+            if (a.r[i].second < b.r[j].second) i++;
+            else j++;
+        }
+        return o;
+    }
+    static CpSet minus(const CpSet& a, const CpSet& b) {
+        CpSet nb = b;
+        nb.negate();
+        return meet(a, nb);
+    }
+    static CpSet symdiff(const CpSet& a, const CpSet& b) {
+        CpSet o = minus(a, b);
+        o.add(minus(b, a));
+        o.canon();
+        return o;
+    }
 };
 
 // ------------------------------------------------------------ syntax tree
-enum Kind { K_EMPTY, K_CLASS, K_CAT, K_ALT, K_REP, K_START, K_END };
+enum Kind { K_EMPTY, K_CLASS, K_CAT, K_ALT, K_REP, K_LOOK };
+
+// zero-width assertions (K_LOOK's mn, N_LOOK's lo)
+enum Look : uint8_t {
+    L_TEXT_START, L_TEXT_END, L_LF_START, L_LF_END, L_CRLF_START, L_CRLF_END,
+    L_WORD, L_NOT_WORD, L_WORD_START, L_WORD_END, L_WORD_START_HALF, L_WORD_END_HALF
+};
 struct Node {
     Kind k;
     CpSet set;
@@ -111,7 +173,7 @@ struct Node {
 };
 
 struct Flags {
-    bool i = false, s = false, x = false, m = false;
+    bool i = false, s = false, x = false, m = false, u = true, R = false;
 };
 
 struct ParseError {
@@ -251,7 +313,10 @@ private:
     }
 
     int class_node(CpSet s, const Flags& f) {
-        if (f.i) s.fold();
+        if (f.i) {
+            if (f.u) s.fold();
+            else s.fold_ascii();
+        }
         s.remove_surrogates();
         s.canon();
         int n = node(K_CLASS);
@@ -274,10 +339,8 @@ private:
                 case 'x': f.x = !neg; break;
                 case 'm': f.m = !neg; break;
                 case 'U': break;  // swaps greediness: same language
-                case 'u':
-                    if (neg) fail("Unicode mode cannot be disabled here");
-                    break;
-                case 'R': break;
+                case 'u': f.u = !neg; break;
+                case 'R': f.R = !neg; break;
                 default: fail("unrecognized flag");
             }
         }
@@ -319,6 +382,7 @@ private:
         if (c == ')') fail("unopened group");
         if (c == '[') return class_node(parse_class(f), Flags{});  // folded inside
         if (c == '.') {
+            if (!f.u) fail("pattern can match invalid UTF-8");
             pos_++;
             CpSet s;
             if (f.s) s.add(0, CP_MAX);
@@ -326,9 +390,11 @@ private:
             return class_node(s, Flags{});
         }
         if (c == '^' || c == '$') {
-            if (f.m) fail("multi-line anchors are not supported");
             pos_++;
-            return node(c == '^' ? K_START : K_END);
+            const bool st = c == '^';
+            if (!f.m) return look(st ? L_TEXT_START : L_TEXT_END);
+            if (f.R) return look(st ? L_CRLF_START : L_CRLF_END);
+            return look(st ? L_LF_START : L_LF_END);
         }
         if (c == '\\') {
             pos_++;
@@ -336,11 +402,12 @@ private:
             const char e = peek();
             if (e == 'A' || e == 'z') {
                 pos_++;
-                return node(e == 'A' ? K_START : K_END);
+                return look(e == 'A' ? L_TEXT_START : L_TEXT_END);
             }
+            if (e == 'b' || e == 'B' || e == '<' || e == '>') return word_boundary(f);
             CpSet s;
-            if (perl_class(s)) return class_node(s, f);
-            const uint32_t cp = escape_cp();
+            if (perl_class(s, f.u)) return class_node(s, f);
+            const uint32_t cp = escape_cp(f.u);
             s.add(cp, cp);
             return class_node(s, f);
         }
@@ -348,6 +415,36 @@ private:
         uint32_t cp = next_cp();
         s.add(cp, cp);
         return class_node(s, f);
+    }
+
+    int look(Look l) {
+        const int n = node(K_LOOK);
+        ar_[n].mn = l;
+        return n;
+    }
+
+    // \b \B \< \> \b{start} \b{end} \b{start-half} \b{end-half}; pos_ at
+    // the letter. "\b{" followed by a non-letter is \b and a repetition.
+    int word_boundary(const Flags& f) {
+        const char e = peek();
+        pos_++;
+        Look l = e == 'B' ? L_NOT_WORD : e == '<' ? L_WORD_START : e == '>' ? L_WORD_END : L_WORD;
+        auto name_char = [](char c) { return (c >= 'a' && c <= 'z') || (c >= 'A' && c <= 'Z') || c == '-'; };
+        if (e == 'b' && pos_ + 1 < p_.size() && p_[pos_] == '{' && name_char(p_[pos_ + 1])) {
+            size_t q = pos_ + 1;
+            while (q < p_.size() && name_char(p_[q])) q++;
+            if (q >= p_.size() || p_[q] != '}') fail("unclosed special word boundary");
+            const std::string name = p_.substr(pos_ + 1, q - pos_ - 1);
+            if (name == "start") l = L_WORD_START;
+            else if (name == "end") l = L_WORD_END;
+            else if (name == "start-half") l = L_WORD_START_HALF;
+            else if (name == "end-half") l = L_WORD_END_HALF;
+            else fail("unrecognized special word boundary");
+            pos_ = q + 1;
+        }
+        if (f.u)
+            fail("Unicode word boundaries cannot be built into a DFA (use an ASCII one, such as (?-u:\\b))");
+        return look(l);
     }
 
     uint32_t hex_digits(int n_fixed) {
@@ -377,9 +474,16 @@ private:
     }
 
     // the scalar denoted by an escape (pos_ at the character after '\')
-    uint32_t escape_cp() {
+    // (byte mode: \xHH above 0x7F is a byte, which regex-syntax refuses in
+    // UTF-8 mode; \x{..}, \u and \U always denote scalars)
+    uint32_t escape_cp(bool u) {
         const char e = peek();
         pos_++;
+        if (e == 'x' && !u && (eof() || peek() != '{')) {
+            const uint32_t v = hex_digits(2);
+            if (v > 0x7F) fail("pattern can match invalid UTF-8");
+            return v;
+        }
         switch (e) {
             case 'n': return '\n';
             case 't': return '\t';
@@ -392,11 +496,11 @@ private:
             case 'U': return hex_digits(8);
             default: break;
         }
-        const unsigned char u = (unsigned char)e;
-        if (u < 0x80 && !((e >= '0' && e <= '9') || (e >= 'a' && e <= 'z') || (e >= 'A' && e <= 'Z')))
-            return u;  // escaped punctuation or space
+        const unsigned char ue = (unsigned char)e;
+        if (ue < 0x80 && !((e >= '0' && e <= '9') || (e >= 'a' && e <= 'z') || (e >= 'A' && e <= 'Z')))
+            return ue;  // escaped punctuation or space
         pos_--;
-        if (e == 'b' || e == 'B' || e == '<' || e == '>') fail("word boundary assertions are not supported");
+        if (e == 'b' || e == 'B' || e == '<' || e == '>') fail("word boundary assertions are not allowed in classes");
         if (e >= '0' && e <= '9') fail("backreferences are not supported");
         fail("unrecognized escape sequence");
     }
@@ -434,14 +538,26 @@ private:
         s.add(0x1F170, 0x1F189);
     }
 
-    // \d \D \s \S \w \W \p{..} \P{..} (Unicode); pos_ at the letter
-    bool perl_class(CpSet& s) {
+    // \d \D \s \S \w \W \p{..} \P{..}; pos_ at the letter. Byte mode
+    // (u false): ASCII \d \s \w, whose negations match bytes above 0x7F
+    // and are refused; \p is refused.
+    bool perl_class(CpSet& s, bool u) {
         const char e = peek();
         CpSet b;
+        if (!u && (e == 'd' || e == 'D' || e == 's' || e == 'S' || e == 'w' || e == 'W')) {
+            if (e == 'D' || e == 'S' || e == 'W') fail("pattern can match invalid UTF-8");
+            if (e == 'd') b.add('0', '9');
+            else if (e == 's') { b.add('\t', '\r'); b.add(' ', ' '); }
+            else { b.add('0', '9'); b.add('A', 'Z'); b.add('_', '_'); b.add('a', 'z'); }
+            pos_++;
+            s.add(b);
+            return true;
+        }
         if (e == 'd' || e == 'D') add_cats(b, cats({"Nd"}));
         else if (e == 's' || e == 'S') add_white_space(b);
         else if (e == 'w' || e == 'W') add_word(b);
         else if (e == 'p' || e == 'P') {
+            if (!u) fail("Unicode classes are not allowed when Unicode mode is disabled");
             pos_++;
             std::string name;
             if (!eof() && peek() == '{') {
@@ -559,29 +675,53 @@ private:
     }
 
     // one class member that is a single scalar (for ranges); -1 if not
-    int64_t class_char(CpSet& into, bool* was_set) {
+    int64_t class_char(CpSet& into, bool* was_set, bool u) {
         *was_set = false;
+        uint32_t cp;
         if (peek() == '\\') {
             pos_++;
             if (eof()) fail("incomplete escape sequence");
             CpSet s;
-            if (perl_class(s)) {
+            if (perl_class(s, u)) {
                 into.add(s);
                 *was_set = true;
                 return -1;
             }
-            return escape_cp();
+            cp = escape_cp(u);
+        } else {
+            cp = next_cp();
         }
-        return next_cp();
+        if (!u && cp > 0x7F) fail("Unicode not allowed here (a class with Unicode mode disabled)");
+        return cp;
     }
 
+    // fold the operands of a set operation, as regex-syntax does before it
+    // applies the operation (and again to the result)
+    static void fold_by(CpSet& s, const Flags& f) {
+        if (!f.i) return;
+        if (f.u) s.fold();
+        else s.fold_ascii();
+    }
+
+    // [..]: unions of items, joined left to right by && -- ~~, then the
+    // negation; byte mode refuses a class (nested ones included) that ends up
+    // with members above 0x7F
     CpSet parse_class(const Flags& f) {
         const size_t open = pos_;
         pos_++;  // '['
         bool neg = false;
         if (!eof() && peek() == '^') { pos_++; neg = true; }
-        CpSet s;
+        CpSet acc, s;
+        char op = 0;
         bool first = true;
+        auto apply = [&]() {
+            if (!op) { acc = s; return; }
+            fold_by(acc, f);
+            fold_by(s, f);
+            acc.canon();
+            s.canon();
+            acc = op == '&' ? CpSet::meet(acc, s) : op == '-' ? CpSet::minus(acc, s) : CpSet::symdiff(acc, s);
+        };
         for (;;) {
             if (eof()) { pos_ = open; fail("unclosed character class"); }
             const char c = peek();
@@ -594,16 +734,21 @@ private:
                 continue;
             }
             if ((c == '&' || c == '-' || c == '~') && pos_ + 1 < p_.size() && p_[pos_ + 1] == c &&
-                !(c == '-' && pos_ + 2 < p_.size() && p_[pos_ + 2] == ']'))
-                fail("character class set operations are not supported");
+                !(c == '-' && pos_ + 2 < p_.size() && p_[pos_ + 2] == ']')) {
+                apply();
+                op = c;
+                s = CpSet{};
+                pos_ += 2;
+                continue;
+            }
             bool was_set;
-            int64_t lo = class_char(s, &was_set);
+            int64_t lo = class_char(s, &was_set, f.u);
             if (was_set) continue;
             if (!eof() && peek() == '-' && pos_ + 1 < p_.size() && p_[pos_ + 1] != ']') {
                 pos_++;
                 bool ws2;
                 CpSet dummy;
-                int64_t hi = class_char(dummy, &ws2);
+                int64_t hi = class_char(dummy, &ws2, f.u);
                 if (ws2) fail("invalid character class range");
                 if (hi < lo) fail("invalid character class range");
                 s.add((uint32_t)lo, (uint32_t)hi);
@@ -611,14 +756,17 @@ private:
                 s.add((uint32_t)lo, (uint32_t)lo);
             }
         }
-        if (f.i) s.fold();
-        if (neg) s.negate();
-        return s;
+        apply();
+        fold_by(acc, f);
+        if (neg) acc.negate();
+        acc.canon();
+        if (!f.u && (neg || !acc.is_ascii())) { pos_ = open; fail("pattern can match invalid UTF-8"); }
+        return acc;
     }
 };
 
 // ------------------------------------------------------------ Thompson NFA
-enum NKind : uint8_t { N_BYTE, N_SPLIT, N_EPS, N_MATCH, N_START, N_END };
+enum NKind : uint8_t { N_BYTE, N_SPLIT, N_EPS, N_MATCH, N_LOOK };  // N_LOOK: assertion lo, then a
 struct NState {
     NKind k;
     uint8_t lo, hi;
@@ -640,8 +788,7 @@ public:
         const Node& nd = ar[n];
         switch (nd.k) {
             case K_EMPTY: return next;
-            case K_START: return add(N_START, next);
-            case K_END: return add(N_END, next);
+            case K_LOOK: return add(N_LOOK, next, 0, (uint8_t)nd.mn);
             case K_CLASS: return cls(nd.set, next);
             case K_CAT: {
                 uint32_t s = next;
@@ -732,16 +879,50 @@ struct VecHash {
     }
 };
 
+// class of the byte before a position, as far as the assertions can tell
+enum Ctx : uint32_t { C_START, C_WORD, C_LF, C_CR, C_OTHER };
+inline bool word_byte(int b) {
+    return (b >= '0' && b <= '9') || (b >= 'A' && b <= 'Z') || b == '_' || (b >= 'a' && b <= 'z');
+}
+inline uint32_t ctx_of(int b) { return word_byte(b) ? C_WORD : b == '\n' ? C_LF : b == '\r' ? C_CR : C_OTHER; }
+// does assertion l hold between prev and next (a byte, or -1 at the end)?
+// (regex-automata's Look semantics; CRLF lines never split "\r\n")
+inline bool look_holds(uint8_t l, uint32_t prev, int next) {
+    const bool wp = prev == C_WORD, wn = next >= 0 && word_byte(next);
+    switch (l) {
+        case L_TEXT_START: return prev == C_START;
+        case L_TEXT_END: return next < 0;
+        case L_LF_START: return prev == C_START || prev == C_LF;
+        case L_LF_END: return next < 0 || next == '\n';
+        case L_CRLF_START: return prev == C_START || prev == C_LF || (prev == C_CR && next != '\n');
+        case L_CRLF_END: return next < 0 || next == '\r' || (next == '\n' && prev != C_CR);
+        case L_WORD: return wp != wn;
+        case L_NOT_WORD: return wp == wn;
+        case L_WORD_START: return !wp && wn;
+        case L_WORD_END: return wp && !wn;
+        case L_WORD_START_HALF: return !wp;
+        case L_WORD_END_HALF: return !wn;
+        default: return false;
+    }
+}
+
 class Determinizer {
 public:
     Determinizer(const std::vector<NState>& n, uint32_t start, size_t limit_bytes)
         : n_(n), start_(start), limit_(limit_bytes), mark_(n.size(), 0) {}
 
     bool run(zs_host_dfa& out, std::string& err) {
-        // byte equivalence classes from the NFA's byte ranges
+        // byte equivalence classes from the NFA's byte ranges (and, with
+        // assertions, the bytes they tell apart)
         std::vector<uint8_t> cut(257, 0);
-        for (auto& s : n_)
+        bool looks = false;
+        for (auto& s : n_) {
             if (s.k == N_BYTE && s.lo <= s.hi) { cut[s.lo] = 1; cut[(size_t)s.hi + 1] = 1; }
+            if (s.k == N_LOOK) looks = true;
+        }
+        if (looks)
+            for (int b : {(int)'0', '9' + 1, (int)'A', 'Z' + 1, (int)'_', '_' + 1, (int)'a', 'z' + 1, (int)'\n', '\n' + 1, (int)'\r', '\r' + 1})
+                cut[b] = 1;
         uint8_t cls_of[256];
         int nc = 0;
         for (int b = 0; b < 256; b++) {
@@ -755,38 +936,42 @@ public:
         while (stride < (size_t)nc + 1) stride <<= 1;
         const size_t max_states = limit_ / (stride * 4);
 
+        // key: the sorted NFA set, then (when it holds pending assertions)
+        // a marker word with the previous-byte context
         std::unordered_map<std::vector<uint32_t>, uint32_t, VecHash> ids;
         std::vector<std::vector<uint32_t>> sets;
+        std::vector<uint32_t> ctxs;
         std::vector<uint8_t> acc;
         std::vector<uint32_t> tr;  // [state][class]
-        auto intern = [&](std::vector<uint32_t>&& v, bool force_new) -> int64_t {
-            if (!force_new) {
-                auto it = ids.find(v);
-                if (it != ids.end()) return it->second;
-            }
+        auto intern = [&](std::vector<uint32_t>&& v, uint32_t ctx) -> int64_t {
+            bool pend = false;
+            for (uint32_t q : v) pend |= n_[q].k == N_LOOK;
+            if (!pend) ctx = C_OTHER;
+            std::vector<uint32_t> key = v;
+            if (pend) key.push_back(0xFFFFFF00u | ctx);
+            auto it = ids.find(key);
+            if (it != ids.end()) return it->second;
             if (sets.size() >= max_states) return -1;
             uint32_t id = (uint32_t)sets.size();
-            acc.push_back(accepting(v, force_new) ? 1 : 0);
-            if (!force_new) ids.emplace(v, id);
+            acc.push_back(accepting(v, ctx) ? 1 : 0);
+            ids.emplace(std::move(key), id);
             sets.push_back(std::move(v));
+            ctxs.push_back(ctx);
             return id;
         };
-        intern(std::vector<uint32_t>{}, false);  // 0: dead (empty set)
+        intern(std::vector<uint32_t>{}, C_OTHER);  // 0: dead (empty set)
         std::vector<uint32_t> s0;
-        closure({start_}, true, s0);
-        intern(std::move(s0), true);  // 1: start (its closure may pass ^)
+        closure({start_}, s0);
+        intern(std::move(s0), C_START);  // 1: start (a non-empty set)
         for (size_t i = 0; i < sets.size(); i++) {
             tr.resize(sets.size() * nc, 0);
             for (int c = 0; c < nc; c++) {
                 const uint8_t b = rep[c];
                 std::vector<uint32_t> tgt;
-                for (uint32_t q : sets[i]) {
-                    const NState& s = n_[q];
-                    if (s.k == N_BYTE && s.lo <= b && b <= s.hi) tgt.push_back(s.a);
-                }
+                step(sets[i], ctxs[i], b, tgt);
                 std::vector<uint32_t> cl;
-                if (!tgt.empty()) closure(tgt, false, cl);
-                int64_t id = intern(std::move(cl), false);
+                if (!tgt.empty()) closure(tgt, cl);
+                int64_t id = intern(std::move(cl), ctx_of(b));
                 if (id < 0) {
                     err = "DFA exceeded the size limit (" + std::to_string(limit_) + " bytes)";
                     return false;
@@ -806,8 +991,9 @@ private:
     std::vector<uint32_t> mark_;
     uint32_t epoch_ = 0;
 
-    // states reachable by empty moves; keeps byte, match and end-anchor states
-    void closure(const std::vector<uint32_t>& from, bool at_start, std::vector<uint32_t>& out) {
+    // states reachable by empty moves; keeps byte, match and (pending)
+    // assertion states
+    void closure(const std::vector<uint32_t>& from, std::vector<uint32_t>& out) {
         epoch_++;
         std::vector<uint32_t> stack(from.rbegin(), from.rend());
         while (!stack.empty()) {
@@ -817,16 +1003,35 @@ private:
             mark_[q] = epoch_;
             const NState& s = n_[q];
             switch (s.k) {
-                case N_BYTE: case N_MATCH: case N_END: out.push_back(q); break;
+                case N_BYTE: case N_MATCH: case N_LOOK: out.push_back(q); break;
                 case N_EPS: stack.push_back(s.a); break;
                 case N_SPLIT: stack.push_back(s.b); stack.push_back(s.a); break;
-                case N_START: if (at_start) stack.push_back(s.a); break;
             }
         }
         std::sort(out.begin(), out.end());
     }
+    // the NFA states after byte b from this set, whose previous byte was of
+    // class prev: assertions are resolved with (prev, b) on the way
+    void step(const std::vector<uint32_t>& set, uint32_t prev, uint8_t b, std::vector<uint32_t>& tgt) {
+        epoch_++;
+        std::vector<uint32_t> stack(set.rbegin(), set.rend());
+        while (!stack.empty()) {
+            uint32_t q = stack.back();
+            stack.pop_back();
+            if (mark_[q] == epoch_) continue;
+            mark_[q] = epoch_;
+            const NState& s = n_[q];
+            switch (s.k) {
+                case N_BYTE: if (s.lo <= b && b <= s.hi) tgt.push_back(s.a); break;
+                case N_LOOK: if (look_holds(s.lo, prev, b)) stack.push_back(s.a); break;
+                case N_EPS: stack.push_back(s.a); break;
+                case N_SPLIT: stack.push_back(s.b); stack.push_back(s.a); break;
+                default: break;
+            }
+        }
+    }
     // a match is reached at the end of the text from this set
-    bool accepting(const std::vector<uint32_t>& set, bool at_start) {
+    bool accepting(const std::vector<uint32_t>& set, uint32_t prev) {
         epoch_++;
         std::vector<uint32_t> stack(set.begin(), set.end());
         while (!stack.empty()) {
@@ -837,9 +1042,9 @@ private:
             const NState& s = n_[q];
             switch (s.k) {
                 case N_MATCH: return true;
-                case N_END: case N_EPS: stack.push_back(s.a); break;
+                case N_LOOK: if (look_holds(s.lo, prev, -1)) stack.push_back(s.a); break;
+                case N_EPS: stack.push_back(s.a); break;
                 case N_SPLIT: stack.push_back(s.b); stack.push_back(s.a); break;
-                case N_START: if (at_start) stack.push_back(s.a); break;
                 default: break;
             }
         }
