@@ -88,14 +88,15 @@ struct zs_row_state {
     float samp_S;         // sampler softmax denominator (sampler.rs:68) when computed by the rounds
     float obs_S;          // sequential f32 sum (hallucination.rs:134-135, logprobs.rs:36)
     float obs_H;          // sequential f32 entropy (hallucination.rs:139-144)
-    // big rows with a top-p cut: the kept set compacted in index order (zs_k_big)
-    // whose sum and draw run as parallel rounds (zs_k_roundK / zs_k_stitchK)
+    // big rows: the kept set (top-p cut, or every positive p1) compacted in index
+    // order, whose sum and draw run as parallel rounds (zs_k_roundK / zs_k_stitchK)
     uint32_t klist;       // 1: list ready
     uint32_t nk;          // list length
     uint32_t vstar, istar;  // kept: p > v*, or p == v* and id <= i*
     uint32_t kpend;       // 1: the kept list is compacted by zs_k_kcount / zs_k_kwrite
     uint32_t krank;       // rank of the top-p stop among the values equal to v*
     uint32_t kminp;       // min-p applies: p1 = p < kcut ? 0 : p / kkept
+    uint32_t knorm;       // 1: the draw runs on p1 / sum2 (top-p renormalisation); 0: on p1 (no sum2)
     float kcut, kkept;
     float sum2;           // sequential sum of the kept set (sampler.rs:107)
     uint32_t n_cand;      // observer candidates by (x~ desc, id asc)

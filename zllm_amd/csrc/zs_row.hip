@@ -1302,6 +1302,7 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
         st.z_is_x = reuse ? 1u : 0u;
         st.klist = 0;
         st.kpend = 0;
+        st.knorm = 0;
         st.samp_S = -0.0f;
         st.obs_S = -0.0f;
         st.obs_H = 0.0f;

@@ -13,7 +13,7 @@
 //                 entropy, and the sampler's S of the remaining ("big") rows.
 //   zs_k_pv .. zs_k_tp_sort   big rows: survivor values and the top-p bucket plan.
 //   zs_k_big      one 1024-thread workgroup per big row: exact emulation of the
-//                 reference's sequential f32 sums (min-p, top-p, draw).
+//                 reference's sequential f32 sums (min-p, top-p walk).
 //   zs_k_kcount, zs_k_kwrite, zs_k_roundK, zs_k_stitchK   the kept list's sums.
 //   zs_k_final    chosen-token outputs.
 //
@@ -88,7 +88,7 @@ __device__ __forceinline__ big_raw big_fetch(const big_row& R, uint32_t g) {
 }
 // x~ (observers: mask and bans) and z (sampler: patched y, divided by T) of the
 // 4 elements idx0..idx0+3 of group g; the group's patches are those of its
-// ZS_BIG_G / ZS_SUB sub-chunks (per-sub-chunk patch offsets from zs_k_prep).
+// ZS_BIG_G / ZS_SUB sub-chunks (per-sub-chunk patch offsets written by zs_k_row).
 __device__ __forceinline__ void big_finish(const big_row& R, uint32_t g, const big_raw& raw, float (&x)[4],
                                            float (&z)[4]) {
     const uint32_t idx0 = g * ZS_BIG_G + 4 * threadIdx.x;
@@ -1078,8 +1078,6 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
 
     // ---- top-p (sampler.rs:91-115)
     const bool topp = P.top_p < 1.0f && P.top_p > 0.0f;
-    uint32_t vstar = 0, istar = 0xffffffffu;  // kept: p1 > v* or (p1 == v* and idx <= i*)
-    float sum2 = 0.0f;
     if (topp) {
         uint32_t* gv = a.pairs + (size_t)r * a.max_vocab * 2;  // level-0 layout
         uint32_t* tmp = gv + a.max_vocab;                       // level-1 refinement
@@ -1207,53 +1205,31 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
                 o.kcut = cut;
                 o.kkept = kept;
                 o.kpend = 1;
+                o.knorm = 1;
             }
             return;
-        } else {
-            // every positive p kept: sum over the whole row
-            vstar = 0;
-            istar = 0xffffffffu;
-            sum2 = -0.0f;
-            stream_p1([&](uint32_t, const float (&p)[4]) {
-                seq_group<ZS_BIG_NT, 4>(p, 0, sum2, NAN, sh.q);
-                return false;
-            });
         }
     }
-    // ---- draw (sampler.rs:118-127)
-    const float rr = zs_philox_uniform(b.d_seed[r], b.d_counter[r], 0u);
-    uint32_t token = V - 1;
-    if (rr <= 0.0f) {
-        token = 0;
-    } else {
-        float cum = 0.0f;
-        const bool renorm = topp && sum2 > 0.0f;
-        stream_p1([&](uint32_t g, const float (&p)[4]) {
-            float tv[4];
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                float pp = p[q];
-                if (renorm) {
-                    const uint32_t pb = zs_f2u(pp), idx = g * ZS_BIG_G + 4 * t + q;
-                    const bool keep = pb > vstar || (pb == vstar && idx <= istar);
-                    pp = keep ? pp / sum2 : 0.0f;
-                }
-                tv[q] = pp;
-            }
-            int stp = seq_group<ZS_BIG_NT, 4>(tv, 0, cum, rr, sh.q);
-            if (stp >= 0) { token = g * ZS_BIG_G + stp; return true; }
-            return false;
-        });
-    }
+    // ---- every positive p1 kept (no top-p, or a walk that never stopped): the
+    // kept list is every positive p1 in index order (v* = 0: no value equals
+    // it), with sum2 and the renormalised draw after a top-p walk, else the
+    // draw on p1 itself (sampler.rs:118-127), as rounds over all CUs
     if (t == 0) {
-        a.rst[r].token = token;
-        a.rst[r].mode = ZS_MODE_DONE;
+        zs_row_state& o = a.rst[r];
+        o.vstar = 0u;
+        o.krank = 0u;
+        o.istar = 0xffffffffu;
+        o.kminp = minp ? 1u : 0u;
+        o.kcut = cut;
+        o.kkept = kept;
+        o.kpend = 1;
+        o.knorm = topp ? 1u : 0u;
     }
 }
 
 // ===========================================================================
-// Compaction of the kept set {p1 >= v*} in index order (rows with a top-p
-// stop), over all CUs: zs_k_kcount counts per 4096-id group the values above
+// Compaction of the kept set {p1 >= v*} in index order (every big row that
+// reaches the draw; v* = 0 keeps every positive p1), over all CUs: zs_k_kcount counts per 4096-id group the values above
 // and equal to v*; zs_k_kwrite places each group's elements after the groups
 // before it, finds i* (the (rank+1)-th element equal to v*) and adds the
 // approximate sums of the kept list per 1024-entry sub-chunk (the predictions
@@ -1377,7 +1353,7 @@ struct klist_row {
     const uint32_t* kp;
     const uint32_t* ki;
     uint32_t nk, vstar, istar;
-    float inv;  // 0: the kept p themselves (sum2), else p / sum2 (draw)
+    float inv;  // 0: the kept p themselves (sum2, or the draw without top-p), else p / sum2 (draw)
     float sum2;
 };
 __device__ __forceinline__ klist_row make_klist(const zs_sargs& a, uint32_t r, const zs_row_state& st, int kind) {
@@ -1387,8 +1363,8 @@ __device__ __forceinline__ klist_row make_klist(const zs_sargs& a, uint32_t r, c
     L.nk = st.nk;
     L.vstar = st.vstar;
     L.istar = st.istar;
-    L.sum2 = kind ? st.sum2 : 1.0f;
-    L.inv = kind ? 1.0f : 0.0f;
+    L.sum2 = kind && st.knorm ? st.sum2 : 1.0f;
+    L.inv = kind && st.knorm ? 1.0f : 0.0f;
     return L;
 }
 // term i of the list: the kept p (0 for the equal values after i*), divided by
@@ -1409,7 +1385,7 @@ __global__ __launch_bounds__(256) void zs_k_roundK(zs_sargs a) {
     const uint32_t r = blockIdx.y;
     const uint32_t j = blockIdx.x * 4 + zs_wid();
     const zs_row_state& st = a.rst[r];
-    if (!st.klist) return;
+    if (!st.klist || (KIND == 0 && !st.knorm)) return;   // no sum2 without a top-p cut
     const uint32_t nks = (st.nk + ZS_SUB - 1) / ZS_SUB;
     if (j >= nks) return;
     const klist_row L = make_klist(a, r, st, KIND);
@@ -1496,7 +1472,7 @@ template <int KIND>
 __global__ __launch_bounds__(SW_NT) void zs_k_stitchK(zs_sargs a) {
     const uint32_t r = blockIdx.x;
     zs_row_state* stp = a.rst + r;
-    if (!stp->klist) return;
+    if (!stp->klist || (KIND == 0 && !stp->knorm)) return;
     const zs_row_state st = *stp;
     const klist_row L = make_klist(a, r, st, KIND);
     const uint32_t nks = (L.nk + ZS_SUB - 1) / ZS_SUB;
