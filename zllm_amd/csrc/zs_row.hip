@@ -38,11 +38,24 @@
 // tile is redone with the exact ordered scan of zs_seq.h. No prediction and
 // no second pass is needed: the grid is always that of the true running sum.
 #include <hip/hip_runtime.h>
+#ifdef ZS_WALK_DEBUG
+// Debug builds: wall-clock time of zs_k_row's phases (0-5, row count in 7)
+// and of the small path's (8-15), summed over rows (zs_dbg_row_stats).
+__device__ unsigned long long rw_dbg[16];
+#define ZS_SP_T(i)                                               \
+    do {                                                         \
+        if (zs_lane() == 0) {                                    \
+            const unsigned long long c_ = wall_clock64();        \
+            atomicAdd(&rw_dbg[8 + (i)], c_ - sp_t0);             \
+            sp_t0 = c_;                                          \
+        }                                                        \
+    } while (0)
+#endif
 #include "zs_sampler.h"
 
-#define RW_NT 1024
+#define RW_NT 512
 #define RW_NW (RW_NT / 64)
-#define RW_G 4096          // ids per tile: one float4 per thread
+#define RW_G 2048          // ids per tile: one float4 per thread
 #define RW_BUF 2048        // candidate buffer entries (per list)
 #define RW_KEEP 1024       // a list above this is compacted to its top K
 
@@ -55,7 +68,7 @@ struct rw_shared {
             unsigned long long s[RW_BUF];         // P1: sampler candidates
         } b;
     } u;
-    float sval[ZS_SMALL_CAP];
+    alignas(16) float sval[ZS_SMALL_CAP];   // also the small path's scratch
     uint32_t sidx[ZS_SMALL_CAP];
     uint32_t cand_id[ZS_OBS_CAND];
     float cand_x[ZS_OBS_CAND];
@@ -83,6 +96,19 @@ __shared__ rw_shared rw_sh;
 extern __shared__ uint32_t rw_pbits[];
 
 #define RW_PF_SHIFT 30u
+
+#ifdef ZS_WALK_DEBUG
+#define RW_T(i)                                                  \
+    do {                                                         \
+        if (threadIdx.x == 0) {                                  \
+            const unsigned long long c_ = wall_clock64();        \
+            atomicAdd(&rw_dbg[i], c_ - rw_t0);                   \
+            rw_t0 = c_;                                          \
+        }                                                        \
+    } while (0)
+#else
+#define RW_T(i) do { } while (0)
+#endif
 
 // A value every lane holds equally (read from LDS after a barrier), moved to
 // a scalar register so that the compiler branches on it without exec masks.
@@ -308,6 +334,7 @@ struct rw_row {
 struct rw_raw {
     float4 v;
     uint32_t w;   // the allow word holding the 4 ids
+    uint32_t pw;  // the patch bitmap word holding them (rows with patches)
 };
 // A load through a global-address-space pointer (the host pass of the
 // compiler only parses device code, and has no such address space).
@@ -331,12 +358,18 @@ __device__ __forceinline__ rw_raw rw_fetch(const rw_row& R, uint32_t g) {
     const rw_f4 v = rw_gload(reinterpret_cast<const rw_f4*>(R.row + idx0));
     o.v = make_float4(v.x, v.y, v.z, v.w);
     o.w = rw_gload(R.allow_or_row + min(idx0 >> 5, R.wmax));
+    // read with the loads, long before its use
+    o.pw = R.np ? rw_pbits[min((g * RW_G + 4 * threadIdx.x) >> 5, R.words - 1)] : 0u;
     return o;
 }
 // The patched ids among the 4 ids from idx0 (bits of pb): bans set x~ and
 // y to -inf, biased or counted ids take their y from the patch list. Their
 // rank in the sorted list is the number of bitmap bits before them (per-word
-// prefix counts follow the bitmap).
+// prefix counts follow the bitmap). GP: the list is longer than its LDS head,
+// and ranks past it read the row's copy in global memory (a load that the
+// streaming loops must not contain otherwise: the compiler then waits for
+// every load in flight after each tile).
+template <bool GP>
 __device__ __forceinline__ void rw_patch4(const rw_row& R, uint32_t idx0, uint32_t pb, uint32_t wd, float (&x)[4],
                                           float (&y)[4], const rw_shared& sh) {
     uint32_t rank = rw_pbits[R.words + (idx0 >> 5)] + __popc(wd & ((1u << (idx0 & 31)) - 1u));
@@ -345,7 +378,7 @@ __device__ __forceinline__ void rw_patch4(const rw_row& R, uint32_t idx0, uint32
         if (!((pb >> q) & 1u)) continue;
         uint32_t fl;
         float py;
-        if (rank < ZS_PATCH_LDS) { fl = sh.pid[rank] >> RW_PF_SHIFT; py = sh.py[rank]; }
+        if (!GP || rank < ZS_PATCH_LDS) { fl = sh.pid[rank] >> RW_PF_SHIFT; py = sh.py[rank]; }
         else { fl = R.gfl[rank]; py = R.gy[rank]; }
         if (fl & ZS_PF_BAN) { x[q] = -INFINITY; y[q] = -INFINITY; }
         if (fl & ZS_PF_Y) y[q] = py;
@@ -356,6 +389,7 @@ __device__ __forceinline__ void rw_patch4(const rw_row& R, uint32_t idx0, uint32
 // temperature) of the 4 ids g*RW_G + 4t .. +3; ids >= V read -inf. Branch
 // free but for two uniform tests (the row's last tile, patches in the row)
 // and the rare threads holding a patched id.
+template <bool GP>
 __device__ __forceinline__ void rw_elems(const rw_row& R, uint32_t g, const rw_raw& raw, float (&x)[4], float (&y)[4],
                                          const rw_shared& sh) {
     const uint32_t idx0 = g * RW_G + 4 * threadIdx.x;
@@ -372,11 +406,10 @@ __device__ __forceinline__ void rw_elems(const rw_row& R, uint32_t g, const rw_r
 #pragma unroll
     for (int q = 0; q < 4; q++) y[q] = x[q];
     if (R.np) {
-        const uint32_t wi = min(idx0 >> 5, R.words - 1);
-        const uint32_t wd = rw_pbits[wi];
+        const uint32_t wd = raw.pw;
         uint32_t pb = (wd >> (idx0 & 31)) & 15u;
         if (last) pb = idx0 < R.V ? pb : 0u;
-        if (pb) rw_patch4(R, idx0, pb, wd, x, y, sh);
+        if (pb) rw_patch4<GP>(R, idx0, pb, wd, x, y, sh);
     }
 }
 
@@ -389,7 +422,7 @@ __device__ __forceinline__ void rw_elems(const rw_row& R, uint32_t g, const rw_r
 // else ng. The last group is padded with tiles past the row (ids >= V only),
 // which f must treat as neutral. f must not call functions: a call inside the
 // loop saves the registers of the loads in flight, which waits for them.
-template <class F>
+template <bool GP, class F>
 __device__ __forceinline__ uint32_t rw_stream(const rw_row& R, const rw_shared& sh, uint32_t g_begin, const F& f) {
     const uint32_t ng = (R.V + RW_G - 1) / RW_G;
     rw_raw raw[4];
@@ -405,7 +438,7 @@ __device__ __forceinline__ uint32_t rw_stream(const rw_row& R, const rw_shared& 
         for (int u = 0; u < 4; u++) {
             const uint32_t g = g0 + u;
             float x[4], y[4];
-            rw_elems(R, g, raw[u], x, y, sh);
+            rw_elems<GP>(R, g, raw[u], x, y, sh);
             raw[u] = rw_fetch(R, min(g + 4, ng - 1));
             __asm__ volatile("" ::: "memory");   // keep the loads issued here, ahead of their use
             if (rw_uni(f(g, u, x, y) ? 1u : 0u)) return g;
@@ -417,7 +450,7 @@ __device__ __forceinline__ uint32_t rw_stream(const rw_row& R, const rw_shared& 
 // The elements of one tile (the tile a stream stopped at).
 __device__ __forceinline__ void rw_tile(const rw_row& R, const rw_shared& sh, uint32_t g, float (&x)[4], float (&y)[4]) {
     const rw_raw raw = rw_fetch(R, g);
-    rw_elems(R, g, raw, x, y, sh);
+    rw_elems<true>(R, g, raw, x, y, sh);
 }
 
 // ---------------------------------------------------------------------------
@@ -448,17 +481,19 @@ struct rw_list {
 // number at most RW_SEL_CAP (always by the last digit: entries are
 // distinct); those are gathered to the front and sorted by one wave.
 #define RW_SEL_CAP 256
+#define RW_SEL_E (RW_BUF / RW_NT)   // list entries per thread
+static_assert(RW_BUF % RW_NT == 0, "the list is spread evenly over the threads");
 
 __device__ __noinline__ uint32_t rw_select(int which, uint32_t n, uint32_t K1, uint32_t idlim) {
     rw_shared& sh = rw_sh;
     unsigned long long* buf = which ? sh.u.b.s : sh.u.b.o;
     const uint32_t t = threadIdx.x, lane = (uint32_t)zs_lane(), wid = (uint32_t)zs_wid();
     const unsigned long long NONE = ~0ull;   // no member: ids are below 2^32 - 1
-    unsigned long long v[2];
+    unsigned long long v[RW_SEL_E];
     uint32_t lo = 0xffffffffu, hi = 0;       // keys (high words) of the members
     uint32_t c = 0;
 #pragma unroll
-    for (int e = 0; e < 2; e++) {
+    for (int e = 0; e < RW_SEL_E; e++) {
         const uint32_t i = t + (uint32_t)e * RW_NT;
         v[e] = NONE;
         if (i < n) {
@@ -504,7 +539,7 @@ __device__ __noinline__ uint32_t rw_select(int which, uint32_t n, uint32_t K1, u
             __syncthreads();
             const int up = shift + 8;
 #pragma unroll
-            for (int e = 0; e < 2; e++) {
+            for (int e = 0; e < RW_SEL_E; e++) {
                 const bool in = v[e] != NONE && (up >= 64 || (v[e] >> up) == (pre >> up));
                 const uint32_t dg = (uint32_t)(v[e] >> shift) & 255u;
                 if (in) atomicAdd(&sh.sel_hist[pass][dg], 1u);
@@ -544,7 +579,7 @@ __device__ __noinline__ uint32_t rw_select(int which, uint32_t n, uint32_t K1, u
     if (t == 0) sh.sel_n = 0;
     __syncthreads();
 #pragma unroll
-    for (int e = 0; e < 2; e++) {
+    for (int e = 0; e < RW_SEL_E; e++) {
         if (v[e] == NONE || (v[e] >> shift) > (pre >> shift)) continue;
         buf[atomicAdd(&sh.sel_n, 1u)] = v[e];
     }
@@ -728,10 +763,14 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
     const bool want_lp = (P.flags & ZS_ROW_LOGPROBS) != 0;
     const bool want_unc = (P.flags & ZS_ROW_UNCERTAINTY) != 0;
     const bool want_obs = want_lp || want_unc;
+#ifdef ZS_WALK_DEBUG
+    unsigned long long rw_t0 = wall_clock64();
+#endif
 
     // ---------------- P0: patches
     uint32_t has_y = 0;
     const int np = rw_patches(a, r, P, has_y, sh);
+    RW_T(0);
     rw_row R;
     R.gfl = a.p_flags + (size_t)r * a.pstride;
     R.gy = a.p_y + (size_t)r * a.pstride;
@@ -817,8 +856,21 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
             gath = rw_uni(nf) >= Ko;
         }
     }
+    RW_T(1);
     uint32_t g = 0;
     const uint32_t ng = gath ? 0u : (V + RW_G - 1) / RW_G;
+    // the admission thresholds in scalar registers: they change only where
+    // the lists are set up (first tile) and compacted (outside the stream)
+    float r_tfo = -INFINITY, r_tfs = -INFINITY;
+    bool r_allo = true, r_alls = true;
+    uint32_t r_ilim = 0xffffffffu;
+    auto load_thr = [&]() {
+        r_tfo = rw_unif(sh.fthr[0]);
+        r_tfs = rw_unif(sh.fthr[1]);
+        r_allo = rw_uni(thr_o < 0 ? 1u : 0u) != 0u;
+        r_alls = rw_uni(thr_s < 0 ? 1u : 0u) != 0u;
+        r_ilim = rw_uni(sh.inf_lim);
+    };
     if (gath) {
         const float* gcx = rw_scratch(a, r);
         const uint32_t gn = rw_uni(sh.g_n);
@@ -847,7 +899,7 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
         if (smode == 2 && n_s > ZS_SMALL_CAP) s_over = true;
     }
     while (g < ng) {
-        g = rw_stream(R, sh, g, [&](uint32_t g, int u, const float (&x)[4], const float (&y)[4]) {
+        auto tile = [&](uint32_t g, int u, const float (&x)[4], const float (&y)[4]) {
             const uint32_t idx0 = g * RW_G + 4 * t;
             // branch-free statistics (ids >= V read -inf: neutral here)
             omax = fmaxf(omax, fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])));
@@ -936,6 +988,7 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
                         sh.fthr[1] = a1 > kmin ? zs_key_to_float(a1 - 1u) : -INFINITY;
                     }
                     rw_bar();
+                    load_thr();
                 }
             }
             // admissions, compared as values: a key above the threshold key is a
@@ -946,9 +999,9 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
             const uint32_t slot = grp % 3;
             uint32_t po = 0, ps = 0;
             {
-                const float tfo = rw_unif(sh.fthr[0]), tfs = rw_unif(sh.fthr[1]);
-                const bool allo = rw_uni(thr_o < 0 ? 1u : 0u) != 0u, alls = rw_uni(thr_s < 0 ? 1u : 0u) != 0u;
-                const uint32_t ilim = rw_uni(sh.inf_lim);
+                const float tfo = r_tfo, tfs = r_tfs;
+                const bool allo = r_allo, alls = r_alls;
+                const uint32_t ilim = r_ilim;
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
                     po |= ((x[q] > tfo || allo) && (x[q] != -INFINITY || idx0 + q <= ilim)) ? (1u << q) : 0u;
@@ -1013,7 +1066,11 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
             if (smode == 2 && !s_over && n_s > ZS_SMALL_CAP) s_over = true;
             p1stop = ovf != 0xffffffffu || n_o > RW_KEEP || (smode == 1 && n_s > RW_KEEP);
             return p1stop;
-        });
+        };
+        // (rows with more patches than the LDS head take the loop that can
+        // read the rest from global memory)
+        load_thr();
+        g = R.np > ZS_PATCH_LDS ? rw_stream<true>(R, sh, g, tile) : rw_stream<false>(R, sh, g, tile);
         if (!p1stop) break;
         p1stop = false;
         // compactions (rare): a list past RW_KEEP is cut to its first K. After
@@ -1104,6 +1161,7 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
             g = g + 1;
         }
     }
+    RW_T(2);
     // ---- row statistics (one workgroup reduction)
     {
         for (int d = 32; d > 0; d >>= 1) {
@@ -1149,6 +1207,7 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
         }
     }
     const uint32_t z_is_x = (T == 1.0f && !has_y) ? 1u : 0u;
+    RW_T(3);
 
     // ---------------- sampler decisions
     uint32_t token = 0, mode = ZS_MODE_DONE, status = 0, has_thr = 0, thr_key = 0;
@@ -1162,7 +1221,7 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
         } else {
             const uint32_t L = (uint32_t)last_nan;
             unsigned long long gb = 0;
-            rw_stream(R, sh, 0, [&](uint32_t g, int, const float (&x)[4], const float (&y)[4]) {
+            rw_stream<true>(R, sh, 0, [&](uint32_t g, int, const float (&x)[4], const float (&y)[4]) {
                 const uint32_t idx0 = g * RW_G + 4 * t;
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
@@ -1270,6 +1329,7 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
         }
     }
     __syncthreads();
+    RW_T(4);
 
     // ---------------- the row sums, left to zs_sums.hip: S_obs (logprobs and
     // uncertainty), the sampler's S of a big row (unless it equals S_obs: z is
@@ -1313,7 +1373,19 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
         zs_tp_bucket* bk = a.tp_bk + (size_t)r * ZS_TP_NB;
         for (uint32_t i = t; i < ZS_TP_NB; i += RW_NT) { bk[i].cnt = 0u; bk[i].mass = 0.0f; }
     }
+    RW_T(5);
+#ifdef ZS_WALK_DEBUG
+    if (t == 0) atomicAdd(&rw_dbg[7], 1ull);
+#endif
 }
+
+#ifdef ZS_WALK_DEBUG
+extern "C" int zs_dbg_row_stats(unsigned long long* out) {
+    if (hipMemcpyFromSymbol(out, HIP_SYMBOL(rw_dbg), 16 * sizeof(unsigned long long)) != hipSuccess) return -1;
+    static unsigned long long zero[16];
+    return hipMemcpyToSymbol(HIP_SYMBOL(rw_dbg), zero, sizeof(zero)) == hipSuccess ? 0 : -1;
+}
+#endif
 
 extern "C" int zs_row_launch(const zs_sargs& a, hipStream_t stream) {
     const size_t dyn = 4 * ((a.b.V + 31) / 32) * sizeof(uint32_t);

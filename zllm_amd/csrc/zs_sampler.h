@@ -92,15 +92,62 @@ __device__ __forceinline__ void wave_sort_u64_e(unsigned long long (&v)[E]) {
     }
 }
 
+#ifndef ZS_SP_T
+#define ZS_SP_T(i) do { } while (0)
+#endif
+
+// The wave's values (element i = lane * E + e in register e of lane i / E;
+// the first n) written to LDS scratch in element order, for a serial pass.
+template <int E>
+__device__ __forceinline__ void wave_stage_f(float* buf, const float (&v)[E], uint32_t n) {
+    const uint32_t lane = (uint32_t)zs_lane();
+#pragma unroll
+    for (int e = 0; e < E; e++)
+        if (lane * E + e < n) buf[lane * E + e] = v[e];
+    __builtin_amdgcn_s_waitcnt(0);   // the wave's own LDS writes before its reads
+    __builtin_amdgcn_wave_barrier();
+}
+// Index of the first element after which s0 + buf[0] + ... + buf[i] (f32,
+// one addition at a time in order) reaches thresh (never for NaN); n if none.
+// *s gets the sum up to and including that element (all n when none). Every
+// lane runs it on the same LDS values (broadcast reads) and ends with the same
+// result.
+__device__ __forceinline__ uint32_t serial_scan_f(const float* buf, uint32_t n, float s0, float thresh, float* s) {
+    float acc = s0;
+    uint32_t i = 0;
+    for (; i + 4 <= n; i += 4) {
+        const float4 q = *reinterpret_cast<const float4*>(buf + i);
+        acc = acc + q.x;
+        if (acc >= thresh) { *s = acc; return i; }
+        acc = acc + q.y;
+        if (acc >= thresh) { *s = acc; return i + 1; }
+        acc = acc + q.z;
+        if (acc >= thresh) { *s = acc; return i + 2; }
+        acc = acc + q.w;
+        if (acc >= thresh) { *s = acc; return i + 3; }
+    }
+    for (; i < n; i++) {
+        acc = acc + buf[i];
+        if (acc >= thresh) { *s = acc; return i; }
+    }
+    *s = acc;
+    return n;
+}
+
 // Exact sampler over a small survivor set (n <= 64 * E, every other element
 // below the top-k threshold, masked or -inf), by one wave: the reference's
 // sequential f32 sums are done literally, one addition at a time in the
 // reference's order, with no workgroup synchronisation (sampler.rs:46-127).
-// Called by the 64 lanes of one wave; returns the token on every lane.
+// The additions run over LDS copies of the values (sval, sidx: the survivors
+// on entry, then scratch; 16-byte aligned). Called by the 64 lanes of one
+// wave; returns the token on every lane.
 template <int E>
 __device__ uint32_t small_path_wave(uint64_t seed, uint64_t counter, uint32_t V, const zs_row_params& P, uint32_t n, float m,
-                                    const float* sval, const uint32_t* sidx) {
+                                    float* sval, uint32_t* sidx) {
     const uint32_t lane = (uint32_t)zs_lane();
+#ifdef ZS_WALK_DEBUG
+    unsigned long long sp_t0 = wall_clock64();
+#endif
     // survivors by index: element i (sorted) in register i % E of lane i / E
     unsigned long long key[E];
 #pragma unroll
@@ -109,6 +156,7 @@ __device__ uint32_t small_path_wave(uint64_t seed, uint64_t counter, uint32_t V,
         key[e] = i < n ? (((unsigned long long)sidx[i] << 32) | zs_f2u(sval[i])) : ~0ull;
     }
     wave_sort_u64_e<E>(key);
+    ZS_SP_T(0);
     uint32_t id[E];
     float p[E];
 #pragma unroll
@@ -119,17 +167,18 @@ __device__ uint32_t small_path_wave(uint64_t seed, uint64_t counter, uint32_t V,
     }
     // s0 + v[0] + v[1] + ... in order (sampler.rs:68, 80, 107)
     auto seq_sum = [&](const float (&v)[E], float s0) {
-        float s = s0;
-        for (uint32_t L = 0; L * E < n; L++)
-#pragma unroll
-            for (int e = 0; e < E; e++)
-                if (L * E + e < n) s = s + zs_readlane_f(v[e], L);
+        wave_stage_f<E>(sval, v, n);
+        float s;
+        serial_scan_f(sval, n, s0, NAN, &s);
+        __builtin_amdgcn_wave_barrier();
         return s;
     };
     // softmax (sampler.rs:67-69)
+    ZS_SP_T(1);
     const float S = seq_sum(p, -0.0f);
 #pragma unroll
     for (int e = 0; e < E; e++) p[e] = p[e] / S;
+    ZS_SP_T(2);
     // min-p (sampler.rs:72-88)
     if (P.min_p > 0.0f) {
         float pm = 0.0f;
@@ -154,21 +203,22 @@ __device__ uint32_t small_path_wave(uint64_t seed, uint64_t counter, uint32_t V,
             for (int e = 0; e < E; e++)
                 k2[e] = lane * E + e < n ? (((unsigned long long)(~zs_f2u(p[e])) << 32) | id[e]) : ~0ull;
             wave_sort_u64_e<E>(k2);
-            float cum = 0.0f;
-            bool found = false;
-            for (uint32_t L = 0; L * E < n && !found; L++) {
+            ZS_SP_T(3);
+            float ps[E];
 #pragma unroll
-                for (int e = 0; e < E; e++) {
-                    if (found || L * E + e >= n) continue;
-                    const unsigned long long ks = zs_readlane_u64(k2[e], L);
-                    cum = cum + zs_u2f(~(uint32_t)(ks >> 32));
-                    if (cum >= P.top_p) {
-                        vstar = ~(uint32_t)(ks >> 32);
-                        istar = (uint32_t)ks;
-                        found = true;
-                    }
-                }
+            for (int e = 0; e < E; e++) {
+                ps[e] = zs_u2f(~(uint32_t)(k2[e] >> 32));
+                if (lane * E + e < n) sidx[lane * E + e] = (uint32_t)k2[e];
             }
+            wave_stage_f<E>(sval, ps, n);
+            float cum;
+            const uint32_t i = serial_scan_f(sval, n, 0.0f, P.top_p, &cum);
+            if (i < n) {
+                vstar = zs_f2u(sval[i]);
+                istar = sidx[i];
+            }
+            __builtin_amdgcn_wave_barrier();
+            ZS_SP_T(4);
         }
         float f[E];
 #pragma unroll
@@ -181,19 +231,18 @@ __device__ uint32_t small_path_wave(uint64_t seed, uint64_t counter, uint32_t V,
         if (sum > 0.0f)
 #pragma unroll
             for (int e = 0; e < E; e++) p[e] = f[e] / sum;
+        ZS_SP_T(5);
     }
     // draw (sampler.rs:118-127); r == 0 stops at index 0 whatever its p
     const float rr = zs_philox_uniform(seed, counter, 0u);
     if (rr <= 0.0f) return 0;
-    float cum = 0.0f;
-    for (uint32_t L = 0; L * E < n; L++) {
 #pragma unroll
-        for (int e = 0; e < E; e++) {
-            if (L * E + e >= n) continue;
-            cum = cum + zs_readlane_f(p[e], L);
-            if (cum >= rr) return zs_readlane_u(id[e], L);
-        }
-    }
-    return V - 1;
+    for (int e = 0; e < E; e++)
+        if (lane * E + e < n) sidx[lane * E + e] = id[e];
+    wave_stage_f<E>(sval, p, n);
+    float cum;
+    const uint32_t i = serial_scan_f(sval, n, 0.0f, rr, &cum);
+    ZS_SP_T(6);
+    return i < n ? sidx[i] : V - 1;
 }
 
