@@ -54,7 +54,7 @@ struct big_shared {
     uint32_t hist[BK_NB + 1];    // level 0: bucket starts by rank (rank 0 = largest values)
     uint32_t hist1[BK_NB + 1];   // level 1 (refinement of one oversize bucket)
     uint32_t hist2[256];         // level 2: counts of single values
-    uint32_t sortbuf[ZS_SORT_CAP];
+    alignas(16) uint32_t sortbuf[ZS_SORT_CAP];
 };
 
 struct big_row {
@@ -815,7 +815,31 @@ __device__ __forceinline__ uint32_t tp_first(uint32_t lo, uint32_t hi, const F& 
 // The walk itself, by one wave (tp_fast_row rows): returns 1 with the stop
 // (value, rank among equal values) in *wo, 2 when the sum never reaches top_p,
 // 0 when the row must take the workgroup walk.
-__device__ __forceinline__ int tp_walk(const zs_sargs& a, uint32_t r, float top_p, walk_out* wo) {
+// Debug builds: wall-clock time of zs_k_big's phases, summed over rows
+// (zs_dbg_big_stats): 0 top-k select, 1 S, 2 p / min-p, 3 top-p walk on bucket
+// totals, 4 workgroup walk, 5 rest; 6 rows, 7 rows of the workgroup walk.
+#ifdef ZS_WALK_DEBUG
+__device__ unsigned long long bk_dbg[16];
+#define BK_T(i)                                                  \
+    do {                                                         \
+        if (threadIdx.x == 0) {                                  \
+            const unsigned long long c_ = wall_clock64();        \
+            atomicAdd(&bk_dbg[i], c_ - bk_t0);                   \
+            atomicMax(&bk_dbg[10 + (i)], c_ - bk_t0);            \
+            bk_t0 = c_;                                          \
+        }                                                        \
+    } while (0)
+extern "C" int zs_dbg_big_stats(unsigned long long* out) {
+    if (hipMemcpyFromSymbol(out, HIP_SYMBOL(bk_dbg), 16 * sizeof(unsigned long long)) != hipSuccess) return -1;
+    static unsigned long long zero[16];
+    return hipMemcpyToSymbol(HIP_SYMBOL(bk_dbg), zero, sizeof(zero)) == hipSuccess ? 0 : -1;
+}
+#else
+#define BK_T(i) do { } while (0)
+#endif
+
+#define TP_CH 1024   // values per LDS chunk of tp_walk's one-by-one additions
+__device__ __forceinline__ int tp_walk(const zs_sargs& a, uint32_t r, float top_p, walk_out* wo, float* lbuf) {
     const uint32_t lane = (uint32_t)zs_lane();
     const zs_tp_bucket* bk = a.tp_bk + (size_t)r * ZS_TP_NB;
     const uint32_t* gv = a.pairs + (size_t)r * a.max_vocab * 2;
@@ -832,17 +856,26 @@ __device__ __forceinline__ int tp_walk(const zs_sargs& a, uint32_t r, float top_
         k = zs_grid_k(s);
         kthr = zs_grid_thresh(top_p, eg);
     };
-    // the bucket records of the next two groups of 64 are loaded ahead
-    struct grp_ld { uint32_t cnt, meta; unsigned long long tot; };
+    // the bucket records of the next two groups of 64 are loaded ahead; after
+    // a bucket with an event the walk goes on in the same group (lanes from
+    // l0 on), with no reload
+    struct grp_ld { uint32_t cnt, meta, start; unsigned long long tot; };
     auto load = [&](uint32_t b) {
-        grp_ld g = {0u, 0u, 0ull};
-        if (b + lane < ZS_TP_NB) { g.cnt = bk[b + lane].cnt; g.meta = bk[b + lane].meta; g.tot = bk[b + lane].tot; }
+        grp_ld g = {0u, 0u, 0u, 0ull};
+        if (b + lane < ZS_TP_NB) {
+            g.cnt = bk[b + lane].cnt; g.meta = bk[b + lane].meta; g.start = bk[b + lane].start; g.tot = bk[b + lane].tot;
+        }
         return g;
     };
-    uint32_t b0 = 0;
+    uint32_t b0 = 0, l0 = 0;
+#ifdef ZS_WALK_DEBUG
+    uint32_t d_ev = 0, d_ser = 0, d_bs = 0;
+    unsigned long long d_t = 0;
+    auto d_out = [&]() { if (lane == 0) { atomicMax(&bk_dbg[9], (unsigned long long)d_ev); atomicMax(&bk_dbg[15], (unsigned long long)d_ser); atomicMax(&bk_dbg[5], (unsigned long long)d_bs); atomicMax(&bk_dbg[0], d_t); } };
+#endif
     grp_ld cur = load(0), nxt = load(64);
     while (b0 < ZS_TP_NB) {
-        const uint32_t cnt = cur.cnt, meta = cur.meta;
+        const uint32_t cnt = lane >= l0 ? cur.cnt : 0u, meta = cur.meta;
         const bool special = cnt && ((int)(meta & TP_M_EG) != eg || (meta & TP_M_TIE0));
         // totals on the grid, saturated: a group is only added whole while the
         // sum stays below the binade end
@@ -853,21 +886,30 @@ __device__ __forceinline__ int tp_walk(const zs_sargs& a, uint32_t r, float top_
         if (!hm) {
             k += (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
             b0 += 64;
+            l0 = 0;
             cur = nxt;
             nxt = load(b0 + 64);
             continue;
         }
         const uint32_t f = (uint32_t)__ffsll((long long)hm) - 1u;
         k += f ? (uint32_t)__builtin_amdgcn_readlane((int)incl, (int)f - 1) : 0u;
-        const uint32_t b = b0 + f;
-        b0 = b + 1;
-        cur = load(b0);
-        nxt = load(b0 + 64);
         const uint32_t n = __shfl(cnt, (int)f, 64), bm = __shfl(meta, (int)f, 64);
+        const uint32_t st0 = __shfl(cur.start, (int)f, 64);
+        l0 = f + 1;
+        if (l0 == 64) {
+            b0 += 64;
+            l0 = 0;
+            cur = nxt;
+            nxt = load(b0 + 64);
+        }
         if (!(bm & TP_M_SORTED)) {
             return 0;
         }
-        const uint32_t st0 = bk[b].start;
+#ifdef ZS_WALK_DEBUG
+        d_ev++;
+        const unsigned long long d_t0 = wall_clock64();
+        if (n > TP_SERIAL_N) d_bs++;
+#endif
         // the bucket in exact descending order, from the exact sum k * grid
         uint32_t pos = 0;
         bool done = false, stop = false;
@@ -909,18 +951,49 @@ __device__ __forceinline__ int tp_walk(const zs_sargs& a, uint32_t r, float top_
             }
         }
         if (!done && !stop) {
-            // one addition at a time (sampler.rs:103)
+            // one addition at a time (sampler.rs:103) over LDS copies of the
+            // bucket's values, TP_CH at a time: the wave loads a chunk with all
+            // its loads in flight, then every lane adds the same values in
+            // order (broadcast reads). The values are positive: the running
+            // sum never decreases, so one test per 4 values finds whether it
+            // reached top_p among them.
             float ss = zs_grid_value((uint32_t)k, eg);
-            for (uint32_t i = pos; i < n && !stop; i += 64) {
-                const float v = i + lane < n ? zs_u2f(gv[st0 + i + lane]) : 0.0f;
-                const uint32_t m = min(64u, n - i);
-                for (uint32_t j = 0; j < m; j++) {
-                    ss = ss + zs_readlane_f(v, j);
-                    if (ss >= top_p) { stop = true; at = i + j; break; }
+            const uint32_t* src = gv + st0;
+#ifdef ZS_WALK_DEBUG
+            d_ser += n - pos;
+#endif
+            for (uint32_t c0 = pos; c0 < n && !stop; c0 += TP_CH) {
+                const uint32_t m = min((uint32_t)TP_CH, n - c0);
+                uint32_t w[TP_CH / 64];
+#pragma unroll
+                for (int q = 0; q < TP_CH / 64; q++) {
+                    const uint32_t i = lane + 64u * (uint32_t)q;
+                    w[q] = i < m ? src[c0 + i] : 0u;
                 }
+#pragma unroll
+                for (int q = 0; q < TP_CH / 64; q++) lbuf[lane + 64u * (uint32_t)q] = zs_u2f(w[q]);
+                __builtin_amdgcn_s_waitcnt(0);
+                __builtin_amdgcn_wave_barrier();
+                for (uint32_t i = 0; i < m; i += 4) {
+                    const float4 q4 = *reinterpret_cast<const float4*>(lbuf + i);
+                    const float c1 = ss + q4.x, c2 = c1 + q4.y, c3 = c2 + q4.z, c4 = c3 + q4.w;
+                    if (c4 >= top_p) {
+                        const uint32_t e0 = c1 >= top_p ? 0u : c2 >= top_p ? 1u : c3 >= top_p ? 2u : 3u;
+                        stop = true;
+                        at = c0 + i + e0;
+                        ss = e0 == 0 ? c1 : e0 == 1 ? c2 : e0 == 2 ? c3 : c4;
+                        break;
+                    }
+                    ss = c4;
+                }
+                __builtin_amdgcn_wave_barrier();
             }
             if (!stop) set_sum(ss);
         }
+#ifdef ZS_WALK_DEBUG
+        d_t += wall_clock64() - d_t0;
+        if (stop) d_out();
+#endif
         if (stop) {
             const uint32_t vs = gv[st0 + at];
             const uint32_t first = tp_first(0u, at + 1, [&](uint32_t j) { return gv[st0 + j] <= vs; });
@@ -933,11 +1006,17 @@ __device__ __forceinline__ int tp_walk(const zs_sargs& a, uint32_t r, float top_
     return 2;
 }
 
+
 __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
     const uint32_t r = blockIdx.x;
     zs_row_state stt = a.rst[r];
     const bool run_samp = stt.mode == ZS_MODE_BIG;
     if (!run_samp) return;
+#ifdef ZS_WALK_DEBUG
+    unsigned long long bk_t0 = wall_clock64();
+    const unsigned long long bk_start = bk_t0;
+    if (threadIdx.x == 0) atomicAdd(&bk_dbg[6], 1ull);
+#endif
     __shared__ big_shared sh;
     const int t = threadIdx.x;
     const zs_batch& b = a.b;
@@ -996,6 +1075,7 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
         thr_key = prefix;
         has_thr = 1;
     }
+    BK_T(0);
     const bool use_thr = has_thr != 0;
     const float thr = zs_key_to_float(thr_key);
 
@@ -1015,6 +1095,7 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
         }
     }
 
+    BK_T(1);
     // ---- probabilities p = exp(z - max) / S (sampler.rs:69), kept in pv for
     // the later passes; min-p kept mass (sampler.rs:72-88) in the same pass
     const bool minp = P.min_p > 0.0f;
@@ -1076,6 +1157,7 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
         }
     };
 
+    BK_T(2);
     // ---- top-p (sampler.rs:91-115)
     const bool topp = P.top_p < 1.0f && P.top_p > 0.0f;
     if (topp) {
@@ -1092,7 +1174,7 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
         if (!peak && (a.tp_cl[(size_t)r * ZS_TP_CL] & TP_ROW_FAST)) {
             if (t < 64) {
                 walk_out w = {false, 0u, 0u};
-                const int res = tp_walk(a, r, P.top_p, &w);
+                const int res = tp_walk(a, r, P.top_p, &w, reinterpret_cast<float*>(sh.sortbuf));
 
                 if (t == 0) { sh.u[0] = (uint32_t)res; sh.u[1] = w.v; sh.u[2] = w.rank; }
             }
@@ -1101,7 +1183,11 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
             wo = {fw == 1, sh.u[1], sh.u[2]};
             __syncthreads();
         }
+        BK_T(3);
         if (fw == 0) {
+#ifdef ZS_WALK_DEBUG
+        if (threadIdx.x == 0) atomicAdd(&bk_dbg[7], 1ull);
+#endif
         // counts per (rank, copy): 16 copies by lane keep same-address LDS
         // atomics (skewed histograms) at most 4-way
         uint32_t* cc = sh.sortbuf;
@@ -1190,6 +1276,10 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
             done = upto;
         }
         }  // fw == 0
+        BK_T(4);
+#ifdef ZS_WALK_DEBUG
+        if (threadIdx.x == 0) atomicMax(&bk_dbg[8], wall_clock64() - bk_start);
+#endif
         if (peak) wo = {true, pmax1, 0u};
         if (wo.stopped) {
             // The kept set is {p1 > v*} plus the first rank+1 elements equal to
@@ -1210,6 +1300,7 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
             return;
         }
     }
+    BK_T(5);
     // ---- every positive p1 kept (no top-p, or a walk that never stopped): the
     // kept list is every positive p1 in index order (v* = 0: no value equals
     // it), with sum2 and the renormalised draw after a top-p walk, else the
