@@ -257,3 +257,31 @@ def test_helper_workgroups_match_one_per_row():
     from tests.gpu_util import compare
     errs = compare(x, params, {k: v.cpu().numpy() for k, v in a.items()})
     assert not errs, "\n".join(errs[:20])
+
+
+def test_top_logprobs_near_collisions():
+    """top_logprobs ranks equal logprobs by id (logprobs.rs:41-51). Rows built
+    so that many x~ map to one or two logprob values, with the boundary between
+    them set by the last bits of lse: the ids must equal the oracle's in every
+    row not flagged ZS_ST_TOPLP_AMBIG, and the rows must hold such ties."""
+    from tests.gpu_util import compare, oracle_row, run_gpu
+    rng = np.random.default_rng(7)
+    B, V = 32, 8192
+    x = np.full((B, V), -60.0, np.float32)
+    for i in range(B):
+        x[i, rng.integers(0, V)] = np.float32(30.0 + rng.normal() * 0.01)
+        ids = rng.choice(V, 40, replace=False)
+        base = np.float32(rng.uniform(1e-3, 2e-3))
+        x[i, ids] = base + (rng.integers(0, 200, 40) * np.spacing(base)).astype(np.float32)
+        x[i, rng.choice(V, 100, replace=False)] = rng.uniform(-12, -8, 100).astype(np.float32)
+    params = [dict(temperature=1.0, top_k=0, top_p=1.0, top_logprobs=20, seed=i) for i in range(B)]
+    for i in range(0, B, 2):   # bans among the tied ids (x~ = -inf there)
+        tied_ids = np.flatnonzero((x[i] > 5e-4) & (x[i] < 5e-3))
+        params[i]["ban"] = [int(v) for v in rng.choice(tied_ids, 6, replace=False)]
+    refs = [oracle_row(x[i], params[i]) for i in range(B)]
+    tied = sum(len(set(np.asarray(r["top_lps"]).tolist())) < len(r["top_lps"]) for r in refs)
+    assert tied >= B // 2, tied
+    print(f"[case] near-collision rows B={B} V={V} tied={tied}", flush=True)
+    out = run_gpu(x, params)
+    errs = compare(x, params, out, refs=refs)
+    assert not errs, "\n".join(errs[:20])

@@ -1688,7 +1688,55 @@ __global__ __launch_bounds__(64) void zs_k_final(zs_sargs a) {
             }
             if (__ballot(amb)) status |= ZS_ST_TOPLP_AMBIG;
             const uint32_t n = ntl < nc ? ntl : nc;
-            if (mine && rank < n) { tid[rank] = id; tlp[rank] = lp; }
+            // Distinct x~ can round to one lp. When the list of candidates by
+            // (x~ desc, id asc) was cut and its last candidate shares the lp
+            // of the n-th entry, ids outside the list may hold that lp too and
+            // rank before candidates by id: the entries above that lp are the
+            // candidates', the rest are the smallest ids of the whole row at
+            // that lp (found in id order by one scan of the row).
+            bool fill = false;
+            float lpn = -INFINITY;
+            if (n > 0 && nc == ZS_OBS_CAND && nc < b.V) {
+                const unsigned long long at = __ballot(mine && rank == n - 1);
+                lpn = zs_readlane_f(lp, (uint32_t)__ffsll((long long)at) - 1u);
+                float lmin = mine ? lp : INFINITY;
+                for (int d = 32; d > 0; d >>= 1) lmin = fminf(lmin, __shfl_xor(lmin, d, 64));
+                fill = lpn > -INFINITY && lmin == lpn;
+            }
+            if (!fill) {
+                if (mine && rank < n) { tid[rank] = id; tlp[rank] = lp; }
+            } else {
+                if (mine && lp > lpn) { tid[rank] = id; tlp[rank] = lp; }
+                uint32_t got = (uint32_t)__popcll(__ballot(mine && lp > lpn));
+                const float* row = b.d_logits + (size_t)r * b.ld;
+                const bool masked = (P.flags & ZS_ROW_MASKED) && b.d_allow_bits;
+                const uint32_t* pid = a.p_id + (size_t)r * a.pstride;
+                const uint32_t* pfl = a.p_flags + (size_t)r * a.pstride;
+                const uint32_t* psub = a.p_sub + (size_t)r * (a.max_subs + 1);
+                const uint32_t nsub = (b.V + ZS_SUB - 1) / ZS_SUB;
+                for (uint32_t i0 = 0; i0 < b.V && got < n; i0 += 64) {
+                    const uint32_t i = i0 + lane;
+                    bool hit = false;
+                    if (i < b.V) {
+                        float xv = row[i];
+                        if (masked && !zs_allowed_bit(b, r, i)) xv = -INFINITY;
+                        hit = (xv - lse) == lpn;
+                    }
+                    unsigned long long hm = __ballot(hit);
+                    while (hm && got < n) {
+                        const uint32_t idh = i0 + (uint32_t)__ffsll((long long)hm) - 1u;
+                        hm &= hm - 1ull;
+                        // a banned id has x~ = -inf (its patches, lanes in parallel)
+                        const uint32_t p0 = psub[idh / ZS_SUB], p1 = psub[min(idh / ZS_SUB + 1, nsub)];
+                        bool ban = false;
+                        for (uint32_t q = p0 + lane; q < p1; q += 64)
+                            if (pid[q] == idh && (pfl[q] & ZS_PF_BAN)) ban = true;
+                        if (__ballot(ban)) continue;
+                        if (lane == 0) { tid[got] = idh; tlp[got] = lpn; }
+                        got++;
+                    }
+                }
+            }
             if (lane == 0) b.d_top_n[r] = n;
         }
     }
