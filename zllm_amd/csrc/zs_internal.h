@@ -178,6 +178,7 @@ struct zs_ctx {
     uint32_t* tp_cl;             // [rows][ZS_TP_CL] row flags, candidate count, candidate buckets
     uint32_t* tp_pre;            // [rows][2][max_vocab] increment prefixes of presorted buckets
     uint32_t* kcnt;              // [rows][2 * max_chunks] kept-set counts per 4096-id group
+    uint32_t* tp_task;           // [1 + rows * ZS_TP_CAND] buckets to presort: count, then (row << 8 | candidate)
     uint32_t* p_sub;             // [rows][max_subs+1] patch index range per sub-chunk
     uint32_t max_subs;
     zs_spec_chunk* spec_chunks;  // [rows][2*ZS_SPEC_KMAX+1][max_chunks]

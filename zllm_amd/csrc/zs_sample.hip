@@ -453,6 +453,9 @@ __device__ __forceinline__ bool tp_fast_row(const zs_row_state& st, const zs_row
 // also add their positive p to the per-bucket counts and masses.
 __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_pv(zs_sargs a) {
     const uint32_t g = blockIdx.x, r = blockIdx.y;
+    // (the presort task list of this step starts empty: zs_k_tp_plan and
+    // zs_k_tp_inc, launched after this kernel, append to it)
+    if (g == 0 && r == 0 && threadIdx.x == 0) a.tp_task[0] = 0u;
     const zs_row_state& st = a.rst[r];
     if (st.mode != ZS_MODE_BIG || !big_s_from_rounds(st)) return;
     const zs_batch& b = a.b;
@@ -607,6 +610,8 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_tp_plan(zs_sargs a) {
     if (t == 0) {
         cl[0] = TP_ROW_FAST;
         cl[1] = ntot;
+        const uint32_t base = ntot ? atomicAdd(&a.tp_task[0], ntot) : 0u;
+        for (uint32_t j = 0; j < ntot; j++) a.tp_task[1 + base + j] = (r << 8) | j;
     }
 }
 
@@ -647,7 +652,10 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_tp_inc(zs_sargs a) {
             const uint32_t old = atomicOr(&bk[i].meta, TP_M_TIE0);
             if (!(old & (TP_M_TIE0 | TP_M_CAND))) {
                 const uint32_t j = atomicAdd(&cl[1], 1u);
-                if (j < ZS_TP_CAND) cl[2 + j] = i;
+                if (j < ZS_TP_CAND) {
+                    cl[2 + j] = i;
+                    a.tp_task[1 + atomicAdd(&a.tp_task[0], 1u)] = (r << 8) | j;
+                }
             }
         }
     }
@@ -730,8 +738,16 @@ __device__ __forceinline__ void tp_bitonic_step(uint32_t (&v)[4], uint32_t k, ui
     }
 }
 
-__global__ __launch_bounds__(TP_SORT_NT) void zs_k_tp_sort(zs_sargs a) {
-    const uint32_t c = blockIdx.x, r = blockIdx.y;
+#ifdef ZS_WALK_DEBUG
+// debug builds: sorted buckets by size class (<= 256, 1024, 4096), launches
+__device__ unsigned long long ts_dbg[8];
+extern "C" int zs_dbg_sort_stats(unsigned long long* out) {
+    if (hipMemcpyFromSymbol(out, HIP_SYMBOL(ts_dbg), 8 * sizeof(unsigned long long)) != hipSuccess) return -1;
+    static unsigned long long zero[8];
+    return hipMemcpyToSymbol(HIP_SYMBOL(ts_dbg), zero, sizeof(zero)) == hipSuccess ? 0 : -1;
+}
+#endif
+__device__ __forceinline__ void tp_sort_one(const zs_sargs& a, uint32_t c, uint32_t r) {
     const uint32_t t = threadIdx.x;
     const uint32_t* cl = a.tp_cl + (size_t)r * ZS_TP_CL;
     if (!(cl[0] & TP_ROW_FAST) || c >= min(cl[1], (uint32_t)ZS_TP_CAND)) return;
@@ -747,6 +763,9 @@ __global__ __launch_bounds__(TP_SORT_NT) void zs_k_tp_sort(zs_sargs a) {
     uint32_t* po = pe + a.max_vocab;
     uint32_t np2 = 256;
     while (np2 < n) np2 <<= 1;
+#ifdef ZS_WALK_DEBUG
+    if (t == 0) atomicAdd(&ts_dbg[np2 <= 256 ? 0 : np2 <= 1024 ? 1 : 2], 1ull);
+#endif
     uint32_t v[4];
 #pragma unroll
     for (uint32_t e = 0; e < 4u; e++) {
@@ -789,6 +808,17 @@ __global__ __launch_bounds__(TP_SORT_NT) void zs_k_tp_sort(zs_sargs a) {
     }
     tie1 = __syncthreads_or(tie1);
     if (t == 0) atomicOr(&B->meta, TP_M_SORTED | (tie1 ? TP_M_TIE1 : 0u));
+}
+// One workgroup per listed (row, candidate bucket), from the task list of
+// zs_k_tp_plan / zs_k_tp_inc: a small grid whatever the batch, so that rows
+// without candidates cost no workgroups.
+__global__ __launch_bounds__(TP_SORT_NT) void zs_k_tp_sort(zs_sargs a) {
+    const uint32_t nt = a.tp_task[0];
+    for (uint32_t i = blockIdx.x; i < nt; i += gridDim.x) {
+        const uint32_t tk = a.tp_task[1 + i];
+        tp_sort_one(a, tk & 0xffu, tk >> 8);
+        __syncthreads();
+    }
 }
 
 // First j in [lo, hi) with pred(j) (pred monotone: false then true), or hi;
@@ -1791,6 +1821,7 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
     a.tp_cl = ctx->tp_cl;
     a.tp_pre = ctx->tp_pre;
     a.kcnt = ctx->kcnt;
+    a.tp_task = ctx->tp_task;
     a.s_rec = ctx->s_rec;
     a.s_apx = ctx->s_apx;
     a.gath = ctx->gath;
@@ -1838,7 +1869,7 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
     mark("zs_k_tp_plan");
     hipLaunchKernelGGL(zs_k_tp_inc, dim3((bt->V + ZS_BIG_G - 1) / ZS_BIG_G, B), dim3(ZS_BIG_NT), 0, stream, a);
     mark("zs_k_tp_inc");
-    hipLaunchKernelGGL(zs_k_tp_sort, dim3(ZS_TP_CAND, B), dim3(TP_SORT_NT), 0, stream, a);
+    hipLaunchKernelGGL(zs_k_tp_sort, dim3(std::min(512u, B * ZS_TP_CAND)), dim3(TP_SORT_NT), 0, stream, a);
     mark("zs_k_tp_sort");
     hipLaunchKernelGGL(zs_k_big, dim3(B), dim3(ZS_BIG_NT), 0, stream, a);
     mark("zs_k_big");

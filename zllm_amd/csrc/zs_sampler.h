@@ -26,6 +26,7 @@ struct zs_sargs {
     uint32_t* tp_cl;
     uint32_t* tp_pre;
     uint32_t* kcnt;
+    uint32_t* tp_task;   // buckets zs_k_tp_sort presorts: count, then (row << 8 | candidate)
     zs_sub_sum* s_rec;
     float* s_apx;
     float* gath;
