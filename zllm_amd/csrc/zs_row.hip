@@ -1,4 +1,4 @@
-// zs_row.hip -- the front of the sampler step, one 1024-thread workgroup per
+// zs_row.hip -- the front of the sampler step, one 512-thread workgroup per
 // row: everything of a row that needs the whole row, with no other workgroup
 // involved and therefore no device-scope synchronisation and no launch
 // boundary between the phases.
@@ -9,12 +9,13 @@
 //   token = sample_with_rng(y, cfg, r)    sampler.rs:31-128
 //   logprobs / token_uncertainty on x~    logprobs.rs:34-54, hallucination.rs:129-154
 //
-// Phases of zs_k_row (one row workgroup per row; the sampler's S of unmasked
-// rows without top-k in a helper workgroup beside it, see rw_helper):
+// Phases of zs_k_row:
 //   P0  patches: the row's ban / bias / count-map entries merged into one list
 //       sorted by id with the exact patched y of every listed id
-//       (decode_ctrl.rs:107-126 operation order), kept in LDS with a bitmap of
-//       the patched ids, and stored for the later kernels;
+//       (decode_ctrl.rs:107-126 operation order; lists of any length: the
+//       first ZS_PATCH_LDS entries in LDS, the rest in row scratch), ranked by
+//       a bitmap of the patched ids with per-word prefix counts, and stored
+//       for the later kernels;
 //   P1  one read of the logits: observer maximum / NaN / +inf, sampler maximum,
 //       finite count and flags, greedy argmax (last maximal element, a NaN
 //       restarts the fold: sampler.rs:35-43), and candidate lists kept in LDS
@@ -25,18 +26,9 @@
 //   decisions: greedy / non-finite rows get their token; rows whose survivors
 //       fit ZS_SMALL_CAP are sampled exactly by one wave (small_path_wave);
 //       other rows are "big" and continue in zs_sample.hip;
-//   P2  the sequential f32 sums S = sum exp(x~ - max) (observers) and, for big
-//       rows, S = sum exp(z - max) of the sampler (sampler.rs:68), exactly;
-//   P3  the entropy sum of token_uncertainty (hallucination.rs:139-144).
-//
-// Exact sequential sums (P2, P3). The row is walked in tiles of 4096 ids in
-// index order with the exact running sum s known at every tile start: each
-// thread adds its terms' integer increments on the grid of s (zs_math.h), one
-// workgroup reduction gives the tile's total, and s moves by total * grid
-// unless a term of the tile was an exact half-way case (its increment depends
-// on the sum's parity) or the sum leaves its binade inside the tile; such a
-// tile is redone with the exact ordered scan of zs_seq.h. No prediction and
-// no second pass is needed: the grid is always that of the true running sum.
+//   state: which exact sums the row needs (zs_sums.hip: the observers' S and
+//       entropy, a big row's sampler S), over the whole row or over the
+//       allowed ids a masked row gathered to row scratch.
 #include <hip/hip_runtime.h>
 #ifdef ZS_WALK_DEBUG
 // Debug builds: wall-clock time of zs_k_row's phases (0-5, row count in 7)

@@ -9,12 +9,16 @@
 // Kernels (one launch each, in stream order):
 //   zs_k_row      (zs_row.hip) one workgroup per row: patch list, candidate
 //                 lists, the sampler's decisions (greedy, non-finite, top-k and
-//                 small survivor sets sampled on chip), the observers' S and
-//                 entropy, and the sampler's S of the remaining ("big") rows.
-//   zs_k_pv .. zs_k_tp_sort   big rows: survivor values and the top-p bucket plan.
-//   zs_k_big      one 1024-thread workgroup per big row: exact emulation of the
-//                 reference's sequential f32 sums (min-p, top-p walk).
-//   zs_k_kcount, zs_k_kwrite, zs_k_roundK, zs_k_stitchK   the kept list's sums.
+//                 small survivor sets sampled on chip); the other rows are
+//                 "big".
+//   zs_k_sapx, zs_k_sround, zs_k_sstitch   (zs_sums.hip) the exact row sums:
+//                 the observers' S and a big row's sampler S, then the entropy
+//                 (on the context's side stream, joined before zs_k_final).
+//   zs_k_pv .. zs_k_tp_sort   big rows: probabilities and the top-p bucket plan.
+//   zs_k_big      one 1024-thread workgroup per big row: top-k select, min-p,
+//                 the top-p walk.
+//   zs_k_kcount, zs_k_kwrite, zs_k_roundK, zs_k_stitchK   the kept list: its
+//                 sum and the draw.
 //   zs_k_final    chosen-token outputs.
 //
 // Exactness: every value that decides the sampled id is computed with the same
