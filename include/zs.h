@@ -268,9 +268,7 @@ typedef struct zs_batch {
      * begin: independent work (draft verification of the same step) made to
      * wait on it runs beside the sampler, on the CUs its per-row workgroups
      * leave idle (rows finish at different times), instead of after it.
-     * With an event the per-row kernel runs one workgroup per row; without
-     * one it adds helper workgroups for the longest row sums (more work,
-     * shorter sampler). NULL: no event. */
+     * NULL: no event. */
     void* pass_event;
 } zs_batch;
 
