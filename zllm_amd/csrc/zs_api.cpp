@@ -111,7 +111,7 @@ extern "C" void zs_ctx_destroy(zs_ctx* ctx) {
     int dev = 0;
     (void)hipGetDevice(&dev);
     (void)hipSetDevice(ctx->device);
-    for (int i = 0; i < 16; i++)
+    for (int i = 0; i < 24; i++)
         if (ctx->events[i]) (void)hipEventDestroy((hipEvent_t)ctx->events[i]);
     if (ctx->fork_event) (void)hipEventDestroy((hipEvent_t)ctx->fork_event);
     if (ctx->join_event) (void)hipEventDestroy((hipEvent_t)ctx->join_event);
@@ -750,7 +750,7 @@ extern "C" int zs_set_profiling(zs_ctx* ctx, int on) {
         int prev = 0;
         (void)hipGetDevice(&prev);
         (void)hipSetDevice(ctx->device);
-        for (int i = 0; i < 16; i++) {
+        for (int i = 0; i < 24; i++) {
             hipEvent_t e;
             ZS_HIP(ctx, hipEventCreate(&e));
             ctx->events[i] = e;

@@ -78,7 +78,6 @@ struct zs_row_state {
     uint32_t mode;
     uint32_t token;
     uint32_t status;
-    uint32_t z_is_x;      // sampler input equals x~ (T == 1, no bias / penalty)
     // observers over x~
     float obs_max;
     uint32_t obs_special; // lse is NaN (NaN / +inf / all -inf row)
@@ -191,8 +190,8 @@ struct zs_ctx {
     // profiling (zs_set_profiling)
     int profiling;
     int n_timed;
-    void* events[16];      // hipEvent_t
-    const char* timed_names[16];
+    void* events[24];      // hipEvent_t
+    const char* timed_names[24];
     // batched lane (zs_lane_step): per-stream knobs staged through pinned
     // host memory, top-K pool of every stream
     float* lane_temp;            // [4][rows] block: temp, then top_k, top_p, seed (below point into it)

@@ -1198,7 +1198,6 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
             sh.cand_x[t] = zs_key_to_float(~(uint32_t)(sh.u.b.o[t] >> 32));
         }
     }
-    const uint32_t z_is_x = (T == 1.0f && !has_y) ? 1u : 0u;
     RW_T(3);
 
     // ---------------- sampler decisions
@@ -1323,14 +1322,14 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
     __syncthreads();
     RW_T(4);
 
-    // ---------------- the row sums, left to zs_sums.hip: S_obs (logprobs and
-    // uncertainty), the sampler's S of a big row (unless it equals S_obs: z is
-    // x~ and no top-k cut applies), the entropy. A masked row's sums run over
-    // its allowed ids, gathered to row scratch (when at most a quarter of the
-    // row is allowed), else over the whole row with its allow bits.
+    // ---------------- the row sums, left to zs_sums.hip: the sampler's S of a
+    // big row (on the caller's stream, before the big-row kernels), S_obs
+    // (logprobs and uncertainty) and the entropy (on the side stream). A
+    // masked row's sums run over its allowed ids, gathered to row scratch
+    // (when at most a quarter of the row is allowed), else over the whole row
+    // with its allow bits.
     const bool doA = (obs_need & ZS_OBS_S) != 0;
-    const bool reuse = z_is_x && has_thr == 0 && doA;
-    const bool doB = mode == ZS_MODE_BIG && has_thr != 2 && !reuse;
+    const bool doB = mode == ZS_MODE_BIG && has_thr != 2;
     const bool doH = (obs_need & ZS_OBS_H) != 0;
     uint32_t gn = 0;
     if (R.allow && (doA || doB || doH))
@@ -1351,7 +1350,6 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
         st.obs_special = special ? 1u : 0u;
         st.obs_need = obs_need;
         st.n_cand = n_cand;
-        st.z_is_x = reuse ? 1u : 0u;
         st.klist = 0;
         st.kpend = 0;
         st.knorm = 0;

@@ -430,15 +430,12 @@ __device__ __forceinline__ walk_out bk_exact(const uint32_t* vals, uint32_t n, f
 }
 
 // The sampler's softmax denominator of a big row is known before zs_k_big when
-// the rounds summed it (or the observers' S is the same sum: z == x~, no cut).
+// the rounds summed it (every big row but those whose top-k threshold
+// zs_k_big selects).
 __device__ __forceinline__ bool big_s_from_rounds(const zs_row_state& st) {
-    const bool reuse = st.z_is_x && !st.has_thr && (st.obs_need & ZS_OBS_S);
-    return reuse || ((st.rounds >> ZS_SUM_SAMP_S) & 1u);
+    return ((st.rounds >> ZS_SUM_SAMP_S) & 1u) != 0u;
 }
-__device__ __forceinline__ float big_s_value(const zs_row_state& st) {
-    const bool reuse = st.z_is_x && !st.has_thr && (st.obs_need & ZS_OBS_S);
-    return reuse ? st.obs_S : st.samp_S;
-}
+__device__ __forceinline__ float big_s_value(const zs_row_state& st) { return st.samp_S; }
 
 // Rows whose top-p walk runs on bucket totals (zs_k_tp_*): p comes from
 // zs_k_pv, no min-p (the walked values are the p themselves), the top-k
@@ -1113,11 +1110,9 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
     const bool use_thr = has_thr != 0;
     const float thr = zs_key_to_float(thr_key);
 
-    // ---- softmax denominator: from the parallel rounds (sampler S, or the
-    // observers' S when z == x~ and no top-k cut applies), else summed here
-    const bool reuse = stt.z_is_x && !use_thr && (stt.obs_need & ZS_OBS_S);
-    float S = reuse ? stt.obs_S : stt.samp_S;
-    if (!reuse && !((stt.rounds >> ZS_SUM_SAMP_S) & 1u)) {
+    // ---- softmax denominator: from the parallel rounds, else summed here
+    float S = stt.samp_S;
+    if (!((stt.rounds >> ZS_SUM_SAMP_S) & 1u)) {
         S = -0.0f;
         for (uint32_t g = 0; g < ng; g++) {
             float x[4], z[4];
@@ -1845,24 +1840,27 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
     if (a.b.pass_event && hipEventRecord((hipEvent_t)a.b.pass_event, stream) != hipSuccess) return -1;
     if (zs_row_launch(a, stream)) return zs_set_error(ctx, ZS_EHIP, "zs_sample: zs_k_row launch failed");
     mark("zs_k_row");
-    // the row sums: S_obs and the sampler's S here; the entropy (needed only
-    // by zs_k_final) on the context's side stream beside the big-row kernels,
-    // unless profiling, which keeps every kernel on the caller's stream
+    // the row sums: the approximations and the big rows' sampler S here;
+    // S_obs and the entropy (needed only by zs_k_final) on the context's side
+    // stream beside the big-row kernels, unless profiling, which keeps every
+    // kernel on the caller's stream
     {
-        static const char* const names[5] = {"zs_k_sapx", "zs_k_sround1", "zs_k_sstitch1", "zs_k_sround2",
-                                             "zs_k_sstitch2"};
-        for (uint32_t w = 0; w < 3; w++) {
-            if (zs_sums_launch(a, w, stream)) return zs_set_error(ctx, ZS_EHIP, "zs_sample: row sums launch failed");
-            mark(names[w]);
-        }
+        static const char* const names[7] = {"zs_k_sapx", "zs_k_sround1", "zs_k_sstitch1", "zs_k_sround2",
+                                             "zs_k_sstitch2", "zs_k_sround3", "zs_k_sstitch3"};
+        if (zs_sums_launch(a, 0, stream)) return zs_set_error(ctx, ZS_EHIP, "zs_sample: row sums launch failed");
+        mark(names[0]);
         hipStream_t hs = stream;
         if (!prof) {
             hs = (hipStream_t)ctx->side_stream;
             ZS_LAUNCH_CHECK(hipEventRecord((hipEvent_t)ctx->fork_event, stream));
             ZS_LAUNCH_CHECK(hipStreamWaitEvent(hs, (hipEvent_t)ctx->fork_event, 0));
         }
-        for (uint32_t w = 3; w < 5; w++) {
-            if (zs_sums_launch(a, w, hs)) return zs_set_error(ctx, ZS_EHIP, "zs_sample: entropy launch failed");
+        for (uint32_t w = 1; w < 3; w++) {
+            if (zs_sums_launch(a, w, stream)) return zs_set_error(ctx, ZS_EHIP, "zs_sample: row sums launch failed");
+            mark(names[w]);
+        }
+        for (uint32_t w = 3; w < 7; w++) {
+            if (zs_sums_launch(a, w, hs)) return zs_set_error(ctx, ZS_EHIP, "zs_sample: observer sums launch failed");
             mark(names[w]);
         }
         if (!prof) ZS_LAUNCH_CHECK(hipEventRecord((hipEvent_t)ctx->join_event, hs));

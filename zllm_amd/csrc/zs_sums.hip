@@ -522,14 +522,19 @@ __device__ __forceinline__ seq_pair sm_total(const sm_terms& f, const float (&x)
 }
 
 // ---------------------------------------------------------------------------
-// zs_k_sround<STAGE>: stage 1 the two S sums, stage 2 the entropy (which
-// needs the exact S_obs of stage 1).
+// zs_k_sround<STAGE>: one sum per stage: 1 the sampler's S of the big rows
+// (the big-row kernels wait for it), 2 S_obs and 3 the entropy (which needs
+// the exact S_obs), both on the side stream.
 // ---------------------------------------------------------------------------
+template <int STAGE>
+__device__ __forceinline__ constexpr int sm_stage_kind() {
+    return STAGE == 1 ? ZS_SUM_SAMP_S : STAGE == 2 ? ZS_SUM_OBS_S : ZS_SUM_OBS_H;
+}
 template <int STAGE>
 __global__ __launch_bounds__(SM_NT) void zs_k_sround(zs_sargs a) {
     const uint32_t r = blockIdx.y;
     const zs_row_state& st = a.rst[r];
-    const uint32_t mine = STAGE == 1 ? ((1u << ZS_SUM_OBS_S) | (1u << ZS_SUM_SAMP_S)) : (1u << ZS_SUM_OBS_H);
+    const uint32_t mine = 1u << sm_stage_kind<STAGE>();
     const uint32_t jobs = st.rounds & mine;
     if (!jobs) return;
     const zs_row_params P = a.b.d_params[r];
@@ -537,8 +542,8 @@ __global__ __launch_bounds__(SM_NT) void zs_k_sround(zs_sargs a) {
     const uint32_t nsub = (S.n + ZS_SUB - 1) / ZS_SUB;
     if (blockIdx.x * SM_SPB >= nsub) return;
     sm_tab_fill();
-    const int kinds[2] = {STAGE == 1 ? ZS_SUM_OBS_S : ZS_SUM_OBS_H, ZS_SUM_SAMP_S};
-    constexpr int NK = STAGE == 1 ? 2 : 1;
+    const int kinds[1] = {sm_stage_kind<STAGE>()};
+    constexpr int NK = 1;
     sm_terms F[NK];
 #pragma unroll
     for (int u = 0; u < NK; u++) F[u] = sm_terms_of(kinds[u], st, P);
@@ -651,7 +656,7 @@ template <int STAGE>
 __global__ __launch_bounds__(SW_NT) void zs_k_sstitch(zs_sargs a) {
     const uint32_t r = blockIdx.x;
     zs_row_state* stp = a.rst + r;
-    const int kind = STAGE == 1 ? (blockIdx.y == 0 ? ZS_SUM_OBS_S : ZS_SUM_SAMP_S) : ZS_SUM_OBS_H;
+    const int kind = sm_stage_kind<STAGE>();
     if (!((stp->rounds >> kind) & 1u)) return;
     sm_tab_fill();
     const zs_row_state& st = *stp;
@@ -680,17 +685,19 @@ extern "C" int zs_dbg_walk_stats(unsigned long long* out) {
 }
 #endif
 
-// Launches one kernel of the row sums: 0 zs_k_sapx, 1 zs_k_sround<1>,
-// 2 zs_k_sstitch<1>, 3 zs_k_sround<2>, 4 zs_k_sstitch<2>.
+// Launches one kernel of the row sums: 0 zs_k_sapx, then zs_k_sround<s> and
+// zs_k_sstitch<s> as 1, 2 (s = 1), 3, 4 (s = 2), 5, 6 (s = 3).
 extern "C" int zs_sums_launch(const zs_sargs& a, uint32_t which, hipStream_t stream) {
     const uint32_t nsub = (a.b.V + ZS_SUB - 1) / ZS_SUB;
     const dim3 grid((nsub + SM_SPB - 1) / SM_SPB, a.b.B);
     switch (which) {
         case 0: hipLaunchKernelGGL(zs_k_sapx, grid, dim3(SM_NT), 0, stream, a); break;
         case 1: hipLaunchKernelGGL(zs_k_sround<1>, grid, dim3(SM_NT), 0, stream, a); break;
-        case 2: hipLaunchKernelGGL(zs_k_sstitch<1>, dim3(a.b.B, 2), dim3(SW_NT), 0, stream, a); break;
+        case 2: hipLaunchKernelGGL(zs_k_sstitch<1>, dim3(a.b.B), dim3(SW_NT), 0, stream, a); break;
         case 3: hipLaunchKernelGGL(zs_k_sround<2>, grid, dim3(SM_NT), 0, stream, a); break;
-        case 4: hipLaunchKernelGGL(zs_k_sstitch<2>, dim3(a.b.B, 1), dim3(SW_NT), 0, stream, a); break;
+        case 4: hipLaunchKernelGGL(zs_k_sstitch<2>, dim3(a.b.B), dim3(SW_NT), 0, stream, a); break;
+        case 5: hipLaunchKernelGGL(zs_k_sround<3>, grid, dim3(SM_NT), 0, stream, a); break;
+        case 6: hipLaunchKernelGGL(zs_k_sstitch<3>, dim3(a.b.B), dim3(SW_NT), 0, stream, a); break;
         default: return -1;
     }
     return hipGetLastError() == hipSuccess ? 0 : -1;
