@@ -109,7 +109,7 @@ SPEC_K = 4
 # HBM bytes per launch of the C5 batch's dispatches, measured with rocprofv3
 # --pmc FETCH_SIZE / WRITE_SIZE and scaled by the copy-kernel calibration
 # (profiles/c5_kernels_counters.md, the tree of the commit that added it)
-TRAFFIC = {"zs_k_spec_chunk": 1402.4e6, "zs_k_row": 110.2e6, "zs_k_sapx": 83.1e6, "zs_k_sround1": 94.2e6,
+TRAFFIC = {"zs_k_spec_chunk": 1402.4e6, "zs_k_row": 110.2e6, "zs_k_sround1": 94.2e6,
            "zs_k_sround2": 91.6e6, "zs_k_pv": 63.9e6, "zs_k_tp_inc": 36.3e6, "zs_k_big": 0.6e6}
 
 
@@ -542,7 +542,7 @@ def main():
     nb = bits.cpu().numpy().view(np.uint32)
     allowed = [int(np.unpackbits(nb[i].view(np.uint8)).sum()) if W["masked"][i] else 0 for i in range(B)]
     sum_bytes = float(sum(4 * V if not W["masked"][i] else 8 * allowed[i] for i in range(B)))
-    for k in ("zs_k_sapx", "zs_k_sround2", "zs_k_sround3"):   # every row's terms (sround1: big rows only)
+    for k in ("zs_k_sapx2", "zs_k_sround2", "zs_k_sround3"):   # every row's terms (sapx1, sround1: big rows only)
         per_kernel_bytes[k] = sum_bytes
     dom_bytes = per_kernel_bytes.get(dom, step_bytes)
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
@@ -599,7 +599,7 @@ def main():
                                  "achieved": round(per_kernel_bytes[k] / (acc[k] * 1e-3) / 1e9, 1),
                                  "frac": round(per_kernel_bytes[k] / (acc[k] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                                  "traffic": TRAFFIC.get(k)}
-                             for k in ("zs_k_row", "zs_k_sapx", "zs_k_sround2", "zs_k_sround3", "zs_k_pv")
+                             for k in ("zs_k_row", "zs_k_sapx2", "zs_k_sround2", "zs_k_sround3", "zs_k_pv")
                              if k in acc and k in per_kernel_bytes},
         "roofline_sampler": {"bound": "hbm", "kernels": "zs_sample (all its kernels, one stream)",
                              "achieved": round(samp_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",

@@ -171,7 +171,7 @@ struct zs_ctx {
     zs_sub_sum* k_sum;           // [rows][2][max_subs] kept-list rounds (sum2, draw)
     zs_sub_sum* s_rec;           // [rows][ZS_NSUM][max_subs] row-sum sub-chunk totals (zs_k_sround)
     float* gath;                 // [rows][2 * max_vocab + 16] masked rows' gathered allowed ids (x~, y, ids)
-    float* s_hterm;              // [rows][max_vocab + 8] entropy terms of the sub-chunks its stitch walks
+    float* s_hterm;              // [rows][max_vocab + 8] exact terms of the side-stream sums (S_obs, then entropy)
     float* s_apx;                // [rows][max_subs][8] approximate row-sum parts per sub-chunk (zs_k_sapx)
     zs_tp_bucket* tp_bk;         // [rows][ZS_TP_NB] top-p buckets (zs_k_tp_*)
     uint32_t* tp_cl;             // [rows][ZS_TP_CL] row flags, candidate count, candidate buckets

@@ -1845,21 +1845,19 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
     // stream beside the big-row kernels, unless profiling, which keeps every
     // kernel on the caller's stream
     {
-        static const char* const names[7] = {"zs_k_sapx", "zs_k_sround1", "zs_k_sstitch1", "zs_k_sround2",
-                                             "zs_k_sstitch2", "zs_k_sround3", "zs_k_sstitch3"};
-        if (zs_sums_launch(a, 0, stream)) return zs_set_error(ctx, ZS_EHIP, "zs_sample: row sums launch failed");
-        mark(names[0]);
+        static const char* const names[8] = {"zs_k_sapx1", "zs_k_sround1", "zs_k_sstitch1", "zs_k_sapx2",
+                                             "zs_k_sround2", "zs_k_sstitch2", "zs_k_sround3", "zs_k_sstitch3"};
         hipStream_t hs = stream;
         if (!prof) {
             hs = (hipStream_t)ctx->side_stream;
             ZS_LAUNCH_CHECK(hipEventRecord((hipEvent_t)ctx->fork_event, stream));
             ZS_LAUNCH_CHECK(hipStreamWaitEvent(hs, (hipEvent_t)ctx->fork_event, 0));
         }
-        for (uint32_t w = 1; w < 3; w++) {
+        for (uint32_t w = 0; w < 3; w++) {
             if (zs_sums_launch(a, w, stream)) return zs_set_error(ctx, ZS_EHIP, "zs_sample: row sums launch failed");
             mark(names[w]);
         }
-        for (uint32_t w = 3; w < 7; w++) {
+        for (uint32_t w = 3; w < 8; w++) {
             if (zs_sums_launch(a, w, hs)) return zs_set_error(ctx, ZS_EHIP, "zs_sample: observer sums launch failed");
             mark(names[w]);
         }

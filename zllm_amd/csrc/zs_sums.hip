@@ -101,11 +101,10 @@ __device__ __forceinline__ sm_src sm_src_of(const zs_sargs& a, uint32_t r, const
 }
 
 // Exact terms of the sub-chunks that are not safe, per (row, sum), max_vocab
-// floats: for the two S sums scratch the big-row kernels only use after them
-// (the probability array and the top-p prefix area); the entropy, which runs
-// beside the big-row kernels, has an area of its own.
+// floats: the sampler's S (caller's stream, finished before the big-row
+// kernels reuse it) in the top-p prefix area; S_obs and then the entropy, in
+// turn on the side stream beside the big-row kernels, in an area of their own.
 __device__ __forceinline__ float* sm_darea(const zs_sargs& a, uint32_t r, int kind) {
-    if (kind == ZS_SUM_OBS_S) return reinterpret_cast<float*>(a.pv + (size_t)r * a.max_vocab);
     if (kind == ZS_SUM_SAMP_S) return reinterpret_cast<float*>(a.tp_pre + (size_t)r * a.max_vocab * 2);
     return a.s_hterm + (size_t)r * ((size_t)a.max_vocab + 8);
 }
@@ -365,10 +364,13 @@ __device__ __forceinline__ uint32_t sm_sub_of(uint32_t i) {
 // the largest x~ and the largest y.
 // ---------------------------------------------------------------------------
 #define SM_APX 8   // floats per sub-chunk record
+// WHICH 1: the sampler's S (caller's stream); 2: S_obs and the entropy (side
+// stream). Each writes only its own fields of the record.
+template <int WHICH>
 __global__ __launch_bounds__(SM_NT) void zs_k_sapx(zs_sargs a) {
     const uint32_t r = blockIdx.y;
     const zs_row_state& st = a.rst[r];
-    const uint32_t jobs = st.rounds;
+    const uint32_t jobs = st.rounds & (WHICH == 1 ? (1u << ZS_SUM_SAMP_S) : ((1u << ZS_SUM_OBS_S) | (1u << ZS_SUM_OBS_H)));
     if (!jobs) return;
     const zs_row_params P = a.b.d_params[r];
     const sm_src S = sm_src_of(a, r, st, P);
@@ -412,15 +414,16 @@ __global__ __launch_bounds__(SM_NT) void zs_k_sapx(zs_sargs a) {
                 ms = fmaxf(ms, y[q]);
             }
         }
-        so = sm_wave_sum_f(so);
-        ss = sm_wave_sum_f(ss);
-        sd = sm_wave_sum_f(sd);
-        mo = wave_max_f(mo);
-        ms = wave_max_f(ms);
-        if (zs_lane() == 0) {
-            float4* o = reinterpret_cast<float4*>(a.s_apx + ((size_t)r * a.max_subs + j) * SM_APX);
-            o[0] = make_float4(so, ss, sd, mo);
-            o[1] = make_float4(ms, 0.0f, 0.0f, 0.0f);
+        float* o = a.s_apx + ((size_t)r * a.max_subs + j) * SM_APX;
+        if (WHICH == 1) {
+            ss = sm_wave_sum_f(ss);
+            ms = wave_max_f(ms);
+            if (zs_lane() == 0) { o[1] = ss; o[4] = ms; }
+        } else {
+            so = sm_wave_sum_f(so);
+            sd = sm_wave_sum_f(sd);
+            mo = wave_max_f(mo);
+            if (zs_lane() == 0) { o[0] = so; o[2] = sd; o[3] = mo; }
         }
         if (more) Rc = Rn;
     }
@@ -685,19 +688,21 @@ extern "C" int zs_dbg_walk_stats(unsigned long long* out) {
 }
 #endif
 
-// Launches one kernel of the row sums: 0 zs_k_sapx, then zs_k_sround<s> and
-// zs_k_sstitch<s> as 1, 2 (s = 1), 3, 4 (s = 2), 5, 6 (s = 3).
+// Launches one kernel of the row sums: 0 zs_k_sapx<1>, 1 zs_k_sround<1>,
+// 2 zs_k_sstitch<1> (the sampler's S); 3 zs_k_sapx<2>, 4 zs_k_sround<2>,
+// 5 zs_k_sstitch<2> (S_obs), 6 zs_k_sround<3>, 7 zs_k_sstitch<3> (entropy).
 extern "C" int zs_sums_launch(const zs_sargs& a, uint32_t which, hipStream_t stream) {
     const uint32_t nsub = (a.b.V + ZS_SUB - 1) / ZS_SUB;
     const dim3 grid((nsub + SM_SPB - 1) / SM_SPB, a.b.B);
     switch (which) {
-        case 0: hipLaunchKernelGGL(zs_k_sapx, grid, dim3(SM_NT), 0, stream, a); break;
+        case 0: hipLaunchKernelGGL(zs_k_sapx<1>, grid, dim3(SM_NT), 0, stream, a); break;
         case 1: hipLaunchKernelGGL(zs_k_sround<1>, grid, dim3(SM_NT), 0, stream, a); break;
         case 2: hipLaunchKernelGGL(zs_k_sstitch<1>, dim3(a.b.B), dim3(SW_NT), 0, stream, a); break;
-        case 3: hipLaunchKernelGGL(zs_k_sround<2>, grid, dim3(SM_NT), 0, stream, a); break;
-        case 4: hipLaunchKernelGGL(zs_k_sstitch<2>, dim3(a.b.B), dim3(SW_NT), 0, stream, a); break;
-        case 5: hipLaunchKernelGGL(zs_k_sround<3>, grid, dim3(SM_NT), 0, stream, a); break;
-        case 6: hipLaunchKernelGGL(zs_k_sstitch<3>, dim3(a.b.B), dim3(SW_NT), 0, stream, a); break;
+        case 3: hipLaunchKernelGGL(zs_k_sapx<2>, grid, dim3(SM_NT), 0, stream, a); break;
+        case 4: hipLaunchKernelGGL(zs_k_sround<2>, grid, dim3(SM_NT), 0, stream, a); break;
+        case 5: hipLaunchKernelGGL(zs_k_sstitch<2>, dim3(a.b.B), dim3(SW_NT), 0, stream, a); break;
+        case 6: hipLaunchKernelGGL(zs_k_sround<3>, grid, dim3(SM_NT), 0, stream, a); break;
+        case 7: hipLaunchKernelGGL(zs_k_sstitch<3>, dim3(a.b.B), dim3(SW_NT), 0, stream, a); break;
         default: return -1;
     }
     return hipGetLastError() == hipSuccess ? 0 : -1;
