@@ -1,8 +1,10 @@
 """Calibrations of the fast approximations behind certified results: the
 fast f32 exp of the exact sums (relative error below 2^-22 over every input
 of its domain, for the band ZS_EXP_EPS = 2^-21),
-the cheaper exp of the observers' sums (below 2^-17) and the fast Gumbel term of the lane's
-BSAMPLE (within ZS_GUMBEL_EPS / 4 of the exact term for all 2^24 uniforms).
+the cheaper exp of the grid predictions (below 2^-17; only the predictions
+use it, so a larger error would cost time, never exactness) and the fast
+Gumbel term of the lane's BSAMPLE (within ZS_GUMBEL_EPS / 4 of the exact term
+for all 2^24 uniforms). The sweeps print the measured exponents.
 
 The sweeps are test programs (tests/c/calib_*.hip), not part of the
 library: this test compiles each with the library's flags when the binary is
