@@ -285,3 +285,43 @@ def test_top_logprobs_near_collisions():
     out = run_gpu(x, params)
     errs = compare(x, params, out, refs=refs)
     assert not errs, "\n".join(errs[:20])
+
+
+def test_split_rows_across_halves():
+    """Small batches stream each full row with two workgroups (halves of the
+    row, merged by the one that finishes second): statistics, candidate lists
+    and small-survivor sets that straddle the halves must merge to the
+    oracle's results bit for bit."""
+    B, V = 12, 151936
+    mid = (V + 2047) // 2048 // 2 * 2048          # first id of the second half
+    rng = np.random.default_rng(77)
+    x = synth.logits_powerlaw(B, V, 77)
+    x[0, mid + 5] = np.nan                        # greedy: a NaN in the second half restarts the fold there
+    x[0, 10] = 40.0
+    x[1, :] = -np.inf                             # 300 + 150 finite values over both halves: one small set
+    x[1, rng.choice(mid, 300, replace=False)] = rng.normal(0, 2, 300)
+    x[1, mid + rng.choice(V - mid, 150, replace=False)] = rng.normal(0, 2, 150)
+    x[2, :] = -np.inf                             # 300 + 300: past the small-set cap
+    x[2, rng.choice(mid, 300, replace=False)] = rng.normal(0, 2, 300)
+    x[2, mid + rng.choice(V - mid, 300, replace=False)] = rng.normal(0, 2, 300)
+    x[3, :] = -np.inf                             # fewer finite values than top_logprobs candidates
+    x[3, [5, mid + 9]] = [1.0, 2.0]
+    x[4, :] = 0.5                                 # equal values in both halves: ids decide
+    x[5, mid:mid + 64] = 30.0                     # the top entries all in the second half
+    x[6, mid - 32:mid + 32] = 25.0                # top entries across the boundary
+    x[7, V - 1] = 50.0                            # the last id
+    params = [dict(temperature=0.0, top_logprobs=5),
+              dict(temperature=0.9, top_k=0, top_p=0.95, seed=1, top_logprobs=5),
+              dict(temperature=0.9, top_k=0, top_p=0.95, seed=2, top_logprobs=5),
+              dict(temperature=1.0, top_k=0, top_p=1.0, seed=3, top_logprobs=20),
+              dict(temperature=1.0, top_k=20, top_p=0.9, seed=4, top_logprobs=20),
+              dict(temperature=0.7, top_k=50, top_p=1.0, seed=5, top_logprobs=5),
+              dict(temperature=1.2, top_k=128, top_p=0.9, seed=6, top_logprobs=10),
+              dict(temperature=float("inf"), top_k=0, top_p=1.0, seed=7, top_logprobs=3),
+              dict(temperature=1.0, top_k=300, top_p=0.8, seed=8, top_logprobs=5),
+              dict(temperature=0.8, top_k=0, top_p=0.9, seed=9, top_logprobs=5, repeat=1.2,
+                   counts=[(int(i), 2) for i in rng.choice(V, 1000, replace=False)]),
+              dict(temperature=1.0, top_k=0, top_p=0.5, seed=10, top_logprobs=5, min_p=0.02),
+              dict(temperature=0.0, top_logprobs=3)]
+    x[11, [3, mid + 3]] = 60.0                    # greedy tie across the halves: the last one wins
+    _run(x, params)

@@ -123,7 +123,7 @@ extern "C" void zs_ctx_destroy(zs_ctx* ctx) {
         }
     if (ctx->lane_host) (void)hipHostFree(ctx->lane_host);
     void* ptrs[] = {ctx->p_cnt, ctx->p_id, ctx->p_flags, ctx->p_y, ctx->rst, ctx->pairs, ctx->pv, ctx->mask_scratch, ctx->spec_chunks,
-                    ctx->spec_rows, ctx->p_sub, ctx->k_ap, ctx->k_sum, ctx->s_rec, ctx->s_apx, ctx->gath, ctx->s_hterm, ctx->tp_bk, ctx->tp_cl, ctx->tp_pre, ctx->kcnt, ctx->tp_task,
+                    ctx->spec_rows, ctx->p_sub, ctx->k_ap, ctx->k_sum, ctx->s_rec, ctx->s_apx, ctx->gath, ctx->s_hterm, ctx->tp_bk, ctx->tp_cl, ctx->tp_pre, ctx->kcnt, ctx->tp_task, ctx->rw_part, ctx->rw_ctr,
                     ctx->lane_temp, ctx->lane_vals, ctx->lane_ih, ctx->lane_keys,
                     ctx->lane_idxs, ctx->lane_ck, ctx->lane_cn};
     for (void* p : ptrs)
@@ -186,6 +186,11 @@ extern "C" int zs_ctx_create(int device, uint32_t max_rows, uint32_t max_vocab, 
     if (!rc) rc = zs_alloc(ctx, &ctx->tp_pre, R * (size_t)max_vocab * 2 + 8);  // 16-byte loads at the tail
     if (!rc) rc = zs_alloc(ctx, &ctx->kcnt, R * C * 2);
     if (!rc) rc = zs_alloc(ctx, &ctx->tp_task, 1 + R * ZS_TP_CAND);
+    if (!rc) rc = zs_alloc(ctx, &ctx->rw_part, R * 2 * ZS_ROW_PART);
+    if (!rc) rc = zs_alloc(ctx, &ctx->rw_ctr, R);
+    // (set-up only, outside any stream work a caller could capture)
+    if (!rc && (hipMemset(ctx->rw_ctr, 0, R * sizeof(uint32_t)) != hipSuccess || hipDeviceSynchronize() != hipSuccess))
+        rc = ZS_EHIP;
     if (!rc) rc = zs_alloc(ctx, &ctx->spec_rows, R);
     // the lane knobs in one block laid out as the staging areas (temp, top_k,
     // top_p, seed; R each): one copy per call

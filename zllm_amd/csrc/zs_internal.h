@@ -66,6 +66,7 @@ struct zs_sub_sum {
 #define ZS_MODE_BIG 2u    // big-row engine must run
 
 #define ZS_OBS_CAND 28
+#define ZS_ROW_PART 560   // u64 per (row, half) slot of a split row in zs_k_row
 
 // Observer needs (zs_row_state.obs_need).
 #define ZS_OBS_S 1u   // exact sequential sum S = sum exp(x~ - max)
@@ -177,6 +178,8 @@ struct zs_ctx {
     uint32_t* tp_cl;             // [rows][ZS_TP_CL] row flags, candidate count, candidate buckets
     uint32_t* tp_pre;            // [rows][2][max_vocab] increment prefixes of presorted buckets
     uint32_t* kcnt;              // [rows][2 * max_chunks] kept-set counts per 4096-id group
+    unsigned long long* rw_part; // [rows][2][ZS_ROW_PART] the two halves of a split row (zs_k_row)
+    uint32_t* rw_ctr;            // [rows] halves finished (0 between calls)
     uint32_t* tp_task;           // [1 + rows * ZS_TP_CAND] buckets to presort: count, then (row << 8 | candidate)
     uint32_t* p_sub;             // [rows][max_subs+1] patch index range per sub-chunk
     uint32_t max_subs;

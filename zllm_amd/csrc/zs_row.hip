@@ -50,6 +50,11 @@ __device__ unsigned long long rw_dbg[16];
 #define RW_G 2048          // ids per tile: one float4 per thread
 #define RW_BUF 2048        // candidate buffer entries (per list)
 #define RW_KEEP 1024       // a list above this is compacted to its top K
+// per (row, half) slot of a split row: statistics, then the observers' and
+// the sampler's list entries
+#define RW_PART_O 16
+#define RW_PART_S (RW_PART_O + 32)
+#define RW_PART (RW_PART_S + ZS_SMALL_CAP)
 
 struct rw_shared {
     uint32_t pid[4096];             // the patch list's head (ZS_PATCH_LDS): ids (sorted) | flags << 30
@@ -70,6 +75,7 @@ struct rw_shared {
     float fcut[2];                  // largest values cut from the lists
     unsigned long long rl[RW_NW];
     uint32_t n_surv, tok;
+    uint32_t merge;                 // split rows: the halves that finished before this one
     uint32_t ovf[3];                // first tile that lost a list entry, per group slot
     uint32_t thr_o, thr_s;          // candidate admission thresholds (keys)
     float fsh;
@@ -321,7 +327,8 @@ struct rw_row {
     uint32_t V, np, words;
     uint32_t ldm4, wmax;            // last float4 of the row, last readable word
     uint32_t amask;                 // 15 for an unmasked row, else 0
-    uint32_t glast;                 // the row's last tile
+    uint32_t glast;                 // the last tile of the streamed range
+    uint32_t vend, gend;            // the streamed range's end: id (its ids >= vend read -inf) and tile
 };
 struct rw_raw {
     float4 v;
@@ -393,30 +400,30 @@ __device__ __forceinline__ void rw_elems(const rw_row& R, uint32_t g, const rw_r
     const bool last = g >= R.glast;   // uniform
     if (last) {
 #pragma unroll
-        for (int q = 0; q < 4; q++) x[q] = idx0 + q < R.V ? x[q] : -INFINITY;
+        for (int q = 0; q < 4; q++) x[q] = idx0 + q < R.vend ? x[q] : -INFINITY;
     }
 #pragma unroll
     for (int q = 0; q < 4; q++) y[q] = x[q];
     if (R.np) {
         const uint32_t wd = raw.pw;
         uint32_t pb = (wd >> (idx0 & 31)) & 15u;
-        if (last) pb = idx0 < R.V ? pb : 0u;
+        if (last) pb = idx0 < R.vend ? pb : 0u;
         if (pb) rw_patch4<GP>(R, idx0, pb, wd, x, y, sh);
     }
 }
 
-// Calls f(g, u, x, y) for the tiles from g_begin in order, in groups of four
-// (u = 0..3, a constant in each unrolled copy: per-tile state of a group can
-// live in registers indexed by u), with four tiles of loads in flight:
-// unrolled by four so that each load stays in its own registers until used
-// (copying a register whose load is outstanding waits for every load). f
+// Calls f(g, u, x, y) for the tiles from g_begin up to R.gend in order, in
+// groups of four (u = 0..3, a constant in each unrolled copy: per-tile state
+// of a group can live in registers indexed by u), with four tiles of loads in
+// flight: unrolled by four so that each load stays in its own registers until
+// used (copying a register whose load is outstanding waits for every load). f
 // returns true (uniformly) to stop; rw_stream then returns that tile's index,
-// else ng. The last group is padded with tiles past the row (ids >= V only),
-// which f must treat as neutral. f must not call functions: a call inside the
+// else R.gend. The last group is padded with tiles past the range (ids >=
+// R.vend, read as -inf), which f must treat as neutral. f must not call functions: a call inside the
 // loop saves the registers of the loads in flight, which waits for them.
 template <bool GP, class F>
 __device__ __forceinline__ uint32_t rw_stream(const rw_row& R, const rw_shared& sh, uint32_t g_begin, const F& f) {
-    const uint32_t ng = (R.V + RW_G - 1) / RW_G;
+    const uint32_t ng = R.gend;
     rw_raw raw[4];
 #pragma unroll
     for (int u = 0; u < 4; u++) {
@@ -475,6 +482,8 @@ struct rw_list {
 #define RW_SEL_CAP 256
 #define RW_SEL_E (RW_BUF / RW_NT)   // list entries per thread
 static_assert(RW_BUF % RW_NT == 0, "the list is spread evenly over the threads");
+static_assert(RW_PART == ZS_ROW_PART && ZS_OBS_CAND <= RW_PART_S - RW_PART_O && ZS_KS + 1 <= ZS_SMALL_CAP,
+              "the split rows' slots hold the lists");
 
 __device__ __noinline__ uint32_t rw_select(int which, uint32_t n, uint32_t K1, uint32_t idlim) {
     rw_shared& sh = rw_sh;
@@ -743,7 +752,10 @@ __device__ __forceinline__ uint32_t rw_block_row(const zs_batch& b, uint32_t j) 
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
     const zs_batch& b = a.b;
-    const uint32_t r = rw_block_row(b, blockIdx.x);
+    // with a.row_split, workgroups B .. 2B - 1 take the second half of their
+    // row's stream (below)
+    const uint32_t half = (a.row_split && blockIdx.x >= b.B) ? 1u : 0u;
+    const uint32_t r = rw_block_row(b, blockIdx.x - half * b.B);
     const uint32_t t = threadIdx.x;
     const uint32_t V = b.V;
     rw_shared& sh = rw_sh;
@@ -758,16 +770,47 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
 #ifdef ZS_WALK_DEBUG
     unsigned long long rw_t0 = wall_clock64();
 #endif
+    const bool greedy = T <= 0.0f;
+    const bool tinf = T == INFINITY;   // y / inf is NaN for y = +-inf: checked per element
+    const uint32_t* allow = ((P.flags & ZS_ROW_MASKED) && b.d_allow_bits) ? b.d_allow_bits + (size_t)r * b.allow_words
+                                                                          : nullptr;
+    // A row that streams the whole row (not a masked row taking its lists from
+    // at most RW_BUF gathered ids) may split the stream over two workgroups
+    // when the batch leaves CUs free (a.row_split), unless its patch list may
+    // pass the LDS head (both workgroups build it). Both halves decide alike.
+    const uint32_t ngt = (V + RW_G - 1) / RW_G;
+    bool split = false;
+    if (a.row_split && ngt >= 8) {
+        const uint32_t nb = b.d_ban_off ? b.d_ban_off[r + 1] - b.d_ban_off[r] : 0u;
+        const uint32_t nbi = b.d_bias_off ? b.d_bias_off[r + 1] - b.d_bias_off[r] : 0u;
+        const uint32_t nc = (b.d_cnt_off && zs_penalty_active(P)) ? b.d_cnt_off[r + 1] - b.d_cnt_off[r] : 0u;
+        if (nb + nbi + nc <= ZS_PATCH_LDS) {
+            if (!allow || greedy || tinf) {
+                split = true;
+            } else {
+                const uint32_t words = (V + 31) / 32;
+                uint32_t c = 0;
+                for (uint32_t w = t; w < words; w += RW_NT) {
+                    uint32_t aw = allow[w];
+                    if (w == words - 1 && (V & 31)) aw &= (1u << (V & 31)) - 1u;
+                    c += (uint32_t)__popc(aw);
+                }
+                split = rw_uni(block_sum_u<RW_NT>(c, sh.ru[4])) > RW_BUF;
+            }
+        }
+    }
+    if (half && !split) return;
 
-    // ---------------- P0: patches
+    // ---------------- P0: patches (the second half builds its own LDS copy
+    // only: the first writes the row's list out)
     uint32_t has_y = 0;
-    const int np = rw_patches(a, r, P, has_y, sh);
+    const int np = rw_patches(a, r, P, has_y, sh, half == 0);
     RW_T(0);
     rw_row R;
     R.gfl = a.p_flags + (size_t)r * a.pstride;
     R.gy = a.p_y + (size_t)r * a.pstride;
     R.row = b.d_logits + (size_t)r * b.ld;
-    R.allow = ((P.flags & ZS_ROW_MASKED) && b.d_allow_bits) ? b.d_allow_bits + (size_t)r * b.allow_words : nullptr;
+    R.allow = allow;
     R.V = V;
     R.np = rw_uni((uint32_t)np);
     R.words = (V + 31) / 32;
@@ -775,15 +818,18 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
     R.allow_or_row = R.allow ? R.allow : reinterpret_cast<const uint32_t*>(R.row);
     R.wmax = R.allow ? R.words - 1 : R.ldm4;
     R.amask = R.allow ? 0u : 15u;
-    R.glast = (V - 1) / RW_G;
+    // the streamed range: the whole row, or this workgroup's half
+    const uint32_t gmid = ngt / 2;
+    const uint32_t gbeg = (split && half) ? gmid : 0u;
+    R.gend = (split && !half) ? gmid : ngt;
+    R.vend = R.gend == ngt ? V : R.gend * RW_G;
+    R.glast = (R.vend - 1) / RW_G;
 
     // ---------------- P1: statistics and candidate lists
     // The sampler's z = y / T (sampler.rs:47-51) is not formed per element
     // here: division by T > 0 is monotone, so the maximum, the order and the
     // top-k of z follow from those of y (ties created by the rounding are
     // checked when the threshold is set).
-    const bool greedy = T <= 0.0f;
-    const bool tinf = T == INFINITY;   // y / inf is NaN for y = +-inf: checked per element
     const bool has_topk = P.top_k > 0 && P.top_k < V;
     // sampler list: 1 = top-k by y (k <= ZS_KS), 2 = every y > -inf (the
     // small-survivor check when no top-k applies), 0 = none
@@ -837,7 +883,7 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
     // values stay live across the stream below)
     bool gath = false;
     if (t == 0) { sh.g_n = 0; sh.g_done = 0; }
-    if (R.allow && !greedy && !tinf) {
+    if (R.allow && !greedy && !tinf && !split) {
         const float* gcx = rw_scratch(a, r);
         const uint32_t gn = rw_gather_allowed(R.row, R.allow, V, R.np, rw_scratch(a, r), R.gfl, R.gy);
         if (t == 0) { sh.g_n = gn; sh.g_done = 1; }
@@ -849,8 +895,9 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
         }
     }
     RW_T(1);
-    uint32_t g = 0;
-    const uint32_t ng = gath ? 0u : (V + RW_G - 1) / RW_G;
+    uint32_t g = gbeg;
+    const uint32_t ng = gath ? 0u : R.gend;
+    const uint32_t Vend = R.vend;
     // the admission thresholds in scalar registers: they change only where
     // the lists are set up (first tile) and compacted (outside the stream)
     float r_tfo = -INFINITY, r_tfs = -INFINITY;
@@ -907,23 +954,25 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
                 fl |= ZS_CF_Z_NAN;
                 last_nan = max(last_nan, (int)(idx0 + 31 - __clz(ny)));
             }
+            // valid ids of the thread (the last tile only is partial)
+            const uint32_t vm = idx0 + 4 <= Vend ? 15u : (idx0 >= Vend ? 0u : (1u << (Vend - idx0)) - 1u);
             if (tinf) {
+                // y / inf is NaN for a real y = +-inf (ids past the range read
+                // -inf and are no elements)
 #pragma unroll
                 for (int q = 0; q < 4; q++)
-                    if (y[q] == INFINITY || y[q] == -INFINITY) fl |= ZS_CF_Z_NAN;
+                    if (((vm >> q) & 1u) && (y[q] == INFINITY || y[q] == -INFINITY)) fl |= ZS_CF_Z_NAN;
             }
             if (greedy) {
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    if (y[q] != y[q] || idx0 + q >= V) continue;
+                    if (y[q] != y[q] || idx0 + q >= Vend) continue;
                     // -0.0 and +0.0 compare equal in the reference (partial_cmp)
                     const uint32_t k = zs_total_key(y[q] == 0.0f ? 0.0f : y[q]);
                     const unsigned long long c = ((unsigned long long)k << 32) | (idx0 + q + 1);
                     gbest = c > gbest ? c : gbest;
                 }
             }
-            // valid ids of the thread (the last tile only is partial)
-            const uint32_t vm = idx0 + 4 <= V ? 15u : (idx0 >= V ? 0u : (1u << (V - idx0)) - 1u);
             if (!thr_init) {
                 // initial thresholds (first tile): in every wave the c-th largest
                 // thread maximum has at least c elements of that wave at or above
@@ -1093,7 +1142,7 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
             uint32_t kx[4], ky[4];
             keys(x, y, kx, ky);
             const uint32_t idx0 = ovf * RW_G + 4 * t;
-            const uint32_t vm = idx0 + 4 <= V ? 15u : (idx0 >= V ? 0u : (1u << (V - idx0)) - 1u);
+            const uint32_t vm = idx0 + 4 <= Vend ? 15u : (idx0 >= Vend ? 0u : (1u << (Vend - idx0)) - 1u);
             uint32_t po = 0, ps = 0;
             for (int round = 0; ; round++) {
                 // the tile's elements above the current thresholds, minus those placed
@@ -1181,6 +1230,68 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
             gbest = sh.rl[w] > gbest ? sh.rl[w] : gbest;
         }
         __syncthreads();
+    }
+    if (split) {
+        // This half's lists cut to what the row can need from it: the first
+        // Ko observers, the sampler's first Ks + 1 (the next one counts as
+        // turned away), or its small-survivor list. They go to the half's
+        // slot with its statistics; the half that finishes second merges the
+        // other's slot into its own and goes on alone (no waiting: the first
+        // to finish leaves).
+        uint32_t no = 0, ns = 0;
+        if (Ko) no = min(rw_select(0, min(n_o, (uint32_t)RW_BUF), Ko, 0xffffffffu), Ko);
+        if (smode == 1) {
+            const uint32_t c = rw_select(1, min(n_s, (uint32_t)RW_BUF), Ks + 2, 0xffffffffu);
+            if (c > Ks + 1) rejf = fmaxf(rejf, zs_key_to_float(~(uint32_t)(sh.u.b.s[Ks + 1] >> 32)));
+            ns = min(c, Ks + 1);
+        } else if (smode == 2 && !s_over) {
+            ns = n_s;   // at most ZS_SMALL_CAP
+        }
+        RW_T(15);
+        unsigned long long* mine = a.rw_part + ((size_t)r * 2 + half) * RW_PART;
+        if (t == 0) {
+            mine[0] = (unsigned long long)__float_as_uint(omax) | ((unsigned long long)__float_as_uint(ymax) << 32);
+            mine[1] = (unsigned long long)fl | ((unsigned long long)(uint32_t)last_nan << 32);
+            mine[2] = (unsigned long long)__float_as_uint(rejf) | ((unsigned long long)(s_over ? 1u : 0u) << 32);
+            mine[3] = gbest;
+            mine[4] = (unsigned long long)no | ((unsigned long long)ns << 32);
+        }
+        for (uint32_t i = t; i < no; i += RW_NT) mine[RW_PART_O + i] = sh.u.b.o[i];
+        for (uint32_t i = t; i < ns; i += RW_NT) mine[RW_PART_S + i] = sh.u.b.s[i];
+        __threadfence();
+        __syncthreads();
+        if (t == 0) sh.merge = atomicAdd(&a.rw_ctr[r], 1u);
+        __syncthreads();
+        RW_T(6);
+        if (rw_uni(sh.merge) == 0u) return;   // the other half merges
+        if (t == 0) a.rw_ctr[r] = 0u;         // for the next call
+        __threadfence();
+        const unsigned long long* oth = a.rw_part + ((size_t)r * 2 + (1u - half)) * RW_PART;
+        const unsigned long long h0 = oth[0], h1 = oth[1], h2 = oth[2], h3 = oth[3], h4 = oth[4];
+        omax = fmaxf(omax, __uint_as_float((uint32_t)h0));
+        ymax = fmaxf(ymax, __uint_as_float((uint32_t)(h0 >> 32)));
+        fl |= (uint32_t)h1;
+        last_nan = max(last_nan, (int)(uint32_t)(h1 >> 32));
+        rejf = fmaxf(rejf, __uint_as_float((uint32_t)h2));
+        const bool o_over = (h2 >> 32) != 0ull;
+        gbest = h3 > gbest ? h3 : gbest;
+        const uint32_t ono = (uint32_t)h4, ons = (uint32_t)(h4 >> 32);
+        for (uint32_t i = t; i < ono; i += RW_NT) sh.u.b.o[no + i] = oth[RW_PART_O + i];
+        n_o = no + ono;
+        if (smode == 1) {
+            for (uint32_t i = t; i < ons; i += RW_NT) sh.u.b.s[ns + i] = oth[RW_PART_S + i];
+            n_s = ns + ons;
+        } else if (smode == 2) {
+            s_over = s_over || o_over || ns + ons > ZS_SMALL_CAP;
+            if (!s_over)
+                for (uint32_t i = t; i < ons; i += RW_NT) sh.u.b.s[ns + i] = oth[RW_PART_S + i];
+            n_s = ns + ons;
+        }
+        __syncthreads();
+        // later streams (the greedy fold after a NaN) cover the whole row
+        R.gend = ngt;
+        R.vend = V;
+        R.glast = (V - 1) / RW_G;
     }
     const float M = rw_unif(omax);
     const float zmax = rw_unif(zs_temper(ymax, T));   // max z = temper(max y): monotone
@@ -1379,6 +1490,6 @@ extern "C" int zs_dbg_row_stats(unsigned long long* out) {
 
 extern "C" int zs_row_launch(const zs_sargs& a, hipStream_t stream) {
     const size_t dyn = 4 * ((a.b.V + 31) / 32) * sizeof(uint32_t);
-    hipLaunchKernelGGL(zs_k_row, dim3(a.b.B), dim3(RW_NT), dyn, stream, a);
+    hipLaunchKernelGGL(zs_k_row, dim3(a.row_split ? 2 * a.b.B : a.b.B), dim3(RW_NT), dyn, stream, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

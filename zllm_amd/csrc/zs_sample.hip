@@ -118,8 +118,11 @@ __device__ __forceinline__ void big_finish(const big_row& R, uint32_t g, const b
             }
         }
     }
+    // (-inf stays -inf: with T = inf, -inf / T is NaN, but a row with a real
+    // -inf element is non-finite and never reaches these kernels; the -inf
+    // here are ids past the row)
 #pragma unroll
-    for (int q = 0; q < 4; q++) z[q] = zs_temper(z[q], R.T);
+    for (int q = 0; q < 4; q++) z[q] = z[q] == -INFINITY ? -INFINITY : zs_temper(z[q], R.T);
 }
 __device__ __forceinline__ void big_load2(const big_row& R, uint32_t g, float (&x)[4], float (&z)[4],
                                           big_shared& sh) {
@@ -1821,6 +1824,11 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
     a.tp_pre = ctx->tp_pre;
     a.kcnt = ctx->kcnt;
     a.tp_task = ctx->tp_task;
+    a.rw_part = ctx->rw_part;
+    a.rw_ctr = ctx->rw_ctr;
+    // rows split their stream over two workgroups when the batch leaves the
+    // second workgroups CUs of their own
+    a.row_split = 2 * bt->B <= ctx->num_cus ? 1u : 0u;
     a.s_rec = ctx->s_rec;
     a.s_apx = ctx->s_apx;
     a.gath = ctx->gath;

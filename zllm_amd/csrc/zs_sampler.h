@@ -32,15 +32,18 @@ struct zs_sargs {
     float* gath;
     float* s_hterm;
     uint32_t pstride;   // entries per row of the merged patch list (p_id, p_flags, p_y): max_vocab
+    uint32_t row_split; // zs_k_row: 2B workgroups, rows may split their stream in two halves
+    unsigned long long* rw_part;
+    uint32_t* rw_ctr;
 };
 
 #define ZS_ST_FALLBACK 0x200u
 
-// zs_row.hip: the one-workgroup-per-row front of the step (patches, row
-// statistics, candidates, greedy / small rows, the exact S and entropy sums)
+// zs_row.hip: the per-row front of the step (patches, row statistics,
+// candidates, greedy and small rows)
 extern "C" int zs_row_launch(const zs_sargs& a, hipStream_t stream);
-// zs_sums.hip: the row sums S_obs and the sampler's S, then the entropy,
-// spread over the GPU (one kernel per call, `which` 0..4 in launch order)
+// zs_sums.hip: the row sums (the big rows' sampler S; S_obs, then the
+// entropy) spread over the GPU (one kernel per call, `which` 0..7)
 extern "C" int zs_sums_launch(const zs_sargs& a, uint32_t which, hipStream_t stream);
 
 __device__ __forceinline__ bool zs_penalty_active(const zs_row_params& P) {

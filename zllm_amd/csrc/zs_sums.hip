@@ -266,7 +266,10 @@ __device__ __forceinline__ sm_terms sm_terms_of(int kind, const zs_row_state& st
 // y rT; other y (and other T) divide the IEEE way.
 __device__ __forceinline__ float sm_temper(const sm_terms& f, float y) {
     if (f.div == 0u) return y;
-    if (f.div == 2u) return y / f.T;
+    // (-inf / inf is NaN; a row with T = inf and a real -inf element is
+    // non-finite and sums nothing, so its -inf terms here are ids past the
+    // row: no term)
+    if (f.div == 2u) return y == -INFINITY ? -INFINITY : y / f.T;
     const float q0 = y * f.rT;
     const float q1 = fmaf(fmaf(-q0, f.T, y), f.rT, q0);
     const float a = fabsf(y);
