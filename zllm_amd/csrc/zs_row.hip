@@ -1258,14 +1258,22 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
         }
         for (uint32_t i = t; i < no; i += RW_NT) mine[RW_PART_O + i] = sh.u.b.o[i];
         for (uint32_t i = t; i < ns; i += RW_NT) mine[RW_PART_S + i] = sh.u.b.s[i];
-        __threadfence();
+        // (the barrier completes every wave's stores; one device-scope fence
+        // then publishes them before the count, and one makes the other
+        // half's visible after it)
         __syncthreads();
-        if (t == 0) sh.merge = atomicAdd(&a.rw_ctr[r], 1u);
+        if (t == 0) {
+            __threadfence();
+            const uint32_t m = atomicAdd(&a.rw_ctr[r], 1u);
+            if (m) {
+                a.rw_ctr[r] = 0u;   // for the next call
+                __threadfence();
+            }
+            sh.merge = m;
+        }
         __syncthreads();
         RW_T(6);
         if (rw_uni(sh.merge) == 0u) return;   // the other half merges
-        if (t == 0) a.rw_ctr[r] = 0u;         // for the next call
-        __threadfence();
         const unsigned long long* oth = a.rw_part + ((size_t)r * 2 + (1u - half)) * RW_PART;
         const unsigned long long h0 = oth[0], h1 = oth[1], h2 = oth[2], h3 = oth[3], h4 = oth[4];
         omax = fmaxf(omax, __uint_as_float((uint32_t)h0));
