@@ -135,6 +135,7 @@ struct sm_wsh {
     uint32_t first[SW_NW];                 // zero sums: first nonzero term per wave
     float hs;
     uint32_t hstop;
+    alignas(16) float hv[SW_TPT * 64];     // the head: one wave's terms, added one by one from here
     sm_rec rec[ZS_MAX_SUBS];               // the records of the sum being stitched
 };
 __shared__ sm_wsh sm_sh;
@@ -228,19 +229,39 @@ __device__ __forceinline__ float sm_walk(const float (&v)[SW_TPT], float s, floa
             const bool thr = thresh == thresh;
             for (uint32_t w = w0; w <= w1; w++) {
                 if (wid == w) {
+                    // the wave's terms to LDS in term order, then every lane
+                    // adds the same ones in order (broadcast reads, no lane
+                    // reads); the terms are non-negative, so the running sum
+                    // never decreases and one test per 4 terms finds the stop
                     float ss = w != w0 ? sh.hs : s;
                     uint32_t sp = w != w0 ? sh.hstop : 0xffffffffu;
                     const uint32_t base = SW_TPT * 64 * w;
-                    const uint32_t Lb = first > base ? (first - base) / SW_TPT : 0u;
-                    const uint32_t Le = min(64u, (end - base + SW_TPT - 1) / SW_TPT);
-                    for (uint32_t L = Lb; L < Le && sp == 0xffffffffu; L++) {
-#pragma unroll
-                        for (int q = 0; q < SW_TPT; q++) {
-                            const uint32_t e = base + SW_TPT * L + (uint32_t)q;
-                            const bool in = e >= first && e < end && sp == 0xffffffffu;
-                            const float nv = ss + sm_lane_f(v[q], L);
-                            ss = in ? nv : ss;
-                            if (thr && in && nv >= thresh) sp = e;
+                    *reinterpret_cast<float4*>(&sh.hv[SW_TPT * lane]) = make_float4(v[0], v[1], v[2], v[3]);
+                    __builtin_amdgcn_s_waitcnt(0);
+                    __builtin_amdgcn_wave_barrier();
+                    const uint32_t e0 = first > base ? first - base : 0u, e1 = min(end - base, SW_TPT * 64u);
+                    uint32_t e = sp == 0xffffffffu ? e0 : e1;   // (stopped in the wave before: nothing)
+                    for (; e < e1 && (e & 3u); e++) {   // to a multiple of 4
+                        ss = ss + sh.hv[e];
+                        if (thr && ss >= thresh) { sp = base + e; break; }
+                    }
+                    if (sp == 0xffffffffu) {
+                        for (; e + 4 <= e1; e += 4) {
+                            const float4 q4 = *reinterpret_cast<const float4*>(&sh.hv[e]);
+                            const float c1 = ss + q4.x, c2 = c1 + q4.y, c3 = c2 + q4.z, c4 = c3 + q4.w;
+                            if (thr && c4 >= thresh) {
+                                const uint32_t k = c1 >= thresh ? 0u : c2 >= thresh ? 1u : c3 >= thresh ? 2u : 3u;
+                                ss = k == 0u ? c1 : k == 1u ? c2 : k == 2u ? c3 : c4;
+                                sp = base + e + k;
+                                break;
+                            }
+                            ss = c4;
+                        }
+                    }
+                    if (sp == 0xffffffffu) {
+                        for (; e < e1; e++) {
+                            ss = ss + sh.hv[e];
+                            if (thr && ss >= thresh) { sp = base + e; break; }
                         }
                     }
                     if (lane == 0) { sh.hs = ss; sh.hstop = sp; }
