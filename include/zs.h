@@ -113,6 +113,11 @@ int zs_dfa_mask(zs_ctx* ctx, const zs_dfa* dfa, const zs_vocab* vocab, const int
  * zs_dfa_mask walks all its rows. The reference has no call for this (its
  * cache lives as long as the engine); it is for timing the walk. */
 void zs_dfa_memo_clear(zs_dfa* dfa);
+/* The form zs_dfa_mask walks the table in (host only): 0 bit-packed rows in
+ * LDS, 1 sparse rows in LDS, 2 displaced rows in LDS, 3 none fits the LDS
+ * budget (the L2-resident walk). No counterpart in the reference (its DFA
+ * walk is on the CPU); for tests and tuning. */
+int zs_dfa_table_form(const zs_dfa* dfa);
 
 /* ---- grammar compilers (host only: no context, no GPU) -----------------
  * Replace regex-automata's dense::Builder (logit_fsm.rs:62-88: anchored start,

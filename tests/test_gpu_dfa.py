@@ -138,6 +138,46 @@ def test_large_random_dfa_through_l2():
         assert np.array_equal(bits[i], want), (i, s)
 
 
+def _class_dfa(S, ncls, per_state, seed):
+    """S states over ncls byte classes (byte b in class b % ncls); every state
+    has `per_state` classes into random states, the rest into the dead state
+    S - 1; a third of the states accept."""
+    rng = np.random.default_rng(seed)
+    trans = np.full((S, 256), S - 1, np.uint32)
+    for s in range(S - 1):
+        for c in rng.choice(ncls, per_state, replace=False):
+            trans[s, np.arange(c, 256, ncls)] = rng.integers(0, S - 1)
+    dead = np.zeros(S, np.uint8)
+    dead[S - 1] = 1
+    acc = (rng.random(S) < 0.33).astype(np.uint8)
+    acc[S - 1] = 0
+    return trans, dead, acc
+
+
+@pytest.mark.parametrize("S,ncls,per_state,form", [(3000, 40, 4, "displaced"), (3500, 60, 10, "sparse")])
+def test_table_forms_past_the_packed_budget(S, ncls, per_state, form):
+    """Tables too large for bit-packed rows in LDS: displaced rows (one read
+    and a compare per step) and, where those do not fit either, sparse rows.
+    Bitsets equal the oracle's for every row."""
+    V = 8000
+    print(f"[case] form={form} S={S} ncls={ncls} per_state={per_state}", flush=True)
+    offs, data = synth.synthetic_vocab(V, 91)
+    valid = np.ones(V, np.uint8)
+    trans, dead, acc = _class_dfa(S, ncls, per_state, 92)
+    rng = np.random.default_rng(93)
+    states = list(rng.integers(0, S - 1, 12)) + [-1]
+    bits, anyv, dfa, table = _gpu_bits(trans, dead, acc, (offs, data, valid), V - 1, states, V)
+    assert dfa.table_form == form
+    tokens = [bytes(data[offs[t]:offs[t + 1]]) for t in range(V)]
+    od, ov = O.Dfa(trans, dead, acc), O.Vocab(tokens, V - 1)
+    nonzero = 0
+    for i, s in enumerate(states):
+        want = O.pack_bits(np.ones(V, bool)) if s < 0 else O.mask_bits(V, dfa=od, vocab=ov, state=int(s))
+        assert np.array_equal(bits[i], want), (form, i, s)
+        nonzero += int(s >= 0 and want[: (V - 1) // 32].any())
+    assert nonzero > 0
+
+
 COMPILED = {
     "json": "json:",
     "tool_schema": 'json_schema:{"type":"object","properties":{"location":{"type":"string"},'
@@ -169,6 +209,8 @@ def test_compiled_grammar_masks(name):
     table = TokenByteTable.from_csr(c, offs, data, valid, eos)
     fsm = LogitFSM.compile(g, table)
     assert fsm.state == host.start and fsm.dfa.nstates == host.nstates
+    if g == "json:":
+        assert fsm.dfa.table_form == "displaced"
     tokens = [None if not valid[t] else bytes(data[offs[t]:offs[t + 1]]) for t in range(V)]
     od, ov = O.Dfa(host.trans, host.dead, host.accept), O.Vocab(tokens, eos)
     # states along a walk that always takes an allowed token

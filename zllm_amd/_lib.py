@@ -119,6 +119,7 @@ SIGNATURES = {
     "zs_dfa_mask": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32,
                               C.c_void_p, C.c_void_p, C.c_void_p]),
     "zs_dfa_memo_clear": (None, [C.c_void_p]),
+    "zs_dfa_table_form": (C.c_int, [C.c_void_p]),
     "zs_sample": (C.c_int, [C.c_void_p, C.POINTER(Batch), C.c_void_p]),
     "zs_set_profiling": (C.c_int, [C.c_void_p, C.c_int]),
     "zs_spec_verify": (C.c_int, [C.c_void_p, C.POINTER(SpecBatch), C.c_void_p]),

@@ -500,6 +500,76 @@ extern "C" int zs_dfa_create(zs_ctx* ctx, const uint32_t* h_trans, uint32_t nsta
     }
     d->rw = rw;
     d->packed_lds = packed.size() * 4 <= ZS_DFA_LDS_BYTES && rw < 65536 ? 1 : 0;
+    uint32_t staged_words = 0;   // LDS-staged words of a form followed by its base map
+    if (!d->packed_lds) {
+        // Displaced rows (the double-array layout of a trie): good state g
+        // gets a distinct base b_g, and its transition on class c is entry
+        // b_g + c = b_g << 16 | b_target; an entry whose upper half is not the
+        // reading state's base (another state's entry, or an empty one,
+        // 0xffffffff) is a fail. A walk step is one 32-bit LDS read and a
+        // compare. Bases are placed first-fit, states with the most
+        // transitions first; the fail value F is a base no state owns.
+        std::vector<uint32_t> order(ngood), nt(ngood, 0), gs(ngood);
+        for (uint32_t s = 0; s < nstates; s++) {
+            if (bad[s]) continue;
+            const uint32_t g = remap[s];
+            gs[g] = s;
+            for (uint32_t c = 0; c < ncls; c++) nt[g] += cols[c][s] != 0xffffu;
+        }
+        for (uint32_t g = 0; g < ngood; g++) order[g] = g;
+        std::stable_sort(order.begin(), order.end(), [&](uint32_t x, uint32_t y) { return nt[x] > nt[y]; });
+        std::vector<uint8_t> occ, isbase;
+        std::vector<uint32_t> base(ngood, 0);
+        auto grow = [&](size_t n) {
+            if (occ.size() < n) occ.resize(n, 0), isbase.resize(n, 0);
+        };
+        uint32_t first_free = 0, nent = 0;
+        std::vector<uint32_t> cs;
+        for (uint32_t g : order) {
+            const uint32_t s = gs[g];
+            cs.clear();
+            for (uint32_t c = 0; c < ncls; c++)
+                if (cols[c][s] != 0xffffu) cs.push_back(c);
+            uint32_t b = cs.empty() ? 0 : (first_free > cs[0] ? first_free - cs[0] : 0);
+            for (;; b++) {
+                grow((size_t)b + ncls + 1);
+                if (isbase[b]) continue;
+                bool ok = true;
+                for (uint32_t c : cs)
+                    if (occ[b + c]) { ok = false; break; }
+                if (ok) break;
+            }
+            base[g] = b;
+            isbase[b] = 1;
+            for (uint32_t c : cs) occ[b + c] = 1;
+            while (first_free < occ.size() && occ[first_free]) first_free++;
+            nent = std::max(nent, b + ncls);
+        }
+        uint32_t F = 0;
+        while (F < isbase.size() && isbase[F]) F++;
+        nent = std::max(nent, F + ncls);
+        const size_t words = ((size_t)nent + 3) & ~(size_t)3;
+        if (F < 0xffffu && nent <= 0xffffu && (words + ZS_DFA_RD_ROWS / 2) * 4 <= ZS_DFA_LDS_BYTES) {
+            std::vector<uint32_t> rd(words, 0xffffffffu);
+            for (uint32_t g = 0; g < ngood; g++) {
+                const uint32_t s = gs[g];
+                for (uint32_t c = 0; c < ncls; c++) {
+                    const uint16_t tgt = cols[c][s];
+                    if (tgt != 0xffffu) rd[base[g] + c] = base[g] << 16 | base[remap[tgt]];
+                }
+            }
+            // then (not staged) the base of every state by its original id
+            staged_words = (uint32_t)rd.size();
+            rd.resize(rd.size() + (nstates + 1) / 2, 0u);
+            uint16_t* map = reinterpret_cast<uint16_t*>(rd.data() + staged_words);
+            for (uint32_t s = 0; s < nstates; s++) map[s] = bad[s] ? (uint16_t)F : (uint16_t)base[remap[s]];
+            packed.swap(rd);
+            for (uint32_t b = 0; b < 256; b++) clsinfo[b] = cls[b];
+            d->sparse = 2;
+            d->rd_fail = F;
+            d->packed_lds = 1;
+        }
+    }
     if (!d->packed_lds && ncls <= 64) {
         // Sparse rows for tables past the LDS budget (large grammars are
         // mostly fail entries): per good state {class mask lo, hi, first
@@ -556,7 +626,7 @@ extern "C" int zs_dfa_create(zs_ctx* ctx, const uint32_t* h_trans, uint32_t nsta
     if (!rc && d->memo_slots && hipMemset(d->d_memo_key, 0, (size_t)d->memo_slots * 8) != hipSuccess)
         rc = zs_set_error(ctx, ZS_EHIP, "zs_dfa_create: memo clear failed");
     if (!rc) {
-        d->packed_words = (uint32_t)packed.size();
+        d->packed_words = staged_words ? staged_words : (uint32_t)packed.size();
         hipError_t e = hipMemcpy(d->d_packed, packed.data(), packed.size() * 4, hipMemcpyHostToDevice);
         if (e == hipSuccess) e = hipMemcpy(d->d_clsinfo, clsinfo, 256 * 2, hipMemcpyHostToDevice);
         if (e == hipSuccess) e = hipMemcpy(d->d_remap, remap.data(), nstates * 2, hipMemcpyHostToDevice);
@@ -573,6 +643,11 @@ extern "C" int zs_dfa_create(zs_ctx* ctx, const uint32_t* h_trans, uint32_t nsta
     }
     *out = d;
     return ZS_OK;
+}
+
+extern "C" int zs_dfa_table_form(const zs_dfa* d) {
+    if (!d) return -1;
+    return d->packed_lds ? (int)d->sparse : 3;
 }
 
 extern "C" int zs_dfa_is_live(const zs_dfa* d, uint32_t s) { return (d && s < d->nstates) ? d->h_live[s] : 0; }
@@ -674,6 +749,8 @@ extern "C" int zs_dfa_mask(zs_ctx* ctx, const zs_dfa* dfa, const zs_vocab* vocab
     a.remap = dfa->d_remap;
     a.ngood = dfa->ngood;
     a.sparse = dfa->sparse;
+    a.rd_fail = dfa->rd_fail;
+    a.rdmap = dfa->sparse == 2 ? reinterpret_cast<const uint16_t*>(dfa->d_packed + dfa->packed_words) : nullptr;
     a.dense = dfa->dense;
     a.bits = dfa->bits;
     a.rw = dfa->rw;

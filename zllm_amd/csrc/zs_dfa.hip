@@ -105,8 +105,14 @@ __global__ __launch_bounds__(DM_NT) void zs_k_dfa_mask(dm_args a) {
     }
 }
 
-// Persistent walk over the bit-packed table (good states only, `bits`-bit
-// entries, all ones = fail), with the per-state memo. One workgroup per CU
+// Persistent walk over the table staged in LDS, with the per-state memo. The
+// table is in one of three forms: bit-packed rows (good states only,
+// `bits`-bit entries, ngood = fail), sparse rows (a class mask per state and
+// its targets, for tables past the budget with at most 64 classes) or
+// displaced rows (every state is its base in one array of owner << 16 |
+// target entries: one 32-bit read and a compare per step; the first choice for
+// tables past the budget, since it reads a quarter of the sparse form's bytes
+// per step and leaves the step one read deep). One workgroup per CU
 // stages the table in LDS once and plans the call (every workgroup builds the
 // same plan): each constrained row is either a memo hit (its state's slot is
 // valid) or a walk, and rows sharing a state share one walk, whose result
@@ -146,8 +152,9 @@ __device__ __forceinline__ uint32_t dl_hash(uint32_t g) { return (g * 2654435761
 static_assert(DL_HASH == 2048, "dl_hash yields 11 bits");
 
 // SIDE states per token walked side by side, TG tokens together: 4 x 2 when
-// few states survive a first byte, 8 x 1 for dense automata
-template <bool SPARSE, int SIDE, int TG>
+// few states survive a first byte, 8 x 1 for dense automata. FMT: 0
+// bit-packed rows, 1 sparse rows, 2 displaced rows.
+template <int FMT, int SIDE, int TG>
 __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
     __shared__ uint32_t tab[DL_WORDS];
     __shared__ uint16_t ci[256];
@@ -181,6 +188,9 @@ __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
     if (t < DL_MAXROWS) link[t] = 0xffffu;
     if (t == 0) nwl = 0;
     const uint32_t g = st >= 0 ? a.remap[st] : 0xffffu;   // 0xffff: allows nothing
+    // displaced rows: the row's start state as its base, after the table
+    uint16_t* rbase = reinterpret_cast<uint16_t*>(tab + DL_WORDS - ZS_DFA_RD_ROWS / 2);
+    if (FMT == 2 && t < DL_MAXROWS) rbase[t] = st >= 0 ? a.rdmap[st] : (uint16_t)a.rd_fail;
     // a hit needs this tag; the key also names the call that filled the slot
     // (never this one: keys are written by the EOS kernel after the walk, so
     // every workgroup builds the same plan)
@@ -238,12 +248,19 @@ __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
     // the two words from byte st * rwb + cbw, cbw = the byte offset of the word
     // holding bit cb
     const uint16_t* tgt16 = reinterpret_cast<const uint16_t*>(tab + 4 * (a.ngood + 1));
+    const uint32_t fail = FMT == 2 ? a.rd_fail : a.ngood;  // the sink row
     auto step = [&](uint32_t s, uint32_t cb) -> uint32_t {
-        if (SPARSE) {
+        if (FMT == 2) {
+            // states are their bases: the entry at base + class names its
+            // owner in the upper half
+            const uint32_t e = tab[s + cb];
+            return (e >> 16) == s ? (e & 0xffffu) : fail;
+        }
+        if (FMT == 1) {
             // class mask of the state, then the target at the rank of its class
             const uint4 rec = reinterpret_cast<const uint4*>(tab)[s];
             const unsigned long long mask = ((unsigned long long)rec.y << 32) | rec.x;
-            if (!((mask >> cb) & 1ull)) return a.ngood;
+            if (!((mask >> cb) & 1ull)) return fail;
             return tgt16[rec.z + (uint32_t)__popcll(mask & ((1ull << cb) - 1ull))];
         }
         // states < 2^16, row bytes < 2^13: the byte address fits 24 bits
@@ -251,7 +268,6 @@ __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
         const uint32_t* w = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint8_t*>(tab) + ba);
         return __builtin_amdgcn_alignbit(w[1], w[0], cb) & fmask;
     };
-    const uint32_t fail = a.ngood;  // the sink row
     const uint32_t ncover = a.V > a.ntab ? a.V : a.ntab;
     // states per item: as few groups as fill the grid once (every workgroup
     // builds the same nc, so the same split), at most DL_RG states a group
@@ -285,7 +301,7 @@ __global__ __launch_bounds__(DL_NT) void zs_k_dfa_mask_packed(dm_args a) {
         // byte t & 255 for the states 16 * (t >> 8) .. + 15
         if (t <= DL_RG) {
             const uint32_t gg = (uint32_t)t < nr ? wl[g0 + t] >> 16 : 0xffffu;
-            s0r[t] = gg == 0xffffu ? fail : gg;
+            s0r[t] = gg == 0xffffu ? fail : FMT == 2 ? (uint32_t)rbase[wl[g0 + t] & 0xffffu] : gg;
         }
         dl_bar();
         {
@@ -509,12 +525,14 @@ extern "C" int zs_dfa_mask_launch(const dm_args& a, bool packed_lds, uint32_t nc
         const uint32_t ntt = (ncover + ZS_WALK_TILE - 1) / ZS_WALK_TILE;
         const uint32_t items = ntt * a.B;
         const dim3 grid(min(items, ncu));
-        if (a.sparse)
-            hipLaunchKernelGGL((zs_k_dfa_mask_packed<true, 4, 2>), grid, dim3(DL_NT), 0, stream, x);
+        if (a.sparse == 2)
+            hipLaunchKernelGGL((zs_k_dfa_mask_packed<2, 4, 2>), grid, dim3(DL_NT), 0, stream, x);
+        else if (a.sparse)
+            hipLaunchKernelGGL((zs_k_dfa_mask_packed<1, 4, 2>), grid, dim3(DL_NT), 0, stream, x);
         else if (a.dense)
-            hipLaunchKernelGGL((zs_k_dfa_mask_packed<false, 8, 1>), grid, dim3(DL_NT), 0, stream, x);
+            hipLaunchKernelGGL((zs_k_dfa_mask_packed<0, 8, 1>), grid, dim3(DL_NT), 0, stream, x);
         else
-            hipLaunchKernelGGL((zs_k_dfa_mask_packed<false, 4, 2>), grid, dim3(DL_NT), 0, stream, x);
+            hipLaunchKernelGGL((zs_k_dfa_mask_packed<0, 4, 2>), grid, dim3(DL_NT), 0, stream, x);
         if (x.eos_direct) return hipGetLastError() == hipSuccess ? 0 : -1;   // the walk applied the EOS rule
     } else {
         // epoch 0: the caller's own 0/1 flags, cleared first; otherwise the

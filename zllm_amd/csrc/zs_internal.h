@@ -17,6 +17,7 @@
 #define ZS_DFA_MEMO_BYTES (256ull << 20)  // per-DFA device memo of allow bitsets (cap)
 #define ZS_WALK_TILE 2048        // ids per tile of the vocab-parallel DFA walk
 #define ZS_DFA_MAXROWS 1024      // rows of the LDS-table DFA walk (constrained-row list in LDS)
+#define ZS_DFA_RD_ROWS ZS_DFA_MAXROWS  // displaced rows: per-row u16 bases at the end of the table budget
 #define ZS_MAX_CHUNKS (ZS_MAX_VOCAB / ZS_P1_CH)
 // Big-row engine: 1024 threads, 4 consecutive elements per thread.
 #define ZS_BIG_NT 1024
@@ -262,7 +263,12 @@ struct zs_dfa {
     // sparse form instead (tables past the budget with at most 64 classes):
     // d_packed = {mask lo, mask hi, first target, 0} per good state + sink,
     // then u16 targets; d_clsinfo = class index
+    // sparse == 2, displaced rows (tables past the budget): d_packed =
+    // packed_words entries b_g + c -> b_g << 16 | b_target (0xffffffff: none),
+    // then (not staged in LDS) the u16 base of every state by its original id,
+    // rd_fail for bad states; d_clsinfo = class index
     uint32_t sparse;
+    uint32_t rd_fail;
     uint32_t dense;        // over 30% of (good state, byte) transitions reach a good state
     // memo of allow bitsets per good state (logit_fsm.rs:166-182's cache):
     // slot g holds the walk's bitset for good state g (before the EOS rule)
@@ -305,7 +311,9 @@ struct dm_args {
     const uint16_t* clsinfo;
     const uint16_t* remap;
     uint32_t ngood, bits, rw;
-    uint32_t sparse;          // packed table in the sparse row form
+    uint32_t sparse;          // packed table in the sparse row form (1) or displaced rows (2)
+    uint32_t rd_fail;         // displaced rows: the fail value (a base no state owns)
+    const uint16_t* rdmap;    // displaced rows: [nstates] base of each state (rd_fail: bad)
     uint32_t dense;           // most (good state, byte) pairs lead to a good state
     const int32_t* states;
     uint32_t B, V, words;

@@ -229,6 +229,12 @@ class ByteDfa:
             lib().zs_dfa_destroy(self.h)
             self.h = None
 
+    @property
+    def table_form(self) -> str:
+        """The table form the mask walk uses: "packed", "sparse", "displaced"
+        (staged in LDS) or "l2" (past the LDS budget)."""
+        return ("packed", "sparse", "displaced", "l2")[lib().zs_dfa_table_form(self.h)]
+
     def is_live(self, s: int) -> bool:
         return bool(lib().zs_dfa_is_live(self.h, s))
 
