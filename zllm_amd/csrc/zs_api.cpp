@@ -25,6 +25,10 @@ extern "C" int zs_lane_topk_launch(const float* logits, uint32_t B, uint32_t V, 
 extern "C" int zs_lane_sample_topk_launch(const float* vals, const uint32_t* idxs, uint32_t B, uint32_t K,
                                           const float* temp, const uint32_t* top_k, const float* top_p,
                                           const uint32_t* seed, uint32_t* out, hipStream_t stream);
+extern "C" int zs_lane_topk_draw_launch(const float* logits, uint32_t B, uint32_t V, uint64_t ld, uint32_t K,
+                                        float* vals, uint32_t* idxs, unsigned long long* ck, uint32_t* cn,
+                                        const float* temp, const uint32_t* top_k, const float* top_p,
+                                        const uint32_t* seed, uint32_t* out, hipStream_t stream);
 extern "C" int zs_dfa_mask_launch(const dm_args& a, bool lds, uint32_t ncu, uint32_t* any_scratch, hipStream_t stream);
 
 int zs_set_error(zs_ctx* ctx, int code, const char* fmt, ...) {
@@ -1027,11 +1031,9 @@ extern "C" int zs_lane_step(zs_ctx* ctx, const float* d_logits, uint32_t m, uint
         else if (p == ZS_LANE_SAMPLE)
             rc = zs_lane_argmax_launch(d_logits, m, V, ld, ctx->lane_temp, ctx->lane_seed, ctx->lane_ih, ctx->lane_keys, d_out, st);
         else {
-            rc = zs_lane_topk_launch(d_logits, m, V, ld, ZS_LANE_K, ctx->lane_vals, ctx->lane_idxs,
-                                     V <= ctx->max_vocab ? ctx->lane_ck : nullptr, ctx->lane_cn, st);
-            if (!rc)
-                rc = zs_lane_sample_topk_launch(ctx->lane_vals, ctx->lane_idxs, m, ZS_LANE_K, ctx->lane_temp,
-                                                ctx->lane_topk, ctx->lane_topp, ctx->lane_seed, d_out, st);
+            rc = zs_lane_topk_draw_launch(d_logits, m, V, ld, ZS_LANE_K, ctx->lane_vals, ctx->lane_idxs,
+                                          V <= ctx->max_vocab ? ctx->lane_ck : nullptr, ctx->lane_cn, ctx->lane_temp,
+                                          ctx->lane_topk, ctx->lane_topp, ctx->lane_seed, d_out, st);
         }
         if (rc) rc = ZS_EHIP;
     }

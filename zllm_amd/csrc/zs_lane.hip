@@ -356,13 +356,13 @@ __global__ __launch_bounds__(LN_NT) void zs_k_btopk(const float* logits, uint32_
     }
 }
 
-// Two-phase BTOPK for K <= 64: every 8192-id chunk keeps its own top-K by
+// Two-phase BTOPK for K <= 64: every 16384-id chunk keeps its own top-K by
 // (key desc, id asc) -- a superset of the row's top-K restricted to the chunk
 // -- and one workgroup per row sorts the chunk lists. Same result as
 // zs_k_btopk; one read of the row over the whole chip instead of six passes
 // by one workgroup.
 #define TC_NT 256
-#define TC_CH 8192
+#define TC_CH 16384
 #define TC_EPT (TC_CH / TC_NT)
 #define TC_SORT 256
 #define TC_K 64
@@ -513,10 +513,20 @@ __global__ __launch_bounds__(TC_NT) void zs_k_btopk_chunks(const float* logits, 
 // reversed next list holds the 64 best of both as a bitonic sequence, which
 // six exchange steps sort.
 #define TM_ROWS 4
+struct tm_draw {   // the nucleus draw after the merge (zs_lane_step's top-K path)
+    const float* temp;
+    const uint32_t *top_k;
+    const float* top_p;
+    const uint32_t* seed;
+    uint32_t* out;
+};
+__device__ __forceinline__ uint32_t lane_draw64(float v, uint32_t id, uint32_t K, float T, uint32_t top_k, float tp,
+                                                uint32_t seed);
+template <bool DRAW>
 __global__ __launch_bounds__(64 * TM_ROWS) void zs_k_btopk_merge(const float* logits, uint32_t B, uint64_t ld,
                                                                   uint32_t K, const unsigned long long* ck,
                                                                   const uint32_t* cn, uint32_t nch, float* vals,
-                                                                  uint32_t* idxs) {
+                                                                  uint32_t* idxs, tm_draw d) {
     const uint32_t r = blockIdx.x * TM_ROWS + zs_wid();
     if (r >= B) return;
     const int lane = zs_lane();
@@ -533,16 +543,21 @@ __global__ __launch_bounds__(64 * TM_ROWS) void zs_k_btopk_merge(const float* lo
         }
         cur = m;
     }
+    float v = -3.0e38f;
+    uint32_t id = 0xffffffffu;
     if ((uint32_t)lane < K) {
-        const float* row = logits + (size_t)r * ld;
         if (cur != ~0ull) {
-            const uint32_t id = (uint32_t)(cur & 0xffffffffull);
-            vals[(size_t)r * K + lane] = row[id];
-            idxs[(size_t)r * K + lane] = id;
-        } else {
-            vals[(size_t)r * K + lane] = -3.0e38f;
-            idxs[(size_t)r * K + lane] = 0xffffffffu;
+            id = (uint32_t)(cur & 0xffffffffull);
+            v = logits[(size_t)r * ld + id];
         }
+        vals[(size_t)r * K + lane] = v;
+        idxs[(size_t)r * K + lane] = id;
+    }
+    if (DRAW) {
+        // the pool as zs_k_sample_topk64 reads it back
+        const uint32_t res = lane_draw64((uint32_t)lane < K ? v : -INFINITY, (uint32_t)lane < K ? id : 0u, K,
+                                         d.temp[r], d.top_k[r], d.top_p[r], d.seed[r]);
+        if (lane == 0) d.out[r] = res;
     }
 }
 
@@ -592,35 +607,25 @@ __global__ void zs_k_sample_topk(const float* vals, const uint32_t* idxs, uint32
     out[r] = res;
 }
 
-// The same draw with one wave per row for pools of at most 64: the
-// exponentials in parallel, the sequential sums (sampler order, f32) as
-// broadcast chains.
-__global__ __launch_bounds__(64 * TM_ROWS) void zs_k_sample_topk64(const float* vals, const uint32_t* idxs,
-                                                                    uint32_t B, uint32_t K, const float* temp,
-                                                                    const uint32_t* top_k, const float* top_p,
-                                                                    const uint32_t* seed, uint32_t* out) {
-    const uint32_t r = blockIdx.x * TM_ROWS + zs_wid();
-    if (r >= B) return;
+// The same draw by one wave for a pool of at most 64 (lane i holds entry i:
+// value v, id; lanes >= K hold -inf): the exponentials in parallel, the
+// sequential sums (sampler order, f32) as broadcast chains. Returns the id
+// (uniform).
+__device__ __forceinline__ uint32_t lane_draw64(float v, uint32_t id, uint32_t K, float T, uint32_t top_k, float tp,
+                                                uint32_t seed) {
     const int lane = zs_lane();
-    const float v = (uint32_t)lane < K ? vals[(size_t)r * K + lane] : -INFINITY;
-    const uint32_t id = (uint32_t)lane < K ? idxs[(size_t)r * K + lane] : 0u;
     const uint32_t id0 = __shfl(id, 0, 64);
     // n: length of the leading run of values above the sentinel
     const unsigned long long fail = __ballot(!((uint32_t)lane < K && v > -3.0e37f));
     const uint32_t n = fail ? (uint32_t)__ffsll((long long)fail) - 1u : 64u;
-    const float T = temp[r];
-    if (n == 0 || T <= 0.0f) {
-        if (lane == 0) out[r] = id0;
-        return;
-    }
-    const uint32_t kk = top_k[r] == 0 ? n : (top_k[r] < n ? top_k[r] : n);
+    if (n == 0 || T <= 0.0f) return id0;
+    const uint32_t kk = top_k == 0 ? n : (top_k < n ? top_k : n);
     const float maxv = __shfl(v, 0, 64);
     const float e = (uint32_t)lane < kk ? zs_expf((v - maxv) / T) : 0.0f;
     float z = -0.0f;
     for (uint32_t i = 0; i < kk; i++) z = z + __shfl(e, (int)i, 64);
     const float p = e / z;
     uint32_t cut = kk;
-    const float tp = top_p[r];
     if (tp > 0.0f && tp < 1.0f) {
         float cum = 0.0f;
         for (uint32_t i = 0; i < kk; i++) {
@@ -630,14 +635,26 @@ __global__ __launch_bounds__(64 * TM_ROWS) void zs_k_sample_topk64(const float* 
     }
     float zc = -0.0f;
     for (uint32_t i = 0; i < cut; i++) zc = zc + __shfl(p, (int)i, 64);
-    const float target = zs_rng01(seed[r]) * zc;
+    const float target = zs_rng01(seed) * zc;
     float acc = 0.0f;
     uint32_t pick = cut - 1;
     for (uint32_t i = 0; i < cut; i++) {
         acc = acc + __shfl(p, (int)i, 64);
         if (acc >= target) { pick = i; break; }
     }
-    const uint32_t res = __shfl(id, (int)pick, 64);
+    return __shfl(id, (int)pick, 64);
+}
+
+__global__ __launch_bounds__(64 * TM_ROWS) void zs_k_sample_topk64(const float* vals, const uint32_t* idxs,
+                                                                    uint32_t B, uint32_t K, const float* temp,
+                                                                    const uint32_t* top_k, const float* top_p,
+                                                                    const uint32_t* seed, uint32_t* out) {
+    const uint32_t r = blockIdx.x * TM_ROWS + zs_wid();
+    if (r >= B) return;
+    const int lane = zs_lane();
+    const float v = (uint32_t)lane < K ? vals[(size_t)r * K + lane] : -INFINITY;
+    const uint32_t id = (uint32_t)lane < K ? idxs[(size_t)r * K + lane] : 0u;
+    const uint32_t res = lane_draw64(v, id, K, temp[r], top_k[r], top_p[r], seed[r]);
     if (lane == 0) out[r] = res;
 }
 
@@ -655,20 +672,39 @@ extern "C" int zs_lane_argmax_launch(const float* logits, uint32_t B, uint32_t V
     hipLaunchKernelGGL(zs_k_bargmax, dim3(B), dim3(LN_NT), 0, stream, logits, V, ld, out);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
-// ck / cn: scratch of at least B * ceil(V / 8192) * 64 keys and B * ceil(V / 8192)
-// counts (two-phase path, K <= 64, V <= 32 * 8192); nullptr forces one pass
+// ck / cn: scratch of at least B * ceil(V / TC_CH) * 64 keys and B * ceil(V / TC_CH)
+// counts (two-phase path, K <= 64, V <= 32 * TC_CH); nullptr forces one pass
 extern "C" int zs_lane_topk_launch(const float* logits, uint32_t B, uint32_t V, uint64_t ld, uint32_t K,
                                    float* vals, uint32_t* idxs, unsigned long long* ck, uint32_t* cn,
                                    hipStream_t stream) {
     const uint32_t nch = (V + TC_CH - 1) / TC_CH;
     if (ck && cn && K <= TC_K && nch <= TC_MAXCH) {
         hipLaunchKernelGGL(zs_k_btopk_chunks, dim3(nch, B), dim3(TC_NT), 0, stream, logits, V, ld, K, ck, cn, nch);
-        hipLaunchKernelGGL(zs_k_btopk_merge, dim3((B + TM_ROWS - 1) / TM_ROWS), dim3(64 * TM_ROWS), 0, stream,
-                           logits, B, ld, K, ck, cn, nch, vals, idxs);
+        hipLaunchKernelGGL(zs_k_btopk_merge<false>, dim3((B + TM_ROWS - 1) / TM_ROWS), dim3(64 * TM_ROWS), 0, stream,
+                           logits, B, ld, K, ck, cn, nch, vals, idxs, tm_draw{});
     } else {
         hipLaunchKernelGGL(zs_k_btopk, dim3(B), dim3(LN_NT), 0, stream, logits, V, ld, K, vals, idxs);
     }
     return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+// The top-K pool and its nucleus draw: on the two-phase path the merge kernel
+// draws too (one launch and no read-back of the pool), else the two launches.
+extern "C" int zs_lane_sample_topk_launch(const float* vals, const uint32_t* idxs, uint32_t B, uint32_t K,
+                                          const float* temp, const uint32_t* top_k, const float* top_p,
+                                          const uint32_t* seed, uint32_t* out, hipStream_t stream);
+extern "C" int zs_lane_topk_draw_launch(const float* logits, uint32_t B, uint32_t V, uint64_t ld, uint32_t K,
+                                        float* vals, uint32_t* idxs, unsigned long long* ck, uint32_t* cn,
+                                        const float* temp, const uint32_t* top_k, const float* top_p,
+                                        const uint32_t* seed, uint32_t* out, hipStream_t stream) {
+    const uint32_t nch = (V + TC_CH - 1) / TC_CH;
+    if (ck && cn && K <= TC_K && nch <= TC_MAXCH) {
+        hipLaunchKernelGGL(zs_k_btopk_chunks, dim3(nch, B), dim3(TC_NT), 0, stream, logits, V, ld, K, ck, cn, nch);
+        hipLaunchKernelGGL(zs_k_btopk_merge<true>, dim3((B + TM_ROWS - 1) / TM_ROWS), dim3(64 * TM_ROWS), 0, stream,
+                           logits, B, ld, K, ck, cn, nch, vals, idxs, tm_draw{temp, top_k, top_p, seed, out});
+        return hipGetLastError() == hipSuccess ? 0 : -1;
+    }
+    if (zs_lane_topk_launch(logits, B, V, ld, K, vals, idxs, ck, cn, stream)) return -1;
+    return zs_lane_sample_topk_launch(vals, idxs, B, K, temp, top_k, top_p, seed, out, stream);
 }
 extern "C" int zs_lane_sample_topk_launch(const float* vals, const uint32_t* idxs, uint32_t B, uint32_t K,
                                           const float* temp, const uint32_t* top_k, const float* top_p,
