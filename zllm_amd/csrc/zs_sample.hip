@@ -1830,6 +1830,7 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
     // second workgroups CUs of their own
     a.row_split = 2 * bt->B <= ctx->num_cus ? 1u : 0u;
     a.s_rec = ctx->s_rec;
+    a.s_xrec = ctx->s_rec + (size_t)ctx->max_rows * ZS_NSUM * ctx->max_subs;
     a.s_apx = ctx->s_apx;
     a.gath = ctx->gath;
     a.pstride = ctx->max_vocab;

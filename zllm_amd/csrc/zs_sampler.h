@@ -28,6 +28,7 @@ struct zs_sargs {
     uint32_t* kcnt;
     uint32_t* tp_task;   // buckets zs_k_tp_sort presorts: count, then (row << 8 | candidate)
     zs_sub_sum* s_rec;
+    zs_sub_sum* s_xrec;  // crossing records beside s_rec (same indexing)
     float* s_apx;
     float* gath;
     float* s_hterm;

@@ -459,22 +459,16 @@ __device__ __forceinline__ sm_pre sm_pre_of(const zs_sargs& a, uint32_t r, uint3
     return P;
 }
 
-// Predicted grid of sub-chunk j of sum `kind` from the approximate prefix
-// sums: the sub-chunk's range [before, after] widened by the margin must stay
-// in one binade of grids >= SM_EG_MIN. The running sum is never below the
-// largest term added so far (the f32 additions of non-negative terms are
-// monotone), which bounds it from below where the margin would reach under
-// a power of two (a sum resting just above one after its largest term).
-// Returns the grid exponent, or 0.
-__device__ __forceinline__ int sm_predict(const zs_sargs& a, uint32_t r, uint32_t j, int kind, const sm_terms& f,
-                                          const sm_pre& P) {
+// The approximate range of sum `kind` over sub-chunk j: lo below its start,
+// mid the start's estimate, hi above its end (hi widened by the margin).
+__device__ __forceinline__ void sm_range(const zs_sargs& a, uint32_t r, uint32_t j, int kind, const sm_terms& f,
+                                         const sm_pre& P, double& lo, double& mid, double& hi) {
     const float* own = a.s_apx + ((size_t)r * a.max_subs + j) * SM_APX;
-    double lo, hi;
     if (kind == ZS_SUM_OBS_H) {
         const double inv = (double)f.inv, lns = (double)f.lns;
-        lo = inv * (lns * P.so - P.sd);
+        mid = inv * (lns * P.so - P.sd);
         hi = inv * (lns * (P.so + (double)own[0]) - (P.sd + (double)own[2]));
-        lo *= 1.0 - SM_MARGIN;
+        lo = mid * (1.0 - SM_MARGIN);
     } else {
         // the largest term before j, exactly: expf(max x~ - M), or expf(z -
         // zmax) of the largest y (z = y / T is monotone in y; not under a
@@ -483,14 +477,117 @@ __device__ __forceinline__ int sm_predict(const zs_sargs& a, uint32_t r, uint32_
         float tmax = 0.0f;
         if (kind == ZS_SUM_OBS_S) tmax = sm_exact(f, P.mo - f.M);
         else if (!f.use_thr) tmax = sm_exact(f, sm_temper(f, P.ms) - f.zmax);
+        mid = pre;
         lo = fmax(pre * (1.0 - SM_MARGIN), (double)tmax);
         hi = pre + (double)(kind == ZS_SUM_SAMP_S ? own[1] : own[0]);
     }
     hi *= 1.0 + SM_MARGIN;
+}
+// Predicted grid of sub-chunk j of a sum from its approximate range
+// (sm_range): the range widened by the margin must stay in one binade of
+// grids >= SM_EG_MIN. The running sum is never below the
+// largest term added so far (the f32 additions of non-negative terms are
+// monotone), which bounds it from below where the margin would reach under
+// a power of two (a sum resting just above one after its largest term).
+// Returns the grid exponent, or 0.
+__device__ __forceinline__ int sm_predict(uint32_t j, double lo, double hi) {
     if (j == 0 || !(lo > 0x1p-99) || !(hi < 0x1p100)) return 0;
     const int blo = ilogb(lo), bhi = ilogb(hi);
     if (blo != bhi) return 0;
     return blo + 127;   // zs_grid_exp of a normal float in that binade
+}
+
+// Crossing records of unpredictable sub-chunks (zs_walk.h's sm_xrec): when
+// the approximate range puts the start surely in one binade and the end in
+// the next, the exit term x is guessed from the start's estimate, and the
+// pairs of the terms before x (grid eg) and after it (grid eg + 1) are taken
+// over the exact terms, a quarter (4 terms a lane) at a time in summation
+// order (quarter, lane, element). sm_cross_grid: the start grid, or 0 (no
+// record), and the estimated start on that grid.
+__device__ __forceinline__ int sm_cross_grid(uint32_t j, double lo, double mid, double hi, uint32_t* kt) {
+    if (j == 0 || !(lo > 0x1p-99) || !(hi < 0x1p100)) return 0;
+    const int b = ilogb(lo);
+    if (ilogb(mid * (1.0 + SM_MARGIN)) != b || ilogb(hi) != b + 1) return 0;
+    *kt = (uint32_t)ldexp(mid, 23 - b);
+    return b + 127;
+}
+// Increments of 4 exact terms on the grid of scale sc (those in `valid`) and
+// their half-way flags: the walk's rule (zs_walk.h).
+__device__ __forceinline__ void sm_exact_incs4(const float (&v)[4], float sc, uint32_t valid, uint32_t (&inc)[4],
+                                               uint32_t& tie) {
+    tie = 0u;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const float qe = fminf(v[e] * sc, SM_QCAP);
+        float rq = rintf(qe);
+        const bool h = fabsf(qe - rq) == 0.5f && ((valid >> e) & 1u);
+        if (h) rq = floorf(qe);
+        tie |= (h ? 1u : 0u) << e;
+        inc[e] = ((valid >> e) & 1u) ? (uint32_t)rq : 0u;
+    }
+}
+// The ordered pair of the wave's increments (lanes in order, elements in
+// `valid` in order): a plain sum unless a half-way term is among them.
+__device__ __forceinline__ seq_pair sm_wave_pair4(const uint32_t (&inc)[4], uint32_t tie, uint32_t valid) {
+    if (!__builtin_amdgcn_readfirstlane((int)(__ballot(tie != 0u) != 0ull))) {
+        uint32_t t = 0u;
+#pragma unroll
+        for (int e = 0; e < 4; e++) t = zs_sat_add(t, ((valid >> e) & 1u) ? inc[e] : 0u);
+        const uint32_t w = sm_wave_sum_sat(t);
+        return seq_pair{w, w};
+    }
+    seq_pair lp = {0u, 0u};
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+        if ((valid >> e) & 1u) lp = seq_compose(lp, ((tie >> e) & 1u) ? sm_pair_tie(inc[e]) : seq_pair{inc[e], inc[e]});
+    return sm_wave_pair_reduce(lp);
+}
+struct sm_xstate {
+    uint32_t carry, xpos;
+    seq_pair pre, post;
+    float vx;
+};
+// One quarter qi of exact terms (this lane's 4 of it, dv).
+__device__ __forceinline__ void sm_cross_quarter(sm_xstate& X, const float (&dv)[4], int qi, int eg) {
+    const uint32_t lane = (uint32_t)zs_lane();
+    const uint32_t p0 = 256u * (uint32_t)qi + 4u * lane;   // this lane's first position in the quarter
+    if (X.xpos == 0xffffffffu) {
+        uint32_t inc[4], tie;
+        sm_exact_incs4(dv, sm_scale(eg), 0xfu, inc, tie);
+        uint32_t lt = 0u;
+#pragma unroll
+        for (int e = 0; e < 4; e++) lt = zs_sat_add(lt, inc[e]);
+        const uint32_t incl = sm_wave_scan_sat(lt);
+        const unsigned long long m = __ballot(zs_sat_add(X.carry, incl) >= ZS_BINADE);
+        uint32_t vm = 0xfu;   // this lane's terms before the exit
+        if (m) {
+            const int L = __ffsll((long long)m) - 1;
+            uint32_t kk = zs_sat_add(X.carry, incl - lt), ex = 3u;
+            bool found = false;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                kk = zs_sat_add(kk, inc[e]);
+                if (!found && kk >= ZS_BINADE) { ex = (uint32_t)e; found = true; }
+            }
+            ex = (uint32_t)__builtin_amdgcn_readlane((int)ex, L);
+            X.xpos = 256u * (uint32_t)qi + 4u * (uint32_t)L + ex;
+            const float dq = ex == 0u ? dv[0] : ex == 1u ? dv[1] : ex == 2u ? dv[2] : dv[3];
+            X.vx = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(dq), L));
+            vm = 0u;
+#pragma unroll
+            for (int e = 0; e < 4; e++) vm |= (p0 + (uint32_t)e < X.xpos ? 1u : 0u) << e;
+        }
+        X.pre = seq_compose(X.pre, sm_wave_pair4(inc, tie & vm, vm));
+        X.carry = zs_sat_add(X.carry, (uint32_t)__builtin_amdgcn_readlane((int)incl, 63));
+    }
+    if (X.xpos != 0xffffffffu) {
+        uint32_t vm = 0u;
+#pragma unroll
+        for (int e = 0; e < 4; e++) vm |= (p0 + (uint32_t)e > X.xpos ? 1u : 0u) << e;
+        uint32_t inc2[4], tie2;
+        sm_exact_incs4(dv, sm_scale(eg + 1), vm, inc2, tie2);
+        X.post = seq_compose(X.post, sm_wave_pair4(inc2, tie2, vm));
+    }
 }
 
 // Sub-chunk total on grid eg (uniform): the increment pair of the wave's
@@ -536,6 +633,8 @@ template <int STAGE>
 __device__ __forceinline__ constexpr int sm_stage_kind() {
     return STAGE == 1 ? ZS_SUM_SAMP_S : STAGE == 2 ? ZS_SUM_OBS_S : ZS_SUM_OBS_H;
 }
+// exact terms of a wave's sub-chunk for its crossing record
+__shared__ float sm_xbuf[SM_NT / 64][ZS_SUB];
 template <int STAGE>
 __global__ __launch_bounds__(SM_NT) void zs_k_sround(zs_sargs a) {
     const uint32_t r = blockIdx.y;
@@ -569,13 +668,19 @@ __global__ __launch_bounds__(SM_NT) void zs_k_sround(zs_sargs a) {
         for (int u = 0; u < NK; u++) {
             if (!((jobs >> kinds[u]) & 1u)) continue;
             const sm_terms& f = F[u];
-            const int eg = sm_predict(a, r, j, kinds[u], f, sm_pre_of(a, r, j));
+            double lo, mid, hi;
+            sm_range(a, r, j, kinds[u], f, sm_pre_of(a, r, j), lo, mid, hi);
+            const int eg = sm_predict(j, lo, hi);
             if (eg) {
                 const seq_pair t = sm_total(f, x, y, eg);
                 if (zs_lane() == 0) rec[(size_t)kinds[u] * a.max_subs] = sm_rec{eg, SM_SAFE, t.e, t.o};
             } else {
-                // the stitch walks this sub-chunk from its exact terms
-                if (zs_lane() == 0) rec[(size_t)kinds[u] * a.max_subs] = sm_rec{0, 0u, 0u, 0u};
+                // the stitch walks this sub-chunk from its exact terms,
+                // unless its crossing record holds (exact terms also kept in
+                // LDS for it)
+                uint32_t kt = 0u;
+                const int xeg = sm_cross_grid(j, lo, mid, hi, &kt);
+                float* xb = sm_xbuf[zs_wid()];
                 float* da = sm_darea(a, r, kinds[u]) + (size_t)j * ZS_SUB;
                 // (a rolled loop over the quarters: sixteen inlined exact
                 // exponentials would hold too many registers)
@@ -598,7 +703,31 @@ __global__ __launch_bounds__(SM_NT) void zs_k_sround(zs_sargs a) {
                         for (int e = 0; e < 4; e++)
                             if (j * ZS_SUB + p + e < S.n) da[p + e] = dv[e];
                     }
+                    if (xeg) {
+                        // (terms past the row: none, as in the walk)
+                        float dz[4];
+#pragma unroll
+                        for (int e = 0; e < 4; e++) dz[e] = j * ZS_SUB + p + e < S.n ? dv[e] : 0.0f;
+                        *reinterpret_cast<sm_f4*>(xb + p) = sm_f4{dz[0], dz[1], dz[2], dz[3]};
+                    }
                 }
+                sm_rec cr = {0, 0u, 0u, 0u};
+                if (xeg) {
+                    sm_xstate X = {kt, 0xffffffffu, {0u, 0u}, {0u, 0u}, 0.0f};
+#pragma unroll
+                    for (int qi = 0; qi < 4; qi++) {
+                        const sm_f4 q4 = *reinterpret_cast<const sm_f4*>(xb + sm_pos<false>((uint32_t)zs_lane(), qi));
+                        const float dv[4] = {q4.x, q4.y, q4.z, q4.w};
+                        sm_cross_quarter(X, dv, qi, xeg);
+                    }
+                    if (X.xpos != 0xffffffffu) {
+                        cr = sm_rec{xeg, SM_CROSS, X.pre.e, X.pre.o};
+                        if (zs_lane() == 0)
+                            reinterpret_cast<sm_xrec*>(a.s_xrec)[((size_t)r * ZS_NSUM + kinds[u]) * a.max_subs + j] =
+                                sm_xrec{X.xpos, X.vx, X.post.e, X.post.o};
+                    }
+                }
+                if (zs_lane() == 0) rec[(size_t)kinds[u] * a.max_subs] = cr;
             }
         }
         if (more) Rc = Rn;
@@ -671,11 +800,16 @@ __global__ __launch_bounds__(SW_NT) void zs_k_sstitch(zs_sargs a) {
     const sm_terms f = sm_terms_of(kind, st, P);
     const uint32_t nsub = (S.n + ZS_SUB - 1) / ZS_SUB;
     const sm_rec* rec = reinterpret_cast<const sm_rec*>(a.s_rec) + ((size_t)r * ZS_NSUM + kind) * a.max_subs;
-    for (uint32_t i = threadIdx.x; i < nsub; i += SW_NT) sm_sh.rec[i] = rec[i];
+    const sm_xrec* xrec = reinterpret_cast<const sm_xrec*>(a.s_xrec) + ((size_t)r * ZS_NSUM + kind) * a.max_subs;
+    for (uint32_t i = threadIdx.x; i < nsub; i += SW_NT) {
+        const sm_rec e = rec[i];
+        sm_sh.rec[i] = e;
+        if (e.flags & SM_CROSS) sm_sh.xrec[i] = xrec[i];
+    }
     __syncthreads();
     sm_row_tp tp{S, f, sm_darea(a, r, kind)};
     uint32_t stop;
-    const float s = sm_stitch<sm_row_tp, sm_f4>(tp, nsub, kind == ZS_SUM_OBS_H ? 0.0f : -0.0f, NAN, &stop);
+    const float s = sm_stitch<sm_row_tp, sm_f4, true>(tp, nsub, kind == ZS_SUM_OBS_H ? 0.0f : -0.0f, NAN, &stop);
     if (threadIdx.x == 0) {
         if (kind == ZS_SUM_OBS_S) stp->obs_S = s;
         else if (kind == ZS_SUM_SAMP_S) stp->samp_S = s;

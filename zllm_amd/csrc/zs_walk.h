@@ -37,8 +37,20 @@ static_assert(SW_NT * SW_TPT == ZS_SUB, "one workgroup per sub-chunk walk");
 // Per (sum, sub-chunk) record of a round kernel.
 struct sm_rec {
     int32_t eg;       // grid exponent the totals are on
-    uint32_t flags;   // SM_SAFE: totals valid
+    uint32_t flags;   // SM_SAFE: totals valid; SM_CROSS: a crossing record (below)
     uint32_t d0, d1;  // increments from an even / odd start (saturated at ZS_INC_CAP)
+};
+// A sub-chunk where the running sum is expected to leave its binade once, at
+// term x: its sm_rec holds the start grid eg, SM_CROSS and the increment pair
+// of terms 0 .. x-1 on grid eg; this record the exact term x and the pair of
+// terms x+1 .. on grid eg + 1. The stitch checks the guess from the exact
+// running sum (no exit before x, an exit at x into binade eg + 1, none after)
+// and walks the sub-chunk when it fails.
+#define SM_CROSS 2u
+struct sm_xrec {
+    uint32_t x;
+    float vx;
+    uint32_t p0, p1;
 };
 
 // 2^(150 - eg): the scale of grid eg (eg >= 24).
@@ -137,6 +149,7 @@ struct sm_wsh {
     uint32_t hstop;
     alignas(16) float hv[SW_TPT * 64];     // the head: one wave's terms, added one by one from here
     sm_rec rec[ZS_MAX_SUBS];               // the records of the sum being stitched
+    sm_xrec xrec[ZS_MAX_SUBS];             // its crossing records (when the caller has them)
 };
 __shared__ sm_wsh sm_sh;
 #define SW_STOP 0x80000000u
@@ -447,7 +460,33 @@ __device__ __forceinline__ uint32_t sm_next_fragile(uint32_t j, uint32_t nsub) {
 // loads of a sub-chunk the records send to the walk (two walks ahead),
 // tp.take(j, raw, v) turns them into terms, tp.direct(j, v) computes them
 // for a sub-chunk whose record was safe but whose total did not apply.
-template <class TP, class RAW>
+// A crossing record of sub-chunk j applied to the exact running sum s
+// (uniform): true with the new sum, or with *stop set when the threshold is
+// reached at its term x; false when its guess does not hold.
+__device__ __forceinline__ bool sm_cross(uint32_t j, float& s, float thresh, uint32_t* stop) {
+    const sm_rec e = sm_sh.rec[j];
+    if (!(e.flags & SM_CROSS) || s == 0.0f) return false;
+    const int eg = zs_grid_exp(s);
+    if (e.eg != eg) return false;
+    const sm_xrec xr = sm_sh.xrec[j];
+    const uint32_t k = zs_grid_k(s);
+    const uint32_t k1 = zs_sat_add(k, (k & 1u) ? e.d1 : e.d0);
+    if (k1 >= ZS_BINADE || k1 >= zs_grid_thresh(thresh, eg)) return false;
+    const float sx = zs_grid_value(k1, eg) + xr.vx;   // the term that leaves the binade
+    if (zs_grid_exp(sx) != eg + 1) return false;
+    if (sx >= thresh) {
+        *stop = j * ZS_SUB + xr.x;
+        s = sx;
+        return true;
+    }
+    const uint32_t kx = zs_grid_k(sx);
+    const uint32_t k2 = zs_sat_add(kx, (kx & 1u) ? xr.p1 : xr.p0);
+    if (k2 >= ZS_BINADE || k2 >= zs_grid_thresh(thresh, eg + 1)) return false;
+    s = zs_grid_value(k2, eg + 1);
+    return true;
+}
+
+template <class TP, class RAW, bool XR = false>
 __device__ __forceinline__ float sm_stitch(TP& tp, uint32_t nsub, float s, float thresh, uint32_t* stop) {
     const uint32_t lane = (uint32_t)zs_lane();
     *stop = 0xffffffffu;
@@ -479,6 +518,23 @@ __device__ __forceinline__ float sm_stitch(TP& tp, uint32_t nsub, float s, float
                 SW_T(11, 1);
                 s = zs_grid_value((uint32_t)__builtin_amdgcn_readlane((int)kend, (int)n_ok - 1), eg);
                 j += n_ok;
+                continue;
+            }
+        }
+        if (XR && j == nf0) {
+            uint32_t sp = 0xffffffffu;
+            if (sm_cross(j, s, thresh, &sp)) {
+                SW_T(13, 1);
+                if (sp != 0xffffffffu) {
+                    *stop = sp;
+                    break;
+                }
+                // the prefetched terms of j are not needed: on to the next fragile one
+                nf0 = nf1;
+                q0 = q1;
+                nf1 = nf0 < nsub ? sm_next_fragile(nf0 + 1, nsub) : nsub;
+                if (nf1 < nsub) tp.fetch(nf1, q1);
+                j++;
                 continue;
             }
         }
