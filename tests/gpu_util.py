@@ -126,8 +126,10 @@ def compare(x, params_list, out, allow=None, check_stats=True, refs=None):
         elif check_stats:
             if not close(out["entropy"][i], ref["entropy"], 1e-5, 2e-5):
                 errs.append(f"row {i}: entropy {out['entropy'][i]} vs {ref['entropy']}")
-            if not close(out["max_prob"][i], ref["max_prob"]):
-                errs.append(f"row {i}: max_prob {out['max_prob'][i]} vs {ref['max_prob']}")
+            # max_prob is 1 / S_obs on both sides (f32 division): equal bits
+            # iff the observers' exact sequential sum S_obs is
+            if np.float32(out["max_prob"][i]).view(np.uint32) != np.float32(ref["max_prob"]).view(np.uint32):
+                errs.append(f"row {i}: max_prob {out['max_prob'][i]!r} vs {ref['max_prob']!r} (bits)")
             if not close(out["margin"][i], ref["margin"], 1e-5, 2e-6):
                 errs.append(f"row {i}: margin {out['margin'][i]} vs {ref['margin']}")
             if not close(out["chosen_lp"][i], ref["chosen_lp"], 1e-5, 1e-5):
