@@ -1522,7 +1522,65 @@ __global__ __launch_bounds__(256) void zs_k_roundK(zs_sargs a) {
     const double delta = 1.0 / 256.0;
     const double lm = lo * (1.0 - delta), hm = hi * (1.0 + delta);
     sm_rec e = {0, 0u, 0u, 0u};
-    if (j != 0 && lm > 0x1p-99 && hm < 0x1p100 && ilogb(lm) == ilogb(hm)) {
+    // a sub-chunk where the sum surely starts in one binade and ends in the
+    // next: its crossing record (zs_walk.h's sm_xrec), the exit term guessed
+    // from the approximate start
+    if (j != 0 && lm > 0x1p-99 && hm < 0x1p100 && ilogb(lm) == ilogb(lo * (1.0 + delta)) &&
+        ilogb(hm) == ilogb(lm) + 1) {
+        const int eg = ilogb(lm) + 127;
+        const float sc = sm_scale(eg), sc2 = sm_scale(eg + 1);
+        uint32_t carry = (uint32_t)ldexp(lo, 150 - eg), xpos = 0xffffffffu;
+        seq_pair pre = {0u, 0u}, post = {0u, 0u};
+        float vx = 0.0f;
+        for (int q = 0; q < ZS_SUB / 64; q++) {
+            const float v = klist_term(L, j * ZS_SUB + q * 64 + zs_lane());
+            const uint32_t pos = (uint32_t)q * 64u + (uint32_t)zs_lane();
+            if (xpos == 0xffffffffu) {
+                const float qv = fminf(v * sc, SM_QCAP);
+                float rq = rintf(qv);
+                const bool h = fabsf(qv - rq) == 0.5f;
+                if (h) rq = floorf(qv);
+                const uint32_t inc = (uint32_t)rq;
+                const uint32_t incl = sm_wave_scan_sat(inc);
+                const unsigned long long m = __ballot(zs_sat_add(carry, incl) >= ZS_BINADE);
+                bool before = true;
+                if (m) {
+                    const int Lx = __ffsll((long long)m) - 1;
+                    xpos = (uint32_t)q * 64u + (uint32_t)Lx;
+                    vx = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(v), Lx));
+                    before = pos < xpos;
+                }
+                const uint32_t ti = before ? inc : 0u;
+                if (!__builtin_amdgcn_readfirstlane((int)(__ballot(h && before) != 0ull))) {
+                    const uint32_t t = sm_wave_sum_sat(ti);
+                    pre = seq_compose(pre, seq_pair{t, t});
+                } else {
+                    pre = seq_compose(pre, sm_wave_pair_reduce(!before ? seq_pair{0u, 0u}
+                                                               : h ? sm_pair_tie(inc) : seq_pair{inc, inc}));
+                }
+                carry = zs_sat_add(carry, (uint32_t)__builtin_amdgcn_readlane((int)incl, 63));
+            }
+            if (xpos != 0xffffffffu) {
+                const bool after = pos > xpos;
+                const float qv = fminf(v * sc2, SM_QCAP);
+                float rq = rintf(qv);
+                const bool h = fabsf(qv - rq) == 0.5f && after;
+                if (h) rq = floorf(qv);
+                const uint32_t inc = after ? (uint32_t)rq : 0u;
+                if (!__builtin_amdgcn_readfirstlane((int)(__ballot(h) != 0ull))) {
+                    const uint32_t t = sm_wave_sum_sat(inc);
+                    post = seq_compose(post, seq_pair{t, t});
+                } else {
+                    post = seq_compose(post, sm_wave_pair_reduce(h ? sm_pair_tie(inc) : seq_pair{inc, inc}));
+                }
+            }
+        }
+        if (xpos != 0xffffffffu) {
+            e = sm_rec{eg, SM_CROSS, pre.e, pre.o};
+            if (zs_lane() == 0)
+                reinterpret_cast<sm_xrec*>(a.k_xsum)[((size_t)r * 2 + KIND) * a.max_subs + j] = sm_xrec{xpos, vx, post.e, post.o};
+        }
+    } else if (j != 0 && lm > 0x1p-99 && hm < 0x1p100 && ilogb(lm) == ilogb(hm)) {
         e.eg = ilogb(lm) + 127;
         const float sc = sm_scale(e.eg);
         uint32_t inc[ZS_SUB / 64], tie = 0u, tot = 0u;
@@ -1600,7 +1658,12 @@ __global__ __launch_bounds__(SW_NT) void zs_k_stitchK(zs_sargs a) {
     const klist_row L = make_klist(a, r, st, KIND);
     const uint32_t nks = (L.nk + ZS_SUB - 1) / ZS_SUB;
     const sm_rec* ks = reinterpret_cast<const sm_rec*>(a.k_sum) + ((size_t)r * 2 + KIND) * a.max_subs;
-    for (uint32_t j = threadIdx.x; j < nks; j += SW_NT) sm_sh.rec[j] = ks[j];
+    const sm_xrec* kx = reinterpret_cast<const sm_xrec*>(a.k_xsum) + ((size_t)r * 2 + KIND) * a.max_subs;
+    for (uint32_t j = threadIdx.x; j < nks; j += SW_NT) {
+        const sm_rec e = ks[j];
+        sm_sh.rec[j] = e;
+        if (e.flags & SM_CROSS) sm_sh.xrec[j] = kx[j];
+    }
     __syncthreads();
     float thresh = NAN;
     if (KIND == 1) {
@@ -1616,7 +1679,7 @@ __global__ __launch_bounds__(SW_NT) void zs_k_stitchK(zs_sargs a) {
     }
     klist_tp tp{L};
     uint32_t stop;
-    const float s = sm_stitch<klist_tp, klist_raw>(tp, nks, KIND ? 0.0f : -0.0f, thresh, &stop);
+    const float s = sm_stitch<klist_tp, klist_raw, true>(tp, nks, KIND ? 0.0f : -0.0f, thresh, &stop);
     if (threadIdx.x == 0) {
         if (KIND == 0) {
             stp->sum2 = s;
@@ -1819,6 +1882,7 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
     a.max_subs = ctx->max_subs;
     a.k_ap = ctx->k_ap;
     a.k_sum = ctx->k_sum;
+    a.k_xsum = ctx->k_sum + (size_t)ctx->max_rows * 2 * ctx->max_subs;
     a.tp_bk = ctx->tp_bk;
     a.tp_cl = ctx->tp_cl;
     a.tp_pre = ctx->tp_pre;

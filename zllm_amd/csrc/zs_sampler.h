@@ -22,6 +22,7 @@ struct zs_sargs {
     uint32_t max_subs;
     double* k_ap;
     zs_sub_sum* k_sum;
+    zs_sub_sum* k_xsum;  // crossing records beside k_sum (same indexing)
     zs_tp_bucket* tp_bk;
     uint32_t* tp_cl;
     uint32_t* tp_pre;
