@@ -645,8 +645,11 @@ __device__ __forceinline__ float* rw_scratch(const zs_sargs& a, uint32_t r) {
 // masked id's term is zero, which leaves a running sum unchanged). cx, cy
 // hold round_up(n, 4) values each (the tail padded with -inf); cy = cx +
 // round_up(n, 4); the ids follow at cy + round_up(n, 4). Returns n, or 0
-// when no id or more than a quarter of the row is allowed (then the sums run
-// over the whole row). Uniform.
+// when no id, more than RW_BUF ids or more than a quarter of the row is
+// allowed (then the sums run over the whole row with its allow bits: each
+// thread's loop over its allowed ids, with a dependent load per id, took 29 us
+// on rows with tens of thousands of them, more than P1's whole stream saves).
+// Uniform.
 __device__ __noinline__ uint32_t rw_gather_allowed(const float* row, const uint32_t* allow, uint32_t V, uint32_t np,
                                                    float* cx, const uint32_t* gfl, const float* gy) {
     rw_shared& sh = rw_sh;
@@ -662,7 +665,7 @@ __device__ __noinline__ uint32_t rw_gather_allowed(const float* row, const uint3
     uint32_t n;
     uint32_t pos = block_excl_scan_u<RW_NT>(c, sh.ru[4], &n);
     n = rw_uni(n);
-    if (n == 0 || n > V / 4 || V < 16) return 0;   // V >= 16: 3 round_up(n, 4) + 3 values fit 2 V
+    if (n == 0 || n > RW_BUF || n > V / 4 || V < 16) return 0;   // V >= 16: 3 round_up(n, 4) + 3 values fit 2 V
     const uint32_t n4 = (n + 3) & ~3u;
     float* cy = cx + n4;
     for (uint32_t w = w0; w < w1; w++) {
@@ -1445,8 +1448,8 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
     // big row (on the caller's stream, before the big-row kernels), S_obs
     // (logprobs and uncertainty) and the entropy (on the side stream). A
     // masked row's sums run over its allowed ids, gathered to row scratch
-    // (when at most a quarter of the row is allowed), else over the whole row
-    // with its allow bits.
+    // (when at most RW_BUF and a quarter of the row are allowed), else over
+    // the whole row with its allow bits.
     const bool doA = (obs_need & ZS_OBS_S) != 0;
     const bool doB = mode == ZS_MODE_BIG && has_thr != 2;
     const bool doH = (obs_need & ZS_OBS_H) != 0;
