@@ -79,8 +79,10 @@ struct big_raw {
     float4 v;
     uint32_t w;
 };
-__device__ __forceinline__ big_raw big_fetch(const big_row& R, uint32_t g) {
-    const uint32_t idx0 = g * ZS_BIG_G + 4 * threadIdx.x;
+// (tix: the thread's slot of the group's ZS_BIG_NT; a smaller workgroup takes
+// several slots)
+__device__ __forceinline__ big_raw big_fetch(const big_row& R, uint32_t g, uint32_t tix = threadIdx.x) {
+    const uint32_t idx0 = g * ZS_BIG_G + 4 * tix;
     big_raw o;
     o.v = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
     o.w = 0xffffffffu;
@@ -94,8 +96,8 @@ __device__ __forceinline__ big_raw big_fetch(const big_row& R, uint32_t g) {
 // 4 elements idx0..idx0+3 of group g; the group's patches are those of its
 // ZS_BIG_G / ZS_SUB sub-chunks (per-sub-chunk patch offsets written by zs_k_row).
 __device__ __forceinline__ void big_finish(const big_row& R, uint32_t g, const big_raw& raw, float (&x)[4],
-                                           float (&z)[4]) {
-    const uint32_t idx0 = g * ZS_BIG_G + 4 * threadIdx.x;
+                                           float (&z)[4], uint32_t tix = threadIdx.x) {
+    const uint32_t idx0 = g * ZS_BIG_G + 4 * tix;
     x[0] = raw.v.x; x[1] = raw.v.y; x[2] = raw.v.z; x[3] = raw.v.w;
 #pragma unroll
     for (int q = 0; q < 4; q++) {
@@ -455,7 +457,11 @@ __device__ __forceinline__ bool tp_fast_row(const zs_row_state& st, const zs_row
 // exponentials are the bulk of a big row's arithmetic, spread here over the
 // whole GPU instead of one workgroup per row. Rows of the bucket-total walk
 // also add their positive p to the per-bucket counts and masses.
-__global__ __launch_bounds__(ZS_BIG_NT) void zs_k_pv(zs_sargs a) {
+// 256-thread workgroups, each thread 4 of the group's ZS_BIG_NT slots: most
+// rows of a batch are not big, and launching their workgroups' waves (which
+// only read the row state) costs in proportion to the waves
+#define PV_NT 256
+__global__ __launch_bounds__(PV_NT) void zs_k_pv(zs_sargs a) {
     const uint32_t g = blockIdx.x, r = blockIdx.y;
     // (the presort task list of this step starts empty: zs_k_tp_plan and
     // zs_k_tp_inc, launched after this kernel, append to it)
@@ -464,31 +470,37 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_pv(zs_sargs a) {
     if (st.mode != ZS_MODE_BIG || !big_s_from_rounds(st)) return;
     const zs_batch& b = a.b;
     const uint32_t V = b.V;
-    const uint32_t idx0 = g * ZS_BIG_G + 4 * threadIdx.x;
     const zs_row_params P = b.d_params[r];
     const bool hist = tp_fast_row(st, P);
     __shared__ uint32_t hc[ZS_TP_NB];
     __shared__ float hm[ZS_TP_NB];
     if (hist) {
-        for (uint32_t i = threadIdx.x; i < ZS_TP_NB; i += ZS_BIG_NT) { hc[i] = 0u; hm[i] = 0.0f; }
+        for (uint32_t i = threadIdx.x; i < ZS_TP_NB; i += PV_NT) { hc[i] = 0u; hm[i] = 0.0f; }
         __syncthreads();
     }
-    if (idx0 < V) {
-        big_row R;
-        R.row = b.d_logits + (size_t)r * b.ld;
-        R.masked = (P.flags & ZS_ROW_MASKED) && b.d_allow_bits;
-        R.allow = R.masked ? b.d_allow_bits + (size_t)r * b.allow_words : nullptr;
-        R.pid = a.p_id + (size_t)r * a.pstride;
-        R.pfl = a.p_flags + (size_t)r * a.pstride;
-        R.py = a.p_y + (size_t)r * a.pstride;
-        R.psub = a.p_sub + (size_t)r * (a.max_subs + 1);
-        R.nsub = (V + ZS_SUB - 1) / ZS_SUB;
-        R.V = V;
-        R.T = P.temperature;
-        const bool use_thr = st.has_thr != 0;
-        const float thr = zs_key_to_float(st.thr_key), m = st.z_max, S = big_s_value(st);
+    big_row R;
+    R.row = b.d_logits + (size_t)r * b.ld;
+    R.masked = (P.flags & ZS_ROW_MASKED) && b.d_allow_bits;
+    R.allow = R.masked ? b.d_allow_bits + (size_t)r * b.allow_words : nullptr;
+    R.pid = a.p_id + (size_t)r * a.pstride;
+    R.pfl = a.p_flags + (size_t)r * a.pstride;
+    R.py = a.p_y + (size_t)r * a.pstride;
+    R.psub = a.p_sub + (size_t)r * (a.max_subs + 1);
+    R.nsub = (V + ZS_SUB - 1) / ZS_SUB;
+    R.V = V;
+    R.T = P.temperature;
+    const bool use_thr = st.has_thr != 0;
+    const float thr = zs_key_to_float(st.thr_key), m = st.z_max, S = big_s_value(st);
+    constexpr int NS = ZS_BIG_NT / PV_NT;
+    big_raw raw[NS];
+#pragma unroll
+    for (int u = 0; u < NS; u++) raw[u] = big_fetch(R, g, threadIdx.x + u * PV_NT);
+#pragma unroll
+    for (int u = 0; u < NS; u++) {
+        const uint32_t tix = threadIdx.x + u * PV_NT, idx0 = g * ZS_BIG_G + 4 * tix;
+        if (idx0 >= V) break;
         float x[4], z[4];
-        big_finish(R, g, big_fetch(R, g), x, z);
+        big_finish(R, g, raw[u], x, z, tix);
         uint4 o;
         uint32_t* ob = reinterpret_cast<uint32_t*>(&o);
 #pragma unroll
@@ -509,7 +521,7 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_pv(zs_sargs a) {
     if (hist) {
         __syncthreads();
         zs_tp_bucket* bk = a.tp_bk + (size_t)r * ZS_TP_NB;
-        for (uint32_t i = threadIdx.x; i < ZS_TP_NB; i += ZS_BIG_NT) {
+        for (uint32_t i = threadIdx.x; i < ZS_TP_NB; i += PV_NT) {
             if (hc[i]) {
                 atomicAdd(&bk[i].cnt, hc[i]);
                 atomicAdd(&bk[i].mass, hm[i]);
@@ -1936,7 +1948,7 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
         }
         if (!prof) ZS_LAUNCH_CHECK(hipEventRecord((hipEvent_t)ctx->join_event, hs));
     }
-    hipLaunchKernelGGL(zs_k_pv, dim3((bt->V + ZS_BIG_G - 1) / ZS_BIG_G, B), dim3(ZS_BIG_NT), 0, stream, a);
+    hipLaunchKernelGGL(zs_k_pv, dim3((bt->V + ZS_BIG_G - 1) / ZS_BIG_G, B), dim3(PV_NT), 0, stream, a);
     mark("zs_k_pv");
     hipLaunchKernelGGL(zs_k_tp_plan, dim3(B), dim3(ZS_BIG_NT), 0, stream, a);
     mark("zs_k_tp_plan");
