@@ -1379,42 +1379,51 @@ __device__ __forceinline__ float kc_p1(const zs_row_state& st, uint32_t pb) {
     return p;
 }
 
-__global__ __launch_bounds__(ZS_BIG_NT) void zs_k_kcount(zs_sargs a) {
+// (256-thread workgroups as zs_k_pv; so is zs_k_kwrite)
+__global__ __launch_bounds__(PV_NT) void zs_k_kcount(zs_sargs a) {
     const uint32_t g = blockIdx.x, r = blockIdx.y;
     const zs_row_state& st = a.rst[r];
     if (!st.kpend) return;
     const uint32_t t = threadIdx.x, V = a.b.V;
-    const uint32_t idx0 = g * ZS_BIG_G + 4 * t;
-    const uint4 v = idx0 < V ? *reinterpret_cast<const uint4*>(a.pv + (size_t)r * a.max_vocab + idx0) : make_uint4(0u, 0u, 0u, 0u);
-    const uint32_t pb[4] = {v.x, v.y, v.z, v.w};
     const uint32_t vs = st.vstar;
+    constexpr int NS = ZS_BIG_NT / PV_NT;
+    uint4 v[NS];
+#pragma unroll
+    for (int u = 0; u < NS; u++) {
+        const uint32_t idx0 = g * ZS_BIG_G + 4 * (t + u * PV_NT);
+        v[u] = idx0 < V ? *reinterpret_cast<const uint4*>(a.pv + (size_t)r * a.max_vocab + idx0) : make_uint4(0u, 0u, 0u, 0u);
+    }
     uint32_t c = 0;  // (above << 16) | equal
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-        const float p = kc_p1(st, pb[q]);
-        const uint32_t b = zs_f2u(p);
-        if (p > 0.0f && b >= vs) c += b > vs ? 0x10000u : 1u;
+    for (int u = 0; u < NS; u++) {
+        const uint32_t pb[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float p = kc_p1(st, pb[q]);
+            const uint32_t b = zs_f2u(p);
+            if (p > 0.0f && b >= vs) c += b > vs ? 0x10000u : 1u;
+        }
     }
-    __shared__ uint32_t sh[ZS_BIG_NT / 64];
+    __shared__ uint32_t sh[PV_NT / 64];
     c = wave_sum_u(c);
     if (zs_lane() == 0) sh[zs_wid()] = c;
     __syncthreads();
     if (t == 0) {
         uint32_t tot = 0;
-        for (int i = 0; i < ZS_BIG_NT / 64; i++) tot += sh[i];
+        for (int i = 0; i < PV_NT / 64; i++) tot += sh[i];
         a.kcnt[(size_t)r * a.nch * 2 + g] = tot;
     }
     // the kept-list sub-chunk sums are added by zs_k_kwrite
     if (t < ZS_BIG_G / ZS_SUB) a.k_ap[(size_t)r * a.max_subs + g * (ZS_BIG_G / ZS_SUB) + t] = 0.0;
 }
 
-__global__ __launch_bounds__(ZS_BIG_NT) void zs_k_kwrite(zs_sargs a) {
+__global__ __launch_bounds__(PV_NT) void zs_k_kwrite(zs_sargs a) {
     const uint32_t g = blockIdx.x, r = blockIdx.y;
     zs_row_state& st = a.rst[r];
     if (!st.kpend) return;
     const uint32_t t = threadIdx.x, V = a.b.V;
     const uint32_t ng = (V + ZS_BIG_G - 1) / ZS_BIG_G;
-    __shared__ uint32_t sh[ZS_BIG_NT / 64];
+    __shared__ uint32_t sh[PV_NT / 64];
     __shared__ uint32_t base_sh[3];
     __shared__ double lap[ZS_BIG_G / ZS_SUB + 1];
     const uint32_t* kc = a.kcnt + (size_t)r * a.nch * 2;
@@ -1433,40 +1442,52 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_kwrite(zs_sargs a) {
         if (t == 0) { base_sh[0] = pre_all; base_sh[1] = pre_eq; base_sh[2] = tot_all; }
     }
     if (t <= ZS_BIG_G / ZS_SUB) lap[t] = 0.0;
-    __syncthreads();
-    const uint32_t base = base_sh[0], eq0 = base_sh[1];
-    const uint32_t idx0 = g * ZS_BIG_G + 4 * t;
-    const uint4 v = idx0 < V ? *reinterpret_cast<const uint4*>(a.pv + (size_t)r * a.max_vocab + idx0) : make_uint4(0u, 0u, 0u, 0u);
-    const uint32_t pb[4] = {v.x, v.y, v.z, v.w};
-    const uint32_t vs = st.vstar, rank = st.krank;
-    uint32_t kb[4];
-    uint32_t c = 0;  // (kept << 16) | equal
+    constexpr int NS = ZS_BIG_NT / PV_NT;
+    uint4 v[NS];
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-        const float p = kc_p1(st, pb[q]);
-        kb[q] = zs_f2u(p);
-        if (p > 0.0f && kb[q] >= vs) c += 0x10000u + (kb[q] == vs ? 1u : 0u);
+    for (int u = 0; u < NS; u++) {
+        const uint32_t idx0 = g * ZS_BIG_G + 4 * (t + u * PV_NT);
+        v[u] = idx0 < V ? *reinterpret_cast<const uint4*>(a.pv + (size_t)r * a.max_vocab + idx0) : make_uint4(0u, 0u, 0u, 0u);
     }
-    uint32_t tot;
-    uint32_t ex = block_excl_scan_u<ZS_BIG_NT>(c, sh, &tot);
-    uint32_t pos = base + (ex >> 16), eq = eq0 + (ex & 0xffffu);
+    __syncthreads();
+    uint32_t pos = base_sh[0], eq = base_sh[1];
+    const uint32_t sub0 = pos / ZS_SUB;
+    const uint32_t vs = st.vstar, rank = st.krank;
     uint32_t* kp = a.pairs + (size_t)r * a.max_vocab * 2;
     uint32_t* ki = kp + a.max_vocab;
-    const uint32_t sub0 = base / ZS_SUB;
+    // the slots in index order: slot u of every thread, then slot u + 1
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-        if (!(zs_u2f(kb[q]) > 0.0f && kb[q] >= vs)) continue;
-        const uint32_t idx = idx0 + q;
-        kp[pos] = kb[q];
-        ki[pos] = idx;
-        bool in = true;
-        if (kb[q] == vs) {
-            if (eq == rank) st.istar = idx;
-            in = eq <= rank;
-            eq++;
+    for (int u = 0; u < NS; u++) {
+        const uint32_t idx0 = g * ZS_BIG_G + 4 * (t + u * PV_NT);
+        const uint32_t pb[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+        uint32_t kb[4];
+        uint32_t c = 0;  // (kept << 16) | equal
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float p = kc_p1(st, pb[q]);
+            kb[q] = zs_f2u(p);
+            if (p > 0.0f && kb[q] >= vs) c += 0x10000u + (kb[q] == vs ? 1u : 0u);
         }
-        if (in) atomicAdd(&lap[pos / ZS_SUB - sub0], (double)zs_u2f(kb[q]));
-        pos++;
+        uint32_t tot;
+        const uint32_t ex = block_excl_scan_u<PV_NT>(c, sh, &tot);
+        uint32_t ps = pos + (ex >> 16), e = eq + (ex & 0xffffu);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            if (!(zs_u2f(kb[q]) > 0.0f && kb[q] >= vs)) continue;
+            const uint32_t idx = idx0 + q;
+            kp[ps] = kb[q];
+            ki[ps] = idx;
+            bool in = true;
+            if (kb[q] == vs) {
+                if (e == rank) st.istar = idx;
+                in = e <= rank;
+                e++;
+            }
+            if (in) atomicAdd(&lap[ps / ZS_SUB - sub0], (double)zs_u2f(kb[q]));
+            ps++;
+        }
+        pos += tot >> 16;
+        eq += tot & 0xffffu;
     }
     __syncthreads();
     if (t <= ZS_BIG_G / ZS_SUB && lap[t] != 0.0) atomicAdd(&a.k_ap[(size_t)r * a.max_subs + sub0 + t], lap[t]);
@@ -1958,8 +1979,8 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
     mark("zs_k_tp_sort");
     hipLaunchKernelGGL(zs_k_big, dim3(B), dim3(ZS_BIG_NT), 0, stream, a);
     mark("zs_k_big");
-    hipLaunchKernelGGL(zs_k_kcount, dim3((bt->V + ZS_BIG_G - 1) / ZS_BIG_G, B), dim3(ZS_BIG_NT), 0, stream, a);
-    hipLaunchKernelGGL(zs_k_kwrite, dim3((bt->V + ZS_BIG_G - 1) / ZS_BIG_G, B), dim3(ZS_BIG_NT), 0, stream, a);
+    hipLaunchKernelGGL(zs_k_kcount, dim3((bt->V + ZS_BIG_G - 1) / ZS_BIG_G, B), dim3(PV_NT), 0, stream, a);
+    hipLaunchKernelGGL(zs_k_kwrite, dim3((bt->V + ZS_BIG_G - 1) / ZS_BIG_G, B), dim3(PV_NT), 0, stream, a);
     mark("zs_k_kcompact");
     const uint32_t nsubk = (bt->V + ZS_SUB - 1) / ZS_SUB;
     hipLaunchKernelGGL(zs_k_roundK<0>, dim3((nsubk + 3) / 4, B), dim3(256), 0, stream, a);
