@@ -180,8 +180,8 @@ extern "C" int zs_ctx_create(int device, uint32_t max_rows, uint32_t max_vocab, 
     if (!rc) rc = zs_alloc(ctx, &ctx->spec_chunks, R * (2 * ZS_SPEC_KMAX + 1) * C);
     if (!rc) rc = zs_alloc(ctx, &ctx->p_sub, R * (ctx->max_subs + 1));
     if (!rc) rc = zs_alloc(ctx, &ctx->k_ap, R * ctx->max_subs);
-    if (!rc) rc = zs_alloc(ctx, &ctx->k_sum, 2 * R * 2 * ctx->max_subs);   // records, then crossing records
-    if (!rc) rc = zs_alloc(ctx, &ctx->s_rec, 2 * R * ZS_NSUM * ctx->max_subs);   // records, then crossing records
+    if (!rc) rc = zs_alloc(ctx, &ctx->k_sum, 3 * R * 2 * ctx->max_subs);   // records, then crossing records (24 bytes each)
+    if (!rc) rc = zs_alloc(ctx, &ctx->s_rec, 3 * R * ZS_NSUM * ctx->max_subs);   // records, then crossing records (24 bytes each)
     if (!rc) rc = zs_alloc(ctx, &ctx->s_apx, R * 8 * ctx->max_subs);
     if (!rc) rc = zs_alloc(ctx, &ctx->gath, R * (2 * (size_t)max_vocab + 16));
     if (!rc) rc = zs_alloc(ctx, &ctx->s_hterm, R * ((size_t)max_vocab + 8));

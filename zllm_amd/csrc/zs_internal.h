@@ -170,8 +170,8 @@ struct zs_ctx {
     void* mask_scratch;    // DFA mask viability flags [rows]
     uint32_t mask_epoch;   // last epoch handed to the packed DFA mask
     double* k_ap;                // [rows][max_subs] approximate sums of the kept list per sub-chunk
-    zs_sub_sum* k_sum;           // [2][rows][2][max_subs] kept-list rounds (sum2, draw), then crossing records
-    zs_sub_sum* s_rec;           // [2][rows][ZS_NSUM][max_subs] row-sum sub-chunk records (zs_k_sround), then crossing records
+    zs_sub_sum* k_sum;           // [3][rows][2][max_subs] kept-list rounds (sum2, draw), then crossing records
+    zs_sub_sum* s_rec;           // [3][rows][ZS_NSUM][max_subs] row-sum sub-chunk records (zs_k_sround), then crossing records
     float* gath;                 // [rows][2 * max_vocab + 16] masked rows' gathered allowed ids (x~, y, ids)
     float* s_hterm;              // [rows][max_vocab + 8] exact terms of the side-stream sums (S_obs, then entropy)
     float* s_apx;                // [rows][max_subs][8] approximate row-sum parts per sub-chunk (zs_k_sapx)

@@ -1558,12 +1558,15 @@ __global__ __launch_bounds__(256) void zs_k_roundK(zs_sargs a) {
     // a sub-chunk where the sum surely starts in one binade and ends in the
     // next: its crossing record (zs_walk.h's sm_xrec), the exit term guessed
     // from the approximate start
-    if (j != 0 && lm > 0x1p-99 && hm < 0x1p100 && ilogb(lm) == ilogb(lo * (1.0 + delta)) &&
-        ilogb(hm) == ilogb(lm) + 1) {
-        const int eg = ilogb(lm) + 127;
+    // (SM_ALT, the start estimate within the margin of the next binade: the
+    // pair of all the terms on the next grid as well)
+    const int bl = lm > 0x1p-99 ? ilogb(lm) : 0, bs = lm > 0x1p-99 ? ilogb(lo * (1.0 + delta)) : 0;
+    if (j != 0 && lm > 0x1p-99 && hm < 0x1p100 && (bs == bl || bs == bl + 1) && ilogb(hm) == bl + 1) {
+        const int eg = bl + 127;
+        const bool alt = bs == bl + 1;
         const float sc = sm_scale(eg), sc2 = sm_scale(eg + 1);
-        uint32_t carry = (uint32_t)ldexp(lo, 150 - eg), xpos = 0xffffffffu;
-        seq_pair pre = {0u, 0u}, post = {0u, 0u};
+        uint32_t carry = min((uint32_t)ldexp(lo, 150 - eg), ZS_BINADE - 1u), xpos = 0xffffffffu;
+        seq_pair pre = {0u, 0u}, post = {0u, 0u}, all2 = {0u, 0u};
         float vx = 0.0f;
         for (int q = 0; q < ZS_SUB / 64; q++) {
             const float v = klist_term(L, j * ZS_SUB + q * 64 + zs_lane());
@@ -1593,25 +1596,39 @@ __global__ __launch_bounds__(256) void zs_k_roundK(zs_sargs a) {
                 }
                 carry = zs_sat_add(carry, (uint32_t)__builtin_amdgcn_readlane((int)incl, 63));
             }
-            if (xpos != 0xffffffffu) {
-                const bool after = pos > xpos;
+            if (xpos != 0xffffffffu || alt) {
                 const float qv = fminf(v * sc2, SM_QCAP);
                 float rq = rintf(qv);
-                const bool h = fabsf(qv - rq) == 0.5f && after;
-                if (h) rq = floorf(qv);
-                const uint32_t inc = after ? (uint32_t)rq : 0u;
-                if (!__builtin_amdgcn_readfirstlane((int)(__ballot(h) != 0ull))) {
-                    const uint32_t t = sm_wave_sum_sat(inc);
-                    post = seq_compose(post, seq_pair{t, t});
-                } else {
-                    post = seq_compose(post, sm_wave_pair_reduce(h ? sm_pair_tie(inc) : seq_pair{inc, inc}));
+                const bool hh = fabsf(qv - rq) == 0.5f;
+                if (hh) rq = floorf(qv);
+                const uint32_t inc2 = (uint32_t)rq;
+                if (xpos != 0xffffffffu) {
+                    const bool after = pos > xpos;
+                    const bool h = hh && after;
+                    const uint32_t inc = after ? inc2 : 0u;
+                    if (!__builtin_amdgcn_readfirstlane((int)(__ballot(h) != 0ull))) {
+                        const uint32_t t = sm_wave_sum_sat(inc);
+                        post = seq_compose(post, seq_pair{t, t});
+                    } else {
+                        post = seq_compose(post, sm_wave_pair_reduce(h ? sm_pair_tie(inc) : seq_pair{inc, inc}));
+                    }
+                }
+                if (alt) {
+                    if (!__builtin_amdgcn_readfirstlane((int)(__ballot(hh) != 0ull))) {
+                        const uint32_t t = sm_wave_sum_sat(inc2);
+                        all2 = seq_compose(all2, seq_pair{t, t});
+                    } else {
+                        all2 = seq_compose(all2, sm_wave_pair_reduce(hh ? sm_pair_tie(inc2) : seq_pair{inc2, inc2}));
+                    }
                 }
             }
         }
-        if (xpos != 0xffffffffu) {
-            e = sm_rec{eg, SM_CROSS, pre.e, pre.o};
+        const uint32_t fl = (xpos != 0xffffffffu ? SM_CROSS : 0u) | (alt ? SM_ALT : 0u);
+        if (fl) {
+            e = sm_rec{eg, fl, pre.e, pre.o};
             if (zs_lane() == 0)
-                reinterpret_cast<sm_xrec*>(a.k_xsum)[((size_t)r * 2 + KIND) * a.max_subs + j] = sm_xrec{xpos, vx, post.e, post.o};
+                reinterpret_cast<sm_xrec*>(a.k_xsum)[((size_t)r * 2 + KIND) * a.max_subs + j] =
+                    sm_xrec{xpos, vx, post.e, post.o, all2.e, all2.o};
         }
     } else if (j != 0 && lm > 0x1p-99 && hm < 0x1p100 && ilogb(lm) == ilogb(hm)) {
         e.eg = ilogb(lm) + 127;
@@ -1687,6 +1704,7 @@ __global__ __launch_bounds__(SW_NT) void zs_k_stitchK(zs_sargs a) {
     const uint32_t r = blockIdx.x;
     zs_row_state* stp = a.rst + r;
     if (!stp->klist || (KIND == 0 && !stp->knorm)) return;
+    const unsigned long long k0 = SW_CLK();
     const zs_row_state st = *stp;
     const klist_row L = make_klist(a, r, st, KIND);
     const uint32_t nks = (L.nk + ZS_SUB - 1) / ZS_SUB;
@@ -1695,7 +1713,7 @@ __global__ __launch_bounds__(SW_NT) void zs_k_stitchK(zs_sargs a) {
     for (uint32_t j = threadIdx.x; j < nks; j += SW_NT) {
         const sm_rec e = ks[j];
         sm_sh.rec[j] = e;
-        if (e.flags & SM_CROSS) sm_sh.xrec[j] = kx[j];
+        if (e.flags & (SM_CROSS | SM_ALT)) sm_sh.xrec[j] = kx[j];
     }
     __syncthreads();
     float thresh = NAN;
@@ -1710,9 +1728,11 @@ __global__ __launch_bounds__(SW_NT) void zs_k_stitchK(zs_sargs a) {
         }
         thresh = rr;
     }
+    const unsigned long long k1 = SW_CLK();
     klist_tp tp{L};
     uint32_t stop;
-    const float s = sm_stitch<klist_tp, klist_raw, true>(tp, nks, KIND ? 0.0f : -0.0f, thresh, &stop);
+    const float s = sm_stitch<klist_tp, klist_raw>(tp, nks, KIND ? 0.0f : -0.0f, thresh, &stop);
+    SW_K(KIND, SW_CLK() - k0, k1 - k0);
     if (threadIdx.x == 0) {
         if (KIND == 0) {
             stp->sum2 = s;
@@ -1996,3 +2016,11 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
     if (e != hipSuccess) return zs_set_error(ctx, ZS_EHIP, "zs_sample launch: %s", hipGetErrorString(e));
     return ZS_OK;
 }
+
+#ifdef ZS_WALK_DEBUG
+extern "C" int zs_dbg_walk_stats_k(unsigned long long* out) {
+    if (hipMemcpyFromSymbol(out, HIP_SYMBOL(sw_dbg), 32 * sizeof(unsigned long long)) != hipSuccess) return -1;
+    static unsigned long long zero[32];
+    return hipMemcpyToSymbol(HIP_SYMBOL(sw_dbg), zero, sizeof(zero)) == hipSuccess ? 0 : -1;
+}
+#endif

@@ -503,12 +503,16 @@ __device__ __forceinline__ int sm_predict(uint32_t j, double lo, double hi) {
 // pairs of the terms before x (grid eg) and after it (grid eg + 1) are taken
 // over the exact terms, a quarter (4 terms a lane) at a time in summation
 // order (quarter, lane, element). sm_cross_grid: the start grid, or 0 (no
-// record), and the estimated start on that grid.
-__device__ __forceinline__ int sm_cross_grid(uint32_t j, double lo, double mid, double hi, uint32_t* kt) {
+// record), the estimated start on that grid (below the binade's end), and
+// whether the start may already be in the next binade (SM_ALT: the pair of
+// all the terms on the next grid as well).
+__device__ __forceinline__ int sm_cross_grid(uint32_t j, double lo, double mid, double hi, uint32_t* kt,
+                                             bool* alt) {
     if (j == 0 || !(lo > 0x1p-99) || !(hi < 0x1p100)) return 0;
-    const int b = ilogb(lo);
-    if (ilogb(mid * (1.0 + SM_MARGIN)) != b || ilogb(hi) != b + 1) return 0;
-    *kt = (uint32_t)ldexp(mid, 23 - b);
+    const int b = ilogb(lo), bm = ilogb(mid * (1.0 + SM_MARGIN));
+    if (ilogb(hi) != b + 1 || (bm != b && bm != b + 1)) return 0;
+    *alt = bm == b + 1;
+    *kt = min((uint32_t)ldexp(mid, 23 - b), ZS_BINADE - 1u);
     return b + 127;
 }
 // Increments of 4 exact terms on the grid of scale sc (those in `valid`) and
@@ -544,11 +548,12 @@ __device__ __forceinline__ seq_pair sm_wave_pair4(const uint32_t (&inc)[4], uint
 }
 struct sm_xstate {
     uint32_t carry, xpos;
-    seq_pair pre, post;
+    seq_pair pre, post, alt;
     float vx;
 };
-// One quarter qi of exact terms (this lane's 4 of it, dv).
-__device__ __forceinline__ void sm_cross_quarter(sm_xstate& X, const float (&dv)[4], int qi, int eg) {
+// One quarter qi of exact terms (this lane's 4 of it, dv); alt: the pair of
+// all of them on grid eg + 1 as well.
+__device__ __forceinline__ void sm_cross_quarter(sm_xstate& X, const float (&dv)[4], int qi, int eg, bool alt) {
     const uint32_t lane = (uint32_t)zs_lane();
     const uint32_t p0 = 256u * (uint32_t)qi + 4u * lane;   // this lane's first position in the quarter
     if (X.xpos == 0xffffffffu) {
@@ -580,13 +585,16 @@ __device__ __forceinline__ void sm_cross_quarter(sm_xstate& X, const float (&dv)
         X.pre = seq_compose(X.pre, sm_wave_pair4(inc, tie & vm, vm));
         X.carry = zs_sat_add(X.carry, (uint32_t)__builtin_amdgcn_readlane((int)incl, 63));
     }
-    if (X.xpos != 0xffffffffu) {
-        uint32_t vm = 0u;
-#pragma unroll
-        for (int e = 0; e < 4; e++) vm |= (p0 + (uint32_t)e > X.xpos ? 1u : 0u) << e;
+    if (X.xpos != 0xffffffffu || alt) {
         uint32_t inc2[4], tie2;
-        sm_exact_incs4(dv, sm_scale(eg + 1), vm, inc2, tie2);
-        X.post = seq_compose(X.post, sm_wave_pair4(inc2, tie2, vm));
+        sm_exact_incs4(dv, sm_scale(eg + 1), 0xfu, inc2, tie2);
+        if (X.xpos != 0xffffffffu) {
+            uint32_t vm = 0u;
+#pragma unroll
+            for (int e = 0; e < 4; e++) vm |= (p0 + (uint32_t)e > X.xpos ? 1u : 0u) << e;
+            X.post = seq_compose(X.post, sm_wave_pair4(inc2, tie2 & vm, vm));
+        }
+        if (alt) X.alt = seq_compose(X.alt, sm_wave_pair4(inc2, tie2, 0xfu));
     }
 }
 
@@ -679,7 +687,8 @@ __global__ __launch_bounds__(SM_NT) void zs_k_sround(zs_sargs a) {
                 // unless its crossing record holds (exact terms also kept in
                 // LDS for it)
                 uint32_t kt = 0u;
-                const int xeg = sm_cross_grid(j, lo, mid, hi, &kt);
+                bool alt = false;
+                const int xeg = sm_cross_grid(j, lo, mid, hi, &kt, &alt);
                 float* xb = sm_xbuf[zs_wid()];
                 float* da = sm_darea(a, r, kinds[u]) + (size_t)j * ZS_SUB;
                 // (a rolled loop over the quarters: sixteen inlined exact
@@ -713,18 +722,19 @@ __global__ __launch_bounds__(SM_NT) void zs_k_sround(zs_sargs a) {
                 }
                 sm_rec cr = {0, 0u, 0u, 0u};
                 if (xeg) {
-                    sm_xstate X = {kt, 0xffffffffu, {0u, 0u}, {0u, 0u}, 0.0f};
+                    sm_xstate X = {kt, 0xffffffffu, {0u, 0u}, {0u, 0u}, {0u, 0u}, 0.0f};
 #pragma unroll
                     for (int qi = 0; qi < 4; qi++) {
                         const sm_f4 q4 = *reinterpret_cast<const sm_f4*>(xb + sm_pos<false>((uint32_t)zs_lane(), qi));
                         const float dv[4] = {q4.x, q4.y, q4.z, q4.w};
-                        sm_cross_quarter(X, dv, qi, xeg);
+                        sm_cross_quarter(X, dv, qi, xeg, alt);
                     }
-                    if (X.xpos != 0xffffffffu) {
-                        cr = sm_rec{xeg, SM_CROSS, X.pre.e, X.pre.o};
+                    const uint32_t fl = (X.xpos != 0xffffffffu ? SM_CROSS : 0u) | (alt ? SM_ALT : 0u);
+                    if (fl) {
+                        cr = sm_rec{xeg, fl, X.pre.e, X.pre.o};
                         if (zs_lane() == 0)
                             reinterpret_cast<sm_xrec*>(a.s_xrec)[((size_t)r * ZS_NSUM + kinds[u]) * a.max_subs + j] =
-                                sm_xrec{X.xpos, X.vx, X.post.e, X.post.o};
+                                sm_xrec{X.xpos, X.vx, X.post.e, X.post.o, X.alt.e, X.alt.o};
                     }
                 }
                 if (zs_lane() == 0) rec[(size_t)kinds[u] * a.max_subs] = cr;
@@ -793,6 +803,7 @@ __global__ __launch_bounds__(SW_NT) void zs_k_sstitch(zs_sargs a) {
     zs_row_state* stp = a.rst + r;
     const int kind = sm_stage_kind<STAGE>();
     if (!((stp->rounds >> kind) & 1u)) return;
+    const unsigned long long k0 = SW_CLK();
     sm_tab_fill();
     const zs_row_state& st = *stp;
     const zs_row_params P = a.b.d_params[r];
@@ -804,12 +815,14 @@ __global__ __launch_bounds__(SW_NT) void zs_k_sstitch(zs_sargs a) {
     for (uint32_t i = threadIdx.x; i < nsub; i += SW_NT) {
         const sm_rec e = rec[i];
         sm_sh.rec[i] = e;
-        if (e.flags & SM_CROSS) sm_sh.xrec[i] = xrec[i];
+        if (e.flags & (SM_CROSS | SM_ALT)) sm_sh.xrec[i] = xrec[i];
     }
     __syncthreads();
+    const unsigned long long k1 = SW_CLK();
     sm_row_tp tp{S, f, sm_darea(a, r, kind)};
     uint32_t stop;
-    const float s = sm_stitch<sm_row_tp, sm_f4, true>(tp, nsub, kind == ZS_SUM_OBS_H ? 0.0f : -0.0f, NAN, &stop);
+    const float s = sm_stitch<sm_row_tp, sm_f4>(tp, nsub, kind == ZS_SUM_OBS_H ? 0.0f : -0.0f, NAN, &stop);
+    SW_K(STAGE - 1, SW_CLK() - k0, k1 - k0);
     if (threadIdx.x == 0) {
         if (kind == ZS_SUM_OBS_S) stp->obs_S = s;
         else if (kind == ZS_SUM_SAMP_S) stp->samp_S = s;
@@ -818,9 +831,14 @@ __global__ __launch_bounds__(SW_NT) void zs_k_sstitch(zs_sargs a) {
 }
 
 #ifdef ZS_WALK_DEBUG
+extern "C" int zs_dbg_walk_hist(unsigned long long* out) {
+    if (hipMemcpyFromSymbol(out, HIP_SYMBOL(sw_hist), 64 * sizeof(unsigned long long)) != hipSuccess) return -1;
+    static unsigned long long zero[64];
+    return hipMemcpyToSymbol(HIP_SYMBOL(sw_hist), zero, sizeof(zero)) == hipSuccess ? 0 : -1;
+}
 extern "C" int zs_dbg_walk_stats(unsigned long long* out) {
-    if (hipMemcpyFromSymbol(out, HIP_SYMBOL(sw_dbg), 16 * sizeof(unsigned long long)) != hipSuccess) return -1;
-    static unsigned long long zero[16];
+    if (hipMemcpyFromSymbol(out, HIP_SYMBOL(sw_dbg), 32 * sizeof(unsigned long long)) != hipSuccess) return -1;
+    static unsigned long long zero[32];
     return hipMemcpyToSymbol(HIP_SYMBOL(sw_dbg), zero, sizeof(zero)) == hipSuccess ? 0 : -1;
 }
 #endif

@@ -46,11 +46,17 @@ struct sm_rec {
 // terms x+1 .. on grid eg + 1. The stitch checks the guess from the exact
 // running sum (no exit before x, an exit at x into binade eg + 1, none after)
 // and walks the sub-chunk when it fails.
+// SM_ALT: the start may already be in binade eg + 1 (the crossing near the
+// sub-chunk's start, on either side of it): the record also holds the pair
+// of all the terms on grid eg + 1 (a0, a1), applied when the exact running
+// sum is found there. (SM_ALT without SM_CROSS: only that pair is valid.)
 #define SM_CROSS 2u
+#define SM_ALT 4u
 struct sm_xrec {
     uint32_t x;
     float vx;
     uint32_t p0, p1;
+    uint32_t a0, a1;
 };
 
 // 2^(150 - eg): the scale of grid eg (eg >= 24).
@@ -156,11 +162,15 @@ __shared__ sm_wsh sm_sh;
 
 #ifdef ZS_WALK_DEBUG
 // working diagnostics: cycles per walk phase (summed over workgroups)
-__device__ unsigned long long sw_dbg[16];
+__device__ unsigned long long sw_dbg[32];
+__device__ unsigned long long sw_hist[64];
 __shared__ unsigned long long sw_acc[16];
 #define SW_T(i, c) do { if (threadIdx.x == 0) sw_acc[i] += (unsigned long long)(c); } while (0)
 #define SW_CLK() clock64()
+#define SW_K(k, tot, pre) do { if (threadIdx.x == 0) { atomicMax(&sw_dbg[16 + 3 * (k)], (unsigned long long)(tot)); \
+    atomicAdd(&sw_dbg[17 + 3 * (k)], (unsigned long long)(tot)); atomicAdd(&sw_dbg[18 + 3 * (k)], (unsigned long long)(pre)); } } while (0)
 #else
+#define SW_K(k, tot, pre) ((void)0)
 #define SW_T(i, c) ((void)0)
 #define SW_CLK() 0ull
 #endif
@@ -257,6 +267,21 @@ __device__ __forceinline__ float sm_walk(const float (&v)[SW_TPT], float s, floa
                     for (; e < e1 && (e & 3u); e++) {   // to a multiple of 4
                         ss = ss + sh.hv[e];
                         if (thr && ss >= thresh) { sp = base + e; break; }
+                    }
+                    // 32 terms per batch of LDS reads (their latency off the
+                    // chain of additions); a batch that reaches the threshold
+                    // is done again below, 4 terms at a time, to find the term
+                    if (sp == 0xffffffffu) {
+                        for (; e + 32 <= e1; e += 32) {
+                            float4 q8[8];
+#pragma unroll
+                            for (int i = 0; i < 8; i++) q8[i] = *reinterpret_cast<const float4*>(&sh.hv[e + 4 * i]);
+                            float c = ss;
+#pragma unroll
+                            for (int i = 0; i < 8; i++) c = (((c + q8[i].x) + q8[i].y) + q8[i].z) + q8[i].w;
+                            if (thr && c >= thresh) break;
+                            ss = c;
+                        }
                     }
                     if (sp == 0xffffffffu) {
                         for (; e + 4 <= e1; e += 4) {
@@ -443,37 +468,58 @@ __device__ __forceinline__ float sm_walk(const float (&v)[SW_TPT], float s, floa
     return s;
 }
 
-// First sub-chunk from j whose record is not safe (nsub: none); uniform.
+// First sub-chunk from j whose record is neither safe nor a crossing record
+// (nsub: none): the next one whose terms the stitch will surely need; uniform.
 __device__ __forceinline__ uint32_t sm_next_fragile(uint32_t j, uint32_t nsub) {
     for (uint32_t i0 = j; i0 < nsub; i0 += 64) {
         const uint32_t i = i0 + (uint32_t)zs_lane();
-        const unsigned long long m = __ballot(i < nsub && !(sm_sh.rec[i].flags & SM_SAFE));
+        const unsigned long long m = __ballot(i < nsub && !(sm_sh.rec[i].flags & (SM_SAFE | SM_CROSS | SM_ALT)));
         if (m) return i0 + (uint32_t)(__ffsll((long long)m) - 1);
     }
     return nsub;
 }
 
-// The sum over nsub sub-chunks whose records are in sm_sh.rec, from s, with
-// the stop threshold `thresh` (NaN: none): *stop = the global index of the
-// term where the sum reaches it, else 0xffffffff. The term provider TP gives
-// the thread's 4 exact terms of a sub-chunk: tp.fetch(j, raw) issues the
-// loads of a sub-chunk the records send to the walk (two walks ahead),
-// tp.take(j, raw, v) turns them into terms, tp.direct(j, v) computes them
-// for a sub-chunk whose record was safe but whose total did not apply.
+// The sum over nsub sub-chunks whose records are in sm_sh.rec (crossing
+// records in sm_sh.xrec), from s, with the stop threshold `thresh` (NaN:
+// none): *stop = the global index of the term where the sum reaches it, else
+// 0xffffffff. The term provider TP gives the thread's 4 exact terms of a
+// sub-chunk: tp.fetch(j, raw) issues the loads of the stored exact terms of
+// a sub-chunk the round kernel left without a safe record (those with neither
+// a safe nor a crossing record two walks ahead; a crossing record's terms
+// only when it does not hold), tp.take(j, raw, v) turns them into terms,
+// tp.direct(j, v) computes them for a sub-chunk whose record was safe but
+// whose total did not apply.
 // A crossing record of sub-chunk j applied to the exact running sum s
 // (uniform): true with the new sum, or with *stop set when the threshold is
 // reached at its term x; false when its guess does not hold.
 __device__ __forceinline__ bool sm_cross(uint32_t j, float& s, float thresh, uint32_t* stop) {
     const sm_rec e = sm_sh.rec[j];
-    if (!(e.flags & SM_CROSS) || s == 0.0f) return false;
+    const sm_xrec xr = sm_sh.xrec[j];   // (read with the record: meaningful only with SM_CROSS / SM_ALT)
+    if (!(e.flags & (SM_CROSS | SM_ALT)) || s == 0.0f) return false;
     const int eg = zs_grid_exp(s);
-    if (e.eg != eg) return false;
-    const sm_xrec xr = sm_sh.xrec[j];
     const uint32_t k = zs_grid_k(s);
+    if ((e.flags & SM_ALT) && eg == e.eg + 1) {
+        // already past the crossing: every term on this grid
+        const uint32_t ka = zs_sat_add(k, (k & 1u) ? xr.a1 : xr.a0);
+        if (ka >= ZS_BINADE || ka >= zs_grid_thresh(thresh, eg)) return false;
+        s = zs_grid_value(ka, eg);
+        return true;
+    }
+    if (e.eg != eg || !(e.flags & SM_CROSS)) {
+#ifdef ZS_WALK_DEBUG
+        if (threadIdx.x == 0) atomicAdd(&sw_dbg[30], 1ull);
+#endif
+        return false;
+    }
     const uint32_t k1 = zs_sat_add(k, (k & 1u) ? e.d1 : e.d0);
-    if (k1 >= ZS_BINADE || k1 >= zs_grid_thresh(thresh, eg)) return false;
+    if (k1 >= ZS_BINADE || k1 >= zs_grid_thresh(thresh, eg)) { SW_T(15, 1); return false; }
     const float sx = zs_grid_value(k1, eg) + xr.vx;   // the term that leaves the binade
-    if (zs_grid_exp(sx) != eg + 1) return false;
+    if (zs_grid_exp(sx) != eg + 1) {
+#ifdef ZS_WALK_DEBUG
+        if (threadIdx.x == 0) atomicAdd(&sw_dbg[31], 1ull);
+#endif
+        return false;
+    }
     if (sx >= thresh) {
         *stop = j * ZS_SUB + xr.x;
         s = sx;
@@ -486,7 +532,7 @@ __device__ __forceinline__ bool sm_cross(uint32_t j, float& s, float thresh, uin
     return true;
 }
 
-template <class TP, class RAW, bool XR = false>
+template <class TP, class RAW>
 __device__ __forceinline__ float sm_stitch(TP& tp, uint32_t nsub, float s, float thresh, uint32_t* stop) {
     const uint32_t lane = (uint32_t)zs_lane();
     *stop = 0xffffffffu;
@@ -500,7 +546,9 @@ __device__ __forceinline__ float sm_stitch(TP& tp, uint32_t nsub, float s, float
     if (nf1 < nsub) tp.fetch(nf1, q1);
     uint32_t j = 0;
     while (j < nsub) {
-        if (s != 0.0f) {
+        const unsigned long long g0 = SW_CLK();
+        const uint32_t fj = sm_sh.rec[j].flags;
+        if (s != 0.0f && (fj & SM_SAFE)) {
             // sub-chunks j .. j+63 on the grid of s, applied up to the first
             // one that is not safe, is on another grid, leaves the binade or
             // reaches the threshold
@@ -515,13 +563,14 @@ __device__ __forceinline__ float sm_stitch(TP& tp, uint32_t nsub, float s, float
             const unsigned long long bad = __ballot(!(ok && kend < ZS_BINADE && kend < kthr));
             const uint32_t n_ok = bad ? (uint32_t)(__ffsll((long long)bad) - 1) : 64u;
             if (n_ok) {
-                SW_T(11, 1);
+                SW_T(11, 1); SW_T(14, SW_CLK() - g0);
                 s = zs_grid_value((uint32_t)__builtin_amdgcn_readlane((int)kend, (int)n_ok - 1), eg);
                 j += n_ok;
                 continue;
             }
         }
-        if (XR && j == nf0) {
+        const bool xr = (fj & (SM_CROSS | SM_ALT)) != 0u;
+        if (xr) {
             uint32_t sp = 0xffffffffu;
             if (sm_cross(j, s, thresh, &sp)) {
                 SW_T(13, 1);
@@ -529,27 +578,37 @@ __device__ __forceinline__ float sm_stitch(TP& tp, uint32_t nsub, float s, float
                     *stop = sp;
                     break;
                 }
-                // the prefetched terms of j are not needed: on to the next fragile one
-                nf0 = nf1;
-                q0 = q1;
-                nf1 = nf0 < nsub ? sm_next_fragile(nf0 + 1, nsub) : nsub;
-                if (nf1 < nsub) tp.fetch(nf1, q1);
                 j++;
+                SW_T(12, SW_CLK() - g0);
                 continue;
             }
         }
         float v[SW_TPT];
         const unsigned long long l0 = SW_CLK();
-        if (j == nf0) {
+        if (xr) {
+            // a crossing record that did not hold: its stored terms
+            RAW qx;
+            tp.fetch(j, qx);
+            tp.take(j, qx, v);
+        } else if (j == nf0) {
+#ifdef ZS_WALK_DEBUG
+            if (threadIdx.x == 0 && !(sm_sh.rec[j].flags & SM_CROSS)) atomicAdd(&sw_dbg[28], 1ull);
+#endif
             tp.take(j, q0, v);
             nf0 = nf1;
             q0 = q1;
             nf1 = nf0 < nsub ? sm_next_fragile(nf0 + 1, nsub) : nsub;
             if (nf1 < nsub) tp.fetch(nf1, q1);
         } else {
+#ifdef ZS_WALK_DEBUG
+            if (threadIdx.x == 0) atomicAdd(&sw_dbg[27], 1ull);
+#endif
             tp.direct(j, v);
         }
         uint32_t sp;
+#ifdef ZS_WALK_DEBUG
+        if (threadIdx.x == 0) atomicAdd(&sw_hist[j < 31u ? j : (j + 32u >= nsub ? 63u - (nsub - 1u - j) : 31u)], 1ull);
+#endif
         const unsigned long long l1 = SW_CLK();
         SW_T(8, l1 - l0); SW_T(9, 1);
         s = sm_walk(v, s, thresh, &sp);
