@@ -1555,6 +1555,21 @@ __global__ __launch_bounds__(256) void zs_k_roundK(zs_sargs a) {
     const double delta = 1.0 / 256.0;
     const double lm = lo * (1.0 - delta), hm = hi * (1.0 + delta);
     sm_rec e = {0, 0u, 0u, 0u};
+    if (j == 0) {
+        // sub-chunk 0 from the sum's start value, term by term (with the
+        // draw's stop threshold, the uniform zs_k_stitchK compares with)
+        __shared__ float k0buf[ZS_SUB];
+#pragma unroll
+        for (int q = 0; q < ZS_SUB / 64; q++) k0buf[q * 64 + zs_lane()] = klist_term(L, q * 64 + zs_lane());
+        __builtin_amdgcn_s_waitcnt(0);
+        __builtin_amdgcn_wave_barrier();
+        const float thr = KIND == 1 ? zs_philox_uniform(a.b.d_seed[r], a.b.d_counter[r], 0u) : NAN;
+        uint32_t sp;
+        const float s0 = sm_serial(k0buf, ZS_SUB, KIND ? 0.0f : -0.0f, thr, &sp);
+        if (zs_lane() == 0)
+            reinterpret_cast<sm_rec*>(a.k_sum)[((size_t)r * 2 + KIND) * a.max_subs] = sm_rec{0, SM_EXACT, __float_as_uint(s0), sp};
+        return;
+    }
     // a sub-chunk where the sum surely starts in one binade and ends in the
     // next: its crossing record (zs_walk.h's sm_xrec), the exit term guessed
     // from the approximate start

@@ -712,7 +712,7 @@ __global__ __launch_bounds__(SM_NT) void zs_k_sround(zs_sargs a) {
                         for (int e = 0; e < 4; e++)
                             if (j * ZS_SUB + p + e < S.n) da[p + e] = dv[e];
                     }
-                    if (xeg) {
+                    if (xeg || j == 0) {
                         // (terms past the row: none, as in the walk)
                         float dz[4];
 #pragma unroll
@@ -721,7 +721,14 @@ __global__ __launch_bounds__(SM_NT) void zs_k_sround(zs_sargs a) {
                     }
                 }
                 sm_rec cr = {0, 0u, 0u, 0u};
-                if (xeg) {
+                if (j == 0) {
+                    // sub-chunk 0 from the sum's start value, term by term
+                    __builtin_amdgcn_s_waitcnt(0);
+                    __builtin_amdgcn_wave_barrier();
+                    uint32_t sp;
+                    const float s0 = sm_serial(xb, ZS_SUB, kinds[u] == ZS_SUM_OBS_H ? 0.0f : -0.0f, NAN, &sp);
+                    cr = sm_rec{0, SM_EXACT, __float_as_uint(s0), 0xffffffffu};
+                } else if (xeg) {
                     sm_xstate X = {kt, 0xffffffffu, {0u, 0u}, {0u, 0u}, {0u, 0u}, 0.0f};
 #pragma unroll
                     for (int qi = 0; qi < 4; qi++) {

@@ -52,6 +52,11 @@ struct sm_rec {
 // sum is found there. (SM_ALT without SM_CROSS: only that pair is valid.)
 #define SM_CROSS 2u
 #define SM_ALT 4u
+// SM_EXACT (sub-chunk 0 only): the round kernel, which knows the sum's start
+// value, added the sub-chunk's terms one by one itself: d0 holds the bits of
+// the sum after them, d1 the term where it reached the stop threshold (or
+// 0xffffffff).
+#define SM_EXACT 8u
 struct sm_xrec {
     uint32_t x;
     float vx;
@@ -468,12 +473,41 @@ __device__ __forceinline__ float sm_walk(const float (&v)[SW_TPT], float s, floa
     return s;
 }
 
+// The sequential f32 sum of buf[0 .. n-1] (LDS, n a multiple of 32) from s,
+// one addition per term in order, stopping at the first term where it
+// reaches thresh (NaN: never): *stop = that term, else 0xffffffff. The terms
+// are read 32 at a time, so their loads stay off the chain of additions; a
+// batch that reaches the threshold is added again term by term.
+__device__ __forceinline__ float sm_serial(const float* buf, uint32_t n, float s, float thresh, uint32_t* stop) {
+    *stop = 0xffffffffu;
+    const bool thr = thresh == thresh;
+    for (uint32_t e = 0; e < n; e += 32) {
+        float4 q8[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) q8[i] = *reinterpret_cast<const float4*>(buf + e + 4 * i);
+        float c = s;
+#pragma unroll
+        for (int i = 0; i < 8; i++) c = (((c + q8[i].x) + q8[i].y) + q8[i].z) + q8[i].w;
+        if (thr && c >= thresh) {
+            for (uint32_t i = e; i < e + 32; i++) {
+                s = s + buf[i];
+                if (s >= thresh) {
+                    *stop = i;
+                    return s;
+                }
+            }
+        }
+        s = c;
+    }
+    return s;
+}
+
 // First sub-chunk from j whose record is neither safe nor a crossing record
 // (nsub: none): the next one whose terms the stitch will surely need; uniform.
 __device__ __forceinline__ uint32_t sm_next_fragile(uint32_t j, uint32_t nsub) {
     for (uint32_t i0 = j; i0 < nsub; i0 += 64) {
         const uint32_t i = i0 + (uint32_t)zs_lane();
-        const unsigned long long m = __ballot(i < nsub && !(sm_sh.rec[i].flags & (SM_SAFE | SM_CROSS | SM_ALT)));
+        const unsigned long long m = __ballot(i < nsub && !(sm_sh.rec[i].flags & (SM_SAFE | SM_CROSS | SM_ALT | SM_EXACT)));
         if (m) return i0 + (uint32_t)(__ffsll((long long)m) - 1);
     }
     return nsub;
@@ -545,6 +579,14 @@ __device__ __forceinline__ float sm_stitch(TP& tp, uint32_t nsub, float s, float
     if (nf0 < nsub) tp.fetch(nf0, q0);
     if (nf1 < nsub) tp.fetch(nf1, q1);
     uint32_t j = 0;
+    if (nsub && (sm_sh.rec[0].flags & SM_EXACT)) {
+        s = __uint_as_float(sm_sh.rec[0].d0);
+        if (sm_sh.rec[0].d1 != 0xffffffffu) {
+            *stop = sm_sh.rec[0].d1;
+            return s;
+        }
+        j = 1;
+    }
     while (j < nsub) {
         const unsigned long long g0 = SW_CLK();
         const uint32_t fj = sm_sh.rec[j].flags;
