@@ -33,12 +33,6 @@
 #include "zs_sampler.h"
 #include "zs_walk.h"
 
-// Saturating sum over the wave (the kept-list sums' per-wave totals).
-__device__ __forceinline__ uint32_t wave_sum_sat(uint32_t v) {
-    for (int d = 32; d > 0; d >>= 1) v = zs_sat_add(v, __shfl_xor(v, d, 64));
-    return v;
-}
-
 // ===========================================================================
 // zs_k_big: exact emulation of the reference's sequential sums over a full row.
 // ===========================================================================
@@ -1523,19 +1517,39 @@ __device__ __forceinline__ klist_row make_klist(const zs_sargs& a, uint32_t r, c
     L.inv = kind && st.knorm ? 1.0f : 0.0f;
     return L;
 }
-// term i of the list: the kept p (0 for the equal values after i*), divided by
-// sum2 for the draw
-__device__ __forceinline__ float klist_term(const klist_row& L, uint32_t i) {
-    if (i >= L.nk) return 0.0f;
-    const uint32_t pb = L.kp[i];
-    if (!(pb > L.vstar || L.ki[i] <= L.istar)) return 0.0f;
-    const float p = zs_u2f(pb);
-    return L.inv != 0.0f ? p / L.sum2 : p;
+// A wave's 16 terms of sub-chunk j (tv[q]: entry j * ZS_SUB + 64 q + lane),
+// every load issued before the first is used. Term i of the list: the kept p
+// (0 for the equal values after i*, and past the list), divided by sum2 for
+// the draw.
+__device__ __forceinline__ void klist_terms16(const klist_row& L, uint32_t j, float (&tv)[ZS_SUB / 64]) {
+    // (unconditional loads at an index clamped into the list, L.nk >= 1: a
+    // bounds test around each would become a branch that waits for it)
+    uint32_t pb[ZS_SUB / 64], id[ZS_SUB / 64];
+#pragma unroll
+    for (int q = 0; q < ZS_SUB / 64; q++) {
+        const uint32_t i = min(j * ZS_SUB + (uint32_t)q * 64u + (uint32_t)zs_lane(), L.nk - 1u);
+        pb[q] = L.kp[i];
+        id[q] = L.ki[i];
+    }
+#pragma unroll
+    for (int q = 0; q < ZS_SUB / 64; q++) {
+        const uint32_t i = j * ZS_SUB + (uint32_t)q * 64u + (uint32_t)zs_lane();
+        float p = 0.0f;
+        if (i < L.nk && (pb[q] > L.vstar || id[q] <= L.istar)) {
+            p = zs_u2f(pb[q]);
+            if (L.inv != 0.0f) p = p / L.sum2;
+        }
+        tv[q] = p;
+    }
 }
 
 // one wave per (sub-chunk, row): the increment pair of the sub-chunk on the
 // grid predicted from the approximate prefix (terms in order: the q-th 64
 // entries, lanes in order)
+#ifdef ZS_WALK_DEBUG
+__device__ unsigned long long sw_wt[64 * 160];
+__device__ unsigned long long sw_wt2[64 * 160];
+#endif
 template <int KIND>
 __global__ __launch_bounds__(256) void zs_k_roundK(zs_sargs a) {
     const uint32_t r = blockIdx.y;
@@ -1544,23 +1558,35 @@ __global__ __launch_bounds__(256) void zs_k_roundK(zs_sargs a) {
     if (!st.klist || (KIND == 0 && !st.knorm)) return;   // no sum2 without a top-p cut
     const uint32_t nks = (st.nk + ZS_SUB - 1) / ZS_SUB;
     if (j >= nks) return;
+    const unsigned long long t0 = SW_CLK();
     const klist_row L = make_klist(a, r, st, KIND);
     const double* ap = a.k_ap + (size_t)r * a.max_subs;
     // approximate prefix before sub-chunk j and after it
     double pre = 0.0;
     for (uint32_t i = zs_lane(); i < j; i += 64) pre += ap[i];
     pre = wave_sum_d(pre);
+#ifdef ZS_WALK_DEBUG
+    const unsigned long long t1 = SW_CLK();
+#endif
     const double scale = KIND ? 1.0 / (double)L.sum2 : 1.0;
     const double lo = pre * scale, hi = (pre + ap[j]) * scale;
     const double delta = 1.0 / 256.0;
     const double lm = lo * (1.0 - delta), hm = hi * (1.0 + delta);
     sm_rec e = {0, 0u, 0u, 0u};
+    float tv[ZS_SUB / 64];
+    klist_terms16(L, j, tv);
+#ifdef ZS_WALK_DEBUG
+    float tvs = 0.0f;
+    for (int q = 0; q < ZS_SUB / 64; q++) tvs += tv[q];
+    const unsigned long long t2 = SW_CLK() + (tvs == 12345.0f ? 1 : 0);
+    if (zs_lane() == 0 && r < 64) sw_wt2[r * 160 + j] = (t1 - t0) | ((t2 - t0) << 32);
+#endif
     if (j == 0) {
         // sub-chunk 0 from the sum's start value, term by term (with the
         // draw's stop threshold, the uniform zs_k_stitchK compares with)
         __shared__ float k0buf[ZS_SUB];
 #pragma unroll
-        for (int q = 0; q < ZS_SUB / 64; q++) k0buf[q * 64 + zs_lane()] = klist_term(L, q * 64 + zs_lane());
+        for (int q = 0; q < ZS_SUB / 64; q++) k0buf[q * 64 + zs_lane()] = tv[q];
         __builtin_amdgcn_s_waitcnt(0);
         __builtin_amdgcn_wave_barrier();
         const float thr = KIND == 1 ? zs_philox_uniform(a.b.d_seed[r], a.b.d_counter[r], 0u) : NAN;
@@ -1568,6 +1594,9 @@ __global__ __launch_bounds__(256) void zs_k_roundK(zs_sargs a) {
         const float s0 = sm_serial(k0buf, ZS_SUB, KIND ? 0.0f : -0.0f, thr, &sp);
         if (zs_lane() == 0)
             reinterpret_cast<sm_rec*>(a.k_sum)[((size_t)r * 2 + KIND) * a.max_subs] = sm_rec{0, SM_EXACT, __float_as_uint(s0), sp};
+#ifdef ZS_WALK_DEBUG
+        if (zs_lane() == 0 && r < 64) sw_wt[r * 160 + j] = SW_CLK() - t0;
+#endif
         return;
     }
     // a sub-chunk where the sum surely starts in one binade and ends in the
@@ -1583,8 +1612,9 @@ __global__ __launch_bounds__(256) void zs_k_roundK(zs_sargs a) {
         uint32_t carry = min((uint32_t)ldexp(lo, 150 - eg), ZS_BINADE - 1u), xpos = 0xffffffffu;
         seq_pair pre = {0u, 0u}, post = {0u, 0u}, all2 = {0u, 0u};
         float vx = 0.0f;
+#pragma unroll
         for (int q = 0; q < ZS_SUB / 64; q++) {
-            const float v = klist_term(L, j * ZS_SUB + q * 64 + zs_lane());
+            const float v = tv[q];
             const uint32_t pos = (uint32_t)q * 64u + (uint32_t)zs_lane();
             if (xpos == 0xffffffffu) {
                 const float qv = fminf(v * sc, SM_QCAP);
@@ -1651,7 +1681,7 @@ __global__ __launch_bounds__(256) void zs_k_roundK(zs_sargs a) {
         uint32_t inc[ZS_SUB / 64], tie = 0u, tot = 0u;
 #pragma unroll
         for (int q = 0; q < ZS_SUB / 64; q++) {
-            const float qv = fminf(klist_term(L, j * ZS_SUB + q * 64 + zs_lane()) * sc, SM_QCAP);
+            const float qv = fminf(tv[q] * sc, SM_QCAP);
             float rq = rintf(qv);
             if (fabsf(qv - rq) == 0.5f) {
                 tie |= 1u << q;
@@ -1676,6 +1706,9 @@ __global__ __launch_bounds__(256) void zs_k_roundK(zs_sargs a) {
         e.d1 = all.o;
     }
     if (zs_lane() == 0) reinterpret_cast<sm_rec*>(a.k_sum)[((size_t)r * 2 + KIND) * a.max_subs + j] = e;
+#ifdef ZS_WALK_DEBUG
+    if (zs_lane() == 0 && r < 64) sw_wt[r * 160 + j] = (SW_CLK() - t0) | ((unsigned long long)(e.flags) << 48);
+#endif
 }
 
 // Kept-list terms for sm_stitch: thread t's 4 consecutive entries.
@@ -2019,10 +2052,13 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
     mark("zs_k_kcompact");
     const uint32_t nsubk = (bt->V + ZS_SUB - 1) / ZS_SUB;
     hipLaunchKernelGGL(zs_k_roundK<0>, dim3((nsubk + 3) / 4, B), dim3(256), 0, stream, a);
+    mark("zs_k_roundK0");
     hipLaunchKernelGGL(zs_k_stitchK<0>, dim3(B), dim3(SW_NT), 0, stream, a);
+    mark("zs_k_stitchK0");
     hipLaunchKernelGGL(zs_k_roundK<1>, dim3((nsubk + 3) / 4, B), dim3(256), 0, stream, a);
+    mark("zs_k_roundK1");
     hipLaunchKernelGGL(zs_k_stitchK<1>, dim3(B), dim3(SW_NT), 0, stream, a);
-    mark("zs_k_kept");
+    mark("zs_k_stitchK1");
     if (!prof) ZS_LAUNCH_CHECK(hipStreamWaitEvent(stream, (hipEvent_t)ctx->join_event, 0));
     hipLaunchKernelGGL(zs_k_final, dim3(B), dim3(64), 0, stream, a);
     mark("zs_k_final");
@@ -2033,6 +2069,10 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
 }
 
 #ifdef ZS_WALK_DEBUG
+extern "C" int zs_dbg_wave_times(unsigned long long* out) {
+    if (hipMemcpyFromSymbol(out + 64 * 160, HIP_SYMBOL(sw_wt2), 64 * 160 * sizeof(unsigned long long)) != hipSuccess) return -1;
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(sw_wt), 64 * 160 * sizeof(unsigned long long)) == hipSuccess ? 0 : -1;
+}
 extern "C" int zs_dbg_walk_stats_k(unsigned long long* out) {
     if (hipMemcpyFromSymbol(out, HIP_SYMBOL(sw_dbg), 32 * sizeof(unsigned long long)) != hipSuccess) return -1;
     static unsigned long long zero[32];

@@ -111,25 +111,19 @@ __device__ __forceinline__ uint32_t sm_wave_scan_sat(uint32_t x) {
 }
 
 // Ordered reduction of pairs over the wave (lanes in increasing order; the
-// result is uniform).
+// result is uniform): the last lane of the DPP scan (the composition is
+// associative), which keeps it off the LDS permute path of lane shuffles.
 __device__ __forceinline__ seq_pair sm_wave_pair_reduce(seq_pair p) {
-    const uint32_t lane = (uint32_t)zs_lane();
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        seq_pair o;
-        o.e = (uint32_t)__shfl_down((int)p.e, d, 64);
-        o.o = (uint32_t)__shfl_down((int)p.o, d, 64);
-        if ((lane & (2u * d - 1u)) == 0u && lane + d < 64u) p = seq_compose(p, o);
-    }
-    p.e = (uint32_t)__builtin_amdgcn_readfirstlane((int)p.e);
-    p.o = (uint32_t)__builtin_amdgcn_readfirstlane((int)p.o);
+    p = sm_wave_pair_scan(p);
+    p.e = (uint32_t)__builtin_amdgcn_readlane((int)p.e, 63);
+    p.o = (uint32_t)__builtin_amdgcn_readlane((int)p.o, 63);
     return p;
 }
 
+// Saturating sum over the wave (uniform), the same way (the clamp at
+// ZS_INC_CAP of non-negative terms is associative).
 __device__ __forceinline__ uint32_t sm_wave_sum_sat(uint32_t v) {
-#pragma unroll
-    for (int d = 32; d > 0; d >>= 1) v = zs_sat_add(v, (uint32_t)__shfl_xor((int)v, d, 64));
-    return (uint32_t)__builtin_amdgcn_readfirstlane((int)v);
+    return (uint32_t)__builtin_amdgcn_readlane((int)sm_wave_scan_sat(v), 63);
 }
 
 __device__ __forceinline__ float sm_lane_f(float v, uint32_t l) {
