@@ -95,6 +95,8 @@ struct zs_row_state {
     uint32_t nk;          // list length
     uint32_t vstar, istar;  // kept: p > v*, or p == v* and id <= i*
     uint32_t kpend;       // 1: the kept list is compacted by zs_k_kcount / zs_k_kwrite
+    uint32_t kident;      // 1: the kept list is the row's p in index order (every positive p, no
+                          //    min-p; its zeros add nothing): zs_k_kcount only sums its sub-chunks
     uint32_t krank;       // rank of the top-p stop among the values equal to v*
     uint32_t kminp;       // min-p applies: p1 = p < kcut ? 0 : p / kkept
     uint32_t knorm;       // 1: the draw runs on p1 / sum2 (top-p renormalisation); 0: on p1 (no sum2)

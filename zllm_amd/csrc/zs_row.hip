@@ -1474,6 +1474,7 @@ __global__ __launch_bounds__(RW_NT) void zs_k_row(zs_sargs a) {
         st.n_cand = n_cand;
         st.klist = 0;
         st.kpend = 0;
+        st.kident = 0;
         st.knorm = 0;
         st.samp_S = -0.0f;
         st.obs_S = -0.0f;

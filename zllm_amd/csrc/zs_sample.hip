@@ -1352,6 +1352,7 @@ __global__ __launch_bounds__(ZS_BIG_NT) void zs_k_big(zs_sargs a) {
         o.kcut = cut;
         o.kkept = kept;
         o.kpend = 1;
+        o.kident = minp ? 0u : 1u;
         o.knorm = topp ? 1u : 0u;
     }
 }
@@ -1376,7 +1377,7 @@ __device__ __forceinline__ float kc_p1(const zs_row_state& st, uint32_t pb) {
 // (256-thread workgroups as zs_k_pv; so is zs_k_kwrite)
 __global__ __launch_bounds__(PV_NT) void zs_k_kcount(zs_sargs a) {
     const uint32_t g = blockIdx.x, r = blockIdx.y;
-    const zs_row_state& st = a.rst[r];
+    zs_row_state& st = a.rst[r];
     if (!st.kpend) return;
     const uint32_t t = threadIdx.x, V = a.b.V;
     const uint32_t vs = st.vstar;
@@ -1386,6 +1387,27 @@ __global__ __launch_bounds__(PV_NT) void zs_k_kcount(zs_sargs a) {
     for (int u = 0; u < NS; u++) {
         const uint32_t idx0 = g * ZS_BIG_G + 4 * (t + u * PV_NT);
         v[u] = idx0 < V ? *reinterpret_cast<const uint4*>(a.pv + (size_t)r * a.max_vocab + idx0) : make_uint4(0u, 0u, 0u, 0u);
+    }
+    if (st.kident) {
+        // the list is the row's p itself: its approximate sum per sub-chunk
+        // (slot u of the threads holds sub-chunk u of the group)
+        static_assert(ZS_BIG_G / ZS_SUB == NS && 4 * PV_NT == ZS_SUB, "slot u = sub-chunk u of the group");
+        __shared__ double ssum[NS][PV_NT / 64];
+#pragma unroll
+        for (int u = 0; u < NS; u++) {
+            const double d = wave_sum_d((double)zs_u2f(v[u].x) + (double)zs_u2f(v[u].y) + (double)zs_u2f(v[u].z) +
+                                        (double)zs_u2f(v[u].w));
+            if (zs_lane() == 0) ssum[u][zs_wid()] = d;
+        }
+        __syncthreads();
+        const uint32_t sub = g * NS + t;
+        if (t < NS && sub < (V + ZS_SUB - 1) / ZS_SUB)
+            a.k_ap[(size_t)r * a.max_subs + sub] = ssum[t][0] + ssum[t][1] + ssum[t][2] + ssum[t][3];
+        if (g == 0 && t == 0) {
+            st.nk = V;
+            st.klist = 1;
+        }
+        return;
     }
     uint32_t c = 0;  // (above << 16) | equal
 #pragma unroll
@@ -1414,7 +1436,7 @@ __global__ __launch_bounds__(PV_NT) void zs_k_kcount(zs_sargs a) {
 __global__ __launch_bounds__(PV_NT) void zs_k_kwrite(zs_sargs a) {
     const uint32_t g = blockIdx.x, r = blockIdx.y;
     zs_row_state& st = a.rst[r];
-    if (!st.kpend) return;
+    if (!st.kpend || st.kident) return;
     const uint32_t t = threadIdx.x, V = a.b.V;
     const uint32_t ng = (V + ZS_BIG_G - 1) / ZS_BIG_G;
     __shared__ uint32_t sh[PV_NT / 64];
@@ -1501,15 +1523,20 @@ __global__ __launch_bounds__(PV_NT) void zs_k_kwrite(zs_sargs a) {
 // ===========================================================================
 struct klist_row {
     const uint32_t* kp;
-    const uint32_t* ki;
+    const uint32_t* ki;   // (null for a row whose list is its p in index order: entry i is id i)
     uint32_t nk, vstar, istar;
     float inv;  // 0: the kept p themselves (sum2, or the draw without top-p), else p / sum2 (draw)
     float sum2;
 };
 __device__ __forceinline__ klist_row make_klist(const zs_sargs& a, uint32_t r, const zs_row_state& st, int kind) {
     klist_row L;
-    L.kp = a.pairs + (size_t)r * a.max_vocab * 2;
-    L.ki = L.kp + a.max_vocab;
+    if (st.kident) {
+        L.kp = a.pv + (size_t)r * a.max_vocab;
+        L.ki = nullptr;
+    } else {
+        L.kp = a.pairs + (size_t)r * a.max_vocab * 2;
+        L.ki = L.kp + a.max_vocab;
+    }
     L.nk = st.nk;
     L.vstar = st.vstar;
     L.istar = st.istar;
@@ -1529,7 +1556,7 @@ __device__ __forceinline__ void klist_terms16(const klist_row& L, uint32_t j, fl
     for (int q = 0; q < ZS_SUB / 64; q++) {
         const uint32_t i = min(j * ZS_SUB + (uint32_t)q * 64u + (uint32_t)zs_lane(), L.nk - 1u);
         pb[q] = L.kp[i];
-        id[q] = L.ki[i];
+        id[q] = L.ki ? L.ki[i] : i;
     }
 #pragma unroll
     for (int q = 0; q < ZS_SUB / 64; q++) {
@@ -1723,7 +1750,7 @@ struct klist_tp {
     __device__ __forceinline__ void fetch(uint32_t j, klist_raw& raw) const {
         const uint32_t i = at(j);
         raw.p = *reinterpret_cast<const uint4*>(L.kp + i);
-        raw.i = *reinterpret_cast<const uint4*>(L.ki + i);
+        raw.i = L.ki ? *reinterpret_cast<const uint4*>(L.ki + i) : make_uint4(i, i + 1u, i + 2u, i + 3u);
     }
     __device__ __forceinline__ void take(uint32_t j, const klist_raw& raw, float (&v)[SW_TPT]) const {
         const uint32_t i0 = j * ZS_SUB + SW_TPT * threadIdx.x;
@@ -1785,7 +1812,7 @@ __global__ __launch_bounds__(SW_NT) void zs_k_stitchK(zs_sargs a) {
         if (KIND == 0) {
             stp->sum2 = s;
         } else {
-            stp->token = stop != 0xffffffffu ? L.ki[stop] : a.b.V - 1;
+            stp->token = stop != 0xffffffffu ? (L.ki ? L.ki[stop] : stop) : a.b.V - 1;
             stp->mode = ZS_MODE_DONE;
         }
     }
