@@ -109,8 +109,8 @@ SPEC_K = 4
 # HBM bytes per launch of the C5 batch's dispatches, measured with rocprofv3
 # --pmc FETCH_SIZE / WRITE_SIZE and scaled by the copy-kernel calibration
 # (profiles/c5_kernels_counters.md, the tree of the commit that added it)
-TRAFFIC = {"zs_k_spec_chunk": 1402.4e6, "zs_k_row": 110.2e6, "zs_k_sapx1": 24.7e6, "zs_k_sround1": 28.0e6,
-           "zs_k_sapx2": 81.9e6, "zs_k_sround2": 91.6e6, "zs_k_sround3": 91.9e6, "zs_k_pv": 63.9e6,
+TRAFFIC = {"zs_k_spec_chunk": 1402.4e6, "zs_k_row": 107.8e6, "zs_k_sapx1": 26.6e6, "zs_k_sround1": 30.1e6,
+           "zs_k_sapx2": 87.1e6, "zs_k_sround2": 97.2e6, "zs_k_sround3": 97.5e6, "zs_k_pv": 64.1e6,
            "zs_k_tp_inc": 36.4e6, "zs_k_big": 0.6e6}
 
 
