@@ -1573,10 +1573,6 @@ __device__ __forceinline__ void klist_terms16(const klist_row& L, uint32_t j, fl
 // one wave per (sub-chunk, row): the increment pair of the sub-chunk on the
 // grid predicted from the approximate prefix (terms in order: the q-th 64
 // entries, lanes in order)
-#ifdef ZS_WALK_DEBUG
-__device__ unsigned long long sw_wt[64 * 160];
-__device__ unsigned long long sw_wt2[64 * 160];
-#endif
 template <int KIND>
 __global__ __launch_bounds__(256) void zs_k_roundK(zs_sargs a) {
     const uint32_t r = blockIdx.y;
@@ -1585,16 +1581,12 @@ __global__ __launch_bounds__(256) void zs_k_roundK(zs_sargs a) {
     if (!st.klist || (KIND == 0 && !st.knorm)) return;   // no sum2 without a top-p cut
     const uint32_t nks = (st.nk + ZS_SUB - 1) / ZS_SUB;
     if (j >= nks) return;
-    const unsigned long long t0 = SW_CLK();
     const klist_row L = make_klist(a, r, st, KIND);
     const double* ap = a.k_ap + (size_t)r * a.max_subs;
     // approximate prefix before sub-chunk j and after it
     double pre = 0.0;
     for (uint32_t i = zs_lane(); i < j; i += 64) pre += ap[i];
     pre = wave_sum_d(pre);
-#ifdef ZS_WALK_DEBUG
-    const unsigned long long t1 = SW_CLK();
-#endif
     const double scale = KIND ? 1.0 / (double)L.sum2 : 1.0;
     const double lo = pre * scale, hi = (pre + ap[j]) * scale;
     const double delta = 1.0 / 256.0;
@@ -1602,12 +1594,6 @@ __global__ __launch_bounds__(256) void zs_k_roundK(zs_sargs a) {
     sm_rec e = {0, 0u, 0u, 0u};
     float tv[ZS_SUB / 64];
     klist_terms16(L, j, tv);
-#ifdef ZS_WALK_DEBUG
-    float tvs = 0.0f;
-    for (int q = 0; q < ZS_SUB / 64; q++) tvs += tv[q];
-    const unsigned long long t2 = SW_CLK() + (tvs == 12345.0f ? 1 : 0);
-    if (zs_lane() == 0 && r < 64) sw_wt2[r * 160 + j] = (t1 - t0) | ((t2 - t0) << 32);
-#endif
     if (j == 0) {
         // sub-chunk 0 from the sum's start value, term by term (with the
         // draw's stop threshold, the uniform zs_k_stitchK compares with)
@@ -1621,9 +1607,6 @@ __global__ __launch_bounds__(256) void zs_k_roundK(zs_sargs a) {
         const float s0 = sm_serial(k0buf, ZS_SUB, KIND ? 0.0f : -0.0f, thr, &sp);
         if (zs_lane() == 0)
             reinterpret_cast<sm_rec*>(a.k_sum)[((size_t)r * 2 + KIND) * a.max_subs] = sm_rec{0, SM_EXACT, __float_as_uint(s0), sp};
-#ifdef ZS_WALK_DEBUG
-        if (zs_lane() == 0 && r < 64) sw_wt[r * 160 + j] = SW_CLK() - t0;
-#endif
         return;
     }
     // a sub-chunk where the sum surely starts in one binade and ends in the
@@ -1733,9 +1716,6 @@ __global__ __launch_bounds__(256) void zs_k_roundK(zs_sargs a) {
         e.d1 = all.o;
     }
     if (zs_lane() == 0) reinterpret_cast<sm_rec*>(a.k_sum)[((size_t)r * 2 + KIND) * a.max_subs + j] = e;
-#ifdef ZS_WALK_DEBUG
-    if (zs_lane() == 0 && r < 64) sw_wt[r * 160 + j] = (SW_CLK() - t0) | ((unsigned long long)(e.flags) << 48);
-#endif
 }
 
 // Kept-list terms for sm_stitch: thread t's 4 consecutive entries.
@@ -2096,10 +2076,6 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
 }
 
 #ifdef ZS_WALK_DEBUG
-extern "C" int zs_dbg_wave_times(unsigned long long* out) {
-    if (hipMemcpyFromSymbol(out + 64 * 160, HIP_SYMBOL(sw_wt2), 64 * 160 * sizeof(unsigned long long)) != hipSuccess) return -1;
-    return hipMemcpyFromSymbol(out, HIP_SYMBOL(sw_wt), 64 * 160 * sizeof(unsigned long long)) == hipSuccess ? 0 : -1;
-}
 extern "C" int zs_dbg_walk_stats_k(unsigned long long* out) {
     if (hipMemcpyFromSymbol(out, HIP_SYMBOL(sw_dbg), 32 * sizeof(unsigned long long)) != hipSuccess) return -1;
     static unsigned long long zero[32];
