@@ -1014,17 +1014,34 @@ __device__ __forceinline__ int tp_walk(const zs_sargs& a, uint32_t r, float top_
                 for (int q = 0; q < TP_CH / 64; q++) lbuf[lane + 64u * (uint32_t)q] = zs_u2f(w[q]);
                 __builtin_amdgcn_s_waitcnt(0);
                 __builtin_amdgcn_wave_barrier();
-                for (uint32_t i = 0; i < m; i += 4) {
-                    const float4 q4 = *reinterpret_cast<const float4*>(lbuf + i);
-                    const float c1 = ss + q4.x, c2 = c1 + q4.y, c3 = c2 + q4.z, c4 = c3 + q4.w;
-                    if (c4 >= top_p) {
-                        const uint32_t e0 = c1 >= top_p ? 0u : c2 >= top_p ? 1u : c3 >= top_p ? 2u : 3u;
-                        stop = true;
-                        at = c0 + i + e0;
-                        ss = e0 == 0 ? c1 : e0 == 1 ? c2 : e0 == 2 ? c3 : c4;
-                        break;
+                // 32 values per batch of LDS reads (their latency off the
+                // chain of additions; the zeros past m add nothing to the
+                // positive sum); the batch that reaches top_p is added again
+                // 4 values at a time to find the value
+                static_assert(TP_CH % 32 == 0, "whole batches inside a chunk");
+                for (uint32_t i0 = 0; i0 < m && !stop; i0 += 32) {
+                    float4 q8[8];
+#pragma unroll
+                    for (int u = 0; u < 8; u++) q8[u] = *reinterpret_cast<const float4*>(lbuf + i0 + 4 * u);
+                    float c = ss;
+#pragma unroll
+                    for (int u = 0; u < 8; u++) c = (((c + q8[u].x) + q8[u].y) + q8[u].z) + q8[u].w;
+                    if (c < top_p) {
+                        ss = c;
+                        continue;
                     }
-                    ss = c4;
+                    for (uint32_t i = i0; i < i0 + 32; i += 4) {
+                        const float4 q4 = *reinterpret_cast<const float4*>(lbuf + i);
+                        const float c1 = ss + q4.x, c2 = c1 + q4.y, c3 = c2 + q4.z, c4 = c3 + q4.w;
+                        if (c4 >= top_p) {
+                            const uint32_t e0 = c1 >= top_p ? 0u : c2 >= top_p ? 1u : c3 >= top_p ? 2u : 3u;
+                            stop = true;
+                            at = c0 + i + e0;
+                            ss = e0 == 0 ? c1 : e0 == 1 ? c2 : e0 == 2 ? c3 : c4;
+                            break;
+                        }
+                        ss = c4;
+                    }
                 }
                 __builtin_amdgcn_wave_barrier();
             }
