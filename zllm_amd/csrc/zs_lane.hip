@@ -609,8 +609,8 @@ __global__ void zs_k_sample_topk(const float* vals, const uint32_t* idxs, uint32
 
 // The same draw by one wave for a pool of at most 64 (lane i holds entry i:
 // value v, id; lanes >= K hold -inf): the exponentials in parallel, the
-// sequential sums (sampler order, f32) as broadcast chains. Returns the id
-// (uniform).
+// sequential sums (sampler order, f32) as chains of lane reads (the index is
+// uniform: v_readlane, no LDS permute). Returns the id (uniform).
 __device__ __forceinline__ uint32_t lane_draw64(float v, uint32_t id, uint32_t K, float T, uint32_t top_k, float tp,
                                                 uint32_t seed) {
     const int lane = zs_lane();
@@ -623,23 +623,23 @@ __device__ __forceinline__ uint32_t lane_draw64(float v, uint32_t id, uint32_t K
     const float maxv = __shfl(v, 0, 64);
     const float e = (uint32_t)lane < kk ? zs_expf((v - maxv) / T) : 0.0f;
     float z = -0.0f;
-    for (uint32_t i = 0; i < kk; i++) z = z + __shfl(e, (int)i, 64);
+    for (uint32_t i = 0; i < kk; i++) z = z + zs_readlane_f(e, i);
     const float p = e / z;
     uint32_t cut = kk;
     if (tp > 0.0f && tp < 1.0f) {
         float cum = 0.0f;
         for (uint32_t i = 0; i < kk; i++) {
-            cum = cum + __shfl(p, (int)i, 64);
+            cum = cum + zs_readlane_f(p, i);
             if (cum >= tp) { cut = i + 1; break; }
         }
     }
     float zc = -0.0f;
-    for (uint32_t i = 0; i < cut; i++) zc = zc + __shfl(p, (int)i, 64);
+    for (uint32_t i = 0; i < cut; i++) zc = zc + zs_readlane_f(p, i);
     const float target = zs_rng01(seed) * zc;
     float acc = 0.0f;
     uint32_t pick = cut - 1;
     for (uint32_t i = 0; i < cut; i++) {
-        acc = acc + __shfl(p, (int)i, 64);
+        acc = acc + zs_readlane_f(p, i);
         if (acc >= target) { pick = i; break; }
     }
     return __shfl(id, (int)pick, 64);
