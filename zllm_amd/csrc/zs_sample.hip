@@ -1776,7 +1776,7 @@ __global__ __launch_bounds__(SW_NT) void zs_k_stitchK(zs_sargs a) {
     const uint32_t r = blockIdx.x;
     zs_row_state* stp = a.rst + r;
     if (!stp->klist || (KIND == 0 && !stp->knorm)) return;
-    const unsigned long long k0 = SW_CLK();
+    [[maybe_unused]] const unsigned long long k0 = SW_CLK();
     const zs_row_state st = *stp;
     const klist_row L = make_klist(a, r, st, KIND);
     const uint32_t nks = (L.nk + ZS_SUB - 1) / ZS_SUB;
@@ -1800,7 +1800,7 @@ __global__ __launch_bounds__(SW_NT) void zs_k_stitchK(zs_sargs a) {
         }
         thresh = rr;
     }
-    const unsigned long long k1 = SW_CLK();
+    [[maybe_unused]] const unsigned long long k1 = SW_CLK();
     klist_tp tp{L};
     uint32_t stop;
     const float s = sm_stitch<klist_tp, klist_raw>(tp, nks, KIND ? 0.0f : -0.0f, thresh, &stop);
@@ -2025,7 +2025,6 @@ extern "C" int zs_sample_launch(zs_ctx* ctx, const zs_batch* bt, hipStream_t str
     a.pstride = ctx->max_vocab;
     a.s_hterm = ctx->s_hterm;
     const uint32_t B = bt->B;
-    const uint32_t nch = (bt->V + ZS_P1_CH - 1) / ZS_P1_CH;
     const bool prof = ctx->profiling != 0;
     int ev = 0;
     auto mark = [&](const char* name) {

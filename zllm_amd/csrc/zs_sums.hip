@@ -810,7 +810,7 @@ __global__ __launch_bounds__(SW_NT) void zs_k_sstitch(zs_sargs a) {
     zs_row_state* stp = a.rst + r;
     const int kind = sm_stage_kind<STAGE>();
     if (!((stp->rounds >> kind) & 1u)) return;
-    const unsigned long long k0 = SW_CLK();
+    [[maybe_unused]] const unsigned long long k0 = SW_CLK();
     sm_tab_fill();
     const zs_row_state& st = *stp;
     const zs_row_params P = a.b.d_params[r];
@@ -825,7 +825,7 @@ __global__ __launch_bounds__(SW_NT) void zs_k_sstitch(zs_sargs a) {
         if (e.flags & (SM_CROSS | SM_ALT)) sm_sh.xrec[i] = xrec[i];
     }
     __syncthreads();
-    const unsigned long long k1 = SW_CLK();
+    [[maybe_unused]] const unsigned long long k1 = SW_CLK();
     sm_row_tp tp{S, f, sm_darea(a, r, kind)};
     uint32_t stop;
     const float s = sm_stitch<sm_row_tp, sm_f4>(tp, nsub, kind == ZS_SUM_OBS_H ? 0.0f : -0.0f, NAN, &stop);

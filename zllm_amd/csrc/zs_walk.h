@@ -244,7 +244,7 @@ __device__ __forceinline__ float sm_walk(const float (&v)[SW_TPT], float s, floa
             s = s + 0.0f;
             if (first == 0xffffffffu) return s;
             const uint32_t end = min(first + SM_HEAD, (uint32_t)ZS_SUB);
-            const unsigned long long h0 = SW_CLK();
+            [[maybe_unused]] const unsigned long long h0 = SW_CLK();
             // the head's terms lie in at most two waves: each wave adds the
             // ones it holds, in order, the first wave's before the second's
             const uint32_t w0 = first / (SW_TPT * 64), w1 = (end - 1) / (SW_TPT * 64);
@@ -313,7 +313,7 @@ __device__ __forceinline__ float sm_walk(const float (&v)[SW_TPT], float s, floa
             if (sp != 0xffffffffu) { *stop = sp; return s; }
             continue;
         }
-        const unsigned long long c0 = SW_CLK();
+        [[maybe_unused]] const unsigned long long c0 = SW_CLK();
         const int eg = zs_grid_exp(s);
         const uint32_t k = zs_grid_k(s);
         const uint32_t kthr = zs_grid_thresh(thresh, eg);
@@ -354,7 +354,7 @@ __device__ __forceinline__ float sm_walk(const float (&v)[SW_TPT], float s, floa
             }
             tie2 = 1u;
         }
-        const unsigned long long c1 = SW_CLK();
+        [[maybe_unused]] const unsigned long long c1 = SW_CLK();
         // inclusive scans over the wave: plain sums unless a half-way term
         // makes the increments depend on the parity
         const bool wtie = __builtin_amdgcn_readfirstlane((int)(__ballot(tie != 0u) != 0ull)) != 0;
@@ -377,9 +377,9 @@ __device__ __forceinline__ float sm_walk(const float (&v)[SW_TPT], float s, floa
             sh.w2[par][wid] = w2;
             sh.wt2[par][wid] = anyt2w ? 1u : 0u;
         }
-        const unsigned long long c2 = SW_CLK();
+        [[maybe_unused]] const unsigned long long c2 = SW_CLK();
         sm_bar();
-        const unsigned long long c3 = SW_CLK();
+        [[maybe_unused]] const unsigned long long c3 = SW_CLK();
         seq_pair pre = {0u, 0u};   // the waves before this one
         uint32_t pre2 = 0u, all2 = 0u, anyt2 = 0u;
 #pragma unroll
@@ -447,9 +447,9 @@ __device__ __forceinline__ float sm_walk(const float (&v)[SW_TPT], float s, floa
         }
         if (lane == 0) sh.cross[par][wid] = bad ? 1u : 0u;
         if (t == SW_NT - 1) sh.tot_s[par] = (kend < ZS_BINADE && kend < kthr) ? zs_grid_value(kend, eg) : 0.0f;
-        const unsigned long long c4 = SW_CLK();
+        [[maybe_unused]] const unsigned long long c4 = SW_CLK();
         sm_bar();
-        const unsigned long long c5 = SW_CLK();
+        [[maybe_unused]] const unsigned long long c5 = SW_CLK();
         SW_T(0, c1 - c0); SW_T(1, c2 - c1); SW_T(2, c3 - c2); SW_T(3, c4 - c3); SW_T(4, c5 - c4); SW_T(5, 1);
         int cw = -1;
 #pragma unroll
@@ -582,7 +582,7 @@ __device__ __forceinline__ float sm_stitch(TP& tp, uint32_t nsub, float s, float
         j = 1;
     }
     while (j < nsub) {
-        const unsigned long long g0 = SW_CLK();
+        [[maybe_unused]] const unsigned long long g0 = SW_CLK();
         const uint32_t fj = sm_sh.rec[j].flags;
         if (s != 0.0f && (fj & SM_SAFE)) {
             // sub-chunks j .. j+63 on the grid of s, applied up to the first
@@ -620,7 +620,7 @@ __device__ __forceinline__ float sm_stitch(TP& tp, uint32_t nsub, float s, float
             }
         }
         float v[SW_TPT];
-        const unsigned long long l0 = SW_CLK();
+        [[maybe_unused]] const unsigned long long l0 = SW_CLK();
         if (xr) {
             // a crossing record that did not hold: its stored terms
             RAW qx;
@@ -645,7 +645,7 @@ __device__ __forceinline__ float sm_stitch(TP& tp, uint32_t nsub, float s, float
 #ifdef ZS_WALK_DEBUG
         if (threadIdx.x == 0) atomicAdd(&sw_hist[j < 31u ? j : (j + 32u >= nsub ? 63u - (nsub - 1u - j) : 31u)], 1ull);
 #endif
-        const unsigned long long l1 = SW_CLK();
+        [[maybe_unused]] const unsigned long long l1 = SW_CLK();
         SW_T(8, l1 - l0); SW_T(9, 1);
         s = sm_walk(v, s, thresh, &sp);
         sm_bar();
